@@ -1,0 +1,263 @@
+/*
+ * nest_splat.h -- C ABI of the MI355X (gfx950) forward renderer for neural
+ * shell texture splatting: 2D-surfel preprocess, tile binning with a radix
+ * sort, per-tile compositing with an in-loop multi-level hash-grid lookup,
+ * view-direction MLP decode on MFMA, RVQ attribute decode.
+ *
+ * Conventions
+ *  - Every pointer named "device" is HIP device memory owned by the caller;
+ *    the library never allocates device memory.  Scratch comes in through
+ *    caller-provided workspaces whose sizes the *_workspace_size / *_layout
+ *    queries report.
+ *  - Every launch is ordered on the caller's stream (a hipStream_t passed as
+ *    void*, NULL = the null stream).  The only host synchronisation is the
+ *    read-back of the number of tile/splat pairs in nest_forward_geometry
+ *    (the reference reads it the same way, rasterizer_impl.cu:359).
+ *  - Every entry point returns NEST_OK (0) or a negative status.  Arguments
+ *    are validated before the first launch, so an error return leaves every
+ *    output untouched.  nest_last_error() gives the message of the last failed
+ *    call on the calling thread.
+ *  - Reference citations are relative to the NilKel/nest-splatting tree:
+ *      CR/  = submodules/diff-surfel-rasterization/cuda_rasterizer/
+ *      DSR/ = submodules/diff-surfel-rasterization/
+ *      GE/  = gridencoder/,  HE = hash_encoder/modules.py
+ */
+#ifndef NEST_SPLAT_H
+#define NEST_SPLAT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NEST_ABI_VERSION 1
+
+#define NEST_OK 0
+#define NEST_ERR_INVALID_ARGUMENT (-1)
+#define NEST_ERR_UNSUPPORTED (-2)
+#define NEST_ERR_WORKSPACE (-3)
+#define NEST_ERR_HIP (-4)
+#define NEST_ERR_OVERFLOW (-5)
+
+#define NEST_DTYPE_F32 0
+#define NEST_DTYPE_F16 1
+#define NEST_DTYPE_BF16 2
+
+#define NEST_MAX_LEVELS 32
+#define NEST_MAX_CHANNELS 128
+#define NEST_OTHERS_CHANNELS 14 /* allmap channels, CR/auxiliary.h:24-31 */
+
+/* Per-frame rasterizer settings: GaussianRasterizationSettings
+ * (DSR/diff_surfel_rasterization/__init__.py:277-293).  Matrices are the
+ * reference's flat float[16] world_view_transform / full_proj_transform. */
+typedef struct nest_raster_settings {
+  uint32_t struct_size;
+  int32_t image_height;
+  int32_t image_width;
+  float tanfovx;
+  float tanfovy;
+  float scale_modifier;
+  float viewmatrix[16];
+  float projmatrix[16];
+  float campos[3];
+  float beta;
+  int32_t prefiltered;
+  int32_t debug;              /* synchronise and check after every stage */
+  int32_t if_contract;
+  uint32_t max_intersections; /* 0 = unlimited */
+} nest_raster_settings;
+
+/* Hash grid seen by the render loop: HashGridSettings (DSRpy:295-302) plus the
+ * GridEncoder parameters of GE/grid.py:164-165.  offsets and gridrange are
+ * host copies of the reference's device tensors. */
+typedef struct nest_hashgrid {
+  uint32_t struct_size;
+  uint32_t levels;            /* L queried; 0 selects the colours_precomp path */
+  uint32_t level_dim;         /* F: 1, 2, 4 or 8 */
+  float log2_scale;           /* S = log2(per_level_scale) */
+  uint32_t base_resolution;   /* H */
+  int32_t align_corners;
+  int32_t interpolation;      /* 0 linear, 1 smoothstep */
+  int32_t table_dtype;        /* NEST_DTYPE_F32 or NEST_DTYPE_F16 */
+  const void *table;          /* device, [table_rows, F] */
+  int64_t table_rows;         /* rows of the table; must be >= offsets[levels] */
+  int32_t offsets[NEST_MAX_LEVELS + 1];
+  float gridrange[2];
+} nest_hashgrid;
+
+/* Splat attributes (device, float32, contiguous), as the reference passes them
+ * to _C.rasterize_gaussians (DSRpy:105-146). */
+typedef struct nest_splats {
+  uint32_t struct_size;
+  int32_t P;
+  const float *means3D;        /* [P,3] */
+  const float *scales;         /* [P,2] activated */
+  const float *rotations;      /* [P,4] (w,x,y,z) */
+  const float *opacities;      /* [P,1] activated */
+  const float *homotrans;      /* [P,4,4] build_H, hash path */
+  const float *ap_level;       /* [P,1] appearance level, NULL = no cap */
+  const float *colors_precomp; /* [P,channels], colour path (levels == 0) */
+} nest_splats;
+
+/* Frame outputs (device): out_color [channels,H,W], out_others [14,H,W] and
+ * radii [P], the tensors RasterizeGaussiansCUDA returns
+ * (DSR/rasterize_points.cu:156-166, :241). */
+typedef struct nest_frame_outputs {
+  uint32_t struct_size;
+  int32_t channels;
+  float *out_color;
+  float *out_others;
+  int32_t *radii;
+} nest_frame_outputs;
+
+/* Optional per-stage device times in milliseconds, measured with HIP events on
+ * the caller's stream (adds one synchronisation per stage when enabled). */
+#define NEST_STAGE_PREPROCESS 0
+#define NEST_STAGE_SCAN 1
+#define NEST_STAGE_DUPLICATE 2
+#define NEST_STAGE_SORT 3
+#define NEST_STAGE_RANGES 4
+#define NEST_STAGE_RENDER 5
+#define NEST_STAGE_COUNT 6
+typedef struct nest_timing {
+  uint32_t struct_size;
+  int32_t enabled;
+  float ms[NEST_STAGE_COUNT];
+} nest_timing;
+
+/* ---- library ---------------------------------------------------------- */
+
+int nest_abi_version(void);
+const char *nest_last_error(void);
+
+/* ---- workspaces: GeometryState / BinningState / ImageState --------------
+ * Replace the byte-buffer carving of CR/rasterizer_impl.cu:212-250 and
+ * CR/rasterizer_impl.h:21-73.  Layout queries give the byte offset of each
+ * array so callers (and tests) can read intermediate results. */
+#define NEST_GEOM_DEPTH 0          /* f32 [P]                         */
+#define NEST_GEOM_XY 1             /* f32 [P,2]                       */
+#define NEST_GEOM_TILES 2          /* u32 [P]    tiles touched        */
+#define NEST_GEOM_OFFSETS 3        /* u32 [P]    inclusive scan       */
+#define NEST_GEOM_RECORDS 4        /* f32 [P,32] packed render record:
+                                      0-2 Tu, 3-5 Tv, 6-8 Tw, 9-10 xy,
+                                      11 opacity, 12-14 view normal,
+                                      15 floor(ap_level) as uint32 bits,
+                                      16-18 / 19-21 / 22-24 homotrans
+                                      columns 0 / 1 / 3, 25 depth      */
+#define NEST_GEOM_RADII 5          /* i32 [P]                         */
+#define NEST_GEOM_SCAN_TMP 6       /* scan scratch                    */
+#define NEST_GEOM_FIELDS 7
+int nest_geom_layout(int32_t P, size_t offsets[NEST_GEOM_FIELDS], size_t *total_bytes);
+
+#define NEST_BIN_KEYS_UNSORTED 0   /* u64 [NR] */
+#define NEST_BIN_VALS_UNSORTED 1   /* u32 [NR] */
+#define NEST_BIN_KEYS 2            /* u64 [NR] sorted */
+#define NEST_BIN_VALS 3            /* u32 [NR] sorted (point_list) */
+#define NEST_BIN_SORT_TMP 4
+#define NEST_BIN_FIELDS 5
+int nest_binning_layout(int64_t num_rendered, size_t offsets[NEST_BIN_FIELDS], size_t *total_bytes);
+
+#define NEST_IMG_RANGES 0          /* u32 [tiles,2] */
+#define NEST_IMG_FINAL_T 1         /* f32 [3,H,W]  (T, M1, M2)   */
+#define NEST_IMG_N_CONTRIB 2       /* u32 [2,H,W]  (last, median) */
+#define NEST_IMG_FIELDS 3
+int nest_image_layout(int32_t width, int32_t height, size_t offsets[NEST_IMG_FIELDS], size_t *total_bytes);
+
+/* ---- forward rasterizer -------------------------------------------------
+ * Together these two calls are RasterizeGaussiansCUDA
+ * (DSR/rasterize_points.cu:40-242) / CudaRasterizer::Rasterizer::forward
+ * (CR/rasterizer_impl.cu:255-440) for render_mode 0, split at the
+ * num_rendered read-back (CR/rasterizer_impl.cu:359) so that the caller can
+ * size the binning workspace in between, as the resize callbacks
+ * (DSR/rasterize_points.cu:31-37) do in the reference.
+ *
+ * nest_forward_geometry: preprocessCUDA (CR/forward.cu:323-441) plus the
+ * inclusive scan of tiles touched (CR/rasterizer_impl.cu:355); writes radii
+ * and the total number of tile/splat pairs (after a stream sync). */
+int nest_forward_geometry(const nest_raster_settings *settings, const nest_splats *splats,
+                          void *geom_ws, size_t geom_bytes, int32_t *radii,
+                          int64_t *num_rendered, nest_timing *timing, void *stream);
+
+/* nest_forward_render: duplicateWithKeys (CR/rasterizer_impl.cu:70-111),
+ * the radix sort on (tile|depth) keys (:378-386), identifyTileRanges
+ * (:173-195, :388) and renderCUDAsurfelForward<C, mode 0>
+ * (CR/forward.cu:639-2049, dispatch :2052-2158).  out_color channels must be
+ * >= levels*level_dim; channels past levels*level_dim are written as zero. */
+int nest_forward_render(const nest_raster_settings *settings, const nest_hashgrid *grid,
+                        const nest_splats *splats, void *geom_ws, size_t geom_bytes,
+                        void *binning_ws, size_t binning_bytes, void *image_ws, size_t image_bytes,
+                        int64_t num_rendered, const nest_frame_outputs *out,
+                        nest_timing *timing, void *stream);
+
+/* ---- building blocks ----------------------------------------------------- */
+
+/* cub::DeviceScan::InclusiveSum on uint32 (CR/rasterizer_impl.cu:223, :355). */
+size_t nest_scan_workspace_size(int64_t n);
+int nest_inclusive_scan_u32(const uint32_t *in, uint32_t *out, int64_t n, void *ws, size_t ws_bytes,
+                            void *stream);
+
+/* cub::DeviceRadixSort::SortPairs, stable, on key bits [0, end_bit)
+ * (CR/rasterizer_impl.cu:245-249, :381-386). */
+size_t nest_sort_workspace_size(int64_t n);
+int nest_sort_pairs_u64(const uint64_t *keys_in, const uint32_t *vals_in, uint64_t *keys_out,
+                        uint32_t *vals_out, int64_t n, int32_t end_bit, void *ws, size_t ws_bytes,
+                        void *stream);
+
+/* GridEncoder forward: grid_encode_forward (GE/src/gridencoder.cu:450-473,
+ * kernel_grid :87-242) for gridtype hash (0) or tiled (1).  inputs [B,D] in
+ * [0,1], embeddings [emb_rows, C] of emb_dtype (F32 or F16) with
+ * emb_rows >= offsets[L], offsets a host array of L+1 entries.  outputs
+ * [B, L*C] of emb_dtype: the permuted layout GE/grid.py:59 returns, written
+ * directly. */
+int nest_grid_encode(const float *inputs, int64_t B, int32_t D, const void *embeddings,
+                     int64_t emb_rows, int32_t emb_dtype, const int32_t *offsets_host, int32_t L, int32_t C, float S,
+                     int32_t H, int32_t gridtype, int32_t align_corners, int32_t interpolation,
+                     void *outputs, void *stream);
+
+/* View-direction MLP decode: INGP.rgb_decode/get_color (HE:587-602) with the
+ * SphericalHarmonics degree-4 view encoding of (d+1)/2 (HE:551-558, :727-730)
+ * and a bias-free ReLU MLP in -> width -> width -> 3 with sigmoid output
+ * (HE:560-572), fused with the mask and background composition of
+ * gaussian_renderer/__init__.py:1013-1021.
+ *  feat: float32, element (pixel n, channel c) at feat[c*feat_cstride + n*feat_nstride]
+ *  dirs: unit view directions [N,3] float32, or NULL to derive them per pixel
+ *        as (x, y, 1) @ ray_matrix (cam2rays, utils/point_utils.py:31-46,
+ *        normalised) for N = height*width pixels in row-major order
+ *  alpha: [N] or NULL; rgb = alpha > 0 ? rgb : 0, then + (1-alpha)*bg when
+ *        bg[0]+bg[1]+bg[2] > 0
+ *  weights: w1 [width, C+16], w2 [width, width], w3 [3, width] row-major in
+ *        dtype (F16 and BF16 run on MFMA, F32 on the vector ALU)
+ *  out: element (channel o, pixel n) at out[o*out_ostride + n*out_nstride] */
+typedef struct nest_mlp {
+  uint32_t struct_size;
+  int32_t in_features;       /* C */
+  int32_t width;             /* hidden width: 16..256, multiple of 16 */
+  int32_t dtype;
+  const void *w1;
+  const void *w2;
+  const void *w3;
+} nest_mlp;
+int nest_mlp_decode(const nest_mlp *mlp, const float *feat, int64_t feat_cstride, int64_t feat_nstride,
+                    int64_t N, int32_t width, const float *dirs, const float ray_matrix[9],
+                    const float *alpha, const float bg[3], float *out, int64_t out_ostride,
+                    int64_t out_nstride, void *stream);
+
+/* Residual-VQ attribute decode (no reference counterpart; defined by the
+ * RVQ workload of the benchmark suite):
+ *   raw[p][d] = bias[d] + (((cb[0][i0][d] + cb[1][i1][d]) + cb[2][i2][d]) + ...)
+ * codebooks [stages, K, dim] float32, indices [P, stages] uint16, bias a host
+ * array of dim floats or NULL.  activation: 0 none, 1 exp, 2 normalise
+ * (v / max(|v|, 1e-12)), 3 sigmoid -- the GaussianModel activations
+ * (scene/gaussian_model.py:26-41).  out [P,dim]; raw_out [P,dim] or NULL.
+ * An index >= codebook_size is never dereferenced: that splat decodes to NaN. */
+int nest_rvq_decode(int64_t P, int32_t stages, int32_t codebook_size, int32_t dim,
+                    const float *codebooks, const uint16_t *indices, const float *bias,
+                    int32_t activation, float *out, float *raw_out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NEST_SPLAT_H */

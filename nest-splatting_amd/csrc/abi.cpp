@@ -1,0 +1,558 @@
+// C ABI of the forward renderer: argument validation, workspace layout,
+// stage sequencing on the caller's stream.
+//
+// Host orchestration counterpart of CudaRasterizer::Rasterizer::forward
+// (submodules/diff-surfel-rasterization/cuda_rasterizer/rasterizer_impl.cu:
+// 255-440) and RasterizeGaussiansCUDA (submodules/diff-surfel-rasterization/
+// rasterize_points.cu:40-242).  Differences by design: every launch goes to
+// the caller's stream instead of the legacy default stream, the library never
+// allocates (workspaces come from the caller), the hash-grid offsets and grid
+// range arrive as host values instead of device tensors read with .item(), and
+// an unsupported configuration is an error instead of a printf and zeros.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/nest_splat.h"
+#include "nest_internal.h"
+
+using namespace nest;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(NEST_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+size_t align_up(size_t v, size_t a = 256) { return (v + a - 1) / a * a; }
+
+// Sequential carving of one workspace into 256-byte aligned arrays.
+struct Carver {
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    const size_t o = off;
+    off = align_up(off + bytes);
+    return o;
+  }
+};
+
+uint32_t higher_msb(uint32_t n) {  // getHigherMsb, rasterizer_impl.cu:35-50
+  uint32_t msb = sizeof(n) * 4;
+  uint32_t step = msb;
+  while (step > 1) {
+    step /= 2;
+    if (n >> msb) msb += step;
+    else msb -= step;
+  }
+  if (n >> msb) msb++;
+  return msb;
+}
+
+// Per-level constants of query_feature / kernel_grid (hashgrid.h:122-131,
+// gridencoder.cu:130-132) and the outcome of get_grid_index's uint32 stride
+// loop (hashgrid.h:22-40) for D dimensions.
+int build_levels(const int32_t* offsets, uint32_t L, float S, uint32_t H, bool align_corners, int D, bool hash_type,
+                 LevelTable& lv) {
+  if (L > NEST_MAX_LEVELS) return fail(NEST_ERR_UNSUPPORTED, "at most %d hash levels are supported (got %u)", NEST_MAX_LEVELS, L);
+  memset(&lv, 0, sizeof(lv));
+  for (uint32_t l = 0; l < L; l++) {
+    if (offsets[l] < 0 || offsets[l + 1] <= offsets[l])
+      return fail(NEST_ERR_INVALID_ARGUMENT, "hash-grid offsets must be non-negative and strictly increasing (level %u)", l);
+    const uint32_t hsize = (uint32_t)(offsets[l + 1] - offsets[l]);
+    const float e = (float)l * S;
+    const float scale = (float)std::exp2((double)e) * (float)H - 1.0f;
+    const uint32_t res = (uint32_t)std::ceil(scale) + 1u;
+    const uint32_t res1 = align_corners ? res : res + 1u;
+    uint32_t stride = 1, ndims = 0;
+    for (int d = 0; d < D && stride <= hsize; d++) {
+      ndims++;
+      stride *= res1;
+    }
+    const bool hashed = hash_type && stride > hsize;
+    uint64_t bound = 0, st = 1;
+    for (uint32_t d = 0; d < ndims; d++) {
+      bound += (uint64_t)res * st;
+      st *= res1;
+    }
+    uint32_t flags = 0;
+    if (hashed) flags |= 1u;
+    if ((hsize & (hsize - 1u)) == 0) flags |= 2u;
+    if (!hashed && bound < hsize) flags |= 4u;
+    flags |= ndims << 8;
+    lv.scale[l] = scale;
+    lv.res1[l] = res1;
+    lv.hsize[l] = hsize;
+    lv.base[l] = (uint32_t)offsets[l];
+    lv.flags[l] = flags;
+  }
+  return NEST_OK;
+}
+
+struct StageTimer {
+  nest_timing* t;
+  hipStream_t s;
+  hipEvent_t a = nullptr, b = nullptr;
+  StageTimer(nest_timing* t_, hipStream_t s_) : t(t_ && t_->enabled ? t_ : nullptr), s(s_) {
+    if (t) {
+      hipEventCreate(&a);
+      hipEventCreate(&b);
+    }
+  }
+  ~StageTimer() {
+    if (a) hipEventDestroy(a);
+    if (b) hipEventDestroy(b);
+  }
+  void begin() {
+    if (t) hipEventRecord(a, s);
+  }
+  void end(int stage) {
+    if (!t) return;
+    hipEventRecord(b, s);
+    hipEventSynchronize(b);
+    float ms = 0.f;
+    hipEventElapsedTime(&ms, a, b);
+    t->ms[stage] = ms;
+  }
+};
+
+int check_stage(hipError_t e, const char* what, bool debug, hipStream_t s) {
+  if (e != hipSuccess) return hip_fail(e, what);
+  if (debug) {
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, what);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, what);
+  }
+  return NEST_OK;
+}
+
+int check_settings(const nest_raster_settings* rs) {
+  if (!rs) return fail(NEST_ERR_INVALID_ARGUMENT, "settings is NULL");
+  if (rs->struct_size != sizeof(nest_raster_settings))
+    return fail(NEST_ERR_INVALID_ARGUMENT, "nest_raster_settings.struct_size is %u, expected %zu", rs->struct_size,
+                sizeof(nest_raster_settings));
+  if (rs->image_width <= 0 || rs->image_height <= 0)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "image size must be positive (got %dx%d)", rs->image_width, rs->image_height);
+  if ((int64_t)rs->image_width * rs->image_height > (int64_t)1 << 31)
+    return fail(NEST_ERR_UNSUPPORTED, "image has more than 2^31 pixels");
+  return NEST_OK;
+}
+
+int check_splats(const nest_splats* sp, bool need_geometry) {
+  if (!sp) return fail(NEST_ERR_INVALID_ARGUMENT, "splats is NULL");
+  if (sp->struct_size != sizeof(nest_splats))
+    return fail(NEST_ERR_INVALID_ARGUMENT, "nest_splats.struct_size is %u, expected %zu", sp->struct_size, sizeof(nest_splats));
+  if (sp->P < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "P must be >= 0 (got %d)", sp->P);
+  if (need_geometry && sp->P > 0 && (!sp->means3D || !sp->scales || !sp->rotations || !sp->opacities))
+    return fail(NEST_ERR_INVALID_ARGUMENT, "means3D, scales, rotations and opacities are required");
+  return NEST_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nest_abi_version(void) { return NEST_ABI_VERSION; }
+
+const char* nest_last_error(void) { return g_last_error.c_str(); }
+
+int nest_geom_layout(int32_t P, size_t offsets[NEST_GEOM_FIELDS], size_t* total) {
+  if (P < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "P must be >= 0");
+  const size_t n = (size_t)(P > 0 ? P : 1);
+  Carver c;
+  size_t o[NEST_GEOM_FIELDS];
+  o[NEST_GEOM_DEPTH] = c.take(n * 4);
+  o[NEST_GEOM_XY] = c.take(n * 8);
+  o[NEST_GEOM_TILES] = c.take(n * 4);
+  o[NEST_GEOM_OFFSETS] = c.take(n * 4);
+  o[NEST_GEOM_RECORDS] = c.take(n * kRecordFloats * 4);
+  o[NEST_GEOM_RADII] = c.take(n * 4);
+  o[NEST_GEOM_SCAN_TMP] = c.take(scan_ws_bytes((int64_t)n));
+  if (offsets)
+    for (int i = 0; i < NEST_GEOM_FIELDS; i++) offsets[i] = o[i];
+  if (total) *total = c.off;
+  return NEST_OK;
+}
+
+int nest_binning_layout(int64_t NR, size_t offsets[NEST_BIN_FIELDS], size_t* total) {
+  if (NR < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "num_rendered must be >= 0");
+  const size_t n = (size_t)(NR > 0 ? NR : 1);
+  Carver c;
+  size_t o[NEST_BIN_FIELDS];
+  o[NEST_BIN_KEYS_UNSORTED] = c.take(n * 8);
+  o[NEST_BIN_VALS_UNSORTED] = c.take(n * 4);
+  o[NEST_BIN_KEYS] = c.take(n * 8);
+  o[NEST_BIN_VALS] = c.take(n * 4);
+  o[NEST_BIN_SORT_TMP] = c.take(sort_ws_bytes((int64_t)n));
+  if (offsets)
+    for (int i = 0; i < NEST_BIN_FIELDS; i++) offsets[i] = o[i];
+  if (total) *total = c.off;
+  return NEST_OK;
+}
+
+int nest_image_layout(int32_t W, int32_t H, size_t offsets[NEST_IMG_FIELDS], size_t* total) {
+  if (W <= 0 || H <= 0) return fail(NEST_ERR_INVALID_ARGUMENT, "image size must be positive");
+  const size_t tiles = (size_t)((W + kTile - 1) / kTile) * (size_t)((H + kTile - 1) / kTile);
+  const size_t HW = (size_t)W * H;
+  Carver c;
+  size_t o[NEST_IMG_FIELDS];
+  o[NEST_IMG_RANGES] = c.take(tiles * 8);
+  o[NEST_IMG_FINAL_T] = c.take(HW * 3 * 4);
+  o[NEST_IMG_N_CONTRIB] = c.take(HW * 2 * 4);
+  if (offsets)
+    for (int i = 0; i < NEST_IMG_FIELDS; i++) offsets[i] = o[i];
+  if (total) *total = c.off;
+  return NEST_OK;
+}
+
+int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp, void* geom_ws, size_t geom_bytes,
+                          int32_t* radii, int64_t* num_rendered, nest_timing* timing, void* stream) {
+  int rc = check_settings(rs);
+  if (rc) return rc;
+  if ((rc = check_splats(sp, true))) return rc;
+  if (!num_rendered) return fail(NEST_ERR_INVALID_ARGUMENT, "num_rendered is NULL");
+  if (rs->prefiltered) return fail(NEST_ERR_UNSUPPORTED, "prefiltered=True is not supported");
+  size_t off[NEST_GEOM_FIELDS], need = 0;
+  nest_geom_layout(sp->P, off, &need);
+  if (!geom_ws || geom_bytes < need)
+    return fail(NEST_ERR_WORKSPACE, "geometry workspace too small: %zu bytes given, %zu needed", geom_bytes, need);
+  *num_rendered = 0;
+  if (sp->P == 0) return NEST_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* g = static_cast<char*>(geom_ws);
+  const int W = rs->image_width, H = rs->image_height;
+
+  PreprocessParams p{};
+  p.P = sp->P;
+  p.W = W;
+  p.H = H;
+  p.gx = (uint32_t)((W + kTile - 1) / kTile);
+  p.gy = (uint32_t)((H + kTile - 1) / kTile);
+  p.scale_mod = rs->scale_modifier;
+  memcpy(p.view, rs->viewmatrix, sizeof(p.view));
+  memcpy(p.proj, rs->projmatrix, sizeof(p.proj));
+  p.means = sp->means3D;
+  p.scales = sp->scales;
+  p.rots = sp->rotations;
+  p.opac = sp->opacities;
+  p.homotrans = sp->homotrans;
+  p.ap_level = sp->ap_level;
+  p.radii = reinterpret_cast<int32_t*>(g + off[NEST_GEOM_RADII]);
+  p.radii_user = radii;
+  p.xy = reinterpret_cast<float*>(g + off[NEST_GEOM_XY]);
+  p.depth = reinterpret_cast<float*>(g + off[NEST_GEOM_DEPTH]);
+  p.tiles = reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_TILES]);
+  p.records = reinterpret_cast<float*>(g + off[NEST_GEOM_RECORDS]);
+
+  StageTimer tm(timing, s);
+  tm.begin();
+  if ((rc = check_stage(launch_preprocess(p, s), "preprocess", rs->debug, s))) return rc;
+  tm.end(NEST_STAGE_PREPROCESS);
+  tm.begin();
+  uint32_t* offs = reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_OFFSETS]);
+  void* scan_ws = g + off[NEST_GEOM_SCAN_TMP];
+  if ((rc = check_stage(launch_scan_u32(p.tiles, offs, sp->P, scan_ws, s), "scan", rs->debug, s))) return rc;
+  tm.end(NEST_STAGE_SCAN);
+  // The scan leaves the 64-bit grand total after the per-block partials.
+  const int64_t nb = ((int64_t)sp->P + 4095) / 4096;
+  uint64_t total = 0;
+  hipError_t e = hipMemcpyAsync(&total, static_cast<uint64_t*>(scan_ws) + nb, sizeof(total), hipMemcpyDeviceToHost, s);
+  if (e != hipSuccess) return hip_fail(e, "num_rendered read-back");
+  e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "num_rendered read-back");
+  if (total > 0xffffffffull)
+    return fail(NEST_ERR_OVERFLOW, "%llu tile/splat pairs exceed the 32-bit offsets of the binning stage",
+                (unsigned long long)total);
+  *num_rendered = (int64_t)total;
+  return NEST_OK;
+}
+
+int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr, const nest_splats* sp, void* geom_ws,
+                        size_t geom_bytes, void* binning_ws, size_t binning_bytes, void* image_ws, size_t image_bytes,
+                        int64_t NR, const nest_frame_outputs* out, nest_timing* timing, void* stream) {
+  int rc = check_settings(rs);
+  if (rc) return rc;
+  if ((rc = check_splats(sp, false))) return rc;
+  if (!gr || gr->struct_size != sizeof(nest_hashgrid))
+    return fail(NEST_ERR_INVALID_ARGUMENT, "nest_hashgrid missing or struct_size mismatch");
+  if (!out || out->struct_size != sizeof(nest_frame_outputs))
+    return fail(NEST_ERR_INVALID_ARGUMENT, "nest_frame_outputs missing or struct_size mismatch");
+  if (!out->out_color || !out->out_others) return fail(NEST_ERR_INVALID_ARGUMENT, "out_color and out_others are required");
+  if (out->channels < 1 || out->channels > NEST_MAX_CHANNELS)
+    return fail(NEST_ERR_UNSUPPORTED, "out_color channels must be in [1, %d] (got %d)", NEST_MAX_CHANNELS, out->channels);
+  if (NR < 0 || NR > 0xffffffffll) return fail(NEST_ERR_INVALID_ARGUMENT, "num_rendered out of range");
+  const int W = rs->image_width, H = rs->image_height;
+  const uint32_t gx = (uint32_t)((W + kTile - 1) / kTile), gy = (uint32_t)((H + kTile - 1) / kTile);
+  const uint32_t ntiles = gx * gy;
+
+  RenderParams rp{};
+  rp.W = W;
+  rp.H = H;
+  rp.gx = gx;
+  rp.gy = gy;
+  rp.ntiles = ntiles;
+  rp.C = out->channels;
+  rp.level = (int)gr->levels;
+  rp.beta = rs->beta;
+  rp.max_intersections = rs->max_intersections;
+  if (gr->levels > 0) {
+    if (gr->level_dim != 1 && gr->level_dim != 2 && gr->level_dim != 4 && gr->level_dim != 8)
+      return fail(NEST_ERR_UNSUPPORTED, "level_dim must be 1, 2, 4 or 8 (got %u)", gr->level_dim);
+    if (gr->levels > NEST_MAX_LEVELS || gr->levels * gr->level_dim > NEST_MAX_CHANNELS)
+      return fail(NEST_ERR_UNSUPPORTED, "levels*level_dim must be <= %d (got %u*%u)", NEST_MAX_CHANNELS, gr->levels,
+                  gr->level_dim);
+    if ((uint32_t)out->channels < gr->levels * gr->level_dim)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "out_color has %d channels, the hash grid produces %u", out->channels,
+                  gr->levels * gr->level_dim);
+    if (gr->table_dtype != NEST_DTYPE_F32 && gr->table_dtype != NEST_DTYPE_F16)
+      return fail(NEST_ERR_UNSUPPORTED, "hash table dtype must be float32 or float16");
+    if (gr->interpolation != 0 && gr->interpolation != 1)
+      return fail(NEST_ERR_UNSUPPORTED, "interpolation must be 0 (linear) or 1 (smoothstep)");
+    if (!gr->table) return fail(NEST_ERR_INVALID_ARGUMENT, "hash table pointer is NULL");
+    if (gr->offsets[gr->levels] > gr->table_rows)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "hash table has %lld rows, offsets[%u] = %d", (long long)gr->table_rows,
+                  gr->levels, gr->offsets[gr->levels]);
+    if (!(gr->gridrange[1] > gr->gridrange[0])) return fail(NEST_ERR_INVALID_ARGUMENT, "gridrange must satisfy min < max");
+    if (sp->P > 0 && !sp->homotrans) return fail(NEST_ERR_INVALID_ARGUMENT, "homotrans is required on the hash path");
+    if ((rc = build_levels(gr->offsets, gr->levels, gr->log2_scale, gr->base_resolution, gr->align_corners != 0, 3, true,
+                           rp.grid.lv)))
+      return rc;
+    GridParams& g = rp.grid;
+    g.L = gr->levels;
+    g.F = gr->level_dim;
+    g.interp = (uint32_t)gr->interpolation;
+    g.contract = rs->if_contract ? 1u : 0u;
+    g.vmin = gr->gridrange[0];
+    g.vmax = gr->gridrange[1];
+    if (!g.contract) {
+      g.inv_size = 1.0f / (g.vmax - g.vmin);
+      g.vmid = 0.0f;
+    } else {
+      g.vmid = (g.vmax + g.vmin) * 0.5f;
+      g.inv_size = 1.0f / ((g.vmax - g.vmin) * 0.5f);
+    }
+    g.pos_offset = gr->align_corners ? 0.0f : 0.5f;
+    g.half = gr->table_dtype == NEST_DTYPE_F16 ? 1u : 0u;
+    g.table = gr->table;
+  } else {
+    if (sp->P > 0 && !sp->colors_precomp)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "levels == 0 selects the colour path, which needs colors_precomp");
+  }
+
+  size_t go[NEST_GEOM_FIELDS], gneed = 0, bo[NEST_BIN_FIELDS], bneed = 0, io[NEST_IMG_FIELDS], ineed = 0;
+  nest_geom_layout(sp->P, go, &gneed);
+  nest_binning_layout(NR, bo, &bneed);
+  nest_image_layout(W, H, io, &ineed);
+  if (!geom_ws || geom_bytes < gneed)
+    return fail(NEST_ERR_WORKSPACE, "geometry workspace too small: %zu bytes given, %zu needed", geom_bytes, gneed);
+  if (NR > 0 && (!binning_ws || binning_bytes < bneed))
+    return fail(NEST_ERR_WORKSPACE, "binning workspace too small: %zu bytes given, %zu needed", binning_bytes, bneed);
+  if (!image_ws || image_bytes < ineed)
+    return fail(NEST_ERR_WORKSPACE, "image workspace too small: %zu bytes given, %zu needed", image_bytes, ineed);
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* g = static_cast<char*>(geom_ws);
+  char* b = static_cast<char*>(binning_ws);
+  char* im = static_cast<char*>(image_ws);
+  uint32_t* ranges = reinterpret_cast<uint32_t*>(im + io[NEST_IMG_RANGES]);
+  StageTimer tm(timing, s);
+
+  uint64_t* keys_u = nullptr;
+  uint32_t* vals_u = nullptr;
+  uint64_t* keys = nullptr;
+  uint32_t* vals = nullptr;
+  if (NR > 0) {
+    keys_u = reinterpret_cast<uint64_t*>(b + bo[NEST_BIN_KEYS_UNSORTED]);
+    vals_u = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_VALS_UNSORTED]);
+    keys = reinterpret_cast<uint64_t*>(b + bo[NEST_BIN_KEYS]);
+    vals = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_VALS]);
+    tm.begin();
+    rc = check_stage(launch_duplicate(sp->P, nullptr, reinterpret_cast<const float*>(g + go[NEST_GEOM_XY]),
+                                      reinterpret_cast<const float*>(g + go[NEST_GEOM_DEPTH]),
+                                      reinterpret_cast<const int32_t*>(g + go[NEST_GEOM_RADII]),
+                                      reinterpret_cast<const uint32_t*>(g + go[NEST_GEOM_OFFSETS]), gx, gy, keys_u, vals_u, s),
+                     "duplicate", rs->debug, s);
+    if (rc) return rc;
+    tm.end(NEST_STAGE_DUPLICATE);
+    tm.begin();
+    const int bit = (int)higher_msb(ntiles);
+    rc = check_stage(launch_sort_pairs(keys_u, vals_u, keys, vals, NR, 32 + bit, b + bo[NEST_BIN_SORT_TMP], s), "sort",
+                     rs->debug, s);
+    if (rc) return rc;
+    tm.end(NEST_STAGE_SORT);
+  }
+  tm.begin();
+  if ((rc = check_stage(launch_tile_ranges(keys, NR, ranges, ntiles, s), "tile ranges", rs->debug, s))) return rc;
+  tm.end(NEST_STAGE_RANGES);
+
+  rp.ranges = ranges;
+  rp.point_list = vals;
+  rp.records = reinterpret_cast<const float*>(g + go[NEST_GEOM_RECORDS]);
+  rp.colors = sp->colors_precomp;
+  rp.out_color = out->out_color;
+  rp.out_others = out->out_others;
+  rp.final_T = reinterpret_cast<float*>(im + io[NEST_IMG_FINAL_T]);
+  rp.n_contrib = reinterpret_cast<uint32_t*>(im + io[NEST_IMG_N_CONTRIB]);
+  tm.begin();
+  if ((rc = check_stage(launch_render(rp, s), "render", rs->debug, s))) return rc;
+  tm.end(NEST_STAGE_RENDER);
+  return NEST_OK;
+}
+
+size_t nest_scan_workspace_size(int64_t n) { return scan_ws_bytes(n > 0 ? n : 1); }
+
+int nest_inclusive_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* ws, size_t ws_bytes, void* stream) {
+  if (n < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "n must be >= 0");
+  if (n == 0) return NEST_OK;
+  if (!in || !out) return fail(NEST_ERR_INVALID_ARGUMENT, "in/out is NULL");
+  if (!ws || ws_bytes < scan_ws_bytes(n))
+    return fail(NEST_ERR_WORKSPACE, "scan workspace too small: %zu bytes given, %zu needed", ws_bytes, scan_ws_bytes(n));
+  hipError_t e = launch_scan_u32(in, out, n, ws, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? NEST_OK : hip_fail(e, "scan");
+}
+
+size_t nest_sort_workspace_size(int64_t n) { return sort_ws_bytes(n > 0 ? n : 1); }
+
+int nest_sort_pairs_u64(const uint64_t* keys_in, const uint32_t* vals_in, uint64_t* keys_out, uint32_t* vals_out,
+                        int64_t n, int32_t end_bit, void* ws, size_t ws_bytes, void* stream) {
+  if (n < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "n must be >= 0");
+  if (end_bit < 1 || end_bit > 64) return fail(NEST_ERR_INVALID_ARGUMENT, "end_bit must be in [1, 64]");
+  if (n == 0) return NEST_OK;
+  if (n > 0xffffffffll) return fail(NEST_ERR_UNSUPPORTED, "at most 2^32-1 pairs");
+  if (!keys_in || !vals_in || !keys_out || !vals_out) return fail(NEST_ERR_INVALID_ARGUMENT, "NULL key/value pointer");
+  if (!ws || ws_bytes < sort_ws_bytes(n))
+    return fail(NEST_ERR_WORKSPACE, "sort workspace too small: %zu bytes given, %zu needed", ws_bytes, sort_ws_bytes(n));
+  hipError_t e = launch_sort_pairs(const_cast<uint64_t*>(keys_in), const_cast<uint32_t*>(vals_in), keys_out, vals_out, n,
+                                   end_bit, ws, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? NEST_OK : hip_fail(e, "sort");
+}
+
+int nest_grid_encode(const float* inputs, int64_t B, int32_t D, const void* embeddings, int64_t emb_rows, int32_t emb_dtype,
+                     const int32_t* offsets_host, int32_t L, int32_t C, float S, int32_t H, int32_t gridtype,
+                     int32_t align_corners, int32_t interpolation, void* outputs, void* stream) {
+  if (B < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "B must be >= 0");
+  if (D < 2 || D > 5) return fail(NEST_ERR_UNSUPPORTED, "GridEncoding: D must be 2, 3, 4 or 5 (got %d)", D);
+  if (C != 1 && C != 2 && C != 4 && C != 8 && C != 16)
+    return fail(NEST_ERR_UNSUPPORTED, "GridEncoding: C must be 1, 2, 4, 8 or 16 (got %d)", C);
+  if (L < 1 || L > NEST_MAX_LEVELS) return fail(NEST_ERR_UNSUPPORTED, "GridEncoding: L must be in [1, %d]", NEST_MAX_LEVELS);
+  if (emb_dtype != NEST_DTYPE_F32 && emb_dtype != NEST_DTYPE_F16)
+    return fail(NEST_ERR_UNSUPPORTED, "GridEncoding: embeddings must be float32 or float16");
+  if (gridtype != 0 && gridtype != 1) return fail(NEST_ERR_INVALID_ARGUMENT, "gridtype must be 0 (hash) or 1 (tiled)");
+  if (interpolation != 0 && interpolation != 1) return fail(NEST_ERR_INVALID_ARGUMENT, "interpolation must be 0 or 1");
+  if (!offsets_host) return fail(NEST_ERR_INVALID_ARGUMENT, "offsets is NULL");
+  if (offsets_host[L] > emb_rows)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "embeddings have %lld rows, offsets[%d] = %d", (long long)emb_rows, L, offsets_host[L]);
+  if (B == 0) return NEST_OK;
+  if (!inputs || !embeddings || !outputs) return fail(NEST_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  GridEncodeParams p{};
+  int rc = build_levels(offsets_host, (uint32_t)L, S, (uint32_t)H, align_corners != 0, D, gridtype == 0, p.lv);
+  if (rc) return rc;
+  p.inputs = inputs;
+  p.B = B;
+  p.D = D;
+  p.C = C;
+  p.L = L;
+  p.gridtype = gridtype;
+  p.align_corners = align_corners;
+  p.interp = interpolation;
+  p.half = emb_dtype == NEST_DTYPE_F16;
+  p.table = embeddings;
+  p.outputs = outputs;
+  hipError_t e = launch_grid_encode(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? NEST_OK : hip_fail(e, "grid_encode");
+}
+
+int nest_mlp_decode(const nest_mlp* mlp, const float* feat, int64_t feat_cs, int64_t feat_ns, int64_t N, int32_t width,
+                    const float* dirs, const float ray_matrix[9], const float* alpha, const float bg[3], float* out,
+                    int64_t out_os, int64_t out_ns, void* stream) {
+  if (!mlp || mlp->struct_size != sizeof(nest_mlp)) return fail(NEST_ERR_INVALID_ARGUMENT, "nest_mlp missing or struct_size mismatch");
+  if (N < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "N must be >= 0");
+  if (mlp->in_features < 1 || mlp->in_features > NEST_MAX_CHANNELS)
+    return fail(NEST_ERR_UNSUPPORTED, "in_features must be in [1, %d]", NEST_MAX_CHANNELS);
+  const int dt = mlp->dtype;
+  if (dt != NEST_DTYPE_F32 && dt != NEST_DTYPE_F16 && dt != NEST_DTYPE_BF16)
+    return fail(NEST_ERR_UNSUPPORTED, "MLP dtype must be float32, float16 or bfloat16");
+  if (dt == NEST_DTYPE_F32) {
+    if (mlp->width != 16 && mlp->width != 32 && mlp->width != 64)
+      return fail(NEST_ERR_UNSUPPORTED, "float32 MLP width must be 16, 32 or 64 (got %d)", mlp->width);
+  } else {
+    if (mlp->width != 32 && mlp->width != 64 && mlp->width != 128)
+      return fail(NEST_ERR_UNSUPPORTED, "MFMA MLP width must be 32, 64 or 128 (got %d)", mlp->width);
+    if (mlp->in_features % 16 != 0)
+      return fail(NEST_ERR_UNSUPPORTED, "MFMA MLP needs in_features to be a multiple of 16 (got %d)", mlp->in_features);
+  }
+  if (!dirs && (!ray_matrix || width <= 0))
+    return fail(NEST_ERR_INVALID_ARGUMENT, "either dirs or ray_matrix with the image width is required");
+  if (N == 0) return NEST_OK;
+  if (!feat || !out || !mlp->w1 || !mlp->w2 || !mlp->w3) return fail(NEST_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  MlpParams p{};
+  p.C = mlp->in_features;
+  p.width = mlp->width;
+  p.dtype = dt;
+  p.w1 = mlp->w1;
+  p.w2 = mlp->w2;
+  p.w3 = mlp->w3;
+  p.feat = feat;
+  p.feat_cs = feat_cs;
+  p.feat_ns = feat_ns;
+  p.N = N;
+  p.img_w = width > 0 ? width : 1;
+  p.dirs = dirs;
+  if (ray_matrix) memcpy(p.M, ray_matrix, sizeof(p.M));
+  p.alpha = alpha;
+  if (bg) {
+    memcpy(p.bg, bg, sizeof(p.bg));
+    p.use_bg = (bg[0] + bg[1] + bg[2]) > 0.0f;
+  }
+  p.out = out;
+  p.out_os = out_os;
+  p.out_ns = out_ns;
+  hipError_t e = launch_mlp(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? NEST_OK : hip_fail(e, "mlp_decode");
+}
+
+int nest_rvq_decode(int64_t P, int32_t stages, int32_t K, int32_t dim, const float* cb, const uint16_t* idx,
+                    const float* bias, int32_t activation, float* out, float* raw_out, void* stream) {
+  if (P < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "P must be >= 0");
+  if (stages < 1 || stages > 16) return fail(NEST_ERR_UNSUPPORTED, "stages must be in [1, 16]");
+  if (K < 1 || K > 65536) return fail(NEST_ERR_UNSUPPORTED, "codebook size must be in [1, 65536]");
+  if (dim != 1 && dim != 2 && dim != 3 && dim != 4 && dim != 8)
+    return fail(NEST_ERR_UNSUPPORTED, "dim must be 1, 2, 3, 4 or 8 (got %d)", dim);
+  if (activation < 0 || activation > 3) return fail(NEST_ERR_INVALID_ARGUMENT, "activation must be 0..3");
+  if (P == 0) return NEST_OK;
+  if (!cb || !idx || !out) return fail(NEST_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  RvqParams p{};
+  p.P = P;
+  p.stages = stages;
+  p.K = K;
+  p.dim = dim;
+  p.cb = cb;
+  p.idx = idx;
+  if (bias) {
+    for (int d = 0; d < dim; d++) p.bias[d] = bias[d];
+    p.has_bias = 1;
+  }
+  p.activation = activation;
+  p.out = out;
+  p.raw = raw_out;
+  hipError_t e = launch_rvq(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? NEST_OK : hip_fail(e, "rvq_decode");
+}
+
+}  // extern "C"

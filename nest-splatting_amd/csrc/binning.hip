@@ -1,0 +1,403 @@
+// Tile binning: inclusive scan of tiles touched, duplicate-with-keys, a stable
+// LSD radix sort of (tile << 32 | depth bits, splat id) pairs and per-tile
+// range identification.
+//
+// Semantics: CR/rasterizer_impl.cu:355 (cub::DeviceScan::InclusiveSum),
+// :70-111 (duplicateWithKeys), :35-50 + :381-386 (getHigherMsb +
+// cub::DeviceRadixSort::SortPairs on bits [0, 32+bit)), :173-195 + :388
+// (identifyTileRanges after a memset), with CR = submodules/
+// diff-surfel-rasterization/cuda_rasterizer.
+//
+// Sort design (gfx950, 64-lane waves): reduce-then-scan LSD radix with 8-bit
+// digits.  Each 256-thread block owns 4096 keys; a wave ranks its 1024 keys in
+// 16 rounds of 64 with eight ballots per round (multi-split by digit), keeping
+// the per-wave digit counters in LDS.  That gives a stable rank without LDS
+// atomics, and the (digit, block) offsets come from one device-wide exclusive
+// scan of the block histograms.  No kernel waits on another block, so there is
+// no inter-block spin.
+#include "nest_internal.h"
+#include "nest_math.h"
+
+namespace nest {
+
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 16;
+constexpr int kScanTile = kScanThreads * kScanItems;  // 4096
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// block scan helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint64_t wave_inclusive_scan_u64(uint64_t v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint64_t o = __shfl_up(v, d, kWave);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Exclusive scan of one value per thread over a 256-thread block; returns
+// the exclusive prefix and writes the block total to *total.
+__device__ __forceinline__ uint64_t block_exclusive_scan_u64(uint64_t v, uint64_t* total) {
+  __shared__ uint64_t wsum[kScanThreads / kWave];
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  const uint64_t inc = wave_inclusive_scan_u64(v);
+  if (lane == kWave - 1) wsum[wid] = inc;
+  __syncthreads();
+  uint64_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kScanThreads / kWave; w++) {
+    const uint64_t s = wsum[w];
+    if (w < wid) before += s;
+    all += s;
+  }
+  __syncthreads();
+  *total = all;
+  return before + inc - v;
+}
+
+// Pass 1: per-block totals (64-bit so an overflowing u32 total is detected).
+__global__ void __launch_bounds__(kScanThreads) scan_reduce_kernel(const uint32_t* __restrict__ in, int64_t n,
+                                                                  uint64_t* __restrict__ partial) {
+  const int64_t base = (int64_t)blockIdx.x * kScanTile;
+  uint64_t s = 0;
+#pragma unroll
+  for (int k = 0; k < kScanItems; k++) {
+    const int64_t i = base + (int64_t)k * kScanThreads + threadIdx.x;
+    if (i < n) s += in[i];
+  }
+  uint64_t total;
+  block_exclusive_scan_u64(s, &total);
+  if (threadIdx.x == 0) partial[blockIdx.x] = total;
+}
+
+// Pass 2: exclusive scan of the block totals in place, one block.  partial
+// has nb entries; partial[nb] receives the grand total.
+__global__ void __launch_bounds__(kScanThreads) scan_partials_kernel(uint64_t* __restrict__ partial, int64_t nb) {
+  const int64_t per = (nb + kScanThreads - 1) / kScanThreads;
+  const int64_t lo = (int64_t)threadIdx.x * per;
+  const int64_t hi = lo + per < nb ? lo + per : nb;
+  uint64_t s = 0;
+  for (int64_t i = lo; i < hi; i++) s += partial[i];
+  uint64_t total;
+  uint64_t run = block_exclusive_scan_u64(s, &total);
+  for (int64_t i = lo; i < hi; i++) {
+    const uint64_t v = partial[i];
+    partial[i] = run;
+    run += v;
+  }
+  if (threadIdx.x == 0) partial[nb] = total;
+}
+
+// LDS index with one pad word per 16, so that lane t reading its 16
+// consecutive items (stride 17 words) hits distinct banks.
+__device__ __forceinline__ int padded(int i) { return i + (i >> 4); }
+
+// Pass 3: rescan each tile of 4096 items with its block offset.  Items are
+// loaded coalesced (item k*256 + t), transposed through LDS so that each
+// thread scans 16 consecutive items, and stored coalesced again.
+template <bool kExclusive>
+__global__ void __launch_bounds__(kScanThreads) scan_down_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
+                                                                int64_t n, const uint64_t* __restrict__ partial) {
+  __shared__ uint32_t tile[kScanTile + kScanTile / 16];
+  const int64_t base = (int64_t)blockIdx.x * kScanTile;
+#pragma unroll
+  for (int k = 0; k < kScanItems; k++) {
+    const int idx = k * kScanThreads + threadIdx.x;
+    const int64_t i = base + idx;
+    tile[padded(idx)] = i < n ? in[i] : 0u;
+  }
+  __syncthreads();
+  uint32_t v[kScanItems];
+  uint64_t s = 0;
+#pragma unroll
+  for (int k = 0; k < kScanItems; k++) {
+    v[k] = tile[padded(threadIdx.x * kScanItems + k)];
+    s += v[k];
+  }
+  uint64_t total;
+  uint64_t run = block_exclusive_scan_u64(s, &total) + partial[blockIdx.x];
+#pragma unroll
+  for (int k = 0; k < kScanItems; k++) {
+    if (kExclusive) {
+      tile[padded(threadIdx.x * kScanItems + k)] = (uint32_t)run;
+      run += v[k];
+    } else {
+      run += v[k];
+      tile[padded(threadIdx.x * kScanItems + k)] = (uint32_t)run;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kScanItems; k++) {
+    const int idx = k * kScanThreads + threadIdx.x;
+    const int64_t i = base + idx;
+    if (i < n) out[i] = tile[padded(idx)];
+  }
+}
+
+size_t scan_ws_bytes(int64_t n) {
+  const int64_t nb = (n + kScanTile - 1) / kScanTile;
+  return (size_t)(nb + 1) * sizeof(uint64_t);
+}
+
+static hipError_t scan_impl(const uint32_t* in, uint32_t* out, int64_t n, void* ws, bool exclusive, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  const int64_t nb = (n + kScanTile - 1) / kScanTile;
+  uint64_t* partial = static_cast<uint64_t*>(ws);
+  hipLaunchKernelGGL(scan_reduce_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, n, partial);
+  hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, s, partial, nb);
+  if (exclusive)
+    hipLaunchKernelGGL(scan_down_kernel<true>, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n, partial);
+  else
+    hipLaunchKernelGGL(scan_down_kernel<false>, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n, partial);
+  return hipGetLastError();
+}
+
+hipError_t launch_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* ws, hipStream_t s) {
+  return scan_impl(in, out, n, ws, false, s);
+}
+
+// ---------------------------------------------------------------------------
+// fill, duplicate, ranges
+// ---------------------------------------------------------------------------
+
+__global__ void fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t value, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = value;
+}
+
+hipError_t launch_fill_u32(uint32_t* dst, uint32_t value, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst, value, n);
+  return hipGetLastError();
+}
+
+// duplicateWithKeys: one lane per splat, pairs emitted row-major over the
+// splat's tile rectangle at the splat's scanned offset.
+__global__ void __launch_bounds__(256) duplicate_kernel(int P, const float2* __restrict__ xy, const float* __restrict__ depth,
+                                                       const int32_t* __restrict__ radii, const uint32_t* __restrict__ offsets,
+                                                       uint32_t gx, uint32_t gy, uint64_t* __restrict__ keys,
+                                                       uint32_t* __restrict__ vals) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P) return;
+  const int r = radii[i];
+  if (r <= 0) return;
+  uint32_t off = (i == 0) ? 0u : offsets[i - 1];
+  const float2 c = xy[i];
+  uint32_t x0, y0, x1, y1;
+  tile_rect(c.x, c.y, r, gx, gy, x0, y0, x1, y1);
+  const uint64_t dbits = (uint64_t)__float_as_uint(depth[i]);
+  for (uint32_t y = y0; y < y1; y++)
+    for (uint32_t x = x0; x < x1; x++) {
+      keys[off] = ((uint64_t)(y * gx + x) << 32) | dbits;
+      vals[off] = (uint32_t)i;
+      off++;
+    }
+}
+
+hipError_t launch_duplicate(int P, const float* /*records*/, const float* xy, const float* depth, const int32_t* radii,
+                            const uint32_t* offsets, uint32_t gx, uint32_t gy, uint64_t* keys, uint32_t* vals,
+                            hipStream_t s) {
+  if (P <= 0) return hipSuccess;
+  hipLaunchKernelGGL(duplicate_kernel, dim3((P + 255) / 256), dim3(256), 0, s, P,
+                     reinterpret_cast<const float2*>(xy), depth, radii, offsets, gx, gy, keys, vals);
+  return hipGetLastError();
+}
+
+__global__ void tile_ranges_kernel(const uint64_t* __restrict__ keys, int64_t n, uint2* __restrict__ ranges) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t t = (uint32_t)(keys[i] >> 32);
+  if (i == 0) {
+    ranges[t].x = 0;
+  } else {
+    const uint32_t pt = (uint32_t)(keys[i - 1] >> 32);
+    if (t != pt) {
+      ranges[pt].y = (uint32_t)i;
+      ranges[t].x = (uint32_t)i;
+    }
+  }
+  if (i == n - 1) ranges[t].y = (uint32_t)n;
+}
+
+hipError_t launch_tile_ranges(const uint64_t* keys, int64_t n, uint32_t* ranges, uint32_t ntiles, hipStream_t s) {
+  hipError_t e = launch_fill_u32(ranges, 0u, 2 * (int64_t)ntiles, s);
+  if (e != hipSuccess || n <= 0) return e;
+  hipLaunchKernelGGL(tile_ranges_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, keys, n,
+                     reinterpret_cast<uint2*>(ranges));
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// radix sort
+// ---------------------------------------------------------------------------
+
+constexpr int kRadixBits = 8;
+constexpr int kRadix = 1 << kRadixBits;
+constexpr int kSortThreads = 256;
+constexpr int kSortRounds = 16;                          // rounds of 64 keys per wave
+constexpr int kSortWaves = kSortThreads / kWave;         // 4
+constexpr int kSortTile = kSortThreads * kSortRounds;    // 4096 keys per block
+
+// Lanes of the calling wave whose 8-bit digit equals d, restricted to 'valid'.
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t valid) {
+  uint64_t peers = valid;
+#pragma unroll
+  for (int b = 0; b < kRadixBits; b++) {
+    const uint64_t m = __ballot((d >> b) & 1u);
+    peers &= ((d >> b) & 1u) ? m : ~m;
+  }
+  return peers;
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int lane = threadIdx.x & (kWave - 1);
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Per-block digit histogram, written digit-major: counts[d * nblocks + b].
+__global__ void __launch_bounds__(kSortThreads) radix_hist_kernel(const uint64_t* __restrict__ keys, int64_t n, int shift,
+                                                                 uint32_t* __restrict__ counts, uint32_t nblocks) {
+  __shared__ uint32_t hist[kSortWaves][kRadix];
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&hist[0][0])[i] = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)wid * (kWave * kSortRounds);
+  for (int r = 0; r < kSortRounds; r++) {
+    const int64_t i = base + r * kWave + lane;
+    const bool ok = i < n;
+    const uint32_t d = ok ? (uint32_t)(keys[i] >> shift) & (kRadix - 1) : 0u;
+    const uint64_t valid = __ballot(ok);
+    const uint64_t peers = match_digit(d, valid);
+    const int leader = __ffsll((unsigned long long)peers) - 1;
+    if (ok && lane == leader) hist[wid][d] += (uint32_t)__popcll(peers);
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < kRadix; d += kSortThreads) {
+    uint32_t s = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; w++) s += hist[w][d];
+    counts[(size_t)d * nblocks + blockIdx.x] = s;
+  }
+}
+
+// Stable scatter of one digit pass.  offsets is the exclusive scan of counts.
+__global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const uint64_t* __restrict__ keys_in,
+                                                                    const uint32_t* __restrict__ vals_in,
+                                                                    uint64_t* __restrict__ keys_out,
+                                                                    uint32_t* __restrict__ vals_out, int64_t n, int shift,
+                                                                    const uint32_t* __restrict__ offsets, uint32_t nblocks) {
+  __shared__ uint32_t hist[kSortWaves][kRadix];
+  __shared__ uint32_t gbase[kRadix];
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&hist[0][0])[i] = 0;
+  for (int d = threadIdx.x; d < kRadix; d += kSortThreads) gbase[d] = offsets[(size_t)d * nblocks + blockIdx.x];
+  __syncthreads();
+
+  const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)wid * (kWave * kSortRounds);
+  uint64_t key[kSortRounds];
+  uint32_t val[kSortRounds];
+  uint32_t rank[kSortRounds];
+#pragma unroll
+  for (int r = 0; r < kSortRounds; r++) {
+    const int64_t i = base + r * kWave + lane;
+    if (i < n) {
+      key[r] = keys_in[i];
+      val[r] = vals_in[i];
+    } else {
+      key[r] = 0;
+      val[r] = 0;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kSortRounds; r++) {
+    const int64_t i = base + r * kWave + lane;
+    const bool ok = i < n;
+    const uint32_t d = (uint32_t)(key[r] >> shift) & (kRadix - 1);
+    const uint64_t valid = __ballot(ok);
+    const uint64_t peers = match_digit(d, valid);
+    uint32_t before = 0;
+    if (ok) before = hist[wid][d];
+    rank[r] = before + (uint32_t)__popcll(peers & lanemask_lt());
+    const int leader = __ffsll((unsigned long long)peers) - 1;
+    if (ok && lane == leader) hist[wid][d] = before + (uint32_t)__popcll(peers);
+  }
+  __syncthreads();
+  if (threadIdx.x < kRadix) {
+    const int d = threadIdx.x;
+    uint32_t run = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; w++) {
+      const uint32_t c = hist[w][d];
+      hist[w][d] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kSortRounds; r++) {
+    const int64_t i = base + r * kWave + lane;
+    if (i < n) {
+      const uint32_t d = (uint32_t)(key[r] >> shift) & (kRadix - 1);
+      const uint32_t pos = gbase[d] + hist[wid][d] + rank[r];
+      keys_out[pos] = key[r];
+      vals_out[pos] = val[r];
+    }
+  }
+}
+
+static int64_t sort_blocks(int64_t n) { return (n + kSortTile - 1) / kSortTile; }
+
+// Workspace: ping-pong keys/vals, digit counts, scan partials.
+size_t sort_ws_bytes(int64_t n) {
+  const int64_t nb = sort_blocks(n);
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  const int64_t ncounts = (int64_t)kRadix * nb;
+  return al((size_t)n * 8) + al((size_t)n * 4) + 2 * al((size_t)ncounts * 4) + al(scan_ws_bytes(ncounts));
+}
+
+hipError_t launch_sort_pairs(uint64_t* keys_in, uint32_t* vals_in, uint64_t* keys_out, uint32_t* vals_out, int64_t n,
+                             int end_bit, void* ws, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  const int64_t nb = sort_blocks(n);
+  const int64_t ncounts = (int64_t)kRadix * nb;
+  char* w = static_cast<char*>(ws);
+  uint64_t* tk = reinterpret_cast<uint64_t*>(w);
+  w += al((size_t)n * 8);
+  uint32_t* tv = reinterpret_cast<uint32_t*>(w);
+  w += al((size_t)n * 4);
+  uint32_t* counts = reinterpret_cast<uint32_t*>(w);
+  w += al((size_t)ncounts * 4);
+  uint32_t* offs = reinterpret_cast<uint32_t*>(w);
+  w += al((size_t)ncounts * 4);
+  void* scan_ws = w;
+
+  int passes = (end_bit + kRadixBits - 1) / kRadixBits;
+  if (passes < 1) passes = 1;
+  const uint64_t* sk = keys_in;
+  const uint32_t* sv = vals_in;
+  for (int pass = 0; pass < passes; pass++) {
+    // choose destinations so that the last pass lands in *_out and the input
+    // buffers are never written
+    const bool to_out = ((passes - 1 - pass) % 2) == 0;
+    uint64_t* dk = to_out ? keys_out : tk;
+    uint32_t* dv = to_out ? vals_out : tv;
+    const int shift = pass * kRadixBits;
+    hipLaunchKernelGGL(radix_hist_kernel, dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, n, shift, counts,
+                       (uint32_t)nb);
+    hipError_t e = scan_impl(counts, offs, ncounts, scan_ws, true, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(radix_scatter_kernel, dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, sv, dk, dv, n, shift,
+                       offs, (uint32_t)nb);
+    sk = dk;
+    sv = dv;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace nest

@@ -1,0 +1,305 @@
+// View-direction MLP decode of the composited feature map.
+//
+// Semantics: INGP.get_color / rgb_decode (hash_encoder/modules.py:587-602):
+// x = [feature (C), SH16((d+1)/2)] -> ReLU(W1 x) -> ReLU(W2 .) -> W3 . (no
+// biases, HE:560-572) -> sigmoid -> first 3 outputs, then the mask and
+// background of gaussian_renderer/__init__.py:1013-1021.  View directions are
+// cam2rays (utils/point_utils.py:31-46) normalised, evaluated per pixel from a
+// 3x3 matrix so no ray buffer is read.  The SH basis is the degree-3 real SH
+// (16 terms) of the SphericalHarmonics encoding (HE:551-558), evaluated on
+// 2u-1 of the encoder input u = (d+1)/2.
+//
+// MFMA formulation (f16 / bf16, fp32 accumulate), one 64-lane wave per 16
+// pixels: every layer computes Y^T = W X^T with v_mfma_f32_16x16x16, A = the
+// weights (LDS, padded rows), B = the activations.  The accumulator layout of
+// 16x16x16 (lane l holds rows 4*(l/16)..+3 of column l%16) is exactly the B
+// operand layout of the next layer's K-chunk, so hidden activations never
+// leave registers: ReLU, round to 16 bits, feed.
+#include <hip/hip_fp16.h>
+
+#include "nest_internal.h"
+#include "nest_math.h"
+
+namespace nest {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint16_t to_bf16_rne(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x7fffffu)) return (uint16_t)((x | 0x400000u) >> 16);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+
+__device__ __forceinline__ uint16_t to_f16_rne(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+template <bool kBF16>
+__device__ __forceinline__ uint16_t to16(float f) {
+  if constexpr (kBF16) return to_bf16_rne(f);
+  else return to_f16_rne(f);
+}
+
+template <bool kBF16>
+__device__ __forceinline__ f32x4 mfma16(uint2 a, uint2 b, f32x4 c) {
+  if constexpr (kBF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ uint2 pack4(uint16_t a, uint16_t b, uint16_t c, uint16_t d) {
+  return make_uint2((uint32_t)a | ((uint32_t)b << 16), (uint32_t)c | ((uint32_t)d << 16));
+}
+
+// SH16 of the unit direction d, computed on x = 2u - 1 with u = (d + 1) / 2.
+__device__ __forceinline__ void sh16(float dx, float dy, float dz, float o[16]) {
+  const float ux = (dx + 1.0f) / 2.0f, uy = (dy + 1.0f) / 2.0f, uz = (dz + 1.0f) / 2.0f;
+  const float x = ux * 2.0f - 1.0f, y = uy * 2.0f - 1.0f, z = uz * 2.0f - 1.0f;
+  const float xy = x * y, xz = x * z, yz = y * z, x2 = x * x, y2 = y * y, z2 = z * z;
+  o[0] = 0.28209479177387814f;
+  o[1] = -0.48860251190291987f * y;
+  o[2] = 0.48860251190291987f * z;
+  o[3] = -0.48860251190291987f * x;
+  o[4] = 1.0925484305920792f * xy;
+  o[5] = -1.0925484305920792f * yz;
+  o[6] = 0.94617469575755997f * z2 - 0.31539156525251999f;
+  o[7] = -1.0925484305920792f * xz;
+  o[8] = 0.54627421529603959f * x2 - 0.54627421529603959f * y2;
+  o[9] = 0.59004358992664352f * y * (-3.0f * x2 + y2);
+  o[10] = 2.8906114426405538f * xy * z;
+  o[11] = 0.45704579946446572f * y * (1.0f - 5.0f * z2);
+  o[12] = 0.3731763325901154f * z * (5.0f * z2 - 3.0f);
+  o[13] = 0.45704579946446572f * x * (1.0f - 5.0f * z2);
+  o[14] = 1.4453057213202769f * z * (x2 - y2);
+  o[15] = 0.59004358992664352f * x * (-x2 + 3.0f * y2);
+}
+
+__device__ __forceinline__ void pixel_dir(const MlpParams& p, int64_t n, float& dx, float& dy, float& dz) {
+  if (p.dirs) {
+    dx = p.dirs[3 * n + 0];
+    dy = p.dirs[3 * n + 1];
+    dz = p.dirs[3 * n + 2];
+    return;
+  }
+  const float x = (float)(n % p.img_w), y = (float)(n / p.img_w);
+  const float* M = p.M;
+  const float rx = x * M[0] + y * M[3] + M[6];
+  const float ry = x * M[1] + y * M[4] + M[7];
+  const float rz = x * M[2] + y * M[5] + M[8];
+  const float len = fmaxf(sqrtf(rx * rx + ry * ry + rz * rz), 1e-12f);
+  dx = rx / len;
+  dy = ry / len;
+  dz = rz / len;
+}
+
+__device__ __forceinline__ float finish_rgb(const MlpParams& p, int64_t n, float logit, int o) {
+  float r = 1.0f / (1.0f + expf_ref(-logit));
+  if (p.alpha) {
+    const float a = p.alpha[n];
+    r = a > 0.0f ? r : 0.0f;
+    if (p.use_bg) r = r + (1.0f - a) * p.bg[o];
+  }
+  return r;
+}
+
+constexpr int kMlpThreads = 256;
+
+// NT = width / 16.  KC1 = ceil((C + 16) / 16) K-chunks in layer 1.
+template <int NT, bool kBF16>
+__global__ void __launch_bounds__(kMlpThreads) mlp_mfma_kernel(const MlpParams p) {
+  extern __shared__ uint16_t lds[];
+  const int C = p.C;
+  const int KC1 = (C + 16 + 15) / 16;
+  const int ld1 = KC1 * 16 + 4, ld2 = NT * 16 + 4, ld3 = NT * 16 + 4;
+  uint16_t* w1 = lds;
+  uint16_t* w2 = w1 + NT * 16 * ld1;
+  uint16_t* w3 = w2 + NT * 16 * ld2;
+  const int Kin = C + 16;
+  const uint16_t* g1 = static_cast<const uint16_t*>(p.w1);
+  const uint16_t* g2 = static_cast<const uint16_t*>(p.w2);
+  const uint16_t* g3 = static_cast<const uint16_t*>(p.w3);
+  for (int i = threadIdx.x; i < NT * 16 * ld1; i += kMlpThreads) {
+    const int r = i / ld1, k = i % ld1;
+    w1[i] = k < Kin ? g1[r * Kin + k] : (uint16_t)0;
+  }
+  for (int i = threadIdx.x; i < NT * 16 * ld2; i += kMlpThreads) {
+    const int r = i / ld2, k = i % ld2;
+    w2[i] = k < NT * 16 ? g2[r * NT * 16 + k] : (uint16_t)0;
+  }
+  for (int i = threadIdx.x; i < 16 * ld3; i += kMlpThreads) {
+    const int r = i / ld3, k = i % ld3;
+    w3[i] = (r < 3 && k < NT * 16) ? g3[r * NT * 16 + k] : (uint16_t)0;
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int64_t ntile = (p.N + 15) / 16;
+  const int64_t wave = (int64_t)blockIdx.x * (kMlpThreads / 64) + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * (kMlpThreads / 64);
+
+  for (int64_t t = wave; t < ntile; t += nwaves) {
+    const int64_t n = t * 16 + col;
+    const bool valid = n < p.N;
+    const int64_t nn = valid ? n : p.N - 1;
+
+    float dx, dy, dz;
+    pixel_dir(p, nn, dx, dy, dz);
+    float sh[16];
+    sh16(dx, dy, dz, sh);
+
+    f32x4 acc1[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++) acc1[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kc = 0; kc < KC1; kc++) {
+      float xv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int k = kc * 16 + grp * 4 + i;
+        if (k < C) {
+          xv[i] = p.feat[(int64_t)k * p.feat_cs + nn * p.feat_ns];
+        } else {
+          const int s = k - C;
+          float v = 0.0f;
+#pragma unroll
+          for (int q = 0; q < 16; q++) v = (s == q) ? sh[q] : v;
+          xv[i] = v;
+        }
+      }
+      const uint2 b = pack4(to16<kBF16>(xv[0]), to16<kBF16>(xv[1]), to16<kBF16>(xv[2]), to16<kBF16>(xv[3]));
+#pragma unroll
+      for (int nt = 0; nt < NT; nt++) {
+        const uint2 a = *reinterpret_cast<const uint2*>(w1 + (nt * 16 + col) * ld1 + kc * 16 + grp * 4);
+        acc1[nt] = mfma16<kBF16>(a, b, acc1[nt]);
+      }
+    }
+    uint2 h1[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++)
+      h1[i] = pack4(to16<kBF16>(fmaxf(acc1[i][0], 0.f)), to16<kBF16>(fmaxf(acc1[i][1], 0.f)),
+                    to16<kBF16>(fmaxf(acc1[i][2], 0.f)), to16<kBF16>(fmaxf(acc1[i][3], 0.f)));
+    f32x4 acc2[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++) acc2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < NT; kc++) {
+#pragma unroll
+      for (int nt = 0; nt < NT; nt++) {
+        const uint2 a = *reinterpret_cast<const uint2*>(w2 + (nt * 16 + col) * ld2 + kc * 16 + grp * 4);
+        acc2[nt] = mfma16<kBF16>(a, h1[kc], acc2[nt]);
+      }
+    }
+    f32x4 acc3 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < NT; kc++) {
+      const uint2 h2 = pack4(to16<kBF16>(fmaxf(acc2[kc][0], 0.f)), to16<kBF16>(fmaxf(acc2[kc][1], 0.f)),
+                             to16<kBF16>(fmaxf(acc2[kc][2], 0.f)), to16<kBF16>(fmaxf(acc2[kc][3], 0.f)));
+      const uint2 a = *reinterpret_cast<const uint2*>(w3 + col * ld3 + kc * 16 + grp * 4);
+      acc3 = mfma16<kBF16>(a, h2, acc3);
+    }
+    if (grp == 0 && valid) {
+#pragma unroll
+      for (int o = 0; o < 3; o++) p.out[o * p.out_os + n * p.out_ns] = finish_rgb(p, n, acc3[o], o);
+    }
+  }
+}
+
+// float32 path on the vector ALU: one lane per pixel, weights in LDS.
+template <int NW>
+__global__ void __launch_bounds__(kMlpThreads) mlp_f32_kernel(const MlpParams p) {
+  extern __shared__ float wl[];
+  const int C = p.C, Kin = C + 16;
+  float* w1 = wl;
+  float* w2 = w1 + NW * Kin;
+  float* w3 = w2 + NW * NW;
+  const float* g1 = static_cast<const float*>(p.w1);
+  const float* g2 = static_cast<const float*>(p.w2);
+  const float* g3 = static_cast<const float*>(p.w3);
+  for (int i = threadIdx.x; i < NW * Kin; i += kMlpThreads) w1[i] = g1[i];
+  for (int i = threadIdx.x; i < NW * NW; i += kMlpThreads) w2[i] = g2[i];
+  for (int i = threadIdx.x; i < 3 * NW; i += kMlpThreads) w3[i] = g3[i];
+  __syncthreads();
+  for (int64_t n = (int64_t)blockIdx.x * kMlpThreads + threadIdx.x; n < p.N; n += (int64_t)gridDim.x * kMlpThreads) {
+    float dx, dy, dz;
+    pixel_dir(p, n, dx, dy, dz);
+    float sh[16];
+    sh16(dx, dy, dz, sh);
+    float h1[NW];
+#pragma unroll
+    for (int j = 0; j < NW; j++) h1[j] = 0.0f;
+    for (int k = 0; k < C; k++) {
+      const float xk = p.feat[(int64_t)k * p.feat_cs + n * p.feat_ns];
+#pragma unroll
+      for (int j = 0; j < NW; j++) h1[j] += w1[j * Kin + k] * xk;
+    }
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+#pragma unroll
+      for (int j = 0; j < NW; j++) h1[j] += w1[j * Kin + C + s] * sh[s];
+    }
+#pragma unroll
+    for (int j = 0; j < NW; j++) h1[j] = fmaxf(h1[j], 0.0f);
+    float o0 = 0.f, o1 = 0.f, o2 = 0.f;
+    for (int j = 0; j < NW; j++) {
+      float h = 0.0f;
+#pragma unroll
+      for (int k = 0; k < NW; k++) h += w2[j * NW + k] * h1[k];
+      h = fmaxf(h, 0.0f);
+      o0 += w3[j] * h;
+      o1 += w3[NW + j] * h;
+      o2 += w3[2 * NW + j] * h;
+    }
+    p.out[0 * p.out_os + n * p.out_ns] = finish_rgb(p, n, o0, 0);
+    p.out[1 * p.out_os + n * p.out_ns] = finish_rgb(p, n, o1, 1);
+    p.out[2 * p.out_os + n * p.out_ns] = finish_rgb(p, n, o2, 2);
+  }
+}
+
+template <int NT, bool kBF16>
+static hipError_t launch_mfma(const MlpParams& p, hipStream_t s) {
+  const int KC1 = (p.C + 16 + 15) / 16;
+  const size_t lds = sizeof(uint16_t) * ((size_t)NT * 16 * (KC1 * 16 + 4) + (size_t)NT * 16 * (NT * 16 + 4) +
+                                         16 * (size_t)(NT * 16 + 4));
+  const int64_t ntile = (p.N + 15) / 16;
+  const int64_t want = (ntile + 3) / 4;
+  const unsigned blocks = (unsigned)(want < 2048 ? (want > 0 ? want : 1) : 2048);
+  hipLaunchKernelGGL((mlp_mfma_kernel<NT, kBF16>), dim3(blocks), dim3(kMlpThreads), lds, s, p);
+  return hipGetLastError();
+}
+
+template <int NW>
+static hipError_t launch_f32(const MlpParams& p, hipStream_t s) {
+  const size_t lds = sizeof(float) * ((size_t)NW * (p.C + 16) + (size_t)NW * NW + 3 * (size_t)NW);
+  const int64_t want = (p.N + kMlpThreads - 1) / kMlpThreads;
+  const unsigned blocks = (unsigned)(want < 2048 ? (want > 0 ? want : 1) : 2048);
+  hipLaunchKernelGGL(mlp_f32_kernel<NW>, dim3(blocks), dim3(kMlpThreads), lds, s, p);
+  return hipGetLastError();
+}
+
+template <bool kBF16>
+static hipError_t launch_mfma_width(const MlpParams& p, hipStream_t s) {
+  switch (p.width) {
+    case 32: return launch_mfma<2, kBF16>(p, s);
+    case 64: return launch_mfma<4, kBF16>(p, s);
+    case 128: return launch_mfma<8, kBF16>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_mlp(const MlpParams& p, hipStream_t s) {
+  if (p.N <= 0) return hipSuccess;
+  if (p.dtype == NEST_DTYPE_F32) {
+    switch (p.width) {
+      case 16: return launch_f32<16>(p, s);
+      case 32: return launch_f32<32>(p, s);
+      case 64: return launch_f32<64>(p, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  return p.dtype == NEST_DTYPE_BF16 ? launch_mfma_width<true>(p, s) : launch_mfma_width<false>(p, s);
+}
+
+}  // namespace nest

@@ -1,0 +1,159 @@
+// Launch parameters shared between the C ABI (abi.cpp) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/nest_splat.h"
+
+namespace nest {
+
+constexpr int kTile = 16;               // 16x16 pixel tiles (CR/config.h:17-18)
+constexpr int kRecordFloats = 32;       // packed per-splat render record, 128 B
+
+// Packed render record (float index within the 32-float record):
+//   0..2 Tu   3..5 Tv   6..8 Tw   9..10 xy   11 opacity
+//  12..14 normal   15 appearance level (uint32 bits, floor(ap_level))
+//  16..18 SuTu (homotrans col 0)   19..21 SvTv (col 1)   22..24 pk (col 3)
+//  25 depth   26..31 unused
+enum RecordField {
+  kRecTu = 0, kRecTv = 3, kRecTw = 6, kRecXY = 9, kRecOpacity = 11,
+  kRecNormal = 12, kRecAp = 15, kRecSu = 16, kRecSv = 19, kRecPk = 22, kRecDepth = 25
+};
+
+struct PreprocessParams {
+  int P;
+  int W, H;
+  uint32_t gx, gy;
+  float scale_mod;
+  float view[16];
+  float proj[16];
+  const float* means;
+  const float* scales;
+  const float* rots;
+  const float* opac;
+  const float* homotrans;   // may be null (colour path)
+  const float* ap_level;    // may be null
+  // outputs
+  int32_t* radii;
+  int32_t* radii_user;      // optional second copy (the caller's radii tensor)
+  float* xy;
+  float* depth;
+  uint32_t* tiles;
+  float* records;
+};
+
+// Per-level constants of the hash grid, computed on the host in the same
+// float order as the reference's query_feature (CR/hashgrid.h:122-131).
+struct LevelTable {
+  float scale[NEST_MAX_LEVELS];
+  uint32_t res1[NEST_MAX_LEVELS];      // resolution + 1 (or resolution if align_corners)
+  uint32_t hsize[NEST_MAX_LEVELS];     // offsets[l+1] - offsets[l]
+  uint32_t base[NEST_MAX_LEVELS];      // offsets[l] (entries, not floats)
+  uint32_t flags[NEST_MAX_LEVELS];     // bit0 hashed, bit1 power-of-two size, bits 2.. stride count
+};
+
+struct GridParams {
+  uint32_t L;           // levels queried
+  uint32_t F;
+  uint32_t interp;
+  uint32_t contract;
+  float vmin, vmax;
+  float inv_size;       // 1/(vmax-vmin) or 1/((vmax-vmin)*0.5) in contract mode
+  float vmid;
+  float pos_offset;     // 0.5 or 0 (align_corners)
+  uint32_t half;        // table entries are binary16
+  const void* table;
+  LevelTable lv;
+};
+
+struct RenderParams {
+  int W, H;
+  uint32_t gx, gy;
+  uint32_t ntiles;
+  int C;                 // out_color channels
+  int level;             // 0 colour path, >0 hash
+  float beta;
+  uint32_t max_intersections;
+  const uint32_t* ranges;     // [tiles][2]
+  const uint32_t* point_list;
+  const float* records;       // [P][32]
+  const float* colors;        // [P][C] colour path
+  float* out_color;
+  float* out_others;
+  float* final_T;
+  uint32_t* n_contrib;
+  GridParams grid;
+};
+
+// Host-side launchers (defined in the .hip files).  Each returns the
+// hipGetLastError() of its launches.
+hipError_t launch_preprocess(const PreprocessParams& p, hipStream_t s);
+hipError_t launch_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* ws, hipStream_t s);
+size_t scan_ws_bytes(int64_t n);
+hipError_t launch_duplicate(int P, const float* records_or_null, const float* xy, const float* depth,
+                            const int32_t* radii, const uint32_t* offsets, uint32_t gx, uint32_t gy,
+                            uint64_t* keys, uint32_t* vals, hipStream_t s);
+size_t sort_ws_bytes(int64_t n);
+// Sorts (keys_in, vals_in) into (keys_out, vals_out).  The inputs are used as
+// ping-pong buffers and are clobbered.
+hipError_t launch_sort_pairs(uint64_t* keys_in, uint32_t* vals_in, uint64_t* keys_out, uint32_t* vals_out,
+                             int64_t n, int end_bit, void* ws, hipStream_t s);
+hipError_t launch_tile_ranges(const uint64_t* keys, int64_t n, uint32_t* ranges, uint32_t ntiles, hipStream_t s);
+hipError_t launch_render(const RenderParams& p, hipStream_t s);
+hipError_t launch_fill_u32(uint32_t* dst, uint32_t value, int64_t n, hipStream_t s);
+
+struct GridEncodeParams {
+  const float* inputs;
+  int64_t B;
+  int D;
+  int C;                // features per level
+  int L;
+  int gridtype;
+  int align_corners;
+  int interp;
+  int half;
+  const void* table;
+  void* outputs;
+  LevelTable lv;
+};
+hipError_t launch_grid_encode(const GridEncodeParams& p, hipStream_t s);
+
+struct MlpParams {
+  int C;
+  int width;
+  int dtype;
+  const void* w1;
+  const void* w2;
+  const void* w3;
+  const float* feat;
+  int64_t feat_cs, feat_ns;
+  int64_t N;
+  int img_w;
+  const float* dirs;
+  float M[9];
+  const float* alpha;
+  float bg[3];
+  int use_bg;
+  float* out;
+  int64_t out_os, out_ns;
+};
+hipError_t launch_mlp(const MlpParams& p, hipStream_t s);
+
+struct RvqParams {
+  int64_t P;
+  int stages;
+  int K;
+  int dim;
+  const float* cb;
+  const uint16_t* idx;
+  float bias[8];
+  int has_bias;
+  int activation;
+  float* out;
+  float* raw;
+};
+hipError_t launch_rvq(const RvqParams& p, hipStream_t s);
+
+}  // namespace nest

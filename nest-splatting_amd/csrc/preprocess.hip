@@ -1,0 +1,137 @@
+// Splat preprocess: projection of 2D surfels, screen AABB, tiles touched, and
+// the packed 128-byte render record.
+//
+// Semantics: preprocessCUDA (CR/forward.cu:323-441) with compute_transmat
+// (:237-290), compute_aabb (:294-320), in_frustum / quat_to_rotmat / getRect
+// (CR/auxiliary.h:72-82, :190-240) -- CR = submodules/diff-surfel-rasterization/
+// cuda_rasterizer.  The SH->RGB evaluation of the reference is dead work on
+// the hash path and is not done here.
+//
+// One lane per splat; every input is read once with 4/8/16-byte loads and the
+// record is written as eight 16-byte stores (one 128-byte line per splat), so
+// the render kernel can stage a splat with a single line fetch.
+#include "nest_internal.h"
+#include "nest_math.h"
+
+namespace nest {
+
+__global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams p) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.P) return;
+
+  // Defaults for culled splats (CR/forward.cu:353-354).
+  p.radii[i] = 0;
+  if (p.radii_user) p.radii_user[i] = 0;
+  p.tiles[i] = 0;
+
+  const float px = p.means[3 * i + 0], py = p.means[3 * i + 1], pz = p.means[3 * i + 2];
+  const float* V = p.view;
+  const float vx = V[0] * px + V[4] * py + V[8] * pz + V[12];
+  const float vy = V[1] * px + V[5] * py + V[9] * pz + V[13];
+  const float vz = V[2] * px + V[6] * py + V[10] * pz + V[14];
+  if (vz <= 0.2f) return;  // near cull, CR/auxiliary.h:205
+
+  // quat_to_rotmat with rsqrtf -> 1/sqrtf (CR/auxiliary.h:218-240).
+  const float4 q = reinterpret_cast<const float4*>(p.rots)[i];
+  const float s = 1.0f / sqrtf(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+  const float w = q.x * s, x = q.y * s, y = q.z * s, z = q.w * s;
+  const float R00 = 1.f - 2.f * (y * y + z * z);
+  const float R01 = 2.f * (x * y + w * z);
+  const float R02 = 2.f * (x * z - w * y);
+  const float R10 = 2.f * (x * y - w * z);
+  const float R11 = 1.f - 2.f * (x * x + z * z);
+  const float R12 = 2.f * (y * z + w * x);
+  const float R20 = 2.f * (x * z + w * y);
+  const float R21 = 2.f * (y * z - w * x);
+  const float R22 = 1.f - 2.f * (x * x + y * y);
+  const float2 sc = reinterpret_cast<const float2*>(p.scales)[i];
+  const float s0 = p.scale_mod * sc.x, s1 = p.scale_mod * sc.y;
+  const float L00 = R00 * s0, L01 = R01 * s0, L02 = R02 * s0;  // column 0 of R*S
+  const float L10 = R10 * s1, L11 = R11 * s1, L12 = R12 * s1;  // column 1
+
+  // T = transpose(splat2world) * world2ndc * ndc2pix (CR/forward.cu:255-274)
+  const float* A = p.proj;
+  float M[3][4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    M[0][c] = L00 * A[c] + L01 * A[4 + c] + L02 * A[8 + c];
+    M[1][c] = L10 * A[c] + L11 * A[4 + c] + L12 * A[8 + c];
+    M[2][c] = px * A[c] + py * A[4 + c] + pz * A[8 + c] + A[12 + c];
+  }
+  const float hw = (float)p.W / 2.0f, hh = (float)p.H / 2.0f;
+  const float cw = (float)(p.W - 1) / 2.0f, ch = (float)(p.H - 1) / 2.0f;
+  float Tu[3], Tv[3], Tw[3];
+#pragma unroll
+  for (int r = 0; r < 3; r++) {
+    Tu[r] = M[r][0] * hw + M[r][3] * cw;
+    Tv[r] = M[r][1] * hh + M[r][3] * ch;
+    Tw[r] = M[r][3];
+  }
+
+  // View-space normal of the splat's third axis, normalised, facing the camera.
+  float nx = V[0] * R20 + V[4] * R21 + V[8] * R22;
+  float ny = V[1] * R20 + V[5] * R21 + V[9] * R22;
+  float nz = V[2] * R20 + V[6] * R21 + V[10] * R22;
+  const float nlen = sqrtf(nx * nx + ny * ny + nz * nz);
+  if (nlen > 1e-7f) { nx = nx / nlen; ny = ny / nlen; nz = nz / nlen; }
+  const float cosv = -(vx * nx + vy * ny + vz * nz);
+  if (cosv == 0.0f) return;
+  const float mul = cosv > 0.0f ? 1.0f : -1.0f;
+  nx = mul * nx; ny = mul * ny; nz = mul * nz;
+
+  // compute_aabb with cutoff 4.
+  const float cut2 = 16.0f;
+  const float d = cut2 * (Tw[0] * Tw[0]) + cut2 * (Tw[1] * Tw[1]) + -1.0f * (Tw[2] * Tw[2]);
+  if (d == 0.0f) return;
+  const float invd = 1.0f / d;
+  const float f0 = invd * cut2, f1 = invd * cut2, f2 = invd * -1.0f;
+  const float pimx = f0 * (Tu[0] * Tw[0]) + f1 * (Tu[1] * Tw[1]) + f2 * (Tu[2] * Tw[2]);
+  const float pimy = f0 * (Tv[0] * Tw[0]) + f1 * (Tv[1] * Tw[1]) + f2 * (Tv[2] * Tw[2]);
+  const float h0x = pimx * pimx - (f0 * (Tu[0] * Tu[0]) + f1 * (Tu[1] * Tu[1]) + f2 * (Tu[2] * Tu[2]));
+  const float h0y = pimy * pimy - (f0 * (Tv[0] * Tv[0]) + f1 * (Tv[1] * Tv[1]) + f2 * (Tv[2] * Tv[2]));
+  const float ex = sqrtf(fmaxf(1e-4f, h0x));
+  const float ey = sqrtf(fmaxf(1e-4f, h0y));
+  const float radius = ceilf(fmaxf(fmaxf(ex, ey), 4.0f * 0.707106f));
+  const int ir = f2i_sat(radius);
+
+  uint32_t x0, y0, x1, y1;
+  tile_rect(pimx, pimy, ir, p.gx, p.gy, x0, y0, x1, y1);
+  const uint32_t area = (x1 - x0) * (y1 - y0);
+  if (area == 0) return;
+
+  const float opacity = p.opac[i];
+  p.depth[i] = vz;
+  p.radii[i] = ir;
+  if (p.radii_user) p.radii_user[i] = ir;
+  reinterpret_cast<float2*>(p.xy)[i] = make_float2(pimx, pimy);
+  p.tiles[i] = area;
+
+  uint32_t ap = 0xffffffffu;
+  if (p.ap_level) ap = f2u_sat(floorf(p.ap_level[i]));
+  float su0 = 0.f, su1 = 0.f, su2 = 0.f, sv0 = 0.f, sv1 = 0.f, sv2 = 0.f, pk0 = 0.f, pk1 = 0.f, pk2 = 0.f;
+  if (p.homotrans) {
+    const float4* Hm = reinterpret_cast<const float4*>(p.homotrans) + 4 * (size_t)i;
+    const float4 r0 = Hm[0], r1 = Hm[1], r2 = Hm[2];
+    su0 = r0.x; su1 = r1.x; su2 = r2.x;
+    sv0 = r0.y; sv1 = r1.y; sv2 = r2.y;
+    pk0 = r0.w; pk1 = r1.w; pk2 = r2.w;
+  }
+  float4* rec = reinterpret_cast<float4*>(p.records) + 8 * (size_t)i;
+  rec[0] = make_float4(Tu[0], Tu[1], Tu[2], Tv[0]);
+  rec[1] = make_float4(Tv[1], Tv[2], Tw[0], Tw[1]);
+  rec[2] = make_float4(Tw[2], pimx, pimy, opacity);
+  rec[3] = make_float4(nx, ny, nz, __uint_as_float(ap));
+  rec[4] = make_float4(su0, su1, su2, sv0);
+  rec[5] = make_float4(sv1, sv2, pk0, pk1);
+  rec[6] = make_float4(pk2, vz, 0.f, 0.f);
+  rec[7] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+hipError_t launch_preprocess(const PreprocessParams& p, hipStream_t s) {
+  if (p.P <= 0) return hipSuccess;
+  const int blocks = (p.P + 255) / 256;
+  hipLaunchKernelGGL(preprocess_kernel, dim3(blocks), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace nest

@@ -1,0 +1,260 @@
+// Per-tile compositing of 2D surfels with an in-loop hash-grid lookup at every
+// accepted ray/splat hit.
+//
+// Semantics: renderCUDAsurfelForward<C, mode 0> of
+// submodules/diff-surfel-rasterization/cuda_rasterizer/forward.cu:639-2049
+// (state :719-785, batch fetch :791-831, intersection loop :834-971, case 0
+// :1127-1145, accumulation :1914-1916, appearance colour :1945-1957, output
+// :2008-2048), and query_feature (hashgrid.h:53-212).
+//
+// Layout: one 256-thread workgroup per 16x16 tile, one lane per pixel (four
+// 64-lane waves of 16x4 pixels).  The tile's sorted splats are staged in LDS in
+// batches of 256 packed records (7 x 16 B per splat, structure-of-arrays so a
+// wave reads a record with broadcast ds_read_b128).  Workgroup ids are mapped
+// to tiles so that each XCD renders one contiguous band of tiles, keeping the
+// hash-table and record lines of neighbouring tiles in the same L2.
+#include "hashgrid.h"
+#include "nest_internal.h"
+#include "nest_math.h"
+
+namespace nest {
+
+constexpr int kRenderThreads = 256;
+constexpr int kRecChunks = 7;  // float4 chunks of the record used by the render
+
+// Workgroup i runs on XCD i % 8; give XCD x a contiguous range of tiles.
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t i, uint32_t n) {
+  const uint32_t q = n >> 3, rem = n & 7u;
+  const uint32_t x = i & 7u, k = i >> 3;
+  const uint32_t start = x < rem ? x * (q + 1u) : rem * (q + 1u) + (x - rem) * q;
+  return start + k;
+}
+
+// NACC: accumulator channels held per lane.  HASH: hash path (NACC = NL*F) or
+// colour path (NACC >= C).
+template <int F, int NACC, bool kHash, bool kHalf>
+__global__ void __launch_bounds__(kRenderThreads) render_kernel(const RenderParams p) {
+  __shared__ float4 srec[kRecChunks][kRenderThreads];
+
+  const uint32_t tile = xcd_tile(blockIdx.x, p.ntiles);
+  const uint32_t tx = tile % p.gx, ty = tile / p.gx;
+  const uint32_t px = tx * kTile + (threadIdx.x & 15u);
+  const uint32_t py = ty * kTile + (threadIdx.x >> 4);
+  const bool inside = px < (uint32_t)p.W && py < (uint32_t)p.H;
+  const float pxf = (float)px, pyf = (float)py;
+  bool done = !inside;
+
+  const uint2 range = reinterpret_cast<const uint2*>(p.ranges)[tile];
+
+  float T = 1.0f;
+  uint32_t contributor = 0, last_contributor = 0, render_number = 0;
+  float acc[NACC];
+#pragma unroll
+  for (int c = 0; c < NACC; c++) acc[c] = 0.0f;
+  float N0 = 0.f, N1 = 0.f, N2 = 0.f, vis0 = 0.f, vis1 = 0.f, vis2 = 0.f;
+  float D = 0.f, M1 = 0.f, M2 = 0.f, distortion = 0.f, median_depth = 0.f, median_contributor = -1.0f;
+  float pos_x = 0.f, pos_y = 0.f, pos_z = 0.f;
+  const float mfac = 100.0f / (100.0f - 0.2f);
+
+  const GridParams& g = p.grid;
+  const uint32_t L = g.L;
+
+  for (uint32_t start = range.x; start < range.y; start += kRenderThreads) {
+    if (__syncthreads_count(done) == kRenderThreads) break;
+    const uint32_t e = start + threadIdx.x;
+    if (e < range.y) {
+      const uint32_t id = p.point_list[e];
+      const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id;
+#pragma unroll
+      for (int c = 0; c < kRecChunks; c++) srec[c][threadIdx.x] = rec[c];
+      srec[6][threadIdx.x].z = __uint_as_float(id);
+    }
+    __syncthreads();
+    const uint32_t n = min((uint32_t)kRenderThreads, range.y - start);
+    for (uint32_t j = 0; !done && j < n; j++) {
+      contributor++;
+      const float4 q0 = srec[0][j], q1 = srec[1][j], q2 = srec[2][j];
+      const float Tu0 = q0.x, Tu1 = q0.y, Tu2 = q0.z, Tv0 = q0.w;
+      const float Tv1 = q1.x, Tv2 = q1.y, Tw0 = q1.z, Tw1 = q1.w;
+      const float Tw2 = q2.x;
+      const float k0 = pxf * Tw0 - Tu0, k1 = pxf * Tw1 - Tu1, k2 = pxf * Tw2 - Tu2;
+      const float l0 = pyf * Tw0 - Tv0, l1 = pyf * Tw1 - Tv1, l2 = pyf * Tw2 - Tv2;
+      const float p0 = k1 * l2 - k2 * l1, p1 = k2 * l0 - k0 * l2, p2 = k0 * l1 - k1 * l0;
+      if (p2 == 0.0f) continue;
+      const float sx = p0 / p2, sy = p1 / p2;
+      const float rho3d = sx * sx + sy * sy;
+      const float dx = q2.y - pxf, dy = q2.z - pyf;
+      const float rho2d = 2.0f * (dx * dx + dy * dy);
+      const float rho = fminf(rho3d, rho2d);
+      const bool use3d = rho3d <= rho2d;
+      const float depth = use3d ? (sx * Tw0 + sy * Tw1) + Tw2 : Tw2;
+      if (depth < 0.2f) continue;
+      const float power = -0.5f * rho;
+      if (power > 0.0f) continue;
+      float G = expf_ref(power);
+      if (p.beta > 0.0f) G = (float)((1.0 + (double)p.beta) * (double)G / (1.0 + (double)p.beta * (double)G));
+      const float alpha = fminf(0.99f, q2.w * G);
+      if (alpha < 1.0f / 255.0f) continue;
+      const float test_T = T * (1 - alpha);
+      if (test_T < 0.0001f) {
+        done = true;
+        continue;
+      }
+      const float w = alpha * T;
+      render_number++;
+      if (p.max_intersections > 0 && render_number >= p.max_intersections) done = true;
+
+      const float4 q3 = srec[3][j];
+      const float Aa = 1 - T;
+      const float m = mfac * (1 - 0.2f / depth);
+      distortion += (m * m * Aa + M2 - 2 * m * M1) * w;
+      D += depth * w;
+      M1 += m * w;
+      M2 += m * m * w;
+      if (T > 0.5f) {
+        median_depth = depth;
+        median_contributor = (float)contributor;
+      }
+      N0 += q3.x * w;
+      N1 += q3.y * w;
+      N2 += q3.z * w;
+
+      if constexpr (!kHash) {
+        const uint32_t id = __float_as_uint(srec[6][j].z);
+        const float* col = p.colors + (size_t)id * p.C;
+#pragma unroll
+        for (int c = 0; c < NACC; c++)
+          if (c < p.C) acc[c] += col[c] * w;
+      } else {
+        const float4 q4 = srec[4][j], q5 = srec[5][j], q6 = srec[6][j];
+        float xyz[3];
+        if (use3d) {
+          xyz[0] = sx * q4.x + sy * q4.w + q5.z;
+          xyz[1] = sx * q4.y + sy * q5.x + q5.w;
+          xyz[2] = sx * q4.z + sy * q5.y + q6.x;
+        } else {
+          xyz[0] = q5.z;
+          xyz[1] = q5.w;
+          xyz[2] = q6.x;
+        }
+        pos_x += w * xyz[0];
+        pos_y += w * xyz[1];
+        pos_z += w * xyz[2];
+        const uint32_t ap = __float_as_uint(q3.w);
+
+        // normalisation to [0,1]^3 (hashgrid.h:66-98)
+        float u[3];
+        bool oob = false;
+        if (!g.contract) {
+#pragma unroll
+          for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmin) * g.inv_size;
+          oob = (u[0] < 0 || u[0] > 1 || u[1] < 0 || u[1] > 1 || u[2] < 0 || u[2] > 1);
+        } else {
+#pragma unroll
+          for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmid) * g.inv_size;
+          const float nrm = sqrtf(u[0] * u[0] + u[1] * u[1] + u[2] * u[2]);
+          const float inv_nrm = 1.0f / nrm;
+          const float st = (nrm <= 1.0f) ? 1.0f : (2.0f - inv_nrm) * inv_nrm;
+#pragma unroll
+          for (int d = 0; d < 3; d++) {
+            u[d] = st * u[d];
+            u[d] = (u[d] + 2.0f) * 0.25f;
+          }
+        }
+        const uint32_t max_level = oob ? 0u : (ap < L ? ap : L);
+#pragma unroll
+        for (int l = 0; l < NACC / F; l++) {
+          if ((uint32_t)l < max_level) {
+            float r[F];
+            level_interp<F, kHalf>(g.lv, l, g.table, g.pos_offset, g.interp, u, r);
+#pragma unroll
+            for (int f = 0; f < F; f++) acc[l * F + f] += r[f] * w;
+          } else {
+#pragma unroll
+            for (int f = 0; f < F; f++) acc[l * F + f] += 0.0f * w;
+          }
+        }
+        float apc0, apc1;
+        if (ap <= 4u) {
+          apc0 = (float)((double)(uint32_t)(ap - 2u) * 0.5);
+          apc1 = 1.0f;
+        } else {
+          apc0 = 1.0f;
+          apc1 = (float)(1.0 - (double)(uint32_t)(ap - 4u) * 0.5);
+        }
+        vis0 += apc0 * w;
+        vis1 += apc1 * w;
+        vis2 += 0.0f * w;
+      }
+      T = test_T;
+      last_contributor = contributor;
+    }
+  }
+
+  if (!inside) return;
+  const size_t HW = (size_t)p.W * p.H;
+  const size_t pid = (size_t)p.W * py + px;
+  p.final_T[pid] = T;
+  p.final_T[pid + HW] = M1;
+  p.final_T[pid + 2 * HW] = M2;
+  p.n_contrib[pid] = last_contributor;
+  p.n_contrib[pid + HW] = f2u_sat(median_contributor);
+#pragma unroll
+  for (int c = 0; c < NACC; c++)
+    if (c < p.C) p.out_color[(size_t)c * HW + pid] = acc[c];
+  for (int c = NACC; c < p.C; c++) p.out_color[(size_t)c * HW + pid] = 0.0f;
+  float* O = p.out_others;
+  O[pid + 0 * HW] = D;
+  O[pid + 1 * HW] = 1 - T;
+  O[pid + 2 * HW] = N0;
+  O[pid + 3 * HW] = N1;
+  O[pid + 4 * HW] = N2;
+  O[pid + 5 * HW] = median_depth;
+  O[pid + 6 * HW] = distortion;
+  O[pid + 7 * HW] = (float)render_number;
+  O[pid + 8 * HW] = pos_x;
+  O[pid + 9 * HW] = pos_y;
+  O[pid + 10 * HW] = pos_z;
+  O[pid + 11 * HW] = vis0;
+  O[pid + 12 * HW] = vis1;
+  O[pid + 13 * HW] = vis2;
+}
+
+template <int F, int NACC, bool kHash, bool kHalf>
+static hipError_t launch_one(const RenderParams& p, hipStream_t s) {
+  hipLaunchKernelGGL((render_kernel<F, NACC, kHash, kHalf>), dim3(p.ntiles), dim3(kRenderThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int F, bool kHalf>
+static hipError_t launch_hash_levels(const RenderParams& p, hipStream_t s) {
+  const uint32_t L = p.grid.L;
+  if constexpr (F * 8 <= NEST_MAX_CHANNELS)
+    if (L <= 8) return launch_one<F, F * 8, true, kHalf>(p, s);
+  if constexpr (F * 16 <= NEST_MAX_CHANNELS)
+    if (L <= 16) return launch_one<F, F * 16, true, kHalf>(p, s);
+  if constexpr (F * 32 <= NEST_MAX_CHANNELS)
+    if (L <= 32) return launch_one<F, F * 32, true, kHalf>(p, s);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_render(const RenderParams& p, hipStream_t s) {
+  if (p.ntiles == 0) return hipSuccess;
+  if (p.level == 0) {
+    if (p.C <= 3) return launch_one<1, 3, false, false>(p, s);
+    if (p.C <= 16) return launch_one<1, 16, false, false>(p, s);
+    if (p.C <= 32) return launch_one<1, 32, false, false>(p, s);
+    if (p.C <= 64) return launch_one<1, 64, false, false>(p, s);
+    return launch_one<1, 128, false, false>(p, s);
+  }
+  const bool half = p.grid.half != 0;
+  switch (p.grid.F) {
+    case 1: return half ? launch_hash_levels<1, true>(p, s) : launch_hash_levels<1, false>(p, s);
+    case 2: return half ? launch_hash_levels<2, true>(p, s) : launch_hash_levels<2, false>(p, s);
+    case 4: return half ? launch_hash_levels<4, true>(p, s) : launch_hash_levels<4, false>(p, s);
+    case 8: return half ? launch_hash_levels<8, true>(p, s) : launch_hash_levels<8, false>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace nest

@@ -1,0 +1,160 @@
+"""Drop-in forward rasterizer for 2D Gaussian surfels with an in-loop hash-grid
+texture lookup, running on libnest_splat (gfx950 HIP kernels).
+
+Same call surface as submodules/diff-surfel-rasterization/
+diff_surfel_rasterization/__init__.py:21-414 of the reference:
+GaussianRasterizationSettings (:277-293), HashGridSettings (:295-302),
+GaussianRasterizer(raster_settings, hashgrid_settings).forward(...) returning
+(color [C,H,W], radii [P], allmap [14,H,W], trans_avg, cover) (:172, :321-396),
+markVisible (:310-319) and rasterize_gaussians (:21-66).
+
+Scope: the forward pass of render mode 0 ("baseline"): hash-grid features
+when HashGridSettings.L > 0, precomputed per-splat colours when L == 0.  Modes,
+kernels and options that the reference implements for other methods raise
+NotImplementedError instead of returning zeros; backward raises as well
+(forward-only renderer).
+"""
+from __future__ import annotations
+
+from typing import NamedTuple
+
+import numpy as np
+import torch
+import torch.nn as nn
+
+from nest_splat import rasterizer as _rz
+from nest_splat import _lib
+
+
+def cpu_deep_copy_tuple(input_tuple):
+    return tuple(item.cpu().clone() if isinstance(item, torch.Tensor) else item for item in input_tuple)
+
+
+def _empty(t):
+    return t is None or (isinstance(t, torch.Tensor) and t.numel() == 0)
+
+
+def rasterize_gaussians(means3D, means2D, sh, colors_precomp, opacities, scales, rotations, cov3Ds_precomp, homotrans,
+                        ap_level, features, offsets, gridrange, features_diffuse, offsets_diffuse, gridrange_diffuse,
+                        raster_settings, hashgrid_settings, render_mode, shapes, kernel_type):
+    return _RasterizeGaussians.apply(means3D, means2D, sh, colors_precomp, opacities, scales, rotations,
+                                     cov3Ds_precomp, homotrans, ap_level, features, offsets, gridrange,
+                                     features_diffuse, offsets_diffuse, gridrange_diffuse, raster_settings,
+                                     hashgrid_settings, render_mode, shapes, kernel_type)
+
+
+def _channels(hashgrid_settings) -> int:
+    sd = getattr(hashgrid_settings, "shape_dims", None)
+    if sd is None or (isinstance(sd, torch.Tensor) and sd.numel() != 3) or (not isinstance(sd, torch.Tensor) and len(sd) != 3):
+        return 3
+    v = _rz.host_array(sd, np.int64)
+    return int(v[2])
+
+
+class _RasterizeGaussians(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, means3D, means2D, sh, colors_precomp, opacities, scales, rotations, cov3Ds_precomp, homotrans,
+                ap_level, features, offsets, gridrange, features_diffuse, offsets_diffuse, gridrange_diffuse,
+                raster_settings, hashgrid_settings, render_mode, shapes, kernel_type):
+        if (render_mode & 0xFF) != 0:
+            raise NotImplementedError(f"render_mode {render_mode}: only mode 0 (baseline) is implemented")
+        if kernel_type != 0:
+            raise NotImplementedError(f"kernel_type {kernel_type}: only the Gaussian kernel (0) is implemented")
+        if not _empty(cov3Ds_precomp):
+            raise NotImplementedError("precomputed transforms (cov3D_precomp) are not implemented")
+        if not _empty(features_diffuse):
+            raise NotImplementedError("a second (diffuse) hash grid is not implemented")
+        if raster_settings.record_transmittance:
+            raise NotImplementedError("record_transmittance=True is not implemented")
+        C = _channels(hashgrid_settings)
+        level = int(hashgrid_settings.L)
+        if level > 0:
+            if _empty(features) or _empty(offsets) or _empty(gridrange):
+                raise ValueError("hash-grid rendering (L > 0) needs features, offsets and gridrange")
+            grid = _rz.HashGridDesc(levels=level, level_dim=int(features.shape[1]),
+                                    log2_scale=float(hashgrid_settings.S), base_resolution=int(hashgrid_settings.H),
+                                    table=features.detach().contiguous(), offsets=_rz.host_array(offsets, np.int64),
+                                    gridrange=_rz.host_array(gridrange, np.float32),
+                                    align_corners=bool(hashgrid_settings.align_corners),
+                                    interpolation=int(hashgrid_settings.interpolation))
+            colors = None
+        else:
+            if _empty(colors_precomp):
+                raise NotImplementedError("SH evaluation in the rasterizer is not implemented; pass colors_precomp")
+            grid = _rz.HashGridDesc(0, 1, 0.0, 0, None, np.zeros(1, np.int64), np.zeros(2, np.float32))
+            colors = colors_precomp.detach()
+            if colors.dim() != 2 or colors.shape[1] != C:
+                raise ValueError(f"colors_precomp must be [P, {C}] (shape_dims[2])")
+        s = raster_settings
+        settings = _rz.make_settings(s.image_height, s.image_width, s.tanfovx, s.tanfovy, s.viewmatrix, s.projmatrix,
+                                     s.campos, s.scale_modifier, s.beta, s.if_contract, s.max_intersections,
+                                     s.prefiltered, s.debug)
+        res = _rz.rasterize_forward(settings, grid, means3D.detach(), opacities.detach(), scales.detach(),
+                                    rotations.detach(), homotrans=None if _empty(homotrans) else homotrans.detach(),
+                                    ap_level=None if _empty(ap_level) else ap_level.detach(), colors_precomp=colors,
+                                    channels=C)
+        ctx.num_rendered = res.num_rendered
+        dev = means3D.device
+        trans_avg = torch.zeros((0, 1), dtype=torch.float32, device=dev)
+        cover = torch.zeros((0, 1), dtype=torch.float32, device=dev)
+        return res.color, res.radii, res.others, trans_avg, cover
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError("this rasterizer implements the forward pass only")
+
+
+class GaussianRasterizationSettings(NamedTuple):
+    image_height: int
+    image_width: int
+    tanfovx: float
+    tanfovy: float
+    bg: torch.Tensor
+    scale_modifier: float
+    viewmatrix: torch.Tensor
+    projmatrix: torch.Tensor
+    sh_degree: int
+    campos: torch.Tensor
+    prefiltered: bool
+    debug: bool
+    beta: float
+    if_contract: bool
+    record_transmittance: bool
+    max_intersections: int = 0  # 0 means no limit
+
+
+class HashGridSettings(NamedTuple):
+    L: int
+    S: float
+    H: int
+    align_corners: bool
+    interpolation: int
+    shape_dims: torch.Tensor  # [GS, HS, OS]
+
+
+class GaussianRasterizer(nn.Module):
+    def __init__(self, raster_settings, hashgrid_settings):
+        super().__init__()
+        self.raster_settings = raster_settings
+        self.hashgrid_settings = hashgrid_settings
+
+    def markVisible(self, positions):
+        raise NotImplementedError("markVisible is not implemented by this forward renderer")
+
+    def forward(self, means3D, means2D, opacities, shs=None, colors_precomp=None, scales=None, rotations=None,
+                cov3D_precomp=None, homotrans=None, ap_level=None, features=None, offsets=None, gridrange=None,
+                features_diffuse=None, offsets_diffuse=None, gridrange_diffuse=None, render_mode=0, shapes=None,
+                kernel_type=0):
+        if (shs is None and colors_precomp is None) or (shs is not None and colors_precomp is not None):
+            raise Exception('Please provide excatly one of either SHs or precomputed colors!')
+        if ((scales is None or rotations is None) and cov3D_precomp is None) or \
+                ((scales is not None or rotations is not None) and cov3D_precomp is not None):
+            raise Exception('Please provide exactly one of either scale/rotation pair or precomputed 3D covariance!')
+        return rasterize_gaussians(means3D, means2D, shs, colors_precomp, opacities, scales, rotations, cov3D_precomp,
+                                   homotrans, ap_level, features, offsets, gridrange, features_diffuse,
+                                   offsets_diffuse, gridrange_diffuse, self.raster_settings, self.hashgrid_settings,
+                                   render_mode, shapes, kernel_type)
+
+
+def compute_relocation(opacity_old, scale_old, N, binoms, n_max):
+    raise NotImplementedError("MCMC relocation belongs to training and is not part of this forward renderer")

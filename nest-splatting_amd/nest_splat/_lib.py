@@ -1,0 +1,169 @@
+"""ctypes binding of libnest_splat.so (the C ABI declared in include/nest_splat.h).
+
+Torch owns every device buffer; this module only passes raw pointers, sizes
+and the current HIP stream.  There is no fallback: if the library is missing
+every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as ct
+import os
+from typing import Optional
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libnest_splat.so")
+
+NEST_OK = 0
+NEST_ERR_INVALID_ARGUMENT = -1
+NEST_ERR_UNSUPPORTED = -2
+NEST_ERR_WORKSPACE = -3
+NEST_ERR_HIP = -4
+NEST_ERR_OVERFLOW = -5
+
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+MAX_LEVELS = 32
+MAX_CHANNELS = 128
+OTHERS_CHANNELS = 14
+
+GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP = range(7)
+GEOM_FIELDS = 7
+BIN_KEYS_UNSORTED, BIN_VALS_UNSORTED, BIN_KEYS, BIN_VALS, BIN_SORT_TMP = range(5)
+BIN_FIELDS = 5
+IMG_RANGES, IMG_FINAL_T, IMG_N_CONTRIB = range(3)
+IMG_FIELDS = 3
+STAGES = ("preprocess", "scan", "duplicate", "sort", "ranges", "render")
+
+
+class RasterSettings(ct.Structure):
+    _fields_ = [("struct_size", ct.c_uint32), ("image_height", ct.c_int32), ("image_width", ct.c_int32),
+                ("tanfovx", ct.c_float), ("tanfovy", ct.c_float), ("scale_modifier", ct.c_float),
+                ("viewmatrix", ct.c_float * 16), ("projmatrix", ct.c_float * 16), ("campos", ct.c_float * 3),
+                ("beta", ct.c_float), ("prefiltered", ct.c_int32), ("debug", ct.c_int32),
+                ("if_contract", ct.c_int32), ("max_intersections", ct.c_uint32)]
+
+
+class HashGrid(ct.Structure):
+    _fields_ = [("struct_size", ct.c_uint32), ("levels", ct.c_uint32), ("level_dim", ct.c_uint32),
+                ("log2_scale", ct.c_float), ("base_resolution", ct.c_uint32), ("align_corners", ct.c_int32),
+                ("interpolation", ct.c_int32), ("table_dtype", ct.c_int32), ("table", ct.c_void_p),
+                ("table_rows", ct.c_int64), ("offsets", ct.c_int32 * (MAX_LEVELS + 1)),
+                ("gridrange", ct.c_float * 2)]
+
+
+class Splats(ct.Structure):
+    _fields_ = [("struct_size", ct.c_uint32), ("P", ct.c_int32), ("means3D", ct.c_void_p), ("scales", ct.c_void_p),
+                ("rotations", ct.c_void_p), ("opacities", ct.c_void_p), ("homotrans", ct.c_void_p),
+                ("ap_level", ct.c_void_p), ("colors_precomp", ct.c_void_p)]
+
+
+class FrameOutputs(ct.Structure):
+    _fields_ = [("struct_size", ct.c_uint32), ("channels", ct.c_int32), ("out_color", ct.c_void_p),
+                ("out_others", ct.c_void_p), ("radii", ct.c_void_p)]
+
+
+class Timing(ct.Structure):
+    _fields_ = [("struct_size", ct.c_uint32), ("enabled", ct.c_int32), ("ms", ct.c_float * 6)]
+
+
+class Mlp(ct.Structure):
+    _fields_ = [("struct_size", ct.c_uint32), ("in_features", ct.c_int32), ("width", ct.c_int32),
+                ("dtype", ct.c_int32), ("w1", ct.c_void_p), ("w2", ct.c_void_p), ("w3", ct.c_void_p)]
+
+
+EXPORTS = {
+    "nest_abi_version": (ct.c_int, []),
+    "nest_last_error": (ct.c_char_p, []),
+    "nest_geom_layout": (ct.c_int, [ct.c_int32, ct.POINTER(ct.c_size_t), ct.POINTER(ct.c_size_t)]),
+    "nest_binning_layout": (ct.c_int, [ct.c_int64, ct.POINTER(ct.c_size_t), ct.POINTER(ct.c_size_t)]),
+    "nest_image_layout": (ct.c_int, [ct.c_int32, ct.c_int32, ct.POINTER(ct.c_size_t), ct.POINTER(ct.c_size_t)]),
+    "nest_forward_geometry": (ct.c_int, [ct.POINTER(RasterSettings), ct.POINTER(Splats), ct.c_void_p, ct.c_size_t,
+                                         ct.c_void_p, ct.POINTER(ct.c_int64), ct.POINTER(Timing), ct.c_void_p]),
+    "nest_forward_render": (ct.c_int, [ct.POINTER(RasterSettings), ct.POINTER(HashGrid), ct.POINTER(Splats),
+                                       ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_size_t,
+                                       ct.c_int64, ct.POINTER(FrameOutputs), ct.POINTER(Timing), ct.c_void_p]),
+    "nest_scan_workspace_size": (ct.c_size_t, [ct.c_int64]),
+    "nest_inclusive_scan_u32": (ct.c_int, [ct.c_void_p, ct.c_void_p, ct.c_int64, ct.c_void_p, ct.c_size_t,
+                                           ct.c_void_p]),
+    "nest_sort_workspace_size": (ct.c_size_t, [ct.c_int64]),
+    "nest_sort_pairs_u64": (ct.c_int, [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int64, ct.c_int32,
+                                       ct.c_void_p, ct.c_size_t, ct.c_void_p]),
+    "nest_grid_encode": (ct.c_int, [ct.c_void_p, ct.c_int64, ct.c_int32, ct.c_void_p, ct.c_int64, ct.c_int32,
+                                    ct.POINTER(ct.c_int32), ct.c_int32, ct.c_int32, ct.c_float, ct.c_int32, ct.c_int32,
+                                    ct.c_int32, ct.c_int32, ct.c_void_p, ct.c_void_p]),
+    "nest_mlp_decode": (ct.c_int, [ct.POINTER(Mlp), ct.c_void_p, ct.c_int64, ct.c_int64, ct.c_int64, ct.c_int32,
+                                   ct.c_void_p, ct.POINTER(ct.c_float), ct.c_void_p, ct.POINTER(ct.c_float),
+                                   ct.c_void_p, ct.c_int64, ct.c_int64, ct.c_void_p]),
+    "nest_rvq_decode": (ct.c_int, [ct.c_int64, ct.c_int32, ct.c_int32, ct.c_int32, ct.c_void_p, ct.c_void_p,
+                                   ct.POINTER(ct.c_float), ct.c_int32, ct.c_void_p, ct.c_void_p, ct.c_void_p]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python nest-splatting_amd/build.py` "
+                               "(or __graft_entry__.build()); there is no CPU fallback")
+        L = ct.CDLL(LIB_PATH)
+        for name, (res, args) in EXPORTS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        if L.nest_abi_version() != 1:
+            raise RuntimeError("libnest_splat.so ABI version mismatch")
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == NEST_OK:
+        return
+    msg = lib().nest_last_error().decode(errors="replace")
+    if rc == NEST_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def ptr(t: Optional[torch.Tensor]):
+    if t is None or t.numel() == 0:
+        return None
+    return ct.c_void_p(t.data_ptr())
+
+
+def stream_ptr(device=None):
+    return ct.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def geom_layout(P: int):
+    offs = (ct.c_size_t * GEOM_FIELDS)()
+    tot = ct.c_size_t()
+    check(lib().nest_geom_layout(P, offs, ct.byref(tot)), "nest_geom_layout")
+    return list(offs), tot.value
+
+
+def binning_layout(NR: int):
+    offs = (ct.c_size_t * BIN_FIELDS)()
+    tot = ct.c_size_t()
+    check(lib().nest_binning_layout(NR, offs, ct.byref(tot)), "nest_binning_layout")
+    return list(offs), tot.value
+
+
+def image_layout(W: int, H: int):
+    offs = (ct.c_size_t * IMG_FIELDS)()
+    tot = ct.c_size_t()
+    check(lib().nest_image_layout(W, H, offs, ct.byref(tot)), "nest_image_layout")
+    return list(offs), tot.value
+
+
+def view(buf: torch.Tensor, offset: int, dtype: torch.dtype, shape) -> torch.Tensor:
+    """A typed view into a uint8 workspace at a byte offset."""
+    n = 1
+    for s in shape:
+        n *= s
+    es = torch.empty((), dtype=dtype).element_size()
+    return buf[offset: offset + n * es].view(dtype).view(*shape)

@@ -1,0 +1,244 @@
+"""Forward rasterisation through libnest_splat: the host side of
+RasterizeGaussiansCUDA (submodules/diff-surfel-rasterization/
+rasterize_points.cu:40-242) for render mode 0.
+
+Outputs and workspaces are torch tensors on the splats' device; the library
+fills them with stream-ordered kernels on torch's current stream.  The one
+host synchronisation is the tile/splat pair count read back between the
+geometry and render stages, exactly where the reference reads num_rendered.
+"""
+from __future__ import annotations
+
+import ctypes as ct
+from dataclasses import dataclass, field
+from typing import Dict, Optional
+
+import numpy as np
+import torch
+
+from . import _lib as L
+
+
+def host_array(x, dtype) -> np.ndarray:
+    """Host copy of a small tensor or array.  Device tensors are copied once
+    (a synchronisation) and the copy is cached on the tensor object."""
+    if isinstance(x, torch.Tensor):
+        cached = getattr(x, "_nest_host_copy", None)
+        if cached is not None and cached[0] == x._version:
+            return cached[1]
+        arr = x.detach().cpu().numpy().astype(dtype).reshape(-1)
+        try:
+            x._nest_host_copy = (x._version, arr)
+        except Exception:
+            pass
+        return arr
+    return np.asarray(x, dtype=dtype).reshape(-1)
+
+
+@dataclass
+class HashGridDesc:
+    """Hash grid seen by the render kernel (HashGridSettings + get_params)."""
+
+    levels: int
+    level_dim: int
+    log2_scale: float
+    base_resolution: int
+    table: Optional[torch.Tensor]
+    offsets: np.ndarray
+    gridrange: np.ndarray
+    align_corners: bool = False
+    interpolation: int = 0
+
+    def to_c(self) -> L.HashGrid:
+        g = L.HashGrid()
+        g.struct_size = ct.sizeof(L.HashGrid)
+        g.levels = int(self.levels)
+        g.level_dim = int(self.level_dim)
+        g.log2_scale = float(self.log2_scale)
+        g.base_resolution = int(self.base_resolution)
+        g.align_corners = int(bool(self.align_corners))
+        g.interpolation = int(self.interpolation)
+        if self.levels > 0:
+            t = self.table
+            if t.dtype == torch.float32:
+                g.table_dtype = L.DTYPE_F32
+            elif t.dtype == torch.float16:
+                g.table_dtype = L.DTYPE_F16
+            else:
+                raise NotImplementedError(f"hash table dtype {t.dtype} is not supported (float32/float16)")
+            if not t.is_contiguous():
+                raise ValueError("hash table must be contiguous")
+            if not t.is_cuda:
+                raise ValueError("hash table must be a device tensor")
+            if t.data_ptr() % 16 != 0:
+                t = self.table = t.clone()
+            g.table = t.data_ptr()
+            g.table_rows = int(t.shape[0])
+            if self.levels > L.MAX_LEVELS:
+                raise NotImplementedError(f"at most {L.MAX_LEVELS} levels")
+            offs = np.asarray(self.offsets, dtype=np.int64)
+            if offs.shape[0] < self.levels + 1:
+                raise ValueError(f"offsets has {offs.shape[0]} entries, need {self.levels + 1}")
+            for i in range(self.levels + 1):
+                g.offsets[i] = int(offs[i])
+            g.gridrange[0] = float(self.gridrange[0])
+            g.gridrange[1] = float(self.gridrange[1])
+        return g
+
+
+def make_settings(H: int, W: int, tanfovx: float, tanfovy: float, viewmatrix, projmatrix, campos=(0, 0, 0),
+                  scale_modifier: float = 1.0, beta: float = 0.0, if_contract: bool = False,
+                  max_intersections: int = 0, prefiltered: bool = False, debug: bool = False) -> L.RasterSettings:
+    s = L.RasterSettings()
+    s.struct_size = ct.sizeof(L.RasterSettings)
+    s.image_height = int(H)
+    s.image_width = int(W)
+    s.tanfovx = float(tanfovx)
+    s.tanfovy = float(tanfovy)
+    s.scale_modifier = float(scale_modifier)
+    vm = host_array(viewmatrix, np.float32)
+    pm = host_array(projmatrix, np.float32)
+    cp = host_array(campos, np.float32)
+    for i in range(16):
+        s.viewmatrix[i] = float(vm[i])
+        s.projmatrix[i] = float(pm[i])
+    for i in range(3):
+        s.campos[i] = float(cp[i]) if cp.size == 3 else 0.0
+    s.beta = float(beta)
+    s.prefiltered = int(bool(prefiltered))
+    s.debug = int(bool(debug))
+    s.if_contract = int(bool(if_contract))
+    s.max_intersections = int(max_intersections)
+    return s
+
+
+@dataclass
+class ForwardResult:
+    num_rendered: int
+    color: torch.Tensor
+    others: torch.Tensor
+    radii: torch.Tensor
+    geom: torch.Tensor
+    binning: torch.Tensor
+    image: torch.Tensor
+    timing_ms: Dict[str, float] = field(default_factory=dict)
+
+
+def aligned(t: torch.Tensor, align: int = 16) -> torch.Tensor:
+    """Contiguous tensor whose data pointer is a multiple of ``align`` bytes
+    (the kernels read splat attributes and table rows with 8/16-byte loads)."""
+    t = t.contiguous()
+    if t.data_ptr() % align != 0:
+        t = t.clone()
+    return t
+
+
+def _contig_f32(t: Optional[torch.Tensor], name: str) -> Optional[torch.Tensor]:
+    if t is None or t.numel() == 0:
+        return None
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32 (got {t.dtype})")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    return aligned(t)
+
+
+def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: torch.Tensor, opacities: torch.Tensor,
+                      scales: torch.Tensor, rotations: torch.Tensor, homotrans: Optional[torch.Tensor] = None,
+                      ap_level: Optional[torch.Tensor] = None, colors_precomp: Optional[torch.Tensor] = None,
+                      channels: int = 3, timing: bool = False) -> ForwardResult:
+    if means3D.ndim != 2 or means3D.shape[1] != 3:
+        raise ValueError("means3D must have dimensions (num_points, 3)")
+    dev = means3D.device
+    P = int(means3D.shape[0])
+    H, W = settings.image_height, settings.image_width
+    means3D = _contig_f32(means3D, "means3D")
+    opacities = _contig_f32(opacities, "opacities")
+    scales = _contig_f32(scales, "scales")
+    rotations = _contig_f32(rotations, "rotations")
+    homotrans = _contig_f32(homotrans, "homotrans")
+    ap_level = _contig_f32(ap_level, "ap_level")
+    colors_precomp = _contig_f32(colors_precomp, "colors_precomp")
+    if P > 0:
+        for t, n, k in ((scales, "scales", 2), (rotations, "rotations", 4)):
+            if t is None or t.numel() != P * k:
+                raise ValueError(f"{n} must have {P}x{k} elements")
+        if opacities is None or opacities.numel() != P:
+            raise ValueError("opacities must have P elements")
+        if homotrans is not None and homotrans.numel() != P * 16:
+            raise ValueError("homotrans must be [P, 4, 4]")
+        if ap_level is not None and ap_level.numel() != P:
+            raise ValueError("ap_level must have P elements")
+        if colors_precomp is not None and colors_precomp.numel() != P * channels:
+            raise ValueError(f"colors_precomp must be [P, {channels}]")
+
+    sp = L.Splats()
+    sp.struct_size = ct.sizeof(L.Splats)
+    sp.P = P
+    sp.means3D = L.ptr(means3D)
+    sp.scales = L.ptr(scales)
+    sp.rotations = L.ptr(rotations)
+    sp.opacities = L.ptr(opacities)
+    sp.homotrans = L.ptr(homotrans)
+    sp.ap_level = L.ptr(ap_level)
+    sp.colors_precomp = L.ptr(colors_precomp)
+    g = grid.to_c()
+
+    color = torch.empty((channels, H, W), dtype=torch.float32, device=dev)
+    others = torch.empty((L.OTHERS_CHANNELS, H, W), dtype=torch.float32, device=dev)
+    radii = torch.zeros((P,), dtype=torch.int32, device=dev)
+    _, gbytes = L.geom_layout(P)
+    geom = torch.empty((gbytes,), dtype=torch.uint8, device=dev)
+    _, ibytes = L.image_layout(W, H)
+    image = torch.empty((ibytes,), dtype=torch.uint8, device=dev)
+    tm = L.Timing()
+    tm.struct_size = ct.sizeof(L.Timing)
+    tm.enabled = int(bool(timing))
+    stream = L.stream_ptr(dev)
+    nr = ct.c_int64(0)
+    lib = L.lib()
+    L.check(lib.nest_forward_geometry(ct.byref(settings), ct.byref(sp), L.ptr(geom), gbytes, L.ptr(radii),
+                                      ct.byref(nr), ct.byref(tm), stream), "nest_forward_geometry")
+    NR = int(nr.value)
+    _, bbytes = L.binning_layout(NR)
+    binning = torch.empty((bbytes,), dtype=torch.uint8, device=dev)
+    out = L.FrameOutputs()
+    out.struct_size = ct.sizeof(L.FrameOutputs)
+    out.channels = int(channels)
+    out.out_color = color.data_ptr()
+    out.out_others = others.data_ptr()
+    out.radii = radii.data_ptr()
+    L.check(lib.nest_forward_render(ct.byref(settings), ct.byref(g), ct.byref(sp), L.ptr(geom), gbytes,
+                                    L.ptr(binning), bbytes, L.ptr(image), ibytes, NR, ct.byref(out), ct.byref(tm),
+                                    stream), "nest_forward_render")
+    res = ForwardResult(NR, color, others, radii, geom, binning, image)
+    if timing:
+        res.timing_ms = {n: float(tm.ms[i]) for i, n in enumerate(L.STAGES)}
+    return res
+
+
+def geometry_arrays(res: ForwardResult, P: int) -> Dict[str, torch.Tensor]:
+    """Typed views of the geometry workspace (for tests and debugging)."""
+    o, _ = L.geom_layout(P)
+    n = max(P, 1)
+    return dict(depth=L.view(res.geom, o[L.GEOM_DEPTH], torch.float32, (n,))[:P],
+                xy=L.view(res.geom, o[L.GEOM_XY], torch.float32, (n, 2))[:P],
+                tiles=L.view(res.geom, o[L.GEOM_TILES], torch.int32, (n,))[:P],
+                offsets=L.view(res.geom, o[L.GEOM_OFFSETS], torch.int32, (n,))[:P],
+                records=L.view(res.geom, o[L.GEOM_RECORDS], torch.float32, (n, 32))[:P],
+                radii=L.view(res.geom, o[L.GEOM_RADII], torch.int32, (n,))[:P])
+
+
+def binning_arrays(res: ForwardResult, W: int, H: int) -> Dict[str, torch.Tensor]:
+    NR = res.num_rendered
+    n = max(NR, 1)
+    o, _ = L.binning_layout(NR)
+    io, _ = L.image_layout(W, H)
+    tiles = ((W + 15) // 16) * ((H + 15) // 16)
+    return dict(keys_unsorted=L.view(res.binning, o[L.BIN_KEYS_UNSORTED], torch.int64, (n,))[:NR],
+                vals_unsorted=L.view(res.binning, o[L.BIN_VALS_UNSORTED], torch.int32, (n,))[:NR],
+                keys=L.view(res.binning, o[L.BIN_KEYS], torch.int64, (n,))[:NR],
+                vals=L.view(res.binning, o[L.BIN_VALS], torch.int32, (n,))[:NR],
+                ranges=L.view(res.image, io[L.IMG_RANGES], torch.int32, (tiles, 2)),
+                final_T=L.view(res.image, io[L.IMG_FINAL_T], torch.float32, (3, H, W)),
+                n_contrib=L.view(res.image, io[L.IMG_N_CONTRIB], torch.int32, (2, H, W)))

@@ -1,0 +1,818 @@
+/*
+ * nest_oracle.c -- CPU oracle for the forward render hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP library in
+ * nest-splatting_amd/csrc is compared against.  Only tests/, the smoke entry
+ * point and the bench's cpu_baseline leg load it.  Nothing in the product path
+ * may link, import or call it.
+ *
+ * It is a scalar restatement of the reference's forward semantics (render
+ * mode 0, "baseline" hash-textured 2D surfels) written from the reference
+ * source text.  Every function names the reference file:line it follows.
+ * Paths are relative to the reference root; abbreviations:
+ *   CR/  = submodules/diff-surfel-rasterization/cuda_rasterizer/
+ *   GE/  = gridencoder/
+ *   HE   = hash_encoder/modules.py
+ *
+ * Floating-point contract shared with the HIP kernels
+ * ---------------------------------------------------
+ * The reference leaves the exact bits to nvcc (FMA contraction, approximate
+ * exp/exp2f/rsqrtf), which cannot be reproduced on any other compiler.  The
+ * oracle therefore fixes one IEEE-754 binary32 evaluation order:
+ *   - every expression is evaluated left to right, exactly as written in the
+ *     reference, with no fused multiply-add (built with -ffp-contract=off);
+ *   - exp() is or_expf() below (Cephes-style range reduction + minimax
+ *     polynomial, S. L. Moshier, "Methods and Programs for Mathematical
+ *     Functions", 1989), not the platform libm;
+ *   - rsqrtf(x) becomes 1.0f / sqrtf(x) (both correctly rounded);
+ *   - exp2f(l*S) becomes (float)exp2((double)(l*S)) computed once per level;
+ *   - double literals of the reference (hashgrid.h:70-96) are evaluated in
+ *     float, which is bit-identical because double rounding is innocuous for
+ *     + - * / sqrt when 53 >= 2*24+2;
+ *   - float -> int/uint conversions saturate and map NaN to 0 (the GPU
+ *     conversion instructions do this; C leaves it undefined);
+ *   - min/max are fminf/fmaxf.
+ * The HIP kernels follow the same contract, so integer results (radii, rects,
+ * tiles touched, sort keys, tile ranges, hit counts) must match bit for bit.
+ *
+ * Parity status: the reference holds no tests, fixtures or golden vectors for
+ * this path, so every function here is pinned by the checks in
+ * tests/test_oracle.py (closed forms, invariants, brute force, special cases).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define OR_BLOCK 16
+#define OR_NEAR 0.2f
+#define OR_FAR 100.0f
+
+/* ------------------------------------------------------------------ */
+/* scalar helpers                                                       */
+/* ------------------------------------------------------------------ */
+
+static inline float bits_to_f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint32_t f_to_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+/* exp(x) for binary32.  Range reduction x = k*ln2 + r with ln2 split in a
+ * 9-bit head (exact products for |k| < 2^15) and a tail, degree-5 minimax
+ * polynomial for (e^r - 1 - r)/r^2 on |r| <= ln2/2, scaling by 2^k through the
+ * exponent field.  x < -87 flushes to 0 (results below 2^-126 are never
+ * needed: the render discards alpha < 1/255), x > 88 saturates to +inf. */
+float or_expf(float x)
+{
+    if (x != x) return x;
+    if (x < -87.0f) return 0.0f;
+    if (x > 88.0f) return INFINITY;
+    float t = x * 1.44269504088896341f;
+    float fk = floorf(t + 0.5f);
+    float r = x - fk * 0.693359375f;
+    r = r - fk * -2.12194440e-4f;
+    float z = r * r;
+    float p = 1.9875691500e-4f;
+    p = p * r + 1.3981999507e-3f;
+    p = p * r + 8.3334519073e-3f;
+    p = p * r + 4.1665795894e-2f;
+    p = p * r + 1.6666665459e-1f;
+    p = p * r + 5.0000001201e-1f;
+    float y = p * z + r + 1.0f;
+    int k = (int)fk;
+    return y * bits_to_f((uint32_t)(k + 127) << 23);
+}
+
+/* float -> int32 with saturation to +-2^30 and NaN -> 0 after clamping. */
+static inline int f2i_sat(float x)
+{
+    x = fmaxf(x, -1073741824.0f);
+    x = fminf(x, 1073741824.0f);
+    return (int)x;
+}
+
+/* float -> uint32, truncating; negatives and NaN -> 0, saturating on top. */
+static inline uint32_t f2u_sat(float x)
+{
+    if (!(x >= 0.0f)) return 0u;
+    if (x >= 4294967040.0f) return 4294967040u;
+    return (uint32_t)x;
+}
+
+/* IEEE binary16 <-> binary32, round to nearest even. */
+float or_half_to_float(uint16_t h)
+{
+    uint32_t s = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    uint32_t out;
+    if (e == 0) {
+        if (m == 0) {
+            out = s;
+        } else {
+            int sh = 0;
+            while (!(m & 0x400u)) { m <<= 1; sh++; }
+            m &= 0x3ffu;
+            out = s | ((uint32_t)(113 - sh) << 23) | (m << 13);
+        }
+    } else if (e == 31) {
+        out = s | 0x7f800000u | (m << 13);
+    } else {
+        out = s | ((e + 112u) << 23) | (m << 13);
+    }
+    return bits_to_f(out);
+}
+
+uint16_t or_float_to_half(float f)
+{
+    uint32_t x = f_to_bits(f);
+    uint32_t s = (x >> 16) & 0x8000u;
+    uint32_t e = (x >> 23) & 0xffu;
+    uint32_t m = x & 0x7fffffu;
+    if (e == 255) return (uint16_t)(s | 0x7c00u | (m ? 0x200u : 0u));
+    int ue = (int)e - 127 + 15;
+    if (ue >= 31) return (uint16_t)(s | 0x7c00u);
+    if (ue <= 0) {
+        if (ue < -10) return (uint16_t)s;
+        m |= 0x800000u;
+        int shift = 14 - ue;
+        uint32_t hm = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (hm & 1u))) hm++;
+        return (uint16_t)(s | hm);
+    }
+    uint32_t hm = m >> 13;
+    uint32_t rem = m & 0x1fffu;
+    uint32_t out = s | ((uint32_t)ue << 10) | hm;
+    if (rem > 0x1000u || (rem == 0x1000u && (hm & 1u))) out++;
+    return (uint16_t)out;
+}
+
+float or_round_bf16(float f)
+{
+    uint32_t x = f_to_bits(f);
+    if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x7fffffu)) return bits_to_f(x | 0x400000u);
+    uint32_t lsb = (x >> 16) & 1u;
+    x += 0x7fffu + lsb;
+    return bits_to_f(x & 0xffff0000u);
+}
+
+float or_round_f16(float f) { return or_half_to_float(or_float_to_half(f)); }
+
+/* ------------------------------------------------------------------ */
+/* preprocess: CR/forward.cu:323-441, CR/forward.cu:237-320,           */
+/* CR/auxiliary.h:72-123, :190-297                                      */
+/* ------------------------------------------------------------------ */
+
+/* Per-splat projection of a 2D surfel.  Outputs follow CR/forward.cu:436-440:
+ * depth, radius, screen centre, T = [Tu Tv Tw] (9 floats), view normal +
+ * opacity, tiles touched.  Culled splats get radius 0 and tiles 0 and leave
+ * the other outputs untouched (the GPU writes zeros there; callers compare
+ * only visible splats). */
+void or_preprocess(int P, const float *means, const float *scales, const float *rots,
+                   const float *opac, float scale_mod, const float *view, const float *proj,
+                   int W, int H, int32_t *radii, float *xy, float *depth, float *transmat,
+                   float *normal_opacity, uint32_t *tiles)
+{
+    const uint32_t gx = (uint32_t)((W + OR_BLOCK - 1) / OR_BLOCK);
+    const uint32_t gy = (uint32_t)((H + OR_BLOCK - 1) / OR_BLOCK);
+    const float hw = (float)W / 2.0f, hh = (float)H / 2.0f;
+    const float cw = (float)(W - 1) / 2.0f, ch = (float)(H - 1) / 2.0f;
+    for (int i = 0; i < P; i++) {
+        radii[i] = 0;
+        tiles[i] = 0;
+        const float px = means[3 * i + 0], py = means[3 * i + 1], pz = means[3 * i + 2];
+        /* in_frustum: CR/auxiliary.h:190-215 (only the view-space near test matters) */
+        float vx = view[0] * px + view[4] * py + view[8] * pz + view[12];
+        float vy = view[1] * px + view[5] * py + view[9] * pz + view[13];
+        float vz = view[2] * px + view[6] * py + view[10] * pz + view[14];
+        if (vz <= 0.2f) continue;
+
+        /* quat_to_rotmat: CR/auxiliary.h:218-240 (rot = (w,x,y,z) in .x.y.z.w) */
+        const float q0 = rots[4 * i + 0], q1 = rots[4 * i + 1], q2 = rots[4 * i + 2], q3 = rots[4 * i + 3];
+        float s = 1.0f / sqrtf(q3 * q3 + q0 * q0 + q1 * q1 + q2 * q2);
+        float w = q0 * s, x = q1 * s, y = q2 * s, z = q3 * s;
+        float R[3][3]; /* R[col][row] */
+        R[0][0] = 1.f - 2.f * (y * y + z * z);
+        R[0][1] = 2.f * (x * y + w * z);
+        R[0][2] = 2.f * (x * z - w * y);
+        R[1][0] = 2.f * (x * y - w * z);
+        R[1][1] = 1.f - 2.f * (x * x + z * z);
+        R[1][2] = 2.f * (y * z + w * x);
+        R[2][0] = 2.f * (x * z + w * y);
+        R[2][1] = 2.f * (y * z - w * x);
+        R[2][2] = 1.f - 2.f * (x * x + y * y);
+        /* L = R * diag(sx*mod, sy*mod, 1): columns scaled (CR/auxiliary.h:291-297, forward.cu:252) */
+        const float s0 = scale_mod * scales[2 * i + 0], s1 = scale_mod * scales[2 * i + 1];
+        float L0[3] = {R[0][0] * s0, R[0][1] * s0, R[0][2] * s0};
+        float L1[3] = {R[1][0] * s1, R[1][1] * s1, R[1][2] * s1};
+        float L2[3] = {R[2][0], R[2][1], R[2][2]};
+
+        /* T = transpose(splat2world) * world2ndc * ndc2pix: forward.cu:255-274.
+         * M1 = B(3x4) * A(4x4) with A[r][c] = proj[4r+c], summed k = 0..3. */
+        float M1[3][4];
+        for (int c = 0; c < 4; c++) {
+            M1[0][c] = L0[0] * proj[c] + L0[1] * proj[4 + c] + L0[2] * proj[8 + c];
+            M1[1][c] = L1[0] * proj[c] + L1[1] * proj[4 + c] + L1[2] * proj[8 + c];
+            M1[2][c] = px * proj[c] + py * proj[4 + c] + pz * proj[8 + c] + proj[12 + c];
+        }
+        /* Tu/Tv/Tw are the pixel-x, pixel-y and depth rows over (u, v, 1). */
+        float Tu[3], Tv[3], Tw[3];
+        for (int r = 0; r < 3; r++) {
+            Tu[r] = M1[r][0] * hw + M1[r][3] * cw;
+            Tv[r] = M1[r][1] * hh + M1[r][3] * ch;
+            Tw[r] = M1[r][3];
+        }
+        /* view normal: transformVec4x3(L2, view), normalised (forward.cu:275-288) */
+        float nx = view[0] * L2[0] + view[4] * L2[1] + view[8] * L2[2];
+        float ny = view[1] * L2[0] + view[5] * L2[1] + view[9] * L2[2];
+        float nz = view[2] * L2[0] + view[6] * L2[1] + view[10] * L2[2];
+        float nlen = sqrtf(nx * nx + ny * ny + nz * nz);
+        if (nlen > 1e-7f) { nx = nx / nlen; ny = ny / nlen; nz = nz / nlen; }
+        /* DUAL_VISIABLE: forward.cu:384-389 */
+        float cosv = -(vx * nx + vy * ny + vz * nz);
+        if (cosv == 0.0f) continue;
+        float mul = cosv > 0.0f ? 1.0f : -1.0f;
+        nx = mul * nx; ny = mul * ny; nz = mul * nz;
+
+        /* compute_aabb, cutoff 4: forward.cu:294-320 */
+        const float cut2 = 16.0f;
+        float d = cut2 * (Tw[0] * Tw[0]) + cut2 * (Tw[1] * Tw[1]) + -1.0f * (Tw[2] * Tw[2]);
+        if (d == 0.0f) continue;
+        float invd = 1.0f / d;
+        float f0 = invd * cut2, f1 = invd * cut2, f2 = invd * -1.0f;
+        float pimx = f0 * (Tu[0] * Tw[0]) + f1 * (Tu[1] * Tw[1]) + f2 * (Tu[2] * Tw[2]);
+        float pimy = f0 * (Tv[0] * Tw[0]) + f1 * (Tv[1] * Tw[1]) + f2 * (Tv[2] * Tw[2]);
+        float h0x = pimx * pimx - (f0 * (Tu[0] * Tu[0]) + f1 * (Tu[1] * Tu[1]) + f2 * (Tu[2] * Tu[2]));
+        float h0y = pimy * pimy - (f0 * (Tv[0] * Tv[0]) + f1 * (Tv[1] * Tv[1]) + f2 * (Tv[2] * Tv[2]));
+        float ex = sqrtf(fmaxf(1e-4f, h0x));
+        float ey = sqrtf(fmaxf(1e-4f, h0y));
+        float radius = ceilf(fmaxf(fmaxf(ex, ey), 4.0f * 0.707106f));
+        int ir = f2i_sat(radius);
+
+        /* getRect: CR/auxiliary.h:72-82.  "p + r + BLOCK_X - 1" associates as
+         * ((p + r) + 16) - 1 in float. */
+        float fr = (float)ir;
+        int a0 = f2i_sat((pimx - fr) / 16.0f), a1 = f2i_sat((pimy - fr) / 16.0f);
+        int b0 = f2i_sat((pimx + fr + 16.0f - 1.0f) / 16.0f), b1 = f2i_sat((pimy + fr + 16.0f - 1.0f) / 16.0f);
+        uint32_t rminx = a0 < 0 ? 0u : ((uint32_t)a0 < gx ? (uint32_t)a0 : gx);
+        uint32_t rminy = a1 < 0 ? 0u : ((uint32_t)a1 < gy ? (uint32_t)a1 : gy);
+        uint32_t rmaxx = b0 < 0 ? 0u : ((uint32_t)b0 < gx ? (uint32_t)b0 : gx);
+        uint32_t rmaxy = b1 < 0 ? 0u : ((uint32_t)b1 < gy ? (uint32_t)b1 : gy);
+        uint32_t area = (rmaxx - rminx) * (rmaxy - rminy);
+        if (area == 0) continue;
+
+        depth[i] = vz;
+        radii[i] = ir;
+        xy[2 * i + 0] = pimx;
+        xy[2 * i + 1] = pimy;
+        for (int r = 0; r < 3; r++) {
+            transmat[9 * i + r] = Tu[r];
+            transmat[9 * i + 3 + r] = Tv[r];
+            transmat[9 * i + 6 + r] = Tw[r];
+        }
+        normal_opacity[4 * i + 0] = nx;
+        normal_opacity[4 * i + 1] = ny;
+        normal_opacity[4 * i + 2] = nz;
+        normal_opacity[4 * i + 3] = opac[i];
+        tiles[i] = area;
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* binning: CR/rasterizer_impl.cu:35-111, :173-195, :355-396            */
+/* ------------------------------------------------------------------ */
+
+/* Inclusive prefix sum (cub::DeviceScan::InclusiveSum, rasterizer_impl.cu:355). */
+void or_inclusive_scan_u32(int n, const uint32_t *in, uint32_t *out)
+{
+    uint32_t acc = 0;
+    for (int i = 0; i < n; i++) { acc += in[i]; out[i] = acc; }
+}
+
+/* getHigherMsb: rasterizer_impl.cu:35-50 */
+uint32_t or_higher_msb(uint32_t n)
+{
+    uint32_t msb = sizeof(n) * 4;
+    uint32_t step = msb;
+    while (step > 1) {
+        step /= 2;
+        if (n >> msb) msb += step; else msb -= step;
+    }
+    if (n >> msb) msb++;
+    return msb;
+}
+
+/* duplicateWithKeys: rasterizer_impl.cu:70-111.  Keys are
+ * (tile << 32) | float_bits(depth), emitted row-major over the rect. */
+void or_duplicate_keys(int P, const float *xy, const float *depth, const int32_t *radii,
+                       const uint32_t *offsets, uint32_t gx, uint32_t gy, uint64_t *keys, uint32_t *vals)
+{
+    for (int i = 0; i < P; i++) {
+        if (radii[i] <= 0) continue;
+        uint32_t off = (i == 0) ? 0u : offsets[i - 1];
+        float fr = (float)radii[i];
+        float px = xy[2 * i], py = xy[2 * i + 1];
+        int a0 = f2i_sat((px - fr) / 16.0f), a1 = f2i_sat((py - fr) / 16.0f);
+        int b0 = f2i_sat((px + fr + 16.0f - 1.0f) / 16.0f), b1 = f2i_sat((py + fr + 16.0f - 1.0f) / 16.0f);
+        uint32_t rminx = a0 < 0 ? 0u : ((uint32_t)a0 < gx ? (uint32_t)a0 : gx);
+        uint32_t rminy = a1 < 0 ? 0u : ((uint32_t)a1 < gy ? (uint32_t)a1 : gy);
+        uint32_t rmaxx = b0 < 0 ? 0u : ((uint32_t)b0 < gx ? (uint32_t)b0 : gx);
+        uint32_t rmaxy = b1 < 0 ? 0u : ((uint32_t)b1 < gy ? (uint32_t)b1 : gy);
+        uint32_t dbits = f_to_bits(depth[i]);
+        for (uint32_t y = rminy; y < rmaxy; y++)
+            for (uint32_t x = rminx; x < rmaxx; x++) {
+                uint64_t key = (uint64_t)(y * gx + x);
+                keys[off] = (key << 32) | dbits;
+                vals[off] = (uint32_t)i;
+                off++;
+            }
+    }
+}
+
+typedef struct { uint64_t k; uint32_t v; } or_pair;
+
+static int or_pair_cmp(const void *a, const void *b)
+{
+    const or_pair *x = (const or_pair *)a, *y = (const or_pair *)b;
+    if (x->k != y->k) return x->k < y->k ? -1 : 1;
+    if (x->v != y->v) return x->v < y->v ? -1 : 1;
+    return 0;
+}
+
+/* Stable ascending sort by key (cub::DeviceRadixSort::SortPairs on bits
+ * [0, 32+bit), rasterizer_impl.cu:381-386).  Values enter in ascending index
+ * order per key, so stability equals ordering by (key, value). */
+void or_sort_pairs(int n, uint64_t *keys, uint32_t *vals)
+{
+    or_pair *tmp = (or_pair *)malloc(sizeof(or_pair) * (size_t)(n > 0 ? n : 1));
+    for (int i = 0; i < n; i++) { tmp[i].k = keys[i]; tmp[i].v = vals[i]; }
+    qsort(tmp, (size_t)n, sizeof(or_pair), or_pair_cmp);
+    for (int i = 0; i < n; i++) { keys[i] = tmp[i].k; vals[i] = tmp[i].v; }
+    free(tmp);
+}
+
+/* identifyTileRanges + memset: rasterizer_impl.cu:173-195, :388 */
+void or_tile_ranges(int n, const uint64_t *keys, int ntiles, uint32_t *ranges)
+{
+    memset(ranges, 0, sizeof(uint32_t) * 2 * (size_t)ntiles);
+    for (int i = 0; i < n; i++) {
+        uint32_t t = (uint32_t)(keys[i] >> 32);
+        if (i == 0) ranges[2 * t] = 0;
+        else {
+            uint32_t pt = (uint32_t)(keys[i - 1] >> 32);
+            if (t != pt) { ranges[2 * pt + 1] = (uint32_t)i; ranges[2 * t] = (uint32_t)i; }
+        }
+        if (i == n - 1) ranges[2 * t + 1] = (uint32_t)n;
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* hash grid: CR/hashgrid.h:7-212, GE/src/gridencoder.cu:50-242         */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    int L;              /* levels queried (active levels)            */
+    int F;              /* features per level                        */
+    float S;            /* log2(per_level_scale)                     */
+    int H;              /* base resolution                           */
+    int align_corners;
+    int interp;         /* 0 linear, 1 smoothstep                    */
+    int contract;
+    float vmin, vmax;   /* gridrange                                  */
+    const int32_t *offsets; /* [L+1] entries                         */
+    const void *table;  /* [offsets[L], F]                            */
+    int half_table;     /* 1: binary16 entries, else binary32         */
+} or_grid;
+
+/* exp2f(l*S)*H - 1 and its resolution (hashgrid.h:128-130) */
+void or_level_scale(float S, int H, int l, float *scale, uint32_t *res)
+{
+    float e = (float)l * S;
+    float sc = (float)exp2((double)e) * (float)H - 1.0f;
+    *scale = sc;
+    *res = (uint32_t)ceilf(sc) + 1u;
+}
+
+/* get_grid_index + fast_hash: hashgrid.h:7-40 (D = 3) */
+static inline uint32_t grid_index(int align, uint32_t hsize, uint32_t res, const uint32_t g[3])
+{
+    uint32_t stride = 1, index = 0;
+    for (uint32_t d = 0; d < 3 && stride <= hsize; d++) {
+        index += g[d] * stride;
+        stride *= align ? res : (res + 1u);
+    }
+    if (stride > hsize) index = g[0] * 1u ^ g[1] * 2654435761u ^ g[2] * 805459861u;
+    return index % hsize;
+}
+
+static inline float table_at(const or_grid *G, size_t i)
+{
+    if (G->half_table) return or_half_to_float(((const uint16_t *)G->table)[i]);
+    return ((const float *)G->table)[i];
+}
+
+/* Normalisation to [0,1]^3 (hashgrid.h:66-98).  Returns 1 when out of bounds. */
+static int grid_normalise(const or_grid *G, const float xyz[3], float u[3])
+{
+    if (!G->contract) {
+        float inv = 1.0f / (G->vmax - G->vmin);
+        for (int d = 0; d < 3; d++) u[d] = (xyz[d] - G->vmin) * inv;
+        return (u[0] < 0 || u[0] > 1 || u[1] < 0 || u[1] > 1 || u[2] < 0 || u[2] > 1);
+    }
+    float vmid = (G->vmax + G->vmin) * 0.5f;
+    float inv = 1.0f / ((G->vmax - G->vmin) * 0.5f);
+    for (int d = 0; d < 3; d++) u[d] = (xyz[d] - vmid) * inv;
+    float norm = sqrtf(u[0] * u[0] + u[1] * u[1] + u[2] * u[2]);
+    float inv_norm = 1.0f / norm;
+    float st = (norm <= 1.0f) ? 1.0f : (2.0f - inv_norm) * inv_norm;
+    for (int d = 0; d < 3; d++) {
+        u[d] = st * u[d];
+        u[d] = (u[d] + 2.0f) * 0.25f;
+    }
+    return 0;
+}
+
+/* Trilinear (or smoothstep) interpolation of one level at u in [0,1]^3
+ * (hashgrid.h:122-180). */
+static void grid_level(const or_grid *G, int l, const float u[3], float *out)
+{
+    uint32_t hsize = (uint32_t)(G->offsets[l + 1] - G->offsets[l]);
+    float scale; uint32_t res;
+    or_level_scale(G->S, G->H, l, &scale, &res);
+    size_t base = (size_t)(uint32_t)G->offsets[l] * (size_t)G->F;
+    float pos[3]; uint32_t g[3];
+    for (int d = 0; d < 3; d++) {
+        pos[d] = u[d] * scale + (G->align_corners ? 0.0f : 0.5f);
+        g[d] = f2u_sat(floorf(pos[d]));
+        pos[d] = pos[d] - (float)g[d];
+        if (G->interp == 1) pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
+    }
+    float acc[16];
+    for (int c = 0; c < G->F; c++) acc[c] = 0.0f;
+    for (uint32_t corner = 0; corner < 8; corner++) {
+        float w = 1.0f;
+        uint32_t q[3];
+        for (int d = 0; d < 3; d++) {
+            if ((corner & (1u << d)) == 0) { w *= 1 - pos[d]; q[d] = g[d]; }
+            else { w *= pos[d]; q[d] = g[d] + 1u; }
+        }
+        uint32_t idx = grid_index(G->align_corners, hsize, res, q);
+        for (int c = 0; c < G->F; c++) acc[c] += w * table_at(G, base + (size_t)idx * G->F + c);
+    }
+    for (int c = 0; c < G->F; c++) out[c] = acc[c];
+}
+
+/* query_feature<false, C, F>: hashgrid.h:53-212.  feat has C entries. */
+void or_query_feature(const or_grid *G, const float xyz[3], uint32_t ap, int C, float *feat)
+{
+    float u[3];
+    int oob = grid_normalise(G, xyz, u);
+    for (int c = 0; c < C; c++) feat[c] = 0.0f;
+    if (oob) return;
+    uint32_t max_level = ap < (uint32_t)G->L ? ap : (uint32_t)G->L;
+    for (uint32_t l = 0; l < max_level; l++) grid_level(G, (int)l, u, feat + l * G->F);
+}
+
+/* Standalone GridEncoder.forward (GE/src/gridencoder.cu:87-242, D = 3,
+ * gridtype hash).  Output layout [B, L*F] (the permuted result of
+ * GE/grid.py:59).  With a binary16 table the accumulator is binary16 as the
+ * scalar_t accumulator of the reference: each step rounds w*g to binary16,
+ * adds in binary32 and rounds the sum back to binary16 (at::Half += float). */
+void or_grid_encode(const or_grid *G, int B, const float *inputs, float *out)
+{
+    const int L = G->L, F = G->F;
+    for (int b = 0; b < B; b++) {
+        const float *u = inputs + 3 * (size_t)b;
+        int oob = (u[0] < 0 || u[0] > 1 || u[1] < 0 || u[1] > 1 || u[2] < 0 || u[2] > 1);
+        for (int l = 0; l < L; l++) {
+            float *o = out + (size_t)b * L * F + (size_t)l * F;
+            if (oob) { for (int c = 0; c < F; c++) o[c] = 0.0f; continue; }
+            if (!G->half_table) { grid_level(G, l, u, o); continue; }
+            uint32_t hsize = (uint32_t)(G->offsets[l + 1] - G->offsets[l]);
+            float scale; uint32_t res;
+            or_level_scale(G->S, G->H, l, &scale, &res);
+            size_t base = (size_t)(uint32_t)G->offsets[l] * (size_t)F;
+            float pos[3]; uint32_t g[3];
+            for (int d = 0; d < 3; d++) {
+                pos[d] = u[d] * scale + (G->align_corners ? 0.0f : 0.5f);
+                g[d] = f2u_sat(floorf(pos[d]));
+                pos[d] = pos[d] - (float)g[d];
+                if (G->interp == 1) pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
+            }
+            float acc[16];
+            for (int c = 0; c < F; c++) acc[c] = 0.0f;
+            for (uint32_t corner = 0; corner < 8; corner++) {
+                float w = 1.0f; uint32_t q[3];
+                for (int d = 0; d < 3; d++) {
+                    if ((corner & (1u << d)) == 0) { w *= 1 - pos[d]; q[d] = g[d]; }
+                    else { w *= pos[d]; q[d] = g[d] + 1u; }
+                }
+                uint32_t idx = grid_index(G->align_corners, hsize, res, q);
+                for (int c = 0; c < F; c++)
+                    acc[c] = or_round_f16(acc[c] + or_round_f16(w * table_at(G, base + (size_t)idx * F + c)));
+            }
+            for (int c = 0; c < F; c++) o[c] = acc[c];
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* render, mode 0: CR/forward.cu:639-1145, :1914-2048                   */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    int W, H;
+    int C;                 /* output feature channels (>= L*F)             */
+    int level;             /* 0: per-splat colours path, >0: hash grid     */
+    float beta;
+    uint32_t max_intersections;
+    const uint32_t *ranges;      /* [tiles][2]                            */
+    const uint32_t *point_list;  /* sorted splat ids                       */
+    const float *xy;             /* [P][2]                                 */
+    const float *transmat;       /* [P][9]                                 */
+    const float *normal_opacity; /* [P][4]                                 */
+    const float *homotrans;      /* [P][16]                                */
+    const float *ap_level;       /* [P]                                    */
+    const float *colors;         /* [P][C] when level == 0                 */
+    or_grid grid;
+    /* outputs */
+    float *out_color;            /* [C][H][W]                              */
+    float *out_others;           /* [14][H][W]                             */
+    float *final_T;              /* [3][H][W]                              */
+    uint32_t *n_contrib;         /* [2][H][W]                              */
+} or_render_args;
+
+static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, uint32_t py, float *feat_scratch)
+{
+    const int W = A->W, H = A->H, C = A->C;
+    const size_t HW = (size_t)W * (size_t)H;
+    const size_t pid = (size_t)W * py + px;
+    const float pxf = (float)px, pyf = (float)py;
+    uint32_t r0 = A->ranges[2 * tile], r1 = A->ranges[2 * tile + 1];
+    float T = 1.0f;
+    uint32_t contributor = 0, last_contributor = 0, render_number = 0;
+    float Cacc[256];
+    for (int c = 0; c < C; c++) Cacc[c] = 0.0f;
+    float N[3] = {0, 0, 0}, vis[3] = {0, 0, 0};
+    float D = 0, M1 = 0, M2 = 0, distortion = 0, median_depth = 0, median_contributor = -1.0f;
+    float pos_x = 0, pos_y = 0, pos_z = 0;
+    const float mfac = OR_FAR / (OR_FAR - OR_NEAR);
+    int done = 0;
+    for (uint32_t e = r0; e < r1 && !done; e++) {
+        contributor++;
+        const uint32_t id = A->point_list[e];
+        const float *Tm = A->transmat + 9 * (size_t)id;
+        const float Tu0 = Tm[0], Tu1 = Tm[1], Tu2 = Tm[2];
+        const float Tv0 = Tm[3], Tv1 = Tm[4], Tv2 = Tm[5];
+        const float Tw0 = Tm[6], Tw1 = Tm[7], Tw2 = Tm[8];
+        float k0 = pxf * Tw0 - Tu0, k1 = pxf * Tw1 - Tu1, k2 = pxf * Tw2 - Tu2;
+        float l0 = pyf * Tw0 - Tv0, l1 = pyf * Tw1 - Tv1, l2 = pyf * Tw2 - Tv2;
+        float p0 = k1 * l2 - k2 * l1, p1 = k2 * l0 - k0 * l2, p2 = k0 * l1 - k1 * l0;
+        if (p2 == 0.0f) continue;
+        float sx = p0 / p2, sy = p1 / p2;
+        float rho3d = sx * sx + sy * sy;
+        float dx = A->xy[2 * id] - pxf, dy = A->xy[2 * id + 1] - pyf;
+        float rho2d = 2.0f * (dx * dx + dy * dy);
+        float rho = fminf(rho3d, rho2d);
+        int use3d = rho3d <= rho2d;
+        float depth = use3d ? (sx * Tw0 + sy * Tw1) + Tw2 : Tw2;
+        if (depth < OR_NEAR) continue;
+        const float *no = A->normal_opacity + 4 * (size_t)id;
+        float power = -0.5f * rho;
+        if (power > 0.0f) continue;
+        float G = or_expf(power);
+        if (A->beta > 0.0f) G = (float)((1.0 + (double)A->beta) * (double)G / (1.0 + (double)A->beta * (double)G));
+        float alpha = fminf(0.99f, no[3] * G);
+        if (alpha < 1.0f / 255.0f) continue;
+        float test_T = T * (1 - alpha);
+        if (test_T < 0.0001f) { done = 1; continue; }
+        float w = alpha * T;
+        render_number++;
+        if (A->max_intersections > 0 && render_number >= A->max_intersections) done = 1;
+
+        float Aa = 1 - T;
+        float m = mfac * (1 - OR_NEAR / depth);
+        distortion += (m * m * Aa + M2 - 2 * m * M1) * w;
+        D += depth * w;
+        M1 += m * w;
+        M2 += m * m * w;
+        if (T > 0.5f) { median_depth = depth; median_contributor = (float)contributor; }
+        N[0] += no[0] * w; N[1] += no[1] * w; N[2] += no[2] * w;
+
+        if (A->level == 0) {
+            const float *col = A->colors + (size_t)id * C;
+            for (int c = 0; c < C; c++) Cacc[c] += col[c] * w;
+        } else {
+            const float *Hm = A->homotrans + 16 * (size_t)id;
+            float xyz[3];
+            if (use3d) {
+                xyz[0] = sx * Hm[0] + sy * Hm[1] + Hm[3];
+                xyz[1] = sx * Hm[4] + sy * Hm[5] + Hm[7];
+                xyz[2] = sx * Hm[8] + sy * Hm[9] + Hm[11];
+            } else {
+                xyz[0] = Hm[3]; xyz[1] = Hm[7]; xyz[2] = Hm[11];
+            }
+            pos_x += w * xyz[0]; pos_y += w * xyz[1]; pos_z += w * xyz[2];
+            uint32_t ap = f2u_sat(floorf(A->ap_level[id]));
+            or_query_feature(&A->grid, xyz, ap, C, feat_scratch);
+            for (int c = 0; c < C; c++) Cacc[c] += feat_scratch[c] * w;
+            float apc0, apc1;
+            if (ap <= 4u) { apc0 = (float)((double)(uint32_t)(ap - 2u) * 0.5); apc1 = 1.0f; }
+            else { apc0 = 1.0f; apc1 = (float)(1.0 - (double)(uint32_t)(ap - 4u) * 0.5); }
+            vis[0] += apc0 * w; vis[1] += apc1 * w; vis[2] += 0.0f * w;
+        }
+        T = test_T;
+        last_contributor = contributor;
+    }
+    A->final_T[pid] = T;
+    A->final_T[pid + HW] = M1;
+    A->final_T[pid + 2 * HW] = M2;
+    A->n_contrib[pid] = last_contributor;
+    A->n_contrib[pid + HW] = f2u_sat(median_contributor);
+    for (int c = 0; c < C; c++) A->out_color[(size_t)c * HW + pid] = Cacc[c];
+    float *O = A->out_others;
+    O[pid + 0 * HW] = D;
+    O[pid + 1 * HW] = 1 - T;
+    O[pid + 2 * HW] = N[0];
+    O[pid + 3 * HW] = N[1];
+    O[pid + 4 * HW] = N[2];
+    O[pid + 5 * HW] = median_depth;
+    O[pid + 6 * HW] = distortion;
+    O[pid + 7 * HW] = (float)render_number;
+    O[pid + 8 * HW] = pos_x;
+    O[pid + 9 * HW] = pos_y;
+    O[pid + 10 * HW] = pos_z;
+    O[pid + 11 * HW] = vis[0];
+    O[pid + 12 * HW] = vis[1];
+    O[pid + 13 * HW] = vis[2];
+}
+
+/* Renders every tile row ty with ty % row_stride == row_phase (row_stride 1 =
+ * the whole image).  Pixels of skipped rows are left untouched.  Tiles are
+ * independent, so OpenMP threads over tiles change nothing in the result. */
+void or_render(const or_render_args *A, int row_stride, int row_phase, int nthreads)
+{
+    const int gx = (A->W + OR_BLOCK - 1) / OR_BLOCK, gy = (A->H + OR_BLOCK - 1) / OR_BLOCK;
+    if (row_stride < 1) row_stride = 1;
+    int nrows = 0;
+    for (int ty = 0; ty < gy; ty++) if (ty % row_stride == row_phase) nrows++;
+    const int ntiles = nrows * gx;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        float feat[256];
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 4)
+#endif
+        for (int t = 0; t < ntiles; t++) {
+            int rr = t / gx, tx = t % gx;
+            int ty = row_phase + rr * row_stride;
+            uint32_t tile = (uint32_t)(ty * gx + tx);
+            for (int yy = 0; yy < OR_BLOCK; yy++)
+                for (int xx = 0; xx < OR_BLOCK; xx++) {
+                    uint32_t px = (uint32_t)(tx * OR_BLOCK + xx), py = (uint32_t)(ty * OR_BLOCK + yy);
+                    if (px >= (uint32_t)A->W || py >= (uint32_t)A->H) continue;
+                    render_pixel(A, tile, px, py, feat);
+                }
+        }
+    }
+    (void)nthreads;
+}
+
+int or_max_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* ------------------------------------------------------------------ */
+/* view-direction MLP decode: HE:551-602, HE:727-730                    */
+/* ------------------------------------------------------------------ */
+
+/* Real spherical harmonics of degree 0..3 (16 terms) of a unit direction,
+ * in the standard ordering l = 0..3, m = -l..l with the Condon-Shortley phase
+ * (the basis of utils/sh_utils.py and of the SphericalHarmonics encoding used
+ * at HE:551-558).  The input is the encoder's [0,1] coordinate, mapped back
+ * with x = 2u - 1. */
+void or_sh16(const float u[3], float *o)
+{
+    float x = u[0] * 2.0f - 1.0f, y = u[1] * 2.0f - 1.0f, z = u[2] * 2.0f - 1.0f;
+    float xy = x * y, xz = x * z, yz = y * z, x2 = x * x, y2 = y * y, z2 = z * z;
+    o[0] = 0.28209479177387814f;
+    o[1] = -0.48860251190291987f * y;
+    o[2] = 0.48860251190291987f * z;
+    o[3] = -0.48860251190291987f * x;
+    o[4] = 1.0925484305920792f * xy;
+    o[5] = -1.0925484305920792f * yz;
+    o[6] = 0.94617469575755997f * z2 - 0.31539156525251999f;
+    o[7] = -1.0925484305920792f * xz;
+    o[8] = 0.54627421529603959f * x2 - 0.54627421529603959f * y2;
+    o[9] = 0.59004358992664352f * y * (-3.0f * x2 + y2);
+    o[10] = 2.8906114426405538f * xy * z;
+    o[11] = 0.45704579946446572f * y * (1.0f - 5.0f * z2);
+    o[12] = 0.3731763325901154f * z * (5.0f * z2 - 3.0f);
+    o[13] = 0.45704579946446572f * x * (1.0f - 5.0f * z2);
+    o[14] = 1.4453057213202769f * z * (x2 - y2);
+    o[15] = 0.59004358992664352f * x * (-x2 + 3.0f * y2);
+}
+
+static inline float round_dtype(float v, int dtype)
+{
+    if (dtype == 1) return or_round_f16(v);
+    if (dtype == 2) return or_round_bf16(v);
+    return v;
+}
+
+/* rgb = sigmoid(W3 relu(W2 relu(W1 [feat, SH16((d+1)/2)])))[:3], no biases
+ * (HE:560-572, :587-602), then the mask and background of GR:1014-1021.
+ * feat is channel-major [C][npix] (the rasterizer's out_color layout).
+ * dirs holds unit view directions [npix][3].  dtype 0/1/2 = fp32/fp16/bf16:
+ * the layer inputs and weights are rounded to that type, the dot products are
+ * accumulated in double and rounded to binary32 once. */
+void or_mlp(int npix, int C, const float *feat, const float *dirs, const float *alpha,
+            const float *W1, const float *W2, const float *W3, int Nw, int dtype,
+            const float *bg, float *rgb_out /* [3][npix] */)
+{
+    const int Din = C + 16;
+    float *x = (float *)malloc(sizeof(float) * (size_t)(Din + 2 * Nw));
+    float *h1 = x + Din, *h2 = h1 + Nw;
+    int use_bg = bg && (bg[0] + bg[1] + bg[2] > 0.0f);
+    for (int p = 0; p < npix; p++) {
+        for (int c = 0; c < C; c++) x[c] = round_dtype(feat[(size_t)c * npix + p], dtype);
+        float u[3];
+        for (int d = 0; d < 3; d++) u[d] = (dirs[3 * (size_t)p + d] + 1.0f) / 2.0f;
+        or_sh16(u, x + C);
+        for (int j = 0; j < 16; j++) x[C + j] = round_dtype(x[C + j], dtype);
+        for (int n = 0; n < Nw; n++) {
+            double acc = 0.0;
+            for (int k = 0; k < Din; k++) acc += (double)round_dtype(W1[(size_t)n * Din + k], dtype) * (double)x[k];
+            float v = (float)acc;
+            h1[n] = round_dtype(v > 0.0f ? v : 0.0f, dtype);
+        }
+        for (int n = 0; n < Nw; n++) {
+            double acc = 0.0;
+            for (int k = 0; k < Nw; k++) acc += (double)round_dtype(W2[(size_t)n * Nw + k], dtype) * (double)h1[k];
+            float v = (float)acc;
+            h2[n] = round_dtype(v > 0.0f ? v : 0.0f, dtype);
+        }
+        float a = alpha ? alpha[p] : 1.0f;
+        for (int o = 0; o < 3; o++) {
+            double acc = 0.0;
+            for (int k = 0; k < Nw; k++) acc += (double)round_dtype(W3[(size_t)o * Nw + k], dtype) * (double)h2[k];
+            double sg = 1.0 / (1.0 + exp(-acc));
+            float r = (float)sg;
+            if (alpha) r = (a > 0.0f) ? r : 0.0f;
+            if (use_bg) r = r + (1.0f - a) * bg[o];
+            rgb_out[(size_t)o * npix + p] = r;
+        }
+    }
+    free(x);
+}
+
+/* ------------------------------------------------------------------ */
+/* RVQ decode (no counterpart in the reference)                          */
+/* ------------------------------------------------------------------ */
+
+/* v[p][d] = bias[d] + (((cb[0][i0][d] + cb[1][i1][d]) + cb[2][i2][d]) + cb[3][i3][d])
+ * for S stages in order; codebooks [S][K][dim], indices [P][S] uint16, bias
+ * [dim] or NULL (then the stage sum is returned as is). */
+void or_rvq_decode(int P, int S, int K, int dim, const float *cb, const uint16_t *idx,
+                   const float *bias, float *out)
+{
+    for (int p = 0; p < P; p++)
+        for (int d = 0; d < dim; d++) {
+            float v = 0.0f;
+            for (int s = 0; s < S; s++) {
+                uint32_t i = idx[(size_t)p * S + s];
+                float c = cb[((size_t)s * K + i) * dim + d];
+                v = (s == 0) ? c : v + c;
+            }
+            out[(size_t)p * dim + d] = bias ? bias[d] + v : v;
+        }
+}
+
+/* Activations of scene/gaussian_model.py:26-41 applied to decoded attributes
+ * with this file's exp: scale = exp(v), rotation = v / max(|v|, 1e-12),
+ * opacity = 1 / (1 + exp(-v)). */
+void or_activate(int P, const float *sc_raw, const float *rot_raw, const float *op_raw,
+                 float *scales, float *rots, float *opac)
+{
+    for (int p = 0; p < P; p++) {
+        scales[2 * p] = or_expf(sc_raw[2 * p]);
+        scales[2 * p + 1] = or_expf(sc_raw[2 * p + 1]);
+        const float *q = rot_raw + 4 * (size_t)p;
+        float n = sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+        n = fmaxf(n, 1e-12f);
+        for (int k = 0; k < 4; k++) rots[4 * p + k] = q[k] / n;
+        opac[p] = 1.0f / (1.0f + or_expf(-op_raw[p]));
+    }
+}
