@@ -88,10 +88,17 @@ __global__ void __launch_bounds__(256) grid_encode_kernel(const GridEncodeParams
       load_entry<C, kHalf>(p.table, base + idx, v);
 #pragma unroll
       for (int ch = 0; ch < C; ch++) {
-        if constexpr (kHalf)
-          acc[ch] = round_half(acc[ch] + round_half(w * v[ch]));
-        else
+        if constexpr (kHalf) {
+          // at::Half += float: the float32 product is rounded to float32 and
+          // then to float16.  The empty asm keeps the product a float32
+          // value; without it the backend folds multiply and conversion into
+          // one v_fma_mixlo_f16 with a single rounding.
+          float prod = w * v[ch];
+          asm volatile("" : "+v"(prod));
+          acc[ch] = round_half(acc[ch] + round_half(prod));
+        } else {
           acc[ch] += w * v[ch];
+        }
       }
     }
   }

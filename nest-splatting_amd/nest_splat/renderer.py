@@ -1,0 +1,229 @@
+"""render(): counterpart of the baseline hash-textured branch of
+gaussian_renderer/__init__.py:23-1062 (parameter gathering :178-213, raster
+settings and call :694-760, allmap post-processing :762-797, MLP decode, mask
+and background :905-1021, output keys :1025-1046).
+
+The rasterizer runs through the drop-in diff_surfel_rasterization API; the MLP
+decode runs fused (view directions, SH encoding, MLP, sigmoid, mask,
+background) in one kernel on the channel-major feature map, so the
+permute().contiguous() copy of the reference disappears.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+import torch.nn.functional as torch_F
+
+from . import rasterizer as rz
+from .camera import Camera, view_ray_matrix
+from .mlp import NestMLP
+
+
+def build_rotation(r: torch.Tensor) -> torch.Tensor:
+    """utils/general_utils.py:78-99."""
+    norm = torch.sqrt(r[:, 0] * r[:, 0] + r[:, 1] * r[:, 1] + r[:, 2] * r[:, 2] + r[:, 3] * r[:, 3])
+    q = r / norm[:, None]
+    R = torch.zeros((q.size(0), 3, 3), device=r.device)
+    w, x, y, z = q[:, 0], q[:, 1], q[:, 2], q[:, 3]
+    R[:, 0, 0] = 1 - 2 * (y * y + z * z)
+    R[:, 0, 1] = 2 * (x * y - w * z)
+    R[:, 0, 2] = 2 * (x * z + w * y)
+    R[:, 1, 0] = 2 * (x * y + w * z)
+    R[:, 1, 1] = 1 - 2 * (x * x + z * z)
+    R[:, 1, 2] = 2 * (y * z - w * x)
+    R[:, 2, 0] = 2 * (x * z - w * y)
+    R[:, 2, 1] = 2 * (y * z + w * x)
+    R[:, 2, 2] = 1 - 2 * (x * x + y * y)
+    return R
+
+
+def build_H(rots: torch.Tensor, scales: torch.Tensor, xyzs: torch.Tensor) -> torch.Tensor:
+    """utils/general_utils.py:101-113."""
+    batch = rots.shape[0]
+    s = torch.zeros(batch, 1, 3, device=rots.device)
+    s[:, 0, :2] = scales
+    h = torch.zeros(batch, 4, 4, device=rots.device)
+    h[:, :3, :3] = torch.mul(s, rots)
+    h[:, :3, 3] = xyzs
+    h[:, 3, 3] = 1.0
+    return h
+
+
+class SplatModel:
+    """The GaussianModel getters the forward render reads
+    (scene/gaussian_model.py:231-317), over activated attributes."""
+
+    def __init__(self, xyz, scaling, rotation, opacity, ap_level=None, homotrans=None):
+        self._xyz = xyz
+        self._scaling = scaling
+        self._rotation = rotation
+        self._opacity = opacity.reshape(-1, 1)
+        self._ap = ap_level if ap_level is not None else torch.full((xyz.shape[0], 1), 24.0, device=xyz.device)
+        self._homotrans = homotrans
+
+    @property
+    def get_xyz(self):
+        return self._xyz
+
+    @property
+    def get_scaling(self):
+        return self._scaling
+
+    @property
+    def get_rotation(self):
+        return self._rotation
+
+    @property
+    def get_opacity(self):
+        return self._opacity
+
+    @property
+    def get_appearance_level(self):
+        return self._ap
+
+    def get_homotrans(self):
+        if self._homotrans is not None:
+            return self._homotrans
+        return build_H(build_rotation(self._rotation), self._scaling, self._xyz)
+
+
+class HashINGP:
+    """The INGP attributes the baseline render reads (hash_encoder/modules.py):
+    hash_encoding (a GridEncoder), gridrange, contract, active_levels, levels,
+    level_dim and rgb_decode."""
+
+    def __init__(self, encoding, mlp: NestMLP, gridrange, contract: bool = False, active_levels: Optional[int] = None):
+        self.hash_encoding = encoding
+        self.mlp_rgb = mlp
+        self.gridrange = torch.as_tensor(np.asarray(gridrange, dtype=np.float32))
+        self._gridrange_host = np.asarray(gridrange, dtype=np.float32)
+        self.contract = contract
+        self.levels = encoding.num_levels
+        self.level_dim = encoding.level_dim
+        self.active_levels = self.levels if active_levels is None else active_levels
+
+    def rgb_decode(self, features, ray_unit):
+        return self.mlp_rgb.rgb_decode(features, ray_unit)
+
+
+@dataclass
+class Pipe:
+    depth_ratio: float = 0.0
+
+
+def _matrix(x, device) -> torch.Tensor:
+    if isinstance(x, torch.Tensor):
+        return x.to(device=device, dtype=torch.float32)
+    return torch.from_numpy(np.asarray(x, dtype=np.float32)).to(device)
+
+
+def depth_to_normal(cam, depth: torch.Tensor) -> torch.Tensor:
+    """utils/point_utils.py:10-29, :48-60."""
+    W, H = cam.image_width, cam.image_height
+    dev = depth.device
+    wv = _matrix(cam.world_view_transform, dev)
+    c2w = torch.linalg.inv(wv.T)
+    M = torch.from_numpy(view_ray_matrix(cam)).to(dev)
+    gx, gy = torch.meshgrid(torch.arange(W, device=dev).float(), torch.arange(H, device=dev).float(), indexing="xy")
+    pts = torch.stack([gx, gy, torch.ones_like(gx)], dim=-1).reshape(-1, 3)
+    rays_d = pts @ M
+    rays_o = c2w[:3, 3]
+    points = (depth.reshape(-1, 1) * rays_d + rays_o).reshape(H, W, 3)
+    out = torch.zeros_like(points)
+    dx = points[2:, 1:-1] - points[:-2, 1:-1]
+    dy = points[1:-1, 2:] - points[1:-1, :-2]
+    out[1:-1, 1:-1, :] = torch_F.normalize(torch.cross(dx, dy, dim=-1), dim=-1)
+    return out
+
+
+def render(viewpoint_camera, pc, pipe, bg_color: torch.Tensor, scaling_modifier=1.0, ingp: HashINGP = None, beta=0,
+           max_intersections=0, skip_mlp=False, with_surface=True):
+    from diff_surfel_rasterization import GaussianRasterizationSettings, GaussianRasterizer, HashGridSettings
+
+    dev = pc.get_xyz.device
+    tanfovx = math.tan(viewpoint_camera.FoVx * 0.5)
+    tanfovy = math.tan(viewpoint_camera.FoVy * 0.5)
+    means3D = pc.get_xyz
+    means2D = torch.zeros_like(means3D)
+    enc = ingp.hash_encoding
+    features, offsets, _, per_level_scale, base_resolution, align_corners, interpolation = enc.get_params()
+    host = getattr(enc, "_offsets_host", None)
+    if host is not None:
+        offsets._nest_host_copy = (offsets._version, np.asarray(host, dtype=np.float64).astype(np.int64))
+    gridrange = ingp.gridrange
+    gridrange._nest_host_copy = (gridrange._version, ingp._gridrange_host)
+    levels = ingp.active_levels
+    output_dim = ingp.levels * ingp.level_dim
+    shape_dims = torch.tensor([0, output_dim, output_dim], dtype=torch.int32)
+    raster_settings = GaussianRasterizationSettings(
+        image_height=int(viewpoint_camera.image_height), image_width=int(viewpoint_camera.image_width),
+        tanfovx=tanfovx, tanfovy=tanfovy, bg=bg_color, scale_modifier=scaling_modifier,
+        viewmatrix=viewpoint_camera.world_view_transform, projmatrix=viewpoint_camera.full_proj_transform,
+        sh_degree=0, campos=viewpoint_camera.camera_center, prefiltered=False, debug=False, beta=beta,
+        if_contract=ingp.contract, record_transmittance=False, max_intersections=max_intersections)
+    hashgrid_settings = HashGridSettings(L=levels, S=math.log2(per_level_scale), H=base_resolution,
+                                         align_corners=align_corners, interpolation=interpolation,
+                                         shape_dims=shape_dims)
+    rasterizer = GaussianRasterizer(raster_settings=raster_settings, hashgrid_settings=hashgrid_settings)
+    shs = torch.empty((0,), device=dev)
+    rendered_image, radii, allmap, _, _ = rasterizer(
+        means3D=means3D, means2D=means2D, shs=shs, colors_precomp=None, opacities=pc.get_opacity,
+        scales=pc.get_scaling, rotations=pc.get_rotation, homotrans=pc.get_homotrans(),
+        ap_level=pc.get_appearance_level, cov3D_precomp=None, features=features, offsets=offsets,
+        gridrange=gridrange, render_mode=0, shapes=None, kernel_type=0)
+
+    render_alpha = allmap[1:2]
+    rets = {"viewspace_points": means2D, "visibility_filter": radii > 0, "radii": radii, "features": rendered_image,
+            "allmap": allmap}
+    H, W = int(viewpoint_camera.image_height), int(viewpoint_camera.image_width)
+    if skip_mlp:
+        rgb = torch.zeros(3, H, W, device=dev)
+        if bg_color.sum() > 0:
+            rgb = rgb + (1.0 - render_alpha) * bg_color.to(dev).unsqueeze(-1).unsqueeze(-1)
+    else:
+        bg = bg_color if float(bg_color.sum()) > 0 else None
+        rgb = ingp.mlp_rgb.decode_image(rendered_image, view_ray_matrix(viewpoint_camera), alpha=render_alpha, bg=bg)
+    rets["render"] = rgb
+
+    if with_surface:
+        wv = _matrix(viewpoint_camera.world_view_transform, dev)
+        render_normal = (allmap[2:5].permute(1, 2, 0) @ (wv[:3, :3].T)).permute(2, 0, 1)
+        render_depth_median = torch.nan_to_num(allmap[5:6], 0, 0)
+        render_depth_expected = torch.nan_to_num(allmap[0:1] / render_alpha, 0, 0)
+        render_dist = allmap[6:7]
+        dr = getattr(pipe, "depth_ratio", 0.0)
+        surf_depth = render_depth_expected * (1 - dr) + dr * render_depth_median
+        surf_normal = depth_to_normal(viewpoint_camera, surf_depth).permute(2, 0, 1) * render_alpha.detach()
+        rets.update({"rend_alpha": render_alpha, "rend_normal": render_normal, "rend_dist": render_dist,
+                     "surf_depth": surf_depth, "surf_normal": surf_normal, "gaussian_num": allmap[7:8],
+                     "depth_expected": render_depth_expected, "depth_median": render_depth_median})
+    return rets
+
+
+def scene_to_device(scene, device="cuda:0"):
+    """(SplatModel, HashINGP) for a synthetic Scene."""
+    from gridencoder import GridEncoder
+
+    sp = scene.spec
+    dev = torch.device(device)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    pc = SplatModel(t(scene.means), t(scene.scales), t(scene.rotations), t(scene.opacity), t(scene.ap_level),
+                    homotrans=t(scene.homotrans))
+    enc = GridEncoder(3, sp.L, sp.F, sp.per_level_scale, sp.base_res, sp.log2T).to(dev)
+    with torch.no_grad():
+        tab = t(scene.table)
+        enc.embeddings = torch.nn.Parameter(tab, requires_grad=False)
+    mlp = NestMLP(sp.C, sp.mlp_width, sp.mlp_dtype, scene.W1, scene.W2, scene.W3).to(dev)
+    ingp = HashINGP(enc, mlp, sp.gridrange, sp.contract)
+    return pc, ingp
+
+
+def render_scene(scene, cam_index=0, device="cuda:0", with_surface=False, max_intersections=0):
+    pc, ingp = scene_to_device(scene, device)
+    cam = scene.cameras[cam_index]
+    bg = torch.tensor(scene.spec.bg, dtype=torch.float32, device=device)
+    return render(cam, pc, Pipe(), bg, ingp=ingp, with_surface=with_surface, max_intersections=max_intersections)

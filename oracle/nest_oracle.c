@@ -436,6 +436,9 @@ static int grid_normalise(const or_grid *G, const float xyz[3], float u[3])
     return 0;
 }
 
+/* Exported for the tests: normalised grid coordinate of xyz; returns oob. */
+int or_grid_normalise(const or_grid *G, const float *xyz, float *u) { return grid_normalise(G, xyz, u); }
+
 /* Trilinear (or smoothstep) interpolation of one level at u in [0,1]^3
  * (hashgrid.h:122-180). */
 static void grid_level(const or_grid *G, int l, const float u[3], float *out)

@@ -70,6 +70,8 @@ def lib():
         L.or_tile_ranges.argtypes = [ct.c_int, u64p, ct.c_int, u32p]
         L.or_render.argtypes = [ct.POINTER(OrRenderArgs), ct.c_int, ct.c_int, ct.c_int]
         L.or_query_feature.argtypes = [ct.POINTER(OrGrid), f32p, ct.c_uint32, ct.c_int, f32p]
+        L.or_grid_normalise.argtypes = [ct.POINTER(OrGrid), f32p, f32p]
+        L.or_grid_normalise.restype = ct.c_int
         L.or_grid_encode.argtypes = [ct.POINTER(OrGrid), ct.c_int, f32p, f32p]
         L.or_level_scale.argtypes = [ct.c_float, ct.c_int, ct.c_int, ct.POINTER(ct.c_float), ct.POINTER(ct.c_uint32)]
         L.or_mlp.argtypes = [ct.c_int, ct.c_int, f32p, f32p, ct.c_void_p, f32p, f32p, f32p, ct.c_int, ct.c_int,
@@ -196,6 +198,12 @@ def query_feature(grid: OrGrid, xyz, ap, C):
     feat = np.zeros(C, np.float32)
     lib().or_query_feature(ct.byref(grid), _c(xyz, np.float32), int(ap), C, feat)
     return feat
+
+
+def grid_normalise(grid: OrGrid, xyz):
+    u = np.zeros(3, np.float32)
+    oob = lib().or_grid_normalise(ct.byref(grid), _c(xyz, np.float32), u)
+    return u, bool(oob)
 
 
 def grid_encode(grid: OrGrid, inputs):

@@ -1,0 +1,176 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+include/nest_splat.h declares, reports layouts, and rejects bad arguments
+before launching anything (error codes and messages, outputs untouched)."""
+import ctypes as ct
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _lib():
+    from nest_splat import _lib as L
+    if not os.path.exists(L.LIB_PATH):
+        pytest.fail(f"{L.LIB_PATH} not built (run __graft_entry__.build())")
+    return L
+
+
+def declared_functions():
+    src = open(os.path.join(ROOT, "include", "nest_splat.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char \*)\s*(nest_\w+)\(", src, re.M)))
+
+
+def test_exports_match_header():
+    L = _lib()
+    lib = L.lib()
+    names = declared_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in L.EXPORTS, f"{n} has no ctypes signature"
+    assert lib.nest_abi_version() == 1
+
+
+def test_struct_sizes_match_c_layout():
+    """ctypes mirrors of the ABI structs have the sizes the library checks
+    (a mismatch is reported as NEST_ERR_INVALID_ARGUMENT, see below)."""
+    L = _lib()
+    assert ct.sizeof(L.RasterSettings) == 4 * (6 + 16 + 16 + 3 + 1 + 4)
+    assert ct.sizeof(L.HashGrid) % 8 == 0
+    assert ct.sizeof(L.Splats) == 8 + 7 * 8
+    assert ct.sizeof(L.FrameOutputs) == 8 + 3 * 8
+    assert ct.sizeof(L.Mlp) == 16 + 3 * 8
+
+
+def test_layouts_are_aligned_and_monotone():
+    L = _lib()
+    for P in (0, 1, 1000, 1 << 20):
+        offs, tot = L.geom_layout(P)
+        assert all(o % 256 == 0 for o in offs) and offs == sorted(offs) and tot >= offs[-1]
+        assert offs[L.GEOM_RECORDS + 1] - offs[L.GEOM_RECORDS] >= max(P, 1) * 128
+    offs, tot = L.binning_layout(5_000_000)
+    assert offs[L.BIN_KEYS] - offs[L.BIN_KEYS_UNSORTED] >= 5_000_000 * 12
+    offs, tot = L.image_layout(1600, 1064)
+    assert offs[L.IMG_FINAL_T] >= 6700 * 8 and tot >= 1600 * 1064 * 20
+
+
+def _settings(L, **kw):
+    s = L.RasterSettings()
+    s.struct_size = ct.sizeof(L.RasterSettings)
+    s.image_height, s.image_width = 64, 64
+    for k, v in kw.items():
+        setattr(s, k, v)
+    return s
+
+
+def _splats(L, P=10):
+    sp = L.Splats()
+    sp.struct_size = ct.sizeof(L.Splats)
+    sp.P = P
+    return sp
+
+
+def test_geometry_rejects_bad_arguments():
+    L = _lib()
+    lib = L.lib()
+    nr = ct.c_int64(-7)
+    tm = L.Timing()
+    ws = (ct.c_uint8 * 16)()
+    # wrong struct size
+    s = _settings(L, struct_size=3)
+    rc = lib.nest_forward_geometry(ct.byref(s), ct.byref(_splats(L)), ws, 16, None, ct.byref(nr), ct.byref(tm), None)
+    assert rc == L.NEST_ERR_INVALID_ARGUMENT and b"struct_size" in lib.nest_last_error()
+    # non-positive image
+    s = _settings(L, image_width=0)
+    rc = lib.nest_forward_geometry(ct.byref(s), ct.byref(_splats(L)), ws, 16, None, ct.byref(nr), ct.byref(tm), None)
+    assert rc == L.NEST_ERR_INVALID_ARGUMENT and b"image size" in lib.nest_last_error()
+    # missing attribute pointers
+    s = _settings(L)
+    rc = lib.nest_forward_geometry(ct.byref(s), ct.byref(_splats(L)), ws, 16, None, ct.byref(nr), ct.byref(tm), None)
+    assert rc == L.NEST_ERR_INVALID_ARGUMENT and b"required" in lib.nest_last_error()
+    # workspace too small (pointers are never dereferenced on this path)
+    sp = _splats(L)
+    sp.means3D = sp.scales = sp.rotations = sp.opacities = 1
+    rc = lib.nest_forward_geometry(ct.byref(s), ct.byref(sp), ws, 16, None, ct.byref(nr), ct.byref(tm), None)
+    assert rc == L.NEST_ERR_WORKSPACE and b"too small" in lib.nest_last_error()
+    assert nr.value == -7  # outputs untouched on error
+    # prefiltered is unsupported
+    s = _settings(L, prefiltered=1)
+    rc = lib.nest_forward_geometry(ct.byref(s), ct.byref(sp), ws, 16, None, ct.byref(nr), ct.byref(tm), None)
+    assert rc == L.NEST_ERR_UNSUPPORTED
+
+
+def test_render_rejects_bad_grids():
+    L = _lib()
+    lib = L.lib()
+    s = _settings(L)
+    sp = _splats(L, 0)
+    g = L.HashGrid()
+    g.struct_size = ct.sizeof(L.HashGrid)
+    g.levels, g.level_dim = 16, 3
+    out = L.FrameOutputs()
+    out.struct_size = ct.sizeof(L.FrameOutputs)
+    out.channels = 48
+    out.out_color = out.out_others = 1
+    ws = (ct.c_uint8 * 16)()
+    args = lambda: (ct.byref(s), ct.byref(g), ct.byref(sp), ws, 16, ws, 16, ws, 16, 0, ct.byref(out), None, None)
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_UNSUPPORTED  # level_dim 3
+    g.level_dim = 4
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_INVALID_ARGUMENT  # 48 < 64 channels
+    assert b"channels" in lib.nest_last_error()
+    out.channels = 64
+    g.table = 1
+    g.table_rows = 10
+    g.gridrange[0], g.gridrange[1] = -1.0, 1.0
+    for i in range(17):
+        g.offsets[i] = i * 1024
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_INVALID_ARGUMENT  # table too small
+    assert b"rows" in lib.nest_last_error()
+    g.table_rows = 16 * 1024
+    g.offsets[5] = g.offsets[4]
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_INVALID_ARGUMENT  # empty level
+    g.offsets[5] = 5 * 1024
+    g.gridrange[1] = -1.0
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_INVALID_ARGUMENT  # empty range
+    g.gridrange[1] = 1.0
+    out.channels = 200
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_UNSUPPORTED
+    out.channels = 64
+    # workspace checks come after argument checks and before any launch
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_WORKSPACE
+
+
+def test_building_block_validation():
+    L = _lib()
+    lib = L.lib()
+    assert lib.nest_sort_workspace_size(1000) > 1000 * 12
+    assert lib.nest_scan_workspace_size(1 << 20) >= 8 * 256
+    assert lib.nest_sort_pairs_u64(None, None, None, None, 10, 70, None, 0, None) == L.NEST_ERR_INVALID_ARGUMENT
+    assert lib.nest_sort_pairs_u64(None, None, None, None, 0, 45, None, 0, None) == L.NEST_OK
+    assert lib.nest_inclusive_scan_u32(None, None, -1, None, 0, None) == L.NEST_ERR_INVALID_ARGUMENT
+    offs = (ct.c_int32 * 17)(*[i * 64 for i in range(17)])
+    assert lib.nest_grid_encode(None, 10, 6, None, 0, 0, offs, 16, 2, 0.5, 16, 0, 0, 0, None, None) == L.NEST_ERR_UNSUPPORTED
+    assert lib.nest_grid_encode(None, 10, 3, None, 0, 0, offs, 16, 3, 0.5, 16, 0, 0, 0, None, None) == L.NEST_ERR_UNSUPPORTED
+    assert lib.nest_grid_encode(None, 10, 3, None, 100, 0, offs, 16, 2, 0.5, 16, 0, 0, 0, None, None) == \
+        L.NEST_ERR_INVALID_ARGUMENT  # 100 rows < offsets[16]
+    m = L.Mlp()
+    m.struct_size = ct.sizeof(L.Mlp)
+    m.in_features, m.width, m.dtype = 24, 64, L.DTYPE_BF16
+    assert lib.nest_mlp_decode(ct.byref(m), None, 1, 1, 10, 8, None, None, None, None, None, 1, 1, None) == \
+        L.NEST_ERR_UNSUPPORTED  # MFMA path needs C % 16 == 0
+    m.in_features, m.width = 32, 48
+    assert lib.nest_mlp_decode(ct.byref(m), None, 1, 1, 10, 8, None, None, None, None, None, 1, 1, None) == \
+        L.NEST_ERR_UNSUPPORTED
+    assert lib.nest_rvq_decode(10, 4, 4096, 5, None, None, None, 0, None, None, None) == L.NEST_ERR_UNSUPPORTED
+    assert lib.nest_rvq_decode(10, 4, 4096, 2, None, None, None, 7, None, None, None) == L.NEST_ERR_INVALID_ARGUMENT
+
+
+def test_python_errors_are_raised():
+    L = _lib()
+    with pytest.raises(NotImplementedError):
+        L.check(L.NEST_ERR_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        L.check(L.NEST_ERR_HIP, "x")

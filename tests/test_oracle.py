@@ -1,0 +1,402 @@
+"""Pins the CPU oracle (oracle/nest_oracle.c) without the reference.
+
+The reference holds no tests, fixtures or golden vectors for this path, so
+every oracle function is checked against what the mathematics fixes: closed
+forms, invariants, brute force on small inputs, independent library routines
+(numpy float16/bfloat16 rounding, scipy spherical harmonics), and special
+cases with exactly known answers.  Each check is chosen so that a plausible
+slip (swapped operand, wrong sign or index, dropped term) fails it.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from scenes import scene
+
+
+# ---------------------------------------------------------------- scalar math
+
+def test_expf_accuracy(oracle):
+    xs = np.concatenate([np.linspace(-87.0, 0.0, 20001), np.linspace(0.0, 88.0, 2001),
+                         -np.logspace(-8, 1.9, 3001)]).astype(np.float32)
+    ours = oracle.expf(xs).astype(np.float64)
+    ref = np.exp(xs.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    err = np.abs(ours - ref) / ulp
+    assert err.max() <= 2.0, err.max()
+    assert oracle.expf([0.0])[0] == 1.0
+    assert oracle.expf([-100.0])[0] == 0.0 and np.isinf(oracle.expf([100.0])[0])
+    assert np.isnan(oracle.expf([np.nan])[0])
+
+
+def test_half_and_bf16_rounding_match_numpy(oracle):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.uniform(-0.2, 0.2, 20000), rng.uniform(-1e-4, 1e-4, 5000),
+                        rng.standard_normal(5000) * 1e3]).astype(np.float32)
+    h = rng.integers(0, 0x7bff, 5000).astype(np.uint16).view(np.float16).astype(np.float32)
+    ties = ((h.astype(np.float64) + np.nextafter(h, np.float32(np.inf)).astype(np.float64)) / 2).astype(np.float32)
+    x = np.concatenate([x, ties])
+    f16 = np.array([oracle.lib().or_round_f16(float(v)) for v in x], np.float32)
+    np.testing.assert_array_equal(f16, x.astype(np.float16).astype(np.float32))
+    # bfloat16: torch's round-to-nearest-even conversion is the independent check
+    import torch
+    bf = np.array([oracle.lib().or_round_bf16(float(v)) for v in x], np.float32)
+    np.testing.assert_array_equal(bf, torch.from_numpy(x).to(torch.bfloat16).float().numpy())
+    np.testing.assert_array_equal(oracle.round_bf16(x), bf)
+
+
+def test_higher_msb_is_bit_length(oracle):
+    for n in list(range(1, 5000)) + [6700, 8160, 8191, 8192, 2 ** 20 + 1, 2 ** 31 - 1]:
+        assert oracle.higher_msb(n) == n.bit_length(), n
+
+
+# ---------------------------------------------------------------- preprocess
+
+def _project(cam, pts):
+    """Pixel coordinates of world points through full_proj_transform and the
+    rasterizer's ndc->pixel map ((ndc + 1) * W - 1) / 2 (auxiliary.h:67-70)."""
+    P = np.concatenate([pts, np.ones((pts.shape[0], 1))], axis=1) @ cam.full_proj_transform.astype(np.float64)
+    ndc = P[:, :3] / P[:, 3:4]
+    x = ((ndc[:, 0] + 1) * cam.image_width - 1) * 0.5
+    y = ((ndc[:, 1] + 1) * cam.image_height - 1) * 0.5
+    view = np.concatenate([pts, np.ones((pts.shape[0], 1))], axis=1) @ cam.world_view_transform.astype(np.float64)
+    return x, y, view[:, 2]
+
+
+def test_preprocess_homography_round_trip(oracle):
+    """For p = c + a*sx*R0 + b*sy*R1 the transform T maps (a, b) to the pixel
+    of p and Tw.(a,b,1) to its view depth (the 2DGS ray-splat homography)."""
+    sc = scene("shell_small")
+    cam = sc.cameras[0]
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, cam.image_width, cam.image_height)
+    vis = np.nonzero(pre["radii"] > 0)[0][:300]
+    rng = np.random.default_rng(1)
+    from nest_splat.scene import build_rotation_np
+    R = build_rotation_np(sc.rotations[vis]).astype(np.float64)
+    for k, i in enumerate(vis):
+        a, b = rng.uniform(-2, 2, 2)
+        p = sc.means[i] + a * sc.scales[i, 0] * R[k][:, 0] + b * sc.scales[i, 1] * R[k][:, 1]
+        x, y, z = _project(cam, p[None, :].astype(np.float64))
+        T = pre["transmat"][i].astype(np.float64)
+        uv1 = np.array([a, b, 1.0])
+        den = T[6:9] @ uv1
+        assert abs(T[0:3] @ uv1 / den - x[0]) < 2e-3 * max(1, abs(x[0]))
+        assert abs(T[3:6] @ uv1 / den - y[0]) < 2e-3 * max(1, abs(y[0]))
+        assert abs(den - z[0]) < 1e-4 * max(1, abs(z[0]))
+        assert abs(pre["depth"][i] - (cam.world_view_transform.astype(np.float64).T @ np.append(sc.means[i], 1))[2]) < 1e-5
+
+
+def test_preprocess_aabb_contains_cutoff_ellipse(oracle):
+    sc = scene("cfg1")
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    vis = pre["radii"] > 0
+    assert vis.sum() > 100
+    th = np.linspace(0, 2 * np.pi, 64, endpoint=False)
+    uv = np.stack([4 * np.cos(th), 4 * np.sin(th), np.ones_like(th)], 0)
+    for i in np.nonzero(vis)[0]:
+        T = pre["transmat"][i].astype(np.float64).reshape(3, 3)
+        den = T[2] @ uv
+        if np.any(den <= 0):
+            continue
+        px, py = T[0] @ uv / den, T[1] @ uv / den
+        r = pre["radii"][i]
+        cx, cy = pre["xy"][i]
+        assert np.all(np.abs(px - cx) <= r + 1e-2) and np.all(np.abs(py - cy) <= r + 1e-2)
+        assert r >= 3  # ceil(4 * 0.707106)
+    # normals face the camera: -p_view . n > 0
+    for i in np.nonzero(vis)[0][:200]:
+        pv = (cam.world_view_transform.astype(np.float64).T @ np.append(sc.means[i], 1))[:3]
+        assert -pv @ pre["normal_opacity"][i, :3] > 0
+
+
+def test_preprocess_near_cull_and_tiles(oracle):
+    sc = scene("cfg1")
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    depth = (np.concatenate([sc.means, np.ones((sc.spec.P, 1), np.float32)], 1) @ cam.world_view_transform)[:, 2]
+    assert np.all(pre["radii"][depth <= 0.2] == 0)
+    # tiles touched = brute-force tile rectangle of getRect (auxiliary.h:72-82)
+    gx, gy = (W + 15) // 16, (H + 15) // 16
+    for i in np.nonzero(pre["radii"] > 0)[0]:
+        r = np.float32(pre["radii"][i])
+        x, y = pre["xy"][i]
+        lo = [min(g, max(0, int(np.float32((v - r) / np.float32(16))))) for v, g in ((x, gx), (y, gy))]
+        hi = [min(g, max(0, int(np.float32(np.float32(np.float32(v + r) + np.float32(16)) - np.float32(1)) / np.float32(16))))
+              for v, g in ((x, gx), (y, gy))]
+        assert pre["tiles"][i] == (hi[0] - lo[0]) * (hi[1] - lo[1])
+
+
+# ------------------------------------------------------------------- binning
+
+@pytest.mark.parametrize("name", ["cfg1", "shell_small"])
+def test_binning_matches_brute_force(oracle, name):
+    sc = scene(name)
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    NR = b["num_rendered"]
+    assert NR == int(pre["tiles"].astype(np.int64).sum())
+    np.testing.assert_array_equal(b["offsets"], np.cumsum(pre["tiles"].astype(np.int64)).astype(np.uint32))
+    # keys: tile << 32 | float bits of the depth, values in index order per splat
+    ku, vu = b["keys_unsorted"], b["vals_unsorted"]
+    np.testing.assert_array_equal(ku & np.uint64(0xFFFFFFFF), pre["depth"][vu].view(np.uint32).astype(np.uint64))
+    assert np.all(np.diff(vu.astype(np.int64)) >= 0)
+    # stable sort == lexicographic (key, index) order (numpy lexsort)
+    order = np.lexsort((vu, ku))
+    np.testing.assert_array_equal(b["keys"], ku[order])
+    np.testing.assert_array_equal(b["vals"], vu[order])
+    assert np.all(np.diff(b["keys"].astype(np.float64)) >= 0)
+    # ranges = searchsorted of the tile ids; they partition [0, NR)
+    tiles = (b["keys"] >> np.uint64(32)).astype(np.int64)
+    nt = ((W + 15) // 16) * ((H + 15) // 16)
+    lo = np.searchsorted(tiles, np.arange(nt), "left")
+    hi = np.searchsorted(tiles, np.arange(nt), "right")
+    present = hi > lo
+    np.testing.assert_array_equal(b["ranges"][present, 0], lo[present])
+    np.testing.assert_array_equal(b["ranges"][present, 1], hi[present])
+    assert np.all(b["ranges"][~present] == 0)
+    assert int((b["ranges"][:, 1].astype(np.int64) - b["ranges"][:, 0]).sum()) == NR
+
+
+# --------------------------------------------------------------------- hash
+
+def _grid(oracle, L, F, T, H, S, table, align=False, contract=False, gridrange=(0.0, 1.0)):
+    offs = (np.arange(L + 1) * T).astype(np.int32)
+    return oracle.make_grid(L, F, S, H, offs, table, gridrange, contract, align), offs
+
+
+def test_hash_index_known_answers(oracle):
+    """A query exactly on a grid vertex (align_corners, scale 16) puts weight 1
+    on corner 0, so a table holding its own row numbers returns the index
+    function: dense g0 + r g1 + r^2 g2 when r^3 <= T, else the xor hash mod T."""
+    for T, dense in ((8192, True), (1024, False)):
+        table = np.arange(T, dtype=np.float32)[:, None]
+        g, _ = _grid(oracle, 1, 1, T, 17, 0.0, table, align=True)
+        rng = np.random.default_rng(T)
+        for _ in range(200):
+            q = rng.integers(0, 16, 3)
+            u = (q / 16.0).astype(np.float32)
+            out = oracle.grid_encode(g, u[None, :])[0, 0]
+            if dense:
+                idx = int(q[0] + 17 * q[1] + 289 * q[2])
+            else:
+                idx = (int(q[0]) ^ ((int(q[1]) * 2654435761) & 0xFFFFFFFF) ^ ((int(q[2]) * 805459861) & 0xFFFFFFFF)) % T
+            assert out == float(idx), (q, out, idx)
+
+
+def test_trilinear_reproduces_affine_table(oracle):
+    """On a dense level a table holding a*q + b at vertex q is interpolated
+    exactly to a*pos + b (pos = u*scale + 0.5)."""
+    H, T = 16, 16 ** 3 * 2
+    a = np.array([0.01, -0.02, 0.005])
+    idx = np.arange(T)
+    r = 16 + 1
+    q = np.stack([idx % r, (idx // r) % r, idx // (r * r)], 1).astype(np.float64)
+    table = (q @ a + 0.3).astype(np.float32)[:, None]
+    g, _ = _grid(oracle, 1, 1, T, H, 0.0, table)
+    rng = np.random.default_rng(3)
+    u = rng.uniform(0, 1, (500, 3)).astype(np.float32)
+    out = oracle.grid_encode(g, u)[:, 0]
+    pos = u.astype(np.float64) * 15 + 0.5
+    np.testing.assert_allclose(out, pos @ a + 0.3, atol=2e-6)
+    # weights sum to one: a constant table comes back unchanged (to rounding)
+    g1, _ = _grid(oracle, 1, 1, 1 << 12, H, 0.0, np.full((1 << 12, 1), 0.5, np.float32))
+    np.testing.assert_allclose(oracle.grid_encode(g1, u)[:, 0], 0.5, atol=1e-7)
+
+
+def test_contract_matches_python_mirror(oracle):
+    """hashgrid.h:77-97 and its Python mirror INGP._encode_3D
+    (hash_encoder/modules.py:697-725, "should be the same with query_feature")."""
+    import torch
+    g, _ = _grid(oracle, 1, 1, 64, 4, 0.0, np.zeros((64, 1), np.float32), contract=True, gridrange=(-1.0, 1.0))
+    rng = np.random.default_rng(5)
+    pts = np.concatenate([rng.uniform(-1, 1, (300, 3)), rng.standard_normal((300, 3)) * 8]).astype(np.float32)
+    vmin, vmax = -1.0, 1.0
+    t = torch.from_numpy(pts)
+    vmid, vsize = (vmin + vmax) * 0.5, (vmax - vmin) * 0.5
+    n = (t - vmid) / vsize
+    norm = n.norm(dim=-1, keepdim=True)
+    inv = 1.0 / norm
+    st = torch.where(norm <= 1.0, torch.ones_like(norm), (2.0 - inv) * inv)
+    mirror = ((n * st + 2.0) * 0.25).numpy()
+    for k in range(pts.shape[0]):
+        u, oob = oracle.grid_normalise(g, pts[k])
+        assert not oob
+        np.testing.assert_allclose(u, mirror[k], rtol=0, atol=2e-7)
+        assert np.all(u >= 0) and np.all(u <= 1)
+    # outside the grid range without contraction: out of bounds
+    g2, _ = _grid(oracle, 1, 1, 64, 4, 0.0, np.zeros((64, 1), np.float32), gridrange=(-1.0, 1.0))
+    assert oracle.grid_normalise(g2, np.array([1.5, 0, 0], np.float32))[1]
+    assert not oracle.grid_normalise(g2, np.array([1.0, -1.0, 0], np.float32))[1]
+
+
+# -------------------------------------------------------------------- render
+
+def _single_splat_scene(n=1, opacity=0.5, W=64, H=48, off=(0.0, 0.0, 0.0)):
+    """n identical splats facing a camera on the -y axis, centred on the ray of
+    pixel (32, 24)."""
+    from nest_splat.camera import look_at
+    cam = look_at((0.0, -3.0, 0.0), (0.0, 0.0, 0.0), 50.0, W, H)
+    M = np.linalg.inv(cam.world_view_transform.astype(np.float64).T)  # camera-to-world
+    z = M[:3, 2]
+    # centre on the camera axis: principal point of the rasterizer is ((W-1)/2, (H-1)/2)
+    means = np.tile((np.array(off) + 0 * z)[None, :], (n, 1)).astype(np.float32)
+    # rotation mapping +z to the viewing axis: splat plane faces the camera
+    q = np.tile(np.array([np.cos(np.pi / 4), np.sin(np.pi / 4), 0, 0], np.float32), (n, 1))
+    scales = np.full((n, 2), 0.2, np.float32)
+    opac = np.full((n, 1), opacity, np.float32)
+    return cam, means, scales, q, opac
+
+
+def test_stacked_splats_termination_closed_form(oracle):
+    """k coplanar copies of an alpha = 0.5 splat: at the splat centre the
+    pixel accepts n hits with (1-a)^n >= 1e-4 > (1-a)^(n+1): n = 13."""
+    cam, means, scales, q, opac = _single_splat_scene(n=20, opacity=0.5, W=63, H=47)
+    W, H = cam.image_width, cam.image_height
+    pre = oracle.preprocess(means, scales, q, opac, cam.world_view_transform, cam.full_proj_transform, W, H)
+    assert np.all(pre["radii"] > 0)
+    b = oracle.binning(pre, W, H)
+    cols = np.ones((20, 3), np.float32)
+    r = oracle.render(pre, b, W, H, 3, None, colors=cols)
+    cx, cy = (W - 1) // 2, (H - 1) // 2
+    assert pre["xy"][0, 0] == pytest.approx(cx, abs=1e-3) and pre["xy"][0, 1] == pytest.approx(cy, abs=1e-3)
+    assert r["others"][7, cy, cx] == 13
+    assert r["others"][1, cy, cx] == np.float32(1) - np.float32(0.5) ** 13
+    np.testing.assert_allclose(r["color"][:, cy, cx], 1 - 0.5 ** 13, rtol=1e-6)
+    # max_intersections caps the count and accumulates the capping hit
+    r2 = oracle.render(pre, b, W, H, 3, None, colors=cols, max_intersections=4)
+    assert r2["others"][7, cy, cx] == 4
+    assert r2["others"][1, cy, cx] == np.float32(1) - np.float32(0.5) ** 4
+
+
+def test_single_splat_hash_feature_closed_form(oracle):
+    """One splat at the pixel centre: G = 1, alpha = opacity, the feature is
+    alpha * query(centre); out-of-range hit points count but add no feature."""
+    cam, means, scales, q, opac = _single_splat_scene(n=1, opacity=0.7, W=63, H=47)
+    W, H = cam.image_width, cam.image_height
+    from nest_splat.scene import build_homotrans_np
+    homo = build_homotrans_np(q, scales, means)
+    pre = oracle.preprocess(means, scales, q, opac, cam.world_view_transform, cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    L, F, T = 4, 2, 1 << 10
+    table = np.full((L * T, F), 0.25, np.float32)
+    g, offs = _grid(oracle, L, F, T, 8, 1.0, table, gridrange=(-1.0, 1.0))
+    r = oracle.render(pre, b, W, H, L * F, g, homotrans=homo, ap_level=np.full((1, 1), 24.0, np.float32))
+    cx, cy = (W - 1) // 2, (H - 1) // 2
+    alpha = np.float32(0.7)
+    assert r["others"][7, cy, cx] == 1 and r["others"][1, cy, cx] == pytest.approx(alpha, abs=1e-6)
+    np.testing.assert_allclose(r["color"][:, cy, cx], alpha * 0.25, rtol=1e-5)
+    np.testing.assert_allclose(r["others"][8:11, cy, cx], alpha * means[0], atol=1e-6)
+    # appearance level caps the queried levels: ap = 2 -> only 2 levels
+    r_ap = oracle.render(pre, b, W, H, L * F, g, homotrans=homo, ap_level=np.full((1, 1), 2.0, np.float32))
+    np.testing.assert_allclose(r_ap["color"][:2 * F, cy, cx], alpha * 0.25, rtol=1e-5)
+    assert not r_ap["color"][2 * F:, cy, cx].any()
+    # appearance colour at ap = 2: ((2-2)*0.5, 1, 0) * w
+    np.testing.assert_allclose(r_ap["others"][11:14, cy, cx], [0.0, alpha, 0.0], atol=1e-6)
+    # a grid range that excludes the splat: hit counted, zero features
+    g_far, _ = _grid(oracle, L, F, T, 8, 1.0, table, gridrange=(5.0, 6.0))
+    r_far = oracle.render(pre, b, W, H, L * F, g_far, homotrans=homo, ap_level=np.full((1, 1), 24.0, np.float32))
+    assert r_far["others"][7, cy, cx] == 1 and not r_far["color"].any()
+
+
+def test_render_pixel_outputs_consistent(oracle):
+    """Invariants of the compositing loop on a full scene: alpha in [0, 1),
+    1 - alpha = final T, expected depth within [0.2, far], hit count <= the
+    contributor count, and background pixels untouched."""
+    sc = scene("shell_small")
+    r = oracle.render_scene(sc, with_mlp=False)
+    o = r["others"]
+    assert np.all((o[1] >= 0) & (o[1] < 1))
+    np.testing.assert_array_equal(o[1], np.float32(1) - r["final_T"][0])
+    cov = o[1] > 0.5
+    dexp = o[0][cov] / o[1][cov]
+    assert np.all(dexp > 0.2) and np.all(dexp < 100)
+    assert np.all(o[7] <= r["n_contrib"][0])
+    assert np.all(o[7][o[1] == 0] == 0)
+
+
+# ----------------------------------------------------------------------- MLP
+
+def test_sh16_against_scipy(oracle):
+    """The degree-3 real SH basis with the Condon-Shortley phase, ordered
+    l = 0..3, m = -l..l (utils/sh_utils.py, HE:551-558): Y_lm = sqrt(2) Im Y_l^|m|
+    (m < 0), Y_l0, sqrt(2) Re Y_l^m (m > 0) from scipy's complex harmonics."""
+    from scipy.special import sph_harm_y
+    rng = np.random.default_rng(7)
+    for _ in range(50):
+        d = rng.standard_normal(3)
+        d /= np.linalg.norm(d)
+        theta, phi = np.arccos(d[2]), np.arctan2(d[1], d[0])
+        ref = []
+        for l in range(4):
+            for m in range(-l, l + 1):
+                y = sph_harm_y(l, abs(m), theta, phi)
+                ref.append(np.sqrt(2) * y.imag if m < 0 else (y.real if m == 0 else np.sqrt(2) * y.real))
+        u = ((d + 1) / 2).astype(np.float32)
+        np.testing.assert_allclose(oracle.sh16(u), ref, atol=2e-6)
+
+
+def test_mlp_closed_forms(oracle):
+    rng = np.random.default_rng(9)
+    C, N, npix = 16, 32, 200
+    feat = rng.uniform(-1, 1, (C, npix)).astype(np.float32)
+    dirs = rng.standard_normal((npix, 3)).astype(np.float32)
+    dirs /= np.linalg.norm(dirs, axis=1, keepdims=True)
+    W1 = np.zeros((N, C + 16), np.float32)
+    W2 = np.eye(N, dtype=np.float32)
+    W3 = np.zeros((3, N), np.float32)
+    for o in range(3):
+        W1[o, o] = 1.0
+        W3[o, o] = 1.0
+    out = oracle.mlp(feat, dirs, None, W1, W2, W3, "f32")
+    expect = 1.0 / (1.0 + np.exp(-np.maximum(feat[:3], 0)))
+    np.testing.assert_allclose(out, expect, rtol=1e-6)
+    # zero output layer -> sigmoid(0) = 0.5 exactly; mask and white background
+    alpha = rng.uniform(0, 1, npix).astype(np.float32)
+    alpha[::5] = 0
+    bg = np.ones(3, np.float32)
+    out0 = oracle.mlp(feat, dirs, alpha, W1, W2, np.zeros_like(W3), "f32", bg)
+    exp0 = np.where(alpha > 0, np.float32(0.5), np.float32(0)) + (1 - alpha) * 1.0
+    np.testing.assert_allclose(out0, np.broadcast_to(exp0, (3, npix)), rtol=1e-7)
+    # the SH inputs feed the first layer: weight on SH term 0 (constant C0)
+    W1s = np.zeros_like(W1)
+    W1s[0, C] = 1.0
+    outs = oracle.mlp(feat, dirs, None, W1s, W2, W3, "f32")
+    np.testing.assert_allclose(outs[0], 1 / (1 + np.exp(-0.28209479177387814)), rtol=1e-6)
+    # dtype emulation: bf16 rounds the inputs
+    outb = oracle.mlp(feat, dirs, None, W1, W2, W3, "bf16")
+    fb = oracle.round_bf16(feat[:3])
+    np.testing.assert_allclose(outb, 1.0 / (1.0 + np.exp(-np.maximum(fb, 0))), rtol=1e-6)
+
+
+# ----------------------------------------------------------------------- RVQ
+
+def test_rvq_decode_is_ordered_float32_sum(oracle):
+    rng = np.random.default_rng(11)
+    S, K, dim, P = 4, 64, 4, 500
+    cb = (rng.standard_normal((S, K, dim)) * 0.1).astype(np.float32)
+    idx = rng.integers(0, K, (P, S)).astype(np.uint16)
+    bias = np.array([1.0, 0.0, -0.5, 2.0], np.float32)
+    out = oracle.rvq_decode(cb, idx, bias)
+    acc = cb[0][idx[:, 0]]
+    for s in range(1, S):
+        acc = (acc + cb[s][idx[:, s]]).astype(np.float32)
+    np.testing.assert_array_equal(out, (bias[None, :] + acc).astype(np.float32))
+    # order matters in float32: the reversed sum differs somewhere
+    rev = cb[3][idx[:, 3]]
+    for s in (2, 1, 0):
+        rev = (rev + cb[s][idx[:, s]]).astype(np.float32)
+    assert not np.array_equal(acc, rev)
+    sc, rot, op = oracle.activate(out[:, :2], out, out[:, 0])
+    np.testing.assert_allclose(sc, np.exp(out[:, :2]), rtol=3e-7)
+    np.testing.assert_allclose(np.linalg.norm(rot, axis=1), 1.0, rtol=1e-6)
+    np.testing.assert_allclose(op, 1 / (1 + np.exp(-out[:, 0].astype(np.float64))), rtol=1e-6)
