@@ -1,0 +1,219 @@
+#!/usr/bin/env python3
+"""Headline benchmark: rendered Mpix/s of the forward path (preprocess ->
+binning -> tile render with in-loop hash lookup -> MLP decode) on the
+1M-splat, 1600x1064, 16-level hash-textured unbounded scene, with the render
+kernel's HBM roofline fraction and the CPU oracle timed on this host.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config cfg3]
+
+Prints one JSON line.  One process drives one GPU; --gpus above 1 exits with a
+message (frames shard by camera or by tile band).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "nest-splatting_amd")
+for _p in (PKG, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "rendered Mpix/s (raster+hash+MLP), 1M splats @1600x1064; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def render_algorithmic_bytes(NR: int, hits: int, HW: int, L: int, F: int, e: int, C: int) -> int:
+    """Logical bytes of one render launch: 104 B per staged tile/splat pair,
+    L*8*F*e B of hash gathers per accepted hit, (4C + 56) B of outputs per
+    pixel (colour map + 14 allmap channels)."""
+    return 104 * NR + L * 8 * F * e * hits + HW * (4 * C + 56)
+
+
+def cpu_baseline(scene, gpu_hits_total: int, row_stride: int, threads: int):
+    """Oracle (oracle/nest_oracle.c) on this host: full preprocess and
+    binning, render of every row_stride-th tile row with `threads` OpenMP
+    threads, MLP of the sampled pixels; scaled to one frame by the sample's
+    share of tile/splat pairs plus hits (render) and of pixels (MLP)."""
+    import numpy as np
+    from oracle import oracle as O
+
+    sp = scene.spec
+    cam = scene.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    t0 = time.perf_counter()
+    pre = O.preprocess(scene.means, scene.scales, scene.rotations, scene.opacity, cam.world_view_transform,
+                       cam.full_proj_transform, W, H)
+    t1 = time.perf_counter()
+    b = O.binning(pre, W, H)
+    t2 = time.perf_counter()
+    grid = O.make_grid(sp.L, sp.F, sp.S, sp.base_res, scene.offsets, scene.table, sp.gridrange, sp.contract)
+    phase = row_stride // 2
+    r = O.render(pre, b, W, H, sp.C, grid, homotrans=scene.homotrans, ap_level=scene.ap_level,
+                 row_stride=row_stride, row_phase=phase, threads=threads)
+    t3 = time.perf_counter()
+    gx, gy = (W + 15) // 16, (H + 15) // 16
+    rows = [ty for ty in range(gy) if ty % row_stride == phase]
+    pix = np.zeros((H, W), bool)
+    for ty in rows:
+        pix[ty * 16:(ty + 1) * 16] = True
+    tiles = np.array([ty * gx + tx for ty in rows for tx in range(gx)])
+    nr_sample = int((b["ranges"][tiles, 1].astype(np.int64) - b["ranges"][tiles, 0]).sum())
+    hits_sample = int(r["others"][7][pix].sum())
+    share = (nr_sample + hits_sample) / max(1, b["num_rendered"] + gpu_hits_total)
+    idx = np.nonzero(pix.reshape(-1))[0]
+    dirs = O.ray_dirs(cam)[idx]
+    feat = r["color"].reshape(sp.C, -1)[:, idx]
+    alpha = r["others"][1].reshape(-1)[idx]
+    t4 = time.perf_counter()
+    O.mlp(np.ascontiguousarray(feat), dirs, alpha, scene.W1, scene.W2, scene.W3, sp.mlp_dtype,
+          np.asarray(sp.bg, np.float32))
+    t5 = time.perf_counter()
+    pix_share = idx.size / (W * H)
+    frame_s = (t1 - t0) + (t2 - t1) + (t3 - t2) / share + (t5 - t4) / pix_share
+    return {
+        "value": W * H / frame_s / 1e6,
+        "unit": "Mpix/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle C port: full preprocess ({t1 - t0:.2f} s, 1 thread) and binning ({t2 - t1:.2f} s, "
+                   f"1 thread); render of every {row_stride}th tile row ({len(rows)} of {gy} rows, {t3 - t2:.2f} s, "
+                   f"{threads} OpenMP threads, scaled by its {share:.4f} share of pairs+hits); fp32-accumulated MLP "
+                   f"of those {idx.size} pixels ({t5 - t4:.2f} s, 1 thread, scaled by pixel share); "
+                   f"extrapolated frame {frame_s:.2f} s"),
+        "frame_s": frame_s,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="cfg3")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-row-stride", type=int, default=16)
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "render_traffic_cfg3.json"),
+                    help="JSON with counter-measured HBM bytes per render launch (from rocprofv3 --pmc)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this benchmark drives exactly one GPU per process; multi-GPU figures are not "
+                                   "produced (frames shard by camera or tile band across processes, see DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from nest_splat import _lib as L
+    from nest_splat import rasterizer as rz
+    from nest_splat.camera import view_ray_matrix
+    from nest_splat.mlp import NestMLP
+    from nest_splat.scene import get_spec, make_scene
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    L.lib()
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    spec = get_spec(args.config)
+    scene = make_scene(spec)
+    log(f"[bench] scene {spec.name}: {spec.P} splats, {spec.W}x{spec.H}, table {scene.table.nbytes / 2**20:.0f} MiB "
+        f"({time.perf_counter() - t0:.1f} s)")
+    cam = scene.cameras[0]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    means, opac, scales, rots = t(scene.means), t(scene.opacity), t(scene.scales), t(scene.rotations)
+    homo, ap_level, table = t(scene.homotrans), t(scene.ap_level), t(scene.table)
+    settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy, cam.world_view_transform,
+                                cam.full_proj_transform, cam.camera_center, if_contract=spec.contract)
+    grid = rz.HashGridDesc(spec.L, spec.F, spec.S, spec.base_res, table, scene.offsets,
+                           np.asarray(spec.gridrange, np.float32))
+    mlp = NestMLP(spec.C, spec.mlp_width, spec.mlp_dtype, scene.W1, scene.W2, scene.W3).to(dev)
+    M = view_ray_matrix(cam)
+    bg = torch.tensor(spec.bg, dtype=torch.float32) if sum(spec.bg) > 0 else None
+    HW = spec.W * spec.H
+
+    def step(tm=None):
+        res = rz.rasterize_forward(settings, grid, means, opac, scales, rots, homotrans=homo, ap_level=ap_level,
+                                   channels=spec.C, timing=tm if tm is not None else False)
+        rgb = mlp.decode_image(res.color, M, alpha=res.others[1], bg=bg)
+        return res, rgb
+
+    for i in range(args.warmup):
+        res, rgb = step()
+    torch.cuda.synchronize()
+    log(f"[bench] warmup done ({args.warmup} steps)")
+    tms = [L.new_timing(True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for k in range(args.steps):
+        res, rgb = step(tms[k])
+    torch.cuda.synchronize()
+    t_end = time.perf_counter()
+    stages = [L.timing_read(tm) for tm in tms]
+    for tm in tms:
+        L.timing_release(tm)
+    elapsed = t_end - t_start
+    ms_per_step = elapsed / args.steps * 1e3
+    mpix = HW * args.steps / elapsed / 1e6
+    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step, {mpix:.1f} Mpix/s")
+
+    hits_total = int(res.others[7].double().sum().item())
+    NR = res.num_rendered
+    render_ms = float(np.mean([s["render"] for s in stages]))
+    stage_ms = {k: float(np.mean([s[k] for s in stages])) for k in stages[0]}
+    e = scene.table.dtype.itemsize
+    alg = render_algorithmic_bytes(NR, hits_total, HW, spec.L, spec.F, e, spec.C)
+    achieved = alg / (render_ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(args.traffic):
+        try:
+            with open(args.traffic) as f:
+                traffic = json.load(f).get("render_bytes_per_launch")
+        except Exception:
+            traffic = None
+    out = {
+        "metric": METRIC,
+        "value": round(mpix, 3),
+        "unit": "Mpix/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded scene generator, random-init hash table and Xavier MLP weights)",
+        "config": {"workload": f"{spec.name}: {spec.P} 2D surfels, 70% in a unit ball and 30% out to r=20 "
+                               f"(contracted), {spec.W}x{spec.H}, hash grid L={spec.L} F={spec.F} "
+                               f"T=2^{spec.log2T} {spec.table_dtype}, MLP {spec.C + 16}-{spec.mlp_width}-"
+                               f"{spec.mlp_width}-3 {spec.mlp_dtype}",
+                   "splats": spec.P, "width": spec.W, "height": spec.H, "num_rendered": NR,
+                   "hits_per_pixel": round(hits_total / HW, 3)},
+        "frames_per_s": round(1e3 / ms_per_step, 3),
+        "stages_ms": {k: round(v, 4) for k, v in stage_ms.items()},
+        "roofline": {"bound": "hbm", "kernel": "render_kernel (tile compositing + hash gathers)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": alg, "render_ms": round(render_ms, 4)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        threads = len(os.sched_getaffinity(0))
+        log(f"[bench] cpu baseline on {threads} threads ...")
+        cb = cpu_baseline(scene, hits_total, args.cpu_row_stride, threads)
+        out["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cb.items() if k != "frame_s"}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -112,8 +112,11 @@ typedef struct nest_frame_outputs {
   int32_t *radii;
 } nest_frame_outputs;
 
-/* Optional per-stage device times in milliseconds, measured with HIP events on
- * the caller's stream (adds one synchronisation per stage when enabled). */
+/* Optional per-stage device times.  When enabled, the forward calls record a
+ * pair of HIP events around each stage on the caller's stream (no extra
+ * synchronisation); nest_timing_read() waits for the last recorded event and
+ * fills ms[].  The events are created on first use and owned by the struct
+ * until nest_timing_release(). */
 #define NEST_STAGE_PREPROCESS 0
 #define NEST_STAGE_SCAN 1
 #define NEST_STAGE_DUPLICATE 2
@@ -125,7 +128,11 @@ typedef struct nest_timing {
   uint32_t struct_size;
   int32_t enabled;
   float ms[NEST_STAGE_COUNT];
+  void *events[2 * NEST_STAGE_COUNT]; /* library-owned hipEvent_t handles */
+  uint32_t recorded;                  /* bit s set: stage s was recorded */
 } nest_timing;
+int nest_timing_read(nest_timing *timing);
+int nest_timing_release(nest_timing *timing);
 
 /* ---- library ---------------------------------------------------------- */
 

@@ -104,30 +104,34 @@ int build_levels(const int32_t* offsets, uint32_t L, float S, uint32_t H, bool a
   return NEST_OK;
 }
 
+// Records a start/stop event pair per stage into the caller's nest_timing;
+// nothing waits here, nest_timing_read() collects the times later.
 struct StageTimer {
   nest_timing* t;
   hipStream_t s;
-  hipEvent_t a = nullptr, b = nullptr;
-  StageTimer(nest_timing* t_, hipStream_t s_) : t(t_ && t_->enabled ? t_ : nullptr), s(s_) {
-    if (t) {
-      hipEventCreate(&a);
-      hipEventCreate(&b);
+  int stage = -1;
+  StageTimer(nest_timing* t_, hipStream_t s_) : t(t_ && t_->enabled ? t_ : nullptr), s(s_) {}
+  void begin(int st) {
+    if (!t || st < 0 || st >= NEST_STAGE_COUNT) return;
+    stage = st;
+    for (int k = 0; k < 2; k++) {
+      void*& ev = t->events[2 * st + k];
+      if (!ev) {
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess) {
+          stage = -1;
+          return;
+        }
+        ev = e;
+      }
     }
+    hipEventRecord(static_cast<hipEvent_t>(t->events[2 * st]), s);
   }
-  ~StageTimer() {
-    if (a) hipEventDestroy(a);
-    if (b) hipEventDestroy(b);
-  }
-  void begin() {
-    if (t) hipEventRecord(a, s);
-  }
-  void end(int stage) {
-    if (!t) return;
-    hipEventRecord(b, s);
-    hipEventSynchronize(b);
-    float ms = 0.f;
-    hipEventElapsedTime(&ms, a, b);
-    t->ms[stage] = ms;
+  void end() {
+    if (!t || stage < 0) return;
+    hipEventRecord(static_cast<hipEvent_t>(t->events[2 * stage + 1]), s);
+    t->recorded |= 1u << stage;
+    stage = -1;
   }
 };
 
@@ -261,14 +265,14 @@ int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp,
   p.records = reinterpret_cast<float*>(g + off[NEST_GEOM_RECORDS]);
 
   StageTimer tm(timing, s);
-  tm.begin();
+  tm.begin(NEST_STAGE_PREPROCESS);
   if ((rc = check_stage(launch_preprocess(p, s), "preprocess", rs->debug, s))) return rc;
-  tm.end(NEST_STAGE_PREPROCESS);
-  tm.begin();
+  tm.end();
+  tm.begin(NEST_STAGE_SCAN);
   uint32_t* offs = reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_OFFSETS]);
   void* scan_ws = g + off[NEST_GEOM_SCAN_TMP];
   if ((rc = check_stage(launch_scan_u32(p.tiles, offs, sp->P, scan_ws, s), "scan", rs->debug, s))) return rc;
-  tm.end(NEST_STAGE_SCAN);
+  tm.end();
   // The scan leaves the 64-bit grand total after the per-block partials.
   const int64_t nb = ((int64_t)sp->P + 4095) / 4096;
   uint64_t total = 0;
@@ -382,24 +386,24 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     vals_u = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_VALS_UNSORTED]);
     keys = reinterpret_cast<uint64_t*>(b + bo[NEST_BIN_KEYS]);
     vals = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_VALS]);
-    tm.begin();
+    tm.begin(NEST_STAGE_DUPLICATE);
     rc = check_stage(launch_duplicate(sp->P, nullptr, reinterpret_cast<const float*>(g + go[NEST_GEOM_XY]),
                                       reinterpret_cast<const float*>(g + go[NEST_GEOM_DEPTH]),
                                       reinterpret_cast<const int32_t*>(g + go[NEST_GEOM_RADII]),
                                       reinterpret_cast<const uint32_t*>(g + go[NEST_GEOM_OFFSETS]), gx, gy, keys_u, vals_u, s),
                      "duplicate", rs->debug, s);
     if (rc) return rc;
-    tm.end(NEST_STAGE_DUPLICATE);
-    tm.begin();
+    tm.end();
+    tm.begin(NEST_STAGE_SORT);
     const int bit = (int)higher_msb(ntiles);
     rc = check_stage(launch_sort_pairs(keys_u, vals_u, keys, vals, NR, 32 + bit, b + bo[NEST_BIN_SORT_TMP], s), "sort",
                      rs->debug, s);
     if (rc) return rc;
-    tm.end(NEST_STAGE_SORT);
+    tm.end();
   }
-  tm.begin();
+  tm.begin(NEST_STAGE_RANGES);
   if ((rc = check_stage(launch_tile_ranges(keys, NR, ranges, ntiles, s), "tile ranges", rs->debug, s))) return rc;
-  tm.end(NEST_STAGE_RANGES);
+  tm.end();
 
   rp.ranges = ranges;
   rp.point_list = vals;
@@ -409,9 +413,36 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   rp.out_others = out->out_others;
   rp.final_T = reinterpret_cast<float*>(im + io[NEST_IMG_FINAL_T]);
   rp.n_contrib = reinterpret_cast<uint32_t*>(im + io[NEST_IMG_N_CONTRIB]);
-  tm.begin();
+  tm.begin(NEST_STAGE_RENDER);
   if ((rc = check_stage(launch_render(rp, s), "render", rs->debug, s))) return rc;
-  tm.end(NEST_STAGE_RENDER);
+  tm.end();
+  return NEST_OK;
+}
+
+int nest_timing_read(nest_timing* t) {
+  if (!t || t->struct_size != sizeof(nest_timing)) return fail(NEST_ERR_INVALID_ARGUMENT, "nest_timing missing or struct_size mismatch");
+  for (int st = 0; st < NEST_STAGE_COUNT; st++) {
+    t->ms[st] = 0.0f;
+    if (!(t->recorded & (1u << st))) continue;
+    hipEvent_t a = static_cast<hipEvent_t>(t->events[2 * st]), b = static_cast<hipEvent_t>(t->events[2 * st + 1]);
+    hipError_t e = hipEventSynchronize(b);
+    if (e != hipSuccess) return hip_fail(e, "nest_timing_read");
+    float ms = 0.0f;
+    e = hipEventElapsedTime(&ms, a, b);
+    if (e != hipSuccess) return hip_fail(e, "nest_timing_read");
+    t->ms[st] = ms;
+  }
+  t->recorded = 0;
+  return NEST_OK;
+}
+
+int nest_timing_release(nest_timing* t) {
+  if (!t || t->struct_size != sizeof(nest_timing)) return fail(NEST_ERR_INVALID_ARGUMENT, "nest_timing missing or struct_size mismatch");
+  for (int i = 0; i < 2 * NEST_STAGE_COUNT; i++) {
+    if (t->events[i]) hipEventDestroy(static_cast<hipEvent_t>(t->events[i]));
+    t->events[i] = nullptr;
+  }
+  t->recorded = 0;
   return NEST_OK;
 }
 

@@ -64,7 +64,24 @@ class FrameOutputs(ct.Structure):
 
 
 class Timing(ct.Structure):
-    _fields_ = [("struct_size", ct.c_uint32), ("enabled", ct.c_int32), ("ms", ct.c_float * 6)]
+    _fields_ = [("struct_size", ct.c_uint32), ("enabled", ct.c_int32), ("ms", ct.c_float * 6),
+                ("events", ct.c_void_p * 12), ("recorded", ct.c_uint32)]
+
+
+def new_timing(enabled: bool = True) -> Timing:
+    t = Timing()
+    t.struct_size = ct.sizeof(Timing)
+    t.enabled = int(bool(enabled))
+    return t
+
+
+def timing_read(t: Timing) -> dict:
+    check(lib().nest_timing_read(ct.byref(t)), "nest_timing_read")
+    return {n: float(t.ms[i]) for i, n in enumerate(STAGES)}
+
+
+def timing_release(t: Timing) -> None:
+    check(lib().nest_timing_release(ct.byref(t)), "nest_timing_release")
 
 
 class Mlp(ct.Structure):
@@ -83,6 +100,8 @@ EXPORTS = {
     "nest_forward_render": (ct.c_int, [ct.POINTER(RasterSettings), ct.POINTER(HashGrid), ct.POINTER(Splats),
                                        ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_size_t,
                                        ct.c_int64, ct.POINTER(FrameOutputs), ct.POINTER(Timing), ct.c_void_p]),
+    "nest_timing_read": (ct.c_int, [ct.POINTER(Timing)]),
+    "nest_timing_release": (ct.c_int, [ct.POINTER(Timing)]),
     "nest_scan_workspace_size": (ct.c_size_t, [ct.c_int64]),
     "nest_inclusive_scan_u32": (ct.c_int, [ct.c_void_p, ct.c_void_p, ct.c_int64, ct.c_void_p, ct.c_size_t,
                                            ct.c_void_p]),

@@ -191,9 +191,8 @@ def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: t
     geom = torch.empty((gbytes,), dtype=torch.uint8, device=dev)
     _, ibytes = L.image_layout(W, H)
     image = torch.empty((ibytes,), dtype=torch.uint8, device=dev)
-    tm = L.Timing()
-    tm.struct_size = ct.sizeof(L.Timing)
-    tm.enabled = int(bool(timing))
+    own_timing = not isinstance(timing, L.Timing)
+    tm = L.new_timing(bool(timing)) if own_timing else timing
     stream = L.stream_ptr(dev)
     nr = ct.c_int64(0)
     lib = L.lib()
@@ -212,8 +211,9 @@ def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: t
                                     L.ptr(binning), bbytes, L.ptr(image), ibytes, NR, ct.byref(out), ct.byref(tm),
                                     stream), "nest_forward_render")
     res = ForwardResult(NR, color, others, radii, geom, binning, image)
-    if timing:
-        res.timing_ms = {n: float(tm.ms[i]) for i, n in enumerate(L.STAGES)}
+    if own_timing and timing:
+        res.timing_ms = L.timing_read(tm)
+        L.timing_release(tm)
     return res
 
 

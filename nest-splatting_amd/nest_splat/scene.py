@@ -72,9 +72,10 @@ SPECS = {
     "cfg2": SceneSpec("cfg2", 20262, 100_000, 800, 800, "shell", -4.5, 0.3, 1.0, 1.0,
                       16, 2, 19, 16, GROWTH_16, (-1.5, 1.5), False, "f32", 64, "f16",
                       bg=(1.0, 1.0, 1.0)),
-    # unbounded 1M-splat scene, the headline workload; opacity
-    # and scale tuned on the oracle for a mean of ~40 accepted hits per pixel
-    "cfg3": SceneSpec("cfg3", 20263, 1_000_000, 1600, 1064, "ball_unbounded", -4.5, 0.3, -2.6, 1.0,
+    # unbounded 1M-splat scene, the headline workload; scales and opacities
+    # as in cfg2, camera at distance 2.6: the oracle measures a mean of 41.6
+    # accepted hits per pixel (every pixel is covered)
+    "cfg3": SceneSpec("cfg3", 20263, 1_000_000, 1600, 1064, "ball_unbounded", -4.5, 0.3, 1.0, 1.0,
                       16, 4, 21, 16, GROWTH_16, (-1.0, 1.0), True, "f32", 64, "bf16",
                       cam_dist=2.6),
     # RVQ-compressed attributes
