@@ -103,6 +103,9 @@ def main():
     ap.add_argument("--cpu-row-stride", type=int, default=16)
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "render_traffic_cfg3.json"),
                     help="JSON with counter-measured HBM bytes per render launch (from rocprofv3 --pmc)")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="before the frames, copy this many MiB device-to-device (a plain copy kernel of known "
+                         "size whose FETCH_SIZE / WRITE_SIZE scale the render kernel's counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -147,6 +150,15 @@ def main():
         rgb = mlp.decode_image(res.color, M, alpha=res.others[1], bg=bg)
         return res, rgb
 
+    if args.copy_calibration_mb > 0:
+        n = args.copy_calibration_mb * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: 3 x {args.copy_calibration_mb} MiB device copies")
+        del src, dst
     for i in range(args.warmup):
         res, rgb = step()
     torch.cuda.synchronize()

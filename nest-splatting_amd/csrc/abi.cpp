@@ -354,6 +354,11 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     g.pos_offset = gr->align_corners ? 0.0f : 0.5f;
     g.half = gr->table_dtype == NEST_DTYPE_F16 ? 1u : 0u;
     g.table = gr->table;
+    const uint64_t tbytes = (uint64_t)gr->table_rows * gr->level_dim * (g.half ? 2u : 4u);
+    if (tbytes >= (1ull << 32))
+      return fail(NEST_ERR_UNSUPPORTED, "hash table of %llu bytes: at most 4 GiB (32-bit buffer offsets)",
+                  (unsigned long long)tbytes);
+    g.table_bytes = (uint32_t)tbytes;
   } else {
     if (sp->P > 0 && !sp->colors_precomp)
       return fail(NEST_ERR_INVALID_ARGUMENT, "levels == 0 selects the colour path, which needs colors_precomp");

@@ -97,7 +97,7 @@ __global__ void __launch_bounds__(256) grid_encode_kernel(const GridEncodeParams
           asm volatile("" : "+v"(prod));
           acc[ch] = round_half(acc[ch] + round_half(prod));
         } else {
-          acc[ch] += w * v[ch];
+          acc[ch] = fmaf(w, v[ch], acc[ch]);
         }
       }
     }

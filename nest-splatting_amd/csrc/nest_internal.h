@@ -64,6 +64,7 @@ struct GridParams {
   float vmid;
   float pos_offset;     // 0.5 or 0 (align_corners)
   uint32_t half;        // table entries are binary16
+  uint32_t table_bytes; // byte size of the table (< 4 GiB: 32-bit buffer offsets)
   const void* table;
   LevelTable lv;
 };

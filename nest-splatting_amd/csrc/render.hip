@@ -32,8 +32,12 @@ __device__ __forceinline__ uint32_t xcd_tile(uint32_t i, uint32_t n) {
 
 // NACC: accumulator channels held per lane.  HASH: hash path (NACC = NL*F) or
 // colour path (NACC >= C).
+// amdgpu_waves_per_eu(3): at C = 64 the accumulators and eight in-flight
+// corner loads need ~170 VGPRs; capping at 168 gives three waves per SIMD
+// without scratch spills (four would spill).
 template <int F, int NACC, bool kHash, bool kHalf>
-__global__ void __launch_bounds__(kRenderThreads) render_kernel(const RenderParams p) {
+__global__ void __launch_bounds__(kRenderThreads) __attribute__((amdgpu_waves_per_eu(3, 8)))
+render_kernel(const RenderParams p) {
   __shared__ float4 srec[kRecChunks][kRenderThreads];
 
   const uint32_t tile = xcd_tile(blockIdx.x, p.ntiles);
@@ -58,6 +62,7 @@ __global__ void __launch_bounds__(kRenderThreads) render_kernel(const RenderPara
 
   const GridParams& g = p.grid;
   const uint32_t L = g.L;
+  const __amdgpu_buffer_rsrc_t rsrc = table_rsrc(g.table, g.table_bytes);
 
   for (uint32_t start = range.x; start < range.y; start += kRenderThreads) {
     if (__syncthreads_count(done) == kRenderThreads) break;
@@ -124,7 +129,7 @@ __global__ void __launch_bounds__(kRenderThreads) render_kernel(const RenderPara
         const float* col = p.colors + (size_t)id * p.C;
 #pragma unroll
         for (int c = 0; c < NACC; c++)
-          if (c < p.C) acc[c] += col[c] * w;
+          if (c < p.C) acc[c] = fmaf(col[c], w, acc[c]);
       } else {
         const float4 q4 = srec[4][j], q5 = srec[5][j], q6 = srec[6][j];
         float xyz[3];
@@ -161,17 +166,16 @@ __global__ void __launch_bounds__(kRenderThreads) render_kernel(const RenderPara
             u[d] = (u[d] + 2.0f) * 0.25f;
           }
         }
+        // Levels at or past max_level contribute fmaf(0, w, acc) == acc (the
+        // accumulators never hold -0), so they are skipped.
         const uint32_t max_level = oob ? 0u : (ap < L ? ap : L);
 #pragma unroll
         for (int l = 0; l < NACC / F; l++) {
           if ((uint32_t)l < max_level) {
             float r[F];
-            level_interp<F, kHalf>(g.lv, l, g.table, g.pos_offset, g.interp, u, r);
+            level_interp_rsrc<F, kHalf>(rsrc, g.lv, l, g.pos_offset, g.interp, u, r);
 #pragma unroll
-            for (int f = 0; f < F; f++) acc[l * F + f] += r[f] * w;
-          } else {
-#pragma unroll
-            for (int f = 0; f < F; f++) acc[l * F + f] += 0.0f * w;
+            for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(r[f], w, acc[l * F + f]);
           }
         }
         float apc0, apc1;

@@ -20,7 +20,11 @@
  * exp/exp2f/rsqrtf), which cannot be reproduced on any other compiler.  The
  * oracle therefore fixes one IEEE-754 binary32 evaluation order:
  *   - every expression is evaluated left to right, exactly as written in the
- *     reference, with no fused multiply-add (built with -ffp-contract=off);
+ *     reference, with no implicit contraction (built with -ffp-contract=off);
+ *   - the feature accumulations are explicit fused multiply-adds (fmaf), as
+ *     nvcc contracts them in the reference: the per-corner sum
+ *     results += w * table (hashgrid.h:177, gridencoder.cu:185) and the
+ *     per-hit C += feat * w (forward.cu:1916, :1095);
  *   - exp() is or_expf() below (Cephes-style range reduction + minimax
  *     polynomial, S. L. Moshier, "Methods and Programs for Mathematical
  *     Functions", 1989), not the platform libm;
@@ -464,7 +468,7 @@ static void grid_level(const or_grid *G, int l, const float u[3], float *out)
             else { w *= pos[d]; q[d] = g[d] + 1u; }
         }
         uint32_t idx = grid_index(G->align_corners, hsize, res, q);
-        for (int c = 0; c < G->F; c++) acc[c] += w * table_at(G, base + (size_t)idx * G->F + c);
+        for (int c = 0; c < G->F; c++) acc[c] = fmaf(w, table_at(G, base + (size_t)idx * G->F + c), acc[c]);
     }
     for (int c = 0; c < G->F; c++) out[c] = acc[c];
 }
@@ -608,7 +612,7 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
 
         if (A->level == 0) {
             const float *col = A->colors + (size_t)id * C;
-            for (int c = 0; c < C; c++) Cacc[c] += col[c] * w;
+            for (int c = 0; c < C; c++) Cacc[c] = fmaf(col[c], w, Cacc[c]);
         } else {
             const float *Hm = A->homotrans + 16 * (size_t)id;
             float xyz[3];
@@ -622,7 +626,7 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
             pos_x += w * xyz[0]; pos_y += w * xyz[1]; pos_z += w * xyz[2];
             uint32_t ap = f2u_sat(floorf(A->ap_level[id]));
             or_query_feature(&A->grid, xyz, ap, C, feat_scratch);
-            for (int c = 0; c < C; c++) Cacc[c] += feat_scratch[c] * w;
+            for (int c = 0; c < C; c++) Cacc[c] = fmaf(feat_scratch[c], w, Cacc[c]);
             float apc0, apc1;
             if (ap <= 4u) { apc0 = (float)((double)(uint32_t)(ap - 2u) * 0.5); apc1 = 1.0f; }
             else { apc0 = 1.0f; apc1 = (float)(1.0 - (double)(uint32_t)(ap - 4u) * 0.5); }
