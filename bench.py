@@ -93,7 +93,54 @@ def cpu_baseline(scene, gpu_hits_total: int, row_stride: int, threads: int):
     }
 
 
+def summarize_pmc(fetch_dir: str, write_dir: str, out_path: str) -> dict:
+    """Reduce two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE, both with
+    --copy-calibration-mb) to HBM bytes per render launch.  Each counter is
+    scaled by bytes-moved / counter-reading of the largest plain copy kernel
+    (__amd_rocclr_copyBuffer) in the same run."""
+    import csv
+    import glob
+
+    def rows(d):
+        out = []
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            out += list(csv.DictReader(open(f)))
+        return out
+
+    res = {}
+    for tag, d, counter in (("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")):
+        rs = [r for r in rows(d) if r["Counter_Name"] == counter]
+        copies = [float(r["Counter_Value"]) for r in rs if "copyBuffer" in r["Kernel_Name"]]
+        render = [float(r["Counter_Value"]) for r in rs if "render_kernel" in r["Kernel_Name"]]
+        if not copies or not render:
+            raise SystemExit(f"no copy/render rows for {counter} under {d}")
+        copy_kib = max(copies)
+        res[f"{tag}_copy_counter_kib"] = copy_kib
+        res[f"{tag}_render_counter_kib"] = sum(render) / len(render)
+        res[f"{tag}_launches"] = len(render)
+    return res
+
+
+def finish_traffic(res: dict, copy_mib: int, out_path: str) -> dict:
+    moved_kib = copy_mib * 1024.0
+    res["copy_mib"] = copy_mib
+    res["fetch_scale"] = moved_kib / res["fetch_copy_counter_kib"]
+    res["write_scale"] = moved_kib / res["write_copy_counter_kib"]
+    res["render_fetch_bytes"] = res["fetch_render_counter_kib"] * 1024 * res["fetch_scale"]
+    res["render_write_bytes"] = res["write_render_counter_kib"] * 1024 * res["write_scale"]
+    res["render_bytes_per_launch"] = int(res["render_fetch_bytes"] + res["render_write_bytes"])
+    with open(out_path, "w") as f:
+        json.dump(res, f, indent=1)
+    return res
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--pmc-summary":
+        # python bench.py --pmc-summary FETCH_DIR WRITE_DIR COPY_MIB OUT.json
+        fetch_dir, write_dir, copy_mib, out_path = sys.argv[2:6]
+        r = finish_traffic(summarize_pmc(fetch_dir, write_dir, out_path), int(copy_mib), out_path)
+        print(json.dumps(r))
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
