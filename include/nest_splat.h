@@ -152,7 +152,9 @@ const char *nest_last_error(void);
                                       11 opacity, 12-14 view normal,
                                       15 floor(ap_level) as uint32 bits,
                                       16-18 / 19-21 / 22-24 homotrans
-                                      columns 0 / 1 / 3, 25 depth      */
+                                      columns 0 / 1 / 3, 25 rho cut,
+                                      27 depth, 28-31 acceptance bbox
+                                      (x0, x1, y0, y1)                 */
 #define NEST_GEOM_RADII 5          /* i32 [P]                         */
 #define NEST_GEOM_SCAN_TMP 6       /* scan scratch                    */
 #define NEST_GEOM_FIELDS 7

@@ -359,6 +359,7 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
       return fail(NEST_ERR_UNSUPPORTED, "hash table of %llu bytes: at most 4 GiB (32-bit buffer offsets)",
                   (unsigned long long)tbytes);
     g.table_bytes = (uint32_t)tbytes;
+    g.table_rows = (uint32_t)gr->table_rows;
   } else {
     if (sp->P > 0 && !sp->colors_precomp)
       return fail(NEST_ERR_INVALID_ARGUMENT, "levels == 0 selects the colour path, which needs colors_precomp");

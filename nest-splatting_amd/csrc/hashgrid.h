@@ -188,6 +188,145 @@ __device__ __forceinline__ void level_interp_rsrc(__amdgpu_buffer_rsrc_t rsrc, c
   }
 }
 
+// Struct-buffer view of the table: one record per entry (stride = entry
+// bytes in descriptor dword1[29:16]), num_records = rows, so the buffer unit
+// scales the entry index (idxen addressing) and range-checks it.  clang has
+// no struct-buffer load builtins, so the LLVM intrinsics are bound by name.
+typedef int nest_i32x4 __attribute__((ext_vector_type(4)));
+typedef int nest_i32x2 __attribute__((ext_vector_type(2)));
+typedef float nest_f32x4 __attribute__((ext_vector_type(4)));
+typedef float nest_f32x2 __attribute__((ext_vector_type(2)));
+__device__ nest_f32x4 nest_struct_load_v4f32(nest_i32x4 rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.buffer.load.v4f32");
+__device__ nest_f32x2 nest_struct_load_v2f32(nest_i32x4 rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.buffer.load.v2f32");
+__device__ float nest_struct_load_f32(nest_i32x4 rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.buffer.load.f32");
+__device__ nest_i32x4 nest_struct_load_v4i32(nest_i32x4 rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.buffer.load.v4i32");
+__device__ nest_i32x2 nest_struct_load_v2i32(nest_i32x4 rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.buffer.load.v2i32");
+__device__ int nest_struct_load_i32(nest_i32x4 rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.buffer.load.i32");
+__device__ short nest_struct_load_i16(nest_i32x4 rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.buffer.load.i16");
+
+template <int F, bool kHalf>
+__device__ __forceinline__ nest_i32x4 table_rsrc_rows(const void* table, uint32_t rows) {
+  constexpr int kStride = F * (kHalf ? 2 : 4);
+  const uint64_t a = reinterpret_cast<uint64_t>(table);
+  nest_i32x4 r;
+  r.x = (int)(uint32_t)(a & 0xffffffffu);
+  r.y = (int)((uint32_t)((a >> 32) & 0xffffu) | ((uint32_t)kStride << 16));
+  r.z = (int)rows;
+  r.w = 0x00020000;
+  return r;
+}
+
+__device__ __forceinline__ float lo_half(uint32_t x) { return __half2float(__ushort_as_half((unsigned short)(x & 0xffffu))); }
+__device__ __forceinline__ float hi_half(uint32_t x) { return __half2float(__ushort_as_half((unsigned short)(x >> 16))); }
+
+template <int F, bool kHalf>
+__device__ __forceinline__ void struct_entry(nest_i32x4 r, uint32_t index, uint32_t soff, float v[F]) {
+  const int vi = (int)index, so = (int)soff;
+  if constexpr (!kHalf) {
+    if constexpr (F == 4) {
+      const nest_f32x4 a = nest_struct_load_v4f32(r, vi, 0, so, 0);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    } else if constexpr (F == 2) {
+      const nest_f32x2 a = nest_struct_load_v2f32(r, vi, 0, so, 0);
+      v[0] = a.x; v[1] = a.y;
+    } else if constexpr (F == 1) {
+      v[0] = nest_struct_load_f32(r, vi, 0, so, 0);
+    } else {
+#pragma unroll
+      for (int q = 0; q < F / 4; q++) {
+        const nest_f32x4 a = nest_struct_load_v4f32(r, vi, 16 * q, so, 0);
+        v[4 * q + 0] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w;
+      }
+    }
+  } else {
+    if constexpr (F == 4) {
+      const nest_i32x2 a = nest_struct_load_v2i32(r, vi, 0, so, 0);
+      v[0] = lo_half((uint32_t)a.x); v[1] = hi_half((uint32_t)a.x);
+      v[2] = lo_half((uint32_t)a.y); v[3] = hi_half((uint32_t)a.y);
+    } else if constexpr (F == 2) {
+      const uint32_t a = (uint32_t)nest_struct_load_i32(r, vi, 0, so, 0);
+      v[0] = lo_half(a); v[1] = hi_half(a);
+    } else if constexpr (F == 8) {
+      const nest_i32x4 a = nest_struct_load_v4i32(r, vi, 0, so, 0);
+      const uint32_t w[4] = {(uint32_t)a.x, (uint32_t)a.y, (uint32_t)a.z, (uint32_t)a.w};
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        v[2 * q] = lo_half(w[q]);
+        v[2 * q + 1] = hi_half(w[q]);
+      }
+    } else {
+      v[0] = lo_half((uint32_t)(uint16_t)nest_struct_load_i16(r, vi, 0, so, 0));
+    }
+  }
+}
+
+// Level l of the hash grid at u in [0,1]^3 through a struct-buffer view:
+// same corner order, weights, index and fused accumulation as
+// level_interp_rsrc.  The cell fraction pos - floor(pos) is computed with
+// v_fract (exact for the non-negative pos here, equal to the reference's
+// pos - (float)(uint)floor(pos) below 2^24), and the entry index goes to the
+// buffer unit unscaled.
+template <int F, bool kHalf>
+__device__ __forceinline__ void level_interp_struct(nest_i32x4 rsrc, const LevelTable& lv, int l,
+                                                    float pos_offset, uint32_t interp, const float u[3], float out[F]) {
+  const float scale = lv.scale[l];
+  const uint32_t res1 = lv.res1[l];
+  const uint32_t hsize = lv.hsize[l];
+  const uint32_t flags = lv.flags[l];
+  const uint32_t soff = lv.base[l] * (uint32_t)(F * (kHalf ? 2 : 4));
+  float pos[3];
+  uint32_t g[3];
+#pragma unroll
+  for (int d = 0; d < 3; d++) {
+    const float x = u[d] * scale + pos_offset;
+    g[d] = f2u_sat(floorf(x));
+    pos[d] = (x >= 0.0f && x < 16777216.0f) ? __builtin_amdgcn_fractf(x) : x - (float)g[d];
+    if (interp == 1) pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
+  }
+  const float wx[2] = {1 - pos[0], pos[0]}, wy[2] = {1 - pos[1], pos[1]}, wz[2] = {1 - pos[2], pos[2]};
+  uint32_t idx[8];
+  if (flags & kLvHashed) {
+    const uint32_t a[2] = {g[0], g[0] + 1u};
+    const uint32_t b0 = g[1] * 2654435761u, c0 = g[2] * 805459861u;
+    const uint32_t b[2] = {b0, b0 + 2654435761u}, c[2] = {c0, c0 + 805459861u};
+    const uint32_t ab[4] = {a[0] ^ b[0], a[1] ^ b[0], a[0] ^ b[1], a[1] ^ b[1]};
+#pragma unroll
+    for (int k = 0; k < 8; k++) idx[k] = ab[k & 3] ^ c[k >> 2];
+  } else {
+    const uint32_t r2 = res1 * res1;
+    const uint32_t base = g[0] + g[1] * res1 + g[2] * r2;
+#pragma unroll
+    for (int k = 0; k < 8; k++) idx[k] = base + ((k & 1) ? 1u : 0u) + ((k & 2) ? res1 : 0u) + ((k & 4) ? r2 : 0u);
+  }
+  if (!(flags & kLvNoMod)) {
+    if (flags & kLvPow2) {
+#pragma unroll
+      for (int k = 0; k < 8; k++) idx[k] &= hsize - 1u;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; k++) idx[k] %= hsize;
+    }
+  }
+  float vals[8][F];
+#pragma unroll
+  for (int k = 0; k < 8; k++) struct_entry<F, kHalf>(rsrc, idx[k], soff, vals[k]);
+#pragma unroll
+  for (int f = 0; f < F; f++) out[f] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const float w = (1.0f * wx[k & 1]) * wy[(k >> 1) & 1] * wz[k >> 2];
+#pragma unroll
+    for (int f = 0; f < F; f++) out[f] = fmaf(w, vals[k][f], out[f]);
+  }
+}
+
 // Trilinear (interp 0) or smoothstep (interp 1) interpolation of level l at
 // u in [0,1]^3.  out[f] = sum over corners 0..7 of w_corner * table, summed
 // in corner order from +0 with fused multiply-adds.

@@ -16,10 +16,12 @@ constexpr int kRecordFloats = 32;       // packed per-splat render record, 128 B
 //   0..2 Tu   3..5 Tv   6..8 Tw   9..10 xy   11 opacity
 //  12..14 normal   15 appearance level (uint32 bits, floor(ap_level))
 //  16..18 SuTu (homotrans col 0)   19..21 SvTv (col 1)   22..24 pk (col 3)
-//  25 depth   26..31 unused
+//  25 rho cut (alpha < 1/255 beyond it)   26 splat id (set when staged)
+//  27 depth   28..31 acceptance bbox x0, x1, y0, y1 (pixels)
 enum RecordField {
   kRecTu = 0, kRecTv = 3, kRecTw = 6, kRecXY = 9, kRecOpacity = 11,
-  kRecNormal = 12, kRecAp = 15, kRecSu = 16, kRecSv = 19, kRecPk = 22, kRecDepth = 25
+  kRecNormal = 12, kRecAp = 15, kRecSu = 16, kRecSv = 19, kRecPk = 22, kRecCut = 25, kRecId = 26,
+  kRecDepth = 27, kRecBBox = 28
 };
 
 struct PreprocessParams {
@@ -65,6 +67,7 @@ struct GridParams {
   float pos_offset;     // 0.5 or 0 (align_corners)
   uint32_t half;        // table entries are binary16
   uint32_t table_bytes; // byte size of the table (< 4 GiB: 32-bit buffer offsets)
+  uint32_t table_rows;  // entries of the table (records of the struct-buffer view)
   const void* table;
   LevelTable lv;
 };

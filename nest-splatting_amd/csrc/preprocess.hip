@@ -116,6 +116,43 @@ __global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams 
     sv0 = r0.y; sv1 = r1.y; sv2 = r2.y;
     pk0 = r0.w; pk1 = r1.w; pk2 = r2.w;
   }
+  // Rejection bounds for the render loop.  A pair is rejected by the alpha
+  // test (alpha < 1/255) whenever rho = min(rho3d, rho2d) > 2 ln(255 o); the
+  // cut below adds a relative 1e-6 for the expf/rounding error and 1e-4
+  // absolute, so any pair the render skips with it is one the exact test
+  // rejects.  The acceptance region {rho3d <= cut} U {rho2d <= cut} is
+  // bounded by the bbox of the projected disk |s|^2 <= cut (the conic bbox of
+  // CR/forward.cu:294-320 at cutoff^2 = cut, valid when the whole disk lies in
+  // front of the camera: cut*(Tw0^2+Tw1^2) < Tw2^2) and the disk of radius
+  // sqrt(cut/2) around xy, widened by one pixel.
+  float cut = -1.0f;
+  float bx0 = 1.0f, bx1 = -1.0f, by0 = 1.0f, by1 = -1.0f;  // empty: never accepted
+  if (opacity > 0.0f) {
+    const double c = 2.0 * log(255.0 * (double)opacity * (1.0 + 1e-6)) + 1e-4;
+    if (c >= 0.0) {
+      cut = (float)c;
+      const double rd = sqrt(c * 0.5) + 1.0;
+      bx0 = (float)(pimx - rd); bx1 = (float)(pimx + rd);
+      by0 = (float)(pimy - rd); by1 = (float)(pimy + rd);
+      const double w0 = Tw[0], w1 = Tw[1], w2 = Tw[2];
+      const double dd = c * (w0 * w0 + w1 * w1) - w2 * w2;
+      if (dd < 0.0 && w2 > 0.0) {
+        const double f0 = c / dd, f2 = -1.0 / dd;
+        const double ex_c = f0 * (Tu[0] * w0) + f0 * (Tu[1] * w1) + f2 * (Tu[2] * w2);
+        const double ey_c = f0 * (Tv[0] * w0) + f0 * (Tv[1] * w1) + f2 * (Tv[2] * w2);
+        const double hx2 = ex_c * ex_c - (f0 * ((double)Tu[0] * Tu[0]) + f0 * ((double)Tu[1] * Tu[1]) + f2 * ((double)Tu[2] * Tu[2]));
+        const double hy2 = ey_c * ey_c - (f0 * ((double)Tv[0] * Tv[0]) + f0 * ((double)Tv[1] * Tv[1]) + f2 * ((double)Tv[2] * Tv[2]));
+        const double hx = sqrt(hx2 > 0.0 ? hx2 : 0.0) + 1.0, hy = sqrt(hy2 > 0.0 ? hy2 : 0.0) + 1.0;
+        bx0 = (float)fmin((double)bx0, ex_c - hx); bx1 = (float)fmax((double)bx1, ex_c + hx);
+        by0 = (float)fmin((double)by0, ey_c - hy); by1 = (float)fmax((double)by1, ey_c + hy);
+      } else {
+        bx0 = -3.0e38f; bx1 = 3.0e38f; by0 = -3.0e38f; by1 = 3.0e38f;  // unbounded image: never cull
+      }
+    }
+  } else if (!(opacity <= 0.0f)) {  // NaN opacity: no bound, always take the exact path
+    cut = __int_as_float(0x7fc00000);
+    bx0 = -3.0e38f; bx1 = 3.0e38f; by0 = -3.0e38f; by1 = 3.0e38f;
+  }
   float4* rec = reinterpret_cast<float4*>(p.records) + 8 * (size_t)i;
   rec[0] = make_float4(Tu[0], Tu[1], Tu[2], Tv[0]);
   rec[1] = make_float4(Tv[1], Tv[2], Tw[0], Tw[1]);
@@ -123,8 +160,8 @@ __global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams 
   rec[3] = make_float4(nx, ny, nz, __uint_as_float(ap));
   rec[4] = make_float4(su0, su1, su2, sv0);
   rec[5] = make_float4(sv1, sv2, pk0, pk1);
-  rec[6] = make_float4(pk2, vz, 0.f, 0.f);
-  rec[7] = make_float4(0.f, 0.f, 0.f, 0.f);
+  rec[6] = make_float4(pk2, cut, 0.f, vz);
+  rec[7] = make_float4(bx0, bx1, by0, by1);
 }
 
 hipError_t launch_preprocess(const PreprocessParams& p, hipStream_t s) {

@@ -1,4 +1,4 @@
-// Per-tile compositing of 2D surfels with an in-loop hash-grid lookup at every
+// Per-tile compositing of 2D surfels with a hash-grid lookup at every
 // accepted ray/splat hit.
 //
 // Semantics: renderCUDAsurfelForward<C, mode 0> of
@@ -8,11 +8,21 @@
 // :2008-2048), and query_feature (hashgrid.h:53-212).
 //
 // Layout: one 256-thread workgroup per 16x16 tile, one lane per pixel (four
-// 64-lane waves of 16x4 pixels).  The tile's sorted splats are staged in LDS in
-// batches of 256 packed records (7 x 16 B per splat, structure-of-arrays so a
-// wave reads a record with broadcast ds_read_b128).  Workgroup ids are mapped
-// to tiles so that each XCD renders one contiguous band of tiles, keeping the
-// hash-table and record lines of neighbouring tiles in the same L2.
+// 64-lane waves of 16x4 pixels).  The tile's sorted splats are staged in LDS
+// in batches of 256 packed 128-byte records (structure-of-arrays float4
+// chunks, so a wave reads a record with broadcast ds_read_b128).  Workgroup
+// ids map to tiles so that each XCD renders one contiguous band of tiles.
+//
+// Work split inside a wave:
+//  - compositing runs splat by splat for all 64 pixels: a whole-wave skip when
+//    the wave's pixel block is outside the splat's acceptance bbox, a per-lane
+//    rcp-based early reject, then the exact test;
+//  - an accepted hit updates the depth/normal/distortion state at once and
+//    enqueues (grid coordinate, weight, level count) in a per-lane LDS queue;
+//  - when any lane's queue is full, the wave drains every lane's queue in
+//    order: round r looks up every lane's r-th pending hit.  The gathers thus
+//    run with most lanes active instead of only the lanes that accepted one
+//    splat, and each pixel still accumulates its hits in front-to-back order.
 #include "hashgrid.h"
 #include "nest_internal.h"
 #include "nest_math.h"
@@ -20,7 +30,8 @@
 namespace nest {
 
 constexpr int kRenderThreads = 256;
-constexpr int kRecChunks = 7;  // float4 chunks of the record used by the render
+constexpr int kRecChunks = 8;  // float4 chunks of the record staged per splat
+constexpr int kQueue = 4;      // pending hash lookups per pixel
 
 // Workgroup i runs on XCD i % 8; give XCD x a contiguous range of tiles.
 __device__ __forceinline__ uint32_t xcd_tile(uint32_t i, uint32_t n) {
@@ -30,15 +41,45 @@ __device__ __forceinline__ uint32_t xcd_tile(uint32_t i, uint32_t n) {
   return start + k;
 }
 
-// NACC: accumulator channels held per lane.  HASH: hash path (NACC = NL*F) or
-// colour path (NACC >= C).
+// Hash lookups of `rounds` queued hits per lane (lanes with fewer pending
+// hits idle in the later rounds), accumulated into acc in queue order.
+template <int F, int NACC, bool kHalf>
+__device__ __forceinline__ void drain_queue(const GridParams& g, nest_i32x4 rsrc, float4 (*hq)[kRenderThreads],
+                                            uint8_t (*hl)[kRenderThreads], int qn, int rounds, float* acc) {
+  for (int r = 0; r < rounds; r++) {
+    if (r < qn) {
+      const float4 e = hq[r][threadIdx.x];
+      const uint32_t maxl = hl[r][threadIdx.x];
+      const float u[3] = {e.x, e.y, e.z};
+#pragma unroll
+      for (int l = 0; l < NACC / F; l++) {
+        if ((uint32_t)l < maxl) {
+          float v[F];
+          level_interp_struct<F, kHalf>(rsrc, g.lv, l, g.pos_offset, g.interp, u, v);
+#pragma unroll
+          for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(v[f], e.w, acc[l * F + f]);
+        }
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ int wave_max_small(int v) {
+  int m = 0;
+#pragma unroll
+  for (int r = 1; r <= kQueue; r++)
+    if (__ballot(v >= r)) m = r;
+  return m;
+}
+
 // amdgpu_waves_per_eu(3): at C = 64 the accumulators and eight in-flight
-// corner loads need ~170 VGPRs; capping at 168 gives three waves per SIMD
-// without scratch spills (four would spill).
+// corner loads need ~170 VGPRs; capping at 168 gives three waves per SIMD.
 template <int F, int NACC, bool kHash, bool kHalf>
 __global__ void __launch_bounds__(kRenderThreads) __attribute__((amdgpu_waves_per_eu(3, 8)))
 render_kernel(const RenderParams p) {
   __shared__ float4 srec[kRecChunks][kRenderThreads];
+  __shared__ float4 hq[kHash ? kQueue : 1][kRenderThreads];
+  __shared__ uint8_t hl[kHash ? kQueue : 1][kRenderThreads];
 
   const uint32_t tile = xcd_tile(blockIdx.x, p.ntiles);
   const uint32_t tx = tile % p.gx, ty = tile / p.gx;
@@ -47,6 +88,9 @@ render_kernel(const RenderParams p) {
   const bool inside = px < (uint32_t)p.W && py < (uint32_t)p.H;
   const float pxf = (float)px, pyf = (float)py;
   bool done = !inside;
+  // pixel block of this wave: 16 columns x 4 rows
+  const float wx0 = (float)(tx * kTile), wx1 = wx0 + 15.0f;
+  const float wy0 = (float)(ty * kTile + 4u * (threadIdx.x >> 6)), wy1 = wy0 + 3.0f;
 
   const uint2 range = reinterpret_cast<const uint2*>(p.ranges)[tile];
 
@@ -55,144 +99,182 @@ render_kernel(const RenderParams p) {
   float acc[NACC];
 #pragma unroll
   for (int c = 0; c < NACC; c++) acc[c] = 0.0f;
-  float N0 = 0.f, N1 = 0.f, N2 = 0.f, vis0 = 0.f, vis1 = 0.f, vis2 = 0.f;
+  float N0 = 0.f, N1 = 0.f, N2 = 0.f, vis0 = 0.f, vis1 = 0.f;
   float D = 0.f, M1 = 0.f, M2 = 0.f, distortion = 0.f, median_depth = 0.f, median_contributor = -1.0f;
   float pos_x = 0.f, pos_y = 0.f, pos_z = 0.f;
   const float mfac = 100.0f / (100.0f - 0.2f);
 
   const GridParams& g = p.grid;
   const uint32_t L = g.L;
-  const __amdgpu_buffer_rsrc_t rsrc = table_rsrc(g.table, g.table_bytes);
+  nest_i32x4 rsrc{};
+  if constexpr (kHash) rsrc = table_rsrc_rows<F, kHalf>(g.table, g.table_rows);
+  int qn = 0;
 
-  for (uint32_t start = range.x; start < range.y; start += kRenderThreads) {
-    if (__syncthreads_count(done) == kRenderThreads) break;
-    const uint32_t e = start + threadIdx.x;
-    if (e < range.y) {
-      const uint32_t id = p.point_list[e];
-      const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id;
+  // Batches of 256 splats.  The splat index j is uniform across the wave;
+  // lanes that are done skip the body, as the reference's per-lane loop
+  // stops.  The wave pauses at a splat after which some lane's queue is full
+  // and drains, and the last pass (no splats left, or every pixel of the tile
+  // done) drains what remains, so the drain has a single call site.
+  uint32_t start = range.x;
+  for (;;) {
+    const bool all_done = __syncthreads_count(done) == kRenderThreads;
+    const bool last = start >= range.y || all_done;
+    uint32_t n = 0;
+    if (!last) {
+      const uint32_t e = start + threadIdx.x;
+      if (e < range.y) {
+        const uint32_t id = p.point_list[e];
+        const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id;
 #pragma unroll
-      for (int c = 0; c < kRecChunks; c++) srec[c][threadIdx.x] = rec[c];
-      srec[6][threadIdx.x].z = __uint_as_float(id);
+        for (int c = 0; c < kRecChunks; c++) srec[c][threadIdx.x] = rec[c];
+        srec[6][threadIdx.x].z = __uint_as_float(id);
+      }
+      __syncthreads();
+      n = min((uint32_t)kRenderThreads, range.y - start);
     }
-    __syncthreads();
-    const uint32_t n = min((uint32_t)kRenderThreads, range.y - start);
-    for (uint32_t j = 0; !done && j < n; j++) {
+    uint32_t j = 0;
+    for (;;) {
+    while (j < n) {
+      if (!done) {
       contributor++;
-      const float4 q0 = srec[0][j], q1 = srec[1][j], q2 = srec[2][j];
-      const float Tu0 = q0.x, Tu1 = q0.y, Tu2 = q0.z, Tv0 = q0.w;
-      const float Tv1 = q1.x, Tv2 = q1.y, Tw0 = q1.z, Tw1 = q1.w;
-      const float Tw2 = q2.x;
-      const float k0 = pxf * Tw0 - Tu0, k1 = pxf * Tw1 - Tu1, k2 = pxf * Tw2 - Tu2;
-      const float l0 = pyf * Tw0 - Tv0, l1 = pyf * Tw1 - Tv1, l2 = pyf * Tw2 - Tv2;
-      const float p0 = k1 * l2 - k2 * l1, p1 = k2 * l0 - k0 * l2, p2 = k0 * l1 - k1 * l0;
-      if (p2 == 0.0f) continue;
-      const float sx = p0 / p2, sy = p1 / p2;
-      const float rho3d = sx * sx + sy * sy;
-      const float dx = q2.y - pxf, dy = q2.z - pyf;
-      const float rho2d = 2.0f * (dx * dx + dy * dy);
-      const float rho = fminf(rho3d, rho2d);
-      const bool use3d = rho3d <= rho2d;
-      const float depth = use3d ? (sx * Tw0 + sy * Tw1) + Tw2 : Tw2;
-      if (depth < 0.2f) continue;
-      const float power = -0.5f * rho;
-      if (power > 0.0f) continue;
-      float G = expf_ref(power);
-      if (p.beta > 0.0f) G = (float)((1.0 + (double)p.beta) * (double)G / (1.0 + (double)p.beta * (double)G));
-      const float alpha = fminf(0.99f, q2.w * G);
-      if (alpha < 1.0f / 255.0f) continue;
-      const float test_T = T * (1 - alpha);
-      if (test_T < 0.0001f) {
-        done = true;
-        continue;
-      }
-      const float w = alpha * T;
-      render_number++;
-      if (p.max_intersections > 0 && render_number >= p.max_intersections) done = true;
-
-      const float4 q3 = srec[3][j];
-      const float Aa = 1 - T;
-      const float m = mfac * (1 - 0.2f / depth);
-      distortion += (m * m * Aa + M2 - 2 * m * M1) * w;
-      D += depth * w;
-      M1 += m * w;
-      M2 += m * m * w;
-      if (T > 0.5f) {
-        median_depth = depth;
-        median_contributor = (float)contributor;
-      }
-      N0 += q3.x * w;
-      N1 += q3.y * w;
-      N2 += q3.z * w;
-
-      if constexpr (!kHash) {
-        const uint32_t id = __float_as_uint(srec[6][j].z);
-        const float* col = p.colors + (size_t)id * p.C;
-#pragma unroll
-        for (int c = 0; c < NACC; c++)
-          if (c < p.C) acc[c] = fmaf(col[c], w, acc[c]);
-      } else {
-        const float4 q4 = srec[4][j], q5 = srec[5][j], q6 = srec[6][j];
-        float xyz[3];
-        if (use3d) {
-          xyz[0] = sx * q4.x + sy * q4.w + q5.z;
-          xyz[1] = sx * q4.y + sy * q5.x + q5.w;
-          xyz[2] = sx * q4.z + sy * q5.y + q6.x;
-        } else {
-          xyz[0] = q5.z;
-          xyz[1] = q5.w;
-          xyz[2] = q6.x;
+      do {
+        // Whole-wave skip: the wave's pixel block lies outside the splat's
+        // acceptance bbox, so the alpha test rejects every pixel of it.
+        const float4 bb = srec[7][j];
+        if (bb.y < wx0 || bb.x > wx1 || bb.w < wy0 || bb.z > wy1) break;
+        const float4 q0 = srec[0][j], q1 = srec[1][j], q2 = srec[2][j];
+        const float Tu0 = q0.x, Tu1 = q0.y, Tu2 = q0.z, Tv0 = q0.w;
+        const float Tv1 = q1.x, Tv2 = q1.y, Tw0 = q1.z, Tw1 = q1.w;
+        const float Tw2 = q2.x;
+        const float k0 = pxf * Tw0 - Tu0, k1 = pxf * Tw1 - Tu1, k2 = pxf * Tw2 - Tu2;
+        const float l0 = pyf * Tw0 - Tv0, l1 = pyf * Tw1 - Tv1, l2 = pyf * Tw2 - Tv2;
+        const float p0 = k1 * l2 - k2 * l1, p1 = k2 * l0 - k0 * l2, p2 = k0 * l1 - k1 * l0;
+        if (p2 == 0.0f) break;
+        const float dx = q2.y - pxf, dy = q2.z - pyf;
+        const float rho2d = 2.0f * (dx * dx + dy * dy);
+        // Per-lane early reject: an rcp-based rho3d within 1e-6 of the exact
+        // one, scaled down by 1e-5, above the splat's cut and rho2d above it
+        // too means alpha < 1/255 in the exact test.  NaNs take the exact path.
+        {
+          const float cut = srec[6][j].y;
+          const float rc = __builtin_amdgcn_rcpf(p2);
+          const float sxa = p0 * rc, sya = p1 * rc;
+          if ((sxa * sxa + sya * sya) * 0.99999f > cut && rho2d > cut) break;
         }
-        pos_x += w * xyz[0];
-        pos_y += w * xyz[1];
-        pos_z += w * xyz[2];
-        const uint32_t ap = __float_as_uint(q3.w);
+        const float sx = p0 / p2, sy = p1 / p2;
+        const float rho3d = sx * sx + sy * sy;
+        const float rho = fminf(rho3d, rho2d);
+        const bool use3d = rho3d <= rho2d;
+        const float depth = use3d ? (sx * Tw0 + sy * Tw1) + Tw2 : Tw2;
+        if (depth < 0.2f) break;
+        const float power = -0.5f * rho;
+        if (power > 0.0f) break;
+        float G = expf_ref(power);
+        if (p.beta > 0.0f) G = (float)((1.0 + (double)p.beta) * (double)G / (1.0 + (double)p.beta * (double)G));
+        const float alpha = fminf(0.99f, q2.w * G);
+        if (alpha < 1.0f / 255.0f) break;
+        const float test_T = T * (1 - alpha);
+        if (test_T < 0.0001f) {
+          done = true;
+          break;
+        }
+        const float w = alpha * T;
+        render_number++;
+        if (p.max_intersections > 0 && render_number >= p.max_intersections) done = true;
 
-        // normalisation to [0,1]^3 (hashgrid.h:66-98)
-        float u[3];
-        bool oob = false;
-        if (!g.contract) {
+        const float4 q3 = srec[3][j];
+        const float Aa = 1 - T;
+        const float m = mfac * (1 - 0.2f / depth);
+        distortion += (m * m * Aa + M2 - 2 * m * M1) * w;
+        D += depth * w;
+        M1 += m * w;
+        M2 += m * m * w;
+        if (T > 0.5f) {
+          median_depth = depth;
+          median_contributor = (float)contributor;
+        }
+        N0 += q3.x * w;
+        N1 += q3.y * w;
+        N2 += q3.z * w;
+
+        if constexpr (!kHash) {
+          const uint32_t id = __float_as_uint(srec[6][j].z);
+          const float* col = p.colors + (size_t)id * p.C;
 #pragma unroll
-          for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmin) * g.inv_size;
-          oob = (u[0] < 0 || u[0] > 1 || u[1] < 0 || u[1] > 1 || u[2] < 0 || u[2] > 1);
+          for (int c = 0; c < NACC; c++)
+            if (c < p.C) acc[c] = fmaf(col[c], w, acc[c]);
         } else {
-#pragma unroll
-          for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmid) * g.inv_size;
-          const float nrm = sqrtf(u[0] * u[0] + u[1] * u[1] + u[2] * u[2]);
-          const float inv_nrm = 1.0f / nrm;
-          const float st = (nrm <= 1.0f) ? 1.0f : (2.0f - inv_nrm) * inv_nrm;
-#pragma unroll
-          for (int d = 0; d < 3; d++) {
-            u[d] = st * u[d];
-            u[d] = (u[d] + 2.0f) * 0.25f;
+          const float4 q4 = srec[4][j], q5 = srec[5][j], q6 = srec[6][j];
+          float xyz[3];
+          if (use3d) {
+            xyz[0] = sx * q4.x + sy * q4.w + q5.z;
+            xyz[1] = sx * q4.y + sy * q5.x + q5.w;
+            xyz[2] = sx * q4.z + sy * q5.y + q6.x;
+          } else {
+            xyz[0] = q5.z;
+            xyz[1] = q5.w;
+            xyz[2] = q6.x;
           }
-        }
-        // Levels at or past max_level contribute fmaf(0, w, acc) == acc (the
-        // accumulators never hold -0), so they are skipped.
-        const uint32_t max_level = oob ? 0u : (ap < L ? ap : L);
+          pos_x += w * xyz[0];
+          pos_y += w * xyz[1];
+          pos_z += w * xyz[2];
+          const uint32_t ap = __float_as_uint(q3.w);
+
+          // normalisation to [0,1]^3 (hashgrid.h:66-98)
+          float u[3];
+          bool oob = false;
+          if (!g.contract) {
 #pragma unroll
-        for (int l = 0; l < NACC / F; l++) {
-          if ((uint32_t)l < max_level) {
-            float r[F];
-            level_interp_rsrc<F, kHalf>(rsrc, g.lv, l, g.pos_offset, g.interp, u, r);
+            for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmin) * g.inv_size;
+            oob = (u[0] < 0 || u[0] > 1 || u[1] < 0 || u[1] > 1 || u[2] < 0 || u[2] > 1);
+          } else {
 #pragma unroll
-            for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(r[f], w, acc[l * F + f]);
+            for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmid) * g.inv_size;
+            const float nrm = sqrtf(u[0] * u[0] + u[1] * u[1] + u[2] * u[2]);
+            const float inv_nrm = 1.0f / nrm;
+            const float st = (nrm <= 1.0f) ? 1.0f : (2.0f - inv_nrm) * inv_nrm;
+#pragma unroll
+            for (int d = 0; d < 3; d++) {
+              u[d] = st * u[d];
+              u[d] = (u[d] + 2.0f) * 0.25f;
+            }
           }
+          // Levels at or past max_level contribute fmaf(0, w, acc) == acc
+          // (the accumulators never hold -0), so they are not queried.
+          const uint32_t max_level = oob ? 0u : (ap < L ? ap : L);
+          hq[qn][threadIdx.x] = make_float4(u[0], u[1], u[2], w);
+          hl[qn][threadIdx.x] = (uint8_t)(max_level < 255u ? max_level : 255u);
+          qn++;
+          float apc0, apc1;
+          if (ap <= 4u) {
+            apc0 = (float)((double)(uint32_t)(ap - 2u) * 0.5);
+            apc1 = 1.0f;
+          } else {
+            apc0 = 1.0f;
+            apc1 = (float)(1.0 - (double)(uint32_t)(ap - 4u) * 0.5);
+          }
+          vis0 += apc0 * w;
+          vis1 += apc1 * w;
         }
-        float apc0, apc1;
-        if (ap <= 4u) {
-          apc0 = (float)((double)(uint32_t)(ap - 2u) * 0.5);
-          apc1 = 1.0f;
-        } else {
-          apc0 = 1.0f;
-          apc1 = (float)(1.0 - (double)(uint32_t)(ap - 4u) * 0.5);
-        }
-        vis0 += apc0 * w;
-        vis1 += apc1 * w;
-        vis2 += 0.0f * w;
+        T = test_T;
+        last_contributor = contributor;
+      } while (false);
       }
-      T = test_T;
-      last_contributor = contributor;
+      j++;
+      if (kHash && __ballot(qn == kQueue)) break;
+      if (__ballot(!done) == 0) j = n;
     }
+    const bool batch_end = j >= n;
+    if constexpr (kHash) {
+      if (__ballot(qn == kQueue) || (last && __ballot(qn > 0))) {
+        drain_queue<F, NACC, kHalf>(g, rsrc, hq, hl, qn, wave_max_small(qn), acc);
+        qn = 0;
+      }
+    }
+    if (batch_end) break;
+    }
+    if (last) break;
+    start += kRenderThreads;
   }
 
   if (!inside) return;
@@ -221,7 +303,7 @@ render_kernel(const RenderParams p) {
   O[pid + 10 * HW] = pos_z;
   O[pid + 11 * HW] = vis0;
   O[pid + 12 * HW] = vis1;
-  O[pid + 13 * HW] = vis2;
+  O[pid + 13 * HW] = 0.0f;  // the third appearance channel only ever adds 0 * w
 }
 
 template <int F, int NACC, bool kHash, bool kHalf>
