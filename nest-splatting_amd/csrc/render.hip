@@ -41,35 +41,27 @@ __device__ __forceinline__ uint32_t xcd_tile(uint32_t i, uint32_t n) {
   return start + k;
 }
 
-// Hash lookups of `rounds` queued hits per lane (lanes with fewer pending
-// hits idle in the later rounds), accumulated into acc in queue order.
+// One drain round: every lane with a pending hit looks up its oldest one
+// (ring-buffer head) and accumulates it; lanes with an empty queue idle.
 template <int F, int NACC, bool kHalf>
-__device__ __forceinline__ void drain_queue(const GridParams& g, nest_i32x4 rsrc, float4 (*hq)[kRenderThreads],
-                                            uint8_t (*hl)[kRenderThreads], int qn, int rounds, float* acc) {
-  for (int r = 0; r < rounds; r++) {
-    if (r < qn) {
-      const float4 e = hq[r][threadIdx.x];
-      const uint32_t maxl = hl[r][threadIdx.x];
-      const float u[3] = {e.x, e.y, e.z};
+__device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc, float4 (*hq)[kRenderThreads],
+                                            uint8_t (*hl)[kRenderThreads], int& qhead, int& qn, float* acc) {
+  if (qn > 0) {
+    const float4 e = hq[qhead][threadIdx.x];
+    const uint32_t maxl = hl[qhead][threadIdx.x];
+    const float u[3] = {e.x, e.y, e.z};
 #pragma unroll
-      for (int l = 0; l < NACC / F; l++) {
-        if ((uint32_t)l < maxl) {
-          float v[F];
-          level_interp_struct<F, kHalf>(rsrc, g.lv, l, g.pos_offset, g.interp, u, v);
+    for (int l = 0; l < NACC / F; l++) {
+      if ((uint32_t)l < maxl) {
+        float v[F];
+        level_interp_struct<F, kHalf>(rsrc, g.lv, l, g.pos_offset, g.interp, u, v);
 #pragma unroll
-          for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(v[f], e.w, acc[l * F + f]);
-        }
+        for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(v[f], e.w, acc[l * F + f]);
       }
     }
+    qhead = (qhead + 1) & (kQueue - 1);
+    qn--;
   }
-}
-
-__device__ __forceinline__ int wave_max_small(int v) {
-  int m = 0;
-#pragma unroll
-  for (int r = 1; r <= kQueue; r++)
-    if (__ballot(v >= r)) m = r;
-  return m;
 }
 
 // amdgpu_waves_per_eu(3): at C = 64 the accumulators and eight in-flight
@@ -108,7 +100,7 @@ render_kernel(const RenderParams p) {
   const uint32_t L = g.L;
   nest_i32x4 rsrc{};
   if constexpr (kHash) rsrc = table_rsrc_rows<F, kHalf>(g.table, g.table_rows);
-  int qn = 0;
+  int qn = 0, qhead = 0;  // per-lane ring buffer of pending lookups
 
   // Batches of 256 splats.  The splat index j is uniform across the wave;
   // lanes that are done skip the body, as the reference's per-lane loop
@@ -242,8 +234,9 @@ render_kernel(const RenderParams p) {
           // Levels at or past max_level contribute fmaf(0, w, acc) == acc
           // (the accumulators never hold -0), so they are not queried.
           const uint32_t max_level = oob ? 0u : (ap < L ? ap : L);
-          hq[qn][threadIdx.x] = make_float4(u[0], u[1], u[2], w);
-          hl[qn][threadIdx.x] = (uint8_t)(max_level < 255u ? max_level : 255u);
+          const int slot = (qhead + qn) & (kQueue - 1);
+          hq[slot][threadIdx.x] = make_float4(u[0], u[1], u[2], w);
+          hl[slot][threadIdx.x] = (uint8_t)(max_level < 255u ? max_level : 255u);
           qn++;
           float apc0, apc1;
           if (ap <= 4u) {
@@ -266,9 +259,10 @@ render_kernel(const RenderParams p) {
     }
     const bool batch_end = j >= n;
     if constexpr (kHash) {
+      // one round whenever a lane is full; at the end, rounds until empty
       if (__ballot(qn == kQueue) || (last && __ballot(qn > 0))) {
-        drain_queue<F, NACC, kHalf>(g, rsrc, hq, hl, qn, wave_max_small(qn), acc);
-        qn = 0;
+        drain_round<F, NACC, kHalf>(g, rsrc, hq, hl, qhead, qn, acc);
+        if (last) continue;
       }
     }
     if (batch_end) break;
