@@ -273,14 +273,20 @@ __device__ __forceinline__ void struct_entry(nest_i32x4 r, uint32_t index, uint3
 // v_fract (exact for the non-negative pos here, equal to the reference's
 // pos - (float)(uint)floor(pos) below 2^24), and the entry index goes to the
 // buffer unit unscaled.
+struct LevelCorners {
+  uint32_t idx[8];   // entry index of corner k (bit 0: +x, bit 1: +y, bit 2: +z)
+  uint32_t soff;     // byte offset of the level in the table
+  float wx[2], wy[2], wz[2];
+};
+
 template <int F, bool kHalf>
-__device__ __forceinline__ void level_interp_struct(nest_i32x4 rsrc, const LevelTable& lv, int l,
-                                                    float pos_offset, uint32_t interp, const float u[3], float out[F]) {
+__device__ __forceinline__ void level_corners(const LevelTable& lv, int l, float pos_offset, uint32_t interp,
+                                              const float u[3], LevelCorners& cn) {
   const float scale = lv.scale[l];
   const uint32_t res1 = lv.res1[l];
   const uint32_t hsize = lv.hsize[l];
   const uint32_t flags = lv.flags[l];
-  const uint32_t soff = lv.base[l] * (uint32_t)(F * (kHalf ? 2 : 4));
+  cn.soff = lv.base[l] * (uint32_t)(F * (kHalf ? 2 : 4));
   float pos[3];
   uint32_t g[3];
 #pragma unroll
@@ -290,8 +296,10 @@ __device__ __forceinline__ void level_interp_struct(nest_i32x4 rsrc, const Level
     pos[d] = (x >= 0.0f && x < 16777216.0f) ? __builtin_amdgcn_fractf(x) : x - (float)g[d];
     if (interp == 1) pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
   }
-  const float wx[2] = {1 - pos[0], pos[0]}, wy[2] = {1 - pos[1], pos[1]}, wz[2] = {1 - pos[2], pos[2]};
-  uint32_t idx[8];
+  cn.wx[0] = 1 - pos[0]; cn.wx[1] = pos[0];
+  cn.wy[0] = 1 - pos[1]; cn.wy[1] = pos[1];
+  cn.wz[0] = 1 - pos[2]; cn.wz[1] = pos[2];
+  uint32_t* idx = cn.idx;
   if (flags & kLvHashed) {
     const uint32_t a[2] = {g[0], g[0] + 1u};
     const uint32_t b0 = g[1] * 2654435761u, c0 = g[2] * 805459861u;
@@ -314,17 +322,37 @@ __device__ __forceinline__ void level_interp_struct(nest_i32x4 rsrc, const Level
       for (int k = 0; k < 8; k++) idx[k] %= hsize;
     }
   }
-  float vals[8][F];
+}
+
+// Loads the eight corner entries of cn.
+template <int F, bool kHalf>
+__device__ __forceinline__ void corners_load(nest_i32x4 rsrc, const LevelCorners& cn, float vals[8][F]) {
 #pragma unroll
-  for (int k = 0; k < 8; k++) struct_entry<F, kHalf>(rsrc, idx[k], soff, vals[k]);
+  for (int k = 0; k < 8; k++) struct_entry<F, kHalf>(rsrc, cn.idx[k], cn.soff, vals[k]);
+}
+
+// Interpolated value: out = fmaf(w_k, entry_k, out) over corners 0..7 in
+// order, out starting at 0.
+template <int F>
+__device__ __forceinline__ void corners_sum(const LevelCorners& cn, const float vals[8][F], float out[F]) {
 #pragma unroll
   for (int f = 0; f < F; f++) out[f] = 0.0f;
 #pragma unroll
   for (int k = 0; k < 8; k++) {
-    const float w = (1.0f * wx[k & 1]) * wy[(k >> 1) & 1] * wz[k >> 2];
+    const float w = (1.0f * cn.wx[k & 1]) * cn.wy[(k >> 1) & 1] * cn.wz[k >> 2];
 #pragma unroll
     for (int f = 0; f < F; f++) out[f] = fmaf(w, vals[k][f], out[f]);
   }
+}
+
+template <int F, bool kHalf>
+__device__ __forceinline__ void level_interp_struct(nest_i32x4 rsrc, const LevelTable& lv, int l,
+                                                    float pos_offset, uint32_t interp, const float u[3], float out[F]) {
+  LevelCorners cn;
+  level_corners<F, kHalf>(lv, l, pos_offset, interp, u, cn);
+  float vals[8][F];  // all eight loads in flight before the first use
+  corners_load<F, kHalf>(rsrc, cn, vals);
+  corners_sum<F>(cn, vals, out);
 }
 
 // Trilinear (interp 0) or smoothstep (interp 1) interpolation of level l at

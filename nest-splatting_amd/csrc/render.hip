@@ -29,9 +29,21 @@
 
 namespace nest {
 
+// Launch shape, measured on the 1M-splat 1600x1064 L=16 F=4 scene (render ms):
+//   batch 256 / queue 4 / 3 waves per SIMD / 8 corner loads in flight  10.2
+//   batch 128 (4 workgroups per CU by LDS), 4 waves, 4 loads in flight 13.1
+//   batch 128, queue 8, 3 waves                                        10.2
+//   2 waves (more VGPRs), two levels' 16 loads in flight               11.5
+// The gathers are latency-bound: loads in flight per SIMD count for more
+// than occupancy.
 constexpr int kRenderThreads = 256;
+constexpr int kBatch = 256;    // splats staged in LDS per batch
 constexpr int kRecChunks = 8;  // float4 chunks of the record staged per splat
+constexpr int kLanesPerRec = kRenderThreads / kBatch;
+constexpr int kChunksPerLane = kRecChunks / kLanesPerRec;
 constexpr int kQueue = 4;      // pending hash lookups per pixel
+static_assert(kBatch == 64 || kBatch == 128 || kBatch == 256, "batch");
+static_assert((kQueue & (kQueue - 1)) == 0, "queue length is a power of two");
 
 // Workgroup i runs on XCD i % 8; give XCD x a contiguous range of tiles.
 __device__ __forceinline__ uint32_t xcd_tile(uint32_t i, uint32_t n) {
@@ -64,12 +76,13 @@ __device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc
   }
 }
 
-// amdgpu_waves_per_eu(3): at C = 64 the accumulators and eight in-flight
-// corner loads need ~170 VGPRs; capping at 168 gives three waves per SIMD.
+// LDS (32 KB of staged records + 17 KB of queue) allows three workgroups per
+// CU; amdgpu_waves_per_eu(3) gives the matching 168-VGPR budget, which holds
+// 64 accumulators and eight in-flight 16-byte corner loads.
 template <int F, int NACC, bool kHash, bool kHalf>
 __global__ void __launch_bounds__(kRenderThreads) __attribute__((amdgpu_waves_per_eu(3, 8)))
 render_kernel(const RenderParams p) {
-  __shared__ float4 srec[kRecChunks][kRenderThreads];
+  __shared__ float4 srec[kRecChunks][kBatch];
   __shared__ float4 hq[kHash ? kQueue : 1][kRenderThreads];
   __shared__ uint8_t hl[kHash ? kQueue : 1][kRenderThreads];
 
@@ -113,16 +126,19 @@ render_kernel(const RenderParams p) {
     const bool last = start >= range.y || all_done;
     uint32_t n = 0;
     if (!last) {
-      const uint32_t e = start + threadIdx.x;
+      // kLanesPerRec adjacent lanes stage record r, kChunksPerLane chunks each
+      const uint32_t r = threadIdx.x / kLanesPerRec;
+      const uint32_t h = (threadIdx.x % kLanesPerRec) * kChunksPerLane;
+      const uint32_t e = start + r;
       if (e < range.y) {
         const uint32_t id = p.point_list[e];
-        const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id;
+        const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id + h;
 #pragma unroll
-        for (int c = 0; c < kRecChunks; c++) srec[c][threadIdx.x] = rec[c];
-        srec[6][threadIdx.x].z = __uint_as_float(id);
+        for (int c = 0; c < kChunksPerLane; c++) srec[h + c][r] = rec[c];
+        if (h <= 6 && 6 < h + kChunksPerLane) srec[6][r].z = __uint_as_float(id);
       }
       __syncthreads();
-      n = min((uint32_t)kRenderThreads, range.y - start);
+      n = min((uint32_t)kBatch, range.y - start);
     }
     uint32_t j = 0;
     for (;;) {
@@ -268,7 +284,7 @@ render_kernel(const RenderParams p) {
     if (batch_end) break;
     }
     if (last) break;
-    start += kRenderThreads;
+    start += kBatch;
   }
 
   if (!inside) return;
