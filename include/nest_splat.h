@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 1
+#define NEST_ABI_VERSION 2
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -157,12 +157,20 @@ const char *nest_last_error(void);
                                       (x0, x1, y0, y1)                 */
 #define NEST_GEOM_RADII 5          /* i32 [P]                         */
 #define NEST_GEOM_SCAN_TMP 6       /* scan scratch                    */
-#define NEST_GEOM_FIELDS 7
+#define NEST_GEOM_DEPTH_ORDER 7    /* u32 [P]    splat ids by (depth bits, id),
+                                      culled splats last (written by
+                                      nest_forward_render)             */
+#define NEST_GEOM_ORDER_OFFSETS 8  /* u32 [P]    exclusive scan of tiles
+                                      touched in that order            */
+#define NEST_GEOM_ORDER_TMP 9      /* depth sort scratch              */
+#define NEST_GEOM_FIELDS 10
 int nest_geom_layout(int32_t P, size_t offsets[NEST_GEOM_FIELDS], size_t *total_bytes);
 
-#define NEST_BIN_KEYS_UNSORTED 0   /* u64 [NR] */
-#define NEST_BIN_VALS_UNSORTED 1   /* u32 [NR] */
-#define NEST_BIN_KEYS 2            /* u64 [NR] sorted */
+/* The pairs are emitted in depth order and sorted on the tile bits only;
+ * KEYS and VALS equal the reference's point_list_keys and point_list. */
+#define NEST_BIN_PAIR_TILES 0      /* u32 [NR] tile id of each pair, pairs in depth order */
+#define NEST_BIN_PAIR_IDS 1        /* u32 [NR] splat id of each pair, same order          */
+#define NEST_BIN_KEYS 2            /* u64 [NR] sorted (tile << 32 | depth bits) */
 #define NEST_BIN_VALS 3            /* u32 [NR] sorted (point_list) */
 #define NEST_BIN_SORT_TMP 4
 #define NEST_BIN_FIELDS 5

@@ -188,6 +188,9 @@ int nest_geom_layout(int32_t P, size_t offsets[NEST_GEOM_FIELDS], size_t* total)
   o[NEST_GEOM_RECORDS] = c.take(n * kRecordFloats * 4);
   o[NEST_GEOM_RADII] = c.take(n * 4);
   o[NEST_GEOM_SCAN_TMP] = c.take(scan_ws_bytes((int64_t)n));
+  o[NEST_GEOM_DEPTH_ORDER] = c.take(n * 4);
+  o[NEST_GEOM_ORDER_OFFSETS] = c.take(n * 4);
+  o[NEST_GEOM_ORDER_TMP] = c.take(depth_order_ws_bytes((int)n));
   if (offsets)
     for (int i = 0; i < NEST_GEOM_FIELDS; i++) offsets[i] = o[i];
   if (total) *total = c.off;
@@ -199,11 +202,11 @@ int nest_binning_layout(int64_t NR, size_t offsets[NEST_BIN_FIELDS], size_t* tot
   const size_t n = (size_t)(NR > 0 ? NR : 1);
   Carver c;
   size_t o[NEST_BIN_FIELDS];
-  o[NEST_BIN_KEYS_UNSORTED] = c.take(n * 8);
-  o[NEST_BIN_VALS_UNSORTED] = c.take(n * 4);
+  o[NEST_BIN_PAIR_TILES] = c.take(n * 4);
+  o[NEST_BIN_PAIR_IDS] = c.take(n * 4);
   o[NEST_BIN_KEYS] = c.take(n * 8);
   o[NEST_BIN_VALS] = c.take(n * 4);
-  o[NEST_BIN_SORT_TMP] = c.take(sort_ws_bytes((int64_t)n));
+  o[NEST_BIN_SORT_TMP] = c.take(tile_sort_ws_bytes((int64_t)n));
   if (offsets)
     for (int i = 0; i < NEST_BIN_FIELDS; i++) offsets[i] = o[i];
   if (total) *total = c.off;
@@ -383,27 +386,32 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   uint32_t* ranges = reinterpret_cast<uint32_t*>(im + io[NEST_IMG_RANGES]);
   StageTimer tm(timing, s);
 
-  uint64_t* keys_u = nullptr;
-  uint32_t* vals_u = nullptr;
   uint64_t* keys = nullptr;
   uint32_t* vals = nullptr;
   if (NR > 0) {
-    keys_u = reinterpret_cast<uint64_t*>(b + bo[NEST_BIN_KEYS_UNSORTED]);
-    vals_u = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_VALS_UNSORTED]);
+    uint32_t* pair_tiles = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_PAIR_TILES]);
+    uint32_t* pair_ids = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_PAIR_IDS]);
     keys = reinterpret_cast<uint64_t*>(b + bo[NEST_BIN_KEYS]);
     vals = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_VALS]);
+    const float* depth = reinterpret_cast<const float*>(g + go[NEST_GEOM_DEPTH]);
+    const int32_t* gradii = reinterpret_cast<const int32_t*>(g + go[NEST_GEOM_RADII]);
+    uint32_t* order = reinterpret_cast<uint32_t*>(g + go[NEST_GEOM_DEPTH_ORDER]);
+    uint32_t* order_offsets = reinterpret_cast<uint32_t*>(g + go[NEST_GEOM_ORDER_OFFSETS]);
+    // duplicate stage: depth order of the splats, then their pairs in that order
     tm.begin(NEST_STAGE_DUPLICATE);
-    rc = check_stage(launch_duplicate(sp->P, nullptr, reinterpret_cast<const float*>(g + go[NEST_GEOM_XY]),
-                                      reinterpret_cast<const float*>(g + go[NEST_GEOM_DEPTH]),
-                                      reinterpret_cast<const int32_t*>(g + go[NEST_GEOM_RADII]),
-                                      reinterpret_cast<const uint32_t*>(g + go[NEST_GEOM_OFFSETS]), gx, gy, keys_u, vals_u, s),
+    rc = check_stage(launch_depth_order(sp->P, depth, gradii, reinterpret_cast<const uint32_t*>(g + go[NEST_GEOM_TILES]),
+                                        order, order_offsets, g + go[NEST_GEOM_ORDER_TMP], s),
+                     "depth order", rs->debug, s);
+    if (rc) return rc;
+    rc = check_stage(launch_duplicate_ordered(sp->P, order, order_offsets, reinterpret_cast<const float*>(g + go[NEST_GEOM_XY]),
+                                              gradii, gx, gy, NR, pair_tiles, pair_ids, s),
                      "duplicate", rs->debug, s);
     if (rc) return rc;
     tm.end();
     tm.begin(NEST_STAGE_SORT);
     const int bit = (int)higher_msb(ntiles);
-    rc = check_stage(launch_sort_pairs(keys_u, vals_u, keys, vals, NR, 32 + bit, b + bo[NEST_BIN_SORT_TMP], s), "sort",
-                     rs->debug, s);
+    rc = check_stage(launch_sort_tiles(pair_tiles, pair_ids, keys, vals, NR, bit, depth, b + bo[NEST_BIN_SORT_TMP], s),
+                     "sort", rs->debug, s);
     if (rc) return rc;
     tm.end();
   }
@@ -475,8 +483,7 @@ int nest_sort_pairs_u64(const uint64_t* keys_in, const uint32_t* vals_in, uint64
   if (!keys_in || !vals_in || !keys_out || !vals_out) return fail(NEST_ERR_INVALID_ARGUMENT, "NULL key/value pointer");
   if (!ws || ws_bytes < sort_ws_bytes(n))
     return fail(NEST_ERR_WORKSPACE, "sort workspace too small: %zu bytes given, %zu needed", ws_bytes, sort_ws_bytes(n));
-  hipError_t e = launch_sort_pairs(const_cast<uint64_t*>(keys_in), const_cast<uint32_t*>(vals_in), keys_out, vals_out, n,
-                                   end_bit, ws, static_cast<hipStream_t>(stream));
+  hipError_t e = launch_sort_pairs(keys_in, vals_in, keys_out, vals_out, n, end_bit, ws, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? NEST_OK : hip_fail(e, "sort");
 }
 

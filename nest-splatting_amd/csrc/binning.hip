@@ -6,7 +6,9 @@
 // :70-111 (duplicateWithKeys), :35-50 + :381-386 (getHigherMsb +
 // cub::DeviceRadixSort::SortPairs on bits [0, 32+bit)), :173-195 + :388
 // (identifyTileRanges after a memset), with CR = submodules/
-// diff-surfel-rasterization/cuda_rasterizer.
+// diff-surfel-rasterization/cuda_rasterizer.  The sorted keys and values are
+// produced by a depth sort of the splats followed by a tile-bits sort of the
+// pairs (the last section below explains why the order is the same).
 //
 // Sort design (gfx950, 64-lane waves): reduce-then-scan LSD radix with 8-bit
 // digits.  Each 256-thread block owns 4096 keys; a wave ranks its 1024 keys in
@@ -176,59 +178,30 @@ hipError_t launch_fill_u32(uint32_t* dst, uint32_t value, int64_t n, hipStream_t
   return hipGetLastError();
 }
 
-// duplicateWithKeys: one lane per splat, pairs emitted row-major over the
-// splat's tile rectangle at the splat's scanned offset.
-__global__ void __launch_bounds__(256) duplicate_kernel(int P, const float2* __restrict__ xy, const float* __restrict__ depth,
-                                                       const int32_t* __restrict__ radii, const uint32_t* __restrict__ offsets,
-                                                       uint32_t gx, uint32_t gy, uint64_t* __restrict__ keys,
-                                                       uint32_t* __restrict__ vals) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= P) return;
-  const int r = radii[i];
-  if (r <= 0) return;
-  uint32_t off = (i == 0) ? 0u : offsets[i - 1];
-  const float2 c = xy[i];
-  uint32_t x0, y0, x1, y1;
-  tile_rect(c.x, c.y, r, gx, gy, x0, y0, x1, y1);
-  const uint64_t dbits = (uint64_t)__float_as_uint(depth[i]);
-  for (uint32_t y = y0; y < y1; y++)
-    for (uint32_t x = x0; x < x1; x++) {
-      keys[off] = ((uint64_t)(y * gx + x) << 32) | dbits;
-      vals[off] = (uint32_t)i;
-      off++;
-    }
-}
-
-hipError_t launch_duplicate(int P, const float* /*records*/, const float* xy, const float* depth, const int32_t* radii,
-                            const uint32_t* offsets, uint32_t gx, uint32_t gy, uint64_t* keys, uint32_t* vals,
-                            hipStream_t s) {
-  if (P <= 0) return hipSuccess;
-  hipLaunchKernelGGL(duplicate_kernel, dim3((P + 255) / 256), dim3(256), 0, s, P,
-                     reinterpret_cast<const float2*>(xy), depth, radii, offsets, gx, gy, keys, vals);
-  return hipGetLastError();
-}
-
-__global__ void tile_ranges_kernel(const uint64_t* __restrict__ keys, int64_t n, uint2* __restrict__ ranges) {
+// Tile ids at or past ntiles (only possible when the caller's pair count
+// exceeds the pairs written) are not recorded.
+__global__ void tile_ranges_kernel(const uint64_t* __restrict__ keys, int64_t n, uint2* __restrict__ ranges,
+                                   uint32_t ntiles) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const uint32_t t = (uint32_t)(keys[i] >> 32);
   if (i == 0) {
-    ranges[t].x = 0;
+    if (t < ntiles) ranges[t].x = 0;
   } else {
     const uint32_t pt = (uint32_t)(keys[i - 1] >> 32);
     if (t != pt) {
-      ranges[pt].y = (uint32_t)i;
-      ranges[t].x = (uint32_t)i;
+      if (pt < ntiles) ranges[pt].y = (uint32_t)i;
+      if (t < ntiles) ranges[t].x = (uint32_t)i;
     }
   }
-  if (i == n - 1) ranges[t].y = (uint32_t)n;
+  if (i == n - 1 && t < ntiles) ranges[t].y = (uint32_t)n;
 }
 
 hipError_t launch_tile_ranges(const uint64_t* keys, int64_t n, uint32_t* ranges, uint32_t ntiles, hipStream_t s) {
   hipError_t e = launch_fill_u32(ranges, 0u, 2 * (int64_t)ntiles, s);
   if (e != hipSuccess || n <= 0) return e;
   hipLaunchKernelGGL(tile_ranges_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, keys, n,
-                     reinterpret_cast<uint2*>(ranges));
+                     reinterpret_cast<uint2*>(ranges), ntiles);
   return hipGetLastError();
 }
 
@@ -260,7 +233,8 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 }
 
 // Per-block digit histogram, written digit-major: counts[d * nblocks + b].
-__global__ void __launch_bounds__(kSortThreads) radix_hist_kernel(const uint64_t* __restrict__ keys, int64_t n, int shift,
+template <typename K>
+__global__ void __launch_bounds__(kSortThreads) radix_hist_kernel(const K* __restrict__ keys, int64_t n, int shift,
                                                                  uint32_t* __restrict__ counts, uint32_t nblocks) {
   __shared__ uint32_t hist[kSortWaves][kRadix];
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
@@ -286,11 +260,15 @@ __global__ void __launch_bounds__(kSortThreads) radix_hist_kernel(const uint64_t
 }
 
 // Stable scatter of one digit pass.  offsets is the exclusive scan of counts.
-__global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const uint64_t* __restrict__ keys_in,
+// KOut == uint64_t with K == uint32_t composes the output key as
+// (key << 32) | low_bits[val] (the tile/depth key of the binning stage).
+template <typename K, typename KOut>
+__global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __restrict__ keys_in,
                                                                     const uint32_t* __restrict__ vals_in,
-                                                                    uint64_t* __restrict__ keys_out,
+                                                                    KOut* __restrict__ keys_out,
                                                                     uint32_t* __restrict__ vals_out, int64_t n, int shift,
-                                                                    const uint32_t* __restrict__ offsets, uint32_t nblocks) {
+                                                                    const uint32_t* __restrict__ offsets, uint32_t nblocks,
+                                                                    const uint32_t* __restrict__ low_bits) {
   __shared__ uint32_t hist[kSortWaves][kRadix];
   __shared__ uint32_t gbase[kRadix];
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
@@ -299,7 +277,7 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const uint6
   __syncthreads();
 
   const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)wid * (kWave * kSortRounds);
-  uint64_t key[kSortRounds];
+  K key[kSortRounds];
   uint32_t val[kSortRounds];
   uint32_t rank[kSortRounds];
 #pragma unroll
@@ -307,7 +285,7 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const uint6
     const int64_t i = base + r * kWave + lane;
     if (i < n) {
       key[r] = keys_in[i];
-      val[r] = vals_in[i];
+      val[r] = vals_in ? vals_in[i] : (uint32_t)i;
     } else {
       key[r] = 0;
       val[r] = 0;
@@ -344,60 +322,189 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const uint6
     if (i < n) {
       const uint32_t d = (uint32_t)(key[r] >> shift) & (kRadix - 1);
       const uint32_t pos = gbase[d] + hist[wid][d] + rank[r];
-      keys_out[pos] = key[r];
+      if constexpr (sizeof(KOut) > sizeof(K))
+        keys_out[pos] = ((KOut)key[r] << 32) | (KOut)low_bits[val[r]];
+      else
+        keys_out[pos] = key[r];
       vals_out[pos] = val[r];
     }
   }
 }
 
 static int64_t sort_blocks(int64_t n) { return (n + kSortTile - 1) / kSortTile; }
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// Workspace: ping-pong keys/vals, digit counts, scan partials.
-size_t sort_ws_bytes(int64_t n) {
-  const int64_t nb = sort_blocks(n);
-  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
-  const int64_t ncounts = (int64_t)kRadix * nb;
-  return al((size_t)n * 8) + al((size_t)n * 4) + 2 * al((size_t)ncounts * 4) + al(scan_ws_bytes(ncounts));
+// Workspace: ping-pong keys/vals (two sets when the last pass widens the
+// key), digit counts and their scan.
+template <typename K, typename KOut>
+static size_t sort_ws_bytes_t(int64_t n) {
+  constexpr int sets = sizeof(KOut) == sizeof(K) ? 1 : 2;
+  const int64_t ncounts = (int64_t)kRadix * sort_blocks(n);
+  return sets * (align256((size_t)n * sizeof(K)) + align256((size_t)n * 4)) + 2 * align256((size_t)ncounts * 4) +
+         align256(scan_ws_bytes(ncounts));
 }
 
-hipError_t launch_sort_pairs(uint64_t* keys_in, uint32_t* vals_in, uint64_t* keys_out, uint32_t* vals_out, int64_t n,
-                             int end_bit, void* ws, hipStream_t s) {
+// Stable LSD sort of (keys_in, vals_in) on key bits [0, end_bit) into
+// (keys_out, vals_out).  The inputs are never written.  vals_in == nullptr
+// stands for vals_in[i] = i.  With KOut wider than K the last pass writes
+// (key << 32) | low_bits[val].
+template <typename K, typename KOut>
+static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, KOut* keys_out, uint32_t* vals_out, int64_t n,
+                            int end_bit, const uint32_t* low_bits, void* ws, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  constexpr bool kSame = sizeof(KOut) == sizeof(K);
   const int64_t nb = sort_blocks(n);
   const int64_t ncounts = (int64_t)kRadix * nb;
   char* w = static_cast<char*>(ws);
-  uint64_t* tk = reinterpret_cast<uint64_t*>(w);
-  w += al((size_t)n * 8);
-  uint32_t* tv = reinterpret_cast<uint32_t*>(w);
-  w += al((size_t)n * 4);
+  K* tk[2];
+  uint32_t* tv[2];
+  for (int t = 0; t < (kSame ? 1 : 2); t++) {
+    tk[t] = reinterpret_cast<K*>(w);
+    w += align256((size_t)n * sizeof(K));
+    tv[t] = reinterpret_cast<uint32_t*>(w);
+    w += align256((size_t)n * 4);
+  }
   uint32_t* counts = reinterpret_cast<uint32_t*>(w);
-  w += al((size_t)ncounts * 4);
+  w += align256((size_t)ncounts * 4);
   uint32_t* offs = reinterpret_cast<uint32_t*>(w);
-  w += al((size_t)ncounts * 4);
+  w += align256((size_t)ncounts * 4);
   void* scan_ws = w;
 
   int passes = (end_bit + kRadixBits - 1) / kRadixBits;
   if (passes < 1) passes = 1;
-  const uint64_t* sk = keys_in;
+  const K* sk = keys_in;
   const uint32_t* sv = vals_in;
   for (int pass = 0; pass < passes; pass++) {
-    // choose destinations so that the last pass lands in *_out and the input
-    // buffers are never written
-    const bool to_out = ((passes - 1 - pass) % 2) == 0;
-    uint64_t* dk = to_out ? keys_out : tk;
-    uint32_t* dv = to_out ? vals_out : tv;
+    const bool last = pass == passes - 1;
     const int shift = pass * kRadixBits;
-    hipLaunchKernelGGL(radix_hist_kernel, dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, n, shift, counts,
+    hipLaunchKernelGGL(radix_hist_kernel<K>, dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, n, shift, counts,
                        (uint32_t)nb);
     hipError_t e = scan_impl(counts, offs, ncounts, scan_ws, true, s);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(radix_scatter_kernel, dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, sv, dk, dv, n, shift,
-                       offs, (uint32_t)nb);
+    K* dk;
+    uint32_t* dv;
+    if constexpr (kSame) {
+      // alternate so that the last pass lands in *_out
+      const bool to_out = ((passes - 1 - pass) % 2) == 0;
+      dk = to_out ? reinterpret_cast<K*>(keys_out) : tk[0];
+      dv = to_out ? vals_out : tv[0];
+    } else {
+      dk = tk[pass & 1];
+      dv = tv[pass & 1];
+    }
+    if (!kSame && last)
+      hipLaunchKernelGGL((radix_scatter_kernel<K, KOut>), dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, sv, keys_out,
+                         vals_out, n, shift, offs, (uint32_t)nb, low_bits);
+    else
+      hipLaunchKernelGGL((radix_scatter_kernel<K, K>), dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, sv, dk, dv, n,
+                         shift, offs, (uint32_t)nb, low_bits);
     sk = dk;
     sv = dv;
   }
   return hipGetLastError();
+}
+
+size_t sort_ws_bytes(int64_t n) { return sort_ws_bytes_t<uint64_t, uint64_t>(n); }
+
+hipError_t launch_sort_pairs(const uint64_t* keys_in, const uint32_t* vals_in, uint64_t* keys_out, uint32_t* vals_out,
+                             int64_t n, int end_bit, void* ws, hipStream_t s) {
+  return sort_impl<uint64_t, uint64_t>(keys_in, vals_in, keys_out, vals_out, n, end_bit, nullptr, ws, s);
+}
+
+// ---------------------------------------------------------------------------
+// binning in depth order
+// ---------------------------------------------------------------------------
+//
+// The reference sorts every (tile << 32 | depth bits, splat) pair on all
+// 32 + tile bits.  Sorting the splats by depth first (stable, so equal depths
+// keep splat order), emitting each splat's pairs in that order and then
+// stable-sorting the pairs on the tile bits alone yields the same order:
+// within a tile, by depth bits, then by splat index, which is where the
+// reference's stable sort of the splat-ordered pairs puts equal keys.  The
+// pair sort then runs on 4-byte keys over ceil(tile bits / 8) passes instead
+// of 8-byte keys over ceil((32 + tile bits) / 8) passes.
+
+// Depth keys: depth bits of the visible splats (depth > 0, so the bit order is
+// the float order); culled splats, which emit no pairs, go last.
+__global__ void depth_keys_kernel(int P, const float* __restrict__ depth, const int32_t* __restrict__ radii,
+                                  uint32_t* __restrict__ keys) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P) return;
+  keys[i] = radii[i] > 0 ? __float_as_uint(depth[i]) : 0xffffffffu;
+}
+
+__global__ void gather_u32_kernel(int P, const uint32_t* __restrict__ src, const uint32_t* __restrict__ order,
+                                  uint32_t* __restrict__ dst) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < P) dst[i] = src[order[i]];
+}
+
+size_t depth_order_ws_bytes(int P) {
+  const int64_t n = P > 0 ? P : 1;
+  return align256((size_t)n * 4) * 2 + sort_ws_bytes_t<uint32_t, uint32_t>(n);
+}
+
+hipError_t launch_depth_order(int P, const float* depth, const int32_t* radii, const uint32_t* tiles, uint32_t* order,
+                              uint32_t* ordered_offsets, void* ws, hipStream_t s) {
+  if (P <= 0) return hipSuccess;
+  char* w = static_cast<char*>(ws);
+  uint32_t* keys = reinterpret_cast<uint32_t*>(w);
+  w += align256((size_t)P * 4);
+  uint32_t* keys_sorted = reinterpret_cast<uint32_t*>(w);
+  w += align256((size_t)P * 4);
+  const unsigned grid = (unsigned)((P + 255) / 256);
+  hipLaunchKernelGGL(depth_keys_kernel, dim3(grid), dim3(256), 0, s, P, depth, radii, keys);
+  hipError_t e = sort_impl<uint32_t, uint32_t>(keys, nullptr, keys_sorted, order, P, 32, nullptr, w, s);
+  if (e != hipSuccess) return e;
+  // tiles touched in depth order, scanned (exclusive) in place; the sort's
+  // workspace is free again and holds the scan partials
+  hipLaunchKernelGGL(gather_u32_kernel, dim3(grid), dim3(256), 0, s, P, tiles, order, keys);
+  return scan_impl(keys, ordered_offsets, P, w, true, s);
+}
+
+// One lane per splat in depth order: its pairs (tile id, splat id) at its
+// scanned offset, row-major over the tile rectangle.  Writes stop at n_pairs
+// (the pair buffers' length), whatever count the caller passed.
+__global__ void __launch_bounds__(256) duplicate_ordered_kernel(int P, const uint32_t* __restrict__ order,
+                                                               const uint32_t* __restrict__ offsets,
+                                                               const float2* __restrict__ xy,
+                                                               const int32_t* __restrict__ radii, uint32_t gx,
+                                                               uint32_t gy, uint32_t n_pairs,
+                                                               uint32_t* __restrict__ tile_keys,
+                                                               uint32_t* __restrict__ ids) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= P) return;
+  const uint32_t i = order[k];
+  const int r = radii[i];
+  if (r <= 0) return;
+  uint32_t off = offsets[k];
+  const float2 c = xy[i];
+  uint32_t x0, y0, x1, y1;
+  tile_rect(c.x, c.y, r, gx, gy, x0, y0, x1, y1);
+  for (uint32_t y = y0; y < y1; y++)
+    for (uint32_t x = x0; x < x1; x++) {
+      if (off >= n_pairs) return;
+      tile_keys[off] = y * gx + x;
+      ids[off] = i;
+      off++;
+    }
+}
+
+hipError_t launch_duplicate_ordered(int P, const uint32_t* order, const uint32_t* offsets, const float* xy,
+                                    const int32_t* radii, uint32_t gx, uint32_t gy, int64_t n_pairs,
+                                    uint32_t* tile_keys, uint32_t* ids, hipStream_t s) {
+  if (P <= 0 || n_pairs <= 0) return hipSuccess;
+  hipLaunchKernelGGL(duplicate_ordered_kernel, dim3((P + 255) / 256), dim3(256), 0, s, P, order, offsets,
+                     reinterpret_cast<const float2*>(xy), radii, gx, gy, (uint32_t)n_pairs, tile_keys, ids);
+  return hipGetLastError();
+}
+
+size_t tile_sort_ws_bytes(int64_t n) { return sort_ws_bytes_t<uint32_t, uint64_t>(n); }
+
+hipError_t launch_sort_tiles(const uint32_t* tile_keys, const uint32_t* ids, uint64_t* keys_out, uint32_t* vals_out,
+                             int64_t n, int tile_bits, const float* depth, void* ws, hipStream_t s) {
+  return sort_impl<uint32_t, uint64_t>(tile_keys, ids, keys_out, vals_out, n, tile_bits,
+                                       reinterpret_cast<const uint32_t*>(depth), ws, s);
 }
 
 }  // namespace nest

@@ -96,14 +96,26 @@ struct RenderParams {
 hipError_t launch_preprocess(const PreprocessParams& p, hipStream_t s);
 hipError_t launch_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* ws, hipStream_t s);
 size_t scan_ws_bytes(int64_t n);
-hipError_t launch_duplicate(int P, const float* records_or_null, const float* xy, const float* depth,
-                            const int32_t* radii, const uint32_t* offsets, uint32_t gx, uint32_t gy,
-                            uint64_t* keys, uint32_t* vals, hipStream_t s);
 size_t sort_ws_bytes(int64_t n);
-// Sorts (keys_in, vals_in) into (keys_out, vals_out).  The inputs are used as
-// ping-pong buffers and are clobbered.
-hipError_t launch_sort_pairs(uint64_t* keys_in, uint32_t* vals_in, uint64_t* keys_out, uint32_t* vals_out,
+// Stable sort of (keys_in, vals_in) on key bits [0, end_bit) into
+// (keys_out, vals_out); the inputs are not written.
+hipError_t launch_sort_pairs(const uint64_t* keys_in, const uint32_t* vals_in, uint64_t* keys_out, uint32_t* vals_out,
                              int64_t n, int end_bit, void* ws, hipStream_t s);
+// Splat ids in (depth bits, id) order, culled splats last, and the exclusive
+// scan of their tiles touched in that order.
+size_t depth_order_ws_bytes(int P);
+hipError_t launch_depth_order(int P, const float* depth, const int32_t* radii, const uint32_t* tiles, uint32_t* order,
+                              uint32_t* ordered_offsets, void* ws, hipStream_t s);
+// (tile id, splat id) pairs of the splats in depth order; at most n_pairs
+// are written.
+hipError_t launch_duplicate_ordered(int P, const uint32_t* order, const uint32_t* offsets, const float* xy,
+                                    const int32_t* radii, uint32_t gx, uint32_t gy, int64_t n_pairs,
+                                    uint32_t* tile_keys, uint32_t* ids, hipStream_t s);
+// Stable sort of the depth-ordered pairs on tile bits [0, tile_bits): writes
+// the (tile << 32 | depth bits) keys and the splat ids in tile/depth order.
+size_t tile_sort_ws_bytes(int64_t n);
+hipError_t launch_sort_tiles(const uint32_t* tile_keys, const uint32_t* ids, uint64_t* keys_out, uint32_t* vals_out,
+                             int64_t n, int tile_bits, const float* depth, void* ws, hipStream_t s);
 hipError_t launch_tile_ranges(const uint64_t* keys, int64_t n, uint32_t* ranges, uint32_t ntiles, hipStream_t s);
 hipError_t launch_render(const RenderParams& p, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* dst, uint32_t value, int64_t n, hipStream_t s);

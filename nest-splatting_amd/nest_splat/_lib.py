@@ -27,9 +27,11 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP = range(7)
-GEOM_FIELDS = 7
-BIN_KEYS_UNSORTED, BIN_VALS_UNSORTED, BIN_KEYS, BIN_VALS, BIN_SORT_TMP = range(5)
+ABI_VERSION = 2
+(GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
+ GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP) = range(10)
+GEOM_FIELDS = 10
+BIN_PAIR_TILES, BIN_PAIR_IDS, BIN_KEYS, BIN_VALS, BIN_SORT_TMP = range(5)
 BIN_FIELDS = 5
 IMG_RANGES, IMG_FINAL_T, IMG_N_CONTRIB = range(3)
 IMG_FIELDS = 3
@@ -133,7 +135,7 @@ def lib():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
-        if L.nest_abi_version() != 1:
+        if L.nest_abi_version() != ABI_VERSION:
             raise RuntimeError("libnest_splat.so ABI version mismatch")
         _lib = L
     return _lib

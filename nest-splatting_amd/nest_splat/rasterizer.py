@@ -226,7 +226,9 @@ def geometry_arrays(res: ForwardResult, P: int) -> Dict[str, torch.Tensor]:
                 tiles=L.view(res.geom, o[L.GEOM_TILES], torch.int32, (n,))[:P],
                 offsets=L.view(res.geom, o[L.GEOM_OFFSETS], torch.int32, (n,))[:P],
                 records=L.view(res.geom, o[L.GEOM_RECORDS], torch.float32, (n, 32))[:P],
-                radii=L.view(res.geom, o[L.GEOM_RADII], torch.int32, (n,))[:P])
+                radii=L.view(res.geom, o[L.GEOM_RADII], torch.int32, (n,))[:P],
+                depth_order=L.view(res.geom, o[L.GEOM_DEPTH_ORDER], torch.int32, (n,))[:P],
+                order_offsets=L.view(res.geom, o[L.GEOM_ORDER_OFFSETS], torch.int32, (n,))[:P])
 
 
 def binning_arrays(res: ForwardResult, W: int, H: int) -> Dict[str, torch.Tensor]:
@@ -235,8 +237,8 @@ def binning_arrays(res: ForwardResult, W: int, H: int) -> Dict[str, torch.Tensor
     o, _ = L.binning_layout(NR)
     io, _ = L.image_layout(W, H)
     tiles = ((W + 15) // 16) * ((H + 15) // 16)
-    return dict(keys_unsorted=L.view(res.binning, o[L.BIN_KEYS_UNSORTED], torch.int64, (n,))[:NR],
-                vals_unsorted=L.view(res.binning, o[L.BIN_VALS_UNSORTED], torch.int32, (n,))[:NR],
+    return dict(pair_tiles=L.view(res.binning, o[L.BIN_PAIR_TILES], torch.int32, (n,))[:NR],
+                pair_ids=L.view(res.binning, o[L.BIN_PAIR_IDS], torch.int32, (n,))[:NR],
                 keys=L.view(res.binning, o[L.BIN_KEYS], torch.int64, (n,))[:NR],
                 vals=L.view(res.binning, o[L.BIN_VALS], torch.int32, (n,))[:NR],
                 ranges=L.view(res.image, io[L.IMG_RANGES], torch.int32, (tiles, 2)),

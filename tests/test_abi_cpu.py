@@ -31,7 +31,9 @@ def test_exports_match_header():
     for n in names:
         assert hasattr(lib, n), n
         assert n in L.EXPORTS, f"{n} has no ctypes signature"
-    assert lib.nest_abi_version() == 1
+    src = open(os.path.join(ROOT, "include", "nest_splat.h")).read()
+    header_version = int(re.search(r"#define NEST_ABI_VERSION (\d+)", src).group(1))
+    assert lib.nest_abi_version() == header_version == L.ABI_VERSION
 
 
 def test_struct_sizes_match_c_layout():
@@ -51,8 +53,12 @@ def test_layouts_are_aligned_and_monotone():
         offs, tot = L.geom_layout(P)
         assert all(o % 256 == 0 for o in offs) and offs == sorted(offs) and tot >= offs[-1]
         assert offs[L.GEOM_RECORDS + 1] - offs[L.GEOM_RECORDS] >= max(P, 1) * 128
+        assert offs[L.GEOM_ORDER_TMP] - offs[L.GEOM_DEPTH_ORDER] >= max(P, 1) * 8
+        assert tot - offs[L.GEOM_ORDER_TMP] >= max(P, 1) * 16  # depth keys + sort ping-pong
     offs, tot = L.binning_layout(5_000_000)
-    assert offs[L.BIN_KEYS] - offs[L.BIN_KEYS_UNSORTED] >= 5_000_000 * 12
+    assert offs[L.BIN_KEYS] - offs[L.BIN_PAIR_TILES] >= 5_000_000 * 8
+    assert offs[L.BIN_SORT_TMP] - offs[L.BIN_KEYS] >= 5_000_000 * 12
+    assert tot - offs[L.BIN_SORT_TMP] >= 5_000_000 * 16  # two u32 key/value ping-pong sets
     offs, tot = L.image_layout(1600, 1064)
     assert offs[L.IMG_FINAL_T] >= 6700 * 8 and tot >= 1600 * 1064 * 20
 

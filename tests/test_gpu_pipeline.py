@@ -46,6 +46,21 @@ def run_oracle(O, sc, cam_index=0, max_intersections=0):
     return pre, b, r
 
 
+def depth_ordered_pairs(pre, b):
+    """Splat order by (depth bits, index) with culled splats last, tiles
+    touched in that order, and for each depth-ordered pair its position in
+    the oracle's splat-ordered pair list."""
+    vis = pre["radii"] > 0
+    dkey = np.where(vis, pre["depth"].astype(np.float32).view(np.uint32), np.uint32(0xFFFFFFFF))
+    order = np.argsort(dkey, kind="stable").astype(np.uint32)
+    tiles = pre["tiles"].astype(np.int64)
+    starts = b["offsets"].astype(np.int64) - tiles  # inclusive scan -> first pair of each splat
+    lens = tiles[order]
+    NR = int(lens.sum())
+    src = np.repeat(starts[order] - (np.cumsum(lens) - lens), lens) + np.arange(NR)
+    return order, lens.astype(np.uint32), src
+
+
 @pytest.mark.parametrize("name", SCENES)
 def test_preprocess_binning_render_parity(oracle, name):
     from nest_splat import rasterizer as rz
@@ -71,8 +86,13 @@ def test_preprocess_binning_render_parity(oracle, name):
 
     assert res.num_rendered == b["num_rendered"]
     ba = {k: v.cpu().numpy() for k, v in rz.binning_arrays(res, sc.spec.W, sc.spec.H).items()}
-    np.testing.assert_array_equal(ba["keys_unsorted"].view(np.uint64), b["keys_unsorted"])
-    np.testing.assert_array_equal(ba["vals_unsorted"].view(np.uint32), b["vals_unsorted"])
+    # intermediate of the depth-first binning: the oracle's splat-ordered
+    # pairs regrouped splat by splat in (depth bits, index) order
+    order, lens, src = depth_ordered_pairs(pre, b)
+    np.testing.assert_array_equal(ga["depth_order"].view(np.uint32), order)
+    np.testing.assert_array_equal(ga["order_offsets"].view(np.uint32), np.cumsum(lens) - lens)
+    np.testing.assert_array_equal(ba["pair_tiles"].view(np.uint32), (b["keys_unsorted"][src] >> 32).astype(np.uint32))
+    np.testing.assert_array_equal(ba["pair_ids"].view(np.uint32), b["vals_unsorted"][src])
     np.testing.assert_array_equal(ba["keys"].view(np.uint64), b["keys"])
     np.testing.assert_array_equal(ba["vals"].view(np.uint32), b["vals"])
     np.testing.assert_array_equal(ba["ranges"].view(np.uint32), b["ranges"])

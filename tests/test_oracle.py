@@ -167,6 +167,44 @@ def test_binning_matches_brute_force(oracle, name):
     assert int((b["ranges"][:, 1].astype(np.int64) - b["ranges"][:, 0]).sum()) == NR
 
 
+def test_depth_first_binning_equals_pair_sort(oracle):
+    """The GPU binning sorts splats by depth bits (stable), emits their pairs
+    in that order and stable-sorts the pairs on the tile id alone.  That must
+    give the reference's sort of the splat-ordered (tile << 32 | depth) pairs,
+    ties included: depths are quantised to force many equal keys, and some
+    splats are culled."""
+    sc = scene("shell_small")
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    rng = np.random.default_rng(5)
+    pre["depth"] = np.round(pre["depth"] * 4.0).astype(np.float32) / np.float32(4.0)
+    cull = rng.random(pre["radii"].shape[0]) < 0.1
+    pre["radii"][cull] = 0
+    pre["tiles"][cull] = 0
+    b = oracle.binning(pre, W, H)
+    assert len(np.unique(b["keys"])) < b["num_rendered"]  # ties present
+    vis = pre["radii"] > 0
+    dkey = np.where(vis, pre["depth"].view(np.uint32), np.uint32(0xFFFFFFFF))
+    order = np.argsort(dkey, kind="stable")
+    gx = (W + 15) // 16
+    tiles_of, ids_of = [], []
+    for i in order:
+        if pre["radii"][i] <= 0:
+            continue
+        sel = b["vals_unsorted"] == i
+        tiles_of.append((b["keys_unsorted"][sel] >> np.uint64(32)).astype(np.int64))
+        ids_of.append(np.full(int(sel.sum()), i, np.uint32))
+    pair_tiles = np.concatenate(tiles_of)
+    pair_ids = np.concatenate(ids_of)
+    assert pair_tiles.max() < gx * ((H + 15) // 16)
+    perm = np.argsort(pair_tiles, kind="stable")
+    np.testing.assert_array_equal(pair_ids[perm], b["vals"])
+    composed = (pair_tiles[perm].astype(np.uint64) << np.uint64(32)) | pre["depth"][pair_ids[perm]].view(np.uint32).astype(np.uint64)
+    np.testing.assert_array_equal(composed, b["keys"])
+
+
 # --------------------------------------------------------------------- hash
 
 def _grid(oracle, L, F, T, H, S, table, align=False, contract=False, gridrange=(0.0, 1.0)):
