@@ -260,7 +260,9 @@ __global__ void __launch_bounds__(kSortThreads) radix_hist_kernel(const K* __res
 }
 
 // Stable scatter of one digit pass.  offsets is the exclusive scan of counts.
-// KOut == uint64_t with K == uint32_t composes the output key as
+// The block's keys are first placed in LDS in digit order (stable), then
+// written out so that consecutive lanes write consecutive positions of each
+// digit's run.  KOut == uint64_t with K == uint32_t composes the output key as
 // (key << 32) | low_bits[val] (the tile/depth key of the binning stage).
 template <typename K, typename KOut>
 __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __restrict__ keys_in,
@@ -269,8 +271,11 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
                                                                     uint32_t* __restrict__ vals_out, int64_t n, int shift,
                                                                     const uint32_t* __restrict__ offsets, uint32_t nblocks,
                                                                     const uint32_t* __restrict__ low_bits) {
+  static_assert(kRadix == kSortThreads, "one digit per thread in the block scan");
   __shared__ uint32_t hist[kSortWaves][kRadix];
-  __shared__ uint32_t gbase[kRadix];
+  __shared__ uint32_t gbase[kRadix];  // global start of the digit's run, minus its local start
+  __shared__ K skey[kSortTile];
+  __shared__ uint32_t sval[kSortTile];
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
   for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&hist[0][0])[i] = 0;
   for (int d = threadIdx.x; d < kRadix; d += kSortThreads) gbase[d] = offsets[(size_t)d * nblocks + blockIdx.x];
@@ -305,7 +310,9 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
     if (ok && lane == leader) hist[wid][d] = before + (uint32_t)__popcll(peers);
   }
   __syncthreads();
-  if (threadIdx.x < kRadix) {
+  // thread d: wave-exclusive prefix of digit d, then the block-exclusive
+  // prefix over digits (the digit's local start)
+  {
     const int d = threadIdx.x;
     uint32_t run = 0;
 #pragma unroll
@@ -314,6 +321,11 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
       hist[w][d] = run;
       run += c;
     }
+    uint64_t total;
+    const uint32_t lstart = (uint32_t)block_exclusive_scan_u64(run, &total);
+#pragma unroll
+    for (int w = 0; w < kSortWaves; w++) hist[w][d] += lstart;
+    gbase[d] -= lstart;
   }
   __syncthreads();
 #pragma unroll
@@ -321,13 +333,23 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
     const int64_t i = base + r * kWave + lane;
     if (i < n) {
       const uint32_t d = (uint32_t)(key[r] >> shift) & (kRadix - 1);
-      const uint32_t pos = gbase[d] + hist[wid][d] + rank[r];
-      if constexpr (sizeof(KOut) > sizeof(K))
-        keys_out[pos] = ((KOut)key[r] << 32) | (KOut)low_bits[val[r]];
-      else
-        keys_out[pos] = key[r];
-      vals_out[pos] = val[r];
+      const uint32_t lp = hist[wid][d] + rank[r];
+      skey[lp] = key[r];
+      sval[lp] = val[r];
     }
+  }
+  __syncthreads();
+  const int64_t left = n - (int64_t)blockIdx.x * kSortTile;
+  const int count = left < kSortTile ? (int)left : kSortTile;
+  for (int j = threadIdx.x; j < count; j += kSortThreads) {
+    const K k = skey[j];
+    const uint32_t v = sval[j];
+    const uint32_t pos = gbase[(uint32_t)(k >> shift) & (kRadix - 1)] + (uint32_t)j;
+    if constexpr (sizeof(KOut) > sizeof(K))
+      keys_out[pos] = ((KOut)k << 32) | (KOut)low_bits[v];
+    else
+      keys_out[pos] = k;
+    vals_out[pos] = v;
   }
 }
 
@@ -462,40 +484,68 @@ hipError_t launch_depth_order(int P, const float* depth, const int32_t* radii, c
   return scan_impl(keys, ordered_offsets, P, w, true, s);
 }
 
-// One lane per splat in depth order: its pairs (tile id, splat id) at its
-// scanned offset, row-major over the tile rectangle.  Writes stop at n_pairs
-// (the pair buffers' length), whatever count the caller passed.
-__global__ void __launch_bounds__(256) duplicate_ordered_kernel(int P, const uint32_t* __restrict__ order,
-                                                               const uint32_t* __restrict__ offsets,
-                                                               const float2* __restrict__ xy,
-                                                               const int32_t* __restrict__ radii, uint32_t gx,
-                                                               uint32_t gy, uint32_t n_pairs,
-                                                               uint32_t* __restrict__ tile_keys,
-                                                               uint32_t* __restrict__ ids) {
-  const int k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= P) return;
-  const uint32_t i = order[k];
-  const int r = radii[i];
-  if (r <= 0) return;
-  uint32_t off = offsets[k];
-  const float2 c = xy[i];
-  uint32_t x0, y0, x1, y1;
-  tile_rect(c.x, c.y, r, gx, gy, x0, y0, x1, y1);
-  for (uint32_t y = y0; y < y1; y++)
-    for (uint32_t x = x0; x < x1; x++) {
-      if (off >= n_pairs) return;
-      tile_keys[off] = y * gx + x;
-      ids[off] = i;
-      off++;
+// A workgroup owns 256 consecutive splats of the depth order, whose pairs
+// form one contiguous run of the output.  Each splat's (offset, id, tile
+// rectangle) goes to LDS; lanes then write consecutive pair positions
+// (coalesced), each finding its splat by binary search over the offsets.
+// Pair q of a splat is tile (y0 + q / w, x0 + q % w): row-major over the
+// rectangle, as the reference emits them.  Writes stop at n_pairs (the pair
+// buffers' length), whatever count the caller passed.
+constexpr int kDupThreads = 256;
+
+__global__ void __launch_bounds__(kDupThreads) duplicate_ordered_kernel(int P, const uint32_t* __restrict__ order,
+                                                                       const uint32_t* __restrict__ offsets,
+                                                                       const float2* __restrict__ xy,
+                                                                       const int32_t* __restrict__ radii, uint32_t gx,
+                                                                       uint32_t gy, uint32_t n_pairs,
+                                                                       uint32_t* __restrict__ tile_keys,
+                                                                       uint32_t* __restrict__ ids) {
+  __shared__ uint32_t s_off[kDupThreads], s_id[kDupThreads], s_x0[kDupThreads], s_y0[kDupThreads], s_w[kDupThreads];
+  const int k0 = blockIdx.x * kDupThreads;
+  const int k = k0 + (int)threadIdx.x;
+  // end of this group's run: the next group's first offset, or the total
+  const uint32_t end = (k0 + kDupThreads < P) ? offsets[k0 + kDupThreads] : n_pairs;
+  uint32_t off = end, id = 0, x0 = 0, y0 = 0, w = 1;
+  if (k < P) {
+    off = offsets[k];
+    id = order[k];
+    const int r = radii[id];
+    if (r > 0) {
+      uint32_t x1, y1;
+      tile_rect(xy[id].x, xy[id].y, r, gx, gy, x0, y0, x1, y1);
+      w = x1 > x0 ? x1 - x0 : 1u;
     }
+  }
+  s_off[threadIdx.x] = off;
+  s_id[threadIdx.x] = id;
+  s_x0[threadIdx.x] = x0;
+  s_y0[threadIdx.x] = y0;
+  s_w[threadIdx.x] = w;
+  __syncthreads();
+  const uint32_t begin = s_off[0];
+  const uint32_t stop = end < n_pairs ? end : n_pairs;
+  for (uint32_t p = begin + threadIdx.x; p < stop; p += kDupThreads) {
+    // last splat s with s_off[s] <= p; splats without pairs share their
+    // offset with the next one and are never chosen
+    int s = 0;
+#pragma unroll
+    for (int step = kDupThreads / 2; step > 0; step >>= 1)
+      if (s_off[s + step] <= p) s += step;
+    const uint32_t q = p - s_off[s];
+    const uint32_t ws = s_w[s];
+    const uint32_t dy = q / ws;
+    tile_keys[p] = (s_y0[s] + dy) * gx + s_x0[s] + (q - dy * ws);
+    ids[p] = s_id[s];
+  }
 }
 
 hipError_t launch_duplicate_ordered(int P, const uint32_t* order, const uint32_t* offsets, const float* xy,
                                     const int32_t* radii, uint32_t gx, uint32_t gy, int64_t n_pairs,
                                     uint32_t* tile_keys, uint32_t* ids, hipStream_t s) {
   if (P <= 0 || n_pairs <= 0) return hipSuccess;
-  hipLaunchKernelGGL(duplicate_ordered_kernel, dim3((P + 255) / 256), dim3(256), 0, s, P, order, offsets,
-                     reinterpret_cast<const float2*>(xy), radii, gx, gy, (uint32_t)n_pairs, tile_keys, ids);
+  hipLaunchKernelGGL(duplicate_ordered_kernel, dim3((P + kDupThreads - 1) / kDupThreads), dim3(kDupThreads), 0, s, P,
+                     order, offsets, reinterpret_cast<const float2*>(xy), radii, gx, gy, (uint32_t)n_pairs, tile_keys,
+                     ids);
   return hipGetLastError();
 }
 
