@@ -19,31 +19,30 @@
 //    rcp-based early reject, then the exact test;
 //  - an accepted hit updates the depth/normal/distortion state at once and
 //    enqueues (grid coordinate, weight, level count) in a per-lane LDS queue;
-//  - when any lane's queue is full, the wave drains every lane's queue in
-//    order: round r looks up every lane's r-th pending hit.  The gathers thus
-//    run with most lanes active instead of only the lanes that accepted one
-//    splat, and each pixel still accumulates its hits in front-to-back order.
+//  - when any lane's queue is full the wave drains: up to 64 pending hits,
+//    oldest first, are spread one per lane whatever pixel they belong to, so
+//    the gathers and the interpolation run with all lanes busy; each pixel's
+//    lane then accumulates its own hits in front-to-back order.
 #include "hashgrid.h"
 #include "nest_internal.h"
 #include "nest_math.h"
 
 namespace nest {
 
-// Launch shape, measured on the 1M-splat 1600x1064 L=16 F=4 scene (render ms):
+// Launch shape, measured on the 1M-splat 1600x1064 L=16 F=4 scene (render ms,
+// drain one hit per lane per round):
 //   batch 256 / queue 4 / 3 waves per SIMD / 8 corner loads in flight  10.2
 //   batch 128 (4 workgroups per CU by LDS), 4 waves, 4 loads in flight 13.1
 //   batch 128, queue 8, 3 waves                                        10.2
 //   2 waves (more VGPRs), two levels' 16 loads in flight               11.5
-// The gathers are latency-bound: loads in flight per SIMD count for more
-// than occupancy.
+// Loads in flight per SIMD count for more than occupancy.  Spreading the
+// pending hits over all lanes (drain_compact) then took it to 9.7: a round
+// drain keeps only ~47 of 64 lanes busy.
 constexpr int kRenderThreads = 256;
 constexpr int kBatch = 256;    // splats staged in LDS per batch
 constexpr int kRecChunks = 8;  // float4 chunks of the record staged per splat
-constexpr int kLanesPerRec = kRenderThreads / kBatch;
-constexpr int kChunksPerLane = kRecChunks / kLanesPerRec;
 constexpr int kQueue = 4;      // pending hash lookups per pixel
-static_assert(kBatch == 64 || kBatch == 128 || kBatch == 256, "batch");
-static_assert((kQueue & (kQueue - 1)) == 0, "queue length is a power of two");
+constexpr int kWaveLanes = 64;
 
 // Workgroup i runs on XCD i % 8; give XCD x a contiguous range of tiles.
 __device__ __forceinline__ uint32_t xcd_tile(uint32_t i, uint32_t n) {
@@ -53,8 +52,14 @@ __device__ __forceinline__ uint32_t xcd_tile(uint32_t i, uint32_t n) {
   return start + k;
 }
 
-// One drain round: every lane with a pending hit looks up its oldest one
-// (ring-buffer head) and accumulates it; lanes with an empty queue idle.
+__device__ __forceinline__ uint64_t lanemask_lt64() {
+  const uint32_t lane = threadIdx.x & (kWaveLanes - 1);
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// One drain round (any F): every lane with a pending hit looks up its oldest
+// one (ring-buffer head) and accumulates each level below its level count;
+// lanes with an empty queue idle.
 template <int F, int NACC, bool kHalf>
 __device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc, float4 (*hq)[kRenderThreads],
                                             uint8_t (*hl)[kRenderThreads], int& qhead, int& qn, float* acc) {
@@ -76,6 +81,170 @@ __device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc
   }
 }
 
+// Compacted drain (F <= 4): the wave takes up to 64 pending hits, depth-major
+// (every lane's head first, then second entries, ...), so each lane's share
+// is the oldest `take` entries of its queue.  Lane k looks up hit k for every
+// level and writes each level's F values into that hit's own queue slot; the
+// owning lane then accumulates its hits in queue order, acc = fmaf(v, w, acc).
+// Levels at or past a hit's level count are written as 0, and
+// fmaf(0, w, acc) == acc (w is finite and the accumulators never hold -0), as
+// in the round drain.  isrc is this wave's 64-byte item table: owner lane |
+// slot << 6.
+template <int F, int NACC, bool kHalf>
+__device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rsrc, float4 (*hq)[kRenderThreads],
+                                              uint8_t (*hl)[kRenderThreads], uint8_t* isrc, int& qhead, int& qn,
+                                              float* acc) {
+  static_assert(F <= 4, "a level's values fit one queue slot");
+  const uint32_t lane = threadIdx.x & (kWaveLanes - 1);
+  const uint32_t wbase = threadIdx.x - lane;
+  const uint64_t lt = lanemask_lt64();
+  uint32_t base = 0;
+  int take = 0;
+#pragma unroll
+  for (int d = 0; d < kQueue; d++) {
+    const uint64_t m = __ballot(qn > d);
+    const uint32_t k = base + (uint32_t)__popcll(m & lt);
+    if (qn > d && k < (uint32_t)kWaveLanes) {
+      isrc[k] = (uint8_t)(lane | ((uint32_t)((qhead + d) & (kQueue - 1)) << 6));
+      take = d + 1;
+    }
+    base += (uint32_t)__popcll(m);
+  }
+  const uint32_t items = base < (uint32_t)kWaveLanes ? base : (uint32_t)kWaveLanes;
+  __builtin_amdgcn_wave_barrier();
+  const bool work = lane < items;
+  float u[3] = {0.0f, 0.0f, 0.0f};
+  uint32_t nlev = 0, col = 0, wslot = 0;
+  if (work) {
+    const uint32_t s = isrc[lane];
+    col = wbase + (s & 63u);
+    wslot = s >> 6;
+    const float4 e = hq[wslot][col];
+    u[0] = e.x;
+    u[1] = e.y;
+    u[2] = e.z;
+    nlev = hl[wslot][col];
+  }
+  float wd[kQueue];
+#pragma unroll
+  for (int d = 0; d < kQueue; d++) wd[d] = d < take ? hq[(qhead + d) & (kQueue - 1)][threadIdx.x].w : 0.0f;
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int l = 0; l < NACC / F; l++) {
+    if (work) {
+      float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if ((uint32_t)l < nlev) level_interp_struct<F, kHalf>(rsrc, g.lv, l, g.pos_offset, g.interp, u, v);
+      hq[wslot][col] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int d = 0; d < kQueue; d++) {
+      if (d < take) {
+        const float4 r = hq[(qhead + d) & (kQueue - 1)][threadIdx.x];
+        const float rv[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(rv[f], wd[d], acc[l * F + f]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  qhead = (qhead + take) & (kQueue - 1);
+  qn -= take;
+}
+
+// Exact ray/surfel test of pixel (pxf, pyf) against a record's chunks 0-2
+// and its rho cut (CR/forward.cu:834-900 for the 2DGS kernel_type 0): the
+// homogeneous plane intersection, the 3D/2D rho choice, the near test on the
+// intersection depth and alpha = min(0.99, opacity * G).  Returns false when
+// the pixel rejects the splat.
+struct SplatHit {
+  float sx, sy, depth, alpha;
+  bool use3d;
+};
+
+__device__ __forceinline__ bool splat_hit(float4 q0, float4 q1, float4 q2, float cut, float pxf, float pyf, float beta,
+                                          SplatHit& h) {
+  const float Tu0 = q0.x, Tu1 = q0.y, Tu2 = q0.z, Tv0 = q0.w;
+  const float Tv1 = q1.x, Tv2 = q1.y, Tw0 = q1.z, Tw1 = q1.w;
+  const float Tw2 = q2.x;
+  const float k0 = pxf * Tw0 - Tu0, k1 = pxf * Tw1 - Tu1, k2 = pxf * Tw2 - Tu2;
+  const float l0 = pyf * Tw0 - Tv0, l1 = pyf * Tw1 - Tv1, l2 = pyf * Tw2 - Tv2;
+  const float p0 = k1 * l2 - k2 * l1, p1 = k2 * l0 - k0 * l2, p2 = k0 * l1 - k1 * l0;
+  if (p2 == 0.0f) return false;
+  const float dx = q2.y - pxf, dy = q2.z - pyf;
+  const float rho2d = 2.0f * (dx * dx + dy * dy);
+  // Per-lane early reject: an rcp-based rho3d within 1e-6 of the exact one,
+  // scaled down by 1e-5, above the splat's cut and rho2d above it too means
+  // alpha < 1/255 in the exact test.  NaNs take the exact path.
+  {
+    const float rc = __builtin_amdgcn_rcpf(p2);
+    const float sxa = p0 * rc, sya = p1 * rc;
+    if ((sxa * sxa + sya * sya) * 0.99999f > cut && rho2d > cut) return false;
+  }
+  const float sx = p0 / p2, sy = p1 / p2;
+  const float rho3d = sx * sx + sy * sy;
+  const float rho = fminf(rho3d, rho2d);
+  const bool use3d = rho3d <= rho2d;
+  const float depth = use3d ? (sx * Tw0 + sy * Tw1) + Tw2 : Tw2;
+  if (depth < 0.2f) return false;
+  const float power = -0.5f * rho;
+  if (power > 0.0f) return false;
+  float G = expf_ref(power);
+  if (beta > 0.0f) G = (float)((1.0 + (double)beta) * (double)G / (1.0 + (double)beta * (double)G));
+  const float alpha = fminf(0.99f, q2.w * G);
+  if (alpha < 1.0f / 255.0f) return false;
+  h.sx = sx;
+  h.sy = sy;
+  h.depth = depth;
+  h.alpha = alpha;
+  h.use3d = use3d;
+  return true;
+}
+
+// World point of an accepted hit: homotrans columns 0, 1, 3 (record chunks
+// 4-6) applied to (sx, sy, 1), or the splat centre when rho2d won.
+__device__ __forceinline__ void hit_world(float4 q4, float4 q5, float4 q6, const SplatHit& h, float xyz[3]) {
+  if (h.use3d) {
+    xyz[0] = h.sx * q4.x + h.sy * q4.w + q5.z;
+    xyz[1] = h.sx * q4.y + h.sy * q5.x + q5.w;
+    xyz[2] = h.sx * q4.z + h.sy * q5.y + q6.x;
+  } else {
+    xyz[0] = q5.z;
+    xyz[1] = q5.w;
+    xyz[2] = q6.x;
+  }
+}
+
+// Normalisation to [0,1]^3 (hashgrid.h:66-98): affine in normal mode (oob
+// outside the grid), the unbounded contraction otherwise.
+__device__ __forceinline__ void grid_coord(const GridParams& g, const float xyz[3], float u[3], bool& oob) {
+  oob = false;
+  if (!g.contract) {
+#pragma unroll
+    for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmin) * g.inv_size;
+    oob = (u[0] < 0 || u[0] > 1 || u[1] < 0 || u[1] > 1 || u[2] < 0 || u[2] > 1);
+  } else {
+#pragma unroll
+    for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmid) * g.inv_size;
+    const float nrm = sqrtf(u[0] * u[0] + u[1] * u[1] + u[2] * u[2]);
+    const float inv_nrm = 1.0f / nrm;
+    const float st = (nrm <= 1.0f) ? 1.0f : (2.0f - inv_nrm) * inv_nrm;
+#pragma unroll
+    for (int d = 0; d < 3; d++) {
+      u[d] = st * u[d];
+      u[d] = (u[d] + 2.0f) * 0.25f;
+    }
+  }
+}
+
+// Levels queried for a hit.  Levels at or past max_level contribute
+// fmaf(0, w, acc) == acc (the accumulators never hold -0), so they are not
+// queried.
+__device__ __forceinline__ uint8_t hit_levels(bool oob, uint32_t ap, uint32_t L) {
+  const uint32_t max_level = oob ? 0u : (ap < L ? ap : L);
+  return (uint8_t)(max_level < 255u ? max_level : 255u);
+}
+
 // LDS (32 KB of staged records + 17 KB of queue) allows three workgroups per
 // CU; amdgpu_waves_per_eu(3) gives the matching 168-VGPR budget, which holds
 // 64 accumulators and eight in-flight 16-byte corner loads.
@@ -85,6 +254,7 @@ render_kernel(const RenderParams p) {
   __shared__ float4 srec[kRecChunks][kBatch];
   __shared__ float4 hq[kHash ? kQueue : 1][kRenderThreads];
   __shared__ uint8_t hl[kHash ? kQueue : 1][kRenderThreads];
+  __shared__ uint8_t isrc[kHash ? kRenderThreads : 1];  // compacted-drain item tables, 64 per wave
 
   const uint32_t tile = xcd_tile(blockIdx.x, p.ntiles);
   const uint32_t tx = tile % p.gx, ty = tile / p.gx;
@@ -94,8 +264,9 @@ render_kernel(const RenderParams p) {
   const float pxf = (float)px, pyf = (float)py;
   bool done = !inside;
   // pixel block of this wave: 16 columns x 4 rows
+  const uint32_t wid = threadIdx.x / kWaveLanes;
   const float wx0 = (float)(tx * kTile), wx1 = wx0 + 15.0f;
-  const float wy0 = (float)(ty * kTile + 4u * (threadIdx.x >> 6)), wy1 = wy0 + 3.0f;
+  const float wy0 = (float)(ty * kTile + 4u * wid), wy1 = wy0 + 3.0f;
 
   const uint2 range = reinterpret_cast<const uint2*>(p.ranges)[tile];
 
@@ -126,16 +297,13 @@ render_kernel(const RenderParams p) {
     const bool last = start >= range.y || all_done;
     uint32_t n = 0;
     if (!last) {
-      // kLanesPerRec adjacent lanes stage record r, kChunksPerLane chunks each
-      const uint32_t r = threadIdx.x / kLanesPerRec;
-      const uint32_t h = (threadIdx.x % kLanesPerRec) * kChunksPerLane;
-      const uint32_t e = start + r;
+      const uint32_t e = start + threadIdx.x;
       if (e < range.y) {
         const uint32_t id = p.point_list[e];
-        const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id + h;
+        const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id;
 #pragma unroll
-        for (int c = 0; c < kChunksPerLane; c++) srec[h + c][r] = rec[c];
-        if (h <= 6 && 6 < h + kChunksPerLane) srec[6][r].z = __uint_as_float(id);
+        for (int c = 0; c < kRecChunks; c++) srec[c][threadIdx.x] = rec[c];
+        srec[6][threadIdx.x].z = __uint_as_float(id);
       }
       __syncthreads();
       n = min((uint32_t)kBatch, range.y - start);
@@ -150,47 +318,19 @@ render_kernel(const RenderParams p) {
         // acceptance bbox, so the alpha test rejects every pixel of it.
         const float4 bb = srec[7][j];
         if (bb.y < wx0 || bb.x > wx1 || bb.w < wy0 || bb.z > wy1) break;
-        const float4 q0 = srec[0][j], q1 = srec[1][j], q2 = srec[2][j];
-        const float Tu0 = q0.x, Tu1 = q0.y, Tu2 = q0.z, Tv0 = q0.w;
-        const float Tv1 = q1.x, Tv2 = q1.y, Tw0 = q1.z, Tw1 = q1.w;
-        const float Tw2 = q2.x;
-        const float k0 = pxf * Tw0 - Tu0, k1 = pxf * Tw1 - Tu1, k2 = pxf * Tw2 - Tu2;
-        const float l0 = pyf * Tw0 - Tv0, l1 = pyf * Tw1 - Tv1, l2 = pyf * Tw2 - Tv2;
-        const float p0 = k1 * l2 - k2 * l1, p1 = k2 * l0 - k0 * l2, p2 = k0 * l1 - k1 * l0;
-        if (p2 == 0.0f) break;
-        const float dx = q2.y - pxf, dy = q2.z - pyf;
-        const float rho2d = 2.0f * (dx * dx + dy * dy);
-        // Per-lane early reject: an rcp-based rho3d within 1e-6 of the exact
-        // one, scaled down by 1e-5, above the splat's cut and rho2d above it
-        // too means alpha < 1/255 in the exact test.  NaNs take the exact path.
-        {
-          const float cut = srec[6][j].y;
-          const float rc = __builtin_amdgcn_rcpf(p2);
-          const float sxa = p0 * rc, sya = p1 * rc;
-          if ((sxa * sxa + sya * sya) * 0.99999f > cut && rho2d > cut) break;
-        }
-        const float sx = p0 / p2, sy = p1 / p2;
-        const float rho3d = sx * sx + sy * sy;
-        const float rho = fminf(rho3d, rho2d);
-        const bool use3d = rho3d <= rho2d;
-        const float depth = use3d ? (sx * Tw0 + sy * Tw1) + Tw2 : Tw2;
-        if (depth < 0.2f) break;
-        const float power = -0.5f * rho;
-        if (power > 0.0f) break;
-        float G = expf_ref(power);
-        if (p.beta > 0.0f) G = (float)((1.0 + (double)p.beta) * (double)G / (1.0 + (double)p.beta * (double)G));
-        const float alpha = fminf(0.99f, q2.w * G);
-        if (alpha < 1.0f / 255.0f) break;
-        const float test_T = T * (1 - alpha);
+        SplatHit hit;
+        if (!splat_hit(srec[0][j], srec[1][j], srec[2][j], srec[6][j].y, pxf, pyf, p.beta, hit)) break;
+        const float test_T = T * (1 - hit.alpha);
         if (test_T < 0.0001f) {
           done = true;
           break;
         }
-        const float w = alpha * T;
+        const float w = hit.alpha * T;
         render_number++;
         if (p.max_intersections > 0 && render_number >= p.max_intersections) done = true;
 
         const float4 q3 = srec[3][j];
+        const float depth = hit.depth;
         const float Aa = 1 - T;
         const float m = mfac * (1 - 0.2f / depth);
         distortion += (m * m * Aa + M2 - 2 * m * M1) * w;
@@ -212,47 +352,18 @@ render_kernel(const RenderParams p) {
           for (int c = 0; c < NACC; c++)
             if (c < p.C) acc[c] = fmaf(col[c], w, acc[c]);
         } else {
-          const float4 q4 = srec[4][j], q5 = srec[5][j], q6 = srec[6][j];
           float xyz[3];
-          if (use3d) {
-            xyz[0] = sx * q4.x + sy * q4.w + q5.z;
-            xyz[1] = sx * q4.y + sy * q5.x + q5.w;
-            xyz[2] = sx * q4.z + sy * q5.y + q6.x;
-          } else {
-            xyz[0] = q5.z;
-            xyz[1] = q5.w;
-            xyz[2] = q6.x;
-          }
+          hit_world(srec[4][j], srec[5][j], srec[6][j], hit, xyz);
           pos_x += w * xyz[0];
           pos_y += w * xyz[1];
           pos_z += w * xyz[2];
           const uint32_t ap = __float_as_uint(q3.w);
-
-          // normalisation to [0,1]^3 (hashgrid.h:66-98)
           float u[3];
-          bool oob = false;
-          if (!g.contract) {
-#pragma unroll
-            for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmin) * g.inv_size;
-            oob = (u[0] < 0 || u[0] > 1 || u[1] < 0 || u[1] > 1 || u[2] < 0 || u[2] > 1);
-          } else {
-#pragma unroll
-            for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmid) * g.inv_size;
-            const float nrm = sqrtf(u[0] * u[0] + u[1] * u[1] + u[2] * u[2]);
-            const float inv_nrm = 1.0f / nrm;
-            const float st = (nrm <= 1.0f) ? 1.0f : (2.0f - inv_nrm) * inv_nrm;
-#pragma unroll
-            for (int d = 0; d < 3; d++) {
-              u[d] = st * u[d];
-              u[d] = (u[d] + 2.0f) * 0.25f;
-            }
-          }
-          // Levels at or past max_level contribute fmaf(0, w, acc) == acc
-          // (the accumulators never hold -0), so they are not queried.
-          const uint32_t max_level = oob ? 0u : (ap < L ? ap : L);
+          bool oob;
+          grid_coord(g, xyz, u, oob);
           const int slot = (qhead + qn) & (kQueue - 1);
           hq[slot][threadIdx.x] = make_float4(u[0], u[1], u[2], w);
-          hl[slot][threadIdx.x] = (uint8_t)(max_level < 255u ? max_level : 255u);
+          hl[slot][threadIdx.x] = hit_levels(oob, ap, L);
           qn++;
           float apc0, apc1;
           if (ap <= 4u) {
@@ -275,9 +386,12 @@ render_kernel(const RenderParams p) {
     }
     const bool batch_end = j >= n;
     if constexpr (kHash) {
-      // one round whenever a lane is full; at the end, rounds until empty
+      // whenever a lane is full; at the end, until every queue is empty
       if (__ballot(qn == kQueue) || (last && __ballot(qn > 0))) {
-        drain_round<F, NACC, kHalf>(g, rsrc, hq, hl, qhead, qn, acc);
+        if constexpr (F <= 4)
+          drain_compact<F, NACC, kHalf>(g, rsrc, hq, hl, isrc + wid * kWaveLanes, qhead, qn, acc);
+        else
+          drain_round<F, NACC, kHalf>(g, rsrc, hq, hl, qhead, qn, acc);
         if (last) continue;
       }
     }
