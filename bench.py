@@ -40,8 +40,8 @@ def render_algorithmic_bytes(NR: int, hits: int, HW: int, L: int, F: int, e: int
 
 def cpu_baseline(scene, gpu_hits_total: int, row_stride: int, threads: int):
     """Oracle (oracle/nest_oracle.c) on this host: full preprocess and
-    binning, render of every row_stride-th tile row with `threads` OpenMP
-    threads, MLP of the sampled pixels; scaled to one frame by the sample's
+    binning, render of every row_stride-th tile row and MLP of its pixels with
+    `threads` OpenMP threads; scaled to one frame by the sample's
     share of tile/splat pairs plus hits (render) and of pixels (MLP)."""
     import numpy as np
     from oracle import oracle as O
@@ -75,7 +75,7 @@ def cpu_baseline(scene, gpu_hits_total: int, row_stride: int, threads: int):
     alpha = r["others"][1].reshape(-1)[idx]
     t4 = time.perf_counter()
     O.mlp(np.ascontiguousarray(feat), dirs, alpha, scene.W1, scene.W2, scene.W3, sp.mlp_dtype,
-          np.asarray(sp.bg, np.float32))
+          np.asarray(sp.bg, np.float32), threads=threads)
     t5 = time.perf_counter()
     pix_share = idx.size / (W * H)
     frame_s = (t1 - t0) + (t2 - t1) + (t3 - t2) / share + (t5 - t4) / pix_share
@@ -87,7 +87,7 @@ def cpu_baseline(scene, gpu_hits_total: int, row_stride: int, threads: int):
         "sample": (f"oracle C port: full preprocess ({t1 - t0:.2f} s, 1 thread) and binning ({t2 - t1:.2f} s, "
                    f"1 thread); render of every {row_stride}th tile row ({len(rows)} of {gy} rows, {t3 - t2:.2f} s, "
                    f"{threads} OpenMP threads, scaled by its {share:.4f} share of pairs+hits); fp32-accumulated MLP "
-                   f"of those {idx.size} pixels ({t5 - t4:.2f} s, 1 thread, scaled by pixel share); "
+                   f"of those {idx.size} pixels ({t5 - t4:.2f} s, {threads} OpenMP threads, scaled by pixel share); "
                    f"extrapolated frame {frame_s:.2f} s"),
         "frame_s": frame_s,
     }
@@ -147,7 +147,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-row-stride", type=int, default=16)
+    ap.add_argument("--cpu-row-stride", type=int, default=4)
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "render_traffic_cfg3.json"),
                     help="JSON with counter-measured HBM bytes per render launch (from rocprofv3 --pmc)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,

@@ -747,12 +747,17 @@ static inline float round_dtype(float v, int dtype)
  * accumulated in double and rounded to binary32 once. */
 void or_mlp(int npix, int C, const float *feat, const float *dirs, const float *alpha,
             const float *W1, const float *W2, const float *W3, int Nw, int dtype,
-            const float *bg, float *rgb_out /* [3][npix] */)
+            const float *bg, float *rgb_out /* [3][npix] */, int nthreads)
 {
     const int Din = C + 16;
+    int use_bg = bg && (bg[0] + bg[1] + bg[2] > 0.0f);
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+    {
+    /* pixels are independent: each thread owns its activations */
     float *x = (float *)malloc(sizeof(float) * (size_t)(Din + 2 * Nw));
     float *h1 = x + Din, *h2 = h1 + Nw;
-    int use_bg = bg && (bg[0] + bg[1] + bg[2] > 0.0f);
+#pragma omp for schedule(static)
     for (int p = 0; p < npix; p++) {
         for (int c = 0; c < C; c++) x[c] = round_dtype(feat[(size_t)c * npix + p], dtype);
         float u[3];
@@ -783,6 +788,7 @@ void or_mlp(int npix, int C, const float *feat, const float *dirs, const float *
         }
     }
     free(x);
+    }
 }
 
 /* ------------------------------------------------------------------ */

@@ -75,7 +75,7 @@ def lib():
         L.or_grid_encode.argtypes = [ct.POINTER(OrGrid), ct.c_int, f32p, f32p]
         L.or_level_scale.argtypes = [ct.c_float, ct.c_int, ct.c_int, ct.POINTER(ct.c_float), ct.POINTER(ct.c_uint32)]
         L.or_mlp.argtypes = [ct.c_int, ct.c_int, f32p, f32p, ct.c_void_p, f32p, f32p, f32p, ct.c_int, ct.c_int,
-                             ct.c_void_p, f32p]
+                             ct.c_void_p, f32p, ct.c_int]
         L.or_sh16.argtypes = [f32p, f32p]
         L.or_rvq_decode.argtypes = [ct.c_int, ct.c_int, ct.c_int, ct.c_int, f32p, u16p, ct.c_void_p, f32p]
         L.or_activate.argtypes = [ct.c_int, f32p, f32p, f32p, f32p, f32p, f32p]
@@ -223,15 +223,17 @@ def sh16(u):
 DTYPES = {"f32": 0, "f16": 1, "bf16": 2}
 
 
-def mlp(feat_cm, dirs, alpha, W1, W2, W3, dtype="f32", bg=None):
-    """feat_cm: [C, npix] channel-major; dirs: [npix, 3] unit; returns [3, npix]."""
+def mlp(feat_cm, dirs, alpha, W1, W2, W3, dtype="f32", bg=None, threads=0):
+    """feat_cm: [C, npix] channel-major; dirs: [npix, 3] unit; returns [3, npix].
+    threads: OpenMP threads over pixels (0 = the runtime default)."""
     C, npix = feat_cm.shape
     out = np.zeros((3, npix), np.float32)
     a = None if alpha is None else _c(alpha, np.float32).reshape(-1)
     b = None if bg is None else _c(bg, np.float32)
     lib().or_mlp(npix, C, _c(feat_cm, np.float32), _c(dirs, np.float32),
                  None if a is None else a.ctypes.data, _c(W1, np.float32), _c(W2, np.float32),
-                 _c(W3, np.float32), W1.shape[0], DTYPES[dtype], None if b is None else b.ctypes.data, out)
+                 _c(W3, np.float32), W1.shape[0], DTYPES[dtype], None if b is None else b.ctypes.data, out,
+                 int(threads))
     return out
 
 
