@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 2
+#define NEST_ABI_VERSION 3
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -99,6 +99,11 @@ typedef struct nest_splats {
   const float *homotrans;      /* [P,4,4] build_H, hash path */
   const float *ap_level;       /* [P,1] appearance level, NULL = no cap */
   const float *colors_precomp; /* [P,channels], colour path (levels == 0) */
+  const float *shs;            /* [P,sh_coeffs,3] SH coefficients: colour path with
+                                  3 channels when colors_precomp is NULL
+                                  (computeColorFromSH, CR/forward.cu:21-72) */
+  int32_t sh_degree;           /* active SH degree, 0..3 */
+  int32_t sh_coeffs;           /* coefficients per splat, >= (sh_degree+1)^2 */
 } nest_splats;
 
 /* Frame outputs (device): out_color [channels,H,W], out_others [14,H,W] and
@@ -163,7 +168,9 @@ const char *nest_last_error(void);
 #define NEST_GEOM_ORDER_OFFSETS 8  /* u32 [P]    exclusive scan of tiles
                                       touched in that order            */
 #define NEST_GEOM_ORDER_TMP 9      /* depth sort scratch              */
-#define NEST_GEOM_FIELDS 10
+#define NEST_GEOM_RGB 10           /* f32 [P,3]  colour from SH (when shs is set) */
+#define NEST_GEOM_CLAMPED 11       /* u8  [P,3]  SH colour channel clamped to 0 */
+#define NEST_GEOM_FIELDS 12
 int nest_geom_layout(int32_t P, size_t offsets[NEST_GEOM_FIELDS], size_t *total_bytes);
 
 /* The pairs are emitted in depth order and sorted on the tile bits only;
@@ -207,6 +214,14 @@ int nest_forward_render(const nest_raster_settings *settings, const nest_hashgri
                         void *binning_ws, size_t binning_bytes, void *image_ws, size_t image_bytes,
                         int64_t num_rendered, const nest_frame_outputs *out,
                         nest_timing *timing, void *stream);
+
+/* markVisible (DSR/rasterize_points.cu:452-470, CR/rasterizer_impl.cu:198-210,
+ * checkFrustum :54-66): present[i] = 1 when the view-space depth of
+ * means3D[i] exceeds 0.2 (in_frustum, CR/auxiliary.h:190-215), else 0.
+ * viewmatrix is the host copy of the 4x4 world-to-view matrix (the flat
+ * float[16] the kernels read); present is a device byte array [P]. */
+int nest_mark_visible(int32_t P, const float *means3D, const float viewmatrix[16], uint8_t *present,
+                      void *stream);
 
 /* ---- building blocks ----------------------------------------------------- */
 

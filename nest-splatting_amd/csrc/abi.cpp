@@ -165,8 +165,19 @@ int check_splats(const nest_splats* sp, bool need_geometry) {
   if (sp->P < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "P must be >= 0 (got %d)", sp->P);
   if (need_geometry && sp->P > 0 && (!sp->means3D || !sp->scales || !sp->rotations || !sp->opacities))
     return fail(NEST_ERR_INVALID_ARGUMENT, "means3D, scales, rotations and opacities are required");
+  if (sp->shs && !sp->colors_precomp) {
+    if (sp->sh_degree < 0 || sp->sh_degree > 3)
+      return fail(NEST_ERR_UNSUPPORTED, "SH degree must be 0..3 (got %d)", sp->sh_degree);
+    if (sp->sh_coeffs < (sp->sh_degree + 1) * (sp->sh_degree + 1))
+      return fail(NEST_ERR_INVALID_ARGUMENT, "%d SH coefficients per splat cannot hold degree %d", sp->sh_coeffs,
+                  sp->sh_degree);
+  }
   return NEST_OK;
 }
+
+// SH colours are evaluated when SH coefficients come without precomputed
+// colours (CR/forward.cu:417-424).
+bool sh_colours(const nest_splats* sp) { return sp->shs && !sp->colors_precomp; }
 
 }  // namespace
 
@@ -191,6 +202,8 @@ int nest_geom_layout(int32_t P, size_t offsets[NEST_GEOM_FIELDS], size_t* total)
   o[NEST_GEOM_DEPTH_ORDER] = c.take(n * 4);
   o[NEST_GEOM_ORDER_OFFSETS] = c.take(n * 4);
   o[NEST_GEOM_ORDER_TMP] = c.take(depth_order_ws_bytes((int)n));
+  o[NEST_GEOM_RGB] = c.take(n * 12);
+  o[NEST_GEOM_CLAMPED] = c.take(n * 3);
   if (offsets)
     for (int i = 0; i < NEST_GEOM_FIELDS; i++) offsets[i] = o[i];
   if (total) *total = c.off;
@@ -266,6 +279,14 @@ int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp,
   p.depth = reinterpret_cast<float*>(g + off[NEST_GEOM_DEPTH]);
   p.tiles = reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_TILES]);
   p.records = reinterpret_cast<float*>(g + off[NEST_GEOM_RECORDS]);
+  if (sh_colours(sp)) {
+    p.shs = sp->shs;
+    p.sh_degree = sp->sh_degree;
+    p.sh_coeffs = sp->sh_coeffs;
+    memcpy(p.campos, rs->campos, sizeof(p.campos));
+    p.rgb = reinterpret_cast<float*>(g + off[NEST_GEOM_RGB]);
+    p.clamped = reinterpret_cast<uint8_t*>(g + off[NEST_GEOM_CLAMPED]);
+  }
 
   StageTimer tm(timing, s);
   tm.begin(NEST_STAGE_PREPROCESS);
@@ -364,8 +385,11 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     g.table_bytes = (uint32_t)tbytes;
     g.table_rows = (uint32_t)gr->table_rows;
   } else {
-    if (sp->P > 0 && !sp->colors_precomp)
-      return fail(NEST_ERR_INVALID_ARGUMENT, "levels == 0 selects the colour path, which needs colors_precomp");
+    if (sp->P > 0 && !sp->colors_precomp && !sp->shs)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "levels == 0 selects the colour path, which needs colors_precomp or shs");
+    // SH colours are RGB (NUM_CHANNELS, CR/rasterizer_impl.cu:320-323)
+    if (sh_colours(sp) && out->channels != 3)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "colours from SH have 3 channels, out_color has %d", out->channels);
   }
 
   size_t go[NEST_GEOM_FIELDS], gneed = 0, bo[NEST_BIN_FIELDS], bneed = 0, io[NEST_IMG_FIELDS], ineed = 0;
@@ -422,7 +446,9 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   rp.ranges = ranges;
   rp.point_list = vals;
   rp.records = reinterpret_cast<const float*>(g + go[NEST_GEOM_RECORDS]);
-  rp.colors = sp->colors_precomp;
+  // feature_ptr of CR/rasterizer_impl.cu:399: precomputed colours, else the
+  // colours preprocess evaluated from SH
+  rp.colors = sh_colours(sp) ? reinterpret_cast<const float*>(g + go[NEST_GEOM_RGB]) : sp->colors_precomp;
   rp.out_color = out->out_color;
   rp.out_others = out->out_others;
   rp.final_T = reinterpret_cast<float*>(im + io[NEST_IMG_FINAL_T]);
@@ -431,6 +457,15 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   if ((rc = check_stage(launch_render(rp, s), "render", rs->debug, s))) return rc;
   tm.end();
   return NEST_OK;
+}
+
+int nest_mark_visible(int32_t P, const float* means3D, const float viewmatrix[16], uint8_t* present, void* stream) {
+  if (P < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "P must be >= 0 (got %d)", P);
+  if (P == 0) return NEST_OK;
+  if (!means3D || !viewmatrix || !present)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "means3D, viewmatrix and present are required");
+  hipError_t e = launch_mark_visible(P, means3D, viewmatrix, present, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? NEST_OK : hip_fail(e, "mark_visible");
 }
 
 int nest_timing_read(nest_timing* t) {

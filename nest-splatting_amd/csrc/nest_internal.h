@@ -37,6 +37,10 @@ struct PreprocessParams {
   const float* opac;
   const float* homotrans;   // may be null (colour path)
   const float* ap_level;    // may be null
+  const float* shs;         // [P, sh_coeffs, 3] or null: RGB from SH for the colour path
+  int sh_degree;
+  int sh_coeffs;
+  float campos[3];
   // outputs
   int32_t* radii;
   int32_t* radii_user;      // optional second copy (the caller's radii tensor)
@@ -44,7 +48,12 @@ struct PreprocessParams {
   float* depth;
   uint32_t* tiles;
   float* records;
+  float* rgb;               // [P, 3], written when shs is set
+  uint8_t* clamped;         // [P, 3], written when shs is set
 };
+
+// markVisible: present[i] = 1 when splat i lies beyond the near plane.
+hipError_t launch_mark_visible(int P, const float* means, const float view[16], uint8_t* present, hipStream_t s);
 
 // Per-level constants of the hash grid, computed on the host in the same
 // float order as the reference's query_feature (CR/hashgrid.h:122-131).

@@ -3,9 +3,9 @@
 //
 // Semantics: preprocessCUDA (CR/forward.cu:323-441) with compute_transmat
 // (:237-290), compute_aabb (:294-320), in_frustum / quat_to_rotmat / getRect
-// (CR/auxiliary.h:72-82, :190-240) -- CR = submodules/diff-surfel-rasterization/
-// cuda_rasterizer.  The SH->RGB evaluation of the reference is dead work on
-// the hash path and is not done here.
+// (CR/auxiliary.h:72-82, :190-240) and, for the colour path without
+// precomputed colours, computeColorFromSH (CR/forward.cu:21-72, called at
+// :417-424) -- CR = submodules/diff-surfel-rasterization/cuda_rasterizer.
 //
 // One lane per splat; every input is read once with 4/8/16-byte loads and the
 // record is written as eight 16-byte stores (one 128-byte line per splat), so
@@ -14,6 +14,54 @@
 #include "nest_math.h"
 
 namespace nest {
+
+// Real spherical-harmonic normalisations of degrees 0-3 in the basis order of
+// the 3DGS colour model: C0 = 1/(2 sqrt(pi)), C1 = sqrt(3/(4 pi)),
+// C2 = {sqrt(15/pi)/2, -sqrt(15/pi)/2, sqrt(5/pi)/4, -sqrt(15/pi)/2,
+// sqrt(15/pi)/4}, C3 = {-sqrt(35/(2 pi))/4, sqrt(105/pi)/2, -sqrt(21/(2 pi))/4,
+// sqrt(7/pi)/4, -sqrt(21/(2 pi))/4, sqrt(105/pi)/4, -sqrt(35/(2 pi))/4}.
+constexpr float kShC0 = 0.28209479177387814f;
+constexpr float kShC1 = 0.4886025119029199f;
+constexpr float kShC2[5] = {1.0925484305920792f, -1.0925484305920792f, 0.31539156525252005f, -1.0925484305920792f,
+                            0.5462742152960396f};
+constexpr float kShC3[7] = {-0.5900435899266435f, 2.890611442640554f, -0.4570457994644658f, 0.3731763325901154f,
+                            -0.4570457994644658f, 1.445305721320277f, -0.5900435899266435f};
+
+// RGB of splat i from its SH coefficients (sh: M rows of 3 floats) seen from
+// campos, evaluated term by term in the reference's order; + 0.5, then
+// negative channels clamp to 0 and are flagged.
+__device__ __forceinline__ void sh_to_rgb(int deg, const float* sh, float px, float py, float pz, const float* campos,
+                                          float rgb[3], uint8_t clamped[3]) {
+  float dx = px - campos[0], dy = py - campos[1], dz = pz - campos[2];
+  const float len = sqrtf(dx * dx + dy * dy + dz * dz);
+  dx = dx / len;
+  dy = dy / len;
+  dz = dz / len;
+#pragma unroll
+  for (int c = 0; c < 3; c++) {
+    float r = kShC0 * sh[c];
+    if (deg > 0) {
+      const float x = dx, y = dy, z = dz;
+      r = r - kShC1 * y * sh[3 + c] + kShC1 * z * sh[6 + c] - kShC1 * x * sh[9 + c];
+      if (deg > 1) {
+        const float xx = x * x, yy = y * y, zz = z * z;
+        const float xy = x * y, yz = y * z, xz = x * z;
+        r = r + kShC2[0] * xy * sh[12 + c] + kShC2[1] * yz * sh[15 + c] + kShC2[2] * (2.0f * zz - xx - yy) * sh[18 + c] +
+            kShC2[3] * xz * sh[21 + c] + kShC2[4] * (xx - yy) * sh[24 + c];
+        if (deg > 2) {
+          r = r + kShC3[0] * y * (3.0f * xx - yy) * sh[27 + c] + kShC3[1] * xy * z * sh[30 + c] +
+              kShC3[2] * y * (4.0f * zz - xx - yy) * sh[33 + c] +
+              kShC3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy) * sh[36 + c] +
+              kShC3[4] * x * (4.0f * zz - xx - yy) * sh[39 + c] + kShC3[5] * z * (xx - yy) * sh[42 + c] +
+              kShC3[6] * x * (xx - 3.0f * yy) * sh[45 + c];
+        }
+      }
+    }
+    r += 0.5f;
+    clamped[c] = r < 0.0f ? 1 : 0;
+    rgb[c] = r < 0.0f ? 0.0f : r;
+  }
+}
 
 __global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams p) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -105,6 +153,16 @@ __global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams 
   if (p.radii_user) p.radii_user[i] = ir;
   reinterpret_cast<float2*>(p.xy)[i] = make_float2(pimx, pimy);
   p.tiles[i] = area;
+  if (p.shs) {
+    float rgb[3];
+    uint8_t cl[3];
+    sh_to_rgb(p.sh_degree, p.shs + (size_t)i * p.sh_coeffs * 3, px, py, pz, p.campos, rgb, cl);
+#pragma unroll
+    for (int c = 0; c < 3; c++) {
+      p.rgb[3 * (size_t)i + c] = rgb[c];
+      p.clamped[3 * (size_t)i + c] = cl[c];
+    }
+  }
 
   uint32_t ap = 0xffffffffu;
   if (p.ap_level) ap = f2u_sat(floorf(p.ap_level[i]));
@@ -168,6 +226,30 @@ hipError_t launch_preprocess(const PreprocessParams& p, hipStream_t s) {
   if (p.P <= 0) return hipSuccess;
   const int blocks = (p.P + 255) / 256;
   hipLaunchKernelGGL(preprocess_kernel, dim3(blocks), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+// checkFrustum / in_frustum (CR/rasterizer_impl.cu:54-66, CR/auxiliary.h:
+// 190-215): only the near test p_view.z > 0.2 decides; the projected point the
+// reference also computes is unused there.
+struct ViewMatrix {
+  float m[16];
+};
+
+__global__ void __launch_bounds__(256) mark_visible_kernel(int P, const float* __restrict__ means, const ViewMatrix V,
+                                                           uint8_t* __restrict__ present) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P) return;
+  const float px = means[3 * i + 0], py = means[3 * i + 1], pz = means[3 * i + 2];
+  const float vz = V.m[2] * px + V.m[6] * py + V.m[10] * pz + V.m[14];
+  present[i] = vz <= 0.2f ? 0 : 1;
+}
+
+hipError_t launch_mark_visible(int P, const float* means, const float view[16], uint8_t* present, hipStream_t s) {
+  if (P <= 0) return hipSuccess;
+  ViewMatrix V;
+  for (int k = 0; k < 16; k++) V.m[k] = view[k];
+  hipLaunchKernelGGL(mark_visible_kernel, dim3((P + 255) / 256), dim3(256), 0, s, P, means, V, present);
   return hipGetLastError();
 }
 

@@ -9,7 +9,8 @@ GaussianRasterizer(raster_settings, hashgrid_settings).forward(...) returning
 markVisible (:310-319) and rasterize_gaussians (:21-66).
 
 Scope: the forward pass of render mode 0 ("baseline"): hash-grid features
-when HashGridSettings.L > 0, precomputed per-splat colours when L == 0.  Modes,
+when HashGridSettings.L > 0; when L == 0, precomputed per-splat colours or
+RGB evaluated from SH coefficients (degree <= 3) in preprocess.  Modes,
 kernels and options that the reference implements for other methods raise
 NotImplementedError instead of returning zeros; backward raises as well
 (forward-only renderer).
@@ -79,12 +80,19 @@ class _RasterizeGaussians(torch.autograd.Function):
                                     interpolation=int(hashgrid_settings.interpolation))
             colors = None
         else:
-            if _empty(colors_precomp):
-                raise NotImplementedError("SH evaluation in the rasterizer is not implemented; pass colors_precomp")
             grid = _rz.HashGridDesc(0, 1, 0.0, 0, None, np.zeros(1, np.int64), np.zeros(2, np.float32))
-            colors = colors_precomp.detach()
-            if colors.dim() != 2 or colors.shape[1] != C:
-                raise ValueError(f"colors_precomp must be [P, {C}] (shape_dims[2])")
+            if _empty(colors_precomp):
+                # colours from SH in preprocess (CR/forward.cu:417-424); RGB only
+                # (CR/rasterizer_impl.cu:320-323)
+                if _empty(sh):
+                    raise ValueError("the colour path (L == 0) needs colors_precomp or shs")
+                if C != 3:
+                    raise RuntimeError("For non-RGB, provide precomputed Gaussian colors!")
+                colors = None
+            else:
+                colors = colors_precomp.detach()
+                if colors.dim() != 2 or colors.shape[1] != C:
+                    raise ValueError(f"colors_precomp must be [P, {C}] (shape_dims[2])")
         s = raster_settings
         settings = _rz.make_settings(s.image_height, s.image_width, s.tanfovx, s.tanfovy, s.viewmatrix, s.projmatrix,
                                      s.campos, s.scale_modifier, s.beta, s.if_contract, s.max_intersections,
@@ -92,7 +100,8 @@ class _RasterizeGaussians(torch.autograd.Function):
         res = _rz.rasterize_forward(settings, grid, means3D.detach(), opacities.detach(), scales.detach(),
                                     rotations.detach(), homotrans=None if _empty(homotrans) else homotrans.detach(),
                                     ap_level=None if _empty(ap_level) else ap_level.detach(), colors_precomp=colors,
-                                    channels=C)
+                                    channels=C, shs=None if (level > 0 or colors is not None or _empty(sh)) else
+                                    sh.detach(), sh_degree=int(raster_settings.sh_degree))
         ctx.num_rendered = res.num_rendered
         dev = means3D.device
         trans_avg = torch.zeros((0, 1), dtype=torch.float32, device=dev)
@@ -139,7 +148,9 @@ class GaussianRasterizer(nn.Module):
         self.hashgrid_settings = hashgrid_settings
 
     def markVisible(self, positions):
-        raise NotImplementedError("markVisible is not implemented by this forward renderer")
+        # Mark visible points (based on frustum culling for camera) with a boolean
+        with torch.no_grad():
+            return _rz.mark_visible(positions, self.raster_settings.viewmatrix)
 
     def forward(self, means3D, means2D, opacities, shs=None, colors_precomp=None, scales=None, rotations=None,
                 cov3D_precomp=None, homotrans=None, ap_level=None, features=None, offsets=None, gridrange=None,

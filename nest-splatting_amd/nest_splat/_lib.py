@@ -27,10 +27,10 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
- GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP) = range(10)
-GEOM_FIELDS = 10
+ GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
+GEOM_FIELDS = 12
 BIN_PAIR_TILES, BIN_PAIR_IDS, BIN_KEYS, BIN_VALS, BIN_SORT_TMP = range(5)
 BIN_FIELDS = 5
 IMG_RANGES, IMG_FINAL_T, IMG_N_CONTRIB = range(3)
@@ -57,7 +57,8 @@ class HashGrid(ct.Structure):
 class Splats(ct.Structure):
     _fields_ = [("struct_size", ct.c_uint32), ("P", ct.c_int32), ("means3D", ct.c_void_p), ("scales", ct.c_void_p),
                 ("rotations", ct.c_void_p), ("opacities", ct.c_void_p), ("homotrans", ct.c_void_p),
-                ("ap_level", ct.c_void_p), ("colors_precomp", ct.c_void_p)]
+                ("ap_level", ct.c_void_p), ("colors_precomp", ct.c_void_p), ("shs", ct.c_void_p),
+                ("sh_degree", ct.c_int32), ("sh_coeffs", ct.c_int32)]
 
 
 class FrameOutputs(ct.Structure):
@@ -102,6 +103,7 @@ EXPORTS = {
     "nest_forward_render": (ct.c_int, [ct.POINTER(RasterSettings), ct.POINTER(HashGrid), ct.POINTER(Splats),
                                        ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_size_t,
                                        ct.c_int64, ct.POINTER(FrameOutputs), ct.POINTER(Timing), ct.c_void_p]),
+    "nest_mark_visible": (ct.c_int, [ct.c_int32, ct.c_void_p, ct.POINTER(ct.c_float), ct.c_void_p, ct.c_void_p]),
     "nest_timing_read": (ct.c_int, [ct.POINTER(Timing)]),
     "nest_timing_release": (ct.c_int, [ct.POINTER(Timing)]),
     "nest_scan_workspace_size": (ct.c_size_t, [ct.c_int64]),

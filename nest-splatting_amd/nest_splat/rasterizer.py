@@ -146,7 +146,11 @@ def _contig_f32(t: Optional[torch.Tensor], name: str) -> Optional[torch.Tensor]:
 def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: torch.Tensor, opacities: torch.Tensor,
                       scales: torch.Tensor, rotations: torch.Tensor, homotrans: Optional[torch.Tensor] = None,
                       ap_level: Optional[torch.Tensor] = None, colors_precomp: Optional[torch.Tensor] = None,
-                      channels: int = 3, timing: bool = False) -> ForwardResult:
+                      channels: int = 3, timing: bool = False, shs: Optional[torch.Tensor] = None,
+                      sh_degree: int = 0) -> ForwardResult:
+    """One forward frame.  The colour path (grid.levels == 0) takes colours
+    from colors_precomp, or, when it is None, evaluates them from shs
+    [P, M, 3] at degree sh_degree in preprocess (3 channels)."""
     if means3D.ndim != 2 or means3D.shape[1] != 3:
         raise ValueError("means3D must have dimensions (num_points, 3)")
     dev = means3D.device
@@ -159,6 +163,7 @@ def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: t
     homotrans = _contig_f32(homotrans, "homotrans")
     ap_level = _contig_f32(ap_level, "ap_level")
     colors_precomp = _contig_f32(colors_precomp, "colors_precomp")
+    shs = _contig_f32(shs, "shs") if shs is not None and shs.numel() > 0 else None
     if P > 0:
         for t, n, k in ((scales, "scales", 2), (rotations, "rotations", 4)):
             if t is None or t.numel() != P * k:
@@ -171,6 +176,8 @@ def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: t
             raise ValueError("ap_level must have P elements")
         if colors_precomp is not None and colors_precomp.numel() != P * channels:
             raise ValueError(f"colors_precomp must be [P, {channels}]")
+        if shs is not None and (shs.numel() % (P * 3) != 0 or shs.shape[0] != P):
+            raise ValueError("shs must be [P, M, 3]")
 
     sp = L.Splats()
     sp.struct_size = ct.sizeof(L.Splats)
@@ -182,6 +189,9 @@ def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: t
     sp.homotrans = L.ptr(homotrans)
     sp.ap_level = L.ptr(ap_level)
     sp.colors_precomp = L.ptr(colors_precomp)
+    sp.shs = L.ptr(shs)
+    sp.sh_degree = int(sh_degree)
+    sp.sh_coeffs = int(shs.numel() // (3 * P)) if shs is not None and P > 0 else 0
     g = grid.to_c()
 
     color = torch.empty((channels, H, W), dtype=torch.float32, device=dev)
@@ -228,7 +238,28 @@ def geometry_arrays(res: ForwardResult, P: int) -> Dict[str, torch.Tensor]:
                 records=L.view(res.geom, o[L.GEOM_RECORDS], torch.float32, (n, 32))[:P],
                 radii=L.view(res.geom, o[L.GEOM_RADII], torch.int32, (n,))[:P],
                 depth_order=L.view(res.geom, o[L.GEOM_DEPTH_ORDER], torch.int32, (n,))[:P],
-                order_offsets=L.view(res.geom, o[L.GEOM_ORDER_OFFSETS], torch.int32, (n,))[:P])
+                order_offsets=L.view(res.geom, o[L.GEOM_ORDER_OFFSETS], torch.int32, (n,))[:P],
+                rgb=L.view(res.geom, o[L.GEOM_RGB], torch.float32, (n, 3))[:P],
+                clamped=L.view(res.geom, o[L.GEOM_CLAMPED], torch.uint8, (n, 3))[:P])
+
+
+def mark_visible(means3D: torch.Tensor, viewmatrix) -> torch.Tensor:
+    """markVisible (DSR/rasterize_points.cu:452-470): bool [P], True where the
+    view-space depth of the point exceeds 0.2."""
+    if means3D.ndim != 2 or means3D.shape[1] != 3:
+        raise ValueError("means3D must have dimensions (num_points, 3)")
+    P = int(means3D.shape[0])
+    present = torch.zeros((P,), dtype=torch.bool, device=means3D.device)
+    if P == 0:
+        return present
+    means3D = _contig_f32(means3D, "means3D")
+    vm = host_array(viewmatrix, np.float32)
+    if vm.size != 16:
+        raise ValueError("viewmatrix must have 16 elements")
+    view = (ct.c_float * 16)(*[float(v) for v in vm])
+    L.check(L.lib().nest_mark_visible(P, L.ptr(means3D), view, L.ptr(present), L.stream_ptr(means3D.device)),
+            "nest_mark_visible")
+    return present
 
 
 def binning_arrays(res: ForwardResult, W: int, H: int) -> Dict[str, torch.Tensor]:

@@ -286,6 +286,78 @@ void or_preprocess(int P, const float *means, const float *scales, const float *
     }
 }
 
+/* computeColorFromSH (CR/forward.cu:21-72), called by preprocessCUDA after the
+ * tile-rectangle test (:417-424), i.e. for the splats that end with radii > 0.
+ * shs [P][M][3]; dir = (mean - campos) / |mean - campos|; the terms are
+ * summed in the order of the source, + 0.5, negative channels clamp to 0 and
+ * are flagged.  The normalisation constants are the real-SH ones:
+ * C0 = 1/(2 sqrt(pi)), C1 = sqrt(3/(4 pi)), C2 = sqrt(15/pi)/2 (xy, yz, xz
+ * terms, signs +,-,-), sqrt(5/pi)/4, sqrt(15/pi)/4; C3 = sqrt(35/(2 pi))/4,
+ * sqrt(105/pi)/2, sqrt(21/(2 pi))/4, sqrt(7/pi)/4, sqrt(105/pi)/4 with the
+ * signs of the source.  Splats with radii == 0 are left untouched. */
+void or_sh_colors(int P, int deg, int M, const float *means, const float *campos, const float *shs,
+                  const int32_t *radii, float *rgb, uint8_t *clamped)
+{
+    static const float C0 = 0.28209479177387814f, C1 = 0.4886025119029199f;
+    static const float C2[5] = {1.0925484305920792f, -1.0925484305920792f, 0.31539156525252005f,
+                                -1.0925484305920792f, 0.5462742152960396f};
+    static const float C3[7] = {-0.5900435899266435f, 2.890611442640554f, -0.4570457994644658f,
+                                0.3731763325901154f, -0.4570457994644658f, 1.445305721320277f,
+                                -0.5900435899266435f};
+    for (int i = 0; i < P; i++) {
+        if (radii[i] <= 0) continue;
+        float d[3];
+        for (int k = 0; k < 3; k++) d[k] = means[3 * i + k] - campos[k];
+        float len = sqrtf(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]);
+        for (int k = 0; k < 3; k++) d[k] = d[k] / len;
+        const float x = d[0], y = d[1], z = d[2];
+        const float *sh = shs + (size_t)i * M * 3;
+        for (int c = 0; c < 3; c++) {
+#define SH(k) sh[3 * (k) + c]
+            float r = C0 * SH(0);
+            if (deg > 0) {
+                r = r - C1 * y * SH(1);
+                r = r + C1 * z * SH(2);
+                r = r - C1 * x * SH(3);
+                if (deg > 1) {
+                    float xx = x * x, yy = y * y, zz = z * z;
+                    float xy = x * y, yz = y * z, xz = x * z;
+                    r = r + C2[0] * xy * SH(4);
+                    r = r + C2[1] * yz * SH(5);
+                    r = r + C2[2] * (2.0f * zz - xx - yy) * SH(6);
+                    r = r + C2[3] * xz * SH(7);
+                    r = r + C2[4] * (xx - yy) * SH(8);
+                    if (deg > 2) {
+                        r = r + C3[0] * y * (3.0f * xx - yy) * SH(9);
+                        r = r + C3[1] * xy * z * SH(10);
+                        r = r + C3[2] * y * (4.0f * zz - xx - yy) * SH(11);
+                        r = r + C3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy) * SH(12);
+                        r = r + C3[4] * x * (4.0f * zz - xx - yy) * SH(13);
+                        r = r + C3[5] * z * (xx - yy) * SH(14);
+                        r = r + C3[6] * x * (xx - 3.0f * yy) * SH(15);
+                    }
+                }
+            }
+#undef SH
+            r = r + 0.5f;
+            clamped[3 * i + c] = r < 0.0f ? 1 : 0;
+            rgb[3 * i + c] = r < 0.0f ? 0.0f : r;
+        }
+    }
+}
+
+/* markVisible / checkFrustum / in_frustum (CR/rasterizer_impl.cu:54-66,
+ * :198-210; CR/auxiliary.h:190-215): visible iff the view-space depth
+ * transformPoint4x3(p, view).z exceeds 0.2. */
+void or_mark_visible(int P, const float *means, const float *view, uint8_t *present)
+{
+    for (int i = 0; i < P; i++) {
+        const float px = means[3 * i], py = means[3 * i + 1], pz = means[3 * i + 2];
+        const float vz = view[2] * px + view[6] * py + view[10] * pz + view[14];
+        present[i] = vz <= 0.2f ? 0 : 1;
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* binning: CR/rasterizer_impl.cu:35-111, :173-195, :355-396            */
 /* ------------------------------------------------------------------ */

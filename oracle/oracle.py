@@ -79,6 +79,9 @@ def lib():
         L.or_sh16.argtypes = [f32p, f32p]
         L.or_rvq_decode.argtypes = [ct.c_int, ct.c_int, ct.c_int, ct.c_int, f32p, u16p, ct.c_void_p, f32p]
         L.or_activate.argtypes = [ct.c_int, f32p, f32p, f32p, f32p, f32p, f32p]
+        u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+        L.or_sh_colors.argtypes = [ct.c_int, ct.c_int, ct.c_int, f32p, f32p, f32p, i32p, f32p, u8p]
+        L.or_mark_visible.argtypes = [ct.c_int, f32p, f32p, u8p]
         L.or_max_threads.restype = ct.c_int
         _lib = L
     return _lib
@@ -113,6 +116,25 @@ def level_scale(S: float, H: int, l: int):
     res = ct.c_uint32()
     lib().or_level_scale(ct.c_float(S), H, l, ct.byref(sc), ct.byref(res))
     return sc.value, res.value
+
+
+def sh_colors(pre, means, campos, shs, deg):
+    """computeColorFromSH for the splats preprocess kept (radii > 0): returns
+    (rgb [P,3], clamped [P,3] uint8); other rows stay 0."""
+    P = means.shape[0]
+    shs = _c(shs, np.float32).reshape(P, -1, 3)
+    rgb = np.zeros((P, 3), np.float32)
+    clamped = np.zeros((P, 3), np.uint8)
+    lib().or_sh_colors(P, int(deg), shs.shape[1], _c(means, np.float32), _c(campos, np.float32).reshape(-1),
+                       shs, _c(pre["radii"], np.int32), rgb, clamped)
+    return rgb, clamped
+
+
+def mark_visible(means, view):
+    P = means.shape[0]
+    out = np.zeros(P, np.uint8)
+    lib().or_mark_visible(P, _c(means, np.float32), _c(view, np.float32).reshape(-1), out)
+    return out.astype(bool)
 
 
 def preprocess(means, scales, rots, opac, view, proj, W, H, scale_mod=1.0):

@@ -42,7 +42,7 @@ def test_struct_sizes_match_c_layout():
     L = _lib()
     assert ct.sizeof(L.RasterSettings) == 4 * (6 + 16 + 16 + 3 + 1 + 4)
     assert ct.sizeof(L.HashGrid) % 8 == 0
-    assert ct.sizeof(L.Splats) == 8 + 7 * 8
+    assert ct.sizeof(L.Splats) == 8 + 8 * 8 + 8
     assert ct.sizeof(L.FrameOutputs) == 8 + 3 * 8
     assert ct.sizeof(L.Mlp) == 16 + 3 * 8
 
@@ -107,6 +107,18 @@ def test_geometry_rejects_bad_arguments():
     s = _settings(L, prefiltered=1)
     rc = lib.nest_forward_geometry(ct.byref(s), ct.byref(sp), ws, 16, None, ct.byref(nr), ct.byref(tm), None)
     assert rc == L.NEST_ERR_UNSUPPORTED
+    # SH colours: degree 0..3 with enough coefficients per splat
+    s = _settings(L)
+    sp.shs, sp.sh_degree, sp.sh_coeffs = 1, 4, 25
+    rc = lib.nest_forward_geometry(ct.byref(s), ct.byref(sp), ws, 16, None, ct.byref(nr), ct.byref(tm), None)
+    assert rc == L.NEST_ERR_UNSUPPORTED and b"degree" in lib.nest_last_error()
+    sp.sh_degree, sp.sh_coeffs = 3, 9
+    rc = lib.nest_forward_geometry(ct.byref(s), ct.byref(sp), ws, 16, None, ct.byref(nr), ct.byref(tm), None)
+    assert rc == L.NEST_ERR_INVALID_ARGUMENT and b"coefficients" in lib.nest_last_error()
+    # with precomputed colours the SH arguments are not used
+    sp.colors_precomp = 1
+    rc = lib.nest_forward_geometry(ct.byref(s), ct.byref(sp), ws, 16, None, ct.byref(nr), ct.byref(tm), None)
+    assert rc == L.NEST_ERR_WORKSPACE
 
 
 def test_render_rejects_bad_grids():
@@ -157,6 +169,10 @@ def test_building_block_validation():
     assert lib.nest_sort_pairs_u64(None, None, None, None, 10, 70, None, 0, None) == L.NEST_ERR_INVALID_ARGUMENT
     assert lib.nest_sort_pairs_u64(None, None, None, None, 0, 45, None, 0, None) == L.NEST_OK
     assert lib.nest_inclusive_scan_u32(None, None, -1, None, 0, None) == L.NEST_ERR_INVALID_ARGUMENT
+    view = (ct.c_float * 16)()
+    assert lib.nest_mark_visible(-1, None, view, None, None) == L.NEST_ERR_INVALID_ARGUMENT
+    assert lib.nest_mark_visible(0, None, view, None, None) == L.NEST_OK
+    assert lib.nest_mark_visible(5, None, view, None, None) == L.NEST_ERR_INVALID_ARGUMENT
     offs = (ct.c_int32 * 17)(*[i * 64 for i in range(17)])
     assert lib.nest_grid_encode(None, 10, 6, None, 0, 0, offs, 16, 2, 0.5, 16, 0, 0, 0, None, None) == L.NEST_ERR_UNSUPPORTED
     assert lib.nest_grid_encode(None, 10, 3, None, 0, 0, offs, 16, 3, 0.5, 16, 0, 0, 0, None, None) == L.NEST_ERR_UNSUPPORTED

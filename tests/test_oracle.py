@@ -383,6 +383,85 @@ def test_sh16_against_scipy(oracle):
         np.testing.assert_allclose(oracle.sh16(u), ref, atol=2e-6)
 
 
+def _sh_basis_from_colours(oracle, dirs, deg):
+    """Y_k(dir) read out of or_sh_colors: coefficient k = 0.1 on every channel
+    (so r = 0.1 Y_k + 0.5 stays positive, no clamping), camera at the origin,
+    splat centres on the unit directions."""
+    P = dirs.shape[0]
+    K = (deg + 1) ** 2
+    pre = {"radii": np.ones(P, np.int32)}
+    out = np.zeros((K, P))
+    for k in range(K):
+        shs = np.zeros((P, 16, 3), np.float32)
+        shs[:, k, :] = 0.1
+        rgb, clamped = oracle.sh_colors(pre, dirs.astype(np.float32), np.zeros(3, np.float32), shs, deg)
+        assert not clamped.any()
+        assert np.array_equal(rgb[:, 0], rgb[:, 1]) and np.array_equal(rgb[:, 0], rgb[:, 2])
+        out[k] = (rgb[:, 0].astype(np.float64) - 0.5) / 0.1
+    return out
+
+
+def test_sh_colour_basis_against_scipy(oracle):
+    """computeColorFromSH's 16 basis functions are the real SH with the
+    Condon-Shortley phase, ordered l = 0..3, m = -l..l (the convention the
+    SH16 test pins against scipy): constants, signs and order together."""
+    from scipy.special import sph_harm_y
+    rng = np.random.default_rng(17)
+    d = rng.standard_normal((64, 3))
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    Y = _sh_basis_from_colours(oracle, d, 3)
+    theta, phi = np.arccos(d[:, 2]), np.arctan2(d[:, 1], d[:, 0])
+    k = 0
+    for l in range(4):
+        for m in range(-l, l + 1):
+            y = sph_harm_y(l, abs(m), theta, phi)
+            ref = np.sqrt(2) * y.imag if m < 0 else (y.real if m == 0 else np.sqrt(2) * y.real)
+            np.testing.assert_allclose(Y[k], ref, atol=2e-5, err_msg=f"l={l} m={m}")
+            k += 1
+
+
+def test_sh_colour_degree_clamp_and_culled(oracle):
+    rng = np.random.default_rng(3)
+    P = 40
+    means = rng.standard_normal((P, 3)).astype(np.float32) + np.float32(3.0)
+    campos = np.array([0.5, -0.25, 0.0], np.float32)
+    shs = rng.uniform(-1, 1, (P, 16, 3)).astype(np.float32)
+    radii = np.ones(P, np.int32)
+    radii[::7] = 0
+    pre = {"radii": radii}
+    # a degree ignores the coefficients above it
+    for deg in range(4):
+        K = (deg + 1) ** 2
+        masked = shs.copy()
+        masked[:, K:, :] = 1e6
+        a, ca = oracle.sh_colors(pre, means, campos, shs, deg)
+        b, cb = oracle.sh_colors(pre, means, campos, masked, deg)
+        np.testing.assert_array_equal(a, b)
+        np.testing.assert_array_equal(ca, cb)
+    # degree 0: max(C0 sh0 + 0.5, 0) exactly, flag where clamped
+    rgb, cl = oracle.sh_colors(pre, means, campos, shs * np.float32(4.0), 0)
+    r0 = np.float32(0.28209479177387814) * (shs[:, 0, :] * np.float32(4.0)) + np.float32(0.5)
+    keep = radii > 0
+    np.testing.assert_array_equal(rgb[keep], np.maximum(r0, 0)[keep])
+    np.testing.assert_array_equal(cl[keep].astype(bool), (r0 < 0)[keep])
+    assert cl[keep].any() and (~cl[keep].astype(bool)).any()
+    # culled splats are not evaluated
+    assert not rgb[~keep].any() and not cl[~keep].any()
+
+
+def test_mark_visible_near_plane(oracle):
+    """in_frustum keeps a point iff its view-space z exceeds 0.2."""
+    rng = np.random.default_rng(4)
+    means = rng.uniform(-2, 2, (500, 3)).astype(np.float32)
+    means[:10, 2] = np.float32(0.2)
+    view = np.eye(4, dtype=np.float32)
+    view[3, :3] = [0.1, -0.3, 0.0]  # row-vector translation (flat index 12..14)
+    vis = oracle.mark_visible(means, view)
+    z = means[:, 2] * np.float32(1.0) + np.float32(0.0)
+    np.testing.assert_array_equal(vis, z > np.float32(0.2))
+    assert not vis[:10].any()
+
+
 def test_mlp_closed_forms(oracle):
     rng = np.random.default_rng(9)
     C, N, npix = 16, 32, 200
