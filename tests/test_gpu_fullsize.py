@@ -1,0 +1,183 @@
+"""Parity at the benchmark sizes: the 1M-splat 1600x1064 unbounded scene and
+the 4M-splat 1920x1080 fp16-table scene (two of its eight cameras).
+
+The GPU renders the whole frame.  The oracle computes preprocess for every
+splat and the render of every k-th tile row; the GPU must match it bit for
+bit there (radii, pair lists, tile ranges, feature map, allmap, final T,
+contributor counts), and the MLP decode within its tolerance.  For the 1M
+scene the whole sorted pair list is compared; for the 4M scene (hundreds of
+millions of pairs) the oracle's pairs are filtered to the sampled tile rows
+and stable-sorted there, which is the same order the full stable sort gives
+those tiles.  Whole-frame invariants cover the rows the oracle skips."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _log(*a):
+    print("[fullsize]", *a, flush=True)
+
+
+def _gpu_frame(sc, cam_index):
+    from nest_splat import rasterizer as rz
+    from nest_splat.camera import view_ray_matrix
+    from nest_splat.mlp import NestMLP
+    sp = sc.spec
+    cam = sc.cameras[cam_index]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy, cam.world_view_transform,
+                                cam.full_proj_transform, cam.camera_center, if_contract=sp.contract)
+    grid = rz.HashGridDesc(sp.L, sp.F, sp.S, sp.base_res, t(sc.table), sc.offsets,
+                           np.asarray(sp.gridrange, np.float32))
+    res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
+                               homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), channels=sp.C)
+    mlp = NestMLP(sp.C, sp.mlp_width, sp.mlp_dtype, sc.W1, sc.W2, sc.W3).to(DEV)
+    bg = torch.tensor(sp.bg, dtype=torch.float32) if sum(sp.bg) > 0 else None
+    rgb = mlp.decode_image(res.color, view_ray_matrix(cam), alpha=res.others[1], bg=bg)
+    torch.cuda.synchronize()
+    return res, rgb
+
+
+def _sampled_rows(H, stride, phase):
+    gy = (H + 15) // 16
+    return [ty for ty in range(gy) if ty % stride == phase]
+
+
+def _partial_binning(oracle, pre, W, H, rows):
+    """Pairs of the tiles in `rows`, in the order the reference's stable sort
+    gives them, with their ranges (other tiles empty)."""
+    from oracle.oracle import lib as olib
+    gx, gy = (W + 15) // 16, (H + 15) // 16
+    P = pre["radii"].shape[0]
+    offs = np.zeros(P, np.uint32)
+    olib().or_inclusive_scan_u32(P, np.ascontiguousarray(pre["tiles"], np.uint32), offs)
+    NR = int(offs[-1])
+    keys = np.zeros(max(NR, 1), np.uint64)
+    vals = np.zeros(max(NR, 1), np.uint32)
+    olib().or_duplicate_keys(P, pre["xy"], pre["depth"], pre["radii"], offs, gx, gy, keys, vals)
+    keys, vals = keys[:NR], vals[:NR]
+    tile = (keys >> np.uint64(32)).astype(np.int64)
+    sel = np.isin(tile // gx, rows)
+    k, v = keys[sel], vals[sel]
+    order = np.argsort(k, kind="stable")
+    k, v = k[order], v[order]
+    ranges = np.zeros((gx * gy, 2), np.uint32)
+    t = (k >> np.uint64(32)).astype(np.int64)
+    if t.size:
+        starts = np.flatnonzero(np.r_[True, t[1:] != t[:-1]])
+        ends = np.r_[starts[1:], t.size]
+        ranges[t[starts], 0] = starts
+        ranges[t[starts], 1] = ends
+    return dict(num_rendered=NR, keys=k, vals=v, ranges=ranges)
+
+
+def _check_rows(sc, cam_index, res, rgb, r, rows, oracle):
+    sp = sc.spec
+    cam = sc.cameras[cam_index]
+    W, H = cam.image_width, cam.image_height
+    pix = np.zeros((H, W), bool)
+    for ty in rows:
+        pix[ty * 16:(ty + 1) * 16] = True
+    col = res.color.cpu().numpy()
+    oth = res.others.cpu().numpy()
+    from nest_splat import rasterizer as rz
+    ba = rz.binning_arrays(res, W, H)
+    ft = ba["final_T"].cpu().numpy()
+    nc = ba["n_contrib"].cpu().numpy().view(np.uint32)
+    np.testing.assert_array_equal(col[:, pix], r["color"][:, pix])
+    np.testing.assert_array_equal(oth[:, pix], r["others"][:, pix])
+    np.testing.assert_array_equal(ft[:, pix], r["final_T"][:, pix])
+    np.testing.assert_array_equal(nc[:, pix], r["n_contrib"][:, pix])
+    # MLP on the sampled pixels, tolerance of the bf16/fp16 MFMA path
+    idx = np.flatnonzero(pix.reshape(-1))
+    dirs = oracle.ray_dirs(cam)[idx]
+    ref = oracle.mlp(np.ascontiguousarray(r["color"].reshape(sp.C, -1)[:, idx]), dirs,
+                     r["others"][1].reshape(-1)[idx], sc.W1, sc.W2, sc.W3, sp.mlp_dtype,
+                     np.asarray(sp.bg, np.float32), threads=0)
+    np.testing.assert_allclose(rgb.cpu().numpy().reshape(3, -1)[:, idx], ref, atol=2e-3, rtol=0)
+    # whole-frame invariants
+    T = oth[1]
+    assert np.all((T >= 0) & (T <= 1))
+    np.testing.assert_array_equal(oth[1], 1 - ft[0])
+    assert np.all(oth[7] >= 0) and np.all(oth[7] == np.floor(oth[7]))
+    assert np.all(np.isfinite(col))
+    return int(pix.sum())
+
+
+@pytest.mark.timeout(600)
+def test_benchmark_scene_1m(oracle):
+    from nest_splat.scene import get_spec, make_scene
+    from nest_splat import rasterizer as rz
+    sc = make_scene(get_spec("cfg3"))
+    sp = sc.spec
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    _log("cfg3 GPU frame")
+    res, rgb = _gpu_frame(sc, 0)
+    _log("cfg3 oracle preprocess + binning")
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    np.testing.assert_array_equal(res.radii.cpu().numpy(), pre["radii"])
+    assert res.num_rendered == b["num_rendered"]
+    ba = rz.binning_arrays(res, W, H)
+    np.testing.assert_array_equal(ba["keys"].cpu().numpy().view(np.uint64), b["keys"])
+    np.testing.assert_array_equal(ba["vals"].cpu().numpy().view(np.uint32), b["vals"])
+    np.testing.assert_array_equal(ba["ranges"].cpu().numpy().view(np.uint32), b["ranges"])
+    stride, phase = 8, 3
+    _log("cfg3 oracle render, every", stride, "th tile row")
+    grid = oracle.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    r = oracle.render(pre, b, W, H, sp.C, grid, homotrans=sc.homotrans, ap_level=sc.ap_level, row_stride=stride,
+                      row_phase=phase)
+    n = _check_rows(sc, 0, res, rgb, r, _sampled_rows(H, stride, phase), oracle)
+    _log("cfg3 ok,", n, "pixels compared bit for bit")
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("cam_index", [0, 3])
+def test_stress_scene_4m(oracle, cam_index):
+    from nest_splat.scene import get_spec, make_scene
+    from nest_splat import rasterizer as rz
+    global _cfg5
+    try:
+        sc = _cfg5
+    except NameError:
+        _log("cfg5 scene (4M splats)")
+        sc = _cfg5 = make_scene(get_spec("cfg5"))
+    sp = sc.spec
+    cam = sc.cameras[cam_index]
+    W, H = cam.image_width, cam.image_height
+    _log(f"cfg5 cam {cam_index} GPU frame")
+    res, rgb = _gpu_frame(sc, cam_index)
+    _log(f"cfg5 cam {cam_index} oracle preprocess")
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    np.testing.assert_array_equal(res.radii.cpu().numpy(), pre["radii"])
+    stride, phase = 16, 7 if cam_index == 0 else 2
+    rows = _sampled_rows(H, stride, phase)
+    _log(f"cfg5 cam {cam_index} oracle pairs of tile rows {rows}")
+    b = _partial_binning(oracle, pre, W, H, rows)
+    assert res.num_rendered == b["num_rendered"]
+    ba = rz.binning_arrays(res, W, H)
+    granges = ba["ranges"].cpu().numpy().view(np.uint32)
+    gvals = ba["vals"].cpu().numpy().view(np.uint32)
+    gx = (W + 15) // 16
+    for ty in rows:
+        for tx in range(gx):
+            ti = ty * gx + tx
+            lo, hi = b["ranges"][ti]
+            glo, ghi = granges[ti]
+            assert ghi - glo == hi - lo, (ti, ghi - glo, hi - lo)
+            np.testing.assert_array_equal(gvals[glo:ghi], b["vals"][lo:hi])
+    # the whole sorted key array is ordered by (tile, depth bits)
+    keys = ba["keys"].cpu().numpy().view(np.uint64)
+    assert np.all(keys[1:] >= keys[:-1])
+    _log(f"cfg5 cam {cam_index} oracle render of {len(rows)} tile rows")
+    grid = oracle.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    r = oracle.render(pre, b, W, H, sp.C, grid, homotrans=sc.homotrans, ap_level=sc.ap_level, row_stride=stride,
+                      row_phase=phase)
+    n = _check_rows(sc, cam_index, res, rgb, r, rows, oracle)
+    _log(f"cfg5 cam {cam_index} ok, {n} pixels compared bit for bit")
