@@ -279,13 +279,17 @@ struct LevelCorners {
   float wx[2], wy[2], wz[2];
 };
 
-template <int F, bool kHalf>
+// kStructured: the caller has checked that levels [0, n_dense) are dense with
+// no modulo and the rest hashed with a power-of-two size (the usual grid:
+// coarse levels fit their table, fine ones are hashed); the index path is then
+// chosen by one compare instead of the flag tests.
+template <int F, bool kHalf, bool kStructured = false>
 __device__ __forceinline__ void level_corners(const LevelTable& lv, int l, float pos_offset, uint32_t interp,
-                                              const float u[3], LevelCorners& cn) {
+                                              const float u[3], LevelCorners& cn, uint32_t n_dense = 0) {
   const float scale = lv.scale[l];
   const uint32_t res1 = lv.res1[l];
   const uint32_t hsize = lv.hsize[l];
-  const uint32_t flags = lv.flags[l];
+  const uint32_t flags = kStructured ? ((uint32_t)l < n_dense ? kLvNoMod : (kLvHashed | kLvPow2)) : lv.flags[l];
   cn.soff = lv.base[l] * (uint32_t)(F * (kHalf ? 2 : 4));
   float pos[3];
   uint32_t g[3];
@@ -345,11 +349,12 @@ __device__ __forceinline__ void corners_sum(const LevelCorners& cn, const float 
   }
 }
 
-template <int F, bool kHalf>
+template <int F, bool kHalf, bool kStructured = false>
 __device__ __forceinline__ void level_interp_struct(nest_i32x4 rsrc, const LevelTable& lv, int l,
-                                                    float pos_offset, uint32_t interp, const float u[3], float out[F]) {
+                                                    float pos_offset, uint32_t interp, const float u[3], float out[F],
+                                                    uint32_t n_dense = 0) {
   LevelCorners cn;
-  level_corners<F, kHalf>(lv, l, pos_offset, interp, u, cn);
+  level_corners<F, kHalf, kStructured>(lv, l, pos_offset, interp, u, cn, n_dense);
   float vals[8][F];  // all eight loads in flight before the first use
   corners_load<F, kHalf>(rsrc, cn, vals);
   corners_sum<F>(cn, vals, out);

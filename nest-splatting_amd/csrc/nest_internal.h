@@ -77,6 +77,8 @@ struct GridParams {
   uint32_t half;        // table entries are binary16
   uint32_t table_bytes; // byte size of the table (< 4 GiB: 32-bit buffer offsets)
   uint32_t table_rows;  // entries of the table (records of the struct-buffer view)
+  uint32_t structured;  // levels [0, n_dense) dense without modulo, the rest hashed power-of-two
+  uint32_t n_dense;
   const void* table;
   LevelTable lv;
 };

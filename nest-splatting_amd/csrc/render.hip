@@ -60,7 +60,7 @@ __device__ __forceinline__ uint64_t lanemask_lt64() {
 // One drain round (any F): every lane with a pending hit looks up its oldest
 // one (ring-buffer head) and accumulates each level below its level count;
 // lanes with an empty queue idle.
-template <int F, int NACC, bool kHalf>
+template <int F, int NACC, bool kHalf, bool kStructured>
 __device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc, float4 (*hq)[kRenderThreads],
                                             uint8_t (*hl)[kRenderThreads], int& qhead, int& qn, float* acc) {
   if (qn > 0) {
@@ -71,7 +71,7 @@ __device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc
     for (int l = 0; l < NACC / F; l++) {
       if ((uint32_t)l < maxl) {
         float v[F];
-        level_interp_struct<F, kHalf>(rsrc, g.lv, l, g.pos_offset, g.interp, u, v);
+        level_interp_struct<F, kHalf, kStructured>(rsrc, g.lv, l, g.pos_offset, g.interp, u, v, g.n_dense);
 #pragma unroll
         for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(v[f], e.w, acc[l * F + f]);
       }
@@ -90,7 +90,7 @@ __device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc
 // fmaf(0, w, acc) == acc (w is finite and the accumulators never hold -0), as
 // in the round drain.  isrc is this wave's 64-byte item table: owner lane |
 // slot << 6.
-template <int F, int NACC, bool kHalf>
+template <int F, int NACC, bool kHalf, bool kStructured>
 __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rsrc, float4 (*hq)[kRenderThreads],
                                               uint8_t (*hl)[kRenderThreads], uint8_t* isrc, int& qhead, int& qn,
                                               float* acc) {
@@ -133,7 +133,8 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
   for (int l = 0; l < NACC / F; l++) {
     if (work) {
       float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if ((uint32_t)l < nlev) level_interp_struct<F, kHalf>(rsrc, g.lv, l, g.pos_offset, g.interp, u, v);
+      if ((uint32_t)l < nlev)
+        level_interp_struct<F, kHalf, kStructured>(rsrc, g.lv, l, g.pos_offset, g.interp, u, v, g.n_dense);
       hq[wslot][col] = make_float4(v[0], v[1], v[2], v[3]);
     }
     __builtin_amdgcn_wave_barrier();
@@ -248,7 +249,7 @@ __device__ __forceinline__ uint8_t hit_levels(bool oob, uint32_t ap, uint32_t L)
 // LDS (32 KB of staged records + 17 KB of queue) allows three workgroups per
 // CU; amdgpu_waves_per_eu(3) gives the matching 168-VGPR budget, which holds
 // 64 accumulators and eight in-flight 16-byte corner loads.
-template <int F, int NACC, bool kHash, bool kHalf>
+template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false>
 __global__ void __launch_bounds__(kRenderThreads) __attribute__((amdgpu_waves_per_eu(3, 8)))
 render_kernel(const RenderParams p) {
   __shared__ float4 srec[kRecChunks][kBatch];
@@ -389,9 +390,9 @@ render_kernel(const RenderParams p) {
       // whenever a lane is full; at the end, until every queue is empty
       if (__ballot(qn == kQueue) || (last && __ballot(qn > 0))) {
         if constexpr (F <= 4)
-          drain_compact<F, NACC, kHalf>(g, rsrc, hq, hl, isrc + wid * kWaveLanes, qhead, qn, acc);
+          drain_compact<F, NACC, kHalf, kStructured>(g, rsrc, hq, hl, isrc + wid * kWaveLanes, qhead, qn, acc);
         else
-          drain_round<F, NACC, kHalf>(g, rsrc, hq, hl, qhead, qn, acc);
+          drain_round<F, NACC, kHalf, kStructured>(g, rsrc, hq, hl, qhead, qn, acc);
         if (last) continue;
       }
     }
@@ -430,22 +431,28 @@ render_kernel(const RenderParams p) {
   O[pid + 13 * HW] = 0.0f;  // the third appearance channel only ever adds 0 * w
 }
 
-template <int F, int NACC, bool kHash, bool kHalf>
+template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false>
 static hipError_t launch_one(const RenderParams& p, hipStream_t s) {
-  hipLaunchKernelGGL((render_kernel<F, NACC, kHash, kHalf>), dim3(p.ntiles), dim3(kRenderThreads), 0, s, p);
+  hipLaunchKernelGGL((render_kernel<F, NACC, kHash, kHalf, kStructured>), dim3(p.ntiles), dim3(kRenderThreads), 0, s,
+                     p);
   return hipGetLastError();
 }
 
-template <int F, bool kHalf>
+template <int F, bool kHalf, bool kStructured>
 static hipError_t launch_hash_levels(const RenderParams& p, hipStream_t s) {
   const uint32_t L = p.grid.L;
   if constexpr (F * 8 <= NEST_MAX_CHANNELS)
-    if (L <= 8) return launch_one<F, F * 8, true, kHalf>(p, s);
+    if (L <= 8) return launch_one<F, F * 8, true, kHalf, kStructured>(p, s);
   if constexpr (F * 16 <= NEST_MAX_CHANNELS)
-    if (L <= 16) return launch_one<F, F * 16, true, kHalf>(p, s);
+    if (L <= 16) return launch_one<F, F * 16, true, kHalf, kStructured>(p, s);
   if constexpr (F * 32 <= NEST_MAX_CHANNELS)
-    if (L <= 32) return launch_one<F, F * 32, true, kHalf>(p, s);
+    if (L <= 32) return launch_one<F, F * 32, true, kHalf, kStructured>(p, s);
   return hipErrorInvalidValue;
+}
+
+template <int F, bool kHalf>
+static hipError_t launch_hash(const RenderParams& p, hipStream_t s) {
+  return p.grid.structured ? launch_hash_levels<F, kHalf, true>(p, s) : launch_hash_levels<F, kHalf, false>(p, s);
 }
 
 hipError_t launch_render(const RenderParams& p, hipStream_t s) {
@@ -459,10 +466,10 @@ hipError_t launch_render(const RenderParams& p, hipStream_t s) {
   }
   const bool half = p.grid.half != 0;
   switch (p.grid.F) {
-    case 1: return half ? launch_hash_levels<1, true>(p, s) : launch_hash_levels<1, false>(p, s);
-    case 2: return half ? launch_hash_levels<2, true>(p, s) : launch_hash_levels<2, false>(p, s);
-    case 4: return half ? launch_hash_levels<4, true>(p, s) : launch_hash_levels<4, false>(p, s);
-    case 8: return half ? launch_hash_levels<8, true>(p, s) : launch_hash_levels<8, false>(p, s);
+    case 1: return half ? launch_hash<1, true>(p, s) : launch_hash<1, false>(p, s);
+    case 2: return half ? launch_hash<2, true>(p, s) : launch_hash<2, false>(p, s);
+    case 4: return half ? launch_hash<4, true>(p, s) : launch_hash<4, false>(p, s);
+    case 8: return half ? launch_hash<8, true>(p, s) : launch_hash<8, false>(p, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -127,6 +127,31 @@ def test_second_camera_parity(oracle):
     np.testing.assert_array_equal(res.color.cpu().numpy(), r["color"])
 
 
+@pytest.mark.parametrize("sizes,name", [("non_pow2", "unbounded_small"), ("mixed", "shells_small")])
+def test_irregular_level_sizes_parity(oracle, sizes, name):
+    """Level sizes that are not all powers of two (hashed levels reduced by a
+    modulo, a hashed level between dense ones): the render takes the general
+    per-level index path instead of the dense-prefix/power-of-two one."""
+    import dataclasses
+    sc = scene(name)  # f32 and f16 tables
+    L, T = sc.spec.L, 1 << sc.spec.log2T
+    if sizes == "non_pow2":
+        hs = np.full(L, T - 40, np.int64)
+    else:  # power-of-two and other sizes alternating; level 1 hashed into 64 entries
+        hs = np.where(np.arange(L) % 2 == 0, T, T - 8 * 37).astype(np.int64)
+        hs[1] = 64
+    offsets = np.concatenate([[0], np.cumsum(hs)]).astype(np.int32)
+    rng = np.random.default_rng(7)
+    table = (rng.standard_normal((int(offsets[-1]), sc.spec.F)) * 0.5).astype(sc.table.dtype)
+    sc2 = dataclasses.replace(sc, offsets=offsets, table=table)
+    print(f"[case] irregular level sizes {sizes} {name} {table.dtype} P={sc.spec.P}", flush=True)
+    res = run_gpu(sc2)
+    _, b, r = run_oracle(oracle, sc2)
+    assert res.num_rendered == b["num_rendered"]
+    np.testing.assert_array_equal(res.others.cpu().numpy(), r["others"])
+    np.testing.assert_array_equal(res.color.cpu().numpy(), r["color"])
+
+
 def test_deterministic_repeat():
     sc = scene("unbounded_small")
     a = run_gpu(sc)
