@@ -385,10 +385,11 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     g.table_bytes = (uint32_t)tbytes;
     g.table_rows = (uint32_t)gr->table_rows;
     // structured grid: a prefix of dense levels without modulo, then hashed
-    // levels with power-of-two sizes (flag bits: 1 hashed, 2 pow2, 4 nomod)
+    // levels with power-of-two sizes (flag bits: 1 hashed, 2 pow2, 4 nomod),
+    // trilinear interpolation
     uint32_t nd = 0;
     while (nd < g.L && (g.lv.flags[nd] & 5u) == 4u) nd++;
-    bool structured = true;
+    bool structured = g.interp == 0;
     for (uint32_t l = nd; l < g.L; l++) structured = structured && (g.lv.flags[l] & 3u) == 3u;
     g.structured = structured ? 1u : 0u;
     g.n_dense = nd;

@@ -50,7 +50,7 @@ __global__ void __launch_bounds__(256) grid_encode_kernel(const GridEncodeParams
 #pragma unroll
     for (int d = 0; d < D; d++) {
       pos[d] = u[d] * scale + off;
-      g[d] = f2u_sat(floorf(pos[d]));
+      g[d] = f2u_sat(pos[d]);  // == f2u_sat(floorf(pos[d]))
       pos[d] = pos[d] - (float)g[d];
       if (p.interp == 1) pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
     }

@@ -19,21 +19,6 @@ constexpr uint32_t kLvHashed = 1u;   // (res1)^3 > hashmap size in the uint32 lo
 constexpr uint32_t kLvPow2 = 2u;     // hashmap size is a power of two
 constexpr uint32_t kLvNoMod = 4u;    // dense and the linear index cannot reach the size
 
-__device__ __forceinline__ uint32_t level_index(uint32_t flags, uint32_t res1, uint32_t hsize, uint32_t q0, uint32_t q1,
-                                                uint32_t q2) {
-  uint32_t idx;
-  if (flags & kLvHashed) {
-    idx = (q0 * 1u) ^ (q1 * 2654435761u) ^ (q2 * 805459861u);
-  } else {
-    idx = q0;
-    idx += q1 * res1;
-    idx += q2 * (res1 * res1);
-  }
-  if (flags & kLvNoMod) return idx;
-  if (flags & kLvPow2) return idx & (hsize - 1u);
-  return idx % hsize;
-}
-
 // F consecutive table values of entry e, widened to float.
 template <int F, bool kHalf>
 __device__ __forceinline__ void load_entry(const void* table, size_t e, float v[F]) {
@@ -69,122 +54,6 @@ __device__ __forceinline__ void load_entry(const void* table, size_t e, float v[
 #pragma unroll
       for (int f = 0; f < F; f++) v[f] = __half2float(t[e * F + f]);
     }
-  }
-}
-
-// Buffer resource over the whole table (num_records = its byte size, so an
-// out-of-range offset would read zero instead of faulting).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t table_rsrc(const void* table, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(table), (short)0, (int)bytes, 0x00020000);
-}
-
-// F values of entry e (entry-relative byte offset voff) of the level whose
-// first entry starts at byte soff, widened to float.  32-bit offsets, the
-// level base in a scalar register.
-template <int F, bool kHalf>
-__device__ __forceinline__ void buffer_entry(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float v[F]) {
-  if constexpr (!kHalf) {
-    if constexpr (F == 4) {
-      const float4 a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    } else if constexpr (F == 2) {
-      const float2 a = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
-      v[0] = a.x; v[1] = a.y;
-    } else if constexpr (F == 1) {
-      v[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
-    } else {
-#pragma unroll
-      for (int q = 0; q < F / 4; q++) {
-        const float4 a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16u * q, soff, 0));
-        v[4 * q + 0] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w;
-      }
-    }
-  } else {
-    if constexpr (F == 4) {
-      const uint2 a = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
-      v[0] = __half2float(__ushort_as_half((unsigned short)(a.x & 0xffffu)));
-      v[1] = __half2float(__ushort_as_half((unsigned short)(a.x >> 16)));
-      v[2] = __half2float(__ushort_as_half((unsigned short)(a.y & 0xffffu)));
-      v[3] = __half2float(__ushort_as_half((unsigned short)(a.y >> 16)));
-    } else if constexpr (F == 2) {
-      const uint32_t a = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
-      v[0] = __half2float(__ushort_as_half((unsigned short)(a & 0xffffu)));
-      v[1] = __half2float(__ushort_as_half((unsigned short)(a >> 16)));
-    } else if constexpr (F == 8) {
-      const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-      const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        v[2 * q] = __half2float(__ushort_as_half((unsigned short)(w[q] & 0xffffu)));
-        v[2 * q + 1] = __half2float(__ushort_as_half((unsigned short)(w[q] >> 16)));
-      }
-    } else {
-      const uint32_t a = __builtin_amdgcn_raw_buffer_load_b32(r, voff & ~3u, soff, 0);
-      v[0] = __half2float(__ushort_as_half((unsigned short)((voff & 2u) ? (a >> 16) : (a & 0xffffu))));
-    }
-  }
-}
-
-// Trilinear (interp 0) or smoothstep (interp 1) interpolation of level l at
-// u in [0,1]^3 through a buffer resource.  Same corner order, weights and
-// index as level_interp; the corner indices are strength-reduced: with
-// q = g + b (b in {0,1}^3) the hash is (g0+b0) ^ (g1*P1 + b1*P1) ^
-// (g2*P2 + b2*P2) and the dense index (g0 + g1 r + g2 r^2) + (b0 + b1 r +
-// b2 r^2), both exact in uint32 arithmetic, so each level needs two integer
-// multiplies instead of two per corner.  out[f] accumulates fmaf(w, v, out[f])
-// in corner order from +0.
-template <int F, bool kHalf>
-__device__ __forceinline__ void level_interp_rsrc(__amdgpu_buffer_rsrc_t rsrc, const LevelTable& lv, int l,
-                                                  float pos_offset, uint32_t interp, const float u[3], float out[F]) {
-  const float scale = lv.scale[l];
-  const uint32_t res1 = lv.res1[l];
-  const uint32_t hsize = lv.hsize[l];
-  const uint32_t flags = lv.flags[l];
-  const uint32_t soff = lv.base[l] * (uint32_t)(F * (kHalf ? 2 : 4));
-  constexpr uint32_t kShift = (F * (kHalf ? 2 : 4)) == 32 ? 5 : (F * (kHalf ? 2 : 4)) == 16 ? 4
-                            : (F * (kHalf ? 2 : 4)) == 8 ? 3 : (F * (kHalf ? 2 : 4)) == 4 ? 2 : 1;
-  float pos[3];
-  uint32_t g[3];
-#pragma unroll
-  for (int d = 0; d < 3; d++) {
-    pos[d] = u[d] * scale + pos_offset;
-    g[d] = f2u_sat(floorf(pos[d]));
-    pos[d] = pos[d] - (float)g[d];
-    if (interp == 1) pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
-  }
-  const float wx[2] = {1 - pos[0], pos[0]}, wy[2] = {1 - pos[1], pos[1]}, wz[2] = {1 - pos[2], pos[2]};
-  uint32_t idx[8];
-  if (flags & kLvHashed) {
-    const uint32_t a[2] = {g[0], g[0] + 1u};
-    const uint32_t b0 = g[1] * 2654435761u, c0 = g[2] * 805459861u;
-    const uint32_t b[2] = {b0, b0 + 2654435761u}, c[2] = {c0, c0 + 805459861u};
-#pragma unroll
-    for (int k = 0; k < 8; k++) idx[k] = a[k & 1] ^ b[(k >> 1) & 1] ^ c[k >> 2];
-  } else {
-    const uint32_t r2 = res1 * res1;
-    const uint32_t base = g[0] + g[1] * res1 + g[2] * r2;
-#pragma unroll
-    for (int k = 0; k < 8; k++) idx[k] = base + ((k & 1) ? 1u : 0u) + ((k & 2) ? res1 : 0u) + ((k & 4) ? r2 : 0u);
-  }
-  if (!(flags & kLvNoMod)) {
-    if (flags & kLvPow2) {
-#pragma unroll
-      for (int k = 0; k < 8; k++) idx[k] &= hsize - 1u;
-    } else {
-#pragma unroll
-      for (int k = 0; k < 8; k++) idx[k] %= hsize;
-    }
-  }
-  float vals[8][F];
-#pragma unroll
-  for (int k = 0; k < 8; k++) buffer_entry<F, kHalf>(rsrc, idx[k] << kShift, soff, vals[k]);
-#pragma unroll
-  for (int f = 0; f < F; f++) out[f] = 0.0f;
-#pragma unroll
-  for (int k = 0; k < 8; k++) {
-    const float w = (1.0f * wx[k & 1]) * wy[(k >> 1) & 1] * wz[k >> 2];
-#pragma unroll
-    for (int f = 0; f < F; f++) out[f] = fmaf(w, vals[k][f], out[f]);
   }
 }
 
@@ -267,12 +136,14 @@ __device__ __forceinline__ void struct_entry(nest_i32x4 r, uint32_t index, uint3
   }
 }
 
-// Level l of the hash grid at u in [0,1]^3 through a struct-buffer view:
-// same corner order, weights, index and fused accumulation as
-// level_interp_rsrc.  The cell fraction pos - floor(pos) is computed with
-// v_fract (exact for the non-negative pos here, equal to the reference's
-// pos - (float)(uint)floor(pos) below 2^24), and the entry index goes to the
-// buffer unit unscaled.
+// Level l of the hash grid at u in [0,1]^3 through a struct-buffer view, with
+// the reference's corner order (bit 0 +x, bit 1 +y, bit 2 +z), weights
+// w = ((1 * wx) * wy) * wz and fused accumulation out = fmaf(w, v, out) from
+// +0.  The corner indices are strength-reduced: with q = g + b (b in {0,1}^3)
+// the hash is (g0+b0) ^ (g1*P1 + b1*P1) ^ (g2*P2 + b2*P2) and the dense index
+// (g0 + g1 r + g2 r^2) + (b0 + b1 r + b2 r^2), both exact in uint32
+// arithmetic, so a level needs two integer multiplies instead of two per
+// corner.  The entry index goes to the buffer unit unscaled.
 struct LevelCorners {
   uint32_t idx[8];   // entry index of corner k (bit 0: +x, bit 1: +y, bit 2: +z)
   uint32_t soff;     // byte offset of the level in the table
@@ -280,9 +151,10 @@ struct LevelCorners {
 };
 
 // kStructured: the caller has checked that levels [0, n_dense) are dense with
-// no modulo and the rest hashed with a power-of-two size (the usual grid:
-// coarse levels fit their table, fine ones are hashed); the index path is then
-// chosen by one compare instead of the flag tests.
+// no modulo, the rest hashed with a power-of-two size (the usual grid: coarse
+// levels fit their table, fine ones are hashed) and that the interpolation is
+// trilinear; the index path is then chosen by one compare instead of the flag
+// tests.
 template <int F, bool kHalf, bool kStructured = false>
 __device__ __forceinline__ void level_corners(const LevelTable& lv, int l, float pos_offset, uint32_t interp,
                                               const float u[3], LevelCorners& cn, uint32_t n_dense = 0) {
@@ -295,10 +167,11 @@ __device__ __forceinline__ void level_corners(const LevelTable& lv, int l, float
   uint32_t g[3];
 #pragma unroll
   for (int d = 0; d < 3; d++) {
+    // g = (uint32)floor(x) with the saturating conversion, pos = x - (float)g
     const float x = u[d] * scale + pos_offset;
-    g[d] = f2u_sat(floorf(x));
-    pos[d] = (x >= 0.0f && x < 16777216.0f) ? __builtin_amdgcn_fractf(x) : x - (float)g[d];
-    if (interp == 1) pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
+    g[d] = f2u_sat(x);
+    pos[d] = x - (float)g[d];
+    if (!kStructured && interp == 1) pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
   }
   cn.wx[0] = 1 - pos[0]; cn.wx[1] = pos[0];
   cn.wy[0] = 1 - pos[1]; cn.wy[1] = pos[1];
@@ -358,51 +231,6 @@ __device__ __forceinline__ void level_interp_struct(nest_i32x4 rsrc, const Level
   float vals[8][F];  // all eight loads in flight before the first use
   corners_load<F, kHalf>(rsrc, cn, vals);
   corners_sum<F>(cn, vals, out);
-}
-
-// Trilinear (interp 0) or smoothstep (interp 1) interpolation of level l at
-// u in [0,1]^3.  out[f] = sum over corners 0..7 of w_corner * table, summed
-// in corner order from +0 with fused multiply-adds.
-template <int F, bool kHalf>
-__device__ __forceinline__ void level_interp(const LevelTable& lv, int l, const void* table, float pos_offset,
-                                             uint32_t interp, const float u[3], float out[F]) {
-  const float scale = lv.scale[l];
-  const uint32_t res1 = lv.res1[l];
-  const uint32_t hsize = lv.hsize[l];
-  const uint32_t flags = lv.flags[l];
-  const size_t base = lv.base[l];
-  float pos[3];
-  uint32_t g[3];
-#pragma unroll
-  for (int d = 0; d < 3; d++) {
-    pos[d] = u[d] * scale + pos_offset;
-    g[d] = f2u_sat(floorf(pos[d]));
-    pos[d] = pos[d] - (float)g[d];
-    if (interp == 1) pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
-  }
-#pragma unroll
-  for (int f = 0; f < F; f++) out[f] = 0.0f;
-  // issue all eight gathers before consuming them
-  uint32_t idx[8];
-  float wts[8];
-#pragma unroll
-  for (int c = 0; c < 8; c++) {
-    float w = 1.0f;
-    w *= (c & 1) ? pos[0] : 1 - pos[0];
-    w *= (c & 2) ? pos[1] : 1 - pos[1];
-    w *= (c & 4) ? pos[2] : 1 - pos[2];
-    wts[c] = w;
-    idx[c] = level_index(flags, res1, hsize, g[0] + ((c & 1) ? 1u : 0u), g[1] + ((c & 2) ? 1u : 0u),
-                         g[2] + ((c & 4) ? 1u : 0u));
-  }
-  float vals[8][F];
-#pragma unroll
-  for (int c = 0; c < 8; c++) load_entry<F, kHalf>(table, base + idx[c], vals[c]);
-#pragma unroll
-  for (int c = 0; c < 8; c++) {
-#pragma unroll
-    for (int f = 0; f < F; f++) out[f] = fmaf(wts[c], vals[c][f], out[f]);
-  }
 }
 
 }  // namespace nest

@@ -48,11 +48,15 @@ __device__ __forceinline__ int f2i_sat(float x) {
   return (int)x;
 }
 
-// float -> uint32 truncation; negatives and NaN give 0, large values saturate.
+// float -> uint32 truncation; negatives and NaN give 0, 2^32 and above give
+// 0xFFFFFFFF.  v_cvt_u32_f32 clamps exactly so (a C cast of an out-of-range
+// value is undefined, and the guarded C form compiles to branches).  Since
+// truncation equals floor for x >= 0 and both sides give 0 below,
+// f2u_sat(x) == f2u_sat(floorf(x)) for every x.
 __device__ __forceinline__ uint32_t f2u_sat(float x) {
-  if (!(x >= 0.0f)) return 0u;
-  if (x >= 4294967040.0f) return 4294967040u;
-  return (uint32_t)x;
+  uint32_t r;
+  asm("v_cvt_u32_f32 %0, %1" : "=v"(r) : "v"(x));
+  return r;
 }
 
 __device__ __forceinline__ uint32_t clamp_tile(int v, uint32_t g) {

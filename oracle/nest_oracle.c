@@ -97,11 +97,13 @@ static inline int f2i_sat(float x)
     return (int)x;
 }
 
-/* float -> uint32, truncating; negatives and NaN -> 0, saturating on top. */
+/* float -> uint32, truncating; negatives and NaN -> 0, 2^32 and above ->
+ * 0xFFFFFFFF (the clamping of the GPU float -> u32 conversion the reference's
+ * implicit casts compile to). */
 static inline uint32_t f2u_sat(float x)
 {
     if (!(x >= 0.0f)) return 0u;
-    if (x >= 4294967040.0f) return 4294967040u;
+    if (x >= 4294967296.0f) return 4294967295u;
     return (uint32_t)x;
 }
 

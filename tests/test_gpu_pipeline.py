@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 SCENES = ["cfg1", "shell_small", "unbounded_small", "shells_small"]
 
 
-def run_gpu(sc, cam_index=0, max_intersections=0):
+def run_gpu(sc, cam_index=0, max_intersections=0, align_corners=False, interp=0):
     from nest_splat import rasterizer as rz
     sp = sc.spec
     cam = sc.cameras[cam_index]
@@ -26,21 +26,23 @@ def run_gpu(sc, cam_index=0, max_intersections=0):
     settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy,
                                 cam.world_view_transform, cam.full_proj_transform, cam.camera_center,
                                 if_contract=sp.contract, max_intersections=max_intersections)
-    grid = rz.HashGridDesc(sp.L, sp.F, sp.S, sp.base_res, t(sc.table), sc.offsets, np.asarray(sp.gridrange, np.float32))
+    grid = rz.HashGridDesc(sp.L, sp.F, sp.S, sp.base_res, t(sc.table), sc.offsets, np.asarray(sp.gridrange, np.float32),
+                           align_corners=align_corners, interpolation=interp)
     res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
                                homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), channels=sp.C)
     torch.cuda.synchronize()
     return res
 
 
-def run_oracle(O, sc, cam_index=0, max_intersections=0):
+def run_oracle(O, sc, cam_index=0, max_intersections=0, align_corners=False, interp=0):
     sp = sc.spec
     cam = sc.cameras[cam_index]
     W, H = cam.image_width, cam.image_height
     pre = O.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
                        cam.full_proj_transform, W, H)
     b = O.binning(pre, W, H)
-    grid = O.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    grid = O.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract,
+                       align_corners=align_corners, interp=interp)
     r = O.render(pre, b, W, H, sp.C, grid, homotrans=sc.homotrans, ap_level=sc.ap_level,
                  max_intersections=max_intersections)
     return pre, b, r
@@ -147,6 +149,21 @@ def test_irregular_level_sizes_parity(oracle, sizes, name):
     print(f"[case] irregular level sizes {sizes} {name} {table.dtype} P={sc.spec.P}", flush=True)
     res = run_gpu(sc2)
     _, b, r = run_oracle(oracle, sc2)
+    assert res.num_rendered == b["num_rendered"]
+    np.testing.assert_array_equal(res.others.cpu().numpy(), r["others"])
+    np.testing.assert_array_equal(res.color.cpu().numpy(), r["color"])
+
+
+@pytest.mark.parametrize("name,align,interp", [("unbounded_small", False, 1), ("shell_small", True, 0),
+                                               ("shells_small", True, 1)])
+def test_align_corners_and_smoothstep_parity(oracle, name, align, interp):
+    """align_corners (pos offset 0, resolution cells) and smoothstep
+    weights (hashgrid.h smoothstep); smoothstep takes the general per-level
+    path, trilinear the dense-prefix/power-of-two one."""
+    sc = scene(name)
+    print(f"[case] {name} align_corners={align} interp={interp}", flush=True)
+    res = run_gpu(sc, align_corners=align, interp=interp)
+    _, b, r = run_oracle(oracle, sc, align_corners=align, interp=interp)
     assert res.num_rendered == b["num_rendered"]
     np.testing.assert_array_equal(res.others.cpu().numpy(), r["others"])
     np.testing.assert_array_equal(res.color.cpu().numpy(), r["color"])
