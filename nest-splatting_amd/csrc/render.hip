@@ -129,14 +129,31 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
 #pragma unroll
   for (int d = 0; d < kQueue; d++) wd[d] = d < take ? hq[(qhead + d) & (kQueue - 1)][threadIdx.x].w : 0.0f;
   __builtin_amdgcn_wave_barrier();
+  // Software-pipelined over levels: level l+1's gathers are issued as soon as
+  // level l is interpolated (its load registers are free then), so they are
+  // in flight during level l's hand-off through LDS and the owners' sums.
+  constexpr int kLevels = NACC / F;
+  LevelCorners cn;
+  float vals[8][F];
+  bool look = work && 0u < nlev;
+  if (look) {
+    level_corners<F, kHalf, kStructured>(g.lv, 0, g.pos_offset, g.interp, u, cn, g.n_dense);
+    corners_load<F, kHalf>(rsrc, cn, vals);
+  }
 #pragma unroll
-  for (int l = 0; l < NACC / F; l++) {
-    if (work) {
-      float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if ((uint32_t)l < nlev)
-        level_interp_struct<F, kHalf, kStructured>(rsrc, g.lv, l, g.pos_offset, g.interp, u, v, g.n_dense);
-      hq[wslot][col] = make_float4(v[0], v[1], v[2], v[3]);
+  for (int l = 0; l < kLevels; l++) {
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (look) corners_sum<F>(cn, vals, v);
+    bool next = false;
+    if (l + 1 < kLevels) {
+      next = work && (uint32_t)(l + 1) < nlev;
+      if (next) {
+        level_corners<F, kHalf, kStructured>(g.lv, l + 1, g.pos_offset, g.interp, u, cn, g.n_dense);
+        corners_load<F, kHalf>(rsrc, cn, vals);
+      }
     }
+    if (work) hq[wslot][col] = make_float4(v[0], v[1], v[2], v[3]);
+    look = next;
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int d = 0; d < kQueue; d++) {
