@@ -235,6 +235,7 @@ int nest_image_layout(int32_t W, int32_t H, size_t offsets[NEST_IMG_FIELDS], siz
   o[NEST_IMG_RANGES] = c.take(tiles * 8);
   o[NEST_IMG_FINAL_T] = c.take(HW * 3 * 4);
   o[NEST_IMG_N_CONTRIB] = c.take(HW * 2 * 4);
+  o[NEST_IMG_LEVELS] = c.take(sizeof(LevelQuad) * NEST_MAX_LEVELS);
   if (offsets)
     for (int i = 0; i < NEST_IMG_FIELDS; i++) offsets[i] = o[i];
   if (total) *total = c.off;
@@ -462,6 +463,7 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   rp.out_others = out->out_others;
   rp.final_T = reinterpret_cast<float*>(im + io[NEST_IMG_FINAL_T]);
   rp.n_contrib = reinterpret_cast<uint32_t*>(im + io[NEST_IMG_N_CONTRIB]);
+  rp.grid.lq = reinterpret_cast<LevelQuad*>(im + io[NEST_IMG_LEVELS]);
   tm.begin(NEST_STAGE_RENDER);
   if ((rc = check_stage(launch_render(rp, s), "render", rs->debug, s))) return rc;
   tm.end();

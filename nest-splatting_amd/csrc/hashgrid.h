@@ -150,46 +150,54 @@ struct LevelCorners {
   float wx[2], wy[2], wz[2];
 };
 
-// kStructured: the caller has checked that levels [0, n_dense) are dense with
-// no modulo, the rest hashed with a power-of-two size (the usual grid: coarse
-// levels fit their table, fine ones are hashed) and that the interpolation is
-// trilinear; the index path is then chosen by one compare instead of the flag
-// tests.
-template <int F, bool kHalf, bool kStructured = false>
-__device__ __forceinline__ void level_corners(const LevelTable& lv, int l, float pos_offset, uint32_t interp,
-                                              const float u[3], LevelCorners& cn, uint32_t n_dense = 0) {
-  const float scale = lv.scale[l];
-  const uint32_t res1 = lv.res1[l];
-  const uint32_t hsize = lv.hsize[l];
-  const uint32_t flags = kStructured ? ((uint32_t)l < n_dense ? kLvNoMod : (kLvHashed | kLvPow2)) : lv.flags[l];
-  cn.soff = lv.base[l] * (uint32_t)(F * (kHalf ? 2 : 4));
+// Cell of u at a level: g = (uint32)floor(x) with the saturating conversion,
+// pos = x - (float)g, x = u * scale + pos_offset, then the corner weights.
+__device__ __forceinline__ void cell_weights(float scale, float pos_offset, bool smooth, const float u[3], uint32_t g[3],
+                                             LevelCorners& cn) {
   float pos[3];
-  uint32_t g[3];
 #pragma unroll
   for (int d = 0; d < 3; d++) {
-    // g = (uint32)floor(x) with the saturating conversion, pos = x - (float)g
     const float x = u[d] * scale + pos_offset;
     g[d] = f2u_sat(x);
     pos[d] = x - (float)g[d];
-    if (!kStructured && interp == 1) pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
+    if (smooth) pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
   }
   cn.wx[0] = 1 - pos[0]; cn.wx[1] = pos[0];
   cn.wy[0] = 1 - pos[1]; cn.wy[1] = pos[1];
   cn.wz[0] = 1 - pos[2]; cn.wz[1] = pos[2];
+}
+
+__device__ __forceinline__ void hashed_corners(const uint32_t g[3], uint32_t idx[8]) {
+  const uint32_t a[2] = {g[0], g[0] + 1u};
+  const uint32_t b0 = g[1] * 2654435761u, c0 = g[2] * 805459861u;
+  const uint32_t b[2] = {b0, b0 + 2654435761u}, c[2] = {c0, c0 + 805459861u};
+  const uint32_t ab[4] = {a[0] ^ b[0], a[1] ^ b[0], a[0] ^ b[1], a[1] ^ b[1]};
+#pragma unroll
+  for (int k = 0; k < 8; k++) idx[k] = ab[k & 3] ^ c[k >> 2];
+}
+
+__device__ __forceinline__ void dense_corners(const uint32_t g[3], uint32_t res1, uint32_t r2, uint32_t idx[8]) {
+  const uint32_t base = g[0] + g[1] * res1 + g[2] * r2;
+#pragma unroll
+  for (int k = 0; k < 8; k++) idx[k] = base + ((k & 1) ? 1u : 0u) + ((k & 2) ? res1 : 0u) + ((k & 4) ? r2 : 0u);
+}
+
+// Any level layout: the level's flags pick hashed or dense indexing and the
+// modulo (none, power-of-two mask, or %).
+template <int F, bool kHalf>
+__device__ __forceinline__ void level_corners(const LevelTable& lv, int l, float pos_offset, uint32_t interp,
+                                              const float u[3], LevelCorners& cn) {
+  const uint32_t res1 = lv.res1[l];
+  const uint32_t hsize = lv.hsize[l];
+  const uint32_t flags = lv.flags[l];
+  cn.soff = lv.base[l] * (uint32_t)(F * (kHalf ? 2 : 4));
+  uint32_t g[3];
+  cell_weights(lv.scale[l], pos_offset, interp == 1, u, g, cn);
   uint32_t* idx = cn.idx;
-  if (flags & kLvHashed) {
-    const uint32_t a[2] = {g[0], g[0] + 1u};
-    const uint32_t b0 = g[1] * 2654435761u, c0 = g[2] * 805459861u;
-    const uint32_t b[2] = {b0, b0 + 2654435761u}, c[2] = {c0, c0 + 805459861u};
-    const uint32_t ab[4] = {a[0] ^ b[0], a[1] ^ b[0], a[0] ^ b[1], a[1] ^ b[1]};
-#pragma unroll
-    for (int k = 0; k < 8; k++) idx[k] = ab[k & 3] ^ c[k >> 2];
-  } else {
-    const uint32_t r2 = res1 * res1;
-    const uint32_t base = g[0] + g[1] * res1 + g[2] * r2;
-#pragma unroll
-    for (int k = 0; k < 8; k++) idx[k] = base + ((k & 1) ? 1u : 0u) + ((k & 2) ? res1 : 0u) + ((k & 4) ? r2 : 0u);
-  }
+  if (flags & kLvHashed)
+    hashed_corners(g, idx);
+  else
+    dense_corners(g, res1, res1 * res1, idx);
   if (!(flags & kLvNoMod)) {
     if (flags & kLvPow2) {
 #pragma unroll
@@ -198,6 +206,22 @@ __device__ __forceinline__ void level_corners(const LevelTable& lv, int l, float
 #pragma unroll
       for (int k = 0; k < 8; k++) idx[k] %= hsize;
     }
+  }
+}
+
+// The common grid (levels [0, n_dense) dense with no modulo, the rest hashed
+// into power-of-two sizes, trilinear weights) from the level's 16-byte
+// record: one uniform test of q.b picks the index path.
+__device__ __forceinline__ void quad_corners(const LevelQuad& q, float pos_offset, const float u[3], LevelCorners& cn) {
+  cn.soff = q.soff;
+  uint32_t g[3];
+  cell_weights(q.scale, pos_offset, false, u, g, cn);
+  if (q.b != 0) {
+    dense_corners(g, q.a, q.b, cn.idx);
+  } else {
+    hashed_corners(g, cn.idx);
+#pragma unroll
+    for (int k = 0; k < 8; k++) cn.idx[k] &= q.a;
   }
 }
 
@@ -220,17 +244,6 @@ __device__ __forceinline__ void corners_sum(const LevelCorners& cn, const float 
 #pragma unroll
     for (int f = 0; f < F; f++) out[f] = fmaf(w, vals[k][f], out[f]);
   }
-}
-
-template <int F, bool kHalf, bool kStructured = false>
-__device__ __forceinline__ void level_interp_struct(nest_i32x4 rsrc, const LevelTable& lv, int l,
-                                                    float pos_offset, uint32_t interp, const float u[3], float out[F],
-                                                    uint32_t n_dense = 0) {
-  LevelCorners cn;
-  level_corners<F, kHalf, kStructured>(lv, l, pos_offset, interp, u, cn, n_dense);
-  float vals[8][F];  // all eight loads in flight before the first use
-  corners_load<F, kHalf>(rsrc, cn, vals);
-  corners_sum<F>(cn, vals, out);
 }
 
 }  // namespace nest

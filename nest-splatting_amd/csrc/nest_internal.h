@@ -65,6 +65,17 @@ struct LevelTable {
   uint32_t flags[NEST_MAX_LEVELS];     // bit0 hashed, bit1 power-of-two size, bits 2.. stride count
 };
 
+// Per-level constants of the common-grid lookup (see GridParams::structured),
+// one 16-byte record per level so that a level costs one scalar load:
+// dense levels {scale, res1, res1^2, byte offset}, hashed levels
+// {scale, size - 1, 0, byte offset}.
+struct LevelQuad {
+  float scale;
+  uint32_t a;     // res1 (dense) or size - 1 (hashed, power of two)
+  uint32_t b;     // res1 * res1 (dense) or 0 (hashed)
+  uint32_t soff;  // first entry of the level, in bytes
+};
+
 struct GridParams {
   uint32_t L;           // levels queried
   uint32_t F;
@@ -79,6 +90,7 @@ struct GridParams {
   uint32_t table_rows;  // entries of the table (records of the struct-buffer view)
   uint32_t structured;  // levels [0, n_dense) dense without modulo, the rest hashed power-of-two
   uint32_t n_dense;
+  LevelQuad* lq;        // [L] device copy of the level records (structured grids), written by launch_render
   const void* table;
   LevelTable lv;
 };

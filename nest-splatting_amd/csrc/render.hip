@@ -57,6 +57,34 @@ __device__ __forceinline__ uint64_t lanemask_lt64() {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
+// Level records of the common grid (LevelQuad as four u32), read through the
+// scalar cache.
+typedef unsigned int nest_u32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(4))) nest_u32x4* LevelQuadPtr;
+
+// Corner indices, weights and level offset of level l at u.  Common grid:
+// the level's 16-byte record, read with one scalar load at this point (the
+// empty asm makes the pointer opaque per level, so the 16 levels' records are
+// not all hoisted into registers kept across the whole kernel).  Other grids:
+// the level table in the kernel arguments.
+template <int F, bool kHalf, bool kStructured>
+__device__ __forceinline__ void level_setup(const GridParams& g, LevelQuadPtr lqb, int l, const float u[3],
+                                            LevelCorners& cn) {
+  if constexpr (kStructured) {
+    LevelQuadPtr ql = lqb;
+    asm volatile("" : "+s"(ql));
+    const nest_u32x4 r = ql[l];
+    LevelQuad q;
+    q.scale = __uint_as_float(r.x);
+    q.a = r.y;
+    q.b = r.z;
+    q.soff = r.w;
+    quad_corners(q, g.pos_offset, u, cn);
+  } else {
+    level_corners<F, kHalf>(g.lv, l, g.pos_offset, g.interp, u, cn);
+  }
+}
+
 // One drain round (any F): every lane with a pending hit looks up its oldest
 // one (ring-buffer head) and accumulates each level below its level count;
 // lanes with an empty queue idle.
@@ -67,11 +95,16 @@ __device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc
     const float4 e = hq[qhead][threadIdx.x];
     const uint32_t maxl = hl[qhead][threadIdx.x];
     const float u[3] = {e.x, e.y, e.z};
+    const LevelQuadPtr lqb = (LevelQuadPtr)g.lq;
 #pragma unroll
     for (int l = 0; l < NACC / F; l++) {
       if ((uint32_t)l < maxl) {
+        LevelCorners cn;
+        level_setup<F, kHalf, kStructured>(g, lqb, l, u, cn);
+        float vals[8][F];
+        corners_load<F, kHalf>(rsrc, cn, vals);
         float v[F];
-        level_interp_struct<F, kHalf, kStructured>(rsrc, g.lv, l, g.pos_offset, g.interp, u, v, g.n_dense);
+        corners_sum<F>(cn, vals, v);
 #pragma unroll
         for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(v[f], e.w, acc[l * F + f]);
       }
@@ -133,11 +166,12 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
   // level l is interpolated (its load registers are free then), so they are
   // in flight during level l's hand-off through LDS and the owners' sums.
   constexpr int kLevels = NACC / F;
+  const LevelQuadPtr lqb = (LevelQuadPtr)g.lq;
   LevelCorners cn;
   float vals[8][F];
   bool look = work && 0u < nlev;
   if (look) {
-    level_corners<F, kHalf, kStructured>(g.lv, 0, g.pos_offset, g.interp, u, cn, g.n_dense);
+    level_setup<F, kHalf, kStructured>(g, lqb, 0, u, cn);
     corners_load<F, kHalf>(rsrc, cn, vals);
   }
 #pragma unroll
@@ -148,7 +182,7 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
     if (l + 1 < kLevels) {
       next = work && (uint32_t)(l + 1) < nlev;
       if (next) {
-        level_corners<F, kHalf, kStructured>(g.lv, l + 1, g.pos_offset, g.interp, u, cn, g.n_dense);
+        level_setup<F, kHalf, kStructured>(g, lqb, l + 1, u, cn);
         corners_load<F, kHalf>(rsrc, cn, vals);
       }
     }
@@ -467,9 +501,36 @@ static hipError_t launch_hash_levels(const RenderParams& p, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
+struct LevelQuads {
+  LevelQuad q[NEST_MAX_LEVELS];
+};
+
+// Copies the level records from the kernel arguments to device memory, where
+// the render reads them with scalar loads.
+__global__ void level_quads_kernel(LevelQuads lq, uint32_t L, LevelQuad* dst) {
+  if (threadIdx.x != 0) return;
+#pragma unroll
+  for (int l = 0; l < NEST_MAX_LEVELS; l++)
+    if ((uint32_t)l < L) dst[l] = lq.q[l];
+}
+
 template <int F, bool kHalf>
 static hipError_t launch_hash(const RenderParams& p, hipStream_t s) {
-  return p.grid.structured ? launch_hash_levels<F, kHalf, true>(p, s) : launch_hash_levels<F, kHalf, false>(p, s);
+  if (!p.grid.structured) return launch_hash_levels<F, kHalf, false>(p, s);
+  const GridParams& g = p.grid;
+  LevelQuads lq = {};
+  for (uint32_t l = 0; l < g.L; l++) {
+    LevelQuad& q = lq.q[l];
+    q.scale = g.lv.scale[l];
+    const bool dense = l < g.n_dense;
+    q.a = dense ? g.lv.res1[l] : g.lv.hsize[l] - 1u;
+    q.b = dense ? g.lv.res1[l] * g.lv.res1[l] : 0u;
+    q.soff = g.lv.base[l] * (uint32_t)(F * (kHalf ? 2 : 4));
+  }
+  hipLaunchKernelGGL(level_quads_kernel, dim3(1), dim3(64), 0, s, lq, g.L, g.lq);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_hash_levels<F, kHalf, true>(p, s);
 }
 
 hipError_t launch_render(const RenderParams& p, hipStream_t s) {
