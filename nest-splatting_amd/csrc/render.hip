@@ -67,13 +67,16 @@ typedef const __attribute__((address_space(4))) nest_u32x4* LevelQuadPtr;
 // empty asm makes the pointer opaque per level, so the 16 levels' records are
 // not all hoisted into registers kept across the whole kernel).  Other grids:
 // the level table in the kernel arguments.
+__device__ __forceinline__ nest_u32x4 level_record(LevelQuadPtr lqb, int l) {
+  LevelQuadPtr ql = lqb;
+  asm volatile("" : "+s"(ql));
+  return ql[l];
+}
+
 template <int F, bool kHalf, bool kStructured>
-__device__ __forceinline__ void level_setup(const GridParams& g, LevelQuadPtr lqb, int l, const float u[3],
+__device__ __forceinline__ void level_setup(const GridParams& g, nest_u32x4 r, int l, const float u[3],
                                             LevelCorners& cn) {
   if constexpr (kStructured) {
-    LevelQuadPtr ql = lqb;
-    asm volatile("" : "+s"(ql));
-    const nest_u32x4 r = ql[l];
     LevelQuad q;
     q.scale = __uint_as_float(r.x);
     q.a = r.y;
@@ -100,7 +103,9 @@ __device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc
     for (int l = 0; l < NACC / F; l++) {
       if ((uint32_t)l < maxl) {
         LevelCorners cn;
-        level_setup<F, kHalf, kStructured>(g, lqb, l, u, cn);
+        nest_u32x4 rec = {0u, 0u, 0u, 0u};
+        if constexpr (kStructured) rec = level_record(lqb, l);
+        level_setup<F, kHalf, kStructured>(g, rec, l, u, cn);
         float vals[8][F];
         corners_load<F, kHalf>(rsrc, cn, vals);
         float v[F];
@@ -170,24 +175,31 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
   LevelCorners cn;
   float vals[8][F];
   bool look = work && 0u < nlev;
+  nest_u32x4 rec = {0u, 0u, 0u, 0u}, rec_next = {0u, 0u, 0u, 0u};
+  if constexpr (kStructured) rec = level_record(lqb, 0);
   if (look) {
-    level_setup<F, kHalf, kStructured>(g, lqb, 0, u, cn);
+    level_setup<F, kHalf, kStructured>(g, rec, 0, u, cn);
     corners_load<F, kHalf>(rsrc, cn, vals);
   }
+  if constexpr (kStructured) rec_next = level_record(lqb, 1);
 #pragma unroll
   for (int l = 0; l < kLevels; l++) {
+    nest_u32x4 rec_after = {0u, 0u, 0u, 0u};
+    if constexpr (kStructured)
+      if (l + 2 < kLevels) rec_after = level_record(lqb, l + 2);
     float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (look) corners_sum<F>(cn, vals, v);
     bool next = false;
     if (l + 1 < kLevels) {
       next = work && (uint32_t)(l + 1) < nlev;
       if (next) {
-        level_setup<F, kHalf, kStructured>(g, lqb, l + 1, u, cn);
+        level_setup<F, kHalf, kStructured>(g, rec_next, l + 1, u, cn);
         corners_load<F, kHalf>(rsrc, cn, vals);
       }
     }
     if (work) hq[wslot][col] = make_float4(v[0], v[1], v[2], v[3]);
     look = next;
+    rec_next = rec_after;
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int d = 0; d < kQueue; d++) {
