@@ -266,6 +266,7 @@ int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp,
   p.gx = (uint32_t)((W + kTile - 1) / kTile);
   p.gy = (uint32_t)((H + kTile - 1) / kTile);
   p.scale_mod = rs->scale_modifier;
+  p.beta = rs->beta;
   memcpy(p.view, rs->viewmatrix, sizeof(p.view));
   memcpy(p.proj, rs->projmatrix, sizeof(p.proj));
   p.means = sp->means3D;

@@ -29,6 +29,7 @@ struct PreprocessParams {
   int W, H;
   uint32_t gx, gy;
   float scale_mod;
+  float beta;               // render's G -> (1+beta) G / (1+beta G) activation (0: off)
   float view[16];
   float proj[16];
   const float* means;

@@ -175,18 +175,21 @@ __global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams 
     pk0 = r0.w; pk1 = r1.w; pk2 = r2.w;
   }
   // Rejection bounds for the render loop.  A pair is rejected by the alpha
-  // test (alpha < 1/255) whenever rho = min(rho3d, rho2d) > 2 ln(255 o); the
-  // cut below adds a relative 1e-6 for the expf/rounding error and 1e-4
-  // absolute, so any pair the render skips with it is one the exact test
-  // rejects.  The acceptance region {rho3d <= cut} U {rho2d <= cut} is
+  // test (alpha < 1/255) whenever rho = min(rho3d, rho2d) > 2 ln(255 o); with
+  // the beta activation G' = (1+b) G / (1+b G) the bound is
+  // 2 ln(255 o (1+b) - b) (G' = 1/(255 o) solved for G).  The cut below adds
+  // a relative 1e-6 for the expf/rounding error and 1e-4 absolute, so any
+  // pair the render skips with it is one the exact test rejects.  The acceptance region {rho3d <= cut} U {rho2d <= cut} is
   // bounded by the bbox of the projected disk |s|^2 <= cut (the conic bbox of
   // CR/forward.cu:294-320 at cutoff^2 = cut, valid when the whole disk lies in
   // front of the camera: cut*(Tw0^2+Tw1^2) < Tw2^2) and the disk of radius
   // sqrt(cut/2) around xy, widened by one pixel.
   float cut = -1.0f;
   float bx0 = 1.0f, bx1 = -1.0f, by0 = 1.0f, by1 = -1.0f;  // empty: never accepted
-  if (opacity > 0.0f) {
-    const double c = 2.0 * log(255.0 * (double)opacity * (1.0 + 1e-6)) + 1e-4;
+  const double bb = p.beta > 0.0f ? (double)p.beta : 0.0;
+  const double xo = 255.0 * (double)opacity * (1.0 + bb) - bb;
+  if (opacity > 0.0f && xo > 0.0) {
+    const double c = 2.0 * log(xo * (1.0 + 1e-6)) + 1e-4;
     if (c >= 0.0) {
       cut = (float)c;
       const double rd = sqrt(c * 0.5) + 1.0;

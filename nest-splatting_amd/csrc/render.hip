@@ -254,7 +254,9 @@ __device__ __forceinline__ bool splat_hit(float4 q0, float4 q1, float4 q2, float
   const float power = -0.5f * rho;
   if (power > 0.0f) return false;
   float G = expf_ref(power);
-  if (beta > 0.0f) G = (float)((1.0 + (double)beta) * (double)G / (1.0 + (double)beta * (double)G));
+  // (1.0 + beta) * G / (1.0 + beta * G) with float beta and G (CR/forward.cu:915-916): the product
+  // beta * G is a float product, the rest double
+  if (beta > 0.0f) G = (float)((1.0 + (double)beta) * (double)G / (1.0 + (double)(beta * G)));
   const float alpha = fminf(0.99f, q2.w * G);
   if (alpha < 1.0f / 255.0f) return false;
   h.sx = sx;

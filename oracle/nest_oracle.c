@@ -666,7 +666,8 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
         float power = -0.5f * rho;
         if (power > 0.0f) continue;
         float G = or_expf(power);
-        if (A->beta > 0.0f) G = (float)((1.0 + (double)A->beta) * (double)G / (1.0 + (double)A->beta * (double)G));
+        /* (1.0 + beta) * G / (1.0 + beta * G): beta * G is a float product (forward.cu:915-916) */
+        if (A->beta > 0.0f) G = (float)((1.0 + (double)A->beta) * (double)G / (1.0 + (double)(A->beta * G)));
         float alpha = fminf(0.99f, no[3] * G);
         if (alpha < 1.0f / 255.0f) continue;
         float test_T = T * (1 - alpha);

@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 SCENES = ["cfg1", "shell_small", "unbounded_small", "shells_small"]
 
 
-def run_gpu(sc, cam_index=0, max_intersections=0, align_corners=False, interp=0):
+def run_gpu(sc, cam_index=0, max_intersections=0, align_corners=False, interp=0, beta=0.0):
     from nest_splat import rasterizer as rz
     sp = sc.spec
     cam = sc.cameras[cam_index]
@@ -25,7 +25,7 @@ def run_gpu(sc, cam_index=0, max_intersections=0, align_corners=False, interp=0)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
     settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy,
                                 cam.world_view_transform, cam.full_proj_transform, cam.camera_center,
-                                if_contract=sp.contract, max_intersections=max_intersections)
+                                beta=beta, if_contract=sp.contract, max_intersections=max_intersections)
     grid = rz.HashGridDesc(sp.L, sp.F, sp.S, sp.base_res, t(sc.table), sc.offsets, np.asarray(sp.gridrange, np.float32),
                            align_corners=align_corners, interpolation=interp)
     res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
@@ -34,7 +34,7 @@ def run_gpu(sc, cam_index=0, max_intersections=0, align_corners=False, interp=0)
     return res
 
 
-def run_oracle(O, sc, cam_index=0, max_intersections=0, align_corners=False, interp=0):
+def run_oracle(O, sc, cam_index=0, max_intersections=0, align_corners=False, interp=0, beta=0.0):
     sp = sc.spec
     cam = sc.cameras[cam_index]
     W, H = cam.image_width, cam.image_height
@@ -44,7 +44,7 @@ def run_oracle(O, sc, cam_index=0, max_intersections=0, align_corners=False, int
     grid = O.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract,
                        align_corners=align_corners, interp=interp)
     r = O.render(pre, b, W, H, sp.C, grid, homotrans=sc.homotrans, ap_level=sc.ap_level,
-                 max_intersections=max_intersections)
+                 max_intersections=max_intersections, beta=beta)
     return pre, b, r
 
 
@@ -165,6 +165,21 @@ def test_align_corners_and_smoothstep_parity(oracle, name, align, interp):
     res = run_gpu(sc, align_corners=align, interp=interp)
     _, b, r = run_oracle(oracle, sc, align_corners=align, interp=interp)
     assert res.num_rendered == b["num_rendered"]
+    np.testing.assert_array_equal(res.others.cpu().numpy(), r["others"])
+    np.testing.assert_array_equal(res.color.cpu().numpy(), r["color"])
+
+
+@pytest.mark.parametrize("name,beta", [("shell_small", 0.5), ("unbounded_small", 4.0)])
+def test_beta_activation_parity(oracle, name, beta):
+    """G -> (1+beta) G / (1+beta G) (CR/forward.cu:915-916): hits with alpha in
+    [1/255, ...) beyond the beta = 0 cut must be kept, so the render's early
+    reject uses the beta-aware bound."""
+    sc = scene(name)
+    print(f"[case] {name} beta={beta}", flush=True)
+    res = run_gpu(sc, beta=beta)
+    _, b, r = run_oracle(oracle, sc, beta=beta)
+    _, _, r0 = run_oracle(oracle, sc)
+    assert (r["others"][7] > r0["others"][7]).any()  # beta accepts more hits than beta = 0
     np.testing.assert_array_equal(res.others.cpu().numpy(), r["others"])
     np.testing.assert_array_equal(res.color.cpu().numpy(), r["color"])
 
