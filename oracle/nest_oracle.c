@@ -904,3 +904,6 @@ void or_activate(int P, const float *sc_raw, const float *rot_raw, const float *
         opac[p] = 1.0f / (1.0f + or_expf(-op_raw[p]));
     }
 }
+
+/* Backward pass (training): a separate file of the same translation unit. */
+#include "nest_oracle_bwd.c"

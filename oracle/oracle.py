@@ -48,6 +48,17 @@ class OrRenderArgs(ct.Structure):
                 ("n_contrib", ct.c_void_p)]
 
 
+class OrRenderBwdArgs(ct.Structure):
+    _fields_ = [("W", ct.c_int), ("H", ct.c_int), ("C", ct.c_int), ("level", ct.c_int), ("beta", ct.c_float),
+                ("ranges", ct.c_void_p), ("point_list", ct.c_void_p), ("xy", ct.c_void_p),
+                ("transmat", ct.c_void_p), ("normal_opacity", ct.c_void_p), ("homotrans", ct.c_void_p),
+                ("ap_level", ct.c_void_p), ("colors", ct.c_void_p), ("grid", OrGrid),
+                ("final_T", ct.c_void_p), ("n_contrib", ct.c_void_p), ("dL_dpix", ct.c_void_p),
+                ("dL_dothers", ct.c_void_p), ("dtable", ct.c_void_p), ("dtransmat", ct.c_void_p),
+                ("dhomo", ct.c_void_p), ("dmean2D", ct.c_void_p), ("dnormal", ct.c_void_p),
+                ("dopacity", ct.c_void_p), ("dcolors", ct.c_void_p), ("gradsum", ct.c_void_p)]
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -79,6 +90,11 @@ def lib():
         L.or_sh16.argtypes = [f32p, f32p]
         L.or_rvq_decode.argtypes = [ct.c_int, ct.c_int, ct.c_int, ct.c_int, f32p, u16p, ct.c_void_p, f32p]
         L.or_activate.argtypes = [ct.c_int, f32p, f32p, f32p, f32p, f32p, f32p]
+        L.or_render_backward.argtypes = [ct.POINTER(OrRenderBwdArgs)]
+        L.or_preprocess_backward.argtypes = [ct.c_int, f32p, f32p, f32p, i32p, f32p, f32p, f32p, ct.c_int, ct.c_int,
+                                             ct.c_void_p, ct.c_int, ct.c_int, f32p, ct.c_void_p, ct.c_void_p, f32p,
+                                             f32p, f32p, f32p, f32p, f32p, f32p, ct.c_void_p]
+        L.or_grid_encode_backward.argtypes = [ct.POINTER(OrGrid), ct.c_int, f32p, f32p, f32p, ct.c_void_p]
         u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
         L.or_sh_colors.argtypes = [ct.c_int, ct.c_int, ct.c_int, f32p, f32p, f32p, i32p, f32p, u8p]
         L.or_mark_visible.argtypes = [ct.c_int, f32p, f32p, u8p]
@@ -214,6 +230,96 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
     args.n_contrib = out["n_contrib"].ctypes.data
     lib().or_render(ct.byref(args), row_stride, row_phase, threads)
     return out
+
+
+def render_backward(pre, binres, fwd, W, H, C, grid: Optional[OrGrid], dL_dpix, dL_dothers, homotrans=None,
+                    ap_level=None, colors=None, beta=0.0):
+    """renderCUDAsurfelBackward (mode 0) for every pixel, given the forward's
+    final_T / n_contrib (fwd = render(...)'s result).  Returns the per-splat
+    gradients (dtransmat [P,9], dhomo [P,9], dmean2D [P,3], dnormal [P,3],
+    dopacity [P], dcolors [P,C], gradsum [P]) and dtable [rows, F]."""
+    P = pre["radii"].shape[0]
+    rows = 0 if grid is None else grid._keep[1].shape[0]
+    F = 1 if grid is None else grid.F
+    out = dict(dtransmat=np.zeros((P, 9), np.float32), dhomo=np.zeros((P, 9), np.float32),
+               dmean2D=np.zeros((P, 3), np.float32), dnormal=np.zeros((P, 3), np.float32),
+               dopacity=np.zeros(P, np.float32), dcolors=np.zeros((P, C), np.float32),
+               gradsum=np.zeros(P, np.float32), dtable=np.zeros((max(rows, 1), F), np.float32))
+    keep = []
+
+    def ptr(a, dt):
+        if a is None:
+            return None
+        a = _c(a, dt)
+        keep.append(a)
+        return a.ctypes.data
+
+    a = OrRenderBwdArgs()
+    a.W, a.H, a.C = W, H, C
+    a.level = 0 if grid is None else grid.L
+    a.beta = beta
+    a.ranges = ptr(binres["ranges"], np.uint32)
+    a.point_list = ptr(binres["vals"] if binres["num_rendered"] else np.zeros(1, np.uint32), np.uint32)
+    a.xy = ptr(pre["xy"], np.float32)
+    a.transmat = ptr(pre["transmat"], np.float32)
+    a.normal_opacity = ptr(pre["normal_opacity"], np.float32)
+    a.homotrans = ptr(homotrans, np.float32)
+    a.ap_level = ptr(ap_level, np.float32)
+    a.colors = ptr(colors, np.float32)
+    if grid is not None:
+        a.grid = grid
+    a.final_T = ptr(fwd["final_T"], np.float32)
+    a.n_contrib = ptr(fwd["n_contrib"], np.uint32)
+    a.dL_dpix = ptr(dL_dpix, np.float32)
+    a.dL_dothers = ptr(dL_dothers, np.float32)
+    for k in ("dtable", "dtransmat", "dhomo", "dmean2D", "dnormal", "dopacity", "dcolors", "gradsum"):
+        setattr(a, k, out[k].ctypes.data)
+    lib().or_render_backward(ct.byref(a))
+    if rows == 0:
+        out["dtable"] = np.zeros((0, F), np.float32)
+    return out
+
+
+def preprocess_backward(means, scales, rots, radii, transmat, view, proj, W, H, dtransmat, dhomo, dnormal, dmean2D,
+                        shs=None, sh_degree=0, campos=(0.0, 0.0, 0.0), clamped=None, dcolors=None):
+    """preprocessCUDA backward: returns dmeans [P,3], dscales [P,2], drots [P,4],
+    dmean2D [P,3] (the densification statistic) and dshs [P,M,3]."""
+    P = means.shape[0]
+    dm2 = _c(dmean2D, np.float32).copy()
+    out = dict(dmeans=np.zeros((P, 3), np.float32), dscales=np.zeros((P, 2), np.float32),
+               drots=np.zeros((P, 4), np.float32))
+    M = 0
+    sh_arr = None
+    if shs is not None:
+        sh_arr = _c(shs, np.float32).reshape(P, -1, 3)
+        M = sh_arr.shape[1]
+    dshs = np.zeros((P, max(M, 1), 3), np.float32)
+    cl = None if clamped is None else _c(clamped, np.uint8)
+    dc = None if dcolors is None else _c(dcolors, np.float32)
+    lib().or_preprocess_backward(P, _c(means, np.float32), _c(scales, np.float32), _c(rots, np.float32),
+                                 _c(radii, np.int32), _c(transmat, np.float32), _c(view, np.float32).reshape(-1),
+                                 _c(proj, np.float32).reshape(-1), W, H,
+                                 None if sh_arr is None else sh_arr.ctypes.data, int(sh_degree), M,
+                                 _c(campos, np.float32).reshape(-1), None if cl is None else cl.ctypes.data,
+                                 None if dc is None else dc.ctypes.data, _c(dtransmat, np.float32),
+                                 _c(dhomo, np.float32), _c(dnormal, np.float32), dm2, out["dmeans"],
+                                 out["dscales"], out["drots"], dshs.ctypes.data)
+    out["dmean2D"] = dm2
+    out["dshs"] = dshs[:, :M]
+    return out
+
+
+def grid_encode_backward(grid: OrGrid, inputs, grad, with_inputs=True):
+    """GridEncoder backward: (grad_table [rows, F], grad_inputs [B,3] or None);
+    grad is the forward output's gradient [B, L*F]."""
+    inputs = _c(inputs, np.float32)
+    B = inputs.shape[0]
+    rows = grid._keep[1].shape[0]
+    gt = np.zeros((rows, grid.F), np.float32)
+    gi = np.zeros((B, 3), np.float32) if with_inputs else None
+    lib().or_grid_encode_backward(ct.byref(grid), B, inputs, _c(grad, np.float32), gt,
+                                  None if gi is None else gi.ctypes.data)
+    return gt, gi
 
 
 def query_feature(grid: OrGrid, xyz, ap, C):
