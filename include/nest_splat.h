@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 4
+#define NEST_ABI_VERSION 5
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -217,6 +217,49 @@ int nest_forward_render(const nest_raster_settings *settings, const nest_hashgri
                         int64_t num_rendered, const nest_frame_outputs *out,
                         nest_timing *timing, void *stream);
 
+/* ---- backward (training) ------------------------------------------------
+ * nest_backward is RasterizeGaussiansBackwardCUDA
+ * (DSR/rasterize_points.cu:243-471) / CudaRasterizer::Rasterizer::backward
+ * (CR/rasterizer_impl.cu:444-600) for render mode 0 with the Gaussian
+ * kernel: renderCUDAsurfelBackward (CR/backward.cu:445-2049) then
+ * preprocessCUDA backward (CR/backward.cu:2216-2274).  It reads the
+ * workspaces of the nest_forward_geometry / nest_forward_render calls of the
+ * same frame (unchanged since) and the same settings, grid and splats.  Every
+ * gradient output is overwritten.  Hash tables must be binary32; at most 64
+ * output channels.  dL_dmeans2D receives the reference's densification
+ * statistic (dL/dTu.z * depth * W/2, dL/dTv.z * depth * H/2), not a
+ * gradient.  Per-splat and table gradients are summed with float atomics, so
+ * their low bits vary from run to run, as in the reference. */
+#define NEST_BWD_DTRANSMAT 0       /* f32 [P,9]  dL/dT of the render            */
+#define NEST_BWD_DHOMO 1           /* f32 [P,9]  dL/dhomotrans (columns 0, 1, 3) */
+#define NEST_BWD_DNORMAL 2         /* f32 [P,3]  dL/dnormal (view space)        */
+#define NEST_BWD_DCOLORS 3         /* f32 [P,C]  colour gradient when io->dL_dcolors is NULL */
+#define NEST_BWD_GRADSUM 4         /* f32 [P]    |dL/dfeature| sum when io->dL_dgradsum is NULL */
+#define NEST_BWD_FIELDS 5
+int nest_backward_layout(int32_t P, int32_t channels, size_t offsets[NEST_BWD_FIELDS], size_t *total_bytes);
+
+typedef struct {
+    uint32_t struct_size;            /* sizeof(nest_backward_io) */
+    int32_t channels;                /* C of the forward's out_color */
+    const float *dL_dout_color;      /* [C,H,W] */
+    const float *dL_dout_others;     /* [14,H,W]; channels 0-6 carry gradient */
+    float *dL_dmeans3D;              /* [P,3] */
+    float *dL_dmeans2D;              /* [P,3] densification statistic */
+    float *dL_dcolors;               /* [P,C] colour path, or NULL */
+    float *dL_dopacity;              /* [P] */
+    float *dL_dshs;                  /* [P,sh_coeffs,3] when the colours came from SH */
+    float *dL_dscales;               /* [P,2] */
+    float *dL_drotations;            /* [P,4] */
+    float *dL_dfeatures;             /* [table_rows, level_dim] hash path */
+    float *dL_dgradsum;              /* [P] hash path (returned for ap_level), or NULL */
+} nest_backward_io;
+
+int nest_backward(const nest_raster_settings *settings, const nest_hashgrid *grid, const nest_splats *splats,
+                  const void *geom_ws, size_t geom_bytes, const void *binning_ws, size_t binning_bytes,
+                  const void *image_ws, size_t image_bytes, int64_t num_rendered, const nest_backward_io *io,
+                  void *bwd_ws, size_t bwd_bytes, void *stream);
+
+
 /* markVisible (DSR/rasterize_points.cu:452-470, CR/rasterizer_impl.cu:198-210,
  * checkFrustum :54-66): present[i] = 1 when the view-space depth of
  * means3D[i] exceeds 0.2 (in_frustum, CR/auxiliary.h:190-215), else 0.
@@ -249,6 +292,16 @@ int nest_grid_encode(const float *inputs, int64_t B, int32_t D, const void *embe
                      int64_t emb_rows, int32_t emb_dtype, const int32_t *offsets_host, int32_t L, int32_t C, float S,
                      int32_t H, int32_t gridtype, int32_t align_corners, int32_t interpolation,
                      void *outputs, void *stream);
+
+/* GridEncoder.backward (GE/grid.py:70-91, GE/src/gridencoder.cu:245-366):
+ * grad_embeddings [emb_rows, C] is overwritten with the table gradient of
+ * grad [B, L*C]; grad_inputs [B, D] (or NULL) receives the input gradient
+ * through the forward's dy_dx (gridencoder.cu:196-242).  Arguments as
+ * nest_grid_encode; D must be 3 and the embeddings binary32. */
+int nest_grid_encode_backward(const float *inputs, int64_t B, int32_t D, const void *embeddings, int64_t emb_rows,
+                              int32_t emb_dtype, const int32_t *offsets_host, int32_t L, int32_t C, float S, int32_t H,
+                              int32_t gridtype, int32_t align_corners, int32_t interpolation, const float *grad,
+                              float *grad_embeddings, float *grad_inputs, void *stream);
 
 /* View-direction MLP decode: INGP.rgb_decode/get_color (HE:587-602) with the
  * SphericalHarmonics degree-4 view encoding of (d+1)/2 (HE:551-558, :727-730)

@@ -23,7 +23,8 @@ BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "nest_splat", "libnest_splat.so")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 
-SOURCES = ["abi.cpp", "preprocess.hip", "binning.hip", "render.hip", "grid_encode.hip", "mlp.hip", "rvq.hip"]
+SOURCES = ["abi.cpp", "preprocess.hip", "binning.hip", "render.hip", "backward.hip", "grid_encode.hip", "mlp.hip",
+           "rvq.hip"]
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 ARCH = os.environ.get("NEST_OFFLOAD_ARCH", "gfx950")

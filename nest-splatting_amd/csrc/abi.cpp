@@ -179,6 +179,75 @@ int check_splats(const nest_splats* sp, bool need_geometry) {
 // colours (CR/forward.cu:417-424).
 bool sh_colours(const nest_splats* sp) { return sp->shs && !sp->colors_precomp; }
 
+// Validates the hash-grid settings (or, for levels == 0, the colour inputs)
+// for a render with `channels` output channels and fills g (shared by the
+// forward render and its backward).
+int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const nest_splats* sp, int channels,
+               GridParams& g) {
+  int rc = NEST_OK;
+  if (gr->levels > 0) {
+    if (gr->level_dim != 1 && gr->level_dim != 2 && gr->level_dim != 4 && gr->level_dim != 8)
+      return fail(NEST_ERR_UNSUPPORTED, "level_dim must be 1, 2, 4 or 8 (got %u)", gr->level_dim);
+    if (gr->levels > NEST_MAX_LEVELS || gr->levels * gr->level_dim > NEST_MAX_CHANNELS)
+      return fail(NEST_ERR_UNSUPPORTED, "levels*level_dim must be <= %d (got %u*%u)", NEST_MAX_CHANNELS, gr->levels,
+                  gr->level_dim);
+    if ((uint32_t)channels < gr->levels * gr->level_dim)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "out_color has %d channels, the hash grid produces %u", channels,
+                  gr->levels * gr->level_dim);
+    if (gr->table_dtype != NEST_DTYPE_F32 && gr->table_dtype != NEST_DTYPE_F16)
+      return fail(NEST_ERR_UNSUPPORTED, "hash table dtype must be float32 or float16");
+    if (gr->interpolation != 0 && gr->interpolation != 1)
+      return fail(NEST_ERR_UNSUPPORTED, "interpolation must be 0 (linear) or 1 (smoothstep)");
+    if (!gr->table) return fail(NEST_ERR_INVALID_ARGUMENT, "hash table pointer is NULL");
+    if (gr->offsets[gr->levels] > gr->table_rows)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "hash table has %lld rows, offsets[%u] = %d", (long long)gr->table_rows,
+                  gr->levels, gr->offsets[gr->levels]);
+    if (!(gr->gridrange[1] > gr->gridrange[0])) return fail(NEST_ERR_INVALID_ARGUMENT, "gridrange must satisfy min < max");
+    if (sp->P > 0 && !sp->homotrans) return fail(NEST_ERR_INVALID_ARGUMENT, "homotrans is required on the hash path");
+    if ((rc = build_levels(gr->offsets, gr->levels, gr->log2_scale, gr->base_resolution, gr->align_corners != 0, 3, true,
+                           g.lv)))
+      return rc;
+    g.L = gr->levels;
+    g.F = gr->level_dim;
+    g.interp = (uint32_t)gr->interpolation;
+    g.contract = rs->if_contract ? 1u : 0u;
+    g.vmin = gr->gridrange[0];
+    g.vmax = gr->gridrange[1];
+    if (!g.contract) {
+      g.inv_size = 1.0f / (g.vmax - g.vmin);
+      g.vmid = 0.0f;
+    } else {
+      g.vmid = (g.vmax + g.vmin) * 0.5f;
+      g.inv_size = 1.0f / ((g.vmax - g.vmin) * 0.5f);
+    }
+    g.pos_offset = gr->align_corners ? 0.0f : 0.5f;
+    g.half = gr->table_dtype == NEST_DTYPE_F16 ? 1u : 0u;
+    g.table = gr->table;
+    const uint64_t tbytes = (uint64_t)gr->table_rows * gr->level_dim * (g.half ? 2u : 4u);
+    if (tbytes >= (1ull << 32))
+      return fail(NEST_ERR_UNSUPPORTED, "hash table of %llu bytes: at most 4 GiB (32-bit buffer offsets)",
+                  (unsigned long long)tbytes);
+    g.table_bytes = (uint32_t)tbytes;
+    g.table_rows = (uint32_t)gr->table_rows;
+    // structured grid: a prefix of dense levels without modulo, then hashed
+    // levels with power-of-two sizes (flag bits: 1 hashed, 2 pow2, 4 nomod),
+    // trilinear interpolation
+    uint32_t nd = 0;
+    while (nd < g.L && (g.lv.flags[nd] & 5u) == 4u) nd++;
+    bool structured = g.interp == 0;
+    for (uint32_t l = nd; l < g.L; l++) structured = structured && (g.lv.flags[l] & 3u) == 3u;
+    g.structured = structured ? 1u : 0u;
+    g.n_dense = nd;
+  } else {
+    if (sp->P > 0 && !sp->colors_precomp && !sp->shs)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "levels == 0 selects the colour path, which needs colors_precomp or shs");
+    // SH colours are RGB (NUM_CHANNELS, CR/rasterizer_impl.cu:320-323)
+    if (sh_colours(sp) && channels != 3)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "colours from SH have 3 channels, out_color has %d", channels);
+  }
+  return NEST_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -341,67 +410,7 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   rp.level = (int)gr->levels;
   rp.beta = rs->beta;
   rp.max_intersections = rs->max_intersections;
-  if (gr->levels > 0) {
-    if (gr->level_dim != 1 && gr->level_dim != 2 && gr->level_dim != 4 && gr->level_dim != 8)
-      return fail(NEST_ERR_UNSUPPORTED, "level_dim must be 1, 2, 4 or 8 (got %u)", gr->level_dim);
-    if (gr->levels > NEST_MAX_LEVELS || gr->levels * gr->level_dim > NEST_MAX_CHANNELS)
-      return fail(NEST_ERR_UNSUPPORTED, "levels*level_dim must be <= %d (got %u*%u)", NEST_MAX_CHANNELS, gr->levels,
-                  gr->level_dim);
-    if ((uint32_t)out->channels < gr->levels * gr->level_dim)
-      return fail(NEST_ERR_INVALID_ARGUMENT, "out_color has %d channels, the hash grid produces %u", out->channels,
-                  gr->levels * gr->level_dim);
-    if (gr->table_dtype != NEST_DTYPE_F32 && gr->table_dtype != NEST_DTYPE_F16)
-      return fail(NEST_ERR_UNSUPPORTED, "hash table dtype must be float32 or float16");
-    if (gr->interpolation != 0 && gr->interpolation != 1)
-      return fail(NEST_ERR_UNSUPPORTED, "interpolation must be 0 (linear) or 1 (smoothstep)");
-    if (!gr->table) return fail(NEST_ERR_INVALID_ARGUMENT, "hash table pointer is NULL");
-    if (gr->offsets[gr->levels] > gr->table_rows)
-      return fail(NEST_ERR_INVALID_ARGUMENT, "hash table has %lld rows, offsets[%u] = %d", (long long)gr->table_rows,
-                  gr->levels, gr->offsets[gr->levels]);
-    if (!(gr->gridrange[1] > gr->gridrange[0])) return fail(NEST_ERR_INVALID_ARGUMENT, "gridrange must satisfy min < max");
-    if (sp->P > 0 && !sp->homotrans) return fail(NEST_ERR_INVALID_ARGUMENT, "homotrans is required on the hash path");
-    if ((rc = build_levels(gr->offsets, gr->levels, gr->log2_scale, gr->base_resolution, gr->align_corners != 0, 3, true,
-                           rp.grid.lv)))
-      return rc;
-    GridParams& g = rp.grid;
-    g.L = gr->levels;
-    g.F = gr->level_dim;
-    g.interp = (uint32_t)gr->interpolation;
-    g.contract = rs->if_contract ? 1u : 0u;
-    g.vmin = gr->gridrange[0];
-    g.vmax = gr->gridrange[1];
-    if (!g.contract) {
-      g.inv_size = 1.0f / (g.vmax - g.vmin);
-      g.vmid = 0.0f;
-    } else {
-      g.vmid = (g.vmax + g.vmin) * 0.5f;
-      g.inv_size = 1.0f / ((g.vmax - g.vmin) * 0.5f);
-    }
-    g.pos_offset = gr->align_corners ? 0.0f : 0.5f;
-    g.half = gr->table_dtype == NEST_DTYPE_F16 ? 1u : 0u;
-    g.table = gr->table;
-    const uint64_t tbytes = (uint64_t)gr->table_rows * gr->level_dim * (g.half ? 2u : 4u);
-    if (tbytes >= (1ull << 32))
-      return fail(NEST_ERR_UNSUPPORTED, "hash table of %llu bytes: at most 4 GiB (32-bit buffer offsets)",
-                  (unsigned long long)tbytes);
-    g.table_bytes = (uint32_t)tbytes;
-    g.table_rows = (uint32_t)gr->table_rows;
-    // structured grid: a prefix of dense levels without modulo, then hashed
-    // levels with power-of-two sizes (flag bits: 1 hashed, 2 pow2, 4 nomod),
-    // trilinear interpolation
-    uint32_t nd = 0;
-    while (nd < g.L && (g.lv.flags[nd] & 5u) == 4u) nd++;
-    bool structured = g.interp == 0;
-    for (uint32_t l = nd; l < g.L; l++) structured = structured && (g.lv.flags[l] & 3u) == 3u;
-    g.structured = structured ? 1u : 0u;
-    g.n_dense = nd;
-  } else {
-    if (sp->P > 0 && !sp->colors_precomp && !sp->shs)
-      return fail(NEST_ERR_INVALID_ARGUMENT, "levels == 0 selects the colour path, which needs colors_precomp or shs");
-    // SH colours are RGB (NUM_CHANNELS, CR/rasterizer_impl.cu:320-323)
-    if (sh_colours(sp) && out->channels != 3)
-      return fail(NEST_ERR_INVALID_ARGUMENT, "colours from SH have 3 channels, out_color has %d", out->channels);
-  }
+  if ((rc = setup_grid(rs, gr, sp, out->channels, rp.grid))) return rc;
 
   size_t go[NEST_GEOM_FIELDS], gneed = 0, bo[NEST_BIN_FIELDS], bneed = 0, io[NEST_IMG_FIELDS], ineed = 0;
   nest_geom_layout(sp->P, go, &gneed);
@@ -567,6 +576,194 @@ int nest_grid_encode(const float* inputs, int64_t B, int32_t D, const void* embe
   p.outputs = outputs;
   hipError_t e = launch_grid_encode(p, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? NEST_OK : hip_fail(e, "grid_encode");
+}
+
+int nest_grid_encode_backward(const float* inputs, int64_t B, int32_t D, const void* embeddings, int64_t emb_rows,
+                              int32_t emb_dtype, const int32_t* offsets_host, int32_t L, int32_t C, float S, int32_t H,
+                              int32_t gridtype, int32_t align_corners, int32_t interpolation, const float* grad,
+                              float* grad_embeddings, float* grad_inputs, void* stream) {
+  if (B < 0 || emb_rows < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "B and emb_rows must be >= 0");
+  if (D != 3) return fail(NEST_ERR_UNSUPPORTED, "GridEncoding backward: D must be 3 (got %d)", D);
+  if (C != 1 && C != 2 && C != 4 && C != 8)
+    return fail(NEST_ERR_UNSUPPORTED, "GridEncoding backward: C must be 1, 2, 4 or 8 (got %d)", C);
+  if (L < 1 || L > NEST_MAX_LEVELS) return fail(NEST_ERR_UNSUPPORTED, "GridEncoding: L must be in [1, %d]", NEST_MAX_LEVELS);
+  if (emb_dtype != NEST_DTYPE_F32) return fail(NEST_ERR_UNSUPPORTED, "GridEncoding backward: embeddings must be float32");
+  if (gridtype != 0 && gridtype != 1) return fail(NEST_ERR_INVALID_ARGUMENT, "gridtype must be 0 (hash) or 1 (tiled)");
+  if (interpolation != 0 && interpolation != 1) return fail(NEST_ERR_INVALID_ARGUMENT, "interpolation must be 0 or 1");
+  if (!offsets_host) return fail(NEST_ERR_INVALID_ARGUMENT, "offsets is NULL");
+  if (offsets_host[L] > emb_rows)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "embeddings have %lld rows, offsets[%d] = %d", (long long)emb_rows, L, offsets_host[L]);
+  if (emb_rows > 0xffffffffll / C) return fail(NEST_ERR_UNSUPPORTED, "embedding table too large");
+  if (!grad_embeddings || (B > 0 && (!inputs || !embeddings || !grad)))
+    return fail(NEST_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  GridEncodeBwdParams p{};
+  int rc = build_levels(offsets_host, (uint32_t)L, S, (uint32_t)H, align_corners != 0, 3, gridtype == 0, p.lv);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_fill_u32(reinterpret_cast<uint32_t*>(grad_embeddings), 0u, emb_rows * C, s);
+  if (e != hipSuccess) return hip_fail(e, "grid_encode_backward fill");
+  if (B == 0) return NEST_OK;
+  p.inputs = inputs;
+  p.B = B;
+  p.F = C;
+  p.L = L;
+  p.align_corners = align_corners;
+  p.interp = interpolation;
+  p.table = static_cast<const float*>(embeddings);
+  p.table_rows = (uint32_t)emb_rows;
+  p.grad = grad;
+  p.grad_table = grad_embeddings;
+  p.grad_inputs = grad_inputs;
+  e = launch_grid_encode_backward(p, s);
+  return e == hipSuccess ? NEST_OK : hip_fail(e, "grid_encode_backward");
+}
+
+int nest_backward_layout(int32_t P, int32_t channels, size_t offsets[NEST_BWD_FIELDS], size_t* total) {
+  if (P < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "P must be >= 0");
+  if (channels < 1 || channels > NEST_MAX_CHANNELS)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "channels must be in [1, %d]", NEST_MAX_CHANNELS);
+  const size_t n = (size_t)(P > 0 ? P : 1);
+  Carver c;
+  size_t o[NEST_BWD_FIELDS];
+  o[NEST_BWD_DTRANSMAT] = c.take(n * 9 * 4);
+  o[NEST_BWD_DHOMO] = c.take(n * 9 * 4);
+  o[NEST_BWD_DNORMAL] = c.take(n * 3 * 4);
+  o[NEST_BWD_DCOLORS] = c.take(n * (size_t)channels * 4);
+  o[NEST_BWD_GRADSUM] = c.take(n * 4);
+  if (offsets)
+    for (int i = 0; i < NEST_BWD_FIELDS; i++) offsets[i] = o[i];
+  if (total) *total = c.off;
+  return NEST_OK;
+}
+
+int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const nest_splats* sp, const void* geom_ws,
+                  size_t geom_bytes, const void* binning_ws, size_t binning_bytes, const void* image_ws,
+                  size_t image_bytes, int64_t NR, const nest_backward_io* io, void* bwd_ws, size_t bwd_bytes,
+                  void* stream) {
+  int rc = check_settings(rs);
+  if (rc) return rc;
+  if ((rc = check_splats(sp, true))) return rc;
+  if (!gr || gr->struct_size != sizeof(nest_hashgrid))
+    return fail(NEST_ERR_INVALID_ARGUMENT, "nest_hashgrid missing or struct_size mismatch");
+  if (!io || io->struct_size != sizeof(nest_backward_io))
+    return fail(NEST_ERR_INVALID_ARGUMENT, "nest_backward_io missing or struct_size mismatch");
+  const int C = io->channels;
+  if (C < 1 || C > 64) return fail(NEST_ERR_UNSUPPORTED, "backward: channels must be in [1, 64] (got %d)", C);
+  if (!io->dL_dout_color || !io->dL_dout_others)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dout_color and dL_dout_others are required");
+  if (!io->dL_dmeans3D || !io->dL_dmeans2D || !io->dL_dopacity || !io->dL_dscales || !io->dL_drotations)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dmeans3D, dL_dmeans2D, dL_dopacity, dL_dscales and "
+                                           "dL_drotations are required");
+  if (NR < 0 || NR > 0xffffffffll) return fail(NEST_ERR_INVALID_ARGUMENT, "num_rendered out of range");
+  GridParams g{};
+  if ((rc = setup_grid(rs, gr, sp, C, g))) return rc;
+  const bool hash = gr->levels > 0;
+  const bool from_sh = !hash && sh_colours(sp);
+  if (hash && g.half) return fail(NEST_ERR_UNSUPPORTED, "backward: the hash table must be float32");
+  if (hash && !io->dL_dfeatures) return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dfeatures is required");
+  if (from_sh && !io->dL_dshs) return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dshs is required with SH colours");
+
+  const int W = rs->image_width, H = rs->image_height, P = sp->P;
+  const uint32_t gx = (uint32_t)((W + kTile - 1) / kTile), gy = (uint32_t)((H + kTile - 1) / kTile);
+  size_t go[NEST_GEOM_FIELDS], gneed = 0, bo[NEST_BIN_FIELDS], bneed = 0, io_[NEST_IMG_FIELDS], ineed = 0;
+  size_t wo[NEST_BWD_FIELDS], wneed = 0;
+  nest_geom_layout(P, go, &gneed);
+  nest_binning_layout(NR, bo, &bneed);
+  nest_image_layout(W, H, io_, &ineed);
+  nest_backward_layout(P, C, wo, &wneed);
+  if (!geom_ws || geom_bytes < gneed)
+    return fail(NEST_ERR_WORKSPACE, "geometry workspace too small: %zu bytes given, %zu needed", geom_bytes, gneed);
+  if (NR > 0 && (!binning_ws || binning_bytes < bneed))
+    return fail(NEST_ERR_WORKSPACE, "binning workspace too small: %zu bytes given, %zu needed", binning_bytes, bneed);
+  if (!image_ws || image_bytes < ineed)
+    return fail(NEST_ERR_WORKSPACE, "image workspace too small: %zu bytes given, %zu needed", image_bytes, ineed);
+  if (!bwd_ws || bwd_bytes < wneed)
+    return fail(NEST_ERR_WORKSPACE, "backward workspace too small: %zu bytes given, %zu needed", bwd_bytes, wneed);
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const char* gw = static_cast<const char*>(geom_ws);
+  const char* im = static_cast<const char*>(image_ws);
+  char* bw = static_cast<char*>(bwd_ws);
+  float* dtransmat = reinterpret_cast<float*>(bw + wo[NEST_BWD_DTRANSMAT]);
+  float* dhomo = reinterpret_cast<float*>(bw + wo[NEST_BWD_DHOMO]);
+  float* dnormal = reinterpret_cast<float*>(bw + wo[NEST_BWD_DNORMAL]);
+  float* dcolors = io->dL_dcolors ? io->dL_dcolors : reinterpret_cast<float*>(bw + wo[NEST_BWD_DCOLORS]);
+  float* gradsum = io->dL_dgradsum ? io->dL_dgradsum : reinterpret_cast<float*>(bw + wo[NEST_BWD_GRADSUM]);
+  const int M = from_sh ? sp->sh_coeffs : 0;
+  // zero every gradient output and the accumulators
+  struct Fill {
+    float* p;
+    int64_t n;
+  } fills[] = {{dtransmat, (int64_t)P * 9}, {dhomo, (int64_t)P * 9}, {dnormal, (int64_t)P * 3},
+               {dcolors, (int64_t)P * C}, {gradsum, (int64_t)P}, {io->dL_dmeans3D, (int64_t)P * 3},
+               {io->dL_dmeans2D, (int64_t)P * 3}, {io->dL_dopacity, (int64_t)P}, {io->dL_dscales, (int64_t)P * 2},
+               {io->dL_drotations, (int64_t)P * 4}, {from_sh ? io->dL_dshs : nullptr, (int64_t)P * M * 3},
+               {hash ? io->dL_dfeatures : nullptr, hash ? (int64_t)gr->table_rows * gr->level_dim : 0}};
+  for (const Fill& f : fills) {
+    if (!f.p || f.n == 0) continue;
+    hipError_t e = launch_fill_u32(reinterpret_cast<uint32_t*>(f.p), 0u, f.n, s);
+    if (e != hipSuccess) return hip_fail(e, "backward fill");
+  }
+  if (P == 0) return NEST_OK;
+
+  RenderBwdParams rp{};
+  rp.W = W;
+  rp.H = H;
+  rp.gx = gx;
+  rp.gy = gy;
+  rp.ntiles = gx * gy;
+  rp.C = C;
+  rp.level = (int)gr->levels;
+  rp.beta = rs->beta;
+  rp.ranges = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_RANGES]);
+  rp.point_list = NR > 0 ? reinterpret_cast<const uint32_t*>(static_cast<const char*>(binning_ws) + bo[NEST_BIN_VALS])
+                         : nullptr;
+  rp.records = reinterpret_cast<const float*>(gw + go[NEST_GEOM_RECORDS]);
+  rp.colors = from_sh ? reinterpret_cast<const float*>(gw + go[NEST_GEOM_RGB]) : sp->colors_precomp;
+  rp.final_T = reinterpret_cast<const float*>(im + io_[NEST_IMG_FINAL_T]);
+  rp.n_contrib = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_N_CONTRIB]);
+  rp.dL_dpix = io->dL_dout_color;
+  rp.dL_dothers = io->dL_dout_others;
+  rp.dtable = hash ? io->dL_dfeatures : nullptr;
+  rp.dtransmat = dtransmat;
+  rp.dhomo = dhomo;
+  rp.dmean2D = io->dL_dmeans2D;
+  rp.dnormal = dnormal;
+  rp.dopacity = io->dL_dopacity;
+  rp.dcolors = dcolors;
+  rp.gradsum = gradsum;
+  rp.grid = g;
+  if (NR > 0) {
+    hipError_t e = launch_render_backward(rp, s);
+    if ((rc = check_stage(e, "render backward", rs->debug, s))) return rc;
+  }
+
+  PreprocessBwdParams pp{};
+  pp.P = P;
+  pp.W = W;
+  pp.H = H;
+  memcpy(pp.view, rs->viewmatrix, sizeof(pp.view));
+  memcpy(pp.proj, rs->projmatrix, sizeof(pp.proj));
+  memcpy(pp.campos, rs->campos, sizeof(pp.campos));
+  pp.means = sp->means3D;
+  pp.scales = sp->scales;
+  pp.rots = sp->rotations;
+  pp.radii = reinterpret_cast<const int32_t*>(gw + go[NEST_GEOM_RADII]);
+  pp.records = reinterpret_cast<const float*>(gw + go[NEST_GEOM_RECORDS]);
+  pp.shs = from_sh ? sp->shs : nullptr;
+  pp.sh_degree = sp->sh_degree;
+  pp.sh_coeffs = M;
+  pp.clamped = reinterpret_cast<const uint8_t*>(gw + go[NEST_GEOM_CLAMPED]);
+  pp.dcolors = dcolors;
+  pp.dtransmat = dtransmat;
+  pp.dhomo = dhomo;
+  pp.dnormal = dnormal;
+  pp.dmean2D = io->dL_dmeans2D;
+  pp.dmeans = io->dL_dmeans3D;
+  pp.dscales = io->dL_dscales;
+  pp.drots = io->dL_drotations;
+  pp.dshs = from_sh ? io->dL_dshs : nullptr;
+  return check_stage(launch_preprocess_backward(pp, s), "preprocess backward", rs->debug, s);
 }
 
 int nest_mlp_decode(const nest_mlp* mlp, const float* feat, int64_t feat_cs, int64_t feat_ns, int64_t N, int32_t width,

@@ -1,0 +1,715 @@
+// Backward pass (training) of the render, mode 0 with the Gaussian kernel,
+// of preprocess, and of the standalone GridEncoder.
+//
+// Semantics: renderCUDAsurfelBackward of
+// submodules/diff-surfel-rasterization/cuda_rasterizer/backward.cu:445-2049
+// (mode 0, kernel_type 0), query_feature<true> (hashgrid.h:53-299),
+// compute_transmat_aabb / preprocessCUDA / computeColorFromSH backward
+// (backward.cu:20-140, :2056-2274), kernel_grid_backward and
+// kernel_input_backward with the forward's dy_dx (gridencoder/src/
+// gridencoder.cu:196-366).
+//
+// Layout of the render backward: one 256-thread workgroup per 16x16 tile, one
+// lane per pixel, the tile's splats walked back to front in LDS-staged
+// batches of the forward's packed records.  Two restructurings against the
+// reference, both the same sums in another order:
+//  - the reference keeps three C-long arrays per pixel (accum_rec,
+//    last_color, dL_dpixel).  The back-to-front blend accum_rec =
+//    a*last + (1-a)*accum_rec is linear with the same coefficients for every
+//    channel, and only its dot product with dL_dpixel enters dL/dalpha, so a
+//    pixel carries two scalars (the blend's and the last colour's dot
+//    products with dL_dpixel) and reads its dL_dpixel values from memory
+//    where a level needs them (cache-resident, coalesced across the wave);
+//    the |grad| sum of a hit is w * sum |dL_dpixel|, summed once per pixel;
+//  - every lane of a wave visits the same staged splat at the same time, so
+//    the per-splat gradients (transmat, homotrans, mean2D, normal, opacity,
+//    |grad| sum, colours) are summed over the wave with cross-lane shuffles
+//    and added with one atomic per wave instead of one per pixel.
+// Table gradients are hardware float atomics (global_atomic_add_f32) at
+// every corner, as in the reference.
+#include <hip/hip_fp16.h>
+
+#include "hashgrid.h"
+#include "nest_internal.h"
+#include "nest_math.h"
+
+namespace nest {
+
+namespace {
+
+constexpr int kBwdThreads = 256;
+constexpr int kBwdChunks = 7;  // record chunks 0-6: T, xy, opacity, normal, ap, homotrans columns
+
+__device__ __forceinline__ uint32_t bwd_xcd_tile(uint32_t i, uint32_t n) {
+  const uint32_t q = n >> 3, rem = n & 7u;
+  const uint32_t x = i & 7u, k = i >> 3;
+  const uint32_t start = x < rem ? x * (q + 1u) : rem * (q + 1u) + (x - rem) * q;
+  return start + k;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ void atomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
+
+// query_feature<true>: for the hit at xyz with per-channel gradient
+// gf(ch) = w * dpix[ch], adds w_corner * gf to the table at every corner of
+// every queried level, and returns dot = sum_ch feat[ch] * dpix[ch] (the
+// recomputed feature's projection on dL/dpixel) and dL/dxyz (hashgrid.h:
+// 213-299, grad_scale of :66-97).
+template <int F>
+__device__ __forceinline__ void hash_backward(const GridParams& g, nest_i32x4 rsrc, const float xyz[3], uint32_t maxl,
+                                              float w, const float* dpix, size_t HW, float* dtable, float& dot,
+                                              float dxyz[3]) {
+  dot = 0.0f;
+  dxyz[0] = dxyz[1] = dxyz[2] = 0.0f;
+  float u[3];
+  float grad_scale;
+  if (!g.contract) {
+#pragma unroll
+    for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmin) * g.inv_size;
+    if (u[0] < 0 || u[0] > 1 || u[1] < 0 || u[1] > 1 || u[2] < 0 || u[2] > 1) return;
+    grad_scale = g.inv_size;
+  } else {
+#pragma unroll
+    for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmid) * g.inv_size;
+    const float nrm = sqrtf(u[0] * u[0] + u[1] * u[1] + u[2] * u[2]);
+    const float inv_nrm = 1.0f / nrm;
+    const float st = (nrm <= 1.0f) ? 1.0f : (2.0f - inv_nrm) * inv_nrm;
+#pragma unroll
+    for (int d = 0; d < 3; d++) {
+      u[d] = st * u[d];
+      u[d] = (u[d] + 2.0f) * 0.25f;
+    }
+    grad_scale = g.inv_size * st * 0.25f;
+  }
+  const LevelTable& lv = g.lv;
+  for (int l = 0; l < (int)maxl; l++) {
+    const float scale = lv.scale[l];
+    float pos[3], der[3];
+    uint32_t gc[3];
+#pragma unroll
+    for (int d = 0; d < 3; d++) {
+      const float x = u[d] * scale + g.pos_offset;
+      gc[d] = f2u_sat(x);
+      pos[d] = x - (float)gc[d];
+      if (g.interp == 1) {
+        der[d] = 6.0f * pos[d] * (1.0f - pos[d]);
+        pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
+      } else {
+        der[d] = 1.0f;
+      }
+    }
+    LevelCorners cn;
+    level_corners<F, false>(lv, l, g.pos_offset, 0u, u, cn);  // indices of the same cell
+    // weights of the (possibly smoothstepped) fractions, corner order
+    cn.wx[0] = 1 - pos[0]; cn.wx[1] = pos[0];
+    cn.wy[0] = 1 - pos[1]; cn.wy[1] = pos[1];
+    cn.wz[0] = 1 - pos[2]; cn.wz[1] = pos[2];
+    float vals[8][F];
+    corners_load<F, false>(rsrc, cn, vals);
+    float dp[F], gf[F];
+#pragma unroll
+    for (int f = 0; f < F; f++) {
+      dp[f] = dpix[(size_t)(l * F + f) * HW];
+      gf[f] = w * dp[f];
+    }
+    float feat[F];
+#pragma unroll
+    for (int f = 0; f < F; f++) feat[f] = 0.0f;
+    float* dl = dtable + (size_t)lv.base[l] * F;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const float wk = (1.0f * cn.wx[k & 1]) * cn.wy[(k >> 1) & 1] * cn.wz[k >> 2];
+#pragma unroll
+      for (int f = 0; f < F; f++) {
+        feat[f] = fmaf(wk, vals[k][f], feat[f]);
+        atomic_add(dl + (size_t)cn.idx[k] * F + f, wk * gf[f]);
+      }
+    }
+#pragma unroll
+    for (int f = 0; f < F; f++) dot += feat[f] * dp[f];
+    // dy/dxyz: corner pairs along each axis (hashgrid.h:241-276)
+#pragma unroll
+    for (int gd = 0; gd < 3; gd++) {
+      float rg[F];
+#pragma unroll
+      for (int f = 0; f < F; f++) rg[f] = 0.0f;
+#pragma unroll
+      for (int idx = 0; idx < 4; idx++) {
+        float wgt = scale * grad_scale;
+        int kl = 0;
+#pragma unroll
+        for (int nd = 0; nd < 2; nd++) {
+          const int d = (nd >= gd) ? nd + 1 : nd;
+          const int bit = (idx >> nd) & 1;
+          wgt *= bit ? pos[d] : 1 - pos[d];
+          kl |= bit << d;
+        }
+        const int kr = kl | (1 << gd);
+#pragma unroll
+        for (int f = 0; f < F; f++) rg[f] += wgt * (vals[kr][f] - vals[kl][f]) * der[gd];
+      }
+#pragma unroll
+      for (int f = 0; f < F; f++) dxyz[gd] += gf[f] * rg[f];
+    }
+  }
+}
+
+template <int F, bool kHash>
+__global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const RenderBwdParams p) {
+  __shared__ float4 srec[kBwdChunks][kBwdThreads];
+  __shared__ uint32_t sid[kBwdThreads];
+
+  const uint32_t tile = bwd_xcd_tile(blockIdx.x, p.ntiles);
+  const uint32_t tx = tile % p.gx, ty = tile / p.gx;
+  const uint32_t px = tx * kTile + (threadIdx.x & 15u);
+  const uint32_t py = ty * kTile + (threadIdx.x >> 4);
+  const bool inside = px < (uint32_t)p.W && py < (uint32_t)p.H;
+  const float pxf = (float)px, pyf = (float)py;
+  const size_t HW = (size_t)p.W * p.H;
+  const size_t pid = inside ? (size_t)py * p.W + px : 0;
+  const uint2 range = reinterpret_cast<const uint2*>(p.ranges)[tile];
+  const int C = p.C;
+
+  const float* dpix = p.dL_dpix + pid;  // channel c at dpix[c * HW]
+  float sum_abs = 0.0f;
+  if (inside)
+    for (int c = 0; c < C; c++) sum_abs += fabsf(dpix[(size_t)c * HW]);
+  const float* dO = p.dL_dothers;
+  const float dL_ddepth = inside ? dO[pid] : 0.0f;
+  const float dL_daccum = inside ? dO[HW + pid] : 0.0f;
+  const float dn2[3] = {inside ? dO[2 * HW + pid] : 0.0f, inside ? dO[3 * HW + pid] : 0.0f,
+                        inside ? dO[4 * HW + pid] : 0.0f};
+  const float dL_dmedian = inside ? dO[5 * HW + pid] : 0.0f;
+  const float dL_dreg = inside ? dO[6 * HW + pid] : 0.0f;
+
+  const float T_final = inside ? p.final_T[pid] : 0.0f;
+  float T = T_final;
+  const uint32_t last_contributor = inside ? p.n_contrib[pid] : 0u;
+  const int median_contributor = inside ? (int)p.n_contrib[pid + HW] : 0;
+  const float final_D = inside ? p.final_T[pid + HW] : 0.0f;
+  const float final_D2 = inside ? p.final_T[pid + 2 * HW] : 0.0f;
+  const float final_A = 1 - T_final;
+
+  float acc_dot = 0.0f, last_dot = 0.0f;  // accum_rec . dpix, last_color . dpix
+  float last_depth = 0.0f, last_normal[3] = {0.0f, 0.0f, 0.0f};
+  float accum_depth_rec = 0.0f, accum_alpha_rec = 0.0f, accum_normal_rec[3] = {0.0f, 0.0f, 0.0f};
+  float last_dL_dT = 0.0f, last_alpha = 0.0f;
+
+  const GridParams& g = p.grid;
+  nest_i32x4 rsrc{};
+  if constexpr (kHash) rsrc = table_rsrc_rows<F, false>(g.table, g.table_rows);
+
+  uint32_t contributor = range.y - range.x;
+  const uint32_t total = range.y - range.x;
+  for (uint32_t done_n = 0; done_n < total; done_n += kBwdThreads) {
+    const uint32_t n = min((uint32_t)kBwdThreads, total - done_n);
+    __syncthreads();
+    if (threadIdx.x < n) {
+      const uint32_t e = range.y - 1u - done_n - threadIdx.x;
+      const uint32_t id = p.point_list[e];
+      const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id;
+#pragma unroll
+      for (int c = 0; c < kBwdChunks; c++)
+        if (kHash || c < 4) srec[c][threadIdx.x] = rec[c];
+      sid[threadIdx.x] = id;
+    }
+    __syncthreads();
+    for (uint32_t j = 0; j < n; j++) {
+      contributor--;
+      const float4 q0 = srec[0][j], q1 = srec[1][j], q2 = srec[2][j], q3 = srec[3][j];
+      const uint32_t id = sid[j];
+      const float Tu[3] = {q0.x, q0.y, q0.z}, Tv[3] = {q0.w, q1.x, q1.y}, Tw[3] = {q1.z, q1.w, q2.x};
+      const float k[3] = {pxf * Tw[0] - Tu[0], pxf * Tw[1] - Tu[1], pxf * Tw[2] - Tu[2]};
+      const float l[3] = {pyf * Tw[0] - Tv[0], pyf * Tw[1] - Tv[1], pyf * Tw[2] - Tv[2]};
+      const float pp[3] = {k[1] * l[2] - k[2] * l[1], k[2] * l[0] - k[0] * l[2], k[0] * l[1] - k[1] * l[0]};
+      bool act = inside && contributor < last_contributor && pp[2] != 0.0f;
+      float s[2] = {0.0f, 0.0f}, rho3d = 0.0f, rho2d = 0.0f, d[2] = {0.0f, 0.0f}, c_d = 0.0f;
+      float G = 0.0f, demon = 1.0f, alpha = 0.0f;
+      bool use3d = false;
+      if (act) {
+        s[0] = pp[0] / pp[2];
+        s[1] = pp[1] / pp[2];
+        rho3d = s[0] * s[0] + s[1] * s[1];
+        d[0] = q2.y - pxf;
+        d[1] = q2.z - pyf;
+        rho2d = 2.0f * (d[0] * d[0] + d[1] * d[1]);
+        const float rho = fminf(rho3d, rho2d);
+        use3d = rho3d <= rho2d;
+        c_d = use3d ? (s[0] * Tw[0] + s[1] * Tw[1]) + Tw[2] : Tw[2];
+        const float power = -0.5f * rho;
+        act = c_d >= 0.2f && power <= 0.0f;
+        if (act) {
+          G = expf_ref(power);
+          if (p.beta > 0.0f) {
+            demon = (float)(1.0 + (double)(p.beta * G));
+            G = (float)((1.0 + (double)p.beta) * (double)G / (double)demon);
+          }
+          alpha = fminf(0.99f, q2.w * G);
+          act = alpha >= 1.0f / 255.0f;
+        }
+      }
+      // per-splat gradient contributions of this lane (zero when inactive)
+      float gT[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0}, gH[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+      float gM[2] = {0.0f, 0.0f}, gN[3] = {0.0f, 0.0f, 0.0f}, gO = 0.0f, gS = 0.0f;
+      float wcol = 0.0f;  // dchannel_dcolor of the colour path
+      if (act) {
+        T = T / (1.f - alpha);
+        const float wgt = alpha * T;
+        float dot;
+        float dxyz[3] = {0.0f, 0.0f, 0.0f};
+        if constexpr (!kHash) {
+          const float* col = p.colors + (size_t)id * C;
+          dot = 0.0f;
+          for (int ch = 0; ch < C; ch++) dot += col[ch] * dpix[(size_t)ch * HW];
+          wcol = wgt;
+        } else {
+          const float4 q4 = srec[4][j], q5 = srec[5][j], q6 = srec[6][j];
+          float xyz[3];
+          if (use3d) {
+            xyz[0] = s[0] * q4.x + s[1] * q4.w + q5.z;
+            xyz[1] = s[0] * q4.y + s[1] * q5.x + q5.w;
+            xyz[2] = s[0] * q4.z + s[1] * q5.y + q6.x;
+          } else {
+            xyz[0] = q5.z; xyz[1] = q5.w; xyz[2] = q6.x;
+          }
+          gS = wgt * sum_abs;
+          const uint32_t ap = __float_as_uint(q3.w);
+          const uint32_t maxl = ap < g.L ? ap : g.L;
+          hash_backward<F>(g, rsrc, xyz, maxl, wgt, dpix, HW, p.dtable, dot, dxyz);
+          if (use3d) {
+            gH[0] = dxyz[0] * s[0]; gH[1] = dxyz[1] * s[0]; gH[2] = dxyz[2] * s[0];
+            gH[3] = dxyz[0] * s[1]; gH[4] = dxyz[1] * s[1]; gH[5] = dxyz[2] * s[1];
+          }
+          gH[6] = dxyz[0]; gH[7] = dxyz[1]; gH[8] = dxyz[2];
+        }
+        // colour term of dL/dalpha (backward.cu:1799-1808 as dot products)
+        acc_dot = last_alpha * last_dot + (1.f - last_alpha) * acc_dot;
+        last_dot = dot;
+        float dL_dalpha = dot - acc_dot;
+        // RENDER_AXUTILITY terms (backward.cu:1815-1855)
+        float dL_dz = 0.0f;
+        const float m_d = 100.0f / (100.0f - 0.2f) * (1 - 0.2f / c_d);
+        const float dmd_dd = (100.0f * 0.2f) / ((100.0f - 0.2f) * c_d * c_d);
+        if ((int)contributor == median_contributor - 1) dL_dz += dL_dmedian;
+        const float dL_dweight = (final_D2 + m_d * m_d * final_A - 2 * m_d * final_D) * dL_dreg;
+        dL_dalpha += dL_dweight - last_dL_dT;
+        last_dL_dT = dL_dweight * alpha + (1 - alpha) * last_dL_dT;
+        const float dL_dmd = 2.0f * (T * alpha) * (m_d * final_A - final_D) * dL_dreg;
+        dL_dz += dL_dmd * dmd_dd;
+        accum_depth_rec = last_alpha * last_depth + (1.f - last_alpha) * accum_depth_rec;
+        last_depth = c_d;
+        dL_dalpha += (c_d - accum_depth_rec) * dL_ddepth;
+        accum_alpha_rec = last_alpha * 1.0f + (1.f - last_alpha) * accum_alpha_rec;
+        dL_dalpha += (1 - accum_alpha_rec) * dL_daccum;
+        const float nrm[3] = {q3.x, q3.y, q3.z};
+#pragma unroll
+        for (int ch = 0; ch < 3; ch++) {
+          accum_normal_rec[ch] = last_alpha * last_normal[ch] + (1.f - last_alpha) * accum_normal_rec[ch];
+          last_normal[ch] = nrm[ch];
+          dL_dalpha += (nrm[ch] - accum_normal_rec[ch]) * dn2[ch];
+          gN[ch] = alpha * T * dn2[ch];
+        }
+        dL_dalpha *= T;
+        last_alpha = alpha;
+        float dL_dG = q2.w * dL_dalpha;
+        if (p.beta > 0.0f) {
+          const float dG_dg = (float)((1.0 + (double)p.beta) / (double)(demon * demon));
+          dL_dG *= dG_dg;
+        }
+        dL_dz += alpha * T * dL_ddepth;
+        float dL_duv[2] = {0.0f, 0.0f};
+        if constexpr (kHash) {
+          if (use3d) {
+            const float4 q4 = srec[4][j], q5 = srec[5][j];
+            dL_duv[0] = dxyz[0] * q4.x + dxyz[1] * q4.y + dxyz[2] * q4.z;
+            dL_duv[1] = dxyz[0] * q4.w + dxyz[1] * q5.x + dxyz[2] * q5.y;
+          }
+        }
+        if (use3d) {
+          const float dG_factor = -G;
+          float dL_ds[2] = {dL_dG * dG_factor * s[0] + dL_dz * Tw[0], dL_dG * dG_factor * s[1] + dL_dz * Tw[1]};
+          dL_ds[0] += dL_duv[0];
+          dL_ds[1] += dL_duv[1];
+          const float dsx_pz = dL_ds[0] / pp[2], dsy_pz = dL_ds[1] / pp[2];
+          const float dp[3] = {dsx_pz, dsy_pz, -(dsx_pz * s[0] + dsy_pz * s[1])};
+          const float dk[3] = {l[1] * dp[2] - l[2] * dp[1], l[2] * dp[0] - l[0] * dp[2], l[0] * dp[1] - l[1] * dp[0]};
+          const float dl[3] = {dp[1] * k[2] - dp[2] * k[1], dp[2] * k[0] - dp[0] * k[2], dp[0] * k[1] - dp[1] * k[0]};
+          const float dz_dTw[3] = {s[0], s[1], 1.0f};
+#pragma unroll
+          for (int r = 0; r < 3; r++) {
+            gT[r] = -dk[r];
+            gT[3 + r] = -dl[r];
+            gT[6 + r] = pxf * dk[r] + pyf * dl[r] + dL_dz * dz_dTw[r];
+          }
+        } else {
+          const float dG_factor_2d = -G * 2.0f;
+          gM[0] = dL_dG * (dG_factor_2d * d[0]);
+          gM[1] = dL_dG * (dG_factor_2d * d[1]);
+          gT[8] = dL_dz;
+        }
+        gO = G * dL_dalpha;
+      }
+      // wave sums and one atomic per wave and splat
+      if (__ballot(act) != 0ull) {
+        const bool lead = (threadIdx.x & 63u) == 0u;
+#pragma unroll
+        for (int r = 0; r < 9; r++) {
+          const float v = wave_sum(gT[r]);
+          if (lead && v != 0.0f) atomic_add(p.dtransmat + 9 * (size_t)id + r, v);
+        }
+        if constexpr (kHash) {
+#pragma unroll
+          for (int r = 0; r < 9; r++) {
+            const float v = wave_sum(gH[r]);
+            if (lead && v != 0.0f) atomic_add(p.dhomo + 9 * (size_t)id + r, v);
+          }
+          const float vs = wave_sum(gS);
+          if (lead && vs != 0.0f) atomic_add(p.gradsum + id, vs);
+        } else {
+          for (int ch = 0; ch < C; ch++) {
+            const float v = wave_sum(inside ? wcol * dpix[(size_t)ch * HW] : 0.0f);
+            if (lead && v != 0.0f) atomic_add(p.dcolors + (size_t)id * C + ch, v);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+          const float v = wave_sum(gM[r]);
+          if (lead && v != 0.0f) atomic_add(p.dmean2D + 3 * (size_t)id + r, v);
+        }
+#pragma unroll
+        for (int r = 0; r < 3; r++) {
+          const float v = wave_sum(gN[r]);
+          if (lead && v != 0.0f) atomic_add(p.dnormal + 3 * (size_t)id + r, v);
+        }
+        const float vo = wave_sum(gO);
+        if (lead && vo != 0.0f) atomic_add(p.dopacity + id, vo);
+      }
+    }
+  }
+}
+
+template <int F, bool kHash>
+hipError_t launch_bwd_one(const RenderBwdParams& p, hipStream_t s) {
+  hipLaunchKernelGGL((render_backward_kernel<F, kHash>), dim3(p.ntiles), dim3(kBwdThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+// preprocessCUDA backward (backward.cu:2216-2274) with compute_transmat_aabb
+// (:2056-2214) and computeColorFromSH backward (:20-140).
+__global__ void __launch_bounds__(256) preprocess_backward_kernel(const PreprocessBwdParams p) {
+  const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (idx >= p.P || !(p.radii[idx] > 0)) return;
+  const float po[3] = {p.means[3 * (size_t)idx], p.means[3 * (size_t)idx + 1], p.means[3 * (size_t)idx + 2]};
+  const float* q = p.rots + 4 * (size_t)idx;
+  const float sq = 1.0f / sqrtf(q[3] * q[3] + q[0] * q[0] + q[1] * q[1] + q[2] * q[2]);
+  const float qw = q[0] * sq, qx = q[1] * sq, qy = q[2] * sq, qz = q[3] * sq;
+  float R[3][3];  // R[col][row]
+  R[0][0] = 1.f - 2.f * (qy * qy + qz * qz); R[0][1] = 2.f * (qx * qy + qw * qz); R[0][2] = 2.f * (qx * qz - qw * qy);
+  R[1][0] = 2.f * (qx * qy - qw * qz); R[1][1] = 1.f - 2.f * (qx * qx + qz * qz); R[1][2] = 2.f * (qy * qz + qw * qx);
+  R[2][0] = 2.f * (qx * qz + qw * qy); R[2][1] = 2.f * (qy * qz - qw * qx); R[2][2] = 1.f - 2.f * (qx * qx + qy * qy);
+  const float sc[2] = {p.scales[2 * (size_t)idx], p.scales[2 * (size_t)idx + 1]};
+  float Lc[3][3];
+#pragma unroll
+  for (int r = 0; r < 3; r++) {
+    Lc[0][r] = R[0][r] * (1.0f * sc[0]);
+    Lc[1][r] = R[1][r] * (1.0f * sc[1]);
+    Lc[2][r] = R[2][r];
+  }
+  const float M[3][4] = {{Lc[0][0], Lc[0][1], Lc[0][2], 0.0f}, {Lc[1][0], Lc[1][1], Lc[1][2], 0.0f},
+                         {po[0], po[1], po[2], 1.0f}};
+  const float N[3][4] = {{(float)p.W / 2.0f, 0.0f, 0.0f, (float)(p.W - 1) / 2.0f},
+                         {0.0f, (float)p.H / 2.0f, 0.0f, (float)(p.H - 1) / 2.0f}, {0.0f, 0.0f, 0.0f, 1.0f}};
+  float Pm[3][4];
+#pragma unroll
+  for (int c = 0; c < 3; c++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float a = p.proj[4 * r + 0] * N[c][0];
+      a = a + p.proj[4 * r + 1] * N[c][1];
+      a = a + p.proj[4 * r + 2] * N[c][2];
+      a = a + p.proj[4 * r + 3] * N[c][3];
+      Pm[c][r] = a;
+    }
+  float Tt[3][3];
+#pragma unroll
+  for (int c = 0; c < 3; c++)
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      float a = M[i][0] * Pm[c][0];
+      a = a + M[i][1] * Pm[c][1];
+      a = a + M[i][2] * Pm[c][2];
+      a = a + M[i][3] * Pm[c][3];
+      Tt[c][i] = a;
+    }
+  const float* v = p.view;
+  const float nrm[3] = {v[0] * Lc[2][0] + v[4] * Lc[2][1] + v[8] * Lc[2][2],
+                        v[1] * Lc[2][0] + v[5] * Lc[2][1] + v[9] * Lc[2][2],
+                        v[2] * Lc[2][0] + v[6] * Lc[2][1] + v[10] * Lc[2][2]};
+  const float* dTm = p.dtransmat + 9 * (size_t)idx;
+  float dT[9];
+#pragma unroll
+  for (int r = 0; r < 9; r++) dT[r] = dTm[r];
+  float* dm2 = p.dmean2D + 3 * (size_t)idx;
+  const float m2x = dm2[0], m2y = dm2[1];
+  if (m2x != 0 || m2y != 0) {
+    const float tv[3] = {9.0f, 9.0f, -1.0f};
+    const float T2sq[3] = {Tt[2][0] * Tt[2][0], Tt[2][1] * Tt[2][1], Tt[2][2] * Tt[2][2]};
+    const float dd = tv[0] * T2sq[0] + tv[1] * T2sq[1] + tv[2] * T2sq[2];
+    const float inv = 1.0f / dd;
+    const float f[3] = {tv[0] * inv, tv[1] * inv, tv[2] * inv};
+    float dT0[3], dT1[3], dT3[3], df[3];
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+      dT0[r] = m2x * f[r] * Tt[2][r];
+      dT1[r] = m2y * f[r] * Tt[2][r];
+      dT3[r] = m2x * f[r] * Tt[0][r] + m2y * f[r] * Tt[1][r];
+      df[r] = m2x * Tt[0][r] * Tt[2][r] + m2y * Tt[1][r] * Tt[2][r];
+    }
+    const float dL_dd = (float)((double)(df[0] * f[0] + df[1] * f[1] + df[2] * f[2]) * (-1.0 / (double)dd));
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+      dT3[r] += dL_dd * (tv[r] * Tt[2][r] * 2.0f);
+      dT[r] += dT0[r];
+      dT[3 + r] += dT1[r];
+      dT[6 + r] += dT3[r];
+    }
+  }
+  const float* hh = p.dhomo + 9 * (size_t)idx;
+  float dM[3][4];
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float a = Pm[0][r] * dT[0 + i];
+      a = a + Pm[1][r] * dT[3 + i];
+      a = a + Pm[2][r] * dT[6 + i];
+      dM[i][r] = a + (r < 3 ? hh[3 * i + r] : 0.0f);
+    }
+  const float* gn = p.dnormal + 3 * (size_t)idx;
+  const float nlen = sqrtf(nrm[0] * nrm[0] + nrm[1] * nrm[1] + nrm[2] * nrm[2]);
+  float gu[3] = {0.0f, 0.0f, 0.0f};
+  if (nlen > 1e-7f) {
+    const float dot = gn[0] * nrm[0] + gn[1] * nrm[1] + gn[2] * nrm[2];
+#pragma unroll
+    for (int r = 0; r < 3; r++) gu[r] = (gn[r] - dot * nrm[r] / nlen) / nlen;
+  }
+  float dtn[3] = {v[0] * gu[0] + v[1] * gu[1] + v[2] * gu[2], v[4] * gu[0] + v[5] * gu[1] + v[6] * gu[2],
+                  v[8] * gu[0] + v[9] * gu[1] + v[10] * gu[2]};
+  const float pv[3] = {v[0] * po[0] + v[4] * po[1] + v[8] * po[2] + v[12],
+                       v[1] * po[0] + v[5] * po[1] + v[9] * po[2] + v[13],
+                       v[2] * po[0] + v[6] * po[1] + v[10] * po[2] + v[14]};
+  const float cosv = -(pv[0] * nrm[0] + pv[1] * nrm[1] + pv[2] * nrm[2]);
+  const float mul = cosv > 0 ? 1.0f : -1.0f;
+#pragma unroll
+  for (int r = 0; r < 3; r++) dtn[r] = mul * dtn[r];
+  float dR[3][3];
+#pragma unroll
+  for (int r = 0; r < 3; r++) {
+    dR[0][r] = dM[0][r] * sc[0];
+    dR[1][r] = dM[1][r] * sc[1];
+    dR[2][r] = dtn[r];
+  }
+  float* dq = p.drots + 4 * (size_t)idx;
+  dq[0] = 2.f * (qx * (dR[1][2] - dR[2][1]) + qy * (dR[2][0] - dR[0][2]) + qz * (dR[0][1] - dR[1][0]));
+  dq[1] = 2.f * (-2.f * qx * (dR[1][1] + dR[2][2]) + qy * (dR[0][1] + dR[1][0]) + qz * (dR[0][2] + dR[2][0]) +
+                 qw * (dR[1][2] - dR[2][1]));
+  dq[2] = 2.f * (qx * (dR[0][1] + dR[1][0]) - 2.f * qy * (dR[0][0] + dR[2][2]) + qz * (dR[1][2] + dR[2][1]) +
+                 qw * (dR[2][0] - dR[0][2]));
+  dq[3] = 2.f * (qx * (dR[0][2] + dR[2][0]) + qy * (dR[1][2] + dR[2][1]) - 2.f * qz * (dR[0][0] + dR[1][1]) +
+                 qw * (dR[0][1] - dR[1][0]));
+  p.dscales[2 * (size_t)idx + 0] = dM[0][0] * R[0][0] + dM[0][1] * R[0][1] + dM[0][2] * R[0][2];
+  p.dscales[2 * (size_t)idx + 1] = dM[1][0] * R[1][0] + dM[1][1] * R[1][1] + dM[1][2] * R[1][2];
+  float dmean[3] = {dM[2][0], dM[2][1], dM[2][2]};
+
+  if (p.shs) {
+    // computeColorFromSH backward (backward.cu:20-140)
+    const float C0 = 0.28209479177387814f, C1 = 0.4886025119029199f;
+    const float C2[5] = {1.0925484305920792f, -1.0925484305920792f, 0.31539156525252005f, -1.0925484305920792f,
+                         0.5462742152960396f};
+    const float C3[7] = {-0.5900435899266435f, 2.890611442640554f, -0.4570457994644658f, 0.3731763325901154f,
+                         -0.4570457994644658f, 1.445305721320277f, -0.5900435899266435f};
+    const float dir[3] = {po[0] - p.campos[0], po[1] - p.campos[1], po[2] - p.campos[2]};
+    const float len = sqrtf(dir[0] * dir[0] + dir[1] * dir[1] + dir[2] * dir[2]);
+    const float x = dir[0] / len, y = dir[1] / len, z = dir[2] / len;
+    const int M = p.sh_coeffs, deg = p.sh_degree;
+    const float* sh = p.shs + (size_t)idx * M * 3;
+    float gc[3];
+#pragma unroll
+    for (int c = 0; c < 3; c++)
+      gc[c] = p.dcolors[3 * (size_t)idx + c] * (p.clamped[3 * (size_t)idx + c] ? 0.0f : 1.0f);
+    float* dsh = p.dshs + (size_t)idx * M * 3;
+    float ddx[3] = {0, 0, 0}, ddy[3] = {0, 0, 0}, ddz[3] = {0, 0, 0};
+    auto SH = [&](int i, int c) { return sh[3 * i + c]; };
+    auto put = [&](int i, float w) {
+#pragma unroll
+      for (int c = 0; c < 3; c++) dsh[3 * i + c] = w * gc[c];
+    };
+    put(0, C0);
+    if (deg > 0) {
+      put(1, -C1 * y); put(2, C1 * z); put(3, -C1 * x);
+#pragma unroll
+      for (int c = 0; c < 3; c++) { ddx[c] = -C1 * SH(3, c); ddy[c] = -C1 * SH(1, c); ddz[c] = C1 * SH(2, c); }
+      if (deg > 1) {
+        const float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+        put(4, C2[0] * xy); put(5, C2[1] * yz); put(6, C2[2] * (2.f * zz - xx - yy));
+        put(7, C2[3] * xz); put(8, C2[4] * (xx - yy));
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+          ddx[c] += C2[0] * y * SH(4, c) + C2[2] * 2.f * -x * SH(6, c) + C2[3] * z * SH(7, c) + C2[4] * 2.f * x * SH(8, c);
+          ddy[c] += C2[0] * x * SH(4, c) + C2[1] * z * SH(5, c) + C2[2] * 2.f * -y * SH(6, c) + C2[4] * 2.f * -y * SH(8, c);
+          ddz[c] += C2[1] * y * SH(5, c) + C2[2] * 2.f * 2.f * z * SH(6, c) + C2[3] * x * SH(7, c);
+        }
+        if (deg > 2) {
+          put(9, C3[0] * y * (3.f * xx - yy)); put(10, C3[1] * xy * z); put(11, C3[2] * y * (4.f * zz - xx - yy));
+          put(12, C3[3] * z * (2.f * zz - 3.f * xx - 3.f * yy)); put(13, C3[4] * x * (4.f * zz - xx - yy));
+          put(14, C3[5] * z * (xx - yy)); put(15, C3[6] * x * (xx - 3.f * yy));
+#pragma unroll
+          for (int c = 0; c < 3; c++) {
+            ddx[c] += (C3[0] * SH(9, c) * 3.f * 2.f * xy + C3[1] * SH(10, c) * yz + C3[2] * SH(11, c) * -2.f * xy +
+                       C3[3] * SH(12, c) * -3.f * 2.f * xz + C3[4] * SH(13, c) * (-3.f * xx + 4.f * zz - yy) +
+                       C3[5] * SH(14, c) * 2.f * xz + C3[6] * SH(15, c) * 3.f * (xx - yy));
+            ddy[c] += (C3[0] * SH(9, c) * 3.f * (xx - yy) + C3[1] * SH(10, c) * xz +
+                       C3[2] * SH(11, c) * (-3.f * yy + 4.f * zz - xx) + C3[3] * SH(12, c) * -3.f * 2.f * yz +
+                       C3[4] * SH(13, c) * -2.f * xy + C3[5] * SH(14, c) * -2.f * yz + C3[6] * SH(15, c) * -3.f * 2.f * xy);
+            ddz[c] += (C3[1] * SH(10, c) * xy + C3[2] * SH(11, c) * 4.f * 2.f * yz +
+                       C3[3] * SH(12, c) * 3.f * (2.f * zz - xx - yy) + C3[4] * SH(13, c) * 4.f * 2.f * xz +
+                       C3[5] * SH(14, c) * (xx - yy));
+          }
+        }
+      }
+    }
+    for (int i = (deg + 1) * (deg + 1); i < M; i++) put(i, 0.0f);
+    const float ddir[3] = {ddx[0] * gc[0] + ddx[1] * gc[1] + ddx[2] * gc[2],
+                           ddy[0] * gc[0] + ddy[1] * gc[1] + ddy[2] * gc[2],
+                           ddz[0] * gc[0] + ddz[1] * gc[1] + ddz[2] * gc[2]};
+    const float sum2 = dir[0] * dir[0] + dir[1] * dir[1] + dir[2] * dir[2];
+    const float invsum32 = 1.0f / sqrtf(sum2 * sum2 * sum2);
+    dmean[0] += ((+sum2 - dir[0] * dir[0]) * ddir[0] - dir[1] * dir[0] * ddir[1] - dir[2] * dir[0] * ddir[2]) * invsum32;
+    dmean[1] += (-dir[0] * dir[1] * ddir[0] + (sum2 - dir[1] * dir[1]) * ddir[1] - dir[2] * dir[1] * ddir[2]) * invsum32;
+    dmean[2] += (-dir[0] * dir[2] * ddir[0] - dir[1] * dir[2] * ddir[1] + (sum2 - dir[2] * dir[2]) * ddir[2]) * invsum32;
+  }
+  p.dmeans[3 * (size_t)idx + 0] = dmean[0];
+  p.dmeans[3 * (size_t)idx + 1] = dmean[1];
+  p.dmeans[3 * (size_t)idx + 2] = dmean[2];
+  // densification statistic (backward.cu:2268-2271): the render's dL/dT
+  const float depth = p.records[32 * (size_t)idx + 8];
+  dm2[0] = (float)((double)(dTm[2] * depth) * 0.5 * (double)(float)p.W);
+  dm2[1] = (float)((double)(dTm[5] * depth) * 0.5 * (double)(float)p.H);
+}
+
+// kernel_grid_backward + kernel_input_backward (gridencoder.cu:245-366) with
+// the dy_dx of kernel_grid (:196-242), D = 3, binary32 tables: one lane per
+// point, levels in order, table gradients as float atomics, the input
+// gradient summed level by level and written once.
+template <int F>
+__global__ void __launch_bounds__(256) grid_encode_backward_kernel(const GridEncodeBwdParams p) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= p.B) return;
+  const float u[3] = {p.inputs[3 * b], p.inputs[3 * b + 1], p.inputs[3 * b + 2]};
+  const bool oob = u[0] < 0 || u[0] > 1 || u[1] < 0 || u[1] > 1 || u[2] < 0 || u[2] > 1;
+  float gi[3] = {0.0f, 0.0f, 0.0f};
+  if (!oob) {
+    const nest_i32x4 rsrc = table_rsrc_rows<F, false>(p.table, p.table_rows);
+    const float off = p.align_corners ? 0.0f : 0.5f;
+    for (int l = 0; l < p.L; l++) {
+      const float scale = p.lv.scale[l];
+      float pos[3], der[3];
+#pragma unroll
+      for (int d = 0; d < 3; d++) {
+        const float x = u[d] * scale + off;
+        pos[d] = x - (float)f2u_sat(x);
+        if (p.interp == 1) {
+          der[d] = 6.0f * pos[d] * (1.0f - pos[d]);
+          pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
+        } else {
+          der[d] = 1.0f;
+        }
+      }
+      LevelCorners cn;
+      level_corners<F, false>(p.lv, l, off, 0u, u, cn);
+      cn.wx[0] = 1 - pos[0]; cn.wx[1] = pos[0];
+      cn.wy[0] = 1 - pos[1]; cn.wy[1] = pos[1];
+      cn.wz[0] = 1 - pos[2]; cn.wz[1] = pos[2];
+      float gr[F];
+#pragma unroll
+      for (int f = 0; f < F; f++) gr[f] = p.grad[(size_t)b * p.L * F + (size_t)l * F + f];
+      float* dl = p.grad_table + (size_t)p.lv.base[l] * F;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const float wk = (1.0f * cn.wx[k & 1]) * cn.wy[(k >> 1) & 1] * cn.wz[k >> 2];
+#pragma unroll
+        for (int f = 0; f < F; f++) atomic_add(dl + (size_t)cn.idx[k] * F + f, wk * gr[f]);
+      }
+      if (!p.grad_inputs) continue;
+      float vals[8][F];
+      corners_load<F, false>(rsrc, cn, vals);
+#pragma unroll
+      for (int gd = 0; gd < 3; gd++) {
+        float rg[F];
+#pragma unroll
+        for (int f = 0; f < F; f++) rg[f] = 0.0f;
+#pragma unroll
+        for (int idx = 0; idx < 4; idx++) {
+          float wgt = scale;
+          int kl = 0;
+#pragma unroll
+          for (int nd = 0; nd < 2; nd++) {
+            const int d = (nd >= gd) ? nd + 1 : nd;
+            const int bit = (idx >> nd) & 1;
+            wgt *= bit ? pos[d] : 1 - pos[d];
+            kl |= bit << d;
+          }
+          const int kr = kl | (1 << gd);
+#pragma unroll
+          for (int f = 0; f < F; f++) rg[f] += wgt * (vals[kr][f] - vals[kl][f]) * der[gd];
+        }
+#pragma unroll
+        for (int f = 0; f < F; f++) gi[gd] += gr[f] * rg[f];
+      }
+    }
+  }
+  if (p.grad_inputs) {
+#pragma unroll
+    for (int d = 0; d < 3; d++) p.grad_inputs[3 * b + d] = gi[d];
+  }
+}
+
+}  // namespace
+
+hipError_t launch_grid_encode_backward(const GridEncodeBwdParams& p, hipStream_t s) {
+  if (p.B == 0) return hipSuccess;
+  const dim3 grid((unsigned)((p.B + 255) / 256));
+  switch (p.F) {
+    case 1: hipLaunchKernelGGL(grid_encode_backward_kernel<1>, grid, dim3(256), 0, s, p); break;
+    case 2: hipLaunchKernelGGL(grid_encode_backward_kernel<2>, grid, dim3(256), 0, s, p); break;
+    case 4: hipLaunchKernelGGL(grid_encode_backward_kernel<4>, grid, dim3(256), 0, s, p); break;
+    case 8: hipLaunchKernelGGL(grid_encode_backward_kernel<8>, grid, dim3(256), 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_render_backward(const RenderBwdParams& p, hipStream_t s) {
+  if (p.ntiles == 0) return hipSuccess;
+  if (p.level == 0) return launch_bwd_one<1, false>(p, s);
+  switch (p.grid.F) {
+    case 1: return launch_bwd_one<1, true>(p, s);
+    case 2: return launch_bwd_one<2, true>(p, s);
+    case 4: return launch_bwd_one<4, true>(p, s);
+    case 8: return launch_bwd_one<8, true>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_preprocess_backward(const PreprocessBwdParams& p, hipStream_t s) {
+  if (p.P == 0) return hipSuccess;
+  hipLaunchKernelGGL(preprocess_backward_kernel, dim3((p.P + 255) / 256), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace nest

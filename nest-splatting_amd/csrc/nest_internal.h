@@ -144,6 +144,81 @@ hipError_t launch_tile_ranges(const uint64_t* keys, int64_t n, uint32_t* ranges,
 hipError_t launch_render(const RenderParams& p, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* dst, uint32_t value, int64_t n, hipStream_t s);
 
+// Backward of the render (renderCUDAsurfelBackward, mode 0).  Reads the
+// forward's records, point list, ranges, final_T and n_contrib; accumulates
+// into zero-filled gradient arrays.
+struct RenderBwdParams {
+  int W, H;
+  uint32_t gx, gy;
+  uint32_t ntiles;
+  int C;
+  int level;                  // 0 colour path, >0 hash
+  float beta;
+  const uint32_t* ranges;
+  const uint32_t* point_list;
+  const float* records;       // [P][32]
+  const float* colors;        // [P][C] colour path
+  const float* final_T;       // [3][H][W]
+  const uint32_t* n_contrib;  // [2][H][W]
+  const float* dL_dpix;       // [C][H][W]
+  const float* dL_dothers;    // [14][H][W]
+  float* dtable;              // [rows][F] hash path
+  float* dtransmat;           // [P][9]
+  float* dhomo;               // [P][9]
+  float* dmean2D;             // [P][3]
+  float* dnormal;             // [P][3]
+  float* dopacity;            // [P]
+  float* dcolors;             // [P][C] colour path
+  float* gradsum;             // [P] hash path
+  GridParams grid;
+};
+hipError_t launch_render_backward(const RenderBwdParams& p, hipStream_t s);
+
+// Backward of preprocess (preprocessCUDA backward with compute_transmat_aabb
+// and computeColorFromSH), one lane per splat with radii > 0.
+struct PreprocessBwdParams {
+  int P, W, H;
+  float view[16];
+  float proj[16];
+  float campos[3];
+  const float* means;
+  const float* scales;
+  const float* rots;
+  const int32_t* radii;
+  const float* records;       // [P][32]: Tw.z (depth of the statistic)
+  const float* shs;           // [P][sh_coeffs][3] or null
+  int sh_degree, sh_coeffs;
+  const uint8_t* clamped;     // [P][3]
+  const float* dcolors;       // [P][3] when shs
+  const float* dtransmat;     // [P][9]
+  const float* dhomo;         // [P][9]
+  const float* dnormal;       // [P][3]
+  float* dmean2D;             // [P][3]: read, then overwritten with the statistic
+  float* dmeans;              // [P][3]
+  float* dscales;             // [P][2]
+  float* drots;               // [P][4]
+  float* dshs;                // [P][sh_coeffs][3] when shs
+};
+hipError_t launch_preprocess_backward(const PreprocessBwdParams& p, hipStream_t s);
+
+// GridEncoder backward, D = 3, binary32 table: table gradient (accumulated
+// into a zero-filled array) and, when grad_inputs is set, the input gradient.
+struct GridEncodeBwdParams {
+  const float* inputs;    // [B][3]
+  int64_t B;
+  int F;
+  int L;
+  int align_corners;
+  int interp;
+  const float* table;
+  uint32_t table_rows;
+  const float* grad;      // [B][L*F]
+  float* grad_table;      // [rows][F]
+  float* grad_inputs;     // [B][3] or null
+  LevelTable lv;
+};
+hipError_t launch_grid_encode_backward(const GridEncodeBwdParams& p, hipStream_t s);
+
 struct GridEncodeParams {
   const float* inputs;
   int64_t B;

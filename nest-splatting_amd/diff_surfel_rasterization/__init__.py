@@ -8,12 +8,15 @@ GaussianRasterizer(raster_settings, hashgrid_settings).forward(...) returning
 (color [C,H,W], radii [P], allmap [14,H,W], trans_avg, cover) (:172, :321-396),
 markVisible (:310-319) and rasterize_gaussians (:21-66).
 
-Scope: the forward pass of render mode 0 ("baseline"): hash-grid features
-when HashGridSettings.L > 0; when L == 0, precomputed per-splat colours or
-RGB evaluated from SH coefficients (degree <= 3) in preprocess.  Modes,
-kernels and options that the reference implements for other methods raise
-NotImplementedError instead of returning zeros; backward raises as well
-(forward-only renderer).
+Scope: render mode 0 ("baseline") with the Gaussian kernel, forward and
+backward: hash-grid features when HashGridSettings.L > 0; when L == 0,
+precomputed per-splat colours or RGB evaluated from SH coefficients
+(degree <= 3) in preprocess.  The backward returns the reference's gradients
+(DSRpy:174-275): means3D, the means2D densification statistic, SH,
+colours, opacities, scales, rotations, the hash table, and the |grad| sum in
+the ap_level slot; it needs a float32 hash table and at most 64 channels.
+Modes, kernels and options that the reference implements for other methods
+raise NotImplementedError instead of returning zeros.
 """
 from __future__ import annotations
 
@@ -103,14 +106,37 @@ class _RasterizeGaussians(torch.autograd.Function):
                                     channels=C, shs=None if (level > 0 or colors is not None or _empty(sh)) else
                                     sh.detach(), sh_degree=int(raster_settings.sh_degree))
         ctx.num_rendered = res.num_rendered
+        ctx.fw = dict(res=res, settings=settings, grid=grid, C=C, colors=colors,
+                      shs=None if (level > 0 or colors is not None or _empty(sh)) else sh.detach(),
+                      sh_degree=int(raster_settings.sh_degree),
+                      homotrans=None if _empty(homotrans) else homotrans.detach(),
+                      ap_level=None if _empty(ap_level) else ap_level.detach())
+        ctx.save_for_backward(means3D, opacities, scales, rotations)
         dev = means3D.device
         trans_avg = torch.zeros((0, 1), dtype=torch.float32, device=dev)
         cover = torch.zeros((0, 1), dtype=torch.float32, device=dev)
         return res.color, res.radii, res.others, trans_avg, cover
 
     @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError("this rasterizer implements the forward pass only")
+    def backward(ctx, grad_out_color, grad_radii, grad_depth, grad_0, grad_1):
+        means3D, opacities, scales, rotations = ctx.saved_tensors
+        fw = ctx.fw
+        g = _rz.rasterize_backward(fw["settings"], fw["grid"], fw["res"], means3D.detach(), opacities.detach(),
+                                   scales.detach(), rotations.detach(), grad_out_color, grad_depth,
+                                   homotrans=fw["homotrans"], ap_level=fw["ap_level"], colors_precomp=fw["colors"],
+                                   channels=fw["C"], shs=fw["shs"], sh_degree=fw["sh_degree"])
+        need = ctx.needs_input_grad
+
+        def pick(i, t, shape=None):
+            if not need[i] or t is None:
+                return None
+            return t.reshape(shape) if shape is not None else t
+
+        ap = fw["ap_level"]
+        return (pick(0, g.dmeans3D), pick(1, g.dmeans2D), pick(2, g.dshs), pick(3, g.dcolors),
+                pick(4, g.dopacity, opacities.shape), pick(5, g.dscales), pick(6, g.drotations), None, None,
+                pick(9, g.dgradsum, None if ap is None else ap.shape), pick(10, g.dfeatures),
+                None, None, None, None, None, None, None, None, None, None)
 
 
 class GaussianRasterizationSettings(NamedTuple):

@@ -8,8 +8,10 @@ interpolation='linear'); forward(inputs, bound=1) with inputs in [0, 1]
 returns [..., num_levels * level_dim]; get_params() returns (embeddings,
 offsets, num_levels, per_level_scale, base_resolution, align_corners,
 interp_id).  Under autocast with an even level_dim the table is used in
-float16 (GE/grid.py:43-44).  Backward and total-variation gradients are
-training features and raise NotImplementedError.
+float16 (GE/grid.py:43-44).  Backward (GE/grid.py:67-91) gives the table
+gradient and, when the inputs require grad, the input gradient, for D = 3 and
+float32 tables; other cases and total-variation gradients raise
+NotImplementedError.
 """
 from __future__ import annotations
 
@@ -54,18 +56,67 @@ def grid_encode_forward(inputs: torch.Tensor, embeddings: torch.Tensor, offsets_
     return out
 
 
+def grid_encode_backward(inputs: torch.Tensor, embeddings: torch.Tensor, offsets_host: np.ndarray,
+                         per_level_scale: float, base_resolution: int, grad: torch.Tensor, calc_grad_inputs: bool,
+                         gridtype: int = 0, align_corners: bool = False, interpolation: int = 0):
+    """_grid_encode.backward (GE/grid.py:67-91): (grad_inputs or None,
+    grad_embeddings) for grad [B, L * C]."""
+    inputs = inputs.contiguous()
+    if inputs.dtype != torch.float32:
+        inputs = inputs.float()
+    B, D = inputs.shape
+    if D != 3:
+        raise NotImplementedError(f"GridEncoder backward supports input_dim 3 (got {D})")
+    if embeddings.dtype != torch.float32:
+        raise NotImplementedError("GridEncoder backward supports float32 embeddings")
+    L_ = int(offsets_host.shape[0]) - 1
+    C = int(embeddings.shape[1])
+    emb = embeddings.detach().contiguous()
+    if emb.data_ptr() % 16:
+        emb = emb.clone()
+    grad = grad.contiguous().float()
+    grad_emb = torch.empty_like(emb)
+    grad_in = torch.empty((B, 3), dtype=torch.float32, device=inputs.device) if calc_grad_inputs else None
+    offs = (ct.c_int32 * (L_ + 1))(*[int(v) for v in offsets_host])
+    L.check(L.lib().nest_grid_encode_backward(L.ptr(inputs), B, D, L.ptr(emb), int(emb.shape[0]), L.DTYPE_F32, offs,
+                                              L_, C, float(np.log2(per_level_scale)), int(base_resolution),
+                                              int(gridtype), int(bool(align_corners)), int(interpolation),
+                                              L.ptr(grad), L.ptr(grad_emb), L.ptr(grad_in),
+                                              L.stream_ptr(inputs.device)), "nest_grid_encode_backward")
+    return grad_in, grad_emb
+
+
 class _GridEncode(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, inputs, embeddings, offsets_host, per_level_scale, base_resolution, gridtype, align_corners,
-                interpolation):
+    def forward(ctx, inputs, embeddings, offsets_host, per_level_scale, base_resolution, calc_grad_inputs, gridtype,
+                align_corners, interpolation):
         if torch.is_autocast_enabled() and embeddings.shape[1] % 2 == 0:
             embeddings = embeddings.to(torch.half)
+        ctx.save_for_backward(inputs, embeddings)
+        ctx.params = (offsets_host, per_level_scale, base_resolution, bool(calc_grad_inputs), gridtype,
+                      align_corners, interpolation)
         return grid_encode_forward(inputs, embeddings, offsets_host, per_level_scale, base_resolution, gridtype,
                                    align_corners, interpolation)
 
     @staticmethod
     def backward(ctx, grad):
-        raise NotImplementedError("GridEncoder backward is a training feature and is not implemented")
+        inputs, embeddings = ctx.saved_tensors
+        offsets_host, pls, base, calc, gridtype, align, interp = ctx.params
+        grad_in, grad_emb = grid_encode_backward(inputs, embeddings, offsets_host, pls, base, grad, calc, gridtype,
+                                                 align, interp)
+        if grad_in is not None:
+            grad_in = grad_in.to(inputs.dtype)
+        return grad_in, grad_emb, None, None, None, None, None, None, None
+
+
+def grid_encode(inputs, embeddings, offsets, per_level_scale, base_resolution, calc_grad_inputs=False, gridtype=0,
+                align_corners=False, interpolation=0):
+    """grid_encode = _grid_encode.apply of GE/grid.py:95 (offsets may be a
+    device tensor; its host copy is read once)."""
+    from nest_splat.rasterizer import host_array
+    offsets_host = host_array(offsets, np.int64).astype(np.int64)
+    return _GridEncode.apply(inputs, embeddings, offsets_host, per_level_scale, base_resolution, calc_grad_inputs,
+                             gridtype, align_corners, interpolation)
 
 
 class GridEncoder(nn.Module):
@@ -110,7 +161,8 @@ class GridEncoder(nn.Module):
         prefix_shape = list(inputs.shape[:-1])
         inputs = inputs.reshape(-1, self.input_dim)
         outputs = _GridEncode.apply(inputs, self.embeddings, self._offsets_host, self.per_level_scale,
-                                    self.base_resolution, self.gridtype_id, self.align_corners, self.interp_id)
+                                    self.base_resolution, inputs.requires_grad, self.gridtype_id, self.align_corners,
+                                    self.interp_id)
         return outputs.view(prefix_shape + [self.output_dim])
 
     def get_params(self):

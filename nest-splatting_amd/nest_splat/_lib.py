@@ -27,7 +27,7 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
  GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
 GEOM_FIELDS = 12
@@ -35,6 +35,8 @@ BIN_PAIR_TILES, BIN_PAIR_IDS, BIN_KEYS, BIN_VALS, BIN_SORT_TMP = range(5)
 BIN_FIELDS = 5
 IMG_RANGES, IMG_FINAL_T, IMG_N_CONTRIB, IMG_LEVELS = range(4)
 IMG_FIELDS = 4
+BWD_DTRANSMAT, BWD_DHOMO, BWD_DNORMAL, BWD_DCOLORS, BWD_GRADSUM = range(5)
+BWD_FIELDS = 5
 STAGES = ("preprocess", "scan", "duplicate", "sort", "ranges", "render")
 
 
@@ -64,6 +66,14 @@ class Splats(ct.Structure):
 class FrameOutputs(ct.Structure):
     _fields_ = [("struct_size", ct.c_uint32), ("channels", ct.c_int32), ("out_color", ct.c_void_p),
                 ("out_others", ct.c_void_p), ("radii", ct.c_void_p)]
+
+
+class BackwardIO(ct.Structure):
+    _fields_ = [("struct_size", ct.c_uint32), ("channels", ct.c_int32), ("dL_dout_color", ct.c_void_p),
+                ("dL_dout_others", ct.c_void_p), ("dL_dmeans3D", ct.c_void_p), ("dL_dmeans2D", ct.c_void_p),
+                ("dL_dcolors", ct.c_void_p), ("dL_dopacity", ct.c_void_p), ("dL_dshs", ct.c_void_p),
+                ("dL_dscales", ct.c_void_p), ("dL_drotations", ct.c_void_p), ("dL_dfeatures", ct.c_void_p),
+                ("dL_dgradsum", ct.c_void_p)]
 
 
 class Timing(ct.Structure):
@@ -104,6 +114,10 @@ EXPORTS = {
                                        ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_size_t,
                                        ct.c_int64, ct.POINTER(FrameOutputs), ct.POINTER(Timing), ct.c_void_p]),
     "nest_mark_visible": (ct.c_int, [ct.c_int32, ct.c_void_p, ct.POINTER(ct.c_float), ct.c_void_p, ct.c_void_p]),
+    "nest_backward_layout": (ct.c_int, [ct.c_int32, ct.c_int32, ct.POINTER(ct.c_size_t), ct.POINTER(ct.c_size_t)]),
+    "nest_backward": (ct.c_int, [ct.POINTER(RasterSettings), ct.POINTER(HashGrid), ct.POINTER(Splats), ct.c_void_p,
+                                 ct.c_size_t, ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_size_t, ct.c_int64,
+                                 ct.POINTER(BackwardIO), ct.c_void_p, ct.c_size_t, ct.c_void_p]),
     "nest_timing_read": (ct.c_int, [ct.POINTER(Timing)]),
     "nest_timing_release": (ct.c_int, [ct.POINTER(Timing)]),
     "nest_scan_workspace_size": (ct.c_size_t, [ct.c_int64]),
@@ -115,6 +129,10 @@ EXPORTS = {
     "nest_grid_encode": (ct.c_int, [ct.c_void_p, ct.c_int64, ct.c_int32, ct.c_void_p, ct.c_int64, ct.c_int32,
                                     ct.POINTER(ct.c_int32), ct.c_int32, ct.c_int32, ct.c_float, ct.c_int32, ct.c_int32,
                                     ct.c_int32, ct.c_int32, ct.c_void_p, ct.c_void_p]),
+    "nest_grid_encode_backward": (ct.c_int, [ct.c_void_p, ct.c_int64, ct.c_int32, ct.c_void_p, ct.c_int64, ct.c_int32,
+                                             ct.POINTER(ct.c_int32), ct.c_int32, ct.c_int32, ct.c_float, ct.c_int32,
+                                             ct.c_int32, ct.c_int32, ct.c_int32, ct.c_void_p, ct.c_void_p, ct.c_void_p,
+                                             ct.c_void_p]),
     "nest_mlp_decode": (ct.c_int, [ct.POINTER(Mlp), ct.c_void_p, ct.c_int64, ct.c_int64, ct.c_int64, ct.c_int32,
                                    ct.c_void_p, ct.POINTER(ct.c_float), ct.c_void_p, ct.POINTER(ct.c_float),
                                    ct.c_void_p, ct.c_int64, ct.c_int64, ct.c_void_p]),

@@ -143,19 +143,12 @@ def _contig_f32(t: Optional[torch.Tensor], name: str) -> Optional[torch.Tensor]:
     return aligned(t)
 
 
-def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: torch.Tensor, opacities: torch.Tensor,
-                      scales: torch.Tensor, rotations: torch.Tensor, homotrans: Optional[torch.Tensor] = None,
-                      ap_level: Optional[torch.Tensor] = None, colors_precomp: Optional[torch.Tensor] = None,
-                      channels: int = 3, timing: bool = False, shs: Optional[torch.Tensor] = None,
-                      sh_degree: int = 0) -> ForwardResult:
-    """One forward frame.  The colour path (grid.levels == 0) takes colours
-    from colors_precomp, or, when it is None, evaluates them from shs
-    [P, M, 3] at degree sh_degree in preprocess (3 channels)."""
+def _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, channels, shs, sh_degree):
+    """nest_splats over the device tensors (re-aligned copies where needed);
+    returns (struct, tensors kept alive for the call)."""
     if means3D.ndim != 2 or means3D.shape[1] != 3:
         raise ValueError("means3D must have dimensions (num_points, 3)")
-    dev = means3D.device
     P = int(means3D.shape[0])
-    H, W = settings.image_height, settings.image_width
     means3D = _contig_f32(means3D, "means3D")
     opacities = _contig_f32(opacities, "opacities")
     scales = _contig_f32(scales, "scales")
@@ -192,6 +185,22 @@ def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: t
     sp.shs = L.ptr(shs)
     sp.sh_degree = int(sh_degree)
     sp.sh_coeffs = int(shs.numel() // (3 * P)) if shs is not None and P > 0 else 0
+    return sp, (means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, shs)
+
+
+def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: torch.Tensor, opacities: torch.Tensor,
+                      scales: torch.Tensor, rotations: torch.Tensor, homotrans: Optional[torch.Tensor] = None,
+                      ap_level: Optional[torch.Tensor] = None, colors_precomp: Optional[torch.Tensor] = None,
+                      channels: int = 3, timing: bool = False, shs: Optional[torch.Tensor] = None,
+                      sh_degree: int = 0) -> ForwardResult:
+    """One forward frame.  The colour path (grid.levels == 0) takes colours
+    from colors_precomp, or, when it is None, evaluates them from shs
+    [P, M, 3] at degree sh_degree in preprocess (3 channels)."""
+    dev = means3D.device
+    P = int(means3D.shape[0])
+    H, W = settings.image_height, settings.image_width
+    sp, keep = _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, channels, shs,
+                       sh_degree)
     g = grid.to_c()
 
     color = torch.empty((channels, H, W), dtype=torch.float32, device=dev)
@@ -225,6 +234,76 @@ def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: t
         res.timing_ms = L.timing_read(tm)
         L.timing_release(tm)
     return res
+
+
+@dataclass
+class BackwardResult:
+    dmeans3D: torch.Tensor      # [P, 3]
+    dmeans2D: torch.Tensor      # [P, 3] densification statistic of the reference
+    dcolors: torch.Tensor       # [P, C]
+    dopacity: torch.Tensor      # [P, 1]
+    dshs: Optional[torch.Tensor]  # [P, M, 3] when the colours came from SH
+    dscales: torch.Tensor       # [P, 2]
+    drotations: torch.Tensor    # [P, 4]
+    dfeatures: Optional[torch.Tensor]  # [rows, F] hash path
+    dgradsum: torch.Tensor      # [P, 1]
+
+
+def rasterize_backward(settings: L.RasterSettings, grid: HashGridDesc, res: ForwardResult, means3D: torch.Tensor,
+                       opacities: torch.Tensor, scales: torch.Tensor, rotations: torch.Tensor,
+                       dL_dcolor: torch.Tensor, dL_dothers: Optional[torch.Tensor],
+                       homotrans: Optional[torch.Tensor] = None, ap_level: Optional[torch.Tensor] = None,
+                       colors_precomp: Optional[torch.Tensor] = None, channels: int = 3,
+                       shs: Optional[torch.Tensor] = None, sh_degree: int = 0) -> BackwardResult:
+    """Backward of one forward frame (nest_backward): the inputs are those
+    of the rasterize_forward call that produced ``res``."""
+    dev = means3D.device
+    P = int(means3D.shape[0])
+    H, W = settings.image_height, settings.image_width
+    sp, keep = _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, channels, shs,
+                       sh_degree)
+    g = grid.to_c()
+    if dL_dcolor is None:
+        dL_dcolor = torch.zeros((channels, H, W), dtype=torch.float32, device=dev)
+    if dL_dothers is None:
+        dL_dothers = torch.zeros((L.OTHERS_CHANNELS, H, W), dtype=torch.float32, device=dev)
+    dL_dcolor = dL_dcolor.to(torch.float32).contiguous()
+    dL_dothers = dL_dothers.to(torch.float32).contiguous()
+    if tuple(dL_dcolor.shape) != (channels, H, W) or tuple(dL_dothers.shape) != (L.OTHERS_CHANNELS, H, W):
+        raise ValueError("gradient shapes must match the forward outputs")
+    f32 = dict(dtype=torch.float32, device=dev)
+    out = BackwardResult(
+        dmeans3D=torch.empty((P, 3), **f32), dmeans2D=torch.empty((P, 3), **f32),
+        dcolors=torch.empty((P, channels), **f32), dopacity=torch.empty((P, 1), **f32),
+        dshs=None, dscales=torch.empty((P, 2), **f32), drotations=torch.empty((P, 4), **f32),
+        dfeatures=None, dgradsum=torch.empty((P, 1), **f32))
+    if grid.levels > 0:
+        out.dfeatures = torch.empty(tuple(grid.table.shape), **f32)
+    elif colors_precomp is None or colors_precomp.numel() == 0:
+        out.dshs = torch.empty(tuple(shs.shape), **f32)
+    io = L.BackwardIO()
+    io.struct_size = ct.sizeof(L.BackwardIO)
+    io.channels = int(channels)
+    io.dL_dout_color = dL_dcolor.data_ptr()
+    io.dL_dout_others = dL_dothers.data_ptr()
+    io.dL_dmeans3D = out.dmeans3D.data_ptr()
+    io.dL_dmeans2D = out.dmeans2D.data_ptr()
+    io.dL_dcolors = out.dcolors.data_ptr()
+    io.dL_dopacity = out.dopacity.data_ptr()
+    io.dL_dshs = L.ptr(out.dshs)
+    io.dL_dscales = out.dscales.data_ptr()
+    io.dL_drotations = out.drotations.data_ptr()
+    io.dL_dfeatures = L.ptr(out.dfeatures)
+    io.dL_dgradsum = out.dgradsum.data_ptr()
+    offs = (ct.c_size_t * L.BWD_FIELDS)()
+    wbytes = ct.c_size_t(0)
+    L.check(L.lib().nest_backward_layout(P, int(channels), offs, ct.byref(wbytes)), "nest_backward_layout")
+    ws = torch.empty((max(int(wbytes.value), 1),), dtype=torch.uint8, device=dev)
+    L.check(L.lib().nest_backward(ct.byref(settings), ct.byref(g), ct.byref(sp), L.ptr(res.geom), res.geom.numel(),
+                                  L.ptr(res.binning), res.binning.numel(), L.ptr(res.image), res.image.numel(),
+                                  res.num_rendered, ct.byref(io), L.ptr(ws), int(wbytes.value), L.stream_ptr(dev)),
+            "nest_backward")
+    return out
 
 
 def geometry_arrays(res: ForwardResult, P: int) -> Dict[str, torch.Tensor]:

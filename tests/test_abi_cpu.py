@@ -45,6 +45,7 @@ def test_struct_sizes_match_c_layout():
     assert ct.sizeof(L.Splats) == 8 + 8 * 8 + 8
     assert ct.sizeof(L.FrameOutputs) == 8 + 3 * 8
     assert ct.sizeof(L.Mlp) == 16 + 3 * 8
+    assert ct.sizeof(L.BackwardIO) == 8 + 11 * 8
 
 
 def test_layouts_are_aligned_and_monotone():
@@ -159,6 +160,56 @@ def test_render_rejects_bad_grids():
     out.channels = 64
     # workspace checks come after argument checks and before any launch
     assert lib.nest_forward_render(*args()) == L.NEST_ERR_WORKSPACE
+
+
+def test_backward_layout_and_validation():
+    """nest_backward_layout sizes and the argument checks of nest_backward /
+    nest_grid_encode_backward, which return before any launch."""
+    L = _lib()
+    lib = L.lib()
+    offs = (ct.c_size_t * L.BWD_FIELDS)()
+    tot = ct.c_size_t(0)
+    assert lib.nest_backward_layout(1000, 64, offs, ct.byref(tot)) == L.NEST_OK
+    o = list(offs)
+    assert all(v % 256 == 0 for v in o) and o == sorted(o)
+    assert o[L.BWD_DHOMO] - o[L.BWD_DTRANSMAT] >= 1000 * 36 and o[L.BWD_GRADSUM] - o[L.BWD_DCOLORS] >= 1000 * 256
+    assert tot.value >= o[L.BWD_GRADSUM] + 4000
+    assert lib.nest_backward_layout(-1, 3, offs, ct.byref(tot)) == L.NEST_ERR_INVALID_ARGUMENT
+    s = _settings(L)
+    sp = _splats(L, 0)
+    g = L.HashGrid()
+    g.struct_size = ct.sizeof(L.HashGrid)
+    io = L.BackwardIO()
+    io.struct_size = ct.sizeof(L.BackwardIO)
+    io.channels = 3
+    ws = (ct.c_uint8 * 16)()
+    args = lambda: (ct.byref(s), ct.byref(g), ct.byref(sp), ws, 16, ws, 16, ws, 16, 0, ct.byref(io), ws, 16, None)
+    assert lib.nest_backward(*args()) == L.NEST_ERR_INVALID_ARGUMENT  # no gradient inputs
+    assert b"dL_dout_color" in lib.nest_last_error()
+    io.dL_dout_color = io.dL_dout_others = 1
+    assert lib.nest_backward(*args()) == L.NEST_ERR_INVALID_ARGUMENT  # no outputs
+    io.dL_dmeans3D = io.dL_dmeans2D = io.dL_dopacity = io.dL_dscales = io.dL_drotations = 1
+    io.channels = 65
+    assert lib.nest_backward(*args()) == L.NEST_ERR_UNSUPPORTED  # more than 64 channels
+    io.channels = 64
+    g.levels, g.level_dim, g.table, g.table_rows = 16, 4, 1, 16 * 1024
+    g.table_dtype = L.DTYPE_F16
+    g.gridrange[0], g.gridrange[1] = -1.0, 1.0
+    for i in range(17):
+        g.offsets[i] = i * 1024
+    assert lib.nest_backward(*args()) == L.NEST_ERR_UNSUPPORTED  # binary16 table
+    assert b"float32" in lib.nest_last_error()
+    g.table_dtype = L.DTYPE_F32
+    assert lib.nest_backward(*args()) == L.NEST_ERR_INVALID_ARGUMENT  # no dL_dfeatures
+    io.dL_dfeatures = 1
+    assert lib.nest_backward(*args()) == L.NEST_ERR_WORKSPACE
+    io.struct_size = 8
+    assert lib.nest_backward(*args()) == L.NEST_ERR_INVALID_ARGUMENT
+    offs32 = (ct.c_int32 * 3)(0, 64, 128)
+    ge = lambda D, dt: lib.nest_grid_encode_backward(1, 4, D, 1, 128, dt, offs32, 2, 2, 0.5, 4, 0, 0, 0, 1, 1, None,
+                                                      None)
+    assert ge(2, L.DTYPE_F32) == L.NEST_ERR_UNSUPPORTED
+    assert ge(3, L.DTYPE_F16) == L.NEST_ERR_UNSUPPORTED
 
 
 def test_building_block_validation():

@@ -1,0 +1,164 @@
+"""GPU parity of the backward pass (nest_backward, nest_grid_encode_backward)
+against the backward oracle, which the CPU tests pin against float64
+autograd.  The forward state both sides start from is the GPU forward, which
+is bit-exact with the oracle's.  The reference sums every per-splat and
+per-table-entry gradient with float atomics in hardware order; here the GPU
+sums per wave then atomically, the oracle sequentially, so the comparison is
+relative to each gradient array's largest entry: max |gpu - oracle| <= 2e-5
+* max |oracle| (float32 reassociation of sums of up to a few thousand terms).
+"""
+import numpy as np
+import pytest
+import torch
+
+from scenes import scene
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+TOL = 2e-5
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def _setup(oracle, sc, path, beta=0.0, sh_degree=3):
+    from nest_splat import rasterizer as rz
+    sp = sc.spec
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    settings = rz.make_settings(H, W, cam.tanfovx, cam.tanfovy, cam.world_view_transform, cam.full_proj_transform,
+                                cam.camera_center, beta=beta, if_contract=sp.contract)
+    rng = np.random.default_rng(17)
+    P = sp.P
+    kw = dict(homotrans=None, ap_level=None, colors_precomp=None, shs=None, sh_degree=0)
+    if path == "hash":
+        C = sp.C
+        grid = rz.HashGridDesc(sp.L, sp.F, sp.S, sp.base_res, _t(sc.table), sc.offsets,
+                               np.asarray(sp.gridrange, np.float32))
+        ap = sc.ap_level.reshape(-1).copy()
+        ap[::5] = 3.0
+        kw.update(homotrans=_t(sc.homotrans), ap_level=_t(ap))
+    else:
+        grid = rz.HashGridDesc(0, 1, 0.0, 0, None, np.zeros(1, np.int64), np.zeros(2, np.float32))
+        if path == "colors":
+            C = 8
+            colors = rng.uniform(0, 1, (P, C)).astype(np.float32)
+            kw.update(colors_precomp=_t(colors))
+        else:
+            C = 3
+            shs = (rng.standard_normal((P, 16, 3)) * 0.8).astype(np.float32)
+            kw.update(shs=_t(shs), sh_degree=sh_degree)
+    res = rz.rasterize_forward(settings, grid, _t(sc.means), _t(sc.opacity), _t(sc.scales), _t(sc.rotations),
+                               channels=C, **kw)
+    dcol = rng.standard_normal((C, H, W)).astype(np.float32)
+    doth = rng.standard_normal((14, H, W)).astype(np.float32)
+    gb = rz.rasterize_backward(settings, grid, res, _t(sc.means), _t(sc.opacity), _t(sc.scales), _t(sc.rotations),
+                               _t(dcol), _t(doth), channels=C, **kw)
+    torch.cuda.synchronize()
+    gpu = {k: (None if v is None else v.cpu().numpy()) for k, v in vars(gb).items()}
+
+    # oracle on the same forward state
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    campos = np.asarray(cam.camera_center, np.float32)
+    if path == "hash":
+        g = oracle.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+        fwd = oracle.render(pre, b, W, H, C, g, homotrans=sc.homotrans, ap_level=ap, beta=beta)
+        ob = oracle.render_backward(pre, b, fwd, W, H, C, g, dcol, doth, homotrans=sc.homotrans.reshape(-1, 16),
+                                    ap_level=ap, beta=beta)
+        pb = oracle.preprocess_backward(sc.means, sc.scales, sc.rotations, pre["radii"], pre["transmat"],
+                                        cam.world_view_transform, cam.full_proj_transform, W, H, ob["dtransmat"],
+                                        ob["dhomo"], ob["dnormal"], ob["dmean2D"])
+    else:
+        if path == "colors":
+            cols, extra = colors, {}
+        else:
+            cols, clamped = oracle.sh_colors(pre, sc.means, campos, shs, sh_degree)
+            extra = dict(shs=shs, sh_degree=sh_degree, campos=campos, clamped=clamped)
+        fwd = oracle.render(pre, b, W, H, C, None, colors=cols, beta=beta)
+        ob = oracle.render_backward(pre, b, fwd, W, H, C, None, dcol, doth, colors=cols, beta=beta)
+        pb = oracle.preprocess_backward(sc.means, sc.scales, sc.rotations, pre["radii"], pre["transmat"],
+                                        cam.world_view_transform, cam.full_proj_transform, W, H, ob["dtransmat"],
+                                        ob["dhomo"], ob["dnormal"], ob["dmean2D"], dcolors=ob["dcolors"], **extra)
+    np.testing.assert_array_equal(res.color.cpu().numpy(), fwd["color"])  # same forward state
+    ref = dict(dmeans3D=pb["dmeans"], dmeans2D=pb["dmean2D"], dopacity=ob["dopacity"][:, None],
+               dscales=pb["dscales"], drotations=pb["drots"])
+    if path == "hash":
+        ref["dfeatures"] = ob["dtable"].reshape(gpu["dfeatures"].shape)
+        ref["dgradsum"] = ob["gradsum"][:, None]
+    else:
+        ref["dcolors"] = ob["dcolors"]
+        if path == "sh":
+            ref["dshs"] = pb["dshs"]
+    return gpu, ref, pre
+
+
+def _compare(gpu, ref, pre):
+    vis = pre["radii"] > 0
+    for k, r in ref.items():
+        o = gpu[k]
+        assert o.shape == r.shape, (k, o.shape, r.shape)
+        assert np.isfinite(o).all(), k
+        assert np.abs(r).max() > 0, k
+        err = _rel(o, r)
+        print(f"{k}: max rel err {err:.2e}", flush=True)
+        assert err < TOL, (k, err)
+        if k not in ("dfeatures",):
+            assert not o[~vis].any(), k  # culled splats get no gradient
+
+
+@pytest.mark.parametrize("name", ["cfg1", "shell_small", "unbounded_small"])
+def test_backward_hash_parity(oracle, name):
+    sc = scene(name)
+    print(f"[case] backward hash {name} P={sc.spec.P}", flush=True)
+    _compare(*_setup(oracle, sc, "hash"))
+
+
+@pytest.mark.parametrize("path,beta", [("colors", 0.0), ("sh", 0.0), ("colors", 1.5)])
+def test_backward_colour_parity(oracle, path, beta):
+    sc = scene("shell_small")
+    print(f"[case] backward {path} beta={beta}", flush=True)
+    _compare(*_setup(oracle, sc, path, beta=beta))
+
+
+def test_backward_hash_beta_parity(oracle):
+    sc = scene("cfg1")
+    print("[case] backward hash beta=0.8", flush=True)
+    _compare(*_setup(oracle, sc, "hash", beta=0.8))
+
+
+@pytest.mark.parametrize("interp,align", [(0, False), (1, True)])
+def test_grid_encode_backward_parity(oracle, interp, align):
+    from gridencoder import GridEncoder
+    rng = np.random.default_rng(3 + interp)
+    enc = GridEncoder(3, 8, 2, 1.5, 16, 14, align_corners=align,
+                      interpolation="smoothstep" if interp else "linear").to(DEV)
+    with torch.no_grad():
+        enc.embeddings.copy_(torch.from_numpy(rng.standard_normal(tuple(enc.embeddings.shape)).astype(np.float32) * 0.2))
+    B = 5000
+    x = rng.uniform(-0.02, 1.02, (B, 3)).astype(np.float32)
+    xt = _t(x).requires_grad_(True)
+    y = enc(xt)
+    g = rng.standard_normal(tuple(y.shape)).astype(np.float32)
+    y.backward(_t(g))
+    torch.cuda.synchronize()
+    tab = enc.embeddings.detach().cpu().numpy()
+    grid = oracle.make_grid(8, 2, float(np.log2(1.5)), 16, enc._offsets_host, tab, (0.0, 1.0), False,
+                            align_corners=align, interp=interp)
+    gt, gi = oracle.grid_encode_backward(grid, x, g)
+    e_t = _rel(enc.embeddings.grad.cpu().numpy(), gt)
+    e_i = _rel(xt.grad.cpu().numpy(), gi)
+    print(f"grid encode backward: table {e_t:.2e} inputs {e_i:.2e}")
+    assert np.abs(gi).max() > 0 and np.abs(gt).max() > 0
+    assert e_t < TOL and e_i < TOL
+    oob = ((x < 0) | (x > 1)).any(1)
+    assert oob.any() and not xt.grad.cpu().numpy()[oob].any()
