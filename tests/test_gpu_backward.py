@@ -162,3 +162,52 @@ def test_grid_encode_backward_parity(oracle, interp, align):
     assert e_t < TOL and e_i < TOL
     oob = ((x < 0) | (x > 1)).any(1)
     assert oob.any() and not xt.grad.cpu().numpy()[oob].any()
+
+
+def test_autograd_through_drop_in_rasterizer():
+    """GaussianRasterizer forward + loss.backward() (the reference's training
+    call, DSRpy:174-275) lands the same gradients in .grad as a direct
+    nest_backward call, in the reference's slots (means2D gets the
+    densification statistic, ap_level the |grad| sum)."""
+    import math
+    from diff_surfel_rasterization import GaussianRasterizationSettings, GaussianRasterizer, HashGridSettings
+    from nest_splat import rasterizer as rz
+    sc = scene("cfg1")
+    sp = sc.spec
+    cam = sc.cameras[0]
+    rs = GaussianRasterizationSettings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy,
+                                       torch.zeros(3, device=DEV), 1.0, _t(cam.world_view_transform),
+                                       _t(cam.full_proj_transform), 3, _t(cam.camera_center), False, False, 0.0,
+                                       sp.contract, False)
+    hs = HashGridSettings(sp.L, math.log2(sp.per_level_scale), sp.base_res, False, 0,
+                          torch.tensor([0, sp.C, sp.C], dtype=torch.int32, device=DEV))
+    leaf = lambda a: _t(a).requires_grad_(True)
+    means, means2D = leaf(sc.means), torch.zeros(sp.P, 3, device=DEV, requires_grad=True)
+    opac, scales, rots = leaf(sc.opacity), leaf(sc.scales), leaf(sc.rotations)
+    table, ap = leaf(sc.table), leaf(sc.ap_level)
+    color, radii, allmap, _, _ = GaussianRasterizer(rs, hs)(
+        means3D=means, means2D=means2D, opacities=opac, shs=torch.zeros(sp.P, 16, 3, device=DEV), scales=scales,
+        rotations=rots, homotrans=_t(sc.homotrans), ap_level=ap, features=table, offsets=_t(sc.offsets),
+        gridrange=_t(np.asarray(sp.gridrange, np.float32)))
+    rng = np.random.default_rng(23)
+    dcol = _t(rng.standard_normal(tuple(color.shape)).astype(np.float32))
+    doth = _t(rng.standard_normal(tuple(allmap.shape)).astype(np.float32))
+    ((color * dcol).sum() + (allmap * doth).sum()).backward()
+    torch.cuda.synchronize()
+
+    settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy, cam.world_view_transform,
+                                cam.full_proj_transform, cam.camera_center, if_contract=sp.contract)
+    grid = rz.HashGridDesc(sp.L, sp.F, sp.S, sp.base_res, _t(sc.table), sc.offsets,
+                           np.asarray(sp.gridrange, np.float32))
+    res = rz.rasterize_forward(settings, grid, _t(sc.means), _t(sc.opacity), _t(sc.scales), _t(sc.rotations),
+                               homotrans=_t(sc.homotrans), ap_level=_t(sc.ap_level), channels=sp.C)
+    gb = rz.rasterize_backward(settings, grid, res, _t(sc.means), _t(sc.opacity), _t(sc.scales), _t(sc.rotations),
+                               dcol, doth, homotrans=_t(sc.homotrans), ap_level=_t(sc.ap_level), channels=sp.C)
+    torch.cuda.synchronize()
+    pairs = [(means.grad, gb.dmeans3D), (means2D.grad, gb.dmeans2D), (opac.grad, gb.dopacity),
+             (scales.grad, gb.dscales), (rots.grad, gb.drotations), (table.grad, gb.dfeatures),
+             (ap.grad, gb.dgradsum)]
+    for got, ref in pairs:
+        assert got is not None and tuple(got.shape) == tuple(ref.shape)
+        err = _rel(got.cpu().numpy(), ref.cpu().numpy())
+        assert err < 1e-5, err
