@@ -55,108 +55,193 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ void atomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
 
-// query_feature<true>: for the hit at xyz with per-channel gradient
-// gf(ch) = w * dpix[ch], adds w_corner * gf to the table at every corner of
-// every queried level, and returns dot = sum_ch feat[ch] * dpix[ch] (the
-// recomputed feature's projection on dL/dpixel) and dL/dxyz (hashgrid.h:
-// 213-299, grad_scale of :66-97).
+// Table gradient of one level for the wave (uniform control flow): lanes
+// whose hits fall in the same cell (same g) share all eight corner entries.
+// Up to kGroups cells, each cell's 8*F values are summed over its lanes with
+// a recursive-halving reduce-scatter (after it, lane l holds the sum of value
+// l / (64 / 8F)), then one atomic per entry and channel; with more cells every
+// lane adds its own values.  At coarse levels a wave's hits (one splat seen by
+// 64 neighbouring pixels) are nearly always one cell, which is where the
+// per-lane atomics of the reference pile onto the same addresses.
 template <int F>
-__device__ __forceinline__ void hash_backward(const GridParams& g, nest_i32x4 rsrc, const float xyz[3], uint32_t maxl,
-                                              float w, const float* dpix, size_t HW, float* dtable, float& dot,
-                                              float dxyz[3]) {
+__device__ __forceinline__ void scatter_level(bool on, const uint32_t gc[3], const uint32_t idx[8], const float* cv,
+                                              float* dl) {
+  constexpr int NV = 8 * F;
+  constexpr int kGroups = 4;
+  constexpr int kRep = 64 / NV;  // lanes holding each value after the halving steps
+  const uint32_t lane = threadIdx.x & 63u;
+  uint64_t rem = __ballot(on);
+  uint64_t gm[kGroups] = {0ull, 0ull, 0ull, 0ull};
+  int lead[kGroups] = {0, 0, 0, 0};
+#pragma unroll
+  for (int gi = 0; gi < kGroups; gi++) {
+    if (rem == 0ull) break;
+    const int ld = __ffsll((long long)rem) - 1;
+    const uint32_t k0 = __shfl(gc[0], ld, 64), k1 = __shfl(gc[1], ld, 64), k2 = __shfl(gc[2], ld, 64);
+    const uint64_t m = __ballot(on && gc[0] == k0 && gc[1] == k1 && gc[2] == k2) & rem;
+    gm[gi] = m;
+    lead[gi] = ld;
+    rem &= ~m;
+  }
+  if (rem != 0ull) {
+    if (on) {
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+#pragma unroll
+        for (int f = 0; f < F; f++)
+          if (cv[k * F + f] != 0.0f) atomic_add(dl + (size_t)idx[k] * F + f, cv[k * F + f]);
+    }
+    return;
+  }
+#pragma unroll
+  for (int gi = 0; gi < kGroups; gi++) {
+    if (gm[gi] == 0ull) break;
+    const bool mem = ((gm[gi] >> lane) & 1ull) != 0ull;
+    float v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) v[i] = mem ? cv[i] : 0.0f;
+    int vi = 0;
+#pragma unroll
+    for (int st = 0; (NV >> (st + 1)) >= 1; st++) {
+      const int n = NV >> (st + 1);
+      const int off = 32 >> st;
+      const bool up = (lane & (uint32_t)off) != 0u;
+#pragma unroll
+      for (int i = 0; i < n; i++) {
+        const float send = up ? v[i] : v[i + n];
+        const float keep = up ? v[i + n] : v[i];
+        v[i] = keep + __shfl_xor(send, off, 64);
+      }
+      if (up) vi += n;
+    }
+#pragma unroll
+    for (int off = kRep / 2; off >= 1; off >>= 1) v[0] += __shfl_xor(v[0], off, 64);
+    uint32_t bidx[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) bidx[k] = __shfl(idx[k], lead[gi], 64);
+    if ((lane % kRep) == 0u && v[0] != 0.0f) {
+      const int k = vi / F, f = vi % F;
+      uint32_t e = bidx[0];
+#pragma unroll
+      for (int kk = 1; kk < 8; kk++) e = (k == kk) ? bidx[kk] : e;
+      atomic_add(dl + (size_t)e * F + f, v[0]);
+    }
+  }
+}
+
+// query_feature<true> for the wave's hits at grid coordinates u (lanes with
+// lane_levels 0 take part with nothing): recomputes the features' projection
+// dot = sum_ch feat[ch] * dpix[ch], adds w_corner * w * dpix to the table at
+// every corner of every level below lane_levels, and returns dL/dxyz
+// (hashgrid.h:213-299; grad_scale of :66-97).
+template <int F>
+__device__ __forceinline__ void hash_backward_wave(const GridParams& g, nest_i32x4 rsrc, const float u[3],
+                                                   float grad_scale, uint32_t lane_levels, float w,
+                                                   const float* dpix, size_t HW, float* dtable, float& dot,
+                                                   float dxyz[3]) {
   dot = 0.0f;
   dxyz[0] = dxyz[1] = dxyz[2] = 0.0f;
-  float u[3];
-  float grad_scale;
+  const LevelTable& lv = g.lv;
+  for (int l = 0; l < (int)g.L; l++) {
+    const bool on = (uint32_t)l < lane_levels;
+    if (__ballot(on) == 0ull) break;  // levels are a prefix per lane
+    const float scale = lv.scale[l];
+    float cv[8 * F];
+#pragma unroll
+    for (int i = 0; i < 8 * F; i++) cv[i] = 0.0f;
+    uint32_t gc[3] = {0u, 0u, 0u};
+    LevelCorners cn;
+#pragma unroll
+    for (int k = 0; k < 8; k++) cn.idx[k] = 0u;
+    if (on) {
+      float pos[3], der[3];
+#pragma unroll
+      for (int d = 0; d < 3; d++) {
+        const float x = u[d] * scale + g.pos_offset;
+        gc[d] = f2u_sat(x);
+        pos[d] = x - (float)gc[d];
+        if (g.interp == 1) {
+          der[d] = 6.0f * pos[d] * (1.0f - pos[d]);
+          pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
+        } else {
+          der[d] = 1.0f;
+        }
+      }
+      level_corners<F, false>(lv, l, g.pos_offset, 0u, u, cn);  // indices of the same cell
+      cn.wx[0] = 1 - pos[0]; cn.wx[1] = pos[0];
+      cn.wy[0] = 1 - pos[1]; cn.wy[1] = pos[1];
+      cn.wz[0] = 1 - pos[2]; cn.wz[1] = pos[2];
+      float vals[8][F];
+      corners_load<F, false>(rsrc, cn, vals);
+      float dp[F], gf[F], feat[F];
+#pragma unroll
+      for (int f = 0; f < F; f++) {
+        dp[f] = dpix[(size_t)(l * F + f) * HW];
+        gf[f] = w * dp[f];
+        feat[f] = 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const float wk = (1.0f * cn.wx[k & 1]) * cn.wy[(k >> 1) & 1] * cn.wz[k >> 2];
+#pragma unroll
+        for (int f = 0; f < F; f++) {
+          feat[f] = fmaf(wk, vals[k][f], feat[f]);
+          cv[k * F + f] = wk * gf[f];
+        }
+      }
+#pragma unroll
+      for (int f = 0; f < F; f++) dot += feat[f] * dp[f];
+      // dy/dxyz: corner pairs along each axis (hashgrid.h:241-276)
+#pragma unroll
+      for (int gd = 0; gd < 3; gd++) {
+        float rg[F];
+#pragma unroll
+        for (int f = 0; f < F; f++) rg[f] = 0.0f;
+#pragma unroll
+        for (int idx = 0; idx < 4; idx++) {
+          float wgt = scale * grad_scale;
+          int kl = 0;
+#pragma unroll
+          for (int nd = 0; nd < 2; nd++) {
+            const int d = (nd >= gd) ? nd + 1 : nd;
+            const int bit = (idx >> nd) & 1;
+            wgt *= bit ? pos[d] : 1 - pos[d];
+            kl |= bit << d;
+          }
+          const int kr = kl | (1 << gd);
+#pragma unroll
+          for (int f = 0; f < F; f++) rg[f] += wgt * (vals[kr][f] - vals[kl][f]) * der[gd];
+        }
+#pragma unroll
+        for (int f = 0; f < F; f++) dxyz[gd] += gf[f] * rg[f];
+      }
+    }
+    scatter_level<F>(on, gc, cn.idx, cv, dtable + (size_t)lv.base[l] * F);
+  }
+}
+
+// Grid coordinate of xyz and the scalar grad_scale (hashgrid.h:66-97);
+// returns false when the point is outside the grid (no features, no gradient).
+__device__ __forceinline__ bool grid_coord_bwd(const GridParams& g, const float xyz[3], float u[3],
+                                               float& grad_scale) {
   if (!g.contract) {
 #pragma unroll
     for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmin) * g.inv_size;
-    if (u[0] < 0 || u[0] > 1 || u[1] < 0 || u[1] > 1 || u[2] < 0 || u[2] > 1) return;
     grad_scale = g.inv_size;
-  } else {
-#pragma unroll
-    for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmid) * g.inv_size;
-    const float nrm = sqrtf(u[0] * u[0] + u[1] * u[1] + u[2] * u[2]);
-    const float inv_nrm = 1.0f / nrm;
-    const float st = (nrm <= 1.0f) ? 1.0f : (2.0f - inv_nrm) * inv_nrm;
-#pragma unroll
-    for (int d = 0; d < 3; d++) {
-      u[d] = st * u[d];
-      u[d] = (u[d] + 2.0f) * 0.25f;
-    }
-    grad_scale = g.inv_size * st * 0.25f;
+    return !(u[0] < 0 || u[0] > 1 || u[1] < 0 || u[1] > 1 || u[2] < 0 || u[2] > 1);
   }
-  const LevelTable& lv = g.lv;
-  for (int l = 0; l < (int)maxl; l++) {
-    const float scale = lv.scale[l];
-    float pos[3], der[3];
-    uint32_t gc[3];
 #pragma unroll
-    for (int d = 0; d < 3; d++) {
-      const float x = u[d] * scale + g.pos_offset;
-      gc[d] = f2u_sat(x);
-      pos[d] = x - (float)gc[d];
-      if (g.interp == 1) {
-        der[d] = 6.0f * pos[d] * (1.0f - pos[d]);
-        pos[d] = pos[d] * pos[d] * (3.0f - 2.0f * pos[d]);
-      } else {
-        der[d] = 1.0f;
-      }
-    }
-    LevelCorners cn;
-    level_corners<F, false>(lv, l, g.pos_offset, 0u, u, cn);  // indices of the same cell
-    // weights of the (possibly smoothstepped) fractions, corner order
-    cn.wx[0] = 1 - pos[0]; cn.wx[1] = pos[0];
-    cn.wy[0] = 1 - pos[1]; cn.wy[1] = pos[1];
-    cn.wz[0] = 1 - pos[2]; cn.wz[1] = pos[2];
-    float vals[8][F];
-    corners_load<F, false>(rsrc, cn, vals);
-    float dp[F], gf[F];
+  for (int d = 0; d < 3; d++) u[d] = (xyz[d] - g.vmid) * g.inv_size;
+  const float nrm = sqrtf(u[0] * u[0] + u[1] * u[1] + u[2] * u[2]);
+  const float inv_nrm = 1.0f / nrm;
+  const float st = (nrm <= 1.0f) ? 1.0f : (2.0f - inv_nrm) * inv_nrm;
 #pragma unroll
-    for (int f = 0; f < F; f++) {
-      dp[f] = dpix[(size_t)(l * F + f) * HW];
-      gf[f] = w * dp[f];
-    }
-    float feat[F];
-#pragma unroll
-    for (int f = 0; f < F; f++) feat[f] = 0.0f;
-    float* dl = dtable + (size_t)lv.base[l] * F;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const float wk = (1.0f * cn.wx[k & 1]) * cn.wy[(k >> 1) & 1] * cn.wz[k >> 2];
-#pragma unroll
-      for (int f = 0; f < F; f++) {
-        feat[f] = fmaf(wk, vals[k][f], feat[f]);
-        atomic_add(dl + (size_t)cn.idx[k] * F + f, wk * gf[f]);
-      }
-    }
-#pragma unroll
-    for (int f = 0; f < F; f++) dot += feat[f] * dp[f];
-    // dy/dxyz: corner pairs along each axis (hashgrid.h:241-276)
-#pragma unroll
-    for (int gd = 0; gd < 3; gd++) {
-      float rg[F];
-#pragma unroll
-      for (int f = 0; f < F; f++) rg[f] = 0.0f;
-#pragma unroll
-      for (int idx = 0; idx < 4; idx++) {
-        float wgt = scale * grad_scale;
-        int kl = 0;
-#pragma unroll
-        for (int nd = 0; nd < 2; nd++) {
-          const int d = (nd >= gd) ? nd + 1 : nd;
-          const int bit = (idx >> nd) & 1;
-          wgt *= bit ? pos[d] : 1 - pos[d];
-          kl |= bit << d;
-        }
-        const int kr = kl | (1 << gd);
-#pragma unroll
-        for (int f = 0; f < F; f++) rg[f] += wgt * (vals[kr][f] - vals[kl][f]) * der[gd];
-      }
-#pragma unroll
-      for (int f = 0; f < F; f++) dxyz[gd] += gf[f] * rg[f];
-    }
+  for (int d = 0; d < 3; d++) {
+    u[d] = st * u[d];
+    u[d] = (u[d] + 2.0f) * 0.25f;
   }
+  grad_scale = g.inv_size * st * 0.25f;
+  return true;
 }
 
 template <int F, bool kHash>
@@ -257,14 +342,15 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
       float gT[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0}, gH[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
       float gM[2] = {0.0f, 0.0f}, gN[3] = {0.0f, 0.0f, 0.0f}, gO = 0.0f, gS = 0.0f;
       float wcol = 0.0f;  // dchannel_dcolor of the colour path
+      float wgt = 0.0f, dot = 0.0f;
+      float dxyz[3] = {0.0f, 0.0f, 0.0f};
+      float u[3] = {0.0f, 0.0f, 0.0f}, grad_scale = 0.0f;
+      uint32_t lane_levels = 0u;
       if (act) {
         T = T / (1.f - alpha);
-        const float wgt = alpha * T;
-        float dot;
-        float dxyz[3] = {0.0f, 0.0f, 0.0f};
+        wgt = alpha * T;
         if constexpr (!kHash) {
           const float* col = p.colors + (size_t)id * C;
-          dot = 0.0f;
           for (int ch = 0; ch < C; ch++) dot += col[ch] * dpix[(size_t)ch * HW];
           wcol = wgt;
         } else {
@@ -280,7 +366,16 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
           gS = wgt * sum_abs;
           const uint32_t ap = __float_as_uint(q3.w);
           const uint32_t maxl = ap < g.L ? ap : g.L;
-          hash_backward<F>(g, rsrc, xyz, maxl, wgt, dpix, HW, p.dtable, dot, dxyz);
+          lane_levels = grid_coord_bwd(g, xyz, u, grad_scale) ? maxl : 0u;
+        }
+      }
+      if constexpr (kHash) {
+        // every lane takes part (cross-lane sums inside); lanes without a hit have no levels
+        if (__ballot(lane_levels > 0u) != 0ull)
+          hash_backward_wave<F>(g, rsrc, u, grad_scale, lane_levels, wgt, dpix, HW, p.dtable, dot, dxyz);
+      }
+      if (act) {
+        if constexpr (kHash) {
           if (use3d) {
             gH[0] = dxyz[0] * s[0]; gH[1] = dxyz[1] * s[0]; gH[2] = dxyz[2] * s[0];
             gH[3] = dxyz[0] * s[1]; gH[4] = dxyz[1] * s[1]; gH[5] = dxyz[2] * s[1];
