@@ -153,6 +153,9 @@ def main():
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="before the frames, copy this many MiB device-to-device (a plain copy kernel of known "
                          "size whose FETCH_SIZE / WRITE_SIZE scale the render kernel's counters)")
+    ap.add_argument("--backward", type=int, default=0, metavar="K",
+                    help="after the timed forward frames, time K backward passes (nest_backward) of the last frame "
+                         "with random output gradients and report backward_ms (not part of the metric)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -266,6 +269,20 @@ def main():
                      "algorithmic_bytes": alg, "render_ms": round(render_ms, 4)},
         "cpu_baseline": None,
     }
+    if args.backward > 0:
+        gen = torch.Generator(device=dev).manual_seed(0)
+        dcol = torch.randn(tuple(res.color.shape), generator=gen, device=dev)
+        doth = torch.randn(tuple(res.others.shape), generator=gen, device=dev)
+        bwd = lambda: rz.rasterize_backward(settings, grid, res, means, opac, scales, rots, dcol, doth, homotrans=homo,
+                                            ap_level=ap_level, channels=spec.C)
+        bwd()
+        torch.cuda.synchronize()
+        b0 = time.perf_counter()
+        for _ in range(args.backward):
+            bwd()
+        torch.cuda.synchronize()
+        out["backward_ms"] = round((time.perf_counter() - b0) / args.backward * 1e3, 3)
+        log(f"[bench] backward: {out['backward_ms']} ms")
     if not args.no_cpu_baseline:
         threads = len(os.sched_getaffinity(0))
         log(f"[bench] cpu baseline on {threads} threads ...")

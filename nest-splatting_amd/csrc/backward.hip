@@ -57,7 +57,7 @@ __device__ __forceinline__ void atomic_add(float* p, float v) { unsafeAtomicAdd(
 
 // Table gradient of one level for the wave (uniform control flow): lanes
 // whose hits fall in the same cell (same g) share all eight corner entries.
-// Up to kGroups cells, each cell's 8*F values are summed over its lanes with
+// Up to kGroups (8) cells, each cell's 8*F values are summed over its lanes with
 // a recursive-halving reduce-scatter (after it, lane l holds the sum of value
 // l / (64 / 8F)), then one atomic per entry and channel; with more cells every
 // lane adds its own values.  At coarse levels a wave's hits (one splat seen by
@@ -67,12 +67,12 @@ template <int F>
 __device__ __forceinline__ void scatter_level(bool on, const uint32_t gc[3], const uint32_t idx[8], const float* cv,
                                               float* dl) {
   constexpr int NV = 8 * F;
-  constexpr int kGroups = 4;
+  constexpr int kGroups = 8;
   constexpr int kRep = 64 / NV;  // lanes holding each value after the halving steps
   const uint32_t lane = threadIdx.x & 63u;
   uint64_t rem = __ballot(on);
-  uint64_t gm[kGroups] = {0ull, 0ull, 0ull, 0ull};
-  int lead[kGroups] = {0, 0, 0, 0};
+  uint64_t gm[kGroups] = {};
+  int lead[kGroups] = {};
 #pragma unroll
   for (int gi = 0; gi < kGroups; gi++) {
     if (rem == 0ull) break;
