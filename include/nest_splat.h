@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 5
+#define NEST_ABI_VERSION 6
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -74,7 +74,7 @@ typedef struct nest_raster_settings {
  * host copies of the reference's device tensors. */
 typedef struct nest_hashgrid {
   uint32_t struct_size;
-  uint32_t levels;            /* L queried; 0 selects the colours_precomp path */
+  uint32_t levels;            /* L queried; 0 selects the colours_precomp path in mode 0 */
   uint32_t level_dim;         /* F: 1, 2, 4 or 8 */
   float log2_scale;           /* S = log2(per_level_scale) */
   uint32_t base_resolution;   /* H */
@@ -85,7 +85,32 @@ typedef struct nest_hashgrid {
   int64_t table_rows;         /* rows of the table; must be >= offsets[levels] */
   int32_t offsets[NEST_MAX_LEVELS + 1];
   float gridrange[2];
+  /* Feature composition of the render loop, the reference's render_mode
+   * argument (DSRpy:393, CR/forward.cu:1127) with its packed level argument
+   * decoded by the caller (GR:217-242, :334-405):
+   *   NEST_MODE_BASELINE (0): the grid's `levels` levels, or the colour path
+   *     when levels == 0;
+   *   NEST_MODE_CAT (4): hybrid_levels*level_dim per-splat features
+   *     (colors_precomp rows of that width), then the grid's `levels` levels
+   *     (CR/forward.cu:1218-1282; the reference counts those levels from the
+   *     offsets);
+   *   NEST_MODE_ADAPTIVE_CAT_FAST (13), | NEST_MODE_INFERENCE for inference:
+   *     colors_precomp rows of total_levels*level_dim features plus a blend
+   *     weight; the first hybrid_levels*level_dim channels come from the row,
+   *     the next `levels` levels from the grid, blended with the row in
+   *     training; in inference a splat with weight > 0.5 takes its row
+   *     without a grid lookup (CR/forward.cu:965-1101).
+   * Modes 4 and 13 need level_dim 2, 4 or 8 and at most 64 channels of
+   * per-splat plus grid features; `levels` may be 0 there. */
+  int32_t render_mode;
+  uint32_t hybrid_levels;
+  uint32_t total_levels;
 } nest_hashgrid;
+
+#define NEST_MODE_BASELINE 0
+#define NEST_MODE_CAT 4
+#define NEST_MODE_ADAPTIVE_CAT_FAST 13
+#define NEST_MODE_INFERENCE 0x100
 
 /* Splat attributes (device, float32, contiguous), as the reference passes them
  * to _C.rasterize_gaussians (DSRpy:105-146). */
@@ -194,7 +219,7 @@ int nest_image_layout(int32_t width, int32_t height, size_t offsets[NEST_IMG_FIE
 /* ---- forward rasterizer -------------------------------------------------
  * Together these two calls are RasterizeGaussiansCUDA
  * (DSR/rasterize_points.cu:40-242) / CudaRasterizer::Rasterizer::forward
- * (CR/rasterizer_impl.cu:255-440) for render_mode 0, split at the
+ * (CR/rasterizer_impl.cu:255-440) for render_mode 0, 4 and 13, split at the
  * num_rendered read-back (CR/rasterizer_impl.cu:359) so that the caller can
  * size the binning workspace in between, as the resize callbacks
  * (DSR/rasterize_points.cu:31-37) do in the reference.
@@ -208,9 +233,11 @@ int nest_forward_geometry(const nest_raster_settings *settings, const nest_splat
 
 /* nest_forward_render: duplicateWithKeys (CR/rasterizer_impl.cu:70-111),
  * the radix sort on (tile|depth) keys (:378-386), identifyTileRanges
- * (:173-195, :388) and renderCUDAsurfelForward<C, mode 0>
- * (CR/forward.cu:639-2049, dispatch :2052-2158).  out_color channels must be
- * >= levels*level_dim; channels past levels*level_dim are written as zero. */
+ * (:173-195, :388) and renderCUDAsurfelForward<C, render_mode>
+ * (CR/forward.cu:639-2049, dispatch :2052-2158).  out_color channels must
+ * cover the features of the mode (levels*level_dim in mode 0, plus
+ * hybrid_levels*level_dim in mode 4, total_levels*level_dim in mode 13);
+ * channels past them are written as zero. */
 int nest_forward_render(const nest_raster_settings *settings, const nest_hashgrid *grid,
                         const nest_splats *splats, void *geom_ws, size_t geom_bytes,
                         void *binning_ws, size_t binning_bytes, void *image_ws, size_t image_bytes,

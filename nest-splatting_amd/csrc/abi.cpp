@@ -185,6 +185,43 @@ bool sh_colours(const nest_splats* sp) { return sp->shs && !sp->colors_precomp; 
 int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const nest_splats* sp, int channels,
                GridParams& g) {
   int rc = NEST_OK;
+  const int base_mode = gr->render_mode & 0xFF;
+  if ((gr->render_mode & ~0x1FF) != 0 || (base_mode != NEST_MODE_BASELINE && base_mode != NEST_MODE_CAT &&
+                                          base_mode != NEST_MODE_ADAPTIVE_CAT_FAST) ||
+      ((gr->render_mode & NEST_MODE_INFERENCE) && base_mode != NEST_MODE_ADAPTIVE_CAT_FAST))
+    return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: supported are 0, 4, 13 and 13 | 0x100", gr->render_mode);
+  const bool mix = base_mode != NEST_MODE_BASELINE;
+  if (mix) {
+    const uint32_t F = gr->level_dim, hyb = gr->hybrid_levels;
+    if (F != 2 && F != 4 && F != 8)
+      return fail(NEST_ERR_UNSUPPORTED, "render_mode %d needs level_dim 2, 4 or 8 (got %u)", gr->render_mode, F);
+    if (gr->levels > NEST_MAX_LEVELS || hyb > NEST_MAX_LEVELS || gr->total_levels > NEST_MAX_LEVELS)
+      return fail(NEST_ERR_UNSUPPORTED, "levels, hybrid_levels and total_levels must be <= %d", NEST_MAX_LEVELS);
+    uint32_t feat = 0;
+    if (base_mode == NEST_MODE_CAT) {
+      feat = (hyb + gr->levels) * F;
+    } else {
+      if (hyb + gr->levels > gr->total_levels)
+        return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode 13: hybrid_levels + levels (%u + %u) exceed total_levels %u",
+                    hyb, gr->levels, gr->total_levels);
+      feat = gr->total_levels * F;
+    }
+    if (feat > 64u)
+      return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: at most 64 feature channels (got %u)", gr->render_mode, feat);
+    if ((uint32_t)channels < feat)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "out_color has %d channels, render_mode %d produces %u", channels,
+                  gr->render_mode, feat);
+    if (sp->P > 0) {
+      if (!sp->homotrans) return fail(NEST_ERR_INVALID_ARGUMENT, "homotrans is required in render_mode %d", gr->render_mode);
+      if (!sp->colors_precomp && (base_mode == NEST_MODE_ADAPTIVE_CAT_FAST || hyb > 0))
+        return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode %d needs the per-splat features in colors_precomp",
+                    gr->render_mode);
+      // the render queue packs the splat id into 25 bits
+      if (sp->P >= (1 << 25))
+        return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: at most %d splats", gr->render_mode, (1 << 25) - 1);
+    }
+    g.F = F;
+  }
   if (gr->levels > 0) {
     if (gr->level_dim != 1 && gr->level_dim != 2 && gr->level_dim != 4 && gr->level_dim != 8)
       return fail(NEST_ERR_UNSUPPORTED, "level_dim must be 1, 2, 4 or 8 (got %u)", gr->level_dim);
@@ -238,7 +275,7 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
     for (uint32_t l = nd; l < g.L; l++) structured = structured && (g.lv.flags[l] & 3u) == 3u;
     g.structured = structured ? 1u : 0u;
     g.n_dense = nd;
-  } else {
+  } else if (!mix) {
     if (sp->P > 0 && !sp->colors_precomp && !sp->shs)
       return fail(NEST_ERR_INVALID_ARGUMENT, "levels == 0 selects the colour path, which needs colors_precomp or shs");
     // SH colours are RGB (NUM_CHANNELS, CR/rasterizer_impl.cu:320-323)
@@ -411,6 +448,25 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   rp.beta = rs->beta;
   rp.max_intersections = rs->max_intersections;
   if ((rc = setup_grid(rs, gr, sp, out->channels, rp.grid))) return rc;
+  if ((gr->render_mode & 0xFF) != NEST_MODE_BASELINE) {
+    // per-splat features ahead of the grid's (CR/forward.cu:965-1101, :1218-1282)
+    const int F = (int)gr->level_dim;
+    rp.mix = 1;
+    rp.hyb = (int)gr->hybrid_levels;
+    rp.pgd = rp.hyb * F;
+    rp.wslot = -1;
+    if ((gr->render_mode & 0xFF) == NEST_MODE_CAT) {
+      rp.cstride = rp.pgd;
+    } else {
+      const int tdim = (int)gr->total_levels * F;
+      rp.cstride = tdim + 1;
+      rp.wslot = tdim;
+      rp.infer = (gr->render_mode & NEST_MODE_INFERENCE) ? 1 : 0;
+      rp.blend = rp.infer ? 0 : 1;
+      rp.m13 = 1;
+      rp.nfast = gr->total_levels - gr->hybrid_levels;
+    }
+  }
 
   size_t go[NEST_GEOM_FIELDS], gneed = 0, bo[NEST_BIN_FIELDS], bneed = 0, io[NEST_IMG_FIELDS], ineed = 0;
   nest_geom_layout(sp->P, go, &gneed);
@@ -647,6 +703,9 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
     return fail(NEST_ERR_INVALID_ARGUMENT, "nest_hashgrid missing or struct_size mismatch");
   if (!io || io->struct_size != sizeof(nest_backward_io))
     return fail(NEST_ERR_INVALID_ARGUMENT, "nest_backward_io missing or struct_size mismatch");
+  if (gr->render_mode != NEST_MODE_BASELINE)
+    return fail(NEST_ERR_UNSUPPORTED, "backward: render_mode %d is forward-only here (mode 0 has a backward)",
+                gr->render_mode);
   const int C = io->channels;
   if (C < 1 || C > 64) return fail(NEST_ERR_UNSUPPORTED, "backward: channels must be in [1, 64] (got %d)", C);
   if (!io->dL_dout_color || !io->dL_dout_others)

@@ -107,11 +107,23 @@ struct RenderParams {
   const uint32_t* ranges;     // [tiles][2]
   const uint32_t* point_list;
   const float* records;       // [P][32]
-  const float* colors;        // [P][C] colour path
+  const float* colors;        // [P][C] colour path; [P][cstride] per-splat features (mix)
   float* out_color;
   float* out_others;
   float* final_T;
   uint32_t* n_contrib;
+  // Per-splat features ahead of the grid's (render modes 4 and 13): channel
+  // c < pgd of a hit is row[c] (times the row's weight with blend); grid
+  // level l lands on channels pgd + l*F.
+  int mix;                    // 0: mode 0
+  int hyb;                    // per-splat levels ahead of the grid's
+  int pgd;                    // hyb * F
+  int cstride;                // floats per row of colors
+  int wslot;                  // index of the blend weight in a row (mode 13), else -1
+  int infer;                  // mode 13 inference: weight > 0.5 takes the row without the grid
+  int blend;                  // mode 13 training: row * weight + grid * (1 - weight)
+  int m13;                    // mode 13: a hit updates no appearance colour and no last contributor
+  uint32_t nfast;             // levels of the row past pgd that a weight > 0.5 hit takes
   GridParams grid;
 };
 

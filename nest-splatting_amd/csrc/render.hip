@@ -1,11 +1,13 @@
 // Per-tile compositing of 2D surfels with a hash-grid lookup at every
 // accepted ray/splat hit.
 //
-// Semantics: renderCUDAsurfelForward<C, mode 0> of
+// Semantics: renderCUDAsurfelForward<C, render_mode> of
 // submodules/diff-surfel-rasterization/cuda_rasterizer/forward.cu:639-2049
 // (state :719-785, batch fetch :791-831, intersection loop :834-971, case 0
 // :1127-1145, accumulation :1914-1916, appearance colour :1945-1957, output
-// :2008-2048), and query_feature (hashgrid.h:53-212).
+// :2008-2048), and query_feature (hashgrid.h:53-212); render modes 4
+// (hybrid_features, :1218-1282) and 13 (adaptive_cat_fast, :965-1101) in the
+// kMix instantiations.
 //
 // Layout: one 256-thread workgroup per 16x16 tile, one lane per pixel (four
 // 64-lane waves of 16x4 pixels).  The tile's sorted splats are staged in LDS
@@ -216,6 +218,63 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
   qn -= take;
 }
 
+// Drain round of the per-splat feature modes (render modes 4 and 13): every
+// lane with a pending hit takes its oldest one.  Output level l holds grid
+// level l - hyb.  A queued hit's meta word is splat id << 7 | fast << 6 |
+// grid levels to look up; its feature at grid level gl is
+//   fast (weight > 0.5 in inference)  the row's own features, gl < nfast;
+//   blend (training)                  fmaf(wt, row, (1 - wt) * grid), gl < L,
+//                                     grid = 0 past the lookup count;
+//   otherwise                         the grid, gl < the lookup count;
+// and acc = fmaf(feature, w, acc) in queue order, as the other drains.
+template <int F, int NACC, bool kHalf, bool kStructured>
+__device__ __forceinline__ void drain_mixed(const RenderParams& p, nest_i32x4 rsrc, float4 (*hq)[kRenderThreads],
+                                            uint32_t (*hm)[kRenderThreads], int& qhead, int& qn, float* acc) {
+  if (qn > 0) {
+    const GridParams& g = p.grid;
+    const float4 e = hq[qhead][threadIdx.x];
+    const uint32_t meta = hm[qhead][threadIdx.x];
+    const uint32_t nhash = meta & 63u;
+    const bool fast = (meta & 64u) != 0u;
+    const float* row = p.colors + (size_t)(meta >> 7) * (uint32_t)p.cstride;
+    const float wt = p.wslot >= 0 ? row[p.wslot] : 0.0f;
+    const uint32_t nfeat = fast ? p.nfast : (p.blend ? g.L : nhash);
+    row += p.pgd;
+    const float u[3] = {e.x, e.y, e.z};
+    const LevelQuadPtr lqb = (LevelQuadPtr)g.lq;
+#pragma unroll
+    for (int l = 0; l < NACC / F; l++) {
+      const int gl = l - p.hyb;
+      if (gl < 0) continue;
+      if ((uint32_t)gl < nfeat) {
+        float h[F];
+#pragma unroll
+        for (int f = 0; f < F; f++) h[f] = 0.0f;
+        if (!fast && (uint32_t)gl < nhash) {
+          LevelCorners cn;
+          nest_u32x4 rec = {0u, 0u, 0u, 0u};
+          if constexpr (kStructured) rec = level_record(lqb, gl);
+          level_setup<F, kHalf, kStructured>(g, rec, gl, u, cn);
+          float vals[8][F];
+          corners_load<F, kHalf>(rsrc, cn, vals);
+          corners_sum<F>(cn, vals, h);
+        }
+#pragma unroll
+        for (int f = 0; f < F; f++) {
+          float v = h[f];
+          if (fast)
+            v = row[gl * F + f];
+          else if (p.blend)
+            v = fmaf(wt, row[gl * F + f], (1.0f - wt) * h[f]);
+          acc[l * F + f] = fmaf(v, e.w, acc[l * F + f]);
+        }
+      }
+    }
+    qhead = (qhead + 1) & (kQueue - 1);
+    qn--;
+  }
+}
+
 // Exact ray/surfel test of pixel (pxf, pyf) against a record's chunks 0-2
 // and its rho cut (CR/forward.cu:834-900 for the 2DGS kernel_type 0): the
 // homogeneous plane intersection, the 3D/2D rho choice, the near test on the
@@ -314,13 +373,18 @@ __device__ __forceinline__ uint8_t hit_levels(bool oob, uint32_t ap, uint32_t L)
 // LDS (32 KB of staged records + 17 KB of queue) allows three workgroups per
 // CU; amdgpu_waves_per_eu(3) gives the matching 168-VGPR budget, which holds
 // 64 accumulators and eight in-flight 16-byte corner loads.
-template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false>
+//
+// kMix: render modes 4 and 13 (per-splat features ahead of the grid's); the
+// queue then carries a 32-bit meta word per hit (drain_mixed) in place of
+// the level count, 53 KB of LDS in all.
+template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, bool kMix = false>
 __global__ void __launch_bounds__(kRenderThreads) __attribute__((amdgpu_waves_per_eu(3, 8)))
 render_kernel(const RenderParams p) {
   __shared__ float4 srec[kRecChunks][kBatch];
   __shared__ float4 hq[kHash ? kQueue : 1][kRenderThreads];
-  __shared__ uint8_t hl[kHash ? kQueue : 1][kRenderThreads];
-  __shared__ uint8_t isrc[kHash ? kRenderThreads : 1];  // compacted-drain item tables, 64 per wave
+  __shared__ uint8_t hl[kHash && !kMix ? kQueue : 1][kRenderThreads];
+  __shared__ uint32_t hm[kMix ? kQueue : 1][kMix ? kRenderThreads : 1];
+  __shared__ uint8_t isrc[kHash && !kMix ? kRenderThreads : 1];  // compacted-drain item tables, 64 per wave
 
   const uint32_t tile = xcd_tile(blockIdx.x, p.ntiles);
   const uint32_t tx = tile % p.gx, ty = tile / p.gx;
@@ -418,32 +482,64 @@ render_kernel(const RenderParams p) {
           for (int c = 0; c < NACC; c++)
             if (c < p.C) acc[c] = fmaf(col[c], w, acc[c]);
         } else {
-          float xyz[3];
-          hit_world(srec[4][j], srec[5][j], srec[6][j], hit, xyz);
-          pos_x += w * xyz[0];
-          pos_y += w * xyz[1];
-          pos_z += w * xyz[2];
           const uint32_t ap = __float_as_uint(q3.w);
-          float u[3];
-          bool oob;
-          grid_coord(g, xyz, u, oob);
-          const int slot = (qhead + qn) & (kQueue - 1);
-          hq[slot][threadIdx.x] = make_float4(u[0], u[1], u[2], w);
-          hl[slot][threadIdx.x] = hit_levels(oob, ap, L);
-          qn++;
-          float apc0, apc1;
-          if (ap <= 4u) {
-            apc0 = (float)((double)(uint32_t)(ap - 2u) * 0.5);
-            apc1 = 1.0f;
-          } else {
-            apc0 = 1.0f;
-            apc1 = (float)(1.0 - (double)(uint32_t)(ap - 4u) * 0.5);
+          bool fast = false, enq = true;
+          uint32_t meta = 0u;
+          if constexpr (kMix) {
+            // The splat (and so its row) is uniform across the wave: scalar loads.
+            const uint32_t id = __builtin_amdgcn_readfirstlane(__float_as_uint(srec[6][j].z));
+            const float* row = p.colors + (size_t)id * (uint32_t)p.cstride;
+            float wt = 1.0f;
+            if (p.wslot >= 0) {
+              wt = row[p.wslot];
+              fast = p.infer && wt > 0.5f;
+            }
+            // Per-splat channels at once; a fast hit's grid-level channels
+            // too when no earlier hit of the pixel is pending.
+            enq = !(fast && qn == 0);
+            const int ndirect = enq ? p.pgd : p.pgd + (int)p.nfast * F;
+#pragma unroll
+            for (int c = 0; c < NACC; c++)
+              if (c < ndirect) acc[c] = fmaf(p.blend ? row[c] * wt : row[c], w, acc[c]);
+            meta = id << 7 | (fast ? 64u : 0u);
           }
-          vis0 += apc0 * w;
-          vis1 += apc1 * w;
+          float u[3] = {0.0f, 0.0f, 0.0f};
+          uint32_t nh = 0u;
+          if (!fast) {
+            float xyz[3];
+            hit_world(srec[4][j], srec[5][j], srec[6][j], hit, xyz);
+            pos_x += w * xyz[0];
+            pos_y += w * xyz[1];
+            pos_z += w * xyz[2];
+            bool oob;
+            grid_coord(g, xyz, u, oob);
+            nh = hit_levels(oob, ap, L);
+          }
+          if (enq) {
+            const int slot = (qhead + qn) & (kQueue - 1);
+            hq[slot][threadIdx.x] = make_float4(u[0], u[1], u[2], w);
+            if constexpr (kMix)
+              hm[slot][threadIdx.x] = meta | nh;
+            else
+              hl[slot][threadIdx.x] = (uint8_t)nh;
+            qn++;
+          }
+          if (!kMix || !p.m13) {
+            float apc0, apc1;
+            if (ap <= 4u) {
+              apc0 = (float)((double)(uint32_t)(ap - 2u) * 0.5);
+              apc1 = 1.0f;
+            } else {
+              apc0 = 1.0f;
+              apc1 = (float)(1.0 - (double)(uint32_t)(ap - 4u) * 0.5);
+            }
+            vis0 += apc0 * w;
+            vis1 += apc1 * w;
+          }
         }
         T = test_T;
-        last_contributor = contributor;
+        // render mode 13 leaves the hit loop before the last-contributor update (CR/forward.cu:1097-1100)
+        if (!kMix || !p.m13) last_contributor = contributor;
       } while (false);
       }
       j++;
@@ -454,7 +550,9 @@ render_kernel(const RenderParams p) {
     if constexpr (kHash) {
       // whenever a lane is full; at the end, until every queue is empty
       if (__ballot(qn == kQueue) || (last && __ballot(qn > 0))) {
-        if constexpr (F <= 4)
+        if constexpr (kMix)
+          drain_mixed<F, NACC, kHalf, kStructured>(p, rsrc, hq, hm, qhead, qn, acc);
+        else if constexpr (F <= 4)
           drain_compact<F, NACC, kHalf, kStructured>(g, rsrc, hq, hl, isrc + wid * kWaveLanes, qhead, qn, acc);
         else
           drain_round<F, NACC, kHalf, kStructured>(g, rsrc, hq, hl, qhead, qn, acc);
@@ -496,10 +594,10 @@ render_kernel(const RenderParams p) {
   O[pid + 13 * HW] = 0.0f;  // the third appearance channel only ever adds 0 * w
 }
 
-template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false>
+template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, bool kMix = false>
 static hipError_t launch_one(const RenderParams& p, hipStream_t s) {
-  hipLaunchKernelGGL((render_kernel<F, NACC, kHash, kHalf, kStructured>), dim3(p.ntiles), dim3(kRenderThreads), 0, s,
-                     p);
+  hipLaunchKernelGGL((render_kernel<F, NACC, kHash, kHalf, kStructured, kMix>), dim3(p.ntiles), dim3(kRenderThreads),
+                     0, s, p);
   return hipGetLastError();
 }
 
@@ -528,9 +626,24 @@ __global__ void level_quads_kernel(LevelQuads lq, uint32_t L, LevelQuad* dst) {
     if ((uint32_t)l < L) dst[l] = lq.q[l];
 }
 
+// Accumulators of the per-splat feature modes: the output levels the mode
+// writes (hyb + L, or the row's levels in mode 13), 32 or 64 channels.
+template <int F, bool kHalf, bool kStructured>
+static hipError_t launch_mix_levels(const RenderParams& p, hipStream_t s) {
+  const uint32_t need = (uint32_t)p.pgd + (p.grid.L > p.nfast ? p.grid.L : p.nfast) * (uint32_t)F;
+  if (need <= 32u) return launch_one<F, 32, true, kHalf, kStructured, true>(p, s);
+  if (need <= 64u) return launch_one<F, 64, true, kHalf, kStructured, true>(p, s);
+  return hipErrorInvalidValue;
+}
+
 template <int F, bool kHalf>
 static hipError_t launch_hash(const RenderParams& p, hipStream_t s) {
-  if (!p.grid.structured) return launch_hash_levels<F, kHalf, false>(p, s);
+  if (!p.grid.structured) {
+    if constexpr (F >= 2) {
+      if (p.mix) return launch_mix_levels<F, kHalf, false>(p, s);
+    }
+    return launch_hash_levels<F, kHalf, false>(p, s);
+  }
   const GridParams& g = p.grid;
   LevelQuads lq = {};
   for (uint32_t l = 0; l < g.L; l++) {
@@ -544,12 +657,16 @@ static hipError_t launch_hash(const RenderParams& p, hipStream_t s) {
   hipLaunchKernelGGL(level_quads_kernel, dim3(1), dim3(64), 0, s, lq, g.L, g.lq);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if constexpr (F >= 2) {
+    if (p.mix) return launch_mix_levels<F, kHalf, true>(p, s);
+  }
   return launch_hash_levels<F, kHalf, true>(p, s);
 }
 
 hipError_t launch_render(const RenderParams& p, hipStream_t s) {
   if (p.ntiles == 0) return hipSuccess;
-  if (p.level == 0) {
+  if (p.mix && p.grid.F == 1) return hipErrorInvalidValue;
+  if (p.level == 0 && !p.mix) {
     if (p.C <= 3) return launch_one<1, 3, false, false>(p, s);
     if (p.C <= 16) return launch_one<1, 16, false, false>(p, s);
     if (p.C <= 32) return launch_one<1, 32, false, false>(p, s);

@@ -11,7 +11,10 @@ markVisible (:310-319) and rasterize_gaussians (:21-66).
 Scope: render mode 0 ("baseline") with the Gaussian kernel, forward and
 backward: hash-grid features when HashGridSettings.L > 0; when L == 0,
 precomputed per-splat colours or RGB evaluated from SH coefficients
-(degree <= 3) in preprocess.  The backward returns the reference's gradients
+(degree <= 3) in preprocess.  Render modes 4 ("cat": per-splat features of
+the coarse levels ahead of a grid of the fine ones) and 13
+("adaptive_cat_fast", with the inference flag 0x100) forward, with the
+reference's packed L (total << 16 | grid levels << 8 | per-splat levels).  The backward returns the reference's gradients
 (DSRpy:174-275): means3D, the means2D densification statistic, SH,
 colours, opacities, scales, rotations, the hash table, and the |grad| sum in
 the ap_level slot; it needs a float32 hash table and at most 64 channels.
@@ -55,13 +58,49 @@ def _channels(hashgrid_settings) -> int:
     return int(v[2])
 
 
+def _cat_hash_levels(offsets17: np.ndarray) -> int:
+    """Grid levels of render_mode 4 (CR/forward.cu:1231-1238): the largest i
+    in 1..16 with offsets[i] > offsets[i-1], offsets padded with zeros to 17
+    entries (GR:229-233)."""
+    hl = 0
+    for i in range(1, 17):
+        if offsets17[i] > offsets17[i - 1]:
+            hl = i
+    return hl
+
+
+def _mixed_grid(hs, render_mode, level, features, offsets, gridrange):
+    """HashGridDesc of render modes 4 and 13 from the reference's packed
+    level argument: (total << 16) | (grid levels << 8) | per-splat levels
+    (GR:224-226, :395-396; CR/forward.cu:744-767, :971-973, :1228)."""
+    base_mode = render_mode & 0xFF
+    if _empty(features) or _empty(offsets) or _empty(gridrange):
+        raise ValueError(f"render_mode {render_mode} needs features, offsets and gridrange")
+    offs = np.zeros(17, np.int64)
+    o = _rz.host_array(offsets, np.int64).reshape(-1)
+    offs[:min(17, o.shape[0])] = o[:17]
+    hyb = level & 0xFF
+    if base_mode == 4:
+        levels, total = _cat_hash_levels(offs), 0
+    else:
+        levels, total = (level >> 8) & 0xFF, (level >> 16) & 0xFF
+    table = features.detach().contiguous() if levels > 0 else None
+    return _rz.HashGridDesc(levels=levels, level_dim=int(features.shape[1]), log2_scale=float(hs.S),
+                            base_resolution=int(hs.H), table=table, offsets=offs,
+                            gridrange=_rz.host_array(gridrange, np.float32), align_corners=bool(hs.align_corners),
+                            interpolation=int(hs.interpolation), render_mode=int(render_mode), hybrid_levels=hyb,
+                            total_levels=total)
+
+
 class _RasterizeGaussians(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means3D, means2D, sh, colors_precomp, opacities, scales, rotations, cov3Ds_precomp, homotrans,
                 ap_level, features, offsets, gridrange, features_diffuse, offsets_diffuse, gridrange_diffuse,
                 raster_settings, hashgrid_settings, render_mode, shapes, kernel_type):
-        if (render_mode & 0xFF) != 0:
-            raise NotImplementedError(f"render_mode {render_mode}: only mode 0 (baseline) is implemented")
+        base_mode = render_mode & 0xFF
+        if base_mode not in (0, 4, 13) or (render_mode & ~0x1FF) or ((render_mode & 0x100) and base_mode != 13):
+            raise NotImplementedError(f"render_mode {render_mode}: implemented are 0 (baseline), 4 (cat) and "
+                                      f"13 (adaptive_cat_fast, | 0x100 inference)")
         if kernel_type != 0:
             raise NotImplementedError(f"kernel_type {kernel_type}: only the Gaussian kernel (0) is implemented")
         if not _empty(cov3Ds_precomp):
@@ -72,7 +111,16 @@ class _RasterizeGaussians(torch.autograd.Function):
             raise NotImplementedError("record_transmittance=True is not implemented")
         C = _channels(hashgrid_settings)
         level = int(hashgrid_settings.L)
-        if level > 0:
+        if base_mode == 4 and level == 0:
+            base_mode = render_mode = 0  # level 0 is the colour path in every mode but 13 (CR/forward.cu:1091)
+        if base_mode != 0:
+            grid = _mixed_grid(hashgrid_settings, render_mode, level, features, offsets, gridrange)
+            colors = None if _empty(colors_precomp) else colors_precomp.detach()
+            width = grid.row_width(C)
+            if colors is not None and (colors.dim() != 2 or colors.shape[1] != width):
+                raise ValueError(f"render_mode {render_mode}: colors_precomp must be [P, {width}]")
+            level = 1  # no SH colours
+        elif level > 0:
             if _empty(features) or _empty(offsets) or _empty(gridrange):
                 raise ValueError("hash-grid rendering (L > 0) needs features, offsets and gridrange")
             grid = _rz.HashGridDesc(levels=level, level_dim=int(features.shape[1]),
@@ -106,6 +154,7 @@ class _RasterizeGaussians(torch.autograd.Function):
                                     channels=C, shs=None if (level > 0 or colors is not None or _empty(sh)) else
                                     sh.detach(), sh_degree=int(raster_settings.sh_degree))
         ctx.num_rendered = res.num_rendered
+        ctx.render_mode = render_mode
         ctx.fw = dict(res=res, settings=settings, grid=grid, C=C, colors=colors,
                       shs=None if (level > 0 or colors is not None or _empty(sh)) else sh.detach(),
                       sh_degree=int(raster_settings.sh_degree),
@@ -119,6 +168,9 @@ class _RasterizeGaussians(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out_color, grad_radii, grad_depth, grad_0, grad_1):
+        if ctx.render_mode != 0:
+            raise NotImplementedError(f"render_mode {ctx.render_mode} is forward-only here; "
+                                      f"the backward covers mode 0")
         means3D, opacities, scales, rotations = ctx.saved_tensors
         fw = ctx.fw
         g = _rz.rasterize_backward(fw["settings"], fw["grid"], fw["res"], means3D.detach(), opacities.detach(),

@@ -48,10 +48,28 @@ class HashGridDesc:
     gridrange: np.ndarray
     align_corners: bool = False
     interpolation: int = 0
+    # render_mode 4 / 13 (| MODE_INFERENCE): per-splat feature levels ahead of
+    # the grid's `levels` (hybrid_levels) and, for mode 13, the levels of a
+    # splat's feature row (total_levels; the row ends with the blend weight)
+    render_mode: int = 0
+    hybrid_levels: int = 0
+    total_levels: int = 0
+
+    def row_width(self, channels: int) -> int:
+        """Floats per splat of colors_precomp for this render mode."""
+        base = self.render_mode & 0xFF
+        if base == L.MODE_CAT:
+            return self.hybrid_levels * self.level_dim
+        if base == L.MODE_ADAPTIVE_CAT_FAST:
+            return self.total_levels * self.level_dim + 1
+        return channels
 
     def to_c(self) -> L.HashGrid:
         g = L.HashGrid()
         g.struct_size = ct.sizeof(L.HashGrid)
+        g.render_mode = int(self.render_mode)
+        g.hybrid_levels = int(self.hybrid_levels)
+        g.total_levels = int(self.total_levels)
         g.levels = int(self.levels)
         g.level_dim = int(self.level_dim)
         g.log2_scale = float(self.log2_scale)
@@ -143,7 +161,8 @@ def _contig_f32(t: Optional[torch.Tensor], name: str) -> Optional[torch.Tensor]:
     return aligned(t)
 
 
-def _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, channels, shs, sh_degree):
+def _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, channels, shs, sh_degree,
+            row_width=None):
     """nest_splats over the device tensors (re-aligned copies where needed);
     returns (struct, tensors kept alive for the call)."""
     if means3D.ndim != 2 or means3D.shape[1] != 3:
@@ -167,8 +186,9 @@ def _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_p
             raise ValueError("homotrans must be [P, 4, 4]")
         if ap_level is not None and ap_level.numel() != P:
             raise ValueError("ap_level must have P elements")
-        if colors_precomp is not None and colors_precomp.numel() != P * channels:
-            raise ValueError(f"colors_precomp must be [P, {channels}]")
+        width = channels if row_width is None else row_width
+        if colors_precomp is not None and colors_precomp.numel() != P * width:
+            raise ValueError(f"colors_precomp must be [P, {width}]")
         if shs is not None and (shs.numel() % (P * 3) != 0 or shs.shape[0] != P):
             raise ValueError("shs must be [P, M, 3]")
 
@@ -193,14 +213,16 @@ def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: t
                       ap_level: Optional[torch.Tensor] = None, colors_precomp: Optional[torch.Tensor] = None,
                       channels: int = 3, timing: bool = False, shs: Optional[torch.Tensor] = None,
                       sh_degree: int = 0) -> ForwardResult:
-    """One forward frame.  The colour path (grid.levels == 0) takes colours
-    from colors_precomp, or, when it is None, evaluates them from shs
-    [P, M, 3] at degree sh_degree in preprocess (3 channels)."""
+    """One forward frame.  The colour path (grid.levels == 0 in render mode
+    0) takes colours from colors_precomp, or, when it is None, evaluates them
+    from shs [P, M, 3] at degree sh_degree in preprocess (3 channels).  In
+    render modes 4 and 13 colors_precomp holds the per-splat feature rows
+    (grid.row_width floats each)."""
     dev = means3D.device
     P = int(means3D.shape[0])
     H, W = settings.image_height, settings.image_width
     sp, keep = _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, channels, shs,
-                       sh_degree)
+                       sh_degree, grid.row_width(channels))
     g = grid.to_c()
 
     color = torch.empty((channels, H, W), dtype=torch.float32, device=dev)

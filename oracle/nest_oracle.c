@@ -602,7 +602,7 @@ void or_grid_encode(const or_grid *G, int B, const float *inputs, float *out)
 }
 
 /* ------------------------------------------------------------------ */
-/* render, mode 0: CR/forward.cu:639-1145, :1914-2048                   */
+/* render, modes 0, 4, 13: CR/forward.cu:639-1145, :1218-1282, :1914-2048 */
 /* ------------------------------------------------------------------ */
 
 typedef struct {
@@ -625,7 +625,40 @@ typedef struct {
     float *out_others;           /* [14][H][W]                             */
     float *final_T;              /* [3][H][W]                              */
     uint32_t *n_contrib;         /* [2][H][W]                              */
+    /* Feature composition (the reference's render_mode): 0 hash features,
+     * 4 per-splat features then hash features (level's low byte = per-splat
+     * levels), 13 adaptive_cat_fast (level = total << 16 | hash << 8 | per-splat
+     * levels, colors rows of total*F+1 floats, bit 8 of render_mode =
+     * inference).  Other values are not restated. */
+    int render_mode;
 } or_render_args;
+
+/* hashgrid_levels of render_mode 4 (forward.cu:1231-1238): the largest i in
+ * 1..16 with offsets[i] > offsets[i-1], over the offsets padded with zeros
+ * to 17 entries (gaussian_renderer/__init__.py:229-233). */
+static int cat_hash_levels(const or_grid *G)
+{
+    int hl = 0;
+    for (int i = 1; i < 17; i++) {
+        int32_t a = i - 1 <= G->L ? G->offsets[i - 1] : 0;
+        int32_t b = i <= G->L ? G->offsets[i] : 0;
+        if (b > a) hl = i;
+    }
+    return hl;
+}
+
+/* World point of a hit: homotrans columns 0, 1, 3 at (sx, sy, 1), or the
+ * splat centre when rho2d won (forward.cu:1099-1108). */
+static void hit_xyz(const float *Hm, int use3d, float sx, float sy, float xyz[3])
+{
+    if (use3d) {
+        xyz[0] = sx * Hm[0] + sy * Hm[1] + Hm[3];
+        xyz[1] = sx * Hm[4] + sy * Hm[5] + Hm[7];
+        xyz[2] = sx * Hm[8] + sy * Hm[9] + Hm[11];
+    } else {
+        xyz[0] = Hm[3]; xyz[1] = Hm[7]; xyz[2] = Hm[11];
+    }
+}
 
 static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, uint32_t py, float *feat_scratch)
 {
@@ -685,22 +718,68 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
         if (T > 0.5f) { median_depth = depth; median_contributor = (float)contributor; }
         N[0] += no[0] * w; N[1] += no[1] * w; N[2] += no[2] * w;
 
+        if ((A->render_mode & 0xFF) == 13) {
+            /* adaptive_cat_fast (forward.cu:966-1101): the per-splat row is
+             * [total*F features | blend weight]; inference with weight > 0.5
+             * takes the row as it is, without the world point or the grid;
+             * otherwise the first hyb*F channels come from the row (times
+             * the weight in training) and the next hl*F from the grid (blended
+             * with the row in training).  The hit then only updates T: no
+             * appearance colour and no last contributor. */
+            const int infer = (A->render_mode >> 8) & 1;
+            const int total = (A->level >> 16) & 0xFF, hl = (A->level >> 8) & 0xFF, hyb = A->level & 0xFF;
+            const int F = A->grid.F, tdim = total * F;
+            const float *gf = A->colors + (size_t)id * (size_t)(tdim + 1);
+            const float wt = gf[tdim];
+            for (int c = 0; c < C; c++) feat_scratch[c] = 0.0f;
+            if (infer && wt > 0.5f) {
+                for (int i = 0; i < tdim && i < C; i++) feat_scratch[i] = gf[i];
+            } else {
+                float xyz[3];
+                hit_xyz(A->homotrans + 16 * (size_t)id, use3d, sx, sy, xyz);
+                pos_x += w * xyz[0]; pos_y += w * xyz[1]; pos_z += w * xyz[2];
+                uint32_t ap = f2u_sat(floorf(A->ap_level[id]));
+                for (int i = 0; i < hyb * F && i < C; i++) feat_scratch[i] = infer ? gf[i] : gf[i] * wt;
+                if (hl > 0) {
+                    or_grid G = A->grid;
+                    G.L = hl;
+                    float hf[64];
+                    or_query_feature(&G, xyz, ap, 64, hf);
+                    const int fs = hyb * F;
+                    for (int i = 0; i < hl * F && fs + i < C; i++)
+                        feat_scratch[fs + i] = infer ? hf[i] : fmaf(wt, gf[fs + i], (1.0f - wt) * hf[i]);
+                }
+            }
+            for (int c = 0; c < C; c++) Cacc[c] = fmaf(feat_scratch[c], w, Cacc[c]);
+            T = T * (1 - alpha);
+            continue;
+        }
         if (A->level == 0) {
             const float *col = A->colors + (size_t)id * C;
             for (int c = 0; c < C; c++) Cacc[c] = fmaf(col[c], w, Cacc[c]);
         } else {
-            const float *Hm = A->homotrans + 16 * (size_t)id;
             float xyz[3];
-            if (use3d) {
-                xyz[0] = sx * Hm[0] + sy * Hm[1] + Hm[3];
-                xyz[1] = sx * Hm[4] + sy * Hm[5] + Hm[7];
-                xyz[2] = sx * Hm[8] + sy * Hm[9] + Hm[11];
-            } else {
-                xyz[0] = Hm[3]; xyz[1] = Hm[7]; xyz[2] = Hm[11];
-            }
+            hit_xyz(A->homotrans + 16 * (size_t)id, use3d, sx, sy, xyz);
             pos_x += w * xyz[0]; pos_y += w * xyz[1]; pos_z += w * xyz[2];
             uint32_t ap = f2u_sat(floorf(A->ap_level[id]));
-            or_query_feature(&A->grid, xyz, ap, C, feat_scratch);
+            if ((A->render_mode & 0xFF) == 4) {
+                /* hybrid_features (forward.cu:1218-1282): hyb*F per-splat
+                 * features (rows of hyb*F floats), then the grid's hl levels */
+                const int F = A->grid.F, pgd = (A->level & 0xFF) * F;
+                const int hl = cat_hash_levels(&A->grid);
+                for (int c = 0; c < C; c++) feat_scratch[c] = 0.0f;
+                if (pgd > 0 && A->colors)
+                    for (int i = 0; i < pgd && i < C; i++) feat_scratch[i] = A->colors[(size_t)id * pgd + i];
+                if (hl > 0) {
+                    or_grid G = A->grid;
+                    G.L = hl;
+                    float hf[64];
+                    or_query_feature(&G, xyz, ap, 64, hf);
+                    for (int i = 0; i < hl * F && pgd + i < C; i++) feat_scratch[pgd + i] = hf[i];
+                }
+            } else {
+                or_query_feature(&A->grid, xyz, ap, C, feat_scratch);
+            }
             for (int c = 0; c < C; c++) Cacc[c] = fmaf(feat_scratch[c], w, Cacc[c]);
             float apc0, apc1;
             if (ap <= 4u) { apc0 = (float)((double)(uint32_t)(ap - 2u) * 0.5); apc1 = 1.0f; }

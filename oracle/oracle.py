@@ -45,7 +45,7 @@ class OrRenderArgs(ct.Structure):
                 ("transmat", ct.c_void_p), ("normal_opacity", ct.c_void_p), ("homotrans", ct.c_void_p),
                 ("ap_level", ct.c_void_p), ("colors", ct.c_void_p), ("grid", OrGrid),
                 ("out_color", ct.c_void_p), ("out_others", ct.c_void_p), ("final_T", ct.c_void_p),
-                ("n_contrib", ct.c_void_p)]
+                ("n_contrib", ct.c_void_p), ("render_mode", ct.c_int)]
 
 
 class OrRenderBwdArgs(ct.Structure):
@@ -196,7 +196,12 @@ def make_grid(L, F, S, H, offsets, table, gridrange, contract=False, align_corne
 
 
 def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_level=None, colors=None,
-           beta=0.0, max_intersections=0, row_stride=1, row_phase=0, threads=0):
+           beta=0.0, max_intersections=0, row_stride=1, row_phase=0, threads=0, render_mode=0, level=None):
+    """renderCUDAsurfelForward for every pixel.  render_mode 0 (grid levels
+    grid.L, or the colour path without a grid), 4 or 13 (bit 8: inference);
+    for modes 4 and 13, level is the reference's packed level argument
+    (total << 16 | hash levels << 8 | per-splat levels) and colors the
+    per-splat feature rows."""
     HW = W * H
     out = dict(color=np.zeros((C, H, W), np.float32), others=np.zeros((14, H, W), np.float32),
                final_T=np.zeros((3, H, W), np.float32), n_contrib=np.zeros((2, H, W), np.uint32))
@@ -211,7 +216,8 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
 
     args = OrRenderArgs()
     args.W, args.H, args.C = W, H, C
-    args.level = 0 if grid is None else grid.L
+    args.level = (0 if grid is None else grid.L) if level is None else level
+    args.render_mode = render_mode
     args.beta = beta
     args.max_intersections = max_intersections
     args.ranges = ptr(binres["ranges"], np.uint32)

@@ -1,0 +1,176 @@
+"""GPU parity of render modes 4 (cat) and 13 (adaptive_cat_fast, training and
+inference) against the oracle, bit for bit, on the shared small scenes:
+per-splat feature rows ahead of a grid of the scene's first levels, with
+f32 and f16 tables, level_dim 2 and 4, the common-grid lookup and the
+general per-level one (smoothstep), mixed fast/slow splats in inference.
+The drop-in GaussianRasterizer decodes the reference's packed L into the
+same call."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from scenes import scene
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _rows(sc, width, weight_col=None, seed=0):
+    rng = np.random.default_rng(seed)
+    rows = rng.uniform(-1, 1, (sc.spec.P, width)).astype(np.float32)
+    if weight_col is not None:
+        rows[:, weight_col] = rng.uniform(0, 1, sc.spec.P).astype(np.float32)
+    return rows
+
+
+def run_gpu(sc, render_mode, hyb, glevels, total, C, rows, interp=0):
+    from nest_splat import rasterizer as rz
+    sp = sc.spec
+    cam = sc.cameras[0]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy,
+                                cam.world_view_transform, cam.full_proj_transform, cam.camera_center,
+                                if_contract=sp.contract)
+    grid = rz.HashGridDesc(glevels, sp.F, sp.S, sp.base_res, t(sc.table), sc.offsets,
+                           np.asarray(sp.gridrange, np.float32), interpolation=interp, render_mode=render_mode,
+                           hybrid_levels=hyb, total_levels=total)
+    res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
+                               homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), colors_precomp=t(rows), channels=C)
+    torch.cuda.synchronize()
+    return res
+
+
+def run_oracle(O, sc, render_mode, level, grid_levels, C, rows, interp=0):
+    sp = sc.spec
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    pre = O.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                       cam.full_proj_transform, W, H)
+    b = O.binning(pre, W, H)
+    grid = O.make_grid(grid_levels, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract,
+                       interp=interp)
+    r = O.render(pre, b, W, H, C, grid, homotrans=sc.homotrans, ap_level=sc.ap_level, colors=rows,
+                 render_mode=render_mode, level=level)
+    return b, r
+
+
+def _check(res, b, r):
+    from nest_splat import rasterizer as rz
+    sc_W, sc_H = r["color"].shape[2], r["color"].shape[1]
+    assert res.num_rendered == b["num_rendered"]
+    ba = {k: v.cpu().numpy() for k, v in rz.binning_arrays(res, sc_W, sc_H).items()}
+    np.testing.assert_array_equal(ba["n_contrib"].view(np.uint32), r["n_contrib"])
+    np.testing.assert_array_equal(ba["final_T"], r["final_T"])
+    np.testing.assert_array_equal(res.others.cpu().numpy(), r["others"])
+    color = res.color.cpu().numpy()
+    scale = max(np.abs(r["color"]).max(), 1e-30)
+    np.testing.assert_allclose(color, r["color"], rtol=1e-5, atol=1e-5 * scale)
+    np.testing.assert_array_equal(color, r["color"])
+
+
+# (scene, per-splat levels, grid levels, extra zero channels): level_dim 4
+# f32 (contracted) and f16, level_dim 2; 32- and 64-channel accumulators
+CAT_CASES = [("unbounded_small", 4, 10, 0), ("shells_small", 2, 5, 4), ("shell_small", 6, 16, 0),
+             ("shell_small", 0, 9, 2)]
+
+
+@pytest.mark.parametrize("name,hyb,gl,extra", CAT_CASES)
+def test_cat_mode_parity(oracle, name, hyb, gl, extra):
+    sc = scene(name)
+    F = sc.spec.F
+    C = (hyb + gl) * F + extra
+    print(f"[case] mode 4 {name} hyb={hyb} grid levels={gl} C={C}", flush=True)
+    rows = _rows(sc, hyb * F, seed=hyb)
+    res = run_gpu(sc, 4, hyb, gl, 0, C, rows)
+    # the oracle counts the grid levels from the offsets, as the reference
+    b, r = run_oracle(oracle, sc, 4, ((hyb + gl) << 16) | (1 << 8) | hyb, gl, C, rows)
+    _check(res, b, r)
+
+
+# (scene, inference, total levels, per-splat levels, active grid levels, interp)
+ACF_CASES = [("unbounded_small", True, 16, 10, 4, 0), ("shells_small", False, 8, 5, 3, 0),
+             ("shell_small", True, 12, 4, 8, 1), ("unbounded_small", False, 6, 1, 5, 1),
+             ("shells_small", True, 16, 12, 0, 0)]
+
+
+@pytest.mark.parametrize("name,infer,total,hyb,hl,interp", ACF_CASES)
+def test_adaptive_cat_fast_parity(oracle, name, infer, total, hyb, hl, interp):
+    sc = scene(name)
+    F = sc.spec.F
+    tdim = total * F
+    mode = 13 | (0x100 if infer else 0)
+    print(f"[case] mode {mode:#x} {name} total={total} hyb={hyb} hl={hl} interp={interp}", flush=True)
+    rows = _rows(sc, tdim + 1, weight_col=tdim, seed=total + hyb)
+    res = run_gpu(sc, mode, hyb, hl, total, tdim, rows, interp=interp)
+    b, r = run_oracle(oracle, sc, mode, (total << 16) | (hl << 8) | hyb, max(hl, 1), tdim, rows, interp=interp)
+    _check(res, b, r)
+    if infer:
+        assert not r["n_contrib"][0].any()
+
+
+def test_drop_in_decodes_packed_levels(oracle):
+    """GaussianRasterizer with render_mode 4 / 13 | 0x100 and the packed L of
+    the reference's render() (GR:224-226, :395-396)."""
+    from diff_surfel_rasterization import GaussianRasterizationSettings, GaussianRasterizer, HashGridSettings
+    sc = scene("shells_small")
+    sp = sc.spec
+    cam = sc.cameras[0]
+    F = sp.F
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    rs = GaussianRasterizationSettings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy,
+                                       torch.zeros(3, device=DEV), 1.0, t(cam.world_view_transform),
+                                       t(cam.full_proj_transform), 3, t(cam.camera_center), False, False, 0.0,
+                                       sp.contract, False)
+    for mode, total, hyb, gl in ((4, 8, 3, 5), (13 | 0x100, 10, 6, 3)):
+        C = total * F
+        width = hyb * F if mode == 4 else C + 1
+        rows = _rows(sc, width, weight_col=None if mode == 4 else C, seed=mode)
+        offs = np.zeros(17, np.int32)
+        offs[:gl + 1] = np.asarray(sc.offsets)[:gl + 1]
+        packed = (total << 16) | ((1 if mode == 4 else gl) << 8) | hyb
+        hs = HashGridSettings(packed, math.log2(sp.per_level_scale), sp.base_res, False, 0,
+                              torch.tensor([hyb * F, gl * F, C], dtype=torch.int32, device=DEV))
+        print(f"[case] drop-in mode {mode:#x} L={packed:#x}", flush=True)
+        color, radii, allmap, _, _ = GaussianRasterizer(rs, hs)(
+            means3D=t(sc.means), means2D=None, opacities=t(sc.opacity), colors_precomp=t(rows),
+            scales=t(sc.scales), rotations=t(sc.rotations), homotrans=t(sc.homotrans), ap_level=t(sc.ap_level),
+            features=t(sc.table), offsets=t(offs), gridrange=t(np.asarray(sp.gridrange, np.float32)),
+            render_mode=mode)
+        torch.cuda.synchronize()
+        _, r = run_oracle(oracle, sc, mode, packed, gl, C, rows)
+        np.testing.assert_array_equal(allmap.cpu().numpy(), r["others"])
+        np.testing.assert_array_equal(color.cpu().numpy(), r["color"])
+
+
+def test_mode_validation():
+    """Mode arguments the library rejects before any launch."""
+    from nest_splat import rasterizer as rz
+    sc = scene("cfg1")  # level_dim 2
+    sp = sc.spec
+    cam = sc.cameras[0]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy,
+                                cam.world_view_transform, cam.full_proj_transform, cam.camera_center)
+
+    def call(mode, hyb, gl, total, C, width):
+        grid = rz.HashGridDesc(gl, sp.F, sp.S, sp.base_res, t(sc.table), sc.offsets,
+                               np.asarray(sp.gridrange, np.float32), render_mode=mode, hybrid_levels=hyb,
+                               total_levels=total)
+        rows = t(np.zeros((sp.P, width), np.float32))
+        return rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
+                                    homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), colors_precomp=rows,
+                                    channels=C)
+
+    errs = (NotImplementedError, RuntimeError)
+    with pytest.raises(errs, match="render_mode 12"):
+        call(12, 1, 2, 4, 8, 8)
+    with pytest.raises(errs, match="supported"):
+        call(4 | 0x100, 1, 2, 0, 8, 2)
+    with pytest.raises(errs, match="exceed total_levels"):
+        call(13, 3, 3, 5, 10, 11)
+    with pytest.raises(errs, match="channels"):
+        call(4, 2, 4, 0, 10, 4)
+    with pytest.raises(errs, match="<= 32"):
+        call(13, 1, 2, 40, 80, 81)
