@@ -134,6 +134,60 @@ def finish_traffic(res: dict, copy_mib: int, out_path: str) -> dict:
     return res
 
 
+def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_level, table, mlp, M, bg, dev,
+               hyb=10):
+    """Render modes 4 and 13 on the benchmark frame: the first `hyb` of the
+    16 levels become per-splat feature rows, the last 16 - hyb levels the grid
+    (the scene's own tables of those levels, base resolution of level hyb).
+    Mode 13 rows carry a blend weight uniform in [0.15, 1): 59% of the splats
+    take the inference fast path.  Returns per mode the mean render-kernel
+    and frame (render + MLP) milliseconds over K frames."""
+    import numpy as np
+    import torch
+
+    from nest_splat import _lib as L
+    from nest_splat import rasterizer as rz
+    F, Lt = spec.F, spec.L
+    gl = Lt - hyb
+    offs = np.asarray(scene.offsets, np.int64)
+    sub_offsets = offs[hyb:] - offs[hyb]
+    sub_table = table[int(offs[hyb]):int(offs[Lt])]
+    sub_base = int(round(2.0 ** (hyb * spec.S) * spec.base_res))
+    rng = np.random.default_rng(1)
+    tdim = Lt * F
+    rows = (rng.standard_normal((spec.P, tdim + 1)) * 0.1).astype(np.float32)
+    rows[:, tdim] = rng.uniform(0.15, 1.0, spec.P).astype(np.float32)
+    rows13 = torch.from_numpy(rows).to(dev)
+    rows4 = rows13[:, :hyb * F].contiguous()
+    cases = {"cat(4)": (4, rows4, 0), "adaptive_cat_fast(13) training": (13, rows13, Lt),
+             "adaptive_cat_fast(13) inference": (13 | 0x100, rows13, Lt)}
+    res_ms = {}
+    for name, (mode, rows_t, total) in cases.items():
+        grid = rz.HashGridDesc(gl, F, spec.S, sub_base, sub_table, sub_offsets, np.asarray(spec.gridrange, np.float32),
+                               render_mode=mode, hybrid_levels=hyb, total_levels=total)
+
+        def frame(tm=None):
+            res = rz.rasterize_forward(settings, grid, means, opac, scales, rots, homotrans=homo, ap_level=ap_level,
+                                       colors_precomp=rows_t, channels=spec.C,
+                                       timing=tm if tm is not None else False)
+            return res, mlp.decode_image(res.color, M, alpha=res.others[1], bg=bg)
+
+        frame()
+        torch.cuda.synchronize()
+        tms = [L.new_timing(True) for _ in range(K)]
+        t0 = time.perf_counter()
+        for k in range(K):
+            frame(tms[k])
+        torch.cuda.synchronize()
+        frame_ms = (time.perf_counter() - t0) / K * 1e3
+        render_ms = float(np.mean([L.timing_read(tm)["render"] for tm in tms]))
+        for tm in tms:
+            L.timing_release(tm)
+        res_ms[name] = {"render_ms": round(render_ms, 4), "frame_ms": round(frame_ms, 4)}
+        log(f"[bench] {name}: render {render_ms:.3f} ms, frame {frame_ms:.3f} ms")
+    return res_ms
+
+
 def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--pmc-summary":
         # python bench.py --pmc-summary FETCH_DIR WRITE_DIR COPY_MIB OUT.json
@@ -153,6 +207,10 @@ def main():
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="before the frames, copy this many MiB device-to-device (a plain copy kernel of known "
                          "size whose FETCH_SIZE / WRITE_SIZE scale the render kernel's counters)")
+    ap.add_argument("--modes", type=int, default=0, metavar="K",
+                    help="after the timed frames, time K frames of each other render mode (4 cat, 13 "
+                         "adaptive_cat_fast training and inference) on the same splats: per-splat rows of the "
+                         "first 10 levels, a grid of the last 6, and report modes_ms (not part of the metric)")
     ap.add_argument("--backward", type=int, default=0, metavar="K",
                     help="after the timed forward frames, time K backward passes (nest_backward) of the last frame "
                          "with random output gradients and report backward_ms (not part of the metric)")
@@ -269,6 +327,9 @@ def main():
                      "algorithmic_bytes": alg, "render_ms": round(render_ms, 4)},
         "cpu_baseline": None,
     }
+    if args.modes > 0:
+        out["modes_ms"] = time_modes(args.modes, spec, scene, settings, means, opac, scales, rots, homo, ap_level,
+                                     table, mlp, M, bg, dev)
     if args.backward > 0:
         gen = torch.Generator(device=dev).manual_seed(0)
         dcol = torch.randn(tuple(res.color.shape), generator=gen, device=dev)

@@ -457,9 +457,11 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     rp.wslot = -1;
     if ((gr->render_mode & 0xFF) == NEST_MODE_CAT) {
       rp.cstride = rp.pgd;
+      rp.nrow = rp.pgd;
     } else {
       const int tdim = (int)gr->total_levels * F;
       rp.cstride = tdim + 1;
+      rp.nrow = tdim;
       rp.wslot = tdim;
       rp.infer = (gr->render_mode & NEST_MODE_INFERENCE) ? 1 : 0;
       rp.blend = rp.infer ? 0 : 1;

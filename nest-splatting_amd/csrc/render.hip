@@ -25,6 +25,8 @@
 //    oldest first, are spread one per lane whatever pixel they belong to, so
 //    the gathers and the interpolation run with all lanes busy; each pixel's
 //    lane then accumulates its own hits in front-to-back order.
+#include <type_traits>
+
 #include "hashgrid.h"
 #include "nest_internal.h"
 #include "nest_math.h"
@@ -218,6 +220,135 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
   qn -= take;
 }
 
+// Compacted drain of the per-splat feature modes (F <= 4): drain_compact's
+// item table and hand-off, with output level l holding grid level l - hyb
+// and each hit's value at a level computed by drain_mixed's rules.  The
+// lookup lane loads the row entries of fast and blend hits along with the
+// corner gathers, one level ahead.  Hand-offs run only for the output levels
+// that can carry a value, [hyb, hyb + max(L, nfast)).
+template <int F, int NACC, bool kHalf, bool kStructured>
+__device__ __forceinline__ void drain_compact_mix(const RenderParams& p, nest_i32x4 rsrc,
+                                                  float4 (*hq)[kRenderThreads], uint32_t (*hm)[kRenderThreads],
+                                                  uint8_t* isrc, int& qhead, int& qn, float* acc) {
+  static_assert(F <= 4, "a level's values fit one queue slot");
+  const GridParams& g = p.grid;
+  const uint32_t lane = threadIdx.x & (kWaveLanes - 1);
+  const uint32_t wbase = threadIdx.x - lane;
+  const uint64_t lt = lanemask_lt64();
+  uint32_t base = 0;
+  int take = 0;
+#pragma unroll
+  for (int d = 0; d < kQueue; d++) {
+    const uint64_t m = __ballot(qn > d);
+    const uint32_t k = base + (uint32_t)__popcll(m & lt);
+    if (qn > d && k < (uint32_t)kWaveLanes) {
+      isrc[k] = (uint8_t)(lane | ((uint32_t)((qhead + d) & (kQueue - 1)) << 6));
+      take = d + 1;
+    }
+    base += (uint32_t)__popcll(m);
+  }
+  const uint32_t items = base < (uint32_t)kWaveLanes ? base : (uint32_t)kWaveLanes;
+  __builtin_amdgcn_wave_barrier();
+  const bool work = lane < items;
+  float u[3] = {0.0f, 0.0f, 0.0f};
+  uint32_t nhash = 0, nfeat = 0, col = 0, wslot = 0;
+  bool fast = false;
+  const float* row = p.colors;
+  float wt = 0.0f;
+  if (work) {
+    const uint32_t s = isrc[lane];
+    col = wbase + (s & 63u);
+    wslot = s >> 6;
+    const float4 e = hq[wslot][col];
+    u[0] = e.x;
+    u[1] = e.y;
+    u[2] = e.z;
+    const uint32_t meta = hm[wslot][col];
+    nhash = meta & 63u;
+    fast = (meta & 64u) != 0u;
+    row = p.colors + (size_t)(meta >> 7) * (uint32_t)p.cstride;
+    if (p.wslot >= 0) wt = row[p.wslot];
+    row += p.pgd;
+    nfeat = fast ? p.nfast : (p.blend ? g.L : nhash);
+  }
+  const bool rows = fast || p.blend != 0;
+  float wd[kQueue];
+#pragma unroll
+  for (int d = 0; d < kQueue; d++) wd[d] = d < take ? hq[(qhead + d) & (kQueue - 1)][threadIdx.x].w : 0.0f;
+  __builtin_amdgcn_wave_barrier();
+  constexpr int kLevels = NACC / F;
+  const int hyb = p.hyb;
+  const int lend = hyb + (int)(g.L > p.nfast ? g.L : p.nfast);
+  const LevelQuadPtr lqb = (LevelQuadPtr)g.lq;
+  LevelCorners cn;
+  float vals[8][F];
+  float rv[F];
+#pragma unroll
+  for (int f = 0; f < F; f++) rv[f] = 0.0f;
+  bool look = false;
+  nest_u32x4 rec = {0u, 0u, 0u, 0u}, rec_next = {0u, 0u, 0u, 0u};
+  if constexpr (kStructured) rec = level_record(lqb, 0);
+  if (hyb == 0) {
+    look = work && !fast && 0u < nhash;
+    if (look) {
+      level_setup<F, kHalf, kStructured>(g, rec, 0, u, cn);
+      corners_load<F, kHalf>(rsrc, cn, vals);
+    }
+    if (work && rows && 0u < nfeat) {
+#pragma unroll
+      for (int f = 0; f < F; f++) rv[f] = row[f];
+    }
+  }
+  if constexpr (kStructured) rec_next = level_record(lqb, hyb <= 1 ? 1 - hyb : 0);
+#pragma unroll
+  for (int l = 0; l < kLevels; l++) {
+    const int gl = l - hyb;
+    nest_u32x4 rec_after = {0u, 0u, 0u, 0u};
+    if constexpr (kStructured)
+      if (l + 2 < kLevels) rec_after = level_record(lqb, gl + 2 >= 0 ? gl + 2 : 0);
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (gl >= 0 && work && (uint32_t)gl < nfeat) {
+      float h[F];
+#pragma unroll
+      for (int f = 0; f < F; f++) h[f] = 0.0f;
+      if (look) corners_sum<F>(cn, vals, h);
+#pragma unroll
+      for (int f = 0; f < F; f++) v[f] = fast ? rv[f] : (p.blend ? fmaf(wt, rv[f], (1.0f - wt) * h[f]) : h[f]);
+    }
+    bool next = false;
+    if (l + 1 < kLevels && gl + 1 >= 0) {
+      const uint32_t gn = (uint32_t)(gl + 1);
+      next = work && !fast && gn < nhash;
+      if (next) {
+        level_setup<F, kHalf, kStructured>(g, rec_next, (int)gn, u, cn);
+        corners_load<F, kHalf>(rsrc, cn, vals);
+      }
+      if (work && rows && gn < nfeat) {
+#pragma unroll
+        for (int f = 0; f < F; f++) rv[f] = row[gn * F + f];
+      }
+    }
+    look = next;
+    rec_next = rec_after;
+    if (gl >= 0 && l < lend) {
+      if (work) hq[wslot][col] = make_float4(v[0], v[1], v[2], v[3]);
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int d = 0; d < kQueue; d++) {
+        if (d < take) {
+          const float4 r = hq[(qhead + d) & (kQueue - 1)][threadIdx.x];
+          const float rq[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+          for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(rq[f], wd[d], acc[l * F + f]);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  qhead = (qhead + take) & (kQueue - 1);
+  qn -= take;
+}
+
 // Drain round of the per-splat feature modes (render modes 4 and 13): every
 // lane with a pending hit takes its oldest one.  Output level l holds grid
 // level l - hyb.  A queued hit's meta word is splat id << 7 | fast << 6 |
@@ -370,6 +501,30 @@ __device__ __forceinline__ uint8_t hit_levels(bool oob, uint32_t ap, uint32_t L)
   return (uint8_t)(max_level < 255u ? max_level : 255u);
 }
 
+// State of an accepted hit between the per-lane test and the converged
+// feature block of the render modes 4 and 13.
+struct PendingHit {
+  bool on = false;
+  float w = 0.0f, T = 0.0f;
+  SplatHit hit{};
+};
+struct NoPendingHit {};
+
+// Appearance-level colour of a hit (CR/forward.cu:1945-1957): its first two
+// channels; the third only ever adds 0 * w.
+__device__ __forceinline__ void appearance_colour(uint32_t ap, float w, float& vis0, float& vis1) {
+  float apc0, apc1;
+  if (ap <= 4u) {
+    apc0 = (float)((double)(uint32_t)(ap - 2u) * 0.5);
+    apc1 = 1.0f;
+  } else {
+    apc0 = 1.0f;
+    apc1 = (float)(1.0 - (double)(uint32_t)(ap - 4u) * 0.5);
+  }
+  vis0 += apc0 * w;
+  vis1 += apc1 * w;
+}
+
 // LDS (32 KB of staged records + 17 KB of queue) allows three workgroups per
 // CU; amdgpu_waves_per_eu(3) gives the matching 168-VGPR budget, which holds
 // 64 accumulators and eight in-flight 16-byte corner loads.
@@ -384,7 +539,7 @@ render_kernel(const RenderParams p) {
   __shared__ float4 hq[kHash ? kQueue : 1][kRenderThreads];
   __shared__ uint8_t hl[kHash && !kMix ? kQueue : 1][kRenderThreads];
   __shared__ uint32_t hm[kMix ? kQueue : 1][kMix ? kRenderThreads : 1];
-  __shared__ uint8_t isrc[kHash && !kMix ? kRenderThreads : 1];  // compacted-drain item tables, 64 per wave
+  __shared__ uint8_t isrc[kHash ? kRenderThreads : 1];  // compacted-drain item tables, 64 per wave
 
   const uint32_t tile = xcd_tile(blockIdx.x, p.ntiles);
   const uint32_t tx = tile % p.gx, ty = tile / p.gx;
@@ -415,6 +570,9 @@ render_kernel(const RenderParams p) {
   nest_i32x4 rsrc{};
   if constexpr (kHash) rsrc = table_rsrc_rows<F, kHalf>(g.table, g.table_rows);
   int qn = 0, qhead = 0;  // per-lane ring buffer of pending lookups
+  // kMix: an accepted hit's feature part waits for the converged block after
+  // the per-lane test
+  [[maybe_unused]] std::conditional_t<kMix, PendingHit, NoPendingHit> ph;
 
   // Batches of 256 splats.  The splat index j is uniform across the wave;
   // lanes that are done skip the body, as the reference's per-lane loop
@@ -441,6 +599,7 @@ render_kernel(const RenderParams p) {
     uint32_t j = 0;
     for (;;) {
     while (j < n) {
+      if constexpr (kMix) ph.on = false;
       if (!done) {
       contributor++;
       do {
@@ -475,6 +634,13 @@ render_kernel(const RenderParams p) {
         N1 += q3.y * w;
         N2 += q3.z * w;
 
+        if constexpr (kMix) {
+          ph.on = true;
+          ph.w = w;
+          ph.T = test_T;
+          ph.hit = hit;
+          break;
+        }
         if constexpr (!kHash) {
           const uint32_t id = __float_as_uint(srec[6][j].z);
           const float* col = p.colors + (size_t)id * p.C;
@@ -482,65 +648,83 @@ render_kernel(const RenderParams p) {
           for (int c = 0; c < NACC; c++)
             if (c < p.C) acc[c] = fmaf(col[c], w, acc[c]);
         } else {
+          float xyz[3];
+          hit_world(srec[4][j], srec[5][j], srec[6][j], hit, xyz);
+          pos_x += w * xyz[0];
+          pos_y += w * xyz[1];
+          pos_z += w * xyz[2];
           const uint32_t ap = __float_as_uint(q3.w);
-          bool fast = false, enq = true;
-          uint32_t meta = 0u;
-          if constexpr (kMix) {
-            // The splat (and so its row) is uniform across the wave: scalar loads.
-            const uint32_t id = __builtin_amdgcn_readfirstlane(__float_as_uint(srec[6][j].z));
-            const float* row = p.colors + (size_t)id * (uint32_t)p.cstride;
-            float wt = 1.0f;
-            if (p.wslot >= 0) {
-              wt = row[p.wslot];
-              fast = p.infer && wt > 0.5f;
-            }
-            // Per-splat channels at once; a fast hit's grid-level channels
-            // too when no earlier hit of the pixel is pending.
-            enq = !(fast && qn == 0);
-            const int ndirect = enq ? p.pgd : p.pgd + (int)p.nfast * F;
-#pragma unroll
-            for (int c = 0; c < NACC; c++)
-              if (c < ndirect) acc[c] = fmaf(p.blend ? row[c] * wt : row[c], w, acc[c]);
-            meta = id << 7 | (fast ? 64u : 0u);
+          float u[3];
+          bool oob;
+          grid_coord(g, xyz, u, oob);
+          const int slot = (qhead + qn) & (kQueue - 1);
+          hq[slot][threadIdx.x] = make_float4(u[0], u[1], u[2], w);
+          hl[slot][threadIdx.x] = hit_levels(oob, ap, L);
+          qn++;
+          float apc0, apc1;
+          if (ap <= 4u) {
+            apc0 = (float)((double)(uint32_t)(ap - 2u) * 0.5);
+            apc1 = 1.0f;
+          } else {
+            apc0 = 1.0f;
+            apc1 = (float)(1.0 - (double)(uint32_t)(ap - 4u) * 0.5);
           }
-          float u[3] = {0.0f, 0.0f, 0.0f};
-          uint32_t nh = 0u;
-          if (!fast) {
-            float xyz[3];
-            hit_world(srec[4][j], srec[5][j], srec[6][j], hit, xyz);
-            pos_x += w * xyz[0];
-            pos_y += w * xyz[1];
-            pos_z += w * xyz[2];
-            bool oob;
-            grid_coord(g, xyz, u, oob);
-            nh = hit_levels(oob, ap, L);
-          }
-          if (enq) {
-            const int slot = (qhead + qn) & (kQueue - 1);
-            hq[slot][threadIdx.x] = make_float4(u[0], u[1], u[2], w);
-            if constexpr (kMix)
-              hm[slot][threadIdx.x] = meta | nh;
-            else
-              hl[slot][threadIdx.x] = (uint8_t)nh;
-            qn++;
-          }
-          if (!kMix || !p.m13) {
-            float apc0, apc1;
-            if (ap <= 4u) {
-              apc0 = (float)((double)(uint32_t)(ap - 2u) * 0.5);
-              apc1 = 1.0f;
-            } else {
-              apc0 = 1.0f;
-              apc1 = (float)(1.0 - (double)(uint32_t)(ap - 4u) * 0.5);
-            }
-            vis0 += apc0 * w;
-            vis1 += apc1 * w;
-          }
+          vis0 += apc0 * w;
+          vis1 += apc1 * w;
         }
         T = test_T;
-        // render mode 13 leaves the hit loop before the last-contributor update (CR/forward.cu:1097-1100)
-        if (!kMix || !p.m13) last_contributor = contributor;
+        last_contributor = contributor;
       } while (false);
+      }
+      if constexpr (kMix) {
+        // Render modes 4 and 13: the splat's feature row is read once per wave
+        // with one coalesced load (lane k holds entry k), then broadcast lane by
+        // lane; a lane's grid lookups go to its queue.
+        if (__ballot(ph.on) != 0ull) {
+          const uint32_t id = __builtin_amdgcn_readfirstlane(__float_as_uint(srec[6][j].z));
+          const float* row = p.colors + (size_t)id * (uint32_t)p.cstride;
+          const uint32_t lane = threadIdx.x & (kWaveLanes - 1);
+          float mine = lane < (uint32_t)p.nrow ? row[lane] : 0.0f;
+          asm volatile("" : "+v"(mine));  // loaded here, with every lane active
+          const float wt = p.wslot >= 0 ? row[p.wslot] : 1.0f;
+          const bool fast = p.infer && wt > 0.5f;
+          if (ph.on) {
+            // per-splat channels at once; a fast hit's grid-level channels too
+            // when no earlier hit of the pixel is pending
+            const bool enq = !(fast && qn == 0);
+            const int ndirect = enq ? p.pgd : p.pgd + (int)p.nfast * F;
+#pragma unroll
+            for (int c = 0; c < NACC; c++) {
+              if (c < ndirect) {
+                const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), c));
+                acc[c] = fmaf(p.blend ? rv * wt : rv, ph.w, acc[c]);
+              }
+            }
+            const uint32_t ap = __float_as_uint(srec[3][j].w);
+            float u[3] = {0.0f, 0.0f, 0.0f};
+            uint32_t nh = 0u;
+            if (!fast) {
+              float xyz[3];
+              hit_world(srec[4][j], srec[5][j], srec[6][j], ph.hit, xyz);
+              pos_x += ph.w * xyz[0];
+              pos_y += ph.w * xyz[1];
+              pos_z += ph.w * xyz[2];
+              bool oob;
+              grid_coord(g, xyz, u, oob);
+              nh = hit_levels(oob, ap, L);
+            }
+            if (enq) {
+              const int slot = (qhead + qn) & (kQueue - 1);
+              hq[slot][threadIdx.x] = make_float4(u[0], u[1], u[2], ph.w);
+              hm[slot][threadIdx.x] = id << 7 | (fast ? 64u : 0u) | nh;
+              qn++;
+            }
+            if (!p.m13) appearance_colour(ap, ph.w, vis0, vis1);
+            T = ph.T;
+            // render mode 13 leaves the hit loop before the last-contributor update (CR/forward.cu:1097-1100)
+            if (!p.m13) last_contributor = contributor;
+          }
+        }
       }
       j++;
       if (kHash && __ballot(qn == kQueue)) break;
@@ -550,7 +734,9 @@ render_kernel(const RenderParams p) {
     if constexpr (kHash) {
       // whenever a lane is full; at the end, until every queue is empty
       if (__ballot(qn == kQueue) || (last && __ballot(qn > 0))) {
-        if constexpr (kMix)
+        if constexpr (kMix && F <= 4)
+          drain_compact_mix<F, NACC, kHalf, kStructured>(p, rsrc, hq, hm, isrc + wid * kWaveLanes, qhead, qn, acc);
+        else if constexpr (kMix)
           drain_mixed<F, NACC, kHalf, kStructured>(p, rsrc, hq, hm, qhead, qn, acc);
         else if constexpr (F <= 4)
           drain_compact<F, NACC, kHalf, kStructured>(g, rsrc, hq, hl, isrc + wid * kWaveLanes, qhead, qn, acc);
