@@ -26,12 +26,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint16_t to_bf16_rne(float f) {
-  uint32_t x = __float_as_uint(f);
-  if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x7fffffu)) return (uint16_t)((x | 0x400000u) >> 16);
-  x += 0x7fffu + ((x >> 16) & 1u);
-  return (uint16_t)(x >> 16);
-}
+// Round to nearest even: one v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ uint16_t to_bf16_rne(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ uint16_t to_f16_rne(float f) { return __half_as_ushort(__float2half_rn(f)); }
 
@@ -107,9 +103,14 @@ __device__ __forceinline__ float finish_rgb(const MlpParams& p, int64_t n, float
 
 constexpr int kMlpThreads = 256;
 
-// NT = width / 16.  KC1 = ceil((C + 16) / 16) K-chunks in layer 1.
-template <int NT, bool kBF16>
-__global__ void __launch_bounds__(kMlpThreads) mlp_mfma_kernel(const MlpParams p) {
+// NT = width / 16.  KC1 = ceil((C + 16) / 16) K-chunks in layer 1.  KF > 0:
+// C == 16 KF, the features fill KF whole chunks and the SH terms the last
+// one; a lane's 4 KF feature loads of a tile are then issued together (one
+// load latency per tile instead of one per chunk), and a lane evaluates only
+// the 4 SH terms of its row group.
+template <int NT, bool kBF16, int KF>
+__global__ void __launch_bounds__(kMlpThreads) __attribute__((amdgpu_waves_per_eu(NT <= 4 ? 3 : 1)))
+mlp_mfma_kernel(const MlpParams p) {
   extern __shared__ uint16_t lds[];
   const int C = p.C;
   const int KC1 = (C + 16 + 15) / 16;
@@ -146,15 +147,47 @@ __global__ void __launch_bounds__(kMlpThreads) mlp_mfma_kernel(const MlpParams p
     const bool valid = n < p.N;
     const int64_t nn = valid ? n : p.N - 1;
 
+    float xf[KF > 0 ? KF : 1][4];
+    if constexpr (KF > 0) {
+#pragma unroll
+      for (int kc = 0; kc < KF; kc++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) xf[kc][i] = p.feat[(int64_t)(kc * 16 + grp * 4 + i) * p.feat_cs + nn * p.feat_ns];
+    }
     float dx, dy, dz;
     pixel_dir(p, nn, dx, dy, dz);
     float sh[16];
-    sh16(dx, dy, dz, sh);
+    float s4[4];  // KF > 0: the SH terms grp * 4 + i of this lane's row group
+    if constexpr (KF > 0) {
+      // each branch keeps only its own 4 terms of the inlined basis
+      switch (grp) {
+        case 0: sh16(dx, dy, dz, sh); s4[0] = sh[0]; s4[1] = sh[1]; s4[2] = sh[2]; s4[3] = sh[3]; break;
+        case 1: sh16(dx, dy, dz, sh); s4[0] = sh[4]; s4[1] = sh[5]; s4[2] = sh[6]; s4[3] = sh[7]; break;
+        case 2: sh16(dx, dy, dz, sh); s4[0] = sh[8]; s4[1] = sh[9]; s4[2] = sh[10]; s4[3] = sh[11]; break;
+        default: sh16(dx, dy, dz, sh); s4[0] = sh[12]; s4[1] = sh[13]; s4[2] = sh[14]; s4[3] = sh[15]; break;
+      }
+    } else {
+      sh16(dx, dy, dz, sh);
+    }
 
     f32x4 acc1[NT];
 #pragma unroll
     for (int i = 0; i < NT; i++) acc1[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int kc = 0; kc < KC1; kc++) {
+    if constexpr (KF > 0) {
+#pragma unroll
+      for (int kc = 0; kc <= KF; kc++) {
+        float xv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) xv[i] = kc < KF ? xf[kc < KF ? kc : 0][i] : s4[i];
+        const uint2 b = pack4(to16<kBF16>(xv[0]), to16<kBF16>(xv[1]), to16<kBF16>(xv[2]), to16<kBF16>(xv[3]));
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+          const uint2 a = *reinterpret_cast<const uint2*>(w1 + (nt * 16 + col) * ld1 + kc * 16 + grp * 4);
+          acc1[nt] = mfma16<kBF16>(a, b, acc1[nt]);
+        }
+      }
+    }
+    for (int kc = 0; KF == 0 && kc < KC1; kc++) {
       float xv[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -258,16 +291,28 @@ __global__ void __launch_bounds__(kMlpThreads) mlp_f32_kernel(const MlpParams p)
   }
 }
 
-template <int NT, bool kBF16>
-static hipError_t launch_mfma(const MlpParams& p, hipStream_t s) {
+template <int NT, bool kBF16, int KF>
+static hipError_t launch_mfma_kf(const MlpParams& p, hipStream_t s) {
   const int KC1 = (p.C + 16 + 15) / 16;
   const size_t lds = sizeof(uint16_t) * ((size_t)NT * 16 * (KC1 * 16 + 4) + (size_t)NT * 16 * (NT * 16 + 4) +
                                          16 * (size_t)(NT * 16 + 4));
   const int64_t ntile = (p.N + 15) / 16;
   const int64_t want = (ntile + 3) / 4;
   const unsigned blocks = (unsigned)(want < 2048 ? (want > 0 ? want : 1) : 2048);
-  hipLaunchKernelGGL((mlp_mfma_kernel<NT, kBF16>), dim3(blocks), dim3(kMlpThreads), lds, s, p);
+  hipLaunchKernelGGL((mlp_mfma_kernel<NT, kBF16, KF>), dim3(blocks), dim3(kMlpThreads), lds, s, p);
   return hipGetLastError();
+}
+
+// Feature widths that fill whole 16-channel chunks (16, 32, 64) take the
+// batched-load instantiation.
+template <int NT, bool kBF16>
+static hipError_t launch_mfma(const MlpParams& p, hipStream_t s) {
+  switch (p.C) {
+    case 16: return launch_mfma_kf<NT, kBF16, 1>(p, s);
+    case 32: return launch_mfma_kf<NT, kBF16, 2>(p, s);
+    case 64: return launch_mfma_kf<NT, kBF16, 4>(p, s);
+    default: return launch_mfma_kf<NT, kBF16, 0>(p, s);
+  }
 }
 
 template <int NW>
