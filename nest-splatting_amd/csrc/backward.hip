@@ -47,9 +47,52 @@ __device__ __forceinline__ uint32_t bwd_xcd_tile(uint32_t i, uint32_t n) {
   return start + k;
 }
 
+// Cross-lane sums on the VALU (no LDS round trips): v_permlane32_swap /
+// v_permlane16_swap exchange lane halves (bits 5 and 4 of the lane index),
+// DPP row operations the rest.  halve<bit>(lo, hi) is one recursive-halving
+// step: a lane whose index has the bit clear returns lo + its partner's lo,
+// one with the bit set hi + its partner's hi, the partner differing in that
+// bit (for bit 2 the partner is lane ^ 7, which leaves the bits above alone).
+// The swap builtins return (a with its upper half [row] replaced by b's lower
+// one, b with its lower half replaced by a's upper one), so the pair to sum
+// is the two results.
+constexpr int kDppRor8 = 0x128;        // row_ror:8, lane ^ 8 within a row
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror, lane ^ 7
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float halve(int bit, float lo, float hi) {
+  if (bit == 5) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if (bit == 4) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  const bool up = ((threadIdx.x >> bit) & 1u) != 0u;
+  const float send = up ? lo : hi, keep = up ? hi : lo;
+  float got;
+  if (bit == 3)
+    got = dpp_f<kDppRor8>(send);
+  else if (bit == 2)
+    got = dpp_f<kDppHalfMirror>(send);
+  else if (bit == 1)
+    got = dpp_f<kDppQuadXor2>(send);
+  else
+    got = dpp_f<kDppQuadXor1>(send);
+  return keep + got;
+}
+
+// Sum over the 64 lanes, in every lane.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  for (int b = 5; b >= 0; b--) v = halve(b, v, v);
   return v;
 }
 
@@ -57,46 +100,34 @@ __device__ __forceinline__ void atomic_add(float* p, float v) { unsafeAtomicAdd(
 
 // Table gradient of one level for the wave (uniform control flow): lanes
 // whose hits fall in the same cell (same g) share all eight corner entries.
-// Up to kGroups (8) cells, each cell's 8*F values are summed over its lanes with
-// a recursive-halving reduce-scatter (after it, lane l holds the sum of value
-// l / (64 / 8F)), then one atomic per entry and channel; with more cells every
-// lane adds its own values.  At coarse levels a wave's hits (one splat seen by
-// 64 neighbouring pixels) are nearly always one cell, which is where the
-// per-lane atomics of the reference pile onto the same addresses.
+// The cells are taken one at a time (the lowest remaining lane's cell and
+// every lane sharing it); a cell of two or more lanes has its 8*F values
+// summed over its lanes with a recursive-halving reduce-scatter (after it,
+// lane l holds the sum of value l / (64 / 8F)) and added with one atomic per
+// entry and channel; lanes alone in their cell add their own values at the
+// end, all at once.  At coarse levels a wave's hits (one splat seen by 64
+// neighbouring pixels) are nearly always one cell, which is where the
+// per-lane atomics of the reference pile onto the same addresses; at fine
+// levels a cell holds a few lanes.
 template <int F>
 __device__ __forceinline__ void scatter_level(bool on, const uint32_t gc[3], const uint32_t idx[8], const float* cv,
                                               float* dl) {
   constexpr int NV = 8 * F;
-  constexpr int kGroups = 8;
   constexpr int kRep = 64 / NV;  // lanes holding each value after the halving steps
   const uint32_t lane = threadIdx.x & 63u;
   uint64_t rem = __ballot(on);
-  uint64_t gm[kGroups] = {};
-  int lead[kGroups] = {};
-#pragma unroll
-  for (int gi = 0; gi < kGroups; gi++) {
-    if (rem == 0ull) break;
+  uint64_t single = 0ull;
+  while (rem != 0ull) {
     const int ld = __ffsll((long long)rem) - 1;
-    const uint32_t k0 = __shfl(gc[0], ld, 64), k1 = __shfl(gc[1], ld, 64), k2 = __shfl(gc[2], ld, 64);
+    const uint32_t k0 = __builtin_amdgcn_readlane(gc[0], ld), k1 = __builtin_amdgcn_readlane(gc[1], ld),
+                   k2 = __builtin_amdgcn_readlane(gc[2], ld);
     const uint64_t m = __ballot(on && gc[0] == k0 && gc[1] == k1 && gc[2] == k2) & rem;
-    gm[gi] = m;
-    lead[gi] = ld;
     rem &= ~m;
-  }
-  if (rem != 0ull) {
-    if (on) {
-#pragma unroll
-      for (int k = 0; k < 8; k++)
-#pragma unroll
-        for (int f = 0; f < F; f++)
-          if (cv[k * F + f] != 0.0f) atomic_add(dl + (size_t)idx[k] * F + f, cv[k * F + f]);
+    if ((m & (m - 1ull)) == 0ull) {
+      single |= m;
+      continue;
     }
-    return;
-  }
-#pragma unroll
-  for (int gi = 0; gi < kGroups; gi++) {
-    if (gm[gi] == 0ull) break;
-    const bool mem = ((gm[gi] >> lane) & 1ull) != 0ull;
+    const bool mem = ((m >> lane) & 1ull) != 0ull;
     float v[NV];
 #pragma unroll
     for (int i = 0; i < NV; i++) v[i] = mem ? cv[i] : 0.0f;
@@ -104,28 +135,31 @@ __device__ __forceinline__ void scatter_level(bool on, const uint32_t gc[3], con
 #pragma unroll
     for (int st = 0; (NV >> (st + 1)) >= 1; st++) {
       const int n = NV >> (st + 1);
-      const int off = 32 >> st;
-      const bool up = (lane & (uint32_t)off) != 0u;
+      const int bit = 5 - st;
 #pragma unroll
-      for (int i = 0; i < n; i++) {
-        const float send = up ? v[i] : v[i + n];
-        const float keep = up ? v[i + n] : v[i];
-        v[i] = keep + __shfl_xor(send, off, 64);
-      }
-      if (up) vi += n;
+      for (int i = 0; i < n; i++) v[i] = halve(bit, v[i], v[i + n]);
+      if (((lane >> bit) & 1u) != 0u) vi += n;
     }
+    // lanes differing only in the bits below hold the same value index
 #pragma unroll
-    for (int off = kRep / 2; off >= 1; off >>= 1) v[0] += __shfl_xor(v[0], off, 64);
-    uint32_t bidx[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) bidx[k] = __shfl(idx[k], lead[gi], 64);
+    for (int bit = 0; (1 << bit) < kRep; bit++) v[0] = halve(bit, v[0], v[0]);
     if ((lane % kRep) == 0u && v[0] != 0.0f) {
       const int k = vi / F, f = vi % F;
-      uint32_t e = bidx[0];
+      uint32_t e = __builtin_amdgcn_readlane(idx[0], ld);
 #pragma unroll
-      for (int kk = 1; kk < 8; kk++) e = (k == kk) ? bidx[kk] : e;
+      for (int kk = 1; kk < 8; kk++) {
+        const uint32_t ek = __builtin_amdgcn_readlane(idx[kk], ld);
+        e = (k == kk) ? ek : e;
+      }
       atomic_add(dl + (size_t)e * F + f, v[0]);
     }
+  }
+  if (((single >> lane) & 1ull) != 0ull) {
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+#pragma unroll
+      for (int f = 0; f < F; f++)
+        if (cv[k * F + f] != 0.0f) atomic_add(dl + (size_t)idx[k] * F + f, cv[k * F + f]);
   }
 }
 
