@@ -48,12 +48,20 @@ constexpr int kRecChunks = 8;  // float4 chunks of the record staged per splat
 constexpr int kQueue = 4;      // pending hash lookups per pixel
 constexpr int kWaveLanes = 64;
 
-// Workgroup i runs on XCD i % 8; give XCD x a contiguous range of tiles.
+// Workgroup i runs on XCD i % 8.  Tiles are dealt to the XCDs in chunks of
+// kXcdChunk consecutive tiles (XCD x takes chunks x, x + 8, ...; a last
+// partial round of 8 chunks is dealt tile by tile), so every XCD gets work
+// from the whole image while neighbouring tiles still share an XCD's L2.
+// Measured on the 1M-splat frame, render ms: contiguous band per XCD 6.93,
+// chunks of 8 tiles 6.44, of 32 tiles 6.48, no XCD mapping 6.52; on the
+// 800x800 shell scene (splats concentrated mid-image) 3.32 / 2.76 / 2.69 /
+// 2.72: the banded mapping left the XCDs holding the image's empty rows idle.
+constexpr uint32_t kXcdChunk = 8;
 __device__ __forceinline__ uint32_t xcd_tile(uint32_t i, uint32_t n) {
-  const uint32_t q = n >> 3, rem = n & 7u;
   const uint32_t x = i & 7u, k = i >> 3;
-  const uint32_t start = x < rem ? x * (q + 1u) : rem * (q + 1u) + (x - rem) * q;
-  return start + k;
+  const uint32_t full = n / (8u * kXcdChunk);  // complete rounds of 8 chunks
+  if (k < full * kXcdChunk) return (k / kXcdChunk) * 8u * kXcdChunk + x * kXcdChunk + k % kXcdChunk;
+  return full * 8u * kXcdChunk + (k - full * kXcdChunk) * 8u + x;
 }
 
 __device__ __forceinline__ uint64_t lanemask_lt64() {
