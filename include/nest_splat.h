@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 6
+#define NEST_ABI_VERSION 7
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -213,7 +213,9 @@ int nest_binning_layout(int64_t num_rendered, size_t offsets[NEST_BIN_FIELDS], s
 #define NEST_IMG_N_CONTRIB 2       /* u32 [2,H,W]  (last, median) */
 #define NEST_IMG_LEVELS 3          /* 16 B [NEST_MAX_LEVELS] per-level lookup constants
                                       of the hash grid, written by nest_forward_render */
-#define NEST_IMG_FIELDS 4
+#define NEST_IMG_TILE_ORDER 4      /* u32 [tiles]  render launch order: tiles by descending
+                                      pair count (bucketed), written by nest_forward_render */
+#define NEST_IMG_FIELDS 5
 int nest_image_layout(int32_t width, int32_t height, size_t offsets[NEST_IMG_FIELDS], size_t *total_bytes);
 
 /* ---- forward rasterizer -------------------------------------------------

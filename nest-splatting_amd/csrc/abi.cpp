@@ -342,6 +342,7 @@ int nest_image_layout(int32_t W, int32_t H, size_t offsets[NEST_IMG_FIELDS], siz
   o[NEST_IMG_FINAL_T] = c.take(HW * 3 * 4);
   o[NEST_IMG_N_CONTRIB] = c.take(HW * 2 * 4);
   o[NEST_IMG_LEVELS] = c.take(sizeof(LevelQuad) * NEST_MAX_LEVELS);
+  o[NEST_IMG_TILE_ORDER] = c.take(tiles * 4);
   if (offsets)
     for (int i = 0; i < NEST_IMG_FIELDS; i++) offsets[i] = o[i];
   if (total) *total = c.off;
@@ -532,6 +533,7 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   rp.final_T = reinterpret_cast<float*>(im + io[NEST_IMG_FINAL_T]);
   rp.n_contrib = reinterpret_cast<uint32_t*>(im + io[NEST_IMG_N_CONTRIB]);
   rp.grid.lq = reinterpret_cast<LevelQuad*>(im + io[NEST_IMG_LEVELS]);
+  rp.tile_order = reinterpret_cast<uint32_t*>(im + io[NEST_IMG_TILE_ORDER]);
   tm.begin(NEST_STAGE_RENDER);
   if ((rc = check_stage(launch_render(rp, s), "render", rs->debug, s))) return rc;
   tm.end();

@@ -108,6 +108,7 @@ struct RenderParams {
   const uint32_t* point_list;
   const float* records;       // [P][32]
   const float* colors;        // [P][C] colour path; [P][cstride] per-splat features (mix)
+  uint32_t* tile_order;       // [tiles] launch order, written by launch_render
   float* out_color;
   float* out_others;
   float* final_T;

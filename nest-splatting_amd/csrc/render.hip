@@ -48,22 +48,6 @@ constexpr int kRecChunks = 8;  // float4 chunks of the record staged per splat
 constexpr int kQueue = 4;      // pending hash lookups per pixel
 constexpr int kWaveLanes = 64;
 
-// Workgroup i runs on XCD i % 8.  Tiles are dealt to the XCDs in chunks of
-// kXcdChunk consecutive tiles (XCD x takes chunks x, x + 8, ...; a last
-// partial round of 8 chunks is dealt tile by tile), so every XCD gets work
-// from the whole image while neighbouring tiles still share an XCD's L2.
-// Measured on the 1M-splat frame, render ms: contiguous band per XCD 6.93,
-// chunks of 8 tiles 6.44, of 32 tiles 6.48, no XCD mapping 6.52; on the
-// 800x800 shell scene (splats concentrated mid-image) 3.32 / 2.76 / 2.69 /
-// 2.72: the banded mapping left the XCDs holding the image's empty rows idle.
-constexpr uint32_t kXcdChunk = 8;
-__device__ __forceinline__ uint32_t xcd_tile(uint32_t i, uint32_t n) {
-  const uint32_t x = i & 7u, k = i >> 3;
-  const uint32_t full = n / (8u * kXcdChunk);  // complete rounds of 8 chunks
-  if (k < full * kXcdChunk) return (k / kXcdChunk) * 8u * kXcdChunk + x * kXcdChunk + k % kXcdChunk;
-  return full * 8u * kXcdChunk + (k - full * kXcdChunk) * 8u + x;
-}
-
 __device__ __forceinline__ uint64_t lanemask_lt64() {
   const uint32_t lane = threadIdx.x & (kWaveLanes - 1);
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
@@ -549,7 +533,7 @@ render_kernel(const RenderParams p) {
   __shared__ uint32_t hm[kMix ? kQueue : 1][kMix ? kRenderThreads : 1];
   __shared__ uint8_t isrc[kHash ? kRenderThreads : 1];  // compacted-drain item tables, 64 per wave
 
-  const uint32_t tile = xcd_tile(blockIdx.x, p.ntiles);
+  const uint32_t tile = p.tile_order[blockIdx.x];
   const uint32_t tx = tile % p.gx, ty = tile / p.gx;
   const uint32_t px = tx * kTile + (threadIdx.x & 15u);
   const uint32_t py = ty * kTile + (threadIdx.x >> 4);
@@ -807,6 +791,44 @@ static hipError_t launch_hash_levels(const RenderParams& p, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
+// Launch order of the render: tiles by descending pair count, in 256 buckets
+// of 8 log2(count + 1) (any order within a bucket), so the heaviest tiles
+// start first and the launch ends on light ones; workgroup i runs on XCD
+// i % 8, so the heavy tiles are dealt evenly over the XCDs.  A tile's pixels
+// do not depend on when it runs.  One workgroup.
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderBins = 256;
+
+__device__ __forceinline__ uint32_t order_bin(uint32_t n) {
+  const uint32_t b = (uint32_t)(8.0f * log2f((float)n + 1.0f));
+  return (uint32_t)(kOrderBins - 1) - (b < (uint32_t)(kOrderBins - 1) ? b : (uint32_t)(kOrderBins - 1));
+}
+
+__global__ void __launch_bounds__(kOrderThreads) tile_order_kernel(const uint2* ranges, uint32_t ntiles,
+                                                                  uint32_t* order) {
+  __shared__ uint32_t cnt[kOrderBins];
+  for (int b = threadIdx.x; b < kOrderBins; b += kOrderThreads) cnt[b] = 0u;
+  __syncthreads();
+  for (uint32_t t = threadIdx.x; t < ntiles; t += kOrderThreads) {
+    const uint2 r = ranges[t];
+    atomicAdd(&cnt[order_bin(r.y - r.x)], 1u);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t sum = 0u;
+    for (int b = 0; b < kOrderBins; b++) {
+      const uint32_t c = cnt[b];
+      cnt[b] = sum;
+      sum += c;
+    }
+  }
+  __syncthreads();
+  for (uint32_t t = threadIdx.x; t < ntiles; t += kOrderThreads) {
+    const uint2 r = ranges[t];
+    order[atomicAdd(&cnt[order_bin(r.y - r.x)], 1u)] = t;
+  }
+}
+
 struct LevelQuads {
   LevelQuad q[NEST_MAX_LEVELS];
 };
@@ -859,6 +881,10 @@ static hipError_t launch_hash(const RenderParams& p, hipStream_t s) {
 
 hipError_t launch_render(const RenderParams& p, hipStream_t s) {
   if (p.ntiles == 0) return hipSuccess;
+  hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, s, reinterpret_cast<const uint2*>(p.ranges),
+                     p.ntiles, p.tile_order);
+  const hipError_t oe = hipGetLastError();
+  if (oe != hipSuccess) return oe;
   if (p.mix && p.grid.F == 1) return hipErrorInvalidValue;
   if (p.level == 0 && !p.mix) {
     if (p.C <= 3) return launch_one<1, 3, false, false>(p, s);
