@@ -779,6 +779,7 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   rp.level = (int)gr->levels;
   rp.beta = rs->beta;
   rp.ranges = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_RANGES]);
+  rp.tile_order = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_TILE_ORDER]);
   rp.point_list = NR > 0 ? reinterpret_cast<const uint32_t*>(static_cast<const char*>(binning_ws) + bo[NEST_BIN_VALS])
                          : nullptr;
   rp.records = reinterpret_cast<const float*>(gw + go[NEST_GEOM_RECORDS]);

@@ -40,13 +40,6 @@ namespace {
 constexpr int kBwdThreads = 256;
 constexpr int kBwdChunks = 7;  // record chunks 0-6: T, xy, opacity, normal, ap, homotrans columns
 
-__device__ __forceinline__ uint32_t bwd_xcd_tile(uint32_t i, uint32_t n) {
-  const uint32_t q = n >> 3, rem = n & 7u;
-  const uint32_t x = i & 7u, k = i >> 3;
-  const uint32_t start = x < rem ? x * (q + 1u) : rem * (q + 1u) + (x - rem) * q;
-  return start + k;
-}
-
 // Cross-lane sums on the VALU (no LDS round trips): v_permlane32_swap /
 // v_permlane16_swap exchange lane halves (bits 5 and 4 of the lane index),
 // DPP row operations the rest.  halve<bit>(lo, hi) is one recursive-halving
@@ -283,7 +276,7 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
   __shared__ float4 srec[kBwdChunks][kBwdThreads];
   __shared__ uint32_t sid[kBwdThreads];
 
-  const uint32_t tile = bwd_xcd_tile(blockIdx.x, p.ntiles);
+  const uint32_t tile = p.tile_order[blockIdx.x];  // the forward's order: heaviest tiles first
   const uint32_t tx = tile % p.gx, ty = tile / p.gx;
   const uint32_t px = tx * kTile + (threadIdx.x & 15u);
   const uint32_t py = ty * kTile + (threadIdx.x >> 4);

@@ -170,6 +170,7 @@ struct RenderBwdParams {
   float beta;
   const uint32_t* ranges;
   const uint32_t* point_list;
+  const uint32_t* tile_order; // [tiles] the forward's launch order (heaviest tiles first)
   const float* records;       // [P][32]
   const float* colors;        // [P][C] colour path
   const float* final_T;       // [3][H][W]
