@@ -134,6 +134,56 @@ def finish_traffic(res: dict, copy_mib: int, out_path: str) -> dict:
     return res
 
 
+def time_aux_kernels(K, spec, scene, table, dev):
+    """HIP-event times of the RVQ decode (the 4-stage, 4096-entry compressed
+    scene: scale, rotation and opacity in one launch, 52 algorithmic bytes per
+    splat; at its 500k splats and at 4M) and of the GridEncoder forward (1M
+    points of this scene's grid, B·(12 + L·8·F·e + L·F·e) algorithmic bytes),
+    K launches each."""
+    import numpy as np
+    import torch
+
+    from gridencoder.grid import grid_encode_forward
+    from nest_splat import rvq
+    from nest_splat.scene import RVQ_BIAS, get_spec, make_scene
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(K):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / K
+
+    res = {}
+    rs = get_spec("cfg4", P=500_000)
+    rsc = make_scene(rs)
+    for P in (500_000, 4_000_000):
+        # the compressed scene's codebooks; 4M splats repeat its indices 8 times
+        reps = P // rs.P
+        idx = {a: np.tile(rsc.rvq_indices[a], (reps, 1)) for a in rsc.rvq_indices}
+        att = rvq.RVQAttributes.from_numpy(rsc.rvq_codebooks, idx, RVQ_BIAS, dev)
+        ms = timed(lambda: att.decode())
+        nbytes = 52 * P
+        res[f"rvq_decode_{P // 1000}k"] = {"ms": round(ms, 4), "splats": P, "algorithmic_bytes": nbytes,
+                                           "GB/s": round(nbytes / ms / 1e6, 1),
+                                           "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    B = 1_000_000
+    pts = torch.rand((B, 3), generator=torch.Generator(device=dev).manual_seed(3), device=dev)
+    offs = np.asarray(scene.offsets, np.int64)
+    ms = timed(lambda: grid_encode_forward(pts, table, offs, float(2.0 ** spec.S), spec.base_res))
+    e = scene.table.dtype.itemsize
+    nbytes = B * (12 + spec.L * 8 * spec.F * e + spec.L * spec.F * e)
+    res["grid_encode"] = {"ms": round(ms, 4), "points": B, "algorithmic_bytes": nbytes,
+                          "GB/s": round(nbytes / ms / 1e6, 1), "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    log(f"[bench] rvq decode {res['rvq_decode_500k']['ms']} / {res['rvq_decode_4000k']['ms']} ms (500k / 4M splats), "
+        f"grid encode {res['grid_encode']['ms']} ms")
+    return res
+
+
 def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_level, table, mlp, M, bg, dev,
                hyb=10):
     """Render modes 4 and 13 on the benchmark frame: the first `hyb` of the
@@ -211,6 +261,10 @@ def main():
                     help="after the timed frames, time K frames of each other render mode (4 cat, 13 "
                          "adaptive_cat_fast training and inference) on the same splats: per-splat rows of the "
                          "first 10 levels, a grid of the last 6, and report modes_ms (not part of the metric)")
+    ap.add_argument("--kernels", type=int, default=0, metavar="K",
+                    help="after the timed frames, time K launches of the other hot-path kernels on their own: the RVQ "
+                         "decode of the 500k-splat compressed scene and the GridEncoder forward of 1M points on this "
+                         "grid; reports aux_kernels with algorithmic GB/s (not part of the metric)")
     ap.add_argument("--backward", type=int, default=0, metavar="K",
                     help="after the timed forward frames, time K backward passes (nest_backward) of the last frame "
                          "with random output gradients and report backward_ms (not part of the metric)")
@@ -330,6 +384,8 @@ def main():
     if args.modes > 0:
         out["modes_ms"] = time_modes(args.modes, spec, scene, settings, means, opac, scales, rots, homo, ap_level,
                                      table, mlp, M, bg, dev)
+    if args.kernels > 0:
+        out["aux_kernels"] = time_aux_kernels(args.kernels, spec, scene, table, dev)
     if args.backward > 0:
         gen = torch.Generator(device=dev).manual_seed(0)
         dcol = torch.randn(tuple(res.color.shape), generator=gen, device=dev)

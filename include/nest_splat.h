@@ -372,6 +372,25 @@ int nest_rvq_decode(int64_t P, int32_t stages, int32_t codebook_size, int32_t di
                     const float *codebooks, const uint16_t *indices, const float *bias,
                     int32_t activation, float *out, float *raw_out, void *stream);
 
+/* Up to NEST_RVQ_BATCH_MAX attributes (e.g. scale, rotation, opacity) in one
+ * launch, each with the arguments of nest_rvq_decode.  No counterpart in the
+ * reference either; results equal separate nest_rvq_decode calls. */
+#define NEST_RVQ_BATCH_MAX 4
+typedef struct nest_rvq_attr {
+  uint32_t struct_size;
+  int64_t P;
+  int32_t stages;
+  int32_t codebook_size;
+  int32_t dim;
+  int32_t activation;
+  const float *codebooks;
+  const uint16_t *indices;
+  const float *bias;    /* dim floats or NULL */
+  float *out;
+  float *raw_out;       /* or NULL */
+} nest_rvq_attr;
+int nest_rvq_decode_batch(int32_t n, const nest_rvq_attr *attrs, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -879,17 +879,19 @@ int nest_mlp_decode(const nest_mlp* mlp, const float* feat, int64_t feat_cs, int
   return e == hipSuccess ? NEST_OK : hip_fail(e, "mlp_decode");
 }
 
-int nest_rvq_decode(int64_t P, int32_t stages, int32_t K, int32_t dim, const float* cb, const uint16_t* idx,
-                    const float* bias, int32_t activation, float* out, float* raw_out, void* stream) {
+namespace {
+// Validates one attribute's decode arguments and fills p (nothing to launch
+// when P == 0).
+int rvq_params(int64_t P, int32_t stages, int32_t K, int32_t dim, const float* cb, const uint16_t* idx,
+               const float* bias, int32_t activation, float* out, float* raw_out, RvqParams& p) {
   if (P < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "P must be >= 0");
   if (stages < 1 || stages > 16) return fail(NEST_ERR_UNSUPPORTED, "stages must be in [1, 16]");
   if (K < 1 || K > 65536) return fail(NEST_ERR_UNSUPPORTED, "codebook size must be in [1, 65536]");
   if (dim != 1 && dim != 2 && dim != 3 && dim != 4 && dim != 8)
     return fail(NEST_ERR_UNSUPPORTED, "dim must be 1, 2, 3, 4 or 8 (got %d)", dim);
   if (activation < 0 || activation > 3) return fail(NEST_ERR_INVALID_ARGUMENT, "activation must be 0..3");
-  if (P == 0) return NEST_OK;
-  if (!cb || !idx || !out) return fail(NEST_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
-  RvqParams p{};
+  if (P > 0 && (!cb || !idx || !out)) return fail(NEST_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  p = RvqParams{};
   p.P = P;
   p.stages = stages;
   p.K = K;
@@ -903,8 +905,35 @@ int nest_rvq_decode(int64_t P, int32_t stages, int32_t K, int32_t dim, const flo
   p.activation = activation;
   p.out = out;
   p.raw = raw_out;
+  return NEST_OK;
+}
+}  // namespace
+
+int nest_rvq_decode(int64_t P, int32_t stages, int32_t K, int32_t dim, const float* cb, const uint16_t* idx,
+                    const float* bias, int32_t activation, float* out, float* raw_out, void* stream) {
+  RvqParams p{};
+  const int rc = rvq_params(P, stages, K, dim, cb, idx, bias, activation, out, raw_out, p);
+  if (rc || P == 0) return rc;
   hipError_t e = launch_rvq(p, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? NEST_OK : hip_fail(e, "rvq_decode");
+}
+
+int nest_rvq_decode_batch(int32_t n, const nest_rvq_attr* attrs, void* stream) {
+  if (n < 0 || n > NEST_RVQ_BATCH_MAX)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "n must be in [0, %d] (got %d)", NEST_RVQ_BATCH_MAX, n);
+  if (n > 0 && !attrs) return fail(NEST_ERR_INVALID_ARGUMENT, "attrs is NULL");
+  RvqBatch b{};
+  for (int k = 0; k < n; k++) {
+    const nest_rvq_attr& a = attrs[k];
+    if (a.struct_size != sizeof(nest_rvq_attr))
+      return fail(NEST_ERR_INVALID_ARGUMENT, "nest_rvq_attr[%d].struct_size mismatch", k);
+    const int rc = rvq_params(a.P, a.stages, a.codebook_size, a.dim, a.codebooks, a.indices, a.bias, a.activation,
+                              a.out, a.raw_out, b.a[b.n]);
+    if (rc) return rc;
+    if (a.P > 0) b.n++;
+  }
+  hipError_t e = launch_rvq_batch(b, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? NEST_OK : hip_fail(e, "rvq_decode_batch");
 }
 
 }  // extern "C"

@@ -285,5 +285,11 @@ struct RvqParams {
   float* raw;
 };
 hipError_t launch_rvq(const RvqParams& p, hipStream_t s);
+constexpr int kRvqBatchMax = 4;
+struct RvqBatch {
+  RvqParams a[kRvqBatchMax];
+  int n;
+};
+hipError_t launch_rvq_batch(const RvqBatch& b, hipStream_t s);
 
 }  // namespace nest

@@ -30,9 +30,7 @@ __device__ __forceinline__ void load_row(const float* cb, size_t row, float v[DI
 }
 
 template <int DIM>
-__global__ void __launch_bounds__(256) rvq_kernel(const RvqParams p) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= p.P) return;
+__device__ __forceinline__ void rvq_one(const RvqParams& p, int64_t i) {
   float v[DIM];
   const uint16_t* idx = p.idx + i * p.stages;
   bool bad = false;
@@ -79,6 +77,28 @@ __global__ void __launch_bounds__(256) rvq_kernel(const RvqParams p) {
   for (int d = 0; d < DIM; d++) p.out[i * DIM + d] = v[d];
 }
 
+template <int DIM>
+__global__ void __launch_bounds__(256) rvq_kernel(const RvqParams p) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < p.P) rvq_one<DIM>(p, i);
+}
+
+// Several attributes in one launch (blockIdx.y picks the attribute): the
+// decode of a splat set is a few MB, so one launch instead of three is most
+// of its time.
+__global__ void __launch_bounds__(256) rvq_batch_kernel(const RvqBatch b) {
+  const RvqParams& p = b.a[blockIdx.y];
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.P) return;
+  switch (p.dim) {
+    case 1: rvq_one<1>(p, i); break;
+    case 2: rvq_one<2>(p, i); break;
+    case 3: rvq_one<3>(p, i); break;
+    case 4: rvq_one<4>(p, i); break;
+    default: rvq_one<8>(p, i); break;
+  }
+}
+
 hipError_t launch_rvq(const RvqParams& p, hipStream_t s) {
   if (p.P <= 0) return hipSuccess;
   const dim3 grid((unsigned)((p.P + 255) / 256));
@@ -90,6 +110,14 @@ hipError_t launch_rvq(const RvqParams& p, hipStream_t s) {
     case 8: hipLaunchKernelGGL(rvq_kernel<8>, grid, dim3(256), 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_rvq_batch(const RvqBatch& b, hipStream_t s) {
+  int64_t pmax = 0;
+  for (int k = 0; k < b.n; k++) pmax = b.a[k].P > pmax ? b.a[k].P : pmax;
+  if (pmax <= 0 || b.n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rvq_batch_kernel, dim3((unsigned)((pmax + 255) / 256), (unsigned)b.n), dim3(256), 0, s, b);
   return hipGetLastError();
 }
 

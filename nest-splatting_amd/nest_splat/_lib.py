@@ -109,6 +109,15 @@ class Mlp(ct.Structure):
                 ("dtype", ct.c_int32), ("w1", ct.c_void_p), ("w2", ct.c_void_p), ("w3", ct.c_void_p)]
 
 
+class RvqAttr(ct.Structure):
+    _fields_ = [("struct_size", ct.c_uint32), ("P", ct.c_int64), ("stages", ct.c_int32),
+                ("codebook_size", ct.c_int32), ("dim", ct.c_int32), ("activation", ct.c_int32),
+                ("codebooks", ct.c_void_p), ("indices", ct.c_void_p), ("bias", ct.POINTER(ct.c_float)),
+                ("out", ct.c_void_p), ("raw_out", ct.c_void_p)]
+
+
+RVQ_BATCH_MAX = 4
+
 EXPORTS = {
     "nest_abi_version": (ct.c_int, []),
     "nest_last_error": (ct.c_char_p, []),
@@ -145,6 +154,7 @@ EXPORTS = {
                                    ct.c_void_p, ct.c_int64, ct.c_int64, ct.c_void_p]),
     "nest_rvq_decode": (ct.c_int, [ct.c_int64, ct.c_int32, ct.c_int32, ct.c_int32, ct.c_void_p, ct.c_void_p,
                                    ct.POINTER(ct.c_float), ct.c_int32, ct.c_void_p, ct.c_void_p, ct.c_void_p]),
+    "nest_rvq_decode_batch": (ct.c_int, [ct.c_int32, ct.POINTER(RvqAttr), ct.c_void_p]),
 }
 
 _lib = None

@@ -62,11 +62,35 @@ class RVQAttributes:
         return cls(cb, ix, bias)
 
     def decode(self, raw: bool = False) -> Dict[str, torch.Tensor]:
-        out = {}
-        for a in ("scale", "rotation", "opacity"):
+        """Decodes the three attributes in one launch (nest_rvq_decode_batch)."""
+        out, keep = {}, []
+        attrs = (L.RvqAttr * 3)()
+        for k, a in enumerate(("scale", "rotation", "opacity")):
             cb = self.codebooks[a]
-            r = torch.empty((self.indices[a].shape[0], cb.shape[2]), dtype=torch.float32, device=cb.device) if raw else None
-            out[a] = rvq_decode(cb, self.indices[a], self.bias.get(a), ACTIVATION[a], raw_out=r)
+            idx = self.indices[a]
+            if cb.dtype != torch.float32 or cb.dim() != 3 or idx.element_size() != 2 or idx.dim() != 2:
+                raise ValueError(f"{a}: codebooks must be float32 [S, K, dim], indices 16-bit [P, S]")
+            S, K, dim = cb.shape
+            if idx.shape[1] != S:
+                raise ValueError(f"{a}: indices have {idx.shape[1]} stages, codebooks {S}")
+            cb = cb.contiguous()
+            if cb.data_ptr() % 16:
+                cb = cb.clone()
+            idx = idx.contiguous()
+            P = idx.shape[0]
+            o = torch.empty((P, dim), dtype=torch.float32, device=cb.device)
+            r = torch.empty((P, dim), dtype=torch.float32, device=cb.device) if raw else None
+            b = self.bias.get(a)
+            bc = None
+            if b is not None:
+                bv = np.asarray(b, dtype=np.float32).reshape(-1)
+                bc = (ct.c_float * dim)(*[float(v) for v in bv])
+            keep += [cb, idx, bc]
+            attrs[k] = L.RvqAttr(ct.sizeof(L.RvqAttr), P, S, K, dim, ACTIVATION[a], L.ptr(cb), L.ptr(idx),
+                                 ct.cast(bc, ct.POINTER(ct.c_float)) if bc is not None else None, L.ptr(o), L.ptr(r))
+            out[a] = o
             if raw:
                 out[a + "_raw"] = r
+        dev = self.codebooks["scale"].device
+        L.check(L.lib().nest_rvq_decode_batch(3, attrs, L.stream_ptr(dev)), "nest_rvq_decode_batch")
         return out

@@ -239,6 +239,15 @@ def test_building_block_validation():
         L.NEST_ERR_UNSUPPORTED
     assert lib.nest_rvq_decode(10, 4, 4096, 5, None, None, None, 0, None, None, None) == L.NEST_ERR_UNSUPPORTED
     assert lib.nest_rvq_decode(10, 4, 4096, 2, None, None, None, 7, None, None, None) == L.NEST_ERR_INVALID_ARGUMENT
+    attrs = (L.RvqAttr * 5)()
+    for a in attrs:
+        a.struct_size, a.P, a.stages, a.codebook_size, a.dim = ct.sizeof(L.RvqAttr), 0, 4, 4096, 2
+    assert lib.nest_rvq_decode_batch(5, attrs, None) == L.NEST_ERR_INVALID_ARGUMENT  # at most 4 attributes
+    assert lib.nest_rvq_decode_batch(3, attrs, None) == L.NEST_OK  # empty attributes launch nothing
+    attrs[1].dim = 5
+    assert lib.nest_rvq_decode_batch(3, attrs, None) == L.NEST_ERR_UNSUPPORTED
+    attrs[1].dim, attrs[2].struct_size = 2, 8
+    assert lib.nest_rvq_decode_batch(3, attrs, None) == L.NEST_ERR_INVALID_ARGUMENT
 
 
 def test_python_errors_are_raised():
