@@ -235,6 +235,26 @@ def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_lev
             L.timing_release(tm)
         res_ms[name] = {"render_ms": round(render_ms, 4), "frame_ms": round(frame_ms, 4)}
         log(f"[bench] {name}: render {render_ms:.3f} ms, frame {frame_ms:.3f} ms")
+        if mode == 4:
+            # training step of mode 4: the backward of the last frame, every
+            # grid level active, random output gradients
+            res, _ = frame()
+            gen = torch.Generator(device=dev).manual_seed(0)
+            dcol = torch.randn(tuple(res.color.shape), generator=gen, device=dev)
+            doth = torch.randn(tuple(res.others.shape), generator=gen, device=dev)
+
+            def bwd():
+                return rz.rasterize_backward(settings, grid, res, means, opac, scales, rots, dcol, doth,
+                                             homotrans=homo, ap_level=ap_level, colors_precomp=rows_t,
+                                             channels=spec.C)
+            bwd()
+            torch.cuda.synchronize()
+            b0 = time.perf_counter()
+            for _ in range(K):
+                bwd()
+            torch.cuda.synchronize()
+            res_ms[name]["backward_ms"] = round((time.perf_counter() - b0) / K * 1e3, 3)
+            log(f"[bench] {name}: backward {res_ms[name]['backward_ms']} ms")
     return res_ms
 
 
@@ -260,7 +280,8 @@ def main():
     ap.add_argument("--modes", type=int, default=0, metavar="K",
                     help="after the timed frames, time K frames of each other render mode (4 cat, 13 "
                          "adaptive_cat_fast training and inference) on the same splats: per-splat rows of the "
-                         "first 10 levels, a grid of the last 6, and report modes_ms (not part of the metric)")
+                         "first 10 levels, a grid of the last 6, and report modes_ms, with K backward passes of mode 4 "
+                         "(not part of the metric)")
     ap.add_argument("--kernels", type=int, default=0, metavar="K",
                     help="after the timed frames, time K launches of the other hot-path kernels on their own: the RVQ "
                          "decode of the 500k-splat compressed scene and the GridEncoder forward of 1M points on this "

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 7
+#define NEST_ABI_VERSION 8
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -105,6 +105,13 @@ typedef struct nest_hashgrid {
   int32_t render_mode;
   uint32_t hybrid_levels;
   uint32_t total_levels;
+  /* Render mode 4, backward only: the active grid-level count of the
+   * reference's packed level (bits 8-15, coarse-to-fine training).  The
+   * reference's backward copies the offsets only up to it and differentiates
+   * the grid levels up to the last one whose offsets increase within that
+   * copy (CR/backward.cu:576-612, :993-999), while the forward renders all
+   * `levels`; nest_backward does the same.  The forward ignores it. */
+  uint32_t active_levels;
 } nest_hashgrid;
 
 #define NEST_MODE_BASELINE 0
@@ -249,8 +256,11 @@ int nest_forward_render(const nest_raster_settings *settings, const nest_hashgri
 /* ---- backward (training) ------------------------------------------------
  * nest_backward is RasterizeGaussiansBackwardCUDA
  * (DSR/rasterize_points.cu:243-471) / CudaRasterizer::Rasterizer::backward
- * (CR/rasterizer_impl.cu:444-600) for render mode 0 with the Gaussian
- * kernel: renderCUDAsurfelBackward (CR/backward.cu:445-2049) then
+ * (CR/rasterizer_impl.cu:444-600) for render modes 0 and 4 (mode 4:
+ * CR/backward.cu:987-1040, gradients of the per-splat rows into dL_dcolors
+ * [P, hybrid_levels*level_dim], of the grid's active levels into
+ * dL_dfeatures) with the Gaussian kernel: renderCUDAsurfelBackward
+ * (CR/backward.cu:445-2049) then
  * preprocessCUDA backward (CR/backward.cu:2216-2274).  It reads the
  * workspaces of the nest_forward_geometry / nest_forward_render calls of the
  * same frame (unchanged since) and the same settings, grid and splats.  Every
@@ -274,7 +284,8 @@ typedef struct {
     const float *dL_dout_others;     /* [14,H,W]; channels 0-6 carry gradient */
     float *dL_dmeans3D;              /* [P,3] */
     float *dL_dmeans2D;              /* [P,3] densification statistic */
-    float *dL_dcolors;               /* [P,C] colour path, or NULL */
+    float *dL_dcolors;               /* [P,C] colour path, [P,hybrid_levels*level_dim]
+                                        in render mode 4, or NULL */
     float *dL_dopacity;              /* [P] */
     float *dL_dshs;                  /* [P,sh_coeffs,3] when the colours came from SH */
     float *dL_dscales;               /* [P,2] */

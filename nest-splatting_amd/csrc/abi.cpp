@@ -707,9 +707,10 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
     return fail(NEST_ERR_INVALID_ARGUMENT, "nest_hashgrid missing or struct_size mismatch");
   if (!io || io->struct_size != sizeof(nest_backward_io))
     return fail(NEST_ERR_INVALID_ARGUMENT, "nest_backward_io missing or struct_size mismatch");
-  if (gr->render_mode != NEST_MODE_BASELINE)
-    return fail(NEST_ERR_UNSUPPORTED, "backward: render_mode %d is forward-only here (mode 0 has a backward)",
+  if (gr->render_mode != NEST_MODE_BASELINE && gr->render_mode != NEST_MODE_CAT)
+    return fail(NEST_ERR_UNSUPPORTED, "backward: render_mode %d is forward-only here (modes 0 and 4 have a backward)",
                 gr->render_mode);
+  const bool cat = gr->render_mode == NEST_MODE_CAT;
   const int C = io->channels;
   if (C < 1 || C > 64) return fail(NEST_ERR_UNSUPPORTED, "backward: channels must be in [1, 64] (got %d)", C);
   if (!io->dL_dout_color || !io->dL_dout_others)
@@ -721,7 +722,19 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   GridParams g{};
   if ((rc = setup_grid(rs, gr, sp, C, g))) return rc;
   const bool hash = gr->levels > 0;
-  const bool from_sh = !hash && sh_colours(sp);
+  const bool from_sh = !cat && !hash && sh_colours(sp);
+  // mode 4: per-splat rows of pgd floats; the grid levels differentiated are
+  // those up to the last one within the active count whose offsets increase
+  // (CR/backward.cu:576-612, :993-999)
+  const int pgd = cat ? (int)(gr->hybrid_levels * gr->level_dim) : 0;
+  uint32_t cat_levels = 0;
+  if (cat) {
+    const uint32_t act = gr->active_levels < gr->levels ? gr->active_levels : gr->levels;
+    for (uint32_t i = 1; i <= act; i++)
+      if (gr->offsets[i] > gr->offsets[i - 1]) cat_levels = i;
+    g.L = cat_levels;
+  }
+  const int dcol_width = cat ? pgd : C;
   if (hash && g.half) return fail(NEST_ERR_UNSUPPORTED, "backward: the hash table must be float32");
   if (hash && !io->dL_dfeatures) return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dfeatures is required");
   if (from_sh && !io->dL_dshs) return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dshs is required with SH colours");
@@ -758,7 +771,7 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
     float* p;
     int64_t n;
   } fills[] = {{dtransmat, (int64_t)P * 9}, {dhomo, (int64_t)P * 9}, {dnormal, (int64_t)P * 3},
-               {dcolors, (int64_t)P * C}, {gradsum, (int64_t)P}, {io->dL_dmeans3D, (int64_t)P * 3},
+               {dcolors, (int64_t)P * dcol_width}, {gradsum, (int64_t)P}, {io->dL_dmeans3D, (int64_t)P * 3},
                {io->dL_dmeans2D, (int64_t)P * 3}, {io->dL_dopacity, (int64_t)P}, {io->dL_dscales, (int64_t)P * 2},
                {io->dL_drotations, (int64_t)P * 4}, {from_sh ? io->dL_dshs : nullptr, (int64_t)P * M * 3},
                {hash ? io->dL_dfeatures : nullptr, hash ? (int64_t)gr->table_rows * gr->level_dim : 0}};
@@ -776,7 +789,8 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   rp.gy = gy;
   rp.ntiles = gx * gy;
   rp.C = C;
-  rp.level = (int)gr->levels;
+  rp.level = cat ? 1 : (int)gr->levels;  // mode 4 always takes the hash branch
+  rp.pgd = pgd;
   rp.beta = rs->beta;
   rp.ranges = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_RANGES]);
   rp.tile_order = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_TILE_ORDER]);

@@ -271,7 +271,9 @@ __device__ __forceinline__ bool grid_coord_bwd(const GridParams& g, const float 
   return true;
 }
 
-template <int F, bool kHash>
+// kRows: render mode 4, per-splat feature rows (p.colors, p.pgd wide) ahead of
+// the grid's channels (CR/backward.cu:987-1040).
+template <int F, bool kHash, bool kRows>
 __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const RenderBwdParams p) {
   __shared__ float4 srec[kBwdChunks][kBwdThreads];
   __shared__ uint32_t sid[kBwdThreads];
@@ -369,7 +371,7 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
       float gT[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0}, gH[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
       float gM[2] = {0.0f, 0.0f}, gN[3] = {0.0f, 0.0f, 0.0f}, gO = 0.0f, gS = 0.0f;
       float wcol = 0.0f;  // dchannel_dcolor of the colour path
-      float wgt = 0.0f, dot = 0.0f;
+      float wgt = 0.0f, dot = 0.0f, rdot = 0.0f;
       float dxyz[3] = {0.0f, 0.0f, 0.0f};
       float u[3] = {0.0f, 0.0f, 0.0f}, grad_scale = 0.0f;
       uint32_t lane_levels = 0u;
@@ -391,6 +393,11 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
             xyz[0] = q5.z; xyz[1] = q5.w; xyz[2] = q6.x;
           }
           gS = wgt * sum_abs;
+          if constexpr (kRows) {
+            const float* row = p.colors + (size_t)id * p.pgd;
+            for (int ch = 0; ch < p.pgd; ch++) rdot += row[ch] * dpix[(size_t)ch * HW];
+            wcol = wgt;
+          }
           const uint32_t ap = __float_as_uint(q3.w);
           const uint32_t maxl = ap < g.L ? ap : g.L;
           lane_levels = grid_coord_bwd(g, xyz, u, grad_scale) ? maxl : 0u;
@@ -399,7 +406,9 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
       if constexpr (kHash) {
         // every lane takes part (cross-lane sums inside); lanes without a hit have no levels
         if (__ballot(lane_levels > 0u) != 0ull)
-          hash_backward_wave<F>(g, rsrc, u, grad_scale, lane_levels, wgt, dpix, HW, p.dtable, dot, dxyz);
+          hash_backward_wave<F>(g, rsrc, u, grad_scale, lane_levels, wgt, kRows ? dpix + (size_t)p.pgd * HW : dpix, HW,
+                                p.dtable, dot, dxyz);
+        if constexpr (kRows) dot += rdot;
       }
       if (act) {
         if constexpr (kHash) {
@@ -492,6 +501,12 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
           }
           const float vs = wave_sum(gS);
           if (lead && vs != 0.0f) atomic_add(p.gradsum + id, vs);
+          if constexpr (kRows) {
+            for (int ch = 0; ch < p.pgd; ch++) {
+              const float v = wave_sum(wcol * dpix[(size_t)ch * HW]);
+              if (lead && v != 0.0f) atomic_add(p.dcolors + (size_t)id * p.pgd + ch, v);
+            }
+          }
         } else {
           for (int ch = 0; ch < C; ch++) {
             const float v = wave_sum(inside ? wcol * dpix[(size_t)ch * HW] : 0.0f);
@@ -515,9 +530,9 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
   }
 }
 
-template <int F, bool kHash>
+template <int F, bool kHash, bool kRows = false>
 hipError_t launch_bwd_one(const RenderBwdParams& p, hipStream_t s) {
-  hipLaunchKernelGGL((render_backward_kernel<F, kHash>), dim3(p.ntiles), dim3(kBwdThreads), 0, s, p);
+  hipLaunchKernelGGL((render_backward_kernel<F, kHash, kRows>), dim3(p.ntiles), dim3(kBwdThreads), 0, s, p);
   return hipGetLastError();
 }
 
@@ -818,6 +833,14 @@ hipError_t launch_grid_encode_backward(const GridEncodeBwdParams& p, hipStream_t
 
 hipError_t launch_render_backward(const RenderBwdParams& p, hipStream_t s) {
   if (p.ntiles == 0) return hipSuccess;
+  if (p.pgd > 0) {
+    switch (p.grid.F) {
+      case 2: return launch_bwd_one<2, true, true>(p, s);
+      case 4: return launch_bwd_one<4, true, true>(p, s);
+      case 8: return launch_bwd_one<8, true, true>(p, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (p.level == 0) return launch_bwd_one<1, false>(p, s);
   switch (p.grid.F) {
     case 1: return launch_bwd_one<1, true>(p, s);

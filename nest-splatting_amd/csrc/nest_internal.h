@@ -172,7 +172,7 @@ struct RenderBwdParams {
   const uint32_t* point_list;
   const uint32_t* tile_order; // [tiles] the forward's launch order (heaviest tiles first)
   const float* records;       // [P][32]
-  const float* colors;        // [P][C] colour path
+  const float* colors;        // [P][C] colour path, [P][pgd] mode-4 rows
   const float* final_T;       // [3][H][W]
   const uint32_t* n_contrib;  // [2][H][W]
   const float* dL_dpix;       // [C][H][W]
@@ -183,8 +183,9 @@ struct RenderBwdParams {
   float* dmean2D;             // [P][3]
   float* dnormal;             // [P][3]
   float* dopacity;            // [P]
-  float* dcolors;             // [P][C] colour path
+  float* dcolors;             // [P][C] colour path, [P][pgd] per-splat rows
   float* gradsum;             // [P] hash path
+  int pgd;                    // render mode 4: per-splat row width (0 otherwise)
   GridParams grid;
 };
 hipError_t launch_render_backward(const RenderBwdParams& p, hipStream_t s);

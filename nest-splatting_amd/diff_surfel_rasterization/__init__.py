@@ -11,10 +11,12 @@ markVisible (:310-319) and rasterize_gaussians (:21-66).
 Scope: render mode 0 ("baseline") with the Gaussian kernel, forward and
 backward: hash-grid features when HashGridSettings.L > 0; when L == 0,
 precomputed per-splat colours or RGB evaluated from SH coefficients
-(degree <= 3) in preprocess.  Render modes 4 ("cat": per-splat features of
-the coarse levels ahead of a grid of the fine ones) and 13
-("adaptive_cat_fast", with the inference flag 0x100) forward, with the
-reference's packed L (total << 16 | grid levels << 8 | per-splat levels).  The backward returns the reference's gradients
+(degree <= 3) in preprocess.  Render mode 4 ("cat": per-splat features of
+the coarse levels ahead of a grid of the fine ones) forward and backward,
+and 13 ("adaptive_cat_fast", with the inference flag 0x100) forward, with
+the reference's packed L (total << 16 | grid levels << 8 | per-splat
+levels; the backward differentiates the grid levels within the active
+count, CR/backward.cu:576-612).  The backward returns the reference's gradients
 (DSRpy:174-275): means3D, the means2D densification statistic, SH,
 colours, opacities, scales, rotations, the hash table, and the |grad| sum in
 the ap_level slot; it needs a float32 hash table and at most 64 channels.
@@ -89,7 +91,7 @@ def _mixed_grid(hs, render_mode, level, features, offsets, gridrange):
                             base_resolution=int(hs.H), table=table, offsets=offs,
                             gridrange=_rz.host_array(gridrange, np.float32), align_corners=bool(hs.align_corners),
                             interpolation=int(hs.interpolation), render_mode=int(render_mode), hybrid_levels=hyb,
-                            total_levels=total)
+                            total_levels=total, active_levels=(level >> 8) & 0xFF)
 
 
 class _RasterizeGaussians(torch.autograd.Function):
@@ -168,9 +170,9 @@ class _RasterizeGaussians(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out_color, grad_radii, grad_depth, grad_0, grad_1):
-        if ctx.render_mode != 0:
+        if ctx.render_mode not in (0, 4):
             raise NotImplementedError(f"render_mode {ctx.render_mode} is forward-only here; "
-                                      f"the backward covers mode 0")
+                                      f"the backward covers modes 0 and 4")
         means3D, opacities, scales, rotations = ctx.saved_tensors
         fw = ctx.fw
         g = _rz.rasterize_backward(fw["settings"], fw["grid"], fw["res"], means3D.detach(), opacities.detach(),

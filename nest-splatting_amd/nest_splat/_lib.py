@@ -27,7 +27,7 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
  GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
 GEOM_FIELDS = 12
@@ -54,7 +54,8 @@ class HashGrid(ct.Structure):
                 ("interpolation", ct.c_int32), ("table_dtype", ct.c_int32), ("table", ct.c_void_p),
                 ("table_rows", ct.c_int64), ("offsets", ct.c_int32 * (MAX_LEVELS + 1)),
                 ("gridrange", ct.c_float * 2), ("render_mode", ct.c_int32), ("hybrid_levels", ct.c_uint32),
-                ("total_levels", ct.c_uint32)]
+                ("total_levels", ct.c_uint32),
+                ("active_levels", ct.c_uint32)]
 
 
 MODE_BASELINE = 0

@@ -54,6 +54,9 @@ class HashGridDesc:
     render_mode: int = 0
     hybrid_levels: int = 0
     total_levels: int = 0
+    # render_mode 4 backward: the grid levels it differentiates are those up to
+    # the active count (coarse-to-fine training); None = all `levels`
+    active_levels: Optional[int] = None
 
     def row_width(self, channels: int) -> int:
         """Floats per splat of colors_precomp for this render mode."""
@@ -70,6 +73,7 @@ class HashGridDesc:
         g.render_mode = int(self.render_mode)
         g.hybrid_levels = int(self.hybrid_levels)
         g.total_levels = int(self.total_levels)
+        g.active_levels = int(self.levels if self.active_levels is None else self.active_levels)
         g.levels = int(self.levels)
         g.level_dim = int(self.level_dim)
         g.log2_scale = float(self.log2_scale)
@@ -283,7 +287,7 @@ def rasterize_backward(settings: L.RasterSettings, grid: HashGridDesc, res: Forw
     P = int(means3D.shape[0])
     H, W = settings.image_height, settings.image_width
     sp, keep = _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, channels, shs,
-                       sh_degree)
+                       sh_degree, grid.row_width(channels))
     g = grid.to_c()
     if dL_dcolor is None:
         dL_dcolor = torch.zeros((channels, H, W), dtype=torch.float32, device=dev)
@@ -296,7 +300,7 @@ def rasterize_backward(settings: L.RasterSettings, grid: HashGridDesc, res: Forw
     f32 = dict(dtype=torch.float32, device=dev)
     out = BackwardResult(
         dmeans3D=torch.empty((P, 3), **f32), dmeans2D=torch.empty((P, 3), **f32),
-        dcolors=torch.empty((P, channels), **f32), dopacity=torch.empty((P, 1), **f32),
+        dcolors=torch.empty((P, grid.row_width(channels)), **f32), dopacity=torch.empty((P, 1), **f32),
         dshs=None, dscales=torch.empty((P, 2), **f32), drotations=torch.empty((P, 4), **f32),
         dfeatures=None, dgradsum=torch.empty((P, 1), **f32))
     if grid.levels > 0:

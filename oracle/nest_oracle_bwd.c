@@ -136,7 +136,7 @@ static void qf_backward(const or_grid *G, const float xyz[3], uint32_t ap, int C
 }
 
 /* ------------------------------------------------------------------ */
-/* render backward: CR/backward.cu:445-2049 (mode 0, kernel_type 0)     */
+/* render backward: CR/backward.cu:445-2049 (modes 0 and 4, kernel 0)   */
 /* ------------------------------------------------------------------ */
 
 typedef struct {
@@ -164,9 +164,30 @@ typedef struct {
     float *dmean2D;              /* [P][3]                                 */
     float *dnormal;              /* [P][3]                                 */
     float *dopacity;             /* [P]                                    */
-    float *dcolors;              /* [P][C]                                 */
+    float *dcolors;              /* [P][C]; [P][hyb*F] in render mode 4    */
     float *gradsum;              /* [P]                                    */
+    /* 0, or 4 (hybrid_features, CR/backward.cu:987-1040) with `level` the
+     * packed (total << 16) | (active grid levels << 8) | per-splat levels
+     * and colors the [P][hyb*F] per-splat rows */
+    int render_mode;
 } or_render_bwd_args;
+
+/* Grid levels the mode-4 backward differentiates (CR/backward.cu:576-612,
+ * :993-999): the offsets are copied only up to the active count of bits 8-15
+ * (the rest stay 0), and the levels are the largest i in 1..16 with
+ * offsets[i] > offsets[i-1] over that copy.  The forward counts all of the
+ * grid's levels, so with fewer active levels the backward recomputes and
+ * differentiates only the active ones. */
+static int cat_hash_levels_bwd(const or_grid *G, int active)
+{
+    int hl = 0;
+    for (int i = 1; i < 17; i++) {
+        int32_t a = (i - 1 <= active && i - 1 <= G->L) ? G->offsets[i - 1] : 0;
+        int32_t b = (i <= active && i <= G->L) ? G->offsets[i] : 0;
+        if (b > a) hl = i;
+    }
+    return hl;
+}
 
 static void render_pixel_bwd(const or_render_bwd_args *A, uint32_t tile, uint32_t px, uint32_t py, float *scr)
 {
@@ -243,7 +264,7 @@ static void render_pixel_bwd(const or_render_bwd_args *A, uint32_t tile, uint32_
         float dxyz[3] = {0.0f, 0.0f, 0.0f};
         const float *Hm = A->homotrans ? A->homotrans + 16 * (size_t)id : NULL;
 
-        if (A->level == 0) {
+        if (A->level == 0 && A->render_mode == 0) {
             for (int ch = 0; ch < C; ch++) {
                 const float c = A->colors[(size_t)id * C + ch];
                 accum_rec[ch] = last_alpha * last_color[ch] + (1.f - last_alpha) * accum_rec[ch];
@@ -267,7 +288,21 @@ static void render_pixel_bwd(const or_render_bwd_args *A, uint32_t tile, uint32_
             }
             A->gradsum[id] += sum_grad;
             const uint32_t ap = f2u_sat(floorf(A->ap_level[id]));
-            qf_backward(&A->grid, xyz, ap, C, grad_feat, feat, A->dtable, dxyz);
+            if (A->render_mode == 4) {
+                /* rows then the active grid levels (CR/backward.cu:987-1040) */
+                const int pgd = (A->level & 0xFF) * A->grid.F;
+                for (int ch = 0; ch < C; ch++) feat[ch] = 0.0f;
+                for (int i = 0; i < pgd; i++) feat[i] = A->colors[(size_t)id * pgd + i];
+                const int hl = cat_hash_levels_bwd(&A->grid, (A->level >> 8) & 0xFF);
+                if (hl > 0) {
+                    or_grid G = A->grid;
+                    G.L = hl;
+                    qf_backward(&G, xyz, ap, C - pgd, grad_feat + pgd, feat + pgd, A->dtable, dxyz);
+                }
+                for (int i = 0; i < pgd; i++) A->dcolors[(size_t)id * pgd + i] += grad_feat[i];
+            } else {
+                qf_backward(&A->grid, xyz, ap, C, grad_feat, feat, A->dtable, dxyz);
+            }
             for (int ch = 0; ch < C; ch++) {
                 const float c = feat[ch];
                 accum_rec[ch] = last_alpha * last_color[ch] + (1.f - last_alpha) * accum_rec[ch];

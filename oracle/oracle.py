@@ -56,7 +56,8 @@ class OrRenderBwdArgs(ct.Structure):
                 ("final_T", ct.c_void_p), ("n_contrib", ct.c_void_p), ("dL_dpix", ct.c_void_p),
                 ("dL_dothers", ct.c_void_p), ("dtable", ct.c_void_p), ("dtransmat", ct.c_void_p),
                 ("dhomo", ct.c_void_p), ("dmean2D", ct.c_void_p), ("dnormal", ct.c_void_p),
-                ("dopacity", ct.c_void_p), ("dcolors", ct.c_void_p), ("gradsum", ct.c_void_p)]
+                ("dopacity", ct.c_void_p), ("dcolors", ct.c_void_p), ("gradsum", ct.c_void_p),
+                ("render_mode", ct.c_int)]
 
 
 def lib():
@@ -239,17 +240,21 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
 
 
 def render_backward(pre, binres, fwd, W, H, C, grid: Optional[OrGrid], dL_dpix, dL_dothers, homotrans=None,
-                    ap_level=None, colors=None, beta=0.0):
-    """renderCUDAsurfelBackward (mode 0) for every pixel, given the forward's
-    final_T / n_contrib (fwd = render(...)'s result).  Returns the per-splat
-    gradients (dtransmat [P,9], dhomo [P,9], dmean2D [P,3], dnormal [P,3],
-    dopacity [P], dcolors [P,C], gradsum [P]) and dtable [rows, F]."""
+                    ap_level=None, colors=None, beta=0.0, render_mode=0, level=None):
+    """renderCUDAsurfelBackward (modes 0 and 4) for every pixel, given the
+    forward's final_T / n_contrib (fwd = render(...)'s result).  Returns the
+    per-splat gradients (dtransmat [P,9], dhomo [P,9], dmean2D [P,3],
+    dnormal [P,3], dopacity [P], dcolors [P,C], or [P,hyb*F] in mode 4,
+    gradsum [P]) and dtable [rows, F].  Mode 4 takes the packed level
+    (total << 16) | (active grid levels << 8) | per-splat levels and the
+    per-splat rows as colors."""
     P = pre["radii"].shape[0]
     rows = 0 if grid is None else grid._keep[1].shape[0]
     F = 1 if grid is None else grid.F
+    dcol = C if render_mode == 0 else (level & 0xFF) * F
     out = dict(dtransmat=np.zeros((P, 9), np.float32), dhomo=np.zeros((P, 9), np.float32),
                dmean2D=np.zeros((P, 3), np.float32), dnormal=np.zeros((P, 3), np.float32),
-               dopacity=np.zeros(P, np.float32), dcolors=np.zeros((P, C), np.float32),
+               dopacity=np.zeros(P, np.float32), dcolors=np.zeros((P, max(dcol, 1)), np.float32),
                gradsum=np.zeros(P, np.float32), dtable=np.zeros((max(rows, 1), F), np.float32))
     keep = []
 
@@ -262,7 +267,10 @@ def render_backward(pre, binres, fwd, W, H, C, grid: Optional[OrGrid], dL_dpix, 
 
     a = OrRenderBwdArgs()
     a.W, a.H, a.C = W, H, C
-    a.level = 0 if grid is None else grid.L
+    if render_mode not in (0, 4) or (render_mode == 4 and (grid is None or level is None)):
+        raise ValueError(f"render_backward: render_mode {render_mode} needs mode 0, or mode 4 with a grid and level")
+    a.level = (0 if grid is None else grid.L) if render_mode == 0 else level
+    a.render_mode = render_mode
     a.beta = beta
     a.ranges = ptr(binres["ranges"], np.uint32)
     a.point_list = ptr(binres["vals"] if binres["num_rendered"] else np.zeros(1, np.uint32), np.uint32)
@@ -283,6 +291,7 @@ def render_backward(pre, binres, fwd, W, H, C, grid: Optional[OrGrid], dL_dpix, 
     lib().or_render_backward(ct.byref(a))
     if rows == 0:
         out["dtable"] = np.zeros((0, F), np.float32)
+    out["dcolors"] = out["dcolors"][:, :dcol]
     return out
 
 

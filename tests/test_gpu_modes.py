@@ -174,3 +174,142 @@ def test_mode_validation():
         call(4, 2, 4, 0, 10, 4)
     with pytest.raises(errs, match="<= 32"):
         call(13, 1, 2, 40, 80, 81)
+
+
+# (scene, per-splat levels, grid levels, active grid levels): level_dim 2 and
+# 4 (contracted); all levels active, coarse-to-fine (fewer active than
+# rendered) and none active (rows only)
+CAT_BWD_CASES = [("cfg1", 2, 6, 6), ("shell_small", 4, 12, 7), ("unbounded_small", 4, 10, 10), ("cfg1", 3, 5, 0)]
+
+
+@pytest.mark.parametrize("name,hyb,gl,active", CAT_BWD_CASES)
+def test_cat_mode_backward_parity(oracle, name, hyb, gl, active):
+    """nest_backward in render mode 4 against the backward oracle (which the
+    CPU tests pin against float64 autograd), on the same forward state.  The
+    sums run in another order on each side (per wave then atomically on the
+    GPU, sequentially in the oracle): 2e-5 of each array's largest entry."""
+    from nest_splat import rasterizer as rz
+    sc = scene(name)
+    sp = sc.spec
+    F = sp.F
+    pgd = hyb * F
+    C = (hyb + gl) * F
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    print(f"[case] mode 4 backward {name} hyb={hyb} grid levels={gl} active={active}", flush=True)
+    rows = _rows(sc, pgd, seed=hyb + 40)
+    ap = sc.ap_level.reshape(-1).copy()
+    ap[::5] = 3.0
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    settings = rz.make_settings(H, W, cam.tanfovx, cam.tanfovy, cam.world_view_transform, cam.full_proj_transform,
+                                cam.camera_center, if_contract=sp.contract)
+    grid = rz.HashGridDesc(gl, F, sp.S, sp.base_res, t(sc.table), sc.offsets, np.asarray(sp.gridrange, np.float32),
+                           render_mode=4, hybrid_levels=hyb, active_levels=active)
+    kw = dict(homotrans=t(sc.homotrans), ap_level=t(ap), colors_precomp=t(rows), channels=C)
+    res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations), **kw)
+    rng = np.random.default_rng(23)
+    dcol = rng.standard_normal((C, H, W)).astype(np.float32)
+    doth = rng.standard_normal((14, H, W)).astype(np.float32)
+    gb = rz.rasterize_backward(settings, grid, res, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
+                               t(dcol), t(doth), **kw)
+    torch.cuda.synchronize()
+    gpu = {k: (None if v is None else v.cpu().numpy()) for k, v in vars(gb).items()}
+
+    level = ((hyb + gl) << 16) | (active << 8) | hyb
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    g = oracle.make_grid(gl, F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    fwd = oracle.render(pre, b, W, H, C, g, homotrans=sc.homotrans, ap_level=ap, colors=rows, render_mode=4,
+                        level=level)
+    np.testing.assert_array_equal(res.color.cpu().numpy(), fwd["color"])  # same forward state
+    ob = oracle.render_backward(pre, b, fwd, W, H, C, g, dcol, doth, homotrans=sc.homotrans.reshape(-1, 16),
+                                ap_level=ap, colors=rows, render_mode=4, level=level)
+    pb = oracle.preprocess_backward(sc.means, sc.scales, sc.rotations, pre["radii"], pre["transmat"],
+                                    cam.world_view_transform, cam.full_proj_transform, W, H, ob["dtransmat"],
+                                    ob["dhomo"], ob["dnormal"], ob["dmean2D"])
+    ref = dict(dmeans3D=pb["dmeans"], dmeans2D=pb["dmean2D"], dopacity=ob["dopacity"][:, None],
+               dscales=pb["dscales"], drotations=pb["drots"], dcolors=ob["dcolors"], dgradsum=ob["gradsum"][:, None],
+               dfeatures=ob["dtable"].reshape(gpu["dfeatures"].shape))
+    vis = pre["radii"] > 0
+    for k, r in ref.items():
+        o = gpu[k]
+        assert o.shape == r.shape, (k, o.shape, r.shape)
+        assert np.isfinite(o).all(), k
+        if k == "dfeatures" and active == 0:
+            assert not o.any() and not r.any()
+            continue
+        assert np.abs(r).max() > 0, k
+        err = float(np.abs(o.astype(np.float64) - r).max() / np.abs(r).max())
+        print(f"{k}: max rel err {err:.2e}", flush=True)
+        assert err < 2e-5, (k, err)
+        if k != "dfeatures":
+            assert not o[~vis].any(), k
+    if 0 < active < gl:  # the levels past the active ones get no gradient
+        assert not gpu["dfeatures"].reshape(-1)[int(sc.offsets[active]) * F:].any()
+
+
+def test_drop_in_cat_mode_autograd(oracle):
+    """GaussianRasterizer in render mode 4 under autograd, with the
+    reference's packed L (7 of 12 grid levels active): the gradients of the
+    per-splat rows, the table and the means reach the leaves and match the
+    oracle; mode 13 has no backward and says so."""
+    from diff_surfel_rasterization import GaussianRasterizationSettings, GaussianRasterizer, HashGridSettings
+    sc = scene("shell_small")
+    sp = sc.spec
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    F, hyb, gl, active = sp.F, 3, 12, 7
+    pgd, C = hyb * F, (hyb + gl) * F
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    rs = GaussianRasterizationSettings(H, W, cam.tanfovx, cam.tanfovy, torch.zeros(3, device=DEV), 1.0,
+                                       t(cam.world_view_transform), t(cam.full_proj_transform), 3,
+                                       t(cam.camera_center), False, False, 0.0, sp.contract, False)
+    offs = np.zeros(17, np.int32)
+    offs[:gl + 1] = np.asarray(sc.offsets)[:gl + 1]
+    packed = ((hyb + gl) << 16) | (active << 8) | hyb
+    hs = HashGridSettings(packed, math.log2(sp.per_level_scale), sp.base_res, False, 0,
+                          torch.tensor([pgd, gl * F, C], dtype=torch.int32, device=DEV))
+    rows = _rows(sc, pgd, seed=5)
+    leaf = lambda a: t(a).requires_grad_(True)
+    means, rows_t, table = leaf(sc.means), leaf(rows), leaf(sc.table)
+    print(f"[case] drop-in mode 4 autograd L={packed:#x}", flush=True)
+    color, radii, allmap, _, _ = GaussianRasterizer(rs, hs)(
+        means3D=means, means2D=None, opacities=t(sc.opacity), colors_precomp=rows_t, scales=t(sc.scales),
+        rotations=t(sc.rotations), homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), features=table,
+        offsets=t(offs), gridrange=t(np.asarray(sp.gridrange, np.float32)), render_mode=4)
+    rng = np.random.default_rng(29)
+    dcol = rng.standard_normal((C, H, W)).astype(np.float32)
+    doth = rng.standard_normal((14, H, W)).astype(np.float32)
+    doth[7:] = 0  # channels 7-13 carry no gradient
+    ((color * t(dcol)).sum() + (allmap * t(doth)).sum()).backward()
+    torch.cuda.synchronize()
+
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    g = oracle.make_grid(gl, F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    fwd = oracle.render(pre, b, W, H, C, g, homotrans=sc.homotrans, ap_level=sc.ap_level, colors=rows,
+                        render_mode=4, level=packed)
+    np.testing.assert_array_equal(color.detach().cpu().numpy(), fwd["color"])
+    ob = oracle.render_backward(pre, b, fwd, W, H, C, g, dcol, doth, homotrans=sc.homotrans.reshape(-1, 16),
+                                ap_level=sc.ap_level, colors=rows, render_mode=4, level=packed)
+    pb = oracle.preprocess_backward(sc.means, sc.scales, sc.rotations, pre["radii"], pre["transmat"],
+                                    cam.world_view_transform, cam.full_proj_transform, W, H, ob["dtransmat"],
+                                    ob["dhomo"], ob["dnormal"], ob["dmean2D"])
+    for name, ours, ref in (("rows", rows_t.grad, ob["dcolors"]), ("table", table.grad, ob["dtable"]),
+                            ("means3D", means.grad, pb["dmeans"])):
+        o = ours.cpu().numpy().reshape(ref.shape).astype(np.float64)
+        err = float(np.abs(o - ref).max() / np.abs(ref).max())
+        print(f"{name}: max rel err {err:.2e}", flush=True)
+        assert np.abs(ref).max() > 0 and err < 2e-5, (name, err)
+
+    hs13 = HashGridSettings((8 << 16) | (3 << 8) | 2, math.log2(sp.per_level_scale), sp.base_res, False, 0,
+                            torch.tensor([0, 0, 8 * F], dtype=torch.int32, device=DEV))
+    rows13 = leaf(_rows(sc, 8 * F + 1, weight_col=8 * F, seed=6))
+    color13, _, _, _, _ = GaussianRasterizer(rs, hs13)(
+        means3D=t(sc.means), means2D=None, opacities=t(sc.opacity), colors_precomp=rows13, scales=t(sc.scales),
+        rotations=t(sc.rotations), homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), features=t(sc.table),
+        offsets=t(offs), gridrange=t(np.asarray(sp.gridrange, np.float32)), render_mode=13)
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        color13.sum().backward()

@@ -246,3 +246,75 @@ def test_grid_encode_backward_matches_autograd(oracle, interp, align):
     print(f"interp {interp} align {align}: grad_table {e_t:.2e} grad_inputs {e_i:.2e}")
     assert e_t < TOL and e_i < TOL
     assert not gi[oob].any()
+
+
+@pytest.mark.parametrize("hyb,active", [(2, 4), (1, 2), (3, 0)])
+def test_cat_mode_backward_matches_autograd(oracle, hyb, active):
+    """Render mode 4 backward (CR/backward.cu:987-1040): per-splat rows ahead
+    of the grid features.  With every grid level active it is the gradient of
+    the forward.  With fewer active levels the reference differentiates only
+    the active ones and takes the features past them as zero when it rebuilds
+    the blend (the offsets are copied only up to the active count,
+    CR/backward.cu:576-612), so its gradients are those of the forward over a
+    grid of the active levels alone, though the forward rendered them all."""
+    sc = _tiny(seed=20 + hyb)
+    sp = sc.spec
+    F, L = sp.F, sp.L
+    pgd = hyb * F
+    C = pgd + L * F + 2
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    ap = sc.ap_level.reshape(-1).copy()
+    ap[::3] = 2.0
+    rows = np.random.default_rng(hyb).uniform(-1, 1, (sp.P, pgd)).astype(np.float32)
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    assert b["num_rendered"] > 0
+    g = oracle.make_grid(L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    level = ((hyb + L) << 16) | (active << 8) | hyb
+    fwd = oracle.render(pre, b, W, H, C, g, homotrans=sc.homotrans, ap_level=ap, colors=rows, render_mode=4,
+                        level=level)
+    rng = np.random.default_rng(13)
+    dpix = rng.standard_normal(fwd["color"].shape).astype(np.float32)
+    doth = rng.standard_normal(fwd["others"].shape).astype(np.float32)
+    homo = sc.homotrans.reshape(-1, 16).astype(np.float32)
+    gb = oracle.render_backward(pre, b, fwd, W, H, C, g, dpix, doth, homotrans=homo, ap_level=ap, colors=rows,
+                                render_mode=4, level=level)
+    assert gb["dcolors"].shape == (sp.P, pgd)
+
+    leaf = lambda a: torch.tensor(np.asarray(a, np.float64), requires_grad=True)
+    leaves = dict(T=leaf(pre["transmat"]), xy=leaf(pre["xy"]), normal=leaf(pre["normal_opacity"][:, :3]),
+                  opacity=leaf(pre["normal_opacity"][:, 3]), homo=leaf(homo),
+                  table=leaf(sc.table.reshape(-1, sp.F)), rows=leaf(rows))
+    gd = dict(L=min(active, L), F=F, S=sp.S, H=sp.base_res, offsets=sc.offsets, vmin=sp.gridrange[0],
+              vmax=sp.gridrange[1])
+    color, others = TR.render_forward(oracle, pre, b, fwd, W, H, C, leaves, grid=gd, homotrans_np=homo,
+                                      ap_level=ap)
+    nf = pgd + min(active, L) * F
+    assert _rel(color.detach().numpy()[:nf], fwd["color"][:nf]) < 1e-4
+    if active < L:
+        assert np.abs(fwd["color"][nf:pgd + L * F]).max() > 0  # rendered, not differentiated
+    loss = (color * torch.from_numpy(dpix.astype(np.float64))).sum() + \
+        (others * torch.from_numpy(doth[:7].astype(np.float64))).sum()
+    loss.backward()
+    vis = pre["radii"] > 0
+    checks = {"dtransmat": (gb["dtransmat"], leaves["T"].grad), "dmean2D": (gb["dmean2D"][:, :2], leaves["xy"].grad),
+              "dnormal": (gb["dnormal"], leaves["normal"].grad), "dopacity": (gb["dopacity"], leaves["opacity"].grad),
+              "dcolors": (gb["dcolors"], leaves["rows"].grad)}
+    if active > 0:
+        gh = leaves["homo"].grad.numpy()
+        checks["dhomo"] = (gb["dhomo"], gh[:, [0, 4, 8, 1, 5, 9, 3, 7, 11]])
+        checks["dtable"] = (gb["dtable"], leaves["table"].grad)
+    else:
+        assert not gb["dtable"].any() and not gb["dhomo"].any()
+    for name, (ours, ref) in checks.items():
+        ref = ref.numpy() if isinstance(ref, torch.Tensor) else ref
+        if name != "dtable":
+            ours, ref = ours[vis], ref[vis]
+        assert np.abs(ref).max() > 0, name
+        err = _rel(ours, ref)
+        print(f"{name}: rel err {err:.2e}")
+        assert err < TOL, (name, err)
+    if 0 < active < L:  # no gradient reaches the inactive levels
+        assert not gb["dtable"][int(sc.offsets[active]):].any()
