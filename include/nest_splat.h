@@ -99,8 +99,14 @@ typedef struct nest_hashgrid {
    *     weight; the first hybrid_levels*level_dim channels come from the row,
    *     the next `levels` levels from the grid, blended with the row in
    *     training; in inference a splat with weight > 0.5 takes its row
-   *     without a grid lookup (CR/forward.cu:965-1101).
-   * Modes 4 and 13 need level_dim 2, 4 or 8 and at most 64 channels of
+   *     without a grid lookup (CR/forward.cu:965-1101);
+   *   NEST_MODE_ADAPTIVE_CAT (12), | NEST_MODE_INFERENCE for inference: the
+   *     same rows and levels; the first hybrid_levels*level_dim channels take
+   *     the row unweighted, the grid levels are blended with the row in
+   *     training; in inference a splat with weight >= 0.9 takes its row
+   *     without a grid lookup; every hit records its world position,
+   *     appearance colour and last contributor (CR/forward.cu:1593-1713).
+   * Modes 4, 12 and 13 need level_dim 2, 4 or 8 and at most 64 channels of
    * per-splat plus grid features; `levels` may be 0 there. */
   int32_t render_mode;
   uint32_t hybrid_levels;
@@ -116,6 +122,7 @@ typedef struct nest_hashgrid {
 
 #define NEST_MODE_BASELINE 0
 #define NEST_MODE_CAT 4
+#define NEST_MODE_ADAPTIVE_CAT 12
 #define NEST_MODE_ADAPTIVE_CAT_FAST 13
 #define NEST_MODE_INFERENCE 0x100
 
@@ -245,7 +252,7 @@ int nest_forward_geometry(const nest_raster_settings *settings, const nest_splat
  * (:173-195, :388) and renderCUDAsurfelForward<C, render_mode>
  * (CR/forward.cu:639-2049, dispatch :2052-2158).  out_color channels must
  * cover the features of the mode (levels*level_dim in mode 0, plus
- * hybrid_levels*level_dim in mode 4, total_levels*level_dim in mode 13);
+ * hybrid_levels*level_dim in mode 4, total_levels*level_dim in modes 12, 13);
  * channels past them are written as zero. */
 int nest_forward_render(const nest_raster_settings *settings, const nest_hashgrid *grid,
                         const nest_splats *splats, void *geom_ws, size_t geom_bytes,

@@ -186,10 +186,11 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
                GridParams& g) {
   int rc = NEST_OK;
   const int base_mode = gr->render_mode & 0xFF;
-  if ((gr->render_mode & ~0x1FF) != 0 || (base_mode != NEST_MODE_BASELINE && base_mode != NEST_MODE_CAT &&
-                                          base_mode != NEST_MODE_ADAPTIVE_CAT_FAST) ||
-      ((gr->render_mode & NEST_MODE_INFERENCE) && base_mode != NEST_MODE_ADAPTIVE_CAT_FAST))
-    return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: supported are 0, 4, 13 and 13 | 0x100", gr->render_mode);
+  const bool adaptive = base_mode == NEST_MODE_ADAPTIVE_CAT || base_mode == NEST_MODE_ADAPTIVE_CAT_FAST;
+  if ((gr->render_mode & ~0x1FF) != 0 || (base_mode != NEST_MODE_BASELINE && base_mode != NEST_MODE_CAT && !adaptive) ||
+      ((gr->render_mode & NEST_MODE_INFERENCE) && !adaptive))
+    return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: supported are 0, 4, 12, 13, 12 | 0x100 and 13 | 0x100",
+                gr->render_mode);
   const bool mix = base_mode != NEST_MODE_BASELINE;
   if (mix) {
     const uint32_t F = gr->level_dim, hyb = gr->hybrid_levels;
@@ -202,8 +203,8 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
       feat = (hyb + gr->levels) * F;
     } else {
       if (hyb + gr->levels > gr->total_levels)
-        return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode 13: hybrid_levels + levels (%u + %u) exceed total_levels %u",
-                    hyb, gr->levels, gr->total_levels);
+        return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode %d: hybrid_levels + levels (%u + %u) exceed total_levels %u",
+                    base_mode, hyb, gr->levels, gr->total_levels);
       feat = gr->total_levels * F;
     }
     if (feat > 64u)
@@ -460,13 +461,16 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
       rp.cstride = rp.pgd;
       rp.nrow = rp.pgd;
     } else {
+      // modes 12 and 13 (CR/forward.cu:965-1101, :1593-1713)
       const int tdim = (int)gr->total_levels * F;
+      const bool m13 = (gr->render_mode & 0xFF) == NEST_MODE_ADAPTIVE_CAT_FAST;
       rp.cstride = tdim + 1;
       rp.nrow = tdim;
       rp.wslot = tdim;
       rp.infer = (gr->render_mode & NEST_MODE_INFERENCE) ? 1 : 0;
       rp.blend = rp.infer ? 0 : 1;
-      rp.m13 = 1;
+      rp.m13 = m13 ? 1 : 0;
+      rp.wcoarse = (m13 && !rp.infer) ? 1 : 0;
       rp.nfast = gr->total_levels - gr->hybrid_levels;
     }
   }

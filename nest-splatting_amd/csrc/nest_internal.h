@@ -114,19 +114,22 @@ struct RenderParams {
   float* final_T;
   uint32_t* n_contrib;
   GridParams grid;
-  // Per-splat features ahead of the grid's (render modes 4 and 13): channel
-  // c < pgd of a hit is row[c] (times the row's weight with blend); grid
-  // level l lands on channels pgd + l*F.
+  // Per-splat features ahead of the grid's (render modes 4, 12 and 13):
+  // channel c < pgd of a hit is row[c] (times the row's weight with
+  // wcoarse); grid level l lands on channels pgd + l*F.
   int mix;                    // 0: mode 0
   int hyb;                    // per-splat levels ahead of the grid's
   int pgd;                    // hyb * F
   int cstride;                // floats per row of colors
   int nrow;                   // leading floats of a row the render reads as features (<= 64)
-  int wslot;                  // index of the blend weight in a row (mode 13), else -1
-  int infer;                  // mode 13 inference: weight > 0.5 takes the row without the grid
-  int blend;                  // mode 13 training: row * weight + grid * (1 - weight)
-  int m13;                    // mode 13: a hit updates no appearance colour and no last contributor
-  uint32_t nfast;             // levels of the row past pgd that a weight > 0.5 hit takes
+  int wslot;                  // index of the blend weight in a row (modes 12, 13), else -1
+  int infer;                  // inference: a fast hit (weight > 0.5 in mode 13, >= 0.9 in
+                              // mode 12) takes the row without the grid
+  int blend;                  // training: grid levels take row * weight + grid * (1 - weight)
+  int m13;                    // mode 13: a hit updates no appearance colour and no last
+                              // contributor, a fast hit adds no world position
+  int wcoarse;                // mode 13 training: the first pgd channels take row * weight
+  uint32_t nfast;             // levels of the row past pgd that a fast hit takes
 };
 
 // Host-side launchers (defined in the .hip files).  Each returns the

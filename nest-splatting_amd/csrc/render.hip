@@ -679,7 +679,8 @@ render_kernel(const RenderParams p) {
           float mine = lane < (uint32_t)p.nrow ? row[lane] : 0.0f;
           asm volatile("" : "+v"(mine));  // loaded here, with every lane active
           const float wt = p.wslot >= 0 ? row[p.wslot] : 1.0f;
-          const bool fast = p.infer && wt > 0.5f;
+          // inference fast path: weight > 0.5 in mode 13, >= 0.9 in mode 12
+          const bool fast = p.infer && (p.m13 ? wt > 0.5f : wt >= 0.9f);
           if (ph.on) {
             // per-splat channels at once; a fast hit's grid-level channels too
             // when no earlier hit of the pixel is pending
@@ -689,21 +690,23 @@ render_kernel(const RenderParams p) {
             for (int c = 0; c < NACC; c++) {
               if (c < ndirect) {
                 const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), c));
-                acc[c] = fmaf(p.blend ? rv * wt : rv, ph.w, acc[c]);
+                acc[c] = fmaf(p.wcoarse ? rv * wt : rv, ph.w, acc[c]);
               }
             }
             const uint32_t ap = __float_as_uint(srec[3][j].w);
             float u[3] = {0.0f, 0.0f, 0.0f};
             uint32_t nh = 0u;
-            if (!fast) {
+            if (!fast || !p.m13) {  // a mode-13 fast hit has no world point
               float xyz[3];
               hit_world(srec[4][j], srec[5][j], srec[6][j], ph.hit, xyz);
               pos_x += ph.w * xyz[0];
               pos_y += ph.w * xyz[1];
               pos_z += ph.w * xyz[2];
-              bool oob;
-              grid_coord(g, xyz, u, oob);
-              nh = hit_levels(oob, ap, L);
+              if (!fast) {
+                bool oob;
+                grid_coord(g, xyz, u, oob);
+                nh = hit_levels(oob, ap, L);
+              }
             }
             if (enq) {
               const int slot = (qhead + qn) & (kQueue - 1);

@@ -13,7 +13,8 @@ backward: hash-grid features when HashGridSettings.L > 0; when L == 0,
 precomputed per-splat colours or RGB evaluated from SH coefficients
 (degree <= 3) in preprocess.  Render mode 4 ("cat": per-splat features of
 the coarse levels ahead of a grid of the fine ones) forward and backward,
-and 13 ("adaptive_cat_fast", with the inference flag 0x100) forward, with
+12 ("adaptive_cat") and 13 ("adaptive_cat_fast"), each with the inference
+flag 0x100, forward, with
 the reference's packed L (total << 16 | grid levels << 8 | per-splat
 levels; the backward differentiates the grid levels within the active
 count, CR/backward.cu:576-612).  The backward returns the reference's gradients
@@ -72,7 +73,7 @@ def _cat_hash_levels(offsets17: np.ndarray) -> int:
 
 
 def _mixed_grid(hs, render_mode, level, features, offsets, gridrange):
-    """HashGridDesc of render modes 4 and 13 from the reference's packed
+    """HashGridDesc of render modes 4, 12 and 13 from the reference's packed
     level argument: (total << 16) | (grid levels << 8) | per-splat levels
     (GR:224-226, :395-396; CR/forward.cu:744-767, :971-973, :1228)."""
     base_mode = render_mode & 0xFF
@@ -100,9 +101,10 @@ class _RasterizeGaussians(torch.autograd.Function):
                 ap_level, features, offsets, gridrange, features_diffuse, offsets_diffuse, gridrange_diffuse,
                 raster_settings, hashgrid_settings, render_mode, shapes, kernel_type):
         base_mode = render_mode & 0xFF
-        if base_mode not in (0, 4, 13) or (render_mode & ~0x1FF) or ((render_mode & 0x100) and base_mode != 13):
+        if base_mode not in (0, 4, 12, 13) or (render_mode & ~0x1FF) or \
+                ((render_mode & 0x100) and base_mode not in (12, 13)):
             raise NotImplementedError(f"render_mode {render_mode}: implemented are 0 (baseline), 4 (cat) and "
-                                      f"13 (adaptive_cat_fast, | 0x100 inference)")
+                                      f"12 / 13 (adaptive_cat / adaptive_cat_fast, | 0x100 inference)")
         if kernel_type != 0:
             raise NotImplementedError(f"kernel_type {kernel_type}: only the Gaussian kernel (0) is implemented")
         if not _empty(cov3Ds_precomp):
@@ -113,7 +115,7 @@ class _RasterizeGaussians(torch.autograd.Function):
             raise NotImplementedError("record_transmittance=True is not implemented")
         C = _channels(hashgrid_settings)
         level = int(hashgrid_settings.L)
-        if base_mode == 4 and level == 0:
+        if base_mode in (4, 12) and level == 0:
             base_mode = render_mode = 0  # level 0 is the colour path in every mode but 13 (CR/forward.cu:1091)
         if base_mode != 0:
             grid = _mixed_grid(hashgrid_settings, render_mode, level, features, offsets, gridrange)

@@ -629,7 +629,8 @@ typedef struct {
      * 4 per-splat features then hash features (level's low byte = per-splat
      * levels), 13 adaptive_cat_fast (level = total << 16 | hash << 8 | per-splat
      * levels, colors rows of total*F+1 floats, bit 8 of render_mode =
-     * inference).  Other values are not restated. */
+     * inference), 12 adaptive_cat (same level and rows).  Other values are
+     * not restated. */
     int render_mode;
 } or_render_args;
 
@@ -762,7 +763,35 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
             hit_xyz(A->homotrans + 16 * (size_t)id, use3d, sx, sy, xyz);
             pos_x += w * xyz[0]; pos_y += w * xyz[1]; pos_z += w * xyz[2];
             uint32_t ap = f2u_sat(floorf(A->ap_level[id]));
-            if ((A->render_mode & 0xFF) == 4) {
+            if ((A->render_mode & 0xFF) == 12) {
+                /* adaptive_cat (forward.cu:1593-1713): rows [total*F features |
+                 * blend weight]; the first hyb*F channels come from the row;
+                 * training blends the next hl*F with the grid,
+                 * fmaf(wt, row, (1 - wt) * grid); inference takes the whole
+                 * row when wt >= 0.9, else the grid.  Unlike mode 13 the hit
+                 * is a full one: world position, appearance colour and last
+                 * contributor as in mode 0. */
+                const int infer = (A->render_mode >> 8) & 1;
+                const int total = (A->level >> 16) & 0xFF, hl = (A->level >> 8) & 0xFF, hyb = A->level & 0xFF;
+                const int F = A->grid.F, tdim = total * F;
+                const float *gf = A->colors + (size_t)id * (size_t)(tdim + 1);
+                const float wt = gf[tdim];
+                for (int c = 0; c < C; c++) feat_scratch[c] = 0.0f;
+                if (infer && wt >= 0.9f) {
+                    for (int i = 0; i < tdim && i < C; i++) feat_scratch[i] = gf[i];
+                } else {
+                    for (int i = 0; i < hyb * F && i < C; i++) feat_scratch[i] = gf[i];
+                    if (hl > 0) {
+                        or_grid G = A->grid;
+                        G.L = hl;
+                        float hf[64];
+                        or_query_feature(&G, xyz, ap, 64, hf);
+                        const int fs = hyb * F;
+                        for (int i = 0; i < hl * F && fs + i < C; i++)
+                            feat_scratch[fs + i] = infer ? hf[i] : fmaf(wt, gf[fs + i], (1.0f - wt) * hf[i]);
+                    }
+                }
+            } else if ((A->render_mode & 0xFF) == 4) {
                 /* hybrid_features (forward.cu:1218-1282): hyb*F per-splat
                  * features (rows of hyb*F floats), then the grid's hl levels */
                 const int F = A->grid.F, pgd = (A->level & 0xFF) * F;

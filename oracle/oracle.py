@@ -199,8 +199,8 @@ def make_grid(L, F, S, H, offsets, table, gridrange, contract=False, align_corne
 def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_level=None, colors=None,
            beta=0.0, max_intersections=0, row_stride=1, row_phase=0, threads=0, render_mode=0, level=None):
     """renderCUDAsurfelForward for every pixel.  render_mode 0 (grid levels
-    grid.L, or the colour path without a grid), 4 or 13 (bit 8: inference);
-    for modes 4 and 13, level is the reference's packed level argument
+    grid.L, or the colour path without a grid), 4, 12 or 13 (bit 8:
+    inference); for modes 4, 12 and 13, level is the reference's packed level argument
     (total << 16 | hash levels << 8 | per-splat levels) and colors the
     per-splat feature rows."""
     HW = W * H

@@ -1,5 +1,5 @@
-"""GPU parity of render modes 4 (cat) and 13 (adaptive_cat_fast, training and
-inference) against the oracle, bit for bit, on the shared small scenes:
+"""GPU parity of render modes 4 (cat), 12 (adaptive_cat) and 13
+(adaptive_cat_fast), training and inference, against the oracle, bit for bit, on the shared small scenes:
 per-splat feature rows ahead of a grid of the scene's first levels, with
 f32 and f16 tables, level_dim 2 and 4, the common-grid lookup and the
 general per-level one (smoothstep), mixed fast/slow splats in inference.
@@ -110,6 +110,27 @@ def test_adaptive_cat_fast_parity(oracle, name, infer, total, hyb, hl, interp):
         assert not r["n_contrib"][0].any()
 
 
+# (scene, inference, total levels, per-splat levels, active grid levels, interp)
+AC_CASES = [("unbounded_small", False, 16, 10, 6, 0), ("shells_small", True, 8, 5, 3, 0),
+            ("shell_small", True, 12, 4, 8, 1), ("cfg1", False, 8, 3, 5, 1)]
+
+
+@pytest.mark.parametrize("name,infer,total,hyb,hl,interp", AC_CASES)
+def test_adaptive_cat_parity(oracle, name, infer, total, hyb, hl, interp):
+    """Render mode 12 (adaptive_cat): unweighted coarse rows, blended (training)
+    or weight >= 0.9 fast (inference) grid levels, full hits."""
+    sc = scene(name)
+    F = sc.spec.F
+    tdim = total * F
+    mode = 12 | (0x100 if infer else 0)
+    print(f"[case] mode {mode:#x} {name} total={total} hyb={hyb} hl={hl} interp={interp}", flush=True)
+    rows = _rows(sc, tdim + 1, weight_col=tdim, seed=total + hyb + 1)
+    res = run_gpu(sc, mode, hyb, hl, total, tdim, rows, interp=interp)
+    b, r = run_oracle(oracle, sc, mode, (total << 16) | (hl << 8) | hyb, max(hl, 1), tdim, rows, interp=interp)
+    _check(res, b, r)
+    assert r["n_contrib"][0].any()
+
+
 def test_drop_in_decodes_packed_levels(oracle):
     """GaussianRasterizer with render_mode 4 / 13 | 0x100 and the packed L of
     the reference's render() (GR:224-226, :395-396)."""
@@ -164,8 +185,8 @@ def test_mode_validation():
                                     channels=C)
 
     errs = (NotImplementedError, RuntimeError)
-    with pytest.raises(errs, match="render_mode 12"):
-        call(12, 1, 2, 4, 8, 8)
+    with pytest.raises(errs, match="render_mode 14"):
+        call(14, 1, 2, 4, 8, 8)
     with pytest.raises(errs, match="supported"):
         call(4 | 0x100, 1, 2, 0, 8, 2)
     with pytest.raises(errs, match="exceed total_levels"):

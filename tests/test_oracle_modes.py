@@ -229,3 +229,66 @@ def test_mode13_training_per_splat_weights(frame):
         part[pgd:] += (1.0 - float(t)) * fr.mode0(ap=ap)["color"]
         expect += part
     assert _close(r["color"], expect)
+
+
+@pytest.mark.parametrize("t", [1.0, 0.0])
+def test_mode12_training_weight_extremes(frame, t):
+    """adaptive_cat training (CR/forward.cu:1676-1711): the row's first hyb*F
+    channels unweighted, the next grid levels blended; every hit is a full
+    one, so the auxiliary outputs are mode 0's."""
+    fr = frame
+    hyb = 2
+    rows, total, tdim = _rows13(fr, hyb, 1, t)
+    pgd, nf = hyb * fr.F, fr.L * fr.F
+    r = fr.mode(12, (total << 16) | (fr.L << 8) | hyb, tdim, rows)
+    r0 = fr.mode0()
+    if t == 1.0:
+        assert _same(r["color"][:pgd + nf], fr.colour(rows[:, :pgd + nf])["color"])
+    else:
+        assert _same(r["color"][:pgd], fr.colour(rows[:, :pgd])["color"])
+        assert _same(r["color"][pgd:pgd + nf], r0["color"])
+    assert not np.any(r["color"][pgd + nf:])
+    assert _same(r["others"], r0["others"])
+    assert _same(r["final_T"], r0["final_T"])
+    assert np.array_equal(r["n_contrib"], r0["n_contrib"])
+    assert r["n_contrib"][0].any()
+
+
+def test_mode12_training_per_splat_weights(frame):
+    fr = frame
+    hyb = 1
+    ts = np.array([0.25, 0.6, 0.85], np.float32)
+    grp = np.arange(fr.P) % 3
+    rows, total, tdim = _rows13(fr, hyb, 0, ts[grp])
+    pgd = hyb * fr.F
+    r = fr.mode(12, (total << 16) | (fr.L << 8) | hyb, tdim, rows)
+    assert _same(r["color"][:pgd], fr.colour(rows[:, :pgd])["color"])
+    expect = np.zeros((tdim - pgd,) + r["color"].shape[1:], np.float64)
+    for k, t in enumerate(ts):
+        mine = grp == k
+        ap = np.where(mine, fr.sc.ap_level.reshape(-1), 0.0).astype(np.float32)
+        expect += fr.colour(np.where(mine[:, None], rows[:, pgd:tdim] * t, 0.0))["color"]
+        expect += (1.0 - float(t)) * fr.mode0(ap=ap)["color"]
+    assert _close(r["color"][pgd:], expect)
+
+
+def test_mode12_inference_threshold(frame):
+    """adaptive_cat inference (CR/forward.cu:1636-1675): weight >= 0.9 takes
+    the whole row (0.9 itself included), below takes the grid; unlike mode
+    13 the hits keep their world position, appearance colour and last
+    contributor."""
+    fr = frame
+    hyb = 2
+    pgd, nf = hyb * fr.F, fr.L * fr.F
+    r0 = fr.mode0()
+    for wt, fast in ((0.9, True), (0.97, True), (np.nextafter(np.float32(0.9), np.float32(0)), False)):
+        rows, total, tdim = _rows13(fr, hyb, 1, wt)
+        r = fr.mode(12 | 0x100, (total << 16) | (fr.L << 8) | hyb, tdim, rows)
+        if fast:
+            assert _same(r["color"], fr.colour(rows[:, :tdim])["color"])
+        else:
+            assert _same(r["color"][:pgd], fr.colour(rows[:, :pgd])["color"])
+            assert _same(r["color"][pgd:pgd + nf], r0["color"])
+            assert not np.any(r["color"][pgd + nf:])
+        assert _same(r["others"], r0["others"])
+        assert np.array_equal(r["n_contrib"], r0["n_contrib"])
