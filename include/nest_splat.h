@@ -263,10 +263,12 @@ int nest_forward_render(const nest_raster_settings *settings, const nest_hashgri
 /* ---- backward (training) ------------------------------------------------
  * nest_backward is RasterizeGaussiansBackwardCUDA
  * (DSR/rasterize_points.cu:243-471) / CudaRasterizer::Rasterizer::backward
- * (CR/rasterizer_impl.cu:444-600) for render modes 0 and 4 (mode 4:
+ * (CR/rasterizer_impl.cu:444-600) for render modes 0, 4 and 12 (mode 4:
  * CR/backward.cu:987-1040, gradients of the per-splat rows into dL_dcolors
  * [P, hybrid_levels*level_dim], of the grid's active levels into
- * dL_dfeatures) with the Gaussian kernel: renderCUDAsurfelBackward
+ * dL_dfeatures; mode 12 in training, CR/backward.cu:1425-1520, gradients of
+ * the rows and their blend weight into dL_dcolors [P, total_levels*level_dim
+ * + 1]) with the Gaussian kernel: renderCUDAsurfelBackward
  * (CR/backward.cu:445-2049) then
  * preprocessCUDA backward (CR/backward.cu:2216-2274).  It reads the
  * workspaces of the nest_forward_geometry / nest_forward_render calls of the
@@ -292,7 +294,8 @@ typedef struct {
     float *dL_dmeans3D;              /* [P,3] */
     float *dL_dmeans2D;              /* [P,3] densification statistic */
     float *dL_dcolors;               /* [P,C] colour path, [P,hybrid_levels*level_dim]
-                                        in render mode 4, or NULL */
+                                        in render mode 4, [P,total_levels*level_dim+1]
+                                        in render mode 12, or NULL */
     float *dL_dopacity;              /* [P] */
     float *dL_dshs;                  /* [P,sh_coeffs,3] when the colours came from SH */
     float *dL_dscales;               /* [P,2] */

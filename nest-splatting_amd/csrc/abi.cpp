@@ -711,10 +711,13 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
     return fail(NEST_ERR_INVALID_ARGUMENT, "nest_hashgrid missing or struct_size mismatch");
   if (!io || io->struct_size != sizeof(nest_backward_io))
     return fail(NEST_ERR_INVALID_ARGUMENT, "nest_backward_io missing or struct_size mismatch");
-  if (gr->render_mode != NEST_MODE_BASELINE && gr->render_mode != NEST_MODE_CAT)
-    return fail(NEST_ERR_UNSUPPORTED, "backward: render_mode %d is forward-only here (modes 0 and 4 have a backward)",
-                gr->render_mode);
+  if (gr->render_mode != NEST_MODE_BASELINE && gr->render_mode != NEST_MODE_CAT &&
+      gr->render_mode != NEST_MODE_ADAPTIVE_CAT)
+    return fail(NEST_ERR_UNSUPPORTED,
+                "backward: render_mode %d is forward-only here (modes 0, 4 and 12 without the inference flag have a "
+                "backward)", gr->render_mode);
   const bool cat = gr->render_mode == NEST_MODE_CAT;
+  const bool acat = gr->render_mode == NEST_MODE_ADAPTIVE_CAT;
   const int C = io->channels;
   if (C < 1 || C > 64) return fail(NEST_ERR_UNSUPPORTED, "backward: channels must be in [1, 64] (got %d)", C);
   if (!io->dL_dout_color || !io->dL_dout_others)
@@ -726,11 +729,14 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   GridParams g{};
   if ((rc = setup_grid(rs, gr, sp, C, g))) return rc;
   const bool hash = gr->levels > 0;
-  const bool from_sh = !cat && !hash && sh_colours(sp);
+  const bool from_sh = !cat && !acat && !hash && sh_colours(sp);
   // mode 4: per-splat rows of pgd floats; the grid levels differentiated are
   // those up to the last one within the active count whose offsets increase
   // (CR/backward.cu:576-612, :993-999)
-  const int pgd = cat ? (int)(gr->hybrid_levels * gr->level_dim) : 0;
+  const int pgd = (cat || acat) ? (int)(gr->hybrid_levels * gr->level_dim) : 0;
+  // mode 12: rows of total*F features and the blend weight; the grid's levels
+  // are blended (CR/backward.cu:1425-1520)
+  const int tdim = acat ? (int)(gr->total_levels * gr->level_dim) : 0;
   uint32_t cat_levels = 0;
   if (cat) {
     const uint32_t act = gr->active_levels < gr->levels ? gr->active_levels : gr->levels;
@@ -738,7 +744,10 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
       if (gr->offsets[i] > gr->offsets[i - 1]) cat_levels = i;
     g.L = cat_levels;
   }
-  const int dcol_width = cat ? pgd : C;
+  const int dcol_width = cat ? pgd : acat ? tdim + 1 : C;
+  // the workspace's colour-gradient field holds [P, channels]: mode-12 rows are wider
+  if (acat && !io->dL_dcolors)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "backward: render_mode 12 needs dL_dcolors [P, %d]", tdim + 1);
   if (hash && g.half) return fail(NEST_ERR_UNSUPPORTED, "backward: the hash table must be float32");
   if (hash && !io->dL_dfeatures) return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dfeatures is required");
   if (from_sh && !io->dL_dshs) return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dshs is required with SH colours");
@@ -793,8 +802,11 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   rp.gy = gy;
   rp.ntiles = gx * gy;
   rp.C = C;
-  rp.level = cat ? 1 : (int)gr->levels;  // mode 4 always takes the hash branch
+  rp.level = (cat || acat) ? 1 : (int)gr->levels;  // modes 4 and 12 always take the hash branch
   rp.pgd = pgd;
+  rp.cstride = acat ? tdim + 1 : pgd;
+  rp.wslot = acat ? tdim : -1;
+  rp.nfine = acat ? (int)(gr->levels * gr->level_dim) : 0;
   rp.beta = rs->beta;
   rp.ranges = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_RANGES]);
   rp.tile_order = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_TILE_ORDER]);

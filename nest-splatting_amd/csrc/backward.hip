@@ -271,9 +271,12 @@ __device__ __forceinline__ bool grid_coord_bwd(const GridParams& g, const float 
   return true;
 }
 
-// kRows: render mode 4, per-splat feature rows (p.colors, p.pgd wide) ahead of
-// the grid's channels (CR/backward.cu:987-1040).
-template <int F, bool kHash, bool kRows>
+// kRows 1: render mode 4, per-splat feature rows (p.colors, p.pgd wide) ahead
+// of the grid's channels (CR/backward.cu:987-1040).  kRows 2: render mode 12
+// training, rows of p.cstride floats ending with the blend weight (p.wslot):
+// p.pgd coarse channels from the row, then p.nfine channels blended
+// weight * row + (1 - weight) * grid (CR/backward.cu:1425-1520).
+template <int F, bool kHash, int kRows>
 __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const RenderBwdParams p) {
   __shared__ float4 srec[kBwdChunks][kBwdThreads];
   __shared__ uint32_t sid[kBwdThreads];
@@ -371,7 +374,7 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
       float gT[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0}, gH[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
       float gM[2] = {0.0f, 0.0f}, gN[3] = {0.0f, 0.0f, 0.0f}, gO = 0.0f, gS = 0.0f;
       float wcol = 0.0f;  // dchannel_dcolor of the colour path
-      float wgt = 0.0f, dot = 0.0f, rdot = 0.0f;
+      float wgt = 0.0f, dot = 0.0f, rdot = 0.0f, wt = 0.0f, fdot = 0.0f;
       float dxyz[3] = {0.0f, 0.0f, 0.0f};
       float u[3] = {0.0f, 0.0f, 0.0f}, grad_scale = 0.0f;
       uint32_t lane_levels = 0u;
@@ -393,9 +396,15 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
             xyz[0] = q5.z; xyz[1] = q5.w; xyz[2] = q6.x;
           }
           gS = wgt * sum_abs;
-          if constexpr (kRows) {
+          if constexpr (kRows == 1) {
             const float* row = p.colors + (size_t)id * p.pgd;
             for (int ch = 0; ch < p.pgd; ch++) rdot += row[ch] * dpix[(size_t)ch * HW];
+            wcol = wgt;
+          } else if constexpr (kRows == 2) {
+            const float* row = p.colors + (size_t)id * (uint32_t)p.cstride;
+            wt = row[p.wslot];
+            for (int ch = 0; ch < p.pgd; ch++) rdot += row[ch] * dpix[(size_t)ch * HW];
+            for (int i = 0; i < p.nfine; i++) fdot += row[p.pgd + i] * dpix[(size_t)(p.pgd + i) * HW];
             wcol = wgt;
           }
           const uint32_t ap = __float_as_uint(q3.w);
@@ -405,10 +414,19 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
       }
       if constexpr (kHash) {
         // every lane takes part (cross-lane sums inside); lanes without a hit have no levels
+        // mode 12: the grid's share of the gradient is (1 - weight) of it
         if (__ballot(lane_levels > 0u) != 0ull)
-          hash_backward_wave<F>(g, rsrc, u, grad_scale, lane_levels, wgt, kRows ? dpix + (size_t)p.pgd * HW : dpix, HW,
-                                p.dtable, dot, dxyz);
-        if constexpr (kRows) dot += rdot;
+          hash_backward_wave<F>(g, rsrc, u, grad_scale, lane_levels, kRows == 2 ? wgt * (1.0f - wt) : wgt,
+                                kRows ? dpix + (size_t)p.pgd * HW : dpix, HW, p.dtable, dot, dxyz);
+        if constexpr (kRows == 1) {
+          dot += rdot;
+        } else if constexpr (kRows == 2) {
+          // dot is grid . dpix over the fine channels; the hit's features are
+          // the coarse rows and weight * row + (1 - weight) * grid
+          const float hdot = dot;
+          dot = rdot + wt * fdot + (1.0f - wt) * hdot;
+          fdot = wgt * (fdot - hdot);  // dL/dweight
+        }
       }
       if (act) {
         if constexpr (kHash) {
@@ -501,11 +519,19 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
           }
           const float vs = wave_sum(gS);
           if (lead && vs != 0.0f) atomic_add(p.gradsum + id, vs);
-          if constexpr (kRows) {
+          if constexpr (kRows == 1) {
             for (int ch = 0; ch < p.pgd; ch++) {
               const float v = wave_sum(wcol * dpix[(size_t)ch * HW]);
               if (lead && v != 0.0f) atomic_add(p.dcolors + (size_t)id * p.pgd + ch, v);
             }
+          } else if constexpr (kRows == 2) {
+            float* dc = p.dcolors + (size_t)id * (uint32_t)p.cstride;
+            for (int ch = 0; ch < p.pgd + p.nfine; ch++) {
+              const float v = wave_sum((ch < p.pgd ? wcol : wcol * wt) * dpix[(size_t)ch * HW]);
+              if (lead && v != 0.0f) atomic_add(dc + ch, v);
+            }
+            const float vw = wave_sum(act ? fdot : 0.0f);
+            if (lead && vw != 0.0f) atomic_add(dc + p.wslot, vw);
           }
         } else {
           for (int ch = 0; ch < C; ch++) {
@@ -530,7 +556,7 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
   }
 }
 
-template <int F, bool kHash, bool kRows = false>
+template <int F, bool kHash, int kRows = 0>
 hipError_t launch_bwd_one(const RenderBwdParams& p, hipStream_t s) {
   hipLaunchKernelGGL((render_backward_kernel<F, kHash, kRows>), dim3(p.ntiles), dim3(kBwdThreads), 0, s, p);
   return hipGetLastError();
@@ -833,11 +859,19 @@ hipError_t launch_grid_encode_backward(const GridEncodeBwdParams& p, hipStream_t
 
 hipError_t launch_render_backward(const RenderBwdParams& p, hipStream_t s) {
   if (p.ntiles == 0) return hipSuccess;
+  if (p.wslot >= 0) {
+    switch (p.grid.F) {
+      case 2: return launch_bwd_one<2, true, 2>(p, s);
+      case 4: return launch_bwd_one<4, true, 2>(p, s);
+      case 8: return launch_bwd_one<8, true, 2>(p, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (p.pgd > 0) {
     switch (p.grid.F) {
-      case 2: return launch_bwd_one<2, true, true>(p, s);
-      case 4: return launch_bwd_one<4, true, true>(p, s);
-      case 8: return launch_bwd_one<8, true, true>(p, s);
+      case 2: return launch_bwd_one<2, true, 1>(p, s);
+      case 4: return launch_bwd_one<4, true, 1>(p, s);
+      case 8: return launch_bwd_one<8, true, 1>(p, s);
       default: return hipErrorInvalidValue;
     }
   }

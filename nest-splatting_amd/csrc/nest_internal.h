@@ -188,7 +188,10 @@ struct RenderBwdParams {
   float* dopacity;            // [P]
   float* dcolors;             // [P][C] colour path, [P][pgd] per-splat rows
   float* gradsum;             // [P] hash path
-  int pgd;                    // render mode 4: per-splat row width (0 otherwise)
+  int pgd;                    // render modes 4, 12: per-splat (coarse) channels of a row (0 otherwise)
+  int cstride;                // render mode 12: floats per row (total*F + 1)
+  int wslot;                  // render mode 12: index of the blend weight in a row, else -1
+  int nfine;                  // render mode 12: blended channels (grid levels * F)
   GridParams grid;
 };
 hipError_t launch_render_backward(const RenderBwdParams& p, hipStream_t s);

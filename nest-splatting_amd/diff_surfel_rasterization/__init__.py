@@ -11,10 +11,11 @@ markVisible (:310-319) and rasterize_gaussians (:21-66).
 Scope: render mode 0 ("baseline") with the Gaussian kernel, forward and
 backward: hash-grid features when HashGridSettings.L > 0; when L == 0,
 precomputed per-splat colours or RGB evaluated from SH coefficients
-(degree <= 3) in preprocess.  Render mode 4 ("cat": per-splat features of
-the coarse levels ahead of a grid of the fine ones) forward and backward,
-12 ("adaptive_cat") and 13 ("adaptive_cat_fast"), each with the inference
-flag 0x100, forward, with
+(degree <= 3) in preprocess.  Render modes 4 ("cat": per-splat features
+of the coarse levels ahead of a grid of the fine ones) and 12
+("adaptive_cat", blended with the grid by a per-splat weight) forward and
+backward, 12 | 0x100 and 13 ("adaptive_cat_fast") with or without the
+inference flag 0x100 forward, with
 the reference's packed L (total << 16 | grid levels << 8 | per-splat
 levels; the backward differentiates the grid levels within the active
 count, CR/backward.cu:576-612).  The backward returns the reference's gradients
@@ -172,9 +173,9 @@ class _RasterizeGaussians(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out_color, grad_radii, grad_depth, grad_0, grad_1):
-        if ctx.render_mode not in (0, 4):
+        if ctx.render_mode not in (0, 4, 12):
             raise NotImplementedError(f"render_mode {ctx.render_mode} is forward-only here; "
-                                      f"the backward covers modes 0 and 4")
+                                      f"the backward covers modes 0, 4 and 12 (training)")
         means3D, opacities, scales, rotations = ctx.saved_tensors
         fw = ctx.fw
         g = _rz.rasterize_backward(fw["settings"], fw["grid"], fw["res"], means3D.detach(), opacities.detach(),

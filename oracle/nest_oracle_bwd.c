@@ -136,7 +136,7 @@ static void qf_backward(const or_grid *G, const float xyz[3], uint32_t ap, int C
 }
 
 /* ------------------------------------------------------------------ */
-/* render backward: CR/backward.cu:445-2049 (modes 0 and 4, kernel 0)   */
+/* render backward: CR/backward.cu:445-2049 (modes 0, 4, 12; kernel 0)  */
 /* ------------------------------------------------------------------ */
 
 typedef struct {
@@ -164,11 +164,13 @@ typedef struct {
     float *dmean2D;              /* [P][3]                                 */
     float *dnormal;              /* [P][3]                                 */
     float *dopacity;             /* [P]                                    */
-    float *dcolors;              /* [P][C]; [P][hyb*F] in render mode 4    */
+    float *dcolors;              /* [P][C]; [P][hyb*F] in render mode 4,
+                                    [P][total*F+1] in render mode 12        */
     float *gradsum;              /* [P]                                    */
-    /* 0, or 4 (hybrid_features, CR/backward.cu:987-1040) with `level` the
-     * packed (total << 16) | (active grid levels << 8) | per-splat levels
-     * and colors the [P][hyb*F] per-splat rows */
+    /* 0, 4 (hybrid_features, CR/backward.cu:987-1040) or 12 (adaptive_cat
+     * training, :1425-1520) with `level` the packed (total << 16) | (active
+     * grid levels << 8) | per-splat levels and colors the per-splat rows,
+     * [P][hyb*F] in mode 4, [P][total*F+1] in mode 12 */
     int render_mode;
 } or_render_bwd_args;
 
@@ -300,6 +302,38 @@ static void render_pixel_bwd(const or_render_bwd_args *A, uint32_t tile, uint32_
                     qf_backward(&G, xyz, ap, C - pgd, grad_feat + pgd, feat + pgd, A->dtable, dxyz);
                 }
                 for (int i = 0; i < pgd; i++) A->dcolors[(size_t)id * pgd + i] += grad_feat[i];
+            } else if (A->render_mode == 12) {
+                /* adaptive_cat training (CR/backward.cu:1425-1520): rows
+                 * [total*F | weight]; the coarse hyb*F channels pass their
+                 * gradient to the row, the hl grid levels split theirs into
+                 * weight * g for the row, (1 - weight) * g for the table and
+                 * (row - grid) . g for the weight.  The blend terms of dL/dalpha
+                 * use the forward's features (the reference reads an array it
+                 * never wrote here). */
+                const int total = (A->level >> 16) & 0xFF, hl = (A->level >> 8) & 0xFF, hyb = A->level & 0xFF;
+                const int F = A->grid.F, tdim = total * F, fs = hyb * F;
+                const float *gf = A->colors + (size_t)id * (size_t)(tdim + 1);
+                float *dc = A->dcolors + (size_t)id * (size_t)(tdim + 1);
+                const float wt = gf[tdim];
+                for (int ch = 0; ch < C; ch++) feat[ch] = 0.0f;
+                for (int i = 0; i < fs; i++) {
+                    feat[i] = gf[i];
+                    dc[i] += grad_feat[i];
+                }
+                float dweight = 0.0f;
+                if (hl > 0) {
+                    or_grid G = A->grid;
+                    G.L = hl;
+                    float hf[64], gh[64];
+                    for (int i = 0; i < hl * F; i++) gh[i] = (1.0f - wt) * grad_feat[fs + i];
+                    qf_backward(&G, xyz, ap, hl * F, gh, hf, A->dtable, dxyz);
+                    for (int i = 0; i < hl * F; i++) {
+                        dc[fs + i] += wt * grad_feat[fs + i];
+                        dweight += (gf[fs + i] - hf[i]) * grad_feat[fs + i];
+                        feat[fs + i] = fmaf(wt, gf[fs + i], (1.0f - wt) * hf[i]);
+                    }
+                }
+                dc[tdim] += dweight;
             } else {
                 qf_backward(&A->grid, xyz, ap, C, grad_feat, feat, A->dtable, dxyz);
             }

@@ -241,17 +241,26 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
 
 def render_backward(pre, binres, fwd, W, H, C, grid: Optional[OrGrid], dL_dpix, dL_dothers, homotrans=None,
                     ap_level=None, colors=None, beta=0.0, render_mode=0, level=None):
-    """renderCUDAsurfelBackward (modes 0 and 4) for every pixel, given the
+    """renderCUDAsurfelBackward (modes 0, 4 and 12) for every pixel, given the
     forward's final_T / n_contrib (fwd = render(...)'s result).  Returns the
     per-splat gradients (dtransmat [P,9], dhomo [P,9], dmean2D [P,3],
     dnormal [P,3], dopacity [P], dcolors [P,C], or [P,hyb*F] in mode 4,
-    gradsum [P]) and dtable [rows, F].  Mode 4 takes the packed level
+    [P,total*F+1] in mode 12, gradsum [P]) and dtable [rows, F].  Modes 4
+    and 12 take the packed level
     (total << 16) | (active grid levels << 8) | per-splat levels and the
     per-splat rows as colors."""
     P = pre["radii"].shape[0]
     rows = 0 if grid is None else grid._keep[1].shape[0]
     F = 1 if grid is None else grid.F
-    dcol = C if render_mode == 0 else (level & 0xFF) * F
+    if render_mode not in (0, 4, 12) or (render_mode != 0 and (grid is None or level is None)):
+        raise ValueError(f"render_backward: render_mode {render_mode} needs mode 0, or mode 4 or 12 with a grid "
+                         f"and level")
+    if render_mode == 0:
+        dcol = C
+    elif render_mode == 4:
+        dcol = (level & 0xFF) * F
+    else:
+        dcol = ((level >> 16) & 0xFF) * F + 1
     out = dict(dtransmat=np.zeros((P, 9), np.float32), dhomo=np.zeros((P, 9), np.float32),
                dmean2D=np.zeros((P, 3), np.float32), dnormal=np.zeros((P, 3), np.float32),
                dopacity=np.zeros(P, np.float32), dcolors=np.zeros((P, max(dcol, 1)), np.float32),
@@ -267,8 +276,6 @@ def render_backward(pre, binres, fwd, W, H, C, grid: Optional[OrGrid], dL_dpix, 
 
     a = OrRenderBwdArgs()
     a.W, a.H, a.C = W, H, C
-    if render_mode not in (0, 4) or (render_mode == 4 and (grid is None or level is None)):
-        raise ValueError(f"render_backward: render_mode {render_mode} needs mode 0, or mode 4 with a grid and level")
     a.level = (0 if grid is None else grid.L) if render_mode == 0 else level
     a.render_mode = render_mode
     a.beta = beta

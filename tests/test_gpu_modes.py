@@ -270,11 +270,12 @@ def test_cat_mode_backward_parity(oracle, name, hyb, gl, active):
         assert not gpu["dfeatures"].reshape(-1)[int(sc.offsets[active]) * F:].any()
 
 
-def test_drop_in_cat_mode_autograd(oracle):
+def test_drop_in_cat_modes_autograd(oracle):
     """GaussianRasterizer in render mode 4 under autograd, with the
     reference's packed L (7 of 12 grid levels active): the gradients of the
     per-splat rows, the table and the means reach the leaves and match the
-    oracle; mode 13 has no backward and says so."""
+    oracle; mode 12 gives the direct call's gradients; mode 13 has no
+    backward and says so."""
     from diff_surfel_rasterization import GaussianRasterizationSettings, GaussianRasterizer, HashGridSettings
     sc = scene("shell_small")
     sp = sc.spec
@@ -325,6 +326,33 @@ def test_drop_in_cat_mode_autograd(oracle):
         print(f"{name}: max rel err {err:.2e}", flush=True)
         assert np.abs(ref).max() > 0 and err < 2e-5, (name, err)
 
+    # mode 12 (adaptive_cat training) under autograd: the same gradients as
+    # nest_backward called directly
+    from nest_splat import rasterizer as rz
+    packed12 = (8 << 16) | (3 << 8) | 2
+    hs12 = HashGridSettings(packed12, math.log2(sp.per_level_scale), sp.base_res, False, 0,
+                            torch.tensor([0, 0, 8 * F], dtype=torch.int32, device=DEV))
+    rows12 = _rows(sc, 8 * F + 1, weight_col=8 * F, seed=7)
+    rows12_t, table12 = leaf(rows12), leaf(sc.table)
+    color12, _, allmap12, _, _ = GaussianRasterizer(rs, hs12)(
+        means3D=t(sc.means), means2D=None, opacities=t(sc.opacity), colors_precomp=rows12_t, scales=t(sc.scales),
+        rotations=t(sc.rotations), homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), features=table12,
+        offsets=t(offs), gridrange=t(np.asarray(sp.gridrange, np.float32)), render_mode=12)
+    dcol12 = t(rng.standard_normal((8 * F, H, W)).astype(np.float32))
+    ((color12 * dcol12).sum() + (allmap12 * t(doth)).sum()).backward()
+    settings = rz.make_settings(H, W, cam.tanfovx, cam.tanfovy, cam.world_view_transform, cam.full_proj_transform,
+                                cam.camera_center, if_contract=sp.contract)
+    grid12 = rz.HashGridDesc(3, F, sp.S, sp.base_res, t(sc.table), offs.astype(np.int64),
+                             np.asarray(sp.gridrange, np.float32), render_mode=12, hybrid_levels=2, total_levels=8)
+    kw = dict(homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), colors_precomp=t(rows12), channels=8 * F)
+    res12 = rz.rasterize_forward(settings, grid12, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations), **kw)
+    gb12 = rz.rasterize_backward(settings, grid12, res12, t(sc.means), t(sc.opacity), t(sc.scales),
+                                 t(sc.rotations), dcol12, t(doth), **kw)
+    torch.cuda.synchronize()
+    for name, ours, ref in (("rows12", rows12_t.grad, gb12.dcolors), ("table12", table12.grad, gb12.dfeatures)):
+        o, r = ours.cpu().numpy().astype(np.float64), ref.cpu().numpy().reshape(ours.shape)
+        assert np.abs(r).max() > 0 and np.abs(o - r).max() <= 2e-5 * np.abs(r).max(), name
+
     hs13 = HashGridSettings((8 << 16) | (3 << 8) | 2, math.log2(sp.per_level_scale), sp.base_res, False, 0,
                             torch.tensor([0, 0, 8 * F], dtype=torch.int32, device=DEV))
     rows13 = leaf(_rows(sc, 8 * F + 1, weight_col=8 * F, seed=6))
@@ -334,3 +362,74 @@ def test_drop_in_cat_mode_autograd(oracle):
         offsets=t(offs), gridrange=t(np.asarray(sp.gridrange, np.float32)), render_mode=13)
     with pytest.raises(NotImplementedError, match="forward-only"):
         color13.sum().backward()
+
+
+# (scene, total levels, per-splat levels, grid levels)
+AC_BWD_CASES = [("cfg1", 8, 3, 5), ("shell_small", 12, 4, 8), ("unbounded_small", 16, 10, 6), ("cfg1", 6, 2, 0)]
+
+
+@pytest.mark.parametrize("name,total,hyb,gl", AC_BWD_CASES)
+def test_adaptive_cat_backward_parity(oracle, name, total, hyb, gl):
+    """nest_backward in render mode 12 (training) against the backward oracle,
+    which the CPU tests pin against float64 autograd: gradients of the rows
+    and their blend weights, the table and the geometry, within 2e-5 of each
+    array's largest entry."""
+    from nest_splat import rasterizer as rz
+    sc = scene(name)
+    sp = sc.spec
+    F = sp.F
+    tdim = total * F
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    print(f"[case] mode 12 backward {name} total={total} hyb={hyb} grid levels={gl}", flush=True)
+    rows = _rows(sc, tdim + 1, weight_col=tdim, seed=total + 50)
+    ap = sc.ap_level.reshape(-1).copy()
+    ap[::5] = 3.0
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    settings = rz.make_settings(H, W, cam.tanfovx, cam.tanfovy, cam.world_view_transform, cam.full_proj_transform,
+                                cam.camera_center, if_contract=sp.contract)
+    grid = rz.HashGridDesc(gl, F, sp.S, sp.base_res, t(sc.table), sc.offsets, np.asarray(sp.gridrange, np.float32),
+                           render_mode=12, hybrid_levels=hyb, total_levels=total)
+    kw = dict(homotrans=t(sc.homotrans), ap_level=t(ap), colors_precomp=t(rows), channels=tdim)
+    res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations), **kw)
+    rng = np.random.default_rng(31)
+    dcol = rng.standard_normal((tdim, H, W)).astype(np.float32)
+    doth = rng.standard_normal((14, H, W)).astype(np.float32)
+    gb = rz.rasterize_backward(settings, grid, res, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
+                               t(dcol), t(doth), **kw)
+    torch.cuda.synchronize()
+    gpu = {k: (None if v is None else v.cpu().numpy()) for k, v in vars(gb).items()}
+
+    level = (total << 16) | (gl << 8) | hyb
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    g = oracle.make_grid(max(gl, 1), F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    fwd = oracle.render(pre, b, W, H, tdim, g, homotrans=sc.homotrans, ap_level=ap, colors=rows, render_mode=12,
+                        level=level)
+    np.testing.assert_array_equal(res.color.cpu().numpy(), fwd["color"])  # same forward state
+    ob = oracle.render_backward(pre, b, fwd, W, H, tdim, g, dcol, doth, homotrans=sc.homotrans.reshape(-1, 16),
+                                ap_level=ap, colors=rows, render_mode=12, level=level)
+    pb = oracle.preprocess_backward(sc.means, sc.scales, sc.rotations, pre["radii"], pre["transmat"],
+                                    cam.world_view_transform, cam.full_proj_transform, W, H, ob["dtransmat"],
+                                    ob["dhomo"], ob["dnormal"], ob["dmean2D"])
+    ref = dict(dmeans3D=pb["dmeans"], dmeans2D=pb["dmean2D"], dopacity=ob["dopacity"][:, None],
+               dscales=pb["dscales"], drotations=pb["drots"], drows=ob["dcolors"][:, :tdim],
+               dweight=ob["dcolors"][:, tdim], dgradsum=ob["gradsum"][:, None])
+    gpu["drows"], gpu["dweight"] = gpu["dcolors"][:, :tdim], gpu["dcolors"][:, tdim]
+    if gl > 0:
+        ref["dfeatures"] = ob["dtable"].reshape(gpu["dfeatures"].shape)
+    vis = pre["radii"] > 0
+    for k, r in ref.items():
+        o = gpu[k]
+        assert o.shape == r.shape, (k, o.shape, r.shape)
+        assert np.isfinite(o).all(), k
+        if k == "dweight" and gl == 0:
+            assert not o.any() and not r.any()
+            continue
+        assert np.abs(r).max() > 0, k
+        err = float(np.abs(o.astype(np.float64) - r).max() / np.abs(r).max())
+        print(f"{k}: max rel err {err:.2e}", flush=True)
+        assert err < 2e-5, (k, err)
+        if k != "dfeatures":
+            assert not o[~vis].any(), k

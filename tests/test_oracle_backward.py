@@ -318,3 +318,74 @@ def test_cat_mode_backward_matches_autograd(oracle, hyb, active):
         assert err < TOL, (name, err)
     if 0 < active < L:  # no gradient reaches the inactive levels
         assert not gb["dtable"][int(sc.offsets[active]):].any()
+
+
+@pytest.mark.parametrize("hyb,hl,extra,ap_cap", [(2, 3, 1, False), (1, 4, 0, True), (3, 0, 1, False)])
+def test_adaptive_cat_backward_matches_autograd(oracle, hyb, hl, extra, ap_cap):
+    """Render mode 12 training backward (CR/backward.cu:1425-1520): coarse rows
+    unweighted, the hl grid levels blended with the row by its weight; the
+    gradients of the rows (weight included), the table and the geometry are
+    those of the forward.  Per-splat weights in (0, 1); some splats query
+    fewer levels (ap_level 2)."""
+    sc = _tiny(seed=30 + hyb)
+    sp = sc.spec
+    F = sp.F
+    total = hyb + hl + extra
+    tdim, fs = total * F, hyb * F
+    C = tdim
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    ap = sc.ap_level.reshape(-1).copy()
+    if ap_cap:
+        ap[::3] = 2.0
+    rng = np.random.default_rng(hyb + hl)
+    rows = rng.uniform(-1, 1, (sp.P, tdim + 1)).astype(np.float32)
+    rows[:, tdim] = rng.uniform(0.05, 0.95, sp.P).astype(np.float32)
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    assert b["num_rendered"] > 0
+    g = oracle.make_grid(max(hl, 1), F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    level = (total << 16) | (hl << 8) | hyb
+    fwd = oracle.render(pre, b, W, H, C, g, homotrans=sc.homotrans, ap_level=ap, colors=rows, render_mode=12,
+                        level=level)
+    r2 = np.random.default_rng(17)
+    dpix = r2.standard_normal(fwd["color"].shape).astype(np.float32)
+    doth = r2.standard_normal(fwd["others"].shape).astype(np.float32)
+    homo = sc.homotrans.reshape(-1, 16).astype(np.float32)
+    gb = oracle.render_backward(pre, b, fwd, W, H, C, g, dpix, doth, homotrans=homo, ap_level=ap, colors=rows,
+                                render_mode=12, level=level)
+    assert gb["dcolors"].shape == (sp.P, tdim + 1)
+
+    leaf = lambda a: torch.tensor(np.asarray(a, np.float64), requires_grad=True)
+    leaves = dict(T=leaf(pre["transmat"]), xy=leaf(pre["xy"]), normal=leaf(pre["normal_opacity"][:, :3]),
+                  opacity=leaf(pre["normal_opacity"][:, 3]), homo=leaf(homo),
+                  table=leaf(sc.table.reshape(-1, sp.F)), rows=leaf(rows))
+    gd = dict(L=hl, F=F, S=sp.S, H=sp.base_res, offsets=sc.offsets, vmin=sp.gridrange[0], vmax=sp.gridrange[1],
+              hyb12=hyb)
+    color, others = TR.render_forward(oracle, pre, b, fwd, W, H, C, leaves, grid=gd, homotrans_np=homo,
+                                      ap_level=ap)
+    assert _rel(color.detach().numpy(), fwd["color"]) < 1e-4
+    loss = (color * torch.from_numpy(dpix.astype(np.float64))).sum() + \
+        (others * torch.from_numpy(doth[:7].astype(np.float64))).sum()
+    loss.backward()
+    vis = pre["radii"] > 0
+    rg = leaves["rows"].grad.numpy()
+    checks = {"dtransmat": (gb["dtransmat"], leaves["T"].grad), "dmean2D": (gb["dmean2D"][:, :2], leaves["xy"].grad),
+              "dnormal": (gb["dnormal"], leaves["normal"].grad), "dopacity": (gb["dopacity"], leaves["opacity"].grad),
+              "drows": (gb["dcolors"][:, :tdim], rg[:, :tdim])}
+    if hl > 0:
+        gh = leaves["homo"].grad.numpy()
+        checks["dhomo"] = (gb["dhomo"], gh[:, [0, 4, 8, 1, 5, 9, 3, 7, 11]])
+        checks["dtable"] = (gb["dtable"], leaves["table"].grad)
+        checks["dweight"] = (gb["dcolors"][:, tdim], rg[:, tdim])
+    else:
+        assert not gb["dtable"].any() and not gb["dcolors"][:, tdim].any()
+    for name, (ours, ref) in checks.items():
+        ref = ref.numpy() if isinstance(ref, torch.Tensor) else ref
+        if name != "dtable":
+            ours, ref = ours[vis], ref[vis]
+        assert np.abs(ref).max() > 0, name
+        err = _rel(ours, ref)
+        print(f"{name}: rel err {err:.2e}")
+        assert err < TOL, (name, err)

@@ -78,7 +78,8 @@ def render_forward(O, pre, binres, fwd, W, H, C, leaves, grid=None, beta=0.0, ho
     leaves: dict of float64 tensors with requires_grad: T [P,9], xy [P,2],
     normal [P,3], opacity [P], and colors [P,C] (colour path) or homo [P,16]
     and table [rows,F] (hash path), with rows [P,R] ahead of the grid
-    features in render mode 4.  grid: dict(L, F, S, H, offsets, vmin,
+    features in render mode 4, or rows [P,total*F+1] blended with them in
+    render mode 12 (grid["hyb12"] = per-splat levels).  grid: dict(L, F, S, H, offsets, vmin,
     vmax) for the hash path (non-contracted, not align_corners, linear)."""
     HW = W * H
     gx = (W + 15) // 16
@@ -144,11 +145,20 @@ def render_forward(O, pre, binres, fwd, W, H, C, leaves, grid=None, beta=0.0, ho
             feat = leaves["colors"][ids][None].expand(px.shape[0], n, C)
         else:
             rows = leaves.get("rows")
-            pgd = 0 if rows is None else rows.shape[1]
-            feat = _hash_features(O, grid, leaves, ids, acc, use3d, sx32, sy32, sx, sy, homotrans_np, ap_level,
-                                  C - pgd)
-            if rows is not None:  # render mode 4: per-splat rows ahead of the grid features
-                feat = torch.cat([rows[ids][None].expand(px.shape[0], n, pgd), feat], dim=2)
+            if "hyb12" in grid:  # render mode 12: [coarse rows | blended levels | zeros], row ends with the weight
+                fs, nf = grid["hyb12"] * grid["F"], grid["L"] * grid["F"]
+                tdim = rows.shape[1] - 1
+                hf = _hash_features(O, grid, leaves, ids, acc, use3d, sx32, sy32, sx, sy, homotrans_np, ap_level, nf)
+                r = rows[ids][None].expand(px.shape[0], n, tdim + 1)
+                wt = r[..., tdim:]
+                feat = torch.cat([r[..., :fs], wt * r[..., fs:fs + nf] + (1.0 - wt) * hf,
+                                  torch.zeros_like(r[..., :C - fs - nf])], dim=2)
+            else:
+                pgd = 0 if rows is None else rows.shape[1]
+                feat = _hash_features(O, grid, leaves, ids, acc, use3d, sx32, sy32, sx, sy, homotrans_np, ap_level,
+                                      C - pgd)
+                if rows is not None:  # render mode 4: per-splat rows ahead of the grid features
+                    feat = torch.cat([rows[ids][None].expand(px.shape[0], n, pgd), feat], dim=2)
         color[:, pid] = color[:, pid] + torch.einsum("pj,pjc->cp", w, feat)
         nrm = leaves["normal"][ids][None]
         m = FAR / (FAR - NEAR) * (1 - NEAR / torch.where(accT, depth, torch.ones_like(depth)))
