@@ -105,8 +105,13 @@ typedef struct nest_hashgrid {
    *     the row unweighted, the grid levels are blended with the row in
    *     training; in inference a splat with weight >= 0.9 takes its row
    *     without a grid lookup; every hit records its world position,
-   *     appearance colour and last contributor (CR/forward.cu:1593-1713).
-   * Modes 4, 12 and 13 need level_dim 2, 4 or 8 and at most 64 channels of
+   *     appearance colour and last contributor (CR/forward.cu:1593-1713);
+   *   NEST_MODE_ADAPTIVE_ZERO (14), | NEST_MODE_INFERENCE for inference:
+   *     colors_precomp rows of hybrid_levels*level_dim features plus a
+   *     weight; the grid's `levels` levels follow, times the weight, when the
+   *     weight is > 1e-6 (training) or >= 0.1 (inference), else zero; full
+   *     hits (CR/forward.cu:1716-1830).
+   * Modes 4, 12, 13 and 14 need level_dim 2, 4 or 8 and at most 64 channels of
    * per-splat plus grid features; `levels` may be 0 there. */
   int32_t render_mode;
   uint32_t hybrid_levels;
@@ -124,6 +129,7 @@ typedef struct nest_hashgrid {
 #define NEST_MODE_CAT 4
 #define NEST_MODE_ADAPTIVE_CAT 12
 #define NEST_MODE_ADAPTIVE_CAT_FAST 13
+#define NEST_MODE_ADAPTIVE_ZERO 14
 #define NEST_MODE_INFERENCE 0x100
 
 /* Splat attributes (device, float32, contiguous), as the reference passes them
@@ -252,7 +258,7 @@ int nest_forward_geometry(const nest_raster_settings *settings, const nest_splat
  * (:173-195, :388) and renderCUDAsurfelForward<C, render_mode>
  * (CR/forward.cu:639-2049, dispatch :2052-2158).  out_color channels must
  * cover the features of the mode (levels*level_dim in mode 0, plus
- * hybrid_levels*level_dim in mode 4, total_levels*level_dim in modes 12, 13);
+ * hybrid_levels*level_dim in mode 4, total_levels*level_dim in modes 12-14);
  * channels past them are written as zero. */
 int nest_forward_render(const nest_raster_settings *settings, const nest_hashgrid *grid,
                         const nest_splats *splats, void *geom_ws, size_t geom_bytes,
@@ -268,7 +274,9 @@ int nest_forward_render(const nest_raster_settings *settings, const nest_hashgri
  * [P, hybrid_levels*level_dim], of the grid's active levels into
  * dL_dfeatures; mode 12 in training, CR/backward.cu:1425-1520, gradients of
  * the rows and their blend weight into dL_dcolors [P, total_levels*level_dim
- * + 1]) with the Gaussian kernel: renderCUDAsurfelBackward
+ * + 1]; mode 14 in training, CR/backward.cu:1521-1590, into dL_dcolors
+ * [P, hybrid_levels*level_dim + 1]) with the Gaussian kernel:
+ * renderCUDAsurfelBackward
  * (CR/backward.cu:445-2049) then
  * preprocessCUDA backward (CR/backward.cu:2216-2274).  It reads the
  * workspaces of the nest_forward_geometry / nest_forward_render calls of the
@@ -295,7 +303,8 @@ typedef struct {
     float *dL_dmeans2D;              /* [P,3] densification statistic */
     float *dL_dcolors;               /* [P,C] colour path, [P,hybrid_levels*level_dim]
                                         in render mode 4, [P,total_levels*level_dim+1]
-                                        in render mode 12, or NULL */
+                                        in render mode 12, [P,hybrid_levels*level_dim+1]
+                                        in render mode 14, or NULL */
     float *dL_dopacity;              /* [P] */
     float *dL_dshs;                  /* [P,sh_coeffs,3] when the colours came from SH */
     float *dL_dscales;               /* [P,2] */

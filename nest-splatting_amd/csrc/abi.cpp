@@ -186,10 +186,11 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
                GridParams& g) {
   int rc = NEST_OK;
   const int base_mode = gr->render_mode & 0xFF;
-  const bool adaptive = base_mode == NEST_MODE_ADAPTIVE_CAT || base_mode == NEST_MODE_ADAPTIVE_CAT_FAST;
+  const bool adaptive = base_mode == NEST_MODE_ADAPTIVE_CAT || base_mode == NEST_MODE_ADAPTIVE_CAT_FAST ||
+                        base_mode == NEST_MODE_ADAPTIVE_ZERO;
   if ((gr->render_mode & ~0x1FF) != 0 || (base_mode != NEST_MODE_BASELINE && base_mode != NEST_MODE_CAT && !adaptive) ||
       ((gr->render_mode & NEST_MODE_INFERENCE) && !adaptive))
-    return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: supported are 0, 4, 12, 13, 12 | 0x100 and 13 | 0x100",
+    return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: supported are 0, 4, 12, 13, 14 and 12, 13, 14 | 0x100",
                 gr->render_mode);
   const bool mix = base_mode != NEST_MODE_BASELINE;
   if (mix) {
@@ -214,7 +215,7 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
                   gr->render_mode, feat);
     if (sp->P > 0) {
       if (!sp->homotrans) return fail(NEST_ERR_INVALID_ARGUMENT, "homotrans is required in render_mode %d", gr->render_mode);
-      if (!sp->colors_precomp && (base_mode == NEST_MODE_ADAPTIVE_CAT_FAST || hyb > 0))
+      if (!sp->colors_precomp && (adaptive || hyb > 0))
         return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode %d needs the per-splat features in colors_precomp",
                     gr->render_mode);
       // the render queue packs the splat id into 25 bits
@@ -457,9 +458,21 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     rp.hyb = (int)gr->hybrid_levels;
     rp.pgd = rp.hyb * F;
     rp.wslot = -1;
+    rp.fthr = INFINITY;  // no fast hits unless the mode has an inference or skip rule
+    rp.fneg = 0;
     if ((gr->render_mode & 0xFF) == NEST_MODE_CAT) {
       rp.cstride = rp.pgd;
       rp.nrow = rp.pgd;
+    } else if ((gr->render_mode & 0xFF) == NEST_MODE_ADAPTIVE_ZERO) {
+      // mode 14 (CR/forward.cu:1716-1830): rows [pgd | weight], grid * weight
+      rp.cstride = rp.pgd + 1;
+      rp.nrow = rp.pgd;
+      rp.wslot = rp.pgd;
+      rp.infer = (gr->render_mode & NEST_MODE_INFERENCE) ? 1 : 0;
+      rp.gscale = 1;
+      // skips the grid when !(weight >= 0.1) in inference, !(weight > 1e-6) in training
+      rp.fthr = rp.infer ? std::nextafter(0.1f, 0.0f) : 1e-6f;
+      rp.fneg = 1;
     } else {
       // modes 12 and 13 (CR/forward.cu:965-1101, :1593-1713)
       const int tdim = (int)gr->total_levels * F;
@@ -472,6 +485,8 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
       rp.m13 = m13 ? 1 : 0;
       rp.wcoarse = (m13 && !rp.infer) ? 1 : 0;
       rp.nfast = gr->total_levels - gr->hybrid_levels;
+      // inference takes the row when weight > 0.5 (mode 13) or >= 0.9 (mode 12)
+      if (rp.infer) rp.fthr = m13 ? 0.5f : std::nextafter(0.9f, 0.0f);
     }
   }
 
@@ -712,12 +727,13 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   if (!io || io->struct_size != sizeof(nest_backward_io))
     return fail(NEST_ERR_INVALID_ARGUMENT, "nest_backward_io missing or struct_size mismatch");
   if (gr->render_mode != NEST_MODE_BASELINE && gr->render_mode != NEST_MODE_CAT &&
-      gr->render_mode != NEST_MODE_ADAPTIVE_CAT)
+      gr->render_mode != NEST_MODE_ADAPTIVE_CAT && gr->render_mode != NEST_MODE_ADAPTIVE_ZERO)
     return fail(NEST_ERR_UNSUPPORTED,
-                "backward: render_mode %d is forward-only here (modes 0, 4 and 12 without the inference flag have a "
-                "backward)", gr->render_mode);
+                "backward: render_mode %d is forward-only here (modes 0, 4, 12 and 14 without the inference flag "
+                "have a backward)", gr->render_mode);
   const bool cat = gr->render_mode == NEST_MODE_CAT;
   const bool acat = gr->render_mode == NEST_MODE_ADAPTIVE_CAT;
+  const bool azero = gr->render_mode == NEST_MODE_ADAPTIVE_ZERO;
   const int C = io->channels;
   if (C < 1 || C > 64) return fail(NEST_ERR_UNSUPPORTED, "backward: channels must be in [1, 64] (got %d)", C);
   if (!io->dL_dout_color || !io->dL_dout_others)
@@ -729,11 +745,11 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   GridParams g{};
   if ((rc = setup_grid(rs, gr, sp, C, g))) return rc;
   const bool hash = gr->levels > 0;
-  const bool from_sh = !cat && !acat && !hash && sh_colours(sp);
+  const bool from_sh = !cat && !acat && !azero && !hash && sh_colours(sp);
   // mode 4: per-splat rows of pgd floats; the grid levels differentiated are
   // those up to the last one within the active count whose offsets increase
   // (CR/backward.cu:576-612, :993-999)
-  const int pgd = (cat || acat) ? (int)(gr->hybrid_levels * gr->level_dim) : 0;
+  const int pgd = (cat || acat || azero) ? (int)(gr->hybrid_levels * gr->level_dim) : 0;
   // mode 12: rows of total*F features and the blend weight; the grid's levels
   // are blended (CR/backward.cu:1425-1520)
   const int tdim = acat ? (int)(gr->total_levels * gr->level_dim) : 0;
@@ -744,10 +760,11 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
       if (gr->offsets[i] > gr->offsets[i - 1]) cat_levels = i;
     g.L = cat_levels;
   }
-  const int dcol_width = cat ? pgd : acat ? tdim + 1 : C;
+  const int dcol_width = cat ? pgd : acat ? tdim + 1 : azero ? pgd + 1 : C;
   // the workspace's colour-gradient field holds [P, channels]: mode-12 rows are wider
-  if (acat && !io->dL_dcolors)
-    return fail(NEST_ERR_INVALID_ARGUMENT, "backward: render_mode 12 needs dL_dcolors [P, %d]", tdim + 1);
+  if ((acat || azero) && !io->dL_dcolors)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "backward: render_mode %d needs dL_dcolors [P, %d]", gr->render_mode,
+                dcol_width);
   if (hash && g.half) return fail(NEST_ERR_UNSUPPORTED, "backward: the hash table must be float32");
   if (hash && !io->dL_dfeatures) return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dfeatures is required");
   if (from_sh && !io->dL_dshs) return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dshs is required with SH colours");
@@ -802,11 +819,12 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   rp.gy = gy;
   rp.ntiles = gx * gy;
   rp.C = C;
-  rp.level = (cat || acat) ? 1 : (int)gr->levels;  // modes 4 and 12 always take the hash branch
+  rp.level = (cat || acat || azero) ? 1 : (int)gr->levels;  // these modes always take the hash branch
   rp.pgd = pgd;
-  rp.cstride = acat ? tdim + 1 : pgd;
-  rp.wslot = acat ? tdim : -1;
-  rp.nfine = acat ? (int)(gr->levels * gr->level_dim) : 0;
+  rp.cstride = dcol_width;
+  rp.wslot = acat ? tdim : azero ? pgd : -1;
+  rp.azero = azero ? 1 : 0;
+  rp.nfine = (acat || azero) ? (int)(gr->levels * gr->level_dim) : 0;
   rp.beta = rs->beta;
   rp.ranges = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_RANGES]);
   rp.tile_order = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_TILE_ORDER]);

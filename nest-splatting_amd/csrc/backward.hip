@@ -275,7 +275,9 @@ __device__ __forceinline__ bool grid_coord_bwd(const GridParams& g, const float 
 // of the grid's channels (CR/backward.cu:987-1040).  kRows 2: render mode 12
 // training, rows of p.cstride floats ending with the blend weight (p.wslot):
 // p.pgd coarse channels from the row, then p.nfine channels blended
-// weight * row + (1 - weight) * grid (CR/backward.cu:1425-1520).
+// weight * row + (1 - weight) * grid (CR/backward.cu:1425-1520); with p.azero,
+// render mode 14 training: rows [pgd | weight], then weight * grid over p.nfine
+// channels when the weight is > 1e-6 (CR/backward.cu:1521-1590).
 template <int F, bool kHash, int kRows>
 __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const RenderBwdParams p) {
   __shared__ float4 srec[kBwdChunks][kBwdThreads];
@@ -404,19 +406,23 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
             const float* row = p.colors + (size_t)id * (uint32_t)p.cstride;
             wt = row[p.wslot];
             for (int ch = 0; ch < p.pgd; ch++) rdot += row[ch] * dpix[(size_t)ch * HW];
-            for (int i = 0; i < p.nfine; i++) fdot += row[p.pgd + i] * dpix[(size_t)(p.pgd + i) * HW];
+            if (!p.azero)
+              for (int i = 0; i < p.nfine; i++) fdot += row[p.pgd + i] * dpix[(size_t)(p.pgd + i) * HW];
             wcol = wgt;
           }
           const uint32_t ap = __float_as_uint(q3.w);
           const uint32_t maxl = ap < g.L ? ap : g.L;
           lane_levels = grid_coord_bwd(g, xyz, u, grad_scale) ? maxl : 0u;
+          if (kRows == 2 && p.azero && !(wt > 1e-6f)) lane_levels = 0u;  // mode 14 skips the grid
         }
       }
       if constexpr (kHash) {
         // every lane takes part (cross-lane sums inside); lanes without a hit have no levels
-        // mode 12: the grid's share of the gradient is (1 - weight) of it
+        // the grid's share of the gradient: (1 - weight) of it in mode 12,
+        // weight times it in mode 14
         if (__ballot(lane_levels > 0u) != 0ull)
-          hash_backward_wave<F>(g, rsrc, u, grad_scale, lane_levels, kRows == 2 ? wgt * (1.0f - wt) : wgt,
+          hash_backward_wave<F>(g, rsrc, u, grad_scale, lane_levels,
+                                kRows == 2 ? wgt * (p.azero ? wt : 1.0f - wt) : wgt,
                                 kRows ? dpix + (size_t)p.pgd * HW : dpix, HW, p.dtable, dot, dxyz);
         if constexpr (kRows == 1) {
           dot += rdot;
@@ -424,8 +430,13 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
           // dot is grid . dpix over the fine channels; the hit's features are
           // the coarse rows and weight * row + (1 - weight) * grid
           const float hdot = dot;
-          dot = rdot + wt * fdot + (1.0f - wt) * hdot;
-          fdot = wgt * (fdot - hdot);  // dL/dweight
+          if (p.azero) {  // mode 14: coarse rows, then weight * grid
+            dot = rdot + wt * hdot;
+            fdot = wgt * hdot;  // dL/dweight
+          } else {
+            dot = rdot + wt * fdot + (1.0f - wt) * hdot;
+            fdot = wgt * (fdot - hdot);  // dL/dweight
+          }
         }
       }
       if (act) {
@@ -526,7 +537,7 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
             }
           } else if constexpr (kRows == 2) {
             float* dc = p.dcolors + (size_t)id * (uint32_t)p.cstride;
-            for (int ch = 0; ch < p.pgd + p.nfine; ch++) {
+            for (int ch = 0; ch < p.pgd + (p.azero ? 0 : p.nfine); ch++) {
               const float v = wave_sum((ch < p.pgd ? wcol : wcol * wt) * dpix[(size_t)ch * HW]);
               if (lead && v != 0.0f) atomic_add(dc + ch, v);
             }

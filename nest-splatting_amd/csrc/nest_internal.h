@@ -114,7 +114,7 @@ struct RenderParams {
   float* final_T;
   uint32_t* n_contrib;
   GridParams grid;
-  // Per-splat features ahead of the grid's (render modes 4, 12 and 13):
+  // Per-splat features ahead of the grid's (render modes 4, 12, 13, 14):
   // channel c < pgd of a hit is row[c] (times the row's weight with
   // wcoarse); grid level l lands on channels pgd + l*F.
   int mix;                    // 0: mode 0
@@ -129,6 +129,9 @@ struct RenderParams {
   int m13;                    // mode 13: a hit updates no appearance colour and no last
                               // contributor, a fast hit adds no world position
   int wcoarse;                // mode 13 training: the first pgd channels take row * weight
+  int gscale;                 // mode 14: grid levels take grid * weight
+  float fthr;                 // a hit is fast (skips the grid) when (weight > fthr) != fneg;
+  int fneg;                   // fthr = +inf: no fast hits
   uint32_t nfast;             // levels of the row past pgd that a fast hit takes
 };
 
@@ -190,8 +193,9 @@ struct RenderBwdParams {
   float* gradsum;             // [P] hash path
   int pgd;                    // render modes 4, 12: per-splat (coarse) channels of a row (0 otherwise)
   int cstride;                // render mode 12: floats per row (total*F + 1)
-  int wslot;                  // render mode 12: index of the blend weight in a row, else -1
-  int nfine;                  // render mode 12: blended channels (grid levels * F)
+  int wslot;                  // render modes 12, 14: index of the blend weight in a row, else -1
+  int azero;                  // render mode 14: grid levels take grid * weight, no row part
+  int nfine;                  // render modes 12, 14: grid channels after the coarse ones (levels * F)
   GridParams grid;
 };
 hipError_t launch_render_backward(const RenderBwdParams& p, hipStream_t s);

@@ -218,7 +218,7 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
 // lookup lane loads the row entries of fast and blend hits along with the
 // corner gathers, one level ahead.  Hand-offs run only for the output levels
 // that can carry a value, [hyb, hyb + max(L, nfast)).
-template <int F, int NACC, bool kHalf, bool kStructured>
+template <int F, int NACC, bool kHalf, bool kStructured, bool kGs>
 __device__ __forceinline__ void drain_compact_mix(const RenderParams& p, nest_i32x4 rsrc,
                                                   float4 (*hq)[kRenderThreads], uint32_t (*hm)[kRenderThreads],
                                                   uint8_t* isrc, int& qhead, int& qn, float* acc) {
@@ -305,7 +305,8 @@ __device__ __forceinline__ void drain_compact_mix(const RenderParams& p, nest_i3
       for (int f = 0; f < F; f++) h[f] = 0.0f;
       if (look) corners_sum<F>(cn, vals, h);
 #pragma unroll
-      for (int f = 0; f < F; f++) v[f] = fast ? rv[f] : (p.blend ? fmaf(wt, rv[f], (1.0f - wt) * h[f]) : h[f]);
+      for (int f = 0; f < F; f++)
+        v[f] = fast ? rv[f] : (p.blend ? fmaf(wt, rv[f], (1.0f - wt) * h[f]) : (kGs ? wt * h[f] : h[f]));
     }
     bool next = false;
     if (l + 1 < kLevels && gl + 1 >= 0) {
@@ -350,7 +351,7 @@ __device__ __forceinline__ void drain_compact_mix(const RenderParams& p, nest_i3
 //                                     grid = 0 past the lookup count;
 //   otherwise                         the grid, gl < the lookup count;
 // and acc = fmaf(feature, w, acc) in queue order, as the other drains.
-template <int F, int NACC, bool kHalf, bool kStructured>
+template <int F, int NACC, bool kHalf, bool kStructured, bool kGs>
 __device__ __forceinline__ void drain_mixed(const RenderParams& p, nest_i32x4 rsrc, float4 (*hq)[kRenderThreads],
                                             uint32_t (*hm)[kRenderThreads], int& qhead, int& qn, float* acc) {
   if (qn > 0) {
@@ -389,6 +390,8 @@ __device__ __forceinline__ void drain_mixed(const RenderParams& p, nest_i32x4 rs
             v = row[gl * F + f];
           else if (p.blend)
             v = fmaf(wt, row[gl * F + f], (1.0f - wt) * h[f]);
+          else if (kGs)
+            v = wt * h[f];
           acc[l * F + f] = fmaf(v, e.w, acc[l * F + f]);
         }
       }
@@ -521,10 +524,11 @@ __device__ __forceinline__ void appearance_colour(uint32_t ap, float w, float& v
 // CU; amdgpu_waves_per_eu(3) gives the matching 168-VGPR budget, which holds
 // 64 accumulators and eight in-flight 16-byte corner loads.
 //
-// kMix: render modes 4 and 13 (per-splat features ahead of the grid's); the
+// kMix: render modes 4, 12, 13 (1) and 14 (2, grid levels times the weight):
+// per-splat features ahead of the grid's; the
 // queue then carries a 32-bit meta word per hit (drain_mixed) in place of
 // the level count, 53 KB of LDS in all.
-template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, bool kMix = false>
+template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0>
 __global__ void __launch_bounds__(kRenderThreads) __attribute__((amdgpu_waves_per_eu(3, 8)))
 render_kernel(const RenderParams p) {
   __shared__ float4 srec[kRecChunks][kBatch];
@@ -564,7 +568,7 @@ render_kernel(const RenderParams p) {
   int qn = 0, qhead = 0;  // per-lane ring buffer of pending lookups
   // kMix: an accepted hit's feature part waits for the converged block after
   // the per-lane test
-  [[maybe_unused]] std::conditional_t<kMix, PendingHit, NoPendingHit> ph;
+  [[maybe_unused]] std::conditional_t<(kMix != 0), PendingHit, NoPendingHit> ph;
 
   // Batches of 256 splats.  The splat index j is uniform across the wave;
   // lanes that are done skip the body, as the reference's per-lane loop
@@ -679,8 +683,10 @@ render_kernel(const RenderParams p) {
           float mine = lane < (uint32_t)p.nrow ? row[lane] : 0.0f;
           asm volatile("" : "+v"(mine));  // loaded here, with every lane active
           const float wt = p.wslot >= 0 ? row[p.wslot] : 1.0f;
-          // inference fast path: weight > 0.5 in mode 13, >= 0.9 in mode 12
-          const bool fast = p.infer && (p.m13 ? wt > 0.5f : wt >= 0.9f);
+          // fast hits skip the grid: weight > 0.5 in mode 13 inference, >= 0.9 in
+          // mode 12 inference (they take the row), < 0.1 in mode 14 inference and
+          // <= 1e-6 in mode 14 training (their grid levels stay zero)
+          const bool fast = (wt > p.fthr) != (p.fneg != 0);
           if (ph.on) {
             // per-splat channels at once; a fast hit's grid-level channels too
             // when no earlier hit of the pixel is pending
@@ -730,9 +736,10 @@ render_kernel(const RenderParams p) {
       // whenever a lane is full; at the end, until every queue is empty
       if (__ballot(qn == kQueue) || (last && __ballot(qn > 0))) {
         if constexpr (kMix && F <= 4)
-          drain_compact_mix<F, NACC, kHalf, kStructured>(p, rsrc, hq, hm, isrc + wid * kWaveLanes, qhead, qn, acc);
+          drain_compact_mix<F, NACC, kHalf, kStructured, kMix == 2>(p, rsrc, hq, hm, isrc + wid * kWaveLanes, qhead,
+                                                                    qn, acc);
         else if constexpr (kMix)
-          drain_mixed<F, NACC, kHalf, kStructured>(p, rsrc, hq, hm, qhead, qn, acc);
+          drain_mixed<F, NACC, kHalf, kStructured, kMix == 2>(p, rsrc, hq, hm, qhead, qn, acc);
         else if constexpr (F <= 4)
           drain_compact<F, NACC, kHalf, kStructured>(g, rsrc, hq, hl, isrc + wid * kWaveLanes, qhead, qn, acc);
         else
@@ -775,7 +782,7 @@ render_kernel(const RenderParams p) {
   O[pid + 13 * HW] = 0.0f;  // the third appearance channel only ever adds 0 * w
 }
 
-template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, bool kMix = false>
+template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0>
 static hipError_t launch_one(const RenderParams& p, hipStream_t s) {
   hipLaunchKernelGGL((render_kernel<F, NACC, kHash, kHalf, kStructured, kMix>), dim3(p.ntiles), dim3(kRenderThreads),
                      0, s, p);
@@ -850,8 +857,14 @@ __global__ void level_quads_kernel(LevelQuads lq, uint32_t L, LevelQuad* dst) {
 template <int F, bool kHalf, bool kStructured>
 static hipError_t launch_mix_levels(const RenderParams& p, hipStream_t s) {
   const uint32_t need = (uint32_t)p.pgd + (p.grid.L > p.nfast ? p.grid.L : p.nfast) * (uint32_t)F;
-  if (need <= 32u) return launch_one<F, 32, true, kHalf, kStructured, true>(p, s);
-  if (need <= 64u) return launch_one<F, 64, true, kHalf, kStructured, true>(p, s);
+  // mode 14 (grid levels times the weight) has its own drains
+  if (p.gscale) {
+    if (need <= 32u) return launch_one<F, 32, true, kHalf, kStructured, 2>(p, s);
+    if (need <= 64u) return launch_one<F, 64, true, kHalf, kStructured, 2>(p, s);
+    return hipErrorInvalidValue;
+  }
+  if (need <= 32u) return launch_one<F, 32, true, kHalf, kStructured, 1>(p, s);
+  if (need <= 64u) return launch_one<F, 64, true, kHalf, kStructured, 1>(p, s);
   return hipErrorInvalidValue;
 }
 

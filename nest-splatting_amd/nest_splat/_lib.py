@@ -62,6 +62,7 @@ MODE_BASELINE = 0
 MODE_CAT = 4
 MODE_ADAPTIVE_CAT = 12
 MODE_ADAPTIVE_CAT_FAST = 13
+MODE_ADAPTIVE_ZERO = 14
 MODE_INFERENCE = 0x100
 
 

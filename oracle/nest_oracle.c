@@ -629,8 +629,9 @@ typedef struct {
      * 4 per-splat features then hash features (level's low byte = per-splat
      * levels), 13 adaptive_cat_fast (level = total << 16 | hash << 8 | per-splat
      * levels, colors rows of total*F+1 floats, bit 8 of render_mode =
-     * inference), 12 adaptive_cat (same level and rows).  Other values are
-     * not restated. */
+     * inference), 12 adaptive_cat (same level and rows), 14 adaptive_zero
+     * (same level, rows of hyb*F+1 floats).  Other values are not
+     * restated. */
     int render_mode;
 } or_render_args;
 
@@ -763,7 +764,26 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
             hit_xyz(A->homotrans + 16 * (size_t)id, use3d, sx, sy, xyz);
             pos_x += w * xyz[0]; pos_y += w * xyz[1]; pos_z += w * xyz[2];
             uint32_t ap = f2u_sat(floorf(A->ap_level[id]));
-            if ((A->render_mode & 0xFF) == 12) {
+            if ((A->render_mode & 0xFF) == 14) {
+                /* adaptive_zero (forward.cu:1716-1830): rows [hyb*F features |
+                 * weight]; the first hyb*F channels from the row, the next hl
+                 * grid levels times the weight when the weight is > 1e-6
+                 * (training) or >= 0.1 (inference), else zero; full hits. */
+                const int infer = (A->render_mode >> 8) & 1;
+                const int hl = (A->level >> 8) & 0xFF, hyb = A->level & 0xFF;
+                const int F = A->grid.F, pgd = hyb * F;
+                const float *gf = A->colors + (size_t)id * (size_t)(pgd + 1);
+                const float wt = gf[pgd];
+                for (int c = 0; c < C; c++) feat_scratch[c] = 0.0f;
+                for (int i = 0; i < pgd && i < C; i++) feat_scratch[i] = gf[i];
+                if (hl > 0 && (infer ? wt >= 0.1f : wt > 1e-6f)) {
+                    or_grid G = A->grid;
+                    G.L = hl;
+                    float hf[64];
+                    or_query_feature(&G, xyz, ap, 64, hf);
+                    for (int i = 0; i < hl * F && pgd + i < C; i++) feat_scratch[pgd + i] = wt * hf[i];
+                }
+            } else if ((A->render_mode & 0xFF) == 12) {
                 /* adaptive_cat (forward.cu:1593-1713): rows [total*F features |
                  * blend weight]; the first hyb*F channels come from the row;
                  * training blends the next hl*F with the grid,

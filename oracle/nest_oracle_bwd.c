@@ -136,7 +136,7 @@ static void qf_backward(const or_grid *G, const float xyz[3], uint32_t ap, int C
 }
 
 /* ------------------------------------------------------------------ */
-/* render backward: CR/backward.cu:445-2049 (modes 0, 4, 12; kernel 0)  */
+/* render backward: CR/backward.cu:445-2049 (modes 0/4/12/14; kernel 0) */
 /* ------------------------------------------------------------------ */
 
 typedef struct {
@@ -170,7 +170,8 @@ typedef struct {
     /* 0, 4 (hybrid_features, CR/backward.cu:987-1040) or 12 (adaptive_cat
      * training, :1425-1520) with `level` the packed (total << 16) | (active
      * grid levels << 8) | per-splat levels and colors the per-splat rows,
-     * [P][hyb*F] in mode 4, [P][total*F+1] in mode 12 */
+     * [P][hyb*F] in mode 4, [P][total*F+1] in mode 12, 14 (adaptive_zero
+     * training, :1521-1590) with rows [P][hyb*F+1] */
     int render_mode;
 } or_render_bwd_args;
 
@@ -302,6 +303,35 @@ static void render_pixel_bwd(const or_render_bwd_args *A, uint32_t tile, uint32_
                     qf_backward(&G, xyz, ap, C - pgd, grad_feat + pgd, feat + pgd, A->dtable, dxyz);
                 }
                 for (int i = 0; i < pgd; i++) A->dcolors[(size_t)id * pgd + i] += grad_feat[i];
+            } else if (A->render_mode == 14) {
+                /* adaptive_zero training (CR/backward.cu:1521-1590): rows
+                 * [hyb*F | weight]; the coarse channels pass their gradient to
+                 * the row; when the weight is > 1e-6 the hl grid levels pass
+                 * weight * g to the table and grid . g to the weight.  The
+                 * blend terms use the forward's features, as in mode 12. */
+                const int hl = (A->level >> 8) & 0xFF, hyb = A->level & 0xFF;
+                const int F = A->grid.F, pgd = hyb * F;
+                const float *gf = A->colors + (size_t)id * (size_t)(pgd + 1);
+                float *dc = A->dcolors + (size_t)id * (size_t)(pgd + 1);
+                const float wt = gf[pgd];
+                for (int ch = 0; ch < C; ch++) feat[ch] = 0.0f;
+                for (int i = 0; i < pgd; i++) {
+                    feat[i] = gf[i];
+                    dc[i] += grad_feat[i];
+                }
+                float dweight = 0.0f;
+                if (hl > 0 && wt > 1e-6f) {
+                    or_grid G = A->grid;
+                    G.L = hl;
+                    float hf[64], gh[64];
+                    for (int i = 0; i < hl * F; i++) gh[i] = wt * grad_feat[pgd + i];
+                    qf_backward(&G, xyz, ap, hl * F, gh, hf, A->dtable, dxyz);
+                    for (int i = 0; i < hl * F; i++) {
+                        dweight += hf[i] * grad_feat[pgd + i];
+                        feat[pgd + i] = wt * hf[i];
+                    }
+                }
+                dc[pgd] += dweight;
             } else if (A->render_mode == 12) {
                 /* adaptive_cat training (CR/backward.cu:1425-1520): rows
                  * [total*F | weight]; the coarse hyb*F channels pass their

@@ -1,5 +1,5 @@
-"""GPU parity of render modes 4 (cat), 12 (adaptive_cat) and 13
-(adaptive_cat_fast), training and inference, against the oracle, bit for bit, on the shared small scenes:
+"""GPU parity of render modes 4 (cat), 12 (adaptive_cat), 13
+(adaptive_cat_fast) and 14 (adaptive_zero), training and inference, against the oracle, bit for bit, on the shared small scenes:
 per-splat feature rows ahead of a grid of the scene's first levels, with
 f32 and f16 tables, level_dim 2 and 4, the common-grid lookup and the
 general per-level one (smoothstep), mixed fast/slow splats in inference.
@@ -110,6 +110,27 @@ def test_adaptive_cat_fast_parity(oracle, name, infer, total, hyb, hl, interp):
         assert not r["n_contrib"][0].any()
 
 
+# (scene, inference, total levels, per-splat levels, grid levels, interp)
+AZ_CASES = [("unbounded_small", False, 16, 10, 6, 0), ("shells_small", True, 9, 5, 3, 0),
+            ("shell_small", True, 12, 4, 8, 1), ("cfg1", False, 8, 3, 5, 1)]
+
+
+@pytest.mark.parametrize("name,infer,total,hyb,hl,interp", AZ_CASES)
+def test_adaptive_zero_parity(oracle, name, infer, total, hyb, hl, interp):
+    """Render mode 14 (adaptive_zero): coarse rows, then the grid times the
+    weight; weights <= 1e-6 (training) or < 0.1 (inference) skip the grid."""
+    sc = scene(name)
+    F = sc.spec.F
+    pgd = hyb * F
+    mode = 14 | (0x100 if infer else 0)
+    print(f"[case] mode {mode:#x} {name} total={total} hyb={hyb} hl={hl} interp={interp}", flush=True)
+    rows = _rows(sc, pgd + 1, weight_col=pgd, seed=total + hyb + 2)
+    rows[::11, pgd] = 0.0
+    res = run_gpu(sc, mode, hyb, hl, total, total * F, rows, interp=interp)
+    b, r = run_oracle(oracle, sc, mode, (total << 16) | (hl << 8) | hyb, max(hl, 1), total * F, rows, interp=interp)
+    _check(res, b, r)
+
+
 # (scene, inference, total levels, per-splat levels, active grid levels, interp)
 AC_CASES = [("unbounded_small", False, 16, 10, 6, 0), ("shells_small", True, 8, 5, 3, 0),
             ("shell_small", True, 12, 4, 8, 1), ("cfg1", False, 8, 3, 5, 1)]
@@ -185,8 +206,8 @@ def test_mode_validation():
                                     channels=C)
 
     errs = (NotImplementedError, RuntimeError)
-    with pytest.raises(errs, match="render_mode 14"):
-        call(14, 1, 2, 4, 8, 8)
+    with pytest.raises(errs, match="render_mode 11"):
+        call(11, 1, 2, 4, 8, 8)
     with pytest.raises(errs, match="supported"):
         call(4 | 0x100, 1, 2, 0, 8, 2)
     with pytest.raises(errs, match="exceed total_levels"):
@@ -364,16 +385,19 @@ def test_drop_in_cat_modes_autograd(oracle):
         color13.sum().backward()
 
 
-# (scene, total levels, per-splat levels, grid levels)
-AC_BWD_CASES = [("cfg1", 8, 3, 5), ("shell_small", 12, 4, 8), ("unbounded_small", 16, 10, 6), ("cfg1", 6, 2, 0)]
+# (render mode, scene, total levels, per-splat levels, grid levels)
+AC_BWD_CASES = [(12, "cfg1", 8, 3, 5), (12, "shell_small", 12, 4, 8), (12, "unbounded_small", 16, 10, 6),
+                (12, "cfg1", 6, 2, 0), (14, "cfg1", 8, 3, 5), (14, "shell_small", 13, 4, 8),
+                (14, "unbounded_small", 16, 10, 6)]
 
 
-@pytest.mark.parametrize("name,total,hyb,gl", AC_BWD_CASES)
-def test_adaptive_cat_backward_parity(oracle, name, total, hyb, gl):
-    """nest_backward in render mode 12 (training) against the backward oracle,
-    which the CPU tests pin against float64 autograd: gradients of the rows
-    and their blend weights, the table and the geometry, within 2e-5 of each
-    array's largest entry."""
+@pytest.mark.parametrize("mode,name,total,hyb,gl", AC_BWD_CASES)
+def test_adaptive_cat_backward_parity(oracle, mode, name, total, hyb, gl):
+    """nest_backward in render modes 12 (adaptive_cat) and 14 (adaptive_zero),
+    training, against the backward oracle, which the CPU tests pin against
+    float64 autograd: gradients of the rows and their blend weights, the
+    table and the geometry, within 2e-5 of each array's largest entry.  Mode
+    14 rows include weight-0 splats, whose grid levels are skipped."""
     from nest_splat import rasterizer as rz
     sc = scene(name)
     sp = sc.spec
@@ -381,15 +405,18 @@ def test_adaptive_cat_backward_parity(oracle, name, total, hyb, gl):
     tdim = total * F
     cam = sc.cameras[0]
     W, H = cam.image_width, cam.image_height
-    print(f"[case] mode 12 backward {name} total={total} hyb={hyb} grid levels={gl}", flush=True)
-    rows = _rows(sc, tdim + 1, weight_col=tdim, seed=total + 50)
+    print(f"[case] mode {mode} backward {name} total={total} hyb={hyb} grid levels={gl}", flush=True)
+    nw = tdim if mode == 12 else hyb * F  # features ahead of the weight
+    rows = _rows(sc, nw + 1, weight_col=nw, seed=total + 50)
+    if mode == 14:
+        rows[::9, nw] = 0.0
     ap = sc.ap_level.reshape(-1).copy()
     ap[::5] = 3.0
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
     settings = rz.make_settings(H, W, cam.tanfovx, cam.tanfovy, cam.world_view_transform, cam.full_proj_transform,
                                 cam.camera_center, if_contract=sp.contract)
     grid = rz.HashGridDesc(gl, F, sp.S, sp.base_res, t(sc.table), sc.offsets, np.asarray(sp.gridrange, np.float32),
-                           render_mode=12, hybrid_levels=hyb, total_levels=total)
+                           render_mode=mode, hybrid_levels=hyb, total_levels=total)
     kw = dict(homotrans=t(sc.homotrans), ap_level=t(ap), colors_precomp=t(rows), channels=tdim)
     res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations), **kw)
     rng = np.random.default_rng(31)
@@ -405,18 +432,18 @@ def test_adaptive_cat_backward_parity(oracle, name, total, hyb, gl):
                             cam.full_proj_transform, W, H)
     b = oracle.binning(pre, W, H)
     g = oracle.make_grid(max(gl, 1), F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
-    fwd = oracle.render(pre, b, W, H, tdim, g, homotrans=sc.homotrans, ap_level=ap, colors=rows, render_mode=12,
+    fwd = oracle.render(pre, b, W, H, tdim, g, homotrans=sc.homotrans, ap_level=ap, colors=rows, render_mode=mode,
                         level=level)
     np.testing.assert_array_equal(res.color.cpu().numpy(), fwd["color"])  # same forward state
     ob = oracle.render_backward(pre, b, fwd, W, H, tdim, g, dcol, doth, homotrans=sc.homotrans.reshape(-1, 16),
-                                ap_level=ap, colors=rows, render_mode=12, level=level)
+                                ap_level=ap, colors=rows, render_mode=mode, level=level)
     pb = oracle.preprocess_backward(sc.means, sc.scales, sc.rotations, pre["radii"], pre["transmat"],
                                     cam.world_view_transform, cam.full_proj_transform, W, H, ob["dtransmat"],
                                     ob["dhomo"], ob["dnormal"], ob["dmean2D"])
     ref = dict(dmeans3D=pb["dmeans"], dmeans2D=pb["dmean2D"], dopacity=ob["dopacity"][:, None],
-               dscales=pb["dscales"], drotations=pb["drots"], drows=ob["dcolors"][:, :tdim],
-               dweight=ob["dcolors"][:, tdim], dgradsum=ob["gradsum"][:, None])
-    gpu["drows"], gpu["dweight"] = gpu["dcolors"][:, :tdim], gpu["dcolors"][:, tdim]
+               dscales=pb["dscales"], drotations=pb["drots"], drows=ob["dcolors"][:, :nw],
+               dweight=ob["dcolors"][:, nw], dgradsum=ob["gradsum"][:, None])
+    gpu["drows"], gpu["dweight"] = gpu["dcolors"][:, :nw], gpu["dcolors"][:, nw]
     if gl > 0:
         ref["dfeatures"] = ob["dtable"].reshape(gpu["dfeatures"].shape)
     vis = pre["radii"] > 0

@@ -389,3 +389,69 @@ def test_adaptive_cat_backward_matches_autograd(oracle, hyb, hl, extra, ap_cap):
         err = _rel(ours, ref)
         print(f"{name}: rel err {err:.2e}")
         assert err < TOL, (name, err)
+
+
+@pytest.mark.parametrize("hyb,hl,ap_cap", [(2, 3, True), (1, 4, False), (3, 0, False)])
+def test_adaptive_zero_backward_matches_autograd(oracle, hyb, hl, ap_cap):
+    """Render mode 14 training backward (CR/backward.cu:1521-1590): coarse rows,
+    then the grid levels times the row's weight; the gradients of the rows
+    (weight included), the table and the geometry are those of the forward.
+    A few splats carry weight 0 (their grid levels are skipped)."""
+    sc = _tiny(seed=40 + hyb)
+    sp = sc.spec
+    F = sp.F
+    total = hyb + hl + 1
+    pgd, C = hyb * F, total * F
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    ap = sc.ap_level.reshape(-1).copy()
+    if ap_cap:
+        ap[::3] = 2.0
+    rng = np.random.default_rng(hyb + hl + 5)
+    rows = rng.uniform(-1, 1, (sp.P, pgd + 1)).astype(np.float32)
+    rows[:, pgd] = rng.uniform(0.05, 0.95, sp.P).astype(np.float32)
+    rows[::7, pgd] = 0.0
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    g = oracle.make_grid(max(hl, 1), F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    level = (total << 16) | (hl << 8) | hyb
+    fwd = oracle.render(pre, b, W, H, C, g, homotrans=sc.homotrans, ap_level=ap, colors=rows, render_mode=14,
+                        level=level)
+    r2 = np.random.default_rng(19)
+    dpix = r2.standard_normal(fwd["color"].shape).astype(np.float32)
+    doth = r2.standard_normal(fwd["others"].shape).astype(np.float32)
+    homo = sc.homotrans.reshape(-1, 16).astype(np.float32)
+    gb = oracle.render_backward(pre, b, fwd, W, H, C, g, dpix, doth, homotrans=homo, ap_level=ap, colors=rows,
+                                render_mode=14, level=level)
+    assert gb["dcolors"].shape == (sp.P, pgd + 1)
+    leaf = lambda a: torch.tensor(np.asarray(a, np.float64), requires_grad=True)
+    leaves = dict(T=leaf(pre["transmat"]), xy=leaf(pre["xy"]), normal=leaf(pre["normal_opacity"][:, :3]),
+                  opacity=leaf(pre["normal_opacity"][:, 3]), homo=leaf(homo),
+                  table=leaf(sc.table.reshape(-1, sp.F)), rows=leaf(rows))
+    gd = dict(L=hl, F=F, S=sp.S, H=sp.base_res, offsets=sc.offsets, vmin=sp.gridrange[0], vmax=sp.gridrange[1],
+              hyb14=hyb)
+    color, others = TR.render_forward(oracle, pre, b, fwd, W, H, C, leaves, grid=gd, homotrans_np=homo,
+                                      ap_level=ap)
+    assert _rel(color.detach().numpy(), fwd["color"]) < 1e-4
+    loss = (color * torch.from_numpy(dpix.astype(np.float64))).sum() + \
+        (others * torch.from_numpy(doth[:7].astype(np.float64))).sum()
+    loss.backward()
+    vis = pre["radii"] > 0
+    rg = leaves["rows"].grad.numpy()
+    checks = {"dtransmat": (gb["dtransmat"], leaves["T"].grad), "dmean2D": (gb["dmean2D"][:, :2], leaves["xy"].grad),
+              "dnormal": (gb["dnormal"], leaves["normal"].grad), "dopacity": (gb["dopacity"], leaves["opacity"].grad),
+              "drows": (gb["dcolors"][:, :pgd], rg[:, :pgd])}
+    if hl > 0:
+        gh = leaves["homo"].grad.numpy()
+        checks["dhomo"] = (gb["dhomo"], gh[:, [0, 4, 8, 1, 5, 9, 3, 7, 11]])
+        checks["dtable"] = (gb["dtable"], leaves["table"].grad)
+        checks["dweight"] = (gb["dcolors"][:, pgd], rg[:, pgd])
+    for name, (ours, ref) in checks.items():
+        ref = ref.numpy() if isinstance(ref, torch.Tensor) else ref
+        if name != "dtable":
+            ours, ref = ours[vis], ref[vis]
+        assert np.abs(ref).max() > 0, name
+        err = _rel(ours, ref)
+        print(f"{name}: rel err {err:.2e}")
+        assert err < TOL, (name, err)

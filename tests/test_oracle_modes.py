@@ -292,3 +292,32 @@ def test_mode12_inference_threshold(frame):
             assert not np.any(r["color"][pgd + nf:])
         assert _same(r["others"], r0["others"])
         assert np.array_equal(r["n_contrib"], r0["n_contrib"])
+
+
+def test_mode14_adaptive_zero(frame):
+    """adaptive_zero (CR/forward.cu:1716-1830): rows [hyb*F | weight]; the
+    grid levels times the weight when it is > 1e-6 (training) or >= 0.1
+    (inference), else zero; full hits (auxiliary outputs of mode 0)."""
+    fr = frame
+    hyb, L, F = 2, fr.L, fr.F
+    pgd, nf = hyb * F, L * F
+    total = hyb + L + 1
+    tdim = total * F
+    level = (total << 16) | (L << 8) | hyb
+    r0 = fr.mode0()
+    base = np.random.default_rng(11).uniform(-1, 1, (fr.P, pgd + 1)).astype(np.float32)
+    for mode, wt, on in ((14, 1.0, True), (14, 1e-6, False), (14 | 0x100, 0.1, True),
+                         (14 | 0x100, np.nextafter(np.float32(0.1), np.float32(0)), False)):
+        rows = base.copy()
+        rows[:, pgd] = wt
+        r = fr.mode(mode, level, tdim, rows)
+        assert _same(r["color"][:pgd], fr.colour(rows[:, :pgd])["color"])
+        if on and wt == 1.0:
+            assert _same(r["color"][pgd:pgd + nf], r0["color"])
+        elif on:
+            assert _close(r["color"][pgd:pgd + nf], np.float32(wt) * r0["color"].astype(np.float64))
+        else:
+            assert not np.any(r["color"][pgd:])
+        assert not np.any(r["color"][pgd + nf:])
+        assert _same(r["others"], r0["others"])
+        assert np.array_equal(r["n_contrib"], r0["n_contrib"])

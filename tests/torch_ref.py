@@ -145,7 +145,15 @@ def render_forward(O, pre, binres, fwd, W, H, C, leaves, grid=None, beta=0.0, ho
             feat = leaves["colors"][ids][None].expand(px.shape[0], n, C)
         else:
             rows = leaves.get("rows")
-            if "hyb12" in grid:  # render mode 12: [coarse rows | blended levels | zeros], row ends with the weight
+            if "hyb14" in grid:  # render mode 14: [rows | weight * grid | zeros], row ends with the weight
+                # (the grid levels are skipped, value and gradient, when the weight is <= 1e-6)
+                fs, nf = grid["hyb14"] * grid["F"], grid["L"] * grid["F"]
+                hf = _hash_features(O, grid, leaves, ids, acc, use3d, sx32, sy32, sx, sy, homotrans_np, ap_level, nf)
+                r = rows[ids][None].expand(px.shape[0], n, fs + 1)
+                on = (r[..., fs:] > 1e-6).to(hf.dtype).detach()  # weights <= 1e-6 skip the grid
+                feat = torch.cat([r[..., :fs], on * r[..., fs:] * hf,
+                                  torch.zeros((px.shape[0], n, C - fs - nf), dtype=r.dtype)], dim=2)
+            elif "hyb12" in grid:  # render mode 12: [coarse rows | blended levels | zeros], row ends with the weight
                 fs, nf = grid["hyb12"] * grid["F"], grid["L"] * grid["F"]
                 tdim = rows.shape[1] - 1
                 hf = _hash_features(O, grid, leaves, ids, acc, use3d, sx32, sy32, sx, sy, homotrans_np, ap_level, nf)
