@@ -186,13 +186,14 @@ def time_aux_kernels(K, spec, scene, table, dev):
 
 def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_level, table, mlp, M, bg, dev,
                hyb=10):
-    """Render modes 4, 12, 13 and 14 on the benchmark frame: the first `hyb` of
+    """Render modes 4, 7, 12, 13 and 14 on the benchmark frame: the first `hyb` of
     the 16 levels become per-splat feature rows, the last 16 - hyb levels the
     grid (the scene's own tables of those levels, base resolution of level
     hyb).  Mode 12/13 rows carry a blend weight uniform in [0.15, 1): 59% of
     the splats take mode 13's inference fast path (weight > 0.5), 12% mode
-    12's (weight >= 0.9); none skip mode 14's grid (weight < 0.1).  Modes 4,
-    12 and 14 also time their backward.  Returns per mode the mean render-kernel
+    12's (weight >= 0.9); none skip mode 14's grid (weight < 0.1).  Mode 7
+    blends all 16 row levels with the grid.  Modes 4, 7, 12 and 14 also time
+    their backward.  Returns per mode the mean render-kernel
     and frame (render + MLP) milliseconds over K frames."""
     import numpy as np
     import torch
@@ -212,7 +213,7 @@ def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_lev
     rows13 = torch.from_numpy(rows).to(dev)
     rows4 = rows13[:, :hyb * F].contiguous()
     rows14 = torch.cat([rows4, rows13[:, tdim:]], dim=1).contiguous()
-    cases = {"cat(4)": (4, rows4, 0), "adaptive_cat(12) training": (12, rows13, Lt),
+    cases = {"cat(4)": (4, rows4, 0), "adaptive_add(7)": (7, rows13, Lt), "adaptive_cat(12) training": (12, rows13, Lt),
              "adaptive_cat(12) inference": (12 | 0x100, rows13, Lt),
              "adaptive_cat_fast(13) training": (13, rows13, Lt),
              "adaptive_cat_fast(13) inference": (13 | 0x100, rows13, Lt),
@@ -220,8 +221,9 @@ def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_lev
              "adaptive_zero(14) inference": (14 | 0x100, rows14, Lt)}
     res_ms = {}
     for name, (mode, rows_t, total) in cases.items():
+        # mode 7 blends all 16 levels of the row with the 6-level grid (no coarse levels)
         grid = rz.HashGridDesc(gl, F, spec.S, sub_base, sub_table, sub_offsets, np.asarray(spec.gridrange, np.float32),
-                               render_mode=mode, hybrid_levels=hyb, total_levels=total)
+                               render_mode=mode, hybrid_levels=0 if mode == 7 else hyb, total_levels=total)
 
         def frame(tm=None):
             res = rz.rasterize_forward(settings, grid, means, opac, scales, rots, homotrans=homo, ap_level=ap_level,
@@ -242,8 +244,8 @@ def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_lev
             L.timing_release(tm)
         res_ms[name] = {"render_ms": round(render_ms, 4), "frame_ms": round(frame_ms, 4)}
         log(f"[bench] {name}: render {render_ms:.3f} ms, frame {frame_ms:.3f} ms")
-        if mode in (4, 12, 14):
-            # training step of modes 4, 12 and 14: the backward of the last frame,
+        if mode in (4, 7, 12, 14):
+            # training step of modes 4, 7, 12 and 14: the backward of the last frame,
             # every grid level active, random output gradients
             res, _ = frame()
             gen = torch.Generator(device=dev).manual_seed(0)
@@ -285,9 +287,9 @@ def main():
                     help="before the frames, copy this many MiB device-to-device (a plain copy kernel of known "
                          "size whose FETCH_SIZE / WRITE_SIZE scale the render kernel's counters)")
     ap.add_argument("--modes", type=int, default=0, metavar="K",
-                    help="after the timed frames, time K frames of each other render mode (4 cat, 12 "
+                    help="after the timed frames, time K frames of each other render mode (4 cat, 7 adaptive_add, 12 "
                          "adaptive_cat, 13 adaptive_cat_fast and 14 adaptive_zero, training and inference) on the same splats: per-splat rows of the "
-                         "first 10 levels, a grid of the last 6, and report modes_ms, with K backward passes of modes 4, 12 and 14 "
+                         "first 10 levels, a grid of the last 6, and report modes_ms, with K backward passes of modes 4, 7, 12 and 14 "
                          "(not part of the metric)")
     ap.add_argument("--kernels", type=int, default=0, metavar="K",
                     help="after the timed frames, time K launches of the other hot-path kernels on their own: the RVQ "

@@ -100,6 +100,11 @@ typedef struct nest_hashgrid {
    *     the next `levels` levels from the grid, blended with the row in
    *     training; in inference a splat with weight > 0.5 takes its row
    *     without a grid lookup (CR/forward.cu:965-1101);
+   *   NEST_MODE_ADAPTIVE_ADD (7): colors_precomp rows of
+   *     total_levels*level_dim features plus a weight; every channel is
+   *     weight * row + (1 - weight) * grid, the grid's `levels` levels then
+   *     zero (hybrid_levels must be 0; CR/forward.cu:1326-1376); the
+   *     backward writes the weight's gradient times weight * (1 - weight);
    *   NEST_MODE_ADAPTIVE_CAT (12), | NEST_MODE_INFERENCE for inference: the
    *     same rows and levels; the first hybrid_levels*level_dim channels take
    *     the row unweighted, the grid levels are blended with the row in
@@ -111,7 +116,7 @@ typedef struct nest_hashgrid {
    *     weight; the grid's `levels` levels follow, times the weight, when the
    *     weight is > 1e-6 (training) or >= 0.1 (inference), else zero; full
    *     hits (CR/forward.cu:1716-1830).
-   * Modes 4, 12, 13 and 14 need level_dim 2, 4 or 8 and at most 64 channels of
+   * Modes 4, 7 and 12-14 need level_dim 2, 4 or 8 and at most 64 channels of
    * per-splat plus grid features; `levels` may be 0 there. */
   int32_t render_mode;
   uint32_t hybrid_levels;
@@ -127,6 +132,7 @@ typedef struct nest_hashgrid {
 
 #define NEST_MODE_BASELINE 0
 #define NEST_MODE_CAT 4
+#define NEST_MODE_ADAPTIVE_ADD 7
 #define NEST_MODE_ADAPTIVE_CAT 12
 #define NEST_MODE_ADAPTIVE_CAT_FAST 13
 #define NEST_MODE_ADAPTIVE_ZERO 14
@@ -258,7 +264,7 @@ int nest_forward_geometry(const nest_raster_settings *settings, const nest_splat
  * (:173-195, :388) and renderCUDAsurfelForward<C, render_mode>
  * (CR/forward.cu:639-2049, dispatch :2052-2158).  out_color channels must
  * cover the features of the mode (levels*level_dim in mode 0, plus
- * hybrid_levels*level_dim in mode 4, total_levels*level_dim in modes 12-14);
+ * hybrid_levels*level_dim in mode 4, total_levels*level_dim in modes 7, 12-14);
  * channels past them are written as zero. */
 int nest_forward_render(const nest_raster_settings *settings, const nest_hashgrid *grid,
                         const nest_splats *splats, void *geom_ws, size_t geom_bytes,
@@ -274,7 +280,8 @@ int nest_forward_render(const nest_raster_settings *settings, const nest_hashgri
  * [P, hybrid_levels*level_dim], of the grid's active levels into
  * dL_dfeatures; mode 12 in training, CR/backward.cu:1425-1520, gradients of
  * the rows and their blend weight into dL_dcolors [P, total_levels*level_dim
- * + 1]; mode 14 in training, CR/backward.cu:1521-1590, into dL_dcolors
+ * + 1], likewise mode 7, CR/backward.cu:1108-1170; mode 14 in training,
+ * CR/backward.cu:1521-1590, into dL_dcolors
  * [P, hybrid_levels*level_dim + 1]) with the Gaussian kernel:
  * renderCUDAsurfelBackward
  * (CR/backward.cu:445-2049) then

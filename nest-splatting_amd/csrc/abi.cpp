@@ -188,9 +188,11 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
   const int base_mode = gr->render_mode & 0xFF;
   const bool adaptive = base_mode == NEST_MODE_ADAPTIVE_CAT || base_mode == NEST_MODE_ADAPTIVE_CAT_FAST ||
                         base_mode == NEST_MODE_ADAPTIVE_ZERO;
-  if ((gr->render_mode & ~0x1FF) != 0 || (base_mode != NEST_MODE_BASELINE && base_mode != NEST_MODE_CAT && !adaptive) ||
+  if ((gr->render_mode & ~0x1FF) != 0 ||
+      (base_mode != NEST_MODE_BASELINE && base_mode != NEST_MODE_CAT && base_mode != NEST_MODE_ADAPTIVE_ADD &&
+       !adaptive) ||
       ((gr->render_mode & NEST_MODE_INFERENCE) && !adaptive))
-    return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: supported are 0, 4, 12, 13, 14 and 12, 13, 14 | 0x100",
+    return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: supported are 0, 4, 7, 12, 13, 14 and 12, 13, 14 | 0x100",
                 gr->render_mode);
   const bool mix = base_mode != NEST_MODE_BASELINE;
   if (mix) {
@@ -200,6 +202,8 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
     if (gr->levels > NEST_MAX_LEVELS || hyb > NEST_MAX_LEVELS || gr->total_levels > NEST_MAX_LEVELS)
       return fail(NEST_ERR_UNSUPPORTED, "levels, hybrid_levels and total_levels must be <= %d", NEST_MAX_LEVELS);
     uint32_t feat = 0;
+    if (base_mode == NEST_MODE_ADAPTIVE_ADD && hyb != 0)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode 7 has no per-splat coarse levels (hybrid_levels must be 0)");
     if (base_mode == NEST_MODE_CAT) {
       feat = (hyb + gr->levels) * F;
     } else {
@@ -215,7 +219,7 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
                   gr->render_mode, feat);
     if (sp->P > 0) {
       if (!sp->homotrans) return fail(NEST_ERR_INVALID_ARGUMENT, "homotrans is required in render_mode %d", gr->render_mode);
-      if (!sp->colors_precomp && (adaptive || hyb > 0))
+      if (!sp->colors_precomp && (adaptive || base_mode == NEST_MODE_ADAPTIVE_ADD || hyb > 0))
         return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode %d needs the per-splat features in colors_precomp",
                     gr->render_mode);
       // the render queue packs the splat id into 25 bits
@@ -463,6 +467,16 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     if ((gr->render_mode & 0xFF) == NEST_MODE_CAT) {
       rp.cstride = rp.pgd;
       rp.nrow = rp.pgd;
+    } else if ((gr->render_mode & 0xFF) == NEST_MODE_ADAPTIVE_ADD) {
+      // mode 7 (CR/forward.cu:1326-1376): rows [total*F | weight], every level
+      // weight * row + (1 - weight) * grid, the grid zero past its levels
+      const int tdim = (int)gr->total_levels * F;
+      rp.cstride = tdim + 1;
+      rp.nrow = tdim;
+      rp.wslot = tdim;
+      rp.blend = 1;
+      rp.nfast = gr->total_levels;
+      rp.nblend = gr->total_levels;
     } else if ((gr->render_mode & 0xFF) == NEST_MODE_ADAPTIVE_ZERO) {
       // mode 14 (CR/forward.cu:1716-1830): rows [pgd | weight], grid * weight
       rp.cstride = rp.pgd + 1;
@@ -485,6 +499,7 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
       rp.m13 = m13 ? 1 : 0;
       rp.wcoarse = (m13 && !rp.infer) ? 1 : 0;
       rp.nfast = gr->total_levels - gr->hybrid_levels;
+      rp.nblend = gr->levels;
       // inference takes the row when weight > 0.5 (mode 13) or >= 0.9 (mode 12)
       if (rp.infer) rp.fthr = m13 ? 0.5f : std::nextafter(0.9f, 0.0f);
     }
@@ -727,12 +742,15 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   if (!io || io->struct_size != sizeof(nest_backward_io))
     return fail(NEST_ERR_INVALID_ARGUMENT, "nest_backward_io missing or struct_size mismatch");
   if (gr->render_mode != NEST_MODE_BASELINE && gr->render_mode != NEST_MODE_CAT &&
-      gr->render_mode != NEST_MODE_ADAPTIVE_CAT && gr->render_mode != NEST_MODE_ADAPTIVE_ZERO)
+      gr->render_mode != NEST_MODE_ADAPTIVE_ADD && gr->render_mode != NEST_MODE_ADAPTIVE_CAT &&
+      gr->render_mode != NEST_MODE_ADAPTIVE_ZERO)
     return fail(NEST_ERR_UNSUPPORTED,
-                "backward: render_mode %d is forward-only here (modes 0, 4, 12 and 14 without the inference flag "
+                "backward: render_mode %d is forward-only here (modes 0, 4, 7, 12 and 14 without the inference flag "
                 "have a backward)", gr->render_mode);
   const bool cat = gr->render_mode == NEST_MODE_CAT;
-  const bool acat = gr->render_mode == NEST_MODE_ADAPTIVE_CAT;
+  // mode 7 is mode 12 without coarse levels, every level blended
+  const bool aadd = gr->render_mode == NEST_MODE_ADAPTIVE_ADD;
+  const bool acat = gr->render_mode == NEST_MODE_ADAPTIVE_CAT || aadd;
   const bool azero = gr->render_mode == NEST_MODE_ADAPTIVE_ZERO;
   const int C = io->channels;
   if (C < 1 || C > 64) return fail(NEST_ERR_UNSUPPORTED, "backward: channels must be in [1, 64] (got %d)", C);
@@ -824,7 +842,8 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   rp.cstride = dcol_width;
   rp.wslot = acat ? tdim : azero ? pgd : -1;
   rp.azero = azero ? 1 : 0;
-  rp.nfine = (acat || azero) ? (int)(gr->levels * gr->level_dim) : 0;
+  rp.nfine = aadd ? tdim : (acat || azero) ? (int)(gr->levels * gr->level_dim) : 0;
+  rp.wsig = aadd ? 1 : 0;
   rp.beta = rs->beta;
   rp.ranges = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_RANGES]);
   rp.tile_order = reinterpret_cast<const uint32_t*>(im + io_[NEST_IMG_TILE_ORDER]);

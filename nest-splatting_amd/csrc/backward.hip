@@ -436,6 +436,7 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
           } else {
             dot = rdot + wt * fdot + (1.0f - wt) * hdot;
             fdot = wgt * (fdot - hdot);  // dL/dweight
+            if (p.wsig) fdot = fdot * wt * (1.0f - wt);  // mode 7: dL/dlogit of weight = sigmoid(logit)
           }
         }
       }

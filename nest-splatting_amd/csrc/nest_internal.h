@@ -133,6 +133,8 @@ struct RenderParams {
   float fthr;                 // a hit is fast (skips the grid) when (weight > fthr) != fneg;
   int fneg;                   // fthr = +inf: no fast hits
   uint32_t nfast;             // levels of the row past pgd that a fast hit takes
+  uint32_t nblend;            // levels past pgd a blend hit covers: the grid's in modes 12, 13;
+                              // the row's in mode 7 (the grid zero past its levels)
 };
 
 // Host-side launchers (defined in the .hip files).  Each returns the
@@ -195,6 +197,7 @@ struct RenderBwdParams {
   int cstride;                // render mode 12: floats per row (total*F + 1)
   int wslot;                  // render modes 12, 14: index of the blend weight in a row, else -1
   int azero;                  // render mode 14: grid levels take grid * weight, no row part
+  int wsig;                   // render mode 7: the weight slot gets dL/dweight * w * (1 - w)
   int nfine;                  // render modes 12, 14: grid channels after the coarse ones (levels * F)
   GridParams grid;
 };

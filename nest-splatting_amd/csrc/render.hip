@@ -261,7 +261,7 @@ __device__ __forceinline__ void drain_compact_mix(const RenderParams& p, nest_i3
     row = p.colors + (size_t)(meta >> 7) * (uint32_t)p.cstride;
     if (p.wslot >= 0) wt = row[p.wslot];
     row += p.pgd;
-    nfeat = fast ? p.nfast : (p.blend ? g.L : nhash);
+    nfeat = fast ? p.nfast : (p.blend ? p.nblend : nhash);
   }
   const bool rows = fast || p.blend != 0;
   float wd[kQueue];
@@ -362,7 +362,7 @@ __device__ __forceinline__ void drain_mixed(const RenderParams& p, nest_i32x4 rs
     const bool fast = (meta & 64u) != 0u;
     const float* row = p.colors + (size_t)(meta >> 7) * (uint32_t)p.cstride;
     const float wt = p.wslot >= 0 ? row[p.wslot] : 0.0f;
-    const uint32_t nfeat = fast ? p.nfast : (p.blend ? g.L : nhash);
+    const uint32_t nfeat = fast ? p.nfast : (p.blend ? p.nblend : nhash);
     row += p.pgd;
     const float u[3] = {e.x, e.y, e.z};
     const LevelQuadPtr lqb = (LevelQuadPtr)g.lq;

@@ -14,7 +14,8 @@ precomputed per-splat colours or RGB evaluated from SH coefficients
 (degree <= 3) in preprocess.  Render modes 4 ("cat": per-splat features
 of the coarse levels ahead of a grid of the fine ones), 12 ("adaptive_cat",
 blended with the grid by a per-splat weight) and 14 ("adaptive_zero", the
-grid scaled by the weight) forward and backward, 12 | 0x100, 14 | 0x100 and
+grid scaled by the weight) and 7 ("adaptive_add", every level blended)
+forward and backward, 12 | 0x100, 14 | 0x100 and
 13 ("adaptive_cat_fast") with or without the inference flag 0x100 forward,
 with
 the reference's packed L (total << 16 | grid levels << 8 | per-splat
@@ -75,7 +76,7 @@ def _cat_hash_levels(offsets17: np.ndarray) -> int:
 
 
 def _mixed_grid(hs, render_mode, level, features, offsets, gridrange):
-    """HashGridDesc of render modes 4, 12, 13 and 14 from the reference's packed
+    """HashGridDesc of render modes 4, 7, 12, 13 and 14 from the reference's packed
     level argument: (total << 16) | (grid levels << 8) | per-splat levels
     (GR:224-226, :395-396; CR/forward.cu:744-767, :971-973, :1228)."""
     base_mode = render_mode & 0xFF
@@ -103,9 +104,10 @@ class _RasterizeGaussians(torch.autograd.Function):
                 ap_level, features, offsets, gridrange, features_diffuse, offsets_diffuse, gridrange_diffuse,
                 raster_settings, hashgrid_settings, render_mode, shapes, kernel_type):
         base_mode = render_mode & 0xFF
-        if base_mode not in (0, 4, 12, 13, 14) or (render_mode & ~0x1FF) or \
+        if base_mode not in (0, 4, 7, 12, 13, 14) or (render_mode & ~0x1FF) or \
                 ((render_mode & 0x100) and base_mode not in (12, 13, 14)):
-            raise NotImplementedError(f"render_mode {render_mode}: implemented are 0 (baseline), 4 (cat) and "
+            raise NotImplementedError(f"render_mode {render_mode}: implemented are 0 (baseline), 4 (cat), "
+                                      f"7 (adaptive_add) and "
                                       f"12 / 13 / 14 (adaptive_cat / adaptive_cat_fast / adaptive_zero, | 0x100 "
                                       f"inference)")
         if kernel_type != 0:
@@ -118,7 +120,7 @@ class _RasterizeGaussians(torch.autograd.Function):
             raise NotImplementedError("record_transmittance=True is not implemented")
         C = _channels(hashgrid_settings)
         level = int(hashgrid_settings.L)
-        if base_mode in (4, 12, 14) and level == 0:
+        if base_mode in (4, 7, 12, 14) and level == 0:
             base_mode = render_mode = 0  # level 0 is the colour path in every mode but 13 (CR/forward.cu:1091)
         if base_mode != 0:
             grid = _mixed_grid(hashgrid_settings, render_mode, level, features, offsets, gridrange)
@@ -175,9 +177,9 @@ class _RasterizeGaussians(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out_color, grad_radii, grad_depth, grad_0, grad_1):
-        if ctx.render_mode not in (0, 4, 12, 14):
+        if ctx.render_mode not in (0, 4, 7, 12, 14):
             raise NotImplementedError(f"render_mode {ctx.render_mode} is forward-only here; "
-                                      f"the backward covers modes 0, 4, 12 and 14 (training)")
+                                      f"the backward covers modes 0, 4, 7, 12 and 14 (training)")
         means3D, opacities, scales, rotations = ctx.saved_tensors
         fw = ctx.fw
         g = _rz.rasterize_backward(fw["settings"], fw["grid"], fw["res"], means3D.detach(), opacities.detach(),

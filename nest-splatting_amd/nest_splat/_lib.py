@@ -60,6 +60,7 @@ class HashGrid(ct.Structure):
 
 MODE_BASELINE = 0
 MODE_CAT = 4
+MODE_ADAPTIVE_ADD = 7
 MODE_ADAPTIVE_CAT = 12
 MODE_ADAPTIVE_CAT_FAST = 13
 MODE_ADAPTIVE_ZERO = 14

@@ -48,7 +48,7 @@ class HashGridDesc:
     gridrange: np.ndarray
     align_corners: bool = False
     interpolation: int = 0
-    # render_mode 4 / 12 / 13 / 14 (| MODE_INFERENCE): per-splat feature levels ahead
+    # render_mode 4 / 7 / 12 / 13 / 14 (| MODE_INFERENCE): per-splat feature levels ahead
     # of the grid's `levels` (hybrid_levels) and, for modes 12/13, the levels of a
     # splat's feature row (total_levels; the row ends with the blend weight)
     render_mode: int = 0
@@ -65,7 +65,7 @@ class HashGridDesc:
             return self.hybrid_levels * self.level_dim
         if base == L.MODE_ADAPTIVE_ZERO:
             return self.hybrid_levels * self.level_dim + 1
-        if base in (L.MODE_ADAPTIVE_CAT, L.MODE_ADAPTIVE_CAT_FAST):
+        if base in (L.MODE_ADAPTIVE_ADD, L.MODE_ADAPTIVE_CAT, L.MODE_ADAPTIVE_CAT_FAST):
             return self.total_levels * self.level_dim + 1
         return channels
 

@@ -629,7 +629,8 @@ typedef struct {
      * 4 per-splat features then hash features (level's low byte = per-splat
      * levels), 13 adaptive_cat_fast (level = total << 16 | hash << 8 | per-splat
      * levels, colors rows of total*F+1 floats, bit 8 of render_mode =
-     * inference), 12 adaptive_cat (same level and rows), 14 adaptive_zero
+     * inference), 7 adaptive_add (level = total << 16 | hash << 8, rows of
+     * total*F+1 floats), 12 adaptive_cat (same level and rows as 13), 14 adaptive_zero
      * (same level, rows of hyb*F+1 floats).  Other values are not
      * restated. */
     int render_mode;
@@ -764,7 +765,24 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
             hit_xyz(A->homotrans + 16 * (size_t)id, use3d, sx, sy, xyz);
             pos_x += w * xyz[0]; pos_y += w * xyz[1]; pos_z += w * xyz[2];
             uint32_t ap = f2u_sat(floorf(A->ap_level[id]));
-            if ((A->render_mode & 0xFF) == 14) {
+            if ((A->render_mode & 0xFF) == 7) {
+                /* adaptive_add (forward.cu:1326-1376): rows [total*F | weight];
+                 * every channel is weight * row + (1 - weight) * grid, the grid
+                 * being zero past its hl levels; full hits. */
+                const int total = (A->level >> 16) & 0xFF, hl = (A->level >> 8) & 0xFF;
+                const int F = A->grid.F, tdim = total * F;
+                const float *gf = A->colors + (size_t)id * (size_t)(tdim + 1);
+                const float wt = gf[tdim], iw = 1.0f - wt;
+                float hf[64];
+                for (int i = 0; i < 64; i++) hf[i] = 0.0f;
+                if (hl > 0) {
+                    or_grid G = A->grid;
+                    G.L = hl;
+                    or_query_feature(&G, xyz, ap, 64, hf);
+                }
+                for (int c = 0; c < C; c++) feat_scratch[c] = 0.0f;
+                for (int i = 0; i < tdim && i < C && i < 64; i++) feat_scratch[i] = fmaf(wt, gf[i], iw * hf[i]);
+            } else if ((A->render_mode & 0xFF) == 14) {
                 /* adaptive_zero (forward.cu:1716-1830): rows [hyb*F features |
                  * weight]; the first hyb*F channels from the row, the next hl
                  * grid levels times the weight when the weight is > 1e-6

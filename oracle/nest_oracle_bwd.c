@@ -136,7 +136,7 @@ static void qf_backward(const or_grid *G, const float xyz[3], uint32_t ap, int C
 }
 
 /* ------------------------------------------------------------------ */
-/* render backward: CR/backward.cu:445-2049 (modes 0/4/12/14; kernel 0) */
+/* render backward: CR/backward.cu:445-2049 (modes 0/4/7/12/14; kernel 0) */
 /* ------------------------------------------------------------------ */
 
 typedef struct {
@@ -303,6 +303,34 @@ static void render_pixel_bwd(const or_render_bwd_args *A, uint32_t tile, uint32_
                     qf_backward(&G, xyz, ap, C - pgd, grad_feat + pgd, feat + pgd, A->dtable, dxyz);
                 }
                 for (int i = 0; i < pgd; i++) A->dcolors[(size_t)id * pgd + i] += grad_feat[i];
+            } else if (A->render_mode == 7) {
+                /* adaptive_add (CR/backward.cu:1108-1170): rows [total*F |
+                 * weight]; each channel passes weight * g to the row and
+                 * (1 - weight) * g to the grid (hl levels); the weight's slot
+                 * receives sum (row - grid) . g times weight * (1 - weight), the
+                 * gradient of the logit the weight is a sigmoid of.  The blend
+                 * terms use the forward's features. */
+                const int total = (A->level >> 16) & 0xFF, hl = (A->level >> 8) & 0xFF;
+                const int F = A->grid.F, tdim = total * F;
+                const float *gf = A->colors + (size_t)id * (size_t)(tdim + 1);
+                float *dc = A->dcolors + (size_t)id * (size_t)(tdim + 1);
+                const float wt = gf[tdim], iw = 1.0f - wt;
+                float hf[64], gh[64];
+                for (int i = 0; i < 64; i++) hf[i] = 0.0f;
+                if (hl > 0) {
+                    or_grid G = A->grid;
+                    G.L = hl;
+                    for (int i = 0; i < hl * F; i++) gh[i] = iw * grad_feat[i];
+                    qf_backward(&G, xyz, ap, hl * F, gh, hf, A->dtable, dxyz);
+                }
+                for (int ch = 0; ch < C; ch++) feat[ch] = 0.0f;
+                float dweight = 0.0f;
+                for (int i = 0; i < tdim; i++) {
+                    dc[i] += wt * grad_feat[i];
+                    dweight += grad_feat[i] * (gf[i] - hf[i]);
+                    feat[i] = fmaf(wt, gf[i], iw * hf[i]);
+                }
+                dc[tdim] += dweight * wt * iw;
             } else if (A->render_mode == 14) {
                 /* adaptive_zero training (CR/backward.cu:1521-1590): rows
                  * [hyb*F | weight]; the coarse channels pass their gradient to

@@ -199,8 +199,8 @@ def make_grid(L, F, S, H, offsets, table, gridrange, contract=False, align_corne
 def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_level=None, colors=None,
            beta=0.0, max_intersections=0, row_stride=1, row_phase=0, threads=0, render_mode=0, level=None):
     """renderCUDAsurfelForward for every pixel.  render_mode 0 (grid levels
-    grid.L, or the colour path without a grid), 4, 12, 13 or 14 (bit 8:
-    inference); for modes 4, 12, 13 and 14, level is the reference's packed level argument
+    grid.L, or the colour path without a grid), 4, 7, 12, 13 or 14 (bit 8:
+    inference); for modes 4, 7, 12, 13 and 14, level is the reference's packed level argument
     (total << 16 | hash levels << 8 | per-splat levels) and colors the
     per-splat feature rows."""
     HW = W * H
@@ -241,19 +241,19 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
 
 def render_backward(pre, binres, fwd, W, H, C, grid: Optional[OrGrid], dL_dpix, dL_dothers, homotrans=None,
                     ap_level=None, colors=None, beta=0.0, render_mode=0, level=None):
-    """renderCUDAsurfelBackward (modes 0, 4, 12 and 14) for every pixel, given the
+    """renderCUDAsurfelBackward (modes 0, 4, 7, 12 and 14) for every pixel, given the
     forward's final_T / n_contrib (fwd = render(...)'s result).  Returns the
     per-splat gradients (dtransmat [P,9], dhomo [P,9], dmean2D [P,3],
     dnormal [P,3], dopacity [P], dcolors [P,C], or [P,hyb*F] in mode 4,
-    [P,total*F+1] in mode 12, [P,hyb*F+1] in mode 14, gradsum [P]) and
-    dtable [rows, F].  Modes 4, 12 and 14 take the packed level
+    [P,total*F+1] in modes 7 and 12, [P,hyb*F+1] in mode 14, gradsum [P])
+    and dtable [rows, F].  Modes 4, 7, 12 and 14 take the packed level
     (total << 16) | (active grid levels << 8) | per-splat levels and the
     per-splat rows as colors."""
     P = pre["radii"].shape[0]
     rows = 0 if grid is None else grid._keep[1].shape[0]
     F = 1 if grid is None else grid.F
-    if render_mode not in (0, 4, 12, 14) or (render_mode != 0 and (grid is None or level is None)):
-        raise ValueError(f"render_backward: render_mode {render_mode} needs mode 0, or mode 4, 12 or 14 with a grid "
+    if render_mode not in (0, 4, 7, 12, 14) or (render_mode != 0 and (grid is None or level is None)):
+        raise ValueError(f"render_backward: render_mode {render_mode} needs mode 0, or mode 4, 7, 12 or 14 with a grid "
                          f"and level")
     if render_mode == 0:
         dcol = C

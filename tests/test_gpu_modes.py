@@ -1,5 +1,5 @@
-"""GPU parity of render modes 4 (cat), 12 (adaptive_cat), 13
-(adaptive_cat_fast) and 14 (adaptive_zero), training and inference, against the oracle, bit for bit, on the shared small scenes:
+"""GPU parity of render modes 4 (cat), 7 (adaptive_add), 12 (adaptive_cat),
+13 (adaptive_cat_fast) and 14 (adaptive_zero), training and inference, against the oracle, bit for bit, on the shared small scenes:
 per-splat feature rows ahead of a grid of the scene's first levels, with
 f32 and f16 tables, level_dim 2 and 4, the common-grid lookup and the
 general per-level one (smoothstep), mixed fast/slow splats in inference.
@@ -108,6 +108,23 @@ def test_adaptive_cat_fast_parity(oracle, name, infer, total, hyb, hl, interp):
     _check(res, b, r)
     if infer:
         assert not r["n_contrib"][0].any()
+
+
+# (scene, total levels, grid levels, interp); f32 and f16 tables
+AA_CASES = [("unbounded_small", 16, 6, 0), ("shells_small", 8, 5, 0), ("shell_small", 12, 8, 1), ("cfg1", 8, 8, 0)]
+
+
+@pytest.mark.parametrize("name,total,hl,interp", AA_CASES)
+def test_adaptive_add_parity(oracle, name, total, hl, interp):
+    """Render mode 7 (adaptive_add): every channel weight * row + (1 - weight)
+    * grid, the grid zero past its levels; full hits."""
+    sc = scene(name)
+    tdim = total * sc.spec.F
+    print(f"[case] mode 7 {name} total={total} hl={hl} interp={interp}", flush=True)
+    rows = _rows(sc, tdim + 1, weight_col=tdim, seed=total + hl + 3)
+    res = run_gpu(sc, 7, 0, hl, total, tdim, rows, interp=interp)
+    b, r = run_oracle(oracle, sc, 7, (total << 16) | (hl << 8), max(hl, 1), tdim, rows, interp=interp)
+    _check(res, b, r)
 
 
 # (scene, inference, total levels, per-splat levels, grid levels, interp)
@@ -388,13 +405,13 @@ def test_drop_in_cat_modes_autograd(oracle):
 # (render mode, scene, total levels, per-splat levels, grid levels)
 AC_BWD_CASES = [(12, "cfg1", 8, 3, 5), (12, "shell_small", 12, 4, 8), (12, "unbounded_small", 16, 10, 6),
                 (12, "cfg1", 6, 2, 0), (14, "cfg1", 8, 3, 5), (14, "shell_small", 13, 4, 8),
-                (14, "unbounded_small", 16, 10, 6)]
+                (14, "unbounded_small", 16, 10, 6), (7, "cfg1", 8, 0, 5), (7, "unbounded_small", 16, 0, 6)]
 
 
 @pytest.mark.parametrize("mode,name,total,hyb,gl", AC_BWD_CASES)
 def test_adaptive_cat_backward_parity(oracle, mode, name, total, hyb, gl):
-    """nest_backward in render modes 12 (adaptive_cat) and 14 (adaptive_zero),
-    training, against the backward oracle, which the CPU tests pin against
+    """nest_backward in render modes 7 (adaptive_add), 12 (adaptive_cat) and
+    14 (adaptive_zero), training, against the backward oracle, which the CPU tests pin against
     float64 autograd: gradients of the rows and their blend weights, the
     table and the geometry, within 2e-5 of each array's largest entry.  Mode
     14 rows include weight-0 splats, whose grid levels are skipped."""
@@ -406,7 +423,7 @@ def test_adaptive_cat_backward_parity(oracle, mode, name, total, hyb, gl):
     cam = sc.cameras[0]
     W, H = cam.image_width, cam.image_height
     print(f"[case] mode {mode} backward {name} total={total} hyb={hyb} grid levels={gl}", flush=True)
-    nw = tdim if mode == 12 else hyb * F  # features ahead of the weight
+    nw = hyb * F if mode == 14 else tdim  # features ahead of the weight
     rows = _rows(sc, nw + 1, weight_col=nw, seed=total + 50)
     if mode == 14:
         rows[::9, nw] = 0.0

@@ -455,3 +455,66 @@ def test_adaptive_zero_backward_matches_autograd(oracle, hyb, hl, ap_cap):
         err = _rel(ours, ref)
         print(f"{name}: rel err {err:.2e}")
         assert err < TOL, (name, err)
+
+
+@pytest.mark.parametrize("hl,extra,ap_cap", [(3, 2, True), (4, 0, False)])
+def test_adaptive_add_backward_matches_autograd(oracle, hl, extra, ap_cap):
+    """Render mode 7 backward (CR/backward.cu:1108-1170): weight * row +
+    (1 - weight) * grid over all total*F channels.  The rows' and the grid's
+    gradients are the forward's; the weight slot holds the gradient times
+    weight * (1 - weight), the reference's gradient of the logit whose
+    sigmoid the weight is."""
+    sc = _tiny(seed=50 + hl)
+    sp = sc.spec
+    F = sp.F
+    total = hl + extra
+    tdim = total * F
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    ap = sc.ap_level.reshape(-1).copy()
+    if ap_cap:
+        ap[::3] = 2.0
+    rng = np.random.default_rng(hl + 70)
+    rows = rng.uniform(-1, 1, (sp.P, tdim + 1)).astype(np.float32)
+    rows[:, tdim] = rng.uniform(0.05, 0.95, sp.P).astype(np.float32)
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    g = oracle.make_grid(hl, F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    level = (total << 16) | (hl << 8)
+    fwd = oracle.render(pre, b, W, H, tdim, g, homotrans=sc.homotrans, ap_level=ap, colors=rows, render_mode=7,
+                        level=level)
+    r2 = np.random.default_rng(23)
+    dpix = r2.standard_normal(fwd["color"].shape).astype(np.float32)
+    doth = r2.standard_normal(fwd["others"].shape).astype(np.float32)
+    homo = sc.homotrans.reshape(-1, 16).astype(np.float32)
+    gb = oracle.render_backward(pre, b, fwd, W, H, tdim, g, dpix, doth, homotrans=homo, ap_level=ap, colors=rows,
+                                render_mode=7, level=level)
+    leaf = lambda a: torch.tensor(np.asarray(a, np.float64), requires_grad=True)
+    leaves = dict(T=leaf(pre["transmat"]), xy=leaf(pre["xy"]), normal=leaf(pre["normal_opacity"][:, :3]),
+                  opacity=leaf(pre["normal_opacity"][:, 3]), homo=leaf(homo),
+                  table=leaf(sc.table.reshape(-1, sp.F)), rows=leaf(rows))
+    gd = dict(L=hl, F=F, S=sp.S, H=sp.base_res, offsets=sc.offsets, vmin=sp.gridrange[0], vmax=sp.gridrange[1],
+              hyb12=0, nblend=tdim)
+    color, others = TR.render_forward(oracle, pre, b, fwd, W, H, tdim, leaves, grid=gd, homotrans_np=homo,
+                                      ap_level=ap)
+    assert _rel(color.detach().numpy(), fwd["color"]) < 1e-4
+    loss = (color * torch.from_numpy(dpix.astype(np.float64))).sum() + \
+        (others * torch.from_numpy(doth[:7].astype(np.float64))).sum()
+    loss.backward()
+    vis = pre["radii"] > 0
+    rg = leaves["rows"].grad.numpy()
+    w = rows[:, tdim].astype(np.float64)
+    gh = leaves["homo"].grad.numpy()
+    checks = {"dtransmat": (gb["dtransmat"], leaves["T"].grad), "dopacity": (gb["dopacity"], leaves["opacity"].grad),
+              "drows": (gb["dcolors"][:, :tdim], rg[:, :tdim]), "dtable": (gb["dtable"], leaves["table"].grad),
+              "dhomo": (gb["dhomo"], gh[:, [0, 4, 8, 1, 5, 9, 3, 7, 11]]),
+              "dlogit": (gb["dcolors"][:, tdim], rg[:, tdim] * w * (1.0 - w))}
+    for name, (ours, ref) in checks.items():
+        ref = ref.numpy() if isinstance(ref, torch.Tensor) else ref
+        if name != "dtable":
+            ours, ref = ours[vis], ref[vis]
+        assert np.abs(ref).max() > 0, name
+        err = _rel(ours, ref)
+        print(f"{name}: rel err {err:.2e}")
+        assert err < TOL, (name, err)

@@ -321,3 +321,22 @@ def test_mode14_adaptive_zero(frame):
         assert not np.any(r["color"][pgd + nf:])
         assert _same(r["others"], r0["others"])
         assert np.array_equal(r["n_contrib"], r0["n_contrib"])
+
+
+@pytest.mark.parametrize("t", [1.0, 0.0])
+def test_mode7_adaptive_add_weight_extremes(frame, t):
+    """adaptive_add (CR/forward.cu:1326-1376): every channel is
+    weight * row + (1 - weight) * grid, the grid zero past its levels; full
+    hits."""
+    fr = frame
+    rows, total, tdim = _rows13(fr, 0, 2, t)
+    nf = fr.L * fr.F
+    r = fr.mode(7, (total << 16) | (fr.L << 8), tdim, rows)
+    r0 = fr.mode0()
+    if t == 1.0:
+        assert _same(r["color"], fr.colour(rows[:, :tdim])["color"])
+    else:
+        assert _same(r["color"][:nf], r0["color"])
+        assert not np.any(r["color"][nf:])
+    assert _same(r["others"], r0["others"])
+    assert np.array_equal(r["n_contrib"], r0["n_contrib"])

@@ -159,8 +159,10 @@ def render_forward(O, pre, binres, fwd, W, H, C, leaves, grid=None, beta=0.0, ho
                 hf = _hash_features(O, grid, leaves, ids, acc, use3d, sx32, sy32, sx, sy, homotrans_np, ap_level, nf)
                 r = rows[ids][None].expand(px.shape[0], n, tdim + 1)
                 wt = r[..., tdim:]
-                feat = torch.cat([r[..., :fs], wt * r[..., fs:fs + nf] + (1.0 - wt) * hf,
-                                  torch.zeros_like(r[..., :C - fs - nf])], dim=2)
+                nb = grid.get("nblend", nf)  # render mode 7 blends every channel, the grid zero past its levels
+                hf = torch.cat([hf, torch.zeros_like(r[..., :nb - nf])], dim=2)
+                feat = torch.cat([r[..., :fs], wt * r[..., fs:fs + nb] + (1.0 - wt) * hf,
+                                  torch.zeros_like(r[..., :C - fs - nb])], dim=2)
             else:
                 pgd = 0 if rows is None else rows.shape[1]
                 feat = _hash_features(O, grid, leaves, ids, acc, use3d, sx32, sy32, sx, sy, homotrans_np, ap_level,
