@@ -280,7 +280,7 @@ int nest_forward_render(const nest_raster_settings *settings, const nest_hashgri
  * [P, hybrid_levels*level_dim], of the grid's active levels into
  * dL_dfeatures; mode 12 in training, CR/backward.cu:1425-1520, gradients of
  * the rows and their blend weight into dL_dcolors [P, total_levels*level_dim
- * + 1], likewise mode 7, CR/backward.cu:1108-1170; mode 14 in training,
+ * + 1], likewise mode 7, CR/backward.cu:1108-1189; mode 14 in training,
  * CR/backward.cu:1521-1590, into dL_dcolors
  * [P, hybrid_levels*level_dim + 1]) with the Gaussian kernel:
  * renderCUDAsurfelBackward

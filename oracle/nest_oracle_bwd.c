@@ -304,7 +304,7 @@ static void render_pixel_bwd(const or_render_bwd_args *A, uint32_t tile, uint32_
                 }
                 for (int i = 0; i < pgd; i++) A->dcolors[(size_t)id * pgd + i] += grad_feat[i];
             } else if (A->render_mode == 7) {
-                /* adaptive_add (CR/backward.cu:1108-1170): rows [total*F |
+                /* adaptive_add (CR/backward.cu:1108-1189): rows [total*F |
                  * weight]; each channel passes weight * g to the row and
                  * (1 - weight) * g to the grid (hl levels); the weight's slot
                  * receives sum (row - grid) . g times weight * (1 - weight), the

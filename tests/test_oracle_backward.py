@@ -459,7 +459,7 @@ def test_adaptive_zero_backward_matches_autograd(oracle, hyb, hl, ap_cap):
 
 @pytest.mark.parametrize("hl,extra,ap_cap", [(3, 2, True), (4, 0, False)])
 def test_adaptive_add_backward_matches_autograd(oracle, hl, extra, ap_cap):
-    """Render mode 7 backward (CR/backward.cu:1108-1170): weight * row +
+    """Render mode 7 backward (CR/backward.cu:1108-1189): weight * row +
     (1 - weight) * grid over all total*F channels.  The rows' and the grid's
     gradients are the forward's; the weight slot holds the gradient times
     weight * (1 - weight), the reference's gradient of the logit whose
