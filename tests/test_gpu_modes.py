@@ -233,6 +233,19 @@ def test_mode_validation():
         call(4, 2, 4, 0, 10, 4)
     with pytest.raises(errs, match="<= 32"):
         call(13, 1, 2, 40, 80, 81)
+    with pytest.raises(errs, match="hybrid_levels must be 0"):
+        call(7, 1, 2, 4, 8, 9)
+    # modes without a backward in the reference: 13 and the inference flag
+    for mode in (13, 12 | 0x100, 14 | 0x100):
+        grid = rz.HashGridDesc(2, sp.F, sp.S, sp.base_res, t(sc.table), sc.offsets,
+                               np.asarray(sp.gridrange, np.float32), render_mode=mode, hybrid_levels=1,
+                               total_levels=4)
+        rows = t(np.zeros((sp.P, grid.row_width(8)), np.float32))
+        kw = dict(homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), colors_precomp=rows, channels=8)
+        res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations), **kw)
+        with pytest.raises(errs, match="forward-only"):
+            rz.rasterize_backward(settings, grid, res, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
+                                  None, None, **kw)
 
 
 # (scene, per-splat levels, grid levels, active grid levels): level_dim 2 and
