@@ -34,6 +34,11 @@ def test_exports_match_header():
     src = open(os.path.join(ROOT, "include", "nest_splat.h")).read()
     header_version = int(re.search(r"#define NEST_ABI_VERSION (\d+)", src).group(1))
     assert lib.nest_abi_version() == header_version == L.ABI_VERSION
+    # render-mode constants: the header's values are the Python side's
+    modes = dict(re.findall(r"#define NEST_(MODE_\w+) (0x[0-9A-Fa-f]+|\d+)", src))
+    assert len(modes) >= 7
+    for name, value in modes.items():
+        assert getattr(L, name) == int(value, 0), name
 
 
 def test_struct_sizes_match_c_layout():
