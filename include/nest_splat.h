@@ -244,6 +244,14 @@ int nest_binning_layout(int64_t num_rendered, size_t offsets[NEST_BIN_FIELDS], s
 #define NEST_IMG_FIELDS 5
 int nest_image_layout(int32_t width, int32_t height, size_t offsets[NEST_IMG_FIELDS], size_t *total_bytes);
 
+/* Per-level constants of the hash grid as the lookups use them, for the
+ * grid's `levels` levels: scale = exp2(l * S) * H - 1 (float), resolution =
+ * ceil(scale) + 1, hashed = 1 when the level indexes by fast_hash (the
+ * stride loop of get_grid_index exceeds the level's size), else 0 (dense);
+ * query_feature, CR/hashgrid.h:122-124 and :7-40.  Host-only (no device
+ * access); any output pointer may be NULL. */
+int nest_hashgrid_levels(const nest_hashgrid *grid, float *scale, uint32_t *resolution, uint32_t *hashed);
+
 /* ---- forward rasterizer -------------------------------------------------
  * Together these two calls are RasterizeGaussiansCUDA
  * (DSR/rasterize_points.cu:40-242) / CudaRasterizer::Rasterizer::forward

@@ -33,8 +33,18 @@ CFLAGS = [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-ffp-contract
           "-Wall", "-Wno-unused-function", "-Wno-unused-variable", f"-I{INCLUDE}"]
 
 
-def _compile(src: str) -> str:
+def _headers_mtime() -> float:
+    hs = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    hs += [os.path.join(INCLUDE, f) for f in os.listdir(INCLUDE) if f.endswith(".h")]
+    return max(os.path.getmtime(h) for h in hs)
+
+
+def _compile(src: str, incremental: bool = False) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+    if incremental and os.path.exists(obj):
+        newest = max(os.path.getmtime(os.path.join(CSRC, src)), _headers_mtime())
+        if os.path.getmtime(obj) > newest:
+            return obj
     cmd = [HIPCC, *CFLAGS]
     if src.endswith(".cpp"):
         cmd += ["-x", "hip"]
@@ -45,10 +55,12 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int = 4, verbose: bool = True) -> str:
+def build(jobs: int = 4, verbose: bool = True, incremental: bool = False) -> str:
+    """Compiles every source (incremental: only those older than their
+    object file or any header) and links the library."""
     os.makedirs(BUILD, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(lambda src: _compile(src, incremental), SOURCES))
     tmp = OUT + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -63,9 +75,10 @@ def build(jobs: int = 4, verbose: bool = True) -> str:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 4))
+    ap.add_argument("--incremental", action="store_true", help="recompile only sources newer than their objects")
     a = ap.parse_args()
     try:
-        build(a.jobs)
+        build(a.jobs, incremental=a.incremental)
     except RuntimeError as e:
         print(e, file=sys.stderr)
         sys.exit(1)

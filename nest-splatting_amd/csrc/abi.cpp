@@ -355,6 +355,22 @@ int nest_image_layout(int32_t W, int32_t H, size_t offsets[NEST_IMG_FIELDS], siz
   return NEST_OK;
 }
 
+int nest_hashgrid_levels(const nest_hashgrid* gr, float* scale, uint32_t* resolution, uint32_t* hashed) {
+  if (!gr || gr->struct_size < sizeof(nest_hashgrid)) return fail(NEST_ERR_INVALID_ARGUMENT, "grid struct is missing or too small");
+  if (gr->levels == 0) return NEST_OK;
+  LevelTable lv;
+  const int rc = build_levels(gr->offsets, gr->levels, gr->log2_scale, gr->base_resolution, gr->align_corners != 0, 3,
+                              true, lv);
+  if (rc) return rc;
+  for (uint32_t l = 0; l < gr->levels; l++) {
+    if (scale) scale[l] = lv.scale[l];
+    // res1 is resolution (align_corners) or resolution + 1
+    if (resolution) resolution[l] = gr->align_corners ? lv.res1[l] : lv.res1[l] - 1u;
+    if (hashed) hashed[l] = lv.flags[l] & 1u;
+  }
+  return NEST_OK;
+}
+
 int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp, void* geom_ws, size_t geom_bytes,
                           int32_t* radii, int64_t* num_rendered, nest_timing* timing, void* stream) {
   int rc = check_settings(rs);

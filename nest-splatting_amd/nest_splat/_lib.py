@@ -128,6 +128,8 @@ EXPORTS = {
     "nest_geom_layout": (ct.c_int, [ct.c_int32, ct.POINTER(ct.c_size_t), ct.POINTER(ct.c_size_t)]),
     "nest_binning_layout": (ct.c_int, [ct.c_int64, ct.POINTER(ct.c_size_t), ct.POINTER(ct.c_size_t)]),
     "nest_image_layout": (ct.c_int, [ct.c_int32, ct.c_int32, ct.POINTER(ct.c_size_t), ct.POINTER(ct.c_size_t)]),
+    "nest_hashgrid_levels": (ct.c_int, [ct.POINTER(HashGrid), ct.POINTER(ct.c_float), ct.POINTER(ct.c_uint32),
+                                        ct.POINTER(ct.c_uint32)]),
     "nest_forward_geometry": (ct.c_int, [ct.POINTER(RasterSettings), ct.POINTER(Splats), ct.c_void_p, ct.c_size_t,
                                          ct.c_void_p, ct.POINTER(ct.c_int64), ct.POINTER(Timing), ct.c_void_p]),
     "nest_forward_render": (ct.c_int, [ct.POINTER(RasterSettings), ct.POINTER(HashGrid), ct.POINTER(Splats),
@@ -220,6 +222,25 @@ def image_layout(W: int, H: int):
     tot = ct.c_size_t()
     check(lib().nest_image_layout(W, H, offs, ct.byref(tot)), "nest_image_layout")
     return list(offs), tot.value
+
+
+def hashgrid_levels(levels: int, level_dim: int, log2_scale: float, base_resolution: int, offsets,
+                    align_corners: bool = False):
+    """Per-level (scale, resolution, hashed) of a grid as the library's
+    lookups use them (nest_hashgrid_levels; host-only)."""
+    g = HashGrid()
+    g.struct_size = ct.sizeof(HashGrid)
+    g.levels, g.level_dim = int(levels), int(level_dim)
+    g.log2_scale, g.base_resolution = float(log2_scale), int(base_resolution)
+    g.align_corners = int(bool(align_corners))
+    for i, o in enumerate(offsets):
+        g.offsets[i] = int(o)
+    g.table_rows = int(offsets[levels])
+    sc = (ct.c_float * max(1, levels))()
+    res = (ct.c_uint32 * max(1, levels))()
+    hs = (ct.c_uint32 * max(1, levels))()
+    check(lib().nest_hashgrid_levels(ct.byref(g), sc, res, hs), "nest_hashgrid_levels")
+    return [float(v) for v in sc[:levels]], [int(v) for v in res[:levels]], [bool(v) for v in hs[:levels]]
 
 
 def view(buf: torch.Tensor, offset: int, dtype: torch.dtype, shape) -> torch.Tensor:

@@ -190,18 +190,27 @@ def render(viewpoint_camera, pc, pipe, bg_color: torch.Tensor, scaling_modifier=
     rets["render"] = rgb
 
     if with_surface:
-        wv = _matrix(viewpoint_camera.world_view_transform, dev)
-        render_normal = (allmap[2:5].permute(1, 2, 0) @ (wv[:3, :3].T)).permute(2, 0, 1)
-        render_depth_median = torch.nan_to_num(allmap[5:6], 0, 0)
-        render_depth_expected = torch.nan_to_num(allmap[0:1] / render_alpha, 0, 0)
-        render_dist = allmap[6:7]
-        dr = getattr(pipe, "depth_ratio", 0.0)
-        surf_depth = render_depth_expected * (1 - dr) + dr * render_depth_median
-        surf_normal = depth_to_normal(viewpoint_camera, surf_depth).permute(2, 0, 1) * render_alpha.detach()
-        rets.update({"rend_alpha": render_alpha, "rend_normal": render_normal, "rend_dist": render_dist,
-                     "surf_depth": surf_depth, "surf_normal": surf_normal, "gaussian_num": allmap[7:8],
-                     "depth_expected": render_depth_expected, "depth_median": render_depth_median})
+        rets.update(surface_maps(viewpoint_camera, allmap, getattr(pipe, "depth_ratio", 0.0)))
     return rets
+
+
+def surface_maps(cam, allmap: torch.Tensor, depth_ratio: float = 0.0) -> dict:
+    """The allmap post-processing of gaussian_renderer/__init__.py:763-791:
+    world-space normal map, median and expected depth, distortion, the
+    pseudo-surface depth (depth_ratio blends expected and median depth) and
+    its normal from the back-projected depth map, scaled by alpha."""
+    dev = allmap.device
+    render_alpha = allmap[1:2]
+    wv = _matrix(cam.world_view_transform, dev)
+    render_normal = (allmap[2:5].permute(1, 2, 0) @ (wv[:3, :3].T)).permute(2, 0, 1)
+    render_depth_median = torch.nan_to_num(allmap[5:6], 0, 0)
+    render_depth_expected = torch.nan_to_num(allmap[0:1] / render_alpha, 0, 0)
+    render_dist = allmap[6:7]
+    surf_depth = render_depth_expected * (1 - depth_ratio) + depth_ratio * render_depth_median
+    surf_normal = depth_to_normal(cam, surf_depth).permute(2, 0, 1) * render_alpha.detach()
+    return {"rend_alpha": render_alpha, "rend_normal": render_normal, "rend_dist": render_dist,
+            "surf_depth": surf_depth, "surf_normal": surf_normal, "gaussian_num": allmap[7:8],
+            "depth_expected": render_depth_expected, "depth_median": render_depth_median}
 
 
 def scene_to_device(scene, device="cuda:0"):

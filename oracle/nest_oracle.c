@@ -89,6 +89,12 @@ float or_expf(float x)
     return y * bits_to_f((uint32_t)(k + 127) << 23);
 }
 
+/* or_expf over an array (for the tests' float32 replicas of the render). */
+void or_expf_n(int n, const float *x, float *y)
+{
+    for (int i = 0; i < n; i++) y[i] = or_expf(x[i]);
+}
+
 /* float -> int32 with saturation to +-2^30 and NaN -> 0 after clamping. */
 static inline int f2i_sat(float x)
 {

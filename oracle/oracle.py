@@ -68,6 +68,7 @@ def lib():
         L = ct.CDLL(_LIB_PATH)
         L.or_expf.restype = ct.c_float
         L.or_expf.argtypes = [ct.c_float]
+        L.or_expf_n.argtypes = [ct.c_int, f32p, f32p]
         L.or_round_bf16.restype = ct.c_float
         L.or_round_bf16.argtypes = [ct.c_float]
         L.or_round_f16.restype = ct.c_float
@@ -109,9 +110,10 @@ def _c(a, dt):
 
 
 def expf(x) -> np.ndarray:
-    x = np.asarray(x, dtype=np.float32)
-    f = lib().or_expf
-    return np.array([f(float(v)) for v in x.ravel()], dtype=np.float32).reshape(x.shape)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().or_expf_n(x.size, x.reshape(-1), y.reshape(-1))
+    return y
 
 
 def round_bf16(x):

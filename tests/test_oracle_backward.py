@@ -4,7 +4,9 @@ on tiny scenes.  The torch forward is itself checked against the oracle's
 forward outputs first, so the gradients are those of the forward the oracle
 computes.  Tolerances are relative to each gradient array's largest entry:
 the oracle runs in float32 and reconstructs T by division, the torch side is
-float64 with exact products; a dropped or mis-signed term is an O(1) error.
+float64 with exact products.  The largest error measured is 2.8e-5; the
+1e-4 bound leaves 3.5x, while a dropped or mis-signed term is an O(1)
+error.
 """
 import numpy as np
 import pytest
@@ -13,7 +15,7 @@ import torch
 import torch_ref as TR
 from nest_splat.scene import get_spec, make_scene
 
-TOL = 2e-3
+TOL = 1e-4
 
 
 def _tiny(L=4, F=2, P=60, W=48, H=32, log_scale=-2.2, seed=0):

@@ -3,11 +3,12 @@ used to pin the backward oracle by automatic differentiation.
 
 TEST INFRASTRUCTURE ONLY.  The discrete decisions of the forward (which
 tile/splat pairs are accepted, the rho3d/rho2d branch, the per-pixel cut-off
-at the last contributor, the median contributor, the hash-grid cell of every
-corner) are taken from float32 replicas of the oracle's forward or from the
-oracle's own outputs (n_contrib); everything continuous is evaluated in
-float64 torch, so autograd gives the exact derivative of the forward the
-oracle computes.  The gradients the reference defines differently from that
+where T (1 - alpha) falls below 1e-4, the median contributor (the last hit
+taken while T > 0.5), the hash-grid cell of every corner) are taken from
+float32 replicas of the forward's rules, with the oracle's exp; the cut-off
+and median are checked against the oracle's n_contrib.  Everything
+continuous is evaluated in float64 torch, so autograd gives the exact
+derivative of the forward the oracle computes.  The gradients the reference defines differently from that
 derivative are handled as the reference does: the 0.99 alpha clamp is
 differentiated as if absent (straight-through), with beta > 0 the position
 terms carry the activated G' in place of the raw g, the auxiliary outputs
@@ -46,9 +47,9 @@ def grid_index(align, hsize, res, g):
     return (index % np.uint64(hsize)).astype(np.int64)
 
 
-def _pair_decisions(Tm, xy, opa, px, py, beta):
-    """float32 replica of the oracle's per-pair acceptance (nest_oracle.c
-    render_pixel): returns accepted, use3d and the float32 s (for the cells)."""
+def _pair_decisions(O, Tm, xy, opa, px, py, beta):
+    """float32 replica of the per-pair acceptance (CR/forward.cu:834-921):
+    returns accepted, use3d, the float32 s (for the cells) and alpha."""
     Tu, Tv, Tw = Tm[..., 0:3], Tm[..., 3:6], Tm[..., 6:9]
     k = px[..., None] * Tw - Tu
     l = py[..., None] * Tw - Tv
@@ -64,12 +65,37 @@ def _pair_decisions(Tm, xy, opa, px, py, beta):
     rho = np.minimum(rho3d, rho2d)
     depth = np.where(use3d, (sx * Tw[..., 0] + sy * Tw[..., 1]) + Tw[..., 2], Tw[..., 2])
     with np.errstate(over="ignore", invalid="ignore"):
-        G = np.exp(f32(-0.5) * rho).astype(f32)
+        G = O.expf(f32(-0.5) * rho)
         if beta > 0:
             G = ((1.0 + beta) * G.astype(np.float64) / (1.0 + (f32(beta) * G).astype(np.float64))).astype(f32)
         alpha = np.minimum(f32(0.99), opa * G)
     acc = (p2 != 0) & (depth >= f32(NEAR)) & (f32(-0.5) * rho <= 0) & (alpha >= f32(1.0 / 255.0))
-    return acc, use3d, sx, sy
+    return acc, use3d, sx, sy, alpha
+
+
+def _pixel_cutoff(acc, alpha):
+    """Front-to-back float32 transmittance per pixel (rows): a hit whose
+    T (1 - alpha) < 1e-4 ends the pixel uncounted; the median is the last hit
+    taken while T > 0.5 (CR/forward.cu:894-930, :1917-1920).  Returns the hits
+    taken [npix, n], the last contributor and the median contributor
+    (1-based positions in the tile's list, 0 for none)."""
+    npix, n = acc.shape
+    T = np.ones(npix, f32)
+    done = np.zeros(npix, bool)
+    take = np.zeros_like(acc)
+    last = np.zeros(npix, np.int64)
+    med = np.zeros(npix, np.int64)
+    for j in range(n):
+        ok = acc[:, j] & ~done
+        tT = (T * (f32(1) - alpha[:, j])).astype(f32)
+        stop = ok & (tT < f32(1e-4))
+        done |= stop
+        t = ok & ~stop
+        med = np.where(t & (T > f32(0.5)), j + 1, med)
+        last = np.where(t, j + 1, last)
+        take[:, j] = t
+        T = np.where(t, tT, T)
+    return take, last, med
 
 
 def render_forward(O, pre, binres, fwd, W, H, C, leaves, grid=None, beta=0.0, homotrans_np=None, ap_level=None):
@@ -102,11 +128,12 @@ def render_forward(O, pre, binres, fwd, W, H, C, leaves, grid=None, beta=0.0, ho
         pid = py * W + px
         ids = vals[r0:r1].astype(np.int64)
         n = ids.shape[0]
-        acc, use3d, sx32, sy32 = _pair_decisions(Tm32[ids][None], xy32[ids][None], no32[ids, 3][None],
-                                                 px.astype(f32)[:, None], py.astype(f32)[:, None], beta)
-        j = np.arange(n)[None, :]
-        acc &= j < ncon[0, pid][:, None].astype(np.int64)
-        median_j = ncon[1, pid].astype(np.int64) - 1
+        acc, use3d, sx32, sy32, a32 = _pair_decisions(O, Tm32[ids][None], xy32[ids][None], no32[ids, 3][None],
+                                                      px.astype(f32)[:, None], py.astype(f32)[:, None], beta)
+        acc, last, med = _pixel_cutoff(acc, a32)
+        np.testing.assert_array_equal(last, ncon[0, pid])
+        np.testing.assert_array_equal(med, ncon[1, pid])
+        median_j = med - 1
         if not acc.any():
             continue
         accT = torch.from_numpy(acc)
