@@ -8,7 +8,8 @@
  *  - Every pointer named "device" is HIP device memory owned by the caller;
  *    the library never allocates device memory.  Scratch comes in through
  *    caller-provided workspaces whose sizes the *_workspace_size / *_layout
- *    queries report.
+ *    queries report; the one exception is nest_inclusive_scan_u32_noalloc,
+ *    whose scratch is a fixed 512 KiB device array the library owns.
  *  - Every launch is ordered on the caller's stream (a hipStream_t passed as
  *    void*, NULL = the null stream).  The only host synchronisation is the
  *    read-back of the number of tile/splat pairs in nest_forward_geometry
@@ -348,6 +349,18 @@ int nest_mark_visible(int32_t P, const float *means3D, const float viewmatrix[16
 size_t nest_scan_workspace_size(int64_t n);
 int nest_inclusive_scan_u32(const uint32_t *in, uint32_t *out, int64_t n, void *ws, size_t ws_bytes,
                             void *stream);
+
+/* Allocation-free variant of nest_inclusive_scan_u32.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * block partials live in a 512 KiB device array owned by the library, one per
+ * GPU, held until the process ends; n may be at most NEST_SCAN_NOALLOC_MAX
+ * (larger n returns NEST_ERR_WORKSPACE before any launch).  The call
+ * allocates nothing.  All calls on one GPU share that array, so calls that
+ * overlap on one GPU (different streams or threads) race; calls ordered on
+ * one stream do not.  Results equal nest_inclusive_scan_u32's. */
+#define NEST_SCAN_NOALLOC_MAX 268431360 /* 65535 blocks of 4096 elements */
+int nest_inclusive_scan_u32_noalloc(const uint32_t *in, uint32_t *out, int64_t n, void *stream);
 
 /* cub::DeviceRadixSort::SortPairs, stable, on key bits [0, end_bit)
  * (CR/rasterizer_impl.cu:245-249, :381-386). */

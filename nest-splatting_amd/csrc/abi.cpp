@@ -15,6 +15,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/nest_splat.h"
@@ -627,6 +628,61 @@ int nest_timing_release(nest_timing* t) {
 }
 
 size_t nest_scan_workspace_size(int64_t n) { return scan_ws_bytes(n > 0 ? n : 1); }
+
+}  // extern "C"
+
+// Scratch of nest_inclusive_scan_u32_noalloc: the scan's block partials,
+// (ceil(n / 4096) + 1) 64-bit words, in a device array the library owns.
+// Every GPU the library runs on holds its own copy until the process ends;
+// the host-side name is only a stand-in, so kernels get the address that
+// hipGetSymbolAddress reports for the current device.  The scan writes every
+// partial it reads, so nothing has to be cleared between calls.
+constexpr size_t kScanScratchBytes = 512u * 1024u;
+static __device__ __align__(256) uint64_t scratch[kScanScratchBytes / sizeof(uint64_t)];
+static_assert((((int64_t)NEST_SCAN_NOALLOC_MAX + 4095) / 4096 + 1) * 8 <= (int64_t)kScanScratchBytes,
+              "NEST_SCAN_NOALLOC_MAX must fit the scratch");
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device.
+int scratch_on_current_device(void** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(NEST_ERR_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(NEST_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return NEST_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nest_inclusive_scan_u32_noalloc(const uint32_t* in, uint32_t* out, int64_t n, void* stream) {
+  if (n < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "n must be >= 0");
+  if (n == 0) return NEST_OK;
+  if (!in || !out) return fail(NEST_ERR_INVALID_ARGUMENT, "in/out is NULL");
+  if (n > (int64_t)NEST_SCAN_NOALLOC_MAX)
+    return fail(NEST_ERR_WORKSPACE, "allocation-free scan: n = %lld exceeds the %lld elements its %zu-byte scratch holds",
+                (long long)n, (long long)NEST_SCAN_NOALLOC_MAX, kScanScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_on_current_device(&ws);
+  if (rc) return rc;
+  hipError_t e = launch_scan_u32(in, out, n, ws, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? NEST_OK : hip_fail(e, "scan");
+}
 
 int nest_inclusive_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* ws, size_t ws_bytes, void* stream) {
   if (n < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "n must be >= 0");

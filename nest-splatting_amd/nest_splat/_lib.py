@@ -28,6 +28,7 @@ MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
 ABI_VERSION = 8
+SCAN_NOALLOC_MAX = 268431360
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
  GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
 GEOM_FIELDS = 12
@@ -145,6 +146,7 @@ EXPORTS = {
     "nest_scan_workspace_size": (ct.c_size_t, [ct.c_int64]),
     "nest_inclusive_scan_u32": (ct.c_int, [ct.c_void_p, ct.c_void_p, ct.c_int64, ct.c_void_p, ct.c_size_t,
                                            ct.c_void_p]),
+    "nest_inclusive_scan_u32_noalloc": (ct.c_int, [ct.c_void_p, ct.c_void_p, ct.c_int64, ct.c_void_p]),
     "nest_sort_workspace_size": (ct.c_size_t, [ct.c_int64]),
     "nest_sort_pairs_u64": (ct.c_int, [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int64, ct.c_int32,
                                        ct.c_void_p, ct.c_size_t, ct.c_void_p]),
