@@ -6,8 +6,13 @@ kernel's HBM roofline fraction and the CPU oracle timed on this host.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config cfg3]
 
+--config picks the workload: cfg1 (2k splats, 128x128), cfg2 (100k splats,
+800x800), cfg3 (the default and the metric: 1M splats, 1600x1064), cfg4
+(500k RVQ-compressed splats, the decode inside the timed frame), cfg5 (4M
+splats, all eight 1920x1080 cameras per step).
+
 Prints one JSON line.  One process drives one GPU; --gpus above 1 exits with a
-message (frames shard by camera or by tile band).
+message (frames shard by camera or by tile band across processes).
 """
 from __future__ import annotations
 
@@ -32,10 +37,33 @@ def log(*a):
 
 
 def render_algorithmic_bytes(NR: int, hits: int, HW: int, L: int, F: int, e: int, C: int) -> int:
-    """Logical bytes of one render launch: 104 B per staged tile/splat pair,
-    L*8*F*e B of hash gathers per accepted hit, (4C + 56) B of outputs per
-    pixel (colour map + 14 allmap channels)."""
+    """Logical bytes of one render launch, cache hits included: 104 B per
+    staged tile/splat pair, L*8*F*e B of hash gathers per accepted hit,
+    (4C + 56) B of outputs per pixel (colour map + 14 allmap channels)."""
     return 104 * NR + L * 8 * F * e * hits + HW * (4 * C + 56)
+
+
+def render_compulsory_bound(P: int, NR: int, HW: int, table_bytes: int, C: int) -> int:
+    """Upper bound of the bytes one render launch must exchange with HBM once:
+    every splat's 128-B record, the 4-B point list entry per pair, the whole
+    table (the bound takes every entry as touched), the outputs."""
+    return 128 * P + 4 * NR + table_bytes + HW * (4 * C + 56)
+
+
+# What bounds the render kernel, from its counters (TA busy, L1 accesses per
+# clock, VALU share): the 16-byte table gathers' vector-L1 address and tag
+# rate and the latency of the gathers that miss L2.
+RENDER_LIMITER = ("vector L1 address/tag rate of the 16-byte table gathers (about one L1 tag access per CU clock, "
+                  "TA ~70% busy) and the latency of gathers missing L2; HBM traffic is the counter-measured fetch "
+                  "+ write")
+
+
+def load_counters(path: str) -> dict:
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
 
 
 def cpu_baseline(scene, gpu_hits_total: int, row_stride: int, threads: int):
@@ -49,15 +77,24 @@ def cpu_baseline(scene, gpu_hits_total: int, row_stride: int, threads: int):
     sp = scene.spec
     cam = scene.cameras[0]
     W, H = cam.image_width, cam.image_height
+    scales, rots, opac, homo = scene.scales, scene.rotations, scene.opacity, scene.homotrans
+    t_rvq = 0.0
+    if sp.rvq:
+        from nest_splat.scene import RVQ_BIAS, build_homotrans_np
+        tr = time.perf_counter()
+        raw = {a: O.rvq_decode(scene.rvq_codebooks[a], scene.rvq_indices[a], RVQ_BIAS[a]) for a in RVQ_BIAS}
+        scales, rots, op = O.activate(raw["scale"], raw["rotation"], raw["opacity"])
+        opac = op[:, None]
+        homo = build_homotrans_np(rots, scales, scene.means)
+        t_rvq = time.perf_counter() - tr
     t0 = time.perf_counter()
-    pre = O.preprocess(scene.means, scene.scales, scene.rotations, scene.opacity, cam.world_view_transform,
-                       cam.full_proj_transform, W, H)
+    pre = O.preprocess(scene.means, scales, rots, opac, cam.world_view_transform, cam.full_proj_transform, W, H)
     t1 = time.perf_counter()
     b = O.binning(pre, W, H)
     t2 = time.perf_counter()
     grid = O.make_grid(sp.L, sp.F, sp.S, sp.base_res, scene.offsets, scene.table, sp.gridrange, sp.contract)
     phase = row_stride // 2
-    r = O.render(pre, b, W, H, sp.C, grid, homotrans=scene.homotrans, ap_level=scene.ap_level,
+    r = O.render(pre, b, W, H, sp.C, grid, homotrans=homo, ap_level=scene.ap_level,
                  row_stride=row_stride, row_phase=phase, threads=threads)
     t3 = time.perf_counter()
     gx, gy = (W + 15) // 16, (H + 15) // 16
@@ -78,13 +115,14 @@ def cpu_baseline(scene, gpu_hits_total: int, row_stride: int, threads: int):
           np.asarray(sp.bg, np.float32), threads=threads)
     t5 = time.perf_counter()
     pix_share = idx.size / (W * H)
-    frame_s = (t1 - t0) + (t2 - t1) + (t3 - t2) / share + (t5 - t4) / pix_share
+    frame_s = t_rvq + (t1 - t0) + (t2 - t1) + (t3 - t2) / share + (t5 - t4) / pix_share
+    rvq_note = f"RVQ decode + activations + homotrans ({t_rvq:.2f} s, 1 thread); " if sp.rvq else ""
     return {
         "value": W * H / frame_s / 1e6,
         "unit": "Mpix/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle C port: full preprocess ({t1 - t0:.2f} s, 1 thread) and binning ({t2 - t1:.2f} s, "
+        "sample": (f"oracle C port: {rvq_note}full preprocess ({t1 - t0:.2f} s, 1 thread) and binning ({t2 - t1:.2f} s, "
                    f"1 thread); render of every {row_stride}th tile row ({len(rows)} of {gy} rows, {t3 - t2:.2f} s, "
                    f"{threads} OpenMP threads, scaled by its {share:.4f} share of pairs+hits); fp32-accumulated MLP "
                    f"of those {idx.size} pixels ({t5 - t4:.2f} s, {threads} OpenMP threads, scaled by pixel share); "
@@ -93,11 +131,12 @@ def cpu_baseline(scene, gpu_hits_total: int, row_stride: int, threads: int):
     }
 
 
-def summarize_pmc(fetch_dir: str, write_dir: str, out_path: str) -> dict:
+def summarize_pmc(fetch_dir: str, write_dir: str, out_path: str, kernel: str = "render_kernel") -> dict:
     """Reduce two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE, both with
-    --copy-calibration-mb) to HBM bytes per render launch.  Each counter is
-    scaled by bytes-moved / counter-reading of the largest plain copy kernel
-    (__amd_rocclr_copyBuffer) in the same run."""
+    --copy-calibration-mb) to HBM bytes per launch of the kernels whose name
+    contains `kernel`.  Each counter is scaled by bytes-moved /
+    counter-reading of the largest plain copy kernel (__amd_rocclr_copyBuffer)
+    in the same run."""
     import csv
     import glob
 
@@ -111,7 +150,7 @@ def summarize_pmc(fetch_dir: str, write_dir: str, out_path: str) -> dict:
     for tag, d, counter in (("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")):
         rs = [r for r in rows(d) if r["Counter_Name"] == counter]
         copies = [float(r["Counter_Value"]) for r in rs if "copyBuffer" in r["Kernel_Name"]]
-        render = [float(r["Counter_Value"]) for r in rs if "render_kernel" in r["Kernel_Name"]]
+        render = [float(r["Counter_Value"]) for r in rs if kernel in r["Kernel_Name"]]
         if not copies or not render:
             raise SystemExit(f"no copy/render rows for {counter} under {d}")
         copy_kib = max(copies)
@@ -267,22 +306,106 @@ def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_lev
     return res_ms
 
 
+class Workload:
+    """The timed step of one config: its device inputs and a step(timings)
+    closure that renders every camera of the config once (cfg4: decodes the
+    RVQ attributes first) and decodes the feature maps with the MLP."""
+
+    def __init__(self, spec, scene, dev):
+        import numpy as np
+        import torch
+
+        from nest_splat import rasterizer as rz
+        from nest_splat.camera import view_ray_matrix
+        from nest_splat.mlp import NestMLP
+
+        self.spec, self.scene = spec, scene
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        self.means, self.opac, self.scales, self.rots = t(scene.means), t(scene.opacity), t(scene.scales), \
+            t(scene.rotations)
+        self.homo, self.ap_level, self.table = t(scene.homotrans), t(scene.ap_level), t(scene.table)
+        self.grid = rz.HashGridDesc(spec.L, spec.F, spec.S, spec.base_res, self.table, scene.offsets,
+                                    np.asarray(spec.gridrange, np.float32))
+        self.mlp = NestMLP(spec.C, spec.mlp_width, spec.mlp_dtype, scene.W1, scene.W2, scene.W3).to(dev)
+        self.bg = torch.tensor(spec.bg, dtype=torch.float32) if sum(spec.bg) > 0 else None
+        self.cams = scene.cameras
+        self.settings = [rz.make_settings(c.image_height, c.image_width, c.tanfovx, c.tanfovy, c.world_view_transform,
+                                          c.full_proj_transform, c.camera_center, if_contract=spec.contract)
+                         for c in self.cams]
+        self.rays = [view_ray_matrix(c) for c in self.cams]
+        self.rvq = None
+        if spec.rvq:
+            from nest_splat.rvq import RVQAttributes
+            from nest_splat.scene import RVQ_BIAS
+            self.rvq = RVQAttributes.from_numpy(scene.rvq_codebooks, scene.rvq_indices, RVQ_BIAS, dev)
+        self.pixels = sum(c.image_width * c.image_height for c in self.cams)
+        self.mlp_events = []  # (start, stop) HIP events around each timed MLP decode
+
+    def step(self, timings=None):
+        """One step; timings: a list with one nest_timing per camera, or None."""
+        import torch
+
+        from nest_splat import rasterizer as rz
+        from nest_splat.renderer import build_H, build_rotation
+        means, opac, scales, rots, homo = self.means, self.opac, self.scales, self.rots, self.homo
+        if self.rvq is not None:
+            # compressed attributes: decode (exp / normalise / sigmoid fused) and
+            # rebuild homotrans from the decoded rotation and scale, as the
+            # reference rebuilds it every frame (get_homotrans)
+            dec = self.rvq.decode()
+            scales, rots, opac = dec["scale"], dec["rotation"], dec["opacity"]
+            homo = build_H(build_rotation(rots), scales, means)
+        out = []
+        for k, (st, M) in enumerate(zip(self.settings, self.rays)):
+            tm = timings[k] if timings is not None else False
+            res = rz.rasterize_forward(st, self.grid, means, opac, scales, rots, homotrans=homo,
+                                       ap_level=self.ap_level, channels=self.spec.C, timing=tm)
+            ev = None
+            if timings is not None:
+                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                ev[0].record()
+            rgb = self.mlp.decode_image(res.color, M, alpha=res.others[1], bg=self.bg)
+            if ev is not None:
+                ev[1].record()
+                self.mlp_events.append(ev)
+            out.append((res, rgb))
+        return out
+
+
+def describe(spec) -> str:
+    layout = {"cube": "centres uniform in [-1,1]^3", "shell": "noisy unit sphere shell",
+              "ball_unbounded": "70% in a unit ball and 30% out to r=20 (contracted)",
+              "shells": "5 noisy concentric shells (r 0.5-2.5)"}[spec.layout]
+    cams = f"{spec.n_cams} cameras at " if spec.n_cams > 1 else ""
+    rvq = (f", scale/rotation/opacity as {spec.rvq_stages}-stage RVQ codes into {spec.rvq_codebook}-entry codebooks "
+           f"decoded inside the step") if spec.rvq else ""
+    return (f"{spec.name}: {spec.P} 2D surfels, {layout}{rvq}; {cams}{spec.W}x{spec.H}, hash grid L={spec.L} "
+            f"F={spec.F} T=2^{spec.log2T} {spec.table_dtype}, MLP {spec.C + 16}-{spec.mlp_width}-{spec.mlp_width}-3 "
+            f"{spec.mlp_dtype}")
+
+
 def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--pmc-summary":
-        # python bench.py --pmc-summary FETCH_DIR WRITE_DIR COPY_MIB OUT.json
+        # python bench.py --pmc-summary FETCH_DIR WRITE_DIR COPY_MIB OUT.json [KERNEL_SUBSTRING]
         fetch_dir, write_dir, copy_mib, out_path = sys.argv[2:6]
-        r = finish_traffic(summarize_pmc(fetch_dir, write_dir, out_path), int(copy_mib), out_path)
+        kern = sys.argv[6] if len(sys.argv) > 6 else "render_kernel"
+        r = finish_traffic(summarize_pmc(fetch_dir, write_dir, out_path, kern), int(copy_mib), out_path)
         print(json.dumps(r))
         return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="cfg3")
+    ap.add_argument("--config", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-row-stride", type=int, default=4)
-    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "render_traffic_cfg3.json"),
-                    help="JSON with counter-measured HBM bytes per render launch (from rocprofv3 --pmc)")
+    ap.add_argument("--cpu-row-stride", type=int, default=0,
+                    help="CPU baseline: render every k-th tile row (0: per-config default)")
+    ap.add_argument("--traffic", default=None,
+                    help="JSON with counter-measured HBM bytes per render launch (from rocprofv3 --pmc); default "
+                         "profiles/render_traffic_<config>.json")
+    ap.add_argument("--counters", default=None,
+                    help="JSON with the render kernel's L1 counters (TCP_TOTAL_CACHE_ACCESSES, kernel cycles); "
+                         "default profiles/render_counters_<config>.json")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="before the frames, copy this many MiB device-to-device (a plain copy kernel of known "
                          "size whose FETCH_SIZE / WRITE_SIZE scale the render kernel's counters)")
@@ -302,7 +425,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this benchmark drives exactly one GPU per process; multi-GPU figures are not "
-                                   "produced (frames shard by camera or tile band across processes, see DESIGN.md)",
+                                   "produced (frames shard by camera or tile band across processes)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 
@@ -311,8 +434,6 @@ def main():
 
     from nest_splat import _lib as L
     from nest_splat import rasterizer as rz
-    from nest_splat.camera import view_ray_matrix
-    from nest_splat.mlp import NestMLP
     from nest_splat.scene import get_spec, make_scene
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
@@ -321,26 +442,10 @@ def main():
     t0 = time.perf_counter()
     spec = get_spec(args.config)
     scene = make_scene(spec)
-    log(f"[bench] scene {spec.name}: {spec.P} splats, {spec.W}x{spec.H}, table {scene.table.nbytes / 2**20:.0f} MiB "
-        f"({time.perf_counter() - t0:.1f} s)")
-    cam = scene.cameras[0]
-    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-    means, opac, scales, rots = t(scene.means), t(scene.opacity), t(scene.scales), t(scene.rotations)
-    homo, ap_level, table = t(scene.homotrans), t(scene.ap_level), t(scene.table)
-    settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy, cam.world_view_transform,
-                                cam.full_proj_transform, cam.camera_center, if_contract=spec.contract)
-    grid = rz.HashGridDesc(spec.L, spec.F, spec.S, spec.base_res, table, scene.offsets,
-                           np.asarray(spec.gridrange, np.float32))
-    mlp = NestMLP(spec.C, spec.mlp_width, spec.mlp_dtype, scene.W1, scene.W2, scene.W3).to(dev)
-    M = view_ray_matrix(cam)
-    bg = torch.tensor(spec.bg, dtype=torch.float32) if sum(spec.bg) > 0 else None
-    HW = spec.W * spec.H
-
-    def step(tm=None):
-        res = rz.rasterize_forward(settings, grid, means, opac, scales, rots, homotrans=homo, ap_level=ap_level,
-                                   channels=spec.C, timing=tm if tm is not None else False)
-        rgb = mlp.decode_image(res.color, M, alpha=res.others[1], bg=bg)
-        return res, rgb
+    log(f"[bench] scene {spec.name}: {spec.P} splats, {spec.n_cams} x {spec.W}x{spec.H}, table "
+        f"{scene.table.nbytes / 2**20:.0f} MiB ({time.perf_counter() - t0:.1f} s)")
+    wl = Workload(spec, scene, dev)
+    ncam = len(wl.cams)
 
     if args.copy_calibration_mb > 0:
         n = args.copy_calibration_mb * (1 << 20) // 4
@@ -352,38 +457,54 @@ def main():
         log(f"[bench] copy calibration: 3 x {args.copy_calibration_mb} MiB device copies")
         del src, dst
     for i in range(args.warmup):
-        res, rgb = step()
+        frames = wl.step()
     torch.cuda.synchronize()
     log(f"[bench] warmup done ({args.warmup} steps)")
-    tms = [L.new_timing(True) for _ in range(args.steps)]
+    tms = [[L.new_timing(True) for _ in range(ncam)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     for k in range(args.steps):
-        res, rgb = step(tms[k])
+        frames = wl.step(tms[k])
     torch.cuda.synchronize()
     t_end = time.perf_counter()
-    stages = [L.timing_read(tm) for tm in tms]
-    for tm in tms:
-        L.timing_release(tm)
+    stages = [L.timing_read(tm) for row in tms for tm in row]
+    for row in tms:
+        for tm in row:
+            L.timing_release(tm)
     elapsed = t_end - t_start
     ms_per_step = elapsed / args.steps * 1e3
-    mpix = HW * args.steps / elapsed / 1e6
+    mpix = wl.pixels * args.steps / elapsed / 1e6
     log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step, {mpix:.1f} Mpix/s")
 
-    hits_total = int(res.others[7].double().sum().item())
-    NR = res.num_rendered
+    HW = spec.W * spec.H
+    hits_total = [int(res.others[7].double().sum().item()) for res, _ in frames]
+    NRs = [res.num_rendered for res, _ in frames]
     render_ms = float(np.mean([s["render"] for s in stages]))
     stage_ms = {k: float(np.mean([s[k] for s in stages])) for k in stages[0]}
+    stage_ms["mlp"] = float(np.mean([a.elapsed_time(b) for a, b in wl.mlp_events]))
     e = scene.table.dtype.itemsize
-    alg = render_algorithmic_bytes(NR, hits_total, HW, spec.L, spec.F, e, spec.C)
-    achieved = alg / (render_ms * 1e-3) / 1e9
-    traffic = None
-    if os.path.exists(args.traffic):
-        try:
-            with open(args.traffic) as f:
-                traffic = json.load(f).get("render_bytes_per_launch")
-        except Exception:
-            traffic = None
+    alg = float(np.mean([render_algorithmic_bytes(nr, h, HW, spec.L, spec.F, e, spec.C)
+                         for nr, h in zip(NRs, hits_total)]))
+    comp = float(np.mean([render_compulsory_bound(spec.P, nr, HW, scene.table.nbytes, spec.C) for nr in NRs]))
+    tpath = args.traffic or os.path.join(ROOT, "profiles", f"render_traffic_{spec.name}.json")
+    traffic = load_counters(tpath).get("render_bytes_per_launch")
+    cpath = args.counters or os.path.join(ROOT, "profiles", f"render_counters_{spec.name}.json")
+    ctr = load_counters(cpath)
+    achieved = traffic / (render_ms * 1e-3) / 1e9 if traffic else None
+    roofline = {"bound": "hbm", "kernel": "render_kernel (tile compositing + hash gathers)",
+                "achieved": round(achieved, 1) if achieved else None, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None, "traffic": traffic,
+                "traffic_source": os.path.relpath(tpath, ROOT) if traffic else None,
+                "render_ms": round(render_ms, 4),
+                "algorithmic_bytes": int(alg),
+                "algorithmic_GBps_cache_inclusive": round(alg / (render_ms * 1e-3) / 1e9, 1),
+                "compulsory_bytes_bound": int(comp),
+                "limiter": RENDER_LIMITER}
+    if ctr.get("TCP_TOTAL_CACHE_ACCESSES_sum") and ctr.get("kernel_cycles"):
+        roofline["l1_tag_accesses_per_cu_clock"] = round(
+            ctr["TCP_TOTAL_CACHE_ACCESSES_sum"] / (ctr.get("cus", 256) * ctr["kernel_cycles"]), 3)
+    if ctr.get("TA_BUSY_avr") and ctr.get("kernel_cycles"):
+        roofline["ta_busy"] = round(ctr["TA_BUSY_avr"] / ctr["kernel_cycles"], 3)
     out = {
         "metric": METRIC,
         "value": round(mpix, 3),
@@ -397,23 +518,23 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded scene generator, random-init hash table and Xavier MLP weights)",
-        "config": {"workload": f"{spec.name}: {spec.P} 2D surfels, 70% in a unit ball and 30% out to r=20 "
-                               f"(contracted), {spec.W}x{spec.H}, hash grid L={spec.L} F={spec.F} "
-                               f"T=2^{spec.log2T} {spec.table_dtype}, MLP {spec.C + 16}-{spec.mlp_width}-"
-                               f"{spec.mlp_width}-3 {spec.mlp_dtype}",
-                   "splats": spec.P, "width": spec.W, "height": spec.H, "num_rendered": NR,
-                   "hits_per_pixel": round(hits_total / HW, 3)},
-        "frames_per_s": round(1e3 / ms_per_step, 3),
+        "config": {"workload": describe(spec), "splats": spec.P, "width": spec.W, "height": spec.H,
+                   "cameras": ncam, "num_rendered": int(np.mean(NRs)),
+                   "hits_per_pixel": round(sum(hits_total) / (HW * ncam), 3)},
+        "frames_per_s": round(1e3 * ncam / ms_per_step, 3),
         "stages_ms": {k: round(v, 4) for k, v in stage_ms.items()},
-        "roofline": {"bound": "hbm", "kernel": "render_kernel (tile compositing + hash gathers)",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes": alg, "render_ms": round(render_ms, 4)},
+        "roofline": roofline,
         "cpu_baseline": None,
     }
+    res, rgb = frames[-1]
+    means, opac, scales, rots, homo, ap_level, table = wl.means, wl.opac, wl.scales, wl.rots, wl.homo, wl.ap_level, \
+        wl.table
+    settings, grid, mlp, bg = wl.settings[-1], wl.grid, wl.mlp, wl.bg
+    if (args.modes or args.backward) and spec.rvq:
+        raise SystemExit("--modes / --backward run on the uncompressed configs")
     if args.modes > 0:
         out["modes_ms"] = time_modes(args.modes, spec, scene, settings, means, opac, scales, rots, homo, ap_level,
-                                     table, mlp, M, bg, dev)
+                                     table, mlp, wl.rays[-1], bg, dev)
     if args.kernels > 0:
         out["aux_kernels"] = time_aux_kernels(args.kernels, spec, scene, table, dev)
     if args.backward > 0:
@@ -430,10 +551,11 @@ def main():
         torch.cuda.synchronize()
         out["backward_ms"] = round((time.perf_counter() - b0) / args.backward * 1e3, 3)
         log(f"[bench] backward: {out['backward_ms']} ms")
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and ncam == 1:
         threads = len(os.sched_getaffinity(0))
+        stride = args.cpu_row_stride or {"cfg1": 1, "cfg2": 2, "cfg3": 4, "cfg4": 3, "cfg5": 17}[spec.name]
         log(f"[bench] cpu baseline on {threads} threads ...")
-        cb = cpu_baseline(scene, hits_total, args.cpu_row_stride, threads)
+        cb = cpu_baseline(scene, hits_total[0], stride, threads)
         out["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cb.items() if k != "frame_s"}
     print(json.dumps(out), flush=True)
 

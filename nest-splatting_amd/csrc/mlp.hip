@@ -101,6 +101,16 @@ __device__ __forceinline__ float finish_rgb(const MlpParams& p, int64_t n, float
   return r;
 }
 
+// finish_rgb with the pixel's alpha already loaded (1 when there is no mask).
+__device__ __forceinline__ float finish_rgb_alpha(const MlpParams& p, float a, float logit, int o) {
+  float r = 1.0f / (1.0f + expf_ref(-logit));
+  if (p.alpha) {
+    r = a > 0.0f ? r : 0.0f;
+    if (p.use_bg) r = r + (1.0f - a) * p.bg[o];
+  }
+  return r;
+}
+
 constexpr int kMlpThreads = 256;
 
 // NT = width / 16.  KC1 = ceil((C + 16) / 16) K-chunks in layer 1.  KF > 0:
@@ -240,6 +250,272 @@ mlp_mfma_kernel(const MlpParams p) {
   }
 }
 
+// gfx950 formulation with v_mfma_f32_16x16x32 (bf16 / f16): one wave per 64
+// pixels per iteration, for feature maps of 16, 32 or 64 channels and width
+// 32 or 64.
+//  - Loads: lane = pixel, so every feature load is 64 consecutive pixels of
+//    one channel (256 contiguous bytes); the lane rounds its pixel's features
+//    and SH terms to 16 bits into a per-wave LDS row [64 px][K1 + 8], K1 =
+//    C + 16 rounded up to 32 (zero tail).
+//  - Layer 1: B operands are 16-byte LDS reads of that row (pixel col of
+//    N-tile j, channels 32 kc + 8 grp .. + 7), A operands the same slice of W1
+//    in LDS; A and B put channel 32 kc + 8 grp + i in the same (lane group,
+//    element) slot, so the product sums over the chunk's channels.
+//  - Layers 2 and 3: the 16x16 accumulator of M-tile mt holds hidden units
+//    16 mt + 4 grp + i (i < 4) in lane group grp; K-chunk kc of the next layer
+//    takes M-tiles 2 kc and 2 kc + 1, so its slot (grp, i) holds unit
+//    32 kc + 4 grp + i (i < 4) or 32 kc + 16 + 4 grp + i - 4 (i >= 4).  The
+//    weights are stored in LDS with their columns in that order, so hidden
+//    activations stay in registers (ReLU, round to 16 bits, feed).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+template <bool kBF16>
+__device__ __forceinline__ f32x4 mfma32(uint4 a, uint4 b, f32x4 c) {
+  if constexpr (kBF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
+  }
+}
+
+__device__ __forceinline__ uint32_t pack2(uint16_t a, uint16_t b) { return (uint32_t)a | ((uint32_t)b << 16); }
+
+// Raw buffer view of the feature map: per-lane byte offset in a VGPR, the
+// channel's byte offset in an SGPR, so the 64 loads of a tile need no
+// per-channel 64-bit addresses.
+typedef int mlp_i32x4 __attribute__((ext_vector_type(4)));
+__device__ float mlp_raw_load_f32(mlp_i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.f32");
+
+__device__ __forceinline__ mlp_i32x4 feat_rsrc(const float* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  mlp_i32x4 r;
+  r.x = (int)(uint32_t)(a & 0xffffffffu);
+  r.y = (int)(uint32_t)((a >> 32) & 0xffffu);  // stride 0: raw addressing
+  r.z = (int)0xffffffffu;                      // range in bytes
+  r.w = 0x00020000;
+  return r;
+}
+
+// The C features of pixel nn (channel c at byte c * cs4 + nn * ns4).
+template <int C>
+__device__ __forceinline__ void load_features(mlp_i32x4 rsrc, uint32_t cs4, uint32_t voff, float f[C]) {
+#pragma unroll
+  for (int c = 0; c < C; c++) f[c] = mlp_raw_load_f32(rsrc, (int)voff, (int)(cs4 * (uint32_t)c), 0);
+}
+
+// Unit view direction of pixel n of a width-w image: cam2rays rows (x, y, 1) @ M,
+// normalised (32-bit pixel arithmetic; the image has fewer than 2^31 pixels).
+__device__ __forceinline__ void pixel_dir32(const MlpParams& p, uint32_t n, float& dx, float& dy, float& dz) {
+  if (p.dirs) {
+    dx = p.dirs[3 * (size_t)n + 0];
+    dy = p.dirs[3 * (size_t)n + 1];
+    dz = p.dirs[3 * (size_t)n + 2];
+    return;
+  }
+  const uint32_t w = (uint32_t)p.img_w;
+  const uint32_t yi = n / w;
+  const float x = (float)(n - yi * w), y = (float)yi;
+  const float* M = p.M;
+  const float rx = x * M[0] + y * M[3] + M[6];
+  const float ry = x * M[1] + y * M[4] + M[7];
+  const float rz = x * M[2] + y * M[5] + M[8];
+  const float len = fmaxf(sqrtf(rx * rx + ry * ry + rz * rz), 1e-12f);
+  dx = rx / len;
+  dy = ry / len;
+  dz = rz / len;
+}
+
+// Hidden unit of slot q = 32 kc + 8 grp + i of a K-chunk built from two
+// accumulator M-tiles.
+__device__ __forceinline__ int hidden_unit(int q) {
+  const int kc = q >> 5, r = q & 31, grp = r >> 3, i = r & 7;
+  return 32 * kc + (i < 4 ? 4 * grp + i : 16 + 4 * grp + (i - 4));
+}
+
+template <bool kBF16>
+__device__ __forceinline__ uint4 relu_pack8(f32x4 lo, f32x4 hi) {
+  return make_uint4(pack2(to16<kBF16>(fmaxf(lo[0], 0.f)), to16<kBF16>(fmaxf(lo[1], 0.f))),
+                    pack2(to16<kBF16>(fmaxf(lo[2], 0.f)), to16<kBF16>(fmaxf(lo[3], 0.f))),
+                    pack2(to16<kBF16>(fmaxf(hi[0], 0.f)), to16<kBF16>(fmaxf(hi[1], 0.f))),
+                    pack2(to16<kBF16>(fmaxf(hi[2], 0.f)), to16<kBF16>(fmaxf(hi[3], 0.f))));
+}
+
+constexpr int kMlp32Waves = kMlpThreads / 64;
+
+template <int C, int NT>
+struct Mlp32Shape {
+  static constexpr int K1 = ((C + 16) + 31) / 32 * 32;
+  static constexpr int LD1 = K1 + 8;          // halfs per W1 / pixel row (16-byte multiple)
+  static constexpr int LD2 = NT * 16 + 8;     // halfs per W2 / W3 row
+  static constexpr int W1 = 0;
+  static constexpr int W2 = W1 + NT * 16 * LD1;
+  static constexpr int W3 = W2 + NT * 16 * LD2;
+  static constexpr int X = W3 + 16 * LD2;     // per-wave pixel rows
+  static constexpr int TOTAL = X + kMlp32Waves * 64 * LD1;
+};
+
+template <int NT, bool kBF16, int C>
+__global__ void __launch_bounds__(kMlpThreads) __attribute__((amdgpu_waves_per_eu(2)))
+mlp_mfma32_kernel(const MlpParams p) {
+  using S = Mlp32Shape<C, NT>;
+  constexpr int K1 = S::K1, LD1 = S::LD1, LD2 = S::LD2, W = NT * 16;
+  static_assert(NT % 2 == 0, "hidden width must be a multiple of 32");
+  extern __shared__ uint16_t lds[];
+  uint16_t* w1 = lds + S::W1;
+  uint16_t* w2 = lds + S::W2;
+  uint16_t* w3 = lds + S::W3;
+  const uint16_t* g1 = static_cast<const uint16_t*>(p.w1);
+  const uint16_t* g2 = static_cast<const uint16_t*>(p.w2);
+  const uint16_t* g3 = static_cast<const uint16_t*>(p.w3);
+  constexpr int Kin = C + 16;
+  for (int i = threadIdx.x; i < W * LD1; i += kMlpThreads) {
+    const int r = i / LD1, k = i % LD1;
+    w1[i] = k < Kin ? g1[r * Kin + k] : (uint16_t)0;
+  }
+  for (int i = threadIdx.x; i < W * LD2; i += kMlpThreads) {
+    const int r = i / LD2, q = i % LD2;
+    w2[i] = q < W ? g2[r * W + hidden_unit(q)] : (uint16_t)0;
+  }
+  for (int i = threadIdx.x; i < 16 * LD2; i += kMlpThreads) {
+    const int r = i / LD2, q = i % LD2;
+    w3[i] = (r < 3 && q < W) ? g3[r * W + hidden_unit(q)] : (uint16_t)0;
+  }
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  uint16_t* xrow = lds + S::X + (threadIdx.x >> 6) * 64 * LD1;  // this wave's 64 pixel rows
+  // zero tail of the pixel rows (channels C + 16 .. K1 - 1), written once
+  for (int k = Kin; k < K1; k++) xrow[lane * LD1 + k] = 0;
+  __syncthreads();
+
+  // pixel indices and byte offsets fit 32 bits (checked by the launcher)
+  const uint32_t N = (uint32_t)p.N;
+  const uint32_t ntile = (N + 63) / 64;
+  const uint32_t wave = blockIdx.x * kMlp32Waves + (threadIdx.x >> 6);
+  const uint32_t nwaves = gridDim.x * kMlp32Waves;
+  const mlp_i32x4 rsrc = feat_rsrc(p.feat);
+  const uint32_t cs4 = (uint32_t)p.feat_cs * 4u, ns4 = (uint32_t)p.feat_ns * 4u;
+  // Features and alpha of the tile being processed, loaded during the previous
+  // tile (vmcnt counts at most 63 loads in flight, so the next tile's loads
+  // are issued only once nothing of this tile is waited for any more).
+  float f[C];
+  float alpha4[4] = {1.0f, 1.0f, 1.0f, 1.0f};  // lane group 0: its output pixels' alpha
+  auto load_tile = [&](uint32_t tt) {
+    if (p.alpha && grp == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t nj = tt * 64 + 16 * j + col;
+        alpha4[j] = p.alpha[nj < N ? nj : N - 1];
+      }
+    }
+    const uint32_t n0 = tt * 64 + lane;
+    load_features<C>(rsrc, cs4, (n0 < N ? n0 : N - 1) * ns4, f);
+  };
+  if (wave < ntile) load_tile(wave);
+  for (uint32_t t = wave; t < ntile; t += nwaves) {
+    const uint32_t n = t * 64 + lane;
+    const uint32_t nn = n < N ? n : N - 1;
+    float dx, dy, dz;
+    pixel_dir32(p, nn, dx, dy, dz);
+    float sh[16];
+    sh16(dx, dy, dz, sh);
+    uint4* row4 = reinterpret_cast<uint4*>(xrow + lane * LD1);
+#pragma unroll
+    for (int q = 0; q < C / 8; q++)
+      row4[q] = make_uint4(pack2(to16<kBF16>(f[8 * q + 0]), to16<kBF16>(f[8 * q + 1])),
+                           pack2(to16<kBF16>(f[8 * q + 2]), to16<kBF16>(f[8 * q + 3])),
+                           pack2(to16<kBF16>(f[8 * q + 4]), to16<kBF16>(f[8 * q + 5])),
+                           pack2(to16<kBF16>(f[8 * q + 6]), to16<kBF16>(f[8 * q + 7])));
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+      row4[C / 8 + q] = make_uint4(pack2(to16<kBF16>(sh[8 * q + 0]), to16<kBF16>(sh[8 * q + 1])),
+                                   pack2(to16<kBF16>(sh[8 * q + 2]), to16<kBF16>(sh[8 * q + 3])),
+                                   pack2(to16<kBF16>(sh[8 * q + 4]), to16<kBF16>(sh[8 * q + 5])),
+                                   pack2(to16<kBF16>(sh[8 * q + 6]), to16<kBF16>(sh[8 * q + 7])));
+    const float a_out[4] = {alpha4[0], alpha4[1], alpha4[2], alpha4[3]};
+    // the next tile's features and alpha are in flight during this tile's contraction
+    if (t + nwaves < ntile) load_tile(t + nwaves);
+    __builtin_amdgcn_wave_barrier();
+    // layer 1: 4 N-tiles of 16 pixels
+    f32x4 acc1[NT][4];
+#pragma unroll
+    for (int mt = 0; mt < NT; mt++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc1[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < K1 / 32; kc++) {
+      uint4 b[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) b[j] = *reinterpret_cast<const uint4*>(xrow + (16 * j + col) * LD1 + 32 * kc + 8 * grp);
+#pragma unroll
+      for (int mt = 0; mt < NT; mt++) {
+        const uint4 a = *reinterpret_cast<const uint4*>(w1 + (16 * mt + col) * LD1 + 32 * kc + 8 * grp);
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc1[mt][j] = mfma32<kBF16>(a, b[j], acc1[mt][j]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the rows are read; the next tile may overwrite them
+    // layer 2
+    f32x4 acc2[NT][4];
+#pragma unroll
+    for (int mt = 0; mt < NT; mt++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc2[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < NT / 2; kc++) {
+      uint4 b[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) b[j] = relu_pack8<kBF16>(acc1[2 * kc][j], acc1[2 * kc + 1][j]);
+#pragma unroll
+      for (int mt = 0; mt < NT; mt++) {
+        const uint4 a = *reinterpret_cast<const uint4*>(w2 + (16 * mt + col) * LD2 + 32 * kc + 8 * grp);
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc2[mt][j] = mfma32<kBF16>(a, b[j], acc2[mt][j]);
+      }
+    }
+    // layer 3: rows 0-2 of one M-tile are the RGB logits
+    f32x4 acc3[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc3[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < NT / 2; kc++) {
+      const uint4 a = *reinterpret_cast<const uint4*>(w3 + col * LD2 + 32 * kc + 8 * grp);
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc3[j] = mfma32<kBF16>(a, relu_pack8<kBF16>(acc2[2 * kc][j], acc2[2 * kc + 1][j]), acc3[j]);
+    }
+    if (grp == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t nj = t * 64 + 16 * j + col;
+        if (nj < N) {
+#pragma unroll
+          for (int o = 0; o < 3; o++)
+            p.out[o * p.out_os + (int64_t)nj * p.out_ns] = finish_rgb_alpha(p, a_out[j], acc3[j][o], o);
+        }
+      }
+    }
+  }
+}
+
+// The 16x16x32 kernel addresses pixels and feature bytes with 32 bits.
+static bool mlp32_fits(const MlpParams& p, int C) {
+  const uint64_t maxoff = ((uint64_t)(C - 1) * (uint64_t)p.feat_cs + (uint64_t)(p.N - 1) * (uint64_t)p.feat_ns) * 4u;
+  return p.N < (1ll << 31) - 64 && p.feat_cs >= 0 && p.feat_ns >= 0 && maxoff < 0xffffffffull;
+}
+
+template <int NT, bool kBF16, int C>
+static hipError_t launch_mfma32(const MlpParams& p, hipStream_t s) {
+  const size_t lds = sizeof(uint16_t) * (size_t)Mlp32Shape<C, NT>::TOTAL;
+  const int64_t ntile = (p.N + 63) / 64;
+  const int64_t want = (ntile + kMlp32Waves - 1) / kMlp32Waves;
+  const unsigned blocks = (unsigned)(want < 1024 ? (want > 0 ? want : 1) : 1024);
+  hipLaunchKernelGGL((mlp_mfma32_kernel<NT, kBF16, C>), dim3(blocks), dim3(kMlpThreads), lds, s, p);
+  return hipGetLastError();
+}
+
 // float32 path on the vector ALU: one lane per pixel, weights in LDS.
 template <int NW>
 __global__ void __launch_bounds__(kMlpThreads) mlp_f32_kernel(const MlpParams p) {
@@ -326,6 +602,16 @@ static hipError_t launch_f32(const MlpParams& p, hipStream_t s) {
 
 template <bool kBF16>
 static hipError_t launch_mfma_width(const MlpParams& p, hipStream_t s) {
+  // 16, 32 or 64 channels at width 32 or 64: the 16x16x32 kernel
+  if ((p.width == 64 || p.width == 32) && mlp32_fits(p, p.C)) {
+    const bool w64 = p.width == 64;
+    switch (p.C) {
+      case 16: return w64 ? launch_mfma32<4, kBF16, 16>(p, s) : launch_mfma32<2, kBF16, 16>(p, s);
+      case 32: return w64 ? launch_mfma32<4, kBF16, 32>(p, s) : launch_mfma32<2, kBF16, 32>(p, s);
+      case 64: return w64 ? launch_mfma32<4, kBF16, 64>(p, s) : launch_mfma32<2, kBF16, 64>(p, s);
+      default: break;
+    }
+  }
   switch (p.width) {
     case 32: return launch_mfma<2, kBF16>(p, s);
     case 64: return launch_mfma<4, kBF16>(p, s);

@@ -8,8 +8,17 @@
 // scales, normalisation for rotations, sigmoid for opacities, with nest_expf
 // so that the decoded splats are reproducible on the host.
 //
-// One lane per splat: the stage indices come in as one 8-byte load, every
-// codebook row as one dim*4-byte load (the 448 KiB of codebooks stay in L2).
+// Two kernels:
+//  - rvq_lds_kernel (one launch per attribute, a stage's codebook of at most
+//    64 KiB): a workgroup owns 256 * NS splats, keeps their partial sums in
+//    registers, and for each stage copies that stage's codebook into LDS with
+//    direct-to-LDS loads and gathers its rows from there.  Random 16-byte rows gathered straight from
+//    L2 cost ~146 CU-cycles per 64-lane load instruction on gfx950 (the L2 to
+//    L1 path returns whole lines), so the LDS copy (one coalesced stream of
+//    the codebook per workgroup and stage) is what lets the decode run at HBM
+//    speed on the indices and outputs;
+//  - rvq_kernel / rvq_batch_kernel (any shape): one lane per splat, one row
+//    load per stage from the L2-resident codebooks.
 #include "nest_internal.h"
 #include "nest_math.h"
 
@@ -29,24 +38,10 @@ __device__ __forceinline__ void load_row(const float* cb, size_t row, float v[DI
   }
 }
 
-template <int DIM>
-__device__ __forceinline__ void rvq_one(const RvqParams& p, int64_t i) {
-  float v[DIM];
-  const uint16_t* idx = p.idx + i * p.stages;
-  bool bad = false;
-  for (int s = 0; s < p.stages; s++) {
-    const uint32_t k = idx[s];
-    float c[DIM];
-    if (k < (uint32_t)p.K) {
-      load_row<DIM>(p.cb, (size_t)s * p.K + k, c);
-    } else {
-      bad = true;
-#pragma unroll
-      for (int d = 0; d < DIM; d++) c[d] = 0.0f;
-    }
-#pragma unroll
-    for (int d = 0; d < DIM; d++) v[d] = (s == 0) ? c[d] : v[d] + c[d];
-  }
+// Bias, optional raw copy, activation and store of splat i's stage sum v
+// (kVec: one 8/16-byte store, out aligned to 16 bytes).
+template <int DIM, bool kVec>
+__device__ __forceinline__ void rvq_finish(const RvqParams& p, int64_t i, float v[DIM], bool bad) {
   if (bad) {
 #pragma unroll
     for (int d = 0; d < DIM; d++) v[d] = __int_as_float(0x7fc00000);
@@ -73,8 +68,35 @@ __device__ __forceinline__ void rvq_one(const RvqParams& p, int64_t i) {
 #pragma unroll
     for (int d = 0; d < DIM; d++) v[d] = 1.0f / (1.0f + expf_ref(-v[d]));
   }
+  if constexpr (kVec && DIM == 4) {
+    reinterpret_cast<float4*>(p.out)[i] = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (kVec && DIM == 2) {
+    reinterpret_cast<float2*>(p.out)[i] = make_float2(v[0], v[1]);
+  } else {
 #pragma unroll
-  for (int d = 0; d < DIM; d++) p.out[i * DIM + d] = v[d];
+    for (int d = 0; d < DIM; d++) p.out[i * DIM + d] = v[d];
+  }
+}
+
+template <int DIM>
+__device__ __forceinline__ void rvq_one(const RvqParams& p, int64_t i) {
+  float v[DIM];
+  const uint16_t* idx = p.idx + i * p.stages;
+  bool bad = false;
+  for (int s = 0; s < p.stages; s++) {
+    const uint32_t k = idx[s];
+    float c[DIM];
+    if (k < (uint32_t)p.K) {
+      load_row<DIM>(p.cb, (size_t)s * p.K + k, c);
+    } else {
+      bad = true;
+#pragma unroll
+      for (int d = 0; d < DIM; d++) c[d] = 0.0f;
+    }
+#pragma unroll
+    for (int d = 0; d < DIM; d++) v[d] = (s == 0) ? c[d] : v[d] + c[d];
+  }
+  rvq_finish<DIM, false>(p, i, v, bad);
 }
 
 template <int DIM>
@@ -99,8 +121,126 @@ __global__ void __launch_bounds__(256) rvq_batch_kernel(const RvqBatch b) {
   }
 }
 
+// LDS-staged decode of one attribute with 4 stages (indices as one 8-byte
+// load per splat) and K * DIM a multiple of 4.  Splat n of the workgroup's
+// chunk is base + n * 256 + t, so index loads and output stores coalesce.
+constexpr int kRvqThreads = 256;
+
+template <int DIM>
+__device__ __forceinline__ void lds_row(const float* cb, uint32_t k, float c[DIM]) {
+  if constexpr (DIM == 4) {
+    const float4 a = reinterpret_cast<const float4*>(cb)[k];
+    c[0] = a.x; c[1] = a.y; c[2] = a.z; c[3] = a.w;
+  } else if constexpr (DIM == 2) {
+    const float2 a = reinterpret_cast<const float2*>(cb)[k];
+    c[0] = a.x; c[1] = a.y;
+  } else {
+#pragma unroll
+    for (int d = 0; d < DIM; d++) c[d] = cb[k * DIM + d];
+  }
+}
+
+// A stage's codebook is at most 4096 16-byte chunks (64 KiB), a multiple of
+// 64 chunks; each wave copies its 64-chunk runs with direct-to-LDS loads
+// (global_load_lds_dwordx4: lane k's 16 bytes land at the run's LDS address
+// + 16 k), all in flight at once, so a stage costs one L2 round trip.
+constexpr int kRvqMaxChunks = 4096;
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int DIM, int NS>
+__global__ void __launch_bounds__(kRvqThreads) rvq_lds_kernel(const RvqParams p) {
+  extern __shared__ float4 lds_cb4[];
+  const float* lds_cb = reinterpret_cast<const float*>(lds_cb4);
+  const int64_t base = (int64_t)blockIdx.x * (kRvqThreads * NS) + threadIdx.x;
+  const uint32_t K = (uint32_t)p.K;
+  const uint32_t vec4 = K * DIM / 4;  // 16-byte chunks per stage
+  const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  // indices of the chunk's splats (HBM), in flight during the first copy
+  uint2 ix[NS];
+#pragma unroll
+  for (int n = 0; n < NS; n++) {
+    const int64_t i = base + (int64_t)n * kRvqThreads;
+    ix[n] = i < p.P ? reinterpret_cast<const uint2*>(p.idx)[i] : make_uint2(0u, 0u);
+  }
+  const float4* cb4 = reinterpret_cast<const float4*>(p.cb);
+  float v[NS][DIM];
+  bool bad[NS];
+#pragma unroll
+  for (int n = 0; n < NS; n++) bad[n] = false;
+#pragma unroll
+  for (int s = 0; s < 4; s++) {
+    if (s > 0) __syncthreads();  // every lane is done with the previous stage's rows
+    const float4* src = cb4 + (size_t)s * vec4;
+    for (uint32_t c0 = 64u * wid; c0 < vec4; c0 += 64u * (kRvqThreads / 64))
+      __builtin_amdgcn_global_load_lds(src + c0 + lane, (lds_void*)(lds_cb4 + c0), 16, 0, 0);
+    __syncthreads();  // waits for the wave's direct loads, then for every wave
+#pragma unroll
+    for (int n = 0; n < NS; n++) {
+      const uint32_t w = (s < 2) ? ix[n].x : ix[n].y;
+      uint32_t k = (s & 1) ? (w >> 16) : (w & 0xffffu);
+      if (k >= K) {
+        bad[n] = true;
+        k = 0u;
+      }
+      float c[DIM];
+      lds_row<DIM>(lds_cb, k, c);
+#pragma unroll
+      for (int d = 0; d < DIM; d++) v[n][d] = (s == 0) ? c[d] : v[n][d] + c[d];
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < NS; n++) {
+    const int64_t i = base + (int64_t)n * kRvqThreads;
+    if (i < p.P) rvq_finish<DIM, true>(p, i, v[n], bad[n]);
+  }
+}
+
+// The LDS path applies to 4-stage attributes whose stage codebook is whole
+// runs of 64 16-byte chunks and fits 64 KiB (K * dim % 256 == 0), with
+// aligned codebooks, indices and outputs.
+bool rvq_lds_ok(const RvqParams& p) {
+  const size_t stage_bytes = (size_t)p.K * p.dim * sizeof(float);
+  return p.stages == 4 && (p.dim == 1 || p.dim == 2 || p.dim == 4) && stage_bytes <= (size_t)kRvqMaxChunks * 16 &&
+         ((size_t)p.K * p.dim) % 256 == 0 && (reinterpret_cast<uintptr_t>(p.cb) & 15u) == 0 &&
+         (reinterpret_cast<uintptr_t>(p.idx) & 7u) == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15u) == 0;
+}
+
+// Splats per lane: the most that keeps at least 512 workgroups (two per CU),
+// capped per dimension so the partial sums fit the registers.
+template <int DIM>
+static hipError_t launch_rvq_lds_dim(const RvqParams& p, hipStream_t s) {
+  const size_t lds = (size_t)p.K * DIM * sizeof(float);
+  constexpr int kMax = DIM == 4 ? 8 : 16;
+  int ns = kMax;
+  while (ns > 2 && (p.P + (int64_t)kRvqThreads * ns - 1) / ((int64_t)kRvqThreads * ns) < 512) ns /= 2;
+  const int64_t chunk = (int64_t)kRvqThreads * ns;
+  const dim3 grid((unsigned)((p.P + chunk - 1) / chunk));
+  switch (ns) {
+    case 16:
+      if constexpr (kMax >= 16) {
+        hipLaunchKernelGGL((rvq_lds_kernel<DIM, 16>), grid, dim3(kRvqThreads), lds, s, p);
+        break;
+      }
+      [[fallthrough]];
+    case 8: hipLaunchKernelGGL((rvq_lds_kernel<DIM, 8>), grid, dim3(kRvqThreads), lds, s, p); break;
+    case 4: hipLaunchKernelGGL((rvq_lds_kernel<DIM, 4>), grid, dim3(kRvqThreads), lds, s, p); break;
+    default: hipLaunchKernelGGL((rvq_lds_kernel<DIM, 2>), grid, dim3(kRvqThreads), lds, s, p); break;
+  }
+  return hipGetLastError();
+}
+
+static hipError_t launch_rvq_lds(const RvqParams& p, hipStream_t s) {
+  if (p.P <= 0) return hipSuccess;
+  switch (p.dim) {
+    case 1: return launch_rvq_lds_dim<1>(p, s);
+    case 2: return launch_rvq_lds_dim<2>(p, s);
+    default: return launch_rvq_lds_dim<4>(p, s);
+  }
+}
+
 hipError_t launch_rvq(const RvqParams& p, hipStream_t s) {
   if (p.P <= 0) return hipSuccess;
+  if (rvq_lds_ok(p)) return launch_rvq_lds(p, s);
   const dim3 grid((unsigned)((p.P + 255) / 256));
   switch (p.dim) {
     case 1: hipLaunchKernelGGL(rvq_kernel<1>, grid, dim3(256), 0, s, p); break;
@@ -114,6 +254,16 @@ hipError_t launch_rvq(const RvqParams& p, hipStream_t s) {
 }
 
 hipError_t launch_rvq_batch(const RvqBatch& b, hipStream_t s) {
+  // every attribute on the LDS path: one launch each (their LDS sizes differ)
+  bool all_lds = b.n > 0;
+  for (int k = 0; k < b.n; k++) all_lds = all_lds && rvq_lds_ok(b.a[k]);
+  if (all_lds) {  // one launch per attribute, each with its own codebook's LDS size
+    for (int k = 0; k < b.n; k++) {
+      const hipError_t e = launch_rvq_lds(b.a[k], s);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
   int64_t pmax = 0;
   for (int k = 0; k < b.n; k++) pmax = b.a[k].P > pmax ? b.a[k].P : pmax;
   if (pmax <= 0 || b.n <= 0) return hipSuccess;

@@ -381,4 +381,5 @@ def binning_arrays(res: ForwardResult, W: int, H: int) -> Dict[str, torch.Tensor
                 vals=L.view(res.binning, o[L.BIN_VALS], torch.int32, (n,))[:NR],
                 ranges=L.view(res.image, io[L.IMG_RANGES], torch.int32, (tiles, 2)),
                 final_T=L.view(res.image, io[L.IMG_FINAL_T], torch.float32, (3, H, W)),
-                n_contrib=L.view(res.image, io[L.IMG_N_CONTRIB], torch.int32, (2, H, W)))
+                n_contrib=L.view(res.image, io[L.IMG_N_CONTRIB], torch.int32, (2, H, W)),
+                tile_order=L.view(res.image, io[L.IMG_TILE_ORDER], torch.int32, (tiles,)))

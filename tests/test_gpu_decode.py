@@ -18,12 +18,15 @@ def _rand_dirs(rng, n):
     return (d / np.linalg.norm(d, axis=1, keepdims=True)).astype(np.float32)
 
 
-@pytest.mark.parametrize("C,width,dtype", [(16, 64, "f32"), (32, 64, "f16"), (64, 64, "bf16"), (64, 128, "bf16"),
-                                           (32, 32, "f16"), (64, 64, "f16")])
-def test_mlp_rgb_decode(oracle, C, width, dtype):
+@pytest.mark.parametrize("C,width,dtype,N", [(16, 64, "f32", 3000), (32, 64, "f16", 3000), (64, 64, "bf16", 3000),
+                                             (64, 128, "bf16", 3000), (32, 32, "f16", 3000), (64, 64, "f16", 3000),
+                                             (16, 64, "bf16", 3000), (16, 32, "f16", 1000), (64, 64, "bf16", 1),
+                                             (64, 64, "bf16", 63), (48, 64, "f16", 777)])
+def test_mlp_rgb_decode(oracle, C, width, dtype, N):
+    """Every MFMA path (16x16x32 for 16/32/64 channels at width 32/64, the
+    16x16x16 one for others) and the f32 path, ragged N included."""
     from nest_splat.mlp import NestMLP
-    rng = np.random.default_rng(C * 1000 + width)
-    N = 3000
+    rng = np.random.default_rng(C * 1000 + width + N)
     feat = (rng.standard_normal((N, C)) * 0.3).astype(np.float32)
     dirs = _rand_dirs(rng, N)
     m = NestMLP(C, width, dtype, seed=7).to(DEV)
@@ -165,3 +168,28 @@ def test_rvq_out_of_range_index_is_nan():
     idx = torch.tensor([[0, 1], [9, 0], [7, 7]], dtype=torch.int16, device=DEV)
     out = rvq_decode(cb, idx).cpu().numpy()
     assert np.isnan(out[1]).all() and not np.isnan(out[0]).any() and not np.isnan(out[2]).any()
+
+
+@pytest.mark.parametrize("P,S,K,dim", [(70_001, 4, 4096, 4), (9_999, 4, 4096, 2), (1_000, 4, 512, 1),
+                                       (33_333, 3, 1024, 4), (5_000, 4, 2048, 3), (20_000, 4, 65536, 2)])
+def test_rvq_decode_paths_bit_exact(oracle, P, S, K, dim):
+    """Both decode kernels: the LDS-staged one (4 stages, a stage codebook of
+    at most 64 KiB, dim 1, 2 or 4) and the gather one (other shapes), with
+    ragged P, against the oracle's ordered float32 sum; an out-of-range index
+    in either decodes to NaN."""
+    from nest_splat.rvq import rvq_decode
+    rng = np.random.default_rng(P + K)
+    cb = (0.1 * rng.standard_normal((S, K, dim))).astype(np.float32)
+    idx = rng.integers(0, K, (P, S)).astype(np.uint16)
+    idx[0] = K - 1
+    bad = K < 65536
+    if bad:
+        idx[P // 2, S - 1] = K  # one past the codebook
+    bias = rng.standard_normal(dim).astype(np.float32)
+    out = rvq_decode(torch.from_numpy(cb).to(DEV), torch.from_numpy(idx.view(np.int16)).to(DEV), bias=bias).cpu().numpy()
+    good = np.ones(P, bool)
+    if bad:
+        good[P // 2] = False
+        assert np.isnan(out[P // 2]).all()
+    ref = oracle.rvq_decode(cb, np.where(good[:, None], idx, 0).astype(np.uint16), bias)
+    np.testing.assert_array_equal(out[good], ref[good])

@@ -189,3 +189,25 @@ def test_deterministic_repeat():
     a = run_gpu(sc)
     b = run_gpu(sc)
     assert torch.equal(a.color, b.color) and torch.equal(a.others, b.others)
+
+
+@pytest.mark.parametrize("name", ["cfg1", "unbounded_small", "shells_small"])
+def test_tile_launch_order(name):
+    """The render's launch order is a permutation of the tiles, heaviest
+    first: the buckets of 8 log2(pairs + 1) do not increase along it (float32
+    log2 on the device may put a boundary weight one bucket off)."""
+    from nest_splat import rasterizer as rz
+    sc = scene(name)
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    res = run_gpu(sc)
+    ba = rz.binning_arrays(res, W, H)
+    order = ba["tile_order"].cpu().numpy().astype(np.int64)
+    ranges = ba["ranges"].cpu().numpy().view(np.uint32).astype(np.int64)
+    ntiles = ranges.shape[0]
+    np.testing.assert_array_equal(np.sort(order), np.arange(ntiles))
+    w = ranges[:, 1] - ranges[:, 0]
+    bucket = np.minimum(255, np.floor(8.0 * np.log2(w.astype(np.float64) + 1.0))).astype(np.int64)
+    b = bucket[order]
+    assert np.all(np.diff(b) <= 1) and b[0] >= bucket.max() - 1
+    assert np.all(np.maximum.accumulate(b[::-1])[::-1] <= b + 1)
