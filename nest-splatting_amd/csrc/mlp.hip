@@ -506,8 +506,205 @@ static bool mlp32_fits(const MlpParams& p, int C) {
   return p.N < (1ll << 31) - 64 && p.feat_cs >= 0 && p.feat_ns >= 0 && maxoff < 0xffffffffull;
 }
 
+// Block variant for the contiguous channel-major map the render writes
+// (pixel stride 1, channel stride a multiple of 4, 16-byte aligned): the
+// workgroup takes 256 pixels per iteration, and wave w loads channels
+// [w C/4, (w+1) C/4) of all 256 with one float4 (4 pixels) per lane, so each
+// channel is read as one 1 KiB run (channel-major reads in 256-byte runs
+// stall at ~3.6 TB/s on MI355X, 1 KiB runs reach ~6.1 TB/s).  The waves write
+// the 16-bit features into the shared pixel rows, compute their own pixels'
+// SH terms, and after a barrier each wave runs the three layers on its 64
+// rows as mlp_mfma32_kernel does.  The next block's features are in flight
+// during the contraction.
+template <int NT, bool kBF16, int C>
+__global__ void __launch_bounds__(kMlpThreads) __attribute__((amdgpu_waves_per_eu(2)))
+mlp_block_kernel(const MlpParams p) {
+  using S = Mlp32Shape<C, NT>;
+  constexpr int K1 = S::K1, LD1 = S::LD1, LD2 = S::LD2, W = NT * 16;
+  constexpr int CPW = C / 4;  // channels each wave loads
+  static_assert(NT % 2 == 0 && CPW % 4 == 0, "width multiple of 32, channels multiple of 16");
+  extern __shared__ uint16_t lds[];
+  uint16_t* w1 = lds + S::W1;
+  uint16_t* w2 = lds + S::W2;
+  uint16_t* w3 = lds + S::W3;
+  const uint16_t* g1 = static_cast<const uint16_t*>(p.w1);
+  const uint16_t* g2 = static_cast<const uint16_t*>(p.w2);
+  const uint16_t* g3 = static_cast<const uint16_t*>(p.w3);
+  constexpr int Kin = C + 16;
+  for (int i = threadIdx.x; i < W * LD1; i += kMlpThreads) {
+    const int r = i / LD1, k = i % LD1;
+    w1[i] = k < Kin ? g1[r * Kin + k] : (uint16_t)0;
+  }
+  for (int i = threadIdx.x; i < W * LD2; i += kMlpThreads) {
+    const int r = i / LD2, q = i % LD2;
+    w2[i] = q < W ? g2[r * W + hidden_unit(q)] : (uint16_t)0;
+  }
+  for (int i = threadIdx.x; i < 16 * LD2; i += kMlpThreads) {
+    const int r = i / LD2, q = i % LD2;
+    w3[i] = (r < 3 && q < W) ? g3[r * W + hidden_unit(q)] : (uint16_t)0;
+  }
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  uint16_t* xall = lds + S::X;              // [256 pixels][LD1]
+  uint16_t* xrow = xall + wid * 64 * LD1;   // this wave's 64 pixels
+  for (int k = Kin; k < K1; k++) xrow[lane * LD1 + k] = 0;
+
+  const uint32_t N = (uint32_t)p.N;
+  const uint32_t nblk = (N + 255) / 256;
+  const uint32_t cs = (uint32_t)p.feat_cs;
+  const float* fbase = p.feat + (size_t)(wid * CPW) * cs;  // this wave's first channel
+  float4 fv[CPW];
+  auto load_block = [&](uint32_t b) {
+    const uint32_t n0 = b * 256 + 4 * lane;
+    if (n0 + 3 < N) {
+#pragma unroll
+      for (int j = 0; j < CPW; j++) fv[j] = *reinterpret_cast<const float4*>(fbase + (size_t)j * cs + n0);
+    } else {  // last block: clamp each pixel
+      const uint32_t m0 = n0 < N ? n0 : N - 1, m1 = n0 + 1 < N ? n0 + 1 : N - 1;
+      const uint32_t m2 = n0 + 2 < N ? n0 + 2 : N - 1, m3 = n0 + 3 < N ? n0 + 3 : N - 1;
+#pragma unroll
+      for (int j = 0; j < CPW; j++) {
+        const float* c = fbase + (size_t)j * cs;
+        fv[j] = make_float4(c[m0], c[m1], c[m2], c[m3]);
+      }
+    }
+  };
+  float alpha4[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  auto load_alpha = [&](uint32_t b) {
+    if (p.alpha && grp == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t nj = b * 256 + wid * 64 + 16 * j + col;
+        alpha4[j] = p.alpha[nj < N ? nj : N - 1];
+      }
+    }
+  };
+  if (blockIdx.x < nblk) {
+    load_alpha(blockIdx.x);
+    load_block(blockIdx.x);
+  }
+  for (uint32_t b = blockIdx.x; b < nblk; b += gridDim.x) {
+    __syncthreads();  // the previous block's rows are read (and the weights written)
+    // features: 4 pixel rows per lane, this wave's CPW channels, 4 channels per store
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint16_t* dst = xall + (4 * lane + q) * LD1 + wid * CPW;
+#pragma unroll
+      for (int j = 0; j < CPW; j += 4) {
+        const float v0 = q == 0 ? fv[j].x : q == 1 ? fv[j].y : q == 2 ? fv[j].z : fv[j].w;
+        const float v1 = q == 0 ? fv[j + 1].x : q == 1 ? fv[j + 1].y : q == 2 ? fv[j + 1].z : fv[j + 1].w;
+        const float v2 = q == 0 ? fv[j + 2].x : q == 1 ? fv[j + 2].y : q == 2 ? fv[j + 2].z : fv[j + 2].w;
+        const float v3 = q == 0 ? fv[j + 3].x : q == 1 ? fv[j + 3].y : q == 2 ? fv[j + 3].z : fv[j + 3].w;
+        *reinterpret_cast<uint2*>(dst + j) = make_uint2(pack2(to16<kBF16>(v0), to16<kBF16>(v1)),
+                                                        pack2(to16<kBF16>(v2), to16<kBF16>(v3)));
+      }
+    }
+    // SH terms of this wave's pixels
+    {
+      const uint32_t n = b * 256 + wid * 64 + lane;
+      float dx, dy, dz;
+      pixel_dir32(p, n < N ? n : N - 1, dx, dy, dz);
+      float sh[16];
+      sh16(dx, dy, dz, sh);
+      uint4* row4 = reinterpret_cast<uint4*>(xrow + lane * LD1 + C);
+#pragma unroll
+      for (int q = 0; q < 2; q++)
+        row4[q] = make_uint4(pack2(to16<kBF16>(sh[8 * q + 0]), to16<kBF16>(sh[8 * q + 1])),
+                             pack2(to16<kBF16>(sh[8 * q + 2]), to16<kBF16>(sh[8 * q + 3])),
+                             pack2(to16<kBF16>(sh[8 * q + 4]), to16<kBF16>(sh[8 * q + 5])),
+                             pack2(to16<kBF16>(sh[8 * q + 6]), to16<kBF16>(sh[8 * q + 7])));
+    }
+    const float a_out[4] = {alpha4[0], alpha4[1], alpha4[2], alpha4[3]};
+    if (b + gridDim.x < nblk) {  // next block in flight during the contraction
+      load_alpha(b + gridDim.x);
+      load_block(b + gridDim.x);
+    }
+    // every wave's channels are in the rows: wait for this wave's LDS writes
+    // only (lgkmcnt 0, vmcnt and expcnt at their maxima), not for the block in
+    // flight, then the plain barrier (__syncthreads would also wait for it)
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    // two halves of two 16-pixel N-tiles each, so the accumulators (2 x NT x 2
+    // x 4 floats) leave room for the block in flight
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      f32x4 acc1[NT][2];
+#pragma unroll
+      for (int mt = 0; mt < NT; mt++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc1[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < K1 / 32; kc++) {
+        uint4 bb[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          bb[j] = *reinterpret_cast<const uint4*>(xrow + (16 * (2 * h + j) + col) * LD1 + 32 * kc + 8 * grp);
+#pragma unroll
+        for (int mt = 0; mt < NT; mt++) {
+          const uint4 a = *reinterpret_cast<const uint4*>(w1 + (16 * mt + col) * LD1 + 32 * kc + 8 * grp);
+#pragma unroll
+          for (int j = 0; j < 2; j++) acc1[mt][j] = mfma32<kBF16>(a, bb[j], acc1[mt][j]);
+        }
+      }
+      f32x4 acc2[NT][2];
+#pragma unroll
+      for (int mt = 0; mt < NT; mt++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc2[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < NT / 2; kc++) {
+        uint4 bb[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) bb[j] = relu_pack8<kBF16>(acc1[2 * kc][j], acc1[2 * kc + 1][j]);
+#pragma unroll
+        for (int mt = 0; mt < NT; mt++) {
+          const uint4 a = *reinterpret_cast<const uint4*>(w2 + (16 * mt + col) * LD2 + 32 * kc + 8 * grp);
+#pragma unroll
+          for (int j = 0; j < 2; j++) acc2[mt][j] = mfma32<kBF16>(a, bb[j], acc2[mt][j]);
+        }
+      }
+      f32x4 acc3[2];
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc3[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < NT / 2; kc++) {
+        const uint4 a = *reinterpret_cast<const uint4*>(w3 + col * LD2 + 32 * kc + 8 * grp);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          acc3[j] = mfma32<kBF16>(a, relu_pack8<kBF16>(acc2[2 * kc][j], acc2[2 * kc + 1][j]), acc3[j]);
+      }
+      if (grp == 0) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          const uint32_t nj = b * 256 + wid * 64 + 16 * (2 * h + j) + col;
+          if (nj < N) {
+#pragma unroll
+            for (int o = 0; o < 3; o++)
+              p.out[o * p.out_os + (int64_t)nj * p.out_ns] = finish_rgb_alpha(p, a_out[2 * h + j], acc3[j][o], o);
+          }
+        }
+      }
+    }
+  }
+}
+
+static bool mlp_block_fits(const MlpParams& p) {
+  return p.feat_ns == 1 && p.feat_cs % 4 == 0 && (reinterpret_cast<uintptr_t>(p.feat) & 15u) == 0 &&
+         p.N < (1ll << 31) - 256 && (uint64_t)p.feat_cs < (1ull << 31);
+}
+
+template <int NT, bool kBF16, int C>
+static hipError_t launch_block(const MlpParams& p, hipStream_t s) {
+  const size_t lds = sizeof(uint16_t) * (size_t)Mlp32Shape<C, NT>::TOTAL;
+  const int64_t nblk = (p.N + 255) / 256;
+  const unsigned blocks = (unsigned)(nblk < 512 ? (nblk > 0 ? nblk : 1) : 512);
+  hipLaunchKernelGGL((mlp_block_kernel<NT, kBF16, C>), dim3(blocks), dim3(kMlpThreads), lds, s, p);
+  return hipGetLastError();
+}
+
 template <int NT, bool kBF16, int C>
 static hipError_t launch_mfma32(const MlpParams& p, hipStream_t s) {
+  if (mlp_block_fits(p)) return launch_block<NT, kBF16, C>(p, s);
   const size_t lds = sizeof(uint16_t) * (size_t)Mlp32Shape<C, NT>::TOTAL;
   const int64_t ntile = (p.N + 63) / 64;
   const int64_t want = (ntile + kMlp32Waves - 1) / kMlp32Waves;

@@ -193,3 +193,26 @@ def test_rvq_decode_paths_bit_exact(oracle, P, S, K, dim):
         assert np.isnan(out[P // 2]).all()
     ref = oracle.rvq_decode(cb, np.where(good[:, None], idx, 0).astype(np.uint16), bias)
     np.testing.assert_array_equal(out[good], ref[good])
+
+
+@pytest.mark.parametrize("C,width,dtype", [(16, 64, "bf16"), (32, 32, "f16"), (64, 64, "bf16"), (64, 32, "f16"),
+                                           (64, 128, "bf16")])
+def test_mlp_decode_image_blocks(oracle, C, width, dtype):
+    """decode_image on the render's contiguous [C, H, W] map (the 256-pixel
+    block kernel for widths 32 and 64, a partial last block), with a mask and
+    white background, against the oracle."""
+    from nest_splat.camera import look_at, view_ray_matrix
+    from nest_splat.mlp import NestMLP
+    rng = np.random.default_rng(C + width)
+    H, W = 24, 37  # 888 pixels: three full blocks and a partial one
+    color = (rng.standard_normal((C, H, W)) * 0.25).astype(np.float32)
+    alpha = rng.uniform(0, 1, (H, W)).astype(np.float32)
+    alpha[rng.uniform(size=(H, W)) < 0.2] = 0.0
+    m = NestMLP(C, width, dtype, seed=C).to(DEV)
+    cam = look_at((0.5, -3, 0.8), (0, 0, 0), 55.0, W, H)
+    bg = np.array([1.0, 1.0, 1.0], np.float32)
+    img = m.decode_image(torch.from_numpy(color).to(DEV), view_ray_matrix(cam), alpha=torch.from_numpy(alpha).to(DEV),
+                         bg=torch.from_numpy(bg)).cpu().numpy()
+    ref = oracle.mlp(color.reshape(C, -1), oracle.ray_dirs(cam), alpha.reshape(-1), m.W1.detach().cpu().numpy(),
+                     m.W2.detach().cpu().numpy(), m.W3.detach().cpu().numpy(), dtype, bg).reshape(3, H, W)
+    np.testing.assert_allclose(img, ref, atol=1e-3, rtol=0)
