@@ -176,8 +176,10 @@ __device__ __forceinline__ void hashed_corners(const uint32_t g[3], uint32_t idx
   for (int k = 0; k < 8; k++) idx[k] = ab[k & 3] ^ c[k >> 2];
 }
 
+// Dense levels have res1^3 <= the level size < 2^32, so res1, res1^2 and the
+// cell coordinates fit 24 bits: two v_mad_u32_u24 instead of v_mul_lo_u32.
 __device__ __forceinline__ void dense_corners(const uint32_t g[3], uint32_t res1, uint32_t r2, uint32_t idx[8]) {
-  const uint32_t base = g[0] + g[1] * res1 + g[2] * r2;
+  const uint32_t base = g[0] + __umul24(g[1], res1) + __umul24(g[2], r2);
 #pragma unroll
   for (int k = 0; k < 8; k++) idx[k] = base + ((k & 1) ? 1u : 0u) + ((k & 2) ? res1 : 0u) + ((k & 4) ? r2 : 0u);
 }

@@ -161,8 +161,12 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
     nlev = hl[wslot][col];
   }
   float wd[kQueue];
+  const float4* own[kQueue];  // this lane's queue slots, oldest first
 #pragma unroll
-  for (int d = 0; d < kQueue; d++) wd[d] = d < take ? hq[(qhead + d) & (kQueue - 1)][threadIdx.x].w : 0.0f;
+  for (int d = 0; d < kQueue; d++) {
+    own[d] = &hq[(qhead + d) & (kQueue - 1)][threadIdx.x];
+    wd[d] = d < take ? own[d]->w : 0.0f;
+  }
   __builtin_amdgcn_wave_barrier();
   // Software-pipelined over levels: level l+1's gathers are issued as soon as
   // level l is interpolated (its load registers are free then), so they are
@@ -201,7 +205,7 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
 #pragma unroll
     for (int d = 0; d < kQueue; d++) {
       if (d < take) {
-        const float4 r = hq[(qhead + d) & (kQueue - 1)][threadIdx.x];
+        const float4 r = *own[d];
         const float rv[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
         for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(rv[f], wd[d], acc[l * F + f]);
