@@ -253,7 +253,212 @@ hipError_t launch_rvq(const RvqParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Fused, persistent decode of several attributes (all 4-stage, on the LDS
+// path's shapes): one 1024-thread workgroup per CU (16 waves sharing 128 KiB of LDS), the
+// workgroups split between the attributes in proportion to their HBM bytes
+// (8-byte index row plus the output row per splat).  An attribute whose four
+// stage codebooks fit 128 KiB (dim 1 and 2 at 4096 entries) copies them into
+// LDS once per workgroup and keeps them there for all its chunks.  One whose
+// stage pairs fit (dim 4: 2 x 64 KiB) holds one pair at a time and
+// alternates the pair order from chunk to chunk, so each chunk copies one
+// pair, not four stages: an even-numbered chunk gathers stages 0-1 then 2-3,
+// an odd one 2-3 (rows kept) then 0-1.  Either way the value is
+// ((c0 + c1) + c2) + c3 in that order, as the per-splat kernels sum it.  The
+// next chunk's indices are loaded while the current chunk is decoded.
+constexpr int kRvqFusedThreads = 1024;
+constexpr int kRvqFusedNS = 8;                 // splats per lane and chunk
+constexpr int kRvqFusedChunks = 8192;          // 16-byte LDS chunks per workgroup (128 KiB)
+
+struct RvqFused {
+  RvqParams a[kRvqBatchMax];
+  int n;
+  int wg_first[kRvqBatchMax + 1];  // workgroups [wg_first[k], wg_first[k + 1]) decode attribute k
+};
+
+// Copies `chunks` 16-byte chunks (a multiple of 64) from src to the LDS
+// array with direct-to-LDS loads, 64 per wave instruction, all in flight.
+__device__ __forceinline__ void rvq_copy_lds(const float4* src, uint32_t chunks, float4* lds) {
+  const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  for (uint32_t c0 = 64u * wid; c0 < chunks; c0 += 64u * (kRvqFusedThreads / 64))
+    __builtin_amdgcn_global_load_lds(src + c0 + lane, (lds_void*)(lds + c0), 16, 0, 0);
+}
+
+// Stage s's codebook index in a splat's index row (four u16 in a uint2);
+// an index of K or more reads row 0 and marks the splat bad.
+__device__ __forceinline__ uint32_t rvq_stage_index(uint2 w, int s, uint32_t K, bool& bad) {
+  const uint32_t x = (s < 2) ? w.x : w.y;
+  const uint32_t k = (s & 1) ? (x >> 16) : (x & 0xffffu);
+  if (k >= K) {
+    bad = true;
+    return 0u;
+  }
+  return k;
+}
+
+// Index rows of chunk c (zeros past the end).
+template <int NS>
+__device__ __forceinline__ void rvq_load_ix(const uint2* idx2, int64_t P, int64_t c, int64_t nchunks, uint2 (&ix)[NS]) {
+  const int64_t chunk = (int64_t)kRvqFusedThreads * NS;
+#pragma unroll
+  for (int n = 0; n < NS; n++) {
+    const int64_t i = c * chunk + (int64_t)n * kRvqFusedThreads + threadIdx.x;
+    ix[n] = (c < nchunks && i < P) ? idx2[i] : make_uint2(0u, 0u);
+  }
+}
+
+template <int DIM>
+__device__ void rvq_fused_attr(const RvqParams& p, int wg, int nwg, float4* lds4) {
+  constexpr int NS = kRvqFusedNS;
+  const float* lds = reinterpret_cast<const float*>(lds4);
+  const uint32_t K = (uint32_t)p.K;
+  const uint32_t vec4 = K * DIM / 4;  // 16-byte chunks per stage
+  const float* st1 = lds + (size_t)vec4 * 4;  // second stage of a pair
+  const bool resident = 4u * vec4 <= (uint32_t)kRvqFusedChunks;
+  const int64_t chunk = (int64_t)kRvqFusedThreads * NS;
+  const int64_t nchunks = (p.P + chunk - 1) / chunk;
+  const float4* cb4 = reinterpret_cast<const float4*>(p.cb);
+  const uint2* idx2 = reinterpret_cast<const uint2*>(p.idx);
+  uint2 ixn[NS];
+  rvq_load_ix<NS>(idx2, p.P, wg, nchunks, ixn);
+  if (resident) {
+    rvq_copy_lds(cb4, 4u * vec4, lds4);
+    __syncthreads();
+  }
+  int held = -1;  // stage pair in LDS (pair mode): 0 = stages 0-1, 1 = stages 2-3
+  for (int64_t c = wg; c < nchunks; c += nwg) {
+    uint2 ix[NS];
+#pragma unroll
+    for (int n = 0; n < NS; n++) ix[n] = ixn[n];
+    rvq_load_ix<NS>(idx2, p.P, c + nwg, nchunks, ixn);
+    bool bad[NS];
+    float v[NS][DIM];
+#pragma unroll
+    for (int n = 0; n < NS; n++) bad[n] = false;
+    if (resident) {
+#pragma unroll
+      for (int n = 0; n < NS; n++) {
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+          float r[DIM];
+          lds_row<DIM>(lds + (size_t)st * vec4 * 4, rvq_stage_index(ix[n], st, K, bad[n]), r);
+#pragma unroll
+          for (int d = 0; d < DIM; d++) v[n][d] = (st == 0) ? r[d] : v[n][d] + r[d];
+        }
+      }
+    } else if (held == 1) {
+      // stages 2-3 first, their rows kept; then stages 0-1 and the ordered sum
+      float r2[NS][DIM], r3[NS][DIM];
+#pragma unroll
+      for (int n = 0; n < NS; n++) {
+        lds_row<DIM>(lds, rvq_stage_index(ix[n], 2, K, bad[n]), r2[n]);
+        lds_row<DIM>(st1, rvq_stage_index(ix[n], 3, K, bad[n]), r3[n]);
+      }
+      __syncthreads();
+      rvq_copy_lds(cb4, 2u * vec4, lds4);
+      __syncthreads();
+      held = 0;
+#pragma unroll
+      for (int n = 0; n < NS; n++) {
+        float r0[DIM], r1[DIM];
+        lds_row<DIM>(lds, rvq_stage_index(ix[n], 0, K, bad[n]), r0);
+        lds_row<DIM>(st1, rvq_stage_index(ix[n], 1, K, bad[n]), r1);
+#pragma unroll
+        for (int d = 0; d < DIM; d++) v[n][d] = ((r0[d] + r1[d]) + r2[n][d]) + r3[n][d];
+      }
+    } else {
+      // stages 0-1 (copied unless held), then 2-3
+      if (held != 0) {
+        __syncthreads();
+        rvq_copy_lds(cb4, 2u * vec4, lds4);
+        __syncthreads();
+      }
+#pragma unroll
+      for (int n = 0; n < NS; n++) {
+        float r0[DIM], r1[DIM];
+        lds_row<DIM>(lds, rvq_stage_index(ix[n], 0, K, bad[n]), r0);
+        lds_row<DIM>(st1, rvq_stage_index(ix[n], 1, K, bad[n]), r1);
+#pragma unroll
+        for (int d = 0; d < DIM; d++) v[n][d] = r0[d] + r1[d];
+      }
+      __syncthreads();
+      rvq_copy_lds(cb4 + 2u * vec4, 2u * vec4, lds4);
+      __syncthreads();
+      held = 1;
+#pragma unroll
+      for (int n = 0; n < NS; n++) {
+        float r2[DIM], r3[DIM];
+        lds_row<DIM>(lds, rvq_stage_index(ix[n], 2, K, bad[n]), r2);
+        lds_row<DIM>(st1, rvq_stage_index(ix[n], 3, K, bad[n]), r3);
+#pragma unroll
+        for (int d = 0; d < DIM; d++) v[n][d] = (v[n][d] + r2[d]) + r3[d];
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < NS; n++) {
+      const int64_t i = c * chunk + (int64_t)n * kRvqFusedThreads + threadIdx.x;
+      if (i < p.P) rvq_finish<DIM, true>(p, i, v[n], bad[n]);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kRvqFusedThreads, 1) rvq_fused_kernel(const RvqFused f) {
+  __shared__ float4 lds[kRvqFusedChunks];
+  int a = 0;
+  while (a + 1 < f.n && (int)blockIdx.x >= f.wg_first[a + 1]) a++;
+  const RvqParams& p = f.a[a];
+  const int wg = (int)blockIdx.x - f.wg_first[a], nwg = f.wg_first[a + 1] - f.wg_first[a];
+  switch (p.dim) {
+    case 1: rvq_fused_attr<1>(p, wg, nwg, lds); break;
+    case 2: rvq_fused_attr<2>(p, wg, nwg, lds); break;
+    default: rvq_fused_attr<4>(p, wg, nwg, lds); break;
+  }
+}
+
+// The fused path takes attributes on the LDS path's shapes whose stage pair
+// fits 128 KiB.
+static bool rvq_fused_ok(const RvqParams& p) {
+  return rvq_lds_ok(p) && 2ull * (size_t)p.K * p.dim * sizeof(float) <= (size_t)kRvqFusedChunks * 16;
+}
+
+static int rvq_device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
 hipError_t launch_rvq_batch(const RvqBatch& b, hipStream_t s) {
+  // every attribute on the fused path: one persistent launch, one workgroup
+  // per CU, split by HBM bytes (at least one workgroup per non-empty
+  // attribute, none beyond its chunk count)
+  bool all_fused = b.n > 0;
+  for (int k = 0; k < b.n; k++) all_fused = all_fused && rvq_fused_ok(b.a[k]);
+  if (all_fused) {
+    RvqFused f{};
+    f.n = b.n;
+    double total = 0.0;
+    for (int k = 0; k < b.n; k++) {
+      f.a[k] = b.a[k];
+      total += (double)b.a[k].P * (8 + 4 * b.a[k].dim);
+    }
+    if (total <= 0.0) return hipSuccess;
+    const int cus = rvq_device_cus();
+    int next = 0;
+    for (int k = 0; k < b.n; k++) {
+      const RvqParams& p = b.a[k];
+      const int64_t chunks =
+          (p.P + (int64_t)kRvqFusedThreads * kRvqFusedNS - 1) / ((int64_t)kRvqFusedThreads * kRvqFusedNS);
+      int64_t g = (int64_t)((double)cus * (double)p.P * (8 + 4 * p.dim) / total + 0.5);
+      g = chunks <= 0 ? 0 : (g < 1 ? 1 : (g > chunks ? chunks : g));
+      f.wg_first[k] = next;
+      next += (int)g;
+    }
+    f.wg_first[b.n] = next;
+    if (next == 0) return hipSuccess;
+    hipLaunchKernelGGL(rvq_fused_kernel, dim3((unsigned)next), dim3(kRvqFusedThreads), 0, s, f);
+    return hipGetLastError();
+  }
   // every attribute on the LDS path: one launch each (their LDS sizes differ)
   bool all_lds = b.n > 0;
   for (int k = 0; k < b.n; k++) all_lds = all_lds && rvq_lds_ok(b.a[k]);

@@ -162,6 +162,46 @@ def test_rvq_decode_bit_exact(oracle):
     np.testing.assert_array_equal(dec["opacity"].cpu().numpy()[:, 0], op)
 
 
+@pytest.mark.parametrize("P,K_scale,K_rot,K_op", [(1_000_003, 4096, 4096, 4096), (300_001, 4096, 1024, 512),
+                                                   (2_047, 4096, 4096, 4096)])
+def test_rvq_batch_fused_bit_exact(oracle, P, K_scale, K_rot, K_op):
+    """The fused persistent batch decode: ragged P; at 1M splats each
+    workgroup decodes several chunks, so the rotation codebook (4096 x 4,
+    held one stage pair at a time) is gathered in both pair orders, while
+    the scale and opacity codebooks stay resident; a 1024-entry rotation
+    codebook is resident too.  Raw sums and activations against the oracle's
+    ordered float32 sum, an out-of-range index per attribute decoding to NaN."""
+    from nest_splat.rvq import RVQAttributes
+    from nest_splat.scene import RVQ_BIAS
+    rng = np.random.default_rng(P)
+    S = 4
+    dims = {"scale": (2, K_scale), "rotation": (4, K_rot), "opacity": (1, K_op)}
+    cbs = {a: (0.1 * rng.standard_normal((S, K, d))).astype(np.float32) for a, (d, K) in dims.items()}
+    idxs = {a: rng.integers(0, K, (P, S)).astype(np.uint16) for a, (d, K) in dims.items()}
+    badrow = {"scale": P // 3, "rotation": P - 1, "opacity": 1}
+    for a, (d, K) in dims.items():
+        idxs[a][0] = K - 1
+        idxs[a][badrow[a], a == "rotation" and 3 or 1] = K
+    dec = RVQAttributes.from_numpy(cbs, idxs, RVQ_BIAS, DEV).decode(raw=True)
+    torch.cuda.synchronize()
+    for a, (d, K) in dims.items():
+        got = dec[a + "_raw"].cpu().numpy()
+        assert np.isnan(got[badrow[a]]).all()
+        good = np.ones(P, bool)
+        good[badrow[a]] = False
+        ref = oracle.rvq_decode(cbs[a], np.where(good[:, None], idxs[a], 0).astype(np.uint16), RVQ_BIAS[a])
+        np.testing.assert_array_equal(got[good], ref[good])
+        act = dec[a].cpu().numpy()
+        assert np.isnan(act[badrow[a]]).all()
+    raw = {a: np.where(np.isnan(dec[a + "_raw"].cpu().numpy()), 0, dec[a + "_raw"].cpu().numpy()) for a in dims}
+    sc, rot, op = oracle.activate(raw["scale"], raw["rotation"], raw["opacity"])
+    keep = np.ones(P, bool)
+    keep[list(badrow.values())] = False
+    np.testing.assert_array_equal(dec["scale"].cpu().numpy()[keep], sc[keep])
+    np.testing.assert_array_equal(dec["rotation"].cpu().numpy()[keep], rot[keep])
+    np.testing.assert_array_equal(dec["opacity"].cpu().numpy()[keep, 0], op[keep])
+
+
 def test_rvq_out_of_range_index_is_nan():
     from nest_splat.rvq import rvq_decode
     cb = torch.zeros((2, 8, 2), dtype=torch.float32, device=DEV)
