@@ -506,6 +506,15 @@ static bool mlp32_fits(const MlpParams& p, int C) {
   return p.N < (1ll << 31) - 64 && p.feat_cs >= 0 && p.feat_ns >= 0 && maxoff < 0xffffffffull;
 }
 
+// Pixel rows of the block kernel: 16-byte chunk c of row r (a pixel of the
+// 256-pixel block) is stored at chunk (c & ~3) | ((c & 3) ^ ((r >> 4) & 3))
+// of the row.  A lane writes four rows 4 lane + q apart by 832 bytes, which
+// without the swizzle fall into 4 bank positions of a 256-byte bank row (an
+// 8-16-way conflict on every feature store); with it the 16 lanes of a
+// 128-bit store hit 16 distinct 16-byte slots.  The MFMA operand reads take
+// 16 consecutive rows with one (r >> 4), so they stay conflict-free.
+__device__ __forceinline__ int xrow_chunk(int r, int c) { return (c & ~3) | ((c & 3) ^ ((r >> 4) & 3)); }
+
 // Block variant for the contiguous channel-major map the render writes
 // (pixel stride 1, channel stride a multiple of 4, 16-byte aligned): the
 // workgroup takes 256 pixels per iteration, and wave w loads channels
@@ -545,9 +554,9 @@ mlp_block_kernel(const MlpParams p) {
   }
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int col = lane & 15, grp = lane >> 4;
-  uint16_t* xall = lds + S::X;              // [256 pixels][LD1]
+  uint16_t* xall = lds + S::X;              // [256 pixels][LD1], chunks swizzled by xrow_chunk
   uint16_t* xrow = xall + wid * 64 * LD1;   // this wave's 64 pixels
-  for (int k = Kin; k < K1; k++) xrow[lane * LD1 + k] = 0;
+  for (int k = Kin; k < K1; k++) xrow[lane * LD1 + 8 * xrow_chunk(wid * 64 + lane, k >> 3) + (k & 7)] = 0;
 
   const uint32_t N = (uint32_t)p.N;
   const uint32_t nblk = (N + 255) / 256;
@@ -588,15 +597,23 @@ mlp_block_kernel(const MlpParams p) {
     // features: 4 pixel rows per lane, this wave's CPW channels, 4 channels per store
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      uint16_t* dst = xall + (4 * lane + q) * LD1 + wid * CPW;
+      const int r = 4 * lane + q;
+      uint16_t* dst = xall + r * LD1;
+      uint32_t w[CPW / 2];
 #pragma unroll
-      for (int j = 0; j < CPW; j += 4) {
+      for (int j = 0; j < CPW; j += 2) {
         const float v0 = q == 0 ? fv[j].x : q == 1 ? fv[j].y : q == 2 ? fv[j].z : fv[j].w;
         const float v1 = q == 0 ? fv[j + 1].x : q == 1 ? fv[j + 1].y : q == 2 ? fv[j + 1].z : fv[j + 1].w;
-        const float v2 = q == 0 ? fv[j + 2].x : q == 1 ? fv[j + 2].y : q == 2 ? fv[j + 2].z : fv[j + 2].w;
-        const float v3 = q == 0 ? fv[j + 3].x : q == 1 ? fv[j + 3].y : q == 2 ? fv[j + 3].z : fv[j + 3].w;
-        *reinterpret_cast<uint2*>(dst + j) = make_uint2(pack2(to16<kBF16>(v0), to16<kBF16>(v1)),
-                                                        pack2(to16<kBF16>(v2), to16<kBF16>(v3)));
+        w[j / 2] = pack2(to16<kBF16>(v0), to16<kBF16>(v1));
+      }
+      if constexpr (CPW % 8 == 0) {
+#pragma unroll
+        for (int h = 0; h < CPW / 8; h++)
+          *reinterpret_cast<uint4*>(dst + 8 * xrow_chunk(r, wid * (CPW / 8) + h)) =
+              make_uint4(w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]);
+      } else {  // 4 channels per wave: half a chunk
+        const int k0 = wid * CPW;
+        *reinterpret_cast<uint2*>(dst + 8 * xrow_chunk(r, k0 >> 3) + (k0 & 7)) = make_uint2(w[0], w[1]);
       }
     }
     // SH terms of this wave's pixels
@@ -606,13 +623,13 @@ mlp_block_kernel(const MlpParams p) {
       pixel_dir32(p, n < N ? n : N - 1, dx, dy, dz);
       float sh[16];
       sh16(dx, dy, dz, sh);
-      uint4* row4 = reinterpret_cast<uint4*>(xrow + lane * LD1 + C);
 #pragma unroll
       for (int q = 0; q < 2; q++)
-        row4[q] = make_uint4(pack2(to16<kBF16>(sh[8 * q + 0]), to16<kBF16>(sh[8 * q + 1])),
-                             pack2(to16<kBF16>(sh[8 * q + 2]), to16<kBF16>(sh[8 * q + 3])),
-                             pack2(to16<kBF16>(sh[8 * q + 4]), to16<kBF16>(sh[8 * q + 5])),
-                             pack2(to16<kBF16>(sh[8 * q + 6]), to16<kBF16>(sh[8 * q + 7])));
+        *reinterpret_cast<uint4*>(xrow + lane * LD1 + 8 * xrow_chunk(wid * 64 + lane, C / 8 + q)) =
+            make_uint4(pack2(to16<kBF16>(sh[8 * q + 0]), to16<kBF16>(sh[8 * q + 1])),
+                       pack2(to16<kBF16>(sh[8 * q + 2]), to16<kBF16>(sh[8 * q + 3])),
+                       pack2(to16<kBF16>(sh[8 * q + 4]), to16<kBF16>(sh[8 * q + 5])),
+                       pack2(to16<kBF16>(sh[8 * q + 6]), to16<kBF16>(sh[8 * q + 7])));
     }
     const float a_out[4] = {alpha4[0], alpha4[1], alpha4[2], alpha4[3]};
     if (b + gridDim.x < nblk) {  // next block in flight during the contraction
@@ -638,7 +655,8 @@ mlp_block_kernel(const MlpParams p) {
         uint4 bb[2];
 #pragma unroll
         for (int j = 0; j < 2; j++)
-          bb[j] = *reinterpret_cast<const uint4*>(xrow + (16 * (2 * h + j) + col) * LD1 + 32 * kc + 8 * grp);
+          bb[j] = *reinterpret_cast<const uint4*>(xrow + (16 * (2 * h + j) + col) * LD1 +
+                                                  8 * xrow_chunk(wid * 64 + 16 * (2 * h + j), 4 * kc + grp));
 #pragma unroll
         for (int mt = 0; mt < NT; mt++) {
           const uint4 a = *reinterpret_cast<const uint4*>(w1 + (16 * mt + col) * LD1 + 32 * kc + 8 * grp);
