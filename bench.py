@@ -2,7 +2,8 @@
 """Headline benchmark: rendered Mpix/s of the forward path (preprocess ->
 binning -> tile render with in-loop hash lookup -> MLP decode) on the
 1M-splat, 1600x1064, 16-level hash-textured unbounded scene, with the render
-kernel's HBM roofline fraction and the CPU oracle timed on this host.
+kernel's HBM roofline fraction and the benchmark's CPU path (NumPy per-pixel loop,
+torch-CPU hash encode, MLP and RVQ) timed on this host.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config cfg3]
 
@@ -66,68 +67,35 @@ def load_counters(path: str) -> dict:
         return {}
 
 
-def cpu_baseline(scene, gpu_hits_total: int, row_stride: int, threads: int):
-    """Oracle (oracle/nest_oracle.c) on this host: full preprocess and
-    binning, render of every row_stride-th tile row and MLP of its pixels with
-    `threads` OpenMP threads; scaled to one frame by the sample's
-    share of tile/splat pairs plus hits (render) and of pixels (MLP)."""
-    import numpy as np
-    from oracle import oracle as O
-
-    sp = scene.spec
-    cam = scene.cameras[0]
-    W, H = cam.image_width, cam.image_height
-    scales, rots, opac, homo = scene.scales, scene.rotations, scene.opacity, scene.homotrans
-    t_rvq = 0.0
-    if sp.rvq:
-        from nest_splat.scene import RVQ_BIAS, build_homotrans_np
-        tr = time.perf_counter()
-        raw = {a: O.rvq_decode(scene.rvq_codebooks[a], scene.rvq_indices[a], RVQ_BIAS[a]) for a in RVQ_BIAS}
-        scales, rots, op = O.activate(raw["scale"], raw["rotation"], raw["opacity"])
-        opac = op[:, None]
-        homo = build_homotrans_np(rots, scales, scene.means)
-        t_rvq = time.perf_counter() - tr
-    t0 = time.perf_counter()
-    pre = O.preprocess(scene.means, scales, rots, opac, cam.world_view_transform, cam.full_proj_transform, W, H)
-    t1 = time.perf_counter()
-    b = O.binning(pre, W, H)
-    t2 = time.perf_counter()
-    grid = O.make_grid(sp.L, sp.F, sp.S, sp.base_res, scene.offsets, scene.table, sp.gridrange, sp.contract)
-    phase = row_stride // 2
-    r = O.render(pre, b, W, H, sp.C, grid, homotrans=homo, ap_level=scene.ap_level,
-                 row_stride=row_stride, row_phase=phase, threads=threads)
-    t3 = time.perf_counter()
-    gx, gy = (W + 15) // 16, (H + 15) // 16
-    rows = [ty for ty in range(gy) if ty % row_stride == phase]
-    pix = np.zeros((H, W), bool)
-    for ty in rows:
-        pix[ty * 16:(ty + 1) * 16] = True
-    tiles = np.array([ty * gx + tx for ty in rows for tx in range(gx)])
-    nr_sample = int((b["ranges"][tiles, 1].astype(np.int64) - b["ranges"][tiles, 0]).sum())
-    hits_sample = int(r["others"][7][pix].sum())
-    share = (nr_sample + hits_sample) / max(1, b["num_rendered"] + gpu_hits_total)
-    idx = np.nonzero(pix.reshape(-1))[0]
-    dirs = O.ray_dirs(cam)[idx]
-    feat = r["color"].reshape(sp.C, -1)[:, idx]
-    alpha = r["others"][1].reshape(-1)[idx]
-    t4 = time.perf_counter()
-    O.mlp(np.ascontiguousarray(feat), dirs, alpha, scene.W1, scene.W2, scene.W3, sp.mlp_dtype,
-          np.asarray(sp.bg, np.float32), threads=threads)
-    t5 = time.perf_counter()
-    pix_share = idx.size / (W * H)
-    frame_s = t_rvq + (t1 - t0) + (t2 - t1) + (t3 - t2) / share + (t5 - t4) / pix_share
-    rvq_note = f"RVQ decode + activations + homotrans ({t_rvq:.2f} s, 1 thread); " if sp.rvq else ""
+def cpu_baseline(config: str, gpu_hits_total: int, row_stride: int, threads: int):
+    """The CPU path of the benchmark definition, timed on this host: a NumPy
+    transcription of the per-pixel render loop (parallel over tiles with a
+    pool of `threads` processes), torch-CPU hash encode of the accepted hits,
+    torch-CPU MLP and RVQ, with preprocess and binning from the C oracle
+    (oracle/cpu_baseline.py).  It runs in a child process that touches no
+    GPU, on every row_stride-th tile row, and is scaled to a frame by the
+    sample's share of tile/splat pairs plus hits (render loop and hash encode)
+    and of pixels (MLP)."""
+    import subprocess
+    cmd = [sys.executable, "-m", "oracle.cpu_baseline", "--config", config, "--row-stride", str(row_stride),
+           "--workers", str(threads), "--gpu-hits", str(gpu_hits_total)]
+    r = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=900)
+    if r.returncode != 0:
+        raise RuntimeError(f"cpu baseline failed ({r.returncode}): {r.stderr[-2000:]}")
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    st = res["stage_s"]
+    parts = "; ".join(f"{k} {v:.2f} s" for k, v in st.items())
     return {
-        "value": W * H / frame_s / 1e6,
+        "value": res["value"],
         "unit": "Mpix/s",
-        "cores": threads,
+        "cores": res["cores"],
         "kind": "port",
-        "sample": (f"oracle C port: {rvq_note}full preprocess ({t1 - t0:.2f} s, 1 thread) and binning ({t2 - t1:.2f} s, "
-                   f"1 thread); render of every {row_stride}th tile row ({len(rows)} of {gy} rows, {t3 - t2:.2f} s, "
-                   f"{threads} OpenMP threads, scaled by its {share:.4f} share of pairs+hits); fp32-accumulated MLP "
-                   f"of those {idx.size} pixels ({t5 - t4:.2f} s, {threads} OpenMP threads, scaled by pixel share); "
-                   f"extrapolated frame {frame_s:.2f} s"),
-        "frame_s": frame_s,
+        "sample": (f"NumPy per-pixel loop over {res['rows']} of every {row_stride} tile rows ({res['cores']} worker "
+                   f"processes) + torch-CPU hash encode, MLP{' and RVQ' if 'rvq' in st else ''} "
+                   f"({res['cores']} threads), C-oracle preprocess and binning (1 thread): {parts}; scaled by the "
+                   f"sample's {res['share']:.4f} share of pairs+hits and {res['pixel_share']:.4f} of pixels; "
+                   f"extrapolated frame {res['frame_s']:.1f} s"),
+        "frame_s": res["frame_s"],
     }
 
 
@@ -553,9 +521,9 @@ def main():
         log(f"[bench] backward: {out['backward_ms']} ms")
     if not args.no_cpu_baseline and ncam == 1:
         threads = len(os.sched_getaffinity(0))
-        stride = args.cpu_row_stride or {"cfg1": 1, "cfg2": 2, "cfg3": 4, "cfg4": 3, "cfg5": 17}[spec.name]
-        log(f"[bench] cpu baseline on {threads} threads ...")
-        cb = cpu_baseline(scene, hits_total[0], stride, threads)
+        stride = args.cpu_row_stride or {"cfg1": 1, "cfg2": 1, "cfg3": 16, "cfg4": 16, "cfg5": 16}[spec.name]
+        log(f"[bench] cpu baseline on {threads} cores ...")
+        cb = cpu_baseline(spec.name, hits_total[0], stride, threads)
         out["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cb.items() if k != "frame_s"}
     print(json.dumps(out), flush=True)
 
