@@ -519,12 +519,16 @@ def main():
         torch.cuda.synchronize()
         out["backward_ms"] = round((time.perf_counter() - b0) / args.backward * 1e3, 3)
         log(f"[bench] backward: {out['backward_ms']} ms")
-    if not args.no_cpu_baseline and ncam == 1:
+    if not args.no_cpu_baseline:
+        # camera 0 of the config (the rate per camera is the rate per frame)
         threads = len(os.sched_getaffinity(0))
-        stride = args.cpu_row_stride or {"cfg1": 1, "cfg2": 1, "cfg3": 16, "cfg4": 16, "cfg5": 16}[spec.name]
+        stride = args.cpu_row_stride or {"cfg1": 1, "cfg2": 1, "cfg3": 16, "cfg4": 16, "cfg5": 34}[spec.name]
         log(f"[bench] cpu baseline on {threads} cores ...")
         cb = cpu_baseline(spec.name, hits_total[0], stride, threads)
-        out["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cb.items() if k != "frame_s"}
+        out["cpu_baseline"] = {k: (round(v, 6) if isinstance(v, float) else v) for k, v in cb.items() if k != "frame_s"}
+        if spec.name == "cfg1" and threads > 1:
+            one = cpu_baseline(spec.name, hits_total[0], stride, 1)
+            out["cpu_baseline"]["value_1_core"] = round(one["value"], 6)
     print(json.dumps(out), flush=True)
 
 
