@@ -314,7 +314,6 @@ class Workload:
         import torch
 
         from nest_splat import rasterizer as rz
-        from nest_splat.renderer import build_H, build_rotation
         means, opac, scales, rots, homo = self.means, self.opac, self.scales, self.rots, self.homo
         if self.rvq is not None:
             # compressed attributes: decode (exp / normalise / sigmoid fused) and
@@ -322,7 +321,7 @@ class Workload:
             # reference rebuilds it every frame (get_homotrans)
             dec = self.rvq.decode()
             scales, rots, opac = dec["scale"], dec["rotation"], dec["opacity"]
-            homo = build_H(build_rotation(rots), scales, means)
+            homo = rz.build_homotrans(rots, scales, means)
         out = []
         for k, (st, M) in enumerate(zip(self.settings, self.rays)):
             tm = timings[k] if timings is not None else False

@@ -335,6 +335,17 @@ int nest_backward(const nest_raster_settings *settings, const nest_hashgrid *gri
                   void *bwd_ws, size_t bwd_bytes, void *stream);
 
 
+/* GaussianModel.get_homotrans (scene/gaussian_model.py:249-250):
+ * build_H(build_rotation(rotations), scales, means3D) of
+ * utils/general_utils.py:78-113, the [P,4,4] row-major splat-to-world
+ * transforms the forward reads (columns 0, 1 and 3).  rotations [P,4]
+ * (w, x, y, z; normalised here as the reference does), scales [P,2],
+ * means3D [P,3], homotrans [P,4,4]; device float32 arrays, rotations and
+ * homotrans 16-byte aligned, scales 8-byte aligned.  Bit-exact with the
+ * reference's float32 expressions. */
+int nest_build_homotrans(int64_t P, const float *rotations, const float *scales, const float *means3D,
+                         float *homotrans, void *stream);
+
 /* markVisible (DSR/rasterize_points.cu:452-470, CR/rasterizer_impl.cu:198-210,
  * checkFrustum :54-66): present[i] = 1 when the view-space depth of
  * means3D[i] exceeds 0.2 (in_frustum, CR/auxiliary.h:190-215), else 0.

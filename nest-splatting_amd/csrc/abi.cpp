@@ -591,6 +591,19 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   return NEST_OK;
 }
 
+int nest_build_homotrans(int64_t P, const float* rotations, const float* scales, const float* means3D,
+                         float* homotrans, void* stream) {
+  if (P < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "P must be >= 0 (got %lld)", (long long)P);
+  if (P == 0) return NEST_OK;
+  if (!rotations || !scales || !means3D || !homotrans)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "rotations, scales, means3D and homotrans are required");
+  if ((reinterpret_cast<uintptr_t>(rotations) & 15u) || (reinterpret_cast<uintptr_t>(scales) & 7u) ||
+      (reinterpret_cast<uintptr_t>(homotrans) & 15u) || (reinterpret_cast<uintptr_t>(means3D) & 3u))
+    return fail(NEST_ERR_INVALID_ARGUMENT, "rotations and homotrans need 16-byte, scales 8-byte alignment");
+  hipError_t e = launch_build_homotrans(P, rotations, scales, means3D, homotrans, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? NEST_OK : hip_fail(e, "build_homotrans");
+}
+
 int nest_mark_visible(int32_t P, const float* means3D, const float viewmatrix[16], uint8_t* present, void* stream) {
   if (P < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "P must be >= 0 (got %d)", P);
   if (P == 0) return NEST_OK;

@@ -55,6 +55,8 @@ struct PreprocessParams {
 
 // markVisible: present[i] = 1 when splat i lies beyond the near plane.
 hipError_t launch_mark_visible(int P, const float* means, const float view[16], uint8_t* present, hipStream_t s);
+hipError_t launch_build_homotrans(int64_t P, const float* rots, const float* scales, const float* means, float* H,
+                                  hipStream_t s);
 
 // Per-level constants of the hash grid, computed on the host in the same
 // float order as the reference's query_feature (CR/hashgrid.h:122-131).

@@ -256,4 +256,40 @@ hipError_t launch_mark_visible(int P, const float* means, const float view[16], 
   return hipGetLastError();
 }
 
+// get_homotrans (scene/gaussian_model.py:249-250) = build_H(build_rotation(r),
+// s, xyz) of utils/general_utils.py:78-113: the quaternion is normalised with
+// sqrt(((r0 r0 + r1 r1) + r2 r2) + r3 r3) and a division, R is built with the
+// reference's expressions, and H = [[R * (sx, sy, 0) by column, xyz],
+// [0, 0, 0, 1]] row-major; every operation is one float32 rounding in the
+// order the torch expressions evaluate, so the result equals the reference's
+// elementwise kernels bit for bit (column 2 is 0 * R, -0 where R < 0).
+__global__ void __launch_bounds__(256) homotrans_kernel(int64_t P, const float4* __restrict__ rots,
+                                                        const float2* __restrict__ scales,
+                                                        const float* __restrict__ means, float4* __restrict__ H) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P) return;
+  const float4 q = rots[i];
+  const float norm = sqrtf(((q.x * q.x + q.y * q.y) + q.z * q.z) + q.w * q.w);
+  const float r = q.x / norm, x = q.y / norm, y = q.z / norm, z = q.w / norm;
+  const float R00 = 1.0f - 2.0f * (y * y + z * z), R01 = 2.0f * (x * y - r * z), R02 = 2.0f * (x * z + r * y);
+  const float R10 = 2.0f * (x * y + r * z), R11 = 1.0f - 2.0f * (x * x + z * z), R12 = 2.0f * (y * z - r * x);
+  const float R20 = 2.0f * (x * z - r * y), R21 = 2.0f * (y * z + r * x), R22 = 1.0f - 2.0f * (x * x + y * y);
+  const float2 s = scales[i];
+  const float m0 = means[3 * i], m1 = means[3 * i + 1], m2 = means[3 * i + 2];
+  float4* h = H + 4 * i;
+  h[0] = make_float4(s.x * R00, s.y * R01, 0.0f * R02, m0);
+  h[1] = make_float4(s.x * R10, s.y * R11, 0.0f * R12, m1);
+  h[2] = make_float4(s.x * R20, s.y * R21, 0.0f * R22, m2);
+  h[3] = make_float4(0.0f, 0.0f, 0.0f, 1.0f);
+}
+
+hipError_t launch_build_homotrans(int64_t P, const float* rots, const float* scales, const float* means, float* H,
+                                  hipStream_t s) {
+  if (P <= 0) return hipSuccess;
+  hipLaunchKernelGGL(homotrans_kernel, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, s, P,
+                     reinterpret_cast<const float4*>(rots), reinterpret_cast<const float2*>(scales), means,
+                     reinterpret_cast<float4*>(H));
+  return hipGetLastError();
+}
+
 }  // namespace nest

@@ -350,6 +350,24 @@ def geometry_arrays(res: ForwardResult, P: int) -> Dict[str, torch.Tensor]:
                 clamped=L.view(res.geom, o[L.GEOM_CLAMPED], torch.uint8, (n, 3))[:P])
 
 
+def build_homotrans(rotations: torch.Tensor, scales: torch.Tensor, means3D: torch.Tensor) -> torch.Tensor:
+    """get_homotrans (scene/gaussian_model.py:249-250): build_H(build_rotation
+    (rotations), scales, means3D) of utils/general_utils.py:78-113 on the GPU,
+    [P, 4, 4] float32, bit-exact with the reference's torch expressions."""
+    P = int(rotations.shape[0])
+    if rotations.shape != (P, 4) or scales.shape != (P, 2) or means3D.shape != (P, 3):
+        raise ValueError("rotations [P,4], scales [P,2] and means3D [P,3] are required")
+    out = torch.empty((P, 4, 4), dtype=torch.float32, device=rotations.device)
+    if P == 0:
+        return out
+    rot = _contig_f32(rotations, "rotations")
+    sc = _contig_f32(scales, "scales")
+    mn = _contig_f32(means3D, "means3D")
+    L.check(L.lib().nest_build_homotrans(P, L.ptr(rot), L.ptr(sc), L.ptr(mn), L.ptr(out),
+                                         L.stream_ptr(rotations.device)), "nest_build_homotrans")
+    return out
+
+
 def mark_visible(means3D: torch.Tensor, viewmatrix) -> torch.Tensor:
     """markVisible (DSR/rasterize_points.cu:452-470): bool [P], True where the
     view-space depth of the point exceeds 0.2."""

@@ -88,6 +88,9 @@ class SplatModel:
     def get_homotrans(self):
         if self._homotrans is not None:
             return self._homotrans
+        if self._rotation.is_cuda:
+            from .rasterizer import build_homotrans
+            return build_homotrans(self._rotation, self._scaling, self._xyz)
         return build_H(build_rotation(self._rotation), self._scaling, self._xyz)
 
 

@@ -99,3 +99,27 @@ def test_mark_visible_matches_oracle(oracle):
     assert ref[: sc.spec.P][pre["radii"] > 0].all()
     assert GaussianRasterizer(rs, HashGridSettings(0, 0.0, 0, False, 0, torch.empty(0))).markVisible(
         torch.zeros((0, 3), device=DEV)).numel() == 0
+
+
+def test_build_homotrans_bit_exact():
+    """nest_build_homotrans against the reference's torch expressions
+    (build_H(build_rotation(r), s, xyz), utils/general_utils.py:78-113) on the
+    GPU and their float32 numpy restatement: unnormalised quaternions of mixed
+    sign, ragged P, column 2 keeping the sign of 0 * R."""
+    from nest_splat import rasterizer as rz
+    from nest_splat.renderer import build_H, build_rotation
+    from nest_splat.scene import build_homotrans_np
+    rng = np.random.default_rng(19)
+    P = 100_003
+    q = (rng.standard_normal((P, 4)) * rng.uniform(0.1, 3.0, (P, 1))).astype(np.float32)
+    s = np.exp(rng.normal(-4, 1, (P, 2))).astype(np.float32)
+    x = rng.uniform(-20, 20, (P, 3)).astype(np.float32)
+    got = rz.build_homotrans(_t(q), _t(s), _t(x))
+    want = build_H(build_rotation(_t(q)), _t(s), _t(x))
+    torch.cuda.synchronize()
+    g = got.cpu().numpy()
+    np.testing.assert_array_equal(g.view(np.uint32), want.cpu().numpy().view(np.uint32))
+    np.testing.assert_array_equal(g.view(np.uint32), build_homotrans_np(q, s, x).view(np.uint32))
+    assert np.signbit(g[:, :3, 2]).any()
+    assert rz.build_homotrans(torch.zeros((0, 4), device=DEV), torch.zeros((0, 2), device=DEV),
+                              torch.zeros((0, 3), device=DEV)).shape == (0, 4, 4)
