@@ -85,14 +85,23 @@ __device__ __forceinline__ void pixel_dir(const MlpParams& p, int64_t n, float& 
   const float rx = x * M[0] + y * M[3] + M[6];
   const float ry = x * M[1] + y * M[4] + M[7];
   const float rz = x * M[2] + y * M[5] + M[8];
-  const float len = fmaxf(sqrtf(rx * rx + ry * ry + rz * rz), 1e-12f);
-  dx = rx / len;
-  dy = ry / len;
-  dz = rz / len;
+  // 1 / max(|r|, 1e-12) as one hardware reciprocal square root (~1 ulp)
+  const float il = fminf(__builtin_amdgcn_rsqf(rx * rx + ry * ry + rz * rz), 1e12f);
+  dx = rx * il;
+  dy = ry * il;
+  dz = rz * il;
+}
+
+// Output sigmoid 1 / (1 + 2^(-x log2 e)) on the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32; a few ulp, far inside the decode's 1e-3 tolerance):
+// four VALU operations where the exact exp and IEEE division take ~30, and
+// the output rows of a tile sit on a quarter of the lanes.
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
 }
 
 __device__ __forceinline__ float finish_rgb(const MlpParams& p, int64_t n, float logit, int o) {
-  float r = 1.0f / (1.0f + expf_ref(-logit));
+  float r = sigmoid_fast(logit);
   if (p.alpha) {
     const float a = p.alpha[n];
     r = a > 0.0f ? r : 0.0f;
@@ -103,7 +112,7 @@ __device__ __forceinline__ float finish_rgb(const MlpParams& p, int64_t n, float
 
 // finish_rgb with the pixel's alpha already loaded (1 when there is no mask).
 __device__ __forceinline__ float finish_rgb_alpha(const MlpParams& p, float a, float logit, int o) {
-  float r = 1.0f / (1.0f + expf_ref(-logit));
+  float r = sigmoid_fast(logit);
   if (p.alpha) {
     r = a > 0.0f ? r : 0.0f;
     if (p.use_bg) r = r + (1.0f - a) * p.bg[o];
@@ -323,10 +332,11 @@ __device__ __forceinline__ void pixel_dir32(const MlpParams& p, uint32_t n, floa
   const float rx = x * M[0] + y * M[3] + M[6];
   const float ry = x * M[1] + y * M[4] + M[7];
   const float rz = x * M[2] + y * M[5] + M[8];
-  const float len = fmaxf(sqrtf(rx * rx + ry * ry + rz * rz), 1e-12f);
-  dx = rx / len;
-  dy = ry / len;
-  dz = rz / len;
+  // 1 / max(|r|, 1e-12) as one hardware reciprocal square root (~1 ulp)
+  const float il = fminf(__builtin_amdgcn_rsqf(rx * rx + ry * ry + rz * rz), 1e12f);
+  dx = rx * il;
+  dy = ry * il;
+  dz = rz * il;
 }
 
 // Hidden unit of slot q = 32 kc + 8 grp + i of a K-chunk built from two
