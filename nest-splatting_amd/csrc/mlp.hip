@@ -741,9 +741,13 @@ static hipError_t launch_mfma32(const MlpParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// float32 path on the vector ALU: one lane per pixel, weights in LDS.
+// float32 path on the vector ALU: one lane per pixel, weights in LDS, one
+// wave per workgroup so that a small image still spreads over every CU (a
+// 128x128 frame is 256 workgroups instead of 64).
+constexpr int kMlpF32Threads = 64;
+
 template <int NW>
-__global__ void __launch_bounds__(kMlpThreads) mlp_f32_kernel(const MlpParams p) {
+__global__ void __launch_bounds__(kMlpF32Threads) mlp_f32_kernel(const MlpParams p) {
   extern __shared__ float wl[];
   const int C = p.C, Kin = C + 16;
   float* w1 = wl;
@@ -752,11 +756,13 @@ __global__ void __launch_bounds__(kMlpThreads) mlp_f32_kernel(const MlpParams p)
   const float* g1 = static_cast<const float*>(p.w1);
   const float* g2 = static_cast<const float*>(p.w2);
   const float* g3 = static_cast<const float*>(p.w3);
-  for (int i = threadIdx.x; i < NW * Kin; i += kMlpThreads) w1[i] = g1[i];
-  for (int i = threadIdx.x; i < NW * NW; i += kMlpThreads) w2[i] = g2[i];
-  for (int i = threadIdx.x; i < 3 * NW; i += kMlpThreads) w3[i] = g3[i];
+  // W1 transposed to [k][j]: a feature's NW weights are one contiguous run,
+  // read four at a time
+  for (int i = threadIdx.x; i < NW * Kin; i += kMlpF32Threads) w1[(i % Kin) * NW + i / Kin] = g1[i];
+  for (int i = threadIdx.x; i < NW * NW; i += kMlpF32Threads) w2[i] = g2[i];
+  for (int i = threadIdx.x; i < 3 * NW; i += kMlpF32Threads) w3[i] = g3[i];
   __syncthreads();
-  for (int64_t n = (int64_t)blockIdx.x * kMlpThreads + threadIdx.x; n < p.N; n += (int64_t)gridDim.x * kMlpThreads) {
+  for (int64_t n = (int64_t)blockIdx.x * kMlpF32Threads + threadIdx.x; n < p.N; n += (int64_t)gridDim.x * kMlpF32Threads) {
     float dx, dy, dz;
     pixel_dir(p, n, dx, dy, dz);
     float sh[16];
@@ -766,21 +772,42 @@ __global__ void __launch_bounds__(kMlpThreads) mlp_f32_kernel(const MlpParams p)
     for (int j = 0; j < NW; j++) h1[j] = 0.0f;
     for (int k = 0; k < C; k++) {
       const float xk = p.feat[(int64_t)k * p.feat_cs + n * p.feat_ns];
+      const float4* wk = reinterpret_cast<const float4*>(w1 + k * NW);
 #pragma unroll
-      for (int j = 0; j < NW; j++) h1[j] += w1[j * Kin + k] * xk;
+      for (int j = 0; j < NW / 4; j++) {
+        const float4 w = wk[j];
+        h1[4 * j] += w.x * xk;
+        h1[4 * j + 1] += w.y * xk;
+        h1[4 * j + 2] += w.z * xk;
+        h1[4 * j + 3] += w.w * xk;
+      }
     }
 #pragma unroll
     for (int s = 0; s < 16; s++) {
+      const float4* wk = reinterpret_cast<const float4*>(w1 + (C + s) * NW);
 #pragma unroll
-      for (int j = 0; j < NW; j++) h1[j] += w1[j * Kin + C + s] * sh[s];
+      for (int j = 0; j < NW / 4; j++) {
+        const float4 w = wk[j];
+        h1[4 * j] += w.x * sh[s];
+        h1[4 * j + 1] += w.y * sh[s];
+        h1[4 * j + 2] += w.z * sh[s];
+        h1[4 * j + 3] += w.w * sh[s];
+      }
     }
 #pragma unroll
     for (int j = 0; j < NW; j++) h1[j] = fmaxf(h1[j], 0.0f);
     float o0 = 0.f, o1 = 0.f, o2 = 0.f;
     for (int j = 0; j < NW; j++) {
       float h = 0.0f;
+      const float4* wj = reinterpret_cast<const float4*>(w2 + j * NW);
 #pragma unroll
-      for (int k = 0; k < NW; k++) h += w2[j * NW + k] * h1[k];
+      for (int k = 0; k < NW / 4; k++) {
+        const float4 w = wj[k];
+        h += w.x * h1[4 * k];
+        h += w.y * h1[4 * k + 1];
+        h += w.z * h1[4 * k + 2];
+        h += w.w * h1[4 * k + 3];
+      }
       h = fmaxf(h, 0.0f);
       o0 += w3[j] * h;
       o1 += w3[NW + j] * h;
@@ -819,9 +846,9 @@ static hipError_t launch_mfma(const MlpParams& p, hipStream_t s) {
 template <int NW>
 static hipError_t launch_f32(const MlpParams& p, hipStream_t s) {
   const size_t lds = sizeof(float) * ((size_t)NW * (p.C + 16) + (size_t)NW * NW + 3 * (size_t)NW);
-  const int64_t want = (p.N + kMlpThreads - 1) / kMlpThreads;
-  const unsigned blocks = (unsigned)(want < 2048 ? (want > 0 ? want : 1) : 2048);
-  hipLaunchKernelGGL(mlp_f32_kernel<NW>, dim3(blocks), dim3(kMlpThreads), lds, s, p);
+  const int64_t want = (p.N + kMlpF32Threads - 1) / kMlpF32Threads;
+  const unsigned blocks = (unsigned)(want < 8192 ? (want > 0 ? want : 1) : 8192);
+  hipLaunchKernelGGL(mlp_f32_kernel<NW>, dim3(blocks), dim3(kMlpF32Threads), lds, s, p);
   return hipGetLastError();
 }
 
