@@ -248,4 +248,57 @@ __device__ __forceinline__ void corners_sum(const LevelCorners& cn, const float 
   }
 }
 
+// Render path of binary16 tables (F = 2 or 4): the corner entries stay
+// packed (two halves per 32-bit word, bit patterns kept in the float array)
+// and each interpolation step widens its half inside the FMA with
+// v_fma_mix_f32, instead of one v_cvt_f32_f16 per value before it.  The
+// widening is exact and the FMA rounds once, so the result is fmaf(w, h, out)
+// bit for bit; the mix instruction's float32-denormal flush cannot apply,
+// since a product of the cell weights (0, or at least ~1e-21) and a binary16
+// value (0, or at least ~6e-8) is never a float32 denormal.
+template <int F, bool kHalf>
+__device__ __forceinline__ void corners_load_r(nest_i32x4 rsrc, const LevelCorners& cn, float vals[8][F]) {
+  if constexpr (kHalf && (F == 4 || F == 2)) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      if constexpr (F == 4) {
+        const nest_i32x2 a = nest_struct_load_v2i32(rsrc, (int)cn.idx[k], 0, (int)cn.soff, 0);
+        vals[k][0] = __int_as_float(a.x);  // channels 0-1; [2], [3] stay unused
+        vals[k][1] = __int_as_float(a.y);  // channels 2-3
+      } else {
+        vals[k][0] = __int_as_float(nest_struct_load_i32(rsrc, (int)cn.idx[k], 0, (int)cn.soff, 0));
+      }
+    }
+  } else {
+    corners_load<F, kHalf>(rsrc, cn, vals);
+  }
+}
+
+__device__ __forceinline__ float fma_mix_lo(float w, float packed, float acc) {
+  asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(w), "v"(packed));
+  return acc;
+}
+
+__device__ __forceinline__ float fma_mix_hi(float w, float packed, float acc) {
+  asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(w), "v"(packed));
+  return acc;
+}
+
+template <int F, bool kHalf>
+__device__ __forceinline__ void corners_sum_r(const LevelCorners& cn, const float vals[8][F], float out[F]) {
+  if constexpr (kHalf && (F == 4 || F == 2)) {
+#pragma unroll
+    for (int f = 0; f < F; f++) out[f] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const float w = (1.0f * cn.wx[k & 1]) * cn.wy[(k >> 1) & 1] * cn.wz[k >> 2];
+#pragma unroll
+      for (int f = 0; f < F; f++)
+        out[f] = (f & 1) ? fma_mix_hi(w, vals[k][f >> 1], out[f]) : fma_mix_lo(w, vals[k][f >> 1], out[f]);
+    }
+  } else {
+    corners_sum<F>(cn, vals, out);
+  }
+}
+
 }  // namespace nest

@@ -104,9 +104,9 @@ __device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc
         if constexpr (kStructured) rec = level_record(lqb, l);
         level_setup<F, kHalf, kStructured>(g, rec, l, u, cn);
         float vals[8][F];
-        corners_load<F, kHalf>(rsrc, cn, vals);
+        corners_load_r<F, kHalf>(rsrc, cn, vals);
         float v[F];
-        corners_sum<F>(cn, vals, v);
+        corners_sum_r<F, kHalf>(cn, vals, v);
 #pragma unroll
         for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(v[f], e.w, acc[l * F + f]);
       }
@@ -180,7 +180,7 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
   if constexpr (kStructured) rec = level_record(lqb, 0);
   if (look) {
     level_setup<F, kHalf, kStructured>(g, rec, 0, u, cn);
-    corners_load<F, kHalf>(rsrc, cn, vals);
+    corners_load_r<F, kHalf>(rsrc, cn, vals);
   }
   if constexpr (kStructured) rec_next = level_record(lqb, 1);
 #pragma unroll
@@ -189,13 +189,13 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
     if constexpr (kStructured)
       if (l + 2 < kLevels) rec_after = level_record(lqb, l + 2);
     float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (look) corners_sum<F>(cn, vals, v);
+    if (look) corners_sum_r<F, kHalf>(cn, vals, v);
     bool next = false;
     if (l + 1 < kLevels) {
       next = work && (uint32_t)(l + 1) < nlev;
       if (next) {
         level_setup<F, kHalf, kStructured>(g, rec_next, l + 1, u, cn);
-        corners_load<F, kHalf>(rsrc, cn, vals);
+        corners_load_r<F, kHalf>(rsrc, cn, vals);
       }
     }
     if (work) hq[wslot][col] = make_float4(v[0], v[1], v[2], v[3]);
@@ -289,7 +289,7 @@ __device__ __forceinline__ void drain_compact_mix(const RenderParams& p, nest_i3
     look = work && !fast && 0u < nhash;
     if (look) {
       level_setup<F, kHalf, kStructured>(g, rec, 0, u, cn);
-      corners_load<F, kHalf>(rsrc, cn, vals);
+      corners_load_r<F, kHalf>(rsrc, cn, vals);
     }
     if (work && rows && 0u < nfeat) {
 #pragma unroll
@@ -308,7 +308,7 @@ __device__ __forceinline__ void drain_compact_mix(const RenderParams& p, nest_i3
       float h[F];
 #pragma unroll
       for (int f = 0; f < F; f++) h[f] = 0.0f;
-      if (look) corners_sum<F>(cn, vals, h);
+      if (look) corners_sum_r<F, kHalf>(cn, vals, h);
 #pragma unroll
       for (int f = 0; f < F; f++)
         v[f] = fast ? rv[f] : (p.blend ? fmaf(wt, rv[f], (1.0f - wt) * h[f]) : (kGs ? wt * h[f] : h[f]));
@@ -319,7 +319,7 @@ __device__ __forceinline__ void drain_compact_mix(const RenderParams& p, nest_i3
       next = work && !fast && gn < nhash;
       if (next) {
         level_setup<F, kHalf, kStructured>(g, rec_next, (int)gn, u, cn);
-        corners_load<F, kHalf>(rsrc, cn, vals);
+        corners_load_r<F, kHalf>(rsrc, cn, vals);
       }
       if (work && rows && gn < nfeat) {
 #pragma unroll
@@ -385,8 +385,8 @@ __device__ __forceinline__ void drain_mixed(const RenderParams& p, nest_i32x4 rs
           if constexpr (kStructured) rec = level_record(lqb, gl);
           level_setup<F, kHalf, kStructured>(g, rec, gl, u, cn);
           float vals[8][F];
-          corners_load<F, kHalf>(rsrc, cn, vals);
-          corners_sum<F>(cn, vals, h);
+          corners_load_r<F, kHalf>(rsrc, cn, vals);
+          corners_sum_r<F, kHalf>(cn, vals, h);
         }
 #pragma unroll
         for (int f = 0; f < F; f++) {
