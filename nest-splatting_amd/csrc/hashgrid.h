@@ -211,13 +211,32 @@ __device__ __forceinline__ void level_corners(const LevelTable& lv, int l, float
   }
 }
 
+// cell_weights for a looked-up render hit: its grid coordinate u is in
+// [0, 1] (the contraction maps into [0, 1], and out-of-range hits of the
+// affine normalisation look nothing up), so x = u * scale + pos_offset lies
+// in [0, 2^32) and x - (float)f2u_sat(x) is exactly fract(x): one
+// v_fract_f32 instead of a conversion back and a subtraction (NaN stays NaN).
+__device__ __forceinline__ void cell_weights_unit(float scale, float pos_offset, const float u[3], uint32_t g[3],
+                                                  LevelCorners& cn) {
+  float pos[3];
+#pragma unroll
+  for (int d = 0; d < 3; d++) {
+    const float x = u[d] * scale + pos_offset;
+    g[d] = f2u_sat(x);
+    pos[d] = __builtin_amdgcn_fractf(x);
+  }
+  cn.wx[0] = 1 - pos[0]; cn.wx[1] = pos[0];
+  cn.wy[0] = 1 - pos[1]; cn.wy[1] = pos[1];
+  cn.wz[0] = 1 - pos[2]; cn.wz[1] = pos[2];
+}
+
 // The common grid (levels [0, n_dense) dense with no modulo, the rest hashed
 // into power-of-two sizes, trilinear weights) from the level's 16-byte
 // record: one uniform test of q.b picks the index path.
 __device__ __forceinline__ void quad_corners(const LevelQuad& q, float pos_offset, const float u[3], LevelCorners& cn) {
   cn.soff = q.soff;
   uint32_t g[3];
-  cell_weights(q.scale, pos_offset, false, u, g, cn);
+  cell_weights_unit(q.scale, pos_offset, u, g, cn);
   if (q.b != 0) {
     dense_corners(g, q.a, q.b, cn.idx);
   } else {
