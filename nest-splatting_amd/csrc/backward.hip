@@ -11,8 +11,13 @@
 //
 // Layout of the render backward: one 256-thread workgroup per 16x16 tile, one
 // lane per pixel, the tile's splats walked back to front in LDS-staged
-// batches of the forward's packed records.  Two restructurings against the
-// reference, both the same sums in another order:
+// batches of the forward's packed records.  With a grid, a wave splits each
+// batch into segments: a geometry pass queues the segment's hits, the queued
+// hits are spread one per lane for the grid work (table gathers, the
+// features' dot product with dL/dpixel, dL/dxyz, the table-gradient scatter),
+// and a third pass runs the blending recursion over the splats that hit the
+// wave.  Two restructurings against the reference, both the same sums in
+// another order:
 //  - the reference keeps three C-long arrays per pixel (accum_rec,
 //    last_color, dL_dpixel).  The back-to-front blend accum_rec =
 //    a*last + (1-a)*accum_rec is linear with the same coefficients for every
@@ -26,7 +31,11 @@
 //    |grad| sum, colours) are summed over the wave with cross-lane shuffles
 //    and added with one atomic per wave instead of one per pixel.
 // Table gradients are hardware float atomics (global_atomic_add_f32) at
-// every corner, as in the reference.
+// every corner, as in the reference, merged per cell across the wave first.
+// Their cost is one request per (instruction, 64-byte segment): measured on
+// MI355X, 16 lanes adding to one segment run 16x the dword rate of 16 lanes
+// adding to 16 segments, so every scatter below gathers an entry's channels
+// into one instruction.
 #include <hip/hip_fp16.h>
 
 #include "hashgrid.h"
@@ -91,17 +100,47 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ void atomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
 
+// 4x4 transpose across each quad of lanes: on return, a[q] of lane 4m + i
+// holds a[i] of lane 4m + q.  Two exchange steps, lane bit 0 then bit 1: a
+// lane whose bit is clear trades its a[r + s] for its partner's a[r] (s the
+// bit's weight), one with the bit set its a[r] for the partner's a[r + s].
+__device__ __forceinline__ void quad_transpose(float a[4]) {
+  const bool up0 = (threadIdx.x & 1u) != 0u, up1 = (threadIdx.x & 2u) != 0u;
+#pragma unroll
+  for (int r = 0; r < 4; r += 2) {
+    const float got = dpp_f<kDppQuadXor1>(up0 ? a[r] : a[r + 1]);
+    if (up0) a[r] = got; else a[r + 1] = got;
+  }
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const float got = dpp_f<kDppQuadXor2>(up1 ? a[r] : a[r + 2]);
+    if (up1) a[r] = got; else a[r + 2] = got;
+  }
+}
+
+// x of lane 4m + q in every lane of quad m (q a compile-time constant after
+// unrolling).
+__device__ __forceinline__ uint32_t quad_bcast(int q, uint32_t x) {
+  switch (q) {
+    case 0: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x00, 0xF, 0xF, false);
+    case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x55, 0xF, 0xF, false);
+    case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xAA, 0xF, 0xF, false);
+    default: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xFF, 0xF, 0xF, false);
+  }
+}
+
 // Table gradient of one level for the wave (uniform control flow): lanes
 // whose hits fall in the same cell (same g) share all eight corner entries.
 // The cells are taken one at a time (the lowest remaining lane's cell and
 // every lane sharing it); a cell of two or more lanes has its 8*F values
 // summed over its lanes with a recursive-halving reduce-scatter (after it,
 // lane l holds the sum of value l / (64 / 8F)) and added with one atomic per
-// entry and channel; lanes alone in their cell add their own values at the
-// end, all at once.  At coarse levels a wave's hits (one splat seen by 64
-// neighbouring pixels) are nearly always one cell, which is where the
-// per-lane atomics of the reference pile onto the same addresses; at fine
-// levels a cell holds a few lanes.
+// entry and channel; lanes alone in their cell add their values at the end,
+// all at once, the quads of lanes taking turns so that an instruction adds
+// whole entries.  At coarse levels a wave's 64 hits (neighbouring pixels and
+// splats adjacent in depth) are a few cells, which is where the per-lane
+// atomics of the reference pile onto the same addresses; at fine levels a
+// cell holds a few lanes.
 template <int F>
 __device__ __forceinline__ void scatter_level(bool on, const uint32_t gc[3], const uint32_t idx[8], const float* cv,
                                               float* dl) {
@@ -147,12 +186,38 @@ __device__ __forceinline__ void scatter_level(bool on, const uint32_t gc[3], con
       atomic_add(dl + (size_t)e * F + f, v[0]);
     }
   }
-  if (((single >> lane) & 1ull) != 0ull) {
+  if (single == 0ull) return;
+  const bool me = ((single >> lane) & 1ull) != 0ull;
+  if constexpr (F == 1) {
+    if (me) {
 #pragma unroll
-    for (int k = 0; k < 8; k++)
+      for (int k = 0; k < 8; k++)
+        if (cv[k] != 0.0f) atomic_add(dl + idx[k], cv[k]);
+    }
+  } else {
+    // Each quad of lanes takes its four hits in turn, lane p of the quad
+    // adding value 4g + p of the hit: an instruction carries 16 hits' runs of
+    // four consecutive floats (one 16-byte segment each), where a lane per
+    // hit would send each float as its own request.
+    const uint32_t p = lane & 3u;
 #pragma unroll
-      for (int f = 0; f < F; f++)
-        if (cv[k * F + f] != 0.0f) atomic_add(dl + (size_t)idx[k] * F + f, cv[k * F + f]);
+    for (int g = 0; g < 2 * F; g++) {
+      float t[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) t[i] = me ? cv[4 * g + i] : 0.0f;
+      quad_transpose(t);  // t[q]: value 4g + p of the quad's hit q
+      const int k0 = (4 * g) / F;  // corner of the quad's first value
+      const uint32_t f = (uint32_t)((4 * g) % F) + (F == 2 ? (p & 1u) : p);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        uint32_t e = quad_bcast(q, idx[k0]);
+        if constexpr (F == 2) {
+          const uint32_t e1 = quad_bcast(q, idx[k0 + 1]);  // values 2 and 3: the next corner
+          e = (p >> 1) != 0u ? e1 : e;
+        }
+        if (t[q] != 0.0f) atomic_add(dl + (size_t)e * F + f, t[q]);
+      }
+    }
   }
 }
 
@@ -271,59 +336,288 @@ __device__ __forceinline__ bool grid_coord_bwd(const GridParams& g, const float 
   return true;
 }
 
-// kRows 1: render mode 4, per-splat feature rows (p.colors, p.pgd wide) ahead
-// of the grid's channels (CR/backward.cu:987-1040).  kRows 2: render mode 12
-// training, rows of p.cstride floats ending with the blend weight (p.wslot):
-// p.pgd coarse channels from the row, then p.nfine channels blended
-// weight * row + (1 - weight) * grid (CR/backward.cu:1425-1520); with p.azero,
-// render mode 14 training: rows [pgd | weight], then weight * grid over p.nfine
-// channels when the weight is > 1e-6 (CR/backward.cu:1521-1590).
-template <int F, bool kHash, int kRows>
-__global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const RenderBwdParams p) {
-  __shared__ float4 srec[kBwdChunks][kBwdThreads];
+// Per-pixel inputs and back-to-front state of the render backward
+// (backward.cu:1597-1700): the pixel's output gradients, the forward's final
+// T, depth sums and contributor counts, and the blending recursion (the
+// colour blend as its two dot products with dL/dpixel).
+struct BwdPixel {
+  bool inside;
+  float pxf, pyf;
+  const float* dpix;  // channel c at dpix[c * HW]
+  float sum_abs;
+  float dL_ddepth, dL_daccum, dn2[3], dL_dmedian, dL_dreg;
+  uint32_t last_contributor;
+  int median_contributor;
+  float final_D, final_D2, final_A;
+  float T;
+  float acc_dot, last_dot;  // accum_rec . dpix, last_color . dpix
+  float last_depth, last_normal[3];
+  float accum_depth_rec, accum_alpha_rec, accum_normal_rec[3];
+  float last_dL_dT, last_alpha;
+};
+
+// Pixel (x0 + t % 16, y0 + t / 16) of thread t of the tile's workgroup.
+__device__ __forceinline__ void bwd_pixel_init(const RenderBwdParams& p, uint32_t tile, BwdPixel& px) {
+  const uint32_t tx = tile % p.gx, ty = tile / p.gx;
+  const uint32_t x = tx * kTile + (threadIdx.x & 15u);
+  const uint32_t y = ty * kTile + (threadIdx.x >> 4);
+  const bool inside = x < (uint32_t)p.W && y < (uint32_t)p.H;
+  const size_t HW = (size_t)p.W * p.H;
+  const size_t pid = inside ? (size_t)y * p.W + x : 0;
+  px.inside = inside;
+  px.pxf = (float)x;
+  px.pyf = (float)y;
+  px.dpix = p.dL_dpix + pid;
+  px.sum_abs = 0.0f;
+  if (inside)
+    for (int c = 0; c < p.C; c++) px.sum_abs += fabsf(px.dpix[(size_t)c * HW]);
+  const float* dO = p.dL_dothers;
+  px.dL_ddepth = inside ? dO[pid] : 0.0f;
+  px.dL_daccum = inside ? dO[HW + pid] : 0.0f;
+  px.dn2[0] = inside ? dO[2 * HW + pid] : 0.0f;
+  px.dn2[1] = inside ? dO[3 * HW + pid] : 0.0f;
+  px.dn2[2] = inside ? dO[4 * HW + pid] : 0.0f;
+  px.dL_dmedian = inside ? dO[5 * HW + pid] : 0.0f;
+  px.dL_dreg = inside ? dO[6 * HW + pid] : 0.0f;
+  const float T_final = inside ? p.final_T[pid] : 0.0f;
+  px.T = T_final;
+  px.last_contributor = inside ? p.n_contrib[pid] : 0u;
+  px.median_contributor = inside ? (int)p.n_contrib[pid + HW] : 0;
+  px.final_D = inside ? p.final_T[pid + HW] : 0.0f;
+  px.final_D2 = inside ? p.final_T[pid + 2 * HW] : 0.0f;
+  px.final_A = 1 - T_final;
+  px.acc_dot = px.last_dot = 0.0f;
+  px.last_depth = 0.0f;
+  px.accum_depth_rec = px.accum_alpha_rec = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 3; c++) px.last_normal[c] = px.accum_normal_rec[c] = 0.0f;
+  px.last_dL_dT = px.last_alpha = 0.0f;
+}
+
+// Ray/splat intersection of one staged record at the pixel.
+struct BwdHit {
+  float k[3], l[3], pp[3];
+  float s[2], d[2];
+  float c_d, G, demon, alpha;
+  bool use3d;
+};
+
+// The intersection, Gaussian and alpha of a splat at the pixel
+// (backward.cu:1700-1790); true for a hit that passes every test of the
+// forward.  pre: the pixel is inside and the splat precedes its last
+// contributor.
+__device__ __forceinline__ bool bwd_hit(const float4& q0, const float4& q1, const float4& q2, float pxf, float pyf,
+                                        float beta, bool pre, BwdHit& h) {
+  const float Tu[3] = {q0.x, q0.y, q0.z}, Tv[3] = {q0.w, q1.x, q1.y}, Tw[3] = {q1.z, q1.w, q2.x};
+#pragma unroll
+  for (int r = 0; r < 3; r++) {
+    h.k[r] = pxf * Tw[r] - Tu[r];
+    h.l[r] = pyf * Tw[r] - Tv[r];
+  }
+  h.pp[0] = h.k[1] * h.l[2] - h.k[2] * h.l[1];
+  h.pp[1] = h.k[2] * h.l[0] - h.k[0] * h.l[2];
+  h.pp[2] = h.k[0] * h.l[1] - h.k[1] * h.l[0];
+  bool act = pre && h.pp[2] != 0.0f;
+  h.s[0] = h.s[1] = 0.0f;
+  h.d[0] = h.d[1] = 0.0f;
+  h.c_d = 0.0f;
+  h.G = 0.0f;
+  h.demon = 1.0f;
+  h.alpha = 0.0f;
+  h.use3d = false;
+  if (act) {
+    h.s[0] = h.pp[0] / h.pp[2];
+    h.s[1] = h.pp[1] / h.pp[2];
+    const float rho3d = h.s[0] * h.s[0] + h.s[1] * h.s[1];
+    h.d[0] = q2.y - pxf;
+    h.d[1] = q2.z - pyf;
+    const float rho2d = 2.0f * (h.d[0] * h.d[0] + h.d[1] * h.d[1]);
+    const float rho = fminf(rho3d, rho2d);
+    h.use3d = rho3d <= rho2d;
+    h.c_d = h.use3d ? (h.s[0] * Tw[0] + h.s[1] * Tw[1]) + Tw[2] : Tw[2];
+    const float power = -0.5f * rho;
+    act = h.c_d >= 0.2f && power <= 0.0f;
+    if (act) {
+      h.G = expf_ref(power);
+      if (beta > 0.0f) {
+        h.demon = (float)(1.0 + (double)(beta * h.G));
+        h.G = (float)((1.0 + (double)beta) * (double)h.G / (double)h.demon);
+      }
+      h.alpha = fminf(0.99f, q2.w * h.G);
+      act = h.alpha >= 1.0f / 255.0f;
+    }
+  }
+  return act;
+}
+
+// Per-splat gradient contributions of one pixel's hit (zero without one).
+struct BwdGrad {
+  float gT[9], gH[9], gM[2], gN[3], gO;
+};
+
+__device__ __forceinline__ void bwd_grad_zero(BwdGrad& gr) {
+#pragma unroll
+  for (int r = 0; r < 9; r++) gr.gT[r] = gr.gH[r] = 0.0f;
+  gr.gM[0] = gr.gM[1] = 0.0f;
+  gr.gN[0] = gr.gN[1] = gr.gN[2] = 0.0f;
+  gr.gO = 0.0f;
+}
+
+// The blending recursion at a hit (T already divided by 1 - alpha) and the
+// gradients it sends to the splat (backward.cu:1799-1913): dot is the hit's
+// features (or colour) dotted with dL/dpixel, dxyz the gradient of that dot
+// product with respect to the intersection point (zero without a grid),
+// contributor the splat's index in the tile's list.
+template <bool kHash>
+__device__ __forceinline__ void bwd_hit_grad(BwdPixel& px, const BwdHit& h, const float4& q1, const float4& q2,
+                                             const float4& q3, const float4& q4, const float4& q5, float beta,
+                                             uint32_t contributor, float dot, const float dxyz[3], BwdGrad& gr) {
+  const float T = px.T, alpha = h.alpha, c_d = h.c_d;
+  const float Tw[2] = {q1.z, q1.w};
+  if constexpr (kHash) {
+    if (h.use3d) {
+      gr.gH[0] = dxyz[0] * h.s[0]; gr.gH[1] = dxyz[1] * h.s[0]; gr.gH[2] = dxyz[2] * h.s[0];
+      gr.gH[3] = dxyz[0] * h.s[1]; gr.gH[4] = dxyz[1] * h.s[1]; gr.gH[5] = dxyz[2] * h.s[1];
+    }
+    gr.gH[6] = dxyz[0]; gr.gH[7] = dxyz[1]; gr.gH[8] = dxyz[2];
+  }
+  // colour term of dL/dalpha (backward.cu:1799-1808 as dot products)
+  px.acc_dot = px.last_alpha * px.last_dot + (1.f - px.last_alpha) * px.acc_dot;
+  px.last_dot = dot;
+  float dL_dalpha = dot - px.acc_dot;
+  // RENDER_AXUTILITY terms (backward.cu:1815-1855)
+  float dL_dz = 0.0f;
+  const float m_d = 100.0f / (100.0f - 0.2f) * (1 - 0.2f / c_d);
+  const float dmd_dd = (100.0f * 0.2f) / ((100.0f - 0.2f) * c_d * c_d);
+  if ((int)contributor == px.median_contributor - 1) dL_dz += px.dL_dmedian;
+  const float dL_dweight = (px.final_D2 + m_d * m_d * px.final_A - 2 * m_d * px.final_D) * px.dL_dreg;
+  dL_dalpha += dL_dweight - px.last_dL_dT;
+  px.last_dL_dT = dL_dweight * alpha + (1 - alpha) * px.last_dL_dT;
+  const float dL_dmd = 2.0f * (T * alpha) * (m_d * px.final_A - px.final_D) * px.dL_dreg;
+  dL_dz += dL_dmd * dmd_dd;
+  px.accum_depth_rec = px.last_alpha * px.last_depth + (1.f - px.last_alpha) * px.accum_depth_rec;
+  px.last_depth = c_d;
+  dL_dalpha += (c_d - px.accum_depth_rec) * px.dL_ddepth;
+  px.accum_alpha_rec = px.last_alpha * 1.0f + (1.f - px.last_alpha) * px.accum_alpha_rec;
+  dL_dalpha += (1 - px.accum_alpha_rec) * px.dL_daccum;
+  const float nrm[3] = {q3.x, q3.y, q3.z};
+#pragma unroll
+  for (int ch = 0; ch < 3; ch++) {
+    px.accum_normal_rec[ch] = px.last_alpha * px.last_normal[ch] + (1.f - px.last_alpha) * px.accum_normal_rec[ch];
+    px.last_normal[ch] = nrm[ch];
+    dL_dalpha += (nrm[ch] - px.accum_normal_rec[ch]) * px.dn2[ch];
+    gr.gN[ch] = alpha * T * px.dn2[ch];
+  }
+  dL_dalpha *= T;
+  px.last_alpha = alpha;
+  float dL_dG = q2.w * dL_dalpha;
+  if (beta > 0.0f) {
+    const float dG_dg = (float)((1.0 + (double)beta) / (double)(h.demon * h.demon));
+    dL_dG *= dG_dg;
+  }
+  dL_dz += alpha * T * px.dL_ddepth;
+  float dL_duv[2] = {0.0f, 0.0f};
+  if constexpr (kHash) {
+    if (h.use3d) {
+      dL_duv[0] = dxyz[0] * q4.x + dxyz[1] * q4.y + dxyz[2] * q4.z;
+      dL_duv[1] = dxyz[0] * q4.w + dxyz[1] * q5.x + dxyz[2] * q5.y;
+    }
+  }
+  if (h.use3d) {
+    const float dG_factor = -h.G;
+    float dL_ds[2] = {dL_dG * dG_factor * h.s[0] + dL_dz * Tw[0], dL_dG * dG_factor * h.s[1] + dL_dz * Tw[1]};
+    dL_ds[0] += dL_duv[0];
+    dL_ds[1] += dL_duv[1];
+    const float dsx_pz = dL_ds[0] / h.pp[2], dsy_pz = dL_ds[1] / h.pp[2];
+    const float dp[3] = {dsx_pz, dsy_pz, -(dsx_pz * h.s[0] + dsy_pz * h.s[1])};
+    const float* k = h.k;
+    const float* l = h.l;
+    const float dk[3] = {l[1] * dp[2] - l[2] * dp[1], l[2] * dp[0] - l[0] * dp[2], l[0] * dp[1] - l[1] * dp[0]};
+    const float dl[3] = {dp[1] * k[2] - dp[2] * k[1], dp[2] * k[0] - dp[0] * k[2], dp[0] * k[1] - dp[1] * k[0]};
+    const float dz_dTw[3] = {h.s[0], h.s[1], 1.0f};
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+      gr.gT[r] = -dk[r];
+      gr.gT[3 + r] = -dl[r];
+      gr.gT[6 + r] = px.pxf * dk[r] + px.pyf * dl[r] + dL_dz * dz_dTw[r];
+    }
+  } else {
+    const float dG_factor_2d = -h.G * 2.0f;
+    gr.gM[0] = dL_dG * (dG_factor_2d * h.d[0]);
+    gr.gM[1] = dL_dG * (dG_factor_2d * h.d[1]);
+    gr.gT[8] = dL_dz;
+  }
+  gr.gO = h.G * dL_dalpha;
+}
+
+// The wave's per-splat sums (every lane takes part; lanes without a hit add
+// zeros) and one atomic per wave, splat and value.  gS is the |grad| sum,
+// wcol the colour weight (colour path and the per-splat rows), wt the row's
+// blend weight and fdot dL/dweight (render modes 7, 12 and 14).
+template <bool kHash, int kRows>
+__device__ __forceinline__ void bwd_splat_sums(const RenderBwdParams& p, const BwdPixel& px, uint32_t id, bool act,
+                                               const BwdGrad& gr, float gS, float wcol, float wt, float fdot) {
+  const size_t HW = (size_t)p.W * p.H;
+  const float* dpix = px.dpix;
+  const bool lead = (threadIdx.x & 63u) == 0u;
+#pragma unroll
+  for (int r = 0; r < 9; r++) {
+    const float v = wave_sum(gr.gT[r]);
+    if (lead && v != 0.0f) atomic_add(p.dtransmat + 9 * (size_t)id + r, v);
+  }
+  if constexpr (kHash) {
+#pragma unroll
+    for (int r = 0; r < 9; r++) {
+      const float v = wave_sum(gr.gH[r]);
+      if (lead && v != 0.0f) atomic_add(p.dhomo + 9 * (size_t)id + r, v);
+    }
+    const float vs = wave_sum(gS);
+    if (lead && vs != 0.0f) atomic_add(p.gradsum + id, vs);
+    if constexpr (kRows == 1) {
+      for (int ch = 0; ch < p.pgd; ch++) {
+        const float v = wave_sum(wcol * dpix[(size_t)ch * HW]);
+        if (lead && v != 0.0f) atomic_add(p.dcolors + (size_t)id * p.pgd + ch, v);
+      }
+    } else if constexpr (kRows == 2) {
+      float* dc = p.dcolors + (size_t)id * (uint32_t)p.cstride;
+      for (int ch = 0; ch < p.pgd + (p.azero ? 0 : p.nfine); ch++) {
+        const float v = wave_sum((ch < p.pgd ? wcol : wcol * wt) * dpix[(size_t)ch * HW]);
+        if (lead && v != 0.0f) atomic_add(dc + ch, v);
+      }
+      const float vw = wave_sum(act ? fdot : 0.0f);
+      if (lead && vw != 0.0f) atomic_add(dc + p.wslot, vw);
+    }
+  } else {
+    for (int ch = 0; ch < p.C; ch++) {
+      const float v = wave_sum(px.inside ? wcol * dpix[(size_t)ch * HW] : 0.0f);
+      if (lead && v != 0.0f) atomic_add(p.dcolors + (size_t)id * p.C + ch, v);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const float v = wave_sum(gr.gM[r]);
+    if (lead && v != 0.0f) atomic_add(p.dmean2D + 3 * (size_t)id + r, v);
+  }
+#pragma unroll
+  for (int r = 0; r < 3; r++) {
+    const float v = wave_sum(gr.gN[r]);
+    if (lead && v != 0.0f) atomic_add(p.dnormal + 3 * (size_t)id + r, v);
+  }
+  const float vo = wave_sum(gr.gO);
+  if (lead && vo != 0.0f) atomic_add(p.dopacity + id, vo);
+}
+
+// Colour path (no grid): the wave walks the staged splats back to front in
+// lockstep, every lane one pixel.
+__global__ void __launch_bounds__(kBwdThreads) render_backward_colour_kernel(const RenderBwdParams p) {
+  __shared__ float4 srec[4][kBwdThreads];
   __shared__ uint32_t sid[kBwdThreads];
 
   const uint32_t tile = p.tile_order[blockIdx.x];  // the forward's order: heaviest tiles first
-  const uint32_t tx = tile % p.gx, ty = tile / p.gx;
-  const uint32_t px = tx * kTile + (threadIdx.x & 15u);
-  const uint32_t py = ty * kTile + (threadIdx.x >> 4);
-  const bool inside = px < (uint32_t)p.W && py < (uint32_t)p.H;
-  const float pxf = (float)px, pyf = (float)py;
-  const size_t HW = (size_t)p.W * p.H;
-  const size_t pid = inside ? (size_t)py * p.W + px : 0;
   const uint2 range = reinterpret_cast<const uint2*>(p.ranges)[tile];
-  const int C = p.C;
-
-  const float* dpix = p.dL_dpix + pid;  // channel c at dpix[c * HW]
-  float sum_abs = 0.0f;
-  if (inside)
-    for (int c = 0; c < C; c++) sum_abs += fabsf(dpix[(size_t)c * HW]);
-  const float* dO = p.dL_dothers;
-  const float dL_ddepth = inside ? dO[pid] : 0.0f;
-  const float dL_daccum = inside ? dO[HW + pid] : 0.0f;
-  const float dn2[3] = {inside ? dO[2 * HW + pid] : 0.0f, inside ? dO[3 * HW + pid] : 0.0f,
-                        inside ? dO[4 * HW + pid] : 0.0f};
-  const float dL_dmedian = inside ? dO[5 * HW + pid] : 0.0f;
-  const float dL_dreg = inside ? dO[6 * HW + pid] : 0.0f;
-
-  const float T_final = inside ? p.final_T[pid] : 0.0f;
-  float T = T_final;
-  const uint32_t last_contributor = inside ? p.n_contrib[pid] : 0u;
-  const int median_contributor = inside ? (int)p.n_contrib[pid + HW] : 0;
-  const float final_D = inside ? p.final_T[pid + HW] : 0.0f;
-  const float final_D2 = inside ? p.final_T[pid + 2 * HW] : 0.0f;
-  const float final_A = 1 - T_final;
-
-  float acc_dot = 0.0f, last_dot = 0.0f;  // accum_rec . dpix, last_color . dpix
-  float last_depth = 0.0f, last_normal[3] = {0.0f, 0.0f, 0.0f};
-  float accum_depth_rec = 0.0f, accum_alpha_rec = 0.0f, accum_normal_rec[3] = {0.0f, 0.0f, 0.0f};
-  float last_dL_dT = 0.0f, last_alpha = 0.0f;
-
-  const GridParams& g = p.grid;
-  nest_i32x4 rsrc{};
-  if constexpr (kHash) rsrc = table_rsrc_rows<F, false>(g.table, g.table_rows);
-
-  uint32_t contributor = range.y - range.x;
+  const size_t HW = (size_t)p.W * p.H;
+  BwdPixel px;
+  bwd_pixel_init(p, tile, px);
   const uint32_t total = range.y - range.x;
   for (uint32_t done_n = 0; done_n < total; done_n += kBwdThreads) {
     const uint32_t n = min((uint32_t)kBwdThreads, total - done_n);
@@ -333,244 +627,237 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
       const uint32_t id = p.point_list[e];
       const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id;
 #pragma unroll
-      for (int c = 0; c < kBwdChunks; c++)
-        if (kHash || c < 4) srec[c][threadIdx.x] = rec[c];
+      for (int c = 0; c < 4; c++) srec[c][threadIdx.x] = rec[c];
       sid[threadIdx.x] = id;
     }
     __syncthreads();
     for (uint32_t j = 0; j < n; j++) {
-      contributor--;
+      const uint32_t contributor = total - 1u - done_n - j;
       const float4 q0 = srec[0][j], q1 = srec[1][j], q2 = srec[2][j], q3 = srec[3][j];
       const uint32_t id = sid[j];
-      const float Tu[3] = {q0.x, q0.y, q0.z}, Tv[3] = {q0.w, q1.x, q1.y}, Tw[3] = {q1.z, q1.w, q2.x};
-      const float k[3] = {pxf * Tw[0] - Tu[0], pxf * Tw[1] - Tu[1], pxf * Tw[2] - Tu[2]};
-      const float l[3] = {pyf * Tw[0] - Tv[0], pyf * Tw[1] - Tv[1], pyf * Tw[2] - Tv[2]};
-      const float pp[3] = {k[1] * l[2] - k[2] * l[1], k[2] * l[0] - k[0] * l[2], k[0] * l[1] - k[1] * l[0]};
-      bool act = inside && contributor < last_contributor && pp[2] != 0.0f;
-      float s[2] = {0.0f, 0.0f}, rho3d = 0.0f, rho2d = 0.0f, d[2] = {0.0f, 0.0f}, c_d = 0.0f;
-      float G = 0.0f, demon = 1.0f, alpha = 0.0f;
-      bool use3d = false;
+      BwdHit h;
+      const bool act = bwd_hit(q0, q1, q2, px.pxf, px.pyf, p.beta, px.inside && contributor < px.last_contributor, h);
+      BwdGrad gr;
+      bwd_grad_zero(gr);
+      float wcol = 0.0f;
       if (act) {
-        s[0] = pp[0] / pp[2];
-        s[1] = pp[1] / pp[2];
-        rho3d = s[0] * s[0] + s[1] * s[1];
-        d[0] = q2.y - pxf;
-        d[1] = q2.z - pyf;
-        rho2d = 2.0f * (d[0] * d[0] + d[1] * d[1]);
-        const float rho = fminf(rho3d, rho2d);
-        use3d = rho3d <= rho2d;
-        c_d = use3d ? (s[0] * Tw[0] + s[1] * Tw[1]) + Tw[2] : Tw[2];
-        const float power = -0.5f * rho;
-        act = c_d >= 0.2f && power <= 0.0f;
-        if (act) {
-          G = expf_ref(power);
-          if (p.beta > 0.0f) {
-            demon = (float)(1.0 + (double)(p.beta * G));
-            G = (float)((1.0 + (double)p.beta) * (double)G / (double)demon);
-          }
-          alpha = fminf(0.99f, q2.w * G);
-          act = alpha >= 1.0f / 255.0f;
-        }
+        px.T = px.T / (1.f - h.alpha);
+        const float wgt = h.alpha * px.T;
+        const float* col = p.colors + (size_t)id * p.C;
+        float dot = 0.0f;
+        for (int ch = 0; ch < p.C; ch++) dot += col[ch] * px.dpix[(size_t)ch * HW];
+        wcol = wgt;
+        const float dxyz[3] = {0.0f, 0.0f, 0.0f};
+        bwd_hit_grad<false>(px, h, q1, q2, q3, q3, q3, p.beta, contributor, dot, dxyz, gr);
       }
-      // per-splat gradient contributions of this lane (zero when inactive)
-      float gT[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0}, gH[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
-      float gM[2] = {0.0f, 0.0f}, gN[3] = {0.0f, 0.0f, 0.0f}, gO = 0.0f, gS = 0.0f;
-      float wcol = 0.0f;  // dchannel_dcolor of the colour path
-      float wgt = 0.0f, dot = 0.0f, rdot = 0.0f, wt = 0.0f, fdot = 0.0f;
-      float dxyz[3] = {0.0f, 0.0f, 0.0f};
-      float u[3] = {0.0f, 0.0f, 0.0f}, grad_scale = 0.0f;
-      uint32_t lane_levels = 0u;
-      if (act) {
-        T = T / (1.f - alpha);
-        wgt = alpha * T;
-        if constexpr (!kHash) {
-          const float* col = p.colors + (size_t)id * C;
-          for (int ch = 0; ch < C; ch++) dot += col[ch] * dpix[(size_t)ch * HW];
-          wcol = wgt;
-        } else {
-          const float4 q4 = srec[4][j], q5 = srec[5][j], q6 = srec[6][j];
-          float xyz[3];
-          if (use3d) {
-            xyz[0] = s[0] * q4.x + s[1] * q4.w + q5.z;
-            xyz[1] = s[0] * q4.y + s[1] * q5.x + q5.w;
-            xyz[2] = s[0] * q4.z + s[1] * q5.y + q6.x;
-          } else {
-            xyz[0] = q5.z; xyz[1] = q5.w; xyz[2] = q6.x;
-          }
-          gS = wgt * sum_abs;
-          if constexpr (kRows == 1) {
-            const float* row = p.colors + (size_t)id * p.pgd;
-            for (int ch = 0; ch < p.pgd; ch++) rdot += row[ch] * dpix[(size_t)ch * HW];
-            wcol = wgt;
-          } else if constexpr (kRows == 2) {
-            const float* row = p.colors + (size_t)id * (uint32_t)p.cstride;
-            wt = row[p.wslot];
-            for (int ch = 0; ch < p.pgd; ch++) rdot += row[ch] * dpix[(size_t)ch * HW];
-            if (!p.azero)
-              for (int i = 0; i < p.nfine; i++) fdot += row[p.pgd + i] * dpix[(size_t)(p.pgd + i) * HW];
-            wcol = wgt;
-          }
-          const uint32_t ap = __float_as_uint(q3.w);
-          const uint32_t maxl = ap < g.L ? ap : g.L;
-          lane_levels = grid_coord_bwd(g, xyz, u, grad_scale) ? maxl : 0u;
-          if (kRows == 2 && p.azero && !(wt > 1e-6f)) lane_levels = 0u;  // mode 14 skips the grid
-        }
-      }
-      if constexpr (kHash) {
-        // every lane takes part (cross-lane sums inside); lanes without a hit have no levels
-        // the grid's share of the gradient: (1 - weight) of it in mode 12,
-        // weight times it in mode 14
-        if (__ballot(lane_levels > 0u) != 0ull)
-          hash_backward_wave<F>(g, rsrc, u, grad_scale, lane_levels,
-                                kRows == 2 ? wgt * (p.azero ? wt : 1.0f - wt) : wgt,
-                                kRows ? dpix + (size_t)p.pgd * HW : dpix, HW, p.dtable, dot, dxyz);
-        if constexpr (kRows == 1) {
-          dot += rdot;
-        } else if constexpr (kRows == 2) {
-          // dot is grid . dpix over the fine channels; the hit's features are
-          // the coarse rows and weight * row + (1 - weight) * grid
-          const float hdot = dot;
-          if (p.azero) {  // mode 14: coarse rows, then weight * grid
-            dot = rdot + wt * hdot;
-            fdot = wgt * hdot;  // dL/dweight
-          } else {
-            dot = rdot + wt * fdot + (1.0f - wt) * hdot;
-            fdot = wgt * (fdot - hdot);  // dL/dweight
-            if (p.wsig) fdot = fdot * wt * (1.0f - wt);  // mode 7: dL/dlogit of weight = sigmoid(logit)
-          }
-        }
-      }
-      if (act) {
-        if constexpr (kHash) {
-          if (use3d) {
-            gH[0] = dxyz[0] * s[0]; gH[1] = dxyz[1] * s[0]; gH[2] = dxyz[2] * s[0];
-            gH[3] = dxyz[0] * s[1]; gH[4] = dxyz[1] * s[1]; gH[5] = dxyz[2] * s[1];
-          }
-          gH[6] = dxyz[0]; gH[7] = dxyz[1]; gH[8] = dxyz[2];
-        }
-        // colour term of dL/dalpha (backward.cu:1799-1808 as dot products)
-        acc_dot = last_alpha * last_dot + (1.f - last_alpha) * acc_dot;
-        last_dot = dot;
-        float dL_dalpha = dot - acc_dot;
-        // RENDER_AXUTILITY terms (backward.cu:1815-1855)
-        float dL_dz = 0.0f;
-        const float m_d = 100.0f / (100.0f - 0.2f) * (1 - 0.2f / c_d);
-        const float dmd_dd = (100.0f * 0.2f) / ((100.0f - 0.2f) * c_d * c_d);
-        if ((int)contributor == median_contributor - 1) dL_dz += dL_dmedian;
-        const float dL_dweight = (final_D2 + m_d * m_d * final_A - 2 * m_d * final_D) * dL_dreg;
-        dL_dalpha += dL_dweight - last_dL_dT;
-        last_dL_dT = dL_dweight * alpha + (1 - alpha) * last_dL_dT;
-        const float dL_dmd = 2.0f * (T * alpha) * (m_d * final_A - final_D) * dL_dreg;
-        dL_dz += dL_dmd * dmd_dd;
-        accum_depth_rec = last_alpha * last_depth + (1.f - last_alpha) * accum_depth_rec;
-        last_depth = c_d;
-        dL_dalpha += (c_d - accum_depth_rec) * dL_ddepth;
-        accum_alpha_rec = last_alpha * 1.0f + (1.f - last_alpha) * accum_alpha_rec;
-        dL_dalpha += (1 - accum_alpha_rec) * dL_daccum;
-        const float nrm[3] = {q3.x, q3.y, q3.z};
-#pragma unroll
-        for (int ch = 0; ch < 3; ch++) {
-          accum_normal_rec[ch] = last_alpha * last_normal[ch] + (1.f - last_alpha) * accum_normal_rec[ch];
-          last_normal[ch] = nrm[ch];
-          dL_dalpha += (nrm[ch] - accum_normal_rec[ch]) * dn2[ch];
-          gN[ch] = alpha * T * dn2[ch];
-        }
-        dL_dalpha *= T;
-        last_alpha = alpha;
-        float dL_dG = q2.w * dL_dalpha;
-        if (p.beta > 0.0f) {
-          const float dG_dg = (float)((1.0 + (double)p.beta) / (double)(demon * demon));
-          dL_dG *= dG_dg;
-        }
-        dL_dz += alpha * T * dL_ddepth;
-        float dL_duv[2] = {0.0f, 0.0f};
-        if constexpr (kHash) {
-          if (use3d) {
-            const float4 q4 = srec[4][j], q5 = srec[5][j];
-            dL_duv[0] = dxyz[0] * q4.x + dxyz[1] * q4.y + dxyz[2] * q4.z;
-            dL_duv[1] = dxyz[0] * q4.w + dxyz[1] * q5.x + dxyz[2] * q5.y;
-          }
-        }
-        if (use3d) {
-          const float dG_factor = -G;
-          float dL_ds[2] = {dL_dG * dG_factor * s[0] + dL_dz * Tw[0], dL_dG * dG_factor * s[1] + dL_dz * Tw[1]};
-          dL_ds[0] += dL_duv[0];
-          dL_ds[1] += dL_duv[1];
-          const float dsx_pz = dL_ds[0] / pp[2], dsy_pz = dL_ds[1] / pp[2];
-          const float dp[3] = {dsx_pz, dsy_pz, -(dsx_pz * s[0] + dsy_pz * s[1])};
-          const float dk[3] = {l[1] * dp[2] - l[2] * dp[1], l[2] * dp[0] - l[0] * dp[2], l[0] * dp[1] - l[1] * dp[0]};
-          const float dl[3] = {dp[1] * k[2] - dp[2] * k[1], dp[2] * k[0] - dp[0] * k[2], dp[0] * k[1] - dp[1] * k[0]};
-          const float dz_dTw[3] = {s[0], s[1], 1.0f};
-#pragma unroll
-          for (int r = 0; r < 3; r++) {
-            gT[r] = -dk[r];
-            gT[3 + r] = -dl[r];
-            gT[6 + r] = pxf * dk[r] + pyf * dl[r] + dL_dz * dz_dTw[r];
-          }
-        } else {
-          const float dG_factor_2d = -G * 2.0f;
-          gM[0] = dL_dG * (dG_factor_2d * d[0]);
-          gM[1] = dL_dG * (dG_factor_2d * d[1]);
-          gT[8] = dL_dz;
-        }
-        gO = G * dL_dalpha;
-      }
-      // wave sums and one atomic per wave and splat
-      if (__ballot(act) != 0ull) {
-        const bool lead = (threadIdx.x & 63u) == 0u;
-#pragma unroll
-        for (int r = 0; r < 9; r++) {
-          const float v = wave_sum(gT[r]);
-          if (lead && v != 0.0f) atomic_add(p.dtransmat + 9 * (size_t)id + r, v);
-        }
-        if constexpr (kHash) {
-#pragma unroll
-          for (int r = 0; r < 9; r++) {
-            const float v = wave_sum(gH[r]);
-            if (lead && v != 0.0f) atomic_add(p.dhomo + 9 * (size_t)id + r, v);
-          }
-          const float vs = wave_sum(gS);
-          if (lead && vs != 0.0f) atomic_add(p.gradsum + id, vs);
-          if constexpr (kRows == 1) {
-            for (int ch = 0; ch < p.pgd; ch++) {
-              const float v = wave_sum(wcol * dpix[(size_t)ch * HW]);
-              if (lead && v != 0.0f) atomic_add(p.dcolors + (size_t)id * p.pgd + ch, v);
-            }
-          } else if constexpr (kRows == 2) {
-            float* dc = p.dcolors + (size_t)id * (uint32_t)p.cstride;
-            for (int ch = 0; ch < p.pgd + (p.azero ? 0 : p.nfine); ch++) {
-              const float v = wave_sum((ch < p.pgd ? wcol : wcol * wt) * dpix[(size_t)ch * HW]);
-              if (lead && v != 0.0f) atomic_add(dc + ch, v);
-            }
-            const float vw = wave_sum(act ? fdot : 0.0f);
-            if (lead && vw != 0.0f) atomic_add(dc + p.wslot, vw);
-          }
-        } else {
-          for (int ch = 0; ch < C; ch++) {
-            const float v = wave_sum(inside ? wcol * dpix[(size_t)ch * HW] : 0.0f);
-            if (lead && v != 0.0f) atomic_add(p.dcolors + (size_t)id * C + ch, v);
-          }
-        }
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-          const float v = wave_sum(gM[r]);
-          if (lead && v != 0.0f) atomic_add(p.dmean2D + 3 * (size_t)id + r, v);
-        }
-#pragma unroll
-        for (int r = 0; r < 3; r++) {
-          const float v = wave_sum(gN[r]);
-          if (lead && v != 0.0f) atomic_add(p.dnormal + 3 * (size_t)id + r, v);
-        }
-        const float vo = wave_sum(gO);
-        if (lead && vo != 0.0f) atomic_add(p.dopacity + id, vo);
-      }
+      if (__ballot(act) != 0ull) bwd_splat_sums<false, 0>(p, px, id, act, gr, 0.0f, wcol, 0.0f, 0.0f);
     }
   }
 }
 
-template <int F, bool kHash, int kRows = 0>
+// Grid path.  A wave walks a batch of staged splats in segments of three
+// passes:
+//  1. geometry: the splats in lockstep, every lane one pixel; a hit with grid
+//     levels queues (grid coordinate, weight, grad_scale, owner lane, level
+//     count) in the wave's LDS queue, and every splat with a hit in the wave
+//     is listed with its hit and queue masks.  The segment ends when the
+//     queue could overflow at the next splat;
+//  2. grid: the queued hits spread one per lane, so the table gathers, the
+//     feature recomputation, dL/dxyz and the table-gradient scatter run with
+//     every lane busy; each hit's (dot, dxyz) replaces its queue entry;
+//  3. recursion: the listed splats again, in the same order, with the
+//     blending recursion per pixel and the per-splat wave sums.
+// kRows 1: render mode 4, per-splat feature rows (p.colors, p.pgd wide) ahead
+// of the grid's channels (CR/backward.cu:987-1040).  kRows 2: render mode 12
+// training, rows of p.cstride floats ending with the blend weight (p.wslot):
+// p.pgd coarse channels from the row, then p.nfine channels blended
+// weight * row + (1 - weight) * grid (CR/backward.cu:1425-1520); with p.azero,
+// render mode 14 training: rows [pgd | weight], then weight * grid over p.nfine
+// channels when the weight is > 1e-6 (CR/backward.cu:1521-1590).
+constexpr int kBwdQueue = 256;  // queued grid hits per wave
+constexpr int kBwdWaves = kBwdThreads / 64;
+
+template <int F, int kRows>
+__global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const RenderBwdParams p) {
+  __shared__ float4 srec[kBwdChunks][kBwdThreads];
+  __shared__ uint32_t sid[kBwdThreads];
+  __shared__ float4 hq[kBwdWaves][kBwdQueue];     // (u, w), then (dot, dxyz)
+  __shared__ float hgs[kBwdWaves][kBwdQueue];     // grad_scale
+  __shared__ uint16_t hmeta[kBwdWaves][kBwdQueue];  // owner lane | level count << 6
+  __shared__ uint64_t lact[kBwdWaves][kBwdThreads], lpush[kBwdWaves][kBwdThreads];
+  __shared__ uint8_t lj[kBwdWaves][kBwdThreads];
+
+  const uint32_t tile = p.tile_order[blockIdx.x];  // the forward's order: heaviest tiles first
+  const uint2 range = reinterpret_cast<const uint2*>(p.ranges)[tile];
+  const size_t HW = (size_t)p.W * p.H;
+  const uint32_t lane = threadIdx.x & 63u, wid = threadIdx.x >> 6;
+  const uint64_t lt = lane == 0u ? 0ull : (~0ull >> (64u - lane));
+  BwdPixel px;
+  bwd_pixel_init(p, tile, px);
+  const uint32_t tx = tile % p.gx, ty = tile / p.gx;
+  const GridParams& g = p.grid;
+  const nest_i32x4 rsrc = table_rsrc_rows<F, false>(g.table, g.table_rows);
+  const size_t grid_ch = kRows ? (size_t)p.pgd * HW : 0;  // first grid channel of dL/dpixel
+
+  const uint32_t total = range.y - range.x;
+  for (uint32_t done_n = 0; done_n < total; done_n += kBwdThreads) {
+    const uint32_t n = min((uint32_t)kBwdThreads, total - done_n);
+    __syncthreads();
+    if (threadIdx.x < n) {
+      const uint32_t e = range.y - 1u - done_n - threadIdx.x;
+      const uint32_t id = p.point_list[e];
+      const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id;
+#pragma unroll
+      for (int c = 0; c < kBwdChunks; c++) srec[c][threadIdx.x] = rec[c];
+      sid[threadIdx.x] = id;
+    }
+    __syncthreads();
+    for (uint32_t j0 = 0; j0 < n;) {
+      // 1. geometry
+      float T1 = px.T;
+      uint32_t cnt = 0, nl = 0, j = j0;
+      while (j < n) {
+        const uint32_t contributor = total - 1u - done_n - j;
+        const float4 q0 = srec[0][j], q1 = srec[1][j], q2 = srec[2][j];
+        BwdHit h;
+        const bool act =
+            bwd_hit(q0, q1, q2, px.pxf, px.pyf, p.beta, px.inside && contributor < px.last_contributor, h);
+        float u[3] = {0.0f, 0.0f, 0.0f}, grad_scale = 0.0f, hw = 0.0f;
+        uint32_t lane_levels = 0u;
+        if (act) {
+          T1 = T1 / (1.f - h.alpha);
+          const float wgt = h.alpha * T1;
+          const float4 q3 = srec[3][j], q4 = srec[4][j], q5 = srec[5][j], q6 = srec[6][j];
+          float xyz[3];
+          if (h.use3d) {
+            xyz[0] = h.s[0] * q4.x + h.s[1] * q4.w + q5.z;
+            xyz[1] = h.s[0] * q4.y + h.s[1] * q5.x + q5.w;
+            xyz[2] = h.s[0] * q4.z + h.s[1] * q5.y + q6.x;
+          } else {
+            xyz[0] = q5.z; xyz[1] = q5.w; xyz[2] = q6.x;
+          }
+          const uint32_t ap = __float_as_uint(q3.w);
+          const uint32_t maxl = ap < g.L ? ap : g.L;
+          lane_levels = grid_coord_bwd(g, xyz, u, grad_scale) ? maxl : 0u;
+          hw = wgt;
+          if constexpr (kRows == 2) {
+            // the grid's share of the gradient: (1 - weight) of it in mode 12,
+            // weight times it in mode 14, which skips the grid at weight <= 1e-6
+            const float wt = p.colors[(size_t)sid[j] * (uint32_t)p.cstride + p.wslot];
+            if (p.azero && !(wt > 1e-6f)) lane_levels = 0u;
+            hw = wgt * (p.azero ? wt : 1.0f - wt);
+          }
+        }
+        const bool push = lane_levels > 0u;
+        const uint64_t m_act = __ballot(act), m_push = __ballot(push);
+        if (m_act != 0ull) {
+          if (lane == 0u) {
+            lact[wid][nl] = m_act;
+            lpush[wid][nl] = m_push;
+            lj[wid][nl] = (uint8_t)j;
+          }
+          nl++;
+        }
+        if (push) {
+          const uint32_t slot = cnt + (uint32_t)__popcll(m_push & lt);
+          hq[wid][slot] = make_float4(u[0], u[1], u[2], hw);
+          hgs[wid][slot] = grad_scale;
+          hmeta[wid][slot] = (uint16_t)(lane | (lane_levels << 6));
+        }
+        cnt += (uint32_t)__popcll(m_push);
+        j++;
+        if (cnt > (uint32_t)(kBwdQueue - 64)) break;
+      }
+      __builtin_amdgcn_wave_barrier();
+      // 2. grid: table gradient, features' dot product and dL/dxyz per hit
+      for (uint32_t r0 = 0; r0 < cnt; r0 += 64u) {
+        const uint32_t e = r0 + lane;
+        const bool on = e < cnt;
+        float u[3] = {0.0f, 0.0f, 0.0f}, gsc = 0.0f, w = 0.0f;
+        uint32_t lev = 0u;
+        const float* dp = p.dL_dpix;
+        if (on) {
+          const float4 q = hq[wid][e];
+          u[0] = q.x; u[1] = q.y; u[2] = q.z; w = q.w;
+          gsc = hgs[wid][e];
+          const uint32_t m = hmeta[wid][e];
+          lev = m >> 6;
+          const uint32_t t = (wid << 6) | (m & 63u);  // the owner's thread
+          dp = p.dL_dpix + ((size_t)(ty * kTile + (t >> 4)) * p.W + tx * kTile + (t & 15u)) + grid_ch;
+        }
+        float dot, dxyz[3];
+        hash_backward_wave<F>(g, rsrc, u, gsc, lev, w, dp, HW, p.dtable, dot, dxyz);
+        if (on) hq[wid][e] = make_float4(dot, dxyz[0], dxyz[1], dxyz[2]);
+      }
+      __builtin_amdgcn_wave_barrier();
+      // 3. recursion and per-splat sums over the listed splats
+      uint32_t qbase = 0;
+      for (uint32_t i = 0; i < nl; i++) {
+        const uint32_t jj = lj[wid][i];
+        const uint64_t m_act = lact[wid][i], m_push = lpush[wid][i];
+        const bool act = ((m_act >> lane) & 1ull) != 0ull;
+        const bool pushed = ((m_push >> lane) & 1ull) != 0ull;
+        const uint32_t contributor = total - 1u - done_n - jj;
+        const float4 q0 = srec[0][jj], q1 = srec[1][jj], q2 = srec[2][jj], q3 = srec[3][jj];
+        const float4 q4 = srec[4][jj], q5 = srec[5][jj];
+        const uint32_t id = sid[jj];
+        BwdHit h;
+        bwd_hit(q0, q1, q2, px.pxf, px.pyf, p.beta, act, h);
+        BwdGrad gr;
+        bwd_grad_zero(gr);
+        float gS = 0.0f, wcol = 0.0f, wt = 0.0f, fdot = 0.0f;
+        if (act) {
+          px.T = px.T / (1.f - h.alpha);
+          const float wgt = h.alpha * px.T;
+          gS = wgt * px.sum_abs;
+          float rdot = 0.0f, dot = 0.0f, dxyz[3] = {0.0f, 0.0f, 0.0f};
+          if (pushed) {
+            const float4 r = hq[wid][qbase + (uint32_t)__popcll(m_push & lt)];
+            dot = r.x; dxyz[0] = r.y; dxyz[1] = r.z; dxyz[2] = r.w;
+          }
+          if constexpr (kRows == 1) {
+            const float* row = p.colors + (size_t)id * p.pgd;
+            for (int ch = 0; ch < p.pgd; ch++) rdot += row[ch] * px.dpix[(size_t)ch * HW];
+            wcol = wgt;
+            dot += rdot;
+          } else if constexpr (kRows == 2) {
+            // dot is grid . dpix over the fine channels; the hit's features are
+            // the coarse rows and weight * row + (1 - weight) * grid
+            const float* row = p.colors + (size_t)id * (uint32_t)p.cstride;
+            wt = row[p.wslot];
+            for (int ch = 0; ch < p.pgd; ch++) rdot += row[ch] * px.dpix[(size_t)ch * HW];
+            if (!p.azero)
+              for (int i2 = 0; i2 < p.nfine; i2++) fdot += row[p.pgd + i2] * px.dpix[(size_t)(p.pgd + i2) * HW];
+            wcol = wgt;
+            const float hdot = dot;
+            if (p.azero) {  // mode 14: coarse rows, then weight * grid
+              dot = rdot + wt * hdot;
+              fdot = wgt * hdot;  // dL/dweight
+            } else {
+              dot = rdot + wt * fdot + (1.0f - wt) * hdot;
+              fdot = wgt * (fdot - hdot);  // dL/dweight
+              if (p.wsig) fdot = fdot * wt * (1.0f - wt);  // mode 7: dL/dlogit of weight = sigmoid(logit)
+            }
+          }
+          bwd_hit_grad<true>(px, h, q1, q2, q3, q4, q5, p.beta, contributor, dot, dxyz, gr);
+        }
+        qbase += (uint32_t)__popcll(m_push);
+        bwd_splat_sums<true, kRows>(p, px, id, act, gr, gS, wcol, wt, fdot);
+      }
+      __builtin_amdgcn_wave_barrier();
+      j0 = j;
+    }
+  }
+}
+
+template <int F, int kRows = 0>
 hipError_t launch_bwd_one(const RenderBwdParams& p, hipStream_t s) {
-  hipLaunchKernelGGL((render_backward_kernel<F, kHash, kRows>), dim3(p.ntiles), dim3(kBwdThreads), 0, s, p);
+  hipLaunchKernelGGL((render_backward_kernel<F, kRows>), dim3(p.ntiles), dim3(kBwdThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_colour(const RenderBwdParams& p, hipStream_t s) {
+  hipLaunchKernelGGL(render_backward_colour_kernel, dim3(p.ntiles), dim3(kBwdThreads), 0, s, p);
   return hipGetLastError();
 }
 
@@ -873,26 +1160,26 @@ hipError_t launch_render_backward(const RenderBwdParams& p, hipStream_t s) {
   if (p.ntiles == 0) return hipSuccess;
   if (p.wslot >= 0) {
     switch (p.grid.F) {
-      case 2: return launch_bwd_one<2, true, 2>(p, s);
-      case 4: return launch_bwd_one<4, true, 2>(p, s);
-      case 8: return launch_bwd_one<8, true, 2>(p, s);
+      case 2: return launch_bwd_one<2, 2>(p, s);
+      case 4: return launch_bwd_one<4, 2>(p, s);
+      case 8: return launch_bwd_one<8, 2>(p, s);
       default: return hipErrorInvalidValue;
     }
   }
   if (p.pgd > 0) {
     switch (p.grid.F) {
-      case 2: return launch_bwd_one<2, true, 1>(p, s);
-      case 4: return launch_bwd_one<4, true, 1>(p, s);
-      case 8: return launch_bwd_one<8, true, 1>(p, s);
+      case 2: return launch_bwd_one<2, 1>(p, s);
+      case 4: return launch_bwd_one<4, 1>(p, s);
+      case 8: return launch_bwd_one<8, 1>(p, s);
       default: return hipErrorInvalidValue;
     }
   }
-  if (p.level == 0) return launch_bwd_one<1, false>(p, s);
+  if (p.level == 0) return launch_bwd_colour(p, s);
   switch (p.grid.F) {
-    case 1: return launch_bwd_one<1, true>(p, s);
-    case 2: return launch_bwd_one<2, true>(p, s);
-    case 4: return launch_bwd_one<4, true>(p, s);
-    case 8: return launch_bwd_one<8, true>(p, s);
+    case 1: return launch_bwd_one<1>(p, s);
+    case 2: return launch_bwd_one<2>(p, s);
+    case 4: return launch_bwd_one<4>(p, s);
+    case 8: return launch_bwd_one<8>(p, s);
     default: return hipErrorInvalidValue;
   }
 }

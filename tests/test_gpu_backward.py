@@ -116,7 +116,7 @@ def _compare(gpu, ref, pre):
             assert not o[~vis].any(), k  # culled splats get no gradient
 
 
-@pytest.mark.parametrize("name", ["cfg1", "shell_small", "unbounded_small"])
+@pytest.mark.parametrize("name", ["cfg1", "shell_small", "unbounded_small", "unbounded_f8", "unbounded_f1"])
 def test_backward_hash_parity(oracle, name):
     sc = scene(name)
     print(f"[case] backward hash {name} P={sc.spec.P}", flush=True)
