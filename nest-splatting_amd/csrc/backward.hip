@@ -674,18 +674,47 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_colour_kernel(con
 // weight * row + (1 - weight) * grid (CR/backward.cu:1425-1520); with p.azero,
 // render mode 14 training: rows [pgd | weight], then weight * grid over p.nfine
 // channels when the weight is > 1e-6 (CR/backward.cu:1521-1590).
+// Grid inputs of a hit (T already divided): the intersection point xyz, the
+// level count (0: no lookup) and, in render modes 12 and 14, the row's blend
+// weight wt (mode 14 skips the grid at a weight <= 1e-6).
+template <int kRows>
+__device__ __forceinline__ uint32_t bwd_hit_levels(const RenderBwdParams& p, const BwdHit& h, const float4& q3,
+                                                   const float4& q4, const float4& q5, const float4& q6, uint32_t id,
+                                                   float xyz[3], float& wt) {
+  if (h.use3d) {
+    xyz[0] = h.s[0] * q4.x + h.s[1] * q4.w + q5.z;
+    xyz[1] = h.s[0] * q4.y + h.s[1] * q5.x + q5.w;
+    xyz[2] = h.s[0] * q4.z + h.s[1] * q5.y + q6.x;
+  } else {
+    xyz[0] = q5.z; xyz[1] = q5.w; xyz[2] = q6.x;
+  }
+  const uint32_t ap = __float_as_uint(q3.w);
+  const uint32_t maxl = ap < p.grid.L ? ap : p.grid.L;
+  float u[3], grad_scale;
+  uint32_t lane_levels = grid_coord_bwd(p.grid, xyz, u, grad_scale) ? maxl : 0u;
+  wt = 0.0f;
+  if constexpr (kRows == 2) {
+    wt = p.colors[(size_t)id * (uint32_t)p.cstride + p.wslot];
+    if (p.azero && !(wt > 1e-6f)) lane_levels = 0u;
+  }
+  return lane_levels;
+}
+
 constexpr int kBwdQueue = 256;  // queued grid hits per wave
+constexpr int kBwdList = 128;   // listed splats per wave and segment
 constexpr int kBwdWaves = kBwdThreads / 64;
 
+// Three workgroups per CU (51.5 KB of LDS each) where the registers allow:
+// F <= 4 fits 168 VGPRs without spills, F = 8 keeps two.
 template <int F, int kRows>
-__global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const RenderBwdParams p) {
+__global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_eu(F <= 4 ? 3 : 2)))
+render_backward_kernel(const RenderBwdParams p) {
   __shared__ float4 srec[kBwdChunks][kBwdThreads];
   __shared__ uint32_t sid[kBwdThreads];
-  __shared__ float4 hq[kBwdWaves][kBwdQueue];     // (u, w), then (dot, dxyz)
-  __shared__ float hgs[kBwdWaves][kBwdQueue];     // grad_scale
+  __shared__ float4 hq[kBwdWaves][kBwdQueue];       // (xyz, w), then (dot, dxyz)
   __shared__ uint16_t hmeta[kBwdWaves][kBwdQueue];  // owner lane | level count << 6
-  __shared__ uint64_t lact[kBwdWaves][kBwdThreads], lpush[kBwdWaves][kBwdThreads];
-  __shared__ uint8_t lj[kBwdWaves][kBwdThreads];
+  __shared__ uint64_t lact[kBwdWaves][kBwdList];
+  __shared__ uint8_t lj[kBwdWaves][kBwdList];
 
   const uint32_t tile = p.tile_order[blockIdx.x];  // the forward's order: heaviest tiles first
   const uint2 range = reinterpret_cast<const uint2*>(p.ranges)[tile];
@@ -722,51 +751,34 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
         BwdHit h;
         const bool act =
             bwd_hit(q0, q1, q2, px.pxf, px.pyf, p.beta, px.inside && contributor < px.last_contributor, h);
-        float u[3] = {0.0f, 0.0f, 0.0f}, grad_scale = 0.0f, hw = 0.0f;
+        float xyz[3] = {0.0f, 0.0f, 0.0f}, hw = 0.0f;
         uint32_t lane_levels = 0u;
         if (act) {
           T1 = T1 / (1.f - h.alpha);
           const float wgt = h.alpha * T1;
-          const float4 q3 = srec[3][j], q4 = srec[4][j], q5 = srec[5][j], q6 = srec[6][j];
-          float xyz[3];
-          if (h.use3d) {
-            xyz[0] = h.s[0] * q4.x + h.s[1] * q4.w + q5.z;
-            xyz[1] = h.s[0] * q4.y + h.s[1] * q5.x + q5.w;
-            xyz[2] = h.s[0] * q4.z + h.s[1] * q5.y + q6.x;
-          } else {
-            xyz[0] = q5.z; xyz[1] = q5.w; xyz[2] = q6.x;
-          }
-          const uint32_t ap = __float_as_uint(q3.w);
-          const uint32_t maxl = ap < g.L ? ap : g.L;
-          lane_levels = grid_coord_bwd(g, xyz, u, grad_scale) ? maxl : 0u;
-          hw = wgt;
-          if constexpr (kRows == 2) {
-            // the grid's share of the gradient: (1 - weight) of it in mode 12,
-            // weight times it in mode 14, which skips the grid at weight <= 1e-6
-            const float wt = p.colors[(size_t)sid[j] * (uint32_t)p.cstride + p.wslot];
-            if (p.azero && !(wt > 1e-6f)) lane_levels = 0u;
-            hw = wgt * (p.azero ? wt : 1.0f - wt);
-          }
+          float wt;
+          lane_levels = bwd_hit_levels<kRows>(p, h, srec[3][j], srec[4][j], srec[5][j], srec[6][j], sid[j], xyz, wt);
+          // the grid's share of the gradient: (1 - weight) of it in mode 12,
+          // weight times it in mode 14
+          hw = kRows == 2 ? wgt * (p.azero ? wt : 1.0f - wt) : wgt;
         }
         const bool push = lane_levels > 0u;
         const uint64_t m_act = __ballot(act), m_push = __ballot(push);
         if (m_act != 0ull) {
           if (lane == 0u) {
             lact[wid][nl] = m_act;
-            lpush[wid][nl] = m_push;
             lj[wid][nl] = (uint8_t)j;
           }
           nl++;
         }
         if (push) {
           const uint32_t slot = cnt + (uint32_t)__popcll(m_push & lt);
-          hq[wid][slot] = make_float4(u[0], u[1], u[2], hw);
-          hgs[wid][slot] = grad_scale;
+          hq[wid][slot] = make_float4(xyz[0], xyz[1], xyz[2], hw);
           hmeta[wid][slot] = (uint16_t)(lane | (lane_levels << 6));
         }
         cnt += (uint32_t)__popcll(m_push);
         j++;
-        if (cnt > (uint32_t)(kBwdQueue - 64)) break;
+        if (cnt > (uint32_t)(kBwdQueue - 64) || nl == (uint32_t)kBwdList) break;
       }
       __builtin_amdgcn_wave_barrier();
       // 2. grid: table gradient, features' dot product and dL/dxyz per hit
@@ -778,8 +790,9 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
         const float* dp = p.dL_dpix;
         if (on) {
           const float4 q = hq[wid][e];
-          u[0] = q.x; u[1] = q.y; u[2] = q.z; w = q.w;
-          gsc = hgs[wid][e];
+          const float xyz[3] = {q.x, q.y, q.z};
+          w = q.w;
+          grid_coord_bwd(g, xyz, u, gsc);  // inside the grid: the hit was queued
           const uint32_t m = hmeta[wid][e];
           lev = m >> 6;
           const uint32_t t = (wid << 6) | (m & 63u);  // the owner's thread
@@ -794,15 +807,20 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_kernel(const Rend
       uint32_t qbase = 0;
       for (uint32_t i = 0; i < nl; i++) {
         const uint32_t jj = lj[wid][i];
-        const uint64_t m_act = lact[wid][i], m_push = lpush[wid][i];
+        const uint64_t m_act = lact[wid][i];
         const bool act = ((m_act >> lane) & 1ull) != 0ull;
-        const bool pushed = ((m_push >> lane) & 1ull) != 0ull;
         const uint32_t contributor = total - 1u - done_n - jj;
         const float4 q0 = srec[0][jj], q1 = srec[1][jj], q2 = srec[2][jj], q3 = srec[3][jj];
         const float4 q4 = srec[4][jj], q5 = srec[5][jj];
         const uint32_t id = sid[jj];
         BwdHit h;
         bwd_hit(q0, q1, q2, px.pxf, px.pyf, p.beta, act, h);
+        bool pushed = false;  // the hit's queue entry, as in the geometry pass
+        if (act) {
+          float xyz[3], wt0;
+          pushed = bwd_hit_levels<kRows>(p, h, q3, q4, q5, srec[6][jj], id, xyz, wt0) > 0u;
+        }
+        const uint64_t m_push = __ballot(pushed);
         BwdGrad gr;
         bwd_grad_zero(gr);
         float gS = 0.0f, wcol = 0.0f, wt = 0.0f, fdot = 0.0f;
