@@ -194,18 +194,27 @@ def test_deterministic_repeat():
 @pytest.mark.parametrize("name", ["cfg1", "unbounded_small", "shells_small"])
 def test_tile_launch_order(name):
     """The render's launch order is a permutation of the tiles, heaviest
-    first: the buckets of 8 log2(pairs + 1) do not increase along it (float32
-    log2 on the device may put a boundary weight one bucket off)."""
+    first: in the order's positions the buckets of 8 log2(pairs + 1) do not
+    increase (float32 log2 on the device may put a boundary weight one bucket
+    off).  Workgroup b runs on XCD b % 8, and within each group of 8 * 16
+    positions XCD x takes the run of 16 positions from 16 x on, so position pos
+    is workgroup ((pos // 128) * 16 + pos % 16) * 8 + (pos % 128) // 16 (the
+    tail after the last full group keeps pos)."""
     from nest_splat import rasterizer as rz
     sc = scene(name)
     cam = sc.cameras[0]
     W, H = cam.image_width, cam.image_height
     res = run_gpu(sc)
     ba = rz.binning_arrays(res, W, H)
-    order = ba["tile_order"].cpu().numpy().astype(np.int64)
+    by_wg = ba["tile_order"].cpu().numpy().astype(np.int64)
     ranges = ba["ranges"].cpu().numpy().view(np.uint32).astype(np.int64)
     ntiles = ranges.shape[0]
-    np.testing.assert_array_equal(np.sort(order), np.arange(ntiles))
+    np.testing.assert_array_equal(np.sort(by_wg), np.arange(ntiles))
+    pos = np.arange(ntiles)
+    full = ntiles // 128 * 128
+    wg = np.where(pos < full, ((pos // 128) * 16 + pos % 16) * 8 + (pos % 128) // 16, pos)
+    np.testing.assert_array_equal(np.sort(wg), pos)  # a permutation
+    order = by_wg[wg]
     w = ranges[:, 1] - ranges[:, 0]
     bucket = np.minimum(255, np.floor(8.0 * np.log2(w.astype(np.float64) + 1.0))).astype(np.int64)
     b = bucket[order]
