@@ -266,7 +266,15 @@ hipError_t launch_rvq(const RvqParams& p, hipStream_t s) {
 // ((c0 + c1) + c2) + c3 in that order, as the per-splat kernels sum it.  The
 // next chunk's indices are loaded while the current chunk is decoded.
 constexpr int kRvqFusedThreads = 1024;
-constexpr int kRvqFusedNS = 8;                 // splats per lane and chunk
+// Splats per lane and chunk: 8 for an attribute that copies stage pairs per
+// chunk (the copy is paid once per 8192 splats), 4 for one whose codebooks
+// stay resident, whose chunks cost only their HBM bytes, so the workgroup
+// split balances at a finer grain (4M splats: 51.2 -> 49.8 us; 2 per lane:
+// 54.0 us).
+constexpr int kRvqFusedNS = 8;
+constexpr int kRvqFusedNSResident = 4;
+template <int DIM>
+constexpr int rvq_fused_ns() { return DIM == 4 ? kRvqFusedNS : kRvqFusedNSResident; }
 constexpr int kRvqFusedChunks = 8192;          // 16-byte LDS chunks per workgroup (128 KiB)
 
 struct RvqFused {
@@ -308,7 +316,7 @@ __device__ __forceinline__ void rvq_load_ix(const uint2* idx2, int64_t P, int64_
 
 template <int DIM>
 __device__ void rvq_fused_attr(const RvqParams& p, int wg, int nwg, float4* lds4) {
-  constexpr int NS = kRvqFusedNS;
+  constexpr int NS = rvq_fused_ns<DIM>();
   const float* lds = reinterpret_cast<const float*>(lds4);
   const uint32_t K = (uint32_t)p.K;
   const uint32_t vec4 = K * DIM / 4;  // 16-byte chunks per stage
@@ -430,29 +438,47 @@ static int rvq_device_cus() {
 
 hipError_t launch_rvq_batch(const RvqBatch& b, hipStream_t s) {
   // every attribute on the fused path: one persistent launch, one workgroup
-  // per CU, split by HBM bytes (at least one workgroup per non-empty
-  // attribute, none beyond its chunk count)
+  // per CU.  Workgroups are dealt one at a time to the attribute whose
+  // finishing time ceil(chunks / workgroups) x (HBM bytes of a chunk) is
+  // the largest, so the slowest attribute sets the launch's length with no
+  // workgroup left over (at least one per non-empty attribute, none beyond
+  // its chunk count).  Counting the rotation codebook's stage-pair copies
+  // as well (from L2, 128 KiB per chunk) made 4M splats slower, 0.068 ms
+  // against 0.053 ms.
   bool all_fused = b.n > 0;
   for (int k = 0; k < b.n; k++) all_fused = all_fused && rvq_fused_ok(b.a[k]);
   if (all_fused) {
     RvqFused f{};
     f.n = b.n;
-    double total = 0.0;
-    for (int k = 0; k < b.n; k++) {
-      f.a[k] = b.a[k];
-      total += (double)b.a[k].P * (8 + 4 * b.a[k].dim);
-    }
-    if (total <= 0.0) return hipSuccess;
+    for (int k = 0; k < b.n; k++) f.a[k] = b.a[k];
     const int cus = rvq_device_cus();
-    int next = 0;
+    int64_t chunks[kRvqBatchMax], g[kRvqBatchMax];
+    double cost[kRvqBatchMax];
+    int used = 0;
     for (int k = 0; k < b.n; k++) {
       const RvqParams& p = b.a[k];
-      const int64_t chunks =
-          (p.P + (int64_t)kRvqFusedThreads * kRvqFusedNS - 1) / ((int64_t)kRvqFusedThreads * kRvqFusedNS);
-      int64_t g = (int64_t)((double)cus * (double)p.P * (8 + 4 * p.dim) / total + 0.5);
-      g = chunks <= 0 ? 0 : (g < 1 ? 1 : (g > chunks ? chunks : g));
+      const int64_t cs = (int64_t)kRvqFusedThreads * (p.dim == 4 ? kRvqFusedNS : kRvqFusedNSResident);
+      chunks[k] = (p.P + cs - 1) / cs;
+      cost[k] = (double)cs * (8 + 4 * p.dim);  // index row + output row per splat
+      g[k] = chunks[k] > 0 ? 1 : 0;
+      used += (int)g[k];
+    }
+    while (used < cus) {
+      int worst = -1;
+      double wt = 0.0;
+      for (int k = 0; k < b.n; k++) {
+        if (g[k] == 0 || g[k] >= chunks[k]) continue;
+        const double t = (double)((chunks[k] + g[k] - 1) / g[k]) * cost[k];
+        if (t > wt) { wt = t; worst = k; }
+      }
+      if (worst < 0) break;
+      g[worst]++;
+      used++;
+    }
+    int next = 0;
+    for (int k = 0; k < b.n; k++) {
       f.wg_first[k] = next;
-      next += (int)g;
+      next += (int)g[k];
     }
     f.wg_first[b.n] = next;
     if (next == 0) return hipSuccess;
