@@ -116,15 +116,17 @@ __device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc
   }
 }
 
-// Compacted drain (F <= 4): the wave takes up to 64 pending hits, depth-major
-// (every lane's head first, then second entries, ...), so each lane's share
-// is the oldest `take` entries of its queue.  Lane k looks up hit k for every
-// level and writes each level's F values into that hit's own queue slot; the
-// owning lane then accumulates its hits in queue order, acc = fmaf(v, w, acc).
-// Levels at or past a hit's level count are written as 0, and
-// fmaf(0, w, acc) == acc (w is finite and the accumulators never hold -0), as
-// in the round drain.  isrc is this wave's 64-byte item table: owner lane |
-// slot << 6.
+// Compacted drain (F <= 4): every lane with a pending hit looks up its own
+// oldest hit; lanes whose queues are empty take the other lanes' second,
+// third, ... entries, depth-major (every second entry before any third), so
+// each lane's share is still the oldest `take` entries of its queue.  A lane
+// accumulates its own head's values from registers; a lane looking up another
+// lane's hit writes each level's F values into that hit's queue slot, and
+// the owner adds them after its head, in queue order, acc = fmaf(v, w, acc).
+// Levels at or past a hit's level count give 0, and fmaf(0, w, acc) == acc
+// (w is finite and the accumulators never hold -0), as in the round drain.
+// isrc is this wave's 64-byte table of moved hits: owner lane | slot << 6,
+// indexed by the taking lane's rank among the empty lanes.
 template <int F, int NACC, bool kHalf, bool kStructured>
 __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rsrc, float4 (*hq)[kRenderThreads],
                                               uint8_t (*hl)[kRenderThreads], uint8_t* isrc, int& qhead, int& qn,
@@ -133,27 +135,33 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
   const uint32_t lane = threadIdx.x & (kWaveLanes - 1);
   const uint32_t wbase = threadIdx.x - lane;
   const uint64_t lt = lanemask_lt64();
+  const bool head = qn > 0;
+  const uint64_t idle = ~__ballot(head);
+  const uint32_t nidle = (uint32_t)__popcll(idle);
   uint32_t base = 0;
-  int take = 0;
+  int take = head ? 1 : 0;
 #pragma unroll
-  for (int d = 0; d < kQueue; d++) {
+  for (int d = 1; d < kQueue; d++) {
     const uint64_t m = __ballot(qn > d);
     const uint32_t k = base + (uint32_t)__popcll(m & lt);
-    if (qn > d && k < (uint32_t)kWaveLanes) {
+    if (qn > d && k < nidle) {
       isrc[k] = (uint8_t)(lane | ((uint32_t)((qhead + d) & (kQueue - 1)) << 6));
       take = d + 1;
     }
     base += (uint32_t)__popcll(m);
   }
-  const uint32_t items = base < (uint32_t)kWaveLanes ? base : (uint32_t)kWaveLanes;
   __builtin_amdgcn_wave_barrier();
-  const bool work = lane < items;
+  const uint32_t rank = (uint32_t)__popcll(idle & lt);
+  const bool moved = !head && rank < base;
+  const bool work = head || moved;
   float u[3] = {0.0f, 0.0f, 0.0f};
-  uint32_t nlev = 0, col = 0, wslot = 0;
-  if (work) {
-    const uint32_t s = isrc[lane];
+  uint32_t nlev = 0, col = threadIdx.x, wslot = (uint32_t)qhead;
+  if (moved) {
+    const uint32_t s = isrc[rank];
     col = wbase + (s & 63u);
     wslot = s >> 6;
+  }
+  if (work) {
     const float4 e = hq[wslot][col];
     u[0] = e.x;
     u[1] = e.y;
@@ -198,12 +206,16 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
         corners_load_r<F, kHalf>(rsrc, cn, vals);
       }
     }
-    if (work) hq[wslot][col] = make_float4(v[0], v[1], v[2], v[3]);
+    if (moved) hq[wslot][col] = make_float4(v[0], v[1], v[2], v[3]);
+    if (head) {
+#pragma unroll
+      for (int f = 0; f < F; f++) acc[l * F + f] = fmaf(v[f], wd[0], acc[l * F + f]);
+    }
     look = next;
     rec_next = rec_after;
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int d = 0; d < kQueue; d++) {
+    for (int d = 1; d < kQueue; d++) {
       if (d < take) {
         const float4 r = *own[d];
         const float rv[4] = {r.x, r.y, r.z, r.w};
