@@ -241,10 +241,18 @@ __global__ void __launch_bounds__(kSortThreads) radix_hist_kernel(const K* __res
   for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&hist[0][0])[i] = 0;
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)wid * (kWave * kSortRounds);
+  // all of the wave's keys in flight at once, then the rounds
+  K key[kSortRounds];
+#pragma unroll
+  for (int r = 0; r < kSortRounds; r++) {
+    const int64_t i = base + r * kWave + lane;
+    key[r] = i < n ? keys[i] : (K)0;
+  }
+#pragma unroll
   for (int r = 0; r < kSortRounds; r++) {
     const int64_t i = base + r * kWave + lane;
     const bool ok = i < n;
-    const uint32_t d = ok ? (uint32_t)(keys[i] >> shift) & (kRadix - 1) : 0u;
+    const uint32_t d = ok ? (uint32_t)(key[r] >> shift) & (kRadix - 1) : 0u;
     const uint64_t valid = __ballot(ok);
     const uint64_t peers = match_digit(d, valid);
     const int leader = __ffsll((unsigned long long)peers) - 1;
@@ -277,10 +285,7 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
   __shared__ K skey[kSortTile];
   __shared__ uint32_t sval[kSortTile];
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-  for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&hist[0][0])[i] = 0;
-  for (int d = threadIdx.x; d < kRadix; d += kSortThreads) gbase[d] = offsets[(size_t)d * nblocks + blockIdx.x];
-  __syncthreads();
-
+  // the keys and values are in flight together with the digit offsets
   const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)wid * (kWave * kSortRounds);
   K key[kSortRounds];
   uint32_t val[kSortRounds];
@@ -296,6 +301,9 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
       val[r] = 0;
     }
   }
+  for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&hist[0][0])[i] = 0;
+  for (int d = threadIdx.x; d < kRadix; d += kSortThreads) gbase[d] = offsets[(size_t)d * nblocks + blockIdx.x];
+  __syncthreads();
 #pragma unroll
   for (int r = 0; r < kSortRounds; r++) {
     const int64_t i = base + r * kWave + lane;
