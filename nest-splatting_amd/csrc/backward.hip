@@ -283,15 +283,12 @@ __device__ __forceinline__ void hash_backward_wave(const GridParams& g, nest_i32
       }
 #pragma unroll
       for (int f = 0; f < F; f++) dot += feat[f] * dp[f];
-      // dy/dxyz: corner pairs along each axis (hashgrid.h:241-276).  The
-      // reference sums wgt * (v_r - v_l) * der over the pairs per channel and
-      // projects the sums on gf; the same products are summed here as
-      // der * sum_pairs wgt * sum_f gf[f] (v_r[f] - v_l[f]), another order
-      // (the backward's contract is a relative tolerance) with about 60%
-      // of the vector instructions.
+      // dy/dxyz: corner pairs along each axis (hashgrid.h:241-276)
 #pragma unroll
       for (int gd = 0; gd < 3; gd++) {
-        float rg = 0.0f;
+        float rg[F];
+#pragma unroll
+        for (int f = 0; f < F; f++) rg[f] = 0.0f;
 #pragma unroll
         for (int idx = 0; idx < 4; idx++) {
           float wgt = scale * grad_scale;
@@ -304,12 +301,11 @@ __device__ __forceinline__ void hash_backward_wave(const GridParams& g, nest_i32
             kl |= bit << d;
           }
           const int kr = kl | (1 << gd);
-          float pd = 0.0f;
 #pragma unroll
-          for (int f = 0; f < F; f++) pd = fmaf(gf[f], vals[kr][f] - vals[kl][f], pd);
-          rg = fmaf(wgt, pd, rg);
+          for (int f = 0; f < F; f++) rg[f] += wgt * (vals[kr][f] - vals[kl][f]) * der[gd];
         }
-        dxyz[gd] += rg * der[gd];
+#pragma unroll
+        for (int f = 0; f < F; f++) dxyz[gd] += gf[f] * rg[f];
       }
     }
     scatter_level<F>(on, gc, cn.idx, cv, dtable + (size_t)lv.base[l] * F);
