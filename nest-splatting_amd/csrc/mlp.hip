@@ -50,6 +50,95 @@ __device__ __forceinline__ uint2 pack4(uint16_t a, uint16_t b, uint16_t c, uint1
   return make_uint2((uint32_t)a | ((uint32_t)b << 16), (uint32_t)c | ((uint32_t)d << 16));
 }
 
+__device__ __forceinline__ uint32_t pack2(uint16_t a, uint16_t b) { return (uint32_t)a | ((uint32_t)b << 16); }
+
+typedef __bf16 nest_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float nest_f32x2v __attribute__((ext_vector_type(2)));
+typedef short nest_i16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats as a packed pair (a in the low half), rounded to nearest even:
+// one v_cvt_pk_bf16_f32 for bfloat16.
+template <bool kBF16>
+__device__ __forceinline__ uint32_t pack2_16(float a, float b) {
+  if constexpr (kBF16) {
+    const nest_bf16x2 h = __builtin_convertvector((nest_f32x2v){a, b}, nest_bf16x2);
+    return __builtin_bit_cast(uint32_t, h);
+  } else {
+    return pack2(to16<false>(a), to16<false>(b));
+  }
+}
+
+// max(a, 0), max(b, 0) as a packed bfloat16 pair: rounding first and then
+// replacing every half whose sign bit is set (a negative value or -0) by +0,
+// a signed 16-bit maximum with 0 on both halves at once, gives the same bits
+// for finite inputs (rounding to nearest keeps the sign, and a negative value
+// never rounds to +0).
+template <bool kBF16>
+__device__ __forceinline__ uint32_t relu_pack2(float a, float b) {
+  if constexpr (kBF16) {
+    const nest_i16x2 h = __builtin_bit_cast(nest_i16x2, pack2_16<true>(a, b));
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(h, (nest_i16x2){0, 0}));
+  } else {
+    return pack2(to16<false>(fmaxf(a, 0.f)), to16<false>(fmaxf(b, 0.f)));
+  }
+}
+
+
+// Raw buffer view of the feature map: per-lane byte offset in a VGPR, the
+// channel's byte offset in an SGPR, so the 64 loads of a tile need no
+// per-channel 64-bit addresses.
+typedef int mlp_i32x4 __attribute__((ext_vector_type(4)));
+__device__ float mlp_raw_load_f32(mlp_i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.f32");
+
+__device__ __forceinline__ mlp_i32x4 feat_rsrc(const float* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  mlp_i32x4 r;
+  r.x = (int)(uint32_t)(a & 0xffffffffu);
+  r.y = (int)(uint32_t)((a >> 32) & 0xffffu);  // stride 0: raw addressing
+  r.z = (int)0xffffffffu;                      // range in bytes
+  r.w = 0x00020000;
+  return r;
+}
+
+// The C features of pixel nn (channel c at byte c * cs4 + nn * ns4).
+template <int C>
+__device__ __forceinline__ void load_features(mlp_i32x4 rsrc, uint32_t cs4, uint32_t voff, float f[C]) {
+#pragma unroll
+  for (int c = 0; c < C; c++) f[c] = mlp_raw_load_f32(rsrc, (int)voff, (int)(cs4 * (uint32_t)c), 0);
+}
+
+// Unit view direction of pixel n of a width-w image: cam2rays rows (x, y, 1) @ M,
+// normalised (32-bit pixel arithmetic; the image has fewer than 2^31 pixels).
+__device__ __forceinline__ void pixel_dir32(const MlpParams& p, uint32_t n, float& dx, float& dy, float& dz) {
+  if (p.dirs) {
+    dx = p.dirs[3 * (size_t)n + 0];
+    dy = p.dirs[3 * (size_t)n + 1];
+    dz = p.dirs[3 * (size_t)n + 2];
+    return;
+  }
+  const uint32_t w = (uint32_t)p.img_w;
+  const uint32_t yi = n / w;
+  const float x = (float)(n - yi * w), y = (float)yi;
+  const float* M = p.M;
+  const float rx = x * M[0] + y * M[3] + M[6];
+  const float ry = x * M[1] + y * M[4] + M[7];
+  const float rz = x * M[2] + y * M[5] + M[8];
+  // 1 / max(|r|, 1e-12) as one hardware reciprocal square root (~1 ulp)
+  const float il = fminf(__builtin_amdgcn_rsqf(rx * rx + ry * ry + rz * rz), 1e12f);
+  dx = rx * il;
+  dy = ry * il;
+  dz = rz * il;
+}
+
+// Hidden unit of slot q = 32 kc + 8 grp + i of a K-chunk built from two
+// accumulator M-tiles.
+__device__ __forceinline__ int hidden_unit(int q) {
+  const int kc = q >> 5, r = q & 31, grp = r >> 3, i = r & 7;
+  return 32 * kc + (i < 4 ? 4 * grp + i : 16 + 4 * grp + (i - 4));
+}
+
+
 // SH16 of the unit direction d, computed on x = 2u - 1 with u = (d + 1) / 2.
 __device__ __forceinline__ void sh16(float dx, float dy, float dz, float o[16]) {
   const float ux = (dx + 1.0f) / 2.0f, uy = (dy + 1.0f) / 2.0f, uz = (dz + 1.0f) / 2.0f;
@@ -198,7 +287,7 @@ mlp_mfma_kernel(const MlpParams p) {
         float xv[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) xv[i] = kc < KF ? xf[kc < KF ? kc : 0][i] : s4[i];
-        const uint2 b = pack4(to16<kBF16>(xv[0]), to16<kBF16>(xv[1]), to16<kBF16>(xv[2]), to16<kBF16>(xv[3]));
+        const uint2 b = make_uint2(pack2_16<kBF16>(xv[0], xv[1]), pack2_16<kBF16>(xv[2], xv[3]));
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
           const uint2 a = *reinterpret_cast<const uint2*>(w1 + (nt * 16 + col) * ld1 + kc * 16 + grp * 4);
@@ -221,7 +310,7 @@ mlp_mfma_kernel(const MlpParams p) {
           xv[i] = v;
         }
       }
-      const uint2 b = pack4(to16<kBF16>(xv[0]), to16<kBF16>(xv[1]), to16<kBF16>(xv[2]), to16<kBF16>(xv[3]));
+      const uint2 b = make_uint2(pack2_16<kBF16>(xv[0], xv[1]), pack2_16<kBF16>(xv[2], xv[3]));
 #pragma unroll
       for (int nt = 0; nt < NT; nt++) {
         const uint2 a = *reinterpret_cast<const uint2*>(w1 + (nt * 16 + col) * ld1 + kc * 16 + grp * 4);
@@ -231,8 +320,7 @@ mlp_mfma_kernel(const MlpParams p) {
     uint2 h1[NT];
 #pragma unroll
     for (int i = 0; i < NT; i++)
-      h1[i] = pack4(to16<kBF16>(fmaxf(acc1[i][0], 0.f)), to16<kBF16>(fmaxf(acc1[i][1], 0.f)),
-                    to16<kBF16>(fmaxf(acc1[i][2], 0.f)), to16<kBF16>(fmaxf(acc1[i][3], 0.f)));
+      h1[i] = make_uint2(relu_pack2<kBF16>(acc1[i][0], acc1[i][1]), relu_pack2<kBF16>(acc1[i][2], acc1[i][3]));
     f32x4 acc2[NT];
 #pragma unroll
     for (int i = 0; i < NT; i++) acc2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -247,8 +335,7 @@ mlp_mfma_kernel(const MlpParams p) {
     f32x4 acc3 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kc = 0; kc < NT; kc++) {
-      const uint2 h2 = pack4(to16<kBF16>(fmaxf(acc2[kc][0], 0.f)), to16<kBF16>(fmaxf(acc2[kc][1], 0.f)),
-                             to16<kBF16>(fmaxf(acc2[kc][2], 0.f)), to16<kBF16>(fmaxf(acc2[kc][3], 0.f)));
+      const uint2 h2 = make_uint2(relu_pack2<kBF16>(acc2[kc][0], acc2[kc][1]), relu_pack2<kBF16>(acc2[kc][2], acc2[kc][3]));
       const uint2 a = *reinterpret_cast<const uint2*>(w3 + col * ld3 + kc * 16 + grp * 4);
       acc3 = mfma16<kBF16>(a, h2, acc3);
     }
@@ -290,68 +377,11 @@ __device__ __forceinline__ f32x4 mfma32(uint4 a, uint4 b, f32x4 c) {
   }
 }
 
-__device__ __forceinline__ uint32_t pack2(uint16_t a, uint16_t b) { return (uint32_t)a | ((uint32_t)b << 16); }
-
-// Raw buffer view of the feature map: per-lane byte offset in a VGPR, the
-// channel's byte offset in an SGPR, so the 64 loads of a tile need no
-// per-channel 64-bit addresses.
-typedef int mlp_i32x4 __attribute__((ext_vector_type(4)));
-__device__ float mlp_raw_load_f32(mlp_i32x4 rsrc, int voffset, int soffset, int aux)
-    __asm("llvm.amdgcn.raw.buffer.load.f32");
-
-__device__ __forceinline__ mlp_i32x4 feat_rsrc(const float* base) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  mlp_i32x4 r;
-  r.x = (int)(uint32_t)(a & 0xffffffffu);
-  r.y = (int)(uint32_t)((a >> 32) & 0xffffu);  // stride 0: raw addressing
-  r.z = (int)0xffffffffu;                      // range in bytes
-  r.w = 0x00020000;
-  return r;
-}
-
-// The C features of pixel nn (channel c at byte c * cs4 + nn * ns4).
-template <int C>
-__device__ __forceinline__ void load_features(mlp_i32x4 rsrc, uint32_t cs4, uint32_t voff, float f[C]) {
-#pragma unroll
-  for (int c = 0; c < C; c++) f[c] = mlp_raw_load_f32(rsrc, (int)voff, (int)(cs4 * (uint32_t)c), 0);
-}
-
-// Unit view direction of pixel n of a width-w image: cam2rays rows (x, y, 1) @ M,
-// normalised (32-bit pixel arithmetic; the image has fewer than 2^31 pixels).
-__device__ __forceinline__ void pixel_dir32(const MlpParams& p, uint32_t n, float& dx, float& dy, float& dz) {
-  if (p.dirs) {
-    dx = p.dirs[3 * (size_t)n + 0];
-    dy = p.dirs[3 * (size_t)n + 1];
-    dz = p.dirs[3 * (size_t)n + 2];
-    return;
-  }
-  const uint32_t w = (uint32_t)p.img_w;
-  const uint32_t yi = n / w;
-  const float x = (float)(n - yi * w), y = (float)yi;
-  const float* M = p.M;
-  const float rx = x * M[0] + y * M[3] + M[6];
-  const float ry = x * M[1] + y * M[4] + M[7];
-  const float rz = x * M[2] + y * M[5] + M[8];
-  // 1 / max(|r|, 1e-12) as one hardware reciprocal square root (~1 ulp)
-  const float il = fminf(__builtin_amdgcn_rsqf(rx * rx + ry * ry + rz * rz), 1e12f);
-  dx = rx * il;
-  dy = ry * il;
-  dz = rz * il;
-}
-
-// Hidden unit of slot q = 32 kc + 8 grp + i of a K-chunk built from two
-// accumulator M-tiles.
-__device__ __forceinline__ int hidden_unit(int q) {
-  const int kc = q >> 5, r = q & 31, grp = r >> 3, i = r & 7;
-  return 32 * kc + (i < 4 ? 4 * grp + i : 16 + 4 * grp + (i - 4));
-}
 
 template <bool kBF16>
 __device__ __forceinline__ uint4 relu_pack8(f32x4 lo, f32x4 hi) {
-  return make_uint4(pack2(to16<kBF16>(fmaxf(lo[0], 0.f)), to16<kBF16>(fmaxf(lo[1], 0.f))),
-                    pack2(to16<kBF16>(fmaxf(lo[2], 0.f)), to16<kBF16>(fmaxf(lo[3], 0.f))),
-                    pack2(to16<kBF16>(fmaxf(hi[0], 0.f)), to16<kBF16>(fmaxf(hi[1], 0.f))),
-                    pack2(to16<kBF16>(fmaxf(hi[2], 0.f)), to16<kBF16>(fmaxf(hi[3], 0.f))));
+  return make_uint4(relu_pack2<kBF16>(lo[0], lo[1]), relu_pack2<kBF16>(lo[2], lo[3]),
+                    relu_pack2<kBF16>(hi[0], hi[1]), relu_pack2<kBF16>(hi[2], hi[3]));
 }
 
 constexpr int kMlp32Waves = kMlpThreads / 64;
@@ -435,16 +465,12 @@ mlp_mfma32_kernel(const MlpParams p) {
     uint4* row4 = reinterpret_cast<uint4*>(xrow + lane * LD1);
 #pragma unroll
     for (int q = 0; q < C / 8; q++)
-      row4[q] = make_uint4(pack2(to16<kBF16>(f[8 * q + 0]), to16<kBF16>(f[8 * q + 1])),
-                           pack2(to16<kBF16>(f[8 * q + 2]), to16<kBF16>(f[8 * q + 3])),
-                           pack2(to16<kBF16>(f[8 * q + 4]), to16<kBF16>(f[8 * q + 5])),
-                           pack2(to16<kBF16>(f[8 * q + 6]), to16<kBF16>(f[8 * q + 7])));
+      row4[q] = make_uint4(pack2_16<kBF16>(f[8 * q + 0], f[8 * q + 1]), pack2_16<kBF16>(f[8 * q + 2], f[8 * q + 3]),
+                           pack2_16<kBF16>(f[8 * q + 4], f[8 * q + 5]), pack2_16<kBF16>(f[8 * q + 6], f[8 * q + 7]));
 #pragma unroll
     for (int q = 0; q < 2; q++)
-      row4[C / 8 + q] = make_uint4(pack2(to16<kBF16>(sh[8 * q + 0]), to16<kBF16>(sh[8 * q + 1])),
-                                   pack2(to16<kBF16>(sh[8 * q + 2]), to16<kBF16>(sh[8 * q + 3])),
-                                   pack2(to16<kBF16>(sh[8 * q + 4]), to16<kBF16>(sh[8 * q + 5])),
-                                   pack2(to16<kBF16>(sh[8 * q + 6]), to16<kBF16>(sh[8 * q + 7])));
+      row4[C / 8 + q] = make_uint4(pack2_16<kBF16>(sh[8 * q + 0], sh[8 * q + 1]), pack2_16<kBF16>(sh[8 * q + 2], sh[8 * q + 3]),
+                                   pack2_16<kBF16>(sh[8 * q + 4], sh[8 * q + 5]), pack2_16<kBF16>(sh[8 * q + 6], sh[8 * q + 7]));
     const float a_out[4] = {alpha4[0], alpha4[1], alpha4[2], alpha4[3]};
     // the next tile's features and alpha are in flight during this tile's contraction
     if (t + nwaves < ntile) load_tile(t + nwaves);
@@ -614,7 +640,7 @@ mlp_block_kernel(const MlpParams p) {
       for (int j = 0; j < CPW; j += 2) {
         const float v0 = q == 0 ? fv[j].x : q == 1 ? fv[j].y : q == 2 ? fv[j].z : fv[j].w;
         const float v1 = q == 0 ? fv[j + 1].x : q == 1 ? fv[j + 1].y : q == 2 ? fv[j + 1].z : fv[j + 1].w;
-        w[j / 2] = pack2(to16<kBF16>(v0), to16<kBF16>(v1));
+        w[j / 2] = pack2_16<kBF16>(v0, v1);
       }
       if constexpr (CPW % 8 == 0) {
 #pragma unroll
@@ -636,10 +662,8 @@ mlp_block_kernel(const MlpParams p) {
 #pragma unroll
       for (int q = 0; q < 2; q++)
         *reinterpret_cast<uint4*>(xrow + lane * LD1 + 8 * xrow_chunk(wid * 64 + lane, C / 8 + q)) =
-            make_uint4(pack2(to16<kBF16>(sh[8 * q + 0]), to16<kBF16>(sh[8 * q + 1])),
-                       pack2(to16<kBF16>(sh[8 * q + 2]), to16<kBF16>(sh[8 * q + 3])),
-                       pack2(to16<kBF16>(sh[8 * q + 4]), to16<kBF16>(sh[8 * q + 5])),
-                       pack2(to16<kBF16>(sh[8 * q + 6]), to16<kBF16>(sh[8 * q + 7])));
+            make_uint4(pack2_16<kBF16>(sh[8 * q + 0], sh[8 * q + 1]), pack2_16<kBF16>(sh[8 * q + 2], sh[8 * q + 3]),
+                       pack2_16<kBF16>(sh[8 * q + 4], sh[8 * q + 5]), pack2_16<kBF16>(sh[8 * q + 6], sh[8 * q + 7]));
     }
     const float a_out[4] = {alpha4[0], alpha4[1], alpha4[2], alpha4[3]};
     if (b + gridDim.x < nblk) {  // next block in flight during the contraction
