@@ -53,34 +53,32 @@ __device__ __forceinline__ uint2 pack4(uint16_t a, uint16_t b, uint16_t c, uint1
 __device__ __forceinline__ uint32_t pack2(uint16_t a, uint16_t b) { return (uint32_t)a | ((uint32_t)b << 16); }
 
 typedef __bf16 nest_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 nest_f16x2 __attribute__((ext_vector_type(2)));
 typedef float nest_f32x2v __attribute__((ext_vector_type(2)));
 typedef short nest_i16x2 __attribute__((ext_vector_type(2)));
 
 // Two floats as a packed pair (a in the low half), rounded to nearest even:
-// one v_cvt_pk_bf16_f32 for bfloat16.
+// one v_cvt_pk_bf16_f32 or v_cvt_pk_f16_f32.
 template <bool kBF16>
 __device__ __forceinline__ uint32_t pack2_16(float a, float b) {
   if constexpr (kBF16) {
     const nest_bf16x2 h = __builtin_convertvector((nest_f32x2v){a, b}, nest_bf16x2);
     return __builtin_bit_cast(uint32_t, h);
   } else {
-    return pack2(to16<false>(a), to16<false>(b));
+    const nest_f16x2 h = __builtin_convertvector((nest_f32x2v){a, b}, nest_f16x2);
+    return __builtin_bit_cast(uint32_t, h);
   }
 }
 
-// max(a, 0), max(b, 0) as a packed bfloat16 pair: rounding first and then
-// replacing every half whose sign bit is set (a negative value or -0) by +0,
-// a signed 16-bit maximum with 0 on both halves at once, gives the same bits
-// for finite inputs (rounding to nearest keeps the sign, and a negative value
-// never rounds to +0).
+// max(a, 0), max(b, 0) as a packed 16-bit float pair: rounding first and
+// then replacing every half whose sign bit is set (a negative value or -0)
+// by +0, a signed 16-bit maximum with 0 on both halves at once, gives the
+// same bits for finite inputs (rounding to nearest keeps the sign, and a
+// negative value never rounds to +0).
 template <bool kBF16>
 __device__ __forceinline__ uint32_t relu_pack2(float a, float b) {
-  if constexpr (kBF16) {
-    const nest_i16x2 h = __builtin_bit_cast(nest_i16x2, pack2_16<true>(a, b));
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(h, (nest_i16x2){0, 0}));
-  } else {
-    return pack2(to16<false>(fmaxf(a, 0.f)), to16<false>(fmaxf(b, 0.f)));
-  }
+  const nest_i16x2 h = __builtin_bit_cast(nest_i16x2, pack2_16<kBF16>(a, b));
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(h, (nest_i16x2){0, 0}));
 }
 
 
