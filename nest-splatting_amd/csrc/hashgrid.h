@@ -79,6 +79,8 @@ __device__ int nest_struct_load_i32(nest_i32x4 rsrc, int vindex, int voffset, in
     __asm("llvm.amdgcn.struct.buffer.load.i32");
 __device__ short nest_struct_load_i16(nest_i32x4 rsrc, int vindex, int voffset, int soffset, int aux)
     __asm("llvm.amdgcn.struct.buffer.load.i16");
+__device__ nest_i32x4 nest_raw_load_v4i32(nest_i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4i32");
 
 template <int F, bool kHalf>
 __device__ __forceinline__ nest_i32x4 table_rsrc_rows(const void* table, uint32_t rows) {
@@ -89,6 +91,18 @@ __device__ __forceinline__ nest_i32x4 table_rsrc_rows(const void* table, uint32_
   r.y = (int)((uint32_t)((a >> 32) & 0xffffu) | ((uint32_t)kStride << 16));
   r.z = (int)rows;
   r.w = 0x00020000;
+  return r;
+}
+
+// Byte-addressed view of the same table (stride 0, num_records = bytes):
+// 16-byte loads that start at any entry of an 8-byte-entry table.  The table
+// is below 4 GiB (the host checks), so rows * entry bytes fits 32 bits.
+template <int F, bool kHalf>
+__device__ __forceinline__ nest_i32x4 table_rsrc_raw(nest_i32x4 rows_view) {
+  constexpr uint32_t kStride = F * (kHalf ? 2u : 4u);
+  nest_i32x4 r = rows_view;
+  r.y = (int)((uint32_t)r.y & 0xffffu);
+  r.z = (int)((uint32_t)r.z * kStride);
   return r;
 }
 
@@ -147,6 +161,7 @@ __device__ __forceinline__ void struct_entry(nest_i32x4 r, uint32_t index, uint3
 struct LevelCorners {
   uint32_t idx[8];   // entry index of corner k (bit 0: +x, bit 1: +y, bit 2: +z)
   uint32_t soff;     // byte offset of the level in the table
+  uint32_t dense;    // wave-uniform: a dense level without modulo, so idx[2m + 1] == idx[2m] + 1
   float wx[2], wy[2], wz[2];
 };
 
@@ -193,6 +208,7 @@ __device__ __forceinline__ void level_corners(const LevelTable& lv, int l, float
   const uint32_t hsize = lv.hsize[l];
   const uint32_t flags = lv.flags[l];
   cn.soff = lv.base[l] * (uint32_t)(F * (kHalf ? 2 : 4));
+  cn.dense = 0u;
   uint32_t g[3];
   cell_weights(lv.scale[l], pos_offset, interp == 1, u, g, cn);
   uint32_t* idx = cn.idx;
@@ -235,6 +251,7 @@ __device__ __forceinline__ void cell_weights_unit(float scale, float pos_offset,
 // record: one uniform test of q.b picks the index path.
 __device__ __forceinline__ void quad_corners(const LevelQuad& q, float pos_offset, const float u[3], LevelCorners& cn) {
   cn.soff = q.soff;
+  cn.dense = q.b;
   uint32_t g[3];
   cell_weights_unit(q.scale, pos_offset, u, g, cn);
   if (q.b != 0) {
@@ -251,6 +268,46 @@ template <int F, bool kHalf>
 __device__ __forceinline__ void corners_load(nest_i32x4 rsrc, const LevelCorners& cn, float vals[8][F]) {
 #pragma unroll
   for (int k = 0; k < 8; k++) struct_entry<F, kHalf>(rsrc, cn.idx[k], cn.soff, vals[k]);
+}
+
+// quad_corners followed by corners_load_r in one uniform branch, for the
+// common grid with 8-byte entries: a dense level computes only the four
+// x-pair bases and issues four 16-byte loads; a hashed level issues eight
+// 8-byte loads.  Either way the pair of corners 2m, 2m + 1 lands in one
+// 4-dword tuple.
+template <int F, bool kHalf>
+__device__ __forceinline__ void quad_fetch_pairs(const LevelQuad& q, float pos_offset, const float u[3],
+                                                 nest_i32x4 rsrc, LevelCorners& cn, float vals[8][F]) {
+  static_assert((kHalf && F == 4) || (!kHalf && F == 2), "8-byte entries");
+  cn.soff = q.soff;
+  cn.dense = q.b;
+  uint32_t g[3];
+  cell_weights_unit(q.scale, pos_offset, u, g, cn);
+  nest_i32x4 pr[4];
+  if (q.b != 0) {
+    const nest_i32x4 raw = table_rsrc_raw<F, kHalf>(rsrc);
+    const uint32_t base = g[0] + __umul24(g[1], q.a) + __umul24(g[2], q.b);
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      const uint32_t e = base + ((m & 1) ? q.a : 0u) + ((m & 2) ? q.b : 0u);
+      pr[m] = nest_raw_load_v4i32(raw, (int)(e * 8u), (int)q.soff, 0);
+    }
+  } else {
+    hashed_corners(g, cn.idx);
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      const nest_i32x2 a = nest_struct_load_v2i32(rsrc, (int)(cn.idx[2 * m] & q.a), 0, (int)q.soff, 0);
+      const nest_i32x2 b = nest_struct_load_v2i32(rsrc, (int)(cn.idx[2 * m + 1] & q.a), 0, (int)q.soff, 0);
+      pr[m] = nest_i32x4{a.x, a.y, b.x, b.y};
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 4; m++) {
+    vals[2 * m][0] = __int_as_float(pr[m].x);
+    vals[2 * m][1] = __int_as_float(pr[m].y);
+    vals[2 * m + 1][0] = __int_as_float(pr[m].z);
+    vals[2 * m + 1][1] = __int_as_float(pr[m].w);
+  }
 }
 
 // Interpolated value: out = fmaf(w_k, entry_k, out) over corners 0..7 in
@@ -275,8 +332,39 @@ __device__ __forceinline__ void corners_sum(const LevelCorners& cn, const float 
 // bit for bit; the mix instruction's float32-denormal flush cannot apply,
 // since a product of the cell weights (0, or at least ~1e-21) and a binary16
 // value (0, or at least ~6e-8) is never a float32 denormal.
+//
+// Tables of 8-byte entries (binary16 F = 4, binary32 F = 2): on a dense
+// level corners 2m and 2m + 1 (x and x + 1) are neighbouring entries, so one
+// 16-byte load from the byte view fetches both, four loads per level instead
+// of eight; the values and their order are the same.
 template <int F, bool kHalf>
 __device__ __forceinline__ void corners_load_r(nest_i32x4 rsrc, const LevelCorners& cn, float vals[8][F]) {
+  constexpr bool kPair = (kHalf && F == 4) || (!kHalf && F == 2);
+  if constexpr (kPair) {
+    // Both branches leave an x-pair in one 4-dword tuple, so the registers
+    // the loads land in are the same on either side of the uniform branch.
+    nest_i32x4 pr[4];
+    if (cn.dense != 0u) {
+      const nest_i32x4 raw = table_rsrc_raw<F, kHalf>(rsrc);
+#pragma unroll
+      for (int m = 0; m < 4; m++) pr[m] = nest_raw_load_v4i32(raw, (int)(cn.idx[2 * m] * 8u), (int)cn.soff, 0);
+    } else {
+#pragma unroll
+      for (int m = 0; m < 4; m++) {
+        const nest_i32x2 a = nest_struct_load_v2i32(rsrc, (int)cn.idx[2 * m], 0, (int)cn.soff, 0);
+        const nest_i32x2 b = nest_struct_load_v2i32(rsrc, (int)cn.idx[2 * m + 1], 0, (int)cn.soff, 0);
+        pr[m] = nest_i32x4{a.x, a.y, b.x, b.y};
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      vals[2 * m][0] = __int_as_float(pr[m].x);
+      vals[2 * m][1] = __int_as_float(pr[m].y);
+      vals[2 * m + 1][0] = __int_as_float(pr[m].z);
+      vals[2 * m + 1][1] = __int_as_float(pr[m].w);
+    }
+    return;
+  }
   if constexpr (kHalf && (F == 4 || F == 2)) {
 #pragma unroll
     for (int k = 0; k < 8; k++) {

@@ -85,6 +85,24 @@ __device__ __forceinline__ void level_setup(const GridParams& g, nest_u32x4 r, i
   }
 }
 
+// level_setup followed by the corner loads of level l.
+template <int F, bool kHalf, bool kStructured>
+__device__ __forceinline__ void level_fetch(const GridParams& g, nest_u32x4 r, int l, const float u[3],
+                                            nest_i32x4 rsrc, LevelCorners& cn, float vals[8][F]) {
+  constexpr bool kPair = (kHalf && F == 4) || (!kHalf && F == 2);
+  if constexpr (kStructured && kPair) {
+    LevelQuad q;
+    q.scale = __uint_as_float(r.x);
+    q.a = r.y;
+    q.b = r.z;
+    q.soff = r.w;
+    quad_fetch_pairs<F, kHalf>(q, g.pos_offset, u, rsrc, cn, vals);
+  } else {
+    level_setup<F, kHalf, kStructured>(g, r, l, u, cn);
+    corners_load_r<F, kHalf>(rsrc, cn, vals);
+  }
+}
+
 // One drain round (any F): every lane with a pending hit looks up its oldest
 // one (ring-buffer head) and accumulates each level below its level count;
 // lanes with an empty queue idle.
@@ -102,9 +120,8 @@ __device__ __forceinline__ void drain_round(const GridParams& g, nest_i32x4 rsrc
         LevelCorners cn;
         nest_u32x4 rec = {0u, 0u, 0u, 0u};
         if constexpr (kStructured) rec = level_record(lqb, l);
-        level_setup<F, kHalf, kStructured>(g, rec, l, u, cn);
         float vals[8][F];
-        corners_load_r<F, kHalf>(rsrc, cn, vals);
+        level_fetch<F, kHalf, kStructured>(g, rec, l, u, rsrc, cn, vals);
         float v[F];
         corners_sum_r<F, kHalf>(cn, vals, v);
 #pragma unroll
@@ -187,8 +204,7 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
   nest_u32x4 rec = {0u, 0u, 0u, 0u}, rec_next = {0u, 0u, 0u, 0u};
   if constexpr (kStructured) rec = level_record(lqb, 0);
   if (look) {
-    level_setup<F, kHalf, kStructured>(g, rec, 0, u, cn);
-    corners_load_r<F, kHalf>(rsrc, cn, vals);
+    level_fetch<F, kHalf, kStructured>(g, rec, 0, u, rsrc, cn, vals);
   }
   if constexpr (kStructured) rec_next = level_record(lqb, 1);
 #pragma unroll
@@ -202,8 +218,7 @@ __device__ __forceinline__ void drain_compact(const GridParams& g, nest_i32x4 rs
     if (l + 1 < kLevels) {
       next = work && (uint32_t)(l + 1) < nlev;
       if (next) {
-        level_setup<F, kHalf, kStructured>(g, rec_next, l + 1, u, cn);
-        corners_load_r<F, kHalf>(rsrc, cn, vals);
+        level_fetch<F, kHalf, kStructured>(g, rec_next, l + 1, u, rsrc, cn, vals);
       }
     }
     if (moved) hq[wslot][col] = make_float4(v[0], v[1], v[2], v[3]);
@@ -300,8 +315,7 @@ __device__ __forceinline__ void drain_compact_mix(const RenderParams& p, nest_i3
   if (hyb == 0) {
     look = work && !fast && 0u < nhash;
     if (look) {
-      level_setup<F, kHalf, kStructured>(g, rec, 0, u, cn);
-      corners_load_r<F, kHalf>(rsrc, cn, vals);
+      level_fetch<F, kHalf, kStructured>(g, rec, 0, u, rsrc, cn, vals);
     }
     if (work && rows && 0u < nfeat) {
 #pragma unroll
@@ -330,8 +344,7 @@ __device__ __forceinline__ void drain_compact_mix(const RenderParams& p, nest_i3
       const uint32_t gn = (uint32_t)(gl + 1);
       next = work && !fast && gn < nhash;
       if (next) {
-        level_setup<F, kHalf, kStructured>(g, rec_next, (int)gn, u, cn);
-        corners_load_r<F, kHalf>(rsrc, cn, vals);
+        level_fetch<F, kHalf, kStructured>(g, rec_next, (int)gn, u, rsrc, cn, vals);
       }
       if (work && rows && gn < nfeat) {
 #pragma unroll
@@ -395,9 +408,8 @@ __device__ __forceinline__ void drain_mixed(const RenderParams& p, nest_i32x4 rs
           LevelCorners cn;
           nest_u32x4 rec = {0u, 0u, 0u, 0u};
           if constexpr (kStructured) rec = level_record(lqb, gl);
-          level_setup<F, kHalf, kStructured>(g, rec, gl, u, cn);
           float vals[8][F];
-          corners_load_r<F, kHalf>(rsrc, cn, vals);
+          level_fetch<F, kHalf, kStructured>(g, rec, gl, u, rsrc, cn, vals);
           corners_sum_r<F, kHalf>(cn, vals, h);
         }
 #pragma unroll

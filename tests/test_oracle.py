@@ -114,6 +114,80 @@ def test_preprocess_aabb_contains_cutoff_ellipse(oracle):
         assert -pv @ pre["normal_opacity"][i, :3] > 0
 
 
+def _cutoff_ellipse_bbox(sc, cam, ids, cutoff=4.0):
+    """Float64 bounding box of the projected cutoff ellipse of each splat,
+    from the splat's own 3D geometry (not the oracle's homography): the
+    boundary p(t) = c + cutoff (cos t sx R0 + sin t sy R1) is projected
+    through the camera, the extremes of x and y are found on 720 samples and
+    refined on 241 samples around each extreme.  Returns (half extents
+    [n, 2], centres [n, 2]); rows whose boundary crosses the camera plane
+    are NaN."""
+    from nest_splat.scene import build_rotation_np
+    R = build_rotation_np(sc.rotations[ids]).astype(np.float64)
+    c = sc.means[ids].astype(np.float64)
+    s = sc.scales[ids].astype(np.float64)
+    a0 = cutoff * s[:, 0:1] * R[:, :, 0]
+    a1 = cutoff * s[:, 1:2] * R[:, :, 1]
+    PV = cam.full_proj_transform.astype(np.float64)
+    W, H = cam.image_width, cam.image_height
+
+    def pix(t):  # t [n, k] -> x, y, w [n, k]
+        p = c[:, None, :] + np.cos(t)[..., None] * a0[:, None, :] + np.sin(t)[..., None] * a1[:, None, :]
+        hom = np.concatenate([p, np.ones(p.shape[:2] + (1,))], axis=2) @ PV
+        w = hom[..., 3]
+        return ((hom[..., 0] / w + 1) * W - 1) * 0.5, ((hom[..., 1] / w + 1) * H - 1) * 0.5, w
+
+    n = len(ids)
+    t0 = np.linspace(0, 2 * np.pi, 720, endpoint=False)[None, :].repeat(n, 0)
+    x, y, w = pix(t0)
+    bad = np.any(w <= 0, axis=1)
+    dt = 2 * np.pi / 720
+    out = []
+    for v, sign in ((x, 1), (x, -1), (y, 1), (y, -1)):
+        k = np.argmax(sign * v, axis=1)
+        tt = t0[np.arange(n), k][:, None] + np.linspace(-dt, dt, 241)[None, :]
+        xr, yr, _ = pix(tt)
+        vr = xr if v is x else yr
+        out.append(sign * np.max(sign * vr, axis=1))
+    xmax, xmin, ymax, ymin = out
+    half = np.stack([(xmax - xmin) / 2, (ymax - ymin) / 2], 1)
+    cen = np.stack([(xmax + xmin) / 2, (ymax + ymin) / 2], 1)
+    half[bad] = np.nan
+    cen[bad] = np.nan
+    return half, cen
+
+
+@pytest.mark.parametrize("name", ["cfg1", "shell_small"])
+def test_preprocess_radius_is_ceil_of_bbox_half_extent(oracle, name):
+    """radius = ceil(max(h_x, h_y, 4 * 0.707106)) with h the half extent of
+    the bounding box of the projected 4-sigma ellipse (CR/forward.cu:294-320,
+    :396-406), computed here in float64 from the 3D splat; the point image
+    is the box centre.  A radius too large (a dropped sqrt, a wrong cutoff)
+    or too small fails it, and so does a centre taken from the projected
+    mean instead of the box."""
+    sc = scene(name)
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    ids = np.nonzero(pre["radii"] > 0)[0]
+    assert len(ids) > 100
+    checked = 0
+    for lo in range(0, len(ids), 1000):
+        chunk = ids[lo:lo + 1000]
+        half, cen = _cutoff_ellipse_bbox(sc, cam, chunk)
+        ok = np.isfinite(half).all(axis=1)
+        h = np.maximum(half.max(axis=1), np.float64(np.float32(4.0) * np.float32(0.707106)))
+        # float32 rounding in the oracle can move an extent across an integer
+        near_int = np.abs(h - np.round(h)) < 1e-2
+        sel = ok & ~near_int
+        np.testing.assert_array_equal(pre["radii"][chunk][sel], np.ceil(h[sel]).astype(np.int32))
+        xy = pre["xy"][chunk][sel].astype(np.float64)
+        np.testing.assert_allclose(xy, cen[sel], atol=2e-3, rtol=1e-5)
+        checked += int(sel.sum())
+    assert checked > 0.9 * len(ids), (checked, len(ids))
+
+
 def test_preprocess_near_cull_and_tiles(oracle):
     sc = scene("cfg1")
     cam = sc.cameras[0]
