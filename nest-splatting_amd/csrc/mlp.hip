@@ -551,21 +551,29 @@ __device__ __forceinline__ int xrow_chunk(int r, int c) { return (c & ~3) | ((c 
 
 // Block variant for the contiguous channel-major map the render writes
 // (pixel stride 1, channel stride a multiple of 4, 16-byte aligned): the
-// workgroup takes 256 pixels per iteration, and wave w loads channels
-// [w C/4, (w+1) C/4) of all 256 with one float4 (4 pixels) per lane, so each
-// channel is read as one 1 KiB run (channel-major reads in 256-byte runs
+// workgroup takes 256 pixels per iteration, and wave w of NWV loads channels
+// [w C/NWV, (w+1) C/NWV) of all 256 with one float4 (4 pixels) per lane, so
+// each channel is read as one 1 KiB run (channel-major reads in 256-byte runs
 // stall at ~3.6 TB/s on MI355X, 1 KiB runs reach ~6.1 TB/s).  The waves write
 // the 16-bit features into the shared pixel rows, compute their own pixels'
-// SH terms, and after a barrier each wave runs the three layers on its 64
-// rows as mlp_mfma32_kernel does.  The next block's features are in flight
-// during the contraction.
-template <int NT, bool kBF16, int C>
-__global__ void __launch_bounds__(kMlpThreads) __attribute__((amdgpu_waves_per_eu(2)))
+// SH terms, and after a barrier each wave runs the three layers on its
+// 256/NWV rows as mlp_mfma32_kernel does, NJ 16-pixel N-tiles at a time.
+// The next block's features are in flight during the contraction.
+//  - width 32/64: 4 waves of 64 pixels, two N-tiles at a time, LDS sized at
+//    launch (two workgroups per CU);
+//  - width 128: the weights alone take 66 KB of LDS, so one workgroup holds a
+//    CU; 8 waves of 32 pixels keep two waves on every SIMD.
+template <int NT, bool kBF16, int C, int NWV, int NJ>
+__global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2)))
 mlp_block_kernel(const MlpParams p) {
   using S = Mlp32Shape<C, NT>;
   constexpr int K1 = S::K1, LD1 = S::LD1, LD2 = S::LD2, W = NT * 16;
-  constexpr int CPW = C / 4;  // channels each wave loads
-  static_assert(NT % 2 == 0 && CPW % 4 == 0, "width multiple of 32, channels multiple of 16");
+  constexpr int kThreads = 64 * NWV;
+  constexpr int PPW = 256 / NWV;  // pixels each wave contracts
+  constexpr int NTW = PPW / 16;   // their 16-pixel N-tiles
+  constexpr int CPW = C / NWV;    // channels each wave loads
+  static_assert(NT % 2 == 0 && CPW % 4 == 0 && NTW % NJ == 0, "width multiple of 32, 4 channels per wave");
+  static_assert(S::X + 256 * LD1 == S::TOTAL, "256 pixel rows");
   extern __shared__ uint16_t lds[];
   uint16_t* w1 = lds + S::W1;
   uint16_t* w2 = lds + S::W2;
@@ -574,23 +582,24 @@ mlp_block_kernel(const MlpParams p) {
   const uint16_t* g2 = static_cast<const uint16_t*>(p.w2);
   const uint16_t* g3 = static_cast<const uint16_t*>(p.w3);
   constexpr int Kin = C + 16;
-  for (int i = threadIdx.x; i < W * LD1; i += kMlpThreads) {
+  for (int i = threadIdx.x; i < W * LD1; i += kThreads) {
     const int r = i / LD1, k = i % LD1;
     w1[i] = k < Kin ? g1[r * Kin + k] : (uint16_t)0;
   }
-  for (int i = threadIdx.x; i < W * LD2; i += kMlpThreads) {
+  for (int i = threadIdx.x; i < W * LD2; i += kThreads) {
     const int r = i / LD2, q = i % LD2;
     w2[i] = q < W ? g2[r * W + hidden_unit(q)] : (uint16_t)0;
   }
-  for (int i = threadIdx.x; i < 16 * LD2; i += kMlpThreads) {
+  for (int i = threadIdx.x; i < 16 * LD2; i += kThreads) {
     const int r = i / LD2, q = i % LD2;
     w3[i] = (r < 3 && q < W) ? g3[r * W + hidden_unit(q)] : (uint16_t)0;
   }
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int col = lane & 15, grp = lane >> 4;
   uint16_t* xall = lds + S::X;              // [256 pixels][LD1], chunks swizzled by xrow_chunk
-  uint16_t* xrow = xall + wid * 64 * LD1;   // this wave's 64 pixels
-  for (int k = Kin; k < K1; k++) xrow[lane * LD1 + 8 * xrow_chunk(wid * 64 + lane, k >> 3) + (k & 7)] = 0;
+  uint16_t* xrow = xall + wid * PPW * LD1;  // this wave's PPW pixels
+  if (lane < PPW)
+    for (int k = Kin; k < K1; k++) xrow[lane * LD1 + 8 * xrow_chunk(wid * PPW + lane, k >> 3) + (k & 7)] = 0;
 
   const uint32_t N = (uint32_t)p.N;
   const uint32_t nblk = (N + 255) / 256;
@@ -612,12 +621,14 @@ mlp_block_kernel(const MlpParams p) {
       }
     }
   };
-  float alpha4[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  float alpha4[NTW];
+#pragma unroll
+  for (int j = 0; j < NTW; j++) alpha4[j] = 1.0f;
   auto load_alpha = [&](uint32_t b) {
     if (p.alpha && grp == 0) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const uint32_t nj = b * 256 + wid * 64 + 16 * j + col;
+      for (int j = 0; j < NTW; j++) {
+        const uint32_t nj = b * 256 + wid * PPW + 16 * j + col;
         alpha4[j] = p.alpha[nj < N ? nj : N - 1];
       }
     }
@@ -651,86 +662,90 @@ mlp_block_kernel(const MlpParams p) {
       }
     }
     // SH terms of this wave's pixels
-    {
-      const uint32_t n = b * 256 + wid * 64 + lane;
+    if (lane < PPW) {
+      const uint32_t n = b * 256 + wid * PPW + lane;
       float dx, dy, dz;
       pixel_dir32(p, n < N ? n : N - 1, dx, dy, dz);
       float sh[16];
       sh16(dx, dy, dz, sh);
 #pragma unroll
       for (int q = 0; q < 2; q++)
-        *reinterpret_cast<uint4*>(xrow + lane * LD1 + 8 * xrow_chunk(wid * 64 + lane, C / 8 + q)) =
+        *reinterpret_cast<uint4*>(xrow + lane * LD1 + 8 * xrow_chunk(wid * PPW + lane, C / 8 + q)) =
             make_uint4(pack2_16<kBF16>(sh[8 * q + 0], sh[8 * q + 1]), pack2_16<kBF16>(sh[8 * q + 2], sh[8 * q + 3]),
                        pack2_16<kBF16>(sh[8 * q + 4], sh[8 * q + 5]), pack2_16<kBF16>(sh[8 * q + 6], sh[8 * q + 7]));
     }
-    const float a_out[4] = {alpha4[0], alpha4[1], alpha4[2], alpha4[3]};
+    float a_out[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; j++) a_out[j] = alpha4[j];
     if (b + gridDim.x < nblk) {  // next block in flight during the contraction
       load_alpha(b + gridDim.x);
       load_block(b + gridDim.x);
     }
-    // every wave's channels are in the rows: wait for this wave's LDS writes
-    // only (lgkmcnt 0, vmcnt and expcnt at their maxima), not for the block in
-    // flight, then the plain barrier (__syncthreads would also wait for it)
-    __builtin_amdgcn_s_waitcnt(0xC07F);
+    // Every wave's channels are in the rows.  The LDS-only release/acquire
+    // fences order this wave's row stores before the barrier and the other
+    // waves' row reads after it (lgkmcnt 0, no wait for the block in flight);
+    // a plain __syncthreads would also wait for those loads.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
-    // two halves of two 16-pixel N-tiles each, so the accumulators (2 x NT x 2
-    // x 4 floats) leave room for the block in flight
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    // NJ N-tiles at a time, so the accumulators (2 x NT x NJ x 4 floats)
+    // leave room for the block in flight
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      f32x4 acc1[NT][2];
+    for (int h = 0; h < NTW / NJ; h++) {
+      f32x4 acc1[NT][NJ];
 #pragma unroll
       for (int mt = 0; mt < NT; mt++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc1[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NJ; j++) acc1[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < K1 / 32; kc++) {
-        uint4 bb[2];
+        uint4 bb[NJ];
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-          bb[j] = *reinterpret_cast<const uint4*>(xrow + (16 * (2 * h + j) + col) * LD1 +
-                                                  8 * xrow_chunk(wid * 64 + 16 * (2 * h + j), 4 * kc + grp));
+        for (int j = 0; j < NJ; j++)
+          bb[j] = *reinterpret_cast<const uint4*>(xrow + (16 * (NJ * h + j) + col) * LD1 +
+                                                  8 * xrow_chunk(wid * PPW + 16 * (NJ * h + j), 4 * kc + grp));
 #pragma unroll
         for (int mt = 0; mt < NT; mt++) {
           const uint4 a = *reinterpret_cast<const uint4*>(w1 + (16 * mt + col) * LD1 + 32 * kc + 8 * grp);
 #pragma unroll
-          for (int j = 0; j < 2; j++) acc1[mt][j] = mfma32<kBF16>(a, bb[j], acc1[mt][j]);
+          for (int j = 0; j < NJ; j++) acc1[mt][j] = mfma32<kBF16>(a, bb[j], acc1[mt][j]);
         }
       }
-      f32x4 acc2[NT][2];
+      f32x4 acc2[NT][NJ];
 #pragma unroll
       for (int mt = 0; mt < NT; mt++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc2[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NJ; j++) acc2[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < NT / 2; kc++) {
-        uint4 bb[2];
+        uint4 bb[NJ];
 #pragma unroll
-        for (int j = 0; j < 2; j++) bb[j] = relu_pack8<kBF16>(acc1[2 * kc][j], acc1[2 * kc + 1][j]);
+        for (int j = 0; j < NJ; j++) bb[j] = relu_pack8<kBF16>(acc1[2 * kc][j], acc1[2 * kc + 1][j]);
 #pragma unroll
         for (int mt = 0; mt < NT; mt++) {
           const uint4 a = *reinterpret_cast<const uint4*>(w2 + (16 * mt + col) * LD2 + 32 * kc + 8 * grp);
 #pragma unroll
-          for (int j = 0; j < 2; j++) acc2[mt][j] = mfma32<kBF16>(a, bb[j], acc2[mt][j]);
+          for (int j = 0; j < NJ; j++) acc2[mt][j] = mfma32<kBF16>(a, bb[j], acc2[mt][j]);
         }
       }
-      f32x4 acc3[2];
+      f32x4 acc3[NJ];
 #pragma unroll
-      for (int j = 0; j < 2; j++) acc3[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < NJ; j++) acc3[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < NT / 2; kc++) {
         const uint4 a = *reinterpret_cast<const uint4*>(w3 + col * LD2 + 32 * kc + 8 * grp);
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < NJ; j++)
           acc3[j] = mfma32<kBF16>(a, relu_pack8<kBF16>(acc2[2 * kc][j], acc2[2 * kc + 1][j]), acc3[j]);
       }
       if (grp == 0) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-          const uint32_t nj = b * 256 + wid * 64 + 16 * (2 * h + j) + col;
+        for (int j = 0; j < NJ; j++) {
+          const uint32_t nj = b * 256 + wid * PPW + 16 * (NJ * h + j) + col;
           if (nj < N) {
 #pragma unroll
             for (int o = 0; o < 3; o++)
-              p.out[o * p.out_os + (int64_t)nj * p.out_ns] = finish_rgb_alpha(p, a_out[2 * h + j], acc3[j][o], o);
+              p.out[o * p.out_os + (int64_t)nj * p.out_ns] = finish_rgb_alpha(p, a_out[NJ * h + j], acc3[j][o], o);
           }
         }
       }
@@ -743,12 +758,16 @@ static bool mlp_block_fits(const MlpParams& p) {
          p.N < (1ll << 31) - 256 && (uint64_t)p.feat_cs < (1ull << 31);
 }
 
+// Widths 32 and 64: 4 waves, two workgroups per CU (512 in all).  Width 128:
+// 8 waves, one workgroup per CU (256 in all).
 template <int NT, bool kBF16, int C>
 static hipError_t launch_block(const MlpParams& p, hipStream_t s) {
+  constexpr int kWaves = NT >= 8 ? 8 : 4;
   const size_t lds = sizeof(uint16_t) * (size_t)Mlp32Shape<C, NT>::TOTAL;
   const int64_t nblk = (p.N + 255) / 256;
-  const unsigned blocks = (unsigned)(nblk < 512 ? (nblk > 0 ? nblk : 1) : 512);
-  hipLaunchKernelGGL((mlp_block_kernel<NT, kBF16, C>), dim3(blocks), dim3(kMlpThreads), lds, s, p);
+  const int64_t cap = NT >= 8 ? 256 : 512;
+  const unsigned blocks = (unsigned)(nblk < cap ? (nblk > 0 ? nblk : 1) : cap);
+  hipLaunchKernelGGL((mlp_block_kernel<NT, kBF16, C, kWaves, 2>), dim3(blocks), dim3(64 * kWaves), lds, s, p);
   return hipGetLastError();
 }
 
@@ -876,6 +895,8 @@ static hipError_t launch_f32(const MlpParams& p, hipStream_t s) {
 
 template <bool kBF16>
 static hipError_t launch_mfma_width(const MlpParams& p, hipStream_t s) {
+  // 64 channels at width 128 in the render's layout: the 8-wave block kernel
+  if (p.width == 128 && p.C == 64 && mlp32_fits(p, p.C) && mlp_block_fits(p)) return launch_block<8, kBF16, 64>(p, s);
   // 16, 32 or 64 channels at width 32 or 64: the 16x16x32 kernel
   if ((p.width == 64 || p.width == 32) && mlp32_fits(p, p.C)) {
     const bool w64 = p.width == 64;

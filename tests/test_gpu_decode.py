@@ -236,11 +236,11 @@ def test_rvq_decode_paths_bit_exact(oracle, P, S, K, dim):
 
 
 @pytest.mark.parametrize("C,width,dtype", [(16, 64, "bf16"), (32, 32, "f16"), (64, 64, "bf16"), (64, 32, "f16"),
-                                           (64, 128, "bf16")])
+                                           (64, 128, "bf16"), (64, 128, "f16")])
 def test_mlp_decode_image_blocks(oracle, C, width, dtype):
     """decode_image on the render's contiguous [C, H, W] map (the 256-pixel
-    block kernel for widths 32 and 64, a partial last block), with a mask and
-    white background, against the oracle."""
+    block kernel: 4 waves for widths 32 and 64, 8 for width 128; a partial
+    last block), with a mask and white background, against the oracle."""
     from nest_splat.camera import look_at, view_ray_matrix
     from nest_splat.mlp import NestMLP
     rng = np.random.default_rng(C + width)
