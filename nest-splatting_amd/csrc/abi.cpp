@@ -742,6 +742,36 @@ int nest_grid_encode(const float* inputs, int64_t B, int32_t D, const void* embe
   GridEncodeParams p{};
   int rc = build_levels(offsets_host, (uint32_t)L, S, (uint32_t)H, align_corners != 0, D, gridtype == 0, p.lv);
   if (rc) return rc;
+  // the common layout (dense prefix without modulo, then power-of-two hashed
+  // levels; D = 3, binary32, trilinear) takes the render's lookup
+  const uint64_t tbytes = (uint64_t)emb_rows * (uint64_t)C * 4u;
+  if (D == 3 && gridtype == 0 && emb_dtype == NEST_DTYPE_F32 && interpolation == 0 && C <= 8 &&
+      tbytes < (1ull << 32)) {
+    uint32_t nd = 0;
+    while (nd < (uint32_t)L && (p.lv.flags[nd] & 5u) == 4u) nd++;
+    bool structured = true;
+    for (uint32_t l = nd; l < (uint32_t)L; l++) structured = structured && (p.lv.flags[l] & 3u) == 3u;
+    if (structured) {
+      GridEncodeQuadParams q{};
+      q.inputs = inputs;
+      q.B = B;
+      q.F = C;
+      q.L = L;
+      q.pos_offset = align_corners ? 0.0f : 0.5f;
+      q.table = static_cast<const float*>(embeddings);
+      q.table_rows = (uint32_t)emb_rows;
+      q.outputs = static_cast<float*>(outputs);
+      for (uint32_t l = 0; l < (uint32_t)L; l++) {
+        const bool dense = l < nd;
+        q.lq[l].scale = p.lv.scale[l];
+        q.lq[l].a = dense ? p.lv.res1[l] : p.lv.hsize[l] - 1u;
+        q.lq[l].b = dense ? p.lv.res1[l] * p.lv.res1[l] : 0u;
+        q.lq[l].soff = p.lv.base[l] * (uint32_t)C * 4u;
+      }
+      hipError_t e = launch_grid_encode_quad(q, static_cast<hipStream_t>(stream));
+      return e == hipSuccess ? NEST_OK : hip_fail(e, "grid_encode");
+    }
+  }
   p.inputs = inputs;
   p.B = B;
   p.D = D;

@@ -140,6 +140,96 @@ static hipError_t ge_launch_d(const GridEncodeParams& p, hipStream_t s) {
   }
 }
 
+// Common level layout (D = 3, binary32, trilinear; see GridEncodeQuadParams).
+// A workgroup encodes 64 points per iteration: lane = point, and wave w
+// takes levels w, w + 4, ..., so each level's record is one scalar load and
+// its dense-or-hashed branch is uniform.  A level is quad_corners (or, for
+// 8-byte entries, quad_fetch_pairs) and corners_sum, the render's lookup,
+// whose float order is kernel_grid's: w = ((1 * w_x) * w_y) * w_z and
+// out = fmaf(w, v, out) over corners 0..7 from +0 (inputs are in [0, 1] past
+// the range test, so fract(x) is x - floor(x)).  The 64 points' outputs are
+// staged in LDS (rows padded by 4 floats against bank conflicts) and written
+// as one contiguous run.
+constexpr int kGeqThreads = 256;
+constexpr int kGeqPoints = 64;
+
+template <int F>
+__global__ void __launch_bounds__(kGeqThreads) grid_encode_quad_kernel(const GridEncodeQuadParams p) {
+  extern __shared__ float geq_rows[];  // [64][L * F + 4]
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int LF = p.L * F;
+  const int ld = LF + 4;
+  const nest_i32x4 rsrc = table_rsrc_rows<F, false>(p.table, p.table_rows);
+  const int64_t nblk = (p.B + kGeqPoints - 1) / kGeqPoints;
+  for (int64_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
+    const int64_t b = blk * kGeqPoints + lane;
+    float u[3] = {0.0f, 0.0f, 0.0f};
+    bool skip = b >= p.B;
+    if (!skip) {
+      const float* in = p.inputs + 3 * b;
+#pragma unroll
+      for (int d = 0; d < 3; d++) {
+        u[d] = in[d];
+        if (u[d] < 0 || u[d] > 1) skip = true;  // outside the grid: every level is zero
+      }
+    }
+    float* row = geq_rows + lane * ld;
+    for (int l = wid; l < p.L; l += kGeqThreads / 64) {
+      const LevelQuad q = p.lq[l];
+      float v[F];
+#pragma unroll
+      for (int f = 0; f < F; f++) v[f] = 0.0f;
+      if (!skip) {
+        LevelCorners cn;
+        float vals[8][F];
+        if constexpr (F == 2) {
+          quad_fetch_pairs<2, false>(q, p.pos_offset, u, rsrc, cn, vals);
+        } else {
+          quad_corners(q, p.pos_offset, u, cn);
+          corners_load<F, false>(rsrc, cn, vals);
+        }
+        corners_sum<F>(cn, vals, v);
+      }
+#pragma unroll
+      for (int f = 0; f < F; f++) row[l * F + f] = v[f];
+    }
+    __syncthreads();
+    const int64_t n0 = blk * kGeqPoints;
+    const int pts = (int)(p.B - n0 < kGeqPoints ? p.B - n0 : kGeqPoints);
+    float* out = p.outputs + n0 * LF;
+    const int total = pts * LF;
+    if ((LF & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
+      for (int i = 4 * (int)threadIdx.x; i < total; i += 4 * kGeqThreads) {
+        const int pt = i / LF, c = i - pt * LF;
+        const float* r = geq_rows + pt * ld + c;
+        *reinterpret_cast<float4*>(out + i) = make_float4(r[0], r[1], r[2], r[3]);
+      }
+    } else {
+      for (int i = threadIdx.x; i < total; i += kGeqThreads) {
+        const int pt = i / LF;
+        out[i] = geq_rows[pt * ld + (i - pt * LF)];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+hipError_t launch_grid_encode_quad(const GridEncodeQuadParams& p, hipStream_t s) {
+  if (p.B <= 0) return hipSuccess;
+  const int64_t nblk = (p.B + kGeqPoints - 1) / kGeqPoints;
+  const unsigned blocks = (unsigned)(nblk < 4096 ? nblk : 4096);
+  const size_t lds = sizeof(float) * (size_t)kGeqPoints * (size_t)(p.L * p.F + 4);
+  switch (p.F) {
+    case 1: hipLaunchKernelGGL(grid_encode_quad_kernel<1>, dim3(blocks), dim3(kGeqThreads), lds, s, p); break;
+    case 2: hipLaunchKernelGGL(grid_encode_quad_kernel<2>, dim3(blocks), dim3(kGeqThreads), lds, s, p); break;
+    case 4: hipLaunchKernelGGL(grid_encode_quad_kernel<4>, dim3(blocks), dim3(kGeqThreads), lds, s, p); break;
+    case 8: hipLaunchKernelGGL(grid_encode_quad_kernel<8>, dim3(blocks), dim3(kGeqThreads), lds, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_grid_encode(const GridEncodeParams& p, hipStream_t s) {
   if (p.B <= 0) return hipSuccess;
   return p.half ? ge_launch_d<true>(p, s) : ge_launch_d<false>(p, s);

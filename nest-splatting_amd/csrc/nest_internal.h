@@ -266,6 +266,22 @@ struct GridEncodeParams {
 };
 hipError_t launch_grid_encode(const GridEncodeParams& p, hipStream_t s);
 
+// GridEncoder forward on the common level layout (D = 3, binary32 table,
+// trilinear, levels [0, n_dense) dense without modulo and the rest hashed
+// into power-of-two sizes): the render's level records and lookup.
+struct GridEncodeQuadParams {
+  const float* inputs;   // [B][3]
+  int64_t B;
+  int F;
+  int L;
+  float pos_offset;      // 0.5, or 0 with align_corners
+  const float* table;
+  uint32_t table_rows;
+  float* outputs;        // [B][L*F]
+  LevelQuad lq[NEST_MAX_LEVELS];
+};
+hipError_t launch_grid_encode_quad(const GridEncodeQuadParams& p, hipStream_t s);
+
 struct MlpParams {
   int C;
   int width;
