@@ -335,7 +335,7 @@ int nest_backward(const nest_raster_settings *settings, const nest_hashgrid *gri
                   void *bwd_ws, size_t bwd_bytes, void *stream);
 
 
-/* GaussianModel.get_homotrans (scene/gaussian_model.py:249-250):
+/* GaussianModel.get_homotrans (scene/gaussian_model.py:312-317):
  * build_H(build_rotation(rotations), scales, means3D) of
  * utils/general_utils.py:78-113, the [P,4,4] row-major splat-to-world
  * transforms the forward reads (columns 0, 1 and 3).  rotations [P,4]

@@ -275,10 +275,13 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
     g.table_rows = (uint32_t)gr->table_rows;
     // structured grid: a prefix of dense levels without modulo, then hashed
     // levels with power-of-two sizes (flag bits: 1 hashed, 2 pow2, 4 nomod),
-    // trilinear interpolation
+    // trilinear interpolation, cell positions offset by 0.5 (its cell
+    // fraction is fract(x), exact for x >= 0: with the 0.5 offset x stays
+    // positive even for a grid coordinate that rounds a few ulp below 0;
+    // align_corners grids take the general path's x - floor(x))
     uint32_t nd = 0;
     while (nd < g.L && (g.lv.flags[nd] & 5u) == 4u) nd++;
-    bool structured = g.interp == 0;
+    bool structured = g.interp == 0 && !gr->align_corners;
     for (uint32_t l = nd; l < g.L; l++) structured = structured && (g.lv.flags[l] & 3u) == 3u;
     g.structured = structured ? 1u : 0u;
     g.n_dense = nd;

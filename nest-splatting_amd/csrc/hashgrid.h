@@ -229,8 +229,10 @@ __device__ __forceinline__ void level_corners(const LevelTable& lv, int l, float
 
 // cell_weights for a looked-up render hit: its grid coordinate u is in
 // [0, 1] (the contraction maps into [0, 1], and out-of-range hits of the
-// affine normalisation look nothing up), so x = u * scale + pos_offset lies
-// in [0, 2^32) and x - (float)f2u_sat(x) is exactly fract(x): one
+// affine normalisation look nothing up), and the caller's pos_offset is 0.5
+// (the host sends align_corners grids to the general path), so
+// x = u * scale + 0.5 is positive even if the contraction's rounding left u a
+// few ulp below 0, and x - (float)f2u_sat(x) is exactly fract(x): one
 // v_fract_f32 instead of a conversion back and a subtraction (NaN stays NaN).
 __device__ __forceinline__ void cell_weights_unit(float scale, float pos_offset, const float u[3], uint32_t g[3],
                                                   LevelCorners& cn) {

@@ -256,7 +256,7 @@ hipError_t launch_mark_visible(int P, const float* means, const float view[16], 
   return hipGetLastError();
 }
 
-// get_homotrans (scene/gaussian_model.py:249-250) = build_H(build_rotation(r),
+// get_homotrans (scene/gaussian_model.py:312-317) = build_H(build_rotation(r),
 // s, xyz) of utils/general_utils.py:78-113: the quaternion is normalised with
 // sqrt(((r0 r0 + r1 r1) + r2 r2) + r3 r3) and a division, R is built with the
 // reference's expressions, and H = [[R * (sx, sy, 0) by column, xyz],

@@ -834,8 +834,10 @@ static hipError_t launch_hash_levels(const RenderParams& p, hipStream_t s) {
 // of 8 log2(count + 1), so the heaviest tiles start first and the launch ends
 // on light ones; workgroup i runs on XCD i % 8, and each XCD takes runs of 16
 // consecutive positions, so the heavy tiles are dealt evenly over the XCDs
-// while neighbouring tiles of a bucket share an L2 (runs of 16: render
-// 6.156 -> 6.11 ms on the 1M-splat frame; 32 and 64: 6.18 and 6.28).  (Giving each XCD
+// while neighbouring tiles of a bucket tend to share an L2 (on the 1M-splat
+// frame runs of 16 raised the L2 hit rate from 35% to 50% and cut the HBM
+// traffic from 27.7 to 21.4 GB per launch; the render time moved by less
+// than run-to-run noise, and runs of 32 and 64 were slower).  (Giving each XCD
 // a band of tile rows with an eighth of the pairs, heaviest first within the
 // band, raised the L2 hit rate from 35% to 54% on the 1M-splat frame but
 // took the render from 6.16 to 6.83 ms: pair counts balance the XCDs' work
@@ -870,8 +872,10 @@ __global__ void __launch_bounds__(kOrderThreads) tile_order_kernel(const uint2* 
   __syncthreads();
   // Position pos of the descending order goes to workgroup b; within each
   // group of 8 * kRun positions, XCD x (workgroups b with b % 8 == x) takes
-  // the run of kRun consecutive positions starting at x * kRun, so tiles
-  // adjacent in a bucket (bucket order follows tile order) share an L2.
+  // the run of kRun consecutive positions starting at x * kRun.  Positions
+  // within a bucket come from LDS atomics, so their tile order is only as
+  // ordered as the atomics are served (a wave's lanes hold consecutive
+  // tiles); a run then mostly holds nearby tiles, which share an L2.
   constexpr uint32_t kRun = 16u, kGroup = 8u * kRun;
   const uint32_t full = ntiles / kGroup * kGroup;  // the tail keeps pos == b
   for (uint32_t t = threadIdx.x; t < ntiles; t += kOrderThreads) {

@@ -351,9 +351,11 @@ def geometry_arrays(res: ForwardResult, P: int) -> Dict[str, torch.Tensor]:
 
 
 def build_homotrans(rotations: torch.Tensor, scales: torch.Tensor, means3D: torch.Tensor) -> torch.Tensor:
-    """get_homotrans (scene/gaussian_model.py:249-250): build_H(build_rotation
+    """get_homotrans (scene/gaussian_model.py:312-317): build_H(build_rotation
     (rotations), scales, means3D) of utils/general_utils.py:78-113 on the GPU,
-    [P, 4, 4] float32, bit-exact with the reference's torch expressions."""
+    [P, 4, 4] float32, bit-exact with the reference's torch expressions.
+    rotations are the raw quaternions (GaussianModel._rotation): build_rotation
+    normalises them, as the kernel does."""
     P = int(rotations.shape[0])
     if rotations.shape != (P, 4) or scales.shape != (P, 2) or means3D.shape != (P, 3):
         raise ValueError("rotations [P,4], scales [P,2] and means3D [P,3] are required")

@@ -155,11 +155,14 @@ def test_irregular_level_sizes_parity(oracle, sizes, name):
 
 
 @pytest.mark.parametrize("name,align,interp", [("unbounded_small", False, 1), ("shell_small", True, 0),
-                                               ("shells_small", True, 1)])
+                                               ("shells_small", True, 1), ("unbounded_small", True, 0)])
 def test_align_corners_and_smoothstep_parity(oracle, name, align, interp):
     """align_corners (pos offset 0, resolution cells) and smoothstep
-    weights (hashgrid.h smoothstep); smoothstep takes the general per-level
-    path, trilinear the dense-prefix/power-of-two one."""
+    weights (hashgrid.h smoothstep) take the general per-level path (its cell
+    fraction is x - floor(x), also for a contracted coordinate that rounds
+    below 0); trilinear grids without align_corners the dense-prefix/
+    power-of-two one.  The contracted scene with align_corners and far splats
+    is the case where the two would differ if a coordinate fell below 0."""
     sc = scene(name)
     print(f"[case] {name} align_corners={align} interp={interp}", flush=True)
     res = run_gpu(sc, align_corners=align, interp=interp)

@@ -52,7 +52,7 @@ def test_noalloc_scan_matches_workspace_scan():
     assert rc == L.NEST_ERR_WORKSPACE
     assert b"exceeds" in L.lib().nest_last_error()
     assert torch.all(o == 5)
-    # n at the limit's block boundary and n = 1
+    # n on a 4096-item block boundary and n = 1
     for n in (4096 * 37, 1):
         x_np = rng.integers(0, 1000, n, dtype=np.uint32)
         x = torch.from_numpy(x_np.view(np.int32)).to(DEV)
@@ -60,3 +60,27 @@ def test_noalloc_scan_matches_workspace_scan():
         _scan_noalloc(L, x, o)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(o.cpu().numpy().view(np.uint32), np.cumsum(x_np, dtype=np.uint64).astype(np.uint32))
+
+
+def test_noalloc_scan_at_the_scratch_limit():
+    """n = NEST_SCAN_NOALLOC_MAX: 65,535 blocks of 4096, so the block partials
+    fill the scratch up to its last slot (the grand total); 1 GiB in and out.
+    Against the workspace scan, then a smaller call on the same scratch."""
+    from nest_splat import _lib as L
+    n = L.SCAN_NOALLOC_MAX
+    print(f"[noalloc] n = {n} (the limit)", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    x = torch.randint(0, 16, (n,), dtype=torch.int32, device=DEV, generator=g)
+    got = torch.empty(n, dtype=torch.int32, device=DEV)
+    _scan_noalloc(L, x, got)
+    want = _scan_ws(L, x)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    total = int(x.to(torch.int64).sum().item()) & 0xFFFFFFFF
+    assert int(got[-1].item()) & 0xFFFFFFFF == total
+    del want
+    m = 5000
+    small = torch.empty(m, dtype=torch.int32, device=DEV)
+    _scan_noalloc(L, x[:m].contiguous(), small)
+    torch.cuda.synchronize()
+    assert torch.equal(small, got[:m])
