@@ -54,9 +54,10 @@ def render_compulsory_bound(P: int, NR: int, HW: int, table_bytes: int, C: int) 
 # What bounds the render kernel, from its counters (TA busy, L1 accesses per
 # clock, VALU share): the 16-byte table gathers' vector-L1 address and tag
 # rate and the latency of the gathers that miss L2.
-RENDER_LIMITER = ("vector L1 address/tag rate of the 16-byte table gathers (about one L1 tag access per CU clock, "
-                  "TA ~70% busy) and the latency of gathers missing L2; HBM traffic is the counter-measured fetch "
-                  "+ write")
+RENDER_LIMITER = ("the lookup drains' instruction stream: VALU issue ~0.63 and the texture addresser ~0.75 busy on "
+                  "the 1M-splat frame (one L1 tag access per CU clock); with every gather L1-resident the render "
+                  "takes 0.90x its time, without the drains 0.24x; HBM traffic is the counter-measured fetch + "
+                  "write")
 
 
 def load_counters(path: str) -> dict:
@@ -472,6 +473,9 @@ def main():
             ctr["TCP_TOTAL_CACHE_ACCESSES_sum"] / (ctr.get("cus", 256) * ctr["kernel_cycles"]), 3)
     if ctr.get("TA_BUSY_avr") and ctr.get("kernel_cycles"):
         roofline["ta_busy"] = round(ctr["TA_BUSY_avr"] / ctr["kernel_cycles"], 3)
+    if ctr.get("SQ_INSTS_VALU") and ctr.get("kernel_cycles"):
+        # a wave64 VALU instruction occupies its 16-lane SIMD for 4 cycles; 4 SIMDs per CU
+        roofline["valu_issue"] = round(4 * ctr["SQ_INSTS_VALU"] / (4 * ctr.get("cus", 256) * ctr["kernel_cycles"]), 3)
     out = {
         "metric": METRIC,
         "value": round(mpix, 3),
