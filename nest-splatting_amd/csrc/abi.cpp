@@ -567,13 +567,14 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     tm.end();
     tm.begin(NEST_STAGE_SORT);
     const int bit = (int)higher_msb(ntiles);
-    rc = check_stage(launch_sort_tiles(pair_tiles, pair_ids, keys, vals, NR, bit, depth, b + bo[NEST_BIN_SORT_TMP], s),
+    rc = check_stage(launch_sort_tiles(pair_tiles, pair_ids, keys, vals, NR, bit, depth, ranges, ntiles,
+                                       b + bo[NEST_BIN_SORT_TMP], s),
                      "sort", rs->debug, s);
     if (rc) return rc;
     tm.end();
   }
   tm.begin(NEST_STAGE_RANGES);
-  if ((rc = check_stage(launch_tile_ranges(keys, NR, ranges, ntiles, s), "tile ranges", rs->debug, s))) return rc;
+  if ((rc = check_stage(launch_tile_ranges(ranges, NR, ntiles, s), "tile ranges", rs->debug, s))) return rc;
   tm.end();
 
   rp.ranges = ranges;

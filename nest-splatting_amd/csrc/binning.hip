@@ -178,33 +178,6 @@ hipError_t launch_fill_u32(uint32_t* dst, uint32_t value, int64_t n, hipStream_t
   return hipGetLastError();
 }
 
-// Tile ids at or past ntiles (only possible when the caller's pair count
-// exceeds the pairs written) are not recorded.
-__global__ void tile_ranges_kernel(const uint64_t* __restrict__ keys, int64_t n, uint2* __restrict__ ranges,
-                                   uint32_t ntiles) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const uint32_t t = (uint32_t)(keys[i] >> 32);
-  if (i == 0) {
-    if (t < ntiles) ranges[t].x = 0;
-  } else {
-    const uint32_t pt = (uint32_t)(keys[i - 1] >> 32);
-    if (t != pt) {
-      if (pt < ntiles) ranges[pt].y = (uint32_t)i;
-      if (t < ntiles) ranges[t].x = (uint32_t)i;
-    }
-  }
-  if (i == n - 1 && t < ntiles) ranges[t].y = (uint32_t)n;
-}
-
-hipError_t launch_tile_ranges(const uint64_t* keys, int64_t n, uint32_t* ranges, uint32_t ntiles, hipStream_t s) {
-  hipError_t e = launch_fill_u32(ranges, 0u, 2 * (int64_t)ntiles, s);
-  if (e != hipSuccess || n <= 0) return e;
-  hipLaunchKernelGGL(tile_ranges_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, keys, n,
-                     reinterpret_cast<uint2*>(ranges), ntiles);
-  return hipGetLastError();
-}
-
 // ---------------------------------------------------------------------------
 // radix sort
 // ---------------------------------------------------------------------------
@@ -233,52 +206,75 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 }
 
 // Per-block digit histogram, written digit-major: counts[d * nblocks + b].
+// The block's keys are counted with LDS atomics (a count does not depend on
+// the order in which they land).
 template <typename K>
 __global__ void __launch_bounds__(kSortThreads) radix_hist_kernel(const K* __restrict__ keys, int64_t n, int shift,
                                                                  uint32_t* __restrict__ counts, uint32_t nblocks) {
-  __shared__ uint32_t hist[kSortWaves][kRadix];
-  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-  for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&hist[0][0])[i] = 0;
-  __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)wid * (kWave * kSortRounds);
-  // all of the wave's keys in flight at once, then the rounds
+  __shared__ uint32_t hist[kRadix];
+  for (int i = threadIdx.x; i < kRadix; i += kSortThreads) hist[i] = 0;
+  const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  // all of the thread's keys in flight at once
   K key[kSortRounds];
 #pragma unroll
   for (int r = 0; r < kSortRounds; r++) {
-    const int64_t i = base + r * kWave + lane;
+    const int64_t i = base + r * kSortThreads + threadIdx.x;
     key[r] = i < n ? keys[i] : (K)0;
   }
+  __syncthreads();
 #pragma unroll
   for (int r = 0; r < kSortRounds; r++) {
-    const int64_t i = base + r * kWave + lane;
-    const bool ok = i < n;
-    const uint32_t d = ok ? (uint32_t)(key[r] >> shift) & (kRadix - 1) : 0u;
-    const uint64_t valid = __ballot(ok);
-    const uint64_t peers = match_digit(d, valid);
-    const int leader = __ffsll((unsigned long long)peers) - 1;
-    if (ok && lane == leader) hist[wid][d] += (uint32_t)__popcll(peers);
+    const int64_t i = base + r * kSortThreads + threadIdx.x;
+    if (i < n) atomicAdd(&hist[(uint32_t)(key[r] >> shift) & (kRadix - 1)], 1u);
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < kRadix; d += kSortThreads) {
-    uint32_t s = 0;
-#pragma unroll
-    for (int w = 0; w < kSortWaves; w++) s += hist[w][d];
-    counts[(size_t)d * nblocks + blockIdx.x] = s;
-  }
+  for (int d = threadIdx.x; d < kRadix; d += kSortThreads) counts[(size_t)d * nblocks + blockIdx.x] = hist[d];
 }
 
-// Stable scatter of one digit pass.  offsets is the exclusive scan of counts.
-// The block's keys are first placed in LDS in digit order (stable), then
-// written out so that consecutive lanes write consecutive positions of each
-// digit's run.  KOut == uint64_t with K == uint32_t composes the output key as
+// Exclusive scan of each digit's block counts in place, one workgroup per
+// digit (counts[d * nb + b] becomes the count of digit d in the blocks before
+// b); dtot[d] receives the digit's total.  The scatter adds the digits'
+// exclusive prefix: together that is the exclusive scan of the digit-major
+// counts.  The launch also zeroes zero[0, nzero) (the per-tile counters of
+// the tile sort's last pass), since it runs right before that pass.
+__global__ void __launch_bounds__(kScanThreads) digit_scan_kernel(uint32_t* __restrict__ counts, uint32_t nb,
+                                                                 uint32_t* __restrict__ dtot, uint32_t* __restrict__ zero,
+                                                                 uint32_t nzero) {
+  uint32_t* c = counts + (size_t)blockIdx.x * nb;
+  const uint32_t per = (nb + kScanThreads - 1) / kScanThreads;
+  const uint32_t lo = threadIdx.x * per, hi = min(lo + per, nb);
+  uint64_t s = 0;
+  for (uint32_t i = lo; i < hi; i++) s += c[i];
+  uint64_t total;
+  uint64_t run = block_exclusive_scan_u64(s, &total);
+  for (uint32_t i = lo; i < hi; i++) {
+    const uint32_t v = c[i];
+    c[i] = (uint32_t)run;
+    run += v;
+  }
+  if (threadIdx.x == 0) dtot[blockIdx.x] = (uint32_t)total;
+  for (uint32_t i = blockIdx.x * kScanThreads + threadIdx.x; i < nzero; i += gridDim.x * kScanThreads) zero[i] = 0u;
+}
+
+// Stable scatter of one digit pass.  offsets[d * nb + b] is the count of
+// digit d in the blocks before b and dtot[d] the digit's total.  The block's
+// keys are first placed in LDS in digit order (stable), then written out so
+// that consecutive lanes write consecutive positions of each digit's run.
+// KOut == uint64_t with K == uint32_t composes the output key as
 // (key << 32) | low_bits[val] (the tile/depth key of the binning stage).
+// With tile_counts (the last pass of the tile sort, where a block's LDS copy
+// is sorted on the whole key), every run of equal keys in that copy adds its
+// length to tile_counts[2 * key + 1] (the .y of the key's uint2 range); keys
+// at or past ntiles are not counted.
 template <typename K, typename KOut>
 __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __restrict__ keys_in,
                                                                     const uint32_t* __restrict__ vals_in,
                                                                     KOut* __restrict__ keys_out,
                                                                     uint32_t* __restrict__ vals_out, int64_t n, int shift,
                                                                     const uint32_t* __restrict__ offsets, uint32_t nblocks,
-                                                                    const uint32_t* __restrict__ low_bits) {
+                                                                    const uint32_t* __restrict__ dtot,
+                                                                    const uint32_t* __restrict__ low_bits,
+                                                                    uint32_t* __restrict__ tile_counts, uint32_t ntiles) {
   static_assert(kRadix == kSortThreads, "one digit per thread in the block scan");
   __shared__ uint32_t hist[kSortWaves][kRadix];
   __shared__ uint32_t gbase[kRadix];  // global start of the digit's run, minus its local start
@@ -302,7 +298,13 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
     }
   }
   for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&hist[0][0])[i] = 0;
-  for (int d = threadIdx.x; d < kRadix; d += kSortThreads) gbase[d] = offsets[(size_t)d * nblocks + blockIdx.x];
+  {
+    // thread d: the digit's global start, the exclusive prefix of the totals
+    const int d = threadIdx.x;
+    uint64_t all;
+    const uint64_t dstart = block_exclusive_scan_u64(dtot[d], &all);
+    gbase[d] = (uint32_t)dstart + offsets[(size_t)d * nblocks + blockIdx.x];
+  }
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < kSortRounds; r++) {
@@ -358,6 +360,44 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
     else
       keys_out[pos] = k;
     vals_out[pos] = v;
+    if (tile_counts != nullptr && (uint64_t)k < ntiles) {
+      // the run [a, b) of key k adds -a at its first element, b at its last
+      uint32_t* c = tile_counts + 2u * (uint32_t)k + 1u;
+      if (j == 0 || skey[j - 1] != k) atomicSub(c, (uint32_t)j);
+      if (j == count - 1 || skey[j + 1] != k) atomicAdd(c, (uint32_t)(j + 1));
+    }
+  }
+}
+
+// Tile ranges from the per-tile pair counts of the sorted pairs, one
+// workgroup: ranges[t] = [start, start + count) with start the exclusive scan
+// of the counts, and (0, 0) for a tile without pairs, as identifyTileRanges
+// leaves it after the memset.  The counts are read from ranges[t].y (the tile
+// sort's last pass accumulates them there, x zero) and overwritten in place.
+constexpr int kRangeThreads = 1024;
+
+__global__ void __launch_bounds__(kRangeThreads) ranges_from_counts_kernel(uint2* __restrict__ ranges,
+                                                                          uint32_t ntiles) {
+  __shared__ uint32_t wsum[kRangeThreads / kWave];
+  const uint32_t per = (ntiles + kRangeThreads - 1) / kRangeThreads;
+  const uint32_t lo = threadIdx.x * per, hi = min(lo + per, ntiles);
+  uint32_t s = 0;
+  for (uint32_t t = lo; t < hi; t++) s += ranges[t].y;
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  uint32_t inc = s;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t o = __shfl_up(inc, d, kWave);
+    if (lane >= d) inc += o;
+  }
+  if (lane == kWave - 1) wsum[wid] = inc;
+  __syncthreads();
+  uint32_t run = inc - s;
+  for (int w = 0; w < wid; w++) run += wsum[w];
+  for (uint32_t t = lo; t < hi; t++) {
+    const uint32_t c = ranges[t].y;
+    ranges[t] = c != 0u ? make_uint2(run, run + c) : make_uint2(0u, 0u);
+    run += c;
   }
 }
 
@@ -370,17 +410,20 @@ template <typename K, typename KOut>
 static size_t sort_ws_bytes_t(int64_t n) {
   constexpr int sets = sizeof(KOut) == sizeof(K) ? 1 : 2;
   const int64_t ncounts = (int64_t)kRadix * sort_blocks(n);
-  return sets * (align256((size_t)n * sizeof(K)) + align256((size_t)n * 4)) + 2 * align256((size_t)ncounts * 4) +
-         align256(scan_ws_bytes(ncounts));
+  return sets * (align256((size_t)n * sizeof(K)) + align256((size_t)n * 4)) + align256((size_t)ncounts * 4) +
+         align256((size_t)kRadix * 4);
 }
 
 // Stable LSD sort of (keys_in, vals_in) on key bits [0, end_bit) into
 // (keys_out, vals_out).  The inputs are never written.  vals_in == nullptr
 // stands for vals_in[i] = i.  With KOut wider than K the last pass writes
-// (key << 32) | low_bits[val].
+// (key << 32) | low_bits[val].  With tile_counts (ntiles uint2 ranges), the
+// last pass also counts the keys per value (the pairs per tile) into the .y
+// words, after zeroing all 2 * ntiles words.
 template <typename K, typename KOut>
 static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, KOut* keys_out, uint32_t* vals_out, int64_t n,
-                            int end_bit, const uint32_t* low_bits, void* ws, hipStream_t s) {
+                            int end_bit, const uint32_t* low_bits, void* ws, hipStream_t s,
+                            uint32_t* tile_counts = nullptr, uint32_t ntiles = 0) {
   if (n <= 0) return hipSuccess;
   constexpr bool kSame = sizeof(KOut) == sizeof(K);
   const int64_t nb = sort_blocks(n);
@@ -396,9 +439,7 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, KOut* key
   }
   uint32_t* counts = reinterpret_cast<uint32_t*>(w);
   w += align256((size_t)ncounts * 4);
-  uint32_t* offs = reinterpret_cast<uint32_t*>(w);
-  w += align256((size_t)ncounts * 4);
-  void* scan_ws = w;
+  uint32_t* dtot = reinterpret_cast<uint32_t*>(w);
 
   int passes = (end_bit + kRadixBits - 1) / kRadixBits;
   if (passes < 1) passes = 1;
@@ -409,8 +450,9 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, KOut* key
     const int shift = pass * kRadixBits;
     hipLaunchKernelGGL(radix_hist_kernel<K>, dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, n, shift, counts,
                        (uint32_t)nb);
-    hipError_t e = scan_impl(counts, offs, ncounts, scan_ws, true, s);
-    if (e != hipSuccess) return e;
+    uint32_t* tc = last ? tile_counts : nullptr;
+    hipLaunchKernelGGL(digit_scan_kernel, dim3(kRadix), dim3(kScanThreads), 0, s, counts, (uint32_t)nb, dtot, tc,
+                       tc ? 2u * ntiles : 0u);
     K* dk;
     uint32_t* dv;
     if constexpr (kSame) {
@@ -424,10 +466,10 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, KOut* key
     }
     if (!kSame && last)
       hipLaunchKernelGGL((radix_scatter_kernel<K, KOut>), dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, sv, keys_out,
-                         vals_out, n, shift, offs, (uint32_t)nb, low_bits);
+                         vals_out, n, shift, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
     else
       hipLaunchKernelGGL((radix_scatter_kernel<K, K>), dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, sv, dk, dv, n,
-                         shift, offs, (uint32_t)nb, low_bits);
+                         shift, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
     sk = dk;
     sv = dv;
   }
@@ -560,9 +602,20 @@ hipError_t launch_duplicate_ordered(int P, const uint32_t* order, const uint32_t
 size_t tile_sort_ws_bytes(int64_t n) { return sort_ws_bytes_t<uint32_t, uint64_t>(n); }
 
 hipError_t launch_sort_tiles(const uint32_t* tile_keys, const uint32_t* ids, uint64_t* keys_out, uint32_t* vals_out,
-                             int64_t n, int tile_bits, const float* depth, void* ws, hipStream_t s) {
+                             int64_t n, int tile_bits, const float* depth, uint32_t* ranges, uint32_t ntiles, void* ws,
+                             hipStream_t s) {
   return sort_impl<uint32_t, uint64_t>(tile_keys, ids, keys_out, vals_out, n, tile_bits,
-                                       reinterpret_cast<const uint32_t*>(depth), ws, s);
+                                       reinterpret_cast<const uint32_t*>(depth), ws, s, ranges, ntiles);
+}
+
+// identifyTileRanges: with pairs, turns the per-tile counts that
+// launch_sort_tiles left in ranges into [start, end) ranges; without pairs,
+// zeroes the ranges.
+hipError_t launch_tile_ranges(uint32_t* ranges, int64_t n, uint32_t ntiles, hipStream_t s) {
+  if (n <= 0 || ntiles == 0) return launch_fill_u32(ranges, 0u, 2 * (int64_t)ntiles, s);
+  hipLaunchKernelGGL(ranges_from_counts_kernel, dim3(1), dim3(kRangeThreads), 0, s, reinterpret_cast<uint2*>(ranges),
+                     ntiles);
+  return hipGetLastError();
 }
 
 }  // namespace nest
