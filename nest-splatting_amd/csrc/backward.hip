@@ -32,10 +32,10 @@
 //    and added with one atomic per wave instead of one per pixel.
 // Table gradients are hardware float atomics (global_atomic_add_f32) at
 // every corner, as in the reference, merged per cell across the wave first.
-// Their cost is one request per (instruction, 64-byte segment): measured on
-// MI355X, 16 lanes adding to one segment run 16x the dword rate of 16 lanes
-// adding to 16 segments, so every scatter below gathers an entry's channels
-// into one instruction.
+// Their cost is one request per (instruction, 64-byte segment) and, on
+// MI355X, a fixed share of the texture path per instruction however few
+// lanes it carries, so the scatter below stages the cells' sums in LDS and
+// adds them 64 consecutive values per instruction (whole entries).
 #include <hip/hip_fp16.h>
 
 #include "hashgrid.h"
@@ -100,125 +100,152 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ void atomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
 
-// 4x4 transpose across each quad of lanes: on return, a[q] of lane 4m + i
-// holds a[i] of lane 4m + q.  Two exchange steps, lane bit 0 then bit 1: a
-// lane whose bit is clear trades its a[r + s] for its partner's a[r] (s the
-// bit's weight), one with the bit set its a[r] for the partner's a[r + s].
-__device__ __forceinline__ void quad_transpose(float a[4]) {
-  const bool up0 = (threadIdx.x & 1u) != 0u, up1 = (threadIdx.x & 2u) != 0u;
-#pragma unroll
-  for (int r = 0; r < 4; r += 2) {
-    const float got = dpp_f<kDppQuadXor1>(up0 ? a[r] : a[r + 1]);
-    if (up0) a[r] = got; else a[r + 1] = got;
-  }
-#pragma unroll
-  for (int r = 0; r < 2; r++) {
-    const float got = dpp_f<kDppQuadXor2>(up1 ? a[r] : a[r + 2]);
-    if (up1) a[r] = got; else a[r + 2] = got;
+// Staging area of the table-gradient atomics: 256 dwords of LDS per wave,
+// kSlots slots of NV = 8F summed values (a cell's corner values, corner-major)
+// followed by the slots' 8 entry indices.  A flush adds nb slots with packed
+// atomics: lane l of instruction r adds value 64r + l, so an instruction
+// carries 64 consecutive values (for F = 4 sixteen whole 16-byte entries).
+template <int F>
+struct StageLayout {
+  static constexpr int NV = 8 * F;
+  static constexpr uint32_t kSlots = 256 / (NV + 8);
+  static constexpr uint32_t kIdx = kSlots * NV;  // first index dword
+};
+
+template <int F>
+__device__ __forceinline__ void stage_flush(const uint32_t* st, uint32_t nb, float* dl) {
+  constexpr int NV = 8 * F;
+  constexpr uint32_t kIdx = StageLayout<F>::kIdx;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t nval = nb * NV;
+  for (uint32_t f0 = 0; f0 < nval; f0 += 64u) {
+    const uint32_t f = f0 + lane;
+    if (f < nval) {
+      const float val = __uint_as_float(st[f]);
+      const uint32_t h = f / NV, v = f % NV;
+      const uint32_t e = st[kIdx + h * 8u + v / F];
+      if (val != 0.0f) atomic_add(dl + (size_t)e * F + (v % F), val);
+    }
   }
 }
 
-// x of lane 4m + q in every lane of quad m (q a compile-time constant after
-// unrolling).
-__device__ __forceinline__ uint32_t quad_bcast(int q, uint32_t x) {
-  switch (q) {
-    case 0: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x00, 0xF, 0xF, false);
-    case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x55, 0xF, 0xF, false);
-    case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xAA, 0xF, 0xF, false);
-    default: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xFF, 0xF, 0xF, false);
-  }
-}
+constexpr uint32_t kSmallCell = 8;  // cells of up to this many lanes are summed by pointer jumping
 
 // Table gradient of one level for the wave (uniform control flow): lanes
 // whose hits fall in the same cell (same g) share all eight corner entries.
 // The cells are taken one at a time (the lowest remaining lane's cell and
-// every lane sharing it); a cell of two or more lanes has its 8*F values
-// summed over its lanes with a recursive-halving reduce-scatter (after it,
-// lane l holds the sum of value l / (64 / 8F)) and added with one atomic per
-// entry and channel; lanes alone in their cell add their values at the end,
-// all at once, the quads of lanes taking turns so that an instruction adds
-// whole entries.  At coarse levels a wave's 64 hits (neighbouring pixels and
-// splats adjacent in depth) are a few cells, which is where the per-lane
-// atomics of the reference pile onto the same addresses; at fine levels a
-// cell holds a few lanes.
+// every lane sharing it).  A cell of more than kSmallCell lanes has its 8F
+// values summed over its lanes with recursive-halving reduce-scatters, 16
+// values at a time (after one, lane l holds the sum of value l / 4 of the
+// chunk), written straight to a staging slot; the smaller cells are summed all
+// at once after the search by pointer jumping along each cell's lanes, into
+// the cell's lowest lane, which then writes a slot as a lane alone in its cell
+// does.  Full sets of slots are added with packed atomics.  At coarse levels a wave's 64 hits
+// (neighbouring pixels and splats adjacent in depth) are a few cells, which is
+// where the per-lane atomics of the reference pile onto the same addresses; at
+// fine levels a cell holds a few lanes.
 template <int F>
-__device__ __forceinline__ void scatter_level(bool on, const uint32_t gc[3], const uint32_t idx[8], const float* cv,
-                                              float* dl) {
+__device__ __forceinline__ void scatter_level(bool on, const uint32_t gc[3], const uint32_t idx[8], float* cv,
+                                              float* dl, uint32_t* st) {
   constexpr int NV = 8 * F;
-  constexpr int kRep = 64 / NV;  // lanes holding each value after the halving steps
+  constexpr uint32_t kSlots = StageLayout<F>::kSlots;
+  constexpr uint32_t kIdx = StageLayout<F>::kIdx;
   const uint32_t lane = threadIdx.x & 63u;
   uint64_t rem = __ballot(on);
-  uint64_t single = 0ull;
+  uint64_t issue = 0ull;  // lanes holding a small cell's sum (or alone in their cell)
+  // next lane of the lane's small cell as a byte address for ds_bpermute;
+  // bit 31 set: the lane is the last of its cell (or in no small cell)
+  uint32_t succ = 0x80000000u | (lane << 2);
+  uint32_t small_max = 1u;
+  uint32_t nb = 0u;  // staging slots in use
   while (rem != 0ull) {
     const int ld = __ffsll((long long)rem) - 1;
     const uint32_t k0 = __builtin_amdgcn_readlane(gc[0], ld), k1 = __builtin_amdgcn_readlane(gc[1], ld),
                    k2 = __builtin_amdgcn_readlane(gc[2], ld);
-    const uint64_t m = __ballot(on && gc[0] == k0 && gc[1] == k1 && gc[2] == k2) & rem;
+    const uint64_t m = __ballot(gc[0] == k0) & __ballot(gc[1] == k1) & __ballot(gc[2] == k2) & rem;
     rem &= ~m;
-    if ((m & (m - 1ull)) == 0ull) {
-      single |= m;
+    const uint32_t n = (uint32_t)__popcll(m);
+    if (n <= kSmallCell) {
+      issue |= m & (~m + 1ull);
+      if (n > 1u) {
+        const uint64_t after = m & ~((2ull << lane) - 1ull);
+        if (((m >> lane) & 1ull) != 0ull && after != 0ull) succ = (uint32_t)(__ffsll((long long)after) - 1) << 2;
+        small_max = n > small_max ? n : small_max;
+      }
       continue;
     }
     const bool mem = ((m >> lane) & 1ull) != 0ull;
-    float v[NV];
-#pragma unroll
-    for (int i = 0; i < NV; i++) v[i] = mem ? cv[i] : 0.0f;
-    int vi = 0;
-#pragma unroll
-    for (int st = 0; (NV >> (st + 1)) >= 1; st++) {
-      const int n = NV >> (st + 1);
-      const int bit = 5 - st;
-#pragma unroll
-      for (int i = 0; i < n; i++) v[i] = halve(bit, v[i], v[i + n]);
-      if (((lane >> bit) & 1u) != 0u) vi += n;
+    if (nb == kSlots) {
+      stage_flush<F>(st, nb, dl);
+      nb = 0u;
     }
-    // lanes differing only in the bits below hold the same value index
+    // reduce-scatter in chunks of kCh values (fewer live registers)
+    constexpr int kCh = NV < 16 ? NV : 16;
+    constexpr int kRepC = 64 / kCh;
 #pragma unroll
-    for (int bit = 0; (1 << bit) < kRep; bit++) v[0] = halve(bit, v[0], v[0]);
-    if ((lane % kRep) == 0u && v[0] != 0.0f) {
-      const int k = vi / F, f = vi % F;
-      uint32_t e = __builtin_amdgcn_readlane(idx[0], ld);
+    for (int c = 0; c < NV / kCh; c++) {
+      float v[kCh];
 #pragma unroll
-      for (int kk = 1; kk < 8; kk++) {
-        const uint32_t ek = __builtin_amdgcn_readlane(idx[kk], ld);
-        e = (k == kk) ? ek : e;
+      for (int i = 0; i < kCh; i++) v[i] = mem ? cv[c * kCh + i] : 0.0f;
+      int vi = 0;
+#pragma unroll
+      for (int s = 0; (kCh >> (s + 1)) >= 1; s++) {
+        const int h = kCh >> (s + 1);
+        const int bit = 5 - s;
+#pragma unroll
+        for (int i = 0; i < h; i++) v[i] = halve(bit, v[i], v[i + h]);
+        if (((lane >> bit) & 1u) != 0u) vi += h;
       }
-      atomic_add(dl + (size_t)e * F + f, v[0]);
+      // lanes differing only in the bits below hold the same value index
+#pragma unroll
+      for (int bit = 0; (1 << bit) < kRepC; bit++) v[0] = halve(bit, v[0], v[0]);
+      if ((lane % kRepC) == 0u) st[nb * NV + (uint32_t)(c * kCh + vi)] = __float_as_uint(v[0]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    uint32_t e = __builtin_amdgcn_readlane(idx[0], ld);
+#pragma unroll
+    for (int kk = 1; kk < 8; kk++) {
+      const uint32_t ek = __builtin_amdgcn_readlane(idx[kk], ld);
+      e = (lane == (uint32_t)kk) ? ek : e;
+    }
+    if (lane < 8u) st[kIdx + nb * 8u + lane] = e;
+    nb++;
   }
-  if (single == 0ull) return;
-  const bool me = ((single >> lane) & 1ull) != 0ull;
-  if constexpr (F == 1) {
-    if (me) {
+  // small cells: pointer jumping, after which a cell's lowest lane holds the
+  // sum over the cell's lanes
+  for (uint32_t span = 1u; span < small_max; span <<= 1) {
+    const bool has = (succ & 0x80000000u) == 0u;
+    const int addr = (int)(succ & 0xFFu);
 #pragma unroll
-      for (int k = 0; k < 8; k++)
-        if (cv[k] != 0.0f) atomic_add(dl + idx[k], cv[k]);
+    for (int i = 0; i < NV; i++) {
+      const float got = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(cv[i])));
+      if (has) cv[i] += got;
+      if ((i & 7) == 7) __builtin_amdgcn_sched_barrier(0);
     }
-  } else {
-    // Each quad of lanes takes its four hits in turn, lane p of the quad
-    // adding value 4g + p of the hit: an instruction carries 16 hits' runs of
-    // four consecutive floats (one 16-byte segment each), where a lane per
-    // hit would send each float as its own request.
-    const uint32_t p = lane & 3u;
-#pragma unroll
-    for (int g = 0; g < 2 * F; g++) {
-      float t[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) t[i] = me ? cv[4 * g + i] : 0.0f;
-      quad_transpose(t);  // t[q]: value 4g + p of the quad's hit q
-      const int k0 = (4 * g) / F;  // corner of the quad's first value
-      const uint32_t f = (uint32_t)((4 * g) % F) + (F == 2 ? (p & 1u) : p);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        uint32_t e = quad_bcast(q, idx[k0]);
-        if constexpr (F == 2) {
-          const uint32_t e1 = quad_bcast(q, idx[k0 + 1]);  // values 2 and 3: the next corner
-          e = (p >> 1) != 0u ? e1 : e;
-        }
-        if (t[q] != 0.0f) atomic_add(dl + (size_t)e * F + f, t[q]);
-      }
-    }
+    if (span * 2u < small_max) succ = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)succ);
   }
+  const uint32_t n_iss = (uint32_t)__popcll(issue);
+  const uint32_t rank = (uint32_t)__popcll(issue & ((1ull << lane) - 1ull));
+  const bool me = ((issue >> lane) & 1ull) != 0ull;
+  for (uint32_t done = 0; done < n_iss;) {
+    if (nb == kSlots) {
+      stage_flush<F>(st, nb, dl);
+      nb = 0u;
+    }
+    const uint32_t take = min(kSlots - nb, n_iss - done);
+    if (me && rank >= done && rank < done + take) {
+      const uint32_t h = nb + rank - done;
+      float4* sv = reinterpret_cast<float4*>(st + h * NV);
+#pragma unroll
+      for (int i = 0; i < NV / 4; i++) sv[i] = make_float4(cv[4 * i], cv[4 * i + 1], cv[4 * i + 2], cv[4 * i + 3]);
+      uint4* si = reinterpret_cast<uint4*>(st + kIdx + h * 8u);
+      si[0] = make_uint4(idx[0], idx[1], idx[2], idx[3]);
+      si[1] = make_uint4(idx[4], idx[5], idx[6], idx[7]);
+    }
+    nb += take;
+    done += take;
+  }
+  if (nb > 0u) stage_flush<F>(st, nb, dl);
 }
 
 // query_feature<true> for the wave's hits at grid coordinates u (lanes with
@@ -229,8 +256,8 @@ __device__ __forceinline__ void scatter_level(bool on, const uint32_t gc[3], con
 template <int F>
 __device__ __forceinline__ void hash_backward_wave(const GridParams& g, nest_i32x4 rsrc, const float u[3],
                                                    float grad_scale, uint32_t lane_levels, float w,
-                                                   const float* dpix, size_t HW, float* dtable, float& dot,
-                                                   float dxyz[3]) {
+                                                   const float* dpix, size_t HW, float* dtable, uint32_t* st,
+                                                   float& dot, float dxyz[3]) {
   dot = 0.0f;
   dxyz[0] = dxyz[1] = dxyz[2] = 0.0f;
   const LevelTable& lv = g.lv;
@@ -308,7 +335,7 @@ __device__ __forceinline__ void hash_backward_wave(const GridParams& g, nest_i32
         for (int f = 0; f < F; f++) dxyz[gd] += gf[f] * rg[f];
       }
     }
-    scatter_level<F>(on, gc, cn.idx, cv, dtable + (size_t)lv.base[l] * F);
+    scatter_level<F>(on, gc, cn.idx, cv, dtable + (size_t)lv.base[l] * F, st);
   }
 }
 
@@ -799,7 +826,10 @@ render_backward_kernel(const RenderBwdParams p) {
           dp = p.dL_dpix + ((size_t)(ty * kTile + (t >> 4)) * p.W + tx * kTile + (t & 15u)) + grid_ch;
         }
         float dot, dxyz[3];
-        hash_backward_wave<F>(g, rsrc, u, gsc, lev, w, dp, HW, p.dtable, dot, dxyz);
+        // the chunk's queue entries (read above, rewritten below) stage the
+        // table-gradient atomics meanwhile
+        hash_backward_wave<F>(g, rsrc, u, gsc, lev, w, dp, HW, p.dtable, reinterpret_cast<uint32_t*>(&hq[wid][r0]),
+                              dot, dxyz);
         if (on) hq[wid][e] = make_float4(dot, dxyz[0], dxyz[1], dxyz[2]);
       }
       __builtin_amdgcn_wave_barrier();
