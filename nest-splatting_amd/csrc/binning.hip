@@ -11,12 +11,13 @@
 // pairs (the last section below explains why the order is the same).
 //
 // Sort design (gfx950, 64-lane waves): reduce-then-scan LSD radix with 8-bit
-// digits.  Each 256-thread block owns 4096 keys; a wave ranks its 1024 keys in
-// 16 rounds of 64 with eight ballots per round (multi-split by digit), keeping
-// the per-wave digit counters in LDS.  That gives a stable rank without LDS
-// atomics, and the (digit, block) offsets come from one device-wide exclusive
-// scan of the block histograms.  No kernel waits on another block, so there is
-// no inter-block spin.
+// digits, three launches per pass.  Each 256-thread block owns 4096 keys
+// (1024 for sorts of up to 4M keys, so that the splats' depth sort fills the
+// chip); the histogram counts them with LDS atomics; one workgroup per digit
+// scans that digit's block counts; the scatter's waves rank their keys in
+// rounds of 64 with eight ballots per round (multi-split by digit), keeping
+// the per-wave digit counters in LDS, which gives a stable rank without LDS
+// atomics.  No kernel waits on another block, so there is no inter-block spin.
 #include "nest_internal.h"
 #include "nest_math.h"
 
@@ -185,9 +186,10 @@ hipError_t launch_fill_u32(uint32_t* dst, uint32_t value, int64_t n, hipStream_t
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
 constexpr int kSortThreads = 256;
-constexpr int kSortRounds = 16;                          // rounds of 64 keys per wave
+constexpr int kSortRounds = 16;                          // rounds of 64 keys per wave (large sorts)
+constexpr int kSortRoundsSmall = 4;                      // up to kSmallSort keys: 1024 keys per block
+constexpr int64_t kSmallSort = 1 << 22;
 constexpr int kSortWaves = kSortThreads / kWave;         // 4
-constexpr int kSortTile = kSortThreads * kSortRounds;    // 4096 keys per block
 
 // Lanes of the calling wave whose 8-bit digit equals d, restricted to 'valid'.
 __device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t valid) {
@@ -208,24 +210,26 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 // Per-block digit histogram, written digit-major: counts[d * nblocks + b].
 // The block's keys are counted with LDS atomics (a count does not depend on
 // the order in which they land).
-template <typename K>
+template <typename K, int R>
 __global__ void __launch_bounds__(kSortThreads) radix_hist_kernel(const K* __restrict__ keys, int64_t n, int shift,
-                                                                 uint32_t* __restrict__ counts, uint32_t nblocks) {
+                                                                 int nbits, uint32_t* __restrict__ counts,
+                                                                 uint32_t nblocks) {
+  const uint32_t dmask = (1u << nbits) - 1u;
   __shared__ uint32_t hist[kRadix];
   for (int i = threadIdx.x; i < kRadix; i += kSortThreads) hist[i] = 0;
-  const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  const int64_t base = (int64_t)blockIdx.x * (kSortThreads * R);
   // all of the thread's keys in flight at once
-  K key[kSortRounds];
+  K key[R];
 #pragma unroll
-  for (int r = 0; r < kSortRounds; r++) {
+  for (int r = 0; r < R; r++) {
     const int64_t i = base + r * kSortThreads + threadIdx.x;
     key[r] = i < n ? keys[i] : (K)0;
   }
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kSortRounds; r++) {
+  for (int r = 0; r < R; r++) {
     const int64_t i = base + r * kSortThreads + threadIdx.x;
-    if (i < n) atomicAdd(&hist[(uint32_t)(key[r] >> shift) & (kRadix - 1)], 1u);
+    if (i < n) atomicAdd(&hist[(uint32_t)(key[r] >> shift) & dmask], 1u);
   }
   __syncthreads();
   for (int d = threadIdx.x; d < kRadix; d += kSortThreads) counts[(size_t)d * nblocks + blockIdx.x] = hist[d];
@@ -266,11 +270,12 @@ __global__ void __launch_bounds__(kScanThreads) digit_scan_kernel(uint32_t* __re
 // is sorted on the whole key), every run of equal keys in that copy adds its
 // length to tile_counts[2 * key + 1] (the .y of the key's uint2 range); keys
 // at or past ntiles are not counted.
-template <typename K, typename KOut>
+template <typename K, typename KOut, int R>
 __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __restrict__ keys_in,
                                                                     const uint32_t* __restrict__ vals_in,
                                                                     KOut* __restrict__ keys_out,
                                                                     uint32_t* __restrict__ vals_out, int64_t n, int shift,
+                                                                    int nbits,
                                                                     const uint32_t* __restrict__ offsets, uint32_t nblocks,
                                                                     const uint32_t* __restrict__ dtot,
                                                                     const uint32_t* __restrict__ low_bits,
@@ -278,16 +283,17 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
   static_assert(kRadix == kSortThreads, "one digit per thread in the block scan");
   __shared__ uint32_t hist[kSortWaves][kRadix];
   __shared__ uint32_t gbase[kRadix];  // global start of the digit's run, minus its local start
-  __shared__ K skey[kSortTile];
-  __shared__ uint32_t sval[kSortTile];
+  __shared__ K skey[kSortThreads * R];
+  __shared__ uint32_t sval[kSortThreads * R];
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  const uint32_t dmask = (1u << nbits) - 1u;
   // the keys and values are in flight together with the digit offsets
-  const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)wid * (kWave * kSortRounds);
-  K key[kSortRounds];
-  uint32_t val[kSortRounds];
-  uint32_t rank[kSortRounds];
+  const int64_t base = (int64_t)blockIdx.x * (kSortThreads * R) + (int64_t)wid * (kWave * R);
+  K key[R];
+  uint32_t val[R];
+  uint32_t rank[R];
 #pragma unroll
-  for (int r = 0; r < kSortRounds; r++) {
+  for (int r = 0; r < R; r++) {
     const int64_t i = base + r * kWave + lane;
     if (i < n) {
       key[r] = keys_in[i];
@@ -307,10 +313,10 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
   }
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kSortRounds; r++) {
+  for (int r = 0; r < R; r++) {
     const int64_t i = base + r * kWave + lane;
     const bool ok = i < n;
-    const uint32_t d = (uint32_t)(key[r] >> shift) & (kRadix - 1);
+    const uint32_t d = (uint32_t)(key[r] >> shift) & dmask;
     const uint64_t valid = __ballot(ok);
     const uint64_t peers = match_digit(d, valid);
     uint32_t before = 0;
@@ -339,22 +345,22 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
   }
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kSortRounds; r++) {
+  for (int r = 0; r < R; r++) {
     const int64_t i = base + r * kWave + lane;
     if (i < n) {
-      const uint32_t d = (uint32_t)(key[r] >> shift) & (kRadix - 1);
+      const uint32_t d = (uint32_t)(key[r] >> shift) & dmask;
       const uint32_t lp = hist[wid][d] + rank[r];
       skey[lp] = key[r];
       sval[lp] = val[r];
     }
   }
   __syncthreads();
-  const int64_t left = n - (int64_t)blockIdx.x * kSortTile;
-  const int count = left < kSortTile ? (int)left : kSortTile;
+  const int64_t left = n - (int64_t)blockIdx.x * (kSortThreads * R);
+  const int count = left < kSortThreads * R ? (int)left : kSortThreads * R;
   for (int j = threadIdx.x; j < count; j += kSortThreads) {
     const K k = skey[j];
     const uint32_t v = sval[j];
-    const uint32_t pos = gbase[(uint32_t)(k >> shift) & (kRadix - 1)] + (uint32_t)j;
+    const uint32_t pos = gbase[(uint32_t)(k >> shift) & dmask] + (uint32_t)j;
     if constexpr (sizeof(KOut) > sizeof(K))
       keys_out[pos] = ((KOut)k << 32) | (KOut)low_bits[v];
     else
@@ -401,7 +407,13 @@ __global__ void __launch_bounds__(kRangeThreads) ranges_from_counts_kernel(uint2
   }
 }
 
-static int64_t sort_blocks(int64_t n) { return (n + kSortTile - 1) / kSortTile; }
+// Keys per block: 1024 up to kSmallSort keys (more blocks to fill the chip for
+// the splats' depth sort), else 4096 (longer runs per digit in the output).
+static int sort_rounds(int64_t n) { return n <= kSmallSort ? kSortRoundsSmall : kSortRounds; }
+static int64_t sort_blocks(int64_t n) {
+  const int64_t tile = (int64_t)kSortThreads * sort_rounds(n);
+  return (n + tile - 1) / tile;
+}
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // Workspace: ping-pong keys/vals (two sets when the last pass widens the
@@ -427,6 +439,7 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, KOut* key
   if (n <= 0) return hipSuccess;
   constexpr bool kSame = sizeof(KOut) == sizeof(K);
   const int64_t nb = sort_blocks(n);
+  const bool small = sort_rounds(n) == kSortRoundsSmall;
   const int64_t ncounts = (int64_t)kRadix * nb;
   char* w = static_cast<char*>(ws);
   K* tk[2];
@@ -448,8 +461,14 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, KOut* key
   for (int pass = 0; pass < passes; pass++) {
     const bool last = pass == passes - 1;
     const int shift = pass * kRadixBits;
-    hipLaunchKernelGGL(radix_hist_kernel<K>, dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, n, shift, counts,
-                       (uint32_t)nb);
+    // bits of this pass's digit below end_bit (the sort ignores the bits above)
+    const int nbits = end_bit - shift < kRadixBits ? (end_bit - shift > 0 ? end_bit - shift : 1) : kRadixBits;
+    if (small)
+      hipLaunchKernelGGL((radix_hist_kernel<K, kSortRoundsSmall>), dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, n,
+                         shift, nbits, counts, (uint32_t)nb);
+    else
+      hipLaunchKernelGGL((radix_hist_kernel<K, kSortRounds>), dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, n,
+                         shift, nbits, counts, (uint32_t)nb);
     uint32_t* tc = last ? tile_counts : nullptr;
     hipLaunchKernelGGL(digit_scan_kernel, dim3(kRadix), dim3(kScanThreads), 0, s, counts, (uint32_t)nb, dtot, tc,
                        tc ? 2u * ntiles : 0u);
@@ -464,12 +483,21 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, KOut* key
       dk = tk[pass & 1];
       dv = tv[pass & 1];
     }
-    if (!kSame && last)
-      hipLaunchKernelGGL((radix_scatter_kernel<K, KOut>), dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, sv, keys_out,
-                         vals_out, n, shift, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
-    else
-      hipLaunchKernelGGL((radix_scatter_kernel<K, K>), dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk, sv, dk, dv, n,
-                         shift, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
+    if (!kSame && last) {
+      if (small)
+        hipLaunchKernelGGL((radix_scatter_kernel<K, KOut, kSortRoundsSmall>), dim3((unsigned)nb), dim3(kSortThreads), 0,
+                           s, sk, sv, keys_out, vals_out, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
+      else
+        hipLaunchKernelGGL((radix_scatter_kernel<K, KOut, kSortRounds>), dim3((unsigned)nb), dim3(kSortThreads), 0, s,
+                           sk, sv, keys_out, vals_out, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
+    } else {
+      if (small)
+        hipLaunchKernelGGL((radix_scatter_kernel<K, K, kSortRoundsSmall>), dim3((unsigned)nb), dim3(kSortThreads), 0, s,
+                           sk, sv, dk, dv, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
+      else
+        hipLaunchKernelGGL((radix_scatter_kernel<K, K, kSortRounds>), dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk,
+                           sv, dk, dv, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
+    }
     sk = dk;
     sv = dv;
   }

@@ -56,6 +56,32 @@ def test_sort_pairs_u64_is_stable_lexsort(n, end_bit, key_range):
     np.testing.assert_array_equal(v_in.cpu().numpy().view(np.uint32), vals)
 
 
+@pytest.mark.parametrize("n,end_bit", [(5000, 12), (70_000, 21), (5_000_000, 13)])
+def test_sort_pairs_u64_ignores_bits_past_end_bit(n, end_bit):
+    """cub's SortPairs orders on bits [0, end_bit) only: keys with higher bits
+    set keep those bits and their stable order among equal low bits."""
+    L = _L()
+    lib = L.lib()
+    rng = np.random.default_rng(7 * n + end_bit)
+    keys = rng.integers(0, 1 << 40, n, dtype=np.uint64)
+    vals = rng.permutation(n).astype(np.uint32)
+    print(f"[case] sort high bits n={n} end_bit={end_bit}", flush=True)
+    dev = torch.device("cuda:0")
+    k_in = torch.from_numpy(keys.view(np.int64)).to(dev)
+    v_in = torch.from_numpy(vals.view(np.int32)).to(dev)
+    k_out = torch.empty_like(k_in)
+    v_out = torch.empty_like(v_in)
+    ws_bytes = lib.nest_sort_workspace_size(n)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = ct.c_void_p(torch.cuda.current_stream().cuda_stream)
+    L.check(lib.nest_sort_pairs_u64(_ptr(k_in), _ptr(v_in), _ptr(k_out), _ptr(v_out), n, end_bit, _ptr(ws), ws_bytes,
+                                    stream), "sort")
+    torch.cuda.synchronize()
+    order = np.argsort(keys & np.uint64((1 << end_bit) - 1), kind="stable")
+    np.testing.assert_array_equal(k_out.cpu().numpy().view(np.uint64), keys[order])
+    np.testing.assert_array_equal(v_out.cpu().numpy().view(np.uint32), vals[order])
+
+
 @pytest.mark.parametrize("n", [1, 255, 4096, 4097, 1_000_000, 3_000_001])
 def test_inclusive_scan_u32(n):
     L = _L()
