@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 8
+#define NEST_ABI_VERSION 9
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -167,6 +167,14 @@ typedef struct nest_frame_outputs {
   float *out_color;
   float *out_others;
   int32_t *radii;
+  /* record_transmittance (DSR/rasterize_points.cu:169-171, CR/forward.cu:1961-1964):
+   * NULL for both = off.  Otherwise f32 [P] each, zeroed by nest_forward_render,
+   * then every hit that reaches the blend (every render mode but 13, whose
+   * hits leave the loop first) adds 1 to cover_pixels[splat] and the pixel's
+   * transmittance before the hit to trans_avg[splat] (a sum, as in the
+   * reference; the reference's [P, 1] tensors). */
+  float *cover_pixels;
+  float *trans_avg;
 } nest_frame_outputs;
 
 /* Optional per-stage device times.  When enabled, the forward calls record a

@@ -589,6 +589,16 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   rp.n_contrib = reinterpret_cast<uint32_t*>(im + io[NEST_IMG_N_CONTRIB]);
   rp.grid.lq = reinterpret_cast<LevelQuad*>(im + io[NEST_IMG_LEVELS]);
   rp.tile_order = reinterpret_cast<uint32_t*>(im + io[NEST_IMG_TILE_ORDER]);
+  if ((out->cover_pixels == nullptr) != (out->trans_avg == nullptr))
+    return fail(NEST_ERR_INVALID_ARGUMENT, "cover_pixels and trans_avg are set together or not at all");
+  if (out->cover_pixels && sp->P > 0) {
+    // record_transmittance: fresh zeros per frame, as the reference allocates them
+    hipError_t e = launch_fill_u32(reinterpret_cast<uint32_t*>(out->cover_pixels), 0u, sp->P, s);
+    if (e == hipSuccess) e = launch_fill_u32(reinterpret_cast<uint32_t*>(out->trans_avg), 0u, sp->P, s);
+    if (e != hipSuccess) return hip_fail(e, "record_transmittance fill");
+    rp.cover_pixels = out->cover_pixels;
+    rp.trans_avg = out->trans_avg;
+  }
   tm.begin(NEST_STAGE_RENDER);
   if ((rc = check_stage(launch_render(rp, s), "render", rs->debug, s))) return rc;
   tm.end();

@@ -115,6 +115,8 @@ struct RenderParams {
   float* out_others;
   float* final_T;
   uint32_t* n_contrib;
+  float* cover_pixels;        // record_transmittance: [P] hits per splat, or nullptr
+  float* trans_avg;           // [P] sum of the transmittance before each hit
   GridParams grid;
   // Per-splat features ahead of the grid's (render modes 4, 12, 13, 14):
   // channel c < pgd of a hit is row[c] (times the row's weight with

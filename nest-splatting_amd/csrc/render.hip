@@ -811,6 +811,84 @@ render_kernel(const RenderParams p) {
   O[pid + 13 * HW] = 0.0f;  // the third appearance channel only ever adds 0 * w
 }
 
+// record_transmittance (CR/forward.cu:1961-1964), for training frames that
+// ask for it: for every hit that reaches the blend, the reference adds 1 and
+// the pixel's transmittance before the hit to the splat's two counters with
+// per-pixel atomics.  Which hits reach the blend, and the transmittance they
+// see, depend only on the splats' geometry and opacity (the same test as the
+// render kernel's, every render mode but 13, whose hits leave the hit loop
+// before the record, :1090), so a second pass over the tile's splats
+// recomputes them without any feature work and leaves the render kernel's
+// loop untouched.  The wave's lanes visit one splat together: their hits are
+// summed across the wave and added with one atomic per counter (the same sums
+// in another order; the counts are exact).
+__global__ void __launch_bounds__(kRenderThreads) record_transmittance_kernel(const RenderParams p) {
+  __shared__ float4 sgeo[4][kBatch];  // record chunks 0-2 (transform, xy, opacity) and 7 (acceptance bbox)
+  __shared__ float2 scut[kBatch];     // chunk 6: rho cut (x) and splat id bits (y)
+  const uint32_t tile = blockIdx.x;
+  const uint32_t tx = tile % p.gx, ty = tile / p.gx;
+  const uint32_t px = tx * kTile + (threadIdx.x & 15u);
+  const uint32_t py = ty * kTile + (threadIdx.x >> 4);
+  const bool inside = px < (uint32_t)p.W && py < (uint32_t)p.H;
+  const float pxf = (float)px, pyf = (float)py;
+  const uint32_t wid = threadIdx.x / kWaveLanes, lane = threadIdx.x & (kWaveLanes - 1);
+  const float wx0 = (float)(tx * kTile), wx1 = wx0 + 15.0f;
+  const float wy0 = (float)(ty * kTile + 4u * wid), wy1 = wy0 + 3.0f;
+  const uint2 range = reinterpret_cast<const uint2*>(p.ranges)[tile];
+  bool done = !inside;
+  float T = 1.0f;
+  uint32_t render_number = 0;
+  for (uint32_t start = range.x; start < range.y; start += kBatch) {
+    if (__syncthreads_count(done) == kRenderThreads) break;
+    const uint32_t e = start + threadIdx.x;
+    if (e < range.y) {
+      const uint32_t id = p.point_list[e];
+      const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id;
+      sgeo[0][threadIdx.x] = rec[0];
+      sgeo[1][threadIdx.x] = rec[1];
+      sgeo[2][threadIdx.x] = rec[2];
+      sgeo[3][threadIdx.x] = rec[7];
+      scut[threadIdx.x] = make_float2(rec[6].y, __uint_as_float(id));
+    }
+    __syncthreads();
+    const uint32_t n = min((uint32_t)kBatch, range.y - start);
+    for (uint32_t j = 0; j < n; j++) {
+      bool hit_blend = false;
+      float t_before = 0.0f;
+      if (!done) {
+        do {
+          const float4 bb = sgeo[3][j];
+          if (bb.y < wx0 || bb.x > wx1 || bb.w < wy0 || bb.z > wy1) break;
+          SplatHit hit;
+          if (!splat_hit(sgeo[0][j], sgeo[1][j], sgeo[2][j], scut[j].x, pxf, pyf, p.beta, hit)) break;
+          const float test_T = T * (1 - hit.alpha);
+          if (test_T < 0.0001f) {
+            done = true;
+            break;
+          }
+          render_number++;
+          if (p.max_intersections > 0 && render_number >= p.max_intersections) done = true;
+          hit_blend = true;
+          t_before = T;
+          T = test_T;
+        } while (false);
+      }
+      const uint64_t m = __ballot(hit_blend);
+      if (m != 0ull) {
+        float sum = t_before;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, kWaveLanes);
+        if (lane == 0u) {
+          const uint32_t id = __float_as_uint(scut[j].y);
+          atomicAdd(p.cover_pixels + id, (float)__popcll(m));
+          atomicAdd(p.trans_avg + id, sum);
+        }
+      }
+      if (__ballot(!done) == 0ull) break;
+    }
+  }
+}
+
 template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0>
 static hipError_t launch_one(const RenderParams& p, hipStream_t s) {
   hipLaunchKernelGGL((render_kernel<F, NACC, kHash, kHalf, kStructured, kMix>), dim3(p.ntiles), dim3(kRenderThreads),
@@ -946,8 +1024,17 @@ static hipError_t launch_hash(const RenderParams& p, hipStream_t s) {
   return launch_hash_levels<F, kHalf, true>(p, s);
 }
 
+static hipError_t launch_render_kernel(const RenderParams& p, hipStream_t s);
+
 hipError_t launch_render(const RenderParams& p, hipStream_t s) {
   if (p.ntiles == 0) return hipSuccess;
+  const hipError_t re = launch_render_kernel(p, s);
+  if (re != hipSuccess || p.cover_pixels == nullptr || p.m13) return re;
+  hipLaunchKernelGGL(record_transmittance_kernel, dim3(p.ntiles), dim3(kRenderThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+static hipError_t launch_render_kernel(const RenderParams& p, hipStream_t s) {
   hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, s, reinterpret_cast<const uint2*>(p.ranges),
                      p.ntiles, p.tile_order);
   const hipError_t oe = hipGetLastError();

@@ -116,8 +116,6 @@ class _RasterizeGaussians(torch.autograd.Function):
             raise NotImplementedError("precomputed transforms (cov3D_precomp) are not implemented")
         if not _empty(features_diffuse):
             raise NotImplementedError("a second (diffuse) hash grid is not implemented")
-        if raster_settings.record_transmittance:
-            raise NotImplementedError("record_transmittance=True is not implemented")
         C = _channels(hashgrid_settings)
         level = int(hashgrid_settings.L)
         if base_mode in (4, 7, 12, 14) and level == 0:
@@ -161,7 +159,8 @@ class _RasterizeGaussians(torch.autograd.Function):
                                     rotations.detach(), homotrans=None if _empty(homotrans) else homotrans.detach(),
                                     ap_level=None if _empty(ap_level) else ap_level.detach(), colors_precomp=colors,
                                     channels=C, shs=None if (level > 0 or colors is not None or _empty(sh)) else
-                                    sh.detach(), sh_degree=int(raster_settings.sh_degree))
+                                    sh.detach(), sh_degree=int(raster_settings.sh_degree),
+                                    record_transmittance=bool(raster_settings.record_transmittance))
         ctx.num_rendered = res.num_rendered
         ctx.render_mode = render_mode
         ctx.fw = dict(res=res, settings=settings, grid=grid, C=C, colors=colors,
@@ -171,8 +170,13 @@ class _RasterizeGaussians(torch.autograd.Function):
                       ap_level=None if _empty(ap_level) else ap_level.detach())
         ctx.save_for_backward(means3D, opacities, scales, rotations)
         dev = means3D.device
-        trans_avg = torch.zeros((0, 1), dtype=torch.float32, device=dev)
-        cover = torch.zeros((0, 1), dtype=torch.float32, device=dev)
+        if res.trans_avg is not None:
+            # [P, 1] each, as DSR/rasterize_points.cu:169-171 allocates them
+            trans_avg, cover = res.trans_avg.view(-1, 1), res.cover_pixels.view(-1, 1)
+        else:
+            trans_avg = torch.zeros((0, 1), dtype=torch.float32, device=dev)
+            cover = torch.zeros((0, 1), dtype=torch.float32, device=dev)
+        ctx.mark_non_differentiable(trans_avg, cover)
         return res.color, res.radii, res.others, trans_avg, cover
 
     @staticmethod

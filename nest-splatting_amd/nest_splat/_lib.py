@@ -27,7 +27,7 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 SCAN_NOALLOC_MAX = 268431360
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
  GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
@@ -77,7 +77,8 @@ class Splats(ct.Structure):
 
 class FrameOutputs(ct.Structure):
     _fields_ = [("struct_size", ct.c_uint32), ("channels", ct.c_int32), ("out_color", ct.c_void_p),
-                ("out_others", ct.c_void_p), ("radii", ct.c_void_p)]
+                ("out_others", ct.c_void_p), ("radii", ct.c_void_p), ("cover_pixels", ct.c_void_p),
+                ("trans_avg", ct.c_void_p)]
 
 
 class BackwardIO(ct.Structure):

@@ -146,6 +146,10 @@ class ForwardResult:
     binning: torch.Tensor
     image: torch.Tensor
     timing_ms: Dict[str, float] = field(default_factory=dict)
+    # record_transmittance: hits per splat and the sum of the transmittance
+    # before each of them, [P] each (None when not recorded)
+    cover_pixels: Optional[torch.Tensor] = None
+    trans_avg: Optional[torch.Tensor] = None
 
 
 def aligned(t: torch.Tensor, align: int = 16) -> torch.Tensor:
@@ -218,12 +222,14 @@ def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: t
                       scales: torch.Tensor, rotations: torch.Tensor, homotrans: Optional[torch.Tensor] = None,
                       ap_level: Optional[torch.Tensor] = None, colors_precomp: Optional[torch.Tensor] = None,
                       channels: int = 3, timing: bool = False, shs: Optional[torch.Tensor] = None,
-                      sh_degree: int = 0) -> ForwardResult:
+                      sh_degree: int = 0, record_transmittance: bool = False) -> ForwardResult:
     """One forward frame.  The colour path (grid.levels == 0 in render mode
     0) takes colours from colors_precomp, or, when it is None, evaluates them
     from shs [P, M, 3] at degree sh_degree in preprocess (3 channels).  In
     render modes 4 and 13 colors_precomp holds the per-splat feature rows
-    (grid.row_width floats each)."""
+    (grid.row_width floats each).  record_transmittance fills
+    cover_pixels / trans_avg (DSR/rasterize_points.cu:169-171,
+    CR/forward.cu:1961-1964)."""
     dev = means3D.device
     P = int(means3D.shape[0])
     H, W = settings.image_height, settings.image_width
@@ -254,10 +260,16 @@ def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: t
     out.out_color = color.data_ptr()
     out.out_others = others.data_ptr()
     out.radii = radii.data_ptr()
+    cover = trans = None
+    if record_transmittance:
+        cover = torch.empty((P,), dtype=torch.float32, device=dev)
+        trans = torch.empty((P,), dtype=torch.float32, device=dev)
+        out.cover_pixels = cover.data_ptr() if P > 0 else None
+        out.trans_avg = trans.data_ptr() if P > 0 else None
     L.check(lib.nest_forward_render(ct.byref(settings), ct.byref(g), ct.byref(sp), L.ptr(geom), gbytes,
                                     L.ptr(binning), bbytes, L.ptr(image), ibytes, NR, ct.byref(out), ct.byref(tm),
                                     stream), "nest_forward_render")
-    res = ForwardResult(NR, color, others, radii, geom, binning, image)
+    res = ForwardResult(NR, color, others, radii, geom, binning, image, cover_pixels=cover, trans_avg=trans)
     if own_timing and timing:
         res.timing_ms = L.timing_read(tm)
         L.timing_release(tm)

@@ -640,7 +640,25 @@ typedef struct {
      * (same level, rows of hyb*F+1 floats).  Other values are not
      * restated. */
     int render_mode;
+    /* record_transmittance (forward.cu:1961-1964), NULL = off: [P] each;
+     * every hit that reaches the end of the hit body (not mode 13's, which
+     * leave it first) adds 1 and the transmittance before it. */
+    float *cover_pixels;
+    float *trans_avg;
 } or_render_args;
+
+static void record_hit(const or_render_args *A, uint32_t id, float T)
+{
+    if (!A->cover_pixels) return;
+#ifdef _OPENMP
+#pragma omp atomic
+#endif
+    A->cover_pixels[id] += 1.0f;
+#ifdef _OPENMP
+#pragma omp atomic
+#endif
+    A->trans_avg[id] += T;
+}
 
 /* hashgrid_levels of render_mode 4 (forward.cu:1231-1238): the largest i in
  * 1..16 with offsets[i] > offsets[i-1], over the offsets padded with zeros
@@ -859,6 +877,7 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
             else { apc0 = 1.0f; apc1 = (float)(1.0 - (double)(uint32_t)(ap - 4u) * 0.5); }
             vis[0] += apc0 * w; vis[1] += apc1 * w; vis[2] += 0.0f * w;
         }
+        record_hit(A, id, T);
         T = test_T;
         last_contributor = contributor;
     }

@@ -45,7 +45,8 @@ class OrRenderArgs(ct.Structure):
                 ("transmat", ct.c_void_p), ("normal_opacity", ct.c_void_p), ("homotrans", ct.c_void_p),
                 ("ap_level", ct.c_void_p), ("colors", ct.c_void_p), ("grid", OrGrid),
                 ("out_color", ct.c_void_p), ("out_others", ct.c_void_p), ("final_T", ct.c_void_p),
-                ("n_contrib", ct.c_void_p), ("render_mode", ct.c_int)]
+                ("n_contrib", ct.c_void_p), ("render_mode", ct.c_int), ("cover_pixels", ct.c_void_p),
+                ("trans_avg", ct.c_void_p)]
 
 
 class OrRenderBwdArgs(ct.Structure):
@@ -199,15 +200,21 @@ def make_grid(L, F, S, H, offsets, table, gridrange, contract=False, align_corne
 
 
 def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_level=None, colors=None,
-           beta=0.0, max_intersections=0, row_stride=1, row_phase=0, threads=0, render_mode=0, level=None):
+           beta=0.0, max_intersections=0, row_stride=1, row_phase=0, threads=0, render_mode=0, level=None,
+           record_transmittance=False):
     """renderCUDAsurfelForward for every pixel.  render_mode 0 (grid levels
     grid.L, or the colour path without a grid), 4, 7, 12, 13 or 14 (bit 8:
     inference); for modes 4, 7, 12, 13 and 14, level is the reference's packed level argument
     (total << 16 | hash levels << 8 | per-splat levels) and colors the
-    per-splat feature rows."""
+    per-splat feature rows.  record_transmittance adds cover_pixels and
+    trans_avg ([P] each) to the result."""
     HW = W * H
     out = dict(color=np.zeros((C, H, W), np.float32), others=np.zeros((14, H, W), np.float32),
                final_T=np.zeros((3, H, W), np.float32), n_contrib=np.zeros((2, H, W), np.uint32))
+    if record_transmittance:
+        P = len(pre["radii"])
+        out["cover_pixels"] = np.zeros(P, np.float32)
+        out["trans_avg"] = np.zeros(P, np.float32)
     keep = []
 
     def ptr(a, dt):
@@ -237,6 +244,9 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
     args.out_others = out["others"].ctypes.data
     args.final_T = out["final_T"].ctypes.data
     args.n_contrib = out["n_contrib"].ctypes.data
+    if record_transmittance:
+        args.cover_pixels = out["cover_pixels"].ctypes.data
+        args.trans_avg = out["trans_avg"].ctypes.data
     lib().or_render(ct.byref(args), row_stride, row_phase, threads)
     return out
 

@@ -25,7 +25,7 @@ def _rows(sc, width, weight_col=None, seed=0):
     return rows
 
 
-def run_gpu(sc, render_mode, hyb, glevels, total, C, rows, interp=0):
+def run_gpu(sc, render_mode, hyb, glevels, total, C, rows, interp=0, record=False):
     from nest_splat import rasterizer as rz
     sp = sc.spec
     cam = sc.cameras[0]
@@ -37,12 +37,13 @@ def run_gpu(sc, render_mode, hyb, glevels, total, C, rows, interp=0):
                            np.asarray(sp.gridrange, np.float32), interpolation=interp, render_mode=render_mode,
                            hybrid_levels=hyb, total_levels=total)
     res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
-                               homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), colors_precomp=t(rows), channels=C)
+                               homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), colors_precomp=t(rows), channels=C,
+                               record_transmittance=record)
     torch.cuda.synchronize()
     return res
 
 
-def run_oracle(O, sc, render_mode, level, grid_levels, C, rows, interp=0):
+def run_oracle(O, sc, render_mode, level, grid_levels, C, rows, interp=0, record=False):
     sp = sc.spec
     cam = sc.cameras[0]
     W, H = cam.image_width, cam.image_height
@@ -52,7 +53,7 @@ def run_oracle(O, sc, render_mode, level, grid_levels, C, rows, interp=0):
     grid = O.make_grid(grid_levels, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract,
                        interp=interp)
     r = O.render(pre, b, W, H, C, grid, homotrans=sc.homotrans, ap_level=sc.ap_level, colors=rows,
-                 render_mode=render_mode, level=level)
+                 render_mode=render_mode, level=level, record_transmittance=record)
     return b, r
 
 
@@ -201,6 +202,86 @@ def test_drop_in_decodes_packed_levels(oracle):
         _, r = run_oracle(oracle, sc, mode, packed, gl, C, rows)
         np.testing.assert_array_equal(allmap.cpu().numpy(), r["others"])
         np.testing.assert_array_equal(color.cpu().numpy(), r["color"])
+
+
+# (mode, scene, total levels, per-splat levels, grid levels): training and
+# inference; mode 13 records nothing
+REC_CASES = [(4, "unbounded_small", 0, 4, 10), (12, "shell_small", 12, 4, 8), (12 | 0x100, "shells_small", 8, 5, 3),
+             (13, "unbounded_small", 16, 10, 6), (14, "cfg1", 8, 3, 5), (7, "shell_small", 10, 0, 6)]
+
+
+@pytest.mark.parametrize("mode,name,total,hyb,gl", REC_CASES)
+def test_record_transmittance_modes(oracle, mode, name, total, hyb, gl):
+    """record_transmittance in the mixed modes: every hit that reaches the
+    blend records (CR/forward.cu:1961-1964), mode 13's hits leave the loop
+    first (:1090)."""
+    sc = scene(name)
+    F = sc.spec.F
+    base = mode & 0xFF
+    print(f"[case] record_transmittance mode {mode:#x} {name}", flush=True)
+    if base == 4:
+        C = (hyb + gl) * F
+        rows = _rows(sc, hyb * F, seed=hyb)
+        res = run_gpu(sc, 4, hyb, gl, 0, C, rows, record=True)
+        b, r = run_oracle(oracle, sc, 4, ((hyb + gl) << 16) | (1 << 8) | hyb, gl, C, rows, record=True)
+    elif base == 14:
+        rows = _rows(sc, hyb * F + 1, weight_col=hyb * F, seed=total + hyb + 2)
+        rows[::11, hyb * F] = 0.0
+        res = run_gpu(sc, mode, hyb, gl, total, total * F, rows, record=True)
+        b, r = run_oracle(oracle, sc, mode, (total << 16) | (gl << 8) | hyb, max(gl, 1), total * F, rows, record=True)
+    elif base == 7:
+        rows = _rows(sc, total * F + 1, weight_col=total * F, seed=total + gl + 3)
+        res = run_gpu(sc, 7, 0, gl, total, total * F, rows, record=True)
+        b, r = run_oracle(oracle, sc, 7, (total << 16) | (gl << 8), max(gl, 1), total * F, rows, record=True)
+    else:
+        rows = _rows(sc, total * F + 1, weight_col=total * F, seed=total + hyb)
+        res = run_gpu(sc, mode, hyb, gl, total, total * F, rows, record=True)
+        b, r = run_oracle(oracle, sc, mode, (total << 16) | (gl << 8) | hyb, max(gl, 1), total * F, rows,
+                          record=True)
+    _check(res, b, r)
+    cover = res.cover_pixels.cpu().numpy()
+    np.testing.assert_array_equal(cover, r["cover_pixels"])
+    scale = max(float(np.abs(r["trans_avg"]).max()), 1e-30)
+    np.testing.assert_allclose(res.trans_avg.cpu().numpy(), r["trans_avg"], rtol=1e-5, atol=1e-6 * scale)
+    if base == 13:
+        assert not cover.any() and r["others"][7].any()
+    else:
+        assert cover.sum() == r["others"][7].sum() > 0
+
+
+def test_drop_in_record_transmittance(oracle):
+    """GaussianRasterizer with record_transmittance=True returns the
+    reference's (transmittance_avg, cover_pixels) as [P, 1] tensors."""
+    from diff_surfel_rasterization import GaussianRasterizationSettings, GaussianRasterizer, HashGridSettings
+    sc = scene("shell_small")
+    sp = sc.spec
+    cam = sc.cameras[0]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    rs = GaussianRasterizationSettings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy,
+                                       torch.zeros(3, device=DEV), 1.0, t(cam.world_view_transform),
+                                       t(cam.full_proj_transform), 3, t(cam.camera_center), False, False, 0.0,
+                                       sp.contract, True)
+    hs = HashGridSettings(sp.L, math.log2(sp.per_level_scale), sp.base_res, False, 0,
+                          torch.tensor([0, 0, sp.L * sp.F], dtype=torch.int32, device=DEV))
+    print("[case] drop-in record_transmittance", flush=True)
+    out = GaussianRasterizer(rs, hs)(
+        means3D=t(sc.means), means2D=None, opacities=t(sc.opacity), scales=t(sc.scales), rotations=t(sc.rotations),
+        colors_precomp=torch.zeros((sp.P, sp.L * sp.F), device=DEV), homotrans=t(sc.homotrans),
+        ap_level=t(sc.ap_level), features=t(sc.table), offsets=t(np.asarray(sc.offsets)),
+        gridrange=t(np.asarray(sp.gridrange, np.float32)))
+    torch.cuda.synchronize()
+    trans, cover = out[3], out[4]
+    assert trans.shape == (sp.P, 1) and cover.shape == (sp.P, 1)
+    W, H = cam.image_width, cam.image_height
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    grid = oracle.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    r = oracle.render(pre, b, W, H, sp.L * sp.F, grid, homotrans=sc.homotrans, ap_level=sc.ap_level,
+                      record_transmittance=True)
+    np.testing.assert_array_equal(cover.cpu().numpy()[:, 0], r["cover_pixels"])
+    scale = max(float(np.abs(r["trans_avg"]).max()), 1e-30)
+    np.testing.assert_allclose(trans.cpu().numpy()[:, 0], r["trans_avg"], rtol=1e-5, atol=1e-6 * scale)
 
 
 def test_mode_validation():

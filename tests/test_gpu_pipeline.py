@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 SCENES = ["cfg1", "shell_small", "unbounded_small", "shells_small"]
 
 
-def run_gpu(sc, cam_index=0, max_intersections=0, align_corners=False, interp=0, beta=0.0):
+def run_gpu(sc, cam_index=0, max_intersections=0, align_corners=False, interp=0, beta=0.0, record=False):
     from nest_splat import rasterizer as rz
     sp = sc.spec
     cam = sc.cameras[cam_index]
@@ -29,12 +29,13 @@ def run_gpu(sc, cam_index=0, max_intersections=0, align_corners=False, interp=0,
     grid = rz.HashGridDesc(sp.L, sp.F, sp.S, sp.base_res, t(sc.table), sc.offsets, np.asarray(sp.gridrange, np.float32),
                            align_corners=align_corners, interpolation=interp)
     res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
-                               homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), channels=sp.C)
+                               homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), channels=sp.C,
+                               record_transmittance=record)
     torch.cuda.synchronize()
     return res
 
 
-def run_oracle(O, sc, cam_index=0, max_intersections=0, align_corners=False, interp=0, beta=0.0):
+def run_oracle(O, sc, cam_index=0, max_intersections=0, align_corners=False, interp=0, beta=0.0, record=False):
     sp = sc.spec
     cam = sc.cameras[cam_index]
     W, H = cam.image_width, cam.image_height
@@ -44,7 +45,7 @@ def run_oracle(O, sc, cam_index=0, max_intersections=0, align_corners=False, int
     grid = O.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract,
                        align_corners=align_corners, interp=interp)
     r = O.render(pre, b, W, H, sp.C, grid, homotrans=sc.homotrans, ap_level=sc.ap_level,
-                 max_intersections=max_intersections, beta=beta)
+                 max_intersections=max_intersections, beta=beta, record_transmittance=record)
     return pre, b, r
 
 
@@ -223,3 +224,56 @@ def test_tile_launch_order(name):
     b = bucket[order]
     assert np.all(np.diff(b) <= 1) and b[0] >= bucket.max() - 1
     assert np.all(np.maximum.accumulate(b[::-1])[::-1] <= b + 1)
+
+
+def check_record(res, r):
+    """record_transmittance: hit counts exact, transmittance sums within 1e-5
+    of the largest (the GPU sums per wave, the oracle per pixel)."""
+    cover = res.cover_pixels.cpu().numpy()
+    trans = res.trans_avg.cpu().numpy()
+    np.testing.assert_array_equal(cover, r["cover_pixels"])
+    scale = max(float(np.abs(r["trans_avg"]).max()), 1e-30)
+    np.testing.assert_allclose(trans, r["trans_avg"], rtol=1e-5, atol=1e-6 * scale)
+    assert cover.sum() > 0
+
+
+@pytest.mark.parametrize("name,mx", [("cfg1", 0), ("shell_small", 0), ("unbounded_small", 0), ("shell_small", 5)])
+def test_record_transmittance_parity(oracle, name, mx):
+    """record_transmittance=True (CR/forward.cu:1961-1964): per-splat hit
+    counts bit-exact, transmittance sums within tolerance, and the frame's
+    other outputs unchanged by the recording."""
+    sc = scene(name)
+    print(f"[case] record_transmittance {name} max_intersections={mx}", flush=True)
+    res = run_gpu(sc, max_intersections=mx, record=True)
+    pre, b, r = run_oracle(oracle, sc, max_intersections=mx, record=True)
+    check_record(res, r)
+    np.testing.assert_array_equal(res.others.cpu().numpy(), r["others"])
+    plain = run_gpu(sc, max_intersections=mx)
+    assert plain.cover_pixels is None and plain.trans_avg is None
+    np.testing.assert_array_equal(plain.color.cpu().numpy(), res.color.cpu().numpy())
+    np.testing.assert_array_equal(plain.others.cpu().numpy(), res.others.cpu().numpy())
+    # splats culled or off-screen record nothing
+    assert not res.cover_pixels.cpu().numpy()[pre["radii"] == 0].any()
+
+
+def test_record_transmittance_colour_path(oracle):
+    """The colour path (no grid) records the same way."""
+    from nest_splat import rasterizer as rz
+    sc = scene("shell_small")
+    sp = sc.spec
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    print("[case] record_transmittance colour path", flush=True)
+    cols = np.random.default_rng(1).uniform(0, 1, (sp.P, 3)).astype(np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(torch.device("cuda:0"))
+    settings = rz.make_settings(H, W, cam.tanfovx, cam.tanfovy, cam.world_view_transform, cam.full_proj_transform,
+                                cam.camera_center, if_contract=sp.contract)
+    grid = rz.HashGridDesc(0, 1, 0.0, 0, None, np.zeros(1, np.int64), np.zeros(2, np.float32))
+    res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
+                               colors_precomp=t(cols), channels=3, record_transmittance=True)
+    torch.cuda.synchronize()
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    r = oracle.render(pre, b, W, H, 3, None, colors=cols, record_transmittance=True)
+    check_record(res, r)

@@ -150,8 +150,6 @@ def test_unsupported_modes_raise():
             GaussianRasterizer(rs, hs)(render_mode=mode, **kw)
     with pytest.raises(NotImplementedError):
         GaussianRasterizer(rs, hs)(kernel_type=1, **kw)
-    with pytest.raises(NotImplementedError):
-        GaussianRasterizer(rs._replace(record_transmittance=True), hs)(**kw)
     with pytest.raises(Exception):
         GaussianRasterizer(rs, hs)(means3D=t(sc.means), means2D=None, opacities=t(sc.opacity))
     with pytest.raises(ValueError):

@@ -390,6 +390,79 @@ def test_stacked_splats_termination_closed_form(oracle):
     assert r2["others"][1, cy, cx] == np.float32(1) - np.float32(0.5) ** 4
 
 
+def _record_scene(oracle, n=10, W=48, H=40, seed=3):
+    """n splats with opacities in [0.15, 0.4] spread over the central pixels
+    of a small image, so that pixels collect several hits and none
+    terminates (0.6^10 > 1e-4)."""
+    from nest_splat.camera import look_at
+    rng = np.random.default_rng(seed)
+    cam = look_at((0.0, -3.0, 0.0), (0.0, 0.0, 0.0), 50.0, W, H)
+    means = np.stack([rng.uniform(-0.25, 0.25, n), rng.uniform(-0.5, 0.5, n), rng.uniform(-0.2, 0.2, n)], 1)
+    means = means.astype(np.float32)
+    q = rng.normal(size=(n, 4)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    q = (0.7 * q + 0.3 * np.array([np.cos(np.pi / 4), np.sin(np.pi / 4), 0, 0], np.float32)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    scales = rng.uniform(0.08, 0.25, (n, 2)).astype(np.float32)
+    opac = rng.uniform(0.15, 0.4, (n, 1)).astype(np.float32)
+    pre = oracle.preprocess(means, scales, q, opac, cam.world_view_transform, cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    return pre, b, W, H
+
+
+def test_record_transmittance_equals_prefix_renders(oracle):
+    """record_transmittance (forward.cu:1961-1964) from renders the rest of
+    this file pins: splat i is accepted at the pixels where rendering i alone
+    counts a hit, and the transmittance it sees there is the final T of the
+    render in which i and every splat behind it have zero opacity.  A count
+    of rejected hits, or T recorded after the hit, fails this."""
+    pre, b, W, H = _record_scene(oracle)
+    P = len(pre["radii"])
+    cols = np.ones((P, 3), np.float32)
+    full = oracle.render(pre, b, W, H, 3, None, colors=cols, record_transmittance=True)
+    order = np.lexsort((np.arange(P), pre["depth"].view(np.uint32)))  # depth bits, then index
+    rank = np.empty(P, np.int64)
+    rank[order] = np.arange(P)
+    hits = np.zeros((H, W))
+    for i in range(P):
+        alone = dict(pre, normal_opacity=pre["normal_opacity"].copy())
+        alone["normal_opacity"][np.arange(P) != i, 3] = 0.0
+        acc = oracle.render(alone, b, W, H, 3, None, colors=cols)["others"][7] == 1
+        hits += acc
+        front = dict(pre, normal_opacity=pre["normal_opacity"].copy())
+        front["normal_opacity"][rank >= rank[i], 3] = 0.0
+        T_before = oracle.render(front, b, W, H, 3, None, colors=cols)["final_T"][0]
+        assert full["cover_pixels"][i] == acc.sum()
+        np.testing.assert_allclose(full["trans_avg"][i], T_before[acc].astype(np.float64).sum(), rtol=1e-5)
+    assert full["cover_pixels"].sum() > 4 * P  # overlapping splats
+    np.testing.assert_array_equal(full["others"][7], hits)  # nothing terminated early
+
+
+def test_record_transmittance_render_modes(oracle):
+    """Mode 12's hits are full ones (the same record as mode 0 for the same
+    acceptance); mode 13's leave the hit loop first and record nothing
+    (forward.cu:1090)."""
+    pre, b, W, H = _record_scene(oracle, seed=5)
+    P = len(pre["radii"])
+    L, F, T = 2, 2, 1 << 10
+    table = np.full((L * T, F), 0.25, np.float32)
+    g, _ = _grid(oracle, L, F, T, 8, 1.0, table, gridrange=(-1.0, 1.0))
+    from nest_splat.scene import build_homotrans_np
+    rng = np.random.default_rng(0)
+    homo = rng.normal(size=(P, 16)).astype(np.float32)
+    ap = np.full((P, 1), 24.0, np.float32)
+    r0 = oracle.render(pre, b, W, H, L * F, g, homotrans=homo, ap_level=ap, record_transmittance=True)
+    rows = np.concatenate([rng.uniform(size=(P, L * F)), np.full((P, 1), 0.5)], 1).astype(np.float32)
+    lvl = L << 16 | L << 8
+    r12 = oracle.render(pre, b, W, H, L * F, g, homotrans=homo, ap_level=ap, colors=rows, render_mode=12, level=lvl,
+                        record_transmittance=True)
+    np.testing.assert_array_equal(r12["cover_pixels"], r0["cover_pixels"])
+    np.testing.assert_allclose(r12["trans_avg"], r0["trans_avg"], rtol=1e-5)
+    r13 = oracle.render(pre, b, W, H, L * F, g, homotrans=homo, ap_level=ap, colors=rows, render_mode=13, level=lvl,
+                        record_transmittance=True)
+    assert r13["others"][7].sum() > 0 and not r13["cover_pixels"].any() and not r13["trans_avg"].any()
+
+
 def test_single_splat_hash_feature_closed_form(oracle):
     """One splat at the pixel centre: G = 1, alpha = opacity, the feature is
     alpha * query(centre); out-of-range hit points count but add no feature."""
