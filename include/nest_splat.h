@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 9
+#define NEST_ABI_VERSION 10
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -156,6 +156,14 @@ typedef struct nest_splats {
                                   (computeColorFromSH, CR/forward.cu:21-72) */
   int32_t sh_degree;           /* active SH degree, 0..3 */
   int32_t sh_coeffs;           /* coefficients per splat, >= (sh_degree+1)^2 */
+  /* kernel_type (CR/forward.cu:864-921, CR/backward.cu:764-812): 0 Gaussian
+   * (the global beta activation of the settings), 1 beta kernel
+   * opacity * (1 - rho)^shape with rho < 1, 2 flex (the Gaussian with a per-splat
+   * beta activation), 3 general exp(-0.5 * max(rho, 1e-8)^(shape / 2)); the
+   * per-splat parameter is shapes[i] (f32 [P], required for 1-3). */
+  const float *shapes;
+  int32_t kernel_type;
+  int32_t reserved;
 } nest_splats;
 
 /* Frame outputs (device): out_color [channels,H,W], out_others [14,H,W] and

@@ -166,6 +166,11 @@ int check_splats(const nest_splats* sp, bool need_geometry) {
   if (sp->P < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "P must be >= 0 (got %d)", sp->P);
   if (need_geometry && sp->P > 0 && (!sp->means3D || !sp->scales || !sp->rotations || !sp->opacities))
     return fail(NEST_ERR_INVALID_ARGUMENT, "means3D, scales, rotations and opacities are required");
+  if (sp->kernel_type < 0 || sp->kernel_type > 3)
+    return fail(NEST_ERR_UNSUPPORTED, "kernel_type %d: supported are 0 (Gaussian), 1 (beta), 2 (flex), 3 (general)",
+                sp->kernel_type);
+  if (sp->kernel_type != 0 && sp->P > 0 && !sp->shapes)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "kernel_type %d needs shapes [P]", sp->kernel_type);
   if (sp->shs && !sp->colors_precomp) {
     if (sp->sh_degree < 0 || sp->sh_degree > 3)
       return fail(NEST_ERR_UNSUPPORTED, "SH degree must be 0..3 (got %d)", sp->sh_degree);
@@ -408,6 +413,8 @@ int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp,
   p.opac = sp->opacities;
   p.homotrans = sp->homotrans;
   p.ap_level = sp->ap_level;
+  p.kernel_type = sp->kernel_type;
+  p.shapes = sp->shapes;
   p.radii = reinterpret_cast<int32_t*>(g + off[NEST_GEOM_RADII]);
   p.radii_user = radii;
   p.xy = reinterpret_cast<float*>(g + off[NEST_GEOM_XY]);
@@ -474,6 +481,7 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   rp.level = (int)gr->levels;
   rp.beta = rs->beta;
   rp.max_intersections = rs->max_intersections;
+  rp.kernel_type = sp->kernel_type;
   if ((rc = setup_grid(rs, gr, sp, out->channels, rp.grid))) return rc;
   if ((gr->render_mode & 0xFF) != NEST_MODE_BASELINE) {
     // per-splat features ahead of the grid's (CR/forward.cu:965-1101, :1218-1282)
@@ -866,6 +874,9 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   int rc = check_settings(rs);
   if (rc) return rc;
   if ((rc = check_splats(sp, true))) return rc;
+  if (sp->kernel_type != 0)
+    return fail(NEST_ERR_UNSUPPORTED, "backward: kernel_type %d is not implemented (the Gaussian kernel is)",
+                sp->kernel_type);
   if (!gr || gr->struct_size != sizeof(nest_hashgrid))
     return fail(NEST_ERR_INVALID_ARGUMENT, "nest_hashgrid missing or struct_size mismatch");
   if (!io || io->struct_size != sizeof(nest_backward_io))

@@ -42,6 +42,8 @@ struct PreprocessParams {
   int sh_degree;
   int sh_coeffs;
   float campos[3];
+  int kernel_type;          // 0 Gaussian, 1 beta, 2 flex, 3 general
+  const float* shapes;      // [P] per-splat kernel parameter (kernel_type 1-3), copied to record[26]
   // outputs
   int32_t* radii;
   int32_t* radii_user;      // optional second copy (the caller's radii tensor)
@@ -106,6 +108,7 @@ struct RenderParams {
   int level;             // 0 colour path, >0 hash
   float beta;
   uint32_t max_intersections;
+  int kernel_type;            // 0 Gaussian, 1 beta, 2 flex, 3 general (shape in record[26])
   const uint32_t* ranges;     // [tiles][2]
   const uint32_t* point_list;
   const float* records;       // [P][32]

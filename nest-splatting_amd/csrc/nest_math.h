@@ -40,6 +40,55 @@ __device__ __forceinline__ float expf_ref(float x) {
   return y * __int_as_float((k + 127) << 23);
 }
 
+// log(x) in binary32 (Moshier, Methods and Programs for Mathematical
+// Functions, 1989): x = m 2^e with m in [sqrt(1/2), sqrt(2)), f = m - 1,
+// log(1 + f) = f - f^2/2 + f^3 P(f) with a degree-8 minimax P, plus e ln2 in
+// a 9-bit head and a tail.  0 gives -inf, negatives NaN, +inf and NaN
+// themselves; subnormals are scaled by 2^23 first.
+__device__ __forceinline__ float logf_ref(float x) {
+  if (!(x > 0.0f)) return x == 0.0f ? __int_as_float(0xff800000) : __int_as_float(0x7fc00000);
+  if (x == __int_as_float(0x7f800000)) return x;
+  uint32_t u = __float_as_uint(x);
+  int e = 0;
+  if (u < 0x00800000u) {
+    u = __float_as_uint(x * 8388608.0f);
+    e = -23;
+  }
+  e += (int)((u >> 23) & 0xffu) - 126;
+  float m = __uint_as_float((u & 0x007fffffu) | 0x3f000000u);  // [0.5, 1)
+  if (m < 0.707106781186547524f) {
+    e -= 1;
+    m = m + m - 1.0f;
+  } else {
+    m = m - 1.0f;
+  }
+  const float z = m * m;
+  float y = 7.0376836292e-2f;
+  y = y * m + -1.1514610310e-1f;
+  y = y * m + 1.1676998740e-1f;
+  y = y * m + -1.2420140846e-1f;
+  y = y * m + 1.4249322787e-1f;
+  y = y * m + -1.6668057665e-1f;
+  y = y * m + 2.0000714765e-1f;
+  y = y * m + -2.4999993993e-1f;
+  y = y * m + 3.3333331174e-1f;
+  y = y * m * z;
+  const float fe = (float)e;
+  y = y + -2.12194440e-4f * fe;
+  y = y + -0.5f * z;
+  float r = m + y;
+  r = r + 0.693359375f * fe;
+  return r;
+}
+
+// x^y for x >= 0 as expf_ref(y * logf_ref(x)); y == 0 gives 1 (0^0 and
+// NaN^0 included), 0^y 0 for y > 0 and +inf for y < 0.  Not correctly
+// rounded: the relative error grows with |y log x| (about 5e-6 at 88).
+__device__ __forceinline__ float powf_ref(float x, float y) {
+  if (y == 0.0f) return 1.0f;
+  return expf_ref(y * logf_ref(x));
+}
+
 // float -> int with the operand clamped to +-2^30 first (NaN -> -2^30 through
 // fmaxf), so the conversion never leaves the representable range.
 __device__ __forceinline__ int f2i_sat(float x) {

@@ -184,12 +184,33 @@ __global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams 
   // CR/forward.cu:294-320 at cutoff^2 = cut, valid when the whole disk lies in
   // front of the camera: cut*(Tw0^2+Tw1^2) < Tw2^2) and the disk of radius
   // sqrt(cut/2) around xy, widened by one pixel.
+  // The other kernels (CR/forward.cu:864-900) bound rho the same way: the
+  // beta kernel accepts only rho < 1 and alpha >= 1/255 needs
+  // rho <= 1 - (255 o)^(-1/shape); the flex kernel is the Gaussian with the
+  // splat's own beta; the general kernel needs rho <= (2 ln(255 o))^(2/shape).
+  // Their powers are not correctly rounded (powf_ref), hence the wider
+  // relative margins.  A parameter without a finite bound (NaN, or a
+  // non-positive exponent of the general kernel) takes the exact path.
   float cut = -1.0f;
   float bx0 = 1.0f, bx1 = -1.0f, by0 = 1.0f, by1 = -1.0f;  // empty: never accepted
-  const double bb = p.beta > 0.0f ? (double)p.beta : 0.0;
+  const float shape = p.kernel_type != 0 ? p.shapes[i] : 0.0f;
+  const double sh = (double)shape;
+  double bb = p.kernel_type == 0 && p.beta > 0.0f ? (double)p.beta : 0.0;
+  if (p.kernel_type == 2) bb = shape > 0.0f ? sh : 0.0;
   const double xo = 255.0 * (double)opacity * (1.0 + bb) - bb;
-  if (opacity > 0.0f && xo > 0.0) {
-    const double c = 2.0 * log(xo * (1.0 + 1e-6)) + 1e-4;
+  const bool finite_shape = p.kernel_type == 0 || p.kernel_type == 2 || (shape == shape && (p.kernel_type != 3 || shape > 0.0f));
+  if (opacity > 0.0f && xo > 0.0 && finite_shape) {
+    double c = 2.0 * log(xo * (1.0 + 1e-6)) + 1e-4;
+    if (p.kernel_type == 1) {
+      // rho < 1 always; alpha >= 1/255 bounds it further for a positive shape
+      const double o255 = 255.0 * (double)opacity;
+      c = 1.0;
+      if (shape > 0.0f && o255 > 1.0) c = fmin(1.0, 1.0 - pow(o255, -1.0 / sh) + 1e-3);
+      if (o255 <= 1.0 && shape > 0.0f) c = -1.0;  // base^shape <= 1: never 1/255
+    } else if (p.kernel_type == 3) {
+      const double c0 = 2.0 * log(255.0 * (double)opacity) * (1.0 + 1e-4) + 1e-4;
+      c = c0 > 0.0 ? pow(c0, 2.0 / sh) * (1.0 + 1e-3) + 1e-3 : -1.0;
+    }
     if (c >= 0.0) {
       cut = (float)c;
       const double rd = sqrt(c * 0.5) + 1.0;
@@ -210,7 +231,9 @@ __global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams 
         bx0 = -3.0e38f; bx1 = 3.0e38f; by0 = -3.0e38f; by1 = 3.0e38f;  // unbounded image: never cull
       }
     }
-  } else if (!(opacity <= 0.0f)) {  // NaN opacity: no bound, always take the exact path
+  } else if (!(opacity <= 0.0f)) {
+    // NaN opacity, a parameter without a bound, or a beta activation that
+    // keeps every alpha below 1/255: always the exact path
     cut = __int_as_float(0x7fc00000);
     bx0 = -3.0e38f; bx1 = 3.0e38f; by0 = -3.0e38f; by1 = 3.0e38f;
   }
@@ -221,7 +244,7 @@ __global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams 
   rec[3] = make_float4(nx, ny, nz, __uint_as_float(ap));
   rec[4] = make_float4(su0, su1, su2, sv0);
   rec[5] = make_float4(sv1, sv2, pk0, pk1);
-  rec[6] = make_float4(pk2, cut, 0.f, vz);
+  rec[6] = make_float4(pk2, cut, shape, vz);
   rec[7] = make_float4(bx0, bx1, by0, by1);
 }
 

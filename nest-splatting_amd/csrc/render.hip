@@ -440,8 +440,32 @@ struct SplatHit {
   bool use3d;
 };
 
+// kernel_type 1-3 (CR/forward.cu:864-900): alpha from the beta kernel
+// opacity * (1 - rho)^shape (rho < 1 only), the Gaussian with the splat's own
+// beta activation (float arithmetic, as the reference writes it), or the
+// general kernel exp(-0.5 * max(rho, 1e-8)^(shape / 2)).  Returns G, or -1
+// for a rejected pair.
+__device__ __forceinline__ float kernel_g(int kt, float rho, float shape) {
+  if (kt == 1) {
+    if (rho >= 1.0f) return -1.0f;
+    return powf_ref(1.0f - rho, shape);
+  }
+  if (kt == 2) {
+    const float power = -0.5f * rho;
+    if (power > 0.0f) return -1.0f;
+    float G = expf_ref(power);
+    if (shape > 0.0f) G = (1.0f + shape) * G / (1.0f + shape * G);
+    return G;
+  }
+  const float exponent = 0.5f * shape;
+  const float pow_term = powf_ref(fmaxf(rho, 1e-8f), exponent);
+  const float power = -0.5f * pow_term;
+  if (power > 0.0f) return -1.0f;
+  return expf_ref(power);
+}
+
 __device__ __forceinline__ bool splat_hit(float4 q0, float4 q1, float4 q2, float cut, float pxf, float pyf, float beta,
-                                          SplatHit& h) {
+                                          SplatHit& h, int kt = 0, const float& shape = 0.0f) {
   const float Tu0 = q0.x, Tu1 = q0.y, Tu2 = q0.z, Tv0 = q0.w;
   const float Tv1 = q1.x, Tv2 = q1.y, Tw0 = q1.z, Tw1 = q1.w;
   const float Tw2 = q2.x;
@@ -465,12 +489,18 @@ __device__ __forceinline__ bool splat_hit(float4 q0, float4 q1, float4 q2, float
   const bool use3d = rho3d <= rho2d;
   const float depth = use3d ? (sx * Tw0 + sy * Tw1) + Tw2 : Tw2;
   if (depth < 0.2f) return false;
-  const float power = -0.5f * rho;
-  if (power > 0.0f) return false;
-  float G = expf_ref(power);
-  // (1.0 + beta) * G / (1.0 + beta * G) with float beta and G (CR/forward.cu:915-916): the product
-  // beta * G is a float product, the rest double
-  if (beta > 0.0f) G = (float)((1.0 + (double)beta) * (double)G / (1.0 + (double)(beta * G)));
+  float G;
+  if (kt == 0) {
+    const float power = -0.5f * rho;
+    if (power > 0.0f) return false;
+    G = expf_ref(power);
+    // (1.0 + beta) * G / (1.0 + beta * G) with float beta and G (CR/forward.cu:915-916): the product
+    // beta * G is a float product, the rest double
+    if (beta > 0.0f) G = (float)((1.0 + (double)beta) * (double)G / (1.0 + (double)(beta * G)));
+  } else {
+    G = kernel_g(kt, rho, shape);
+    if (G < 0.0f) return false;  // a NaN G goes on, as in the reference (alpha = fminf(0.99, NaN))
+  }
   const float alpha = fminf(0.99f, q2.w * G);
   if (alpha < 1.0f / 255.0f) return false;
   h.sx = sx;
@@ -557,7 +587,9 @@ __device__ __forceinline__ void appearance_colour(uint32_t ap, float w, float& v
 // per-splat features ahead of the grid's; the
 // queue then carries a 32-bit meta word per hit (drain_mixed) in place of
 // the level count, 53 KB of LDS in all.
-template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0>
+// kKT: the splats' kernel comes from p.kernel_type (1-3 possible); without
+// it the kernel is the Gaussian, and the kernel-type branch compiles out.
+template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0, bool kKT = false>
 __global__ void __launch_bounds__(kRenderThreads) __attribute__((amdgpu_waves_per_eu(3, 8)))
 render_kernel(const RenderParams p) {
   __shared__ float4 srec[kRecChunks][kBatch];
@@ -616,7 +648,7 @@ render_kernel(const RenderParams p) {
         const float4* rec = reinterpret_cast<const float4*>(p.records) + 8 * (size_t)id;
 #pragma unroll
         for (int c = 0; c < kRecChunks; c++) srec[c][threadIdx.x] = rec[c];
-        srec[6][threadIdx.x].z = __uint_as_float(id);
+        srec[6][threadIdx.x].w = __uint_as_float(id);  // the depth's slot: the render recomputes depth per hit
       }
       __syncthreads();
       n = min((uint32_t)kBatch, range.y - start);
@@ -633,7 +665,9 @@ render_kernel(const RenderParams p) {
         const float4 bb = srec[7][j];
         if (bb.y < wx0 || bb.x > wx1 || bb.w < wy0 || bb.z > wy1) break;
         SplatHit hit;
-        if (!splat_hit(srec[0][j], srec[1][j], srec[2][j], srec[6][j].y, pxf, pyf, p.beta, hit)) break;
+        if (!splat_hit(srec[0][j], srec[1][j], srec[2][j], srec[6][j].y, pxf, pyf, p.beta, hit,
+                       kKT ? p.kernel_type : 0, srec[6][j].z))
+          break;
         const float test_T = T * (1 - hit.alpha);
         if (test_T < 0.0001f) {
           done = true;
@@ -667,7 +701,7 @@ render_kernel(const RenderParams p) {
           break;
         }
         if constexpr (!kHash) {
-          const uint32_t id = __float_as_uint(srec[6][j].z);
+          const uint32_t id = __float_as_uint(srec[6][j].w);
           const float* col = p.colors + (size_t)id * p.C;
 #pragma unroll
           for (int c = 0; c < NACC; c++)
@@ -706,7 +740,7 @@ render_kernel(const RenderParams p) {
         // with one coalesced load (lane k holds entry k), then broadcast lane by
         // lane; a lane's grid lookups go to its queue.
         if (__ballot(ph.on) != 0ull) {
-          const uint32_t id = __builtin_amdgcn_readfirstlane(__float_as_uint(srec[6][j].z));
+          const uint32_t id = __builtin_amdgcn_readfirstlane(__float_as_uint(srec[6][j].w));
           const float* row = p.colors + (size_t)id * (uint32_t)p.cstride;
           const uint32_t lane = threadIdx.x & (kWaveLanes - 1);
           float mine = lane < (uint32_t)p.nrow ? row[lane] : 0.0f;
@@ -823,8 +857,8 @@ render_kernel(const RenderParams p) {
 // summed across the wave and added with one atomic per counter (the same sums
 // in another order; the counts are exact).
 __global__ void __launch_bounds__(kRenderThreads) record_transmittance_kernel(const RenderParams p) {
-  __shared__ float4 sgeo[4][kBatch];  // record chunks 0-2 (transform, xy, opacity) and 7 (acceptance bbox)
-  __shared__ float2 scut[kBatch];     // chunk 6: rho cut (x) and splat id bits (y)
+  __shared__ float4 sgeo[5][kBatch];  // record chunks 0-2 (transform, xy, opacity), 7 (acceptance bbox) and 6
+                                      // (rho cut in y, kernel shape in z, the splat id bits in w)
   const uint32_t tile = blockIdx.x;
   const uint32_t tx = tile % p.gx, ty = tile / p.gx;
   const uint32_t px = tx * kTile + (threadIdx.x & 15u);
@@ -848,7 +882,8 @@ __global__ void __launch_bounds__(kRenderThreads) record_transmittance_kernel(co
       sgeo[1][threadIdx.x] = rec[1];
       sgeo[2][threadIdx.x] = rec[2];
       sgeo[3][threadIdx.x] = rec[7];
-      scut[threadIdx.x] = make_float2(rec[6].y, __uint_as_float(id));
+      const float4 r6 = rec[6];
+      sgeo[4][threadIdx.x] = make_float4(r6.x, r6.y, r6.z, __uint_as_float(id));
     }
     __syncthreads();
     const uint32_t n = min((uint32_t)kBatch, range.y - start);
@@ -860,7 +895,9 @@ __global__ void __launch_bounds__(kRenderThreads) record_transmittance_kernel(co
           const float4 bb = sgeo[3][j];
           if (bb.y < wx0 || bb.x > wx1 || bb.w < wy0 || bb.z > wy1) break;
           SplatHit hit;
-          if (!splat_hit(sgeo[0][j], sgeo[1][j], sgeo[2][j], scut[j].x, pxf, pyf, p.beta, hit)) break;
+          if (!splat_hit(sgeo[0][j], sgeo[1][j], sgeo[2][j], sgeo[4][j].y, pxf, pyf, p.beta, hit, p.kernel_type,
+                         sgeo[4][j].z))
+            break;
           const float test_T = T * (1 - hit.alpha);
           if (test_T < 0.0001f) {
             done = true;
@@ -879,7 +916,7 @@ __global__ void __launch_bounds__(kRenderThreads) record_transmittance_kernel(co
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, kWaveLanes);
         if (lane == 0u) {
-          const uint32_t id = __float_as_uint(scut[j].y);
+          const uint32_t id = __float_as_uint(sgeo[4][j].w);
           atomicAdd(p.cover_pixels + id, (float)__popcll(m));
           atomicAdd(p.trans_avg + id, sum);
         }
@@ -889,22 +926,22 @@ __global__ void __launch_bounds__(kRenderThreads) record_transmittance_kernel(co
   }
 }
 
-template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0>
+template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0, bool kKT = false>
 static hipError_t launch_one(const RenderParams& p, hipStream_t s) {
-  hipLaunchKernelGGL((render_kernel<F, NACC, kHash, kHalf, kStructured, kMix>), dim3(p.ntiles), dim3(kRenderThreads),
-                     0, s, p);
+  hipLaunchKernelGGL((render_kernel<F, NACC, kHash, kHalf, kStructured, kMix, kKT>), dim3(p.ntiles),
+                     dim3(kRenderThreads), 0, s, p);
   return hipGetLastError();
 }
 
-template <int F, bool kHalf, bool kStructured>
+template <int F, bool kHalf, bool kStructured, bool kKT>
 static hipError_t launch_hash_levels(const RenderParams& p, hipStream_t s) {
   const uint32_t L = p.grid.L;
   if constexpr (F * 8 <= NEST_MAX_CHANNELS)
-    if (L <= 8) return launch_one<F, F * 8, true, kHalf, kStructured>(p, s);
+    if (L <= 8) return launch_one<F, F * 8, true, kHalf, kStructured, 0, kKT>(p, s);
   if constexpr (F * 16 <= NEST_MAX_CHANNELS)
-    if (L <= 16) return launch_one<F, F * 16, true, kHalf, kStructured>(p, s);
+    if (L <= 16) return launch_one<F, F * 16, true, kHalf, kStructured, 0, kKT>(p, s);
   if constexpr (F * 32 <= NEST_MAX_CHANNELS)
-    if (L <= 32) return launch_one<F, F * 32, true, kHalf, kStructured>(p, s);
+    if (L <= 32) return launch_one<F, F * 32, true, kHalf, kStructured, 0, kKT>(p, s);
   return hipErrorInvalidValue;
 }
 
@@ -983,45 +1020,68 @@ __global__ void level_quads_kernel(LevelQuads lq, uint32_t L, LevelQuad* dst) {
 
 // Accumulators of the per-splat feature modes: the output levels the mode
 // writes (hyb + L, or the row's levels in mode 13), 32 or 64 channels.
-template <int F, bool kHalf, bool kStructured>
+template <int F, bool kHalf, bool kStructured, bool kKT>
 static hipError_t launch_mix_levels(const RenderParams& p, hipStream_t s) {
   const uint32_t need = (uint32_t)p.pgd + (p.grid.L > p.nfast ? p.grid.L : p.nfast) * (uint32_t)F;
   // mode 14 (grid levels times the weight) has its own drains
   if (p.gscale) {
-    if (need <= 32u) return launch_one<F, 32, true, kHalf, kStructured, 2>(p, s);
-    if (need <= 64u) return launch_one<F, 64, true, kHalf, kStructured, 2>(p, s);
+    if (need <= 32u) return launch_one<F, 32, true, kHalf, kStructured, 2, kKT>(p, s);
+    if (need <= 64u) return launch_one<F, 64, true, kHalf, kStructured, 2, kKT>(p, s);
     return hipErrorInvalidValue;
   }
-  if (need <= 32u) return launch_one<F, 32, true, kHalf, kStructured, 1>(p, s);
-  if (need <= 64u) return launch_one<F, 64, true, kHalf, kStructured, 1>(p, s);
+  if (need <= 32u) return launch_one<F, 32, true, kHalf, kStructured, 1, kKT>(p, s);
+  if (need <= 64u) return launch_one<F, 64, true, kHalf, kStructured, 1, kKT>(p, s);
   return hipErrorInvalidValue;
 }
 
-template <int F, bool kHalf>
+// kKT (kernel types 1-3) takes the general lookup path only.
+template <int F, bool kHalf, bool kKT>
 static hipError_t launch_hash(const RenderParams& p, hipStream_t s) {
-  if (!p.grid.structured) {
+  if (kKT || !p.grid.structured) {
     if constexpr (F >= 2) {
-      if (p.mix) return launch_mix_levels<F, kHalf, false>(p, s);
+      if (p.mix) return launch_mix_levels<F, kHalf, false, kKT>(p, s);
     }
-    return launch_hash_levels<F, kHalf, false>(p, s);
+    return launch_hash_levels<F, kHalf, false, kKT>(p, s);
   }
-  const GridParams& g = p.grid;
-  LevelQuads lq = {};
-  for (uint32_t l = 0; l < g.L; l++) {
-    LevelQuad& q = lq.q[l];
-    q.scale = g.lv.scale[l];
-    const bool dense = l < g.n_dense;
-    q.a = dense ? g.lv.res1[l] : g.lv.hsize[l] - 1u;
-    q.b = dense ? g.lv.res1[l] * g.lv.res1[l] : 0u;
-    q.soff = g.lv.base[l] * (uint32_t)(F * (kHalf ? 2 : 4));
+  if constexpr (!kKT) {
+    const GridParams& g = p.grid;
+    LevelQuads lq = {};
+    for (uint32_t l = 0; l < g.L; l++) {
+      LevelQuad& q = lq.q[l];
+      q.scale = g.lv.scale[l];
+      const bool dense = l < g.n_dense;
+      q.a = dense ? g.lv.res1[l] : g.lv.hsize[l] - 1u;
+      q.b = dense ? g.lv.res1[l] * g.lv.res1[l] : 0u;
+      q.soff = g.lv.base[l] * (uint32_t)(F * (kHalf ? 2 : 4));
+    }
+    hipLaunchKernelGGL(level_quads_kernel, dim3(1), dim3(64), 0, s, lq, g.L, g.lq);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if constexpr (F >= 2) {
+      if (p.mix) return launch_mix_levels<F, kHalf, true, false>(p, s);
+    }
+    return launch_hash_levels<F, kHalf, true, false>(p, s);
   }
-  hipLaunchKernelGGL(level_quads_kernel, dim3(1), dim3(64), 0, s, lq, g.L, g.lq);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if constexpr (F >= 2) {
-    if (p.mix) return launch_mix_levels<F, kHalf, true>(p, s);
+  return hipErrorInvalidValue;
+}
+
+template <bool kKT>
+static hipError_t launch_render_kind(const RenderParams& p, hipStream_t s) {
+  if (p.level == 0 && !p.mix) {
+    if (p.C <= 3) return launch_one<1, 3, false, false, false, 0, kKT>(p, s);
+    if (p.C <= 16) return launch_one<1, 16, false, false, false, 0, kKT>(p, s);
+    if (p.C <= 32) return launch_one<1, 32, false, false, false, 0, kKT>(p, s);
+    if (p.C <= 64) return launch_one<1, 64, false, false, false, 0, kKT>(p, s);
+    return launch_one<1, 128, false, false, false, 0, kKT>(p, s);
   }
-  return launch_hash_levels<F, kHalf, true>(p, s);
+  const bool half = p.grid.half != 0;
+  switch (p.grid.F) {
+    case 1: return half ? launch_hash<1, true, kKT>(p, s) : launch_hash<1, false, kKT>(p, s);
+    case 2: return half ? launch_hash<2, true, kKT>(p, s) : launch_hash<2, false, kKT>(p, s);
+    case 4: return half ? launch_hash<4, true, kKT>(p, s) : launch_hash<4, false, kKT>(p, s);
+    case 8: return half ? launch_hash<8, true, kKT>(p, s) : launch_hash<8, false, kKT>(p, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 static hipError_t launch_render_kernel(const RenderParams& p, hipStream_t s);
@@ -1040,21 +1100,7 @@ static hipError_t launch_render_kernel(const RenderParams& p, hipStream_t s) {
   const hipError_t oe = hipGetLastError();
   if (oe != hipSuccess) return oe;
   if (p.mix && p.grid.F == 1) return hipErrorInvalidValue;
-  if (p.level == 0 && !p.mix) {
-    if (p.C <= 3) return launch_one<1, 3, false, false>(p, s);
-    if (p.C <= 16) return launch_one<1, 16, false, false>(p, s);
-    if (p.C <= 32) return launch_one<1, 32, false, false>(p, s);
-    if (p.C <= 64) return launch_one<1, 64, false, false>(p, s);
-    return launch_one<1, 128, false, false>(p, s);
-  }
-  const bool half = p.grid.half != 0;
-  switch (p.grid.F) {
-    case 1: return half ? launch_hash<1, true>(p, s) : launch_hash<1, false>(p, s);
-    case 2: return half ? launch_hash<2, true>(p, s) : launch_hash<2, false>(p, s);
-    case 4: return half ? launch_hash<4, true>(p, s) : launch_hash<4, false>(p, s);
-    case 8: return half ? launch_hash<8, true>(p, s) : launch_hash<8, false>(p, s);
-    default: return hipErrorInvalidValue;
-  }
+  return p.kernel_type != 0 ? launch_render_kind<true>(p, s) : launch_render_kind<false>(p, s);
 }
 
 }  // namespace nest

@@ -110,8 +110,11 @@ class _RasterizeGaussians(torch.autograd.Function):
                                       f"7 (adaptive_add) and "
                                       f"12 / 13 / 14 (adaptive_cat / adaptive_cat_fast / adaptive_zero, | 0x100 "
                                       f"inference)")
-        if kernel_type != 0:
-            raise NotImplementedError(f"kernel_type {kernel_type}: only the Gaussian kernel (0) is implemented")
+        if kernel_type not in (0, 1, 2, 3):
+            raise NotImplementedError(f"kernel_type {kernel_type}: implemented are 0 (Gaussian), 1 (beta), 2 (flex) "
+                                      f"and 3 (general)")
+        if kernel_type != 0 and _empty(shapes):
+            raise ValueError(f"kernel_type {kernel_type} needs shapes [P] (CR/forward.cu:864-900)")
         if not _empty(cov3Ds_precomp):
             raise NotImplementedError("precomputed transforms (cov3D_precomp) are not implemented")
         if not _empty(features_diffuse):
@@ -160,9 +163,12 @@ class _RasterizeGaussians(torch.autograd.Function):
                                     ap_level=None if _empty(ap_level) else ap_level.detach(), colors_precomp=colors,
                                     channels=C, shs=None if (level > 0 or colors is not None or _empty(sh)) else
                                     sh.detach(), sh_degree=int(raster_settings.sh_degree),
-                                    record_transmittance=bool(raster_settings.record_transmittance))
+                                    record_transmittance=bool(raster_settings.record_transmittance),
+                                    shapes=None if kernel_type == 0 else shapes.detach().reshape(-1),
+                                    kernel_type=int(kernel_type))
         ctx.num_rendered = res.num_rendered
         ctx.render_mode = render_mode
+        ctx.kernel_type = int(kernel_type)
         ctx.fw = dict(res=res, settings=settings, grid=grid, C=C, colors=colors,
                       shs=None if (level > 0 or colors is not None or _empty(sh)) else sh.detach(),
                       sh_degree=int(raster_settings.sh_degree),
@@ -181,6 +187,9 @@ class _RasterizeGaussians(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out_color, grad_radii, grad_depth, grad_0, grad_1):
+        if ctx.kernel_type != 0:
+            raise NotImplementedError(f"kernel_type {ctx.kernel_type} is forward-only here; the backward covers the "
+                                      f"Gaussian kernel (0)")
         if ctx.render_mode not in (0, 4, 7, 12, 14):
             raise NotImplementedError(f"render_mode {ctx.render_mode} is forward-only here; "
                                       f"the backward covers modes 0, 4, 7, 12 and 14 (training)")

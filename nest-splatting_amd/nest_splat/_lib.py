@@ -27,7 +27,7 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 SCAN_NOALLOC_MAX = 268431360
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
  GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
@@ -72,7 +72,8 @@ class Splats(ct.Structure):
     _fields_ = [("struct_size", ct.c_uint32), ("P", ct.c_int32), ("means3D", ct.c_void_p), ("scales", ct.c_void_p),
                 ("rotations", ct.c_void_p), ("opacities", ct.c_void_p), ("homotrans", ct.c_void_p),
                 ("ap_level", ct.c_void_p), ("colors_precomp", ct.c_void_p), ("shs", ct.c_void_p),
-                ("sh_degree", ct.c_int32), ("sh_coeffs", ct.c_int32)]
+                ("sh_degree", ct.c_int32), ("sh_coeffs", ct.c_int32), ("shapes", ct.c_void_p),
+                ("kernel_type", ct.c_int32), ("reserved", ct.c_int32)]
 
 
 class FrameOutputs(ct.Structure):

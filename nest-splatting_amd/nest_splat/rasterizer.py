@@ -172,7 +172,7 @@ def _contig_f32(t: Optional[torch.Tensor], name: str) -> Optional[torch.Tensor]:
 
 
 def _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, channels, shs, sh_degree,
-            row_width=None):
+            row_width=None, shapes=None, kernel_type=0):
     """nest_splats over the device tensors (re-aligned copies where needed);
     returns (struct, tensors kept alive for the call)."""
     if means3D.ndim != 2 or means3D.shape[1] != 3:
@@ -186,7 +186,10 @@ def _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_p
     ap_level = _contig_f32(ap_level, "ap_level")
     colors_precomp = _contig_f32(colors_precomp, "colors_precomp")
     shs = _contig_f32(shs, "shs") if shs is not None and shs.numel() > 0 else None
+    shapes = _contig_f32(shapes, "shapes") if kernel_type != 0 else None
     if P > 0:
+        if kernel_type != 0 and (shapes is None or shapes.numel() != P):
+            raise ValueError(f"kernel_type {kernel_type} needs shapes with P elements")
         for t, n, k in ((scales, "scales", 2), (rotations, "rotations", 4)):
             if t is None or t.numel() != P * k:
                 raise ValueError(f"{n} must have {P}x{k} elements")
@@ -215,26 +218,30 @@ def _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_p
     sp.shs = L.ptr(shs)
     sp.sh_degree = int(sh_degree)
     sp.sh_coeffs = int(shs.numel() // (3 * P)) if shs is not None and P > 0 else 0
-    return sp, (means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, shs)
+    sp.shapes = L.ptr(shapes)
+    sp.kernel_type = int(kernel_type)
+    return sp, (means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, shs, shapes)
 
 
 def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: torch.Tensor, opacities: torch.Tensor,
                       scales: torch.Tensor, rotations: torch.Tensor, homotrans: Optional[torch.Tensor] = None,
                       ap_level: Optional[torch.Tensor] = None, colors_precomp: Optional[torch.Tensor] = None,
                       channels: int = 3, timing: bool = False, shs: Optional[torch.Tensor] = None,
-                      sh_degree: int = 0, record_transmittance: bool = False) -> ForwardResult:
+                      sh_degree: int = 0, record_transmittance: bool = False, shapes: Optional[torch.Tensor] = None,
+                      kernel_type: int = 0) -> ForwardResult:
     """One forward frame.  The colour path (grid.levels == 0 in render mode
     0) takes colours from colors_precomp, or, when it is None, evaluates them
     from shs [P, M, 3] at degree sh_degree in preprocess (3 channels).  In
     render modes 4 and 13 colors_precomp holds the per-splat feature rows
     (grid.row_width floats each).  record_transmittance fills
     cover_pixels / trans_avg (DSR/rasterize_points.cu:169-171,
-    CR/forward.cu:1961-1964)."""
+    CR/forward.cu:1961-1964).  kernel_type 1 (beta), 2 (flex) or 3 (general)
+    takes the per-splat parameter from shapes [P] (CR/forward.cu:864-900)."""
     dev = means3D.device
     P = int(means3D.shape[0])
     H, W = settings.image_height, settings.image_width
     sp, keep = _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, channels, shs,
-                       sh_degree, grid.row_width(channels))
+                       sh_degree, grid.row_width(channels), shapes=shapes, kernel_type=kernel_type)
     g = grid.to_c()
 
     color = torch.empty((channels, H, W), dtype=torch.float32, device=dev)

@@ -89,6 +89,66 @@ float or_expf(float x)
     return y * bits_to_f((uint32_t)(k + 127) << 23);
 }
 
+/* log(x) for binary32 (Moshier, Methods and Programs for Mathematical
+ * Functions, 1989): x = m 2^e with m in [sqrt(1/2), sqrt(2)), f = m - 1,
+ * log(1 + f) = f - f^2/2 + f^3 P(f) with a degree-8 minimax P, plus e ln2 in
+ * a 9-bit head and a tail.  0 gives -inf, negatives NaN, +inf and NaN
+ * themselves; subnormals are scaled by 2^23 first. */
+float or_logf(float x)
+{
+    if (!(x > 0.0f)) return x == 0.0f ? -INFINITY : NAN;
+    if (x == INFINITY) return x;
+    uint32_t u = f_to_bits(x);
+    int e = 0;
+    if (u < 0x00800000u) {
+        u = f_to_bits(x * 8388608.0f);
+        e = -23;
+    }
+    e += (int)((u >> 23) & 0xffu) - 126;
+    float m = bits_to_f((u & 0x007fffffu) | 0x3f000000u);
+    if (m < 0.707106781186547524f) {
+        e -= 1;
+        m = m + m - 1.0f;
+    } else {
+        m = m - 1.0f;
+    }
+    float z = m * m;
+    float y = 7.0376836292e-2f;
+    y = y * m + -1.1514610310e-1f;
+    y = y * m + 1.1676998740e-1f;
+    y = y * m + -1.2420140846e-1f;
+    y = y * m + 1.4249322787e-1f;
+    y = y * m + -1.6668057665e-1f;
+    y = y * m + 2.0000714765e-1f;
+    y = y * m + -2.4999993993e-1f;
+    y = y * m + 3.3333331174e-1f;
+    y = y * m * z;
+    float fe = (float)e;
+    y = y + -2.12194440e-4f * fe;
+    y = y + -0.5f * z;
+    float r = m + y;
+    r = r + 0.693359375f * fe;
+    return r;
+}
+
+/* x^y for x >= 0 as or_expf(y * or_logf(x)); y == 0 gives 1.  Not
+ * correctly rounded: the relative error grows with |y log x|. */
+float or_powf(float x, float y)
+{
+    if (y == 0.0f) return 1.0f;
+    return or_expf(y * or_logf(x));
+}
+
+void or_logf_n(int n, const float *x, float *y)
+{
+    for (int i = 0; i < n; i++) y[i] = or_logf(x[i]);
+}
+
+void or_powf_n(int n, const float *x, const float *e, float *y)
+{
+    for (int i = 0; i < n; i++) y[i] = or_powf(x[i], e[i]);
+}
+
 /* or_expf over an array (for the tests' float32 replicas of the render). */
 void or_expf_n(int n, const float *x, float *y)
 {
@@ -645,6 +705,12 @@ typedef struct {
      * leave it first) adds 1 and the transmittance before it. */
     float *cover_pixels;
     float *trans_avg;
+    /* kernel_type (forward.cu:864-921): 0 Gaussian (with the global beta),
+     * 1 beta opacity * (1 - rho)^shape for rho < 1, 2 flex (Gaussian with the
+     * splat's own beta, float arithmetic), 3 general
+     * exp(-0.5 * max(rho, 1e-8)^(shape / 2)); shapes [P] for 1-3. */
+    const float *shapes;
+    int kernel_type;
 } or_render_args;
 
 static void record_hit(const or_render_args *A, uint32_t id, float T)
@@ -723,11 +789,29 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
         float depth = use3d ? (sx * Tw0 + sy * Tw1) + Tw2 : Tw2;
         if (depth < OR_NEAR) continue;
         const float *no = A->normal_opacity + 4 * (size_t)id;
-        float power = -0.5f * rho;
-        if (power > 0.0f) continue;
-        float G = or_expf(power);
-        /* (1.0 + beta) * G / (1.0 + beta * G): beta * G is a float product (forward.cu:915-916) */
-        if (A->beta > 0.0f) G = (float)((1.0 + (double)A->beta) * (double)G / (1.0 + (double)(A->beta * G)));
+        float G;
+        if (A->kernel_type == 1) {
+            if (rho >= 1.0f) continue;
+            G = or_powf(1.0f - rho, A->shapes[id]);
+        } else if (A->kernel_type == 2) {
+            float power = -0.5f * rho;
+            if (power > 0.0f) continue;
+            G = or_expf(power);
+            const float b = A->shapes[id];
+            if (b > 0.0f) G = (1.0f + b) * G / (1.0f + b * G);
+        } else if (A->kernel_type == 3) {
+            const float exponent = 0.5f * A->shapes[id];
+            const float pow_term = or_powf(fmaxf(rho, 1e-8f), exponent);
+            float power = -0.5f * pow_term;
+            if (power > 0.0f) continue;
+            G = or_expf(power);
+        } else {
+            float power = -0.5f * rho;
+            if (power > 0.0f) continue;
+            G = or_expf(power);
+            /* (1.0 + beta) * G / (1.0 + beta * G): beta * G is a float product (forward.cu:915-916) */
+            if (A->beta > 0.0f) G = (float)((1.0 + (double)A->beta) * (double)G / (1.0 + (double)(A->beta * G)));
+        }
         float alpha = fminf(0.99f, no[3] * G);
         if (alpha < 1.0f / 255.0f) continue;
         float test_T = T * (1 - alpha);

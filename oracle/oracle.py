@@ -46,7 +46,7 @@ class OrRenderArgs(ct.Structure):
                 ("ap_level", ct.c_void_p), ("colors", ct.c_void_p), ("grid", OrGrid),
                 ("out_color", ct.c_void_p), ("out_others", ct.c_void_p), ("final_T", ct.c_void_p),
                 ("n_contrib", ct.c_void_p), ("render_mode", ct.c_int), ("cover_pixels", ct.c_void_p),
-                ("trans_avg", ct.c_void_p)]
+                ("trans_avg", ct.c_void_p), ("shapes", ct.c_void_p), ("kernel_type", ct.c_int)]
 
 
 class OrRenderBwdArgs(ct.Structure):
@@ -70,6 +70,12 @@ def lib():
         L.or_expf.restype = ct.c_float
         L.or_expf.argtypes = [ct.c_float]
         L.or_expf_n.argtypes = [ct.c_int, f32p, f32p]
+        L.or_logf.restype = ct.c_float
+        L.or_logf.argtypes = [ct.c_float]
+        L.or_powf.restype = ct.c_float
+        L.or_powf.argtypes = [ct.c_float, ct.c_float]
+        L.or_logf_n.argtypes = [ct.c_int, f32p, f32p]
+        L.or_powf_n.argtypes = [ct.c_int, f32p, f32p, f32p]
         L.or_round_bf16.restype = ct.c_float
         L.or_round_bf16.argtypes = [ct.c_float]
         L.or_round_f16.restype = ct.c_float
@@ -114,6 +120,21 @@ def expf(x) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty_like(x)
     lib().or_expf_n(x.size, x.reshape(-1), y.reshape(-1))
+    return y
+
+
+def logf(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().or_logf_n(x.size, x.reshape(-1), y.reshape(-1))
+    return y
+
+
+def powf(x, e) -> np.ndarray:
+    x, e = np.broadcast_arrays(np.asarray(x, np.float32), np.asarray(e, np.float32))
+    x, e = np.ascontiguousarray(x), np.ascontiguousarray(e)
+    y = np.empty_like(x)
+    lib().or_powf_n(x.size, x.reshape(-1), e.reshape(-1), y.reshape(-1))
     return y
 
 
@@ -201,13 +222,14 @@ def make_grid(L, F, S, H, offsets, table, gridrange, contract=False, align_corne
 
 def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_level=None, colors=None,
            beta=0.0, max_intersections=0, row_stride=1, row_phase=0, threads=0, render_mode=0, level=None,
-           record_transmittance=False):
+           record_transmittance=False, shapes=None, kernel_type=0):
     """renderCUDAsurfelForward for every pixel.  render_mode 0 (grid levels
     grid.L, or the colour path without a grid), 4, 7, 12, 13 or 14 (bit 8:
     inference); for modes 4, 7, 12, 13 and 14, level is the reference's packed level argument
     (total << 16 | hash levels << 8 | per-splat levels) and colors the
     per-splat feature rows.  record_transmittance adds cover_pixels and
-    trans_avg ([P] each) to the result."""
+    trans_avg ([P] each) to the result.  kernel_type 1-3 take the per-splat
+    parameter from shapes [P]."""
     HW = W * H
     out = dict(color=np.zeros((C, H, W), np.float32), others=np.zeros((14, H, W), np.float32),
                final_T=np.zeros((3, H, W), np.float32), n_contrib=np.zeros((2, H, W), np.uint32))
@@ -247,6 +269,9 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
     if record_transmittance:
         args.cover_pixels = out["cover_pixels"].ctypes.data
         args.trans_avg = out["trans_avg"].ctypes.data
+    args.kernel_type = kernel_type
+    if kernel_type != 0:
+        args.shapes = ptr(np.asarray(shapes, np.float32).reshape(-1), np.float32)
     lib().or_render(ct.byref(args), row_stride, row_phase, threads)
     return out
 

@@ -47,7 +47,7 @@ def test_struct_sizes_match_c_layout():
     L = _lib()
     assert ct.sizeof(L.RasterSettings) == 4 * (6 + 16 + 16 + 3 + 1 + 4)
     assert ct.sizeof(L.HashGrid) % 8 == 0
-    assert ct.sizeof(L.Splats) == 8 + 8 * 8 + 8
+    assert ct.sizeof(L.Splats) == 8 + 9 * 8 + 16
     assert ct.sizeof(L.FrameOutputs) == 8 + 5 * 8
     assert ct.sizeof(L.Mlp) == 16 + 3 * 8
     assert ct.sizeof(L.BackwardIO) == 8 + 11 * 8

@@ -17,7 +17,8 @@ pytestmark = pytest.mark.gpu
 SCENES = ["cfg1", "shell_small", "unbounded_small", "shells_small"]
 
 
-def run_gpu(sc, cam_index=0, max_intersections=0, align_corners=False, interp=0, beta=0.0, record=False):
+def run_gpu(sc, cam_index=0, max_intersections=0, align_corners=False, interp=0, beta=0.0, record=False,
+            kernel_type=0, shapes=None):
     from nest_splat import rasterizer as rz
     sp = sc.spec
     cam = sc.cameras[cam_index]
@@ -30,12 +31,14 @@ def run_gpu(sc, cam_index=0, max_intersections=0, align_corners=False, interp=0,
                            align_corners=align_corners, interpolation=interp)
     res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
                                homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), channels=sp.C,
-                               record_transmittance=record)
+                               record_transmittance=record, kernel_type=kernel_type,
+                               shapes=None if shapes is None else t(shapes))
     torch.cuda.synchronize()
     return res
 
 
-def run_oracle(O, sc, cam_index=0, max_intersections=0, align_corners=False, interp=0, beta=0.0, record=False):
+def run_oracle(O, sc, cam_index=0, max_intersections=0, align_corners=False, interp=0, beta=0.0, record=False,
+               kernel_type=0, shapes=None):
     sp = sc.spec
     cam = sc.cameras[cam_index]
     W, H = cam.image_width, cam.image_height
@@ -45,7 +48,8 @@ def run_oracle(O, sc, cam_index=0, max_intersections=0, align_corners=False, int
     grid = O.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract,
                        align_corners=align_corners, interp=interp)
     r = O.render(pre, b, W, H, sp.C, grid, homotrans=sc.homotrans, ap_level=sc.ap_level,
-                 max_intersections=max_intersections, beta=beta, record_transmittance=record)
+                 max_intersections=max_intersections, beta=beta, record_transmittance=record,
+                 kernel_type=kernel_type, shapes=shapes)
     return pre, b, r
 
 
@@ -277,3 +281,43 @@ def test_record_transmittance_colour_path(oracle):
     b = oracle.binning(pre, W, H)
     r = oracle.render(pre, b, W, H, 3, None, colors=cols, record_transmittance=True)
     check_record(res, r)
+
+
+def _shapes(kt, P, seed):
+    """Per-splat kernel parameters in the ranges the reference trains them in:
+    beta-kernel shapes around 1-4, flex betas 0-2 (some exactly 0), general
+    exponents 2-8 (plus a few below 2)."""
+    rng = np.random.default_rng(seed)
+    if kt == 1:
+        return rng.uniform(0.2, 4.0, P).astype(np.float32)
+    if kt == 2:
+        v = rng.uniform(0.0, 2.0, P).astype(np.float32)
+        v[::7] = 0.0
+        return v
+    v = rng.uniform(2.0, 8.0, P).astype(np.float32)
+    v[::9] = rng.uniform(0.8, 2.0, v[::9].shape).astype(np.float32)
+    return v
+
+
+@pytest.mark.parametrize("name,kt", [("cfg1", 1), ("shell_small", 2), ("unbounded_small", 3), ("shell_small", 1),
+                                     ("cfg1", 3)])
+def test_kernel_types_parity(oracle, name, kt):
+    """kernel_type 1 (beta), 2 (flex) and 3 (general) (CR/forward.cu:864-900):
+    the frame bit-exact against the oracle, the preprocess bounds of the
+    render's early rejects conservative (no hit missed), and the
+    transmittance record with them."""
+    sc = scene(name)
+    shapes = _shapes(kt, sc.spec.P, kt * 31 + len(name))
+    print(f"[case] kernel_type {kt} {name}", flush=True)
+    res = run_gpu(sc, kernel_type=kt, shapes=shapes, record=True)
+    pre, b, r = run_oracle(oracle, sc, kernel_type=kt, shapes=shapes, record=True)
+    from nest_splat import rasterizer as rz
+    W, H = r["color"].shape[2], r["color"].shape[1]
+    ba = {k: v.cpu().numpy() for k, v in rz.binning_arrays(res, W, H).items()}
+    np.testing.assert_array_equal(res.others.cpu().numpy(), r["others"])
+    np.testing.assert_array_equal(ba["n_contrib"].view(np.uint32), r["n_contrib"])
+    np.testing.assert_array_equal(ba["final_T"], r["final_T"])
+    np.testing.assert_array_equal(res.color.cpu().numpy(), r["color"])
+    check_record(res, r)
+    gauss = run_gpu(sc)
+    assert not np.array_equal(gauss.others.cpu().numpy()[7], r["others"][7])  # the kernel changed the hits

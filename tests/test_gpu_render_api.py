@@ -149,7 +149,9 @@ def test_unsupported_modes_raise():
         with pytest.raises(NotImplementedError):
             GaussianRasterizer(rs, hs)(render_mode=mode, **kw)
     with pytest.raises(NotImplementedError):
-        GaussianRasterizer(rs, hs)(kernel_type=1, **kw)
+        GaussianRasterizer(rs, hs)(kernel_type=4, **kw)
+    with pytest.raises(ValueError):
+        GaussianRasterizer(rs, hs)(kernel_type=1, **kw)  # the beta kernel needs shapes
     with pytest.raises(Exception):
         GaussianRasterizer(rs, hs)(means3D=t(sc.means), means2D=None, opacities=t(sc.opacity))
     with pytest.raises(ValueError):

@@ -30,6 +30,27 @@ def test_expf_accuracy(oracle):
     assert np.isnan(oracle.expf([np.nan])[0])
 
 
+def test_logf_powf_accuracy(oracle):
+    """or_logf (Moshier's logf) within 2 ulp of the float64 log over the
+    binary32 range, subnormals included; or_powf = exp(y log x) within
+    1e-6 (1 + |y log x|) relative of the float64 power; special values."""
+    rng = np.random.default_rng(11)
+    x = np.concatenate([np.float32(2.0) ** rng.uniform(-149, 127, 200_000).astype(np.float32),
+                        rng.uniform(0.5, 2.0, 100_000).astype(np.float32)]).astype(np.float32)
+    x = x[np.isfinite(x) & (x > 0)]
+    got = oracle.logf(x).astype(np.float64)
+    ref = np.log(x.astype(np.float64))
+    ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 2 * ulp + 1e-45)
+    b = rng.uniform(1e-6, 1.0, 100_000).astype(np.float32)
+    e = rng.uniform(0.05, 8.0, 100_000).astype(np.float32)
+    gp = oracle.powf(b, e).astype(np.float64)
+    rp = np.power(b.astype(np.float64), e.astype(np.float64))
+    assert np.all(np.abs(gp - rp) <= 1e-6 * rp * (1 + np.abs(e * np.log(b.astype(np.float64)))) + 1e-37)
+    assert oracle.logf(np.float32([0.0]))[0] == -np.inf and np.isnan(oracle.logf(np.float32([-1.0]))[0])
+    assert oracle.powf(np.float32([0.0, 0.0, 5.0]), np.float32([2.0, 0.0, 0.0])).tolist() == [0.0, 1.0, 1.0]
+
+
 def test_half_and_bf16_rounding_match_numpy(oracle):
     rng = np.random.default_rng(0)
     x = np.concatenate([rng.uniform(-0.2, 0.2, 20000), rng.uniform(-1e-4, 1e-4, 5000),
@@ -461,6 +482,82 @@ def test_record_transmittance_render_modes(oracle):
     r13 = oracle.render(pre, b, W, H, L * F, g, homotrans=homo, ap_level=ap, colors=rows, render_mode=13, level=lvl,
                         record_transmittance=True)
     assert r13["others"][7].sum() > 0 and not r13["cover_pixels"].any() and not r13["trans_avg"].any()
+
+
+def _alpha64(pre, W, H, kernel_type, shape, beta=0.0):
+    """float64 alpha of splat 0 at every pixel (CR/forward.cu:834-921), from
+    the float32 transform the oracle's preprocess wrote; NaN where rejected."""
+    Tm = pre["transmat"][0].astype(np.float64)
+    Tu, Tv, Tw = Tm[0:3], Tm[3:6], Tm[6:9]
+    py, px = np.mgrid[0:H, 0:W].astype(np.float64)
+    k = px[..., None] * Tw - Tu
+    l = py[..., None] * Tw - Tv
+    p = np.cross(k, l)
+    sx, sy = p[..., 0] / p[..., 2], p[..., 1] / p[..., 2]
+    rho3d = sx * sx + sy * sy
+    xy = pre["xy"][0].astype(np.float64)
+    rho2d = 2.0 * ((xy[0] - px) ** 2 + (xy[1] - py) ** 2)
+    rho = np.minimum(rho3d, rho2d)
+    o = float(pre["normal_opacity"][0, 3])
+    with np.errstate(all="ignore"):
+        if kernel_type == 1:
+            G = np.where(rho < 1.0, np.power(np.clip(1.0 - rho, 0, None), shape), np.nan)
+        elif kernel_type == 2:
+            g = np.exp(-0.5 * rho)
+            G = (1.0 + shape) * g / (1.0 + shape * g) if shape > 0 else g
+        elif kernel_type == 3:
+            G = np.exp(-0.5 * np.power(np.maximum(rho, 1e-8), 0.5 * shape))
+        else:
+            g = np.exp(-0.5 * rho)
+            G = (1.0 + beta) * g / (1.0 + beta * g) if beta > 0 else g
+        alpha = np.minimum(0.99, o * G)
+    return np.where(alpha >= 1.0 / 255.0, alpha, np.nan), rho
+
+
+@pytest.mark.parametrize("kt,shape", [(1, 1.0), (1, 2.7), (1, 0.35), (2, 0.8), (2, 0.0), (3, 2.0), (3, 5.5),
+                                      (3, 0.9)])
+def test_kernel_types_alpha_against_float64(oracle, kt, shape):
+    """kernel_type 1-3 (forward.cu:864-900): a single splat's alpha at every
+    pixel (1 - T after its one hit) within 2e-5 of the float64 kernel, and the
+    accepted pixels the same away from the 1/255 and rho = 1 edges."""
+    cam, means, scales, q, opac = _single_splat_scene(n=1, opacity=0.8, W=63, H=47)
+    W, H = cam.image_width, cam.image_height
+    pre = oracle.preprocess(means, scales, q, opac, cam.world_view_transform, cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    r = oracle.render(pre, b, W, H, 3, None, colors=np.ones((1, 3), np.float32), kernel_type=kt,
+                      shapes=np.float32([shape]))
+    a64, rho = _alpha64(pre, W, H, kt, shape)
+    got = r["others"][1].astype(np.float64)
+    hit = r["others"][7] > 0
+    edge = np.abs(a64 - 1.0 / 255.0) < 1e-4
+    if kt == 1:
+        edge |= np.abs(rho - 1.0) < 1e-5
+    sure = ~edge & ~np.isnan(a64)
+    assert np.all(hit[sure]) and not np.any(hit[~edge & np.isnan(a64)])
+    both = hit & ~np.isnan(a64)
+    np.testing.assert_allclose(got[both], a64[both], rtol=2e-5, atol=1e-7)
+    assert hit.sum() > 20
+
+
+def test_kernel_types_reduce_to_the_gaussian(oracle):
+    """The general kernel at shape 2 is the Gaussian (pow(rho, 1) = rho), the
+    flex kernel with every splat's beta b is the Gaussian with the global
+    beta b: same hits, alpha within the rounding of the power or of the
+    activation's float arithmetic."""
+    pre, b, W, H = _record_scene(oracle, seed=9)
+    P = len(pre["radii"])
+    cols = np.random.default_rng(2).uniform(0, 1, (P, 3)).astype(np.float32)
+    r0 = oracle.render(pre, b, W, H, 3, None, colors=cols)
+    r3 = oracle.render(pre, b, W, H, 3, None, colors=cols, kernel_type=3, shapes=np.full(P, 2.0, np.float32))
+    np.testing.assert_array_equal(r3["others"][7], r0["others"][7])
+    np.testing.assert_allclose(r3["color"], r0["color"], rtol=1e-5, atol=1e-6)
+    rb = oracle.render(pre, b, W, H, 3, None, colors=cols, beta=0.7)
+    r2 = oracle.render(pre, b, W, H, 3, None, colors=cols, kernel_type=2, shapes=np.full(P, 0.7, np.float32))
+    np.testing.assert_array_equal(r2["others"][7], rb["others"][7])
+    np.testing.assert_allclose(r2["color"], rb["color"], rtol=1e-5, atol=1e-6)
+    # the beta kernel's support ends at rho = 1: fewer hits than the Gaussian
+    r1 = oracle.render(pre, b, W, H, 3, None, colors=cols, kernel_type=1, shapes=np.full(P, 1.0, np.float32))
+    assert 0 < r1["others"][7].sum() < r0["others"][7].sum()
 
 
 def test_single_splat_hash_feature_closed_form(oracle):
