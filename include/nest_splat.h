@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 10
+#define NEST_ABI_VERSION 11
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -343,6 +343,8 @@ typedef struct {
     float *dL_drotations;            /* [P,4] */
     float *dL_dfeatures;             /* [table_rows, level_dim] hash path */
     float *dL_dgradsum;              /* [P] hash path (returned for ap_level), or NULL */
+    float *dL_dshapes;               /* [P] the splats' kernel parameter (kernel_type 1-3,
+                                        required then; CR/backward.cu:1864-1909), or NULL */
 } nest_backward_io;
 
 int nest_backward(const nest_raster_settings *settings, const nest_hashgrid *grid, const nest_splats *splats,

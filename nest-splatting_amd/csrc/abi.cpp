@@ -874,9 +874,6 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   int rc = check_settings(rs);
   if (rc) return rc;
   if ((rc = check_splats(sp, true))) return rc;
-  if (sp->kernel_type != 0)
-    return fail(NEST_ERR_UNSUPPORTED, "backward: kernel_type %d is not implemented (the Gaussian kernel is)",
-                sp->kernel_type);
   if (!gr || gr->struct_size != sizeof(nest_hashgrid))
     return fail(NEST_ERR_INVALID_ARGUMENT, "nest_hashgrid missing or struct_size mismatch");
   if (!io || io->struct_size != sizeof(nest_backward_io))
@@ -896,6 +893,8 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   if (C < 1 || C > 64) return fail(NEST_ERR_UNSUPPORTED, "backward: channels must be in [1, 64] (got %d)", C);
   if (!io->dL_dout_color || !io->dL_dout_others)
     return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dout_color and dL_dout_others are required");
+  if (sp->kernel_type != 0 && sp->P > 0 && !io->dL_dshapes)
+    return fail(NEST_ERR_INVALID_ARGUMENT, "backward: kernel_type %d needs dL_dshapes [P]", sp->kernel_type);
   if (!io->dL_dmeans3D || !io->dL_dmeans2D || !io->dL_dopacity || !io->dL_dscales || !io->dL_drotations)
     return fail(NEST_ERR_INVALID_ARGUMENT, "backward: dL_dmeans3D, dL_dmeans2D, dL_dopacity, dL_dscales and "
                                            "dL_drotations are required");
@@ -962,7 +961,8 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
                {dcolors, (int64_t)P * dcol_width}, {gradsum, (int64_t)P}, {io->dL_dmeans3D, (int64_t)P * 3},
                {io->dL_dmeans2D, (int64_t)P * 3}, {io->dL_dopacity, (int64_t)P}, {io->dL_dscales, (int64_t)P * 2},
                {io->dL_drotations, (int64_t)P * 4}, {from_sh ? io->dL_dshs : nullptr, (int64_t)P * M * 3},
-               {hash ? io->dL_dfeatures : nullptr, hash ? (int64_t)gr->table_rows * gr->level_dim : 0}};
+               {hash ? io->dL_dfeatures : nullptr, hash ? (int64_t)gr->table_rows * gr->level_dim : 0},
+               {io->dL_dshapes, (int64_t)P}};
   for (const Fill& f : fills) {
     if (!f.p || f.n == 0) continue;
     hipError_t e = launch_fill_u32(reinterpret_cast<uint32_t*>(f.p), 0u, f.n, s);
@@ -1003,6 +1003,8 @@ int nest_backward(const nest_raster_settings* rs, const nest_hashgrid* gr, const
   rp.dopacity = io->dL_dopacity;
   rp.dcolors = dcolors;
   rp.gradsum = gradsum;
+  rp.kernel_type = sp->kernel_type;
+  rp.dshapes = sp->kernel_type != 0 ? io->dL_dshapes : nullptr;
   rp.grid = g;
   if (NR > 0) {
     hipError_t e = launch_render_backward(rp, s);

@@ -426,15 +426,59 @@ struct BwdHit {
   float k[3], l[3], pp[3];
   float s[2], d[2];
   float c_d, G, demon, alpha;
+  // kernel types 1-3: dG/ds = pf * s (3D; 2 pf * d in 2D), dL/dG scale gsc, dG/dshape gs
+  float pf, gsc, gs;
   bool use3d;
 };
+
+// G of kernel types 1-3 and the factors of its gradients, as
+// CR/backward.cu:764-800 and :1864-1909, :1958-2032 write them: the beta
+// kernel's position factor is -shape G / base (half the derivative of
+// (1 - rho)^shape in s, which the reference keeps), the flex kernel's the raw
+// Gaussian's with dL/dG scaled by (1 + b) / demon^2, and no shape gradient
+// at b <= 0.  False for a pair the kernel rejects.
+__device__ __forceinline__ bool bwd_kernel_g(int kt, float rho, float shape, BwdHit& h) {
+  h.gsc = 1.0f;
+  h.gs = 0.0f;
+  if (kt == 1) {
+    if (rho >= 1.0f) return false;
+    const float base = 1.0f - rho;
+    h.G = powf_ref(base, shape);
+    h.pf = base > 1e-7f ? -shape * h.G / base : 0.0f;
+    if (base > 1e-7f) h.gs = h.G * logf_ref(base);
+    return true;
+  }
+  if (kt == 2) {
+    const float power = -0.5f * rho;
+    if (power > 0.0f) return false;
+    const float g = expf_ref(power);
+    h.G = g;
+    h.pf = -g;
+    h.gsc = -1.0f;  // no per-splat beta: the settings' beta scales dL/dG (CR/backward.cu:1910-1914)
+    if (shape > 0.0f) {
+      const float demon = 1.0f + shape * g;
+      h.G = (1.0f + shape) * g / demon;
+      h.gsc = (1.0f + shape) / (demon * demon);
+      h.gs = g * (1.0f - g) / (demon * demon);
+    }
+    return true;
+  }
+  const float rho_safe = fmaxf(rho, 1e-8f);
+  const float pt = powf_ref(rho_safe, 0.5f * shape);
+  const float power = -0.5f * pt;
+  if (power > 0.0f) return false;
+  h.G = expf_ref(power);
+  h.pf = -0.5f * shape * h.G * pt / rho_safe;
+  h.gs = -0.25f * h.G * pt * logf_ref(rho_safe);
+  return true;
+}
 
 // The intersection, Gaussian and alpha of a splat at the pixel
 // (backward.cu:1700-1790); true for a hit that passes every test of the
 // forward.  pre: the pixel is inside and the splat precedes its last
 // contributor.
 __device__ __forceinline__ bool bwd_hit(const float4& q0, const float4& q1, const float4& q2, float pxf, float pyf,
-                                        float beta, bool pre, BwdHit& h) {
+                                        float beta, bool pre, BwdHit& h, int kt = 0, float shape = 0.0f) {
   const float Tu[3] = {q0.x, q0.y, q0.z}, Tv[3] = {q0.w, q1.x, q1.y}, Tw[3] = {q1.z, q1.w, q2.x};
 #pragma unroll
   for (int r = 0; r < 3; r++) {
@@ -462,16 +506,24 @@ __device__ __forceinline__ bool bwd_hit(const float4& q0, const float4& q1, cons
     const float rho = fminf(rho3d, rho2d);
     h.use3d = rho3d <= rho2d;
     h.c_d = h.use3d ? (h.s[0] * Tw[0] + h.s[1] * Tw[1]) + Tw[2] : Tw[2];
-    const float power = -0.5f * rho;
-    act = h.c_d >= 0.2f && power <= 0.0f;
-    if (act) {
-      h.G = expf_ref(power);
-      if (beta > 0.0f) {
-        h.demon = (float)(1.0 + (double)(beta * h.G));
-        h.G = (float)((1.0 + (double)beta) * (double)h.G / (double)h.demon);
+    if (kt == 0) {
+      const float power = -0.5f * rho;
+      act = h.c_d >= 0.2f && power <= 0.0f;
+      if (act) {
+        h.G = expf_ref(power);
+        if (beta > 0.0f) {
+          h.demon = (float)(1.0 + (double)(beta * h.G));
+          h.G = (float)((1.0 + (double)beta) * (double)h.G / (double)h.demon);
+        }
+        h.alpha = fminf(0.99f, q2.w * h.G);
+        act = h.alpha >= 1.0f / 255.0f;
       }
-      h.alpha = fminf(0.99f, q2.w * h.G);
-      act = h.alpha >= 1.0f / 255.0f;
+    } else {
+      act = h.c_d >= 0.2f && bwd_kernel_g(kt, rho, shape, h);
+      if (act) {
+        h.alpha = fminf(0.99f, q2.w * h.G);
+        act = h.alpha >= 1.0f / 255.0f;
+      }
     }
   }
   return act;
@@ -479,7 +531,7 @@ __device__ __forceinline__ bool bwd_hit(const float4& q0, const float4& q1, cons
 
 // Per-splat gradient contributions of one pixel's hit (zero without one).
 struct BwdGrad {
-  float gT[9], gH[9], gM[2], gN[3], gO;
+  float gT[9], gH[9], gM[2], gN[3], gO, gK;
 };
 
 __device__ __forceinline__ void bwd_grad_zero(BwdGrad& gr) {
@@ -488,6 +540,7 @@ __device__ __forceinline__ void bwd_grad_zero(BwdGrad& gr) {
   gr.gM[0] = gr.gM[1] = 0.0f;
   gr.gN[0] = gr.gN[1] = gr.gN[2] = 0.0f;
   gr.gO = 0.0f;
+  gr.gK = 0.0f;
 }
 
 // The blending recursion at a hit (T already divided by 1 - alpha) and the
@@ -498,7 +551,8 @@ __device__ __forceinline__ void bwd_grad_zero(BwdGrad& gr) {
 template <bool kHash>
 __device__ __forceinline__ void bwd_hit_grad(BwdPixel& px, const BwdHit& h, const float4& q1, const float4& q2,
                                              const float4& q3, const float4& q4, const float4& q5, float beta,
-                                             uint32_t contributor, float dot, const float dxyz[3], BwdGrad& gr) {
+                                             uint32_t contributor, float dot, const float dxyz[3], BwdGrad& gr,
+                                             int kt = 0) {
   const float T = px.T, alpha = h.alpha, c_d = h.c_d;
   const float Tw[2] = {q1.z, q1.w};
   if constexpr (kHash) {
@@ -538,9 +592,18 @@ __device__ __forceinline__ void bwd_hit_grad(BwdPixel& px, const BwdHit& h, cons
   dL_dalpha *= T;
   px.last_alpha = alpha;
   float dL_dG = q2.w * dL_dalpha;
-  if (beta > 0.0f) {
-    const float dG_dg = (float)((1.0 + (double)beta) / (double)(h.demon * h.demon));
-    dL_dG *= dG_dg;
+  if (kt == 0) {
+    if (beta > 0.0f) {
+      const float dG_dg = (float)((1.0 + (double)beta) / (double)(h.demon * h.demon));
+      dL_dG *= dG_dg;
+    }
+  } else {
+    gr.gK = dL_dalpha * q2.w * h.gs;  // dL/dshape (CR/backward.cu:1864-1909)
+    if (kt == 2) {
+      // a flex splat without its own beta falls through to the settings'
+      // beta factor with demon = 1 (CR/backward.cu:1875, 1910-1914)
+      dL_dG *= h.gsc >= 0.0f ? h.gsc : (beta > 0.0f ? (float)(1.0 + (double)beta) : 1.0f);
+    }
   }
   dL_dz += alpha * T * px.dL_ddepth;
   float dL_duv[2] = {0.0f, 0.0f};
@@ -551,7 +614,7 @@ __device__ __forceinline__ void bwd_hit_grad(BwdPixel& px, const BwdHit& h, cons
     }
   }
   if (h.use3d) {
-    const float dG_factor = -h.G;
+    const float dG_factor = kt == 0 ? -h.G : h.pf;
     float dL_ds[2] = {dL_dG * dG_factor * h.s[0] + dL_dz * Tw[0], dL_dG * dG_factor * h.s[1] + dL_dz * Tw[1]};
     dL_ds[0] += dL_duv[0];
     dL_ds[1] += dL_duv[1];
@@ -569,7 +632,7 @@ __device__ __forceinline__ void bwd_hit_grad(BwdPixel& px, const BwdHit& h, cons
       gr.gT[6 + r] = px.pxf * dk[r] + px.pyf * dl[r] + dL_dz * dz_dTw[r];
     }
   } else {
-    const float dG_factor_2d = -h.G * 2.0f;
+    const float dG_factor_2d = kt == 0 ? -h.G * 2.0f : h.pf * 2.0f;
     gr.gM[0] = dL_dG * (dG_factor_2d * h.d[0]);
     gr.gM[1] = dL_dG * (dG_factor_2d * h.d[1]);
     gr.gT[8] = dL_dz;
@@ -632,6 +695,10 @@ __device__ __forceinline__ void bwd_splat_sums(const RenderBwdParams& p, const B
   }
   const float vo = wave_sum(gr.gO);
   if (lead && vo != 0.0f) atomic_add(p.dopacity + id, vo);
+  if (p.dshapes != nullptr) {
+    const float vk = wave_sum(gr.gK);
+    if (lead && vk != 0.0f) atomic_add(p.dshapes + id, vk);
+  }
 }
 
 // Colour path (no grid): the wave walks the staged splats back to front in
@@ -639,6 +706,7 @@ __device__ __forceinline__ void bwd_splat_sums(const RenderBwdParams& p, const B
 __global__ void __launch_bounds__(kBwdThreads) render_backward_colour_kernel(const RenderBwdParams p) {
   __shared__ float4 srec[4][kBwdThreads];
   __shared__ uint32_t sid[kBwdThreads];
+  __shared__ float sshape[kBwdThreads];  // kernel types 1-3: record[26]
 
   const uint32_t tile = p.tile_order[blockIdx.x];  // the forward's order: heaviest tiles first
   const uint2 range = reinterpret_cast<const uint2*>(p.ranges)[tile];
@@ -656,6 +724,7 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_colour_kernel(con
 #pragma unroll
       for (int c = 0; c < 4; c++) srec[c][threadIdx.x] = rec[c];
       sid[threadIdx.x] = id;
+      sshape[threadIdx.x] = p.kernel_type != 0 ? rec[6].z : 0.0f;
     }
     __syncthreads();
     for (uint32_t j = 0; j < n; j++) {
@@ -663,7 +732,8 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_colour_kernel(con
       const float4 q0 = srec[0][j], q1 = srec[1][j], q2 = srec[2][j], q3 = srec[3][j];
       const uint32_t id = sid[j];
       BwdHit h;
-      const bool act = bwd_hit(q0, q1, q2, px.pxf, px.pyf, p.beta, px.inside && contributor < px.last_contributor, h);
+      const bool act = bwd_hit(q0, q1, q2, px.pxf, px.pyf, p.beta, px.inside && contributor < px.last_contributor, h,
+                               p.kernel_type, sshape[j]);
       BwdGrad gr;
       bwd_grad_zero(gr);
       float wcol = 0.0f;
@@ -675,7 +745,7 @@ __global__ void __launch_bounds__(kBwdThreads) render_backward_colour_kernel(con
         for (int ch = 0; ch < p.C; ch++) dot += col[ch] * px.dpix[(size_t)ch * HW];
         wcol = wgt;
         const float dxyz[3] = {0.0f, 0.0f, 0.0f};
-        bwd_hit_grad<false>(px, h, q1, q2, q3, q3, q3, p.beta, contributor, dot, dxyz, gr);
+        bwd_hit_grad<false>(px, h, q1, q2, q3, q3, q3, p.beta, contributor, dot, dxyz, gr, p.kernel_type);
       }
       if (__ballot(act) != 0ull) bwd_splat_sums<false, 0>(p, px, id, act, gr, 0.0f, wcol, 0.0f, 0.0f);
     }
@@ -777,7 +847,8 @@ render_backward_kernel(const RenderBwdParams p) {
         const float4 q0 = srec[0][j], q1 = srec[1][j], q2 = srec[2][j];
         BwdHit h;
         const bool act =
-            bwd_hit(q0, q1, q2, px.pxf, px.pyf, p.beta, px.inside && contributor < px.last_contributor, h);
+            bwd_hit(q0, q1, q2, px.pxf, px.pyf, p.beta, px.inside && contributor < px.last_contributor, h,
+                    p.kernel_type, srec[6][j].z);
         float xyz[3] = {0.0f, 0.0f, 0.0f}, hw = 0.0f;
         uint32_t lane_levels = 0u;
         if (act) {
@@ -844,7 +915,7 @@ render_backward_kernel(const RenderBwdParams p) {
         const float4 q4 = srec[4][jj], q5 = srec[5][jj];
         const uint32_t id = sid[jj];
         BwdHit h;
-        bwd_hit(q0, q1, q2, px.pxf, px.pyf, p.beta, act, h);
+        bwd_hit(q0, q1, q2, px.pxf, px.pyf, p.beta, act, h, p.kernel_type, srec[6][jj].z);
         bool pushed = false;  // the hit's queue entry, as in the geometry pass
         if (act) {
           float xyz[3], wt0;
@@ -887,7 +958,7 @@ render_backward_kernel(const RenderBwdParams p) {
               if (p.wsig) fdot = fdot * wt * (1.0f - wt);  // mode 7: dL/dlogit of weight = sigmoid(logit)
             }
           }
-          bwd_hit_grad<true>(px, h, q1, q2, q3, q4, q5, p.beta, contributor, dot, dxyz, gr);
+          bwd_hit_grad<true>(px, h, q1, q2, q3, q4, q5, p.beta, contributor, dot, dxyz, gr, p.kernel_type);
         }
         qbase += (uint32_t)__popcll(m_push);
         bwd_splat_sums<true, kRows>(p, px, id, act, gr, gS, wcol, wt, fdot);

@@ -211,6 +211,8 @@ struct RenderBwdParams {
   int azero;                  // render mode 14: grid levels take grid * weight, no row part
   int wsig;                   // render mode 7: the weight slot gets dL/dweight * w * (1 - w)
   int nfine;                  // render modes 12, 14: grid channels after the coarse ones (levels * F)
+  int kernel_type;            // 0 Gaussian, 1 beta, 2 flex, 3 general (shape in record[26])
+  float* dshapes;             // [P] kernel types 1-3
   GridParams grid;
 };
 hipError_t launch_render_backward(const RenderBwdParams& p, hipStream_t s);

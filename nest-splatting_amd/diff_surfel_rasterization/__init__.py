@@ -170,11 +170,13 @@ class _RasterizeGaussians(torch.autograd.Function):
         ctx.render_mode = render_mode
         ctx.kernel_type = int(kernel_type)
         ctx.fw = dict(res=res, settings=settings, grid=grid, C=C, colors=colors,
+                      shapes=None if kernel_type == 0 else shapes.detach().reshape(-1),
                       shs=None if (level > 0 or colors is not None or _empty(sh)) else sh.detach(),
                       sh_degree=int(raster_settings.sh_degree),
                       homotrans=None if _empty(homotrans) else homotrans.detach(),
                       ap_level=None if _empty(ap_level) else ap_level.detach())
         ctx.save_for_backward(means3D, opacities, scales, rotations)
+        ctx.shapes_shape = None if kernel_type == 0 else tuple(shapes.shape)
         dev = means3D.device
         if res.trans_avg is not None:
             # [P, 1] each, as DSR/rasterize_points.cu:169-171 allocates them
@@ -187,9 +189,6 @@ class _RasterizeGaussians(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out_color, grad_radii, grad_depth, grad_0, grad_1):
-        if ctx.kernel_type != 0:
-            raise NotImplementedError(f"kernel_type {ctx.kernel_type} is forward-only here; the backward covers the "
-                                      f"Gaussian kernel (0)")
         if ctx.render_mode not in (0, 4, 7, 12, 14):
             raise NotImplementedError(f"render_mode {ctx.render_mode} is forward-only here; "
                                       f"the backward covers modes 0, 4, 7, 12 and 14 (training)")
@@ -198,7 +197,8 @@ class _RasterizeGaussians(torch.autograd.Function):
         g = _rz.rasterize_backward(fw["settings"], fw["grid"], fw["res"], means3D.detach(), opacities.detach(),
                                    scales.detach(), rotations.detach(), grad_out_color, grad_depth,
                                    homotrans=fw["homotrans"], ap_level=fw["ap_level"], colors_precomp=fw["colors"],
-                                   channels=fw["C"], shs=fw["shs"], sh_degree=fw["sh_degree"])
+                                   channels=fw["C"], shs=fw["shs"], sh_degree=fw["sh_degree"], shapes=fw["shapes"],
+                                   kernel_type=ctx.kernel_type)
         need = ctx.needs_input_grad
 
         def pick(i, t, shape=None):
@@ -210,7 +210,7 @@ class _RasterizeGaussians(torch.autograd.Function):
         return (pick(0, g.dmeans3D), pick(1, g.dmeans2D), pick(2, g.dshs), pick(3, g.dcolors),
                 pick(4, g.dopacity, opacities.shape), pick(5, g.dscales), pick(6, g.drotations), None, None,
                 pick(9, g.dgradsum, None if ap is None else ap.shape), pick(10, g.dfeatures),
-                None, None, None, None, None, None, None, None, None, None)
+                None, None, None, None, None, None, None, None, pick(19, g.dshapes, ctx.shapes_shape), None)
 
 
 class GaussianRasterizationSettings(NamedTuple):

@@ -27,7 +27,7 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 SCAN_NOALLOC_MAX = 268431360
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
  GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
@@ -87,7 +87,7 @@ class BackwardIO(ct.Structure):
                 ("dL_dout_others", ct.c_void_p), ("dL_dmeans3D", ct.c_void_p), ("dL_dmeans2D", ct.c_void_p),
                 ("dL_dcolors", ct.c_void_p), ("dL_dopacity", ct.c_void_p), ("dL_dshs", ct.c_void_p),
                 ("dL_dscales", ct.c_void_p), ("dL_drotations", ct.c_void_p), ("dL_dfeatures", ct.c_void_p),
-                ("dL_dgradsum", ct.c_void_p)]
+                ("dL_dgradsum", ct.c_void_p), ("dL_dshapes", ct.c_void_p)]
 
 
 class Timing(ct.Structure):

@@ -294,6 +294,7 @@ class BackwardResult:
     drotations: torch.Tensor    # [P, 4]
     dfeatures: Optional[torch.Tensor]  # [rows, F] hash path
     dgradsum: torch.Tensor      # [P, 1]
+    dshapes: Optional[torch.Tensor] = None  # [P] kernel types 1-3
 
 
 def rasterize_backward(settings: L.RasterSettings, grid: HashGridDesc, res: ForwardResult, means3D: torch.Tensor,
@@ -301,14 +302,15 @@ def rasterize_backward(settings: L.RasterSettings, grid: HashGridDesc, res: Forw
                        dL_dcolor: torch.Tensor, dL_dothers: Optional[torch.Tensor],
                        homotrans: Optional[torch.Tensor] = None, ap_level: Optional[torch.Tensor] = None,
                        colors_precomp: Optional[torch.Tensor] = None, channels: int = 3,
-                       shs: Optional[torch.Tensor] = None, sh_degree: int = 0) -> BackwardResult:
+                       shs: Optional[torch.Tensor] = None, sh_degree: int = 0, shapes: Optional[torch.Tensor] = None,
+                       kernel_type: int = 0) -> BackwardResult:
     """Backward of one forward frame (nest_backward): the inputs are those
     of the rasterize_forward call that produced ``res``."""
     dev = means3D.device
     P = int(means3D.shape[0])
     H, W = settings.image_height, settings.image_width
     sp, keep = _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, channels, shs,
-                       sh_degree, grid.row_width(channels))
+                       sh_degree, grid.row_width(channels), shapes=shapes, kernel_type=kernel_type)
     g = grid.to_c()
     if dL_dcolor is None:
         dL_dcolor = torch.zeros((channels, H, W), dtype=torch.float32, device=dev)
@@ -324,6 +326,8 @@ def rasterize_backward(settings: L.RasterSettings, grid: HashGridDesc, res: Forw
         dcolors=torch.empty((P, grid.row_width(channels)), **f32), dopacity=torch.empty((P, 1), **f32),
         dshs=None, dscales=torch.empty((P, 2), **f32), drotations=torch.empty((P, 4), **f32),
         dfeatures=None, dgradsum=torch.empty((P, 1), **f32))
+    if kernel_type != 0:
+        out.dshapes = torch.empty((P,), **f32)
     if grid.levels > 0:
         out.dfeatures = torch.empty(tuple(grid.table.shape), **f32)
     elif colors_precomp is None or colors_precomp.numel() == 0:
@@ -342,6 +346,7 @@ def rasterize_backward(settings: L.RasterSettings, grid: HashGridDesc, res: Forw
     io.dL_drotations = out.drotations.data_ptr()
     io.dL_dfeatures = L.ptr(out.dfeatures)
     io.dL_dgradsum = out.dgradsum.data_ptr()
+    io.dL_dshapes = L.ptr(out.dshapes)
     offs = (ct.c_size_t * L.BWD_FIELDS)()
     wbytes = ct.c_size_t(0)
     L.check(L.lib().nest_backward_layout(P, int(channels), offs, ct.byref(wbytes)), "nest_backward_layout")

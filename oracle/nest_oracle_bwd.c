@@ -173,6 +173,11 @@ typedef struct {
      * [P][hyb*F] in mode 4, [P][total*F+1] in mode 12, 14 (adaptive_zero
      * training, :1521-1590) with rows [P][hyb*F+1] */
     int render_mode;
+    /* kernel_type 1-3 (CR/backward.cu:764-803, :1864-1909, :1963-2039) with
+     * the per-splat shapes [P]; dshapes [P] accumulates dL/dshape */
+    const float *shapes;
+    int kernel_type;
+    float *dshapes;
 } or_render_bwd_args;
 
 /* Grid levels the mode-4 backward differentiates (CR/backward.cu:576-612,
@@ -251,12 +256,54 @@ static void render_pixel_bwd(const or_render_bwd_args *A, uint32_t tile, uint32_
         const float opa = no[3];
 
         float G, demon = 1.0f;
-        const float power = -0.5f * rho;
-        if (power > 0.0f) continue;
-        G = or_expf(power);
-        if (A->beta > 0.0f) {
-            demon = (float)(1.0 + (double)(A->beta * G));
-            G = (float)((1.0 + (double)A->beta) * (double)G / (double)demon);
+        /* kernel types: pf is the reference's dG_factor (2 dG/drho, but
+         * dG/drho for the beta kernel), gs dG/dshape, gsc dG/dG_raw of a flex
+         * splat (CR/backward.cu:764-803, :1963-1981) */
+        float pf = 0.0f, gs = 0.0f, gsc = 1.0f, shp = 0.0f;
+        const int kt = A->kernel_type;
+        if (kt == 1) {
+            if (rho >= 1.0f) continue;
+            const float base = 1.0f - rho;
+            shp = A->shapes[id];
+            G = or_powf(base, shp);
+            if (base > 1e-7f) {
+                pf = -shp * G / base;
+                gs = G * or_logf(base);
+            }
+        } else if (kt == 2) {
+            const float power = -0.5f * rho;
+            if (power > 0.0f) continue;
+            const float g = or_expf(power);
+            shp = A->shapes[id];
+            G = g;
+            pf = -g;
+            if (shp > 0.0f) {
+                demon = 1.0f + shp * g;
+                G = (1.0f + shp) * g / demon;
+                gsc = (1.0f + shp) / (demon * demon);
+                gs = g * (1.0f - g) / (demon * demon);
+            } else if (A->beta > 0.0f) {
+                /* no per-splat beta: the settings' beta factor with demon = 1
+                 * (CR/backward.cu:1875, :1910-1914) */
+                gsc = (float)(1.0 + (double)A->beta);
+            }
+        } else if (kt == 3) {
+            shp = A->shapes[id];
+            const float rho_safe = fmaxf(rho, 1e-8f);
+            const float pt = or_powf(rho_safe, 0.5f * shp);
+            const float power = -0.5f * pt;
+            if (power > 0.0f) continue;
+            G = or_expf(power);
+            pf = -0.5f * shp * G * pt / rho_safe;
+            gs = -0.25f * G * pt * or_logf(rho_safe);
+        } else {
+            const float power = -0.5f * rho;
+            if (power > 0.0f) continue;
+            G = or_expf(power);
+            if (A->beta > 0.0f) {
+                demon = (float)(1.0 + (double)(A->beta * G));
+                G = (float)((1.0 + (double)A->beta) * (double)G / (double)demon);
+            }
         }
         const float alpha = fminf(0.99f, opa * G);
         if (alpha < 1.0f / 255.0f) continue;
@@ -428,7 +475,10 @@ static void render_pixel_bwd(const or_render_bwd_args *A, uint32_t tile, uint32_
         last_alpha = alpha;
 
         float dL_dG = opa * dL_dalpha;
-        if (A->beta > 0.0f) {
+        if (kt != 0) {
+            A->dshapes[id] += dL_dalpha * opa * gs;
+            if (kt == 2) dL_dG *= gsc;
+        } else if (A->beta > 0.0f) {
             const float dG_dg = (float)((1.0 + (double)A->beta) / (double)(demon * demon));
             dL_dG *= dG_dg;
         }
@@ -449,8 +499,8 @@ static void render_pixel_bwd(const or_render_bwd_args *A, uint32_t tile, uint32_
         }
 
         if (use3d) {
-            /* backward.cu:1956-2011 with dG_factor = -G */
-            const float dG_factor = -G;
+            /* backward.cu:1956-2011 with dG_factor = -G (kernel types: pf) */
+            const float dG_factor = kt ? pf : -G;
             float dL_ds[2] = {dL_dG * dG_factor * s[0] + dL_dz * Tw[0], dL_dG * dG_factor * s[1] + dL_dz * Tw[1]};
             dL_ds[0] += dL_duv[0];
             dL_ds[1] += dL_duv[1];
@@ -469,7 +519,7 @@ static void render_pixel_bwd(const or_render_bwd_args *A, uint32_t tile, uint32_
                 t[6 + r] += pxf * dk[r] + pyf * dl[r] + dL_dz * dz_dTw[r];
             }
         } else {
-            const float dG_factor_2d = -G * 2.0f;
+            const float dG_factor_2d = kt ? pf * 2.0f : -G * 2.0f;
             const float dG_ddelx = dG_factor_2d * d[0], dG_ddely = dG_factor_2d * d[1];
             A->dmean2D[3 * (size_t)id + 0] += dL_dG * dG_ddelx;
             A->dmean2D[3 * (size_t)id + 1] += dL_dG * dG_ddely;

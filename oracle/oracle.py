@@ -58,7 +58,8 @@ class OrRenderBwdArgs(ct.Structure):
                 ("dL_dothers", ct.c_void_p), ("dtable", ct.c_void_p), ("dtransmat", ct.c_void_p),
                 ("dhomo", ct.c_void_p), ("dmean2D", ct.c_void_p), ("dnormal", ct.c_void_p),
                 ("dopacity", ct.c_void_p), ("dcolors", ct.c_void_p), ("gradsum", ct.c_void_p),
-                ("render_mode", ct.c_int)]
+                ("render_mode", ct.c_int), ("shapes", ct.c_void_p), ("kernel_type", ct.c_int),
+                ("dshapes", ct.c_void_p)]
 
 
 def lib():
@@ -277,13 +278,14 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
 
 
 def render_backward(pre, binres, fwd, W, H, C, grid: Optional[OrGrid], dL_dpix, dL_dothers, homotrans=None,
-                    ap_level=None, colors=None, beta=0.0, render_mode=0, level=None):
+                    ap_level=None, colors=None, beta=0.0, render_mode=0, level=None, shapes=None, kernel_type=0):
     """renderCUDAsurfelBackward (modes 0, 4, 7, 12 and 14) for every pixel, given the
     forward's final_T / n_contrib (fwd = render(...)'s result).  Returns the
     per-splat gradients (dtransmat [P,9], dhomo [P,9], dmean2D [P,3],
     dnormal [P,3], dopacity [P], dcolors [P,C], or [P,hyb*F] in mode 4,
     [P,total*F+1] in modes 7 and 12, [P,hyb*F+1] in mode 14, gradsum [P])
-    and dtable [rows, F].  Modes 4, 7, 12 and 14 take the packed level
+    and dtable [rows, F]; kernel_type 1-3 (with shapes [P]) adds dshapes [P].
+    Modes 4, 7, 12 and 14 take the packed level
     (total << 16) | (active grid levels << 8) | per-splat levels and the
     per-splat rows as colors."""
     P = pre["radii"].shape[0]
@@ -303,7 +305,8 @@ def render_backward(pre, binres, fwd, W, H, C, grid: Optional[OrGrid], dL_dpix, 
     out = dict(dtransmat=np.zeros((P, 9), np.float32), dhomo=np.zeros((P, 9), np.float32),
                dmean2D=np.zeros((P, 3), np.float32), dnormal=np.zeros((P, 3), np.float32),
                dopacity=np.zeros(P, np.float32), dcolors=np.zeros((P, max(dcol, 1)), np.float32),
-               gradsum=np.zeros(P, np.float32), dtable=np.zeros((max(rows, 1), F), np.float32))
+               gradsum=np.zeros(P, np.float32), dtable=np.zeros((max(rows, 1), F), np.float32),
+               dshapes=np.zeros(P, np.float32))
     keep = []
 
     def ptr(a, dt):
@@ -332,8 +335,13 @@ def render_backward(pre, binres, fwd, W, H, C, grid: Optional[OrGrid], dL_dpix, 
     a.n_contrib = ptr(fwd["n_contrib"], np.uint32)
     a.dL_dpix = ptr(dL_dpix, np.float32)
     a.dL_dothers = ptr(dL_dothers, np.float32)
-    for k in ("dtable", "dtransmat", "dhomo", "dmean2D", "dnormal", "dopacity", "dcolors", "gradsum"):
+    for k in ("dtable", "dtransmat", "dhomo", "dmean2D", "dnormal", "dopacity", "dcolors", "gradsum", "dshapes"):
         setattr(a, k, out[k].ctypes.data)
+    if kernel_type not in (0, 1, 2, 3) or (kernel_type != 0 and shapes is None):
+        raise ValueError(f"render_backward: kernel_type {kernel_type} needs 0-3, with shapes for 1-3")
+    a.kernel_type = kernel_type
+    if kernel_type != 0:
+        a.shapes = ptr(np.asarray(shapes, np.float32).reshape(-1), np.float32)
     lib().or_render_backward(ct.byref(a))
     if rows == 0:
         out["dtable"] = np.zeros((0, F), np.float32)

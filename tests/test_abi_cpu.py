@@ -50,7 +50,7 @@ def test_struct_sizes_match_c_layout():
     assert ct.sizeof(L.Splats) == 8 + 9 * 8 + 16
     assert ct.sizeof(L.FrameOutputs) == 8 + 5 * 8
     assert ct.sizeof(L.Mlp) == 16 + 3 * 8
-    assert ct.sizeof(L.BackwardIO) == 8 + 11 * 8
+    assert ct.sizeof(L.BackwardIO) == 8 + 12 * 8
 
 
 def test_layouts_are_aligned_and_monotone():

@@ -29,7 +29,22 @@ def _rel(a, b):
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
 
 
-def _setup(oracle, sc, path, beta=0.0, sh_degree=3):
+def _shapes(kt, P, seed):
+    """Per-splat kernel parameters: beta-kernel shapes 0.2-4, flex betas 0-2
+    (every 7th 0), general exponents 2-8 (every 9th below 2)."""
+    rng = np.random.default_rng(seed)
+    if kt == 1:
+        return rng.uniform(0.2, 4.0, P).astype(np.float32)
+    if kt == 2:
+        v = rng.uniform(0.0, 2.0, P).astype(np.float32)
+        v[::7] = 0.0
+        return v
+    v = rng.uniform(2.0, 8.0, P).astype(np.float32)
+    v[::9] = rng.uniform(0.8, 2.0, v[::9].shape).astype(np.float32)
+    return v
+
+
+def _setup(oracle, sc, path, beta=0.0, sh_degree=3, kt=0):
     from nest_splat import rasterizer as rz
     sp = sc.spec
     cam = sc.cameras[0]
@@ -39,6 +54,10 @@ def _setup(oracle, sc, path, beta=0.0, sh_degree=3):
     rng = np.random.default_rng(17)
     P = sp.P
     kw = dict(homotrans=None, ap_level=None, colors_precomp=None, shs=None, sh_degree=0)
+    shapes = None
+    if kt:
+        shapes = _shapes(kt, P, 70 + kt)
+        kw.update(shapes=_t(shapes), kernel_type=kt)
     if path == "hash":
         C = sp.C
         grid = rz.HashGridDesc(sp.L, sp.F, sp.S, sp.base_res, _t(sc.table), sc.offsets,
@@ -72,9 +91,10 @@ def _setup(oracle, sc, path, beta=0.0, sh_degree=3):
     campos = np.asarray(cam.camera_center, np.float32)
     if path == "hash":
         g = oracle.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
-        fwd = oracle.render(pre, b, W, H, C, g, homotrans=sc.homotrans, ap_level=ap, beta=beta)
+        fwd = oracle.render(pre, b, W, H, C, g, homotrans=sc.homotrans, ap_level=ap, beta=beta, kernel_type=kt,
+                            shapes=shapes)
         ob = oracle.render_backward(pre, b, fwd, W, H, C, g, dcol, doth, homotrans=sc.homotrans.reshape(-1, 16),
-                                    ap_level=ap, beta=beta)
+                                    ap_level=ap, beta=beta, kernel_type=kt, shapes=shapes)
         pb = oracle.preprocess_backward(sc.means, sc.scales, sc.rotations, pre["radii"], pre["transmat"],
                                         cam.world_view_transform, cam.full_proj_transform, W, H, ob["dtransmat"],
                                         ob["dhomo"], ob["dnormal"], ob["dmean2D"])
@@ -84,8 +104,9 @@ def _setup(oracle, sc, path, beta=0.0, sh_degree=3):
         else:
             cols, clamped = oracle.sh_colors(pre, sc.means, campos, shs, sh_degree)
             extra = dict(shs=shs, sh_degree=sh_degree, campos=campos, clamped=clamped)
-        fwd = oracle.render(pre, b, W, H, C, None, colors=cols, beta=beta)
-        ob = oracle.render_backward(pre, b, fwd, W, H, C, None, dcol, doth, colors=cols, beta=beta)
+        fwd = oracle.render(pre, b, W, H, C, None, colors=cols, beta=beta, kernel_type=kt, shapes=shapes)
+        ob = oracle.render_backward(pre, b, fwd, W, H, C, None, dcol, doth, colors=cols, beta=beta, kernel_type=kt,
+                                    shapes=shapes)
         pb = oracle.preprocess_backward(sc.means, sc.scales, sc.rotations, pre["radii"], pre["transmat"],
                                         cam.world_view_transform, cam.full_proj_transform, W, H, ob["dtransmat"],
                                         ob["dhomo"], ob["dnormal"], ob["dmean2D"], dcolors=ob["dcolors"], **extra)
@@ -99,6 +120,8 @@ def _setup(oracle, sc, path, beta=0.0, sh_degree=3):
         ref["dcolors"] = ob["dcolors"]
         if path == "sh":
             ref["dshs"] = pb["dshs"]
+    if kt:
+        ref["dshapes"] = ob["dshapes"]
     return gpu, ref, pre
 
 
@@ -134,6 +157,18 @@ def test_backward_hash_beta_parity(oracle):
     sc = scene("cfg1")
     print("[case] backward hash beta=0.8", flush=True)
     _compare(*_setup(oracle, sc, "hash", beta=0.8))
+
+
+@pytest.mark.parametrize("name,path,kt,beta", [("cfg1", "hash", 1, 0.0), ("unbounded_small", "hash", 3, 0.0),
+                                               ("shell_small", "hash", 2, 0.8), ("shell_small", "colors", 1, 0.0),
+                                               ("shell_small", "colors", 2, 1.5), ("shell_small", "sh", 3, 0.0)])
+def test_backward_kernel_types_parity(oracle, name, path, kt, beta):
+    """kernel_type 1 (beta), 2 (flex) and 3 (general) (CR/backward.cu:764-803,
+    :1864-1909, :1963-2039): every gradient and dL/dshape against the
+    oracle."""
+    sc = scene(name)
+    print(f"[case] backward kernel_type {kt} {path} {name} beta={beta}", flush=True)
+    _compare(*_setup(oracle, sc, path, beta=beta, kt=kt))
 
 
 @pytest.mark.parametrize("interp,align", [(0, False), (1, True)])
@@ -209,5 +244,49 @@ def test_autograd_through_drop_in_rasterizer():
              (ap.grad, gb.dgradsum)]
     for got, ref in pairs:
         assert got is not None and tuple(got.shape) == tuple(ref.shape)
+        err = _rel(got.cpu().numpy(), ref.cpu().numpy())
+        assert err < 1e-5, err
+
+
+def test_autograd_kernel_type_through_drop_in_rasterizer():
+    """kernel_type 3 through the drop-in: shapes.grad is the [P, 1] dL/dshape
+    of a direct nest_backward call (DSRpy:241-271 returns grad_shapes in the
+    shapes slot)."""
+    from diff_surfel_rasterization import GaussianRasterizationSettings, GaussianRasterizer, HashGridSettings
+    from nest_splat import rasterizer as rz
+    sc = scene("shell_small")
+    sp = sc.spec
+    cam = sc.cameras[0]
+    rs = GaussianRasterizationSettings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy,
+                                       torch.zeros(3, device=DEV), 1.0, _t(cam.world_view_transform),
+                                       _t(cam.full_proj_transform), 0, _t(cam.camera_center), False, False, 0.0,
+                                       sp.contract, False)
+    hs = HashGridSettings(0, 0.0, 0, False, 0, torch.tensor([0, 3, 3], dtype=torch.int32, device=DEV))
+    rng = np.random.default_rng(29)
+    cols = rng.uniform(0, 1, (sp.P, 3)).astype(np.float32)
+    shp = _shapes(3, sp.P, 91).reshape(-1, 1)
+    leaf = lambda a: _t(a).requires_grad_(True)
+    means, opac, scales, rots = leaf(sc.means), leaf(sc.opacity), leaf(sc.scales), leaf(sc.rotations)
+    shapes = leaf(shp)
+    color, radii, allmap, _, _ = GaussianRasterizer(rs, hs)(
+        means3D=means, means2D=torch.zeros(sp.P, 3, device=DEV), opacities=opac, colors_precomp=_t(cols),
+        scales=scales, rotations=rots, shapes=shapes, kernel_type=3)
+    dcol = _t(rng.standard_normal(tuple(color.shape)).astype(np.float32))
+    doth = _t(rng.standard_normal(tuple(allmap.shape)).astype(np.float32))
+    ((color * dcol).sum() + (allmap * doth).sum()).backward()
+    torch.cuda.synchronize()
+
+    settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy, cam.world_view_transform,
+                                cam.full_proj_transform, cam.camera_center, if_contract=sp.contract)
+    grid = rz.HashGridDesc(0, 1, 0.0, 0, None, np.zeros(1, np.int64), np.zeros(2, np.float32))
+    kw = dict(colors_precomp=_t(cols), channels=3, shapes=_t(shp.reshape(-1)), kernel_type=3)
+    res = rz.rasterize_forward(settings, grid, _t(sc.means), _t(sc.opacity), _t(sc.scales), _t(sc.rotations), **kw)
+    gb = rz.rasterize_backward(settings, grid, res, _t(sc.means), _t(sc.opacity), _t(sc.scales), _t(sc.rotations),
+                               dcol, doth, **kw)
+    torch.cuda.synchronize()
+    assert tuple(shapes.grad.shape) == (sp.P, 1)
+    assert np.abs(gb.dshapes.cpu().numpy()).max() > 0
+    for got, ref in [(shapes.grad.reshape(-1), gb.dshapes), (means.grad, gb.dmeans3D), (opac.grad, gb.dopacity),
+                     (scales.grad, gb.dscales), (rots.grad, gb.drotations)]:
         err = _rel(got.cpu().numpy(), ref.cpu().numpy())
         assert err < 1e-5, err

@@ -6,7 +6,10 @@ computes.  Tolerances are relative to each gradient array's largest entry:
 the oracle runs in float32 and reconstructs T by division, the torch side is
 float64 with exact products.  The largest error measured is 2.8e-5; the
 1e-4 bound leaves 3.5x, while a dropped or mis-signed term is an O(1)
-error.
+error.  The kernel types use 2e-4: the beta kernel's steeper position factor
+raises the same entry's error (the splat's Tw.z, where the Gaussian gives
+2.8e-5) to 9.0e-5, while the full derivative in place of the reference's
+half factor is off by 0.47.
 """
 import numpy as np
 import pytest
@@ -16,6 +19,7 @@ import torch_ref as TR
 from nest_splat.scene import get_spec, make_scene
 
 TOL = 1e-4
+TOL_KT = 2e-4
 
 
 def _tiny(L=4, F=2, P=60, W=48, H=32, log_scale=-2.2, seed=0):
@@ -31,7 +35,7 @@ def _rel(a, b):
     return float(np.abs(a - b).max() / scale)
 
 
-def _forward(oracle, sc, grid_on, beta=0.0, ap_level=None):
+def _forward(oracle, sc, grid_on, beta=0.0, ap_level=None, kernel_type=0, shapes=None):
     sp = sc.spec
     cam = sc.cameras[0]
     W, H = cam.image_width, cam.image_height
@@ -40,33 +44,60 @@ def _forward(oracle, sc, grid_on, beta=0.0, ap_level=None):
     b = oracle.binning(pre, W, H)
     if grid_on:
         g = oracle.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
-        r = oracle.render(pre, b, W, H, sp.C, g, homotrans=sc.homotrans, ap_level=ap_level, beta=beta)
+        r = oracle.render(pre, b, W, H, sp.C, g, homotrans=sc.homotrans, ap_level=ap_level, beta=beta,
+                          kernel_type=kernel_type, shapes=shapes)
     else:
         g = None
         colors = np.random.default_rng(5).uniform(0, 1, (sp.P, sp.C)).astype(np.float32)
-        r = oracle.render(pre, b, W, H, sp.C, None, colors=colors, beta=beta)
+        r = oracle.render(pre, b, W, H, sp.C, None, colors=colors, beta=beta, kernel_type=kernel_type, shapes=shapes)
         sc.__dict__["_colors"] = colors
     return pre, b, g, r, W, H
 
 
-@pytest.mark.parametrize("grid_on,beta", [(True, 0.0), (False, 0.0), (False, 1.5), (True, 0.7)])
-def test_render_backward_matches_autograd(oracle, grid_on, beta):
-    sc = _tiny(seed=int(grid_on) * 2 + int(beta > 0))
+def kernel_shapes(kt, P, seed):
+    """Per-splat kernel parameters in the ranges the reference trains them in:
+    beta-kernel shapes 0.2-4, flex betas 0-2 (every 7th exactly 0, so that
+    the splat falls back to the plain Gaussian), general exponents 2-8 (every
+    9th below 2)."""
+    rng = np.random.default_rng(seed)
+    if kt == 1:
+        return rng.uniform(0.2, 4.0, P).astype(np.float32)
+    if kt == 2:
+        v = rng.uniform(0.0, 2.0, P).astype(np.float32)
+        v[::7] = 0.0
+        return v
+    v = rng.uniform(2.0, 8.0, P).astype(np.float32)
+    v[::9] = rng.uniform(0.8, 2.0, v[::9].shape).astype(np.float32)
+    return v
+
+
+@pytest.mark.parametrize("grid_on,beta,kt", [(True, 0.0, 0), (False, 0.0, 0), (False, 1.5, 0), (True, 0.7, 0),
+                                             (False, 0.0, 1), (True, 0.0, 1), (False, 0.0, 2), (False, 0.9, 2),
+                                             (True, 0.0, 3), (False, 0.0, 3)])
+def test_render_backward_matches_autograd(oracle, grid_on, beta, kt):
+    """kernel_type 1-3 also pin dshapes, and their position terms follow the
+    reference's factors (the beta kernel's is half the derivative, a flex
+    splat without its own beta carries the settings' 1 + beta)."""
+    sc = _tiny(seed=int(grid_on) * 2 + int(beta > 0) + 5 * kt)
     sp = sc.spec
     ap = sc.ap_level.reshape(-1).copy()
     ap[::3] = 2.0  # some splats query fewer levels
-    pre, b, g, fwd, W, H = _forward(oracle, sc, grid_on, beta, ap)
+    shapes = None if kt == 0 else kernel_shapes(kt, sp.P, 40 + kt)
+    pre, b, g, fwd, W, H = _forward(oracle, sc, grid_on, beta, ap, kt, shapes)
     assert b["num_rendered"] > 0
     rng = np.random.default_rng(11)
     dpix = rng.standard_normal(fwd["color"].shape).astype(np.float32)
     doth = rng.standard_normal(fwd["others"].shape).astype(np.float32)
     homo = sc.homotrans.reshape(-1, 16).astype(np.float32)
     gb = oracle.render_backward(pre, b, fwd, W, H, sp.C, g, dpix, doth, homotrans=homo if grid_on else None,
-                                ap_level=ap, colors=None if grid_on else sc._colors, beta=beta)
+                                ap_level=ap, colors=None if grid_on else sc._colors, beta=beta, kernel_type=kt,
+                                shapes=shapes)
 
     leaf = lambda a: torch.tensor(np.asarray(a, np.float64), requires_grad=True)
     leaves = dict(T=leaf(pre["transmat"]), xy=leaf(pre["xy"]), normal=leaf(pre["normal_opacity"][:, :3]),
                   opacity=leaf(pre["normal_opacity"][:, 3]))
+    if kt:
+        leaves["shape"] = leaf(shapes)
     gd = None
     if grid_on:
         leaves["homo"] = leaf(homo)
@@ -76,7 +107,7 @@ def test_render_backward_matches_autograd(oracle, grid_on, beta):
     else:
         leaves["colors"] = leaf(sc._colors)
     color, others = TR.render_forward(oracle, pre, b, fwd, W, H, sp.C, leaves, grid=gd, beta=beta,
-                                      homotrans_np=homo, ap_level=ap)
+                                      homotrans_np=homo, ap_level=ap, kernel_type=kt)
     # the torch forward is the oracle's forward
     assert _rel(color.detach().numpy(), fwd["color"]) < 1e-4
     assert _rel(others.detach().numpy(), fwd["others"][:7]) < 1e-3
@@ -97,6 +128,8 @@ def test_render_backward_matches_autograd(oracle, grid_on, beta):
         checks["dtable"] = (gb["dtable"], leaves["table"].grad)
     else:
         checks["dcolors"] = (gb["dcolors"], leaves["colors"].grad)
+    if kt:
+        checks["dshapes"] = (gb["dshapes"], leaves["shape"].grad)
     for name, (ours, ref) in checks.items():
         ref = ref.numpy() if isinstance(ref, torch.Tensor) else ref
         if name != "dtable":
@@ -104,7 +137,7 @@ def test_render_backward_matches_autograd(oracle, grid_on, beta):
         assert np.abs(ref).max() > 0, name
         err = _rel(ours, ref)
         print(f"{name}: rel err {err:.2e}")
-        assert err < TOL, (name, err)
+        assert err < (TOL_KT if kt else TOL), (name, err)
 
 
 def test_preprocess_backward_matches_autograd(oracle):

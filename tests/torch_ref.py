@@ -47,9 +47,10 @@ def grid_index(align, hsize, res, g):
     return (index % np.uint64(hsize)).astype(np.int64)
 
 
-def _pair_decisions(O, Tm, xy, opa, px, py, beta):
+def _pair_decisions(O, Tm, xy, opa, px, py, beta, kernel_type=0, shp=None):
     """float32 replica of the per-pair acceptance (CR/forward.cu:834-921):
-    returns accepted, use3d, the float32 s (for the cells) and alpha."""
+    returns accepted, use3d, the float32 s (for the cells) and alpha.
+    kernel_type 1-3 take the per-splat shapes shp (CR/forward.cu:864-900)."""
     Tu, Tv, Tw = Tm[..., 0:3], Tm[..., 3:6], Tm[..., 6:9]
     k = px[..., None] * Tw - Tu
     l = py[..., None] * Tw - Tv
@@ -64,12 +65,25 @@ def _pair_decisions(O, Tm, xy, opa, px, py, beta):
     use3d = rho3d <= rho2d
     rho = np.minimum(rho3d, rho2d)
     depth = np.where(use3d, (sx * Tw[..., 0] + sy * Tw[..., 1]) + Tw[..., 2], Tw[..., 2])
-    with np.errstate(over="ignore", invalid="ignore"):
-        G = O.expf(f32(-0.5) * rho)
-        if beta > 0:
-            G = ((1.0 + beta) * G.astype(np.float64) / (1.0 + (f32(beta) * G).astype(np.float64))).astype(f32)
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        ok = f32(-0.5) * rho <= 0
+        if kernel_type == 1:
+            ok = rho < f32(1)
+            G = O.powf(np.where(ok, f32(1) - rho, f32(0.5)), shp)
+        elif kernel_type == 2:
+            g = O.expf(f32(-0.5) * rho)
+            b = np.broadcast_to(shp, g.shape).astype(f32)
+            G = np.where(b > 0, (f32(1) + b) * g / (f32(1) + b * g), g).astype(f32)
+        elif kernel_type == 3:
+            pt = O.powf(np.maximum(rho, f32(1e-8)), f32(0.5) * shp)
+            ok = f32(-0.5) * pt <= 0
+            G = O.expf(f32(-0.5) * pt)
+        else:
+            G = O.expf(f32(-0.5) * rho)
+            if beta > 0:
+                G = ((1.0 + beta) * G.astype(np.float64) / (1.0 + (f32(beta) * G).astype(np.float64))).astype(f32)
         alpha = np.minimum(f32(0.99), opa * G)
-    acc = (p2 != 0) & (depth >= f32(NEAR)) & (f32(-0.5) * rho <= 0) & (alpha >= f32(1.0 / 255.0))
+    acc = (p2 != 0) & (depth >= f32(NEAR)) & ok & (alpha >= f32(1.0 / 255.0))
     return acc, use3d, sx, sy, alpha
 
 
@@ -98,7 +112,32 @@ def _pixel_cutoff(acc, alpha):
     return take, last, med
 
 
-def render_forward(O, pre, binres, fwd, W, H, C, leaves, grid=None, beta=0.0, homotrans_np=None, ap_level=None):
+def _kernel_g(kernel_type, rho, shp, beta):
+    """G of kernel_type 1-3 in float64 with the gradients the reference's
+    backward gives it (CR/backward.cu:1864-1909, :1963-2039): the beta
+    kernel's position term is half the derivative (dG/drho where the other
+    kernels use 2 dG/drho), its shape term G ln(1 - rho); a flex splat
+    without its own beta (<= 0) has G = g with the position gradient scaled
+    by 1 + beta of the settings when that is > 0; flex with beta > 0 and the
+    general kernel are exact derivatives."""
+    if kernel_type == 1:
+        rho_h = rho.detach() + 0.5 * (rho - rho.detach())
+        return torch.clamp_min(1.0 - rho_h, 1e-30) ** shp
+    if kernel_type == 2:
+        g = torch.exp(-0.5 * rho)
+        on = shp > 0
+        if beta > 0:
+            g_pos = g.detach() + (g - g.detach()) * (1.0 + beta)
+        else:
+            g_pos = g
+        bsafe = torch.where(on, shp, torch.zeros_like(shp))
+        return torch.where(on, (1.0 + bsafe) * g / (1.0 + bsafe * g), g_pos)
+    pt = torch.clamp_min(rho, 1e-8) ** (0.5 * shp)
+    return torch.exp(-0.5 * pt)
+
+
+def render_forward(O, pre, binres, fwd, W, H, C, leaves, grid=None, beta=0.0, homotrans_np=None, ap_level=None,
+                   kernel_type=0):
     """Differentiable forward of out_color [C,H,W] and allmap channels 0..6.
 
     leaves: dict of float64 tensors with requires_grad: T [P,9], xy [P,2],
@@ -106,7 +145,8 @@ def render_forward(O, pre, binres, fwd, W, H, C, leaves, grid=None, beta=0.0, ho
     and table [rows,F] (hash path), with rows [P,R] ahead of the grid
     features in render mode 4, or rows [P,total*F+1] blended with them in
     render mode 12 (grid["hyb12"] = per-splat levels).  grid: dict(L, F, S, H, offsets, vmin,
-    vmax) for the hash path (non-contracted, not align_corners, linear)."""
+    vmax) for the hash path (non-contracted, not align_corners, linear).
+    kernel_type 1-3 take leaves["shape"] [P]."""
     HW = W * H
     gx = (W + 15) // 16
     ranges = binres["ranges"].reshape(-1, 2)
@@ -128,8 +168,10 @@ def render_forward(O, pre, binres, fwd, W, H, C, leaves, grid=None, beta=0.0, ho
         pid = py * W + px
         ids = vals[r0:r1].astype(np.int64)
         n = ids.shape[0]
+        shp32 = None if kernel_type == 0 else leaves["shape"].detach().numpy().astype(f32)[ids][None]
         acc, use3d, sx32, sy32, a32 = _pair_decisions(O, Tm32[ids][None], xy32[ids][None], no32[ids, 3][None],
-                                                      px.astype(f32)[:, None], py.astype(f32)[:, None], beta)
+                                                      px.astype(f32)[:, None], py.astype(f32)[:, None], beta,
+                                                      kernel_type, shp32)
         acc, last, med = _pixel_cutoff(acc, a32)
         np.testing.assert_array_equal(last, ncon[0, pid])
         np.testing.assert_array_equal(med, ncon[1, pid])
@@ -154,8 +196,13 @@ def render_forward(O, pre, binres, fwd, W, H, C, leaves, grid=None, beta=0.0, ho
         rho2d = 2.0 * (dx * dx + dy * dy)
         rho = torch.where(u3, rho3d, rho2d)
         depth = torch.where(u3, (sx * Tw[..., 0] + sy * Tw[..., 1]) + Tw[..., 2], Tw[..., 2].expand_as(sx))
-        G = torch.exp(-0.5 * torch.where(accT, rho, torch.zeros_like(rho)))
-        if beta > 0:
+        rho_a = torch.where(accT, rho, torch.zeros_like(rho))
+        if kernel_type != 0:
+            G = _kernel_g(kernel_type, rho_a, leaves["shape"][ids][None].expand_as(rho_a), beta)
+            G = torch.where(accT, G, torch.zeros_like(G))
+        else:
+            G = torch.exp(-0.5 * rho_a)
+        if beta > 0 and kernel_type == 0:
             # the reference differentiates the position through -G' s with the
             # activated G' = (1+b) g / (1+b g) where the chain rule has -g s
             # (CR/backward.cu:1910-1913, :1977): value G', gradient scaled by G'/g
