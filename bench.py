@@ -386,6 +386,10 @@ def main():
                     help="after the timed frames, time K launches of the other hot-path kernels on their own: the RVQ "
                          "decode of the 500k-splat compressed scene and the GridEncoder forward of 1M points on this "
                          "grid; reports aux_kernels with algorithmic GB/s (not part of the metric)")
+    ap.add_argument("--record", type=int, default=0, metavar="K",
+                    help="after the timed frames, time K frames with record_transmittance=True (the densification "
+                         "statistic's extra pass) and report record_ms: render stage and frame with and without it "
+                         "(not part of the metric)")
     ap.add_argument("--backward", type=int, default=0, metavar="K",
                     help="after the timed forward frames, time K backward passes (nest_backward) of the last frame "
                          "with random output gradients and report backward_ms (not part of the metric)")
@@ -508,6 +512,27 @@ def main():
                                      table, mlp, wl.rays[-1], bg, dev)
     if args.kernels > 0:
         out["aux_kernels"] = time_aux_kernels(args.kernels, spec, scene, table, dev)
+    if args.record > 0:
+        rec_ms = {}
+        for rec in (False, True):
+            def rframe(tm):
+                r = rz.rasterize_forward(settings, grid, means, opac, scales, rots, homotrans=homo, ap_level=ap_level,
+                                         channels=spec.C, timing=tm, record_transmittance=rec)
+                return r, mlp.decode_image(r.color, wl.rays[-1], alpha=r.others[1], bg=bg)
+            rframe(False)
+            torch.cuda.synchronize()
+            rtms = [L.new_timing(True) for _ in range(args.record)]
+            r0 = time.perf_counter()
+            for k in range(args.record):
+                rframe(rtms[k])
+            torch.cuda.synchronize()
+            fr = (time.perf_counter() - r0) / args.record * 1e3
+            rr = float(np.mean([L.timing_read(tm)["render"] for tm in rtms]))
+            for tm in rtms:
+                L.timing_release(tm)
+            rec_ms["with_record" if rec else "without"] = {"render_ms": round(rr, 4), "frame_ms": round(fr, 4)}
+            log(f"[bench] record_transmittance={rec}: render stage {rr:.3f} ms, frame {fr:.3f} ms")
+        out["record_ms"] = rec_ms
     if args.backward > 0:
         gen = torch.Generator(device=dev).manual_seed(0)
         dcol = torch.randn(tuple(res.color.shape), generator=gen, device=dev)

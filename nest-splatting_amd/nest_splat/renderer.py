@@ -7,6 +7,14 @@ The rasterizer runs through the drop-in diff_surfel_rasterization API; the MLP
 decode runs fused (view directions, SH encoding, MLP, sigmoid, mask,
 background) in one kernel on the channel-major feature map, so the
 permute().contiguous() copy of the reference disappears.
+
+The SH-rasterised appearance modes (gaussian_renderer/__init__.py:88-114,
+:686-692, :799-903) compose the same kernels: ``diffuse`` and ``specular``
+rasterise SH colours (degree 0, resp. the active degree); ``diffuse_ngp`` adds
+the hash grid's MLP colour at the back-projected median depth; and
+``diffuse_offset`` queries the grid at that point moved by the rendered
+colour - 0.5 (clamped to +-0.1), or at the blended splat centres of allmap
+8:11 with ``use_xyz_mode``.
 """
 from __future__ import annotations
 
@@ -57,13 +65,20 @@ class SplatModel:
     """The GaussianModel getters the forward render reads
     (scene/gaussian_model.py:231-317), over activated attributes."""
 
-    def __init__(self, xyz, scaling, rotation, opacity, ap_level=None, homotrans=None):
+    def __init__(self, xyz, scaling, rotation, opacity, ap_level=None, homotrans=None, features=None,
+                 active_sh_degree: int = 0):
         self._xyz = xyz
         self._scaling = scaling
         self._rotation = rotation
         self._opacity = opacity.reshape(-1, 1)
         self._ap = ap_level if ap_level is not None else torch.full((xyz.shape[0], 1), 24.0, device=xyz.device)
         self._homotrans = homotrans
+        self._features = features  # [P, (max_sh_degree + 1)^2, 3] SH coefficients, DC first
+        self.active_sh_degree = active_sh_degree
+
+    @property
+    def get_features(self):
+        return self._features
 
     @property
     def get_xyz(self):
@@ -112,6 +127,36 @@ class HashINGP:
     def rgb_decode(self, features, ray_unit):
         return self.mlp_rgb.rgb_decode(features, ray_unit)
 
+    def __call__(self, points_3D: torch.Tensor, with_xyz: bool = False) -> torch.Tensor:
+        """INGP.forward (hash_encoder/modules.py:574-585): grid features of
+        world points [N, 3], the levels past active_levels masked to zero."""
+        feat = self.encode_3D(points_3D)
+        if self.active_levels < self.levels:
+            mask = torch.zeros_like(feat)
+            mask[..., :self.active_levels * self.level_dim] = 1
+            feat = feat * mask
+        if with_xyz:
+            feat = torch.cat([feat, points_3D], dim=-1)
+        return feat.float()
+
+    def encode_3D(self, points_3D: torch.Tensor) -> torch.Tensor:
+        """INGP._encode_3D (hash_encoder/modules.py:697-725): normalise to
+        [0, 1] over the grid range (through the contraction of the space
+        outside the unit ball when contract is set), then the GridEncoder."""
+        vol_min, vol_max = float(self._gridrange_host[0]), float(self._gridrange_host[1])
+        if not self.contract:
+            x = (points_3D - vol_min) / (vol_max - vol_min)
+        else:
+            vmid = (vol_min + vol_max) * 0.5
+            vsize = (vol_max - vol_min) * 0.5
+            x = (points_3D - vmid) / vsize
+            norm = x.norm(dim=-1, keepdim=True)
+            inv_norm = 1.0 / norm
+            x = x * torch.where(norm <= 1.0, torch.ones_like(norm), (2.0 - inv_norm) * inv_norm)
+            x = (x + 2.0) * 0.25
+        out = self.hash_encoding(x.reshape(-1, 3))
+        return out.view(*x.shape[:-1], out.shape[-1])
+
 
 @dataclass
 class Pipe:
@@ -124,18 +169,30 @@ def _matrix(x, device) -> torch.Tensor:
     return torch.from_numpy(np.asarray(x, dtype=np.float32)).to(device)
 
 
-def depth_to_normal(cam, depth: torch.Tensor) -> torch.Tensor:
-    """utils/point_utils.py:10-29, :48-60."""
+def cam2rays(cam, device) -> tuple:
+    """utils/point_utils.py:31-46: per-pixel ray directions [H*W, 3] (row
+    major, not normalised) and the camera centre [3]."""
     W, H = cam.image_width, cam.image_height
-    dev = depth.device
-    wv = _matrix(cam.world_view_transform, dev)
+    wv = _matrix(cam.world_view_transform, device)
     c2w = torch.linalg.inv(wv.T)
-    M = torch.from_numpy(view_ray_matrix(cam)).to(dev)
-    gx, gy = torch.meshgrid(torch.arange(W, device=dev).float(), torch.arange(H, device=dev).float(), indexing="xy")
+    M = torch.from_numpy(view_ray_matrix(cam)).to(device)
+    gx, gy = torch.meshgrid(torch.arange(W, device=device).float(), torch.arange(H, device=device).float(),
+                            indexing="xy")
     pts = torch.stack([gx, gy, torch.ones_like(gx)], dim=-1).reshape(-1, 3)
-    rays_d = pts @ M
-    rays_o = c2w[:3, 3]
-    points = (depth.reshape(-1, 1) * rays_d + rays_o).reshape(H, W, 3)
+    return pts @ M, c2w[:3, 3]
+
+
+def depths_to_points(cam, depth: torch.Tensor) -> tuple:
+    """utils/point_utils.py:10-29: the depth map [1, H, W] back-projected
+    along the pixel rays; returns points [H*W, 3], rays_d, rays_o."""
+    rays_d, rays_o = cam2rays(cam, depth.device)
+    return depth.reshape(-1, 1) * rays_d + rays_o, rays_d, rays_o
+
+
+def depth_to_normal(cam, depth: torch.Tensor) -> torch.Tensor:
+    """utils/point_utils.py:48-60."""
+    W, H = cam.image_width, cam.image_height
+    points = depths_to_points(cam, depth)[0].reshape(H, W, 3)
     out = torch.zeros_like(points)
     dx = points[2:, 1:-1] - points[:-2, 1:-1]
     dy = points[1:-1, 2:] - points[1:-1, :-2]
@@ -143,8 +200,20 @@ def depth_to_normal(cam, depth: torch.Tensor) -> torch.Tensor:
     return out
 
 
+SH_MODES = ("diffuse", "specular", "diffuse_ngp", "diffuse_offset")
+
+
 def render(viewpoint_camera, pc, pipe, bg_color: torch.Tensor, scaling_modifier=1.0, ingp: HashINGP = None, beta=0,
-           max_intersections=0, skip_mlp=False, with_surface=True):
+           max_intersections=0, skip_mlp=False, with_surface=True, mode: str = "baseline", use_xyz_mode: bool = False,
+           record_transmittance: bool = False):
+    """mode: "baseline" (the hash grid rasterised in the kernel, then the MLP)
+    or one of the SH-rasterised modes "diffuse", "specular", "diffuse_ngp",
+    "diffuse_offset" (the reference's ingp.is_*_mode flags)."""
+    if mode in SH_MODES:
+        return _render_sh(viewpoint_camera, pc, pipe, bg_color, scaling_modifier, ingp, beta, max_intersections,
+                          with_surface, mode, use_xyz_mode, record_transmittance)
+    if mode != "baseline":
+        raise ValueError(f"mode must be 'baseline' or one of {SH_MODES} (got {mode!r})")
     from diff_surfel_rasterization import GaussianRasterizationSettings, GaussianRasterizer, HashGridSettings
 
     dev = pc.get_xyz.device
@@ -194,6 +263,69 @@ def render(viewpoint_camera, pc, pipe, bg_color: torch.Tensor, scaling_modifier=
 
     if with_surface:
         rets.update(surface_maps(viewpoint_camera, allmap, getattr(pipe, "depth_ratio", 0.0)))
+    return rets
+
+
+def _render_sh(cam, pc, pipe, bg_color, scaling_modifier, ingp, beta, max_intersections, with_surface, mode,
+               use_xyz_mode, record_transmittance):
+    """gaussian_renderer/__init__.py:88-114 (mode flags, no grid in the
+    rasteriser), :686-760 (SH degree 0 for the diffuse modes), :799-903 (the
+    grid queried at the back-projected median depth, or offset by the rendered
+    colour), :1013-1046 (background and output keys)."""
+    from diff_surfel_rasterization import GaussianRasterizationSettings, GaussianRasterizer, HashGridSettings
+
+    if pc.get_features is None:
+        raise ValueError(f"mode {mode!r} rasterises SH colours: the splat model needs features")
+    if mode in ("diffuse_ngp", "diffuse_offset") and ingp is None:
+        raise ValueError(f"mode {mode!r} queries the hash grid: pass ingp")
+    dev = pc.get_xyz.device
+    H, W = int(cam.image_height), int(cam.image_width)
+    means2D = torch.zeros_like(pc.get_xyz)
+    raster_settings = GaussianRasterizationSettings(
+        image_height=H, image_width=W, tanfovx=math.tan(cam.FoVx * 0.5), tanfovy=math.tan(cam.FoVy * 0.5),
+        bg=bg_color, scale_modifier=scaling_modifier, viewmatrix=cam.world_view_transform,
+        projmatrix=cam.full_proj_transform, sh_degree=0 if mode != "specular" else int(pc.active_sh_degree),
+        campos=cam.camera_center, prefiltered=False, debug=False, beta=beta, if_contract=False,
+        record_transmittance=record_transmittance, max_intersections=max_intersections)
+    hashgrid_settings = HashGridSettings(L=0, S=0.0, H=0, align_corners=False, interpolation=0,
+                                         shape_dims=torch.tensor([0, 3, 3], dtype=torch.int32))
+    rasterizer = GaussianRasterizer(raster_settings=raster_settings, hashgrid_settings=hashgrid_settings)
+    image, radii, allmap, trans_avg, cover = rasterizer(
+        means3D=pc.get_xyz, means2D=means2D, shs=pc.get_features, colors_precomp=None, opacities=pc.get_opacity,
+        scales=pc.get_scaling, rotations=pc.get_rotation)
+    render_alpha = allmap[1:2]
+    rets = {"viewspace_points": means2D, "visibility_filter": radii > 0, "radii": radii, "allmap": allmap}
+    if mode in ("diffuse_ngp", "diffuse_offset"):
+        mask = render_alpha > 0
+        median = torch.nan_to_num(allmap[5:6], 0, 0)
+        if mode == "diffuse_ngp":
+            rets["gaussian_rgb"] = image.clone()
+            points, rays_d, _ = depths_to_points(cam, median.detach())
+        else:
+            # the rendered colour minus 0.5 is the offset, clamped to +-0.1
+            offset = torch.clamp(image.permute(1, 2, 0).reshape(-1, 3) - 0.5, -0.1, 0.1)
+            rets["gaussian_rgb"] = image.clone() - 0.5
+            if use_xyz_mode:
+                base = allmap[8:11].permute(1, 2, 0).reshape(-1, 3)
+                points = base.detach() + offset
+                rays_d, _ = cam2rays(cam, dev)
+                rets["scout_loss_data"] = {"points_base": base, "points_target": points.detach(),
+                                           "render_mask": mask}
+            else:
+                p0, rays_d, _ = depths_to_points(cam, median.detach())
+                points = p0.detach() + offset
+        feats = ingp(points, with_xyz=False)
+        ngp = ingp.rgb_decode(feats, torch_F.normalize(rays_d, dim=-1).float())
+        ngp = ngp.view(H, W, 3).permute(2, 0, 1) * mask
+        rets["ngp_rgb"] = ngp.clone()
+        image = image + ngp if mode == "diffuse_ngp" else ngp
+    if float(bg_color.sum()) > 0:
+        image = image + (1.0 - render_alpha) * bg_color.to(dev).unsqueeze(-1).unsqueeze(-1)
+    rets["render"] = image
+    if record_transmittance:
+        rets.update({"transmittance_avg": trans_avg, "cover_pixels": cover})
+    if with_surface:
+        rets.update(surface_maps(cam, allmap, getattr(pipe, "depth_ratio", 0.0)))
     return rets
 
 
