@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 11
+#define NEST_ABI_VERSION 12
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -76,7 +76,7 @@ typedef struct nest_raster_settings {
 typedef struct nest_hashgrid {
   uint32_t struct_size;
   uint32_t levels;            /* L queried; 0 selects the colours_precomp path in mode 0 */
-  uint32_t level_dim;         /* F: 1, 2, 4 or 8 */
+  uint32_t level_dim;         /* F: 1, 2, 4 or 8 (3 in render modes 8-10) */
   float log2_scale;           /* S = log2(per_level_scale) */
   uint32_t base_resolution;   /* H */
   int32_t align_corners;
@@ -116,7 +116,17 @@ typedef struct nest_hashgrid {
    *     colors_precomp rows of hybrid_levels*level_dim features plus a
    *     weight; the grid's `levels` levels follow, times the weight, when the
    *     weight is > 1e-6 (training) or >= 0.1 (inference), else zero; full
-   *     hits (CR/forward.cu:1716-1830).
+   *     hits (CR/forward.cu:1716-1830);
+   *   NEST_MODE_HYBRID_SH (8), NEST_MODE_HYBRID_SH_POST (9),
+   *   NEST_MODE_HYBRID_SH_RAW (10) (CR/forward.cu:1378-1542; GR:605-680):
+   *     a grid of at most one level with level_dim 3 (float32) looked up at
+   *     the hit, and colors_precomp rows of 3 raw SH colours (8, 10) or of 48
+   *     SH coefficients channel-major (9; DC terms at 0, 16, 32).  Mode 8
+   *     writes clamp(clamp(raw + 0.5, 0, 1) + sigmoid(grid), 0, 1), mode 10
+   *     sigmoid(raw + grid), mode 9 the coefficients with the grid added to
+   *     the DC terms; `decompose` 1 (gaussian_only) leaves the grid out, 2
+   *     (ngp_only) the colour.  out_color needs 3 (8, 10) or 48 (9)
+   *     channels; the channels past them stay 0.
    * Modes 4, 7 and 12-14 need level_dim 2, 4 or 8 and at most 64 channels of
    * per-splat plus grid features; `levels` may be 0 there. */
   int32_t render_mode;
@@ -129,11 +139,17 @@ typedef struct nest_hashgrid {
    * copy (CR/backward.cu:576-612, :993-999), while the forward renders all
    * `levels`; nest_backward does the same.  The forward ignores it. */
   uint32_t active_levels;
+  /* Render modes 8-10: 0 both parts, 1 gaussian_only, 2 ngp_only (bits 24-31
+   * of the reference's packed level, GR:619-626).  Other modes ignore it. */
+  uint32_t decompose;
 } nest_hashgrid;
 
 #define NEST_MODE_BASELINE 0
 #define NEST_MODE_CAT 4
 #define NEST_MODE_ADAPTIVE_ADD 7
+#define NEST_MODE_HYBRID_SH 8
+#define NEST_MODE_HYBRID_SH_POST 9
+#define NEST_MODE_HYBRID_SH_RAW 10
 #define NEST_MODE_ADAPTIVE_CAT 12
 #define NEST_MODE_ADAPTIVE_CAT_FAST 13
 #define NEST_MODE_ADAPTIVE_ZERO 14

@@ -194,13 +194,35 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
   const int base_mode = gr->render_mode & 0xFF;
   const bool adaptive = base_mode == NEST_MODE_ADAPTIVE_CAT || base_mode == NEST_MODE_ADAPTIVE_CAT_FAST ||
                         base_mode == NEST_MODE_ADAPTIVE_ZERO;
+  const bool hsh = base_mode >= NEST_MODE_HYBRID_SH && base_mode <= NEST_MODE_HYBRID_SH_RAW;
   if ((gr->render_mode & ~0x1FF) != 0 ||
       (base_mode != NEST_MODE_BASELINE && base_mode != NEST_MODE_CAT && base_mode != NEST_MODE_ADAPTIVE_ADD &&
-       !adaptive) ||
+       !adaptive && !hsh) ||
       ((gr->render_mode & NEST_MODE_INFERENCE) && !adaptive))
-    return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: supported are 0, 4, 7, 12, 13, 14 and 12, 13, 14 | 0x100",
-                gr->render_mode);
-  const bool mix = base_mode != NEST_MODE_BASELINE;
+    return fail(NEST_ERR_UNSUPPORTED,
+                "render_mode %d: supported are 0, 4, 7, 8, 9, 10, 12, 13, 14 and 12, 13, 14 | 0x100", gr->render_mode);
+  const bool mix = base_mode != NEST_MODE_BASELINE && !hsh;
+  if (hsh) {
+    // one 3-channel float32 grid level and rows of 3 raw colours or 48 SH
+    // coefficients (CR/forward.cu:1378-1542)
+    if (gr->levels > 1)
+      return fail(NEST_ERR_UNSUPPORTED, "render_mode %d looks up one grid level (levels must be 0 or 1, got %u)",
+                  base_mode, gr->levels);
+    if (gr->levels == 1 && (gr->level_dim != 3 || gr->table_dtype != NEST_DTYPE_F32))
+      return fail(NEST_ERR_UNSUPPORTED, "render_mode %d needs a float32 grid with level_dim 3", base_mode);
+    if (gr->decompose > 2)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "decompose must be 0, 1 or 2 (got %u)", gr->decompose);
+    const int need = base_mode == NEST_MODE_HYBRID_SH_POST ? 48 : 3;
+    if (channels < need)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "out_color has %d channels, render_mode %d produces %d", channels,
+                  base_mode, need);
+    if (sp->P > 0) {
+      if (!sp->homotrans) return fail(NEST_ERR_INVALID_ARGUMENT, "homotrans is required in render_mode %d", base_mode);
+      if (!sp->colors_precomp)
+        return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode %d needs the per-splat rows (%d floats) in colors_precomp",
+                    base_mode, need);
+    }
+  }
   if (mix) {
     const uint32_t F = gr->level_dim, hyb = gr->hybrid_levels;
     if (F != 2 && F != 4 && F != 8)
@@ -235,7 +257,7 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
     g.F = F;
   }
   if (gr->levels > 0) {
-    if (gr->level_dim != 1 && gr->level_dim != 2 && gr->level_dim != 4 && gr->level_dim != 8)
+    if (!hsh && gr->level_dim != 1 && gr->level_dim != 2 && gr->level_dim != 4 && gr->level_dim != 8)
       return fail(NEST_ERR_UNSUPPORTED, "level_dim must be 1, 2, 4 or 8 (got %u)", gr->level_dim);
     if (gr->levels > NEST_MAX_LEVELS || gr->levels * gr->level_dim > NEST_MAX_CHANNELS)
       return fail(NEST_ERR_UNSUPPORTED, "levels*level_dim must be <= %d (got %u*%u)", NEST_MAX_CHANNELS, gr->levels,
@@ -483,7 +505,13 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   rp.max_intersections = rs->max_intersections;
   rp.kernel_type = sp->kernel_type;
   if ((rc = setup_grid(rs, gr, sp, out->channels, rp.grid))) return rc;
-  if ((gr->render_mode & 0xFF) != NEST_MODE_BASELINE) {
+  const int base_mode = gr->render_mode & 0xFF;
+  if (base_mode >= NEST_MODE_HYBRID_SH && base_mode <= NEST_MODE_HYBRID_SH_RAW) {
+    // hybrid SH (CR/forward.cu:1378-1542): rows of 3 raw colours or 48 SH coefficients
+    rp.hsh = base_mode;
+    rp.hsh_dec = (int)gr->decompose;
+    rp.cstride = base_mode == NEST_MODE_HYBRID_SH_POST ? 48 : 3;
+  } else if (base_mode != NEST_MODE_BASELINE) {
     // per-splat features ahead of the grid's (CR/forward.cu:965-1101, :1218-1282)
     const int F = (int)gr->level_dim;
     rp.mix = 1;

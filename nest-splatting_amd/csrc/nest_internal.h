@@ -142,6 +142,11 @@ struct RenderParams {
   uint32_t nfast;             // levels of the row past pgd that a fast hit takes
   uint32_t nblend;            // levels past pgd a blend hit covers: the grid's in modes 12, 13;
                               // the row's in mode 7 (the grid zero past its levels)
+  // Hybrid SH modes 8, 9, 10 (0 otherwise): a hit's channels come from its
+  // colors row (3 or 48 floats) and one 3-channel grid level at the hit;
+  // hsh_dec 1 leaves the grid out, 2 the row's colour.
+  int hsh;
+  int hsh_dec;
 };
 
 // Host-side launchers (defined in the .hip files).  Each returns the

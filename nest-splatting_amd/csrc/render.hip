@@ -579,6 +579,66 @@ __device__ __forceinline__ void appearance_colour(uint32_t ap, float w, float& v
   vis1 += apc1 * w;
 }
 
+// Hybrid SH modes (CR/forward.cu:1378-1542): query_feature<false, 3, 3> with
+// one level at the hit's world point, zero when it is outside the grid, the
+// splat's appearance level is 0 or the grid has no level.
+__device__ __forceinline__ void hsh_query(const GridParams& g, const float xyz[3], uint32_t ap, float h[3]) {
+  h[0] = h[1] = h[2] = 0.0f;
+  if (g.L == 0u) return;
+  float u[3];
+  bool oob;
+  grid_coord(g, xyz, u, oob);
+  if (oob || ap == 0u) return;
+  LevelCorners cn;
+  level_corners<3, false>(g.lv, 0, g.pos_offset, g.interp, u, cn);
+  const float* t = static_cast<const float*>(g.table) + (size_t)g.lv.base[0] * 3u;
+  float vals[8][3];
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const float* e = t + (size_t)cn.idx[k] * 3u;
+    vals[k][0] = e[0];
+    vals[k][1] = e[1];
+    vals[k][2] = e[2];
+  }
+  corners_sum<3>(cn, vals, h);
+}
+
+__device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + expf_ref(-x)); }
+
+// A hit's channels in the hybrid SH modes, accumulated as fmaf(feat, w, acc):
+// mode 8 clamp(clamp(raw + 0.5) + sigmoid(h)), mode 10 sigmoid(raw + h)
+// (decompose 2: of h alone, 1: of raw alone), mode 9 the 48 coefficients
+// with h added to (decompose 2: in place of) the DC terms 0, 16, 32.
+template <int kHsh, int NACC>
+__device__ __forceinline__ void hsh_accumulate(const RenderParams& p, const float* row, const float h[3], float w,
+                                               float* acc) {
+  const int dec = p.hsh_dec;
+  if constexpr (kHsh == 9) {
+#pragma unroll
+    for (int c = 0; c < NACC; c++) {
+      float v = row[c];
+      if (c % 16 == 0 && c < 48) {
+        const float hc = h[c / 16];
+        v = dec == 2 ? hc : (dec == 1 ? v : v + hc);
+      }
+      if (c < p.C) acc[c] = fmaf(v, w, acc[c]);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 3; c++) {
+      float v;
+      if constexpr (kHsh == 8) {
+        const float gc = fmaxf(0.0f, fminf(1.0f, row[c] + 0.5f));
+        const float sc = sigmoid_ref(h[c]);
+        v = dec == 2 ? sc : (dec == 1 ? gc : fmaxf(0.0f, fminf(1.0f, gc + sc)));
+      } else {
+        v = sigmoid_ref(dec == 2 ? h[c] : (dec == 1 ? row[c] : row[c] + h[c]));
+      }
+      if (c < p.C) acc[c] = fmaf(v, w, acc[c]);
+    }
+  }
+}
+
 // LDS (32 KB of staged records + 17 KB of queue) allows three workgroups per
 // CU; amdgpu_waves_per_eu(3) gives the matching 168-VGPR budget, which holds
 // 64 accumulators and eight in-flight 16-byte corner loads.
@@ -589,7 +649,10 @@ __device__ __forceinline__ void appearance_colour(uint32_t ap, float w, float& v
 // the level count, 53 KB of LDS in all.
 // kKT: the splats' kernel comes from p.kernel_type (1-3 possible); without
 // it the kernel is the Gaussian, and the kernel-type branch compiles out.
-template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0, bool kKT = false>
+// kHsh: render modes 8, 9, 10 on the colour path's loop (no queue): each hit
+// looks its one grid level up in place.
+template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0, bool kKT = false,
+          int kHsh = 0>
 __global__ void __launch_bounds__(kRenderThreads) __attribute__((amdgpu_waves_per_eu(3, 8)))
 render_kernel(const RenderParams p) {
   __shared__ float4 srec[kRecChunks][kBatch];
@@ -700,7 +763,22 @@ render_kernel(const RenderParams p) {
           ph.hit = hit;
           break;
         }
-        if constexpr (!kHash) {
+        if constexpr (kHsh != 0) {
+          float xyz[3];
+          hit_world(srec[4][j], srec[5][j], srec[6][j], hit, xyz);
+          pos_x += w * xyz[0];
+          pos_y += w * xyz[1];
+          pos_z += w * xyz[2];
+          const uint32_t ap = __float_as_uint(q3.w);
+          const uint32_t id = __float_as_uint(srec[6][j].w);
+          float h[3];
+          if (p.hsh_dec != 1)
+            hsh_query(g, xyz, ap, h);
+          else
+            h[0] = h[1] = h[2] = 0.0f;
+          hsh_accumulate<kHsh, NACC>(p, p.colors + (size_t)id * (uint32_t)p.cstride, h, w, acc);
+          appearance_colour(ap, w, vis0, vis1);
+        } else if constexpr (!kHash) {
           const uint32_t id = __float_as_uint(srec[6][j].w);
           const float* col = p.colors + (size_t)id * p.C;
 #pragma unroll
@@ -926,9 +1004,10 @@ __global__ void __launch_bounds__(kRenderThreads) record_transmittance_kernel(co
   }
 }
 
-template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0, bool kKT = false>
+template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0, bool kKT = false,
+          int kHsh = 0>
 static hipError_t launch_one(const RenderParams& p, hipStream_t s) {
-  hipLaunchKernelGGL((render_kernel<F, NACC, kHash, kHalf, kStructured, kMix, kKT>), dim3(p.ntiles),
+  hipLaunchKernelGGL((render_kernel<F, NACC, kHash, kHalf, kStructured, kMix, kKT, kHsh>), dim3(p.ntiles),
                      dim3(kRenderThreads), 0, s, p);
   return hipGetLastError();
 }
@@ -1067,6 +1146,9 @@ static hipError_t launch_hash(const RenderParams& p, hipStream_t s) {
 
 template <bool kKT>
 static hipError_t launch_render_kind(const RenderParams& p, hipStream_t s) {
+  if (p.hsh == 8) return launch_one<1, 3, false, false, false, 0, kKT, 8>(p, s);
+  if (p.hsh == 9) return launch_one<1, 48, false, false, false, 0, kKT, 9>(p, s);
+  if (p.hsh == 10) return launch_one<1, 3, false, false, false, 0, kKT, 10>(p, s);
   if (p.level == 0 && !p.mix) {
     if (p.C <= 3) return launch_one<1, 3, false, false, false, 0, kKT>(p, s);
     if (p.C <= 16) return launch_one<1, 16, false, false, false, 0, kKT>(p, s);

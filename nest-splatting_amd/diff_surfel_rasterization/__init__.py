@@ -104,10 +104,10 @@ class _RasterizeGaussians(torch.autograd.Function):
                 ap_level, features, offsets, gridrange, features_diffuse, offsets_diffuse, gridrange_diffuse,
                 raster_settings, hashgrid_settings, render_mode, shapes, kernel_type):
         base_mode = render_mode & 0xFF
-        if base_mode not in (0, 4, 7, 12, 13, 14) or (render_mode & ~0x1FF) or \
+        if base_mode not in (0, 4, 7, 8, 9, 10, 12, 13, 14) or (render_mode & ~0x1FF) or \
                 ((render_mode & 0x100) and base_mode not in (12, 13, 14)):
             raise NotImplementedError(f"render_mode {render_mode}: implemented are 0 (baseline), 4 (cat), "
-                                      f"7 (adaptive_add) and "
+                                      f"7 (adaptive_add), 8 / 9 / 10 (hybrid_SH / hybrid_SH_post / hybrid_SH_raw) and "
                                       f"12 / 13 / 14 (adaptive_cat / adaptive_cat_fast / adaptive_zero, | 0x100 "
                                       f"inference)")
         if kernel_type not in (0, 1, 2, 3):
@@ -121,9 +121,33 @@ class _RasterizeGaussians(torch.autograd.Function):
             raise NotImplementedError("a second (diffuse) hash grid is not implemented")
         C = _channels(hashgrid_settings)
         level = int(hashgrid_settings.L)
-        if base_mode in (4, 7, 12, 14) and level == 0:
+        if base_mode in (4, 7, 8, 9, 10, 12, 14) and level == 0:
             base_mode = render_mode = 0  # level 0 is the colour path in every mode but 13 (CR/forward.cu:1091)
-        if base_mode != 0:
+        if base_mode in (8, 9, 10):
+            # hybrid SH (CR/forward.cu:1378-1542): level = decompose << 24 | SH degree << 16 |
+            # grid levels << 8 (GR:617-626), one 3-channel grid level, rows of 3 raw colours or
+            # 48 SH coefficients in colors_precomp
+            dec, hl = (level >> 24) & 0xFF, (level >> 8) & 0xFF
+            if hl > 1:
+                raise NotImplementedError(f"render_mode {base_mode} looks up one grid level (got {hl})")
+            if hl and (_empty(features) or _empty(offsets) or _empty(gridrange)):
+                raise ValueError(f"render_mode {base_mode} needs features, offsets and gridrange")
+            if _empty(colors_precomp):
+                raise ValueError(f"render_mode {base_mode} needs the per-splat rows in colors_precomp")
+            hs = hashgrid_settings
+            grid = _rz.HashGridDesc(levels=hl, level_dim=int(features.shape[1]) if hl else 3,
+                                    log2_scale=float(hs.S), base_resolution=int(hs.H),
+                                    table=features.detach().contiguous() if hl else None,
+                                    offsets=_rz.host_array(offsets, np.int64) if hl else np.zeros(1, np.int64),
+                                    gridrange=_rz.host_array(gridrange, np.float32) if hl else
+                                    np.zeros(2, np.float32), align_corners=bool(hs.align_corners),
+                                    interpolation=int(hs.interpolation), render_mode=base_mode, decompose=dec)
+            colors = colors_precomp.detach()
+            width = grid.row_width(C)
+            if colors.dim() != 2 or colors.shape[1] != width:
+                raise ValueError(f"render_mode {base_mode}: colors_precomp must be [P, {width}]")
+            level = 1  # no SH colours
+        elif base_mode != 0:
             grid = _mixed_grid(hashgrid_settings, render_mode, level, features, offsets, gridrange)
             colors = None if _empty(colors_precomp) else colors_precomp.detach()
             width = grid.row_width(C)

@@ -57,10 +57,16 @@ class HashGridDesc:
     # render_mode 4 backward: the grid levels it differentiates are those up to
     # the active count (coarse-to-fine training); None = all `levels`
     active_levels: Optional[int] = None
+    # render_mode 8 / 9 / 10 (hybrid SH): 0 both parts, 1 gaussian_only, 2 ngp_only
+    decompose: int = 0
 
     def row_width(self, channels: int) -> int:
         """Floats per splat of colors_precomp for this render mode."""
         base = self.render_mode & 0xFF
+        if base in (L.MODE_HYBRID_SH, L.MODE_HYBRID_SH_RAW):
+            return 3
+        if base == L.MODE_HYBRID_SH_POST:
+            return 48
         if base == L.MODE_CAT:
             return self.hybrid_levels * self.level_dim
         if base == L.MODE_ADAPTIVE_ZERO:
@@ -76,6 +82,7 @@ class HashGridDesc:
         g.hybrid_levels = int(self.hybrid_levels)
         g.total_levels = int(self.total_levels)
         g.active_levels = int(self.levels if self.active_levels is None else self.active_levels)
+        g.decompose = int(self.decompose)
         g.levels = int(self.levels)
         g.level_dim = int(self.level_dim)
         g.log2_scale = float(self.log2_scale)

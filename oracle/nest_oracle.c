@@ -697,8 +697,10 @@ typedef struct {
      * levels, colors rows of total*F+1 floats, bit 8 of render_mode =
      * inference), 7 adaptive_add (level = total << 16 | hash << 8, rows of
      * total*F+1 floats), 12 adaptive_cat (same level and rows as 13), 14 adaptive_zero
-     * (same level, rows of hyb*F+1 floats).  Other values are not
-     * restated. */
+     * (same level, rows of hyb*F+1 floats), 8 / 9 / 10 hybrid_SH /
+     * hybrid_SH_post / hybrid_SH_raw (level = decompose << 24 | SH degree
+     * << 16 | grid levels << 8, rows of 3 / 48 / 3 floats, a one-level
+     * 3-channel grid).  Other values are not restated. */
     int render_mode;
     /* record_transmittance (forward.cu:1961-1964), NULL = off: [P] each;
      * every hit that reaches the end of the hit body (not mode 13's, which
@@ -935,6 +937,47 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
                         const int fs = hyb * F;
                         for (int i = 0; i < hl * F && fs + i < C; i++)
                             feat_scratch[fs + i] = infer ? hf[i] : fmaf(wt, gf[fs + i], (1.0f - wt) * hf[i]);
+                    }
+                }
+            } else if ((A->render_mode & 0xFF) >= 8 && (A->render_mode & 0xFF) <= 10) {
+                /* hybrid_SH (8), hybrid_SH_post (9), hybrid_SH_raw (10)
+                 * (forward.cu:1378-1542), level = decompose << 24 | sh degree
+                 * << 16 | grid levels << 8: one 3-channel grid level at the hit
+                 * (skipped when decompose == 1, gaussian_only, or without grid
+                 * levels) and the splat's colors row, 3 raw SH colours (8, 10)
+                 * or 48 SH coefficients channel-major (9, DC at 0, 16, 32).
+                 * 8: clamp(raw + 0.5) and sigmoid(grid) added and clamped to
+                 * [0, 1] (decompose 2 takes the sigmoid alone, 1 the colour);
+                 * 10: sigmoid(raw + grid) (2: of the grid, 1: of the colour);
+                 * 9: the coefficients with the grid added to (2: in place of)
+                 * the DC terms.  The channels past the mode's stay 0. */
+                const int mode = A->render_mode & 0xFF;
+                const int dec = (A->level >> 24) & 0xFF, hl = (A->level >> 8) & 0xFF;
+                float h[3] = {0.0f, 0.0f, 0.0f};
+                if (hl > 0 && dec != 1) {
+                    or_grid G = A->grid;
+                    G.L = 1;
+                    or_query_feature(&G, xyz, ap, 3, h);
+                }
+                for (int c = 0; c < C; c++) feat_scratch[c] = 0.0f;
+                if (mode == 9) {
+                    const float *sh = A->colors + (size_t)id * 48;
+                    for (int i = 0; i < 48 && i < C; i++) feat_scratch[i] = sh[i];
+                    for (int k = 0; k < 3 && 16 * k < C; k++) {
+                        if (dec == 2) feat_scratch[16 * k] = h[k];
+                        else if (dec != 1) feat_scratch[16 * k] = sh[16 * k] + h[k];
+                    }
+                } else {
+                    const float *raw = A->colors + (size_t)id * 3;
+                    for (int k = 0; k < 3 && k < C; k++) {
+                        if (mode == 8) {
+                            const float g = fmaxf(0.0f, fminf(1.0f, raw[k] + 0.5f));
+                            const float sg = 1.0f / (1.0f + or_expf(-h[k]));
+                            feat_scratch[k] = dec == 2 ? sg : dec == 1 ? g : fmaxf(0.0f, fminf(1.0f, g + sg));
+                        } else {
+                            const float comb = dec == 2 ? h[k] : dec == 1 ? raw[k] : raw[k] + h[k];
+                            feat_scratch[k] = 1.0f / (1.0f + or_expf(-comb));
+                        }
                     }
                 }
             } else if ((A->render_mode & 0xFF) == 4) {

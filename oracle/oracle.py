@@ -228,7 +228,10 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
     grid.L, or the colour path without a grid), 4, 7, 12, 13 or 14 (bit 8:
     inference); for modes 4, 7, 12, 13 and 14, level is the reference's packed level argument
     (total << 16 | hash levels << 8 | per-splat levels) and colors the
-    per-splat feature rows.  record_transmittance adds cover_pixels and
+    per-splat feature rows; for modes 8, 9 and 10 (hybrid SH) level is
+    decompose << 24 | SH degree << 16 | grid levels << 8, colors the rows of
+    3 raw SH colours (8, 10) or 48 SH coefficients (9) and the grid one level
+    of 3 channels.  record_transmittance adds cover_pixels and
     trans_avg ([P] each) to the result.  kernel_type 1-3 take the per-splat
     parameter from shapes [P]."""
     HW = W * H

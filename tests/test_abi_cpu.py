@@ -167,6 +167,43 @@ def test_render_rejects_bad_grids():
     assert lib.nest_forward_render(*args()) == L.NEST_ERR_WORKSPACE
 
 
+def test_render_validates_hybrid_sh_modes():
+    """Render modes 8-10: one float32 grid level of 3 channels, rows in
+    colors_precomp, 3 or 48 output channels, decompose 0-2; checked before
+    any launch."""
+    L = _lib()
+    lib = L.lib()
+    s = _settings(L)
+    sp = _splats(L, 0)
+    g = L.HashGrid()
+    g.struct_size = ct.sizeof(L.HashGrid)
+    g.render_mode = L.MODE_HYBRID_SH_POST
+    g.levels, g.level_dim, g.table, g.table_rows = 1, 3, 1, 4096
+    g.offsets[1] = 4096
+    g.gridrange[0], g.gridrange[1] = -1.0, 1.0
+    out = L.FrameOutputs()
+    out.struct_size = ct.sizeof(L.FrameOutputs)
+    out.channels = 3
+    out.out_color = out.out_others = 1
+    ws = (ct.c_uint8 * 16)()
+    args = lambda: (ct.byref(s), ct.byref(g), ct.byref(sp), ws, 16, ws, 16, ws, 16, 0, ct.byref(out), None, None)
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_INVALID_ARGUMENT  # mode 9 writes 48 channels
+    assert b"48" in lib.nest_last_error()
+    out.channels = 48
+    g.levels = 2
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_UNSUPPORTED  # one level
+    g.levels, g.level_dim = 1, 4
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_UNSUPPORTED  # level_dim 3
+    g.level_dim, g.table_dtype = 3, L.DTYPE_F16
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_UNSUPPORTED  # float32 table
+    g.table_dtype, g.decompose = L.DTYPE_F32, 3
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_INVALID_ARGUMENT
+    g.decompose = 2
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_WORKSPACE  # arguments accepted
+    g.render_mode, out.channels = L.MODE_HYBRID_SH, 3
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_WORKSPACE
+
+
 def test_backward_layout_and_validation():
     """nest_backward_layout sizes and the argument checks of nest_backward /
     nest_grid_encode_backward, which return before any launch."""
