@@ -14,7 +14,9 @@ rasterise SH colours (degree 0, resp. the active degree); ``diffuse_ngp`` adds
 the hash grid's MLP colour at the back-projected median depth; and
 ``diffuse_offset`` queries the grid at that point moved by the rendered
 colour - 0.5 (clamped to +-0.1), or at the blended splat centres of allmap
-8:11 with ``use_xyz_mode``.
+8:11 with ``use_xyz_mode``.  The hybrid SH modes (:600-680, :958-1000) pass
+raw SH colours or the SH coefficients to render modes 8-10 with a one-level
+3-channel grid.
 """
 from __future__ import annotations
 
@@ -201,19 +203,57 @@ def depth_to_normal(cam, depth: torch.Tensor) -> torch.Tensor:
 
 
 SH_MODES = ("diffuse", "specular", "diffuse_ngp", "diffuse_offset")
+# the reference's hybrid SH methods and their render_mode (GR:600-680)
+HYBRID_MODES = {"hybrid_SH": 8, "hybrid_SH_post": 9, "hybrid_SH_raw": 10}
+DECOMPOSE = {None: 0, "gaussian_only": 1, "ngp_only": 2}
+
+# Real spherical-harmonic basis constants up to degree 3 (the normalisation
+# of the real SH Y_lm; the same values as the preprocess kernel's).
+_SH_C0 = 0.28209479177387814
+_SH_C1 = 0.4886025119029199
+_SH_C2 = (1.0925484305920792, -1.0925484305920792, 0.31539156525252005, -1.0925484305920792, 0.5462742152960396)
+_SH_C3 = (-0.5900435899266435, 2.890611442640554, -0.4570457994644658, 0.3731763325901154, -0.4570457994644658,
+          1.445305721320277, -0.5900435899266435)
+
+
+def eval_sh(deg: int, sh: torch.Tensor, dirs: torch.Tensor) -> torch.Tensor:
+    """utils/sh_utils.py:57-117: SH coefficients sh [..., C, (deg+1)^2 or
+    more] at unit directions dirs [..., 3] -> [..., C], no activation."""
+    x, y, z = dirs[..., 0:1], dirs[..., 1:2], dirs[..., 2:3]
+    r = _SH_C0 * sh[..., 0]
+    if deg > 0:
+        r = r - _SH_C1 * y * sh[..., 1] + _SH_C1 * z * sh[..., 2] - _SH_C1 * x * sh[..., 3]
+        if deg > 1:
+            xx, yy, zz = x * x, y * y, z * z
+            xy, yz, xz = x * y, y * z, x * z
+            r = (r + _SH_C2[0] * xy * sh[..., 4] + _SH_C2[1] * yz * sh[..., 5] +
+                 _SH_C2[2] * (2.0 * zz - xx - yy) * sh[..., 6] + _SH_C2[3] * xz * sh[..., 7] +
+                 _SH_C2[4] * (xx - yy) * sh[..., 8])
+            if deg > 2:
+                r = (r + _SH_C3[0] * y * (3 * xx - yy) * sh[..., 9] + _SH_C3[1] * xy * z * sh[..., 10] +
+                     _SH_C3[2] * y * (4 * zz - xx - yy) * sh[..., 11] +
+                     _SH_C3[3] * z * (2 * zz - 3 * xx - 3 * yy) * sh[..., 12] +
+                     _SH_C3[4] * x * (4 * zz - xx - yy) * sh[..., 13] + _SH_C3[5] * z * (xx - yy) * sh[..., 14] +
+                     _SH_C3[6] * x * (xx - 3 * yy) * sh[..., 15])
+    return r
 
 
 def render(viewpoint_camera, pc, pipe, bg_color: torch.Tensor, scaling_modifier=1.0, ingp: HashINGP = None, beta=0,
            max_intersections=0, skip_mlp=False, with_surface=True, mode: str = "baseline", use_xyz_mode: bool = False,
-           record_transmittance: bool = False):
-    """mode: "baseline" (the hash grid rasterised in the kernel, then the MLP)
-    or one of the SH-rasterised modes "diffuse", "specular", "diffuse_ngp",
-    "diffuse_offset" (the reference's ingp.is_*_mode flags)."""
+           record_transmittance: bool = False, decompose_mode: Optional[str] = None):
+    """mode: "baseline" (the hash grid rasterised in the kernel, then the MLP),
+    one of the SH-rasterised modes "diffuse", "specular", "diffuse_ngp",
+    "diffuse_offset", or one of the hybrid SH modes "hybrid_SH",
+    "hybrid_SH_raw", "hybrid_SH_post" with decompose_mode None,
+    "gaussian_only" or "ngp_only" (the reference's ingp.is_*_mode flags)."""
     if mode in SH_MODES:
         return _render_sh(viewpoint_camera, pc, pipe, bg_color, scaling_modifier, ingp, beta, max_intersections,
                           with_surface, mode, use_xyz_mode, record_transmittance)
+    if mode in HYBRID_MODES:
+        return _render_hybrid(viewpoint_camera, pc, pipe, bg_color, scaling_modifier, ingp, beta, max_intersections,
+                              with_surface, mode, decompose_mode, record_transmittance)
     if mode != "baseline":
-        raise ValueError(f"mode must be 'baseline' or one of {SH_MODES} (got {mode!r})")
+        raise ValueError(f"mode must be 'baseline' or one of {SH_MODES + tuple(HYBRID_MODES)} (got {mode!r})")
     from diff_surfel_rasterization import GaussianRasterizationSettings, GaussianRasterizer, HashGridSettings
 
     dev = pc.get_xyz.device
@@ -322,6 +362,78 @@ def _render_sh(cam, pc, pipe, bg_color, scaling_modifier, ingp, beta, max_inters
     if float(bg_color.sum()) > 0:
         image = image + (1.0 - render_alpha) * bg_color.to(dev).unsqueeze(-1).unsqueeze(-1)
     rets["render"] = image
+    if record_transmittance:
+        rets.update({"transmittance_avg": trans_avg, "cover_pixels": cover})
+    if with_surface:
+        rets.update(surface_maps(cam, allmap, getattr(pipe, "depth_ratio", 0.0)))
+    return rets
+
+
+def _render_hybrid(cam, pc, pipe, bg_color, scaling_modifier, ingp, beta, max_intersections, with_surface, mode,
+                   decompose_mode, record_transmittance):
+    """gaussian_renderer/__init__.py:600-680 (raw SH colours, or the 48
+    coefficients, as colors_precomp; the packed level), :958-1000 (the mask,
+    and for hybrid_SH_post the per-pixel SH evaluation along the view ray),
+    :1013-1046.  The grid is ingp's one level of 3 channels."""
+    from diff_surfel_rasterization import GaussianRasterizationSettings, GaussianRasterizer, HashGridSettings
+
+    if pc.get_features is None or ingp is None:
+        raise ValueError(f"mode {mode!r} needs the splats' SH features and the one-level ingp grid")
+    if decompose_mode not in DECOMPOSE:
+        raise ValueError(f"decompose_mode must be one of {tuple(DECOMPOSE)} (got {decompose_mode!r})")
+    rmode = HYBRID_MODES[mode]
+    dev = pc.get_xyz.device
+    H, W = int(cam.image_height), int(cam.image_width)
+    deg = int(pc.active_sh_degree)
+    feats = pc.get_features
+    K = feats.shape[1]
+    shs_view = feats.transpose(1, 2).reshape(-1, 3, K)
+    if rmode == 9:
+        if K != 16:
+            raise ValueError("hybrid_SH_post passes 48 coefficients per splat (SH degree 3 features)")
+        colors = shs_view.reshape(-1, 48)
+    else:
+        campos = _matrix(cam.camera_center, dev).reshape(1, 3)
+        d = pc.get_xyz - campos
+        colors = eval_sh(deg, shs_view, d / d.norm(dim=1, keepdim=True))
+    C = 48 if rmode == 9 else 3
+    enc = ingp.hash_encoding
+    features, offsets, _, per_level_scale, base_resolution, align_corners, interpolation = enc.get_params()
+    host = getattr(enc, "_offsets_host", None)
+    if host is not None:
+        offsets._nest_host_copy = (offsets._version, np.asarray(host, dtype=np.float64).astype(np.int64))
+    gridrange = ingp.gridrange
+    gridrange._nest_host_copy = (gridrange._version, ingp._gridrange_host)
+    level = (DECOMPOSE[decompose_mode] << 24) | (deg << 16) | (1 << 8)
+    raster_settings = GaussianRasterizationSettings(
+        image_height=H, image_width=W, tanfovx=math.tan(cam.FoVx * 0.5), tanfovy=math.tan(cam.FoVy * 0.5),
+        bg=bg_color, scale_modifier=scaling_modifier, viewmatrix=cam.world_view_transform,
+        projmatrix=cam.full_proj_transform, sh_degree=deg, campos=cam.camera_center, prefiltered=False, debug=False,
+        beta=beta, if_contract=ingp.contract, record_transmittance=record_transmittance,
+        max_intersections=max_intersections)
+    hashgrid_settings = HashGridSettings(L=level, S=math.log2(per_level_scale), H=base_resolution,
+                                         align_corners=align_corners, interpolation=interpolation,
+                                         shape_dims=torch.tensor([0, C, C], dtype=torch.int32))
+    rasterizer = GaussianRasterizer(raster_settings=raster_settings, hashgrid_settings=hashgrid_settings)
+    means2D = torch.zeros_like(pc.get_xyz)
+    image, radii, allmap, trans_avg, cover = rasterizer(
+        means3D=pc.get_xyz, means2D=means2D, shs=None, colors_precomp=colors, opacities=pc.get_opacity,
+        scales=pc.get_scaling, rotations=pc.get_rotation, homotrans=pc.get_homotrans(),
+        ap_level=pc.get_appearance_level, features=features, offsets=offsets, gridrange=gridrange,
+        render_mode=rmode)
+    render_alpha = allmap[1:2]
+    mask = render_alpha > 0
+    if rmode == 9:
+        rays_d, _ = cam2rays(cam, dev)
+        coeffs = image.view(48, -1).permute(1, 0).reshape(-1, 3, 16)
+        rgb = torch.clamp_min(eval_sh(deg, coeffs, torch_F.normalize(rays_d, dim=-1)) + 0.5, 0.0)
+        image = rgb.view(H, W, 3).permute(2, 0, 1) * mask
+    else:
+        image = image * mask
+    if float(bg_color.sum()) > 0:
+        image = image + (1.0 - render_alpha) * bg_color.to(dev).unsqueeze(-1).unsqueeze(-1)
+    rets = {"render": image, "viewspace_points": means2D, "visibility_filter": radii > 0, "radii": radii,
+            "allmap": allmap}
     if record_transmittance:
         rets.update({"transmittance_avg": trans_avg, "cover_pixels": cover})
     if with_surface:

@@ -104,3 +104,59 @@ def test_sh_modes_against_oracle(oracle, mode, use_xyz):
         if use_xyz:
             sl = out["scout_loss_data"]
             assert tuple(sl["points_base"].shape) == (sp.W * sp.H, 3)
+
+
+@pytest.mark.parametrize("mode,dec", [("hybrid_SH", None), ("hybrid_SH_raw", "ngp_only"),
+                                      ("hybrid_SH_post", None), ("hybrid_SH_post", "gaussian_only")])
+def test_hybrid_modes_against_oracle(oracle, mode, dec):
+    """render()'s hybrid SH branches (GR:600-680, :958-1000) against the oracle's
+    render modes 8-10 fed with the same rows (raw SH colours from eval_sh, which
+    the CPU tests pin, or the 48 coefficients), the mask, and for hybrid_SH_post
+    the per-pixel SH colour along the view ray."""
+    from gridencoder import GridEncoder
+    from nest_splat.renderer import DECOMPOSE, HYBRID_MODES, HashINGP, Pipe, SplatModel, eval_sh, render
+    from nest_splat.scene import get_spec, make_scene
+    sc = make_scene(get_spec("cfg2", P=20_000, W=256, H=192, L=1, F=3, log2T=16, base_res=512, name="hsh_render"))
+    sp = sc.spec
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    print(f"[case] render {mode} decompose {dec}", flush=True)
+    shs = _sh(sp.P, seed=11)
+    enc = GridEncoder(3, 1, 3, 1.0, sp.base_res, sp.log2T).to(DEV)
+    assert enc.offsets.cpu().numpy().tolist() == [int(v) for v in sc.offsets]
+    with torch.no_grad():
+        enc.embeddings = torch.nn.Parameter(_t(sc.table), requires_grad=False)
+    ingp = HashINGP(enc, None, sp.gridrange, sp.contract)
+    pc = SplatModel(_t(sc.means), _t(sc.scales), _t(sc.rotations), _t(sc.opacity), _t(sc.ap_level),
+                    homotrans=_t(sc.homotrans), features=_t(shs), active_sh_degree=3)
+    bg = np.float32([0.2, 0.1, 0.3])
+    out = render(cam, pc, Pipe(), _t(bg), ingp=ingp, mode=mode, decompose_mode=dec, with_surface=False)
+    torch.cuda.synchronize()
+
+    rmode = HYBRID_MODES[mode]
+    shs_view = torch.from_numpy(shs).transpose(1, 2)
+    if rmode == 9:
+        rows = shs_view.reshape(-1, 48).numpy()
+    else:
+        d = torch.from_numpy(sc.means) - torch.from_numpy(np.asarray(cam.camera_center, np.float32))
+        rows = eval_sh(3, shs_view, d / d.norm(dim=1, keepdim=True)).numpy()
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    grid = oracle.make_grid(1, 3, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    r = oracle.render(pre, b, W, H, 48 if rmode == 9 else 3, grid, homotrans=sc.homotrans, ap_level=sc.ap_level,
+                      colors=np.ascontiguousarray(rows, np.float32), render_mode=rmode,
+                      level=(DECOMPOSE[dec] << 24) | (3 << 16) | (1 << 8))
+    alpha = r["others"][1]
+    mask = (alpha > 0).astype(np.float32)
+    if rmode == 9:
+        coeffs = torch.from_numpy(r["color"].reshape(48, -1).T.copy()).reshape(-1, 3, 16)
+        dirs = torch.from_numpy(oracle.ray_dirs(cam))
+        img = torch.clamp_min(eval_sh(3, coeffs, dirs) + 0.5, 0.0).numpy().T.reshape(3, H, W) * mask
+    else:
+        img = r["color"] * mask
+    img = img + (np.float32(1) - alpha)[None] * bg[:, None, None]
+    got = out["render"].cpu().numpy()
+    err = np.abs(got - img).max()
+    print(f"render {mode}: max err {err:.2e}", flush=True)
+    assert np.abs(img).max() > 0.1 and err < 1e-5

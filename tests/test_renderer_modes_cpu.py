@@ -45,3 +45,26 @@ def test_level_mask_zeroes_inactive_levels():
 def test_unknown_mode_is_an_error():
     with pytest.raises(ValueError):
         render(None, None, None, torch.zeros(3), mode="residual")
+
+
+@pytest.mark.parametrize("deg", [0, 1, 2, 3])
+def test_eval_sh_matches_the_oracle(oracle, deg):
+    """renderer.eval_sh (utils/sh_utils.py:57-117) + 0.5, clamped at 0, is the
+    preprocess's SH colour (CR/forward.cu:21-72), which the oracle restates and
+    scipy's spherical harmonics pin."""
+    from nest_splat.renderer import eval_sh
+    from nest_splat.scene import get_spec, make_scene
+    sc = make_scene(get_spec("cfg1", P=500, name="sh_eval"))
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    shs = np.random.default_rng(deg).normal(0, 0.6, (500, 16, 3)).astype(np.float32)
+    campos = np.asarray(cam.camera_center, np.float32)
+    ref, _ = oracle.sh_colors(pre, sc.means, campos, shs, deg)
+    d = torch.from_numpy(sc.means) - torch.from_numpy(campos)
+    mine = torch.clamp_min(eval_sh(deg, torch.from_numpy(shs).transpose(1, 2), d / d.norm(dim=1, keepdim=True)) + 0.5,
+                           0.0).numpy()
+    vis = pre["radii"] > 0
+    assert vis.sum() > 100
+    assert np.abs(mine[vis] - ref[vis]).max() < 2e-6
