@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 12
+#define NEST_ABI_VERSION 13
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -258,7 +258,9 @@ const char *nest_last_error(void);
 int nest_geom_layout(int32_t P, size_t offsets[NEST_GEOM_FIELDS], size_t *total_bytes);
 
 /* The pairs are emitted in depth order and sorted on the tile bits only;
- * KEYS and VALS equal the reference's point_list_keys and point_list. */
+ * VALS equals the reference's point_list.  nest_forward_render leaves KEYS
+ * unwritten (nothing downstream reads them); nest_binning_keys fills it with
+ * the reference's point_list_keys. */
 #define NEST_BIN_PAIR_TILES 0      /* u32 [NR] tile id of each pair, pairs in depth order */
 #define NEST_BIN_PAIR_IDS 1        /* u32 [NR] splat id of each pair, same order          */
 #define NEST_BIN_KEYS 2            /* u64 [NR] sorted (tile << 32 | depth bits) */
@@ -312,6 +314,17 @@ int nest_forward_render(const nest_raster_settings *settings, const nest_hashgri
                         void *binning_ws, size_t binning_bytes, void *image_ws, size_t image_bytes,
                         int64_t num_rendered, const nest_frame_outputs *out,
                         nest_timing *timing, void *stream);
+
+/* The reference's sorted keys point_list_keys, tile << 32 | depth bits of the
+ * pair's splat (CR/rasterizer_impl.cu:381-386, binningState), written into the
+ * binning workspace's NEST_BIN_KEYS slot from the tile ranges, the sorted point
+ * list and the depths in the workspaces of a nest_forward_render call with the
+ * same image size, P and num_rendered.  The reference has no separate call:
+ * its sort writes them, while nest_forward_render sorts without them because
+ * nothing downstream reads them (the backward walks ranges and point_list). */
+int nest_binning_keys(int32_t width, int32_t height, int32_t P, const void *geom_ws, size_t geom_bytes,
+                      void *binning_ws, size_t binning_bytes, const void *image_ws, size_t image_bytes,
+                      int64_t num_rendered, void *stream);
 
 /* ---- backward (training) ------------------------------------------------
  * nest_backward is RasterizeGaussiansBackwardCUDA

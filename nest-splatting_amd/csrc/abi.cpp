@@ -579,12 +579,10 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   uint32_t* ranges = reinterpret_cast<uint32_t*>(im + io[NEST_IMG_RANGES]);
   StageTimer tm(timing, s);
 
-  uint64_t* keys = nullptr;
   uint32_t* vals = nullptr;
   if (NR > 0) {
     uint32_t* pair_tiles = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_PAIR_TILES]);
     uint32_t* pair_ids = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_PAIR_IDS]);
-    keys = reinterpret_cast<uint64_t*>(b + bo[NEST_BIN_KEYS]);
     vals = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_VALS]);
     const float* depth = reinterpret_cast<const float*>(g + go[NEST_GEOM_DEPTH]);
     const int32_t* gradii = reinterpret_cast<const int32_t*>(g + go[NEST_GEOM_RADII]);
@@ -603,7 +601,8 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     tm.end();
     tm.begin(NEST_STAGE_SORT);
     const int bit = (int)higher_msb(ntiles);
-    rc = check_stage(launch_sort_tiles(pair_tiles, pair_ids, keys, vals, NR, bit, depth, ranges, ntiles,
+    // the sorted keys are not needed downstream: nest_binning_keys composes them on request
+    rc = check_stage(launch_sort_tiles(pair_tiles, pair_ids, nullptr, vals, NR, bit, depth, ranges, ntiles,
                                        b + bo[NEST_BIN_SORT_TMP], s),
                      "sort", rs->debug, s);
     if (rc) return rc;
@@ -758,6 +757,34 @@ int nest_inclusive_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* 
 }
 
 size_t nest_sort_workspace_size(int64_t n) { return sort_ws_bytes(n > 0 ? n : 1); }
+
+int nest_binning_keys(int32_t W, int32_t H, int32_t P, const void* geom_ws, size_t geom_bytes, void* binning_ws,
+                      size_t binning_bytes, const void* image_ws, size_t image_bytes, int64_t NR, void* stream) {
+  if (W <= 0 || H <= 0) return fail(NEST_ERR_INVALID_ARGUMENT, "image size must be positive");
+  if (P < 0) return fail(NEST_ERR_INVALID_ARGUMENT, "P must be >= 0");
+  if (NR < 0 || NR > 0xffffffffll) return fail(NEST_ERR_INVALID_ARGUMENT, "num_rendered out of range");
+  size_t go[NEST_GEOM_FIELDS], gneed = 0, bo[NEST_BIN_FIELDS], bneed = 0, io[NEST_IMG_FIELDS], ineed = 0;
+  nest_geom_layout(P, go, &gneed);
+  nest_binning_layout(NR, bo, &bneed);
+  nest_image_layout(W, H, io, &ineed);
+  if (!geom_ws || geom_bytes < gneed)
+    return fail(NEST_ERR_WORKSPACE, "geometry workspace too small: %zu bytes given, %zu needed", geom_bytes, gneed);
+  if (NR > 0 && (!binning_ws || binning_bytes < bneed))
+    return fail(NEST_ERR_WORKSPACE, "binning workspace too small: %zu bytes given, %zu needed", binning_bytes, bneed);
+  if (!image_ws || image_bytes < ineed)
+    return fail(NEST_ERR_WORKSPACE, "image workspace too small: %zu bytes given, %zu needed", image_bytes, ineed);
+  if (NR == 0) return NEST_OK;
+  const uint32_t ntiles = (uint32_t)(((W + kTile - 1) / kTile) * ((H + kTile - 1) / kTile));
+  const char* g = static_cast<const char*>(geom_ws);
+  char* b = static_cast<char*>(binning_ws);
+  const char* im = static_cast<const char*>(image_ws);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return check_stage(launch_compose_keys(reinterpret_cast<const uint32_t*>(im + io[NEST_IMG_RANGES]),
+                                         reinterpret_cast<const uint32_t*>(b + bo[NEST_BIN_VALS]),
+                                         reinterpret_cast<const float*>(g + go[NEST_GEOM_DEPTH]), ntiles,
+                                         reinterpret_cast<uint64_t*>(b + bo[NEST_BIN_KEYS]), s),
+                     "binning keys", 0, s);
+}
 
 int nest_sort_pairs_u64(const uint64_t* keys_in, const uint32_t* vals_in, uint64_t* keys_out, uint32_t* vals_out,
                         int64_t n, int32_t end_bit, void* ws, size_t ws_bytes, void* stream) {

@@ -265,7 +265,8 @@ __global__ void __launch_bounds__(kScanThreads) digit_scan_kernel(uint32_t* __re
 // keys are first placed in LDS in digit order (stable), then written out so
 // that consecutive lanes write consecutive positions of each digit's run.
 // KOut == uint64_t with K == uint32_t composes the output key as
-// (key << 32) | low_bits[val] (the tile/depth key of the binning stage).
+// (key << 32) | low_bits[val] (the tile/depth key of the binning stage);
+// keys_out NULL writes the values alone.
 // With tile_counts (the last pass of the tile sort, where a block's LDS copy
 // is sorted on the whole key), every run of equal keys in that copy adds its
 // length to tile_counts[2 * key + 1] (the .y of the key's uint2 range); keys
@@ -361,10 +362,14 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
     const K k = skey[j];
     const uint32_t v = sval[j];
     const uint32_t pos = gbase[(uint32_t)(k >> shift) & dmask] + (uint32_t)j;
-    if constexpr (sizeof(KOut) > sizeof(K))
-      keys_out[pos] = ((KOut)k << 32) | (KOut)low_bits[v];
-    else
-      keys_out[pos] = k;
+    // keys_out NULL (the tile sort's last pass in the forward): the values
+    // alone, no depth-bits gather and no key write
+    if (keys_out != nullptr) {
+      if constexpr (sizeof(KOut) > sizeof(K))
+        keys_out[pos] = ((KOut)k << 32) | (KOut)low_bits[v];
+      else
+        keys_out[pos] = k;
+    }
     vals_out[pos] = v;
     if (tile_counts != nullptr && (uint64_t)k < ntiles) {
       // the run [a, b) of key k adds -a at its first element, b at its last
@@ -634,6 +639,26 @@ hipError_t launch_sort_tiles(const uint32_t* tile_keys, const uint32_t* ids, uin
                              hipStream_t s) {
   return sort_impl<uint32_t, uint64_t>(tile_keys, ids, keys_out, vals_out, n, tile_bits,
                                        reinterpret_cast<const uint32_t*>(depth), ws, s, ranges, ntiles);
+}
+
+// The reference's sorted keys, tile << 32 | depth bits of the pair's splat
+// (point_list_keys, CR/rasterizer_impl.cu:381-386), from the tile ranges and
+// the sorted point list: one workgroup per tile, its positions in order.
+__global__ void __launch_bounds__(256) compose_keys_kernel(const uint2* __restrict__ ranges,
+                                                            const uint32_t* __restrict__ point_list,
+                                                            const uint32_t* __restrict__ depth_bits,
+                                                            uint64_t* __restrict__ keys) {
+  const uint32_t t = blockIdx.x;
+  const uint2 r = ranges[t];
+  for (uint32_t i = r.x + threadIdx.x; i < r.y; i += 256u) keys[i] = ((uint64_t)t << 32) | depth_bits[point_list[i]];
+}
+
+hipError_t launch_compose_keys(const uint32_t* ranges, const uint32_t* point_list, const float* depth, uint32_t ntiles,
+                               uint64_t* keys, hipStream_t s) {
+  if (ntiles == 0) return hipSuccess;
+  hipLaunchKernelGGL(compose_keys_kernel, dim3(ntiles), dim3(256), 0, s, reinterpret_cast<const uint2*>(ranges),
+                     point_list, reinterpret_cast<const uint32_t*>(depth), keys);
+  return hipGetLastError();
 }
 
 // identifyTileRanges: with pairs, turns the per-tile counts that

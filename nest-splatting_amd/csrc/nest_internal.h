@@ -170,9 +170,9 @@ hipError_t launch_duplicate_ordered(int P, const uint32_t* order, const uint32_t
                                     const int32_t* radii, uint32_t gx, uint32_t gy, int64_t n_pairs,
                                     uint32_t* tile_keys, uint32_t* ids, hipStream_t s);
 // Stable sort of the depth-ordered pairs on tile bits [0, tile_bits): writes
-// the (tile << 32 | depth bits) keys and the splat ids in tile/depth order,
-// and leaves the pairs per tile in ranges (ntiles uint2, count in .y, x zero)
-// for launch_tile_ranges.
+// the splat ids in tile/depth order, the (tile << 32 | depth bits) keys too
+// unless keys_out is NULL, and leaves the pairs per tile in ranges (ntiles
+// uint2, count in .y, x zero) for launch_tile_ranges.
 size_t tile_sort_ws_bytes(int64_t n);
 hipError_t launch_sort_tiles(const uint32_t* tile_keys, const uint32_t* ids, uint64_t* keys_out, uint32_t* vals_out,
                              int64_t n, int tile_bits, const float* depth, uint32_t* ranges, uint32_t ntiles, void* ws,
@@ -180,6 +180,10 @@ hipError_t launch_sort_tiles(const uint32_t* tile_keys, const uint32_t* ids, uin
 // Per-tile [start, end) of the n sorted pairs from those counts ((0, 0) for a
 // tile without pairs); with n == 0, zeroes the ranges.
 hipError_t launch_tile_ranges(uint32_t* ranges, int64_t n, uint32_t ntiles, hipStream_t s);
+// point_list_keys (tile << 32 | depth bits) of the sorted pairs, from the tile
+// ranges and the point list.
+hipError_t launch_compose_keys(const uint32_t* ranges, const uint32_t* point_list, const float* depth, uint32_t ntiles,
+                               uint64_t* keys, hipStream_t s);
 hipError_t launch_render(const RenderParams& p, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* dst, uint32_t value, int64_t n, hipStream_t s);
 

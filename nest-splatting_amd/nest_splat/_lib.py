@@ -27,7 +27,7 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 SCAN_NOALLOC_MAX = 268431360
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
  GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
@@ -141,6 +141,8 @@ EXPORTS = {
     "nest_forward_render": (ct.c_int, [ct.POINTER(RasterSettings), ct.POINTER(HashGrid), ct.POINTER(Splats),
                                        ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_size_t,
                                        ct.c_int64, ct.POINTER(FrameOutputs), ct.POINTER(Timing), ct.c_void_p]),
+    "nest_binning_keys": (ct.c_int, [ct.c_int32, ct.c_int32, ct.c_int32, ct.c_void_p, ct.c_size_t, ct.c_void_p,
+                                     ct.c_size_t, ct.c_void_p, ct.c_size_t, ct.c_int64, ct.c_void_p]),
     "nest_mark_visible": (ct.c_int, [ct.c_int32, ct.c_void_p, ct.POINTER(ct.c_float), ct.c_void_p, ct.c_void_p]),
     "nest_build_homotrans": (ct.c_int, [ct.c_int64, ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_void_p]),
     "nest_backward_layout": (ct.c_int, [ct.c_int32, ct.c_int32, ct.POINTER(ct.c_size_t), ct.POINTER(ct.c_size_t)]),

@@ -421,7 +421,14 @@ def mark_visible(means3D: torch.Tensor, viewmatrix) -> torch.Tensor:
 
 
 def binning_arrays(res: ForwardResult, W: int, H: int) -> Dict[str, torch.Tensor]:
+    """Views of the frame's workspaces; the sorted keys (the reference's
+    point_list_keys) are composed on this call (nest_binning_keys)."""
     NR = res.num_rendered
+    P = int(res.radii.shape[0])
+    L.check(L.lib().nest_binning_keys(W, H, P, L.ptr(res.geom), res.geom.numel() * res.geom.element_size(),
+                                      L.ptr(res.binning), res.binning.numel() * res.binning.element_size(),
+                                      L.ptr(res.image), res.image.numel() * res.image.element_size(), NR,
+                                      L.stream_ptr(res.geom.device)), "nest_binning_keys")
     n = max(NR, 1)
     o, _ = L.binning_layout(NR)
     io, _ = L.image_layout(W, H)
