@@ -272,6 +272,35 @@ def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_lev
             torch.cuda.synchronize()
             res_ms[name]["backward_ms"] = round((time.perf_counter() - b0) / K * 1e3, 3)
             log(f"[bench] {name}: backward {res_ms[name]['backward_ms']} ms")
+    # hybrid SH modes 8-10: a one-level 3-channel grid at the finest resolution
+    # (2048, 2^21 entries) and rows of 3 raw SH colours or 48 coefficients; the
+    # image is the 3 (or 48) blended channels, no MLP
+    gen = torch.Generator(device=dev).manual_seed(2)
+    htab = (torch.rand((1 << 21, 3), generator=gen, device=dev) - 0.5) * 0.2
+    hgrid_args = (1, 3, 0.0, 2048, htab, np.array([0, 1 << 21], np.int64), np.asarray(spec.gridrange, np.float32))
+    raw = torch.randn((spec.P, 3), generator=gen, device=dev)
+    coeffs = torch.randn((spec.P, 48), generator=gen, device=dev) * 0.3
+    for name, mode, rows_t in (("hybrid_SH(8)", 8, raw), ("hybrid_SH_post(9)", 9, coeffs), ("hybrid_SH_raw(10)", 10, raw)):
+        grid = rz.HashGridDesc(*hgrid_args, render_mode=mode)
+        C = 48 if mode == 9 else 3
+
+        def hframe(tm=None):
+            return rz.rasterize_forward(settings, grid, means, opac, scales, rots, homotrans=homo, ap_level=ap_level,
+                                        colors_precomp=rows_t, channels=C, timing=tm if tm is not None else False)
+
+        hframe()
+        torch.cuda.synchronize()
+        tms = [L.new_timing(True) for _ in range(K)]
+        t0 = time.perf_counter()
+        for k in range(K):
+            hframe(tms[k])
+        torch.cuda.synchronize()
+        frame_ms = (time.perf_counter() - t0) / K * 1e3
+        render_ms = float(np.mean([L.timing_read(tm)["render"] for tm in tms]))
+        for tm in tms:
+            L.timing_release(tm)
+        res_ms[name] = {"render_ms": round(render_ms, 4), "frame_ms": round(frame_ms, 4)}
+        log(f"[bench] {name}: render {render_ms:.3f} ms, frame {frame_ms:.3f} ms")
     return res_ms
 
 
@@ -380,7 +409,8 @@ def main():
     ap.add_argument("--modes", type=int, default=0, metavar="K",
                     help="after the timed frames, time K frames of each other render mode (4 cat, 7 adaptive_add, 12 "
                          "adaptive_cat, 13 adaptive_cat_fast and 14 adaptive_zero, training and inference) on the same splats: per-splat rows of the "
-                         "first 10 levels, a grid of the last 6, and report modes_ms, with K backward passes of modes 4, 7, 12 and 14 "
+                         "first 10 levels, a grid of the last 6, and report modes_ms, with K backward passes of modes 4, 7, 12 and 14; "
+                         "then the hybrid SH modes 8, 9 and 10 over a one-level 3-channel grid "
                          "(not part of the metric)")
     ap.add_argument("--kernels", type=int, default=0, metavar="K",
                     help="after the timed frames, time K launches of the other hot-path kernels on their own: the RVQ "
