@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 13
+#define NEST_ABI_VERSION 14
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -127,6 +127,15 @@ typedef struct nest_hashgrid {
    *     the DC terms; `decompose` 1 (gaussian_only) leaves the grid out, 2
    *     (ngp_only) the colour.  out_color needs 3 (8, 10) or 48 (9)
    *     channels; the channels past them stay 0.
+   *   NEST_MODE_BASELINE_DOUBLE (2), NEST_MODE_BASELINE_BLEND_DOUBLE (3)
+   *     (CR/forward.cu:1146-1217, :1975-2004): a second grid (table2,
+   *     offsets2, gridrange2; the first grid's scale, base resolution and
+   *     flags) queried at each splat's centre into rows2; mode 2 writes the
+   *     first grid's `levels` levels at the hit, then those centre features;
+   *     mode 3 blends only the centre features, then adds the first grid at
+   *     the pixel's blended position with the appearance level of its tile's
+   *     first splat.  level_dim 4; at most 64 channels (levels <= 8 in mode 2,
+   *     16 in mode 3); table2 NULL leaves the centre features 0.
    * Modes 4, 7 and 12-14 need level_dim 2, 4 or 8 and at most 64 channels of
    * per-splat plus grid features; `levels` may be 0 there. */
   int32_t render_mode;
@@ -142,9 +151,21 @@ typedef struct nest_hashgrid {
   /* Render modes 8-10: 0 both parts, 1 gaussian_only, 2 ngp_only (bits 24-31
    * of the reference's packed level, GR:619-626).  Other modes ignore it. */
   uint32_t decompose;
+  /* Render modes 2 and 3: the second ("diffuse") grid, float32
+   * [table2_rows, 4] with its own offsets and range (GR's features_diffuse,
+   * offsets_diffuse, gridrange_diffuse), or table2 NULL; rows2 is the
+   * caller's device scratch of [P, levels * 4] floats that the forward fills
+   * with its features at the splat centres.  Other modes ignore them. */
+  const void *table2;
+  int64_t table2_rows;
+  int32_t offsets2[NEST_MAX_LEVELS + 1];
+  float gridrange2[2];
+  float *rows2;
 } nest_hashgrid;
 
 #define NEST_MODE_BASELINE 0
+#define NEST_MODE_BASELINE_DOUBLE 2
+#define NEST_MODE_BASELINE_BLEND_DOUBLE 3
 #define NEST_MODE_CAT 4
 #define NEST_MODE_ADAPTIVE_ADD 7
 #define NEST_MODE_HYBRID_SH 8

@@ -195,13 +195,40 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
   const bool adaptive = base_mode == NEST_MODE_ADAPTIVE_CAT || base_mode == NEST_MODE_ADAPTIVE_CAT_FAST ||
                         base_mode == NEST_MODE_ADAPTIVE_ZERO;
   const bool hsh = base_mode >= NEST_MODE_HYBRID_SH && base_mode <= NEST_MODE_HYBRID_SH_RAW;
+  const bool dual = base_mode == NEST_MODE_BASELINE_DOUBLE || base_mode == NEST_MODE_BASELINE_BLEND_DOUBLE;
   if ((gr->render_mode & ~0x1FF) != 0 ||
       (base_mode != NEST_MODE_BASELINE && base_mode != NEST_MODE_CAT && base_mode != NEST_MODE_ADAPTIVE_ADD &&
-       !adaptive && !hsh) ||
+       !adaptive && !hsh && !dual) ||
       ((gr->render_mode & NEST_MODE_INFERENCE) && !adaptive))
     return fail(NEST_ERR_UNSUPPORTED,
-                "render_mode %d: supported are 0, 4, 7, 8, 9, 10, 12, 13, 14 and 12, 13, 14 | 0x100", gr->render_mode);
-  const bool mix = base_mode != NEST_MODE_BASELINE && !hsh;
+                "render_mode %d: supported are 0, 2, 3, 4, 7, 8, 9, 10, 12, 13, 14 and 12, 13, 14 | 0x100",
+                gr->render_mode);
+  const bool mix = base_mode != NEST_MODE_BASELINE && !hsh && !dual;
+  if (dual) {
+    // a second grid at the splat centres, 4 features per level in both
+    // (CR/forward.cu:1146-1217)
+    if (gr->levels == 0 || gr->level_dim != 4)
+      return fail(NEST_ERR_UNSUPPORTED, "render_mode %d needs grid levels with level_dim 4 (got %u levels of %u)",
+                  base_mode, gr->levels, gr->level_dim);
+    const uint32_t feat = (base_mode == NEST_MODE_BASELINE_DOUBLE ? 2u : 1u) * gr->levels * 4u;
+    if (feat > 64u)
+      return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: at most 64 feature channels (got %u)", base_mode, feat);
+    if ((uint32_t)channels < feat)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "out_color has %d channels, render_mode %d produces %u", channels,
+                  base_mode, feat);
+    if (gr->table2) {
+      if (gr->offsets2[gr->levels] > gr->table2_rows)
+        return fail(NEST_ERR_INVALID_ARGUMENT, "second table has %lld rows, offsets2[%u] = %d",
+                    (long long)gr->table2_rows, gr->levels, gr->offsets2[gr->levels]);
+      if (!(gr->gridrange2[1] > gr->gridrange2[0]))
+        return fail(NEST_ERR_INVALID_ARGUMENT, "gridrange2 must satisfy min < max");
+    }
+    if (sp->P > 0) {
+      if (!sp->homotrans) return fail(NEST_ERR_INVALID_ARGUMENT, "homotrans is required in render_mode %d", base_mode);
+      if (!gr->rows2)
+        return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode %d needs rows2, a [P, levels * 4] float scratch", base_mode);
+    }
+  }
   if (hsh) {
     // one 3-channel float32 grid level and rows of 3 raw colours or 48 SH
     // coefficients (CR/forward.cu:1378-1542)
@@ -506,7 +533,27 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   rp.kernel_type = sp->kernel_type;
   if ((rc = setup_grid(rs, gr, sp, out->channels, rp.grid))) return rc;
   const int base_mode = gr->render_mode & 0xFF;
-  if (base_mode >= NEST_MODE_HYBRID_SH && base_mode <= NEST_MODE_HYBRID_SH_RAW) {
+  const bool dual = base_mode == NEST_MODE_BASELINE_DOUBLE || base_mode == NEST_MODE_BASELINE_BLEND_DOUBLE;
+  GridParams grid1 = rp.grid;  // mode 3 looks the first grid up after the render
+  if (dual) {
+    // the centre features as per-splat rows ahead of the grid's levels (as in
+    // mode 4); mode 2 then writes the grid's channels first, mode 3 blends the
+    // rows alone
+    rp.mix = 1;
+    rp.hyb = (int)gr->levels;
+    rp.pgd = rp.hyb * 4;
+    rp.cstride = rp.pgd;
+    rp.nrow = rp.pgd;
+    rp.wslot = -1;
+    rp.fthr = INFINITY;
+    rp.fneg = 0;
+    if (base_mode == NEST_MODE_BASELINE_DOUBLE) {
+      rp.rot = rp.pgd;
+      rp.rot_n = 2 * rp.pgd;
+    } else {
+      rp.grid.L = 0;
+    }
+  } else if (base_mode >= NEST_MODE_HYBRID_SH && base_mode <= NEST_MODE_HYBRID_SH_RAW) {
     // hybrid SH (CR/forward.cu:1378-1542): rows of 3 raw colours or 48 SH coefficients
     rp.hsh = base_mode;
     rp.hsh_dec = (int)gr->decompose;
@@ -618,6 +665,7 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   // feature_ptr of CR/rasterizer_impl.cu:399: precomputed colours, else the
   // colours preprocess evaluated from SH
   rp.colors = sh_colours(sp) ? reinterpret_cast<const float*>(g + go[NEST_GEOM_RGB]) : sp->colors_precomp;
+  if (dual) rp.colors = gr->rows2;
   rp.out_color = out->out_color;
   rp.out_others = out->out_others;
   rp.final_T = reinterpret_cast<float*>(im + io[NEST_IMG_FINAL_T]);
@@ -635,7 +683,39 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     rp.trans_avg = out->trans_avg;
   }
   tm.begin(NEST_STAGE_RENDER);
+  if (dual && sp->P > 0) {
+    // the second grid's features at the splat centres (CR/forward.cu:1164-1175)
+    hipError_t e = hipSuccess;
+    if (gr->table2) {
+      GridParams g2 = grid1;
+      if ((rc = build_levels(gr->offsets2, gr->levels, gr->log2_scale, gr->base_resolution, gr->align_corners != 0, 3,
+                             true, g2.lv)))
+        return rc;
+      g2.table = gr->table2;
+      g2.table_rows = (uint32_t)gr->table2_rows;
+      g2.half = 0u;
+      g2.vmin = gr->gridrange2[0];
+      g2.vmax = gr->gridrange2[1];
+      if (!g2.contract) {
+        g2.inv_size = 1.0f / (g2.vmax - g2.vmin);
+        g2.vmid = 0.0f;
+      } else {
+        g2.vmid = (g2.vmax + g2.vmin) * 0.5f;
+        g2.inv_size = 1.0f / ((g2.vmax - g2.vmin) * 0.5f);
+      }
+      e = launch_centre_rows(g2, sp->P, sp->homotrans, sp->ap_level, gr->rows2, s);
+    } else {
+      e = launch_fill_u32(reinterpret_cast<uint32_t*>(gr->rows2), 0u, (int64_t)sp->P * gr->levels * 4, s);
+    }
+    if (e != hipSuccess) return hip_fail(e, "centre features");
+  }
   if ((rc = check_stage(launch_render(rp, s), "render", rs->debug, s))) return rc;
+  if (base_mode == NEST_MODE_BASELINE_BLEND_DOUBLE) {
+    // the first grid at each pixel's blended position (CR/forward.cu:1975-2004)
+    RenderParams ps = rp;
+    ps.grid = grid1;
+    if ((rc = check_stage(launch_spatial_add(ps, sp->ap_level, s), "blended-position grid", rs->debug, s))) return rc;
+  }
   tm.end();
   return NEST_OK;
 }

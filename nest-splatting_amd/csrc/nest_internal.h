@@ -147,6 +147,10 @@ struct RenderParams {
   // hsh_dec 1 leaves the grid out, 2 the row's colour.
   int hsh;
   int hsh_dec;
+  // Render mode 2: the accumulators hold [centre rows | grid]; output channel
+  // of accumulator c < rot_n is (c + rot) % rot_n, so the grid comes first.
+  int rot;
+  int rot_n;
 };
 
 // Host-side launchers (defined in the .hip files).  Each returns the
@@ -185,6 +189,15 @@ hipError_t launch_tile_ranges(uint32_t* ranges, int64_t n, uint32_t ntiles, hipS
 hipError_t launch_compose_keys(const uint32_t* ranges, const uint32_t* point_list, const float* depth, uint32_t ntiles,
                                uint64_t* keys, hipStream_t s);
 hipError_t launch_render(const RenderParams& p, hipStream_t s);
+// Render modes 2 and 3: the second grid g2 (4 features per level, float32)
+// at every splat's centre (homotrans column 3), levels below min(ap, L), into
+// rows [P, L * 4].
+hipError_t launch_centre_rows(const GridParams& g2, int P, const float* homotrans, const float* ap_level, float* rows,
+                              hipStream_t s);
+// Render mode 3 after the render: each pixel's out_color channels [0, L * 4)
+// plus the grid p.grid at its blended position (out_others 8-10) with the
+// appearance level of the tile's first splat (0 without hits or ap_level).
+hipError_t launch_spatial_add(const RenderParams& p, const float* ap_level, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* dst, uint32_t value, int64_t n, hipStream_t s);
 
 // Backward of the render (renderCUDAsurfelBackward, mode 0).  Reads the

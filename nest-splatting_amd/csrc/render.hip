@@ -903,8 +903,14 @@ render_kernel(const RenderParams p) {
   p.n_contrib[pid] = last_contributor;
   p.n_contrib[pid + HW] = f2u_sat(median_contributor);
 #pragma unroll
-  for (int c = 0; c < NACC; c++)
-    if (c < p.C) p.out_color[(size_t)c * HW + pid] = acc[c];
+  for (int c = 0; c < NACC; c++) {
+    if (c < p.C) {
+      int oc = c;
+      if constexpr (kMix != 0)
+        if (c < p.rot_n) oc = (c + p.rot) % p.rot_n;  // render mode 2: the grid's channels first
+      p.out_color[(size_t)oc * HW + pid] = acc[c];
+    }
+  }
   for (int c = NACC; c < p.C; c++) p.out_color[(size_t)c * HW + pid] = 0.0f;
   float* O = p.out_others;
   O[pid + 0 * HW] = D;
@@ -1002,6 +1008,89 @@ __global__ void __launch_bounds__(kRenderThreads) record_transmittance_kernel(co
       if (__ballot(!done) == 0ull) break;
     }
   }
+}
+
+// query_feature<false, 16 * 4, 4> of grid g at xyz (levels below min(ap, L),
+// the rest 0, all 0 outside the grid), for the dual-grid modes' queries away
+// from the hit loop: one lane per point, plain entry loads.  Channel c
+// (< nout) goes to out[c * stride], added to it with kAdd.
+template <bool kHalf, bool kAdd>
+__device__ __forceinline__ void grid_point_features(const GridParams& g, const float xyz[3], uint32_t ap, float* out,
+                                                    size_t stride, uint32_t nout) {
+  float u[3];
+  bool oob;
+  grid_coord(g, xyz, u, oob);
+  const uint32_t maxl = oob ? 0u : (ap < g.L ? ap : g.L);
+  for (uint32_t l = 0; l < g.L; l++) {
+    float h[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (l < maxl) {
+      LevelCorners cn;
+      level_corners<4, kHalf>(g.lv, (int)l, g.pos_offset, g.interp, u, cn);
+      float vals[8][4];
+#pragma unroll
+      for (int k = 0; k < 8; k++) load_entry<4, kHalf>(g.table, (size_t)g.lv.base[l] + cn.idx[k], vals[k]);
+      corners_sum<4>(cn, vals, h);
+    }
+#pragma unroll
+    for (int f = 0; f < 4; f++) {
+      const uint32_t c = 4u * l + (uint32_t)f;
+      if (c < nout) {
+        float* o = out + (size_t)c * stride;
+        *o = kAdd ? *o + h[f] : h[f];
+      }
+    }
+  }
+}
+
+// Render modes 2 and 3 (CR/forward.cu:1164-1175, :1197-1208): the second
+// grid at each splat's centre, the homotrans translation column.
+__global__ void __launch_bounds__(256) centre_rows_kernel(const GridParams g2, int P, const float* __restrict__ homotrans,
+                                                          const float* __restrict__ ap_level, float* __restrict__ rows) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P) return;
+  const float* Hm = homotrans + 16 * (size_t)i;
+  const float pk[3] = {Hm[3], Hm[7], Hm[11]};
+  const uint32_t ap = ap_level ? f2u_sat(floorf(ap_level[i])) : 0xffffffffu;
+  grid_point_features<false, false>(g2, pk, ap, rows + (size_t)i * g2.L * 4u, 1, g2.L * 4u);
+}
+
+hipError_t launch_centre_rows(const GridParams& g2, int P, const float* homotrans, const float* ap_level, float* rows,
+                              hipStream_t s) {
+  if (P <= 0) return hipSuccess;
+  hipLaunchKernelGGL(centre_rows_kernel, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, s, g2, P, homotrans, ap_level,
+                     rows);
+  return hipGetLastError();
+}
+
+// Render mode 3 after the loop (CR/forward.cu:1975-2004), one lane per pixel:
+// the grid at the blended position pos (out_others 8-10, not divided by
+// alpha), appearance level of the tile's first splat when the pixel has a
+// contributor, else 0 (no levels), added to channels [0, L * 4).
+template <bool kHalf>
+__global__ void __launch_bounds__(256) spatial_add_kernel(const RenderParams p, const float* __restrict__ ap_level) {
+  const int64_t HW = (int64_t)p.W * p.H;
+  const int64_t pid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (pid >= HW) return;
+  const uint32_t px = (uint32_t)(pid % p.W), py = (uint32_t)(pid / p.W);
+  uint32_t pap = 0u;
+  if (ap_level != nullptr && p.n_contrib[pid] > 0u) {
+    const uint32_t tile = (py / kTile) * p.gx + px / kTile;
+    const uint32_t first = p.point_list[p.ranges[2u * tile]];
+    pap = f2u_sat(floorf(ap_level[first]));
+  }
+  const float pos[3] = {p.out_others[pid + 8 * HW], p.out_others[pid + 9 * HW], p.out_others[pid + 10 * HW]};
+  grid_point_features<kHalf, true>(p.grid, pos, pap, p.out_color + pid, (size_t)HW, (uint32_t)p.C);
+}
+
+hipError_t launch_spatial_add(const RenderParams& p, const float* ap_level, hipStream_t s) {
+  const int64_t HW = (int64_t)p.W * p.H;
+  if (HW == 0 || p.grid.L == 0) return hipSuccess;
+  const dim3 grid((unsigned)((HW + 255) / 256));
+  if (p.grid.half)
+    hipLaunchKernelGGL(spatial_add_kernel<true>, grid, dim3(256), 0, s, p, ap_level);
+  else
+    hipLaunchKernelGGL(spatial_add_kernel<false>, grid, dim3(256), 0, s, p, ap_level);
+  return hipGetLastError();
 }
 
 template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0, bool kKT = false,

@@ -104,9 +104,10 @@ class _RasterizeGaussians(torch.autograd.Function):
                 ap_level, features, offsets, gridrange, features_diffuse, offsets_diffuse, gridrange_diffuse,
                 raster_settings, hashgrid_settings, render_mode, shapes, kernel_type):
         base_mode = render_mode & 0xFF
-        if base_mode not in (0, 4, 7, 8, 9, 10, 12, 13, 14) or (render_mode & ~0x1FF) or \
+        if base_mode not in (0, 2, 3, 4, 7, 8, 9, 10, 12, 13, 14) or (render_mode & ~0x1FF) or \
                 ((render_mode & 0x100) and base_mode not in (12, 13, 14)):
-            raise NotImplementedError(f"render_mode {render_mode}: implemented are 0 (baseline), 4 (cat), "
+            raise NotImplementedError(f"render_mode {render_mode}: implemented are 0 (baseline), 2 / 3 "
+                                      f"(baseline_double / baseline_blend_double), 4 (cat), "
                                       f"7 (adaptive_add), 8 / 9 / 10 (hybrid_SH / hybrid_SH_post / hybrid_SH_raw) and "
                                       f"12 / 13 / 14 (adaptive_cat / adaptive_cat_fast / adaptive_zero, | 0x100 "
                                       f"inference)")
@@ -117,13 +118,31 @@ class _RasterizeGaussians(torch.autograd.Function):
             raise ValueError(f"kernel_type {kernel_type} needs shapes [P] (CR/forward.cu:864-900)")
         if not _empty(cov3Ds_precomp):
             raise NotImplementedError("precomputed transforms (cov3D_precomp) are not implemented")
-        if not _empty(features_diffuse):
-            raise NotImplementedError("a second (diffuse) hash grid is not implemented")
+        if not _empty(features_diffuse) and base_mode not in (2, 3):
+            raise NotImplementedError("a second (diffuse) hash grid is read by render modes 2 and 3 only")
         C = _channels(hashgrid_settings)
         level = int(hashgrid_settings.L)
-        if base_mode in (4, 7, 8, 9, 10, 12, 14) and level == 0:
+        if base_mode in (2, 3, 4, 7, 8, 9, 10, 12, 14) and level == 0:
             base_mode = render_mode = 0  # level 0 is the colour path in every mode but 13 (CR/forward.cu:1091)
-        if base_mode in (8, 9, 10):
+        if base_mode in (2, 3):
+            # baseline_double / baseline_blend_double (CR/forward.cu:1146-1217): the grid's
+            # levels plus a second grid (features_diffuse, GR's diffuse grid) at the splat
+            # centres, 4 features per level in both
+            if _empty(features) or _empty(offsets) or _empty(gridrange):
+                raise ValueError(f"render_mode {base_mode} needs features, offsets and gridrange")
+            hs = hashgrid_settings
+            second = not (_empty(features_diffuse) or _empty(offsets_diffuse) or _empty(gridrange_diffuse))
+            grid = _rz.HashGridDesc(levels=level, level_dim=int(features.shape[1]), log2_scale=float(hs.S),
+                                    base_resolution=int(hs.H), table=features.detach().contiguous(),
+                                    offsets=_rz.host_array(offsets, np.int64),
+                                    gridrange=_rz.host_array(gridrange, np.float32),
+                                    align_corners=bool(hs.align_corners), interpolation=int(hs.interpolation),
+                                    render_mode=base_mode,
+                                    table2=features_diffuse.detach().contiguous() if second else None,
+                                    offsets2=_rz.host_array(offsets_diffuse, np.int64) if second else None,
+                                    gridrange2=_rz.host_array(gridrange_diffuse, np.float32) if second else None)
+            colors = None
+        elif base_mode in (8, 9, 10):
             # hybrid SH (CR/forward.cu:1378-1542): level = decompose << 24 | SH degree << 16 |
             # grid levels << 8 (GR:617-626), one 3-channel grid level, rows of 3 raw colours or
             # 48 SH coefficients in colors_precomp

@@ -27,7 +27,7 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 SCAN_NOALLOC_MAX = 268431360
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
  GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
@@ -56,10 +56,14 @@ class HashGrid(ct.Structure):
                 ("table_rows", ct.c_int64), ("offsets", ct.c_int32 * (MAX_LEVELS + 1)),
                 ("gridrange", ct.c_float * 2), ("render_mode", ct.c_int32), ("hybrid_levels", ct.c_uint32),
                 ("total_levels", ct.c_uint32),
-                ("active_levels", ct.c_uint32), ("decompose", ct.c_uint32)]
+                ("active_levels", ct.c_uint32), ("decompose", ct.c_uint32), ("table2", ct.c_void_p),
+                ("table2_rows", ct.c_int64), ("offsets2", ct.c_int32 * (MAX_LEVELS + 1)), ("gridrange2", ct.c_float * 2),
+                ("rows2", ct.c_void_p)]
 
 
 MODE_BASELINE = 0
+MODE_BASELINE_DOUBLE = 2
+MODE_BASELINE_BLEND_DOUBLE = 3
 MODE_CAT = 4
 MODE_ADAPTIVE_ADD = 7
 MODE_HYBRID_SH = 8

@@ -9,6 +9,8 @@ geometry and render stages, exactly where the reference reads num_rendered.
 """
 from __future__ import annotations
 
+import dataclasses
+
 import ctypes as ct
 from dataclasses import dataclass, field
 from typing import Dict, Optional
@@ -59,6 +61,15 @@ class HashGridDesc:
     active_levels: Optional[int] = None
     # render_mode 8 / 9 / 10 (hybrid SH): 0 both parts, 1 gaussian_only, 2 ngp_only
     decompose: int = 0
+    # render_mode 2 / 3: the second grid (float32 [rows, 4] table, offsets, range)
+    # queried at the splat centres; table2 None leaves its features 0
+    table2: Optional[torch.Tensor] = None
+    offsets2: Optional[np.ndarray] = None
+    gridrange2: Optional[np.ndarray] = None
+    rows2: Optional[torch.Tensor] = None  # [P, levels * 4] scratch, set by rasterize_forward
+
+    def dual(self) -> bool:
+        return (self.render_mode & 0xFF) in (L.MODE_BASELINE_DOUBLE, L.MODE_BASELINE_BLEND_DOUBLE)
 
     def row_width(self, channels: int) -> int:
         """Floats per splat of colors_precomp for this render mode."""
@@ -114,6 +125,23 @@ class HashGridDesc:
                 g.offsets[i] = int(offs[i])
             g.gridrange[0] = float(self.gridrange[0])
             g.gridrange[1] = float(self.gridrange[1])
+        if self.dual():
+            if self.table2 is not None:
+                t2 = self.table2
+                if t2.dtype != torch.float32 or not t2.is_cuda or t2.dim() != 2 or t2.shape[1] != 4:
+                    raise ValueError("the second grid's table must be a float32 [rows, 4] device tensor")
+                if not t2.is_contiguous() or t2.data_ptr() % 16 != 0:
+                    t2 = self.table2 = t2.contiguous().clone()
+                g.table2 = t2.data_ptr()
+                g.table2_rows = int(t2.shape[0])
+                o2 = np.asarray(self.offsets2, dtype=np.int64)
+                if o2.shape[0] < self.levels + 1:
+                    raise ValueError(f"offsets2 has {o2.shape[0]} entries, need {self.levels + 1}")
+                for i in range(self.levels + 1):
+                    g.offsets2[i] = int(o2[i])
+                g.gridrange2[0] = float(self.gridrange2[0])
+                g.gridrange2[1] = float(self.gridrange2[1])
+            g.rows2 = L.ptr(self.rows2).value if self.rows2 is not None else None
         return g
 
 
@@ -249,6 +277,10 @@ def rasterize_forward(settings: L.RasterSettings, grid: HashGridDesc, means3D: t
     H, W = settings.image_height, settings.image_width
     sp, keep = _splats(means3D, opacities, scales, rotations, homotrans, ap_level, colors_precomp, channels, shs,
                        sh_degree, grid.row_width(channels), shapes=shapes, kernel_type=kernel_type)
+    if grid.dual():
+        # render modes 2 and 3: scratch for the second grid's features at the splat centres
+        grid = dataclasses.replace(grid, rows2=torch.empty((max(P, 1), grid.levels * 4), dtype=torch.float32,
+                                                           device=dev))
     g = grid.to_c()
 
     color = torch.empty((channels, H, W), dtype=torch.float32, device=dev)

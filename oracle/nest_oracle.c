@@ -700,7 +700,9 @@ typedef struct {
      * (same level, rows of hyb*F+1 floats), 8 / 9 / 10 hybrid_SH /
      * hybrid_SH_post / hybrid_SH_raw (level = decompose << 24 | SH degree
      * << 16 | grid levels << 8, rows of 3 / 48 / 3 floats, a one-level
-     * 3-channel grid).  Other values are not restated. */
+     * 3-channel grid), 2 / 3 baseline_double / baseline_blend_double (level =
+     * the levels of both grids, F = 4, the second grid below).  Other values
+     * are not restated. */
     int render_mode;
     /* record_transmittance (forward.cu:1961-1964), NULL = off: [P] each;
      * every hit that reaches the end of the hit body (not mode 13's, which
@@ -713,6 +715,12 @@ typedef struct {
      * exp(-0.5 * max(rho, 1e-8)^(shape / 2)); shapes [P] for 1-3. */
     const float *shapes;
     int kernel_type;
+    /* the second ("diffuse") grid of render modes 2 and 3: its offsets [L+1],
+     * float32 table and range; scale, base resolution and flags are the
+     * first grid's (forward.cu:1164-1175).  table2 NULL: its features are 0. */
+    const int32_t *offsets2;
+    const void *table2;
+    float vmin2, vmax2;
 } or_render_args;
 
 static void record_hit(const or_render_args *A, uint32_t id, float T)
@@ -939,6 +947,39 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
                             feat_scratch[fs + i] = infer ? hf[i] : fmaf(wt, gf[fs + i], (1.0f - wt) * hf[i]);
                     }
                 }
+            } else if ((A->render_mode & 0xFF) == 2 || (A->render_mode & 0xFF) == 3) {
+                /* baseline_double (2, forward.cu:1146-1186): the grid's `level`
+                 * levels at the hit, then the second grid's at the splat centre
+                 * (homotrans column 3), 4 features per level each;
+                 * baseline_blend_double (3, :1187-1217): only the second grid's
+                 * features at the centre (the first grid is queried once per
+                 * pixel after the loop, below).  The channels past them stay 0. */
+                const int L = A->level, F = A->grid.F;
+                float fpk[64];
+                for (int i = 0; i < 64; i++) fpk[i] = 0.0f;
+                if (A->table2) {
+                    or_grid G2 = A->grid;
+                    G2.L = L;
+                    G2.offsets = A->offsets2;
+                    G2.table = A->table2;
+                    G2.half_table = 0;
+                    G2.vmin = A->vmin2;
+                    G2.vmax = A->vmax2;
+                    const float *Hm = A->homotrans + 16 * (size_t)id;
+                    const float pk[3] = {Hm[3], Hm[7], Hm[11]};
+                    or_query_feature(&G2, pk, ap, 64, fpk);
+                }
+                for (int c = 0; c < C; c++) feat_scratch[c] = 0.0f;
+                if ((A->render_mode & 0xFF) == 2) {
+                    float fx[64];
+                    or_grid G1 = A->grid;
+                    G1.L = L;
+                    or_query_feature(&G1, xyz, ap, 64, fx);
+                    for (int i = 0; i < L * F && i < C; i++) feat_scratch[i] = fx[i];
+                    for (int i = 0; i < L * F && L * F + i < C; i++) feat_scratch[L * F + i] = fpk[i];
+                } else {
+                    for (int i = 0; i < L * F && i < C; i++) feat_scratch[i] = fpk[i];
+                }
             } else if ((A->render_mode & 0xFF) >= 8 && (A->render_mode & 0xFF) <= 10) {
                 /* hybrid_SH (8), hybrid_SH_post (9), hybrid_SH_raw (10)
                  * (forward.cu:1378-1542), level = decompose << 24 | sh degree
@@ -1007,6 +1048,24 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
         record_hit(A, id, T);
         T = test_T;
         last_contributor = contributor;
+    }
+    if ((A->render_mode & 0xFF) == 3 && A->level > 0) {
+        /* baseline_blend_double after the loop (forward.cu:1975-2004): the
+         * first grid at the blended position (pos, not divided by alpha) with
+         * the appearance level of the tile's first splat (0 for a pixel
+         * without hits, or without ap_level: no levels), added to the
+         * blended channels */
+        const float bp[3] = {pos_x, pos_y, pos_z};
+        uint32_t pap = 0;
+        if (A->ap_level && last_contributor > 0) {
+            const uint32_t fid = A->point_list[A->ranges[2 * (size_t)tile]];
+            pap = f2u_sat(floorf(A->ap_level[fid]));
+        }
+        float fs[64];
+        or_grid G1 = A->grid;
+        G1.L = A->level;
+        or_query_feature(&G1, bp, pap, 64, fs);
+        for (int c = 0; c < C && c < 64; c++) Cacc[c] = Cacc[c] + fs[c];
     }
     A->final_T[pid] = T;
     A->final_T[pid + HW] = M1;

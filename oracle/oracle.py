@@ -46,7 +46,8 @@ class OrRenderArgs(ct.Structure):
                 ("ap_level", ct.c_void_p), ("colors", ct.c_void_p), ("grid", OrGrid),
                 ("out_color", ct.c_void_p), ("out_others", ct.c_void_p), ("final_T", ct.c_void_p),
                 ("n_contrib", ct.c_void_p), ("render_mode", ct.c_int), ("cover_pixels", ct.c_void_p),
-                ("trans_avg", ct.c_void_p), ("shapes", ct.c_void_p), ("kernel_type", ct.c_int)]
+                ("trans_avg", ct.c_void_p), ("shapes", ct.c_void_p), ("kernel_type", ct.c_int),
+                ("offsets2", ct.c_void_p), ("table2", ct.c_void_p), ("vmin2", ct.c_float), ("vmax2", ct.c_float)]
 
 
 class OrRenderBwdArgs(ct.Structure):
@@ -223,7 +224,7 @@ def make_grid(L, F, S, H, offsets, table, gridrange, contract=False, align_corne
 
 def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_level=None, colors=None,
            beta=0.0, max_intersections=0, row_stride=1, row_phase=0, threads=0, render_mode=0, level=None,
-           record_transmittance=False, shapes=None, kernel_type=0):
+           record_transmittance=False, shapes=None, kernel_type=0, grid2=None):
     """renderCUDAsurfelForward for every pixel.  render_mode 0 (grid levels
     grid.L, or the colour path without a grid), 4, 7, 12, 13 or 14 (bit 8:
     inference); for modes 4, 7, 12, 13 and 14, level is the reference's packed level argument
@@ -233,7 +234,9 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
     3 raw SH colours (8, 10) or 48 SH coefficients (9) and the grid one level
     of 3 channels.  record_transmittance adds cover_pixels and
     trans_avg ([P] each) to the result.  kernel_type 1-3 take the per-splat
-    parameter from shapes [P]."""
+    parameter from shapes [P].  Render modes 2 and 3 (level = the grids'
+    levels, F = 4) take the second grid as grid2 = (offsets, float32 table,
+    gridrange), or None for a missing one."""
     HW = W * H
     out = dict(color=np.zeros((C, H, W), np.float32), others=np.zeros((14, H, W), np.float32),
                final_T=np.zeros((3, H, W), np.float32), n_contrib=np.zeros((2, H, W), np.uint32))
@@ -276,6 +279,10 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
     args.kernel_type = kernel_type
     if kernel_type != 0:
         args.shapes = ptr(np.asarray(shapes, np.float32).reshape(-1), np.float32)
+    if grid2 is not None:
+        args.offsets2 = ptr(grid2[0], np.int32)
+        args.table2 = ptr(grid2[1], np.float32)
+        args.vmin2, args.vmax2 = float(grid2[2][0]), float(grid2[2][1])
     lib().or_render(ct.byref(args), row_stride, row_phase, threads)
     return out
 

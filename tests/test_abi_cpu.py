@@ -204,6 +204,44 @@ def test_render_validates_hybrid_sh_modes():
     assert lib.nest_forward_render(*args()) == L.NEST_ERR_WORKSPACE
 
 
+def test_render_validates_dual_grid_modes():
+    """Render modes 2 and 3: level_dim 4, at most 64 channels, a valid second
+    grid when given, the rows2 scratch; checked before any launch."""
+    L = _lib()
+    lib = L.lib()
+    s = _settings(L)
+    sp = _splats(L, 0)
+    g = L.HashGrid()
+    g.struct_size = ct.sizeof(L.HashGrid)
+    g.render_mode = L.MODE_BASELINE_DOUBLE
+    g.levels, g.level_dim, g.table, g.table_rows = 8, 4, 1, 8 * 1024
+    for i in range(9):
+        g.offsets[i] = g.offsets2[i] = i * 1024
+    g.gridrange[0], g.gridrange[1] = -1.0, 1.0
+    out = L.FrameOutputs()
+    out.struct_size = ct.sizeof(L.FrameOutputs)
+    out.channels = 32
+    out.out_color = out.out_others = 1
+    ws = (ct.c_uint8 * 16)()
+    args = lambda: (ct.byref(s), ct.byref(g), ct.byref(sp), ws, 16, ws, 16, ws, 16, 0, ct.byref(out), None, None)
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_INVALID_ARGUMENT  # mode 2 writes 64 channels
+    out.channels = 64
+    g.levels = 9
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_UNSUPPORTED  # 72 channels
+    g.levels, g.level_dim = 8, 2
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_UNSUPPORTED  # level_dim 4
+    g.level_dim, g.table2, g.table2_rows = 4, 1, 10
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_INVALID_ARGUMENT  # second table too small
+    g.table2_rows = 8 * 1024
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_INVALID_ARGUMENT  # empty gridrange2
+    g.gridrange2[0], g.gridrange2[1] = -2.0, 2.0
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_WORKSPACE  # accepted
+    g.render_mode, g.levels = L.MODE_BASELINE_BLEND_DOUBLE, 16
+    for i in range(17):
+        g.offsets[i] = g.offsets2[i] = i * 512
+    assert lib.nest_forward_render(*args()) == L.NEST_ERR_WORKSPACE  # mode 3: 16 levels, 64 channels
+
+
 def test_backward_layout_and_validation():
     """nest_backward_layout sizes and the argument checks of nest_backward /
     nest_grid_encode_backward, which return before any launch."""
