@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 14
+#define NEST_ABI_VERSION 15
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -135,7 +135,15 @@ typedef struct nest_hashgrid {
    *     mode 3 blends only the centre features, then adds the first grid at
    *     the pixel's blended position with the appearance level of its tile's
    *     first splat.  level_dim 4; at most 64 channels (levels <= 8 in mode 2,
-   *     16 in mode 3); table2 NULL leaves the centre features 0.
+   *     16 in mode 3); table2 NULL leaves the centre features 0;
+   *   NEST_MODE_SURFACE (1), NEST_MODE_SURFACE_RGB (5) (CR/forward.cu:
+   *     1825-1908): float32 grid levels of 12 (mode 1) or 15 (mode 5)
+   *     features at the hit, whose first 12 are four 3-vectors dotted with
+   *     the splat's normal; mode 1 writes max(0, -dot + b) per vector, b the
+   *     second grid's 4 features per level at the splat centre (0 without
+   *     table2), 4 channels per level (levels <= 16); mode 5 max(0, -dot) and
+   *     then the grid's features 12-14 at the centre, 7 channels per level
+   *     (levels <= 9).  rows2 as in modes 2 and 3.
    * Modes 4, 7 and 12-14 need level_dim 2, 4 or 8 and at most 64 channels of
    * per-splat plus grid features; `levels` may be 0 there. */
   int32_t render_mode;
@@ -151,7 +159,7 @@ typedef struct nest_hashgrid {
   /* Render modes 8-10: 0 both parts, 1 gaussian_only, 2 ngp_only (bits 24-31
    * of the reference's packed level, GR:619-626).  Other modes ignore it. */
   uint32_t decompose;
-  /* Render modes 2 and 3: the second ("diffuse") grid, float32
+  /* Render modes 1, 2 and 3: the second ("diffuse") grid, float32
    * [table2_rows, 4] with its own offsets and range (GR's features_diffuse,
    * offsets_diffuse, gridrange_diffuse), or table2 NULL; rows2 is the
    * caller's device scratch of [P, levels * 4] floats that the forward fills
@@ -164,8 +172,10 @@ typedef struct nest_hashgrid {
 } nest_hashgrid;
 
 #define NEST_MODE_BASELINE 0
+#define NEST_MODE_SURFACE 1
 #define NEST_MODE_BASELINE_DOUBLE 2
 #define NEST_MODE_BASELINE_BLEND_DOUBLE 3
+#define NEST_MODE_SURFACE_RGB 5
 #define NEST_MODE_CAT 4
 #define NEST_MODE_ADAPTIVE_ADD 7
 #define NEST_MODE_HYBRID_SH 8

@@ -196,14 +196,39 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
                         base_mode == NEST_MODE_ADAPTIVE_ZERO;
   const bool hsh = base_mode >= NEST_MODE_HYBRID_SH && base_mode <= NEST_MODE_HYBRID_SH_RAW;
   const bool dual = base_mode == NEST_MODE_BASELINE_DOUBLE || base_mode == NEST_MODE_BASELINE_BLEND_DOUBLE;
+  const bool surf = base_mode == NEST_MODE_SURFACE || base_mode == NEST_MODE_SURFACE_RGB;
   if ((gr->render_mode & ~0x1FF) != 0 ||
       (base_mode != NEST_MODE_BASELINE && base_mode != NEST_MODE_CAT && base_mode != NEST_MODE_ADAPTIVE_ADD &&
-       !adaptive && !hsh && !dual) ||
+       !adaptive && !hsh && !dual && !surf) ||
       ((gr->render_mode & NEST_MODE_INFERENCE) && !adaptive))
     return fail(NEST_ERR_UNSUPPORTED,
-                "render_mode %d: supported are 0, 2, 3, 4, 7, 8, 9, 10, 12, 13, 14 and 12, 13, 14 | 0x100",
-                gr->render_mode);
-  const bool mix = base_mode != NEST_MODE_BASELINE && !hsh && !dual;
+                "render_mode %d: supported are 0-5, 7-10, 12, 13, 14 and 12, 13, 14 | 0x100", gr->render_mode);
+  const bool mix = base_mode != NEST_MODE_BASELINE && !hsh && !dual && !surf;
+  if (surf) {
+    // surface potentials: F = 12 (mode 1) or 15 (mode 5) features per level,
+    // float32 (CR/forward.cu:1825-1908)
+    const uint32_t F = base_mode == NEST_MODE_SURFACE ? 12u : 15u, per = base_mode == NEST_MODE_SURFACE ? 4u : 7u;
+    if (gr->levels == 0 || gr->level_dim != F || gr->table_dtype != NEST_DTYPE_F32)
+      return fail(NEST_ERR_UNSUPPORTED, "render_mode %d needs float32 grid levels with level_dim %u", base_mode, F);
+    if (per * gr->levels > 64u)
+      return fail(NEST_ERR_UNSUPPORTED, "render_mode %d: at most 64 feature channels (got %u)", base_mode,
+                  per * gr->levels);
+    if ((uint32_t)channels < per * gr->levels)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "out_color has %d channels, render_mode %d produces %u", channels,
+                  base_mode, per * gr->levels);
+    if (base_mode == NEST_MODE_SURFACE && gr->table2) {
+      if (gr->offsets2[gr->levels] > gr->table2_rows)
+        return fail(NEST_ERR_INVALID_ARGUMENT, "second table has %lld rows, offsets2[%u] = %d",
+                    (long long)gr->table2_rows, gr->levels, gr->offsets2[gr->levels]);
+      if (!(gr->gridrange2[1] > gr->gridrange2[0]))
+        return fail(NEST_ERR_INVALID_ARGUMENT, "gridrange2 must satisfy min < max");
+    }
+    if (sp->P > 0) {
+      if (!sp->homotrans) return fail(NEST_ERR_INVALID_ARGUMENT, "homotrans is required in render_mode %d", base_mode);
+      if (!gr->rows2)
+        return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode %d needs rows2, a [P, levels * 4] float scratch", base_mode);
+    }
+  }
   if (dual) {
     // a second grid at the splat centres, 4 features per level in both
     // (CR/forward.cu:1146-1217)
@@ -284,12 +309,12 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
     g.F = F;
   }
   if (gr->levels > 0) {
-    if (!hsh && gr->level_dim != 1 && gr->level_dim != 2 && gr->level_dim != 4 && gr->level_dim != 8)
+    if (!hsh && !surf && gr->level_dim != 1 && gr->level_dim != 2 && gr->level_dim != 4 && gr->level_dim != 8)
       return fail(NEST_ERR_UNSUPPORTED, "level_dim must be 1, 2, 4 or 8 (got %u)", gr->level_dim);
-    if (gr->levels > NEST_MAX_LEVELS || gr->levels * gr->level_dim > NEST_MAX_CHANNELS)
+    if (gr->levels > NEST_MAX_LEVELS || (!surf && gr->levels * gr->level_dim > NEST_MAX_CHANNELS))
       return fail(NEST_ERR_UNSUPPORTED, "levels*level_dim must be <= %d (got %u*%u)", NEST_MAX_CHANNELS, gr->levels,
                   gr->level_dim);
-    if ((uint32_t)channels < gr->levels * gr->level_dim)
+    if (!surf && (uint32_t)channels < gr->levels * gr->level_dim)
       return fail(NEST_ERR_INVALID_ARGUMENT, "out_color has %d channels, the hash grid produces %u", channels,
                   gr->levels * gr->level_dim);
     if (gr->table_dtype != NEST_DTYPE_F32 && gr->table_dtype != NEST_DTYPE_F16)
@@ -534,8 +559,15 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   if ((rc = setup_grid(rs, gr, sp, out->channels, rp.grid))) return rc;
   const int base_mode = gr->render_mode & 0xFF;
   const bool dual = base_mode == NEST_MODE_BASELINE_DOUBLE || base_mode == NEST_MODE_BASELINE_BLEND_DOUBLE;
+  const bool surf = base_mode == NEST_MODE_SURFACE || base_mode == NEST_MODE_SURFACE_RGB;
   GridParams grid1 = rp.grid;  // mode 3 looks the first grid up after the render
-  if (dual) {
+  if (surf) {
+    // surface potentials: the grid's levels at each hit, the centre rows (the
+    // second grid's 4 features per level in mode 1, the grid's 3 colours per
+    // level in mode 5) in colors
+    rp.hsh = base_mode;
+    rp.cstride = (int)gr->levels * (base_mode == NEST_MODE_SURFACE ? 4 : 3);
+  } else if (dual) {
     // the centre features as per-splat rows ahead of the grid's levels (as in
     // mode 4); mode 2 then writes the grid's channels first, mode 3 blends the
     // rows alone
@@ -665,7 +697,7 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
   // feature_ptr of CR/rasterizer_impl.cu:399: precomputed colours, else the
   // colours preprocess evaluated from SH
   rp.colors = sh_colours(sp) ? reinterpret_cast<const float*>(g + go[NEST_GEOM_RGB]) : sp->colors_precomp;
-  if (dual) rp.colors = gr->rows2;
+  if (dual || surf) rp.colors = gr->rows2;
   rp.out_color = out->out_color;
   rp.out_others = out->out_others;
   rp.final_T = reinterpret_cast<float*>(im + io[NEST_IMG_FINAL_T]);
@@ -683,8 +715,13 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     rp.trans_avg = out->trans_avg;
   }
   tm.begin(NEST_STAGE_RENDER);
-  if (dual && sp->P > 0) {
-    // the second grid's features at the splat centres (CR/forward.cu:1164-1175)
+  if (base_mode == NEST_MODE_SURFACE_RGB && sp->P > 0) {
+    // the grid's colours at the splat centres (CR/forward.cu:1883-1885)
+    hipError_t e = launch_centre_rgb(grid1, sp->P, sp->homotrans, sp->ap_level, gr->rows2, s);
+    if (e != hipSuccess) return hip_fail(e, "centre colours");
+  }
+  if ((dual || base_mode == NEST_MODE_SURFACE) && sp->P > 0) {
+    // the second grid's features at the splat centres (CR/forward.cu:1164-1175, :1836-1849)
     hipError_t e = hipSuccess;
     if (gr->table2) {
       GridParams g2 = grid1;

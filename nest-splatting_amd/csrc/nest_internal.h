@@ -144,7 +144,8 @@ struct RenderParams {
                               // the row's in mode 7 (the grid zero past its levels)
   // Hybrid SH modes 8, 9, 10 (0 otherwise): a hit's channels come from its
   // colors row (3 or 48 floats) and one 3-channel grid level at the hit;
-  // hsh_dec 1 leaves the grid out, 2 the row's colour.
+  // hsh_dec 1 leaves the grid out, 2 the row's colour.  Surface-potential
+  // modes 1 and 5: the grid's levels at the hit and the centre rows in colors.
   int hsh;
   int hsh_dec;
   // Render mode 2: the accumulators hold [centre rows | grid]; output channel
@@ -194,6 +195,10 @@ hipError_t launch_render(const RenderParams& p, hipStream_t s);
 // rows [P, L * 4].
 hipError_t launch_centre_rows(const GridParams& g2, int P, const float* homotrans, const float* ap_level, float* rows,
                               hipStream_t s);
+// Render mode 5: the grid's (15 features per level, float32) features 12-14
+// of each level at every splat's centre, into rows [P, L * 3].
+hipError_t launch_centre_rgb(const GridParams& g, int P, const float* homotrans, const float* ap_level, float* rows,
+                             hipStream_t s);
 // Render mode 3 after the render: each pixel's out_color channels [0, L * 4)
 // plus the grid p.grid at its blended position (out_others 8-10) with the
 // appearance level of the tile's first splat (0 without hits or ap_level).

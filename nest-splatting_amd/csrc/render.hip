@@ -639,6 +639,60 @@ __device__ __forceinline__ void hsh_accumulate(const RenderParams& p, const floa
   }
 }
 
+// Surface potentials (render modes 1 and 5, CR/forward.cu:1825-1908): the
+// grid's levels at the hit, F = 12 (mode 1) or 15 (mode 5) features per
+// level of which the first 12 are four 3-vectors dotted with the splat's
+// normal n (fused multiply-adds from 0).  Mode 1 writes max(0, -dot + b) with
+// b the row's 4 features of the level (the second grid at the splat centre),
+// 4 channels per level; mode 5 max(0, -dot), then the row's 3 colours of the
+// level (the same grid's features 12-14 at the centre), 7 per level.  Levels
+// past min(ap, L), or all of them outside the grid, have zero features.
+template <int kHsh, int NACC>
+__device__ __forceinline__ void surface_accumulate(const RenderParams& p, const float xyz[3], uint32_t ap,
+                                                   const float4& nrm, const float* row, float w, float* acc) {
+  constexpr int F = kHsh == 1 ? 12 : 15, kPer = kHsh == 1 ? 4 : 7, kRow = kHsh == 1 ? 4 : 3;
+  const GridParams& g = p.grid;
+  float u[3];
+  bool oob;
+  grid_coord(g, xyz, u, oob);
+  const uint32_t maxl = oob ? 0u : (ap < g.L ? ap : g.L);
+  const float* t = static_cast<const float*>(g.table);
+  const float n[3] = {nrm.x, nrm.y, nrm.z};
+#pragma unroll
+  for (int l = 0; l < NACC / kPer; l++) {
+    if ((uint32_t)l >= g.L) continue;  // (continue, not break: the loop stays fully unrolled)
+    float fv[12];
+#pragma unroll
+    for (int f = 0; f < 12; f++) fv[f] = 0.0f;
+    if ((uint32_t)l < maxl) {
+      LevelCorners cn;
+      level_corners<F, false>(g.lv, l, g.pos_offset, g.interp, u, cn);
+      // corners_sum's order (w_k = ((1 * wx) * wy) * wz, fmaf per corner from
+      // 0), streamed corner by corner to keep the registers down
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const float wk = (1.0f * cn.wx[k & 1]) * cn.wy[(k >> 1) & 1] * cn.wz[k >> 2];
+        const float* e = t + ((size_t)g.lv.base[l] + cn.idx[k]) * F;
+#pragma unroll
+        for (int f = 0; f < 12; f++) fv[f] = fmaf(wk, e[f], fv[f]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 3; k++) dot = fmaf(fv[3 * i + k], n[k], dot);
+      const float v = kHsh == 1 ? fmaxf(0.0f, -dot + row[l * kRow + i]) : fmaxf(0.0f, -dot);
+      if (l * kPer + i < p.C) acc[l * kPer + i] = fmaf(v, w, acc[l * kPer + i]);
+    }
+    if constexpr (kHsh == 5) {
+#pragma unroll
+      for (int c = 0; c < 3; c++)
+        if (l * kPer + 4 + c < p.C) acc[l * kPer + 4 + c] = fmaf(row[l * kRow + c], w, acc[l * kPer + 4 + c]);
+    }
+  }
+}
+
 // LDS (32 KB of staged records + 17 KB of queue) allows three workgroups per
 // CU; amdgpu_waves_per_eu(3) gives the matching 168-VGPR budget, which holds
 // 64 accumulators and eight in-flight 16-byte corner loads.
@@ -649,8 +703,9 @@ __device__ __forceinline__ void hsh_accumulate(const RenderParams& p, const floa
 // the level count, 53 KB of LDS in all.
 // kKT: the splats' kernel comes from p.kernel_type (1-3 possible); without
 // it the kernel is the Gaussian, and the kernel-type branch compiles out.
-// kHsh: render modes 8, 9, 10 on the colour path's loop (no queue): each hit
-// looks its one grid level up in place.
+// kHsh: render modes 8, 9, 10 (one 3-channel grid level) and 1, 5 (surface
+// potentials) on the colour path's loop (no queue): each hit looks its grid
+// levels up in place.
 template <int F, int NACC, bool kHash, bool kHalf, bool kStructured = false, int kMix = 0, bool kKT = false,
           int kHsh = 0>
 __global__ void __launch_bounds__(kRenderThreads) __attribute__((amdgpu_waves_per_eu(3, 8)))
@@ -771,12 +826,17 @@ render_kernel(const RenderParams p) {
           pos_z += w * xyz[2];
           const uint32_t ap = __float_as_uint(q3.w);
           const uint32_t id = __float_as_uint(srec[6][j].w);
-          float h[3];
-          if (p.hsh_dec != 1)
-            hsh_query(g, xyz, ap, h);
-          else
-            h[0] = h[1] = h[2] = 0.0f;
-          hsh_accumulate<kHsh, NACC>(p, p.colors + (size_t)id * (uint32_t)p.cstride, h, w, acc);
+          const float* row = p.colors + (size_t)id * (uint32_t)p.cstride;
+          if constexpr (kHsh == 1 || kHsh == 5) {
+            surface_accumulate<kHsh, NACC>(p, xyz, ap, q3, row, w, acc);
+          } else {
+            float h[3];
+            if (p.hsh_dec != 1)
+              hsh_query(g, xyz, ap, h);
+            else
+              h[0] = h[1] = h[2] = 0.0f;
+            hsh_accumulate<kHsh, NACC>(p, row, h, w, acc);
+          }
           appearance_colour(ap, w, vis0, vis1);
         } else if constexpr (!kHash) {
           const uint32_t id = __float_as_uint(srec[6][j].w);
@@ -1054,6 +1114,51 @@ __global__ void __launch_bounds__(256) centre_rows_kernel(const GridParams g2, i
   grid_point_features<false, false>(g2, pk, ap, rows + (size_t)i * g2.L * 4u, 1, g2.L * 4u);
 }
 
+// Render mode 5 (CR/forward.cu:1883-1885, :1904-1906): the grid's features
+// 12-14 of each level (15 per level) at each splat's centre, into rows
+// [P, L * 3].
+__global__ void __launch_bounds__(256) centre_rgb_kernel(const GridParams g, int P, const float* __restrict__ homotrans,
+                                                         const float* __restrict__ ap_level, float* __restrict__ rows) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P) return;
+  const float* Hm = homotrans + 16 * (size_t)i;
+  const float pk[3] = {Hm[3], Hm[7], Hm[11]};
+  const uint32_t ap = ap_level ? f2u_sat(floorf(ap_level[i])) : 0xffffffffu;
+  float u[3];
+  bool oob;
+  grid_coord(g, pk, u, oob);
+  const uint32_t maxl = oob ? 0u : (ap < g.L ? ap : g.L);
+  const float* t = static_cast<const float*>(g.table);
+  float* out = rows + (size_t)i * g.L * 3u;
+  for (uint32_t l = 0; l < g.L; l++) {
+    float h[3] = {0.0f, 0.0f, 0.0f};
+    if (l < maxl) {
+      LevelCorners cn;
+      level_corners<15, false>(g.lv, (int)l, g.pos_offset, g.interp, u, cn);
+      float vals[8][3];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const float* e = t + ((size_t)g.lv.base[l] + cn.idx[k]) * 15u + 12u;
+        vals[k][0] = e[0];
+        vals[k][1] = e[1];
+        vals[k][2] = e[2];
+      }
+      corners_sum<3>(cn, vals, h);
+    }
+    out[3 * l + 0] = h[0];
+    out[3 * l + 1] = h[1];
+    out[3 * l + 2] = h[2];
+  }
+}
+
+hipError_t launch_centre_rgb(const GridParams& g, int P, const float* homotrans, const float* ap_level, float* rows,
+                             hipStream_t s) {
+  if (P <= 0) return hipSuccess;
+  hipLaunchKernelGGL(centre_rgb_kernel, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, s, g, P, homotrans, ap_level,
+                     rows);
+  return hipGetLastError();
+}
+
 hipError_t launch_centre_rows(const GridParams& g2, int P, const float* homotrans, const float* ap_level, float* rows,
                               hipStream_t s) {
   if (P <= 0) return hipSuccess;
@@ -1235,6 +1340,8 @@ static hipError_t launch_hash(const RenderParams& p, hipStream_t s) {
 
 template <bool kKT>
 static hipError_t launch_render_kind(const RenderParams& p, hipStream_t s) {
+  if (p.hsh == 1) return launch_one<1, 64, false, false, false, 0, kKT, 1>(p, s);
+  if (p.hsh == 5) return launch_one<1, 63, false, false, false, 0, kKT, 5>(p, s);
   if (p.hsh == 8) return launch_one<1, 3, false, false, false, 0, kKT, 8>(p, s);
   if (p.hsh == 9) return launch_one<1, 48, false, false, false, 0, kKT, 9>(p, s);
   if (p.hsh == 10) return launch_one<1, 3, false, false, false, 0, kKT, 10>(p, s);

@@ -104,10 +104,10 @@ class _RasterizeGaussians(torch.autograd.Function):
                 ap_level, features, offsets, gridrange, features_diffuse, offsets_diffuse, gridrange_diffuse,
                 raster_settings, hashgrid_settings, render_mode, shapes, kernel_type):
         base_mode = render_mode & 0xFF
-        if base_mode not in (0, 2, 3, 4, 7, 8, 9, 10, 12, 13, 14) or (render_mode & ~0x1FF) or \
+        if base_mode not in (0, 1, 2, 3, 4, 5, 7, 8, 9, 10, 12, 13, 14) or (render_mode & ~0x1FF) or \
                 ((render_mode & 0x100) and base_mode not in (12, 13, 14)):
-            raise NotImplementedError(f"render_mode {render_mode}: implemented are 0 (baseline), 2 / 3 "
-                                      f"(baseline_double / baseline_blend_double), 4 (cat), "
+            raise NotImplementedError(f"render_mode {render_mode}: implemented are 0 (baseline), 1 / 5 (surface "
+                                      f"potentials), 2 / 3 (baseline_double / baseline_blend_double), 4 (cat), "
                                       f"7 (adaptive_add), 8 / 9 / 10 (hybrid_SH / hybrid_SH_post / hybrid_SH_raw) and "
                                       f"12 / 13 / 14 (adaptive_cat / adaptive_cat_fast / adaptive_zero, | 0x100 "
                                       f"inference)")
@@ -118,20 +118,22 @@ class _RasterizeGaussians(torch.autograd.Function):
             raise ValueError(f"kernel_type {kernel_type} needs shapes [P] (CR/forward.cu:864-900)")
         if not _empty(cov3Ds_precomp):
             raise NotImplementedError("precomputed transforms (cov3D_precomp) are not implemented")
-        if not _empty(features_diffuse) and base_mode not in (2, 3):
-            raise NotImplementedError("a second (diffuse) hash grid is read by render modes 2 and 3 only")
+        if not _empty(features_diffuse) and base_mode not in (1, 2, 3, 5):
+            raise NotImplementedError("a second (diffuse) hash grid is read by render modes 1, 2 and 3 only")
         C = _channels(hashgrid_settings)
         level = int(hashgrid_settings.L)
-        if base_mode in (2, 3, 4, 7, 8, 9, 10, 12, 14) and level == 0:
+        second_grid = not (_empty(features_diffuse) or _empty(offsets_diffuse) or _empty(gridrange_diffuse))
+        if base_mode in (1, 2, 3, 4, 5, 7, 8, 9, 10, 12, 14) and level == 0:
             base_mode = render_mode = 0  # level 0 is the colour path in every mode but 13 (CR/forward.cu:1091)
-        if base_mode in (2, 3):
+        if base_mode in (1, 2, 3, 5):
             # baseline_double / baseline_blend_double (CR/forward.cu:1146-1217): the grid's
             # levels plus a second grid (features_diffuse, GR's diffuse grid) at the splat
-            # centres, 4 features per level in both
+            # centres, 4 features per level in both; surface potentials (1, 5,
+            # :1825-1908): 12 or 15 features per level, mode 1 with the second grid
+            second = base_mode in (1, 2, 3) and second_grid
             if _empty(features) or _empty(offsets) or _empty(gridrange):
                 raise ValueError(f"render_mode {base_mode} needs features, offsets and gridrange")
             hs = hashgrid_settings
-            second = not (_empty(features_diffuse) or _empty(offsets_diffuse) or _empty(gridrange_diffuse))
             grid = _rz.HashGridDesc(levels=level, level_dim=int(features.shape[1]), log2_scale=float(hs.S),
                                     base_resolution=int(hs.H), table=features.detach().contiguous(),
                                     offsets=_rz.host_array(offsets, np.int64),

@@ -27,7 +27,7 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 SCAN_NOALLOC_MAX = 268431360
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
  GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
@@ -62,8 +62,10 @@ class HashGrid(ct.Structure):
 
 
 MODE_BASELINE = 0
+MODE_SURFACE = 1
 MODE_BASELINE_DOUBLE = 2
 MODE_BASELINE_BLEND_DOUBLE = 3
+MODE_SURFACE_RGB = 5
 MODE_CAT = 4
 MODE_ADAPTIVE_ADD = 7
 MODE_HYBRID_SH = 8

@@ -61,7 +61,7 @@ class HashGridDesc:
     active_levels: Optional[int] = None
     # render_mode 8 / 9 / 10 (hybrid SH): 0 both parts, 1 gaussian_only, 2 ngp_only
     decompose: int = 0
-    # render_mode 2 / 3: the second grid (float32 [rows, 4] table, offsets, range)
+    # render_mode 1 / 2 / 3: the second grid (float32 [rows, 4] table, offsets, range)
     # queried at the splat centres; table2 None leaves its features 0
     table2: Optional[torch.Tensor] = None
     offsets2: Optional[np.ndarray] = None
@@ -69,7 +69,9 @@ class HashGridDesc:
     rows2: Optional[torch.Tensor] = None  # [P, levels * 4] scratch, set by rasterize_forward
 
     def dual(self) -> bool:
-        return (self.render_mode & 0xFF) in (L.MODE_BASELINE_DOUBLE, L.MODE_BASELINE_BLEND_DOUBLE)
+        """Render modes 1, 2, 3 and 5: features at the splat centres, in rows2."""
+        return (self.render_mode & 0xFF) in (L.MODE_SURFACE, L.MODE_BASELINE_DOUBLE, L.MODE_BASELINE_BLEND_DOUBLE,
+                                             L.MODE_SURFACE_RGB)
 
     def row_width(self, channels: int) -> int:
         """Floats per splat of colors_precomp for this render mode."""

@@ -701,8 +701,9 @@ typedef struct {
      * hybrid_SH_post / hybrid_SH_raw (level = decompose << 24 | SH degree
      * << 16 | grid levels << 8, rows of 3 / 48 / 3 floats, a one-level
      * 3-channel grid), 2 / 3 baseline_double / baseline_blend_double (level =
-     * the levels of both grids, F = 4, the second grid below).  Other values
-     * are not restated. */
+     * the levels of both grids, F = 4, the second grid below), 1 / 5 surface
+     * potentials (F = 12 with the second grid's 4 per level, or F = 15).
+     * Other values are not restated. */
     int render_mode;
     /* record_transmittance (forward.cu:1961-1964), NULL = off: [P] each;
      * every hit that reaches the end of the hit body (not mode 13's, which
@@ -946,6 +947,50 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
                         for (int i = 0; i < hl * F && fs + i < C; i++)
                             feat_scratch[fs + i] = infer ? hf[i] : fmaf(wt, gf[fs + i], (1.0f - wt) * hf[i]);
                     }
+                }
+            } else if ((A->render_mode & 0xFF) == 1 || (A->render_mode & 0xFF) == 5) {
+                /* surface potentials (forward.cu:1825-1872 mode 1, :1873-1908
+                 * mode 5): the grid's `level` levels at the hit, 12 (mode 1) or
+                 * 15 (mode 5) features per level, the first 12 four 3-vectors
+                 * dotted with the splat's normal (fused multiply-adds from 0).
+                 * Mode 1: max(0, -dot + b) per vector, b the second grid's 4
+                 * features per level at the splat centre (0 without it); 4
+                 * channels per level.  Mode 5: max(0, -dot), then the same
+                 * grid's features 12-14 at the splat centre; 7 per level. */
+                const int mode = A->render_mode & 0xFF, L = A->level, F = A->grid.F;
+                const int per = mode == 1 ? 4 : 7;
+                static const int kMaxF = 16 * 15;
+                float fv[16 * 15], fc[16 * 15];
+                or_grid G1 = A->grid;
+                G1.L = L;
+                or_query_feature(&G1, xyz, ap, kMaxF, fv);
+                const float *Hm = A->homotrans + 16 * (size_t)id;
+                const float pk[3] = {Hm[3], Hm[7], Hm[11]};
+                for (int i = 0; i < kMaxF; i++) fc[i] = 0.0f;
+                if (mode == 5) {
+                    or_query_feature(&G1, pk, ap, kMaxF, fc);
+                } else if (A->table2) {
+                    or_grid G2 = A->grid;
+                    G2.L = L;
+                    G2.F = 4;
+                    G2.offsets = A->offsets2;
+                    G2.table = A->table2;
+                    G2.half_table = 0;
+                    G2.vmin = A->vmin2;
+                    G2.vmax = A->vmax2;
+                    or_query_feature(&G2, pk, ap, kMaxF, fc);
+                }
+                for (int c = 0; c < C; c++) feat_scratch[c] = 0.0f;
+                for (int l = 0; l < L; l++) {
+                    for (int i = 0; i < 4; i++) {
+                        float dot = 0.0f;
+                        for (int k = 0; k < 3; k++) dot = fmaf(fv[l * F + 3 * i + k], no[k], dot);
+                        const float v = mode == 1 ? fmaxf(0.0f, -dot + fc[l * 4 + i]) : fmaxf(0.0f, -dot);
+                        if (l * per + i < C) feat_scratch[l * per + i] = v;
+                    }
+                    if (mode == 5)
+                        for (int c = 0; c < 3; c++)
+                            if (l * per + 4 + c < C) feat_scratch[l * per + 4 + c] = fc[l * F + 12 + c];
                 }
             } else if ((A->render_mode & 0xFF) == 2 || (A->render_mode & 0xFF) == 3) {
                 /* baseline_double (2, forward.cu:1146-1186): the grid's `level`

@@ -126,3 +126,51 @@ def test_dual_grid_through_drop_in(oracle):
         res = run_gpu(sc, table2, range2, ap, mode)
         np.testing.assert_array_equal(color.cpu().numpy(), res.color.cpu().numpy())
         np.testing.assert_array_equal(allmap.cpu().numpy(), res.others.cpu().numpy())
+
+
+SURF = {
+    # (base spec, overrides, mode): 12 features per level (mode 1, with and without the
+    # second grid) and 15 (mode 5), affine and contracted
+    "shell_m1": ("cfg2", dict(P=20_000, W=256, H=192, L=6, F=12, log2T=14), 1),
+    "unbounded_m1": ("cfg3", dict(P=40_000, W=256, H=160, L=16, F=12, log2T=13), 1),
+    "shell_m5": ("cfg2", dict(P=20_000, W=256, H=192, L=6, F=15, log2T=14), 5),
+    "unbounded_m5": ("cfg3", dict(P=40_000, W=256, H=160, L=9, F=15, log2T=13), 5),
+}
+
+
+@pytest.mark.parametrize("name", list(SURF))
+@pytest.mark.parametrize("second", [True, False])
+def test_surface_modes_parity(oracle, name, second):
+    """Render modes 1 and 5 (CR/forward.cu:1825-1908) bit for bit against the
+    oracle: the potentials dotted with the splat normal per hit, the centre
+    features (mode 1: the second grid; mode 5: the grid's colours)."""
+    from nest_splat import rasterizer as rz
+    base, kw, mode = SURF[name]
+    sc = make_scene(get_spec(base, name=f"surf_{name}", **kw))
+    sp = sc.spec
+    rng = np.random.default_rng(41)
+    table2 = rng.uniform(-0.1, 0.1, ((1 << sp.log2T) * sp.L, 4)).astype(np.float32)
+    range2 = np.float32([sp.gridrange[0] * 1.05, sp.gridrange[1] * 0.9])
+    ap = sc.ap_level.reshape(-1, 1).copy()
+    ap[::6] = 2.0
+    C = (4 if mode == 1 else 7) * sp.L
+    print(f"[case] surface mode {mode} {name} second={second}", flush=True)
+    cam = sc.cameras[0]
+    settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy,
+                                cam.world_view_transform, cam.full_proj_transform, cam.camera_center,
+                                if_contract=sp.contract)
+    grid = rz.HashGridDesc(sp.L, sp.F, sp.S, sp.base_res, _t(sc.table), sc.offsets,
+                           np.asarray(sp.gridrange, np.float32), render_mode=mode,
+                           table2=_t(table2) if second else None, offsets2=sc.offsets if second else None,
+                           gridrange2=range2 if second else None)
+    res = rz.rasterize_forward(settings, grid, _t(sc.means), _t(sc.opacity), _t(sc.scales), _t(sc.rotations),
+                               homotrans=_t(sc.homotrans), ap_level=_t(ap), channels=C)
+    torch.cuda.synchronize()
+    W, H = cam.image_width, cam.image_height
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    og = oracle.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    r = oracle.render(pre, b, W, H, C, og, homotrans=sc.homotrans, ap_level=ap, render_mode=mode, level=sp.L,
+                      grid2=(sc.offsets, table2, range2) if second else None)
+    _check(res, b, r)
