@@ -76,7 +76,8 @@ typedef struct nest_raster_settings {
 typedef struct nest_hashgrid {
   uint32_t struct_size;
   uint32_t levels;            /* L queried; 0 selects the colours_precomp path in mode 0 */
-  uint32_t level_dim;         /* F: 1, 2, 4 or 8 (3 in render modes 8-10) */
+  uint32_t level_dim;         /* F: 1, 2, 4 or 8 (3 in render modes 8-10, 12 in mode 1,
+                                 15 in mode 5) */
   float log2_scale;           /* S = log2(per_level_scale) */
   uint32_t base_resolution;   /* H */
   int32_t align_corners;
