@@ -174,3 +174,34 @@ def test_surface_modes_parity(oracle, name, second):
     r = oracle.render(pre, b, W, H, C, og, homotrans=sc.homotrans, ap_level=ap, render_mode=mode, level=sp.L,
                       grid2=(sc.offsets, table2, range2) if second else None)
     _check(res, b, r)
+
+
+@pytest.mark.parametrize("mode", [1, 2, 3, 5, 8, 9, 10])
+def test_new_modes_on_empty_and_culled_scenes(mode):
+    """No splats, and every splat behind the camera: nothing rendered, zeros
+    out, in each of the inline-lookup and centre-feature modes."""
+    from nest_splat import rasterizer as rz
+    F = {1: 12, 5: 15, 8: 3, 9: 3, 10: 3}.get(mode, 4)
+    L = 1 if mode in (8, 9, 10) else 3
+    sc = make_scene(get_spec("cfg1", L=L, F=F, log2T=10, name=f"empty_{mode}"))
+    sp = sc.spec
+    cam = sc.cameras[0]
+    settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy, cam.world_view_transform,
+                                cam.full_proj_transform)
+    grid = rz.HashGridDesc(L, F, sp.S, sp.base_res, _t(sc.table), sc.offsets, np.asarray(sp.gridrange, np.float32),
+                           render_mode=mode)
+    C = {1: 4 * L, 2: 8 * L, 3: 4 * L, 5: 7 * L, 8: 3, 9: 48, 10: 3}[mode]
+    width = {8: 3, 9: 48, 10: 3}.get(mode)
+    print(f"[case] empty scene, mode {mode}", flush=True)
+    z = lambda *s: torch.zeros(s, device=DEV)
+    res = rz.rasterize_forward(settings, grid, z(0, 3), z(0, 1), z(0, 2), z(0, 4), homotrans=z(0, 4, 4),
+                               ap_level=z(0, 1), colors_precomp=z(0, width) if width else None, channels=C)
+    torch.cuda.synchronize()
+    assert res.num_rendered == 0 and not res.color.any() and not res.others.any()
+    forward = np.asarray(cam.world_view_transform[:3, 2], np.float32)
+    behind = (sc.means - 1000.0 * forward[None, :]).astype(np.float32)
+    rows = torch.ones((sp.P, width), device=DEV) if width else None
+    res = rz.rasterize_forward(settings, grid, _t(behind), _t(sc.opacity), _t(sc.scales), _t(sc.rotations),
+                               homotrans=_t(sc.homotrans), ap_level=_t(sc.ap_level), colors_precomp=rows, channels=C)
+    torch.cuda.synchronize()
+    assert res.num_rendered == 0 and not res.color.any()
