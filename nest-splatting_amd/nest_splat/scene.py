@@ -65,10 +65,10 @@ class SceneSpec:
 GROWTH_16 = math.exp((math.log(2 ** 11) - math.log(2 ** 4)) / 15)  # min_logres 4, max_logres 11
 
 SPECS = {
-    # CPU-runnable plumbing scene
+    # CPU-runnable plumbing scene: 2000 splats in a cube, 128x128
     "cfg1": SceneSpec("cfg1", 20261, 2000, 128, 128, "cube", -3.0, 0.3, 0.0, 1.0,
                       8, 2, 14, 16, 1.5, (-1.5, 1.5), False, "f32", 64, "f32"),
-    # object-scale sphere shell
+    # object-scale sphere shell: 100k splats, 800x800
     "cfg2": SceneSpec("cfg2", 20262, 100_000, 800, 800, "shell", -4.5, 0.3, 1.0, 1.0,
                       16, 2, 19, 16, GROWTH_16, (-1.5, 1.5), False, "f32", 64, "f16",
                       bg=(1.0, 1.0, 1.0)),
@@ -78,11 +78,11 @@ SPECS = {
     "cfg3": SceneSpec("cfg3", 20263, 1_000_000, 1600, 1064, "ball_unbounded", -4.5, 0.3, 1.0, 1.0,
                       16, 4, 21, 16, GROWTH_16, (-1.0, 1.0), True, "f32", 64, "bf16",
                       cam_dist=2.6),
-    # RVQ-compressed attributes
+    # RVQ-compressed attributes: 500k splats, 800x800
     "cfg4": SceneSpec("cfg4", 20264, 500_000, 800, 800, "shell", -4.5, 0.3, 1.0, 1.0,
                       16, 2, 19, 16, GROWTH_16, (-1.5, 1.5), False, "f32", 64, "f16",
                       bg=(1.0, 1.0, 1.0), rvq=True),
-    # stress scene, 8 orbit cameras
+    # stress scene: 4M splats in 5 shells, 8 orbit cameras at 1920x1080
     "cfg5": SceneSpec("cfg5", 20265, 4_000_000, 1920, 1080, "shells", -4.5, 0.3, -3.0, 1.0,
                       16, 4, 22, 16, GROWTH_16, (-3.0, 3.0), False, "f16", 128, "bf16",
                       cam_dist=4.5, n_cams=8),

@@ -1,7 +1,7 @@
 /*
  * nest_oracle.c -- CPU oracle for the forward render hot path.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP library in
+ * TEST INFRASTRUCTURE ONLY.  This file is the oracle that the HIP library in
  * nest-splatting_amd/csrc is compared against.  Only tests/, the smoke entry
  * point and the bench's cpu_baseline leg load it.  Nothing in the product path
  * may link, import or call it.
