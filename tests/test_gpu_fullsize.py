@@ -273,3 +273,77 @@ def test_stress_scene_4m(oracle, cam_index):
                       row_phase=phase)
     n = _check_rows(sc, cam_index, res, rgb, r, rows, oracle)
     _log(f"cfg5 cam {cam_index} ok, {n} pixels compared bit for bit")
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("case", ["adaptive_cat_training", "general_kernel", "hybrid_sh"])
+def test_benchmark_scene_1m_other_modes(oracle, case):
+    """The 1M-splat frame in other configurations, bit for bit on every 16th
+    tile row: render mode 12 in training with the first 10 levels as per-splat
+    rows (weights in [0.15, 1)) and the last 6 as the grid, as bench.py
+    --modes builds it; the general kernel (kernel_type 3, exponents 2-8); and
+    render mode 8 over a one-level 3-channel grid at resolution 2048."""
+    from nest_splat.scene import get_spec, make_scene
+    from nest_splat import rasterizer as rz
+    sc = make_scene(get_spec("cfg3"))
+    sp = sc.spec
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    settings = rz.make_settings(cam.image_height, cam.image_width, cam.tanfovx, cam.tanfovy, cam.world_view_transform,
+                                cam.full_proj_transform, cam.camera_center, if_contract=sp.contract)
+    rng = np.random.default_rng(1)
+    kw, okw = {}, {}
+    if case == "adaptive_cat_training":
+        hyb, F, Lt = 10, sp.F, sp.L
+        offs = np.asarray(sc.offsets, np.int64)
+        sub_offsets = offs[hyb:] - offs[hyb]
+        sub_table = np.ascontiguousarray(sc.table[int(offs[hyb]):int(offs[Lt])])
+        sub_base = int(round(2.0 ** (hyb * sp.S) * sp.base_res))
+        rows = (rng.standard_normal((sp.P, Lt * F + 1)) * 0.1).astype(np.float32)
+        rows[:, Lt * F] = rng.uniform(0.15, 1.0, sp.P).astype(np.float32)
+        C = Lt * F
+        grid = rz.HashGridDesc(Lt - hyb, F, sp.S, sub_base, t(sub_table), sub_offsets,
+                               np.asarray(sp.gridrange, np.float32), render_mode=12, hybrid_levels=hyb,
+                               total_levels=Lt)
+        kw = dict(colors_precomp=t(rows))
+        og = oracle.make_grid(Lt - hyb, F, sp.S, sub_base, sub_offsets, sub_table, sp.gridrange, sp.contract)
+        okw = dict(colors=rows, render_mode=12, level=(Lt << 16) | ((Lt - hyb) << 8) | hyb)
+    elif case == "general_kernel":
+        C = sp.C
+        shapes = rng.uniform(2.0, 8.0, sp.P).astype(np.float32)
+        grid = rz.HashGridDesc(sp.L, sp.F, sp.S, sp.base_res, t(sc.table), sc.offsets,
+                               np.asarray(sp.gridrange, np.float32))
+        kw = dict(shapes=t(shapes), kernel_type=3)
+        og = oracle.make_grid(sp.L, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+        okw = dict(shapes=shapes, kernel_type=3)
+    else:
+        C = 3
+        table = rng.uniform(-0.5, 0.5, (1 << 21, 3)).astype(np.float32)
+        hoffs = np.array([0, 1 << 21], np.int64)
+        rows = rng.standard_normal((sp.P, 3)).astype(np.float32)
+        grid = rz.HashGridDesc(1, 3, 0.0, 2048, t(table), hoffs, np.asarray(sp.gridrange, np.float32), render_mode=8)
+        kw = dict(colors_precomp=t(rows))
+        og = oracle.make_grid(1, 3, 0.0, 2048, hoffs, table, sp.gridrange, sp.contract)
+        okw = dict(colors=rows, render_mode=8, level=(0 << 24) | (3 << 16) | (1 << 8))
+    _log(f"cfg3 {case}: GPU frame")
+    res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
+                               homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), channels=C, **kw)
+    torch.cuda.synchronize()
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    assert res.num_rendered == b["num_rendered"]
+    stride, phase = 16, 7
+    _log(f"cfg3 {case}: oracle render, every {stride}th tile row")
+    r = oracle.render(pre, b, W, H, C, og, homotrans=sc.homotrans, ap_level=sc.ap_level, row_stride=stride,
+                      row_phase=phase, **okw)
+    pix = np.zeros((H, W), bool)
+    for ty in _sampled_rows(H, stride, phase):
+        pix[ty * 16:(ty + 1) * 16] = True
+    ba = rz.binning_arrays(res, W, H)
+    np.testing.assert_array_equal(res.color.cpu().numpy()[:, pix], r["color"][:, pix])
+    np.testing.assert_array_equal(res.others.cpu().numpy()[:, pix], r["others"][:, pix])
+    np.testing.assert_array_equal(ba["n_contrib"].cpu().numpy().view(np.uint32)[:, pix], r["n_contrib"][:, pix])
+    assert np.abs(r["color"][:, pix]).max() > 0
+    _log(f"cfg3 {case} ok, {int(pix.sum())} pixels compared bit for bit")
