@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 15
+#define NEST_ABI_VERSION 16
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -244,7 +244,8 @@ typedef struct nest_frame_outputs {
 #define NEST_STAGE_SORT 3
 #define NEST_STAGE_RANGES 4
 #define NEST_STAGE_RENDER 5
-#define NEST_STAGE_COUNT 6
+#define NEST_STAGE_DEPTH_ORDER 6   /* the splats' depth order, queued by nest_forward_geometry */
+#define NEST_STAGE_COUNT 7
 typedef struct nest_timing {
   uint32_t struct_size;
   int32_t enabled;
@@ -329,7 +330,11 @@ int nest_hashgrid_levels(const nest_hashgrid *grid, float *scale, uint32_t *reso
  *
  * nest_forward_geometry: preprocessCUDA (CR/forward.cu:323-441) plus the
  * inclusive scan of tiles touched (CR/rasterizer_impl.cu:355); writes radii
- * and the total number of tile/splat pairs (after a stream sync). */
+ * and the total number of tile/splat pairs (waiting for that read-back only).
+ * It also queues the splats' depth order, which does not depend on the pair
+ * count, behind the read-back, so the GPU runs it while the caller sizes the
+ * binning workspace; nest_forward_render reads it from the geometry
+ * workspace. */
 int nest_forward_geometry(const nest_raster_settings *settings, const nest_splats *splats,
                           void *geom_ws, size_t geom_bytes, int32_t *radii,
                           int64_t *num_rendered, nest_timing *timing, void *stream);

@@ -518,7 +518,25 @@ int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp,
   uint64_t total = 0;
   hipError_t e = hipMemcpyAsync(&total, static_cast<uint64_t*>(scan_ws) + nb, sizeof(total), hipMemcpyDeviceToHost, s);
   if (e != hipSuccess) return hip_fail(e, "num_rendered read-back");
-  e = hipStreamSynchronize(s);
+  hipEvent_t copied = nullptr;
+  e = hipEventCreateWithFlags(&copied, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(copied, s);
+  if (e != hipSuccess) {
+    if (copied) hipEventDestroy(copied);
+    return hip_fail(e, "num_rendered read-back");
+  }
+  // the splats' depth order (it does not depend on the pair count) runs while
+  // the host waits for the count and then sizes the binning workspace
+  tm.begin(NEST_STAGE_DEPTH_ORDER);
+  rc = check_stage(launch_depth_order(sp->P, p.depth, p.radii, p.tiles,
+                                      reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_DEPTH_ORDER]),
+                                      reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_ORDER_OFFSETS]),
+                                      g + off[NEST_GEOM_ORDER_TMP], s),
+                   "depth order", rs->debug, s);
+  tm.end();
+  e = hipEventSynchronize(copied);
+  hipEventDestroy(copied);
+  if (rc) return rc;
   if (e != hipSuccess) return hip_fail(e, "num_rendered read-back");
   if (total > 0xffffffffull)
     return fail(NEST_ERR_OVERFLOW, "%llu tile/splat pairs exceed the 32-bit offsets of the binning stage",
@@ -665,14 +683,10 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     vals = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_VALS]);
     const float* depth = reinterpret_cast<const float*>(g + go[NEST_GEOM_DEPTH]);
     const int32_t* gradii = reinterpret_cast<const int32_t*>(g + go[NEST_GEOM_RADII]);
-    uint32_t* order = reinterpret_cast<uint32_t*>(g + go[NEST_GEOM_DEPTH_ORDER]);
-    uint32_t* order_offsets = reinterpret_cast<uint32_t*>(g + go[NEST_GEOM_ORDER_OFFSETS]);
-    // duplicate stage: depth order of the splats, then their pairs in that order
+    const uint32_t* order = reinterpret_cast<const uint32_t*>(g + go[NEST_GEOM_DEPTH_ORDER]);
+    const uint32_t* order_offsets = reinterpret_cast<const uint32_t*>(g + go[NEST_GEOM_ORDER_OFFSETS]);
+    // duplicate stage: the pairs of the splats in the depth order nest_forward_geometry queued
     tm.begin(NEST_STAGE_DUPLICATE);
-    rc = check_stage(launch_depth_order(sp->P, depth, gradii, reinterpret_cast<const uint32_t*>(g + go[NEST_GEOM_TILES]),
-                                        order, order_offsets, g + go[NEST_GEOM_ORDER_TMP], s),
-                     "depth order", rs->debug, s);
-    if (rc) return rc;
     rc = check_stage(launch_duplicate_ordered(sp->P, order, order_offsets, reinterpret_cast<const float*>(g + go[NEST_GEOM_XY]),
                                               gradii, gx, gy, NR, pair_tiles, pair_ids, s),
                      "duplicate", rs->debug, s);

@@ -27,7 +27,7 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-ABI_VERSION = 15
+ABI_VERSION = 16
 SCAN_NOALLOC_MAX = 268431360
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
  GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
@@ -38,7 +38,7 @@ IMG_RANGES, IMG_FINAL_T, IMG_N_CONTRIB, IMG_LEVELS, IMG_TILE_ORDER = range(5)
 IMG_FIELDS = 5
 BWD_DTRANSMAT, BWD_DHOMO, BWD_DNORMAL, BWD_DCOLORS, BWD_GRADSUM = range(5)
 BWD_FIELDS = 5
-STAGES = ("preprocess", "scan", "duplicate", "sort", "ranges", "render")
+STAGES = ("preprocess", "scan", "duplicate", "sort", "ranges", "render", "depth_order")
 
 
 class RasterSettings(ct.Structure):
@@ -100,8 +100,8 @@ class BackwardIO(ct.Structure):
 
 
 class Timing(ct.Structure):
-    _fields_ = [("struct_size", ct.c_uint32), ("enabled", ct.c_int32), ("ms", ct.c_float * 6),
-                ("events", ct.c_void_p * 12), ("recorded", ct.c_uint32)]
+    _fields_ = [("struct_size", ct.c_uint32), ("enabled", ct.c_int32), ("ms", ct.c_float * 7),
+                ("events", ct.c_void_p * 14), ("recorded", ct.c_uint32)]
 
 
 def new_timing(enabled: bool = True) -> Timing:
