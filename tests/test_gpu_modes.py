@@ -496,19 +496,32 @@ def test_drop_in_cat_modes_autograd(oracle):
         color13.sum().backward()
 
 
-# (render mode, scene, total levels, per-splat levels, grid levels)
-AC_BWD_CASES = [(12, "cfg1", 8, 3, 5), (12, "shell_small", 12, 4, 8), (12, "unbounded_small", 16, 10, 6),
-                (12, "cfg1", 6, 2, 0), (14, "cfg1", 8, 3, 5), (14, "shell_small", 13, 4, 8),
-                (14, "unbounded_small", 16, 10, 6), (7, "cfg1", 8, 0, 5), (7, "unbounded_small", 16, 0, 6)]
+# (render mode, scene, total levels, per-splat levels, grid levels, kernel type)
+AC_BWD_CASES = [(12, "cfg1", 8, 3, 5, 0), (12, "shell_small", 12, 4, 8, 0), (12, "unbounded_small", 16, 10, 6, 0),
+                (12, "cfg1", 6, 2, 0, 0), (14, "cfg1", 8, 3, 5, 0), (14, "shell_small", 13, 4, 8, 0),
+                (14, "unbounded_small", 16, 10, 6, 0), (7, "cfg1", 8, 0, 5, 0), (7, "unbounded_small", 16, 0, 6, 0),
+                (12, "shell_small", 12, 4, 8, 1), (14, "cfg1", 8, 3, 5, 3), (7, "cfg1", 8, 0, 5, 2)]
 
 
-@pytest.mark.parametrize("mode,name,total,hyb,gl", AC_BWD_CASES)
-def test_adaptive_cat_backward_parity(oracle, mode, name, total, hyb, gl):
+def _kt_shapes(kt, P, seed):
+    rng = np.random.default_rng(seed)
+    if kt == 1:
+        return rng.uniform(0.2, 4.0, P).astype(np.float32)
+    if kt == 2:
+        v = rng.uniform(0.0, 2.0, P).astype(np.float32)
+        v[::7] = 0.0
+        return v
+    return rng.uniform(2.0, 8.0, P).astype(np.float32)
+
+
+@pytest.mark.parametrize("mode,name,total,hyb,gl,kt", AC_BWD_CASES)
+def test_adaptive_cat_backward_parity(oracle, mode, name, total, hyb, gl, kt):
     """nest_backward in render modes 7 (adaptive_add), 12 (adaptive_cat) and
     14 (adaptive_zero), training, against the backward oracle, which the CPU tests pin against
     float64 autograd: gradients of the rows and their blend weights, the
     table and the geometry, within 2e-5 of each array's largest entry.  Mode
-    14 rows include weight-0 splats, whose grid levels are skipped."""
+    14 rows include weight-0 splats, whose grid levels are skipped.  Some
+    cases use kernel types 1-3, with dL/dshape."""
     from nest_splat import rasterizer as rz
     sc = scene(name)
     sp = sc.spec
@@ -529,6 +542,10 @@ def test_adaptive_cat_backward_parity(oracle, mode, name, total, hyb, gl):
     grid = rz.HashGridDesc(gl, F, sp.S, sp.base_res, t(sc.table), sc.offsets, np.asarray(sp.gridrange, np.float32),
                            render_mode=mode, hybrid_levels=hyb, total_levels=total)
     kw = dict(homotrans=t(sc.homotrans), ap_level=t(ap), colors_precomp=t(rows), channels=tdim)
+    shapes = None
+    if kt:
+        shapes = _kt_shapes(kt, sp.P, 60 + kt)
+        kw.update(shapes=t(shapes), kernel_type=kt)
     res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations), **kw)
     rng = np.random.default_rng(31)
     dcol = rng.standard_normal((tdim, H, W)).astype(np.float32)
@@ -544,16 +561,19 @@ def test_adaptive_cat_backward_parity(oracle, mode, name, total, hyb, gl):
     b = oracle.binning(pre, W, H)
     g = oracle.make_grid(max(gl, 1), F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
     fwd = oracle.render(pre, b, W, H, tdim, g, homotrans=sc.homotrans, ap_level=ap, colors=rows, render_mode=mode,
-                        level=level)
+                        level=level, kernel_type=kt, shapes=shapes)
     np.testing.assert_array_equal(res.color.cpu().numpy(), fwd["color"])  # same forward state
     ob = oracle.render_backward(pre, b, fwd, W, H, tdim, g, dcol, doth, homotrans=sc.homotrans.reshape(-1, 16),
-                                ap_level=ap, colors=rows, render_mode=mode, level=level)
+                                ap_level=ap, colors=rows, render_mode=mode, level=level, kernel_type=kt,
+                                shapes=shapes)
     pb = oracle.preprocess_backward(sc.means, sc.scales, sc.rotations, pre["radii"], pre["transmat"],
                                     cam.world_view_transform, cam.full_proj_transform, W, H, ob["dtransmat"],
                                     ob["dhomo"], ob["dnormal"], ob["dmean2D"])
     ref = dict(dmeans3D=pb["dmeans"], dmeans2D=pb["dmean2D"], dopacity=ob["dopacity"][:, None],
                dscales=pb["dscales"], drotations=pb["drots"], drows=ob["dcolors"][:, :nw],
                dweight=ob["dcolors"][:, nw], dgradsum=ob["gradsum"][:, None])
+    if kt:
+        ref["dshapes"] = ob["dshapes"]
     gpu["drows"], gpu["dweight"] = gpu["dcolors"][:, :nw], gpu["dcolors"][:, nw]
     if gl > 0:
         ref["dfeatures"] = ob["dtable"].reshape(gpu["dfeatures"].shape)
