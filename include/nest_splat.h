@@ -107,6 +107,10 @@ typedef struct nest_hashgrid {
    *     weight * row + (1 - weight) * grid, the grid's `levels` levels then
    *     zero (hybrid_levels must be 0; CR/forward.cu:1326-1376); the
    *     backward writes the weight's gradient times weight * (1 - weight);
+   *   NEST_MODE_ADAPTIVE (6): colors_precomp rows of out_color's channel
+   *     count; the first levels*level_dim channels are 0.5 * row + 0.5 * grid
+   *     at the hit, the rest 0 (CR/forward.cu:1283-1325); forward only (the
+   *     reference's backward reads another row layout, CR/backward.cu:1041);
    *   NEST_MODE_ADAPTIVE_CAT (12), | NEST_MODE_INFERENCE for inference: the
    *     same rows and levels; the first hybrid_levels*level_dim channels take
    *     the row unweighted, the grid levels are blended with the row in
@@ -177,6 +181,7 @@ typedef struct nest_hashgrid {
 #define NEST_MODE_BASELINE_DOUBLE 2
 #define NEST_MODE_BASELINE_BLEND_DOUBLE 3
 #define NEST_MODE_SURFACE_RGB 5
+#define NEST_MODE_ADAPTIVE 6
 #define NEST_MODE_CAT 4
 #define NEST_MODE_ADAPTIVE_ADD 7
 #define NEST_MODE_HYBRID_SH 8

@@ -199,10 +199,10 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
   const bool surf = base_mode == NEST_MODE_SURFACE || base_mode == NEST_MODE_SURFACE_RGB;
   if ((gr->render_mode & ~0x1FF) != 0 ||
       (base_mode != NEST_MODE_BASELINE && base_mode != NEST_MODE_CAT && base_mode != NEST_MODE_ADAPTIVE_ADD &&
-       !adaptive && !hsh && !dual && !surf) ||
+       base_mode != NEST_MODE_ADAPTIVE && !adaptive && !hsh && !dual && !surf) ||
       ((gr->render_mode & NEST_MODE_INFERENCE) && !adaptive))
     return fail(NEST_ERR_UNSUPPORTED,
-                "render_mode %d: supported are 0-5, 7-10, 12, 13, 14 and 12, 13, 14 | 0x100", gr->render_mode);
+                "render_mode %d: supported are 0-10, 12, 13, 14 and 12, 13, 14 | 0x100", gr->render_mode);
   const bool mix = base_mode != NEST_MODE_BASELINE && !hsh && !dual && !surf;
   if (surf) {
     // surface potentials: F = 12 (mode 1) or 15 (mode 5) features per level,
@@ -284,8 +284,12 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
     uint32_t feat = 0;
     if (base_mode == NEST_MODE_ADAPTIVE_ADD && hyb != 0)
       return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode 7 has no per-splat coarse levels (hybrid_levels must be 0)");
+    if (base_mode == NEST_MODE_ADAPTIVE && hyb != 0)
+      return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode 6 has no per-splat coarse levels (hybrid_levels must be 0)");
     if (base_mode == NEST_MODE_CAT) {
       feat = (hyb + gr->levels) * F;
+    } else if (base_mode == NEST_MODE_ADAPTIVE) {
+      feat = gr->levels * F;
     } else {
       if (hyb + gr->levels > gr->total_levels)
         return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode %d: hybrid_levels + levels (%u + %u) exceed total_levels %u",
@@ -299,7 +303,8 @@ int setup_grid(const nest_raster_settings* rs, const nest_hashgrid* gr, const ne
                   gr->render_mode, feat);
     if (sp->P > 0) {
       if (!sp->homotrans) return fail(NEST_ERR_INVALID_ARGUMENT, "homotrans is required in render_mode %d", gr->render_mode);
-      if (!sp->colors_precomp && (adaptive || base_mode == NEST_MODE_ADAPTIVE_ADD || hyb > 0))
+      if (!sp->colors_precomp &&
+          (adaptive || base_mode == NEST_MODE_ADAPTIVE_ADD || base_mode == NEST_MODE_ADAPTIVE || hyb > 0))
         return fail(NEST_ERR_INVALID_ARGUMENT, "render_mode %d needs the per-splat features in colors_precomp",
                     gr->render_mode);
       // the render queue packs the splat id into 25 bits
@@ -620,6 +625,15 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     if ((gr->render_mode & 0xFF) == NEST_MODE_CAT) {
       rp.cstride = rp.pgd;
       rp.nrow = rp.pgd;
+    } else if ((gr->render_mode & 0xFF) == NEST_MODE_ADAPTIVE) {
+      // mode 6 (CR/forward.cu:1283-1325): rows of C floats, the first levels*F
+      // channels 0.5 * row + 0.5 * grid; mode 7's blend with a fixed weight
+      rp.cstride = out->channels;
+      rp.nrow = 0;
+      rp.wfix = 0.5f;
+      rp.blend = 1;
+      rp.nfast = gr->levels;
+      rp.nblend = gr->levels;
     } else if ((gr->render_mode & 0xFF) == NEST_MODE_ADAPTIVE_ADD) {
       // mode 7 (CR/forward.cu:1326-1376): rows [total*F | weight], every level
       // weight * row + (1 - weight) * grid, the grid zero past its levels

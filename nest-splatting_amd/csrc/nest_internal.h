@@ -130,6 +130,7 @@ struct RenderParams {
   int cstride;                // floats per row of colors
   int nrow;                   // leading floats of a row the render reads as features (<= 64)
   int wslot;                  // index of the blend weight in a row (modes 12, 13), else -1
+  float wfix;                 // the blend weight without a weight slot (mode 6: 0.5)
   int infer;                  // inference: a fast hit (weight > 0.5 in mode 13, >= 0.9 in
                               // mode 12) takes the row without the grid
   int blend;                  // training: grid levels take row * weight + grid * (1 - weight)

@@ -291,7 +291,7 @@ __device__ __forceinline__ void drain_compact_mix(const RenderParams& p, nest_i3
     nhash = meta & 63u;
     fast = (meta & 64u) != 0u;
     row = p.colors + (size_t)(meta >> 7) * (uint32_t)p.cstride;
-    if (p.wslot >= 0) wt = row[p.wslot];
+    wt = p.wslot >= 0 ? row[p.wslot] : p.wfix;
     row += p.pgd;
     nfeat = fast ? p.nfast : (p.blend ? p.nblend : nhash);
   }
@@ -391,7 +391,7 @@ __device__ __forceinline__ void drain_mixed(const RenderParams& p, nest_i32x4 rs
     const uint32_t nhash = meta & 63u;
     const bool fast = (meta & 64u) != 0u;
     const float* row = p.colors + (size_t)(meta >> 7) * (uint32_t)p.cstride;
-    const float wt = p.wslot >= 0 ? row[p.wslot] : 0.0f;
+    const float wt = p.wslot >= 0 ? row[p.wslot] : p.wfix;
     const uint32_t nfeat = fast ? p.nfast : (p.blend ? p.nblend : nhash);
     row += p.pgd;
     const float u[3] = {e.x, e.y, e.z};

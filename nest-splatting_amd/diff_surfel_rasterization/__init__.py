@@ -8,24 +8,29 @@ GaussianRasterizer(raster_settings, hashgrid_settings).forward(...) returning
 (color [C,H,W], radii [P], allmap [14,H,W], trans_avg, cover) (:172, :321-396),
 markVisible (:310-319) and rasterize_gaussians (:21-66).
 
-Scope: render mode 0 ("baseline") with the Gaussian kernel, forward and
-backward: hash-grid features when HashGridSettings.L > 0; when L == 0,
-precomputed per-splat colours or RGB evaluated from SH coefficients
-(degree <= 3) in preprocess.  Render modes 4 ("cat": per-splat features
-of the coarse levels ahead of a grid of the fine ones), 12 ("adaptive_cat",
-blended with the grid by a per-splat weight) and 14 ("adaptive_zero", the
-grid scaled by the weight) and 7 ("adaptive_add", every level blended)
-forward and backward, 12 | 0x100, 14 | 0x100 and
-13 ("adaptive_cat_fast") with or without the inference flag 0x100 forward,
-with
-the reference's packed L (total << 16 | grid levels << 8 | per-splat
-levels; the backward differentiates the grid levels within the active
-count, CR/backward.cu:576-612).  The backward returns the reference's gradients
-(DSRpy:174-275): means3D, the means2D densification statistic, SH,
-colours, opacities, scales, rotations, the hash table, and the |grad| sum in
-the ap_level slot; it needs a float32 hash table and at most 64 channels.
-Modes, kernels and options that the reference implements for other methods
-raise NotImplementedError instead of returning zeros.
+Scope: render mode 0 ("baseline") with every kernel_type (0 Gaussian, 1 beta,
+2 flex, 3 general), forward and backward: hash-grid features when
+HashGridSettings.L > 0; when L == 0, precomputed per-splat colours or RGB
+evaluated from SH coefficients (degree <= 3) in preprocess.  Render modes 4
+("cat": per-splat features of the coarse levels ahead of a grid of the fine
+ones), 12 ("adaptive_cat", blended with the grid by a per-splat weight), 14
+("adaptive_zero", the grid scaled by the weight) and 7 ("adaptive_add", every
+level blended), forward and backward, with the reference's packed L
+(total << 16 | grid levels << 8 | per-splat levels; the backward
+differentiates the grid levels within the active count,
+CR/backward.cu:576-612).  Forward only (inference flags, or no consistent
+backward in the reference): 12 | 0x100, 14 | 0x100 and 13
+("adaptive_cat_fast", with or without the inference flag 0x100); 6
+("adaptive", half row and half grid); 8, 9 and 10 ("hybrid_SH*", one
+3-channel grid level with per-splat SH colours); 2 and 3 ("baseline_double",
+"baseline_blend_double", a second grid at the splat centres from
+features_diffuse); 1 and 5 (surface potentials).  The backward returns the
+reference's gradients (DSRpy:174-275): means3D, the means2D densification
+statistic, SH, colours, opacities, scales, rotations, the hash table, shapes,
+and the |grad| sum in the ap_level slot; it needs a float32 hash table and at
+most 64 channels.  Modes, kernels and options that the reference implements
+for other methods (render mode 11, precomputed covariances) raise
+NotImplementedError instead of returning zeros.
 """
 from __future__ import annotations
 
@@ -78,7 +83,8 @@ def _cat_hash_levels(offsets17: np.ndarray) -> int:
 def _mixed_grid(hs, render_mode, level, features, offsets, gridrange):
     """HashGridDesc of render modes 4, 7, 12, 13 and 14 from the reference's packed
     level argument: (total << 16) | (grid levels << 8) | per-splat levels
-    (GR:224-226, :395-396; CR/forward.cu:744-767, :971-973, :1228)."""
+    (GR:224-226, :395-396; CR/forward.cu:744-767, :971-973, :1228); mode 6
+    takes the level argument as the grid's level count (CR/forward.cu:1292)."""
     base_mode = render_mode & 0xFF
     if _empty(features) or _empty(offsets) or _empty(gridrange):
         raise ValueError(f"render_mode {render_mode} needs features, offsets and gridrange")
@@ -88,6 +94,10 @@ def _mixed_grid(hs, render_mode, level, features, offsets, gridrange):
     hyb = level & 0xFF
     if base_mode == 4:
         levels, total = _cat_hash_levels(offs), 0
+    elif base_mode == 6:
+        if not 0 < level <= 16:
+            raise NotImplementedError(f"render_mode 6 looks up 1 to 16 grid levels (got {level})")
+        levels, total, hyb = level, level, 0
     else:
         levels, total = (level >> 8) & 0xFF, (level >> 16) & 0xFF
     table = features.detach().contiguous() if levels > 0 else None
@@ -95,7 +105,7 @@ def _mixed_grid(hs, render_mode, level, features, offsets, gridrange):
                             base_resolution=int(hs.H), table=table, offsets=offs,
                             gridrange=_rz.host_array(gridrange, np.float32), align_corners=bool(hs.align_corners),
                             interpolation=int(hs.interpolation), render_mode=int(render_mode), hybrid_levels=hyb,
-                            total_levels=total, active_levels=(level >> 8) & 0xFF)
+                            total_levels=total, active_levels=levels if base_mode == 6 else (level >> 8) & 0xFF)
 
 
 class _RasterizeGaussians(torch.autograd.Function):
@@ -104,11 +114,11 @@ class _RasterizeGaussians(torch.autograd.Function):
                 ap_level, features, offsets, gridrange, features_diffuse, offsets_diffuse, gridrange_diffuse,
                 raster_settings, hashgrid_settings, render_mode, shapes, kernel_type):
         base_mode = render_mode & 0xFF
-        if base_mode not in (0, 1, 2, 3, 4, 5, 7, 8, 9, 10, 12, 13, 14) or (render_mode & ~0x1FF) or \
+        if base_mode not in (0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 12, 13, 14) or (render_mode & ~0x1FF) or \
                 ((render_mode & 0x100) and base_mode not in (12, 13, 14)):
             raise NotImplementedError(f"render_mode {render_mode}: implemented are 0 (baseline), 1 / 5 (surface "
                                       f"potentials), 2 / 3 (baseline_double / baseline_blend_double), 4 (cat), "
-                                      f"7 (adaptive_add), 8 / 9 / 10 (hybrid_SH / hybrid_SH_post / hybrid_SH_raw) and "
+                                      f"6 (adaptive), 7 (adaptive_add), 8 / 9 / 10 (hybrid_SH / hybrid_SH_post / hybrid_SH_raw) and "
                                       f"12 / 13 / 14 (adaptive_cat / adaptive_cat_fast / adaptive_zero, | 0x100 "
                                       f"inference)")
         if kernel_type not in (0, 1, 2, 3):
@@ -123,7 +133,7 @@ class _RasterizeGaussians(torch.autograd.Function):
         C = _channels(hashgrid_settings)
         level = int(hashgrid_settings.L)
         second_grid = not (_empty(features_diffuse) or _empty(offsets_diffuse) or _empty(gridrange_diffuse))
-        if base_mode in (1, 2, 3, 4, 5, 7, 8, 9, 10, 12, 14) and level == 0:
+        if base_mode in (1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 12, 14) and level == 0:
             base_mode = render_mode = 0  # level 0 is the colour path in every mode but 13 (CR/forward.cu:1091)
         if base_mode in (1, 2, 3, 5):
             # baseline_double / baseline_blend_double (CR/forward.cu:1146-1217): the grid's

@@ -67,6 +67,7 @@ MODE_BASELINE_DOUBLE = 2
 MODE_BASELINE_BLEND_DOUBLE = 3
 MODE_SURFACE_RGB = 5
 MODE_CAT = 4
+MODE_ADAPTIVE = 6
 MODE_ADAPTIVE_ADD = 7
 MODE_HYBRID_SH = 8
 MODE_HYBRID_SH_POST = 9

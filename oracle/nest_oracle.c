@@ -702,7 +702,8 @@ typedef struct {
      * << 16 | grid levels << 8, rows of 3 / 48 / 3 floats, a one-level
      * 3-channel grid), 2 / 3 baseline_double / baseline_blend_double (level =
      * the levels of both grids, F = 4, the second grid below), 1 / 5 surface
-     * potentials (F = 12 with the second grid's 4 per level, or F = 15).
+     * potentials (F = 12 with the second grid's 4 per level, or F = 15),
+     * 6 adaptive (level = grid levels, rows of C floats).
      * Other values are not restated. */
     int render_mode;
     /* record_transmittance (forward.cu:1961-1964), NULL = off: [P] each;
@@ -901,6 +902,22 @@ static void render_pixel(const or_render_args *A, uint32_t tile, uint32_t px, ui
                 }
                 for (int c = 0; c < C; c++) feat_scratch[c] = 0.0f;
                 for (int i = 0; i < tdim && i < C && i < 64; i++) feat_scratch[i] = fmaf(wt, gf[i], iw * hf[i]);
+            } else if ((A->render_mode & 0xFF) == 6) {
+                /* adaptive (forward.cu:1283-1325): rows of C floats; the first
+                 * level*F channels are 0.5 * row + 0.5 * grid, the grid's
+                 * `level` levels at the hit (both products are exact, so the
+                 * sum rounds once however it is contracted); full hits. */
+                const int F = A->grid.F, fdim = A->level * F;
+                const float *gf = A->colors + (size_t)id * (size_t)C;
+                float hf[64];
+                for (int i = 0; i < 64; i++) hf[i] = 0.0f;
+                if (A->level > 0) {
+                    or_grid G = A->grid;
+                    G.L = A->level;
+                    or_query_feature(&G, xyz, ap, 64, hf);
+                }
+                for (int c = 0; c < C; c++) feat_scratch[c] = 0.0f;
+                for (int i = 0; i < fdim && i < C && i < 64; i++) feat_scratch[i] = 0.5f * gf[i] + 0.5f * hf[i];
             } else if ((A->render_mode & 0xFF) == 14) {
                 /* adaptive_zero (forward.cu:1716-1830): rows [hyb*F features |
                  * weight]; the first hyb*F channels from the row, the next hl

@@ -236,7 +236,8 @@ def render(pre, binres, W, H, C, grid: Optional[OrGrid], homotrans=None, ap_leve
     trans_avg ([P] each) to the result.  kernel_type 1-3 take the per-splat
     parameter from shapes [P].  Render modes 2 and 3 (level = the grids'
     levels, F = 4) take the second grid as grid2 = (offsets, float32 table,
-    gridrange), or None for a missing one."""
+    gridrange), or None for a missing one.  Render mode 6 (adaptive): level =
+    the grid levels, colors rows of C floats."""
     HW = W * H
     out = dict(color=np.zeros((C, H, W), np.float32), others=np.zeros((14, H, W), np.float32),
                final_T=np.zeros((3, H, W), np.float32), n_contrib=np.zeros((2, H, W), np.uint32))

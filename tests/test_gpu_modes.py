@@ -1,4 +1,4 @@
-"""GPU parity of render modes 4 (cat), 7 (adaptive_add), 12 (adaptive_cat),
+"""GPU parity of render modes 4 (cat), 6 (adaptive), 7 (adaptive_add), 12 (adaptive_cat),
 13 (adaptive_cat_fast) and 14 (adaptive_zero), training and inference, against the oracle, bit for bit, on the shared small scenes:
 per-splat feature rows ahead of a grid of the scene's first levels, with
 f32 and f16 tables, level_dim 2 and 4, the common-grid lookup and the
@@ -128,6 +128,27 @@ def test_adaptive_add_parity(oracle, name, total, hl, interp):
     _check(res, b, r)
 
 
+# (scene, grid levels, extra channels, interp): level_dim 4 f32 (contracted,
+# 64 channels) and f16, level_dim 2; rows wider than the blended channels
+AD_CASES = [("unbounded_small", 16, 0, 0), ("shells_small", 5, 3, 0), ("shell_small", 8, 4, 1), ("cfg1", 6, 2, 0),
+            ("cfg1", 3, 9, 1)]
+
+
+@pytest.mark.parametrize("name,levels,extra,interp", AD_CASES)
+def test_adaptive_parity(oracle, name, levels, extra, interp):
+    """Render mode 6 (adaptive): rows of C floats, the first levels*F channels
+    0.5 * row + 0.5 * grid, the rest 0; full hits."""
+    sc = scene(name)
+    C = levels * sc.spec.F + extra
+    print(f"[case] mode 6 {name} levels={levels} C={C} interp={interp}", flush=True)
+    rows = _rows(sc, C, seed=levels + extra)
+    res = run_gpu(sc, 6, 0, levels, 0, C, rows, interp=interp)
+    b, r = run_oracle(oracle, sc, 6, levels, levels, C, rows, interp=interp)
+    _check(res, b, r)
+    if extra:
+        assert not res.color[levels * sc.spec.F:].any()
+
+
 # (scene, inference, total levels, per-splat levels, grid levels, interp)
 AZ_CASES = [("unbounded_small", False, 16, 10, 6, 0), ("shells_small", True, 9, 5, 3, 0),
             ("shell_small", True, 12, 4, 8, 1), ("cfg1", False, 8, 3, 5, 1)]
@@ -183,13 +204,14 @@ def test_drop_in_decodes_packed_levels(oracle):
                                        torch.zeros(3, device=DEV), 1.0, t(cam.world_view_transform),
                                        t(cam.full_proj_transform), 3, t(cam.camera_center), False, False, 0.0,
                                        sp.contract, False)
-    for mode, total, hyb, gl in ((4, 8, 3, 5), (13 | 0x100, 10, 6, 3)):
+    for mode, total, hyb, gl in ((4, 8, 3, 5), (13 | 0x100, 10, 6, 3), (6, 7, 0, 7)):
         C = total * F
-        width = hyb * F if mode == 4 else C + 1
-        rows = _rows(sc, width, weight_col=None if mode == 4 else C, seed=mode)
+        width = hyb * F if mode == 4 else (C if mode == 6 else C + 1)
+        rows = _rows(sc, width, weight_col=None if mode in (4, 6) else C, seed=mode)
         offs = np.zeros(17, np.int32)
         offs[:gl + 1] = np.asarray(sc.offsets)[:gl + 1]
-        packed = (total << 16) | ((1 if mode == 4 else gl) << 8) | hyb
+        # mode 6 takes L as the grid's level count
+        packed = gl if mode == 6 else (total << 16) | ((1 if mode == 4 else gl) << 8) | hyb
         hs = HashGridSettings(packed, math.log2(sp.per_level_scale), sp.base_res, False, 0,
                               torch.tensor([hyb * F, gl * F, C], dtype=torch.int32, device=DEV))
         print(f"[case] drop-in mode {mode:#x} L={packed:#x}", flush=True)
@@ -316,11 +338,15 @@ def test_mode_validation():
         call(13, 1, 2, 40, 80, 81)
     with pytest.raises(errs, match="hybrid_levels must be 0"):
         call(7, 1, 2, 4, 8, 9)
-    # modes without a backward in the reference: 13 and the inference flag
-    for mode in (13, 12 | 0x100, 14 | 0x100):
+    with pytest.raises(errs, match="hybrid_levels must be 0"):
+        call(6, 1, 2, 0, 8, 8)
+    with pytest.raises(errs, match="channels"):
+        call(6, 0, 4, 0, 6, 6)
+    # modes without a backward in the reference: 13, the inference flag and 6
+    for mode in (13, 12 | 0x100, 14 | 0x100, 6):
         grid = rz.HashGridDesc(2, sp.F, sp.S, sp.base_res, t(sc.table), sc.offsets,
-                               np.asarray(sp.gridrange, np.float32), render_mode=mode, hybrid_levels=1,
-                               total_levels=4)
+                               np.asarray(sp.gridrange, np.float32), render_mode=mode,
+                               hybrid_levels=0 if mode == 6 else 1, total_levels=4)
         rows = t(np.zeros((sp.P, grid.row_width(8)), np.float32))
         kw = dict(homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), colors_precomp=rows, channels=8)
         res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations), **kw)
