@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define NEST_ABI_VERSION 16
+#define NEST_ABI_VERSION 17
 
 #define NEST_OK 0
 #define NEST_ERR_INVALID_ARGUMENT (-1)
@@ -285,14 +285,18 @@ const char *nest_last_error(void);
 #define NEST_GEOM_RADII 5          /* i32 [P]                         */
 #define NEST_GEOM_SCAN_TMP 6       /* scan scratch                    */
 #define NEST_GEOM_DEPTH_ORDER 7    /* u32 [P]    splat ids by (depth bits, id),
-                                      culled splats last (written by
-                                      nest_forward_render)             */
+                                      culled splats last (queued by
+                                      nest_forward_geometry)           */
 #define NEST_GEOM_ORDER_OFFSETS 8  /* u32 [P]    exclusive scan of tiles
                                       touched in that order            */
 #define NEST_GEOM_ORDER_TMP 9      /* depth sort scratch              */
 #define NEST_GEOM_RGB 10           /* f32 [P,3]  colour from SH (when shs is set) */
 #define NEST_GEOM_CLAMPED 11       /* u8  [P,3]  SH colour channel clamped to 0 */
-#define NEST_GEOM_FIELDS 12
+#define NEST_GEOM_RECT 12          /* u32 [P,2]  tile rectangle [x0, x1) x
+                                      [y0, y1) as (x0 | y0 << 16,
+                                      x1 | y1 << 16), zeros when culled */
+#define NEST_GEOM_ORDER_RECT 13    /* u32 [P,2]  the rectangles in depth order */
+#define NEST_GEOM_FIELDS 14
 int nest_geom_layout(int32_t P, size_t offsets[NEST_GEOM_FIELDS], size_t *total_bytes);
 
 /* The pairs are emitted in depth order and sorted on the tile bits only;

@@ -404,6 +404,8 @@ int nest_geom_layout(int32_t P, size_t offsets[NEST_GEOM_FIELDS], size_t* total)
   o[NEST_GEOM_ORDER_TMP] = c.take(depth_order_ws_bytes((int)n));
   o[NEST_GEOM_RGB] = c.take(n * 12);
   o[NEST_GEOM_CLAMPED] = c.take(n * 3);
+  o[NEST_GEOM_RECT] = c.take(n * 8);
+  o[NEST_GEOM_ORDER_RECT] = c.take(n * 8);
   if (offsets)
     for (int i = 0; i < NEST_GEOM_FIELDS; i++) offsets[i] = o[i];
   if (total) *total = c.off;
@@ -482,6 +484,9 @@ int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp,
   p.H = H;
   p.gx = (uint32_t)((W + kTile - 1) / kTile);
   p.gy = (uint32_t)((H + kTile - 1) / kTile);
+  // tile rectangles pack 16-bit tile coordinates
+  if (p.gx > 0xFFFFu || p.gy > 0xFFFFu)
+    return fail(NEST_ERR_UNSUPPORTED, "image of %d x %d pixels: at most 65535 tiles per side", W, H);
   p.scale_mod = rs->scale_modifier;
   p.beta = rs->beta;
   memcpy(p.view, rs->viewmatrix, sizeof(p.view));
@@ -499,6 +504,8 @@ int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp,
   p.xy = reinterpret_cast<float*>(g + off[NEST_GEOM_XY]);
   p.depth = reinterpret_cast<float*>(g + off[NEST_GEOM_DEPTH]);
   p.tiles = reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_TILES]);
+  p.rect = reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_RECT]);
+  p.depth_key = reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_ORDER_TMP]);  // the depth sort's input keys
   p.records = reinterpret_cast<float*>(g + off[NEST_GEOM_RECORDS]);
   if (sh_colours(sp)) {
     p.shs = sp->shs;
@@ -533,9 +540,10 @@ int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp,
   // the splats' depth order (it does not depend on the pair count) runs while
   // the host waits for the count and then sizes the binning workspace
   tm.begin(NEST_STAGE_DEPTH_ORDER);
-  rc = check_stage(launch_depth_order(sp->P, p.depth, p.radii, p.tiles,
+  rc = check_stage(launch_depth_order(sp->P, p.rect,
                                       reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_DEPTH_ORDER]),
                                       reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_ORDER_OFFSETS]),
+                                      reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_ORDER_RECT]),
                                       g + off[NEST_GEOM_ORDER_TMP], s),
                    "depth order", rs->debug, s);
   tm.end();
@@ -696,13 +704,12 @@ int nest_forward_render(const nest_raster_settings* rs, const nest_hashgrid* gr,
     uint32_t* pair_ids = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_PAIR_IDS]);
     vals = reinterpret_cast<uint32_t*>(b + bo[NEST_BIN_VALS]);
     const float* depth = reinterpret_cast<const float*>(g + go[NEST_GEOM_DEPTH]);
-    const int32_t* gradii = reinterpret_cast<const int32_t*>(g + go[NEST_GEOM_RADII]);
     const uint32_t* order = reinterpret_cast<const uint32_t*>(g + go[NEST_GEOM_DEPTH_ORDER]);
     const uint32_t* order_offsets = reinterpret_cast<const uint32_t*>(g + go[NEST_GEOM_ORDER_OFFSETS]);
+    const uint32_t* order_rect = reinterpret_cast<const uint32_t*>(g + go[NEST_GEOM_ORDER_RECT]);
     // duplicate stage: the pairs of the splats in the depth order nest_forward_geometry queued
     tm.begin(NEST_STAGE_DUPLICATE);
-    rc = check_stage(launch_duplicate_ordered(sp->P, order, order_offsets, reinterpret_cast<const float*>(g + go[NEST_GEOM_XY]),
-                                              gradii, gx, gy, NR, pair_tiles, pair_ids, s),
+    rc = check_stage(launch_duplicate_ordered(sp->P, order, order_offsets, order_rect, gx, NR, pair_tiles, pair_ids, s),
                      "duplicate", rs->debug, s);
     if (rc) return rc;
     tm.end();

@@ -99,14 +99,24 @@ __global__ void __launch_bounds__(kScanThreads) scan_partials_kernel(uint64_t* _
 // consecutive items (stride 17 words) hits distinct banks.
 __device__ __forceinline__ int padded(int i) { return i + (i >> 4); }
 
+// Up to this many blocks, pass 3 sums the block totals before it itself (at
+// most 4 loads per thread) and pass 2 is not launched.
+constexpr int64_t kScanFoldBlocks = 1024;
+
 // Pass 3: rescan each tile of 4096 items with its block offset.  Items are
 // loaded coalesced (item k*256 + t), transposed through LDS so that each
-// thread scans 16 consecutive items, and stored coalesced again.
-template <bool kExclusive>
+// thread scans 16 consecutive items, and stored coalesced again.  kFold:
+// partial holds the nb block totals unscanned; each block adds up those
+// before it, and the last block writes the grand total to partial[nb].
+template <bool kExclusive, bool kFold>
 __global__ void __launch_bounds__(kScanThreads) scan_down_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
-                                                                int64_t n, const uint64_t* __restrict__ partial) {
+                                                                int64_t n, uint64_t* __restrict__ partial) {
   __shared__ uint32_t tile[kScanTile + kScanTile / 16];
   const int64_t base = (int64_t)blockIdx.x * kScanTile;
+  uint64_t before = 0;
+  if constexpr (kFold) {
+    for (uint32_t j = threadIdx.x; j < blockIdx.x; j += kScanThreads) before += partial[j];
+  }
 #pragma unroll
   for (int k = 0; k < kScanItems; k++) {
     const int idx = k * kScanThreads + threadIdx.x;
@@ -122,7 +132,15 @@ __global__ void __launch_bounds__(kScanThreads) scan_down_kernel(const uint32_t*
     s += v[k];
   }
   uint64_t total;
-  uint64_t run = block_exclusive_scan_u64(s, &total) + partial[blockIdx.x];
+  uint64_t run = block_exclusive_scan_u64(s, &total);
+  if constexpr (kFold) {
+    uint64_t off;
+    block_exclusive_scan_u64(before, &off);
+    run += off;
+    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) partial[gridDim.x] = off + total;
+  } else {
+    run += partial[blockIdx.x];
+  }
 #pragma unroll
   for (int k = 0; k < kScanItems; k++) {
     if (kExclusive) {
@@ -152,11 +170,22 @@ static hipError_t scan_impl(const uint32_t* in, uint32_t* out, int64_t n, void* 
   const int64_t nb = (n + kScanTile - 1) / kScanTile;
   uint64_t* partial = static_cast<uint64_t*>(ws);
   hipLaunchKernelGGL(scan_reduce_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, n, partial);
+  if (nb <= kScanFoldBlocks) {
+    if (exclusive)
+      hipLaunchKernelGGL((scan_down_kernel<true, true>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
+                         partial);
+    else
+      hipLaunchKernelGGL((scan_down_kernel<false, true>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
+                         partial);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, s, partial, nb);
   if (exclusive)
-    hipLaunchKernelGGL(scan_down_kernel<true>, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n, partial);
+    hipLaunchKernelGGL((scan_down_kernel<true, false>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
+                       partial);
   else
-    hipLaunchKernelGGL(scan_down_kernel<false>, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n, partial);
+    hipLaunchKernelGGL((scan_down_kernel<false, false>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
+                       partial);
   return hipGetLastError();
 }
 
@@ -271,6 +300,9 @@ __global__ void __launch_bounds__(kScanThreads) digit_scan_kernel(uint32_t* __re
 // is sorted on the whole key), every run of equal keys in that copy adds its
 // length to tile_counts[2 * key + 1] (the .y of the key's uint2 range); keys
 // at or past ntiles are not counted.
+// With rect_in (the last pass of the splats' depth sort), each value v also
+// carries its tile rectangle rect_in[v] to rect_out and the rectangle's tile
+// count to area_out, at the value's sorted position.
 template <typename K, typename KOut, int R>
 __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __restrict__ keys_in,
                                                                     const uint32_t* __restrict__ vals_in,
@@ -280,7 +312,10 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
                                                                     const uint32_t* __restrict__ offsets, uint32_t nblocks,
                                                                     const uint32_t* __restrict__ dtot,
                                                                     const uint32_t* __restrict__ low_bits,
-                                                                    uint32_t* __restrict__ tile_counts, uint32_t ntiles) {
+                                                                    uint32_t* __restrict__ tile_counts, uint32_t ntiles,
+                                                                    const uint2* __restrict__ rect_in,
+                                                                    uint2* __restrict__ rect_out,
+                                                                    uint32_t* __restrict__ area_out) {
   static_assert(kRadix == kSortThreads, "one digit per thread in the block scan");
   __shared__ uint32_t hist[kSortWaves][kRadix];
   __shared__ uint32_t gbase[kRadix];  // global start of the digit's run, minus its local start
@@ -371,6 +406,11 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
         keys_out[pos] = k;
     }
     vals_out[pos] = v;
+    if (rect_in != nullptr) {
+      const uint2 rc = rect_in[v];
+      rect_out[pos] = rc;
+      area_out[pos] = ((rc.y & 0xFFFFu) - (rc.x & 0xFFFFu)) * ((rc.y >> 16) - (rc.x >> 16));
+    }
     if (tile_counts != nullptr && (uint64_t)k < ntiles) {
       // the run [a, b) of key k adds -a at its first element, b at its last
       uint32_t* c = tile_counts + 2u * (uint32_t)k + 1u;
@@ -386,14 +426,22 @@ __global__ void __launch_bounds__(kSortThreads) radix_scatter_kernel(const K* __
 // leaves it after the memset.  The counts are read from ranges[t].y (the tile
 // sort's last pass accumulates them there, x zero) and overwritten in place.
 constexpr int kRangeThreads = 1024;
+constexpr uint32_t kRangeLds = 16384;  // counts staged in LDS up to this many tiles
 
 __global__ void __launch_bounds__(kRangeThreads) ranges_from_counts_kernel(uint2* __restrict__ ranges,
                                                                           uint32_t ntiles) {
   __shared__ uint32_t wsum[kRangeThreads / kWave];
+  __shared__ uint32_t cnt[kRangeLds];
   const uint32_t per = (ntiles + kRangeThreads - 1) / kRangeThreads;
   const uint32_t lo = threadIdx.x * per, hi = min(lo + per, ntiles);
+  const bool staged = ntiles <= kRangeLds;
+  if (staged) {
+    // all counts in flight at once (coalesced), then each thread's run from LDS
+    for (uint32_t t = threadIdx.x; t < ntiles; t += kRangeThreads) cnt[t] = ranges[t].y;
+    __syncthreads();
+  }
   uint32_t s = 0;
-  for (uint32_t t = lo; t < hi; t++) s += ranges[t].y;
+  for (uint32_t t = lo; t < hi; t++) s += staged ? cnt[t] : ranges[t].y;
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
   uint32_t inc = s;
 #pragma unroll
@@ -405,6 +453,21 @@ __global__ void __launch_bounds__(kRangeThreads) ranges_from_counts_kernel(uint2
   __syncthreads();
   uint32_t run = inc - s;
   for (int w = 0; w < wid; w++) run += wsum[w];
+  if (staged) {
+    // each run start replaces its count in LDS; the ranges go out coalesced
+    for (uint32_t t = lo; t < hi; t++) {
+      const uint32_t c = cnt[t];
+      cnt[t] = run;
+      run += c;
+    }
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t < ntiles; t += kRangeThreads) {
+      const uint32_t st = cnt[t];
+      const uint32_t en = t + 1 < ntiles ? cnt[t + 1] : st + ranges[t].y;
+      ranges[t] = en != st ? make_uint2(st, en) : make_uint2(0u, 0u);
+    }
+    return;
+  }
   for (uint32_t t = lo; t < hi; t++) {
     const uint32_t c = ranges[t].y;
     ranges[t] = c != 0u ? make_uint2(run, run + c) : make_uint2(0u, 0u);
@@ -413,7 +476,8 @@ __global__ void __launch_bounds__(kRangeThreads) ranges_from_counts_kernel(uint2
 }
 
 // Keys per block: 1024 up to kSmallSort keys (more blocks to fill the chip for
-// the splats' depth sort), else 4096 (longer runs per digit in the output).
+// the splats' depth sort), else 4096 (longer runs per digit in the output;
+// 8192 keys, 69 KB of LDS and 2 waves per SIMD, made the tile passes slower).
 static int sort_rounds(int64_t n) { return n <= kSmallSort ? kSortRoundsSmall : kSortRounds; }
 static int64_t sort_blocks(int64_t n) {
   const int64_t tile = (int64_t)kSortThreads * sort_rounds(n);
@@ -436,11 +500,15 @@ static size_t sort_ws_bytes_t(int64_t n) {
 // stands for vals_in[i] = i.  With KOut wider than K the last pass writes
 // (key << 32) | low_bits[val].  With tile_counts (ntiles uint2 ranges), the
 // last pass also counts the keys per value (the pairs per tile) into the .y
-// words, after zeroing all 2 * ntiles words.
+// words, after zeroing all 2 * ntiles words.  With rect_in, the last pass
+// writes no keys; it moves each value's rectangle and tile count to
+// rect_out / area_out instead (area_out must not alias keys_in unless there
+// is more than one pass).
 template <typename K, typename KOut>
 static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, KOut* keys_out, uint32_t* vals_out, int64_t n,
                             int end_bit, const uint32_t* low_bits, void* ws, hipStream_t s,
-                            uint32_t* tile_counts = nullptr, uint32_t ntiles = 0) {
+                            uint32_t* tile_counts = nullptr, uint32_t ntiles = 0, const uint2* rect_in = nullptr,
+                            uint2* rect_out = nullptr, uint32_t* area_out = nullptr) {
   if (n <= 0) return hipSuccess;
   constexpr bool kSame = sizeof(KOut) == sizeof(K);
   const int64_t nb = sort_blocks(n);
@@ -488,20 +556,27 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, KOut* key
       dk = tk[pass & 1];
       dv = tv[pass & 1];
     }
+    const uint2* ri = last ? rect_in : nullptr;
+    uint2* ro = last ? rect_out : nullptr;
+    uint32_t* ao = last ? area_out : nullptr;
     if (!kSame && last) {
       if (small)
         hipLaunchKernelGGL((radix_scatter_kernel<K, KOut, kSortRoundsSmall>), dim3((unsigned)nb), dim3(kSortThreads), 0,
-                           s, sk, sv, keys_out, vals_out, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
+                           s, sk, sv, keys_out, vals_out, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles,
+                           ri, ro, ao);
       else
         hipLaunchKernelGGL((radix_scatter_kernel<K, KOut, kSortRounds>), dim3((unsigned)nb), dim3(kSortThreads), 0, s,
-                           sk, sv, keys_out, vals_out, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
+                           sk, sv, keys_out, vals_out, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles,
+                           ri, ro, ao);
     } else {
+      K* dko = ri != nullptr ? nullptr : dk;  // the rectangles replace the sorted keys
       if (small)
         hipLaunchKernelGGL((radix_scatter_kernel<K, K, kSortRoundsSmall>), dim3((unsigned)nb), dim3(kSortThreads), 0, s,
-                           sk, sv, dk, dv, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
+                           sk, sv, dko, dv, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles, ri, ro,
+                           ao);
       else
         hipLaunchKernelGGL((radix_scatter_kernel<K, K, kSortRounds>), dim3((unsigned)nb), dim3(kSortThreads), 0, s, sk,
-                           sv, dk, dv, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles);
+                           sv, dko, dv, n, shift, nbits, counts, (uint32_t)nb, dtot, low_bits, tc, ntiles, ri, ro, ao);
     }
     sk = dk;
     sv = dv;
@@ -529,47 +604,36 @@ hipError_t launch_sort_pairs(const uint64_t* keys_in, const uint32_t* vals_in, u
 // pair sort then runs on 4-byte keys over ceil(tile bits / 8) passes instead
 // of 8-byte keys over ceil((32 + tile bits) / 8) passes.
 
-// Depth keys: depth bits of the visible splats (depth > 0, so the bit order is
-// the float order); culled splats, which emit no pairs, go last.
-__global__ void depth_keys_kernel(int P, const float* __restrict__ depth, const int32_t* __restrict__ radii,
-                                  uint32_t* __restrict__ keys) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= P) return;
-  keys[i] = radii[i] > 0 ? __float_as_uint(depth[i]) : 0xffffffffu;
-}
-
-__global__ void gather_u32_kernel(int P, const uint32_t* __restrict__ src, const uint32_t* __restrict__ order,
-                                  uint32_t* __restrict__ dst) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < P) dst[i] = src[order[i]];
-}
-
 size_t depth_order_ws_bytes(int P) {
   const int64_t n = P > 0 ? P : 1;
   return align256((size_t)n * 4) * 2 + sort_ws_bytes_t<uint32_t, uint32_t>(n);
 }
 
-hipError_t launch_depth_order(int P, const float* depth, const int32_t* radii, const uint32_t* tiles, uint32_t* order,
-                              uint32_t* ordered_offsets, void* ws, hipStream_t s) {
+// The depth keys (depth bits of the visible splats, whose depth is > 0.2 so
+// that the bit order is the float order; 0xffffffff for culled splats, which
+// emit no pairs and go last) are written by preprocess at the start of ws.
+hipError_t launch_depth_order(int P, const uint32_t* rect, uint32_t* order, uint32_t* ordered_offsets,
+                              uint32_t* ordered_rect, void* ws, hipStream_t s) {
   if (P <= 0) return hipSuccess;
   char* w = static_cast<char*>(ws);
   uint32_t* keys = reinterpret_cast<uint32_t*>(w);
   w += align256((size_t)P * 4);
   uint32_t* keys_sorted = reinterpret_cast<uint32_t*>(w);
   w += align256((size_t)P * 4);
-  const unsigned grid = (unsigned)((P + 255) / 256);
-  hipLaunchKernelGGL(depth_keys_kernel, dim3(grid), dim3(256), 0, s, P, depth, radii, keys);
-  hipError_t e = sort_impl<uint32_t, uint32_t>(keys, nullptr, keys_sorted, order, P, 32, nullptr, w, s);
+  // 4 passes: the depth keys are read by the first alone, so the last pass
+  // writes the tiles touched in depth order over them, next to the rectangles
+  hipError_t e = sort_impl<uint32_t, uint32_t>(keys, nullptr, keys_sorted, order, P, 32, nullptr, w, s, nullptr, 0,
+                                               reinterpret_cast<const uint2*>(rect),
+                                               reinterpret_cast<uint2*>(ordered_rect), keys);
   if (e != hipSuccess) return e;
-  // tiles touched in depth order, scanned (exclusive) in place; the sort's
-  // workspace is free again and holds the scan partials
-  hipLaunchKernelGGL(gather_u32_kernel, dim3(grid), dim3(256), 0, s, P, tiles, order, keys);
+  // tiles touched in depth order, scanned (exclusive); the sort's workspace
+  // is free again and holds the scan partials
   return scan_impl(keys, ordered_offsets, P, w, true, s);
 }
 
 // A workgroup owns 256 consecutive splats of the depth order, whose pairs
 // form one contiguous run of the output.  Each splat's (offset, id, tile
-// rectangle) goes to LDS; lanes then write consecutive pair positions
+// rectangle, read in depth order) goes to LDS; lanes then write consecutive pair positions
 // (coalesced), each finding its splat by binary search over the offsets.
 // Pair q of a splat is tile (y0 + q / w, x0 + q % w): row-major over the
 // rectangle, as the reference emits them.  Writes stop at n_pairs (the pair
@@ -578,9 +642,8 @@ constexpr int kDupThreads = 256;
 
 __global__ void __launch_bounds__(kDupThreads) duplicate_ordered_kernel(int P, const uint32_t* __restrict__ order,
                                                                        const uint32_t* __restrict__ offsets,
-                                                                       const float2* __restrict__ xy,
-                                                                       const int32_t* __restrict__ radii, uint32_t gx,
-                                                                       uint32_t gy, uint32_t n_pairs,
+                                                                       const uint2* __restrict__ rect, uint32_t gx,
+                                                                       uint32_t n_pairs,
                                                                        uint32_t* __restrict__ tile_keys,
                                                                        uint32_t* __restrict__ ids) {
   __shared__ uint32_t s_off[kDupThreads], s_id[kDupThreads], s_x0[kDupThreads], s_y0[kDupThreads], s_w[kDupThreads];
@@ -592,12 +655,12 @@ __global__ void __launch_bounds__(kDupThreads) duplicate_ordered_kernel(int P, c
   if (k < P) {
     off = offsets[k];
     id = order[k];
-    const int r = radii[id];
-    if (r > 0) {
-      uint32_t x1, y1;
-      tile_rect(xy[id].x, xy[id].y, r, gx, gy, x0, y0, x1, y1);
-      w = x1 > x0 ? x1 - x0 : 1u;
-    }
+    // culled splats have an empty rectangle and no pairs
+    const uint2 rc = rect[k];
+    x0 = rc.x & 0xFFFFu;
+    y0 = rc.x >> 16;
+    const uint32_t x1 = rc.y & 0xFFFFu;
+    w = x1 > x0 ? x1 - x0 : 1u;
   }
   s_off[threadIdx.x] = off;
   s_id[threadIdx.x] = id;
@@ -622,12 +685,11 @@ __global__ void __launch_bounds__(kDupThreads) duplicate_ordered_kernel(int P, c
   }
 }
 
-hipError_t launch_duplicate_ordered(int P, const uint32_t* order, const uint32_t* offsets, const float* xy,
-                                    const int32_t* radii, uint32_t gx, uint32_t gy, int64_t n_pairs,
-                                    uint32_t* tile_keys, uint32_t* ids, hipStream_t s) {
+hipError_t launch_duplicate_ordered(int P, const uint32_t* order, const uint32_t* offsets, const uint32_t* ordered_rect,
+                                    uint32_t gx, int64_t n_pairs, uint32_t* tile_keys, uint32_t* ids, hipStream_t s) {
   if (P <= 0 || n_pairs <= 0) return hipSuccess;
   hipLaunchKernelGGL(duplicate_ordered_kernel, dim3((P + kDupThreads - 1) / kDupThreads), dim3(kDupThreads), 0, s, P,
-                     order, offsets, reinterpret_cast<const float2*>(xy), radii, gx, gy, (uint32_t)n_pairs, tile_keys,
+                     order, offsets, reinterpret_cast<const uint2*>(ordered_rect), gx, (uint32_t)n_pairs, tile_keys,
                      ids);
   return hipGetLastError();
 }

@@ -50,6 +50,8 @@ struct PreprocessParams {
   float* xy;
   float* depth;
   uint32_t* tiles;
+  uint32_t* rect;           // [P, 2] tile rectangle (x0 | y0 << 16, x1 | y1 << 16), zeros when culled
+  uint32_t* depth_key;      // [P] key of the depth order: depth bits, 0xffffffff when culled
   float* records;
   float* rgb;               // [P, 3], written when shs is set
   uint8_t* clamped;         // [P, 3], written when shs is set
@@ -165,16 +167,16 @@ size_t sort_ws_bytes(int64_t n);
 // (keys_out, vals_out); the inputs are not written.
 hipError_t launch_sort_pairs(const uint64_t* keys_in, const uint32_t* vals_in, uint64_t* keys_out, uint32_t* vals_out,
                              int64_t n, int end_bit, void* ws, hipStream_t s);
-// Splat ids in (depth bits, id) order, culled splats last, and the exclusive
-// scan of their tiles touched in that order.
+// Splat ids in (depth bits, id) order, culled splats last, their tile
+// rectangles in that order and the exclusive scan of their tiles touched.
+// ws starts with the P depth keys (PreprocessParams::depth_key).
 size_t depth_order_ws_bytes(int P);
-hipError_t launch_depth_order(int P, const float* depth, const int32_t* radii, const uint32_t* tiles, uint32_t* order,
-                              uint32_t* ordered_offsets, void* ws, hipStream_t s);
-// (tile id, splat id) pairs of the splats in depth order; at most n_pairs
-// are written.
-hipError_t launch_duplicate_ordered(int P, const uint32_t* order, const uint32_t* offsets, const float* xy,
-                                    const int32_t* radii, uint32_t gx, uint32_t gy, int64_t n_pairs,
-                                    uint32_t* tile_keys, uint32_t* ids, hipStream_t s);
+hipError_t launch_depth_order(int P, const uint32_t* rect, uint32_t* order, uint32_t* ordered_offsets,
+                              uint32_t* ordered_rect, void* ws, hipStream_t s);
+// (tile id, splat id) pairs of the splats in depth order, from their
+// rectangles in that order; at most n_pairs are written.
+hipError_t launch_duplicate_ordered(int P, const uint32_t* order, const uint32_t* offsets, const uint32_t* ordered_rect,
+                                    uint32_t gx, int64_t n_pairs, uint32_t* tile_keys, uint32_t* ids, hipStream_t s);
 // Stable sort of the depth-ordered pairs on tile bits [0, tile_bits): writes
 // the splat ids in tile/depth order, the (tile << 32 | depth bits) keys too
 // unless keys_out is NULL, and leaves the pairs per tile in ranges (ntiles

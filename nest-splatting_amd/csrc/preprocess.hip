@@ -71,6 +71,8 @@ __global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams 
   p.radii[i] = 0;
   if (p.radii_user) p.radii_user[i] = 0;
   p.tiles[i] = 0;
+  reinterpret_cast<uint2*>(p.rect)[i] = make_uint2(0u, 0u);
+  p.depth_key[i] = 0xffffffffu;  // culled splats, which emit no pairs, go last
 
   const float px = p.means[3 * i + 0], py = p.means[3 * i + 1], pz = p.means[3 * i + 2];
   const float* V = p.view;
@@ -153,6 +155,8 @@ __global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams 
   if (p.radii_user) p.radii_user[i] = ir;
   reinterpret_cast<float2*>(p.xy)[i] = make_float2(pimx, pimy);
   p.tiles[i] = area;
+  reinterpret_cast<uint2*>(p.rect)[i] = make_uint2(x0 | y0 << 16, x1 | y1 << 16);
+  p.depth_key[i] = __float_as_uint(vz);  // vz > 0.2: the bit order is the float order
   if (p.shs) {
     float rgb[3];
     uint8_t cl[3];

@@ -27,11 +27,11 @@ MAX_LEVELS = 32
 MAX_CHANNELS = 128
 OTHERS_CHANNELS = 14
 
-ABI_VERSION = 16
+ABI_VERSION = 17
 SCAN_NOALLOC_MAX = 268431360
 (GEOM_DEPTH, GEOM_XY, GEOM_TILES, GEOM_OFFSETS, GEOM_RECORDS, GEOM_RADII, GEOM_SCAN_TMP, GEOM_DEPTH_ORDER,
- GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED) = range(12)
-GEOM_FIELDS = 12
+ GEOM_ORDER_OFFSETS, GEOM_ORDER_TMP, GEOM_RGB, GEOM_CLAMPED, GEOM_RECT, GEOM_ORDER_RECT) = range(14)
+GEOM_FIELDS = 14
 BIN_PAIR_TILES, BIN_PAIR_IDS, BIN_KEYS, BIN_VALS, BIN_SORT_TMP = range(5)
 BIN_FIELDS = 5
 IMG_RANGES, IMG_FINAL_T, IMG_N_CONTRIB, IMG_LEVELS, IMG_TILE_ORDER = range(5)

@@ -145,7 +145,7 @@ def test_unsupported_modes_raise():
     hs = HashGridSettings(0, 0.0, 0, False, 0, torch.empty(0))
     kw = dict(means3D=t(sc.means), means2D=None, opacities=t(sc.opacity), colors_precomp=t(sc.means),
               scales=t(sc.scales), rotations=t(sc.rotations))
-    for mode in (11, 6, 4 | 0x100):
+    for mode in (11, 15, 4 | 0x100):
         with pytest.raises(NotImplementedError):
             GaussianRasterizer(rs, hs)(render_mode=mode, **kw)
     with pytest.raises(NotImplementedError):
