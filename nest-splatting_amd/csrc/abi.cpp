@@ -398,8 +398,7 @@ int nest_geom_layout(int32_t P, size_t offsets[NEST_GEOM_FIELDS], size_t* total)
   o[NEST_GEOM_OFFSETS] = c.take(n * 4);
   o[NEST_GEOM_RECORDS] = c.take(n * kRecordFloats * 4);
   o[NEST_GEOM_RADII] = c.take(n * 4);
-  // the scan's workspace, then the per-workgroup tile sums of preprocess
-  o[NEST_GEOM_SCAN_TMP] = c.take(align_up(scan_ws_bytes((int64_t)n), 256) + ((int64_t)n + 255) / 256 * 8);
+  o[NEST_GEOM_SCAN_TMP] = c.take(scan_ws_bytes((int64_t)n));
   o[NEST_GEOM_DEPTH_ORDER] = c.take(n * 4);
   o[NEST_GEOM_ORDER_OFFSETS] = c.take(n * 4);
   o[NEST_GEOM_ORDER_TMP] = c.take(depth_order_ws_bytes((int)n));
@@ -507,7 +506,6 @@ int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp,
   p.tiles = reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_TILES]);
   p.rect = reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_RECT]);
   p.depth_key = reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_ORDER_TMP]);  // the depth sort's input keys
-  p.tile_sums = reinterpret_cast<uint64_t*>(g + off[NEST_GEOM_SCAN_TMP] + align_up(scan_ws_bytes(sp->P), 256));
   p.records = reinterpret_cast<float*>(g + off[NEST_GEOM_RECORDS]);
   if (sh_colours(sp)) {
     p.shs = sp->shs;
@@ -525,8 +523,7 @@ int nest_forward_geometry(const nest_raster_settings* rs, const nest_splats* sp,
   tm.begin(NEST_STAGE_SCAN);
   uint32_t* offs = reinterpret_cast<uint32_t*>(g + off[NEST_GEOM_OFFSETS]);
   void* scan_ws = g + off[NEST_GEOM_SCAN_TMP];
-  if ((rc = check_stage(launch_scan_u32_sums(p.tiles, offs, sp->P, p.tile_sums, scan_ws, s), "scan", rs->debug, s)))
-    return rc;
+  if ((rc = check_stage(launch_scan_u32(p.tiles, offs, sp->P, scan_ws, s), "scan", rs->debug, s))) return rc;
   tm.end();
   // The scan leaves the 64-bit grand total after the per-block partials.
   const int64_t nb = ((int64_t)sp->P + 4095) / 4096;

@@ -105,26 +105,17 @@ constexpr int64_t kScanFoldBlocks = 1024;
 
 // Pass 3: rescan each tile of 4096 items with its block offset.  Items are
 // loaded coalesced (item k*256 + t), transposed through LDS so that each
-// thread scans 16 consecutive items, and stored coalesced again.  kFold 0:
-// partial holds the scanned block offsets.  kFold 1: partial holds the nb
-// block totals unscanned; each block adds up those before it.  kFold 2: the
-// same from sums256, the totals of 256 items.  With kFold the last block
-// writes the grand total to partial[nb].
-template <bool kExclusive, int kFold>
+// thread scans 16 consecutive items, and stored coalesced again.  kFold:
+// partial holds the nb block totals unscanned; each block adds up those
+// before it, and the last block writes the grand total to partial[nb].
+template <bool kExclusive, bool kFold>
 __global__ void __launch_bounds__(kScanThreads) scan_down_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
-                                                                int64_t n, uint64_t* __restrict__ partial,
-                                                                const uint64_t* __restrict__ sums256) {
+                                                                int64_t n, uint64_t* __restrict__ partial) {
   __shared__ uint32_t tile[kScanTile + kScanTile / 16];
   const int64_t base = (int64_t)blockIdx.x * kScanTile;
   uint64_t before = 0;
-  // the loads are unrolled so that they are in flight together
-  if constexpr (kFold == 1) {
-#pragma unroll 4
+  if constexpr (kFold) {
     for (uint32_t j = threadIdx.x; j < blockIdx.x; j += kScanThreads) before += partial[j];
-  } else if constexpr (kFold == 2) {
-    const uint32_t m = blockIdx.x * (uint32_t)(kScanTile / 256);
-#pragma unroll 16
-    for (uint32_t j = threadIdx.x; j < m; j += kScanThreads) before += sums256[j];
   }
 #pragma unroll
   for (int k = 0; k < kScanItems; k++) {
@@ -142,7 +133,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_down_kernel(const uint32_t*
   }
   uint64_t total;
   uint64_t run = block_exclusive_scan_u64(s, &total);
-  if constexpr (kFold != 0) {
+  if constexpr (kFold) {
     uint64_t off;
     block_exclusive_scan_u64(before, &off);
     run += off;
@@ -181,35 +172,25 @@ static hipError_t scan_impl(const uint32_t* in, uint32_t* out, int64_t n, void* 
   hipLaunchKernelGGL(scan_reduce_kernel, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, n, partial);
   if (nb <= kScanFoldBlocks) {
     if (exclusive)
-      hipLaunchKernelGGL((scan_down_kernel<true, 1>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
-                         partial, nullptr);
+      hipLaunchKernelGGL((scan_down_kernel<true, true>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
+                         partial);
     else
-      hipLaunchKernelGGL((scan_down_kernel<false, 1>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
-                         partial, nullptr);
+      hipLaunchKernelGGL((scan_down_kernel<false, true>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
+                         partial);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, s, partial, nb);
   if (exclusive)
-    hipLaunchKernelGGL((scan_down_kernel<true, 0>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
-                       partial, nullptr);
+    hipLaunchKernelGGL((scan_down_kernel<true, false>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
+                       partial);
   else
-    hipLaunchKernelGGL((scan_down_kernel<false, 0>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
-                       partial, nullptr);
+    hipLaunchKernelGGL((scan_down_kernel<false, false>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
+                       partial);
   return hipGetLastError();
 }
 
 hipError_t launch_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* ws, hipStream_t s) {
   return scan_impl(in, out, n, ws, false, s);
-}
-
-hipError_t launch_scan_u32_sums(const uint32_t* in, uint32_t* out, int64_t n, const uint64_t* sums256, void* ws,
-                                hipStream_t s) {
-  if (n <= 0) return hipSuccess;
-  const int64_t nb = (n + kScanTile - 1) / kScanTile;
-  if (nb > kScanFoldBlocks) return scan_impl(in, out, n, ws, false, s);
-  hipLaunchKernelGGL((scan_down_kernel<false, 2>), dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
-                     static_cast<uint64_t*>(ws), sums256);
-  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

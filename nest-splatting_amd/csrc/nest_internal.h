@@ -52,7 +52,6 @@ struct PreprocessParams {
   uint32_t* tiles;
   uint32_t* rect;           // [P, 2] tile rectangle (x0 | y0 << 16, x1 | y1 << 16), zeros when culled
   uint32_t* depth_key;      // [P] key of the depth order: depth bits, 0xffffffff when culled
-  uint64_t* tile_sums;      // [ceil(P / 256)] tiles touched per workgroup of 256 splats, or null
   float* records;
   float* rgb;               // [P, 3], written when shs is set
   uint8_t* clamped;         // [P, 3], written when shs is set
@@ -162,10 +161,6 @@ struct RenderParams {
 // hipGetLastError() of its launches.
 hipError_t launch_preprocess(const PreprocessParams& p, hipStream_t s);
 hipError_t launch_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* ws, hipStream_t s);
-// The same scan given sums256[k] = in[256k] + ... + in[256k + 255] (the
-// grand total lands in the same workspace slot).
-hipError_t launch_scan_u32_sums(const uint32_t* in, uint32_t* out, int64_t n, const uint64_t* sums256, void* ws,
-                                hipStream_t s);
 size_t scan_ws_bytes(int64_t n);
 size_t sort_ws_bytes(int64_t n);
 // Stable sort of (keys_in, vals_in) on key bits [0, end_bit) into

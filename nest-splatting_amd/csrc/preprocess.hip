@@ -63,8 +63,9 @@ __device__ __forceinline__ void sh_to_rgb(int deg, const float* sh, float px, fl
   }
 }
 
-// One splat; returns its tiles touched (0 when culled).
-__device__ __forceinline__ uint32_t preprocess_splat(const PreprocessParams& p, int i) {
+__global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams p) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.P) return;
 
   // Defaults for culled splats (CR/forward.cu:353-354).
   p.radii[i] = 0;
@@ -78,7 +79,7 @@ __device__ __forceinline__ uint32_t preprocess_splat(const PreprocessParams& p, 
   const float vx = V[0] * px + V[4] * py + V[8] * pz + V[12];
   const float vy = V[1] * px + V[5] * py + V[9] * pz + V[13];
   const float vz = V[2] * px + V[6] * py + V[10] * pz + V[14];
-  if (vz <= 0.2f) return 0u;  // near cull, CR/auxiliary.h:205
+  if (vz <= 0.2f) return;  // near cull, CR/auxiliary.h:205
 
   // quat_to_rotmat with rsqrtf -> 1/sqrtf (CR/auxiliary.h:218-240).
   const float4 q = reinterpret_cast<const float4*>(p.rots)[i];
@@ -124,14 +125,14 @@ __device__ __forceinline__ uint32_t preprocess_splat(const PreprocessParams& p, 
   const float nlen = sqrtf(nx * nx + ny * ny + nz * nz);
   if (nlen > 1e-7f) { nx = nx / nlen; ny = ny / nlen; nz = nz / nlen; }
   const float cosv = -(vx * nx + vy * ny + vz * nz);
-  if (cosv == 0.0f) return 0u;
+  if (cosv == 0.0f) return;
   const float mul = cosv > 0.0f ? 1.0f : -1.0f;
   nx = mul * nx; ny = mul * ny; nz = mul * nz;
 
   // compute_aabb with cutoff 4.
   const float cut2 = 16.0f;
   const float d = cut2 * (Tw[0] * Tw[0]) + cut2 * (Tw[1] * Tw[1]) + -1.0f * (Tw[2] * Tw[2]);
-  if (d == 0.0f) return 0u;
+  if (d == 0.0f) return;
   const float invd = 1.0f / d;
   const float f0 = invd * cut2, f1 = invd * cut2, f2 = invd * -1.0f;
   const float pimx = f0 * (Tu[0] * Tw[0]) + f1 * (Tu[1] * Tw[1]) + f2 * (Tu[2] * Tw[2]);
@@ -146,7 +147,7 @@ __device__ __forceinline__ uint32_t preprocess_splat(const PreprocessParams& p, 
   uint32_t x0, y0, x1, y1;
   tile_rect(pimx, pimy, ir, p.gx, p.gy, x0, y0, x1, y1);
   const uint32_t area = (x1 - x0) * (y1 - y0);
-  if (area == 0) return 0u;
+  if (area == 0) return;
 
   const float opacity = p.opac[i];
   p.depth[i] = vz;
@@ -249,23 +250,6 @@ __device__ __forceinline__ uint32_t preprocess_splat(const PreprocessParams& p, 
   rec[5] = make_float4(sv1, sv2, pk0, pk1);
   rec[6] = make_float4(pk2, cut, shape, vz);
   rec[7] = make_float4(bx0, bx1, by0, by1);
-  return area;
-}
-
-// With tile_sums, each workgroup also writes the sum of its 256 splats' tiles
-// touched (the scan of those counts then needs no reduce pass of its own).
-__global__ void __launch_bounds__(256) preprocess_kernel(const PreprocessParams p) {
-  __shared__ uint64_t wsum[256 / 64];
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  const uint32_t t = i < p.P ? preprocess_splat(p, i) : 0u;
-  if (p.tile_sums != nullptr) {
-    uint64_t v = t;
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = v;
-    __syncthreads();
-    if (threadIdx.x == 0) p.tile_sums[blockIdx.x] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-  }
 }
 
 hipError_t launch_preprocess(const PreprocessParams& p, hipStream_t s) {
