@@ -194,10 +194,11 @@ def time_aux_kernels(K, spec, scene, table, dev):
 
 def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_level, table, mlp, M, bg, dev,
                hyb=10):
-    """Render modes 4, 7, 12, 13 and 14 on the benchmark frame: the first `hyb` of
+    """Render modes 4, 6, 7, 12, 13 and 14 on the benchmark frame: the first `hyb` of
     the 16 levels become per-splat feature rows, the last 16 - hyb levels the
     grid (the scene's own tables of those levels, base resolution of level
-    hyb).  Mode 12/13 rows carry a blend weight uniform in [0.15, 1): 59% of
+    hyb); mode 6 blends 64-channel rows half and half with the scene's whole
+    16-level grid.  Mode 12/13 rows carry a blend weight uniform in [0.15, 1): 59% of
     the splats take mode 13's inference fast path (weight > 0.5), 12% mode
     12's (weight >= 0.9); none skip mode 14's grid (weight < 0.1).  Mode 7
     blends all 16 row levels with the grid.  Modes 4, 7, 12 and 14 also time
@@ -221,7 +222,9 @@ def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_lev
     rows13 = torch.from_numpy(rows).to(dev)
     rows4 = rows13[:, :hyb * F].contiguous()
     rows14 = torch.cat([rows4, rows13[:, tdim:]], dim=1).contiguous()
-    cases = {"cat(4)": (4, rows4, 0), "adaptive_add(7)": (7, rows13, Lt), "adaptive_cat(12) training": (12, rows13, Lt),
+    rows6 = rows13[:, :tdim].contiguous()
+    cases = {"cat(4)": (4, rows4, 0), "adaptive(6)": (6, rows6, 0), "adaptive_add(7)": (7, rows13, Lt),
+             "adaptive_cat(12) training": (12, rows13, Lt),
              "adaptive_cat(12) inference": (12 | 0x100, rows13, Lt),
              "adaptive_cat_fast(13) training": (13, rows13, Lt),
              "adaptive_cat_fast(13) inference": (13 | 0x100, rows13, Lt),
@@ -229,9 +232,14 @@ def time_modes(K, spec, scene, settings, means, opac, scales, rots, homo, ap_lev
              "adaptive_zero(14) inference": (14 | 0x100, rows14, Lt)}
     res_ms = {}
     for name, (mode, rows_t, total) in cases.items():
-        # mode 7 blends all 16 levels of the row with the 6-level grid (no coarse levels)
-        grid = rz.HashGridDesc(gl, F, spec.S, sub_base, sub_table, sub_offsets, np.asarray(spec.gridrange, np.float32),
-                               render_mode=mode, hybrid_levels=0 if mode == 7 else hyb, total_levels=total)
+        if mode == 6:
+            grid = rz.HashGridDesc(Lt, F, spec.S, spec.base_res, table, offs, np.asarray(spec.gridrange, np.float32),
+                                   render_mode=6)
+        else:
+            # mode 7 blends all 16 levels of the row with the 6-level grid (no coarse levels)
+            grid = rz.HashGridDesc(gl, F, spec.S, sub_base, sub_table, sub_offsets,
+                                   np.asarray(spec.gridrange, np.float32), render_mode=mode,
+                                   hybrid_levels=0 if mode == 7 else hyb, total_levels=total)
 
         def frame(tm=None):
             res = rz.rasterize_forward(settings, grid, means, opac, scales, rots, homotrans=homo, ap_level=ap_level,
