@@ -149,6 +149,42 @@ def test_adaptive_parity(oracle, name, levels, extra, interp):
         assert not res.color[levels * sc.spec.F:].any()
 
 
+def test_adaptive_record_and_kernel_type(oracle):
+    """Render mode 6 with the transmittance record and the general kernel
+    (kernel_type 3), against the oracle, bit for bit."""
+    from nest_splat import rasterizer as rz
+    sc = scene("shell_small")
+    sp = sc.spec
+    cam = sc.cameras[0]
+    W, H = cam.image_width, cam.image_height
+    levels = 6
+    C = levels * sp.F + 2
+    rows = _rows(sc, C, seed=61)
+    shapes = np.random.default_rng(62).uniform(2.0, 7.0, sp.P).astype(np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    print("[case] mode 6 shell_small, record, kernel_type 3", flush=True)
+    settings = rz.make_settings(H, W, cam.tanfovx, cam.tanfovy, cam.world_view_transform, cam.full_proj_transform,
+                                cam.camera_center, if_contract=sp.contract)
+    grid = rz.HashGridDesc(levels, sp.F, sp.S, sp.base_res, t(sc.table), sc.offsets,
+                           np.asarray(sp.gridrange, np.float32), render_mode=6)
+    res = rz.rasterize_forward(settings, grid, t(sc.means), t(sc.opacity), t(sc.scales), t(sc.rotations),
+                               homotrans=t(sc.homotrans), ap_level=t(sc.ap_level), colors_precomp=t(rows), channels=C,
+                               record_transmittance=True, kernel_type=3, shapes=t(shapes))
+    torch.cuda.synchronize()
+    pre = oracle.preprocess(sc.means, sc.scales, sc.rotations, sc.opacity, cam.world_view_transform,
+                            cam.full_proj_transform, W, H)
+    b = oracle.binning(pre, W, H)
+    g = oracle.make_grid(levels, sp.F, sp.S, sp.base_res, sc.offsets, sc.table, sp.gridrange, sp.contract)
+    r = oracle.render(pre, b, W, H, C, g, homotrans=sc.homotrans, ap_level=sc.ap_level, colors=rows, render_mode=6,
+                      level=levels, record_transmittance=True, kernel_type=3, shapes=shapes)
+    _check(res, b, r)
+    np.testing.assert_array_equal(res.cover_pixels.cpu().numpy().reshape(-1), r["cover_pixels"])
+    # transmittance sums land by atomics in any order: float sums within 1e-5
+    scale = max(float(np.abs(r["trans_avg"]).max()), 1e-30)
+    np.testing.assert_allclose(res.trans_avg.cpu().numpy().reshape(-1), r["trans_avg"], rtol=1e-5, atol=1e-6 * scale)
+    assert r["cover_pixels"].any()
+
+
 # (scene, inference, total levels, per-splat levels, grid levels, interp)
 AZ_CASES = [("unbounded_small", False, 16, 10, 6, 0), ("shells_small", True, 9, 5, 3, 0),
             ("shell_small", True, 12, 4, 8, 1), ("cfg1", False, 8, 3, 5, 1)]
