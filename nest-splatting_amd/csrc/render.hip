@@ -1239,23 +1239,50 @@ __device__ __forceinline__ uint32_t order_bin(uint32_t n) {
   return (uint32_t)(kOrderBins - 1) - (b < (uint32_t)(kOrderBins - 1) ? b : (uint32_t)(kOrderBins - 1));
 }
 
+constexpr int kOrderHeld = 16;  // tiles per thread whose bins stay in registers (16384 tiles)
+
 __global__ void __launch_bounds__(kOrderThreads) tile_order_kernel(const uint2* ranges, uint32_t ntiles,
                                                                   uint32_t* order) {
+  static_assert(kOrderBins == 4 * kWaveLanes, "four bins per lane in the scan");
   __shared__ uint32_t cnt[kOrderBins];
   for (int b = threadIdx.x; b < kOrderBins; b += kOrderThreads) cnt[b] = 0u;
+  // the thread's first kOrderHeld tiles: all range loads in flight at once,
+  // their bins kept for the placement below
+  uint32_t bin[kOrderHeld];
+#pragma unroll
+  for (int k = 0; k < kOrderHeld; k++) {
+    const uint32_t t = threadIdx.x + (uint32_t)k * kOrderThreads;
+    bin[k] = 0xffffffffu;
+    if (t < ntiles) {
+      const uint2 r = ranges[t];
+      bin[k] = order_bin(r.y - r.x);
+    }
+  }
   __syncthreads();
-  for (uint32_t t = threadIdx.x; t < ntiles; t += kOrderThreads) {
+#pragma unroll
+  for (int k = 0; k < kOrderHeld; k++)
+    if (bin[k] != 0xffffffffu) atomicAdd(&cnt[bin[k]], 1u);
+  for (uint32_t t = threadIdx.x + kOrderHeld * kOrderThreads; t < ntiles; t += kOrderThreads) {
     const uint2 r = ranges[t];
     atomicAdd(&cnt[order_bin(r.y - r.x)], 1u);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t sum = 0u;
-    for (int b = 0; b < kOrderBins; b++) {
-      const uint32_t c = cnt[b];
-      cnt[b] = sum;
-      sum += c;
+  // exclusive scan of the bins by one wave, four per lane
+  if (threadIdx.x < kWaveLanes) {
+    const uint32_t l = threadIdx.x;
+    const uint32_t c0 = cnt[4 * l], c1 = cnt[4 * l + 1], c2 = cnt[4 * l + 2], c3 = cnt[4 * l + 3];
+    const uint32_t s = c0 + c1 + c2 + c3;
+    uint32_t inc = s;
+#pragma unroll
+    for (int d = 1; d < kWaveLanes; d <<= 1) {
+      const uint32_t o = __shfl_up(inc, d, kWaveLanes);
+      if (l >= (uint32_t)d) inc += o;
     }
+    const uint32_t ex = inc - s;
+    cnt[4 * l] = ex;
+    cnt[4 * l + 1] = ex + c0;
+    cnt[4 * l + 2] = ex + c0 + c1;
+    cnt[4 * l + 3] = ex + c0 + c1 + c2;
   }
   __syncthreads();
   // Position pos of the descending order goes to workgroup b; within each
@@ -1266,15 +1293,21 @@ __global__ void __launch_bounds__(kOrderThreads) tile_order_kernel(const uint2* 
   // tiles); a run then mostly holds nearby tiles, which share an L2.
   constexpr uint32_t kRun = 16u, kGroup = 8u * kRun;
   const uint32_t full = ntiles / kGroup * kGroup;  // the tail keeps pos == b
-  for (uint32_t t = threadIdx.x; t < ntiles; t += kOrderThreads) {
-    const uint2 r = ranges[t];
-    const uint32_t pos = atomicAdd(&cnt[order_bin(r.y - r.x)], 1u);
+  auto place = [&](uint32_t t, uint32_t tb) {
+    const uint32_t pos = atomicAdd(&cnt[tb], 1u);
     uint32_t b = pos;
     if (pos < full) {
       const uint32_t g = pos / kGroup, w = pos % kGroup;
       b = (g * kRun + w % kRun) * 8u + w / kRun;
     }
     order[b] = t;
+  };
+#pragma unroll
+  for (int k = 0; k < kOrderHeld; k++)
+    if (bin[k] != 0xffffffffu) place(threadIdx.x + (uint32_t)k * kOrderThreads, bin[k]);
+  for (uint32_t t = threadIdx.x + kOrderHeld * kOrderThreads; t < ntiles; t += kOrderThreads) {
+    const uint2 r = ranges[t];
+    place(t, order_bin(r.y - r.x));
   }
 }
 
