@@ -270,20 +270,36 @@ __global__ void __launch_bounds__(kSortThreads) radix_hist_kernel(const K* __res
 // exclusive prefix: together that is the exclusive scan of the digit-major
 // counts.  The launch also zeroes zero[0, nzero) (the per-tile counters of
 // the tile sort's last pass), since it runs right before that pass.
+constexpr int kDigitHeld = 16;  // block counts per thread held in registers (up to 4096 blocks)
+
 __global__ void __launch_bounds__(kScanThreads) digit_scan_kernel(uint32_t* __restrict__ counts, uint32_t nb,
                                                                  uint32_t* __restrict__ dtot, uint32_t* __restrict__ zero,
                                                                  uint32_t nzero) {
   uint32_t* c = counts + (size_t)blockIdx.x * nb;
   const uint32_t per = (nb + kScanThreads - 1) / kScanThreads;
   const uint32_t lo = threadIdx.x * per, hi = min(lo + per, nb);
+  // the thread's first kDigitHeld counts: loads all in flight at once (a loop
+  // with a runtime trip count issues them one by one), kept for the rewrite
+  uint32_t v[kDigitHeld];
+#pragma unroll
+  for (int k = 0; k < kDigitHeld; k++) v[k] = lo + k < hi ? c[lo + k] : 0u;
   uint64_t s = 0;
-  for (uint32_t i = lo; i < hi; i++) s += c[i];
+#pragma unroll
+  for (int k = 0; k < kDigitHeld; k++) s += v[k];
+  for (uint32_t i = lo + kDigitHeld; i < hi; i++) s += c[i];
   uint64_t total;
   uint64_t run = block_exclusive_scan_u64(s, &total);
-  for (uint32_t i = lo; i < hi; i++) {
-    const uint32_t v = c[i];
+#pragma unroll
+  for (int k = 0; k < kDigitHeld; k++) {
+    if (lo + k < hi) {
+      c[lo + k] = (uint32_t)run;
+      run += v[k];
+    }
+  }
+  for (uint32_t i = lo + kDigitHeld; i < hi; i++) {
+    const uint32_t x = c[i];
     c[i] = (uint32_t)run;
-    run += v;
+    run += x;
   }
   if (threadIdx.x == 0) dtot[blockIdx.x] = (uint32_t)total;
   for (uint32_t i = blockIdx.x * kScanThreads + threadIdx.x; i < nzero; i += gridDim.x * kScanThreads) zero[i] = 0u;
@@ -436,8 +452,20 @@ __global__ void __launch_bounds__(kRangeThreads) ranges_from_counts_kernel(uint2
   const uint32_t lo = threadIdx.x * per, hi = min(lo + per, ntiles);
   const bool staged = ntiles <= kRangeLds;
   if (staged) {
-    // all counts in flight at once (coalesced), then each thread's run from LDS
-    for (uint32_t t = threadIdx.x; t < ntiles; t += kRangeThreads) cnt[t] = ranges[t].y;
+    // all counts in flight at once (coalesced, a fixed count per thread), then
+    // each thread's run from LDS
+    static_assert(kRangeLds % kRangeThreads == 0, "whole rounds of loads");
+    uint32_t v[kRangeLds / kRangeThreads];
+#pragma unroll
+    for (int k = 0; k < (int)(kRangeLds / kRangeThreads); k++) {
+      const uint32_t t = threadIdx.x + (uint32_t)k * kRangeThreads;
+      v[k] = t < ntiles ? ranges[t].y : 0u;
+    }
+#pragma unroll
+    for (int k = 0; k < (int)(kRangeLds / kRangeThreads); k++) {
+      const uint32_t t = threadIdx.x + (uint32_t)k * kRangeThreads;
+      if (t < ntiles) cnt[t] = v[k];
+    }
     __syncthreads();
   }
   uint32_t s = 0;
